@@ -1,0 +1,345 @@
+/* Seeded synthetic Qwen3-shaped GGUF files (random-init weights) for the parity tests and the benchmark.
+ *
+ * Every matmul tensor is N(0, std) before quantization (std 0.02), the norms are a constant (1.0), the
+ * metadata is what the reference's GGUF reader checks for a qwen3 file (gguf.c:230-336: block_count,
+ * embedding_length, feed_forward_length, head counts, context_length, key/value length, rope.freq_base,
+ * layer_norm_rms_epsilon 1e-6) and the tensor names are llama.cpp's (model.c:269-299). No tokenizer
+ * block: readers load these files without a tokenizer (RqModelOpts.no_tokenizer).
+ *
+ * Values: row r of tensor t draws from its own splitmix64 stream seeded by (seed, t, r), Box-Muller in
+ * double precision, so a file is a pure function of (shape, types, seed) whatever the thread count.
+ * Encoders (ggml block formats, restated; the layouts are the ones kquants.h:9-33 documents):
+ *   Q8_0: d = amax / 127 (fp16), q = round(x / d) clamped to [-127, 127]
+ *   Q4_K: 8 sub-blocks of 32, per sub-block scale / offset from its range, 6-bit sc and m against d / dmin
+ *   Q6_K: 16 sub-blocks of 16, int8 sub-scales against d, q in 0..63 (value q - 32)
+ * Any valid block decodes the same way on both sides, so these simple encoders suffice for parity. */
+#include <math.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "gw_synth.h"
+
+enum { T_F32 = 0, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
+
+static uint16_t f32_to_f16_rne(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    uint32_t sign = (u >> 16) & 0x8000u, a = u & 0x7fffffffu;
+    if (a >= 0x7f800000u) return (uint16_t)(sign | 0x7c00u | (a > 0x7f800000u ? 0x200u : 0));
+    if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* rounds to inf */
+    if (a < 0x38800000u) { /* subnormal half: m * 2^-24 */
+        float af;
+        memcpy(&af, &a, 4);
+        return (uint16_t)(sign | (uint32_t)nearbyintf(af * 16777216.0f));
+    }
+    uint32_t n = a - 0x38000000u;
+    return (uint16_t)(sign | ((n + 0xfffu + ((n >> 13) & 1)) >> 13));
+}
+
+static float f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000) << 16, e = h >> 10 & 0x1f, m = h & 0x3ff, bits;
+    if (e == 0x1f) bits = sign | 0x7f800000u | m << 13;
+    else if (e) bits = sign | (e + 112) << 23 | m << 13;
+    else if (m) {
+        float f = (float)m * 5.9604644775390625e-8f;
+        memcpy(&bits, &f, 4);
+        bits |= sign;
+    } else bits = sign;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+static uint64_t splitmix(uint64_t *s) {
+    uint64_t z = (*s += 0x9e3779b97f4a7c15ull);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+static void normal_row(float *y, int n, uint64_t seed, uint64_t tensor, uint64_t row, float std) {
+    uint64_t s = seed * 0x2545f4914f6cdd1dull ^ (tensor + 1) * 0x9e3779b97f4a7c15ull ^ (row + 1) * 0xd1b54a32d192ed03ull;
+    splitmix(&s);
+    for (int i = 0; i < n; i += 2) {
+        double u1 = ((splitmix(&s) >> 11) + 1.0) * (1.0 / 9007199254740992.0); /* (0, 1] */
+        double u2 = (splitmix(&s) >> 11) * (1.0 / 9007199254740992.0);
+        double r = sqrt(-2.0 * log(u1)), th = 6.283185307179586 * u2;
+        y[i] = (float)(std * r * cos(th));
+        if (i + 1 < n) y[i + 1] = (float)(std * r * sin(th));
+    }
+}
+
+size_t gw_synth_row_bytes(int type, int k) {
+    if (type == T_Q8_0) return (size_t)k / 32 * 34;
+    if (type == T_Q4_K) return (size_t)k / 256 * 144;
+    if (type == T_Q6_K) return (size_t)k / 256 * 210;
+    return (size_t)k * 4;
+}
+
+static void enc_q8_0(uint8_t *o, const float *x, int k) {
+    for (int g = 0; g < k / 32; g++, o += 34, x += 32) {
+        float amax = 0;
+        for (int i = 0; i < 32; i++) amax = fabsf(x[i]) > amax ? fabsf(x[i]) : amax;
+        float d = amax / 127.0f, id = d > 0 ? 1.0f / d : 0.0f;
+        uint16_t h = f32_to_f16_rne(d);
+        memcpy(o, &h, 2);
+        for (int i = 0; i < 32; i++) {
+            float v = roundf(x[i] * id);
+            v = v > 127 ? 127 : v < -127 ? -127 : v;
+            o[2 + i] = (uint8_t)(int8_t)v;
+        }
+    }
+}
+
+static void enc_q4_k(uint8_t *o, const float *x, int k) {
+    for (int sb = 0; sb < k / 256; sb++, o += 144, x += 256) {
+        float sc[8], mn[8], smax = 0, mmax = 0;
+        for (int j = 0; j < 8; j++) {
+            float lo = x[32 * j], hi = x[32 * j];
+            for (int i = 1; i < 32; i++) {
+                lo = x[32 * j + i] < lo ? x[32 * j + i] : lo;
+                hi = x[32 * j + i] > hi ? x[32 * j + i] : hi;
+            }
+            if (lo > 0) lo = 0; /* w = s * q - m with m >= 0 */
+            sc[j] = (hi - lo) / 15.0f;
+            mn[j] = -lo;
+            smax = sc[j] > smax ? sc[j] : smax;
+            mmax = mn[j] > mmax ? mn[j] : mmax;
+        }
+        uint16_t hd = f32_to_f16_rne(smax / 63.0f), hm = f32_to_f16_rne(mmax / 63.0f);
+        float d = f16_to_f32(hd), dmin = f16_to_f32(hm);
+        int isc[8], im[8];
+        for (int j = 0; j < 8; j++) {
+            int a = d > 0 ? (int)lroundf(sc[j] / d) : 0, b = dmin > 0 ? (int)lroundf(mn[j] / dmin) : 0;
+            isc[j] = a < 0 ? 0 : a > 63 ? 63 : a;
+            im[j] = b < 0 ? 0 : b > 63 ? 63 : b;
+        }
+        memcpy(o, &hd, 2);
+        memcpy(o + 2, &hm, 2);
+        uint8_t *s = o + 4;
+        for (int j = 0; j < 4; j++) {
+            s[j] = (uint8_t)((isc[j] & 63) | (isc[j + 4] >> 4) << 6);
+            s[j + 4] = (uint8_t)((im[j] & 63) | (im[j + 4] >> 4) << 6);
+            s[j + 8] = (uint8_t)((isc[j + 4] & 15) | (im[j + 4] & 15) << 4);
+        }
+        uint8_t q[256];
+        for (int j = 0; j < 8; j++) {
+            float ds = d * isc[j], dm = dmin * im[j];
+            for (int i = 0; i < 32; i++) {
+                int v = ds > 0 ? (int)lroundf((x[32 * j + i] + dm) / ds) : 0;
+                q[32 * j + i] = (uint8_t)(v < 0 ? 0 : v > 15 ? 15 : v);
+            }
+        }
+        for (int c = 0; c < 4; c++)
+            for (int l = 0; l < 32; l++)
+                o[16 + 32 * c + l] = (uint8_t)(q[64 * c + l] | q[64 * c + 32 + l] << 4);
+    }
+}
+
+static void enc_q6_k(uint8_t *o, const float *x, int k) {
+    for (int sb = 0; sb < k / 256; sb++, o += 210, x += 256) {
+        float ss[16], smax = 0;
+        for (int j = 0; j < 16; j++) {
+            float amax = 0;
+            for (int i = 0; i < 16; i++) amax = fabsf(x[16 * j + i]) > amax ? fabsf(x[16 * j + i]) : amax;
+            ss[j] = amax / 31.0f;
+            smax = ss[j] > smax ? ss[j] : smax;
+        }
+        uint16_t hd = f32_to_f16_rne(smax / 127.0f);
+        float d = f16_to_f32(hd);
+        int8_t isc[16];
+        uint8_t q[256];
+        for (int j = 0; j < 16; j++) {
+            int a = d > 0 ? (int)lroundf(ss[j] / d) : 0;
+            isc[j] = (int8_t)(a > 127 ? 127 : a < 0 ? 0 : a);
+            float ds = d * isc[j];
+            for (int i = 0; i < 16; i++) {
+                int v = ds > 0 ? (int)lroundf(x[16 * j + i] / ds) + 32 : 32;
+                q[16 * j + i] = (uint8_t)(v < 0 ? 0 : v > 63 ? 63 : v);
+            }
+        }
+        uint8_t *ql = o, *qh = o + 128;
+        for (int n = 0; n < 2; n++)
+            for (int l = 0; l < 32; l++) {
+                const uint8_t *qq = q + 128 * n;
+                ql[64 * n + l] = (uint8_t)((qq[l] & 15) | (qq[64 + l] & 15) << 4);
+                ql[64 * n + 32 + l] = (uint8_t)((qq[32 + l] & 15) | (qq[96 + l] & 15) << 4);
+                qh[32 * n + l] = (uint8_t)((qq[l] >> 4) | (qq[32 + l] >> 4) << 2 | (qq[64 + l] >> 4) << 4 | (qq[96 + l] >> 4) << 6);
+            }
+        memcpy(o + 192, isc, 16);
+        memcpy(o + 208, &hd, 2);
+    }
+}
+
+void gw_synth_encode_row(int type, uint8_t *o, const float *x, int k) {
+    if (type == T_Q8_0) enc_q8_0(o, x, k);
+    else if (type == T_Q4_K) enc_q4_k(o, x, k);
+    else if (type == T_Q6_K) enc_q6_k(o, x, k);
+    else memcpy(o, x, (size_t)k * 4);
+}
+
+/* ------------------------------------------------------------------------------------ GGUF writing */
+
+typedef struct {
+    char name[64];
+    int type, rows, cols; /* ne = { cols, rows } (rows 0: a vector of cols values) */
+    int norm;             /* a norm vector (constant value) */
+    uint64_t off;
+} SynTensor;
+
+typedef struct { FILE *f; int err; } W;
+
+static void w_bytes(W *w, const void *p, size_t n) {
+    if (!w->err && fwrite(p, 1, n, w->f) != n) w->err = 1;
+}
+static void w_u32(W *w, uint32_t v) { w_bytes(w, &v, 4); }
+static void w_u64(W *w, uint64_t v) { w_bytes(w, &v, 8); }
+static void w_str(W *w, const char *s) { uint64_t n = strlen(s); w_u64(w, n); w_bytes(w, s, n); }
+static void kv_u32(W *w, const char *k, uint32_t v) { w_str(w, k); w_u32(w, 4 /* GV_U32 */); w_u32(w, v); }
+static void kv_f32(W *w, const char *k, float v) { w_str(w, k); w_u32(w, 6 /* GV_F32 */); w_bytes(w, &v, 4); }
+static void kv_s(W *w, const char *k, const char *v) { w_str(w, k); w_u32(w, 8 /* GV_STR */); w_str(w, v); }
+
+typedef struct {
+    const SynTensor *t;
+    int tindex;
+    uint8_t *out; /* the chunk buffer: row r at out + (r - base) * row bytes */
+    int base;
+    uint64_t seed;
+    float std;
+    int r0, r1;
+} Job;
+
+static void *job_run(void *arg) {
+    Job *j = arg;
+    const SynTensor *t = j->t;
+    float *row = malloc((size_t)t->cols * sizeof(float));
+    if (!row) return (void *)1;
+    size_t rb = gw_synth_row_bytes(t->type, t->cols);
+    for (int r = j->r0; r < j->r1; r++) {
+        normal_row(row, t->cols, j->seed, (uint64_t)j->tindex, (uint64_t)r, j->std);
+        gw_synth_encode_row(t->type, j->out + (size_t)(r - j->base) * rb, row, t->cols);
+    }
+    free(row);
+    return NULL;
+}
+
+int gw_synth_gguf(const char *path, const GwSynthCfg *c, unsigned long long seed, int nthreads) {
+    if (!path || !c || c->dim <= 0 || c->n_layers <= 0 || c->n_heads <= 0 || c->n_kv_heads <= 0 || c->head_dim <= 0 ||
+        c->hidden <= 0 || c->vocab <= 0 || c->n_heads % c->n_kv_heads)
+        return -1;
+    int L = c->n_layers, dim = c->dim, qd = c->n_heads * c->head_dim, kvd = c->n_kv_heads * c->head_dim;
+    int td = c->type_default ? c->type_default : T_Q8_0;
+#define TY(x) ((x) ? (x) : td)
+    int nt = 3 + !c->tied + 11 * L, k = 0;
+    SynTensor *T = calloc((size_t)nt, sizeof(SynTensor));
+    if (!T) return -2;
+#define ADD(nm, ty, r, cl, nrm) do { snprintf(T[k].name, sizeof(T[k].name), "%s", nm); T[k].type = (ty); T[k].rows = (r); \
+        T[k].cols = (cl); T[k].norm = (nrm); k++; } while (0)
+    char nm[64];
+    ADD("token_embd.weight", TY(c->type_embd), c->vocab, dim, 0);
+    ADD("output_norm.weight", T_F32, 0, dim, 1);
+    if (!c->tied) ADD("output.weight", TY(c->type_out), c->vocab, dim, 0);
+    for (int l = 0; l < L; l++) {
+        snprintf(nm, sizeof nm, "blk.%d.attn_norm.weight", l); ADD(nm, T_F32, 0, dim, 1);
+        snprintf(nm, sizeof nm, "blk.%d.attn_q.weight", l); ADD(nm, TY(c->type_q), qd, dim, 0);
+        snprintf(nm, sizeof nm, "blk.%d.attn_k.weight", l); ADD(nm, TY(c->type_k), kvd, dim, 0);
+        snprintf(nm, sizeof nm, "blk.%d.attn_v.weight", l); ADD(nm, TY(c->type_v), kvd, dim, 0);
+        snprintf(nm, sizeof nm, "blk.%d.attn_output.weight", l); ADD(nm, TY(c->type_o), dim, qd, 0);
+        snprintf(nm, sizeof nm, "blk.%d.attn_q_norm.weight", l); ADD(nm, T_F32, 0, c->head_dim, 1);
+        snprintf(nm, sizeof nm, "blk.%d.attn_k_norm.weight", l); ADD(nm, T_F32, 0, c->head_dim, 1);
+        snprintf(nm, sizeof nm, "blk.%d.ffn_norm.weight", l); ADD(nm, T_F32, 0, dim, 1);
+        snprintf(nm, sizeof nm, "blk.%d.ffn_gate.weight", l); ADD(nm, TY(c->type_gate), c->hidden, dim, 0);
+        snprintf(nm, sizeof nm, "blk.%d.ffn_up.weight", l); ADD(nm, TY(c->type_up), c->hidden, dim, 0);
+        snprintf(nm, sizeof nm, "blk.%d.ffn_down.weight", l); ADD(nm, TY(c->type_down), dim, c->hidden, 0);
+    }
+    nt = k;
+    const uint64_t align = 32;
+    uint64_t off = 0;
+    for (int i = 0; i < nt; i++) {
+        if ((T[i].type == T_Q4_K || T[i].type == T_Q6_K) && T[i].cols % 256) { free(T); return -1; }
+        if (T[i].type == T_Q8_0 && T[i].cols % 32) { free(T); return -1; }
+        T[i].off = off;
+        uint64_t sz = T[i].rows ? (uint64_t)T[i].rows * gw_synth_row_bytes(T[i].type, T[i].cols) : (uint64_t)T[i].cols * 4;
+        off += (sz + align - 1) / align * align;
+    }
+    FILE *f = fopen(path, "wb");
+    if (!f) { free(T); return -3; }
+    static char buf[1 << 22];
+    setvbuf(f, buf, _IOFBF, sizeof buf);
+    W w = { f, 0 };
+    w_u32(&w, 0x46554747u);
+    w_u32(&w, 3);
+    w_u64(&w, (uint64_t)nt);
+    w_u64(&w, 13);
+    kv_s(&w, "general.architecture", "qwen3");
+    kv_u32(&w, "general.alignment", (uint32_t)align);
+    kv_u32(&w, "qwen3.block_count", (uint32_t)L);
+    kv_u32(&w, "qwen3.embedding_length", (uint32_t)dim);
+    kv_u32(&w, "qwen3.feed_forward_length", (uint32_t)c->hidden);
+    kv_u32(&w, "qwen3.attention.head_count", (uint32_t)c->n_heads);
+    kv_u32(&w, "qwen3.attention.head_count_kv", (uint32_t)c->n_kv_heads);
+    kv_u32(&w, "qwen3.context_length", (uint32_t)(c->ctx_len > 0 ? c->ctx_len : 40960));
+    kv_u32(&w, "qwen3.attention.key_length", (uint32_t)c->head_dim);
+    kv_u32(&w, "qwen3.attention.value_length", (uint32_t)c->head_dim);
+    kv_f32(&w, "qwen3.rope.freq_base", c->rope_theta > 0 ? c->rope_theta : 1e6f);
+    kv_f32(&w, "qwen3.attention.layer_norm_rms_epsilon", 1e-6f);
+    kv_s(&w, "general.name", "gwenedeg-amd synthetic");
+    for (int i = 0; i < nt; i++) {
+        w_str(&w, T[i].name);
+        if (T[i].rows) {
+            w_u32(&w, 2);
+            w_u64(&w, (uint64_t)T[i].cols);
+            w_u64(&w, (uint64_t)T[i].rows);
+        } else {
+            w_u32(&w, 1);
+            w_u64(&w, (uint64_t)T[i].cols);
+        }
+        w_u32(&w, (uint32_t)T[i].type);
+        w_u64(&w, T[i].off);
+    }
+    long pos = ftell(f);
+    static const uint8_t zeros[64];
+    if (pos % (long)align) w_bytes(&w, zeros, (size_t)(align - pos % align));
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 64) nthreads = 64;
+    float std = c->std > 0 ? c->std : 0.02f, nv = c->norm_value != 0 ? c->norm_value : 1.0f;
+    uint64_t written = 0;
+    int rc = 0;
+    for (int i = 0; i < nt && !w.err && !rc; i++) {
+        if (written < T[i].off) { uint64_t pad = T[i].off - written; w_bytes(&w, zeros, (size_t)pad); written += pad; }
+        if (!T[i].rows) {
+            for (int j = 0; j < T[i].cols; j++) w_bytes(&w, &nv, 4);
+            written += (uint64_t)T[i].cols * 4;
+            continue;
+        }
+        size_t rb = gw_synth_row_bytes(T[i].type, T[i].cols), chunk_rows = (size_t)(256u << 20) / rb;
+        if (chunk_rows < 1) chunk_rows = 1;
+        uint8_t *out = malloc(chunk_rows * rb);
+        if (!out) { rc = -2; break; }
+        for (int r0 = 0; r0 < T[i].rows && !rc; r0 += (int)chunk_rows) {
+            int r1 = r0 + (int)chunk_rows < T[i].rows ? r0 + (int)chunk_rows : T[i].rows, n = r1 - r0;
+            int tn = nthreads < n ? nthreads : n;
+            pthread_t th[64];
+            Job jb[64];
+            for (int q = 0; q < tn; q++) {
+                jb[q] = (Job){ &T[i], i, out, r0, seed, std, r0 + (int)(n * (long)q / tn), r0 + (int)(n * (long)(q + 1) / tn) };
+            }
+            for (int q = 0; q < tn; q++)
+                if (pthread_create(&th[q], NULL, job_run, &jb[q])) { rc = -4; tn = q; break; }
+            for (int q = 0; q < tn; q++) {
+                void *res = NULL;
+                pthread_join(th[q], &res);
+                if (res) rc = -2;
+            }
+            if (!rc) w_bytes(&w, out, (size_t)n * rb);
+        }
+        free(out);
+        written += (uint64_t)T[i].rows * rb;
+    }
+    if (fclose(f)) w.err = 1;
+    free(T);
+    return rc ? rc : w.err ? -3 : 0;
+}

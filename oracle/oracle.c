@@ -1,0 +1,702 @@
+/* The oracle: a plain-C restatement of the reference's (j3k0/gwenedeg) arithmetic for the forward hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load it as the checker;
+ * the product never links, calls or falls back to it.
+ *
+ * Compiled with -O2 -fno-fast-math -ffp-contract=off (oracle/Makefile): every fp32 operation below is one IEEE
+ * operation rounded to nearest, in the order written; fmaf() is written where the reference's definition has a
+ * fused multiply-add (the attention's chains: forward.c:1295-1299 with FP_FAST_FMAF on the AVX-512 builds).
+ *
+ * How each part is pinned (tests/test_oracle.py):
+ *   fp16 / f32_f16 / quantize / Q8_0 fold: against the reference's own compiled kernels (oracle/_ref/ref_q8op:
+ *     q8p_gemv_rows / q8p_gemm_item, bit-exact), brute-force integer sums, closed forms and edge cases;
+ *   K-quant fold: against the reference's kq_dot (oracle/_ref/ref_q8op kq, bit-exact) and a float64 dequantized
+ *     product; the dequantization against an independent numpy decode of the block formats;
+ *   attention: one block against a float64 softmax; several blocks against the single-block result (combine);
+ *   the whole forward: against the compiled reference (oracle/_ref/ref_driver) on synthetic models, logits within
+ *     tolerance and identical greedy tokens. rmsnorm / RoPE / SwiGLU are pinned only through that comparison: the
+ *     reference's bits there come from -Ofast (rsqrt estimate + Newton for 1 / sqrtf, reassociated sums) and from
+ *     glibc's vector expf / sincosf, so they are reproduced to tolerance, not to the bit (parity unpinned at bit level).
+ */
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "oracle.h"
+
+#define GS 32
+#define ATT_T 16
+#define ATT_P 256
+#define ATT_DC 32
+
+/* ------------------------------------------------------------------------------------------ formats */
+
+float or_fp16_to_f32(uint16_t h) {
+    /* kquants.h:143-156: exact */
+    uint32_t sign = (uint32_t)(h & 0x8000) << 16, e = h >> 10 & 0x1f, m = h & 0x3ff, bits;
+    if (e == 0x1f) bits = sign | 0x7f800000u | m << 13;
+    else if (e) bits = sign | (e + 112) << 23 | m << 13;
+    else if (m) {
+        float f = (float)m * 5.9604644775390625e-8f;
+        memcpy(&bits, &f, 4);
+        bits |= sign;
+    } else bits = sign;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+uint16_t or_f32_f16(float f) {
+    /* forward.c:1325-1344: round to nearest even, saturating at 65504, subnormals exact, NaN quiet */
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    uint32_t sign = (u >> 16) & 0x8000u, a = u & 0x7fffffffu;
+    uint32_t h;
+    if (a > 0x7f800000u) h = 0x7e00u | ((a >> 13) & 0x3ffu);
+    else if (a >= 0x477ff000u) h = 0x7bffu;
+    else if (a < 0x38800000u) {
+        float fs;
+        memcpy(&fs, &a, 4);
+        h = (uint32_t)rintf(fs * 0x1p24f);
+    } else {
+        uint32_t n = a - 0x38000000u;
+        h = (n + 0xfffu + ((n >> 13) & 1)) >> 13;
+    }
+    return (uint16_t)(sign | h);
+}
+
+/* ------------------------------------------------------------------------------------- quantization */
+
+void or_quantize(int8_t *q, float *s, const float *x, int n) {
+    /* forward.c:803-836: s = wmax * (1 / 127), inv = 127 / wmax, q = trunc(v + copysign(0.49999997, v)), v = x * inv;
+     * an all-zero group: s = 0, q = 0 */
+    for (int g = 0; g < n / GS; g++) {
+        const float *xg = x + (size_t)g * GS;
+        int8_t *qg = q + (size_t)g * GS;
+        float wmax = 0;
+        for (int i = 0; i < GS; i++) {
+            float v = fabsf(xg[i]);
+            if (v > wmax) wmax = v;
+        }
+        s[g] = wmax * (1.0f / 127.0f);
+        if (!(wmax > 0)) {
+            memset(qg, 0, GS);
+            continue;
+        }
+        float inv = 127.0f / wmax;
+        for (int i = 0; i < GS; i++) {
+            float v = xg[i] * inv;
+            qg[i] = (int8_t)(int32_t)(v + copysignf(0.49999997f, v));
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------------------------- Q8_0 */
+
+float or_dot_q8(const int8_t *wq, const float *ws, const int8_t *xq, const float *xs, int k) {
+    /* forward.c:906-916 (the fold as kernels_avx512.h:157-162 states it): per group an exact int32 sum, then
+     * val = val + (ws * xs) * (float) isum, each operation rounded, groups in order */
+    float val = 0;
+    for (int g = 0; g < k / GS; g++) {
+        int32_t isum = 0;
+        for (int i = 0; i < GS; i++)
+            isum += (int32_t)wq[g * GS + i] * (int32_t)xq[g * GS + i];
+        float sc = ws[g] * xs[g];
+        float p = sc * (float)isum;
+        val = val + p;
+    }
+    return val;
+}
+
+void or_q8_matmul(float *out, const int8_t *wq, const float *ws, const int8_t *xq, const float *xs, int M, int N, int K) {
+    for (int m = 0; m < M; m++)
+        for (int n = 0; n < N; n++)
+            out[(size_t)m * N + n] = or_dot_q8(wq + (size_t)n * K, ws + (size_t)n * (K / GS), xq + (size_t)m * K,
+                                               xs + (size_t)m * (K / GS), K);
+}
+
+void or_q8_block_sums(int32_t *isum, const int8_t *wq, const int8_t *xq, int M, int N, int K) {
+    int G = K / GS;
+    for (int m = 0; m < M; m++)
+        for (int n = 0; n < N; n++)
+            for (int g = 0; g < G; g++) {
+                int32_t a = 0;
+                for (int i = 0; i < GS; i++)
+                    a += (int32_t)wq[(size_t)n * K + g * GS + i] * (int32_t)xq[(size_t)m * K + g * GS + i];
+                isum[((size_t)m * N + n) * G + g] = a;
+            }
+}
+
+void or_q8_from_blocks(int8_t *q, float *s, const uint8_t *blk, size_t nblk) {
+    /* model.c:47-59 */
+    for (size_t i = 0; i < nblk; i++, blk += 34) {
+        uint16_t h;
+        memcpy(&h, blk, 2);
+        s[i] = or_fp16_to_f32(h);
+        memcpy(q + 32 * i, blk + 2, 32);
+    }
+}
+
+/* ---------------------------------------------------------------------------------------- K-quants */
+
+enum { T_F32 = 0, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
+
+static uint16_t u16(const uint8_t *p) { uint16_t v; memcpy(&v, p, 2); return v; }
+
+static void q4k_scale_min(const uint8_t *s, int j, int *sc, int *m) {
+    /* kquants.h:169-178 (ggml's get_scale_min_k4) */
+    if (j < 4) {
+        *sc = s[j] & 63;
+        *m = s[j + 4] & 63;
+    } else {
+        *sc = (s[j + 4] & 15) | (s[j - 4] >> 6) << 4;
+        *m = (s[j + 4] >> 4) | (s[j] >> 6) << 4;
+    }
+}
+
+static int q4k_q(const uint8_t *b, int i) { return (b[16 + 32 * (i / 64) + i % 32] >> (4 * (i / 32 % 2))) & 15; } /* :180 */
+
+static int q6k_q(const uint8_t *b, int i) { /* kquants.h:192-198 */
+    int n = i / 128, p = i / 32 % 4, l = i % 32;
+    return ((b[64 * n + 32 * (p & 1) + l] >> (4 * (p >> 1))) & 15) | ((b[128 + 32 * n + l] >> (2 * p)) & 3) << 4;
+}
+
+static int kq_bytes(int type) { return type == T_Q4_K ? 144 : 210; }
+
+void or_kq_dequant_row(int type, const uint8_t *blk, int n, float *y) {
+    /* kquants.h:222-251 (Q4_K, Q6_K) */
+    for (int s = 0; s < n / 256; s++, y += 256) {
+        const uint8_t *b = blk + (size_t)s * kq_bytes(type);
+        if (type == T_Q4_K) {
+            float d = or_fp16_to_f32(u16(b)), dmin = or_fp16_to_f32(u16(b + 2));
+            for (int j = 0; j < 8; j++) {
+                int sc, m;
+                q4k_scale_min(b + 4, j, &sc, &m);
+                float d1 = d * sc, m1 = dmin * m;
+                for (int l = 0; l < 32; l++) y[32 * j + l] = d1 * q4k_q(b, 32 * j + l) - m1;
+            }
+        } else {
+            float d = or_fp16_to_f32(u16(b + 208));
+            for (int i = 0; i < 256; i++) y[i] = d * (float)(int8_t)b[192 + i / 16] * (float)(q6k_q(b, i) - 32);
+        }
+    }
+}
+
+void or_kq_act_prep(float *xf, const int8_t *xq, const float *xs, int n) {
+    /* kquants.h:392-400 */
+    for (int g = 0; g < n / 32; g++) {
+        int32_t sum = 0;
+        for (int i = 0; i < 32; i++) sum += xq[32 * g + i];
+        xf[g] = xs[g] * (float)sum;
+    }
+}
+
+static float kq_dot_row(int type, const uint8_t *row, const int8_t *x, const float *xs, const float *xf, int K) {
+    /* the definition, kquants.h:86-109, on the file's blocks of one weight row */
+    float val = 0;
+    for (int s = 0; s < K / 256; s++) {
+        const uint8_t *b = row + (size_t)s * kq_bytes(type);
+        for (int j = 0; j < 8; j++) {
+            int g = 8 * s + j;
+            const int8_t *xg = x + 32 * g;
+            if (type == T_Q4_K) {
+                int sc, m;
+                q4k_scale_min(b + 4, j, &sc, &m);
+                int32_t isum = 0;
+                for (int i = 0; i < 32; i++) isum += q4k_q(b, 32 * j + i) * xg[i];
+                float ds = or_fp16_to_f32(u16(b)) * (float)sc, dm = or_fp16_to_f32(u16(b + 2)) * (float)m;
+                float a = (ds * xs[g]) * (float)isum;
+                float bb = dm * xf[g];
+                val = val + (a - bb);
+            } else {
+                int32_t I = 0;
+                for (int h = 0; h < 2; h++) {
+                    int jj = 2 * j + h;
+                    int32_t t = 0, xsum = 0;
+                    for (int i = 0; i < 16; i++) {
+                        t += q6k_q(b, 16 * jj + i) * xg[16 * h + i];
+                        xsum += xg[16 * h + i];
+                    }
+                    I += (int32_t)(int8_t)b[192 + jj] * (t - 32 * xsum);
+                }
+                float d = or_fp16_to_f32(u16(b + 208));
+                val = val + (d * xs[g]) * (float)I;
+            }
+        }
+    }
+    return val;
+}
+
+void or_kq_matmul(int type, float *out, const uint8_t *blocks, const int8_t *xq, const float *xs, int M, int N, int K) {
+    size_t rb = (size_t)(K / 256) * kq_bytes(type);
+    float *xf = malloc((size_t)(K / 32) * sizeof(float));
+    for (int m = 0; m < M; m++) {
+        or_kq_act_prep(xf, xq + (size_t)m * K, xs + (size_t)m * (K / 32), K);
+        for (int n = 0; n < N; n++)
+            out[(size_t)m * N + n] = kq_dot_row(type, blocks + (size_t)n * rb, xq + (size_t)m * K, xs + (size_t)m * (K / 32), xf, K);
+    }
+    free(xf);
+}
+
+/* --------------------------------------------------------------------------------------- attention */
+
+float or_exp_att(float x) {
+    /* forward.c:1301-1321 (= att512_exp, kernels_avx512.h:1163-1181): Cephes-style, x clamped at -86 */
+    x = x > -86.0f ? x : -86.0f;
+    float n = rintf(x * 1.44269504088896341f);
+    float r = fmaf(n, -0.693359375f, x);
+    r = fmaf(n, 2.12194440e-4f, r);
+    float z = r * r;
+    float y = 1.9875691500e-4f;
+    y = fmaf(y, r, 1.3981999507e-3f);
+    y = fmaf(y, r, 8.3334519073e-3f);
+    y = fmaf(y, r, 4.1665795894e-2f);
+    y = fmaf(y, r, 1.6666665459e-1f);
+    y = fmaf(y, r, 5.0000001201e-1f);
+    y = fmaf(y, z, r);
+    y = y + 1.0f;
+    uint32_t bits;
+    memcpy(&bits, &y, 4);
+    bits += (uint32_t)(int32_t)n << 23;
+    memcpy(&y, &bits, 4);
+    return y;
+}
+
+size_t or_kv_tile(int t, int h, int n_kv, int hd) {
+    return (((size_t)(t / ATT_P) * n_kv + h) * ATT_P + (size_t)(t % ATT_P / ATT_T) * ATT_T) * hd;
+}
+
+void or_attention_block(float *o, float *ml, const float *q, const uint16_t *kc, const uint16_t *vc, int n, int b, int h,
+                        int n_kv, int hd, float scale) {
+    /* attention_vec (forward.c:1346-1403) on block b of kv head h: positions t0 .. t0 + nb - 1 */
+    int t0 = b * ATT_P, nb = n - t0 < ATT_P ? n - t0 : ATT_P;
+    float S[ATT_P] = { 0 };
+    for (int t = 0; t < nb; t++) {
+        const uint16_t *k = kc + or_kv_tile(t0 + t, h, n_kv, hd);
+        int j = t % ATT_T;
+        float a = 0;
+        for (int i0 = 0; i0 < hd; i0 += ATT_DC) {
+            float c = 0;
+            for (int i = i0; i < i0 + ATT_DC; i++) c = fmaf(q[i], or_fp16_to_f32(k[i * ATT_T + j]), c);
+            a = i0 > 0 ? a + c : c;
+        }
+        S[t] = a * scale;
+    }
+    float m = S[0];
+    for (int t = 1; t < nb; t++)
+        if (S[t] > m) m = S[t];
+    float sum[ATT_T];
+    for (int j = 0; j < ATT_T; j++) sum[j] = 0.0f;
+    for (int t = 0; t < (nb + ATT_T - 1) / ATT_T * ATT_T; t++) {
+        float e = t < nb ? or_exp_att(S[t] - m) : 0.0f;
+        if (t < nb) S[t] = e;
+        sum[t % ATT_T] = sum[t % ATT_T] + e;
+    }
+    for (int w = ATT_T / 2; w >= 1; w /= 2)
+        for (int j = 0; j < w; j++) sum[j] = sum[j] + sum[j + w];
+    ml[0] = m;
+    ml[1] = sum[0];
+    for (int i = 0; i < hd; i++) o[i] = 0.0f;
+    for (int t = 0; t < nb; t++) {
+        const uint16_t *v = vc + or_kv_tile(t0 + t, h, n_kv, hd) + (size_t)(t % ATT_T) * hd;
+        for (int i = 0; i < hd; i++) o[i] = fmaf(S[t], or_fp16_to_f32(v[i]), o[i]);
+    }
+}
+
+void or_att_combine(float *out, int nb, const float *part, size_t stride, int hd) {
+    /* forward.c:1405-1431 */
+    if (nb == 1) {
+        float inv = 1.0f / part[hd + 1];
+        for (int i = 0; i < hd; i++) out[i] = part[i] * inv;
+        return;
+    }
+    float M = part[hd];
+    for (int b = 1; b < nb; b++)
+        if (part[b * stride + hd] > M) M = part[b * stride + hd];
+    float L = 0.0f;
+    for (int i = 0; i < hd; i++) out[i] = 0.0f;
+    for (int b = 0; b < nb; b++) {
+        const float *o = part + b * stride;
+        float c = or_exp_att(o[hd] - M);
+        L = fmaf(c, o[hd + 1], L);
+        for (int i = 0; i < hd; i++) out[i] = fmaf(c, o[i], out[i]);
+    }
+    float inv = 1.0f / L;
+    for (int i = 0; i < hd; i++) out[i] = out[i] * inv;
+}
+
+void or_attention(float *out, const float *q, const uint16_t *kc, const uint16_t *vc, int n, int h, int n_kv, int hd,
+                  float scale) {
+    /* attention_kv (forward.c:1871-1892): one block directly, else the partials of every block, combined */
+    int nb = (n + ATT_P - 1) / ATT_P;
+    size_t st = (size_t)hd + 16;
+    float *part = malloc((size_t)nb * st * sizeof(float));
+    for (int b = 0; b < nb; b++)
+        or_attention_block(part + b * st, part + b * st + hd, q, kc, vc, n, b, h, n_kv, hd, scale);
+    or_att_combine(out, nb, part, st, hd);
+    free(part);
+}
+
+/* ------------------------------------------------------------------------------- norms, RoPE, SwiGLU */
+
+float or_rms_scale(const float *x, int n) {
+    /* rmsnorm's scale (forward.c:886-901) in the operation order gcc -Ofast gives the reference (its rmsnorm and every
+     * inlined copy): 16 lanes, lane j an fma chain over x[j], x[j + 16], ... from 0; the fixed tree (lanes j + 8, then
+     * + 4, + 2, + 1); t = fma(ss, 1 / n, 1e-6); 1 / sqrt(t). The reference takes an rsqrt estimate + one Newton step
+     * there (vrsqrtss, host-specific bits); here both operations are IEEE (n % 16 == 0) */
+    float s[16];
+    for (int j = 0; j < 16; j++) s[j] = 0.0f;
+    for (int j = 0; j < n; j++) s[j % 16] = fmaf(x[j], x[j], s[j % 16]);
+    for (int w = 8; w >= 1; w /= 2)
+        for (int j = 0; j < w; j++) s[j] = s[j] + s[j + w];
+    float inv_n = 1.0f / (float)n;
+    float t = fmaf(s[0], inv_n, 1e-6f);
+    return 1.0f / sqrtf(t);
+}
+
+void or_rmsnorm(float *o, const float *x, const float *w, int n) {
+    /* forward.c:886-901: o = (w * x) * scale (the compiled order of weight[j] * (ss * x[j])) */
+    float r = or_rms_scale(x, n);
+    for (int j = 0; j < n; j++) o[j] = (w[j] * x[j]) * r;
+}
+
+void or_rope_row(float *cs, int hd, int pos, float log_theta) {
+    /* forward.c:1248-1264 (glibc's scalar expf / cosf / sinf here; the reference's loop may take libmvec's) */
+    for (int j = 0; j < hd / 2; j++) {
+        float freq = expf(log_theta * (-(float)j / (hd / 2)));
+        cs[j] = cosf(pos * freq);
+        cs[j + hd / 2] = sinf(pos * freq);
+    }
+}
+
+void or_qk_norm_rope(float *v, int n_heads, const float *w, int hd, const float *cs) {
+    /* forward.c:1266-1284 (rope_dim = head_dim for Qwen3); the rotation as compiled: x' = fma(x, c, -(y * s)),
+     * y' = fma(x, s, y * c) */
+    for (int h = 0; h < n_heads; h++) {
+        float *q = v + (size_t)h * hd;
+        or_rmsnorm(q, q, w, hd);
+        for (int j = 0; j < hd / 2; j++) {
+            float c = cs[j], s = cs[j + hd / 2], x = q[j], y = q[j + hd / 2];
+            float ys = y * s, yc = y * c;
+            q[j] = fmaf(x, c, -ys);
+            q[j + hd / 2] = fmaf(x, s, yc);
+        }
+    }
+}
+
+float or_silu_exp(float x) {
+    /* SiLU's exponential: the reference calls glibc's (vector) expf at min(-h, 80) (forward.c:1953-1958); here the
+     * Cephes-style exp of the attention (exp_att) with the argument clamped to [-86, 80] (80: the reference's clamp;
+     * below -86, 1 + e rounds to 1 either way) */
+    x = x < 80.0f ? x : 80.0f;
+    return or_exp_att(x);
+}
+
+void or_swiglu(float *hb, const float *hb2, int n) {
+    /* forward.c:1953-1958 in the compiled order: (h * h2) * (1 / (1 + e)), e = exp(min(-h, 80)); the reference's
+     * reciprocal is an rcp14 estimate + Newton step, here an IEEE division */
+    for (int i = 0; i < n; i++) {
+        float h = hb[i];
+        float e = or_silu_exp(-h);
+        float r = 1.0f / (1.0f + e);
+        hb[i] = (h * hb2[i]) * r;
+    }
+}
+
+/* ------------------------------------------------------------------------------------------ model */
+
+typedef struct { int type, rows, cols; const uint8_t *data; } OrMat;
+
+struct OrModel {
+    int dim, hidden, L, nh, nkv, hd, vocab, kv_len, cap;
+    float log_theta, att_scale;
+    uint8_t *file;
+    OrMat embd, out, *wq, *wk, *wv, *wo, *w1, *w2, *w3;
+    const float *final_norm, **att_norm, **ffn_norm, **q_norm, **k_norm;
+};
+
+struct OrSeq {
+    const OrModel *m;
+    int len;
+    uint16_t *kc, *vc;
+};
+
+typedef struct { const char *name; size_t nlen; uint64_t ne[4]; uint32_t nd, type; uint64_t off; } GT;
+
+static int rd(const uint8_t *f, size_t sz, size_t *p, void *dst, size_t n) {
+    if (*p + n > sz) return 0;
+    memcpy(dst, f + *p, n);
+    *p += n;
+    return 1;
+}
+
+static size_t row_bytes(int type, int k) {
+    return type == T_Q8_0 ? (size_t)k / 32 * 34 : type == T_Q4_K ? (size_t)k / 256 * 144 : type == T_Q6_K ? (size_t)k / 256 * 210 : (size_t)k * 4;
+}
+
+OrModel *or_model_load(const char *path, int cap, char *err, size_t errlen) {
+    /* a GGUF v3 file as gw_synth writes it (and llama.cpp's qwen3 files): metadata + tensor table, read whole */
+#define FAIL(...) do { snprintf(err, errlen, __VA_ARGS__); goto fail; } while (0)
+    OrModel *m = calloc(1, sizeof(OrModel));
+    GT *T = NULL;
+    FILE *fp = fopen(path, "rb");
+    if (!m || !fp) { snprintf(err, errlen, "cannot open %s", path); if (fp) fclose(fp); free(m); return NULL; }
+    fseek(fp, 0, SEEK_END);
+    size_t sz = (size_t)ftell(fp);
+    fseek(fp, 0, SEEK_SET);
+    m->file = malloc(sz);
+    if (!m->file || fread(m->file, 1, sz, fp) != sz) { fclose(fp); FAIL("read failed"); }
+    fclose(fp);
+    const uint8_t *f = m->file;
+    size_t p = 0;
+    uint32_t magic, ver;
+    uint64_t nt, nkv;
+    if (!rd(f, sz, &p, &magic, 4) || magic != 0x46554747u || !rd(f, sz, &p, &ver, 4) || !rd(f, sz, &p, &nt, 8) ||
+        !rd(f, sz, &p, &nkv, 8))
+        FAIL("not a GGUF file");
+    uint64_t align = 32;
+    int64_t meta[8] = { 0 };
+    float theta = 1e6f;
+    static const char *keys[8] = { "qwen3.block_count", "qwen3.embedding_length", "qwen3.feed_forward_length",
+                                   "qwen3.attention.head_count", "qwen3.attention.head_count_kv", "qwen3.context_length",
+                                   "qwen3.attention.key_length", "general.alignment" };
+    static const size_t vsz[13] = { 1, 1, 2, 2, 4, 4, 4, 1, 0, 0, 8, 8, 8 };
+    for (uint64_t i = 0; i < nkv; i++) {
+        uint64_t kl;
+        if (!rd(f, sz, &p, &kl, 8) || p + kl > sz) FAIL("bad metadata");
+        const char *key = (const char *)f + p;
+        p += kl;
+        uint32_t ty, aty = 0;
+        uint64_t cnt = 1;
+        if (!rd(f, sz, &p, &ty, 4)) FAIL("bad metadata");
+        size_t vpos = p;
+        if (ty == 9) { if (!rd(f, sz, &p, &aty, 4) || !rd(f, sz, &p, &cnt, 8)) FAIL("bad metadata"); }
+        uint32_t et = ty == 9 ? aty : ty;
+        for (uint64_t j = 0; j < cnt; j++) {
+            if (et == 8) { uint64_t sl; if (!rd(f, sz, &p, &sl, 8) || p + sl > sz) FAIL("bad metadata"); p += sl; }
+            else if (et < 13 && vsz[et]) p += vsz[et];
+            else FAIL("bad metadata type");
+        }
+        if (ty == 9) continue;
+        for (int k = 0; k < 8; k++)
+            if (kl == strlen(keys[k]) && !memcmp(key, keys[k], kl)) {
+                uint64_t v = 0;
+                memcpy(&v, f + vpos, vsz[ty] < 8 ? vsz[ty] : 8);
+                meta[k] = (int64_t)v;
+            }
+        if (kl == 20 && !memcmp(key, "qwen3.rope.freq_base", 20)) memcpy(&theta, f + vpos, 4);
+    }
+    if (meta[7]) align = (uint64_t)meta[7];
+    T = calloc(nt, sizeof(GT));
+    for (uint64_t i = 0; i < nt; i++) {
+        uint64_t nl;
+        if (!rd(f, sz, &p, &nl, 8) || p + nl > sz) FAIL("bad tensor table");
+        T[i].name = (const char *)f + p;
+        T[i].nlen = nl;
+        p += nl;
+        if (!rd(f, sz, &p, &T[i].nd, 4) || T[i].nd < 1 || T[i].nd > 4) FAIL("bad tensor table");
+        for (uint32_t d = 0; d < 4; d++) {
+            T[i].ne[d] = 1;
+            if (d < T[i].nd && !rd(f, sz, &p, &T[i].ne[d], 8)) FAIL("bad tensor table");
+        }
+        if (!rd(f, sz, &p, &T[i].type, 4) || !rd(f, sz, &p, &T[i].off, 8)) FAIL("bad tensor table");
+    }
+    size_t data = (p + align - 1) / align * align;
+    m->L = (int)meta[0]; m->dim = (int)meta[1]; m->hidden = (int)meta[2]; m->nh = (int)meta[3]; m->nkv = (int)meta[4];
+    m->hd = meta[6] ? (int)meta[6] : m->dim / m->nh;
+    int ctx = (int)meta[5];
+    m->cap = cap > 0 && cap < ctx ? cap : ctx;
+    m->kv_len = (m->cap + ATT_P - 1) / ATT_P * ATT_P;
+    m->log_theta = (float)log((double)theta);
+    m->att_scale = 1.0f / sqrtf((float)m->hd);
+    if (m->L < 1 || m->dim < 32 || m->nh < 1 || m->nkv < 1 || m->nh % m->nkv) FAIL("bad hyperparameters");
+#define FIND(nm, dst, rows_, cols_) do { int found_ = 0; for (uint64_t i_ = 0; i_ < nt; i_++) \
+        if (T[i_].nlen == strlen(nm) && !memcmp(T[i_].name, nm, T[i_].nlen)) { \
+            (dst).type = (int)T[i_].type; (dst).cols = (int)T[i_].ne[0]; (dst).rows = (int)(T[i_].nd > 1 ? T[i_].ne[1] : 1); \
+            (dst).data = f + data + T[i_].off; found_ = 1; \
+            if ((rows_) && ((dst).rows != (rows_) || (dst).cols != (cols_))) FAIL("tensor %s: bad shape", nm); \
+            if (data + T[i_].off + (size_t)(dst).rows * row_bytes((dst).type, (dst).cols) > sz) FAIL("tensor %s truncated", nm); } \
+        if (!found_) FAIL("tensor %s missing", nm); } while (0)
+    FIND("token_embd.weight", m->embd, 0, 0);
+    m->vocab = m->embd.rows;
+    int has_out = 0;
+    for (uint64_t i = 0; i < nt; i++) has_out |= T[i].nlen == 13 && !memcmp(T[i].name, "output.weight", 13);
+    if (has_out) FIND("output.weight", m->out, m->vocab, m->dim);
+    else m->out = m->embd;
+    OrMat nv;
+    FIND("output_norm.weight", nv, 0, 0);
+    m->final_norm = (const float *)nv.data;
+    int L = m->L, qd = m->nh * m->hd, kvd = m->nkv * m->hd;
+    m->wq = calloc(L, sizeof(OrMat)); m->wk = calloc(L, sizeof(OrMat)); m->wv = calloc(L, sizeof(OrMat));
+    m->wo = calloc(L, sizeof(OrMat)); m->w1 = calloc(L, sizeof(OrMat)); m->w2 = calloc(L, sizeof(OrMat));
+    m->w3 = calloc(L, sizeof(OrMat));
+    m->att_norm = calloc(L, sizeof(float *)); m->ffn_norm = calloc(L, sizeof(float *));
+    m->q_norm = calloc(L, sizeof(float *)); m->k_norm = calloc(L, sizeof(float *));
+    char nm[96];
+    for (int l = 0; l < L; l++) {
+        snprintf(nm, sizeof nm, "blk.%d.attn_q.weight", l); FIND(nm, m->wq[l], qd, m->dim);
+        snprintf(nm, sizeof nm, "blk.%d.attn_k.weight", l); FIND(nm, m->wk[l], kvd, m->dim);
+        snprintf(nm, sizeof nm, "blk.%d.attn_v.weight", l); FIND(nm, m->wv[l], kvd, m->dim);
+        snprintf(nm, sizeof nm, "blk.%d.attn_output.weight", l); FIND(nm, m->wo[l], m->dim, qd);
+        snprintf(nm, sizeof nm, "blk.%d.ffn_gate.weight", l); FIND(nm, m->w1[l], m->hidden, m->dim);
+        snprintf(nm, sizeof nm, "blk.%d.ffn_down.weight", l); FIND(nm, m->w2[l], m->dim, m->hidden);
+        snprintf(nm, sizeof nm, "blk.%d.ffn_up.weight", l); FIND(nm, m->w3[l], m->hidden, m->dim);
+        snprintf(nm, sizeof nm, "blk.%d.attn_norm.weight", l); FIND(nm, nv, 0, 0); m->att_norm[l] = (const float *)nv.data;
+        snprintf(nm, sizeof nm, "blk.%d.ffn_norm.weight", l); FIND(nm, nv, 0, 0); m->ffn_norm[l] = (const float *)nv.data;
+        snprintf(nm, sizeof nm, "blk.%d.attn_q_norm.weight", l); FIND(nm, nv, 0, 0); m->q_norm[l] = (const float *)nv.data;
+        snprintf(nm, sizeof nm, "blk.%d.attn_k_norm.weight", l); FIND(nm, nv, 0, 0); m->k_norm[l] = (const float *)nv.data;
+    }
+    free(T);
+    return m;
+fail:
+    free(T);
+    or_model_free(m);
+    return NULL;
+#undef FIND
+#undef FAIL
+}
+
+void or_model_free(OrModel *m) {
+    if (!m) return;
+    free(m->file);
+    free(m->wq); free(m->wk); free(m->wv); free(m->wo); free(m->w1); free(m->w2); free(m->w3);
+    free(m->att_norm); free(m->ffn_norm); free(m->q_norm); free(m->k_norm);
+    free(m);
+}
+
+void or_model_dims(const OrModel *m, int *d) {
+    d[0] = m->dim; d[1] = m->hidden; d[2] = m->L; d[3] = m->nh; d[4] = m->nkv; d[5] = m->hd; d[6] = m->vocab; d[7] = m->kv_len;
+}
+
+float or_model_att_scale(const OrModel *m) { return m->att_scale; }
+
+OrSeq *or_seq_new(const OrModel *m) {
+    OrSeq *s = calloc(1, sizeof(OrSeq));
+    size_t n = (size_t)m->L * m->kv_len * m->nkv * m->hd;
+    s->m = m;
+    s->kc = calloc(n, 2);
+    s->vc = calloc(n, 2);
+    if (!s->kc || !s->vc) { or_seq_free(s); return NULL; }
+    return s;
+}
+
+void or_seq_free(OrSeq *s) {
+    if (!s) return;
+    free(s->kc);
+    free(s->vc);
+    free(s);
+}
+
+int or_seq_len(const OrSeq *s) { return s->len; }
+void or_seq_truncate(OrSeq *s, int n) { if (n >= 0 && n <= s->len) s->len = n; }
+void or_seq_set_len(OrSeq *s, int n) { s->len = n; }
+
+void or_seq_copy(OrSeq *dst, const OrSeq *src, int n) {
+    size_t per = (size_t)src->m->kv_len * src->m->nkv * src->m->hd;
+    for (int l = 0; l < src->m->L; l++)
+        for (int t = 0; t < n; t++)
+            for (int h = 0; h < src->m->nkv; h++) {
+                size_t o = (size_t)l * per + or_kv_tile(t, h, src->m->nkv, src->m->hd);
+                int j = t % ATT_T, hd = src->m->hd;
+                for (int i = 0; i < hd; i++) {
+                    dst->kc[o + (size_t)i * ATT_T + j] = src->kc[o + (size_t)i * ATT_T + j];
+                    dst->vc[o + (size_t)j * hd + i] = src->vc[o + (size_t)j * hd + i];
+                }
+            }
+    dst->len = n;
+}
+
+const uint16_t *or_seq_cache(const OrSeq *s, int layer, int v) {
+    return (v ? s->vc : s->kc) + (size_t)layer * s->m->kv_len * s->m->nkv * s->m->hd;
+}
+uint16_t *or_seq_cache_mut(OrSeq *s, int layer, int v) {
+    return (v ? s->vc : s->kc) + (size_t)layer * s->m->kv_len * s->m->nkv * s->m->hd;
+}
+
+static void matvec(float *out, const OrMat *w, const int8_t *xq, const float *xs) {
+    /* matvec_rows (forward.c:983-1010) for one activation row: Q8_0 via dot_q8, K-quants via the definition */
+    if (w->type == T_Q8_0) {
+        int K = w->cols, G = K / 32;
+        int8_t *q = malloc((size_t)K);
+        float *s = malloc((size_t)G * sizeof(float));
+        for (int n = 0; n < w->rows; n++) {
+            or_q8_from_blocks(q, s, w->data + (size_t)n * G * 34, (size_t)G);
+            out[n] = or_dot_q8(q, s, xq, xs, K);
+        }
+        free(q);
+        free(s);
+    } else {
+        or_kq_matmul(w->type, out, w->data, xq, xs, 1, w->rows, w->cols);
+    }
+}
+
+static void embed(float *x, const OrMat *t, int token, int dim) {
+    /* embed_row (forward.c:839-881): Q8_0 x = (int8) q * d (one rounding), K-quants by kq_dequant_row */
+    if (t->type == T_Q8_0) {
+        const uint8_t *blk = t->data + (size_t)token * (dim / 32) * 34;
+        for (int g = 0; g < dim / 32; g++, blk += 34) {
+            float s = or_fp16_to_f32(u16(blk));
+            for (int i = 0; i < 32; i++) x[g * 32 + i] = (float)(int8_t)blk[2 + i] * s;
+        }
+    } else if (t->type == T_F32) {
+        memcpy(x, t->data + (size_t)token * dim * 4, (size_t)dim * 4);
+    } else {
+        or_kq_dequant_row(t->type, t->data + (size_t)token * row_bytes(t->type, dim), dim, x);
+    }
+}
+
+int or_forward_token(const OrModel *m, OrSeq *s, int token, float *logits, float *trace) {
+    /* decode_step + decode_worker (forward.c:2568-2813) for one row, the operations of each phase in order */
+    int dim = m->dim, hd = m->hd, nh = m->nh, nkv = m->nkv, kv_mul = nh / nkv, qd = nh * hd, kvd = nkv * hd;
+    int pos = s->len, H = m->hidden;
+    if (pos >= m->cap || token < 0 || token >= m->vocab) return -1;
+    int xsz = dim > qd ? dim : qd;
+    float *x = calloc(dim, 4), *xb = calloc(xsz, 4), *q = calloc(qd, 4), *k = calloc(kvd, 4), *v = calloc(kvd, 4);
+    float *hb = calloc(H, 4), *hb2 = calloc(H, 4), *cs = calloc(hd, 4), *att = calloc(qd, 4);
+    int8_t *xq = calloc(H > xsz ? H : xsz, 1);
+    float *xs = calloc((H > xsz ? H : xsz) / 32, 4);
+    embed(x, &m->embd, token, dim);
+    or_rope_row(cs, hd, pos, m->log_theta);
+    size_t per = (size_t)m->kv_len * kvd;
+    for (int l = 0; l < m->L; l++) {
+        or_rmsnorm(xb, x, m->att_norm[l], dim);
+        or_quantize(xq, xs, xb, dim);
+        matvec(q, &m->wq[l], xq, xs);
+        matvec(k, &m->wk[l], xq, xs);
+        matvec(v, &m->wv[l], xq, xs);
+        or_qk_norm_rope(q, nh, m->q_norm[l], hd, cs);
+        or_qk_norm_rope(k, nkv, m->k_norm[l], hd, cs);
+        uint16_t *kc = s->kc + (size_t)l * per, *vc = s->vc + (size_t)l * per;
+        for (int g = 0; g < nkv; g++) { /* kv_store (forward.c:1901-1951), f16 */
+            size_t o = or_kv_tile(pos, g, nkv, hd);
+            int j = pos % ATT_T;
+            for (int i = 0; i < hd; i++) {
+                kc[o + (size_t)i * ATT_T + j] = or_f32_f16(k[g * hd + i]);
+                vc[o + (size_t)j * hd + i] = or_f32_f16(v[g * hd + i]);
+            }
+        }
+        for (int h = 0; h < nh; h++)
+            or_attention(att + h * hd, q + h * hd, kc, vc, pos + 1, h / kv_mul, nkv, hd, m->att_scale);
+        or_quantize(xq, xs, att, qd);
+        matvec(xb, &m->wo[l], xq, xs);
+        for (int i = 0; i < dim; i++) x[i] += xb[i];
+        or_rmsnorm(xb, x, m->ffn_norm[l], dim);
+        or_quantize(xq, xs, xb, dim);
+        matvec(hb, &m->w1[l], xq, xs);
+        matvec(hb2, &m->w3[l], xq, xs);
+        or_swiglu(hb, hb2, H);
+        or_quantize(xq, xs, hb, H);
+        matvec(xb, &m->w2[l], xq, xs);
+        for (int i = 0; i < dim; i++) x[i] += xb[i];
+        if (trace) memcpy(trace + (size_t)l * dim, x, (size_t)dim * 4);
+    }
+    if (logits) {
+        or_rmsnorm(x, x, m->final_norm, dim);
+        or_quantize(xq, xs, x, dim);
+        matvec(logits, &m->out, xq, xs);
+    }
+    s->len = pos + 1;
+    free(x); free(xb); free(q); free(k); free(v); free(hb); free(hb2); free(cs); free(att); free(xq); free(xs);
+    return 0;
+}

@@ -1,0 +1,130 @@
+/* Driver of the reference's own CPU path (test infrastructure: compiled against the reference's runq.h and
+ * linked with its library objects by oracle/Makefile into oracle/_ref/ref_driver; never part of the product).
+ *
+ * It runs what the parity tests and the CPU baseline need, through the public API only (runq.h):
+ *   prefill of the ids in a file (rq_prefill, chunks of max_batch rows), then greedy decode steps (rq_decode +
+ *   rq_sample at temperature 0: sampler.c:40-60's first maximum), optionally writing every logits row it
+ *   produced (float32), the generated tokens (int32) and the KV cache of the sequence (rq_seq_save's file:
+ *   the blocks "as in memory", seqfile.c:8-27), and timing each phase (best of --reps runs).
+ *   --batch-decode N: N independent sequences, each prefilled with the same prompt, then --steps batched decode
+ *   passes of one row per sequence (rq_forward_batch, RQ_LOGITS_LAST each: batch_decode_worker).
+ * Output: one JSON line on stdout. */
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "runq.h"
+
+static void die(const char *what, int e, RqCtx *c) {
+    fprintf(stderr, "ref_driver: %s failed: %s%s%s\n", what, rq_strerror(e), c ? ": " : "", c ? rq_ctx_error(c) : "");
+    exit(1);
+}
+
+static int *read_ids(const char *path, int *n) {
+    FILE *f = fopen(path, "rb");
+    if (!f) { perror(path); exit(1); }
+    fseek(f, 0, SEEK_END);
+    long sz = ftell(f);
+    fseek(f, 0, SEEK_SET);
+    int *v = malloc(sz > 0 ? (size_t)sz : 4);
+    if (!v || fread(v, 1, (size_t)sz, f) != (size_t)sz) { perror(path); exit(1); }
+    fclose(f);
+    *n = (int)(sz / 4);
+    return v;
+}
+
+static void write_all(FILE *f, const void *p, size_t n) {
+    if (f && fwrite(p, 1, n, f) != n) { perror("write"); exit(1); }
+}
+
+int main(int argc, char **argv) {
+    const char *model = NULL, *ids_path = NULL, *logits_path = NULL, *tokens_path = NULL, *kv_path = NULL;
+    int threads = 0, cap = 0, maxb = 512, steps = 0, reps = 1, all_logits = 0, nbd = 0;
+    for (int i = 1; i < argc; i++) {
+        const char *a = argv[i], *v = i + 1 < argc ? argv[i + 1] : NULL;
+        if (!strcmp(a, "-m") && v) model = v, i++;
+        else if (!strcmp(a, "-t") && v) threads = atoi(v), i++;
+        else if (!strcmp(a, "-c") && v) cap = atoi(v), i++;
+        else if (!strcmp(a, "-b") && v) maxb = atoi(v), i++;
+        else if (!strcmp(a, "--ids") && v) ids_path = v, i++;
+        else if (!strcmp(a, "--steps") && v) steps = atoi(v), i++;
+        else if (!strcmp(a, "--reps") && v) reps = atoi(v), i++;
+        else if (!strcmp(a, "--logits") && v) logits_path = v, i++;
+        else if (!strcmp(a, "--tokens") && v) tokens_path = v, i++;
+        else if (!strcmp(a, "--kv") && v) kv_path = v, i++;
+        else if (!strcmp(a, "--batch-decode") && v) nbd = atoi(v), i++;
+        else if (!strcmp(a, "--all-logits")) all_logits = 1;
+        else { fprintf(stderr, "ref_driver: bad argument %s\n", a); return 2; }
+    }
+    if (!model || !ids_path) { fprintf(stderr, "usage: ref_driver -m MODEL --ids FILE [--steps K] ...\n"); return 2; }
+    const char *warn = rq_threads_init(threads);
+    if (warn) fprintf(stderr, "ref_driver: %s\n", warn);
+    char err[512];
+    RqModelOpts mo;
+    memset(&mo, 0, sizeof mo);
+    mo.no_tokenizer = 1;
+    mo.mem = -1;
+    mo.ctx_len = cap;
+    RqModel *m = rq_model_load(model, &mo, err, sizeof err);
+    if (!m) { fprintf(stderr, "ref_driver: load: %s\n", err); return 1; }
+    RqModelInfo info;
+    rq_model_info(m, &info);
+    int V = info.vocab_size, e, n;
+    int *ids = read_ids(ids_path, &n);
+    int ns = nbd > 0 ? nbd : 1;
+    if (nbd > 0 && maxb < ns) maxb = ns;
+    RqCtx *c = rq_ctx_new(m, maxb, cap, &e);
+    if (!c) die("rq_ctx_new", e, NULL);
+    RqSeq **sq = calloc((size_t)ns, sizeof(RqSeq *));
+    for (int i = 0; i < ns; i++)
+        if (!(sq[i] = rq_seq_new(m, cap, RQ_KV_F16, &e))) die("rq_seq_new", e, NULL);
+    FILE *lf = logits_path ? fopen(logits_path, "wb") : NULL, *tf = tokens_path ? fopen(tokens_path, "wb") : NULL;
+    if ((logits_path && !lf) || (tokens_path && !tf)) { perror("output"); return 1; }
+    float *out = malloc((size_t)(all_logits ? n : ns) * V * sizeof(float));
+    int *tok = malloc((size_t)ns * sizeof(int));
+    RqSegment *sg = malloc((size_t)ns * sizeof(RqSegment));
+    RqSampling smp = { 0 };
+    double tp_best = 1e30, td_best = 1e30;
+    for (int r = 0; r < reps; r++) {
+        int last = r == reps - 1; /* outputs of the last run only */
+        for (int i = 0; i < ns; i++) rq_seq_reset(sq[i]);
+        double t0 = rq_now();
+        float *lg = NULL;
+        for (int i = 0; i < ns; i++) {
+            if ((e = rq_prefill(c, sq[i], ids, n, all_logits ? RQ_LOGITS_ALL : RQ_LOGITS_LAST, all_logits ? out : NULL, &lg)) != RQ_OK)
+                die("rq_prefill", e, c);
+            if (last) write_all(lf, lg, (size_t)(all_logits ? n : 1) * V * sizeof(float));
+            tok[i] = rq_sample(c, sq[i], lg + (size_t)(all_logits ? n - 1 : 0) * V, &smp);
+        }
+        double t1 = rq_now();
+        for (int s = 0; s < steps; s++) {
+            if (last) write_all(tf, tok, (size_t)ns * sizeof(int));
+            if (nbd > 0) {
+                for (int i = 0; i < ns; i++) sg[i] = (RqSegment){ sq[i], &tok[i], 1, RQ_LOGITS_LAST, NULL, NULL };
+                if ((e = rq_forward_batch(c, sg, ns, out, NULL)) != RQ_OK) die("rq_forward_batch", e, c);
+                if (last) write_all(lf, out, (size_t)ns * V * sizeof(float));
+                for (int i = 0; i < ns; i++) tok[i] = rq_sample(c, sq[i], out + (size_t)i * V, &smp);
+            } else {
+                if ((e = rq_decode(c, sq[0], tok[0], &lg)) != RQ_OK) die("rq_decode", e, c);
+                if (last) write_all(lf, lg, (size_t)V * sizeof(float));
+                tok[0] = rq_sample(c, sq[0], lg, &smp);
+            }
+        }
+        double t2 = rq_now();
+        tp_best = t1 - t0 < tp_best ? t1 - t0 : tp_best;
+        td_best = t2 - t1 < td_best ? t2 - t1 : td_best;
+    }
+    if (kv_path && (e = rq_seq_save(sq[0], kv_path)) != RQ_OK) die("rq_seq_save", e, NULL);
+    if (lf) fclose(lf);
+    if (tf) fclose(tf);
+    printf("{\"threads\": %d, \"vocab\": %d, \"prompt\": %d, \"seqs\": %d, \"steps\": %d, \"prefill_s\": %.6f, "
+           "\"decode_s\": %.6f, \"prefill_tok_s\": %.3f, \"decode_tok_s\": %.3f}\n",
+           rq_threads(), V, n, ns, steps, tp_best, td_best, tp_best > 0 ? (double)n * ns / tp_best : 0.0,
+           td_best > 0 && steps ? (double)steps * ns / td_best : 0.0);
+    for (int i = 0; i < ns; i++) rq_seq_free(sq[i]);
+    rq_ctx_free(c);
+    rq_model_free(m);
+    free(ids); free(out); free(tok); free(sg); free(sq);
+    return 0;
+}
