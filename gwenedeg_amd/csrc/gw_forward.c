@@ -1,0 +1,514 @@
+/* The forward passes on the device: sequences (RqSeq: a KV cache in device memory), compute contexts (RqCtx: device
+ * activations, one HIP stream) and rq_decode / rq_prefill / rq_forward_batch (runq.h:222-375).
+ *
+ * One pass = n rows (each a token of some sequence at that sequence's next position) through every layer:
+ *   embed -> per layer: [residual +] rmsnorm + quantize -> q / k / v matmul -> QK-norm + RoPE + K / V store ->
+ *   attention partials per (row block, kv head, 256-position block) -> combine + quantize -> wo matmul ->
+ *   residual + rmsnorm + quantize -> w1 / w3 matmul -> SwiGLU + quantize -> w2 matmul
+ *   -> final residual + rmsnorm + quantize of the selected rows -> classifier -> logits to the host.
+ * The same kernels run every row whatever its batch-mates (decode is a one-row pass), and each output is computed
+ * whole in a fixed order, so a sequence's results do not depend on what it is batched with (runq.h:22-24).
+ * Errors: every argument is validated before any device work (forward.c:3775-3800), so a failed pass changes nothing;
+ * HIP failures come back as RQ_ERR_NOMEM / RQ_ERR_STATE with the text in rq_ctx_error.
+ */
+#define _GNU_SOURCE
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "gw_internal.h"
+
+#define HIPCHK(c, what, x) do { hipError_t e_ = (x); if (e_ != hipSuccess) return ctx_hip(c, what, e_); } while (0)
+
+static int ctx_fail(RqCtx *c, int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(c->err, sizeof(c->err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+static int ctx_hip(RqCtx *c, const char *what, hipError_t e) {
+    return gw_hip_fail(c->err, sizeof(c->err), what, e);
+}
+
+/* ---------------------------------------------------------------------------------------- sequences */
+
+static size_t seq_layer_elems(const RqSeq *s) { return (size_t)s->kv_len * s->m->n_kv_heads * s->m->head_dim; }
+
+RqSeq *rq_seq_new(const RqModel *m, int capacity, int kv_type, int *err) {
+    int e = RQ_OK;
+    RqSeq *s = NULL;
+    if (!m) { e = RQ_ERR_STATE; goto fail; }
+    if (capacity <= 0) capacity = m->seq_len;
+    if (capacity > m->seq_len || kv_type != RQ_KV_F16) { e = RQ_ERR_ARG; goto fail; }
+    s = calloc(1, sizeof(RqSeq));
+    if (!s) { e = RQ_ERR_NOMEM; goto fail; }
+    s->m = m;
+    s->cap = capacity;
+    s->kv_len = (capacity + GW_ATT_P - 1) / GW_ATT_P * GW_ATT_P;
+    size_t bytes = (size_t)m->n_layers * seq_layer_elems(s) * 2;
+    if (hipMalloc((void **)&s->kc, bytes) != hipSuccess || hipMalloc((void **)&s->vc, bytes) != hipSuccess) {
+        e = RQ_ERR_NOMEM;
+        goto fail;
+    }
+    s->tokens = malloc((size_t)capacity * sizeof(int));
+    if (!s->tokens) { e = RQ_ERR_NOMEM; goto fail; }
+    if (err) *err = RQ_OK;
+    return s;
+fail:
+    rq_seq_free(s);
+    if (err) *err = e;
+    return NULL;
+}
+
+void rq_seq_free(RqSeq *s) {
+    if (!s) return;
+    if (s->kc) hipFree(s->kc);
+    if (s->vc) hipFree(s->vc);
+    free(s->tokens);
+    free(s);
+}
+
+void rq_seq_reset(RqSeq *s) { s->len = 0; }
+
+int rq_seq_truncate(RqSeq *s, int n) {
+    if (n < 0 || n > s->len) return RQ_ERR_ARG;
+    s->len = n;
+    return RQ_OK;
+}
+
+int rq_seq_keep(const RqSeq *s, int n) { return n < 0 || n > s->len ? RQ_ERR_ARG : n; }
+int rq_seq_checkpoint_at(RqSeq *s, int pos) { (void)s; (void)pos; return RQ_OK; }
+int rq_seq_checkpoint_rows(RqSeq *s, int pos, int n) { (void)s; (void)pos; (void)n; return RQ_OK; }
+void rq_seq_checkpoint_rows_drop(RqSeq *s) { (void)s; }
+int rq_seq_set_checkpoints(RqSeq *s, int n) { (void)s; return n < 1 || n > 32 ? RQ_ERR_ARG : RQ_OK; }
+int rq_seq_checkpoints(const RqSeq *s, int *pos, int max) { (void)s; (void)pos; (void)max; return 0; }
+int rq_seq_len(const RqSeq *s) { return s->len; }
+int rq_seq_capacity(const RqSeq *s) { return s->cap; }
+const int *rq_seq_tokens(const RqSeq *s) { return s->tokens; }
+void rq_seq_seed(RqSeq *s, unsigned long long seed) { s->rng = seed; }
+unsigned long long *rq_seq_rng(RqSeq *s) { return &s->rng; }
+
+int rq_seq_common_prefix(const RqSeq *s, const int *tokens, int n) {
+    int L = 0;
+    while (L < s->len && L < n && s->tokens[L] == tokens[L]) L++;
+    return L;
+}
+
+int rq_seq_release(RqSeq *s, int keep) { return !s || keep < 0 ? RQ_ERR_ARG : RQ_OK; }
+
+size_t rq_seq_kv_bytes(const RqSeq *s, int n) {
+    n = n < 0 ? 0 : n > s->cap ? s->cap : n;
+    size_t nb = ((size_t)n + GW_ATT_P - 1) / GW_ATT_P;
+    return 2 * (size_t)s->m->n_layers * nb * GW_ATT_P * s->m->n_kv_heads * s->m->head_dim * 2 + (size_t)s->cap * sizeof(int);
+}
+
+int rq_seq_copy(RqSeq *dst, const RqSeq *src, int n) {
+    /* forward.c:553-576: dst := the first n positions of src (whole blocks below n, then the last block's tiles up to
+     * position n - 1 per kv head: the tiled layout of forward.c:1894-1899), device to device */
+    if (!dst || !src || dst == src || dst->m != src->m || n < 0 || n > src->len || n > dst->cap) return RQ_ERR_ARG;
+    const RqModel *m = src->m;
+    int nkv = m->n_kv_heads, hd = m->head_dim, full = n / GW_ATT_P, rem = n % GW_ATT_P;
+    size_t kvd = (size_t)nkv * hd, ntl = (size_t)(rem + GW_ATT_T - 1) / GW_ATT_T;
+    for (int l = 0; l < m->n_layers && n > 0; l++)
+        for (int kv = 0; kv < 2; kv++) {
+            const uint16_t *sb = (kv ? src->vc : src->kc) + (size_t)l * seq_layer_elems(src);
+            uint16_t *db = (kv ? dst->vc : dst->kc) + (size_t)l * seq_layer_elems(dst);
+            if (full && hipMemcpy(db, sb, (size_t)full * GW_ATT_P * kvd * 2, hipMemcpyDeviceToDevice) != hipSuccess)
+                return RQ_ERR_STATE;
+            for (int h = 0; h < nkv && rem; h++) {
+                size_t o = (((size_t)full * nkv + h) * GW_ATT_P) * hd;
+                if (hipMemcpy(db + o, sb + o, ntl * GW_ATT_T * hd * 2, hipMemcpyDeviceToDevice) != hipSuccess) return RQ_ERR_STATE;
+            }
+        }
+    memcpy(dst->tokens, src->tokens, (size_t)n * sizeof(int));
+    dst->len = n;
+    return RQ_OK;
+}
+
+int rq_seq_fill_synthetic(RqSeq *s, int n, unsigned long long seed) {
+    /* runq.h:721-726: n positions of pseudo-random K / V (|K| < 4, |V| < 1), arbitrary valid tokens */
+    if (!s || n < 1 || n > s->cap) return RQ_ERR_ARG;
+    size_t nb = ((size_t)n + GW_ATT_P - 1) / GW_ATT_P, per = nb * GW_ATT_P * s->m->n_kv_heads * s->m->head_dim;
+    for (int l = 0; l < s->m->n_layers; l++)
+        if (gw_k_fill_synthetic(s->kc + (size_t)l * seq_layer_elems(s), s->vc + (size_t)l * seq_layer_elems(s), per,
+                                seed + (unsigned long long)l * 0x1000193ull, 0))
+            return RQ_ERR_STATE;
+    if (hipDeviceSynchronize() != hipSuccess) return RQ_ERR_STATE;
+    for (int i = 0; i < n; i++) s->tokens[i] = (int)((seed + (unsigned long long)i * 7919u) % (unsigned long long)s->m->vocab);
+    s->len = n;
+    return RQ_OK;
+}
+
+/* ----------------------------------------------------------------------------------------- contexts */
+
+static void dfree(void *p) { if (p) hipFree(p); }
+
+void rq_ctx_free(RqCtx *c) {
+    if (!c) return;
+    void *d[] = { c->x, c->xb, c->qkv, c->hb, c->part, c->logits_d, c->hid_d, c->xq, c->hq, c->xs, c->hs, c->argmax_d, c->meta_d };
+    for (size_t i = 0; i < sizeof d / sizeof d[0]; i++) dfree(d[i]);
+    if (c->meta_h) hipHostFree(c->meta_h);
+    if (c->logits) hipHostFree(c->logits);
+    if (c->lg_h) hipHostFree(c->lg_h);
+    if (c->stream) hipStreamDestroy(c->stream);
+    free(c);
+}
+
+static int ctx_part(RqCtx *c, int rows, int nb) {
+    /* the attention partials buffer for rows x n_heads x nb blocks of (head_dim + 2) floats */
+    const RqModel *m = c->m;
+    size_t need = (size_t)rows * m->n_heads * nb * (m->head_dim + 2) * sizeof(float);
+    if (nb > c->att_nb || need > c->part_bytes) {
+        int nbn = nb > c->att_nb ? nb : c->att_nb;
+        int B = c->nb_max > 1 ? c->nb_max : 1;
+        size_t bytes = (size_t)B * m->n_heads * nbn * (m->head_dim + 2) * sizeof(float);
+        HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));
+        dfree(c->part);
+        c->part = NULL;
+        HIPCHK(c, "hipMalloc (attention partials)", hipMalloc((void **)&c->part, bytes));
+        c->part_bytes = bytes;
+        c->att_nb = nbn;
+    }
+    c->pstride = c->att_nb * (m->head_dim + 2);
+    return RQ_OK;
+}
+
+static int ctx_meta(RqCtx *c, size_t bytes) {
+    if (bytes <= c->meta_bytes) return RQ_OK;
+    HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));
+    dfree(c->meta_d);
+    if (c->meta_h) hipHostFree(c->meta_h);
+    c->meta_d = c->meta_h = NULL;
+    c->meta_bytes = 0;
+    size_t nb = bytes * 2;
+    HIPCHK(c, "hipMalloc (pass metadata)", hipMalloc(&c->meta_d, nb));
+    HIPCHK(c, "hipHostMalloc (pass metadata)", hipHostMalloc(&c->meta_h, nb, hipHostMallocDefault));
+    c->meta_bytes = nb;
+    return RQ_OK;
+}
+
+static int ctx_lg(RqCtx *c, size_t rows) {
+    if (rows <= c->lg_h_rows) return RQ_OK;
+    if (c->lg_h) hipHostFree(c->lg_h);
+    c->lg_h = NULL;
+    c->lg_h_rows = 0;
+    HIPCHK(c, "hipHostMalloc (logits)", hipHostMalloc((void **)&c->lg_h, rows * c->m->vocab * sizeof(float), hipHostMallocDefault));
+    c->lg_h_rows = rows;
+    return RQ_OK;
+}
+
+RqCtx *rq_ctx_new(const RqModel *m, int nb_max, int max_ctx, int *err) {
+    int e = RQ_ERR_NOMEM;
+    RqCtx *c = NULL;
+    if (!m) { e = RQ_ERR_STATE; goto fail; }
+    c = calloc(1, sizeof(RqCtx));
+    if (!c) goto fail;
+    c->m = m;
+    c->nb_max = nb_max < 0 ? 0 : nb_max > RQ_BATCH_MAX ? RQ_BATCH_MAX : nb_max;
+    int B = c->nb_max > 1 ? c->nb_max : 1;
+    int dim = m->dim, H = m->hidden, qd = m->n_heads * m->head_dim, kvd = m->n_kv_heads * m->head_dim;
+    c->kmax = dim > qd ? dim : qd;
+    c->kmax = H > c->kmax ? H : c->kmax;
+    c->ldqkv = qd + 2 * kvd;
+    if (hipStreamCreate(&c->stream) != hipSuccess) { e = RQ_ERR_STATE; goto fail; }
+#define DM(p, n) if (hipMalloc((void **)&(p), (size_t)(n)) != hipSuccess) goto fail
+    DM(c->x, (size_t)B * dim * 4);
+    DM(c->xb, (size_t)B * dim * 4);
+    DM(c->qkv, (size_t)B * c->ldqkv * 4);
+    DM(c->hb, (size_t)B * 2 * H * 4);
+    DM(c->xq, (size_t)B * c->kmax);
+    DM(c->xs, (size_t)B * (c->kmax / 32) * 4);
+    DM(c->hq, (size_t)B * H);
+    DM(c->hs, (size_t)B * (H / 32) * 4);
+    DM(c->logits_d, (size_t)B * m->vocab * 4);
+    DM(c->hid_d, (size_t)B * dim * 4);
+    DM(c->argmax_d, (size_t)B * 4);
+#undef DM
+    if (hipHostMalloc((void **)&c->logits, (size_t)m->vocab * 4, hipHostMallocDefault) != hipSuccess) goto fail;
+    if (max_ctx <= 0 || max_ctx > m->seq_len) max_ctx = m->seq_len;
+    if (ctx_part(c, B, (max_ctx + GW_ATT_P - 1) / GW_ATT_P) != RQ_OK) goto fail;
+    if (err) *err = RQ_OK;
+    return c;
+fail:
+    rq_ctx_free(c);
+    if (err) *err = e;
+    return NULL;
+}
+
+int rq_ctx_max_batch(const RqCtx *c) { return c->nb_max; }
+const char *rq_ctx_error(const RqCtx *c) { return c->err; }
+int rq_ctx_profile(const RqCtx *c, const char **names, double *seconds, int max) { (void)c; (void)names; (void)seconds; (void)max; return 0; }
+void *gw_ctx_stream(RqCtx *c) { return c->stream; }
+
+/* ------------------------------------------------------------------------------------------- passes */
+
+typedef struct { int x, y, z, w; } Item; /* attention work item: first row, rows, kv head, key block */
+
+typedef struct {
+    int n, nsel, want_hidden;
+    int tok[GW_RMAX], pos[GW_RMAX], sel[GW_RMAX];
+    RqSeq *seq[GW_RMAX];
+    float *hid[GW_RMAX];     /* per row: where its hidden state goes, or NULL */
+} Pass;
+
+static int run_mm(RqCtx *c, const GwMat *w, int nmat, const int8_t *xq, const float *xs, int ldx, int M, float *out, int ldo,
+                  int mode) {
+    for (int i = 0, col = 0; i < nmat; col += w[i].rows, i++)
+        if (gw_k_matmul(&w[i], xq, xs, ldx, M, out + col, ldo, mode, c->stream))
+            return ctx_fail(c, RQ_ERR_STATE, "matmul launch failed (%d x %d, type %d)", w[i].rows, w[i].cols, w[i].type);
+    return RQ_OK;
+}
+
+#define KCHK(x) do { if (x) return ctx_fail(c, RQ_ERR_STATE, "kernel launch failed: %s", #x); } while (0)
+
+static int fw_pass(RqCtx *c, Pass *P, float *out) {
+    /* the rows of P through the model (every validation done by the caller); out: nsel x vocab logits (host), or
+     * NULL with nsel == 0 */
+    const RqModel *m = c->m;
+    int n = P->n, L = m->n_layers, nh = m->n_heads, nkv = m->n_kv_heads, hd = m->head_dim, dim = m->dim, H = m->hidden;
+    int kv_mul = nh / nkv, rb = 32 / kv_mul > 0 ? 32 / kv_mul : 1, rc;
+    /* attention items: row blocks of <= rb consecutive rows of one sequence, per kv head and key block */
+    int nbmax = 1, nitems = 0;
+    for (int b = 0; b < n; b++) {
+        int nb = (P->pos[b] + 1 + GW_ATT_P - 1) / GW_ATT_P;
+        nbmax = nb > nbmax ? nb : nbmax;
+    }
+    if ((rc = ctx_part(c, n, nbmax)) != RQ_OK) return rc;
+    int nrb = 0;
+    for (int b = 0; b < n;) {
+        int e = b + 1;
+        while (e < n && e - b < rb && P->seq[e] == P->seq[b] && P->pos[e] == P->pos[e - 1] + 1) e++;
+        nitems += nkv * ((P->pos[e - 1] + 1 + GW_ATT_P - 1) / GW_ATT_P);
+        nrb++;
+        b = e;
+    }
+    /* metadata block: tok, pos, sel (int), kc / vc tables per layer (pointers), items */
+    size_t o_tok = 0, o_pos = o_tok + (size_t)n * 4, o_sel = o_pos + (size_t)n * 4, o_ptr = (o_sel + (size_t)n * 4 + 15) / 16 * 16;
+    size_t o_items = o_ptr + (size_t)2 * L * n * sizeof(void *), total = o_items + (size_t)nitems * sizeof(Item);
+    if ((rc = ctx_meta(c, total)) != RQ_OK) return rc;
+    HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream)); /* (the pinned block may still feed a copy) */
+    uint8_t *h = c->meta_h, *d = c->meta_d;
+    memcpy(h + o_tok, P->tok, (size_t)n * 4);
+    memcpy(h + o_pos, P->pos, (size_t)n * 4);
+    memcpy(h + o_sel, P->sel, (size_t)n * 4);
+    uint16_t **ptr = (uint16_t **)(h + o_ptr);
+    for (int l = 0; l < L; l++)
+        for (int b = 0; b < n; b++) {
+            size_t lo = (size_t)l * P->seq[b]->kv_len * nkv * hd;
+            ptr[(size_t)l * n + b] = P->seq[b]->kc + lo;
+            ptr[(size_t)(L + l) * n + b] = P->seq[b]->vc + lo;
+        }
+    Item *it = (Item *)(h + o_items);
+    for (int b = 0, k = 0; b < n;) {
+        int e = b + 1;
+        while (e < n && e - b < rb && P->seq[e] == P->seq[b] && P->pos[e] == P->pos[e - 1] + 1) e++;
+        int nb = (P->pos[e - 1] + 1 + GW_ATT_P - 1) / GW_ATT_P;
+        for (int g = 0; g < nkv; g++)
+            for (int kb = 0; kb < nb; kb++) it[k++] = (Item){ b, e - b, g, kb };
+        b = e;
+    }
+    HIPCHK(c, "hipMemcpyAsync (pass metadata)", hipMemcpyAsync(d, h, total, hipMemcpyHostToDevice, c->stream));
+    const int *tok_d = (const int *)(d + o_tok), *pos_d = (const int *)(d + o_pos), *sel_d = (const int *)(d + o_sel);
+    uint16_t *const *kc_d = (uint16_t *const *)(d + o_ptr), *const *vc_d = kc_d + (size_t)L * n;
+    const void *items_d = d + o_items;
+    hipStream_t s = c->stream;
+    int K = c->kmax;
+
+    if (m->embd.type == GW_Q8_0) KCHK(gw_k_embed_q8(c->x, dim, (const uint8_t *)m->embd.codes, m->embd.scales, tok_d, n, s));
+    else KCHK(gw_k_embed_kq(c->x, dim, m->embd.type, m->embd.blocks, tok_d, n, s));
+    for (int l = 0; l < L; l++) {
+        const GwLayer *y = &m->layer[l];
+        KCHK(gw_k_rmsnorm_quant(c->x, l ? c->xb : NULL, dim, y->att_norm, NULL, n, c->xq, c->xs, K, NULL, s));
+        if ((rc = run_mm(c, y->qkv, y->nqkv, c->xq, c->xs, K, n, c->qkv, c->ldqkv, 0)) != RQ_OK) return rc;
+        KCHK(gw_k_qknorm_rope_store(c->qkv, c->ldqkv, n, nh, nkv, hd, y->q_norm, y->k_norm, m->rope, pos_d,
+                                    kc_d + (size_t)l * n, vc_d + (size_t)l * n, s));
+        KCHK(gw_k_attn_part(items_d, nitems, c->qkv, c->ldqkv, nh, nkv, hd, m->att_scale, pos_d, kc_d + (size_t)l * n,
+                            vc_d + (size_t)l * n, c->part, c->pstride, s));
+        KCHK(gw_k_attn_combine_quant(c->part, c->pstride, nh, hd, pos_d, n, c->xq, c->xs, K, NULL, s));
+        if ((rc = run_mm(c, &y->wo, 1, c->xq, c->xs, K, n, c->xb, dim, 0)) != RQ_OK) return rc;
+        KCHK(gw_k_rmsnorm_quant(c->x, c->xb, dim, y->ffn_norm, NULL, n, c->xq, c->xs, K, NULL, s));
+        if ((rc = run_mm(c, y->w13, y->nw13, c->xq, c->xs, K, n, c->hb, 2 * H, 0)) != RQ_OK) return rc;
+        KCHK(gw_k_swiglu_quant(c->hb, H, n, c->hq, c->hs, s));
+        if ((rc = run_mm(c, &y->w2, 1, c->hq, c->hs, H, n, c->xb, dim, 0)) != RQ_OK) return rc;
+    }
+    int resid_done = 0;
+    if (P->want_hidden) { /* every row's final hidden state (the normed row), then the logits rows below */
+        KCHK(gw_k_rmsnorm_quant(c->x, c->xb, dim, m->final_norm, NULL, n, c->xq, c->xs, K, c->hid_d, s));
+        resid_done = 1;
+    }
+    if (P->nsel > 0) {
+        KCHK(gw_k_rmsnorm_quant(c->x, resid_done ? NULL : c->xb, dim, m->final_norm, sel_d, P->nsel, c->xq, c->xs, K, NULL, s));
+        if ((rc = run_mm(c, &m->cls, 1, c->xq, c->xs, K, P->nsel, c->logits_d, m->vocab, 0)) != RQ_OK) return rc;
+    }
+    if (P->want_hidden) {
+        HIPCHK(c, "hipStreamSynchronize (pass)", hipStreamSynchronize(s));
+        for (int b = 0; b < n; b++)
+            if (P->hid[b])
+                HIPCHK(c, "hipMemcpy (hidden)", hipMemcpy(P->hid[b], c->hid_d + (size_t)b * dim, (size_t)dim * 4, hipMemcpyDeviceToHost));
+    }
+    if (P->nsel > 0 && out) {
+        size_t bytes = (size_t)P->nsel * m->vocab * 4;
+        if (out == c->logits) {
+            HIPCHK(c, "hipMemcpyAsync (logits)", hipMemcpyAsync(out, c->logits_d, bytes, hipMemcpyDeviceToHost, s));
+            HIPCHK(c, "hipStreamSynchronize (pass)", hipStreamSynchronize(s));
+        } else {
+            if ((rc = ctx_lg(c, (size_t)P->nsel)) != RQ_OK) return rc;
+            HIPCHK(c, "hipMemcpyAsync (logits)", hipMemcpyAsync(c->lg_h, c->logits_d, bytes, hipMemcpyDeviceToHost, s));
+            HIPCHK(c, "hipStreamSynchronize (pass)", hipStreamSynchronize(s));
+            memcpy(out, c->lg_h, bytes);
+        }
+    } else {
+        HIPCHK(c, "hipStreamSynchronize (pass)", hipStreamSynchronize(s));
+    }
+    c->prof[0] = P->nsel; /* (rows with logits on the device: gw_ctx_argmax) */
+    return RQ_OK;
+}
+
+static int check_seq(RqCtx *c, const RqSeq *s) {
+    if (!s) return ctx_fail(c, RQ_ERR_ARG, "no sequence");
+    if (s->m != c->m) return ctx_fail(c, RQ_ERR_ARG, "sequence of another model");
+    return RQ_OK;
+}
+
+static int decode_one(RqCtx *c, RqSeq *s, int token, float *logits, float *hidden) {
+    static Pass P; /* (large: not on the stack; one pass at a time per process, as the reference's pool) */
+    P.n = 1;
+    P.tok[0] = token;
+    P.pos[0] = s->len;
+    P.seq[0] = s;
+    P.sel[0] = 0;
+    P.nsel = logits ? 1 : 0;
+    P.want_hidden = hidden != NULL;
+    P.hid[0] = hidden;
+    int rc = fw_pass(c, &P, logits);
+    if (rc != RQ_OK) return rc;
+    s->tokens[s->len] = token;
+    s->len++;
+    return RQ_OK;
+}
+
+int rq_decode(RqCtx *c, RqSeq *s, int token, float **logits) {
+    c->err[0] = 0;
+    int e = check_seq(c, s);
+    if (e != RQ_OK) return e;
+    if (token < 0 || token >= c->m->vocab) return ctx_fail(c, RQ_ERR_ARG, "token %d out of range", token);
+    if (s->len >= s->cap) return ctx_fail(c, RQ_ERR_CONTEXT, "sequence full (%d positions)", s->cap);
+    e = decode_one(c, s, token, logits ? c->logits : NULL, NULL);
+    if (logits) *logits = e == RQ_OK ? c->logits : NULL;
+    return e;
+}
+
+int rq_decode_hidden(RqCtx *c, RqSeq *s, int token, float **logits, float *hidden, const float *h_in) {
+    c->err[0] = 0;
+    if (logits) *logits = NULL;
+    int e = check_seq(c, s);
+    if (e != RQ_OK) return e;
+    if (h_in) return ctx_fail(c, RQ_ERR_ARG, "h_in on a model that is not an MTP view");
+    if (token < 0 || token >= c->m->vocab) return ctx_fail(c, RQ_ERR_ARG, "token %d out of range", token);
+    if (s->len >= s->cap) return ctx_fail(c, RQ_ERR_CONTEXT, "sequence full (%d positions)", s->cap);
+    e = decode_one(c, s, token, logits ? c->logits : NULL, hidden);
+    if (logits && e == RQ_OK) *logits = c->logits;
+    return e;
+}
+
+int rq_forward_batch(RqCtx *c, const RqSegment *sg, int nseg, float *out, float **logits) {
+    /* forward.c:3762-3878's contract: validation first, rows in segment order, selected rows' logits to out in row
+     * order (one selected row and out NULL: the context's buffer) */
+    static Pass P;
+    const RqModel *m = c->m;
+    int n = 0, nsel = 0, any_all = 0;
+    c->err[0] = 0;
+    if (logits) *logits = NULL;
+    if (c->nb_max <= 1) return ctx_fail(c, RQ_ERR_STATE, "context without batch buffers (max_batch %d)", c->nb_max);
+    if (nseg < 1 || nseg > c->nb_max) return ctx_fail(c, RQ_ERR_ARG, "bad segment count %d", nseg);
+    for (int i = 0; i < nseg; i++) {
+        RqSeq *s = sg[i].seq;
+        int e = check_seq(c, s);
+        if (e != RQ_OK) return e;
+        if (sg[i].n < 1 || n + sg[i].n > c->nb_max || sg[i].logits < RQ_LOGITS_NONE || sg[i].logits > RQ_LOGITS_ALL)
+            return ctx_fail(c, RQ_ERR_ARG, "rq_forward_batch: bad segment %d (n %d, %d rows so far, max_batch %d)", i, sg[i].n, n,
+                            c->nb_max);
+        if (s->len + sg[i].n > s->cap)
+            return ctx_fail(c, RQ_ERR_CONTEXT, "rq_forward_batch: %d tokens at position %d past the capacity %d", sg[i].n, s->len,
+                            s->cap);
+        for (int j = 0; j < i; j++)
+            if (sg[j].seq == s) return ctx_fail(c, RQ_ERR_ARG, "sequence in segments %d and %d", j, i);
+        for (int j = 0; j < sg[i].n; j++)
+            if (sg[i].tokens[j] < 0 || sg[i].tokens[j] >= m->vocab) return ctx_fail(c, RQ_ERR_ARG, "token %d out of range", sg[i].tokens[j]);
+        if (sg[i].h_in) return ctx_fail(c, RQ_ERR_ARG, "rq_forward_batch: segment %d: h_in on a model that is not an MTP view", i);
+        n += sg[i].n;
+        nsel += sg[i].logits == RQ_LOGITS_ALL ? sg[i].n : sg[i].logits == RQ_LOGITS_LAST;
+        any_all |= sg[i].logits == RQ_LOGITS_ALL;
+    }
+    int gemv = nsel == 1 && !any_all && !out;
+    if (nsel > 0 && !out && !gemv) return ctx_fail(c, RQ_ERR_ARG, "logits of %d rows need an output buffer", nsel);
+    if (gemv) out = c->logits;
+    P.n = n;
+    P.nsel = 0;
+    P.want_hidden = 0;
+    for (int i = 0, b = 0; i < nseg; i++)
+        for (int j = 0; j < sg[i].n; j++, b++) {
+            P.tok[b] = sg[i].tokens[j];
+            P.pos[b] = sg[i].seq->len + j;
+            P.seq[b] = sg[i].seq;
+            P.hid[b] = sg[i].hidden ? sg[i].hidden + (size_t)j * m->dim : NULL;
+            P.want_hidden |= sg[i].hidden != NULL;
+            if (sg[i].logits == RQ_LOGITS_ALL || (sg[i].logits == RQ_LOGITS_LAST && j == sg[i].n - 1)) P.sel[P.nsel++] = b;
+        }
+    int e = fw_pass(c, &P, nsel ? out : NULL);
+    if (e != RQ_OK) return e;
+    for (int i = 0; i < nseg; i++) {
+        RqSeq *s = sg[i].seq;
+        memcpy(s->tokens + s->len, sg[i].tokens, (size_t)sg[i].n * sizeof(int));
+        s->len += sg[i].n;
+    }
+    if (logits) *logits = nsel ? out : NULL;
+    return RQ_OK;
+}
+
+int rq_prefill(RqCtx *c, RqSeq *s, const int *tokens, int n, int mode, float *out, float **logits) {
+    /* fw_rows (forward.c:3880-3916): chunks of max_batch rows, or token by token through the decode path */
+    int V = c->m->vocab, e = check_seq(c, s);
+    c->err[0] = 0;
+    if (logits) *logits = NULL;
+    if (e != RQ_OK) return e;
+    if (n < 1 || mode < RQ_LOGITS_NONE || mode > RQ_LOGITS_ALL || (mode == RQ_LOGITS_ALL && !out))
+        return ctx_fail(c, RQ_ERR_ARG, "bad prefill arguments (n %d, mode %d)", n, mode);
+    if (s->len + n > s->cap) return ctx_fail(c, RQ_ERR_CONTEXT, "%d tokens at position %d: past the capacity %d", n, s->len, s->cap);
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= V) return ctx_fail(c, RQ_ERR_ARG, "token %d out of range", tokens[i]);
+    float *lg = NULL;
+    if (c->nb_max <= 1) {
+        for (int i = 0; i < n && e == RQ_OK; i++) {
+            int want = mode == RQ_LOGITS_ALL || (mode == RQ_LOGITS_LAST && i == n - 1);
+            e = decode_one(c, s, tokens[i], want ? c->logits : NULL, NULL);
+            if (mode == RQ_LOGITS_ALL && e == RQ_OK) memcpy(out + (size_t)i * V, c->logits, (size_t)V * sizeof(float));
+        }
+        lg = mode == RQ_LOGITS_ALL ? out : mode == RQ_LOGITS_LAST ? c->logits : NULL;
+    } else {
+        int nb = c->nb_max;
+        for (int i = 0; i < n && e == RQ_OK; i += nb) {
+            int k = n - i < nb ? n - i : nb;
+            RqSegment sg = { s, tokens + i, k,
+                             mode == RQ_LOGITS_ALL ? RQ_LOGITS_ALL : mode == RQ_LOGITS_LAST && i + k == n ? RQ_LOGITS_LAST : RQ_LOGITS_NONE,
+                             NULL, NULL };
+            e = rq_forward_batch(c, &sg, 1, mode == RQ_LOGITS_ALL ? out + (size_t)i * V : NULL, &lg);
+        }
+        lg = mode == RQ_LOGITS_ALL ? out : lg;
+    }
+    if (logits && e == RQ_OK) *logits = lg;
+    return e;
+}
+
+int gw_ctx_argmax(RqCtx *c, int *tokens, int n) {
+    int rows = (int)c->prof[0];
+    if (rows <= 0 || n < 1 || n > rows) return ctx_fail(c, RQ_ERR_STATE, "no logits rows on the device (%d)", rows);
+    if (gw_k_argmax(c->logits_d, c->m->vocab, c->m->vocab, n, c->argmax_d, c->stream))
+        return ctx_fail(c, RQ_ERR_STATE, "argmax launch failed");
+    HIPCHK(c, "hipMemcpyAsync (argmax)", hipMemcpyAsync(tokens, c->argmax_d, (size_t)n * 4, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, "hipStreamSynchronize (argmax)", hipStreamSynchronize(c->stream));
+    return RQ_OK;
+}

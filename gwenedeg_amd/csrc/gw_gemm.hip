@@ -1,0 +1,253 @@
+// The matmul dispatch of the forward passes (gw_k_matmul), the load-time repack, and the isolated Q8_0 / K-quant
+// operator of the public ABI (gw_q8_*, gw_kq_matmul, gw_quantize).
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "gw_internal.h"
+
+// GGUF Q8_0 blocks (fp16 d, 32 int8; 34 bytes) -> codes (32 per block) + fp16 scales: the device layout
+__global__ __launch_bounds__(256) void k_q8_unpack(const uint8_t *__restrict__ blk, size_t nblk, int8_t *__restrict__ codes,
+                                                   uint16_t *__restrict__ scales) {
+    size_t b = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (b >= nblk) return;
+    const uint8_t *p = blk + b * 34;
+    scales[b] = (uint16_t)(p[0] | p[1] << 8);
+    uint32_t w[8];
+    #pragma unroll
+    for (int i = 0; i < 8; i++)
+        w[i] = (uint32_t)p[2 + 4 * i] | (uint32_t)p[3 + 4 * i] << 8 | (uint32_t)p[4 + 4 * i] << 16 | (uint32_t)p[5 + 4 * i] << 24;
+    uint4 *d = (uint4 *)(codes + b * 32);
+    d[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    d[1] = make_uint4(w[4], w[5], w[6], w[7]);
+}
+
+// exact int32 group sums, one thread per (m, n, g)
+__global__ __launch_bounds__(256) void k_q8_block_sums(int32_t *__restrict__ isum, const int8_t *__restrict__ W, int N, int K,
+                                                       const int8_t *__restrict__ X, int M) {
+    size_t G = K / 32, i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)M * N * G) return;
+    size_t g = i % G, n = i / G % N, m = i / G / N;
+    const int *w = (const int *)(W + n * K + g * 32), *x = (const int *)(X + m * K + g * 32);
+    int s = 0;
+    #pragma unroll
+    for (int k = 0; k < 8; k++) s = __builtin_amdgcn_sdot4(w[k], x[k], s, false);
+    isum[i] = s;
+}
+
+// pseudo-random f16 K (|K| < 4) and V (|V| < 1) values, for timing runs (rq_seq_fill_synthetic)
+__global__ __launch_bounds__(256) void k_fill_synthetic(uint16_t *kc, uint16_t *vc, size_t n, unsigned long long seed) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    unsigned long long z = seed + i * 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    z ^= z >> 31;
+    float a = (float)(z & 0xffffff) * (1.0f / 16777216.0f), b = (float)((z >> 24) & 0xffffff) * (1.0f / 16777216.0f);
+    kc[i] = __half_as_ushort(__float2half((2.0f * a - 1.0f) * 3.9f));
+    vc[i] = __half_as_ushort(__float2half((2.0f * b - 1.0f) * 0.99f));
+}
+
+// --------------------------------------------------------------------------------------------- K-quants
+
+// the per-group term of the K-quant fold (kquants.h:86-109) for weight row `row` (its blocks at rb) and group g:
+//   Q4_K: a - b, a = (ds * xs) * (float) isum, b = dm * xf, ds = d * sc_j, dm = dmin * m_j (sub-block j = g % 8)
+//   Q6_K: (d * xs) * (float) I, I = sc_j0 * t_j0 + sc_j1 * t_j1, t_j = sum q * xq - 32 * sum xq over 16 values
+template <int TYPE>
+__device__ __forceinline__ float kq_term(const uint8_t *__restrict__ rb, int g, const int8_t *__restrict__ x, float xsg, float xfg) {
+    int s = g >> 3, j = g & 7;
+    if (TYPE == GW_Q4_K) {
+        const uint8_t *b = rb + (size_t)s * 144;
+        const uint8_t *sc = b + 4;
+        int scj, mj;
+        if (j < 4) {
+            scj = sc[j] & 63;
+            mj = sc[j + 4] & 63;
+        } else {
+            scj = (sc[j + 4] & 15) | (sc[j - 4] >> 6) << 4;
+            mj = (sc[j + 4] >> 4) | (sc[j] >> 6) << 4;
+        }
+        const uint8_t *qs = b + 16 + 32 * (j >> 1);
+        int sh = 4 * (j & 1), isum = 0;
+        #pragma unroll
+        for (int l = 0; l < 32; l++) isum += ((qs[l] >> sh) & 15) * (int)x[l];
+        float d = __half2float(__ushort_as_half((uint16_t)(b[0] | b[1] << 8)));
+        float dmin = __half2float(__ushort_as_half((uint16_t)(b[2] | b[3] << 8)));
+        float ds = d * (float)scj, dm = dmin * (float)mj;
+        float a = (ds * xsg) * (float)isum;
+        float bb = dm * xfg;
+        return a - bb;
+    } else {
+        const uint8_t *b = rb + (size_t)s * 210;
+        int n = j >> 2, p = j & 3, I = 0;
+        #pragma unroll
+        for (int h = 0; h < 2; h++) {
+            int t = 0, xsum = 0;
+            #pragma unroll
+            for (int l0 = 0; l0 < 16; l0++) {
+                int l = 16 * h + l0;
+                int lo = (b[64 * n + 32 * (p & 1) + l] >> (4 * (p >> 1))) & 15;
+                int hi = (b[128 + 32 * n + l] >> (2 * p)) & 3;
+                t += (lo | hi << 4) * (int)x[l];
+                xsum += x[l];
+            }
+            I += (int)(int8_t)b[192 + 2 * j + h] * (t - 32 * xsum);
+        }
+        float d = __half2float(__ushort_as_half((uint16_t)(b[208] | b[209] << 8)));
+        return (d * xsg) * (float)I;
+    }
+}
+
+// out[m * ldo + row] = W row . X row m for the K-quant blocks (row-major: K / 256 blocks per row), R rows per block:
+// each thread takes groups g = t, t + 256, ... of every row, its term into LDS; one lane per (m, row) folds in order
+template <int TYPE, int M, int R>
+__global__ __launch_bounds__(256) void k_gemv_kq(const uint8_t *__restrict__ W, int nrows, int K, const int8_t *__restrict__ xq,
+                                                 const float *__restrict__ xs, int ldx, float *out, int ldo, int mode) {
+    extern __shared__ float P[];
+    const int G = K >> 5, PS = G + 1, row0 = blockIdx.x * R, t = threadIdx.x;
+    const size_t rowb = (size_t)(K / 256) * (TYPE == GW_Q4_K ? 144 : 210);
+    for (int g = t; g < G; g += 256) {
+        #pragma unroll
+        for (int m = 0; m < M; m++) {
+            const int8_t *x = xq + (size_t)m * ldx + 32 * g;
+            float xsg = xs[(size_t)m * (ldx >> 5) + g], xfg = 0.0f;
+            if (TYPE == GW_Q4_K) {
+                int sum = 0;
+                #pragma unroll
+                for (int l = 0; l < 32; l++) sum += x[l];
+                xfg = xsg * (float)sum; // kq_act_prep (kquants.h:392-400)
+            }
+            #pragma unroll
+            for (int r = 0; r < R; r++) {
+                int row = row0 + r < nrows ? row0 + r : nrows - 1;
+                P[(m * R + r) * PS + g] = kq_term<TYPE>(W + (size_t)row * rowb, g, x, xsg, xfg);
+            }
+        }
+    }
+    __syncthreads();
+    if (t < M * R) {
+        int m = t / R, r = t % R, row = row0 + r;
+        if (row < nrows) {
+            const float *p = P + t * PS;
+            float v = 0.0f;
+            for (int g = 0; g < G; g++) v = v + p[g];
+            float *o = out + (size_t)m * ldo + row;
+            *o = mode == 1 ? *o + v : v;
+        }
+    }
+}
+
+// x[b] = row tok[b] of a K-quant table, dequantized (kq_dequant_row, kquants.h:222-251; every value one rounding
+// of an exact expression)
+__global__ __launch_bounds__(256) void k_embed_kq(float *__restrict__ x, int dim, int type, const uint8_t *__restrict__ W,
+                                                  const int *__restrict__ tok) {
+    int bidx = blockIdx.x;
+    size_t rowb = (size_t)(dim / 256) * (type == GW_Q4_K ? 144 : 210);
+    const uint8_t *rb = W + (size_t)tok[bidx] * rowb;
+    for (int i = threadIdx.x; i < dim; i += blockDim.x) {
+        int s = i >> 8, k = i & 255;
+        float y;
+        if (type == GW_Q4_K) {
+            const uint8_t *b = rb + (size_t)s * 144, *sc = b + 4;
+            int j = k >> 5, scj, mj;
+            if (j < 4) { scj = sc[j] & 63; mj = sc[j + 4] & 63; }
+            else { scj = (sc[j + 4] & 15) | (sc[j - 4] >> 6) << 4; mj = (sc[j + 4] >> 4) | (sc[j] >> 6) << 4; }
+            float d = __half2float(__ushort_as_half((uint16_t)(b[0] | b[1] << 8)));
+            float dmin = __half2float(__ushort_as_half((uint16_t)(b[2] | b[3] << 8)));
+            int q = (b[16 + 32 * (k / 64) + k % 32] >> (4 * (k / 32 % 2))) & 15;
+            float d1 = d * (float)scj, m1 = dmin * (float)mj;
+            y = d1 * (float)q - m1;
+        } else {
+            const uint8_t *b = rb + (size_t)s * 210;
+            int n = k / 128, p = k / 32 % 4, l = k % 32;
+            int q = ((b[64 * n + 32 * (p & 1) + l] >> (4 * (p >> 1))) & 15) | ((b[128 + 32 * n + l] >> (2 * p)) & 3) << 4;
+            float d = __half2float(__ushort_as_half((uint16_t)(b[208] | b[209] << 8)));
+            y = (d * (float)(int8_t)b[192 + k / 16]) * (float)(q - 32);
+        }
+        x[(size_t)bidx * dim + i] = y;
+    }
+}
+
+template <int TYPE>
+static int launch_gemv_kq(const uint8_t *W, int nrows, int K, const int8_t *xq, const float *xs, int ldx, int M, float *out,
+                          int ldo, int mode, hipStream_t s) {
+    const int R = 4;
+    size_t lds = (size_t)4 * R * (K / 32 + 1) * sizeof(float);
+    for (int m0 = 0; m0 < M; m0 += 4) {
+        int mm = M - m0 < 4 ? M - m0 : 4;
+        dim3 grid((nrows + R - 1) / R);
+        const int8_t *x = xq + (size_t)m0 * ldx;
+        const float *xsc = xs + (size_t)m0 * (ldx / 32);
+        float *o = out + (size_t)m0 * ldo;
+        switch (mm) {
+        case 1: hipLaunchKernelGGL((k_gemv_kq<TYPE, 1, R>), grid, dim3(256), lds, s, W, nrows, K, x, xsc, ldx, o, ldo, mode); break;
+        case 2: hipLaunchKernelGGL((k_gemv_kq<TYPE, 2, R>), grid, dim3(256), lds, s, W, nrows, K, x, xsc, ldx, o, ldo, mode); break;
+        case 3: hipLaunchKernelGGL((k_gemv_kq<TYPE, 3, R>), grid, dim3(256), lds, s, W, nrows, K, x, xsc, ldx, o, ldo, mode); break;
+        default: hipLaunchKernelGGL((k_gemv_kq<TYPE, 4, R>), grid, dim3(256), lds, s, W, nrows, K, x, xsc, ldx, o, ldo, mode); break;
+        }
+    }
+    return (int)hipGetLastError();
+}
+
+extern "C" {
+
+int gw_k_embed_kq(float *x, int dim, int type, const uint8_t *blocks, const int *tok, int n, hipStream_t s) {
+    hipLaunchKernelGGL(k_embed_kq, dim3(n), dim3(256), 0, s, x, dim, type, blocks, tok);
+    return (int)hipGetLastError();
+}
+
+int gw_k_q8_unpack(const uint8_t *blocks, size_t nblk, int8_t *codes, uint16_t *scales, hipStream_t s) {
+    if (!nblk) return 0;
+    hipLaunchKernelGGL(k_q8_unpack, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, s, blocks, nblk, codes, scales);
+    return (int)hipGetLastError();
+}
+
+int gw_k_fill_synthetic(uint16_t *kc, uint16_t *vc, size_t n, unsigned long long seed, hipStream_t s) {
+    if (!n) return 0;
+    hipLaunchKernelGGL(k_fill_synthetic, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, kc, vc, n, seed);
+    return (int)hipGetLastError();
+}
+
+int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int M, float *out, int ldo, int mode, hipStream_t s) {
+    if (w->type == GW_Q8_0)
+        return gw_k_gemv_q8(w->codes, w->scales, w->rows, w->cols, xq, xs, ldx, M, out, ldo, mode, s);
+    if (w->type == GW_Q4_K)
+        return launch_gemv_kq<GW_Q4_K>(w->blocks, w->rows, w->cols, xq, xs, ldx, M, out, ldo, mode, s);
+    if (w->type == GW_Q6_K)
+        return launch_gemv_kq<GW_Q6_K>(w->blocks, w->rows, w->cols, xq, xs, ldx, M, out, ldo, mode, s);
+    return (int)hipErrorInvalidValue;
+}
+
+int gw_q8_pack(const void *blocks, int N, int K, int8_t *codes, uint16_t *scales, void *stream) {
+    if (N <= 0 || K <= 0 || K % 32 || !blocks || !codes || !scales) return RQ_ERR_ARG;
+    return gw_k_q8_unpack((const uint8_t *)blocks, (size_t)N * (K / 32), codes, scales, (hipStream_t)stream) ? RQ_ERR_STATE : RQ_OK;
+}
+
+int gw_quantize(const float *x, int M, int K, int8_t *xq, float *xs, void *stream) {
+    if (M <= 0 || K <= 0 || K % 32 || !x || !xq || !xs) return RQ_ERR_ARG;
+    return gw_k_quant_rows(x, K, K, M, xq, xs, K, (hipStream_t)stream) ? RQ_ERR_STATE : RQ_OK;
+}
+
+int gw_q8_matmul(float *out, const int8_t *codes, const uint16_t *scales, int N, int K, const int8_t *xq, const float *xs,
+                 int M, void *stream) {
+    if (N <= 0 || K <= 0 || M <= 0 || N % 16 || K % 32 || !out || !codes || !scales || !xq || !xs) return RQ_ERR_ARG;
+    GwMat w = { GW_Q8_0, N, K, (int8_t *)codes, (uint16_t *)scales, NULL };
+    return gw_k_matmul(&w, xq, xs, K, M, out, N, 0, (hipStream_t)stream) ? RQ_ERR_STATE : RQ_OK;
+}
+
+int gw_q8_block_sums(int32_t *isum, const int8_t *codes, int N, int K, const int8_t *xq, int M, void *stream) {
+    if (N <= 0 || K <= 0 || M <= 0 || K % 32 || !isum || !codes || !xq) return RQ_ERR_ARG;
+    size_t tot = (size_t)M * N * (K / 32);
+    hipLaunchKernelGGL(k_q8_block_sums, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, (hipStream_t)stream, isum, codes, N,
+                       K, xq, M);
+    return hipGetLastError() ? RQ_ERR_STATE : RQ_OK;
+}
+
+int gw_kq_matmul(float *out, int type, const void *blocks, int N, int K, const int8_t *xq, const float *xs, int M, void *stream) {
+    if (N <= 0 || K <= 0 || M <= 0 || K % 256 || (type != GW_Q4_K && type != GW_Q6_K) || !out || !blocks || !xq || !xs)
+        return RQ_ERR_ARG;
+    GwMat w = { type, N, K, NULL, NULL, (uint8_t *)blocks };
+    return gw_k_matmul(&w, xq, xs, K, M, out, N, 0, (hipStream_t)stream) ? RQ_ERR_STATE : RQ_OK;
+}
+
+} // extern "C"

@@ -1,0 +1,117 @@
+/* Internal declarations of the MI355X backend: the model / sequence / context objects behind the rq_* API and the
+ * C-ABI launchers of the gfx950 kernels (gw_kernels.hip, gw_gemm.hip). */
+#ifndef GW_INTERNAL_H
+#define GW_INTERNAL_H
+
+#ifndef __HIP_PLATFORM_AMD__
+#define __HIP_PLATFORM_AMD__
+#endif
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "gwenedeg_gpu.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { GW_F32 = 0, GW_Q8_0 = 8, GW_Q4_K = 12, GW_Q6_K = 14 }; /* ggml type numbers */
+
+#define GW_ATT_T 16   /* positions per KV cache tile */
+#define GW_ATT_P 256  /* positions per attention block */
+#define GW_RMAX 512   /* rows per pass (RQ_BATCH_MAX) */
+
+/* A weight matrix on the device (rows x cols). Q8_0: int8 codes, row-major, and fp16 scales (cols / 32 per row),
+ * the file's bytes split (34 bytes per 32 weights, as the file). K-quants: the file's blocks, row-major */
+typedef struct {
+    int type, rows, cols;
+    int8_t *codes;
+    uint16_t *scales;
+    uint8_t *blocks;
+} GwMat;
+
+typedef struct {
+    GwMat qkv[3];  /* Q8_0 model: qkv[0] = [wq | wk | wv] rows fused; K-quants: wq, wk, wv (types may differ) */
+    int nqkv;
+    GwMat wo;
+    GwMat w13[2];  /* Q8_0: w13[0] = [w1 | w3] fused; K-quants: w1, w3 */
+    int nw13;
+    GwMat w2;
+    float *att_norm, *ffn_norm, *q_norm, *k_norm; /* device */
+} GwLayer;
+
+struct RqModel {
+    int dim, hidden, n_layers, n_heads, n_kv_heads, head_dim, vocab, seq_len, ctx_max, tied;
+    float rope_theta, log_theta, att_scale;
+    unsigned long long fingerprint;
+    GwMat embd, cls;
+    GwLayer *layer;
+    float *final_norm;
+    float *rope;       /* device: seq_len rows of head_dim floats (cos | sin) */
+    float *norms;      /* the one allocation the norms live in */
+    size_t dev_bytes;  /* device memory held by the weights */
+    int kq;            /* a K-quant matrix present */
+    int device;
+};
+
+struct RqSeq {
+    const RqModel *m;
+    int cap, kv_len, len, hwm;
+    uint16_t *kc, *vc; /* device: n_layers x kv_len x kv_dim f16 each */
+    int *tokens;       /* host */
+    unsigned long long rng;
+};
+
+struct RqCtx {
+    const RqModel *m;
+    int nb_max, att_nb;
+    hipStream_t stream;
+    /* device activations, nb_max rows */
+    float *x, *xb, *qkv, *hb, *part, *logits_d, *hid_d;
+    int8_t *xq, *hq;
+    float *xs, *hs;
+    int *argmax_d;
+    int kmax, ldqkv, pstride;
+    size_t part_bytes;
+    /* per-pass row metadata: one device block, filled from one pinned host block */
+    void *meta_d, *meta_h;
+    size_t meta_bytes;
+    float *logits;     /* host: vocab floats (rq_decode's buffer) */
+    float *lg_h;       /* pinned host staging of logits rows */
+    size_t lg_h_rows;
+    char err[256];
+    double prof[8];
+};
+
+/* model / device helpers (gw_model.c) */
+int gw_device_init(char *err, size_t errlen);
+int gw_hip_fail(char *err, size_t errlen, const char *what, hipError_t e);
+
+/* kernels (gw_kernels.hip) */
+int gw_k_embed_q8(float *x, int dim, const uint8_t *codes, const uint16_t *scales, const int *tok, int n, hipStream_t s);
+int gw_k_embed_kq(float *x, int dim, int type, const uint8_t *blocks, const int *tok, int n, hipStream_t s);
+int gw_k_rmsnorm_quant(float *x, const float *d, int dim, const float *w, const int *sel, int n, int8_t *xq, float *xs,
+                       int ldq, float *hid, hipStream_t s);
+int gw_k_gemv_q8(const int8_t *W, const uint16_t *WS, int nrows, int K, const int8_t *xq, const float *xs, int ldx, int M,
+                 float *out, int ldo, int mode, hipStream_t s);
+int gw_k_qknorm_rope_store(float *qkv, int ldqkv, int n, int nh, int nkv, int hd, const float *qn, const float *kn,
+                           const float *rope, const int *pos, uint16_t *const *kc, uint16_t *const *vc, hipStream_t s);
+int gw_k_attn_part(const void *items, int nitems, const float *qkv, int ldqkv, int nh, int nkv, int hd, float scale,
+                   const int *pos, uint16_t *const *kc, uint16_t *const *vc, float *part, int pstride, hipStream_t s);
+int gw_k_attn_combine_quant(const float *part, int pstride, int nh, int hd, const int *pos, int n, int8_t *aq, float *as,
+                            int ldq, float *att_out, hipStream_t s);
+int gw_k_swiglu_quant(const float *hb, int H, int n, int8_t *hq, float *hs, hipStream_t s);
+int gw_k_quant_rows(const float *x, int n, int ldxf, int rows, int8_t *q, float *sc, int ldq, hipStream_t s);
+int gw_k_argmax(const float *lg, int n, int ld, int rows, int *out, hipStream_t s);
+int gw_k_q8_unpack(const uint8_t *blocks, size_t nblk, int8_t *codes, uint16_t *scales, hipStream_t s);
+int gw_k_fill_synthetic(uint16_t *kc, uint16_t *vc, size_t n, unsigned long long seed, hipStream_t s);
+
+/* the matmul dispatch (gw_gemm.hip): out[m * ldo + row] (+)= W row . X row m for M rows, any supported type */
+int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int M, float *out, int ldo, int mode,
+                hipStream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

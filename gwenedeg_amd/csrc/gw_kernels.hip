@@ -1,0 +1,556 @@
+// gfx950 kernels of the forward hot path (decode GEMV, attention, norms, RoPE, SwiGLU, quantization) and their C-ABI
+// launchers (gw_k_*: plain device pointers, sizes and a stream; declared in gw_internal.h).
+//
+// The arithmetic of every kernel is the reference's definition, operation for operation, so that results are
+// bit-identical to the oracle's restatement of it (IEEE fp32, -ffp-contract=off: an FMA only where written):
+//   quantize     forward.c:803-836       s = wmax * (1/127), inv = 127 / wmax, q = trunc(x * inv + copysign(0.49999997))
+//   Q8_0 fold    forward.c:906-916,      exact int32 sum per group of 32; val = val + (ws * xs) * (float) isum, groups in
+//                kernels_avx512.h:157    order (one lane folds one output)
+//   rmsnorm      forward.c:886-901       16 fma chains (lane j: x[j], x[j+16], ...), the tree +8 +4 +2 +1,
+//                                        t = fma(ss, 1/n, 1e-6), scale = 1 / sqrt(t), o = (w * x) * scale
+//   RoPE         forward.c:1266-1284     x' = fma(x, c, -(y s)), y' = fma(x, s, y c); cos / sin from the host's table
+//   attention    kernels_avx512.h:1109   per 256-position block: scores as 4 chunk fma chains of 32 dims added in order,
+//                forward.c:1346-1431     times scale; m = max; e = exp_att(s - m); l = 16 lane chains + tree; o = fma
+//                                        chain over positions in order; blocks combined in order (att_combine)
+//   f16 KV       forward.c:1325-1344,    f32_f16's rounding; K transposed in 16-position tiles, V row-major
+//                :1894-1951
+//   SwiGLU       forward.c:1953-1958     (h * h2) * (1 / (1 + e)), e = exp_att-style exp of min(-h, 80)
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "gw_internal.h"
+
+#define ATT_T 16
+#define ATT_P 256
+
+// ------------------------------------------------------------------------------------------- helpers
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    // IEEE half -> float (exact; v_cvt_f32_f16)
+    return __half2float(__ushort_as_half(h));
+}
+
+__device__ __forceinline__ uint16_t f2h_ref(float f) {
+    // fp32 -> f16 as the reference's f32_f16 (forward.c:1325-1344): RNE, >= 65520 saturates to 65504, NaN quiet
+    uint32_t u = __float_as_uint(f);
+    uint32_t sign = (u >> 16) & 0x8000u, a = u & 0x7fffffffu;
+    uint32_t n = a - 0x38000000u;
+    uint32_t h = (n + 0xfffu + ((n >> 13) & 1)) >> 13;
+    float fs = __uint_as_float(a < 0x38800000u ? a : 0u);
+    uint32_t sub = (uint32_t)rintf(fs * 16777216.0f);
+    h = a < 0x38800000u ? sub : h;
+    h = a >= 0x477ff000u ? 0x7bffu : h;
+    h = a > 0x7f800000u ? (0x7e00u | ((a >> 13) & 0x3ffu)) : h;
+    return (uint16_t)(sign | h);
+}
+
+__device__ __forceinline__ float exp_att(float x) {
+    // forward.c:1301-1321 (att512_exp): Cephes-style expf, x clamped at -86
+    x = x > -86.0f ? x : -86.0f;
+    float n = rintf(x * 1.44269504088896341f);
+    float r = __builtin_fmaf(n, -0.693359375f, x);
+    r = __builtin_fmaf(n, 2.12194440e-4f, r);
+    float z = r * r;
+    float y = 1.9875691500e-4f;
+    y = __builtin_fmaf(y, r, 1.3981999507e-3f);
+    y = __builtin_fmaf(y, r, 8.3334519073e-3f);
+    y = __builtin_fmaf(y, r, 4.1665795894e-2f);
+    y = __builtin_fmaf(y, r, 1.6666665459e-1f);
+    y = __builtin_fmaf(y, r, 5.0000001201e-1f);
+    y = __builtin_fmaf(y, z, r);
+    y = y + 1.0f;
+    return __uint_as_float(__float_as_uint(y) + ((uint32_t)(int32_t)n << 23));
+}
+
+__device__ __forceinline__ float silu_exp(float x) { return exp_att(x < 80.0f ? x : 80.0f); }
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+// quantize 32 consecutive values of one group (a thread's own), forward.c:803-836
+__device__ __forceinline__ void quant_group(const float *v, int8_t *q, float *s) {
+    float wmax = 0.0f;
+    #pragma unroll
+    for (int i = 0; i < 32; i++) {
+        float a = fabsf(v[i]);
+        wmax = a > wmax ? a : wmax;
+    }
+    *s = wmax * (1.0f / 127.0f);
+    uint32_t w[8];
+    if (!(wmax > 0.0f)) {
+        #pragma unroll
+        for (int i = 0; i < 8; i++) w[i] = 0;
+    } else {
+        float inv = 127.0f / wmax;
+        #pragma unroll
+        for (int i = 0; i < 8; i++) {
+            uint32_t pk = 0;
+            #pragma unroll
+            for (int b = 0; b < 4; b++) {
+                float x = v[4 * i + b] * inv;
+                int32_t qi = (int32_t)(x + copysignf(0.49999997f, x));
+                pk |= ((uint32_t)qi & 0xffu) << (8 * b);
+            }
+            w[i] = pk;
+        }
+    }
+    uint4 *dst = (uint4 *)q;
+    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+}
+
+// rmsnorm scale of n floats in LDS (n % 16 == 0), computed by lanes 0..15 of the calling wave, returned to all lanes
+// of that wave: forward.c:886-901 in the reference's compiled order
+__device__ __forceinline__ float rms_scale_lds(const float *xs_lds, int n) {
+    int lane = threadIdx.x & 63;
+    float s = 0.0f;
+    if (lane < 16)
+        for (int j = lane; j < n; j += 16) s = __builtin_fmaf(xs_lds[j], xs_lds[j], s);
+    for (int w = 8; w >= 1; w >>= 1) {
+        float o = __shfl_down(s, w);
+        s = s + o;
+    }
+    float r = 0.0f;
+    if (lane == 0) {
+        float inv_n = 1.0f / (float)n;
+        float t = __builtin_fmaf(s, inv_n, 1e-6f);
+        r = 1.0f / sqrtf(t);
+    }
+    return __shfl(r, 0);
+}
+
+// --------------------------------------------------------------------------------------- embedding
+
+// x[b] = row tok[b] of a Q8_0 table (embed_row, forward.c:839-881): (int8) q * fp16 d, one rounding
+__global__ __launch_bounds__(256) void k_embed_q8(float *__restrict__ x, int dim, const uint8_t *__restrict__ codes,
+                                                  const uint16_t *__restrict__ scales, const int *__restrict__ tok) {
+    int b = blockIdx.x, t = tok[b];
+    const int8_t *q = (const int8_t *)codes + (size_t)t * dim;
+    const uint16_t *s = scales + (size_t)t * (dim / 32);
+    for (int i = threadIdx.x; i < dim; i += blockDim.x) x[(size_t)b * dim + i] = (float)q[i] * h2f(s[i >> 5]);
+}
+
+// ---------------------------------------------------- residual + rmsnorm + quantize (one row per block)
+
+// row b (= sel[j] if sel, else j): x[b] += d[b] (if d), xn = rmsnorm(x[b], w); xq / xs row j = quantize(xn);
+// hid row j = xn (if hid). xn kept in LDS between the steps (n <= 16384)
+__global__ __launch_bounds__(256) void k_rmsnorm_quant(float *__restrict__ x, const float *__restrict__ d, int n,
+                                                       const float *__restrict__ w, const int *__restrict__ sel,
+                                                       int8_t *__restrict__ xq, float *__restrict__ xs, int ldq,
+                                                       float *__restrict__ hid) {
+    extern __shared__ float lds[];
+    int j = blockIdx.x, b = sel ? sel[j] : j;
+    float *xr = x + (size_t)b * n;
+    const float *dr = d ? d + (size_t)b * n : nullptr;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        float v = xr[i];
+        if (dr) {
+            v = v + dr[i];
+            xr[i] = v;
+        }
+        lds[i] = v;
+    }
+    __syncthreads();
+    __shared__ float rsh;
+    if (threadIdx.x < 64) {
+        float r = rms_scale_lds(lds, n);
+        if (threadIdx.x == 0) rsh = r;
+    }
+    __syncthreads();
+    float r = rsh;
+    for (int g = threadIdx.x; g < n / 32; g += blockDim.x) {
+        float v[32];
+        #pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = (w[g * 32 + i] * lds[g * 32 + i]) * r;
+        if (hid)
+            for (int i = 0; i < 32; i++) hid[(size_t)j * n + g * 32 + i] = v[i];
+        quant_group(v, xq + (size_t)j * ldq + g * 32, xs + (size_t)j * (ldq / 32) + g);
+    }
+}
+
+// ------------------------------------------------------------------------------------- Q8_0 GEMV
+
+// out[m * ldo + row] = W row . X row m for M activation rows, R weight rows per block. Each thread takes half-groups
+// (16 codes) j = t, t + 256, ...: an exact int32 sum by 4 v_dot4 (sdot4), the lane pair's sums added (exact), the even
+// lane's product (ws * xs) * (float) isum into LDS; then one lane per (m, row) folds the groups in order. W: row-major
+// int8 codes (K per row) + fp16 scales (K / 32 per row); X: int8 rows at xq + m * ldx, fp32 scales at xs + m * ldx / 32.
+// mode 1: out = resid + val (the residual add, resid may alias out)
+template <int M, int R>
+__global__ __launch_bounds__(256) void k_gemv_q8(const int8_t *__restrict__ W, const uint16_t *__restrict__ WS, int nrows,
+                                                 int K, const int8_t *__restrict__ xq, const float *__restrict__ xs, int ldx,
+                                                 float *out, int ldo, int mode) {
+    extern __shared__ float P[];
+    const int G = K >> 5, H = K >> 4, PS = G + 1;
+    const int row0 = blockIdx.x * R, t = threadIdx.x;
+    for (int j = t; j < H; j += 256) {
+        int4 xv[M];
+        float xsg[M];
+        #pragma unroll
+        for (int m = 0; m < M; m++) {
+            xv[m] = *(const int4 *)(xq + (size_t)m * ldx + 16 * j);
+            xsg[m] = xs[(size_t)m * (ldx >> 5) + (j >> 1)];
+        }
+        int4 wv[R];
+        float ws[R];
+        #pragma unroll
+        for (int r = 0; r < R; r++) {
+            int row = row0 + r < nrows ? row0 + r : nrows - 1;
+            wv[r] = *(const int4 *)(W + (size_t)row * K + 16 * j);
+            ws[r] = h2f(WS[(size_t)row * G + (j >> 1)]);
+        }
+        #pragma unroll
+        for (int r = 0; r < R; r++) {
+            #pragma unroll
+            for (int m = 0; m < M; m++) {
+                int s = __builtin_amdgcn_sdot4(wv[r].x, xv[m].x, 0, false);
+                s = __builtin_amdgcn_sdot4(wv[r].y, xv[m].y, s, false);
+                s = __builtin_amdgcn_sdot4(wv[r].z, xv[m].z, s, false);
+                s = __builtin_amdgcn_sdot4(wv[r].w, xv[m].w, s, false);
+                s = s + __shfl_xor(s, 1);
+                if (!(j & 1)) {
+                    float sc = ws[r] * xsg[m];
+                    P[(m * R + r) * PS + (j >> 1)] = sc * (float)s;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    if (t < M * R) {
+        int m = t / R, r = t % R, row = row0 + r;
+        if (row < nrows) {
+            const float *p = P + t * PS;
+            float v = 0.0f;
+            for (int g = 0; g < G; g++) v = v + p[g];
+            float *o = out + (size_t)m * ldo + row;
+            *o = mode == 1 ? *o + v : v;
+        }
+    }
+}
+
+// ------------------------------------------------------------------- QK-norm + RoPE + KV cache store
+
+// one 64-lane block per (row, head): heads 0..nh-1 the query heads (rmsnorm with qn, RoPE, in place), nh..nh+nkv-1
+// the key heads (rmsnorm with kn, RoPE, f16 into the K cache), then the value heads (f16 into the V cache).
+// qkv row b: [q (nh hd) | k (nkv hd) | v (nkv hd)]; rope: cos / sin rows per position (hd floats: cos then sin).
+// Caches: row b's layer base kc[b] / vc[b] (f16, the tiled layout of forward.c:1894-1899)
+__global__ __launch_bounds__(64) void k_qknorm_rope_store(float *__restrict__ qkv, int ldqkv, int nh, int nkv, int hd,
+                                                          const float *__restrict__ qn, const float *__restrict__ kn,
+                                                          const float *__restrict__ rope, const int *__restrict__ pos,
+                                                          uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc) {
+    __shared__ float v[256];
+    int b = blockIdx.x, h = blockIdx.y, lane = threadIdx.x, p = pos[b];
+    float *row = qkv + (size_t)b * ldqkv;
+    int half = hd / 2;
+    if (h >= nh + nkv) { // value head: store
+        int g = h - nh - nkv;
+        const float *src = row + (size_t)(nh + nkv) * hd + g * hd;
+        uint16_t *dst = vc[b] + (((size_t)(p / ATT_P) * nkv + g) * ATT_P + (size_t)(p % ATT_P / ATT_T) * ATT_T) * hd +
+                        (size_t)(p % ATT_T) * hd;
+        for (int i = lane; i < hd; i += 64) dst[i] = f2h_ref(src[i]);
+        return;
+    }
+    float *src = row + (size_t)h * hd;
+    for (int i = lane; i < hd; i += 64) v[i] = src[i];
+    __syncthreads();
+    float r = rms_scale_lds(v, hd);
+    const float *w = h < nh ? qn : kn;
+    const float *cs = rope + (size_t)p * hd;
+    for (int i = lane; i < half; i += 64) {
+        float x = (w[i] * v[i]) * r, y = (w[i + half] * v[i + half]) * r;
+        float c = cs[i], s = cs[i + half];
+        float ys = y * s, yc = y * c;
+        float xo = __builtin_fmaf(x, c, -ys), yo = __builtin_fmaf(x, s, yc);
+        if (h < nh) {
+            src[i] = xo;
+            src[i + half] = yo;
+        } else {
+            int g = h - nh;
+            uint16_t *dst = kc[b] + (((size_t)(p / ATT_P) * nkv + g) * ATT_P + (size_t)(p % ATT_P / ATT_T) * ATT_T) * hd +
+                            (p % ATT_T);
+            dst[(size_t)i * ATT_T] = f2h_ref(xo);
+            dst[(size_t)(i + half) * ATT_T] = f2h_ref(yo);
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------------------- attention
+
+// One block per item (first row r0, rows nr of one sequence at consecutive positions, kv head g, key block kb): the
+// partial result of block kb (forward.c:1346-1403 with ml) for each of the nr * kv_mul query vectors that reach it:
+// part[(row * nh + h) * pstride + kb * (hd + 2)] = o[hd] (unnormalized), m, l. Query vector v = (row r0 + v / kv_mul,
+// head g * kv_mul + v % kv_mul) over positions 0..pos(row). hd <= 128, nr * kv_mul <= 32.
+#define ATT_NQ 32
+#define ATT_HDMAX 128
+__global__ __launch_bounds__(256) void k_attn_part(const int4 *__restrict__ items, const float *__restrict__ qkv, int ldqkv,
+                                                   int nh, int nkv, int hd, float scale, const int *__restrict__ pos,
+                                                   uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc,
+                                                   float *__restrict__ part, int pstride) {
+    __shared__ float qs[ATT_NQ * ATT_HDMAX];
+    __shared__ float S[ATT_NQ][ATT_P];
+    __shared__ int np[ATT_NQ];
+    int4 it = items[blockIdx.x];
+    int r0 = it.x, nr = it.y, g = it.z, kb = it.w, kv_mul = nh / nkv, nq = nr * kv_mul, t = threadIdx.x;
+    int t0 = kb * ATT_P;
+    const uint16_t *K = kc[r0] + ((size_t)kb * nkv + g) * ATT_P * hd; // this (block, head): 16 tiles of 16 x hd
+    const uint16_t *V = vc[r0] + ((size_t)kb * nkv + g) * ATT_P * hd;
+    for (int e = t; e < nq * hd; e += 256) {
+        int v = e / hd, i = e % hd;
+        qs[v * hd + i] = qkv[(size_t)(r0 + v / kv_mul) * ldqkv + (size_t)(g * kv_mul + v % kv_mul) * hd + i];
+    }
+    if (t < nq) {
+        int n = pos[r0 + t / kv_mul] + 1 - t0;
+        np[t] = n < 0 ? 0 : n < ATT_P ? n : ATT_P;
+    }
+    __syncthreads();
+    int nmax = 0;
+    for (int v = 0; v < nq; v++) nmax = np[v] > nmax ? np[v] : nmax;
+    // scores: thread t = position t0 + t
+    if (t < nmax) {
+        const uint16_t *kt = K + (size_t)(t / ATT_T) * ATT_T * hd + (t % ATT_T);
+        float a[ATT_NQ];
+        for (int c0 = 0; c0 < hd; c0 += 32) {
+            float c[ATT_NQ];
+            #pragma unroll
+            for (int v = 0; v < ATT_NQ; v++) c[v] = 0.0f;
+            for (int i = c0; i < c0 + 32; i++) {
+                float k = h2f(kt[(size_t)i * ATT_T]);
+                #pragma unroll
+                for (int v = 0; v < ATT_NQ; v++)
+                    if (v < nq) c[v] = __builtin_fmaf(qs[v * hd + i], k, c[v]);
+            }
+            #pragma unroll
+            for (int v = 0; v < ATT_NQ; v++) a[v] = c0 > 0 ? a[v] + c[v] : c[v];
+        }
+        #pragma unroll
+        for (int v = 0; v < ATT_NQ; v++)
+            if (v < nq) S[v][t] = a[v] * scale;
+    }
+    __syncthreads();
+    // softmax per vector: wave w takes vectors w, w + 4, ...
+    int wave = t >> 6, lane = t & 63;
+    for (int v = wave; v < nq; v += 4) {
+        int n = np[v];
+        if (n <= 0) continue;
+        float m = -3.402823466e38f;
+        for (int p = lane; p < n; p += 64) m = fmaxf(m, S[v][p]);
+        m = wave_max(m);
+        for (int p = lane; p < n; p += 64) S[v][p] = exp_att(S[v][p] - m);
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        float s = 0.0f;
+        if (lane < 16)
+            for (int p = lane; p < n; p += 16) s = s + S[v][p];
+        for (int w = 8; w >= 1; w >>= 1) {
+            float o = __shfl_down(s, w);
+            s = s + o;
+        }
+        if (lane == 0) {
+            int row = r0 + v / kv_mul, h = g * kv_mul + v % kv_mul;
+            float *ml = part + ((size_t)row * nh + h) * pstride + (size_t)kb * (hd + 2) + hd;
+            ml[0] = m;
+            ml[1] = s;
+        }
+    }
+    __syncthreads();
+    // o = fma chain over the positions in order: thread = (dim pair d2, vector group vg)
+    int d2 = t & 63, vg = t >> 6;
+    for (int i0 = 2 * d2; i0 < hd; i0 += 128) {
+        float o0[ATT_NQ / 4], o1[ATT_NQ / 4];
+        #pragma unroll
+        for (int k = 0; k < ATT_NQ / 4; k++) o0[k] = o1[k] = 0.0f;
+        for (int p = 0; p < nmax; p++) {
+            uint32_t vv = *(const uint32_t *)(V + (size_t)(p / ATT_T) * ATT_T * hd + (size_t)(p % ATT_T) * hd + i0);
+            float v0 = h2f((uint16_t)(vv & 0xffff)), v1 = h2f((uint16_t)(vv >> 16));
+            #pragma unroll
+            for (int k = 0; k < ATT_NQ / 4; k++) {
+                int v = vg + 4 * k;
+                if (v < nq && p < np[v]) {
+                    float e = S[v][p];
+                    o0[k] = __builtin_fmaf(e, v0, o0[k]);
+                    o1[k] = __builtin_fmaf(e, v1, o1[k]);
+                }
+            }
+        }
+        #pragma unroll
+        for (int k = 0; k < ATT_NQ / 4; k++) {
+            int v = vg + 4 * k;
+            if (v < nq && np[v] > 0) {
+                int row = r0 + v / kv_mul, h = g * kv_mul + v % kv_mul;
+                float *o = part + ((size_t)row * nh + h) * pstride + (size_t)kb * (hd + 2);
+                o[i0] = o0[k];
+                o[i0 + 1] = o1[k];
+            }
+        }
+    }
+}
+
+// one block per row: the attention of each head from its block partials in block order (att_combine,
+// forward.c:1405-1431), then the row's quantization for wo (aq row b, all_heads = nh * hd values; groups inside heads)
+__global__ __launch_bounds__(256) void k_attn_combine_quant(const float *__restrict__ part, int pstride, int nh, int hd,
+                                                            const int *__restrict__ pos, int8_t *__restrict__ aq,
+                                                            float *__restrict__ as, int ldq, float *__restrict__ att_out) {
+    extern __shared__ float o_lds[];
+    int b = blockIdx.x, nb = (pos[b] + 1 + ATT_P - 1) / ATT_P, st = hd + 2;
+    for (int e = threadIdx.x; e < nh * hd; e += blockDim.x) {
+        int h = e / hd, i = e % hd;
+        const float *pb = part + ((size_t)b * nh + h) * pstride;
+        float out;
+        if (nb == 1) {
+            float inv = 1.0f / pb[hd + 1];
+            out = pb[i] * inv;
+        } else {
+            float M = pb[hd];
+            for (int k = 1; k < nb; k++) M = pb[(size_t)k * st + hd] > M ? pb[(size_t)k * st + hd] : M;
+            float L = 0.0f, acc = 0.0f;
+            for (int k = 0; k < nb; k++) {
+                const float *o = pb + (size_t)k * st;
+                float c = exp_att(o[hd] - M);
+                L = __builtin_fmaf(c, o[hd + 1], L);
+                acc = __builtin_fmaf(c, o[i], acc);
+            }
+            float inv = 1.0f / L;
+            out = acc * inv;
+        }
+        o_lds[e] = out;
+        if (att_out) att_out[(size_t)b * nh * hd + e] = out;
+    }
+    __syncthreads();
+    for (int g = threadIdx.x; g < nh * hd / 32; g += blockDim.x)
+        quant_group(o_lds + g * 32, aq + (size_t)b * ldq + g * 32, as + (size_t)b * (ldq / 32) + g);
+}
+
+// ------------------------------------------------------------------------------------ SwiGLU + quantize
+
+// row b of hb = [h (H) | h2 (H)]: v = (h * h2) * (1 / (1 + exp(min(-h, 80)))), quantized into hq / hs row b
+__global__ __launch_bounds__(256) void k_swiglu_quant(const float *__restrict__ hb, int H, int8_t *__restrict__ hq,
+                                                      float *__restrict__ hs) {
+    int b = blockIdx.x;
+    const float *h1 = hb + (size_t)b * 2 * H, *h2 = h1 + H;
+    for (int g = threadIdx.x; g < H / 32; g += blockDim.x) {
+        float v[32];
+        #pragma unroll
+        for (int i = 0; i < 32; i++) {
+            float h = h1[g * 32 + i];
+            float e = silu_exp(-h);
+            float r = 1.0f / (1.0f + e);
+            v[i] = (h * h2[g * 32 + i]) * r;
+        }
+        quant_group(v, hq + (size_t)b * H + g * 32, hs + (size_t)b * (H / 32) + g);
+    }
+}
+
+// ---------------------------------------------------------------------------------------- quantize rows
+
+__global__ __launch_bounds__(256) void k_quant_rows(const float *__restrict__ x, int n, int ldxf, int8_t *__restrict__ q,
+                                                    float *__restrict__ s, int ldq) {
+    int b = blockIdx.x;
+    for (int g = threadIdx.x; g < n / 32; g += blockDim.x) {
+        float v[32];
+        #pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = x[(size_t)b * ldxf + g * 32 + i];
+        quant_group(v, q + (size_t)b * ldq + g * 32, s + (size_t)b * (ldq / 32) + g);
+    }
+}
+
+// ----------------------------------------------------------------------------------------------- argmax
+
+// per row: the first index holding the maximum (sampler.c:40-60)
+__global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ lg, int n, int ld, int *__restrict__ out) {
+    __shared__ float smax[4];
+    __shared__ int sidx[4];
+    const float *r = lg + (size_t)blockIdx.x * ld;
+    float m = -3.402823466e38f;
+    int idx = 0x7fffffff;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        float v = r[i];
+        if (v > m) { m = v; idx = i; }
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+        float m2 = __shfl_xor(m, o);
+        int i2 = __shfl_xor(idx, o);
+        if (m2 > m || (m2 == m && i2 < idx)) { m = m2; idx = i2; }
+    }
+    int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { smax[w] = m; sidx[w] = idx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < 4; k++)
+            if (smax[k] > m || (smax[k] == m && sidx[k] < idx)) { m = smax[k]; idx = sidx[k]; }
+        out[blockIdx.x] = idx;
+    }
+}
+
+// ------------------------------------------------------------------------------------------ launchers
+
+extern "C" {
+
+int gw_k_embed_q8(float *x, int dim, const uint8_t *codes, const uint16_t *scales, const int *tok, int n, hipStream_t s) {
+    hipLaunchKernelGGL(k_embed_q8, dim3(n), dim3(256), 0, s, x, dim, codes, scales, tok);
+    return (int)hipGetLastError();
+}
+
+int gw_k_rmsnorm_quant(float *x, const float *d, int dim, const float *w, const int *sel, int n, int8_t *xq, float *xs, int ldq,
+                       float *hid, hipStream_t s) {
+    hipLaunchKernelGGL(k_rmsnorm_quant, dim3(n), dim3(256), (size_t)dim * sizeof(float), s, x, d, dim, w, sel, xq, xs, ldq, hid);
+    return (int)hipGetLastError();
+}
+
+int gw_k_gemv_q8(const int8_t *W, const uint16_t *WS, int nrows, int K, const int8_t *xq, const float *xs, int ldx, int M,
+                 float *out, int ldo, int mode, hipStream_t s) {
+    // M activation rows in launches of up to 4
+    const int R = 4;
+    size_t lds = (size_t)4 * R * (K / 32 + 1) * sizeof(float);
+    for (int m0 = 0; m0 < M; m0 += 4) {
+        int mm = M - m0 < 4 ? M - m0 : 4;
+        dim3 grid((nrows + R - 1) / R);
+        const int8_t *x = xq + (size_t)m0 * ldx;
+        const float *xsc = xs + (size_t)m0 * (ldx / 32);
+        float *o = out + (size_t)m0 * ldo;
+        switch (mm) {
+        case 1: hipLaunchKernelGGL((k_gemv_q8<1, R>), grid, dim3(256), lds, s, W, WS, nrows, K, x, xsc, ldx, o, ldo, mode); break;
+        case 2: hipLaunchKernelGGL((k_gemv_q8<2, R>), grid, dim3(256), lds, s, W, WS, nrows, K, x, xsc, ldx, o, ldo, mode); break;
+        case 3: hipLaunchKernelGGL((k_gemv_q8<3, R>), grid, dim3(256), lds, s, W, WS, nrows, K, x, xsc, ldx, o, ldo, mode); break;
+        default: hipLaunchKernelGGL((k_gemv_q8<4, R>), grid, dim3(256), lds, s, W, WS, nrows, K, x, xsc, ldx, o, ldo, mode); break;
+        }
+    }
+    return (int)hipGetLastError();
+}
+
+int gw_k_qknorm_rope_store(float *qkv, int ldqkv, int n, int nh, int nkv, int hd, const float *qn, const float *kn,
+                           const float *rope, const int *pos, uint16_t *const *kc, uint16_t *const *vc, hipStream_t s) {
+    hipLaunchKernelGGL(k_qknorm_rope_store, dim3(n, nh + 2 * nkv), dim3(64), 0, s, qkv, ldqkv, nh, nkv, hd, qn, kn, rope, pos, kc, vc);
+    return (int)hipGetLastError();
+}
+
+int gw_k_attn_part(const void *items, int nitems, const float *qkv, int ldqkv, int nh, int nkv, int hd, float scale,
+                   const int *pos, uint16_t *const *kc, uint16_t *const *vc, float *part, int pstride, hipStream_t s) {
+    hipLaunchKernelGGL(k_attn_part, dim3(nitems), dim3(256), 0, s, (const int4 *)items, qkv, ldqkv, nh, nkv, hd, scale, pos, kc, vc, part, pstride);
+    return (int)hipGetLastError();
+}
+
+int gw_k_attn_combine_quant(const float *part, int pstride, int nh, int hd, const int *pos, int n, int8_t *aq, float *as,
+                            int ldq, float *att_out, hipStream_t s) {
+    hipLaunchKernelGGL(k_attn_combine_quant, dim3(n), dim3(256), (size_t)nh * hd * sizeof(float), s, part, pstride, nh, hd, pos,
+                       aq, as, ldq, att_out);
+    return (int)hipGetLastError();
+}
+
+int gw_k_swiglu_quant(const float *hb, int H, int n, int8_t *hq, float *hs, hipStream_t s) {
+    hipLaunchKernelGGL(k_swiglu_quant, dim3(n), dim3(256), 0, s, hb, H, hq, hs);
+    return (int)hipGetLastError();
+}
+
+int gw_k_quant_rows(const float *x, int n, int ldxf, int rows, int8_t *q, float *sc, int ldq, hipStream_t s) {
+    hipLaunchKernelGGL(k_quant_rows, dim3(rows), dim3(256), 0, s, x, n, ldxf, q, sc, ldq);
+    return (int)hipGetLastError();
+}
+
+int gw_k_argmax(const float *lg, int n, int ld, int rows, int *out, hipStream_t s) {
+    hipLaunchKernelGGL(k_argmax, dim3(rows), dim3(256), 0, s, lg, n, ld, out);
+    return (int)hipGetLastError();
+}
+
+} // extern "C"

@@ -1,0 +1,172 @@
+/* gwenedeg_gpu.h: the C ABI of the MI355X backend of gwenedeg's forward hot path (libgwenedeg_amd.so).
+ *
+ * The entry points are the forward half of the reference's public API, src/runq.h, with the same names, argument
+ * meaning, return codes and error behaviour, so that runq.h's callers (engine, CLI, chat, speculative loop, tests)
+ * link against this library instead of the reference's forward.c / model.c weight path. Each declaration cites the
+ * runq.h line it replaces. Types are laid out exactly as runq.h's (same fields, order and widths).
+ *
+ * Scope of the device implementation: Qwen3 dense models (GGUF, Q8_0 / Q4_K / Q6_K matrices), the f16 KV cache
+ * (RQ_KV_F16; other KV types give RQ_ERR_ARG), one GPU, one HIP stream per context. Calls are synchronous at return
+ * (logits valid on the host), as the reference's are. Results are bit-identical for any batch composition: a row's
+ * logits do not depend on the rows it is batched with (the device kernels compute each output whole, in a fixed order).
+ *
+ * Extensions without a counterpart in runq.h are prefixed gw_ (below), e.g. the isolated Q8_0 operator of the
+ * reference's kernels_avx512.h and device-side greedy sampling.
+ */
+#ifndef GWENEDEG_GPU_H
+#define GWENEDEG_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* runq.h:35-44 */
+enum {
+    RQ_OK = 0,
+    RQ_ERR_ARG = -1,
+    RQ_ERR_NOMEM = -2,
+    RQ_ERR_CONTEXT = -3,
+    RQ_ERR_STATE = -4,
+    RQ_ERR_LOAD = -5,
+    RQ_ERR_IO = -6,
+    RQ_ERR_MISMATCH = -7,
+};
+const char *rq_strerror(int err);  /* runq.h:45 */
+double rq_now(void);               /* runq.h:46 */
+const char *rq_threads_init(int n); /* runq.h:53: accepted, no effect (the device runs the passes) */
+int rq_threads(void);              /* runq.h:54 */
+
+typedef struct RqModel RqModel;
+typedef struct RqSeq RqSeq;
+typedef struct RqCtx RqCtx;
+
+#define RQ_CTX_DEFAULT_MAX 40960 /* runq.h:61 */
+
+/* runq.h:63-81 (same layout; tokenizer_only / page_cache / checkpoints / repack are accepted and ignored here: no
+ * tokenizer is built by this library, Qwen3 has no recurrent state, the device layouts are fixed) */
+typedef struct {
+    int ctx_len;
+    int tokenizer_only;
+    int no_tokenizer;
+    double mem;
+    int kv_bits;
+    int page_cache;
+    int checkpoints;
+    int repack;
+} RqModelOpts;
+
+/* runq.h:87-88: a GGUF file (qwen3; Q8_0, Q4_K, Q6_K matrices), its weights repacked into device memory */
+RqModel *rq_model_load(const char *path, const RqModelOpts *opts, char *err, size_t errlen);
+void rq_model_free(RqModel *m);
+
+/* runq.h:132-147 */
+typedef struct {
+    int dim, hidden_dim, n_layers, n_heads, n_kv_heads, head_dim, vocab_size;
+    int seq_len;
+    int ctx_max;
+    int group_size;
+    int shared_classifier;
+    int gguf;
+    int bos, eos;
+    const char *warning;
+    int chat;
+    float rope_theta;
+    int linear_layers;
+    unsigned long long fingerprint;
+} RqModelInfo;
+void rq_model_info(const RqModel *m, RqModelInfo *info);
+
+/* runq.h:214-219 */
+enum { RQ_KV_F32 = 0, RQ_KV_BF16 = 1, RQ_KV_F16 = 2, RQ_KV_Q8 = 3, RQ_KV_BF16_DOT = 5, RQ_KV_F16_DOT = 6, RQ_KV_Q8_DOT = 7,
+       RQ_KV_Q4 = 8, RQ_KV_Q4K4 = 9, RQ_KV_Q4_DOT = 12, RQ_KV_Q4K4_DOT = 13, RQ_KV_DEFAULT = RQ_KV_F16 };
+const char *rq_kv_name(int kv_type); /* runq.h:216 */
+int rq_kv_parse(const char *name);   /* runq.h:217 */
+int rq_kv_bits(int kv_type);         /* runq.h:218 */
+
+/* sequences: runq.h:222-282 (the KV cache lives in device memory, in the reference's tiled layout) */
+RqSeq *rq_seq_new(const RqModel *m, int capacity, int kv_type, int *err); /* runq.h:222 */
+void rq_seq_free(RqSeq *s);                                               /* runq.h:223 */
+void rq_seq_reset(RqSeq *s);                                              /* runq.h:224 */
+int rq_seq_truncate(RqSeq *s, int n);                                     /* runq.h:229 */
+int rq_seq_keep(const RqSeq *s, int n);                                   /* runq.h:230 */
+int rq_seq_checkpoint_at(RqSeq *s, int pos);                              /* runq.h:239: Qwen3, a no-op */
+int rq_seq_checkpoint_rows(RqSeq *s, int pos, int n);                     /* runq.h:247: Qwen3, a no-op */
+void rq_seq_checkpoint_rows_drop(RqSeq *s);                               /* runq.h:248 */
+int rq_seq_set_checkpoints(RqSeq *s, int n);                              /* runq.h:252 */
+int rq_seq_checkpoints(const RqSeq *s, int *pos, int max);                /* runq.h:256: 0 */
+int rq_seq_len(const RqSeq *s);                                           /* runq.h:260 */
+int rq_seq_capacity(const RqSeq *s);                                      /* runq.h:261 */
+const int *rq_seq_tokens(const RqSeq *s);                                 /* runq.h:262 */
+int rq_seq_common_prefix(const RqSeq *s, const int *tokens, int n);       /* runq.h:263 */
+int rq_seq_release(RqSeq *s, int keep);                                   /* runq.h:270 */
+size_t rq_seq_kv_bytes(const RqSeq *s, int n);                            /* runq.h:277 */
+int rq_seq_copy(RqSeq *dst, const RqSeq *src, int n);                     /* runq.h:282: device-to-device */
+void rq_seq_seed(RqSeq *s, unsigned long long seed);                      /* runq.h:315 */
+unsigned long long *rq_seq_rng(RqSeq *s);                                 /* runq.h:319 */
+int rq_seq_fill_synthetic(RqSeq *s, int n, unsigned long long seed);      /* runq.h:726 */
+
+/* contexts: runq.h:325-338 */
+#define RQ_BATCH_MAX 512
+RqCtx *rq_ctx_new(const RqModel *m, int max_batch, int max_ctx, int *err); /* runq.h:332 */
+void rq_ctx_free(RqCtx *c);                                                /* runq.h:333 */
+int rq_ctx_max_batch(const RqCtx *c);                                      /* runq.h:334 */
+const char *rq_ctx_error(const RqCtx *c);                                  /* runq.h:335 */
+int rq_ctx_profile(const RqCtx *c, const char **names, double *seconds, int max); /* runq.h:338 */
+
+/* forward passes: runq.h:341-375 */
+enum { RQ_LOGITS_NONE = 0, RQ_LOGITS_LAST = 1, RQ_LOGITS_ALL = 2 };
+int rq_decode(RqCtx *c, RqSeq *s, int token, float **logits);                                            /* runq.h:346 */
+int rq_decode_hidden(RqCtx *c, RqSeq *s, int token, float **logits, float *hidden, const float *h_in);  /* runq.h:350 */
+int rq_prefill(RqCtx *c, RqSeq *s, const int *tokens, int n, int mode, float *out, float **logits);      /* runq.h:355 */
+typedef struct {
+    RqSeq *seq;
+    const int *tokens;
+    int n;
+    int logits;
+    float *hidden;
+    const float *h_in;
+} RqSegment; /* runq.h:364-374 */
+int rq_forward_batch(RqCtx *c, const RqSegment *seg, int nseg, float *out, float **logits); /* runq.h:375 */
+
+/* runq.h:561 */
+unsigned long long rq_logits_hash(const float *logits, int n);
+
+/* ------------------------------------------------------------------------------------- extensions (gw_) */
+
+/* Device-side greedy sampling of a pass's logits rows: the first maximum of each row (the reference's
+ * sample_argmax, sampler.c:40-60, run on the logits before they leave the device). After rq_decode /
+ * rq_forward_batch on c: tokens[j] = argmax of selected row j, j < n (n <= the rows the last pass selected).
+ * RQ_ERR_STATE if the last pass produced no logits */
+int gw_ctx_argmax(RqCtx *c, int *tokens, int n);
+
+/* The isolated Q8_0 operator (the reference's kernels_avx512.h q8p_pack_blocks :113, q8p_gemv_rows :286 and
+ * q8p_gemm_item :235, and forward.c's quantize :803), on device pointers, on the given HIP stream (NULL: the null
+ * stream); asynchronous. Return RQ_OK or RQ_ERR_ARG (shapes: N % 16 == 0, K % 32 == 0) / RQ_ERR_STATE (launch failed).
+ *   gw_q8_pack:     nblk GGUF Q8_0 blocks (34 bytes each, row-major: N rows of K / 32 blocks) -> codes (N x K int8) and
+ *                   fp16 scales (N x K / 32), the device layout
+ *   gw_quantize:    M rows of K fp32 -> int8 codes + fp32 scales per group of 32 (forward.c:803-836)
+ *   gw_q8_matmul:   out[m * N + n] = W row n . X row m, m < M: exact int32 sums per group, the fold
+ *                   val = val + (ws * xs) * (float) isum in group order (forward.c:906-916), bit-identical to the
+ *                   reference's q8p_gemv_rows / q8p_gemm_item on the same int8 inputs
+ *   gw_q8_block_sums: isum[(m * N + n) * (K / 32) + g], the exact int32 sum of group g (for the bit-exact check) */
+int gw_q8_pack(const void *blocks, int N, int K, int8_t *codes, uint16_t *scales, void *stream);
+int gw_quantize(const float *x, int M, int K, int8_t *xq, float *xs, void *stream);
+int gw_q8_matmul(float *out, const int8_t *codes, const uint16_t *scales, int N, int K, const int8_t *xq, const float *xs,
+                 int M, void *stream);
+int gw_q8_block_sums(int32_t *isum, const int8_t *codes, int N, int K, const int8_t *xq, int M, void *stream);
+
+/* The K-quant operator on the file's blocks (kquants.h:79-109's definition; type 12 Q4_K, 14 Q6_K): out[m * N + n],
+ * blocks: N rows of K / 256 blocks, device memory */
+int gw_kq_matmul(float *out, int type, const void *blocks, int N, int K, const int8_t *xq, const float *xs, int M,
+                 void *stream);
+
+/* The context's stream (a hipStream_t), for callers that time the passes with events on it */
+void *gw_ctx_stream(RqCtx *c);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,121 @@
+"""Kernel-level parity on the GPU through the C ABI (gw_quantize, gw_q8_matmul, gw_q8_block_sums, gw_kq_matmul):
+bit-exact against the oracle on the same seeded inputs (integer sums exact; fp32 outputs the same bits, since both
+compute the reference's fold operation for operation)."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    import gwenedeg_amd as gw
+    return torch, gw
+
+
+def _rand_q8(rng, N, K):
+    wq = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    ws16 = np.abs(rng.normal(0, 1e-3, size=(N, K // 32))).astype(np.float16)
+    return wq, ws16
+
+
+def _to_dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@pytest.mark.parametrize("M,K", [(1, 1024), (3, 4096), (4, 2560), (5, 3072), (8, 12288), (17, 1024)])
+def test_quantize_bitexact(dev, M, K):
+    torch, gw = dev
+    from oracle import oracle as orc
+    rng = np.random.default_rng(M * 1000 + K)
+    x = rng.normal(0, 1, size=(M, K)).astype(np.float32)
+    x[0, :32] = 0.0            # an all-zero group: s = 0, q = 0
+    x[0, 32:64] = 1e-30        # tiny values
+    if M > 1:
+        x[1, 64:96] = -3.5     # a constant group: every q = -127
+    q_ref, s_ref = orc.quantize(x)
+    xd = _to_dev(torch, x)
+    q = torch.zeros((M, K), dtype=torch.int8, device="cuda")
+    s = torch.zeros((M, K // 32), dtype=torch.float32, device="cuda")
+    assert gw.lib.gw_quantize(xd.data_ptr(), M, K, q.data_ptr(), s.data_ptr(), None) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 256, 1024), (1, 1024, 4096), (2, 512, 12288), (4, 64, 2560), (7, 128, 4096),
+                                   (16, 48, 1024), (64, 32, 1024)])
+def test_q8_matmul_bitexact(dev, M, N, K):
+    torch, gw = dev
+    from oracle import oracle as orc
+    rng = np.random.default_rng(N + 7 * K + M)
+    wq, ws16 = _rand_q8(rng, N, K)
+    x = rng.normal(0, 1, size=(M, K)).astype(np.float32)
+    xq, xs = orc.quantize(x)
+    ref = orc.q8_matmul(wq, ws16.astype(np.float32), xq, xs)
+    out = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+    W, WS, XQ, XS = (_to_dev(torch, a) for a in (wq, ws16.view(np.int16), xq, xs))
+    assert gw.lib.gw_q8_matmul(out.data_ptr(), W.data_ptr(), WS.data_ptr(), N, K, XQ.data_ptr(), XS.data_ptr(), M, None) == 0
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"max diff {np.abs(got - ref).max()}"
+
+
+def test_q8_pack_and_block_sums(dev):
+    torch, gw = dev
+    from oracle import oracle as orc
+    rng = np.random.default_rng(5)
+    N, K, M = 96, 2048, 3
+    wq, ws16 = _rand_q8(rng, N, K)
+    blocks = np.zeros((N, K // 32, 34), np.uint8)
+    blocks[:, :, 0:2] = ws16.view(np.uint8).reshape(N, K // 32, 2)
+    blocks[:, :, 2:] = wq.view(np.uint8).reshape(N, K // 32, 32)
+    B = _to_dev(torch, blocks.reshape(-1))
+    codes = torch.zeros((N, K), dtype=torch.int8, device="cuda")
+    scales = torch.zeros((N, K // 32), dtype=torch.int16, device="cuda")
+    assert gw.lib.gw_q8_pack(B.data_ptr(), N, K, codes.data_ptr(), scales.data_ptr(), None) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(codes.cpu().numpy(), wq)
+    assert np.array_equal(scales.cpu().numpy().view(np.uint16), ws16.view(np.uint16))
+    xq = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    xq[0, :32] = 127
+    wq2 = wq.copy()
+    wq2[0, :32] = 127  # the largest group sum: 32 * 127 * 127 = 516,128
+    codes2 = _to_dev(torch, wq2)
+    isum = torch.zeros((M, N, K // 32), dtype=torch.int32, device="cuda")
+    XQ = _to_dev(torch, xq)
+    assert gw.lib.gw_q8_block_sums(isum.data_ptr(), codes2.data_ptr(), N, K, XQ.data_ptr(), M, None) == 0
+    torch.cuda.synchronize()
+    ref = orc.q8_block_sums(wq2, xq)
+    got = isum.cpu().numpy()
+    assert got[0, 0, 0] == 516128
+    assert np.array_equal(got, ref)
+    # brute force in int64 for one row
+    assert np.array_equal(got[1, 7], (wq2[7].astype(np.int64).reshape(-1, 32) * xq[1].astype(np.int64).reshape(-1, 32)).sum(1))
+
+
+@pytest.mark.parametrize("typ", [12, 14])
+@pytest.mark.parametrize("M", [1, 3, 6])
+def test_kq_matmul_bitexact(dev, typ, M):
+    torch, gw = dev
+    from oracle import oracle as orc
+    from gwenedeg_amd import synth
+    rng = np.random.default_rng(typ * 10 + M)
+    N, K = 64, 1024
+    sl = synth.synth_library()
+    rb = sl.gw_synth_row_bytes(typ, K)
+    blocks = np.zeros((N, rb), np.uint8)
+    w = rng.normal(0, 0.02, size=(N, K)).astype(np.float32)
+    for r in range(N):
+        sl.gw_synth_encode_row(typ, blocks[r].ctypes.data, w[r].ctypes.data, K)
+    x = rng.normal(0, 1, size=(M, K)).astype(np.float32)
+    xq, xs = orc.quantize(x)
+    ref = orc.kq_matmul(typ, blocks, xq, xs, N, K)
+    out = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+    Bd, XQ, XS = (_to_dev(torch, a) for a in (blocks.reshape(-1), xq, xs))
+    assert gw.lib.gw_kq_matmul(out.data_ptr(), typ, Bd.data_ptr(), N, K, XQ.data_ptr(), XS.data_ptr(), M, None) == 0
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"max diff {np.abs(got - ref).max()}"
