@@ -97,6 +97,11 @@ _sig = {
     "rq_logits_hash": (ctypes.c_ulonglong, [_F, _I]),
     "gw_ctx_argmax": (_I, [_P, ctypes.POINTER(_I), _I]),
     "gw_ctx_stream": (_P, [_P]),
+    "gw_decode_argmax": (_I, [_P, _P, _I, ctypes.POINTER(_I)]),
+    "gw_ctx_profile_enable": (_I, [_P, _I]),
+    "gw_ctx_gemv_sweep": (_I, [_P, _I, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),
+    "gw_ctx_profile_launches": (ctypes.c_long, [_P, _I]),
+    "rq_ctx_profile": (_I, [_P, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_double), _I]),
     "gw_q8_pack": (_I, [_P, _I, _I, _P, _P, _P]),
     "gw_quantize": (_I, [_P, _I, _I, _P, _P, _P]),
     "gw_q8_matmul": (_I, [_P, _P, _P, _I, _I, _P, _P, _I, _P]),
@@ -274,6 +279,28 @@ class Ctx:
         p = ctypes.POINTER(ctypes.c_float)()
         self._check(lib.rq_forward_batch(self._h, arr, n, _fptr(out), ctypes.byref(p)), "rq_forward_batch")
         return (out[:nsel] if nsel else None), hids
+
+    def decode_argmax(self, seq: Seq, token: int) -> int:
+        """gw_decode_argmax: a decode step whose greedy next token is chosen on the device"""
+        nxt = ctypes.c_int(0)
+        self._check(lib.gw_decode_argmax(self._h, seq._h, int(token), ctypes.byref(nxt)), "gw_decode_argmax")
+        return nxt.value
+
+    def profile(self, on: bool = True):
+        self._check(lib.gw_ctx_profile_enable(self._h, 1 if on else 0), "gw_ctx_profile_enable")
+
+    def profile_read(self) -> dict:
+        """{class: (seconds, launches)} since profile(True)"""
+        names = (ctypes.c_char_p * 16)()
+        secs = (ctypes.c_double * 16)()
+        n = lib.rq_ctx_profile(self._h, names, secs, 16)
+        return {names[i].decode(): (secs[i], lib.gw_ctx_profile_launches(self._h, i)) for i in range(n)}
+
+    def gemv_sweep(self, reps: int = 1):
+        """gw_ctx_gemv_sweep: (seconds per sweep, weight bytes per sweep, launches per sweep)"""
+        t, b, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int()
+        self._check(lib.gw_ctx_gemv_sweep(self._h, reps, ctypes.byref(t), ctypes.byref(b), ctypes.byref(n)), "gw_ctx_gemv_sweep")
+        return t.value, b.value, n.value
 
     def argmax(self, n: int = 1) -> np.ndarray:
         """gw_ctx_argmax: device-side greedy tokens of the last pass's first n logits rows."""

@@ -148,11 +148,17 @@ static void dfree(void *p) { if (p) hipFree(p); }
 
 void rq_ctx_free(RqCtx *c) {
     if (!c) return;
-    void *d[] = { c->x, c->xb, c->qkv, c->hb, c->part, c->logits_d, c->hid_d, c->xq, c->hq, c->xs, c->hs, c->argmax_d, c->meta_d };
+    void *d[] = { c->x, c->xb, c->qkv, c->hb, c->part, c->logits_d, c->hid_d, c->xq, c->hq, c->xs, c->hs, c->argmax_d, c->argmax_scr, c->meta_d };
     for (size_t i = 0; i < sizeof d / sizeof d[0]; i++) dfree(d[i]);
     if (c->meta_h) hipHostFree(c->meta_h);
     if (c->logits) hipHostFree(c->logits);
     if (c->lg_h) hipHostFree(c->lg_h);
+    if (c->ev) {
+        for (int i = 0; i < 2048; i++)
+            if (c->ev[i]) hipEventDestroy(c->ev[i]);
+        free(c->ev);
+        free(c->ev_class);
+    }
     if (c->stream) hipStreamDestroy(c->stream);
     free(c);
 }
@@ -226,6 +232,7 @@ RqCtx *rq_ctx_new(const RqModel *m, int nb_max, int max_ctx, int *err) {
     DM(c->logits_d, (size_t)B * m->vocab * 4);
     DM(c->hid_d, (size_t)B * dim * 4);
     DM(c->argmax_d, (size_t)B * 4);
+    DM(c->argmax_scr, (size_t)B * 512);
 #undef DM
     if (hipHostMalloc((void **)&c->logits, (size_t)m->vocab * 4, hipHostMallocDefault) != hipSuccess) goto fail;
     if (max_ctx <= 0 || max_ctx > m->seq_len) max_ctx = m->seq_len;
@@ -240,8 +247,59 @@ fail:
 
 int rq_ctx_max_batch(const RqCtx *c) { return c->nb_max; }
 const char *rq_ctx_error(const RqCtx *c) { return c->err; }
-int rq_ctx_profile(const RqCtx *c, const char **names, double *seconds, int max) { (void)c; (void)names; (void)seconds; (void)max; return 0; }
 void *gw_ctx_stream(RqCtx *c) { return c->stream; }
+
+/* ---------------------------------------------------------------------------------------- profiling */
+
+static const char *pf_name[GW_PF_N] = { "embed", "rmsnorm+quant", "matmul qkv", "qk-norm+rope+kv", "attention", "combine+quant",
+                                        "matmul wo", "matmul w1+w3", "swiglu+quant", "matmul w2", "classifier" };
+#define GW_EV_MAX 2048
+
+int gw_ctx_profile_enable(RqCtx *c, int on) {
+    if (on && !c->ev) {
+        c->ev = calloc(GW_EV_MAX, sizeof(hipEvent_t));
+        c->ev_class = calloc(GW_EV_MAX, sizeof(int));
+        if (!c->ev || !c->ev_class) return ctx_fail(c, RQ_ERR_NOMEM, "malloc failed");
+        for (int i = 0; i < GW_EV_MAX; i++)
+            if (hipEventCreate(&c->ev[i]) != hipSuccess) return ctx_fail(c, RQ_ERR_STATE, "hipEventCreate failed");
+    }
+    c->prof_on = on;
+    memset(c->prof_s, 0, sizeof c->prof_s);
+    memset(c->prof_n, 0, sizeof c->prof_n);
+    return RQ_OK;
+}
+
+int rq_ctx_profile(const RqCtx *c, const char **names, double *seconds, int max) {
+    /* runq.h:336-338: device time per kernel class, summed over the passes since gw_ctx_profile_enable */
+    if (!c->ev) return 0;
+    int n = max < GW_PF_N ? max : GW_PF_N;
+    for (int i = 0; i < n; i++) {
+        names[i] = pf_name[i];
+        seconds[i] = c->prof_s[i];
+    }
+    return n;
+}
+
+long gw_ctx_profile_launches(const RqCtx *c, int cls) { return cls >= 0 && cls < GW_PF_N ? c->prof_n[cls] : 0; }
+
+static void pf_mark(RqCtx *c, int cls) {
+    /* an event before a kernel of class cls (cls -1: the end mark) */
+    if (!c->prof_on || c->nev >= GW_EV_MAX) return;
+    hipEventRecord(c->ev[c->nev], c->stream);
+    c->ev_class[c->nev++] = cls;
+}
+
+static void pf_collect(RqCtx *c) {
+    /* after the pass's synchronization: each interval to the class of the kernel it started with */
+    for (int i = 0; i + 1 < c->nev; i++) {
+        float ms = 0;
+        if (c->ev_class[i] >= 0 && hipEventElapsedTime(&ms, c->ev[i], c->ev[i + 1]) == hipSuccess) {
+            c->prof_s[c->ev_class[i]] += ms * 1e-3;
+            c->prof_n[c->ev_class[i]]++;
+        }
+    }
+    c->nev = 0;
+}
 
 /* ------------------------------------------------------------------------------------------- passes */
 
@@ -269,7 +327,7 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
      * NULL with nsel == 0 */
     const RqModel *m = c->m;
     int n = P->n, L = m->n_layers, nh = m->n_heads, nkv = m->n_kv_heads, hd = m->head_dim, dim = m->dim, H = m->hidden;
-    int kv_mul = nh / nkv, rb = 32 / kv_mul > 0 ? 32 / kv_mul : 1, rc;
+    int kv_mul = nh / nkv, rb = 16 / kv_mul > 0 ? 16 / kv_mul : 1, rc;
     /* attention items: row blocks of <= rb consecutive rows of one sequence, per kv head and key block */
     int nbmax = 1, nitems = 0;
     for (int b = 0; b < n; b++) {
@@ -317,21 +375,33 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
     hipStream_t s = c->stream;
     int K = c->kmax;
 
+    c->nev = 0;
+    pf_mark(c, GW_PF_EMBED);
     if (m->embd.type == GW_Q8_0) KCHK(gw_k_embed_q8(c->x, dim, (const uint8_t *)m->embd.codes, m->embd.scales, tok_d, n, s));
     else KCHK(gw_k_embed_kq(c->x, dim, m->embd.type, m->embd.blocks, tok_d, n, s));
     for (int l = 0; l < L; l++) {
         const GwLayer *y = &m->layer[l];
+        pf_mark(c, GW_PF_NORM);
         KCHK(gw_k_rmsnorm_quant(c->x, l ? c->xb : NULL, dim, y->att_norm, NULL, n, c->xq, c->xs, K, NULL, s));
+        pf_mark(c, GW_PF_QKV);
         if ((rc = run_mm(c, y->qkv, y->nqkv, c->xq, c->xs, K, n, c->qkv, c->ldqkv, 0)) != RQ_OK) return rc;
+        pf_mark(c, GW_PF_ROPE);
         KCHK(gw_k_qknorm_rope_store(c->qkv, c->ldqkv, n, nh, nkv, hd, y->q_norm, y->k_norm, m->rope, pos_d,
                                     kc_d + (size_t)l * n, vc_d + (size_t)l * n, s));
+        pf_mark(c, GW_PF_ATT);
         KCHK(gw_k_attn_part(items_d, nitems, c->qkv, c->ldqkv, nh, nkv, hd, m->att_scale, pos_d, kc_d + (size_t)l * n,
                             vc_d + (size_t)l * n, c->part, c->pstride, s));
+        pf_mark(c, GW_PF_COMBINE);
         KCHK(gw_k_attn_combine_quant(c->part, c->pstride, nh, hd, pos_d, n, c->xq, c->xs, K, NULL, s));
+        pf_mark(c, GW_PF_WO);
         if ((rc = run_mm(c, &y->wo, 1, c->xq, c->xs, K, n, c->xb, dim, 0)) != RQ_OK) return rc;
+        pf_mark(c, GW_PF_NORM);
         KCHK(gw_k_rmsnorm_quant(c->x, c->xb, dim, y->ffn_norm, NULL, n, c->xq, c->xs, K, NULL, s));
+        pf_mark(c, GW_PF_W13);
         if ((rc = run_mm(c, y->w13, y->nw13, c->xq, c->xs, K, n, c->hb, 2 * H, 0)) != RQ_OK) return rc;
+        pf_mark(c, GW_PF_SWIGLU);
         KCHK(gw_k_swiglu_quant(c->hb, H, n, c->hq, c->hs, s));
+        pf_mark(c, GW_PF_W2);
         if ((rc = run_mm(c, &y->w2, 1, c->hq, c->hs, H, n, c->xb, dim, 0)) != RQ_OK) return rc;
     }
     int resid_done = 0;
@@ -340,9 +410,12 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
         resid_done = 1;
     }
     if (P->nsel > 0) {
+        pf_mark(c, GW_PF_NORM);
         KCHK(gw_k_rmsnorm_quant(c->x, resid_done ? NULL : c->xb, dim, m->final_norm, sel_d, P->nsel, c->xq, c->xs, K, NULL, s));
+        pf_mark(c, GW_PF_CLS);
         if ((rc = run_mm(c, &m->cls, 1, c->xq, c->xs, K, P->nsel, c->logits_d, m->vocab, 0)) != RQ_OK) return rc;
     }
+    pf_mark(c, -1);
     if (P->want_hidden) {
         HIPCHK(c, "hipStreamSynchronize (pass)", hipStreamSynchronize(s));
         for (int b = 0; b < n; b++)
@@ -363,7 +436,8 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
     } else {
         HIPCHK(c, "hipStreamSynchronize (pass)", hipStreamSynchronize(s));
     }
-    c->prof[0] = P->nsel; /* (rows with logits on the device: gw_ctx_argmax) */
+    if (c->prof_on) pf_collect(c);
+    c->last_nsel = P->nsel;
     return RQ_OK;
 }
 
@@ -399,6 +473,30 @@ int rq_decode(RqCtx *c, RqSeq *s, int token, float **logits) {
     e = decode_one(c, s, token, logits ? c->logits : NULL, NULL);
     if (logits) *logits = e == RQ_OK ? c->logits : NULL;
     return e;
+}
+
+int gw_decode_argmax(RqCtx *c, RqSeq *s, int token, int *next) {
+    /* rq_decode + the greedy next token on the device (sample_argmax, sampler.c:40-60): the logits stay on the
+     * device (gw_ctx_argmax reads them again if wanted) */
+    c->err[0] = 0;
+    int e = check_seq(c, s);
+    if (e != RQ_OK) return e;
+    if (!next) return ctx_fail(c, RQ_ERR_ARG, "no output for the token");
+    if (token < 0 || token >= c->m->vocab) return ctx_fail(c, RQ_ERR_ARG, "token %d out of range", token);
+    if (s->len >= s->cap) return ctx_fail(c, RQ_ERR_CONTEXT, "sequence full (%d positions)", s->cap);
+    static Pass P;
+    P.n = 1;
+    P.tok[0] = token;
+    P.pos[0] = s->len;
+    P.seq[0] = s;
+    P.sel[0] = 0;
+    P.nsel = 1;
+    P.want_hidden = 0;
+    P.hid[0] = NULL;
+    if ((e = fw_pass(c, &P, NULL)) != RQ_OK) return e;
+    s->tokens[s->len] = token;
+    s->len++;
+    return gw_ctx_argmax(c, next, 1);
 }
 
 int rq_decode_hidden(RqCtx *c, RqSeq *s, int token, float **logits, float *hidden, const float *h_in) {
@@ -503,10 +601,57 @@ int rq_prefill(RqCtx *c, RqSeq *s, const int *tokens, int n, int mode, float *ou
     return e;
 }
 
+int gw_ctx_gemv_sweep(RqCtx *c, int reps, double *seconds, double *bytes, int *launches) {
+    /* the weight matmuls of one decode step (every layer's q / k / v, wo, w1 / w3, w2, then the classifier) on one
+     * activation row, back to back on the context's stream, reps times, between two HIP events: the device time of the
+     * decode path's weight streaming without the other kernels between them. *bytes: the file-format bytes of those
+     * weights per sweep (Q8_0 34 / 32, Q4_K 144 / 256, Q6_K 210 / 256 per weight); *launches: kernels per sweep */
+    const RqModel *m = c->m;
+    if (reps < 1) return ctx_fail(c, RQ_ERR_ARG, "reps %d", reps);
+    double b = 0;
+    int nl = 0, rc;
+    hipEvent_t e0, e1;
+    HIPCHK(c, "hipEventCreate", hipEventCreate(&e0));
+    HIPCHK(c, "hipEventCreate", hipEventCreate(&e1));
+    HIPCHK(c, "hipEventRecord", hipEventRecord(e0, c->stream));
+    for (int r = 0; r < reps; r++) {
+        for (int l = 0; l < m->n_layers; l++) {
+            const GwLayer *y = &m->layer[l];
+            if ((rc = run_mm(c, y->qkv, y->nqkv, c->xq, c->xs, c->kmax, 1, c->qkv, c->ldqkv, 0)) != RQ_OK) return rc;
+            if ((rc = run_mm(c, &y->wo, 1, c->xq, c->xs, c->kmax, 1, c->xb, m->dim, 0)) != RQ_OK) return rc;
+            if ((rc = run_mm(c, y->w13, y->nw13, c->xq, c->xs, c->kmax, 1, c->hb, 2 * m->hidden, 0)) != RQ_OK) return rc;
+            if ((rc = run_mm(c, &y->w2, 1, c->hq, c->hs, m->hidden, 1, c->xb, m->dim, 0)) != RQ_OK) return rc;
+        }
+        if ((rc = run_mm(c, &m->cls, 1, c->xq, c->xs, c->kmax, 1, c->logits_d, m->vocab, 0)) != RQ_OK) return rc;
+    }
+    HIPCHK(c, "hipEventRecord", hipEventRecord(e1, c->stream));
+    HIPCHK(c, "hipEventSynchronize", hipEventSynchronize(e1));
+    float ms = 0;
+    hipEventElapsedTime(&ms, e0, e1);
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    for (int l = 0; l < m->n_layers; l++) {
+        const GwLayer *y = &m->layer[l];
+        const GwMat *ws[8] = { &y->qkv[0], y->nqkv > 1 ? &y->qkv[1] : NULL, y->nqkv > 2 ? &y->qkv[2] : NULL, &y->wo, &y->w13[0],
+                               y->nw13 > 1 ? &y->w13[1] : NULL, &y->w2, NULL };
+        for (int i = 0; i < 7; i++)
+            if (ws[i]) {
+                b += gw_mat_file_bytes(ws[i]);
+                nl++;
+            }
+    }
+    b += gw_mat_file_bytes(&m->cls);
+    nl++;
+    if (seconds) *seconds = ms * 1e-3 / reps;
+    if (bytes) *bytes = b;
+    if (launches) *launches = nl;
+    return RQ_OK;
+}
+
 int gw_ctx_argmax(RqCtx *c, int *tokens, int n) {
-    int rows = (int)c->prof[0];
+    int rows = c->last_nsel;
     if (rows <= 0 || n < 1 || n > rows) return ctx_fail(c, RQ_ERR_STATE, "no logits rows on the device (%d)", rows);
-    if (gw_k_argmax(c->logits_d, c->m->vocab, c->m->vocab, n, c->argmax_d, c->stream))
+    if (gw_k_argmax(c->logits_d, c->m->vocab, c->m->vocab, n, c->argmax_d, c->argmax_scr, c->stream))
         return ctx_fail(c, RQ_ERR_STATE, "argmax launch failed");
     HIPCHK(c, "hipMemcpyAsync (argmax)", hipMemcpyAsync(tokens, c->argmax_d, (size_t)n * 4, hipMemcpyDeviceToHost, c->stream));
     HIPCHK(c, "hipStreamSynchronize (argmax)", hipStreamSynchronize(c->stream));

@@ -6,6 +6,8 @@
 
 #include "gw_internal.h"
 
+__device__ __forceinline__ float h2f_g(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+
 // GGUF Q8_0 blocks (fp16 d, 32 int8; 34 bytes) -> codes (32 per block) + fp16 scales: the device layout
 __global__ __launch_bounds__(256) void k_q8_unpack(const uint8_t *__restrict__ blk, size_t nblk, int8_t *__restrict__ codes,
                                                    uint16_t *__restrict__ scales) {
@@ -46,6 +48,111 @@ __global__ __launch_bounds__(256) void k_fill_synthetic(uint16_t *kc, uint16_t *
     float a = (float)(z & 0xffffff) * (1.0f / 16777216.0f), b = (float)((z >> 24) & 0xffffff) * (1.0f / 16777216.0f);
     kc[i] = __half_as_ushort(__float2half((2.0f * a - 1.0f) * 3.9f));
     vc[i] = __half_as_ushort(__float2half((2.0f * b - 1.0f) * 0.99f));
+}
+
+// ------------------------------------------------------------------------------------- Q8_0 MFMA GEMM
+
+// out[m * ldo + n] = W row n . X row m for m < M, n < N (prefill / batched rows): per group g of 32 (one K step of
+// v_mfma_i32_32x32x32_i8), the exact int32 sums of a 32 x 32 output tile, then per output the reference's fold
+// val = val + (ws * xs) * (float) isum, groups in order (forward.c:906-916). A block of 256 threads (4 waves) computes a
+// GM x GN tile (wave w: rows 32 (w / (GN / 64)) .., columns 64 (w % (GN / 64)) .., two MFMA tiles); X and W are staged
+// in LDS 4 groups (128 bytes of each row) at a time with 16-byte loads, rows padded to 144 bytes.
+// MFMA operand layout (32 x 32 x 32, int8): lane l holds A[l % 32][16 (l / 32) .. + 15] and B[16 (l / 32) .. + 15][l % 32];
+// result register r of lane l is C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32]
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+#define GM 64
+#define GN 128
+#define GKB 128
+#define GROW 144
+__global__ __launch_bounds__(256) void k_gemm_q8(const int8_t *__restrict__ W, const uint16_t *__restrict__ WS, int N, int K,
+                                                 const int8_t *__restrict__ X, const float *__restrict__ XS, int ldx, int M,
+                                                 float *__restrict__ out, int ldo) {
+    __shared__ __align__(16) int8_t xl[GM * GROW];
+    __shared__ __align__(16) int8_t wl[GN * GROW];
+    __shared__ __align__(16) float xsl[4][GM];
+    __shared__ float wsl[GN][4];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int m0 = blockIdx.y * GM, n0 = blockIdx.x * GN, G = K >> 5;
+    const int wm = (wave >> 1) * 32, wn = (wave & 1) * 64; // the wave's sub-tile
+    float acc[2][16];
+    #pragma unroll
+    for (int j = 0; j < 2; j++)
+        #pragma unroll
+        for (int r = 0; r < 16; r++) acc[j][r] = 0.0f;
+    for (int k0 = 0; k0 < K; k0 += GKB) {
+        const int ng = (K - k0) < GKB ? (K - k0) >> 5 : 4; // groups in this stage
+        // stage: X rows m0.. (GM x 128 B: 512 chunks of 16 B, 2 per thread), W rows n0.. (GN x 128 B: 4 per thread)
+        uint4 xr[2], wr[4];
+        #pragma unroll
+        for (int k = 0; k < 2; k++) {
+            int c = t + 256 * k, row = c >> 3, col = (c & 7) * 16, m = m0 + row < M ? m0 + row : M - 1;
+            xr[k] = col < ng * 32 ? *(const uint4 *)(X + (size_t)m * ldx + k0 + col) : make_uint4(0, 0, 0, 0);
+        }
+        #pragma unroll
+        for (int k = 0; k < 4; k++) {
+            int c = t + 256 * k, row = c >> 3, col = (c & 7) * 16, n = n0 + row < N ? n0 + row : N - 1;
+            wr[k] = col < ng * 32 ? *(const uint4 *)(W + (size_t)n * K + k0 + col) : make_uint4(0, 0, 0, 0);
+        }
+        float xsv = 0.0f, wsv0 = 0.0f, wsv1 = 0.0f;
+        {
+            int row = t >> 2, gg = t & 3, m = m0 + row < M ? m0 + row : M - 1;
+            if (row < GM && gg < ng) xsv = XS[(size_t)m * (ldx >> 5) + (k0 >> 5) + gg];
+            int n = n0 + row < N ? n0 + row : N - 1, n2 = n0 + row + 64 < N ? n0 + row + 64 : N - 1;
+            if (gg < ng) {
+                wsv0 = h2f_g(WS[(size_t)n * G + (k0 >> 5) + gg]);
+                wsv1 = h2f_g(WS[(size_t)n2 * G + (k0 >> 5) + gg]);
+            }
+        }
+        __syncthreads(); // (the previous stage's readers are done)
+        #pragma unroll
+        for (int k = 0; k < 2; k++) {
+            int c = t + 256 * k;
+            *(uint4 *)(xl + (c >> 3) * GROW + (c & 7) * 16) = xr[k];
+        }
+        #pragma unroll
+        for (int k = 0; k < 4; k++) {
+            int c = t + 256 * k;
+            *(uint4 *)(wl + (c >> 3) * GROW + (c & 7) * 16) = wr[k];
+        }
+        {
+            int row = t >> 2, gg = t & 3;
+            if (row < GM) xsl[gg][row] = xsv;
+            wsl[row][gg] = wsv0;
+            wsl[row + 64][gg] = wsv1;
+        }
+        __syncthreads();
+        for (int gg = 0; gg < ng; gg++) {
+            i32x4 a = *(const i32x4 *)(xl + (wm + (lane & 31)) * GROW + gg * 32 + 16 * (lane >> 5));
+            #pragma unroll
+            for (int j = 0; j < 2; j++) {
+                i32x4 b = *(const i32x4 *)(wl + (wn + 32 * j + (lane & 31)) * GROW + gg * 32 + 16 * (lane >> 5));
+                i32x16 z = { 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0 };
+                i32x16 I = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
+                float ws = wsl[wn + 32 * j + (lane & 31)][gg];
+                #pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    float4 xs4 = *(const float4 *)(&xsl[gg][wm + 8 * q + 4 * (lane >> 5)]);
+                    float xsq[4] = { xs4.x, xs4.y, xs4.z, xs4.w };
+                    #pragma unroll
+                    for (int s = 0; s < 4; s++) {
+                        float sc = ws * xsq[s];
+                        float p = sc * (float)I[4 * q + s];
+                        acc[j][4 * q + s] = acc[j][4 * q + s] + p;
+                    }
+                }
+            }
+        }
+    }
+    #pragma unroll
+    for (int j = 0; j < 2; j++) {
+        int n = n0 + wn + 32 * j + (lane & 31);
+        #pragma unroll
+        for (int r = 0; r < 16; r++) {
+            int m = m0 + wm + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (m < M && n < N) out[(size_t)m * ldo + n] = acc[j][r];
+        }
+    }
 }
 
 // --------------------------------------------------------------------------------------------- K-quants
@@ -209,6 +316,11 @@ int gw_k_fill_synthetic(uint16_t *kc, uint16_t *vc, size_t n, unsigned long long
 }
 
 int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int M, float *out, int ldo, int mode, hipStream_t s) {
+    if (w->type == GW_Q8_0 && M > GW_GEMV_MAX_ROWS && mode == 0) {
+        dim3 grid((w->rows + GN - 1) / GN, (M + GM - 1) / GM);
+        hipLaunchKernelGGL(k_gemm_q8, grid, dim3(256), 0, s, w->codes, w->scales, w->rows, w->cols, xq, xs, ldx, M, out, ldo);
+        return (int)hipGetLastError();
+    }
     if (w->type == GW_Q8_0)
         return gw_k_gemv_q8(w->codes, w->scales, w->rows, w->cols, xq, xs, ldx, M, out, ldo, mode, s);
     if (w->type == GW_Q4_K)

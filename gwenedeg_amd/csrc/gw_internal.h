@@ -21,6 +21,7 @@ enum { GW_F32 = 0, GW_Q8_0 = 8, GW_Q4_K = 12, GW_Q6_K = 14 }; /* ggml type numbe
 #define GW_ATT_T 16   /* positions per KV cache tile */
 #define GW_ATT_P 256  /* positions per attention block */
 #define GW_RMAX 512   /* rows per pass (RQ_BATCH_MAX) */
+#define GW_GEMV_MAX_ROWS 4 /* activation rows up to which a Q8_0 matmul takes the GEMV (else the MFMA GEMM) */
 
 /* A weight matrix on the device (rows x cols). Q8_0: int8 codes, row-major, and fp16 scales (cols / 32 per row),
  * the file's bytes split (34 bytes per 32 weights, as the file). K-quants: the file's blocks, row-major */
@@ -72,6 +73,7 @@ struct RqCtx {
     int8_t *xq, *hq;
     float *xs, *hs;
     int *argmax_d;
+    void *argmax_scr;
     int kmax, ldqkv, pstride;
     size_t part_bytes;
     /* per-pass row metadata: one device block, filled from one pinned host block */
@@ -81,8 +83,23 @@ struct RqCtx {
     float *lg_h;       /* pinned host staging of logits rows */
     size_t lg_h_rows;
     char err[256];
-    double prof[8];
+    int last_nsel;     /* logits rows the last pass left on the device (gw_ctx_argmax) */
+    /* profiling (gw_ctx_profile_enable): HIP events around each kernel class of a pass, summed per class */
+    int prof_on, nev;
+    hipEvent_t *ev;
+    int *ev_class;
+    double prof_s[16];
+    long prof_n[16];
 };
+
+enum { GW_PF_EMBED, GW_PF_NORM, GW_PF_QKV, GW_PF_ROPE, GW_PF_ATT, GW_PF_COMBINE, GW_PF_WO, GW_PF_W13, GW_PF_SWIGLU, GW_PF_W2,
+       GW_PF_CLS, GW_PF_N };
+
+/* the file-format bytes of a matrix (Q8_0 34 per 32 weights, Q4_K 144 / 256, Q6_K 210 / 256) */
+static inline double gw_mat_file_bytes(const GwMat *w) {
+    double n = (double)w->rows * w->cols;
+    return w->type == GW_Q8_0 ? n * 34 / 32 : w->type == GW_Q4_K ? n * 144 / 256 : w->type == GW_Q6_K ? n * 210 / 256 : n * 4;
+}
 
 /* model / device helpers (gw_model.c) */
 int gw_device_init(char *err, size_t errlen);
@@ -103,7 +120,7 @@ int gw_k_attn_combine_quant(const float *part, int pstride, int nh, int hd, cons
                             int ldq, float *att_out, hipStream_t s);
 int gw_k_swiglu_quant(const float *hb, int H, int n, int8_t *hq, float *hs, hipStream_t s);
 int gw_k_quant_rows(const float *x, int n, int ldxf, int rows, int8_t *q, float *sc, int ldq, hipStream_t s);
-int gw_k_argmax(const float *lg, int n, int ld, int rows, int *out, hipStream_t s);
+int gw_k_argmax(const float *lg, int n, int ld, int rows, int *out, void *scratch, hipStream_t s); /* scratch: rows x 512 B */
 int gw_k_q8_unpack(const uint8_t *blocks, size_t nblk, int8_t *codes, uint16_t *scales, hipStream_t s);
 int gw_k_fill_synthetic(uint16_t *kc, uint16_t *vc, size_t n, unsigned long long seed, hipStream_t s);
 

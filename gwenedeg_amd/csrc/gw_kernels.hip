@@ -70,45 +70,21 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-// quantize 32 consecutive values of one group (a thread's own), forward.c:803-836
-__device__ __forceinline__ void quant_group(const float *v, int8_t *q, float *s) {
-    float wmax = 0.0f;
-    #pragma unroll
-    for (int i = 0; i < 32; i++) {
-        float a = fabsf(v[i]);
-        wmax = a > wmax ? a : wmax;
-    }
-    *s = wmax * (1.0f / 127.0f);
-    uint32_t w[8];
-    if (!(wmax > 0.0f)) {
-        #pragma unroll
-        for (int i = 0; i < 8; i++) w[i] = 0;
-    } else {
-        float inv = 127.0f / wmax;
-        #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            uint32_t pk = 0;
-            #pragma unroll
-            for (int b = 0; b < 4; b++) {
-                float x = v[4 * i + b] * inv;
-                int32_t qi = (int32_t)(x + copysignf(0.49999997f, x));
-                pk |= ((uint32_t)qi & 0xffu) << (8 * b);
-            }
-            w[i] = pk;
-        }
-    }
-    uint4 *dst = (uint4 *)q;
-    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
-    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
-}
-
-// rmsnorm scale of n floats in LDS (n % 16 == 0), computed by lanes 0..15 of the calling wave, returned to all lanes
-// of that wave: forward.c:886-901 in the reference's compiled order
+// rmsnorm scale of n floats in LDS (n % 128 == 0), computed by lanes 0..15 of the calling wave, returned to all lanes
+// of that wave: forward.c:886-901 in the reference's compiled order (lane j: an fma chain over x[j], x[j + 16], ...,
+// the tree +8 +4 +2 +1, t = fma(ss, 1/n, 1e-6), 1 / sqrt(t)). The chain's LDS reads are issued 8 at a time
 __device__ __forceinline__ float rms_scale_lds(const float *xs_lds, int n) {
     int lane = threadIdx.x & 63;
     float s = 0.0f;
-    if (lane < 16)
-        for (int j = lane; j < n; j += 16) s = __builtin_fmaf(xs_lds[j], xs_lds[j], s);
+    if (lane < 16) {
+        for (int j = lane; j < n; j += 128) {
+            float a[8];
+            #pragma unroll
+            for (int u = 0; u < 8; u++) a[u] = xs_lds[j + 16 * u];
+            #pragma unroll
+            for (int u = 0; u < 8; u++) s = __builtin_fmaf(a[u], a[u], s);
+        }
+    }
     for (int w = 8; w >= 1; w >>= 1) {
         float o = __shfl_down(s, w);
         s = s + o;
@@ -122,52 +98,111 @@ __device__ __forceinline__ float rms_scale_lds(const float *xs_lds, int n) {
     return __shfl(r, 0);
 }
 
+// quantization with one lane per value: the 32 lanes of each half wave are one group of 32 consecutive values
+// (forward.c:803-836: s = wmax * (1/127), inv = 127 / wmax, q = trunc(v * inv + copysign(0.49999997)), 0 if wmax = 0).
+// The calling wave must have all 64 lanes active
+__device__ __forceinline__ void quant_lane32(float v, int8_t *q, float *s) {
+    float wmax = fabsf(v);
+    #pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) {
+        float t = __shfl_xor(wmax, o);
+        wmax = t > wmax ? t : wmax;
+    }
+    if ((threadIdx.x & 31) == 0) *s = wmax * (1.0f / 127.0f);
+    int32_t qi = 0;
+    if (wmax > 0.0f) {
+        float inv = 127.0f / wmax;
+        float x = v * inv;
+        qi = (int32_t)(x + copysignf(0.49999997f, x));
+    }
+    *q = (int8_t)qi;
+}
+
 // --------------------------------------------------------------------------------------- embedding
 
 // x[b] = row tok[b] of a Q8_0 table (embed_row, forward.c:839-881): (int8) q * fp16 d, one rounding
 __global__ __launch_bounds__(256) void k_embed_q8(float *__restrict__ x, int dim, const uint8_t *__restrict__ codes,
                                                   const uint16_t *__restrict__ scales, const int *__restrict__ tok) {
-    int b = blockIdx.x, t = tok[b];
+    int b = blockIdx.x, t = tok[b], i = blockIdx.y * 256 + threadIdx.x;
     const int8_t *q = (const int8_t *)codes + (size_t)t * dim;
     const uint16_t *s = scales + (size_t)t * (dim / 32);
-    for (int i = threadIdx.x; i < dim; i += blockDim.x) x[(size_t)b * dim + i] = (float)q[i] * h2f(s[i >> 5]);
+    if (i < dim) x[(size_t)b * dim + i] = (float)q[i] * h2f(s[i >> 5]);
 }
 
 // ---------------------------------------------------- residual + rmsnorm + quantize (one row per block)
 
 // row b (= sel[j] if sel, else j): x[b] += d[b] (if d), xn = rmsnorm(x[b], w); xq / xs row j = quantize(xn);
-// hid row j = xn (if hid). xn kept in LDS between the steps (n <= 16384)
-__global__ __launch_bounds__(256) void k_rmsnorm_quant(float *__restrict__ x, const float *__restrict__ d, int n,
-                                                       const float *__restrict__ w, const int *__restrict__ sel,
-                                                       int8_t *__restrict__ xq, float *__restrict__ xs, int ldq,
-                                                       float *__restrict__ hid) {
+// hid row j = xn (if hid). 1024 threads, n % 1024 == 0 and n <= 16384 (up to 4 float4 per thread, all loaded first);
+// the row in LDS for the scale's 16 chains
+#define NORM_T 1024
+__global__ __launch_bounds__(NORM_T) void k_rmsnorm_quant(float *__restrict__ x, const float *__restrict__ d, int n,
+                                                          const float *__restrict__ w, const int *__restrict__ sel,
+                                                          int8_t *__restrict__ xq, float *__restrict__ xs, int ldq,
+                                                          float *__restrict__ hid) {
     extern __shared__ float lds[];
-    int j = blockIdx.x, b = sel ? sel[j] : j;
-    float *xr = x + (size_t)b * n;
-    const float *dr = d ? d + (size_t)b * n : nullptr;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        float v = xr[i];
-        if (dr) {
-            v = v + dr[i];
-            xr[i] = v;
+    __shared__ float rsh;
+    int j = blockIdx.x, b = sel ? sel[j] : j, t = threadIdx.x, n4 = n / 4;
+    float4 *xr = (float4 *)(x + (size_t)b * n);
+    const float4 *dr = d ? (const float4 *)(d + (size_t)b * n) : nullptr;
+    const float4 *w4 = (const float4 *)w;
+    float4 v[4], e[4], wv[4];
+    #pragma unroll
+    for (int k = 0; k < 4; k++) {
+        int i = t + NORM_T * k;
+        if (i < n4) {
+            v[k] = xr[i];
+            wv[k] = w4[i];
+            if (dr) e[k] = dr[i];
         }
-        lds[i] = v;
+    }
+    #pragma unroll
+    for (int k = 0; k < 4; k++) {
+        int i = t + NORM_T * k;
+        if (i < n4) {
+            if (dr) {
+                v[k].x = v[k].x + e[k].x;
+                v[k].y = v[k].y + e[k].y;
+                v[k].z = v[k].z + e[k].z;
+                v[k].w = v[k].w + e[k].w;
+                xr[i] = v[k];
+            }
+            ((float4 *)lds)[i] = v[k];
+        }
     }
     __syncthreads();
-    __shared__ float rsh;
-    if (threadIdx.x < 64) {
+    if (t < 64) {
         float r = rms_scale_lds(lds, n);
-        if (threadIdx.x == 0) rsh = r;
+        if (t == 0) rsh = r;
     }
     __syncthreads();
     float r = rsh;
-    for (int g = threadIdx.x; g < n / 32; g += blockDim.x) {
-        float v[32];
-        #pragma unroll
-        for (int i = 0; i < 32; i++) v[i] = (w[g * 32 + i] * lds[g * 32 + i]) * r;
-        if (hid)
-            for (int i = 0; i < 32; i++) hid[(size_t)j * n + g * 32 + i] = v[i];
-        quant_group(v, xq + (size_t)j * ldq + g * 32, xs + (size_t)j * (ldq / 32) + g);
+    // quantize: element e = 4 i + c of float4 i = t + 1024 k; its group's 32 values are 8 consecutive threads' float4s:
+    // the group max over those 8 lanes, one byte per value
+    #pragma unroll
+    for (int k = 0; k < 4; k++) {
+        int i = t + NORM_T * k;
+        if (i < n4) {
+            float o[4] = { (wv[k].x * v[k].x) * r, (wv[k].y * v[k].y) * r, (wv[k].z * v[k].z) * r, (wv[k].w * v[k].w) * r };
+            if (hid) ((float4 *)(hid + (size_t)j * n))[i] = make_float4(o[0], o[1], o[2], o[3]);
+            float wm = fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3])));
+            #pragma unroll
+            for (int sft = 4; sft >= 1; sft >>= 1) {
+                float tt = __shfl_xor(wm, sft);
+                wm = tt > wm ? tt : wm;
+            }
+            if ((t & 7) == 0) xs[(size_t)j * (ldq / 32) + (i >> 3)] = wm * (1.0f / 127.0f);
+            uint32_t pk = 0;
+            if (wm > 0.0f) {
+                float inv = 127.0f / wm;
+                #pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    float y = o[c] * inv;
+                    int32_t qi = (int32_t)(y + copysignf(0.49999997f, y));
+                    pk |= ((uint32_t)qi & 0xffu) << (8 * c);
+                }
+            }
+            *(uint32_t *)(xq + (size_t)j * ldq + 4 * i) = pk;
+        }
     }
 }
 
@@ -175,15 +210,15 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant(float *__restrict__ x, co
 
 // out[m * ldo + row] = W row . X row m for M activation rows, R weight rows per block. Each thread takes half-groups
 // (16 codes) j = t, t + 256, ...: an exact int32 sum by 4 v_dot4 (sdot4), the lane pair's sums added (exact), the even
-// lane's product (ws * xs) * (float) isum into LDS; then one lane per (m, row) folds the groups in order. W: row-major
-// int8 codes (K per row) + fp16 scales (K / 32 per row); X: int8 rows at xq + m * ldx, fp32 scales at xs + m * ldx / 32.
-// mode 1: out = resid + val (the residual add, resid may alias out)
+// lane's product (ws * xs) * (float) isum into LDS; then one lane per (m, row) folds the groups in order (LDS read 4
+// at a time). W: row-major int8 codes (K per row) + fp16 scales (K / 32 per row); X: int8 rows at xq + m * ldx, fp32
+// scales at xs + m * ldx / 32. mode 1: out = out + val (a residual add)
 template <int M, int R>
 __global__ __launch_bounds__(256) void k_gemv_q8(const int8_t *__restrict__ W, const uint16_t *__restrict__ WS, int nrows,
                                                  int K, const int8_t *__restrict__ xq, const float *__restrict__ xs, int ldx,
                                                  float *out, int ldo, int mode) {
     extern __shared__ float P[];
-    const int G = K >> 5, H = K >> 4, PS = G + 1;
+    const int G = K >> 5, H = K >> 4, PS = G + 4;
     const int row0 = blockIdx.x * R, t = threadIdx.x;
     for (int j = t; j < H; j += 256) {
         int4 xv[M];
@@ -221,9 +256,21 @@ __global__ __launch_bounds__(256) void k_gemv_q8(const int8_t *__restrict__ W, c
     if (t < M * R) {
         int m = t / R, r = t % R, row = row0 + r;
         if (row < nrows) {
-            const float *p = P + t * PS;
+            const float4 *p = (const float4 *)(P + t * PS);
             float v = 0.0f;
-            for (int g = 0; g < G; g++) v = v + p[g];
+            for (int g4 = 0; g4 < G / 4; g4 += 4) {
+                float4 a[4];
+                #pragma unroll
+                for (int u = 0; u < 4; u++) a[u] = p[g4 + u < G / 4 ? g4 + u : G / 4 - 1];
+                #pragma unroll
+                for (int u = 0; u < 4; u++)
+                    if (g4 + u < G / 4) {
+                        v = v + a[u].x;
+                        v = v + a[u].y;
+                        v = v + a[u].z;
+                        v = v + a[u].w;
+                    }
+            }
             float *o = out + (size_t)m * ldo + row;
             *o = mode == 1 ? *o + v : v;
         }
@@ -278,68 +325,107 @@ __global__ __launch_bounds__(64) void k_qknorm_rope_store(float *__restrict__ qk
 
 // ----------------------------------------------------------------------------------------- attention
 
-// One block per item (first row r0, rows nr of one sequence at consecutive positions, kv head g, key block kb): the
-// partial result of block kb (forward.c:1346-1403 with ml) for each of the nr * kv_mul query vectors that reach it:
-// part[(row * nh + h) * pstride + kb * (hd + 2)] = o[hd] (unnormalized), m, l. Query vector v = (row r0 + v / kv_mul,
-// head g * kv_mul + v % kv_mul) over positions 0..pos(row). hd <= 128, nr * kv_mul <= 32.
-#define ATT_NQ 32
+// One block of 1024 threads per item (first row r0, rows nr of one sequence at consecutive positions, kv head g, key
+// block kb): the partial result of block kb (forward.c:1346-1403 with ml) for each of the nq = nr * kv_mul query vectors
+// that reach it: part[(row * nh + h) * pstride + kb * (hd + 2)] = o[hd] (unnormalized), m, l. Vector v = (row
+// r0 + v / kv_mul, head g * kv_mul + v % kv_mul) over positions 0..pos(row). Steps:
+//   stage: the block's K and V tiles (16-byte loads, all issued before any LDS write) and the query vectors into LDS;
+//     K rows padded by 32 bytes per 32 dims, so the 4 chunks of a position read different banks
+//   scores: lane (position p, chunk c): the fma chain over dims 32c .. 32c + 31 of every vector; the 4 chunks of a
+//     position are neighbouring lanes, added in order (a = c0 + c1 + c2 + c3, left to right), times scale
+//   softmax: one wave per vector: m = max, e = exp_att(s - m), l = 16 lane chains + the tree
+//   o: lane (vector, dim pair): the fma chains over the positions in order
+// hd <= 128 (hd % 32 == 0), nq <= 16.
+#define ATT_NQ 16
 #define ATT_HDMAX 128
-__global__ __launch_bounds__(256) void k_attn_part(const int4 *__restrict__ items, const float *__restrict__ qkv, int ldqkv,
-                                                   int nh, int nkv, int hd, float scale, const int *__restrict__ pos,
-                                                   uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc,
-                                                   float *__restrict__ part, int pstride) {
-    __shared__ float qs[ATT_NQ * ATT_HDMAX];
+#define ATT_TH 1024
+#define ATT_KROW 1056                   // LDS bytes of 32 K dims of a tile (32 x 32 + 32 padding)
+#define ATT_KTILE (4 * ATT_KROW)        // LDS bytes of a K tile (hd <= 128)
+#define ATT_VTILE (32 * ATT_HDMAX)      // LDS bytes of a V tile
+#define ATT_QS 132                      // LDS floats per query vector (4 chunks of 33)
+__global__ __launch_bounds__(ATT_TH) void k_attn_part(const int4 *__restrict__ items, const float *__restrict__ qkv, int ldqkv,
+                                                      int nh, int nkv, int hd, float scale, const int *__restrict__ pos,
+                                                      uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc,
+                                                      float *__restrict__ part, int pstride) {
+    __shared__ __align__(16) uint8_t ks[16 * ATT_KTILE];
+    __shared__ __align__(16) uint8_t vs[16 * ATT_VTILE];
+    __shared__ float qs[ATT_NQ * ATT_QS];
     __shared__ float S[ATT_NQ][ATT_P];
     __shared__ int np[ATT_NQ];
     int4 it = items[blockIdx.x];
     int r0 = it.x, nr = it.y, g = it.z, kb = it.w, kv_mul = nh / nkv, nq = nr * kv_mul, t = threadIdx.x;
-    int t0 = kb * ATT_P;
-    const uint16_t *K = kc[r0] + ((size_t)kb * nkv + g) * ATT_P * hd; // this (block, head): 16 tiles of 16 x hd
-    const uint16_t *V = vc[r0] + ((size_t)kb * nkv + g) * ATT_P * hd;
-    for (int e = t; e < nq * hd; e += 256) {
+    const int TB = 32 * hd, nchk = hd / 32;
+    const uint8_t *K = (const uint8_t *)(kc[r0] + ((size_t)kb * nkv + g) * ATT_P * hd);
+    const uint8_t *V = (const uint8_t *)(vc[r0] + ((size_t)kb * nkv + g) * ATT_P * hd);
+    int nmx = pos[r0 + nr - 1] + 1 - kb * ATT_P;
+    nmx = nmx < ATT_P ? nmx : ATT_P;
+    int nbytes = (nmx + ATT_T - 1) / ATT_T * TB; // the tiles holding positions < nmx
+    uint4 kr[4], vr[4];
+    #pragma unroll
+    for (int k = 0; k < 4; k++) {
+        int o = (t + ATT_TH * k) * 16;
+        if (o < nbytes) {
+            kr[k] = *(const uint4 *)(K + o);
+            vr[k] = *(const uint4 *)(V + o);
+        }
+    }
+    for (int e = t; e < nq * hd; e += ATT_TH) {
         int v = e / hd, i = e % hd;
-        qs[v * hd + i] = qkv[(size_t)(r0 + v / kv_mul) * ldqkv + (size_t)(g * kv_mul + v % kv_mul) * hd + i];
+        qs[v * ATT_QS + (i >> 5) * 33 + (i & 31)] = qkv[(size_t)(r0 + v / kv_mul) * ldqkv + (size_t)(g * kv_mul + v % kv_mul) * hd + i];
     }
     if (t < nq) {
-        int n = pos[r0 + t / kv_mul] + 1 - t0;
+        int n = pos[r0 + t / kv_mul] + 1 - kb * ATT_P;
         np[t] = n < 0 ? 0 : n < ATT_P ? n : ATT_P;
     }
-    __syncthreads();
-    int nmax = 0;
-    for (int v = 0; v < nq; v++) nmax = np[v] > nmax ? np[v] : nmax;
-    // scores: thread t = position t0 + t
-    if (t < nmax) {
-        const uint16_t *kt = K + (size_t)(t / ATT_T) * ATT_T * hd + (t % ATT_T);
-        float a[ATT_NQ];
-        for (int c0 = 0; c0 < hd; c0 += 32) {
-            float c[ATT_NQ];
-            #pragma unroll
-            for (int v = 0; v < ATT_NQ; v++) c[v] = 0.0f;
-            for (int i = c0; i < c0 + 32; i++) {
-                float k = h2f(kt[(size_t)i * ATT_T]);
-                #pragma unroll
-                for (int v = 0; v < ATT_NQ; v++)
-                    if (v < nq) c[v] = __builtin_fmaf(qs[v * hd + i], k, c[v]);
-            }
-            #pragma unroll
-            for (int v = 0; v < ATT_NQ; v++) a[v] = c0 > 0 ? a[v] + c[v] : c[v];
+    #pragma unroll
+    for (int k = 0; k < 4; k++) {
+        int o = (t + ATT_TH * k) * 16;
+        if (o < nbytes) {
+            int tile = o / TB, w = o % TB;
+            *(uint4 *)(ks + tile * ATT_KTILE + (w >> 10) * ATT_KROW + (w & 1023)) = kr[k];
+            *(uint4 *)(vs + o) = vr[k]; // (V: position p's row at p hd 2 bytes)
         }
-        #pragma unroll
-        for (int v = 0; v < ATT_NQ; v++)
-            if (v < nq) S[v][t] = a[v] * scale;
     }
     __syncthreads();
-    // softmax per vector: wave w takes vectors w, w + 4, ...
+    // scores
+    {
+        int p = t >> 2, c = t & 3;
+        const uint8_t *kt = ks + (p / ATT_T) * ATT_KTILE + c * ATT_KROW + (p % ATT_T) * 2;
+        const float *qc = qs + c * 33;
+        float acc[ATT_NQ];
+        #pragma unroll
+        for (int v = 0; v < ATT_NQ; v++) acc[v] = 0.0f;
+        if (p < nmx && c < nchk) {
+            for (int i = 0; i < 32; i++) {
+                float k = h2f(*(const uint16_t *)(kt + i * 32));
+                #pragma unroll
+                for (int v = 0; v < ATT_NQ; v++)
+                    if (v < nq) acc[v] = __builtin_fmaf(qc[v * ATT_QS + i], k, acc[v]);
+            }
+        }
+        #pragma unroll
+        for (int v = 0; v < ATT_NQ; v++) {
+            if (v < nq) {
+                float c1 = __shfl_down(acc[v], 1), c2 = __shfl_down(acc[v], 2), c3 = __shfl_down(acc[v], 3);
+                float a = acc[v];
+                if (nchk > 1) a = a + c1;
+                if (nchk > 2) a = a + c2;
+                if (nchk > 3) a = a + c3;
+                if (c == 0 && p < nmx) S[v][p] = a * scale;
+            }
+        }
+    }
+    __syncthreads();
+    // softmax: wave v takes vector v
     int wave = t >> 6, lane = t & 63;
-    for (int v = wave; v < nq; v += 4) {
-        int n = np[v];
-        if (n <= 0) continue;
+    if (wave < nq && np[wave] > 0) {
+        int v = wave, n = np[v];
         float m = -3.402823466e38f;
         for (int p = lane; p < n; p += 64) m = fmaxf(m, S[v][p]);
         m = wave_max(m);
         for (int p = lane; p < n; p += 64) S[v][p] = exp_att(S[v][p] - m);
-        __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
         float s = 0.0f;
         if (lane < 16)
             for (int p = lane; p < n; p += 16) s = s + S[v][p];
@@ -355,116 +441,144 @@ __global__ __launch_bounds__(256) void k_attn_part(const int4 *__restrict__ item
         }
     }
     __syncthreads();
-    // o = fma chain over the positions in order: thread = (dim pair d2, vector group vg)
-    int d2 = t & 63, vg = t >> 6;
-    for (int i0 = 2 * d2; i0 < hd; i0 += 128) {
-        float o0[ATT_NQ / 4], o1[ATT_NQ / 4];
-        #pragma unroll
-        for (int k = 0; k < ATT_NQ / 4; k++) o0[k] = o1[k] = 0.0f;
-        for (int p = 0; p < nmax; p++) {
-            uint32_t vv = *(const uint32_t *)(V + (size_t)(p / ATT_T) * ATT_T * hd + (size_t)(p % ATT_T) * hd + i0);
-            float v0 = h2f((uint16_t)(vv & 0xffff)), v1 = h2f((uint16_t)(vv >> 16));
-            #pragma unroll
-            for (int k = 0; k < ATT_NQ / 4; k++) {
-                int v = vg + 4 * k;
-                if (v < nq && p < np[v]) {
-                    float e = S[v][p];
-                    o0[k] = __builtin_fmaf(e, v0, o0[k]);
-                    o1[k] = __builtin_fmaf(e, v1, o1[k]);
+    // o: lane (vector v = wave, dim pair d2)
+    {
+        int v = wave, d2 = lane, i0 = 2 * d2;
+        if (v < nq && i0 < hd && np[v] > 0) {
+            int n = np[v];
+            float o0 = 0.0f, o1 = 0.0f;
+            const uint8_t *vb = vs + i0 * 2;
+            for (int p0 = 0; p0 < n; p0 += 8) {
+                float v0[8], v1[8], e[8];
+                #pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    int p = p0 + u < n ? p0 + u : n - 1;
+                    uint32_t vv = *(const uint32_t *)(vb + p * hd * 2);
+                    v0[u] = h2f((uint16_t)(vv & 0xffff));
+                    v1[u] = h2f((uint16_t)(vv >> 16));
+                    e[u] = S[v][p];
                 }
+                #pragma unroll
+                for (int u = 0; u < 8; u++)
+                    if (p0 + u < n) {
+                        o0 = __builtin_fmaf(e[u], v0[u], o0);
+                        o1 = __builtin_fmaf(e[u], v1[u], o1);
+                    }
             }
-        }
-        #pragma unroll
-        for (int k = 0; k < ATT_NQ / 4; k++) {
-            int v = vg + 4 * k;
-            if (v < nq && np[v] > 0) {
-                int row = r0 + v / kv_mul, h = g * kv_mul + v % kv_mul;
-                float *o = part + ((size_t)row * nh + h) * pstride + (size_t)kb * (hd + 2);
-                o[i0] = o0[k];
-                o[i0 + 1] = o1[k];
-            }
+            int row = r0 + v / kv_mul, h = g * kv_mul + v % kv_mul;
+            float *o = part + ((size_t)row * nh + h) * pstride + (size_t)kb * (hd + 2);
+            o[i0] = o0;
+            o[i0 + 1] = o1;
         }
     }
 }
 
 // one block per row: the attention of each head from its block partials in block order (att_combine,
-// forward.c:1405-1431), then the row's quantization for wo (aq row b, all_heads = nh * hd values; groups inside heads)
-__global__ __launch_bounds__(256) void k_attn_combine_quant(const float *__restrict__ part, int pstride, int nh, int hd,
+// forward.c:1405-1431), then the row's quantization for wo (aq row b, all_heads = nh * hd values, a multiple of 256).
+// Per head the coefficients c_b = exp_att(m_b - M) and 1 / L first (LDS), then the outputs
+#define COMB_T 1024
+__global__ __launch_bounds__(COMB_T) void k_attn_combine_quant(const float *__restrict__ part, int pstride, int nh, int hd,
                                                             const int *__restrict__ pos, int8_t *__restrict__ aq,
                                                             float *__restrict__ as, int ldq, float *__restrict__ att_out) {
-    extern __shared__ float o_lds[];
-    int b = blockIdx.x, nb = (pos[b] + 1 + ATT_P - 1) / ATT_P, st = hd + 2;
-    for (int e = threadIdx.x; e < nh * hd; e += blockDim.x) {
-        int h = e / hd, i = e % hd;
+    extern __shared__ float cl[]; // [nh][nb] coefficients, then [nh] inverses
+    int b = blockIdx.x, nb = (pos[b] + 1 + ATT_P - 1) / ATT_P, st = hd + 2, t = threadIdx.x;
+    float *inv = cl + (size_t)nh * nb;
+    for (int h = t; h < nh; h += COMB_T) {
         const float *pb = part + ((size_t)b * nh + h) * pstride;
-        float out;
         if (nb == 1) {
-            float inv = 1.0f / pb[hd + 1];
-            out = pb[i] * inv;
-        } else {
-            float M = pb[hd];
-            for (int k = 1; k < nb; k++) M = pb[(size_t)k * st + hd] > M ? pb[(size_t)k * st + hd] : M;
-            float L = 0.0f, acc = 0.0f;
-            for (int k = 0; k < nb; k++) {
-                const float *o = pb + (size_t)k * st;
-                float c = exp_att(o[hd] - M);
-                L = __builtin_fmaf(c, o[hd + 1], L);
-                acc = __builtin_fmaf(c, o[i], acc);
-            }
-            float inv = 1.0f / L;
-            out = acc * inv;
+            inv[h] = 1.0f / pb[hd + 1];
+            continue;
         }
-        o_lds[e] = out;
-        if (att_out) att_out[(size_t)b * nh * hd + e] = out;
+        float M = pb[hd];
+        for (int k = 1; k < nb; k++) M = pb[(size_t)k * st + hd] > M ? pb[(size_t)k * st + hd] : M;
+        float L = 0.0f;
+        for (int k = 0; k < nb; k++) {
+            float c = exp_att(pb[(size_t)k * st + hd] - M);
+            cl[h * nb + k] = c;
+            L = __builtin_fmaf(c, pb[(size_t)k * st + hd + 1], L);
+        }
+        inv[h] = 1.0f / L;
+    }
+    // (the single-block case needs no coefficients: its loads go first, before the barrier)
+    float o1[4];
+    if (nb == 1) {
+        #pragma unroll
+        for (int k = 0; k < 4; k++) {
+            int e = t + COMB_T * k;
+            if (e < nh * hd) o1[k] = part[((size_t)b * nh + e / hd) * pstride + e % hd];
+        }
     }
     __syncthreads();
-    for (int g = threadIdx.x; g < nh * hd / 32; g += blockDim.x)
-        quant_group(o_lds + g * 32, aq + (size_t)b * ldq + g * 32, as + (size_t)b * (ldq / 32) + g);
+    for (int k = 0; k < 4; k++) {
+        int e = t + COMB_T * k;
+        if (e >= nh * hd) break;
+        int h = e / hd, i = e % hd;
+        const float *pb = part + ((size_t)b * nh + h) * pstride + i;
+        float out;
+        if (nb == 1) {
+            out = o1[k] * inv[h];
+        } else {
+            float acc = 0.0f;
+            int kb = 0;
+            for (; kb + 8 <= nb; kb += 8) {
+                float o[8];
+                #pragma unroll
+                for (int u = 0; u < 8; u++) o[u] = pb[(size_t)(kb + u) * st];
+                #pragma unroll
+                for (int u = 0; u < 8; u++) acc = __builtin_fmaf(cl[h * nb + kb + u], o[u], acc);
+            }
+            for (; kb < nb; kb++) acc = __builtin_fmaf(cl[h * nb + kb], pb[(size_t)kb * st], acc);
+            out = acc * inv[h];
+        }
+        if (att_out) att_out[(size_t)b * nh * hd + e] = out;
+        quant_lane32(out, aq + (size_t)b * ldq + e, as + (size_t)b * (ldq / 32) + (e >> 5));
+    }
 }
 
 // ------------------------------------------------------------------------------------ SwiGLU + quantize
 
-// row b of hb = [h (H) | h2 (H)]: v = (h * h2) * (1 / (1 + exp(min(-h, 80)))), quantized into hq / hs row b
+// row blockIdx.x of hb = [h (H) | h2 (H)], values 256 blockIdx.y .. + 255: v = (h * h2) * (1 / (1 + exp(min(-h, 80)))),
+// quantized into hq / hs (one lane per value)
 __global__ __launch_bounds__(256) void k_swiglu_quant(const float *__restrict__ hb, int H, int8_t *__restrict__ hq,
                                                       float *__restrict__ hs) {
-    int b = blockIdx.x;
-    const float *h1 = hb + (size_t)b * 2 * H, *h2 = h1 + H;
-    for (int g = threadIdx.x; g < H / 32; g += blockDim.x) {
-        float v[32];
-        #pragma unroll
-        for (int i = 0; i < 32; i++) {
-            float h = h1[g * 32 + i];
-            float e = silu_exp(-h);
-            float r = 1.0f / (1.0f + e);
-            v[i] = (h * h2[g * 32 + i]) * r;
-        }
-        quant_group(v, hq + (size_t)b * H + g * 32, hs + (size_t)b * (H / 32) + g);
-    }
+    int b = blockIdx.x, e = blockIdx.y * 256 + threadIdx.x;
+    const float *h1 = hb + (size_t)b * 2 * H;
+    float h = h1[e];
+    float ex = silu_exp(-h);
+    float r = 1.0f / (1.0f + ex);
+    float v = (h * h1[H + e]) * r;
+    quant_lane32(v, hq + (size_t)b * H + e, hs + (size_t)b * (H / 32) + (e >> 5));
 }
 
 // ---------------------------------------------------------------------------------------- quantize rows
 
 __global__ __launch_bounds__(256) void k_quant_rows(const float *__restrict__ x, int n, int ldxf, int8_t *__restrict__ q,
                                                     float *__restrict__ s, int ldq) {
-    int b = blockIdx.x;
-    for (int g = threadIdx.x; g < n / 32; g += blockDim.x) {
-        float v[32];
-        #pragma unroll
-        for (int i = 0; i < 32; i++) v[i] = x[(size_t)b * ldxf + g * 32 + i];
-        quant_group(v, q + (size_t)b * ldq + g * 32, s + (size_t)b * (ldq / 32) + g);
+    int b = blockIdx.x, e = blockIdx.y * 256 + threadIdx.x;
+    float v = e < n ? x[(size_t)b * ldxf + e] : 0.0f;
+    int8_t qq;
+    float ss;
+    quant_lane32(v, &qq, &ss);
+    if (e < n) {
+        q[(size_t)b * ldq + e] = qq;
+        if ((e & 31) == 0) s[(size_t)b * (ldq / 32) + (e >> 5)] = ss;
     }
 }
 
 // ----------------------------------------------------------------------------------------------- argmax
 
-// per row: the first index holding the maximum (sampler.c:40-60)
-__global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ lg, int n, int ld, int *__restrict__ out) {
+// per row: the first index holding the maximum (sampler.c:40-60), in two steps: ARGMAX_CH chunks of a row, each its
+// (max, first index) into scratch, then one wave per row combines them in chunk order
+#define ARGMAX_CH 64
+__global__ __launch_bounds__(256) void k_argmax_part(const float *__restrict__ lg, int n, int ld, float2 *__restrict__ scr) {
     __shared__ float smax[4];
     __shared__ int sidx[4];
-    const float *r = lg + (size_t)blockIdx.x * ld;
+    int row = blockIdx.x, ch = blockIdx.y, len = (n + ARGMAX_CH - 1) / ARGMAX_CH, i0 = ch * len;
+    int i1 = i0 + len < n ? i0 + len : n;
+    const float *r = lg + (size_t)row * ld;
     float m = -3.402823466e38f;
     int idx = 0x7fffffff;
-    for (int i = threadIdx.x; i < n; i += 256) {
+    for (int i = i0 + threadIdx.x; i < i1; i += 256) {
         float v = r[i];
         if (v > m) { m = v; idx = i; }
     }
@@ -479,8 +593,21 @@ __global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ lg, in
     if (threadIdx.x == 0) {
         for (int k = 1; k < 4; k++)
             if (smax[k] > m || (smax[k] == m && sidx[k] < idx)) { m = smax[k]; idx = sidx[k]; }
-        out[blockIdx.x] = idx;
+        scr[(size_t)row * ARGMAX_CH + ch] = make_float2(m, __int_as_float(idx));
     }
+}
+
+__global__ __launch_bounds__(64) void k_argmax_final(const float2 *__restrict__ scr, int *__restrict__ out) {
+    int row = blockIdx.x, l = threadIdx.x;
+    float2 p = scr[(size_t)row * ARGMAX_CH + l];
+    float m = p.x;
+    int idx = __float_as_int(p.y);
+    for (int o = 32; o >= 1; o >>= 1) {
+        float m2 = __shfl_xor(m, o);
+        int i2 = __shfl_xor(idx, o);
+        if (m2 > m || (m2 == m && i2 < idx)) { m = m2; idx = i2; }
+    }
+    if (l == 0) out[row] = idx;
 }
 
 // ------------------------------------------------------------------------------------------ launchers
@@ -488,13 +615,13 @@ __global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ lg, in
 extern "C" {
 
 int gw_k_embed_q8(float *x, int dim, const uint8_t *codes, const uint16_t *scales, const int *tok, int n, hipStream_t s) {
-    hipLaunchKernelGGL(k_embed_q8, dim3(n), dim3(256), 0, s, x, dim, codes, scales, tok);
+    hipLaunchKernelGGL(k_embed_q8, dim3(n, (dim + 255) / 256), dim3(256), 0, s, x, dim, codes, scales, tok);
     return (int)hipGetLastError();
 }
 
 int gw_k_rmsnorm_quant(float *x, const float *d, int dim, const float *w, const int *sel, int n, int8_t *xq, float *xs, int ldq,
                        float *hid, hipStream_t s) {
-    hipLaunchKernelGGL(k_rmsnorm_quant, dim3(n), dim3(256), (size_t)dim * sizeof(float), s, x, d, dim, w, sel, xq, xs, ldq, hid);
+    hipLaunchKernelGGL(k_rmsnorm_quant, dim3(n), dim3(NORM_T), (size_t)dim * sizeof(float), s, x, d, dim, w, sel, xq, xs, ldq, hid);
     return (int)hipGetLastError();
 }
 
@@ -502,7 +629,7 @@ int gw_k_gemv_q8(const int8_t *W, const uint16_t *WS, int nrows, int K, const in
                  float *out, int ldo, int mode, hipStream_t s) {
     // M activation rows in launches of up to 4
     const int R = 4;
-    size_t lds = (size_t)4 * R * (K / 32 + 1) * sizeof(float);
+    size_t lds = (size_t)4 * R * (K / 32 + 4) * sizeof(float);
     for (int m0 = 0; m0 < M; m0 += 4) {
         int mm = M - m0 < 4 ? M - m0 : 4;
         dim3 grid((nrows + R - 1) / R);
@@ -527,29 +654,31 @@ int gw_k_qknorm_rope_store(float *qkv, int ldqkv, int n, int nh, int nkv, int hd
 
 int gw_k_attn_part(const void *items, int nitems, const float *qkv, int ldqkv, int nh, int nkv, int hd, float scale,
                    const int *pos, uint16_t *const *kc, uint16_t *const *vc, float *part, int pstride, hipStream_t s) {
-    hipLaunchKernelGGL(k_attn_part, dim3(nitems), dim3(256), 0, s, (const int4 *)items, qkv, ldqkv, nh, nkv, hd, scale, pos, kc, vc, part, pstride);
+    hipLaunchKernelGGL(k_attn_part, dim3(nitems), dim3(ATT_TH), 0, s, (const int4 *)items, qkv, ldqkv, nh, nkv, hd, scale, pos, kc, vc, part, pstride);
     return (int)hipGetLastError();
 }
 
 int gw_k_attn_combine_quant(const float *part, int pstride, int nh, int hd, const int *pos, int n, int8_t *aq, float *as,
                             int ldq, float *att_out, hipStream_t s) {
-    hipLaunchKernelGGL(k_attn_combine_quant, dim3(n), dim3(256), (size_t)nh * hd * sizeof(float), s, part, pstride, nh, hd, pos,
-                       aq, as, ldq, att_out);
+    (void)hd;
+    hipLaunchKernelGGL(k_attn_combine_quant, dim3(n), dim3(COMB_T), (size_t)nh * (pstride / (hd + 2) + 1) * sizeof(float), s, part,
+                       pstride, nh, hd, pos, aq, as, ldq, att_out);
     return (int)hipGetLastError();
 }
 
 int gw_k_swiglu_quant(const float *hb, int H, int n, int8_t *hq, float *hs, hipStream_t s) {
-    hipLaunchKernelGGL(k_swiglu_quant, dim3(n), dim3(256), 0, s, hb, H, hq, hs);
+    hipLaunchKernelGGL(k_swiglu_quant, dim3(n, H / 256), dim3(256), 0, s, hb, H, hq, hs);
     return (int)hipGetLastError();
 }
 
 int gw_k_quant_rows(const float *x, int n, int ldxf, int rows, int8_t *q, float *sc, int ldq, hipStream_t s) {
-    hipLaunchKernelGGL(k_quant_rows, dim3(rows), dim3(256), 0, s, x, n, ldxf, q, sc, ldq);
+    hipLaunchKernelGGL(k_quant_rows, dim3(rows, (n + 255) / 256), dim3(256), 0, s, x, n, ldxf, q, sc, ldq);
     return (int)hipGetLastError();
 }
 
-int gw_k_argmax(const float *lg, int n, int ld, int rows, int *out, hipStream_t s) {
-    hipLaunchKernelGGL(k_argmax, dim3(rows), dim3(256), 0, s, lg, n, ld, out);
+int gw_k_argmax(const float *lg, int n, int ld, int rows, int *out, void *scratch, hipStream_t s) {
+    hipLaunchKernelGGL(k_argmax_part, dim3(rows, ARGMAX_CH), dim3(256), 0, s, lg, n, ld, (float2 *)scratch);
+    hipLaunchKernelGGL(k_argmax_final, dim3(rows), dim3(64), 0, s, (const float2 *)scratch, out);
     return (int)hipGetLastError();
 }
 

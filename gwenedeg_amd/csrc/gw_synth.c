@@ -317,6 +317,7 @@ int gw_synth_gguf(const char *path, const GwSynthCfg *c, unsigned long long seed
         }
         size_t rb = gw_synth_row_bytes(T[i].type, T[i].cols), chunk_rows = (size_t)(256u << 20) / rb;
         if (chunk_rows < 1) chunk_rows = 1;
+        if (chunk_rows > (size_t)T[i].rows) chunk_rows = (size_t)T[i].rows;
         uint8_t *out = malloc(chunk_rows * rb);
         if (!out) { rc = -2; break; }
         for (int r0 = 0; r0 < T[i].rows && !rc; r0 += (int)chunk_rows) {

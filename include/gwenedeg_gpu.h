@@ -142,6 +142,24 @@ unsigned long long rq_logits_hash(const float *logits, int n);
  * RQ_ERR_STATE if the last pass produced no logits */
 int gw_ctx_argmax(RqCtx *c, int *tokens, int n);
 
+/* rq_decode (runq.h:346) followed by the greedy choice on the device: *next = the first maximum of the row's logits,
+ * which stay on the device (no vocab-size copy per step; gw_ctx_argmax can read them again). The decode loop of a
+ * greedy generation (rq_gen_step + sample_argmax, chat.c:348, sampler.c:40) without the logits transfer */
+int gw_decode_argmax(RqCtx *c, RqSeq *s, int token, int *next);
+
+/* Per-kernel-class device time (the GPU counterpart of the reference's -DRUNQ_PROFILE phases, forward.c:13-24):
+ * gw_ctx_profile_enable(c, 1) resets the counters and brackets each kernel class of every later pass with HIP events
+ * on the context's stream; rq_ctx_profile then returns the classes' names and summed seconds, and
+ * gw_ctx_profile_launches the number of intervals of class i (its launches). 0 turns it off */
+int gw_ctx_profile_enable(RqCtx *c, int on);
+
+/* The weight matmuls of one decode step (per layer q / k / v, wo, w1 / w3, w2; then the classifier) on one activation
+ * row, back to back, reps times, timed with HIP events on the context's stream: *seconds per sweep, *bytes = their
+ * file-format weight bytes (the algorithmic bytes of a decode step's weight streaming), *launches per sweep. The
+ * counterpart of the reference's pass timing (rq_pass_times, runq.h:196-199) for the GEMV alone */
+int gw_ctx_gemv_sweep(RqCtx *c, int reps, double *seconds, double *bytes, int *launches);
+long gw_ctx_profile_launches(const RqCtx *c, int cls);
+
 /* The isolated Q8_0 operator (the reference's kernels_avx512.h q8p_pack_blocks :113, q8p_gemv_rows :286 and
  * q8p_gemm_item :235, and forward.c's quantize :803), on device pointers, on the given HIP stream (NULL: the null
  * stream); asynchronous. Return RQ_OK or RQ_ERR_ARG (shapes: N % 16 == 0, K % 32 == 0) / RQ_ERR_STATE (launch failed).
