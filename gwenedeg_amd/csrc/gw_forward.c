@@ -335,11 +335,12 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
         nbmax = nb > nbmax ? nb : nbmax;
     }
     if ((rc = ctx_part(c, n, nbmax)) != RQ_OK) return rc;
-    int nrb = 0;
+    int nrb = 0, nq_max = 1;
     for (int b = 0; b < n;) {
         int e = b + 1;
         while (e < n && e - b < rb && P->seq[e] == P->seq[b] && P->pos[e] == P->pos[e - 1] + 1) e++;
         nitems += nkv * ((P->pos[e - 1] + 1 + GW_ATT_P - 1) / GW_ATT_P);
+        nq_max = (e - b) * kv_mul > nq_max ? (e - b) * kv_mul : nq_max;
         nrb++;
         b = e;
     }
@@ -389,7 +390,7 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
         KCHK(gw_k_qknorm_rope_store(c->qkv, c->ldqkv, n, nh, nkv, hd, y->q_norm, y->k_norm, m->rope, pos_d,
                                     kc_d + (size_t)l * n, vc_d + (size_t)l * n, s));
         pf_mark(c, GW_PF_ATT);
-        KCHK(gw_k_attn_part(items_d, nitems, c->qkv, c->ldqkv, nh, nkv, hd, m->att_scale, pos_d, kc_d + (size_t)l * n,
+        KCHK(gw_k_attn_part(items_d, nitems, nq_max, c->qkv, c->ldqkv, nh, nkv, hd, m->att_scale, pos_d, kc_d + (size_t)l * n,
                             vc_d + (size_t)l * n, c->part, c->pstride, s));
         pf_mark(c, GW_PF_COMBINE);
         KCHK(gw_k_attn_combine_quant(c->part, c->pstride, nh, hd, pos_d, n, c->xq, c->xs, K, NULL, s));

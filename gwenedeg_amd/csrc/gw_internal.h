@@ -114,7 +114,7 @@ int gw_k_gemv_q8(const int8_t *W, const uint16_t *WS, int nrows, int K, const in
                  float *out, int ldo, int mode, hipStream_t s);
 int gw_k_qknorm_rope_store(float *qkv, int ldqkv, int n, int nh, int nkv, int hd, const float *qn, const float *kn,
                            const float *rope, const int *pos, uint16_t *const *kc, uint16_t *const *vc, hipStream_t s);
-int gw_k_attn_part(const void *items, int nitems, const float *qkv, int ldqkv, int nh, int nkv, int hd, float scale,
+int gw_k_attn_part(const void *items, int nitems, int nq_max, const float *qkv, int ldqkv, int nh, int nkv, int hd, float scale,
                    const int *pos, uint16_t *const *kc, uint16_t *const *vc, float *part, int pstride, hipStream_t s);
 int gw_k_attn_combine_quant(const float *part, int pstride, int nh, int hd, const int *pos, int n, int8_t *aq, float *as,
                             int ldq, float *att_out, hipStream_t s);

@@ -341,17 +341,18 @@ __global__ __launch_bounds__(64) void k_qknorm_rope_store(float *__restrict__ qk
 #define ATT_TH 1024
 #define ATT_KROW 1056                   // LDS bytes of 32 K dims of a tile (32 x 32 + 32 padding)
 #define ATT_KTILE (4 * ATT_KROW)        // LDS bytes of a K tile (hd <= 128)
-#define ATT_VTILE (32 * ATT_HDMAX)      // LDS bytes of a V tile
-#define ATT_QS 132                      // LDS floats per query vector (4 chunks of 33)
+#define ATT_QC 36                       // LDS floats per 32-dim chunk of a query vector (32 + 4 padding)
+#define ATT_QS (4 * ATT_QC)             // LDS floats per query vector
+template <int NQ>
 __global__ __launch_bounds__(ATT_TH) void k_attn_part(const int4 *__restrict__ items, const float *__restrict__ qkv, int ldqkv,
                                                       int nh, int nkv, int hd, float scale, const int *__restrict__ pos,
                                                       uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc,
                                                       float *__restrict__ part, int pstride) {
     __shared__ __align__(16) uint8_t ks[16 * ATT_KTILE];
-    __shared__ __align__(16) uint8_t vs[16 * ATT_VTILE];
-    __shared__ float qs[ATT_NQ * ATT_QS];
-    __shared__ float S[ATT_NQ][ATT_P];
-    __shared__ int np[ATT_NQ];
+    __shared__ __align__(16) uint8_t vs[16 * 32 * ATT_HDMAX];
+    __shared__ __align__(16) float qs[NQ * ATT_QS];
+    __shared__ float S[NQ][ATT_P];
+    __shared__ int np[NQ];
     int4 it = items[blockIdx.x];
     int r0 = it.x, nr = it.y, g = it.z, kb = it.w, kv_mul = nh / nkv, nq = nr * kv_mul, t = threadIdx.x;
     const int TB = 32 * hd, nchk = hd / 32;
@@ -360,59 +361,65 @@ __global__ __launch_bounds__(ATT_TH) void k_attn_part(const int4 *__restrict__ i
     int nmx = pos[r0 + nr - 1] + 1 - kb * ATT_P;
     nmx = nmx < ATT_P ? nmx : ATT_P;
     int nbytes = (nmx + ATT_T - 1) / ATT_T * TB; // the tiles holding positions < nmx
-    uint4 kr[4], vr[4];
-    #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        int o = (t + ATT_TH * k) * 16;
-        if (o < nbytes) {
-            kr[k] = *(const uint4 *)(K + o);
-            vr[k] = *(const uint4 *)(V + o);
-        }
+    // staging: 16 bytes of K and of V per thread and round, up to 4 rounds (hd <= 128), loads issued before any use
+    uint4 k0, k1, k2, k3, v0, v1, v2, v3;
+#define ATT_LD(k, KR, VR)                                                                                                \
+    if ((t + ATT_TH * k) * 16 < nbytes) {                                                                            \
+        KR = *(const uint4 *)(K + (t + ATT_TH * k) * 16);                                                             \
+        VR = *(const uint4 *)(V + (t + ATT_TH * k) * 16);                                                             \
     }
-    for (int e = t; e < nq * hd; e += ATT_TH) {
-        int v = e / hd, i = e % hd;
-        qs[v * ATT_QS + (i >> 5) * 33 + (i & 31)] = qkv[(size_t)(r0 + v / kv_mul) * ldqkv + (size_t)(g * kv_mul + v % kv_mul) * hd + i];
+    ATT_LD(0, k0, v0) ATT_LD(1, k1, v1) ATT_LD(2, k2, v2) ATT_LD(3, k3, v3)
+#undef ATT_LD
+    for (int e = t; e < NQ * ATT_QS; e += ATT_TH) { // (padding and vectors past nq: zeros)
+        int v = e / ATT_QS, c = e % ATT_QS / ATT_QC, i = e % ATT_QC, d = 32 * c + i;
+        qs[e] = v < nq && i < 32 && d < hd ? qkv[(size_t)(r0 + v / kv_mul) * ldqkv + (size_t)(g * kv_mul + v % kv_mul) * hd + d] : 0.0f;
     }
-    if (t < nq) {
-        int n = pos[r0 + t / kv_mul] + 1 - kb * ATT_P;
+    if (t < NQ) {
+        int n = t < nq ? pos[r0 + t / kv_mul] + 1 - kb * ATT_P : 0;
         np[t] = n < 0 ? 0 : n < ATT_P ? n : ATT_P;
     }
-    #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        int o = (t + ATT_TH * k) * 16;
-        if (o < nbytes) {
-            int tile = o / TB, w = o % TB;
-            *(uint4 *)(ks + tile * ATT_KTILE + (w >> 10) * ATT_KROW + (w & 1023)) = kr[k];
-            *(uint4 *)(vs + o) = vr[k]; // (V: position p's row at p hd 2 bytes)
-        }
+#define ATT_ST(k, KR, VR)                                                                                                \
+    if ((t + ATT_TH * k) * 16 < nbytes) {                                                                            \
+        int o = (t + ATT_TH * k) * 16, tile = o / TB, w = o % TB;                                                     \
+        *(uint4 *)(ks + tile * ATT_KTILE + (w >> 10) * ATT_KROW + (w & 1023)) = KR;                                   \
+        *(uint4 *)(vs + o) = VR; /* (V: position p's row at p hd 2 bytes) */                                          \
     }
+    ATT_ST(0, k0, v0) ATT_ST(1, k1, v1) ATT_ST(2, k2, v2) ATT_ST(3, k3, v3)
+#undef ATT_ST
     __syncthreads();
-    // scores
+    // scores: lane (position p, chunk c), all NQ vectors (no per-vector branches in the chain)
     {
         int p = t >> 2, c = t & 3;
         const uint8_t *kt = ks + (p / ATT_T) * ATT_KTILE + c * ATT_KROW + (p % ATT_T) * 2;
-        const float *qc = qs + c * 33;
-        float acc[ATT_NQ];
+        const float *qc = qs + c * ATT_QC;
+        float acc[NQ];
         #pragma unroll
-        for (int v = 0; v < ATT_NQ; v++) acc[v] = 0.0f;
+        for (int v = 0; v < NQ; v++) acc[v] = 0.0f;
         if (p < nmx && c < nchk) {
-            for (int i = 0; i < 32; i++) {
-                float k = h2f(*(const uint16_t *)(kt + i * 32));
+            for (int i = 0; i < 32; i += 4) {
+                float k[4];
                 #pragma unroll
-                for (int v = 0; v < ATT_NQ; v++)
-                    if (v < nq) acc[v] = __builtin_fmaf(qc[v * ATT_QS + i], k, acc[v]);
+                for (int u = 0; u < 4; u++) k[u] = h2f(*(const uint16_t *)(kt + (i + u) * 32));
+                float4 q4[NQ];
+                #pragma unroll
+                for (int v = 0; v < NQ; v++) q4[v] = *(const float4 *)(qc + v * ATT_QS + i);
+                #pragma unroll
+                for (int v = 0; v < NQ; v++) {
+                    acc[v] = __builtin_fmaf(q4[v].x, k[0], acc[v]);
+                    acc[v] = __builtin_fmaf(q4[v].y, k[1], acc[v]);
+                    acc[v] = __builtin_fmaf(q4[v].z, k[2], acc[v]);
+                    acc[v] = __builtin_fmaf(q4[v].w, k[3], acc[v]);
+                }
             }
         }
         #pragma unroll
-        for (int v = 0; v < ATT_NQ; v++) {
-            if (v < nq) {
-                float c1 = __shfl_down(acc[v], 1), c2 = __shfl_down(acc[v], 2), c3 = __shfl_down(acc[v], 3);
-                float a = acc[v];
-                if (nchk > 1) a = a + c1;
-                if (nchk > 2) a = a + c2;
-                if (nchk > 3) a = a + c3;
-                if (c == 0 && p < nmx) S[v][p] = a * scale;
-            }
+        for (int v = 0; v < NQ; v++) {
+            float c1 = __shfl_down(acc[v], 1), c2 = __shfl_down(acc[v], 2), c3 = __shfl_down(acc[v], 3);
+            float a = acc[v];
+            if (nchk > 1) a = a + c1;
+            if (nchk > 2) a = a + c2;
+            if (nchk > 3) a = a + c3;
+            if (c == 0 && p < nmx && v < nq) S[v][p] = a * scale;
         }
     }
     __syncthreads();
@@ -427,8 +434,17 @@ __global__ __launch_bounds__(ATT_TH) void k_attn_part(const int4 *__restrict__ i
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __builtin_amdgcn_wave_barrier();
         float s = 0.0f;
-        if (lane < 16)
-            for (int p = lane; p < n; p += 16) s = s + S[v][p];
+        if (lane < 16) {
+            int p = lane;
+            for (; p + 48 < n; p += 64) {
+                float e0 = S[v][p], e1 = S[v][p + 16], e2 = S[v][p + 32], e3 = S[v][p + 48];
+                s = s + e0;
+                s = s + e1;
+                s = s + e2;
+                s = s + e3;
+            }
+            for (; p < n; p += 16) s = s + S[v][p];
+        }
         for (int w = 8; w >= 1; w >>= 1) {
             float o = __shfl_down(s, w);
             s = s + o;
@@ -441,29 +457,33 @@ __global__ __launch_bounds__(ATT_TH) void k_attn_part(const int4 *__restrict__ i
         }
     }
     __syncthreads();
-    // o: lane (vector v = wave, dim pair d2)
+    // o: lane (vector v = wave, dim pair d2): the chains over the positions, 8 at a time, then the rest
     {
         int v = wave, d2 = lane, i0 = 2 * d2;
         if (v < nq && i0 < hd && np[v] > 0) {
-            int n = np[v];
+            int n = np[v], p = 0;
             float o0 = 0.0f, o1 = 0.0f;
             const uint8_t *vb = vs + i0 * 2;
-            for (int p0 = 0; p0 < n; p0 += 8) {
-                float v0[8], v1[8], e[8];
+            const int rs = hd * 2;
+            for (; p + 8 <= n; p += 8) {
+                uint32_t vv[8];
+                float e[8];
                 #pragma unroll
                 for (int u = 0; u < 8; u++) {
-                    int p = p0 + u < n ? p0 + u : n - 1;
-                    uint32_t vv = *(const uint32_t *)(vb + p * hd * 2);
-                    v0[u] = h2f((uint16_t)(vv & 0xffff));
-                    v1[u] = h2f((uint16_t)(vv >> 16));
-                    e[u] = S[v][p];
+                    vv[u] = *(const uint32_t *)(vb + (p + u) * rs);
+                    e[u] = S[v][p + u];
                 }
                 #pragma unroll
-                for (int u = 0; u < 8; u++)
-                    if (p0 + u < n) {
-                        o0 = __builtin_fmaf(e[u], v0[u], o0);
-                        o1 = __builtin_fmaf(e[u], v1[u], o1);
-                    }
+                for (int u = 0; u < 8; u++) {
+                    o0 = __builtin_fmaf(e[u], h2f((uint16_t)(vv[u] & 0xffff)), o0);
+                    o1 = __builtin_fmaf(e[u], h2f((uint16_t)(vv[u] >> 16)), o1);
+                }
+            }
+            for (; p < n; p++) {
+                uint32_t vv = *(const uint32_t *)(vb + p * rs);
+                float e = S[v][p];
+                o0 = __builtin_fmaf(e, h2f((uint16_t)(vv & 0xffff)), o0);
+                o1 = __builtin_fmaf(e, h2f((uint16_t)(vv >> 16)), o1);
             }
             int row = r0 + v / kv_mul, h = g * kv_mul + v % kv_mul;
             float *o = part + ((size_t)row * nh + h) * pstride + (size_t)kb * (hd + 2);
@@ -652,9 +672,17 @@ int gw_k_qknorm_rope_store(float *qkv, int ldqkv, int n, int nh, int nkv, int hd
     return (int)hipGetLastError();
 }
 
-int gw_k_attn_part(const void *items, int nitems, const float *qkv, int ldqkv, int nh, int nkv, int hd, float scale,
+int gw_k_attn_part(const void *items, int nitems, int nq_max, const float *qkv, int ldqkv, int nh, int nkv, int hd, float scale,
                    const int *pos, uint16_t *const *kc, uint16_t *const *vc, float *part, int pstride, hipStream_t s) {
-    hipLaunchKernelGGL(k_attn_part, dim3(nitems), dim3(ATT_TH), 0, s, (const int4 *)items, qkv, ldqkv, nh, nkv, hd, scale, pos, kc, vc, part, pstride);
+    int nq = nq_max;
+    const int4 *it = (const int4 *)items;
+#define ATT_LAUNCH(Q) hipLaunchKernelGGL(k_attn_part<Q>, dim3(nitems), dim3(ATT_TH), 0, s, it, qkv, ldqkv, nh, nkv, hd, scale, pos, kc, vc, part, pstride)
+    if (nq <= 1) ATT_LAUNCH(1);
+    else if (nq <= 2) ATT_LAUNCH(2);
+    else if (nq <= 4) ATT_LAUNCH(4);
+    else if (nq <= 8) ATT_LAUNCH(8);
+    else ATT_LAUNCH(16);
+#undef ATT_LAUNCH
     return (int)hipGetLastError();
 }
 
