@@ -6,6 +6,10 @@
  *   attention partials per (row block, kv head, 256-position block) -> combine + quantize -> wo matmul ->
  *   residual + rmsnorm + quantize -> w1 / w3 matmul -> SwiGLU + quantize -> w2 matmul
  *   -> final residual + rmsnorm + quantize of the selected rows -> classifier -> logits to the host.
+ * A one-row pass of an all-Q8_0 model (decode) runs the fused sequence instead: per layer qkv matmul (rmsnorm +
+ * quantize in its prologue) -> QK-norm + RoPE + K / V store -> attention partials -> wo matmul (combine + quantize in
+ * its prologue, + residual) -> w1 / w3 matmul (rmsnorm + quantize in its prologue, SwiGLU in its epilogue) -> w2 matmul
+ * (quantize in its prologue, + residual): the same arithmetic, four kernels fewer per layer.
  * The same kernels run every row whatever its batch-mates (decode is a one-row pass), and each output is computed
  * whole in a fixed order, so a sequence's results do not depend on what it is batched with (runq.h:22-24).
  * Errors: every argument is validated before any device work (forward.c:3775-3800), so a failed pass changes nothing;
@@ -169,6 +173,10 @@ static int ctx_part(RqCtx *c, int rows, int nb) {
     size_t need = (size_t)rows * m->n_heads * nb * (m->head_dim + 2) * sizeof(float);
     if (nb > c->att_nb || need > c->part_bytes) {
         int nbn = nb > c->att_nb ? nb : c->att_nb;
+        /* the combine kernel keeps (m, l, coefficient) of every head and block of a row in LDS */
+        if ((size_t)m->n_heads * (2 * (size_t)nbn + 1) * sizeof(float) > 65536)
+            return ctx_fail(c, RQ_ERR_ARG, "context of %d positions too long for %d heads (attention combine)",
+                            nbn * GW_ATT_P, m->n_heads);
         int B = c->nb_max > 1 ? c->nb_max : 1;
         size_t bytes = (size_t)B * m->n_heads * nbn * (m->head_dim + 2) * sizeof(float);
         HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));
@@ -380,18 +388,43 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
     pf_mark(c, GW_PF_EMBED);
     if (m->embd.type == GW_Q8_0) KCHK(gw_k_embed_q8(c->x, dim, (const uint8_t *)m->embd.codes, m->embd.scales, tok_d, n, s));
     else KCHK(gw_k_embed_kq(c->x, dim, m->embd.type, m->embd.blocks, tok_d, n, s));
+    /* one row of an all-Q8_0 model: the fused decode sequence (gw_gemv.hip: each matmul computes its activation from
+     * the producer's fp32 output; the residual adds go straight into x) */
+    int fused = n == 1 && !m->kq && dim <= 4096 && H <= 12288 && nh * hd <= 4096 && dim % 64 == 0 && H % 64 == 0 &&
+                (nh * hd) % 64 == 0;
     for (int l = 0; l < L; l++) {
         const GwLayer *y = &m->layer[l];
-        pf_mark(c, GW_PF_NORM);
-        KCHK(gw_k_rmsnorm_quant(c->x, l ? c->xb : NULL, dim, y->att_norm, NULL, n, c->xq, c->xs, K, NULL, s));
-        pf_mark(c, GW_PF_QKV);
-        if ((rc = run_mm(c, y->qkv, y->nqkv, c->xq, c->xs, K, n, c->qkv, c->ldqkv, 0)) != RQ_OK) return rc;
+        if (fused) {
+            pf_mark(c, GW_PF_QKV);
+            KCHK(gw_k_gemv1_norm(&y->qkv[0], GW_GV_R_QKV, c->x, y->att_norm, c->qkv, 0, 0, s));
+        } else {
+            pf_mark(c, GW_PF_NORM);
+            KCHK(gw_k_rmsnorm_quant(c->x, l ? c->xb : NULL, dim, y->att_norm, NULL, n, c->xq, c->xs, K, NULL, s));
+            pf_mark(c, GW_PF_QKV);
+            if ((rc = run_mm(c, y->qkv, y->nqkv, c->xq, c->xs, K, n, c->qkv, c->ldqkv, 0)) != RQ_OK) return rc;
+        }
         pf_mark(c, GW_PF_ROPE);
         KCHK(gw_k_qknorm_rope_store(c->qkv, c->ldqkv, n, nh, nkv, hd, y->q_norm, y->k_norm, m->rope, pos_d,
                                     kc_d + (size_t)l * n, vc_d + (size_t)l * n, s));
         pf_mark(c, GW_PF_ATT);
         KCHK(gw_k_attn_part(items_d, nitems, nq_max, c->qkv, c->ldqkv, nh, nkv, hd, m->att_scale, pos_d, kc_d + (size_t)l * n,
                             vc_d + (size_t)l * n, c->part, c->pstride, s));
+        if (fused) {
+            if (nbmax <= GW_GV_NBMAX) {
+                pf_mark(c, GW_PF_WO);
+                KCHK(gw_k_gemv1_combine(&y->wo, GW_GV_R_WO, c->part, c->pstride, hd, nbmax, c->x, 1, s));
+            } else {
+                pf_mark(c, GW_PF_COMBINE);
+                KCHK(gw_k_attn_combine_quant(c->part, c->pstride, nh, hd, pos_d, n, c->xq, c->xs, K, NULL, s));
+                pf_mark(c, GW_PF_WO);
+                KCHK(gw_k_gemv1_q(&y->wo, GW_GV_R_WO, c->xq, c->xs, c->x, 1, s));
+            }
+            pf_mark(c, GW_PF_W13);
+            KCHK(gw_k_gemv1_norm(&y->w13[0], GW_GV_R_W13, c->x, y->ffn_norm, c->hb, 0, y->w13_il, s));
+            pf_mark(c, GW_PF_W2);
+            KCHK(gw_k_gemv1_qf(&y->w2, GW_GV_R_W2, c->hb, c->x, 1, s));
+            continue;
+        }
         pf_mark(c, GW_PF_COMBINE);
         KCHK(gw_k_attn_combine_quant(c->part, c->pstride, nh, hd, pos_d, n, c->xq, c->xs, K, NULL, s));
         pf_mark(c, GW_PF_WO);
@@ -401,11 +434,11 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
         pf_mark(c, GW_PF_W13);
         if ((rc = run_mm(c, y->w13, y->nw13, c->xq, c->xs, K, n, c->hb, 2 * H, 0)) != RQ_OK) return rc;
         pf_mark(c, GW_PF_SWIGLU);
-        KCHK(gw_k_swiglu_quant(c->hb, H, n, c->hq, c->hs, s));
+        KCHK(gw_k_swiglu_quant(c->hb, H, y->w13_il, n, c->hq, c->hs, s));
         pf_mark(c, GW_PF_W2);
         if ((rc = run_mm(c, &y->w2, 1, c->hq, c->hs, H, n, c->xb, dim, 0)) != RQ_OK) return rc;
     }
-    int resid_done = 0;
+    int resid_done = fused; /* (the fused sequence leaves no pending residual in xb) */
     if (P->want_hidden) { /* every row's final hidden state (the normed row), then the logits rows below */
         KCHK(gw_k_rmsnorm_quant(c->x, c->xb, dim, m->final_norm, NULL, n, c->xq, c->xs, K, c->hid_d, s));
         resid_done = 1;

@@ -10,16 +10,22 @@ __device__ __forceinline__ float h2f_g(uint16_t h) { return __half2float(__ushor
 
 // GGUF Q8_0 blocks (fp16 d, 32 int8; 34 bytes) -> codes (32 per block) + fp16 scales: the device layout
 __global__ __launch_bounds__(256) void k_q8_unpack(const uint8_t *__restrict__ blk, size_t nblk, int8_t *__restrict__ codes,
-                                                   uint16_t *__restrict__ scales) {
+                                                   uint16_t *__restrict__ scales, int gpr, int il, int off) {
+    // block b of source row i = b / gpr goes to row i (il = 0) or, interleaved, to row (i / il) 2 il + off + i % il
     size_t b = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (b >= nblk) return;
+    size_t db = b;
+    if (il) {
+        size_t i = b / gpr;
+        db = ((i / il) * 2 * il + off + i % il) * gpr + b % gpr;
+    }
     const uint8_t *p = blk + b * 34;
-    scales[b] = (uint16_t)(p[0] | p[1] << 8);
+    scales[db] = (uint16_t)(p[0] | p[1] << 8);
     uint32_t w[8];
     #pragma unroll
     for (int i = 0; i < 8; i++)
         w[i] = (uint32_t)p[2 + 4 * i] | (uint32_t)p[3 + 4 * i] << 8 | (uint32_t)p[4 + 4 * i] << 16 | (uint32_t)p[5 + 4 * i] << 24;
-    uint4 *d = (uint4 *)(codes + b * 32);
+    uint4 *d = (uint4 *)(codes + db * 32);
     d[0] = make_uint4(w[0], w[1], w[2], w[3]);
     d[1] = make_uint4(w[4], w[5], w[6], w[7]);
 }
@@ -303,9 +309,9 @@ int gw_k_embed_kq(float *x, int dim, int type, const uint8_t *blocks, const int 
     return (int)hipGetLastError();
 }
 
-int gw_k_q8_unpack(const uint8_t *blocks, size_t nblk, int8_t *codes, uint16_t *scales, hipStream_t s) {
+int gw_k_q8_unpack(const uint8_t *blocks, size_t nblk, int8_t *codes, uint16_t *scales, int gpr, int il, int off, hipStream_t s) {
     if (!nblk) return 0;
-    hipLaunchKernelGGL(k_q8_unpack, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, s, blocks, nblk, codes, scales);
+    hipLaunchKernelGGL(k_q8_unpack, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, s, blocks, nblk, codes, scales, gpr, il, off);
     return (int)hipGetLastError();
 }
 
@@ -332,7 +338,7 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
 
 int gw_q8_pack(const void *blocks, int N, int K, int8_t *codes, uint16_t *scales, void *stream) {
     if (N <= 0 || K <= 0 || K % 32 || !blocks || !codes || !scales) return RQ_ERR_ARG;
-    return gw_k_q8_unpack((const uint8_t *)blocks, (size_t)N * (K / 32), codes, scales, (hipStream_t)stream) ? RQ_ERR_STATE : RQ_OK;
+    return gw_k_q8_unpack((const uint8_t *)blocks, (size_t)N * (K / 32), codes, scales, K / 32, 0, 0, (hipStream_t)stream) ? RQ_ERR_STATE : RQ_OK;
 }
 
 int gw_quantize(const float *x, int M, int K, int8_t *xq, float *xs, void *stream) {

@@ -21,6 +21,7 @@ enum { GW_F32 = 0, GW_Q8_0 = 8, GW_Q4_K = 12, GW_Q6_K = 14 }; /* ggml type numbe
 #define GW_ATT_T 16   /* positions per KV cache tile */
 #define GW_ATT_P 256  /* positions per attention block */
 #define GW_RMAX 512   /* rows per pass (RQ_BATCH_MAX) */
+#define GW_W13_IL 4 /* w1 / w3 rows interleaved in the fused Q8_0 matrix (blocks of 4) */
 #define GW_GEMV_MAX_ROWS 4 /* activation rows up to which a Q8_0 matmul takes the GEMV (else the MFMA GEMM) */
 
 /* A weight matrix on the device (rows x cols). Q8_0: int8 codes, row-major, and fp16 scales (cols / 32 per row),
@@ -36,8 +37,9 @@ typedef struct {
     GwMat qkv[3];  /* Q8_0 model: qkv[0] = [wq | wk | wv] rows fused; K-quants: wq, wk, wv (types may differ) */
     int nqkv;
     GwMat wo;
-    GwMat w13[2];  /* Q8_0: w13[0] = [w1 | w3] fused; K-quants: w1, w3 */
-    int nw13;
+    GwMat w13[2];  /* Q8_0: w13[0] = w1 and w3 fused, rows interleaved in blocks of GW_W13_IL (w1 rows 4i..4i+3, then
+                    * w3 rows 4i..4i+3): one 8-row tile holds both halves of 4 SwiGLU outputs; K-quants: w1, w3 */
+    int nw13, w13_il; /* w13_il: GW_W13_IL when fused, else 0 */
     GwMat w2;
     float *att_norm, *ffn_norm, *q_norm, *k_norm; /* device */
 } GwLayer;
@@ -118,11 +120,29 @@ int gw_k_attn_part(const void *items, int nitems, int nq_max, const float *qkv, 
                    const int *pos, uint16_t *const *kc, uint16_t *const *vc, float *part, int pstride, hipStream_t s);
 int gw_k_attn_combine_quant(const float *part, int pstride, int nh, int hd, const int *pos, int n, int8_t *aq, float *as,
                             int ldq, float *att_out, hipStream_t s);
-int gw_k_swiglu_quant(const float *hb, int H, int n, int8_t *hq, float *hs, hipStream_t s);
+/* hb row: [h (H) | h2 (H)] (il = 0) or blocks of il h then il h2 (w1 / w3 rows interleaved by il) */
+int gw_k_swiglu_quant(const float *hb, int H, int il, int n, int8_t *hq, float *hs, hipStream_t s);
 int gw_k_quant_rows(const float *x, int n, int ldxf, int rows, int8_t *q, float *sc, int ldq, hipStream_t s);
 int gw_k_argmax(const float *lg, int n, int ld, int rows, int *out, void *scratch, hipStream_t s); /* scratch: rows x 512 B */
-int gw_k_q8_unpack(const uint8_t *blocks, size_t nblk, int8_t *codes, uint16_t *scales, hipStream_t s);
+/* GGUF Q8_0 blocks (gpr per row) -> codes + scales; il > 0: source row i to row (i / il) 2 il + off + i % il (two
+ * matrices interleaved in blocks of il rows) */
+int gw_k_q8_unpack(const uint8_t *blocks, size_t nblk, int8_t *codes, uint16_t *scales, int gpr, int il, int off, hipStream_t s);
 int gw_k_fill_synthetic(uint16_t *kc, uint16_t *vc, size_t n, unsigned long long seed, hipStream_t s);
+
+/* the single-row Q8_0 GEMV with the activation's producer fused in front (gw_gemv.hip): out[row] (+)= W row . act for
+ * R rows per tile (4, 8, 16); act = the quantized row (q), rmsnorm(x, nw) (norm), the fp32 row x (qf) or the attention
+ * combine of part over the row's nb <= GW_GV_NBMAX key blocks (combine); W Q8_0, W->cols % 64 == 0, <= 12288 (4096 for
+ * R = 16), under 2 GiB. norm with swiglu_il = GW_W13_IL (R = 8, w1 / w3 interleaved): out[j] = swiglu(h_j, h2_j) */
+#define GW_GV_NBMAX 4
+#define GW_GV_R_QKV 4  /* weight rows per tile of the fused decode matmuls */
+#define GW_GV_R_WO 8
+#define GW_GV_R_W13 8
+#define GW_GV_R_W2 4
+int gw_k_gemv1_q(const GwMat *w, int R, const int8_t *xq, const float *xs, float *out, int mode, hipStream_t s);
+int gw_k_gemv1_norm(const GwMat *w, int R, const float *x, const float *nw, float *out, int mode, int swiglu_il, hipStream_t s);
+int gw_k_gemv1_qf(const GwMat *w, int R, const float *x, float *out, int mode, hipStream_t s);
+int gw_k_gemv1_combine(const GwMat *w, int R, const float *part, int pstride, int hd, int nb, float *out, int mode,
+                       hipStream_t s);
 
 /* the matmul dispatch (gw_gemm.hip): out[m * ldo + row] (+)= W row . X row m for M rows, any supported type */
 int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int M, float *out, int ldo, int mode,

@@ -21,102 +21,7 @@
 
 #include "gw_internal.h"
 
-#define ATT_T 16
-#define ATT_P 256
-
-// ------------------------------------------------------------------------------------------- helpers
-
-__device__ __forceinline__ float h2f(uint16_t h) {
-    // IEEE half -> float (exact; v_cvt_f32_f16)
-    return __half2float(__ushort_as_half(h));
-}
-
-__device__ __forceinline__ uint16_t f2h_ref(float f) {
-    // fp32 -> f16 as the reference's f32_f16 (forward.c:1325-1344): RNE, >= 65520 saturates to 65504, NaN quiet
-    uint32_t u = __float_as_uint(f);
-    uint32_t sign = (u >> 16) & 0x8000u, a = u & 0x7fffffffu;
-    uint32_t n = a - 0x38000000u;
-    uint32_t h = (n + 0xfffu + ((n >> 13) & 1)) >> 13;
-    float fs = __uint_as_float(a < 0x38800000u ? a : 0u);
-    uint32_t sub = (uint32_t)rintf(fs * 16777216.0f);
-    h = a < 0x38800000u ? sub : h;
-    h = a >= 0x477ff000u ? 0x7bffu : h;
-    h = a > 0x7f800000u ? (0x7e00u | ((a >> 13) & 0x3ffu)) : h;
-    return (uint16_t)(sign | h);
-}
-
-__device__ __forceinline__ float exp_att(float x) {
-    // forward.c:1301-1321 (att512_exp): Cephes-style expf, x clamped at -86
-    x = x > -86.0f ? x : -86.0f;
-    float n = rintf(x * 1.44269504088896341f);
-    float r = __builtin_fmaf(n, -0.693359375f, x);
-    r = __builtin_fmaf(n, 2.12194440e-4f, r);
-    float z = r * r;
-    float y = 1.9875691500e-4f;
-    y = __builtin_fmaf(y, r, 1.3981999507e-3f);
-    y = __builtin_fmaf(y, r, 8.3334519073e-3f);
-    y = __builtin_fmaf(y, r, 4.1665795894e-2f);
-    y = __builtin_fmaf(y, r, 1.6666665459e-1f);
-    y = __builtin_fmaf(y, r, 5.0000001201e-1f);
-    y = __builtin_fmaf(y, z, r);
-    y = y + 1.0f;
-    return __uint_as_float(__float_as_uint(y) + ((uint32_t)(int32_t)n << 23));
-}
-
-__device__ __forceinline__ float silu_exp(float x) { return exp_att(x < 80.0f ? x : 80.0f); }
-
-__device__ __forceinline__ float wave_max(float v) {
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
-
-// rmsnorm scale of n floats in LDS (n % 128 == 0), computed by lanes 0..15 of the calling wave, returned to all lanes
-// of that wave: forward.c:886-901 in the reference's compiled order (lane j: an fma chain over x[j], x[j + 16], ...,
-// the tree +8 +4 +2 +1, t = fma(ss, 1/n, 1e-6), 1 / sqrt(t)). The chain's LDS reads are issued 8 at a time
-__device__ __forceinline__ float rms_scale_lds(const float *xs_lds, int n) {
-    int lane = threadIdx.x & 63;
-    float s = 0.0f;
-    if (lane < 16) {
-        for (int j = lane; j < n; j += 128) {
-            float a[8];
-            #pragma unroll
-            for (int u = 0; u < 8; u++) a[u] = xs_lds[j + 16 * u];
-            #pragma unroll
-            for (int u = 0; u < 8; u++) s = __builtin_fmaf(a[u], a[u], s);
-        }
-    }
-    for (int w = 8; w >= 1; w >>= 1) {
-        float o = __shfl_down(s, w);
-        s = s + o;
-    }
-    float r = 0.0f;
-    if (lane == 0) {
-        float inv_n = 1.0f / (float)n;
-        float t = __builtin_fmaf(s, inv_n, 1e-6f);
-        r = 1.0f / sqrtf(t);
-    }
-    return __shfl(r, 0);
-}
-
-// quantization with one lane per value: the 32 lanes of each half wave are one group of 32 consecutive values
-// (forward.c:803-836: s = wmax * (1/127), inv = 127 / wmax, q = trunc(v * inv + copysign(0.49999997)), 0 if wmax = 0).
-// The calling wave must have all 64 lanes active
-__device__ __forceinline__ void quant_lane32(float v, int8_t *q, float *s) {
-    float wmax = fabsf(v);
-    #pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) {
-        float t = __shfl_xor(wmax, o);
-        wmax = t > wmax ? t : wmax;
-    }
-    if ((threadIdx.x & 31) == 0) *s = wmax * (1.0f / 127.0f);
-    int32_t qi = 0;
-    if (wmax > 0.0f) {
-        float inv = 127.0f / wmax;
-        float x = v * inv;
-        qi = (int32_t)(x + copysignf(0.49999997f, x));
-    }
-    *q = (int8_t)qi;
-}
+#include "gw_device.h"
 
 // --------------------------------------------------------------------------------------- embedding
 
@@ -209,45 +114,73 @@ __global__ __launch_bounds__(NORM_T) void k_rmsnorm_quant(float *__restrict__ x,
 // ------------------------------------------------------------------------------------- Q8_0 GEMV
 
 // out[m * ldo + row] = W row . X row m for M activation rows, R weight rows per block. Each thread takes half-groups
-// (16 codes) j = t, t + 256, ...: an exact int32 sum by 4 v_dot4 (sdot4), the lane pair's sums added (exact), the even
-// lane's product (ws * xs) * (float) isum into LDS; then one lane per (m, row) folds the groups in order (LDS read 4
-// at a time). W: row-major int8 codes (K per row) + fp16 scales (K / 32 per row); X: int8 rows at xq + m * ldx, fp32
-// scales at xs + m * ldx / 32. mode 1: out = out + val (a residual add)
-template <int M, int R>
+// (16 codes) j = t, t + 256, ..., U of them per pass with every weight load of the pass issued before the first dot (a
+// row of K <= 4096 U codes is one pass): an exact int32 sum by 4 v_dot4 (sdot4), the lane pair's sums added (exact),
+// the even lane's product (ws * xs) * (float) isum into LDS; then one lane per (m, row) folds the groups in order, the
+// LDS reads of the next 32 groups issued before the adds of the current ones. W: row-major int8 codes (K per row) +
+// fp16 scales (K / 32 per row); X: int8 rows at xq + m * ldx, fp32 scales at xs + m * ldx / 32. mode 1: out = out + val
+// (a residual add)
+template <int M, int R, int U>
 __global__ __launch_bounds__(256) void k_gemv_q8(const int8_t *__restrict__ W, const uint16_t *__restrict__ WS, int nrows,
                                                  int K, const int8_t *__restrict__ xq, const float *__restrict__ xs, int ldx,
                                                  float *out, int ldo, int mode) {
     extern __shared__ float P[];
-    const int G = K >> 5, H = K >> 4, PS = G + 4;
+    const int G = K >> 5, H = K >> 4, PS = (G + 7) & ~3; // (rows 16-byte aligned)
     const int row0 = blockIdx.x * R, t = threadIdx.x;
-    for (int j = t; j < H; j += 256) {
-        int4 xv[M];
-        float xsg[M];
+    const int8_t *wr[R];
+    const uint16_t *sr[R];
+    #pragma unroll
+    for (int r = 0; r < R; r++) {
+        int row = row0 + r < nrows ? row0 + r : nrows - 1;
+        wr[r] = W + (size_t)row * K;
+        sr[r] = WS + (size_t)row * G;
+    }
+    for (int j0 = 0; j0 < H; j0 += 256 * U) {
+        // (loads past the row's end read its last chunk again, unconditionally: a load under a branch would wait for
+        // every earlier load first; only the dots below are predicated)
+        int4 wv[U][R];
+        float ws[U][R];
         #pragma unroll
-        for (int m = 0; m < M; m++) {
-            xv[m] = *(const int4 *)(xq + (size_t)m * ldx + 16 * j);
-            xsg[m] = xs[(size_t)m * (ldx >> 5) + (j >> 1)];
+        for (int u = 0; u < U; u++) {
+            int j = j0 + 256 * u + t < H ? j0 + 256 * u + t : H - 1;
+            #pragma unroll
+            for (int r = 0; r < R; r++) wv[u][r] = *(const int4 *)(wr[r] + 16 * j);
         }
-        int4 wv[R];
-        float ws[R];
         #pragma unroll
-        for (int r = 0; r < R; r++) {
-            int row = row0 + r < nrows ? row0 + r : nrows - 1;
-            wv[r] = *(const int4 *)(W + (size_t)row * K + 16 * j);
-            ws[r] = h2f(WS[(size_t)row * G + (j >> 1)]);
+        for (int u = 0; u < U; u++) {
+            int j = j0 + 256 * u + t < H ? j0 + 256 * u + t : H - 1;
+            #pragma unroll
+            for (int r = 0; r < R; r++) ws[u][r] = h2f(sr[r][j >> 1]);
         }
+        int4 xv[U][M];
+        float xsg[U][M];
         #pragma unroll
-        for (int r = 0; r < R; r++) {
+        for (int u = 0; u < U; u++) {
+            int j = j0 + 256 * u + t < H ? j0 + 256 * u + t : H - 1;
             #pragma unroll
             for (int m = 0; m < M; m++) {
-                int s = __builtin_amdgcn_sdot4(wv[r].x, xv[m].x, 0, false);
-                s = __builtin_amdgcn_sdot4(wv[r].y, xv[m].y, s, false);
-                s = __builtin_amdgcn_sdot4(wv[r].z, xv[m].z, s, false);
-                s = __builtin_amdgcn_sdot4(wv[r].w, xv[m].w, s, false);
-                s = s + __shfl_xor(s, 1);
-                if (!(j & 1)) {
-                    float sc = ws[r] * xsg[m];
-                    P[(m * R + r) * PS + (j >> 1)] = sc * (float)s;
+                xv[u][m] = *(const int4 *)(xq + (size_t)m * ldx + 16 * j);
+                xsg[u][m] = xs[(size_t)m * (ldx >> 5) + (j >> 1)];
+            }
+        }
+        #pragma unroll
+        for (int u = 0; u < U; u++) {
+            int j = j0 + 256 * u + t;
+            if (j < H) { // (whole lane pairs: H is even)
+                #pragma unroll
+                for (int r = 0; r < R; r++) {
+                    #pragma unroll
+                    for (int m = 0; m < M; m++) {
+                        int s = __builtin_amdgcn_sdot4(wv[u][r].x, xv[u][m].x, 0, false);
+                        s = __builtin_amdgcn_sdot4(wv[u][r].y, xv[u][m].y, s, false);
+                        s = __builtin_amdgcn_sdot4(wv[u][r].z, xv[u][m].z, s, false);
+                        s = __builtin_amdgcn_sdot4(wv[u][r].w, xv[u][m].w, s, false);
+                        s = s + __shfl_xor(s, 1);
+                        if (!(j & 1)) {
+                            float sc = ws[u][r] * xsg[u][m];
+                            P[(m * R + r) * PS + (j >> 1)] = sc * (float)s;
+                        }
+                    }
                 }
             }
         }
@@ -256,21 +189,36 @@ __global__ __launch_bounds__(256) void k_gemv_q8(const int8_t *__restrict__ W, c
     if (t < M * R) {
         int m = t / R, r = t % R, row = row0 + r;
         if (row < nrows) {
-            const float4 *p = (const float4 *)(P + t * PS);
+            const float *p = P + t * PS;
             float v = 0.0f;
-            for (int g4 = 0; g4 < G / 4; g4 += 4) {
-                float4 a[4];
+            int g = 0;
+            if (G >= 32) {
+                float4 a[8];
                 #pragma unroll
-                for (int u = 0; u < 4; u++) a[u] = p[g4 + u < G / 4 ? g4 + u : G / 4 - 1];
-                #pragma unroll
-                for (int u = 0; u < 4; u++)
-                    if (g4 + u < G / 4) {
+                for (int u = 0; u < 8; u++) a[u] = *(const float4 *)(p + 4 * u);
+                for (g = 32; g + 32 <= G; g += 32) {
+                    float4 b[8];
+                    #pragma unroll
+                    for (int u = 0; u < 8; u++) b[u] = *(const float4 *)(p + g + 4 * u);
+                    #pragma unroll
+                    for (int u = 0; u < 8; u++) {
                         v = v + a[u].x;
                         v = v + a[u].y;
                         v = v + a[u].z;
                         v = v + a[u].w;
                     }
+                    #pragma unroll
+                    for (int u = 0; u < 8; u++) a[u] = b[u];
+                }
+                #pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    v = v + a[u].x;
+                    v = v + a[u].y;
+                    v = v + a[u].z;
+                    v = v + a[u].w;
+                }
             }
+            for (; g < G; g++) v = v + p[g];
             float *o = out + (size_t)m * ldo + row;
             *o = mode == 1 ? *o + v : v;
         }
@@ -495,78 +443,99 @@ __global__ __launch_bounds__(ATT_TH) void k_attn_part(const int4 *__restrict__ i
 
 // one block per row: the attention of each head from its block partials in block order (att_combine,
 // forward.c:1405-1431), then the row's quantization for wo (aq row b, all_heads = nh * hd values, a multiple of 256).
-// Per head the coefficients c_b = exp_att(m_b - M) and 1 / L first (LDS), then the outputs
+// Steps: every block's (m, l) into LDS and the first 8 blocks' o values of the thread's elements into registers, all
+// loads in flight together; per head the coefficients c_b = exp_att(m_b - M) and 1 / L (LDS); then per element the fma
+// chain over the blocks in order
 #define COMB_T 1024
+#define COMB_B 8
 __global__ __launch_bounds__(COMB_T) void k_attn_combine_quant(const float *__restrict__ part, int pstride, int nh, int hd,
                                                             const int *__restrict__ pos, int8_t *__restrict__ aq,
                                                             float *__restrict__ as, int ldq, float *__restrict__ att_out) {
-    extern __shared__ float cl[]; // [nh][nb] coefficients, then [nh] inverses
-    int b = blockIdx.x, nb = (pos[b] + 1 + ATT_P - 1) / ATT_P, st = hd + 2, t = threadIdx.x;
-    float *inv = cl + (size_t)nh * nb;
+    extern __shared__ float cl[]; // [nh][nb] m then coefficients, [nh][nb] l, [nh] inverses
+    int b = blockIdx.x, nb = (pos[b] + 1 + ATT_P - 1) / ATT_P, st = hd + 2, t = threadIdx.x, ne = nh * hd;
+    float *ll = cl + (size_t)nh * nb, *inv = ll + (size_t)nh * nb;
+    const float *pr = part + (size_t)b * nh * pstride;
+    float o[4][COMB_B];
+    #pragma unroll
+    for (int k = 0; k < 4; k++) {
+        int e = t + COMB_T * k;
+        if (e < ne) {
+            const float *pb = pr + (size_t)(e / hd) * pstride + e % hd;
+            #pragma unroll
+            for (int u = 0; u < COMB_B; u++)
+                if (u < nb) o[k][u] = pb[(size_t)u * st];
+        }
+    }
+    for (int i = t; i < nh * nb; i += COMB_T) {
+        const float *ml = pr + (size_t)(i / nb) * pstride + (size_t)(i % nb) * st + hd;
+        cl[i] = ml[0];
+        ll[i] = ml[1];
+    }
+    __syncthreads();
     for (int h = t; h < nh; h += COMB_T) {
-        const float *pb = part + ((size_t)b * nh + h) * pstride;
+        float *ch = cl + (size_t)h * nb;
+        const float *lh = ll + (size_t)h * nb;
         if (nb == 1) {
-            inv[h] = 1.0f / pb[hd + 1];
+            inv[h] = 1.0f / lh[0];
+            ch[0] = 1.0f;
             continue;
         }
-        float M = pb[hd];
-        for (int k = 1; k < nb; k++) M = pb[(size_t)k * st + hd] > M ? pb[(size_t)k * st + hd] : M;
+        float M = ch[0];
+        for (int k = 1; k < nb; k++) M = ch[k] > M ? ch[k] : M;
         float L = 0.0f;
         for (int k = 0; k < nb; k++) {
-            float c = exp_att(pb[(size_t)k * st + hd] - M);
-            cl[h * nb + k] = c;
-            L = __builtin_fmaf(c, pb[(size_t)k * st + hd + 1], L);
+            float c = exp_att(ch[k] - M);
+            ch[k] = c;
+            L = __builtin_fmaf(c, lh[k], L);
         }
         inv[h] = 1.0f / L;
     }
-    // (the single-block case needs no coefficients: its loads go first, before the barrier)
-    float o1[4];
-    if (nb == 1) {
-        #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            int e = t + COMB_T * k;
-            if (e < nh * hd) o1[k] = part[((size_t)b * nh + e / hd) * pstride + e % hd];
-        }
-    }
     __syncthreads();
+    #pragma unroll
     for (int k = 0; k < 4; k++) {
         int e = t + COMB_T * k;
-        if (e >= nh * hd) break;
-        int h = e / hd, i = e % hd;
-        const float *pb = part + ((size_t)b * nh + h) * pstride + i;
-        float out;
-        if (nb == 1) {
-            out = o1[k] * inv[h];
-        } else {
-            float acc = 0.0f;
-            int kb = 0;
-            for (; kb + 8 <= nb; kb += 8) {
-                float o[8];
+        if (e < ne) { // (whole waves: ne % 256 == 0)
+            int h = e / hd;
+            const float *ch = cl + (size_t)h * nb;
+            float out;
+            if (nb == 1) {
+                out = o[k][0] * inv[h];
+            } else {
+                float acc = 0.0f;
                 #pragma unroll
-                for (int u = 0; u < 8; u++) o[u] = pb[(size_t)(kb + u) * st];
-                #pragma unroll
-                for (int u = 0; u < 8; u++) acc = __builtin_fmaf(cl[h * nb + kb + u], o[u], acc);
+                for (int u = 0; u < COMB_B; u++)
+                    if (u < nb) acc = __builtin_fmaf(ch[u], o[k][u], acc);
+                const float *pb = pr + (size_t)h * pstride + e % hd;
+                for (int kb = COMB_B; kb < nb; kb += COMB_B) {
+                    float w[COMB_B];
+                    #pragma unroll
+                    for (int u = 0; u < COMB_B; u++)
+                        if (kb + u < nb) w[u] = pb[(size_t)(kb + u) * st];
+                    #pragma unroll
+                    for (int u = 0; u < COMB_B; u++)
+                        if (kb + u < nb) acc = __builtin_fmaf(ch[kb + u], w[u], acc);
+                }
+                out = acc * inv[h];
             }
-            for (; kb < nb; kb++) acc = __builtin_fmaf(cl[h * nb + kb], pb[(size_t)kb * st], acc);
-            out = acc * inv[h];
+            if (att_out) att_out[(size_t)b * ne + e] = out;
+            quant_lane32(out, aq + (size_t)b * ldq + e, as + (size_t)b * (ldq / 32) + (e >> 5));
         }
-        if (att_out) att_out[(size_t)b * nh * hd + e] = out;
-        quant_lane32(out, aq + (size_t)b * ldq + e, as + (size_t)b * (ldq / 32) + (e >> 5));
     }
 }
 
 // ------------------------------------------------------------------------------------ SwiGLU + quantize
 
-// row blockIdx.x of hb = [h (H) | h2 (H)], values 256 blockIdx.y .. + 255: v = (h * h2) * (1 / (1 + exp(min(-h, 80)))),
-// quantized into hq / hs (one lane per value)
-__global__ __launch_bounds__(256) void k_swiglu_quant(const float *__restrict__ hb, int H, int8_t *__restrict__ hq,
+// row blockIdx.x of hb = [h (H) | h2 (H)] (il = 0) or blocks of il h then il h2 (il > 0), values 256 blockIdx.y .. + 255:
+// v = (h * h2) * (1 / (1 + exp(min(-h, 80)))), quantized into hq / hs (one lane per value)
+__global__ __launch_bounds__(256) void k_swiglu_quant(const float *__restrict__ hb, int H, int il, int8_t *__restrict__ hq,
                                                       float *__restrict__ hs) {
     int b = blockIdx.x, e = blockIdx.y * 256 + threadIdx.x;
     const float *h1 = hb + (size_t)b * 2 * H;
-    float h = h1[e];
+    int i1 = il ? (e / il) * 2 * il + e % il : e, i2 = il ? i1 + il : H + e;
+    float h = h1[i1];
     float ex = silu_exp(-h);
     float r = 1.0f / (1.0f + ex);
-    float v = (h * h1[H + e]) * r;
+    float v = (h * h1[i2]) * r;
     quant_lane32(v, hq + (size_t)b * H + e, hs + (size_t)b * (H / 32) + (e >> 5));
 }
 
@@ -647,21 +616,34 @@ int gw_k_rmsnorm_quant(float *x, const float *d, int dim, const float *w, const 
 
 int gw_k_gemv_q8(const int8_t *W, const uint16_t *WS, int nrows, int K, const int8_t *xq, const float *xs, int ldx, int M,
                  float *out, int ldo, int mode, hipStream_t s) {
-    // M activation rows in launches of up to 4
+    // M activation rows in launches of up to 4; U = the 16-code chunks per thread and pass (all loads of a row issued at
+    // once up to K = 16384)
     const int R = 4;
-    size_t lds = (size_t)4 * R * (K / 32 + 4) * sizeof(float);
+    int H = K / 16, U = (H + 255) / 256;
+    U = U < 1 ? 1 : U > 4 ? 4 : U;
     for (int m0 = 0; m0 < M; m0 += 4) {
         int mm = M - m0 < 4 ? M - m0 : 4;
+        size_t lds = (size_t)mm * R * ((K / 32 + 7) & ~3) * sizeof(float);
         dim3 grid((nrows + R - 1) / R);
         const int8_t *x = xq + (size_t)m0 * ldx;
         const float *xsc = xs + (size_t)m0 * (ldx / 32);
         float *o = out + (size_t)m0 * ldo;
+#define GEMV_L(MM, UU) hipLaunchKernelGGL((k_gemv_q8<MM, R, UU>), grid, dim3(256), lds, s, W, WS, nrows, K, x, xsc, ldx, o, ldo, mode)
+#define GEMV_U(MM)                                                                                                      \
+    switch (U) {                                                                                                        \
+    case 1: GEMV_L(MM, 1); break;                                                                                       \
+    case 2: GEMV_L(MM, 2); break;                                                                                       \
+    case 3: GEMV_L(MM, 3); break;                                                                                       \
+    default: GEMV_L(MM, 4); break;                                                                                      \
+    }
         switch (mm) {
-        case 1: hipLaunchKernelGGL((k_gemv_q8<1, R>), grid, dim3(256), lds, s, W, WS, nrows, K, x, xsc, ldx, o, ldo, mode); break;
-        case 2: hipLaunchKernelGGL((k_gemv_q8<2, R>), grid, dim3(256), lds, s, W, WS, nrows, K, x, xsc, ldx, o, ldo, mode); break;
-        case 3: hipLaunchKernelGGL((k_gemv_q8<3, R>), grid, dim3(256), lds, s, W, WS, nrows, K, x, xsc, ldx, o, ldo, mode); break;
-        default: hipLaunchKernelGGL((k_gemv_q8<4, R>), grid, dim3(256), lds, s, W, WS, nrows, K, x, xsc, ldx, o, ldo, mode); break;
+        case 1: GEMV_U(1); break;
+        case 2: GEMV_U(2); break;
+        case 3: GEMV_U(3); break;
+        default: GEMV_U(4); break;
         }
+#undef GEMV_U
+#undef GEMV_L
     }
     return (int)hipGetLastError();
 }
@@ -689,13 +671,13 @@ int gw_k_attn_part(const void *items, int nitems, int nq_max, const float *qkv, 
 int gw_k_attn_combine_quant(const float *part, int pstride, int nh, int hd, const int *pos, int n, int8_t *aq, float *as,
                             int ldq, float *att_out, hipStream_t s) {
     (void)hd;
-    hipLaunchKernelGGL(k_attn_combine_quant, dim3(n), dim3(COMB_T), (size_t)nh * (pstride / (hd + 2) + 1) * sizeof(float), s, part,
+    hipLaunchKernelGGL(k_attn_combine_quant, dim3(n), dim3(COMB_T), (size_t)nh * (2 * (pstride / (hd + 2)) + 1) * sizeof(float), s, part,
                        pstride, nh, hd, pos, aq, as, ldq, att_out);
     return (int)hipGetLastError();
 }
 
-int gw_k_swiglu_quant(const float *hb, int H, int n, int8_t *hq, float *hs, hipStream_t s) {
-    hipLaunchKernelGGL(k_swiglu_quant, dim3(n, H / 256), dim3(256), 0, s, hb, H, hq, hs);
+int gw_k_swiglu_quant(const float *hb, int H, int il, int n, int8_t *hq, float *hs, hipStream_t s) {
+    hipLaunchKernelGGL(k_swiglu_quant, dim3(n, H / 256), dim3(256), 0, s, hb, H, il, hq, hs);
     return (int)hipGetLastError();
 }
 

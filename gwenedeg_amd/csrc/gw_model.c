@@ -291,9 +291,10 @@ static int stage(Loader *L, const Tn *t) {
     return e == hipSuccess ? RQ_OK : gw_hip_fail(L->err, L->errlen, "hipMemcpy (weights)", e);
 }
 
-/* matrix `name` (rows x cols): Q8_0 unpacked into dst's codes / scales from row r0 on (dst pre-allocated for Q8_0);
+/* matrix `name` (rows x cols): Q8_0 unpacked into dst's codes / scales from row r0 on (dst pre-allocated for Q8_0), or
+ * with il > 0 interleaved with another matrix in blocks of il rows (this one's rows at offset off of each block pair);
  * K-quants: the blocks copied (dst allocated here) */
-static int load_mat(Loader *L, GwMat *dst, int r0, const char *name, int rows, int cols) {
+static int load_mat_il(Loader *L, GwMat *dst, int r0, const char *name, int rows, int cols, int il, int off) {
     int rc = RQ_OK;
     const Tn *t = need(L, name, (uint64_t)cols, (uint64_t)rows, &rc);
     if (!t) return rc;
@@ -301,7 +302,7 @@ static int load_mat(Loader *L, GwMat *dst, int r0, const char *name, int rows, i
         if (dst->type != GW_Q8_0) return lfail(L, RQ_ERR_LOAD, "GGUF: %s: internal type mismatch", name);
         if ((rc = stage(L, t)) != RQ_OK) return rc;
         if (gw_k_q8_unpack(L->stage, (size_t)rows * (cols / 32), dst->codes + (size_t)r0 * cols, dst->scales + (size_t)r0 * (cols / 32),
-                           0))
+                           cols / 32, il, off, 0))
             return lfail(L, RQ_ERR_STATE, "GGUF: %s: repack kernel failed", name);
         hipError_t e = hipDeviceSynchronize();
         return e == hipSuccess ? RQ_OK : gw_hip_fail(L->err, L->errlen, "repack", e);
@@ -319,8 +320,13 @@ static int alloc_q8(Loader *L, GwMat *w, int rows, int cols) {
     w->rows = rows;
     w->cols = cols;
     int rc = dmalloc(L, (void **)&w->codes, (size_t)rows * cols);
-    if (rc == RQ_OK) rc = dmalloc(L, (void **)&w->scales, (size_t)rows * (cols / 32) * 2);
+    /* (rounded up to 4 bytes: the decode GEMV reads each scale as its aligned 32-bit word) */
+    if (rc == RQ_OK) rc = dmalloc(L, (void **)&w->scales, ((size_t)rows * (cols / 32) * 2 + 3) & ~(size_t)3);
     return rc;
+}
+
+static int load_mat(Loader *L, GwMat *dst, int r0, const char *name, int rows, int cols) {
+    return load_mat_il(L, dst, r0, name, rows, cols, 0, 0);
 }
 
 static int tensor_type(Loader *L, const char *name) {
@@ -329,7 +335,9 @@ static int tensor_type(Loader *L, const char *name) {
 }
 
 /* a group of matrices fused into one when all are Q8_0 (rows stacked), else each its own */
-static int load_group(Loader *L, GwMat *out, int *nout, int n, const char *const *names, const int *rows, int cols) {
+static int load_group(Loader *L, GwMat *out, int *nout, int n, const char *const *names, const int *rows, int cols, int il) {
+    /* n matrices of `cols` columns: all Q8_0 -> one matrix of their rows stacked (il = 0) or, for n = 2 of equal rows,
+     * interleaved in blocks of il rows; else n matrices as they are */
     int all_q8 = 1, tot = 0, rc;
     for (int i = 0; i < n; i++) {
         all_q8 &= tensor_type(L, names[i]) == GW_Q8_0;
@@ -338,8 +346,9 @@ static int load_group(Loader *L, GwMat *out, int *nout, int n, const char *const
     if (all_q8) {
         *nout = 1;
         if ((rc = alloc_q8(L, &out[0], tot, cols)) != RQ_OK) return rc;
+        if (il && (n != 2 || rows[0] != rows[1] || rows[0] % il)) return lfail(L, RQ_ERR_LOAD, "GGUF: %s: cannot interleave", names[0]);
         for (int i = 0, r0 = 0; i < n; r0 += rows[i], i++)
-            if ((rc = load_mat(L, &out[0], r0, names[i], rows[i], cols)) != RQ_OK) return rc;
+            if ((rc = load_mat_il(L, &out[0], il ? 0 : r0, names[i], rows[i], cols, il, il * i)) != RQ_OK) return rc;
         return RQ_OK;
     }
     *nout = n;
@@ -507,14 +516,15 @@ RqModel *rq_model_load(const char *path, const RqModelOpts *o, char *err, size_t
         snprintf(nm[2], 96, "blk.%d.attn_v.weight", l);
         const char *qkvn[3] = { nm[0], nm[1], nm[2] };
         int qkvr[3] = { qd, kvd, kvd };
-        if ((rc = load_group(&L, y->qkv, &y->nqkv, 3, qkvn, qkvr, dim)) != RQ_OK) goto out;
+        if ((rc = load_group(&L, y->qkv, &y->nqkv, 3, qkvn, qkvr, dim, 0)) != RQ_OK) goto out;
         snprintf(nm[0], 96, "blk.%d.attn_output.weight", l);
         if ((rc = load_single(&L, &y->wo, nm[0], dim, qd)) != RQ_OK) goto out;
         snprintf(nm[0], 96, "blk.%d.ffn_gate.weight", l);
         snprintf(nm[1], 96, "blk.%d.ffn_up.weight", l);
         const char *w13n[2] = { nm[0], nm[1] };
         int w13r[2] = { H, H };
-        if ((rc = load_group(&L, y->w13, &y->nw13, 2, w13n, w13r, dim)) != RQ_OK) goto out;
+        if ((rc = load_group(&L, y->w13, &y->nw13, 2, w13n, w13r, dim, GW_W13_IL)) != RQ_OK) goto out;
+        y->w13_il = y->nw13 == 1 ? GW_W13_IL : 0;
         snprintf(nm[0], 96, "blk.%d.ffn_down.weight", l);
         if ((rc = load_single(&L, &y->w2, nm[0], dim, H)) != RQ_OK) goto out;
     }

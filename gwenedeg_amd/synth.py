@@ -40,6 +40,11 @@ SHAPES = {
                       ctx_len=4096, tied=0, type_default=Q8_0),
     "tiny_kq": dict(dim=512, hidden=1024, n_layers=2, n_heads=8, n_kv_heads=2, head_dim=128, vocab=2048,
                     ctx_len=4096, tied=0, type_default=Q4_K, type_v=Q6_K, type_down=Q6_K, type_out=Q6_K),
+    # head sizes below 128: 8 query heads on one KV head (hd 64), plain multi-head attention (hd 32)
+    "tiny_hd64": dict(dim=256, hidden=512, n_layers=2, n_heads=8, n_kv_heads=1, head_dim=64, vocab=1000, ctx_len=4096,
+                      tied=1, type_default=Q8_0),
+    "tiny_hd32": dict(dim=256, hidden=768, n_layers=2, n_heads=8, n_kv_heads=8, head_dim=32, vocab=1000, ctx_len=4096,
+                      tied=0, type_default=Q8_0),
 }
 
 
