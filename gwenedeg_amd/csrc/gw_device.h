@@ -10,6 +10,33 @@
 #define ATT_T 16
 #define ATT_P 256
 
+// The reference's host-specific operations, reproduced from tables measured on the host (gw_exact.c; installed into
+// every file of kernels by gw_exact_init through gw_k_set_exact / gw_v_set_exact):
+//   rsqrt_ref(t): its 1.0f / sqrtf(t) = r0 = rsqrtss(t) (the CPU's estimate: gw_rsqrt_tab, 2^bits values for t in
+//     [1, 4) by exponent parity and leading mantissa bits, exact up to the power of 4) and one Newton step
+//     r = fma(t r0, r0, -3) (r0 * -0.5); bits 0: IEEE 1 / sqrtf
+//   swiglu_ref(h, h2): its SwiGLU (forward.c:1953-1958, vectorized): x = min(-h, 80), e = libmvec expf(x) (= exp_base(x)
+//     + the measured ulp difference, gw_exp_delta), d = 1 + e, r0 = vrcp14ps(d) (gw_rcp_tab by mantissa, exact up to
+//     the power of 2), r = (r0 + r0) - r0 (r0 d), (h h2) r; without the tables (a host without AVX-512): (h h2) *
+//     (1 / (1 + exp_att(min(-h, 80)))), the portable definition
+#define GW_RSQRT_MAXBITS 14
+static __constant__ float gw_rsqrt_tab[1 << GW_RSQRT_MAXBITS];
+static __constant__ int gw_rsqrt_bits;
+static __constant__ const float *gw_rcp_tab;
+static __constant__ const uint8_t *gw_exp_delta;
+
+__device__ __forceinline__ float rsqrt_ref(float t) {
+    const int bits = gw_rsqrt_bits;
+    if (!bits) return 1.0f / sqrtf(t);
+    uint32_t u = __float_as_uint(t);
+    int e = (int)(u >> 23) - 127, par = e & 1;
+    float r1 = gw_rsqrt_tab[(((uint32_t)par << 23) | (u & 0x7fffffu)) >> (24 - bits)];
+    float r0 = __uint_as_float(__float_as_uint(r1) - (uint32_t)(((e - par) >> 1) << 23));
+    float a = t * r0;
+    float b = __builtin_fmaf(a, r0, -3.0f);
+    return b * (r0 * -0.5f);
+}
+
 __device__ __forceinline__ float h2f(uint16_t h) {
     // IEEE half -> float (exact; v_cvt_f32_f16)
     return __half2float(__ushort_as_half(h));
@@ -49,6 +76,52 @@ __device__ __forceinline__ float exp_att(float x) {
 
 __device__ __forceinline__ float silu_exp(float x) { return exp_att(x < 80.0f ? x : 80.0f); }
 
+__device__ __forceinline__ float exp_base(float x) {
+    // exp_att's operations without its clamp, for x in [-32, 80] (gw_exact.c's gw_exp_base, operation for operation)
+    float n = rintf(x * 1.44269504088896341f);
+    float r = __builtin_fmaf(n, -0.693359375f, x);
+    r = __builtin_fmaf(n, 2.12194440e-4f, r);
+    float z = r * r;
+    float y = 1.9875691500e-4f;
+    y = __builtin_fmaf(y, r, 1.3981999507e-3f);
+    y = __builtin_fmaf(y, r, 8.3334519073e-3f);
+    y = __builtin_fmaf(y, r, 4.1665795894e-2f);
+    y = __builtin_fmaf(y, r, 1.6666665459e-1f);
+    y = __builtin_fmaf(y, r, 5.0000001201e-1f);
+    y = __builtin_fmaf(y, z, r);
+    y = y + 1.0f;
+    return __uint_as_float(__float_as_uint(y) + ((uint32_t)(int32_t)n << 23));
+}
+
+__device__ __forceinline__ float swiglu_ref(float h, float h2) {
+    const float *rt = gw_rcp_tab;
+    const uint8_t *et = gw_exp_delta;
+    if (!rt) {
+        float ex = silu_exp(-h);
+        float r = 1.0f / (1.0f + ex);
+        return (h * h2) * r;
+    }
+    float p = h * h2;
+    float x = -h;
+    x = x < 80.0f ? x : 80.0f;
+    uint32_t u = __float_as_uint(x), E = (u >> 23) & 0xffu;
+    float d = 1.0f; // (x <= -32: e < 2^-24, 1 + e = 1)
+    if (!(u >> 31) || E < 132u) {
+        float e = exp_base(x);
+        if (E >= 101u) { // the tabulated binades: |x| >= 2^-26 (below it libmvec's expf equals exp_base)
+            uint32_t slot = (u >> 31) ? 33u + (E - 101u) : E - 101u, idx = slot << 23 | (u & 0x7fffffu);
+            int dl = (int)((et[idx >> 1] >> ((idx & 1u) * 4u)) & 15u) - 8;
+            e = __uint_as_float(__float_as_uint(e) + (uint32_t)dl);
+        }
+        d = e + 1.0f;
+    }
+    uint32_t v = __float_as_uint(d);
+    float r0 = __uint_as_float(__float_as_uint(rt[v & 0x7fffffu]) - (((v >> 23) - 127u) << 23));
+    float t = r0 * (r0 * d);
+    float r = (r0 + r0) - t;
+    return p * r;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
     for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
     return v;
@@ -56,7 +129,7 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // rmsnorm scale of n floats in LDS (n % 128 == 0), computed by lanes 0..15 of the calling wave, returned to all lanes
 // of that wave: forward.c:886-901 in the reference's compiled order (lane j: an fma chain over x[j], x[j + 16], ...,
-// the tree +8 +4 +2 +1, t = fma(ss, 1/n, 1e-6), 1 / sqrt(t)); n % 16 == 0. The chain's next 16 LDS reads are
+// the tree +8 +4 +2 +1, t = fma(ss, 1/n, 1e-6), rsqrt_ref(t)); n % 16 == 0. The chain's next 16 LDS reads are
 // issued before the current 16 fmas
 __device__ __forceinline__ float rms_scale_lds(const float *xs_lds, int n) {
     int lane = threadIdx.x & 63;
@@ -90,7 +163,7 @@ __device__ __forceinline__ float rms_scale_lds(const float *xs_lds, int n) {
     if (lane == 0) {
         float inv_n = 1.0f / (float)n;
         float t = __builtin_fmaf(s, inv_n, 1e-6f);
-        r = 1.0f / sqrtf(t);
+        r = rsqrt_ref(t);
     }
     return __shfl(r, 0);
 }

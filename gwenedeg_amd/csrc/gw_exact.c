@@ -1,0 +1,238 @@
+/* The reference's host-specific floating point, measured on this host so that the device reproduces it bit for bit.
+ *
+ * The reference is built with gcc -Ofast (-ffast-math) for AVX-512, and three of its operations are not IEEE-defined:
+ *   1.0f / sqrtf(t)  (rmsnorm forward.c:896, QK-norm, the attention scale forward.c:137): gcc expands it into
+ *                    r0 = rsqrtss(t), the CPU's estimate, and one Newton step r = fma(t r0, r0, -3) (r0 * -0.5)
+ *   SwiGLU's expf    (forward.c:1953-1958): the loop is vectorized, e = glibc libmvec's _ZGVeN16v_expf(min(-h, 80))
+ *   SwiGLU's 1 / d   (d = 1 + e): a vector division, r0 = vrcp14ps(d) (the CPU's estimate) and the Newton step
+ *                    r = (r0 + r0) - r0 (r0 d); out = (h h2) r
+ * The estimates (rsqrtss, vrcp14ps) are table lookups inside the CPU, exact up to the power of 2, so a table of their
+ * values measured here on one binade reproduces them everywhere (verified on seeded inputs before use). libmvec's
+ * expf is a function of the full input: the device computes the attention's Cephes-style exp (exp_att's operations,
+ * no clamp: identical on host and device) and adds libmvec's difference from it, measured here for every float the
+ * SwiGLU can meet where the difference matters (|x| in [2^-26, 32) negative, [2^-26, 128) positive: 64 binades, one
+ * signed 4-bit ulp difference each, 256 MiB). Outside: |x| < 2^-26 the two agree (checked exhaustively for
+ * |x| < 2^-20 on the development host: 36 differences among 1.8e9 inputs, all above 2^-26), x <= -32 gives
+ * 1 + e = 1 exactly either way (e < 2^-24), x is clamped at 80.
+ *
+ * The tables are the host's, not constants: the reference's own results differ between CPUs the same way. A host
+ * without AVX-512 leaves them unset, and the device falls back to IEEE 1 / sqrtf and division and the Cephes exp
+ * (then it matches the oracle's portable definition, not the reference's bits).
+ */
+#define _GNU_SOURCE
+#include <immintrin.h>
+#include <math.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "gw_internal.h"
+
+static inline float f_of(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+static inline uint32_t u_of(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+
+static uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+/* ------------------------------------------------------------------------------------------- rsqrtss */
+
+static inline float host_rsqrtss(float x) { return _mm_cvtss_f32(_mm_rsqrt_ss(_mm_set_ss(x))); }
+
+static float rsqrt_lookup(const float *tab, int bits, float t) {
+    /* t > 0 normal: the table's value for t's exponent parity and leading mantissa bits, scaled by t's power of 4 */
+    uint32_t u = u_of(t);
+    int e = (int)(u >> 23) - 127, par = e & 1;
+    float r1 = tab[(((uint32_t)par << 23) | (u & 0x7fffffu)) >> (24 - bits)];
+    return f_of(u_of(r1) - (uint32_t)(((e - par) >> 1) << 23));
+}
+
+float gw_rsqrt_host(float t) {
+    /* the reference's 1.0f / sqrtf(t) on this host (rsqrtss + gcc's Newton step; constants of its object code) */
+    float r0 = host_rsqrtss(t);
+    float b = fmaf(t * r0, r0, -3.0f);
+    return b * (r0 * -0.5f);
+}
+
+static float rsq_tab[1 << GW_RSQRT_MAXBITS_H];
+static int rsq_bits = -1;
+
+static int rsqrt_measure(void) {
+    /* the fewest leading bits (parity + mantissa) that reproduce rsqrtss on 2^20 seeded inputs over 120 binades */
+    for (int bits = 10; bits <= GW_RSQRT_MAXBITS_H; bits++) {
+        for (uint32_t i = 0; i < (1u << bits); i++) rsq_tab[i] = host_rsqrtss(f_of(0x3f800000u + (i << (24 - bits))));
+        int ok = 1;
+        for (uint64_t k = 1; k <= (1u << 20) && ok; k++) {
+            uint64_t r = mix64(k * 0x9e3779b97f4a7c15ull);
+            float t = f_of(((uint32_t)(127 + (int)(r % 120) - 60) << 23) | (uint32_t)((r >> 8) & 0x7fffffu));
+            ok = u_of(rsqrt_lookup(rsq_tab, bits, t)) == u_of(host_rsqrtss(t));
+        }
+        if (ok) return bits;
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ SwiGLU: vrcp14ps and libmvec expf */
+
+__m512 _ZGVeN16v_expf(__m512);
+
+#define EXP_E0 101   /* first tabulated biased exponent (2^-26) */
+#define EXP_POS 33   /* binades of x > 0: exponents 101..133 ([2^-26, 128)) */
+#define EXP_NEG 31   /* binades of x < 0: exponents 101..131 ((-32, -2^-26]) */
+
+float gw_exp_base(float x) {
+    /* the attention's Cephes-style exp (forward.c:1301-1321's operations) without its clamp, for x in [-32, 80]: the
+     * device's exp_base, operation for operation */
+    float n = rintf(x * 1.44269504088896341f);
+    float r = fmaf(n, -0.693359375f, x);
+    r = fmaf(n, 2.12194440e-4f, r);
+    float z = r * r;
+    float y = 1.9875691500e-4f;
+    y = fmaf(y, r, 1.3981999507e-3f);
+    y = fmaf(y, r, 8.3334519073e-3f);
+    y = fmaf(y, r, 4.1665795894e-2f);
+    y = fmaf(y, r, 1.6666665459e-1f);
+    y = fmaf(y, r, 5.0000001201e-1f);
+    y = fmaf(y, z, r);
+    y = y + 1.0f;
+    return f_of(u_of(y) + ((uint32_t)(int32_t)n << 23));
+}
+
+static float *rcp_tab;       /* vrcp14ps of 1.m, 2^23 floats */
+static uint8_t *exp_delta;   /* 2^29 nibbles: libmvec expf - exp_base in ulps, + 8 */
+static int swiglu_ok = -1;   /* -1 not measured, 0 not reproducible here, 1 tables ready */
+
+typedef struct { int slot0, slot1, bad; } ExpJob;
+
+__attribute__((target("avx512f"))) static void *exp_worker(void *arg) {
+    ExpJob *j = arg;
+    float xs[16] __attribute__((aligned(64))), ys[16] __attribute__((aligned(64)));
+    for (int slot = j->slot0; slot < j->slot1 && !j->bad; slot++) {
+        uint32_t sign = slot >= EXP_POS ? 0x80000000u : 0, e = (uint32_t)(EXP_E0 + (slot >= EXP_POS ? slot - EXP_POS : slot));
+        for (uint32_t m = 0; m < (1u << 23) && !j->bad; m += 16) {
+            for (int k = 0; k < 16; k++) xs[k] = f_of(sign | e << 23 | (m + (uint32_t)k));
+            _mm512_store_ps(ys, _ZGVeN16v_expf(_mm512_load_ps(xs)));
+            for (int k = 0; k < 16; k += 2) {
+                /* (x > 80: never met, the argument is clamped; no difference stored) */
+                int d0 = xs[k] > 80.0f ? 0 : (int)(u_of(ys[k]) - u_of(gw_exp_base(xs[k])));
+                int d1 = xs[k + 1] > 80.0f ? 0 : (int)(u_of(ys[k + 1]) - u_of(gw_exp_base(xs[k + 1])));
+                if (d0 < -7 || d0 > 7 || d1 < -7 || d1 > 7) { j->bad = 1; break; }
+                exp_delta[(((size_t)slot << 23) | (m + (uint32_t)k)) >> 1] = (uint8_t)((d0 + 8) | (d1 + 8) << 4);
+            }
+        }
+    }
+    return NULL;
+}
+
+__attribute__((target("avx512f"))) static float host_rcp14(float x) {
+    return _mm512_cvtss_f32(_mm512_rcp14_ps(_mm512_set1_ps(x)));
+}
+
+static int swiglu_measure(void) {
+    if (!__builtin_cpu_supports("avx512f")) return 0;
+    rcp_tab = malloc((size_t)4 << 23);
+    exp_delta = malloc((size_t)1 << 28);
+    if (!rcp_tab || !exp_delta) return 0;
+    for (uint32_t m = 0; m < (1u << 23); m++) rcp_tab[m] = host_rcp14(f_of(0x3f800000u | m));
+    for (uint64_t k = 1; k <= (1u << 20); k++) { /* exact up to the power of 2, on d in [1, 2^120) */
+        uint64_t r = mix64(k * 0xd1b54a32d192ed03ull);
+        float d = f_of(((uint32_t)(127 + (int)(r % 120)) << 23) | (uint32_t)((r >> 8) & 0x7fffffu));
+        uint32_t v = u_of(d);
+        if (u_of(rcp_tab[v & 0x7fffffu]) - (((v >> 23) - 127) << 23) != u_of(host_rcp14(d))) return 0;
+    }
+    enum { NT = 16 };
+    pthread_t th[NT];
+    ExpJob job[NT];
+    int ns = EXP_POS + EXP_NEG, bad = 0, started = 0;
+    for (int i = 0; i < NT; i++) {
+        job[i] = (ExpJob){ ns * i / NT, ns * (i + 1) / NT, 0 };
+        if (pthread_create(&th[i], NULL, exp_worker, &job[i])) { exp_worker(&job[i]); continue; }
+        started |= 1 << i;
+    }
+    for (int i = 0; i < NT; i++) {
+        if (started & (1 << i)) pthread_join(th[i], NULL);
+        bad |= job[i].bad;
+    }
+    return !bad;
+}
+
+/* ------------------------------------------------------------------------------ per-device installation */
+
+static int dev_done[64];
+static void *dev_rcp[64], *dev_exp[64];
+static pthread_mutex_t mu = PTHREAD_MUTEX_INITIALIZER;
+
+int gw_exact_init(char *err, size_t errlen) {
+    /* the tables measured once per process, installed once per device (the current one) */
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return gw_hip_fail(err, errlen, "hipGetDevice", e);
+    pthread_mutex_lock(&mu);
+    int rc = RQ_OK;
+    if (rsq_bits < 0) rsq_bits = rsqrt_measure();
+    if (swiglu_ok < 0) swiglu_ok = swiglu_measure();
+    if (dev < 64 && !dev_done[dev]) {
+        void *rp = NULL, *ep = NULL;
+        if (swiglu_ok) {
+            e = hipMalloc(&rp, (size_t)4 << 23);
+            if (e == hipSuccess) e = hipMalloc(&ep, (size_t)1 << 28);
+            if (e == hipSuccess) e = hipMemcpy(rp, rcp_tab, (size_t)4 << 23, hipMemcpyHostToDevice);
+            if (e == hipSuccess) e = hipMemcpy(ep, exp_delta, (size_t)1 << 28, hipMemcpyHostToDevice);
+            if (e != hipSuccess) {
+                if (rp) hipFree(rp);
+                if (ep) hipFree(ep);
+                rc = gw_hip_fail(err, errlen, "the SwiGLU tables", e);
+            }
+        }
+        if (rc == RQ_OK) {
+            int k = gw_k_set_exact(rsq_tab, rsq_bits, (const float *)rp, (const uint8_t *)ep);
+            if (!k) k = gw_v_set_exact(rsq_tab, rsq_bits, (const float *)rp, (const uint8_t *)ep);
+            if (k) rc = gw_hip_fail(err, errlen, "hipMemcpyToSymbol (exact tables)", (hipError_t)k);
+            else {
+                dev_done[dev] = 1;
+                dev_rcp[dev] = rp;
+                dev_exp[dev] = ep;
+            }
+        }
+    }
+    pthread_mutex_unlock(&mu);
+    return rc;
+}
+
+float gw_swiglu_tab_host(float h, float h2) {
+    /* the device's swiglu_ref with the tables, on the host (checked against the reference's operations by the tests);
+     * the portable definition without them */
+    if (swiglu_ok < 0) swiglu_ok = swiglu_measure();
+    if (swiglu_ok <= 0) {
+        float x = -h;
+        x = x < 80.0f ? x : 80.0f;
+        x = x > -86.0f ? x : -86.0f;
+        return (h * h2) * (1.0f / (1.0f + gw_exp_base(x)));
+    }
+    float p = h * h2, x = -h;
+    x = x < 80.0f ? x : 80.0f;
+    uint32_t u = u_of(x), E = (u >> 23) & 0xffu;
+    float d = 1.0f;
+    if (!(u >> 31) || E < 132u) {
+        float e = gw_exp_base(x);
+        if (E >= 101u) {
+            uint32_t slot = (u >> 31) ? 33u + (E - 101u) : E - 101u, idx = slot << 23 | (u & 0x7fffffu);
+            int dl = (int)((exp_delta[idx >> 1] >> ((idx & 1u) * 4u)) & 15u) - 8;
+            e = f_of(u_of(e) + (uint32_t)dl);
+        }
+        d = e + 1.0f;
+    }
+    uint32_t v = u_of(d);
+    float r0 = f_of(u_of(rcp_tab[v & 0x7fffffu]) - (((v >> 23) - 127u) << 23));
+    float t = r0 * (r0 * d);
+    float r = (r0 + r0) - t;
+    return p * r;
+}
+
+int gw_exact_mode(void) {
+    /* bit 0: the reference's 1 / sqrtf reproduced; bit 1: its SwiGLU reproduced (after gw_exact_init) */
+    return (rsq_bits > 0) | (swiglu_ok > 0) << 1;
+}

@@ -5,13 +5,13 @@
 // producer's output and the matmul. Prologues (each the arithmetic of the kernel it replaces, operation for operation):
 //   GV_Q        none: the row is already quantized (xq, xs)
 //   GV_NORM     rmsnorm (forward.c:886-901): the row into LDS transposed (chain j's values x[j], x[j + 16], ...
-//               contiguous), the 16 fma chains, the tree, r = 1 / sqrt(fma(ss, 1/n, 1e-6)); o = (w * x) * r
+//               contiguous), the 16 fma chains, the tree, r = rsqrt_ref(fma(ss, 1/n, 1e-6)); o = (w * x) * r
 //   GV_QF       none but the quantization: the fp32 row as it is (the SwiGLU output of the w1 / w3 matmul)
 //   GV_COMBINE  att_combine (forward.c:1405-1431) over the row's <= GV_NBMAX key blocks: M = max m_b, c_b =
 //               exp_att(m_b - M), L = fma chain of c_b l_b, o = (fma chain of c_b o_b) * (1 / L)
 // Epilogue (swiglu_il = 4, with R = 8): the rows are w1 / w3 interleaved in blocks of 4, so a tile's rows r and r + 4
-// are h and h2 of one output; its fold lanes write (h * h2) * (1 / (1 + exp_att(min(-h, 80)))) (SwiGLU,
-// forward.c:1953-1958) to out[tile 4 + r] instead of the two dots
+// are h and h2 of one output; its fold lanes write swiglu_ref(h, h2) (SwiGLU, forward.c:1953-1958) to out[tile 4 + r]
+// instead of the two dots
 // The prologue's loads are issued before the weight loads (vector memory counts complete in order, so the prologue's
 // waits leave the weight loads in flight), the weight loads before any prologue arithmetic.
 // Then as k_gemv_q8: the exact int32 sum of a half-group by 4 v_dot4, the lane pair's sums added, the even lane's
@@ -206,7 +206,7 @@ __global__ __launch_bounds__(NT) void k_gemv1(GvArgs a) {
                     float o = __shfl_down(ss, w);
                     ss = ss + o;
                 }
-                if (t == 0) xf[16 * LS] = 1.0f / sqrtf(__builtin_fmaf(ss, 1.0f / (float)K, 1e-6f));
+                if (t == 0) xf[16 * LS] = rsqrt_ref(__builtin_fmaf(ss, 1.0f / (float)K, 1e-6f));
             }
             __syncthreads();
             float r = xf[16 * LS];
@@ -312,11 +312,7 @@ __global__ __launch_bounds__(NT) void k_gemv1(GvArgs a) {
             if (a.swiglu_il) {
                 // (R = 8: the tile's rows r and r + 4, h and h2 of output tile 4 + r, are lanes t and t + 4 of one wave)
                 float h2 = __shfl_down(v, 4);
-                if (fl && (t & 7) < 4) {
-                    float ex = silu_exp(-v);
-                    float rr = 1.0f / (1.0f + ex);
-                    a.out[(row >> 3) * 4 + (row & 7)] = (v * h2) * rr;
-                }
+                if (fl && (t & 7) < 4) a.out[(row >> 3) * 4 + (row & 7)] = swiglu_ref(v, h2);
             } else if (fl) {
                 a.out[row] = a.mode == 1 ? a.out[row] + v : v;
             }
@@ -372,6 +368,15 @@ static int gv_launch(int pro, int R, const GvArgs &a, hipStream_t s) {
 #undef GV_R
 #undef GV_L
     return (int)hipGetLastError();
+}
+
+int gw_v_set_exact(const float *rsq, int bits, const float *rcp, const uint8_t *expd) {
+    /* this file's copy of the host-measured tables (rsqrt_ref, swiglu_ref) on the current device */
+    hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(gw_rsqrt_bits), &bits, sizeof(int));
+    if (e == hipSuccess && bits) e = hipMemcpyToSymbol(HIP_SYMBOL(gw_rsqrt_tab), rsq, sizeof(float) << bits);
+    if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(gw_rcp_tab), &rcp, sizeof(rcp));
+    if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(gw_exp_delta), &expd, sizeof(expd));
+    return (int)e;
 }
 
 static int gv_check(const GwMat *w, int R) {

@@ -105,6 +105,14 @@ static inline double gw_mat_file_bytes(const GwMat *w) {
 
 /* model / device helpers (gw_model.c) */
 int gw_device_init(char *err, size_t errlen);
+/* the reference's host-specific arithmetic (gw_exact.c): tables measured on this host, installed per device */
+#define GW_RSQRT_MAXBITS_H 14
+int gw_exact_init(char *err, size_t errlen);
+int gw_exact_mode(void);        /* bit 0: 1 / sqrtf reproduced, bit 1: SwiGLU reproduced */
+float gw_rsqrt_host(float t);   /* the reference's 1.0f / sqrtf(t) on this host */
+float gw_exp_base(float x);     /* the device's exp_base, for the table */
+int gw_k_set_exact(const float *rsq, int bits, const float *rcp, const uint8_t *expd); /* gw_kernels.hip's copy */
+int gw_v_set_exact(const float *rsq, int bits, const float *rcp, const uint8_t *expd); /* gw_gemv.hip's copy */
 int gw_hip_fail(char *err, size_t errlen, const char *what, hipError_t e);
 
 /* kernels (gw_kernels.hip) */

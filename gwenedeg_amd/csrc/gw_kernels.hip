@@ -7,14 +7,15 @@
 //   Q8_0 fold    forward.c:906-916,      exact int32 sum per group of 32; val = val + (ws * xs) * (float) isum, groups in
 //                kernels_avx512.h:157    order (one lane folds one output)
 //   rmsnorm      forward.c:886-901       16 fma chains (lane j: x[j], x[j+16], ...), the tree +8 +4 +2 +1,
-//                                        t = fma(ss, 1/n, 1e-6), scale = 1 / sqrt(t), o = (w * x) * scale
+//                                        t = fma(ss, 1/n, 1e-6), scale = rsqrt_ref(t) (the host CPU's rsqrtss +
+//                                        gcc's Newton step), o = (w * x) * scale
 //   RoPE         forward.c:1266-1284     x' = fma(x, c, -(y s)), y' = fma(x, s, y c); cos / sin from the host's table
 //   attention    kernels_avx512.h:1109   per 256-position block: scores as 4 chunk fma chains of 32 dims added in order,
 //                forward.c:1346-1431     times scale; m = max; e = exp_att(s - m); l = 16 lane chains + tree; o = fma
 //                                        chain over positions in order; blocks combined in order (att_combine)
 //   f16 KV       forward.c:1325-1344,    f32_f16's rounding; K transposed in 16-position tiles, V row-major
 //                :1894-1951
-//   SwiGLU       forward.c:1953-1958     (h * h2) * (1 / (1 + e)), e = exp_att-style exp of min(-h, 80)
+//   SwiGLU       forward.c:1953-1958     swiglu_ref: the reference's vector expf and rcp14 + Newton (host tables)
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 #include <stdint.h>
@@ -526,16 +527,13 @@ __global__ __launch_bounds__(COMB_T) void k_attn_combine_quant(const float *__re
 // ------------------------------------------------------------------------------------ SwiGLU + quantize
 
 // row blockIdx.x of hb = [h (H) | h2 (H)] (il = 0) or blocks of il h then il h2 (il > 0), values 256 blockIdx.y .. + 255:
-// v = (h * h2) * (1 / (1 + exp(min(-h, 80)))), quantized into hq / hs (one lane per value)
+// v = swiglu_ref(h, h2) (SwiGLU, forward.c:1953-1958), quantized into hq / hs (one lane per value)
 __global__ __launch_bounds__(256) void k_swiglu_quant(const float *__restrict__ hb, int H, int il, int8_t *__restrict__ hq,
                                                       float *__restrict__ hs) {
     int b = blockIdx.x, e = blockIdx.y * 256 + threadIdx.x;
     const float *h1 = hb + (size_t)b * 2 * H;
     int i1 = il ? (e / il) * 2 * il + e % il : e, i2 = il ? i1 + il : H + e;
-    float h = h1[i1];
-    float ex = silu_exp(-h);
-    float r = 1.0f / (1.0f + ex);
-    float v = (h * h1[i2]) * r;
+    float v = swiglu_ref(h1[i1], h1[i2]);
     quant_lane32(v, hq + (size_t)b * H + e, hs + (size_t)b * (H / 32) + (e >> 5));
 }
 
@@ -612,6 +610,15 @@ int gw_k_rmsnorm_quant(float *x, const float *d, int dim, const float *w, const 
                        float *hid, hipStream_t s) {
     hipLaunchKernelGGL(k_rmsnorm_quant, dim3(n), dim3(NORM_T), (size_t)dim * sizeof(float), s, x, d, dim, w, sel, xq, xs, ldq, hid);
     return (int)hipGetLastError();
+}
+
+int gw_k_set_exact(const float *rsq, int bits, const float *rcp, const uint8_t *expd) {
+    /* this file's copy of the host-measured tables (rsqrt_ref, swiglu_ref) on the current device */
+    hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(gw_rsqrt_bits), &bits, sizeof(int));
+    if (e == hipSuccess && bits) e = hipMemcpyToSymbol(HIP_SYMBOL(gw_rsqrt_tab), rsq, sizeof(float) << bits);
+    if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(gw_rcp_tab), &rcp, sizeof(rcp));
+    if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(gw_exp_delta), &expd, sizeof(expd));
+    return (int)e;
 }
 
 int gw_k_gemv_q8(const int8_t *W, const uint16_t *WS, int nrows, int K, const int8_t *xq, const float *xs, int ldx, int M,

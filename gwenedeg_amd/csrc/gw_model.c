@@ -405,14 +405,17 @@ static unsigned long long fingerprint(const uint8_t *map, size_t size) {
 }
 
 static void rope_table(float *cs, int hd, int npos, float log_theta) {
-    /* rope_row (forward.c:1248-1264) for positions 0..npos-1 */
+    /* rope_row (forward.c:1248-1264) for positions 0..npos-1, with the libm calls the reference's build makes there:
+     * expf, and one sincosf for the cosf / sinf pair */
     for (int pos = 0; pos < npos; pos++, cs += hd)
         for (int j = 0; j < hd / 2; j++) {
-            float freq = expf(log_theta * (-(float)j / (hd / 2)));
-            cs[j] = cosf(pos * freq);
-            cs[j + hd / 2] = sinf(pos * freq);
+            float freq = expf(log_theta * (-(float)j / (hd / 2))), c, sn;
+            sincosf(pos * freq, &sn, &c);
+            cs[j] = c;
+            cs[j + hd / 2] = sn;
         }
 }
+
 
 RqModel *rq_model_load(const char *path, const RqModelOpts *o, char *err, size_t errlen) {
     char dummy[8];
@@ -421,7 +424,7 @@ RqModel *rq_model_load(const char *path, const RqModelOpts *o, char *err, size_t
     RqModelOpts opts;
     memset(&opts, 0, sizeof opts);
     if (o) opts = *o;
-    if (gw_device_init(err, errlen) != RQ_OK) return NULL;
+    if (gw_device_init(err, errlen) != RQ_OK || gw_exact_init(err, errlen) != RQ_OK) return NULL;
     Loader L;
     memset(&L, 0, sizeof L);
     L.err = err;
@@ -495,7 +498,7 @@ RqModel *rq_model_load(const char *path, const RqModelOpts *o, char *err, size_t
     m->seq_len = cap;
     m->rope_theta = theta;
     m->log_theta = (float)log((double)theta);
-    m->att_scale = 1.0f / sqrtf((float)hd);
+    m->att_scale = gw_rsqrt_host((float)hd); /* forward.c:137 as compiled: 1.0f / sqrtf(head_dim) */
     m->fingerprint = fingerprint(L.g.map, L.g.size);
     /* device staging: the largest tensor */
     size_t big = 0;

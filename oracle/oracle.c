@@ -18,6 +18,8 @@
  *     reference's bits there come from -Ofast (rsqrt estimate + Newton for 1 / sqrtf, reassociated sums) and from
  *     glibc's vector expf / sincosf, so they are reproduced to tolerance, not to the bit (parity unpinned at bit level).
  */
+#define _GNU_SOURCE
+#include <immintrin.h>
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -340,11 +342,18 @@ void or_attention(float *out, const float *q, const uint16_t *kc, const uint16_t
 
 /* ------------------------------------------------------------------------------- norms, RoPE, SwiGLU */
 
+float or_rsqrt_ref(float t) {
+    /* the reference's 1.0f / sqrtf(t) as gcc -Ofast compiles it (forward.c:896, :137): r0 = rsqrtss(t), this host's
+     * estimate, then one Newton step r = fma(t r0, r0, -3) (r0 * -0.5) (the constants of our build's object code) */
+    float r0 = _mm_cvtss_f32(_mm_rsqrt_ss(_mm_set_ss(t)));
+    float b = fmaf(t * r0, r0, -3.0f);
+    return b * (r0 * -0.5f);
+}
+
 float or_rms_scale(const float *x, int n) {
     /* rmsnorm's scale (forward.c:886-901) in the operation order gcc -Ofast gives the reference (its rmsnorm and every
      * inlined copy): 16 lanes, lane j an fma chain over x[j], x[j + 16], ... from 0; the fixed tree (lanes j + 8, then
-     * + 4, + 2, + 1); t = fma(ss, 1 / n, 1e-6); 1 / sqrt(t). The reference takes an rsqrt estimate + one Newton step
-     * there (vrsqrtss, host-specific bits); here both operations are IEEE (n % 16 == 0) */
+     * + 4, + 2, + 1); t = fma(ss, 1 / n, 1e-6) (1 / n an IEEE division); or_rsqrt_ref(t) (n % 16 == 0) */
     float s[16];
     for (int j = 0; j < 16; j++) s[j] = 0.0f;
     for (int j = 0; j < n; j++) s[j % 16] = fmaf(x[j], x[j], s[j % 16]);
@@ -352,7 +361,7 @@ float or_rms_scale(const float *x, int n) {
         for (int j = 0; j < w; j++) s[j] = s[j] + s[j + w];
     float inv_n = 1.0f / (float)n;
     float t = fmaf(s[0], inv_n, 1e-6f);
-    return 1.0f / sqrtf(t);
+    return or_rsqrt_ref(t);
 }
 
 void or_rmsnorm(float *o, const float *x, const float *w, int n) {
@@ -362,11 +371,13 @@ void or_rmsnorm(float *o, const float *x, const float *w, int n) {
 }
 
 void or_rope_row(float *cs, int hd, int pos, float log_theta) {
-    /* forward.c:1248-1264 (glibc's scalar expf / cosf / sinf here; the reference's loop may take libmvec's) */
+    /* forward.c:1248-1264 with the libm calls of the reference's build there: glibc's scalar expf, and one sincosf
+     * for the cosf / sinf pair */
     for (int j = 0; j < hd / 2; j++) {
-        float freq = expf(log_theta * (-(float)j / (hd / 2)));
-        cs[j] = cosf(pos * freq);
-        cs[j + hd / 2] = sinf(pos * freq);
+        float freq = expf(log_theta * (-(float)j / (hd / 2))), c, sn;
+        sincosf(pos * freq, &sn, &c);
+        cs[j] = c;
+        cs[j + hd / 2] = sn;
     }
 }
 
@@ -393,9 +404,37 @@ float or_silu_exp(float x) {
     return or_exp_att(x);
 }
 
+static int swiglu_host = -1; /* -1: the reference's operations where this host has them (AVX-512) */
+
+void or_set_swiglu_host(int on) { swiglu_host = on; }
+
+__m512 _ZGVeN16v_expf(__m512); /* glibc libmvec: the vector expf gcc calls in the reference's SwiGLU loop */
+
+__attribute__((target("avx512f"))) static void swiglu_host16(float *hb, const float *hb2, int n) {
+    /* forward.c:1953-1958 as our build of the reference runs it, 16 values at a time: x = min(-h, 80), e = libmvec
+     * expf(x), d = e + 1, r0 = rcp14(d) (this host's estimate), r = (r0 + r0) - (r0 d) r0, out = (h h2) r */
+    for (int i = 0; i < n; i += 16) {
+        __m512 h = _mm512_loadu_ps(hb + i), h2 = _mm512_loadu_ps(hb2 + i);
+        __m512 x = _mm512_min_ps(_mm512_sub_ps(_mm512_setzero_ps(), h), _mm512_set1_ps(80.0f));
+        __m512 d = _mm512_add_ps(_ZGVeN16v_expf(x), _mm512_set1_ps(1.0f));
+        __m512 p = _mm512_mul_ps(h, h2);
+        __m512 r0 = _mm512_rcp14_ps(d);
+        __m512 t = _mm512_mul_ps(r0, _mm512_mul_ps(r0, d));
+        __m512 r = _mm512_sub_ps(_mm512_add_ps(r0, r0), t);
+        _mm512_storeu_ps(hb + i, _mm512_mul_ps(p, r));
+    }
+}
+
 void or_swiglu(float *hb, const float *hb2, int n) {
-    /* forward.c:1953-1958 in the compiled order: (h * h2) * (1 / (1 + e)), e = exp(min(-h, 80)); the reference's
-     * reciprocal is an rcp14 estimate + Newton step, here an IEEE division */
+    /* forward.c:1953-1958 in the compiled order: (h * h2) * (1 / (1 + e)), e = exp(min(-h, 80)). On an AVX-512 host
+     * (default; or_set_swiglu_host(1)): the reference's own operations here, libmvec's vector expf and rcp14 + Newton
+     * (n % 16 == 0), which the device reproduces from tables measured on the host. or_set_swiglu_host(0) or no
+     * AVX-512: the portable definition, e = or_silu_exp, 1 / (1 + e) an IEEE division */
+    if (swiglu_host < 0) swiglu_host = __builtin_cpu_supports("avx512f");
+    if (swiglu_host && n % 16 == 0) {
+        swiglu_host16(hb, hb2, n);
+        return;
+    }
     for (int i = 0; i < n; i++) {
         float h = hb[i];
         float e = or_silu_exp(-h);
@@ -509,14 +548,14 @@ OrModel *or_model_load(const char *path, int cap, char *err, size_t errlen) {
     m->cap = cap > 0 && cap < ctx ? cap : ctx;
     m->kv_len = (m->cap + ATT_P - 1) / ATT_P * ATT_P;
     m->log_theta = (float)log((double)theta);
-    m->att_scale = 1.0f / sqrtf((float)m->hd);
+    m->att_scale = or_rsqrt_ref((float)m->hd); /* forward.c:137 as compiled */
     if (m->L < 1 || m->dim < 32 || m->nh < 1 || m->nkv < 1 || m->nh % m->nkv) FAIL("bad hyperparameters");
-#define FIND(nm, dst, rows_, cols_) do { int found_ = 0; for (uint64_t i_ = 0; i_ < nt; i_++) \
+#define FIND(nm, dst, rows_, cols_) do { int found_ = 0; for (uint64_t i_ = 0; i_ < nt; i_++) { \
         if (T[i_].nlen == strlen(nm) && !memcmp(T[i_].name, nm, T[i_].nlen)) { \
             (dst).type = (int)T[i_].type; (dst).cols = (int)T[i_].ne[0]; (dst).rows = (int)(T[i_].nd > 1 ? T[i_].ne[1] : 1); \
             (dst).data = f + data + T[i_].off; found_ = 1; \
             if ((rows_) && ((dst).rows != (rows_) || (dst).cols != (cols_))) FAIL("tensor %s: bad shape", nm); \
-            if (data + T[i_].off + (size_t)(dst).rows * row_bytes((dst).type, (dst).cols) > sz) FAIL("tensor %s truncated", nm); } \
+            if (data + T[i_].off + (size_t)(dst).rows * row_bytes((dst).type, (dst).cols) > sz) FAIL("tensor %s truncated", nm); } } \
         if (!found_) FAIL("tensor %s missing", nm); } while (0)
     FIND("token_embd.weight", m->embd, 0, 0);
     m->vocab = m->embd.rows;

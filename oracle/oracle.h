@@ -39,12 +39,14 @@ void or_attention_block(float *o, float *ml, const float *q, const uint16_t *kc,
 void or_att_combine(float *out, int nb, const float *part, size_t stride, int hd); /* forward.c:1405-1431 */
 
 /* norms, RoPE, SwiGLU (forward.c:886-901, :1248-1284, :1953-1958) */
+float or_rsqrt_ref(float t);      /* the reference's 1.0f / sqrtf on this host: rsqrtss + Newton */
 float or_rms_scale(const float *x, int n);
 void or_rmsnorm(float *o, const float *x, const float *w, int n);
 float or_silu_exp(float x);
 void or_rope_row(float *cs, int hd, int pos, float log_theta);
 void or_qk_norm_rope(float *v, int n_heads, const float *w, int hd, const float *cs);
 void or_swiglu(float *hb, const float *hb2, int n);
+void or_set_swiglu_host(int on); /* 1: SwiGLU with this host's libmvec expf + rcp14 (the reference's exact bits) */
 
 /* the whole forward pass of one row (decode_worker, forward.c:2568-2813) on a model read from a GGUF file */
 typedef struct OrModel OrModel;

@@ -45,6 +45,8 @@ def lib() -> ctypes.CDLL:
             "or_attention_block": (None, [P, P, P, P, P, I, I, I, I, I, F]),
             "or_att_combine": (None, [P, I, P, ctypes.c_size_t, I]),
             "or_rms_scale": (F, [P, I]),
+            "or_rsqrt_ref": (F, [F]),
+            "or_set_swiglu_host": (None, [I]),
             "or_rmsnorm": (None, [P, P, P, I]),
             "or_silu_exp": (F, [F]),
             "or_rope_row": (None, [P, I, I, F]),
@@ -176,7 +178,7 @@ def have_ref() -> bool:
 
 def run_ref_driver(model: str, ids: np.ndarray, workdir: str, steps: int = 0, threads: int = 0, cap: int = 0,
                    batch: int = 512, all_logits: bool = False, batch_decode: int = 0, reps: int = 1, kv: bool = False,
-                   timeout: float = 600):
+                   hidden: bool = False, timeout: float = 600):
     """The reference's own CPU path (oracle/_ref/ref_driver) on a GGUF file and token ids: returns (info JSON,
     logits rows written, generated tokens, KV file path or None)."""
     os.makedirs(workdir, exist_ok=True)
@@ -195,12 +197,17 @@ def run_ref_driver(model: str, ids: np.ndarray, workdir: str, steps: int = 0, th
         cmd += ["--batch-decode", str(batch_decode)]
     if kv:
         cmd += ["--kv", kv_path]
+    hid_path = os.path.join(workdir, "hidden.bin")
+    if hidden:
+        cmd += ["--hidden", hid_path]
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)
     if r.returncode != 0:
         raise RuntimeError(f"ref_driver failed: {r.stderr[-2000:]}")
     info = json.loads(r.stdout.strip().splitlines()[-1])
     lg = np.fromfile(lg_path, np.float32).reshape(-1, info["vocab"])
-    toks = np.fromfile(tok_path, np.int32) if os.path.getsize(tok_path) else np.zeros(0, np.int32)
+    if hidden:  # (token by token: the rows' logits and final hidden states)
+        return info, lg, np.fromfile(hid_path, np.float32).reshape(-1, info["dim"]), None
+    toks = np.fromfile(tok_path, np.int32) if os.path.exists(tok_path) and os.path.getsize(tok_path) else np.zeros(0, np.int32)
     return info, lg, toks, (kv_path if kv else None)
 
 

@@ -8,6 +8,8 @@
  *   the blocks "as in memory", seqfile.c:8-27), and timing each phase (best of --reps runs).
  *   --batch-decode N: N independent sequences, each prefilled with the same prompt, then --steps batched decode
  *   passes of one row per sequence (rq_forward_batch, RQ_LOGITS_LAST each: batch_decode_worker).
+ *   --hidden FILE: instead, the prompt token by token through rq_decode_hidden (runq.h:350), every row's logits and
+ *   final hidden state (after output_norm, dim floats) written.
  * Output: one JSON line on stdout. */
 #include <stdint.h>
 #include <stdio.h>
@@ -39,7 +41,7 @@ static void write_all(FILE *f, const void *p, size_t n) {
 }
 
 int main(int argc, char **argv) {
-    const char *model = NULL, *ids_path = NULL, *logits_path = NULL, *tokens_path = NULL, *kv_path = NULL;
+    const char *model = NULL, *ids_path = NULL, *logits_path = NULL, *tokens_path = NULL, *kv_path = NULL, *hidden_path = NULL;
     int threads = 0, cap = 0, maxb = 512, steps = 0, reps = 1, all_logits = 0, nbd = 0;
     for (int i = 1; i < argc; i++) {
         const char *a = argv[i], *v = i + 1 < argc ? argv[i + 1] : NULL;
@@ -55,6 +57,7 @@ int main(int argc, char **argv) {
         else if (!strcmp(a, "--kv") && v) kv_path = v, i++;
         else if (!strcmp(a, "--batch-decode") && v) nbd = atoi(v), i++;
         else if (!strcmp(a, "--all-logits")) all_logits = 1;
+        else if (!strcmp(a, "--hidden") && v) hidden_path = v, i++;
         else { fprintf(stderr, "ref_driver: bad argument %s\n", a); return 2; }
     }
     if (!model || !ids_path) { fprintf(stderr, "usage: ref_driver -m MODEL --ids FILE [--steps K] ...\n"); return 2; }
@@ -91,6 +94,21 @@ int main(int argc, char **argv) {
         for (int i = 0; i < ns; i++) rq_seq_reset(sq[i]);
         double t0 = rq_now();
         float *lg = NULL;
+        if (hidden_path) { /* the prompt token by token through rq_decode_hidden: every row's logits and final hidden state */
+            FILE *hf = fopen(hidden_path, "wb");
+            float *hid = malloc((size_t)info.dim * sizeof(float));
+            if (!hf || !hid) { perror(hidden_path); return 1; }
+            for (int j = 0; j < n; j++) {
+                if ((e = rq_decode_hidden(c, sq[0], ids[j], &lg, hid, NULL)) != RQ_OK) die("rq_decode_hidden", e, c);
+                write_all(lf, lg, (size_t)V * sizeof(float));
+                write_all(hf, hid, (size_t)info.dim * sizeof(float));
+            }
+            fclose(hf);
+            free(hid);
+            printf("{\"threads\": %d, \"vocab\": %d, \"dim\": %d, \"prompt\": %d}\n", rq_threads(), V, info.dim, n);
+            if (lf) fclose(lf);
+            return 0;
+        }
         for (int i = 0; i < ns; i++) {
             if ((e = rq_prefill(c, sq[i], ids, n, all_logits ? RQ_LOGITS_ALL : RQ_LOGITS_LAST, all_logits ? out : NULL, &lg)) != RQ_OK)
                 die("rq_prefill", e, c);
