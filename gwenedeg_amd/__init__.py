@@ -50,6 +50,15 @@ def _load(path: str) -> ctypes.CDLL:
 lib = _load(LIB_PATH)
 
 
+lib.gw_exact_mode.restype = ctypes.c_int
+lib.gw_exact_mode.argtypes = []
+
+
+def exact_mode() -> int:
+    """gw_exact_mode: 3 when the device reproduces the reference's host float operations bit for bit (after a load)"""
+    return lib.gw_exact_mode()
+
+
 class RqModelOpts(ctypes.Structure):  # runq.h:63-81
     _fields_ = [("ctx_len", ctypes.c_int), ("tokenizer_only", ctypes.c_int), ("no_tokenizer", ctypes.c_int),
                 ("mem", ctypes.c_double), ("kv_bits", ctypes.c_int), ("page_cache", ctypes.c_int),

@@ -184,6 +184,13 @@ int gw_kq_matmul(float *out, int type, const void *blocks, int N, int K, const i
 /* The context's stream (a hipStream_t), for callers that time the passes with events on it */
 void *gw_ctx_stream(RqCtx *c);
 
+/* Which of the reference's host-specific float operations the device reproduces, measured on this host at the first
+ * rq_model_load (no counterpart in runq.h): bit 0 its 1.0f / sqrtf (rsqrtss + Newton: rmsnorm forward.c:896,
+ * QK-norm, the attention scale forward.c:137), bit 1 its SwiGLU (libmvec vector expf, vrcp14ps + Newton,
+ * forward.c:1953-1958). 3: the device's results equal the reference's CPU path on this host bit for bit; otherwise
+ * the missing operation falls back to IEEE (sqrtf, division) and the attention's exp. 0 before any model load */
+int gw_exact_mode(void);
+
 #ifdef __cplusplus
 }
 #endif
