@@ -2,17 +2,26 @@
 
 One step = the run shape of the reference's config 1 on the metric's model: reset the sequence, prefill a 512-token
 prompt of seeded random ids (rq_prefill, one 512-row pass), then 128 greedy decode steps (rq_decode with the argmax on
-the device, gw_decode_argmax). value = (512 + 128) tokens per step / seconds per step, whole job (one GPU).
+the device, gw_decode_argmax). value = (512 + 128) tokens per step / seconds per step, whole job (one GPU), inputs
+(weights, prompt ids) resident on the device before the timed region starts.
 Weights: random-init, N(0, 0.02) then Q8_0 (a synthetic GGUF written by gwenedeg_amd.synth, seeded); no checkpoint.
 
 Also on the JSON line:
-  roofline      the dominant kernel, the decode GEMV (k_gemv_q8 on one activation row): the decode step's weight
-                matmuls run back to back (gw_ctx_gemv_sweep) and timed with HIP events on the context's stream;
-                achieved = file-format weight bytes per launch / average launch duration, against 8 TB/s HBM
-  cpu_baseline  the reference's own CPU path (oracle/_ref/ref_driver, -Ofast AVX-512 VNNI) on the same GGUF file and
-                prompt, all host cores, a bounded sample (the 512-token prefill + 32 decode steps), scaled to one step
+  roofline          the dominant kernel, the decode GEMV (k_gemv1: every weight matmul of a decode step, 145 launches
+                    per token at 8B, about three quarters of the decode kernel time): right after the timed region, a
+                    replica of the timed step (same prompt, same tokens) in which every kernel records its own start
+                    and stop (hipExtLaunchKernel's events on the context's stream: the dispatch's timestamps; they
+                    cost host time per launch, so that step is not the timed one); achieved = file-format weight
+                    bytes (Q8_0: 34 bytes per 32 weights) per launch / average launch duration, against 8 TB/s. traffic: HBM bytes per launch measured by rocprofv3 FETCH_SIZE +
+                    WRITE_SIZE (scaled by a copy kernel of known size), read from profiles/decode_gemv_traffic.json
+  roofline_prefill  the prefill GEMM (k_gemm_q8, the 512-row matmuls) of the same step: 2 ops per weight per row
+                    against 5.0 POPS dense int8, with the bound the exact per-32 float fold sets on the VALU
+  cpu_baseline      the reference's own CPU path (oracle/_ref/ref_driver, -Ofast AVX-512 VNNI) on the same GGUF file,
+                    prompt and step (512-token prefill + 128 greedy decode steps), all host threads, best of 3 runs
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--prompt 512] [--gen 128] [--no-cpu-baseline]
+       python bench.py --probe [--gen N]   (for rocprofv3 counter runs: warm-up, then one prefill + N decode steps and a
+                                            1 GiB negation, the calibration kernel of the traffic figures; no timing)
 """
 import argparse
 import json
@@ -27,6 +36,10 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
+# the prefill GEMM's exact fold (val = val + (ws * xs) * (float) isum per output and group of 32, each op rounded):
+# 4 VALU lane-ops (convert, 2 multiplies, add) per 64 int8 ops; 256 CUs x 64 fp32 lanes x 2.4 GHz = 39.3 T lane-ops/s
+FOLD_BOUND_TOPS = 256 * 64 * 2.4e9 / 4 * 64 / 1e12
+GEMV_CLASSES = ("matmul qkv", "matmul wo", "matmul w1+w3", "matmul w2", "classifier")
 
 
 def log(*a):
@@ -44,7 +57,8 @@ def main():
     ap.add_argument("--model", default="")
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-decode", type=int, default=32)
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--probe", action="store_true")
     ap.add_argument("--workdir", default=os.environ.get("GW_BENCH_DIR", "/dev/shm/gwenedeg_bench" if os.path.isdir("/dev/shm")
                                                                       else "/tmp/gwenedeg_bench"))
     a = ap.parse_args()
@@ -71,6 +85,10 @@ def main():
     s = m.seq(cap)
     ids = np.random.default_rng(a.seed).integers(0, m.vocab, a.prompt).astype(np.int32)
 
+    if a.probe:
+        probe(torch, gw, c, s, ids, a)
+        return
+
     def step():
         s.reset()
         t0 = time.perf_counter()
@@ -84,13 +102,17 @@ def main():
         t2 = time.perf_counter()
         return t1 - t0, t2 - t1, toks
 
+    c.kernel_timing(True)  # (the event pool is created here, outside the timed region)
     for _ in range(a.warmup):
         step()
+    c.kernel_timing(False)
     torch.cuda.synchronize()
-    tp, td = [], []
+    tp, td, step_ms = [], [], []
     t_start = time.perf_counter()
-    for _ in range(a.steps):
+    for i in range(a.steps):
+        t0 = time.perf_counter()
         p, d, toks = step()
+        step_ms.append(round(1e3 * (time.perf_counter() - t0), 3))
         tp.append(p)
         td.append(d)
     torch.cuda.synchronize()
@@ -99,17 +121,30 @@ def main():
     value = a.steps * (a.prompt + a.gen) / elapsed
     prefill_tok_s = a.prompt / (sum(tp) / len(tp))
     decode_tok_s = a.gen / (sum(td) / len(td))
+    # a replica of the timed step (same prompt, same tokens) in which every kernel records its own start / stop: the
+    # kernels' durations (the events cost host time per launch, so this step itself is not timed)
+    c.kernel_timing(True)
+    _, _, toks_r = step()
+    dec = c.kernel_times(multi=False)  # its decode passes
+    pre = c.kernel_times(multi=True)   # its prefill pass
+    c.kernel_timing(False)
+    assert toks_r == toks, "the replica step chose other tokens"
 
-    # roofline of the dominant kernel: the decode GEMV, on the model's own weights (8 GB per sweep: no cache reuse)
-    c.gemv_sweep(1)
-    sw_s, sw_bytes, sw_n = c.gemv_sweep(3)
-    achieved = sw_bytes / sw_s / 1e9
-    # per-class device time of one profiled decode step (HIP events; classes of rq_ctx_profile)
-    c.profile(True)
-    s.truncate(a.prompt)
-    c.decode_argmax(s, 1)
-    prof = {k: round(v[0] * 1e3, 4) for k, v in c.profile_read().items() if v[1]}
-    c.profile(False)
+    # roofline of the dominant kernel (the decode GEMV) and of the prefill GEMM, from those kernel times
+    info = m.info
+    q, kv = info.n_heads * info.head_dim, info.n_kv_heads * info.head_dim
+    layer_w = info.dim * (q + 2 * kv) + q * info.dim + 3 * info.hidden_dim * info.dim
+    cls_w = info.vocab_size * info.dim
+    tok_bytes = (info.n_layers * layer_w + cls_w) * 34 / 32  # Q8_0 file bytes per decode token
+    g_s = sum(dec[k][0] for k in GEMV_CLASSES)
+    g_n = sum(dec[k][1] for k in GEMV_CLASSES)
+    dec_s = sum(v[0] for v in dec.values())
+    achieved = a.gen * tok_bytes / g_s / 1e9
+    pre_ops = 2.0 * a.prompt * info.n_layers * layer_w  # the 512-row matmuls (the classifier takes one row)
+    m_s = sum(pre[k][0] for k in GEMV_CLASSES[:4])
+    m_n = sum(pre[k][1] for k in GEMV_CLASSES[:4])
+    tops = pre_ops / m_s / 1e12
+    sw_s, sw_bytes, sw_n = c.gemv_sweep(2)
 
     out = {
         "metric": "decode + prefill tok/s (Qwen3-8B-shape Q8_0, 1 GPU); % HBM / int8-MFMA peak",
@@ -129,39 +164,83 @@ def main():
         "prefill_tok_s": round(prefill_tok_s, 1),
         "decode_tok_s": round(decode_tok_s, 2),
         "decode_ms_per_token": round(1e3 / decode_tok_s, 4),
-        "roofline": {"bound": "hbm", "kernel": "k_gemv_q8<1,4> (decode GEMV, one activation row)",
+        "step_ms": step_ms,
+        "roofline": {"bound": "hbm", "kernel": "k_gemv1 (decode GEMV: qkv, wo, w1+w3, w2, classifier)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "launches_per_step": sw_n, "bytes_per_step": sw_bytes,
-                     "avg_launch_us": round(1e6 * sw_s / sw_n, 3),
-                     "algorithmic_bytes_per_launch": round(sw_bytes / sw_n)},
-        "profile_ms_per_decode_step": prof,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_per_launch(),
+                     "launches": g_n, "avg_launch_us": round(1e6 * g_s / g_n, 3),
+                     "algorithmic_bytes_per_launch": round(a.gen * tok_bytes / g_n),
+                     "bytes_per_token": tok_bytes, "share_of_decode_kernel_time": round(g_s / dec_s, 4),
+                     "measured": "each kernel's own start / stop (hipExtLaunchKernel events on the context's stream) "
+                                 f"over the {a.gen} decode passes of a replica of the timed step, run after it",
+                     "sweep_gbs": round(sw_bytes / sw_s / 1e9, 1)},
+        "roofline_prefill": {"bound": "mfma", "kernel": "k_gemm_q8 (prefill GEMM, 512 rows)",
+                             "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
+                             "frac": round(tops / INT8_PEAK_TOPS, 4), "launches": m_n,
+                             "avg_launch_us": round(1e6 * m_s / m_n, 3),
+                             "algorithmic_ops_per_launch": round(pre_ops / m_n),
+                             "fold_bound_tops": round(FOLD_BOUND_TOPS, 1),
+                             "frac_of_fold_bound": round(tops / FOLD_BOUND_TOPS, 4)},
+        "kernel_us_per_decode_token": {k: round(v[0] * 1e6 / a.gen, 2) for k, v in dec.items() if v[1]},
+        "kernel_ms_prefill": {k: round(v[0] * 1e3, 3) for k, v in pre.items() if v[1]},
         "tokens_head": toks[:8],
     }
     if not a.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(path, ids, a)
+        cb = cpu_baseline(path, ids, a)
+        ref_toks = cb.pop("tokens", None)
+        if ref_toks is not None:  # greedy identity on the metric's own workload: the tokens fed at each decode step
+            cb["greedy_tokens_identical"] = ref_toks == toks[:len(ref_toks)]
+        out["cpu_baseline"] = cb
     print(json.dumps(out), flush=True)
 
 
+def traffic_per_launch():
+    """HBM bytes per decode-GEMV launch from the committed counter summary (rocprofv3 FETCH_SIZE + WRITE_SIZE, each
+    scaled by what the counter reads for a copy of known size), or None where it is absent"""
+    f = os.path.join(ROOT, "profiles", "decode_gemv_traffic.json")
+    try:
+        with open(f) as fh:
+            return json.load(fh)["traffic_bytes_per_launch"]
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def probe(torch, gw, c, s, ids, a):
+    """the workload of the counter runs: one warm-up pass, then one prefill and a.gen decode steps as the timed step
+    runs them, then the calibration kernel (a 1 GiB float32 negation: read once, written once)"""
+    c.prefill(s, ids[:16], mode=gw.RQ_LOGITS_LAST)
+    s.reset()
+    c.prefill(s, ids, mode=gw.RQ_LOGITS_LAST)
+    tok = int(c.argmax(1)[0])
+    for _ in range(a.gen):
+        tok = c.decode_argmax(s, tok)
+    src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    torch.neg(src, out=dst)  # one elementwise kernel: 1 GiB read, 1 GiB written
+    torch.cuda.synchronize()
+    log(f"probe done: prefill {len(ids)} + {a.gen} decode steps, copy of {src.numel() * 4} bytes")
+
+
 def cpu_baseline(path, ids, a):
-    """The reference's CPU path on the same file and prompt (oracle/_ref/ref_driver): the prefill + cpu_decode steps,
-    all host cores; the step time is estimated as prefill + gen x the measured per-token decode time"""
+    """The reference's CPU path on the same file, prompt and step (oracle/_ref/ref_driver): the 512-token prefill and
+    the gen greedy decode steps, all host threads, best of cpu_reps runs (about 10 s of CPU work at 8B)"""
     from oracle import oracle as orc
     if not os.path.exists(orc.REF_DRIVER):
         return {"value": None, "unit": "tok/s", "cores": 0, "kind": "reference",
                 "sample": "oracle/_ref/ref_driver not built (needs the reference tree at build time)"}
     cores = len(os.sched_getaffinity(0))
     t0 = time.time()
-    info, _, _, _ = orc.run_ref_driver(path, ids, os.path.join(a.workdir, "cpu"), steps=a.cpu_decode, threads=cores,
-                                       cap=(a.prompt + a.cpu_decode + 255) // 256 * 256, timeout=900)
+    info, _, toks, _ = orc.run_ref_driver(path, ids, os.path.join(a.workdir, "cpu"), steps=a.gen, threads=cores,
+                                          cap=(a.prompt + a.gen + 255) // 256 * 256, reps=a.cpu_reps, timeout=900)
     wall = time.time() - t0
-    per_tok = info["decode_s"] / max(1, a.cpu_decode)
-    step_s = info["prefill_s"] + a.gen * per_tok
+    step_s = info["prefill_s"] + info["decode_s"]
     return {"value": round((a.prompt + a.gen) / step_s, 3), "unit": "tok/s", "cores": cores, "kind": "reference",
             "sample": f"the reference's CPU path (oracle/_ref/ref_driver, -Ofast AVX-512 VNNI, {cores} threads) on the same "
-                      f"GGUF: {a.prompt}-token prefill + {a.cpu_decode} greedy decode steps, step time = prefill + "
-                      f"{a.gen} x per-token decode ({wall:.0f} s wall incl. load)",
-            "prefill_tok_s": round(info["prefill_tok_s"], 2), "decode_tok_s": round(info["decode_tok_s"], 3)}
+                      f"GGUF and prompt: the whole step ({a.prompt}-token prefill + {a.gen} greedy decode steps), best of "
+                      f"{a.cpu_reps} runs ({wall:.0f} s wall incl. load)",
+            "prefill_tok_s": round(info["prefill_tok_s"], 2), "decode_tok_s": round(info["decode_tok_s"], 3),
+            "tokens": [int(t) for t in toks]}
 
 
 if __name__ == "__main__":

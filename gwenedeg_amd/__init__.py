@@ -41,6 +41,15 @@ class RqError(RuntimeError):
         self.code = code
 
 
+# One HIP runtime per process. torch ships its own libamdhip64 (same soname, loaded by path); when the library is
+# loaded first it binds the system runtime, torch then loads a second copy, and the second runtime to initialise finds
+# no device. Importing torch first (when it is installed) makes the library bind to torch's copy.
+try:
+    import torch  # noqa: F401
+except ImportError:
+    pass
+
+
 def _load(path: str) -> ctypes.CDLL:
     if not os.path.exists(path):
         raise ImportError(f"gwenedeg_amd: {path} is not built (run __graft_entry__.build())")
@@ -110,6 +119,9 @@ _sig = {
     "gw_ctx_profile_enable": (_I, [_P, _I]),
     "gw_ctx_gemv_sweep": (_I, [_P, _I, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),
     "gw_ctx_profile_launches": (ctypes.c_long, [_P, _I]),
+    "gw_ctx_kernel_timing": (_I, [_P, _I]),
+    "gw_ctx_kernel_times": (_I, [_P, _I, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_double),
+                                 ctypes.POINTER(ctypes.c_long), _I]),
     "rq_ctx_profile": (_I, [_P, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_double), _I]),
     "gw_q8_pack": (_I, [_P, _I, _I, _P, _P, _P]),
     "gw_quantize": (_I, [_P, _I, _I, _P, _P, _P]),
@@ -304,6 +316,21 @@ class Ctx:
         secs = (ctypes.c_double * 16)()
         n = lib.rq_ctx_profile(self._h, names, secs, 16)
         return {names[i].decode(): (secs[i], lib.gw_ctx_profile_launches(self._h, i)) for i in range(n)}
+
+    def kernel_timing(self, on: bool = True):
+        """gw_ctx_kernel_timing: every later kernel launch of the passes records its own start / stop"""
+        self._check(lib.gw_ctx_kernel_timing(self._h, 1 if on else 0), "gw_ctx_kernel_timing")
+
+    def kernel_times(self, multi: bool = False) -> dict:
+        """{class: (kernel seconds, launches)} of the one-row passes (multi False) or of the passes of several rows,
+        since kernel_timing(True) (gw_ctx_kernel_times)"""
+        names = (ctypes.c_char_p * 16)()
+        secs = (ctypes.c_double * 16)()
+        cnt = (ctypes.c_long * 16)()
+        n = lib.gw_ctx_kernel_times(self._h, 1 if multi else 0, names, secs, cnt, 16)
+        if n < 0:
+            self._check(n, "gw_ctx_kernel_times")
+        return {names[i].decode(): (secs[i], cnt[i]) for i in range(n)}
 
     def gemv_sweep(self, reps: int = 1):
         """gw_ctx_gemv_sweep: (seconds per sweep, weight bytes per sweep, launches per sweep)"""

@@ -4,8 +4,18 @@
 #define GW_DEVICE_H
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <hip/hip_fp16.h>
 #include <stdint.h>
+
+// a kernel launch that records the pending timing pair of gw_time_next_launch, if any (hipExtLaunchKernel's start /
+// stop events: the dispatch's own timestamps)
+#define GW_LAUNCH(K, G, B, LDS, S, ...)                                                                                 \
+    do {                                                                                                                \
+        hipEvent_t e0_, e1_;                                                                                            \
+        gw_take_launch_events(&e0_, &e1_);                                                                              \
+        hipExtLaunchKernelGGL(K, G, B, (uint32_t)(LDS), S, e0_, e1_, 0, __VA_ARGS__);                                   \
+    } while (0)
 
 #define ATT_T 16
 #define ATT_P 256

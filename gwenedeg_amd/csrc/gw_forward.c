@@ -9,7 +9,8 @@
  * A one-row pass of an all-Q8_0 model (decode) runs the fused sequence instead: per layer qkv matmul (rmsnorm +
  * quantize in its prologue) -> QK-norm + RoPE + K / V store -> attention partials -> wo matmul (combine + quantize in
  * its prologue, + residual) -> w1 / w3 matmul (rmsnorm + quantize in its prologue, SwiGLU in its epilogue) -> w2 matmul
- * (quantize in its prologue, + residual): the same arithmetic, four kernels fewer per layer.
+ * (quantize in its prologue, + residual), and the classifier's GEMV computes the final rmsnorm + quantize itself: the
+ * same arithmetic, four kernels fewer per layer.
  * The same kernels run every row whatever its batch-mates (decode is a one-row pass), and each output is computed
  * whole in a fixed order, so a sequence's results do not depend on what it is batched with (runq.h:22-24).
  * Errors: every argument is validated before any device work (forward.c:3775-3800), so a failed pass changes nothing;
@@ -23,6 +24,7 @@
 
 #include "gw_internal.h"
 
+#define GW_KT_MAX 32768 /* timed launches held before a collection (gw_ctx_kernel_timing) */
 #define HIPCHK(c, what, x) do { hipError_t e_ = (x); if (e_ != hipSuccess) return ctx_hip(c, what, e_); } while (0)
 
 static int ctx_fail(RqCtx *c, int code, const char *fmt, ...) {
@@ -163,7 +165,16 @@ void rq_ctx_free(RqCtx *c) {
         free(c->ev);
         free(c->ev_class);
     }
+    if (c->kt_ev) {
+        if (c->kt_n) hipStreamSynchronize(c->stream);
+        for (int i = 0; i < 2 * GW_KT_MAX; i++)
+            if (c->kt_ev[i]) hipEventDestroy(c->kt_ev[i]);
+        free(c->kt_ev);
+        free(c->kt_cls);
+    }
     if (c->stream) hipStreamDestroy(c->stream);
+    free(c->smp);
+    free(c->smp_t);
     free(c);
 }
 
@@ -253,6 +264,26 @@ fail:
     return NULL;
 }
 
+/* the accessors the reference's sampler.c links against (internal.h:326-328, forward.c:772-784): its host scratch
+ * (vocab x 8 bytes, and nt such rows for rq_sample_batch) and the vocabulary size */
+void *ctx_sampler_scratch(RqCtx *c) {
+    if (!c->smp) c->smp = malloc((size_t)c->m->vocab * 8);
+    return c->smp;
+}
+
+void *ctx_sampler_scratch_threads(RqCtx *c, int nt) {
+    if (nt > c->smp_nt) {
+        void *p = malloc((size_t)nt * c->m->vocab * 8);
+        if (!p) return NULL;
+        free(c->smp_t);
+        c->smp_t = p;
+        c->smp_nt = nt;
+    }
+    return c->smp_t;
+}
+
+int ctx_vocab(const RqCtx *c) { return c->m->vocab; }
+
 int rq_ctx_max_batch(const RqCtx *c) { return c->nb_max; }
 const char *rq_ctx_error(const RqCtx *c) { return c->err; }
 void *gw_ctx_stream(RqCtx *c) { return c->stream; }
@@ -290,8 +321,13 @@ int rq_ctx_profile(const RqCtx *c, const char **names, double *seconds, int max)
 
 long gw_ctx_profile_launches(const RqCtx *c, int cls) { return cls >= 0 && cls < GW_PF_N ? c->prof_n[cls] : 0; }
 
+static void kt_next(RqCtx *c, int cls);
+
 static void pf_mark(RqCtx *c, int cls) {
-    /* an event before a kernel of class cls (cls -1: the end mark) */
+    /* before the kernel(s) of class cls (cls -1: the end mark): a marker event (profiling), the timing pair of the next
+     * launch (kernel timing) */
+    c->kt_cur = cls;
+    if (cls >= 0) kt_next(c, cls);
     if (!c->prof_on || c->nev >= GW_EV_MAX) return;
     hipEventRecord(c->ev[c->nev], c->stream);
     c->ev_class[c->nev++] = cls;
@@ -309,7 +345,64 @@ static void pf_collect(RqCtx *c) {
     c->nev = 0;
 }
 
+/* kernel timing: the matmuls' own start / stop timestamps (hipExtLaunchKernel events), no markers between kernels */
+
+static int kt_collect(RqCtx *c) {
+    if (!c->kt_n) return RQ_OK;
+    HIPCHK(c, "hipStreamSynchronize (kernel timing)", hipStreamSynchronize(c->stream));
+    for (int i = 0; i < c->kt_n; i++) {
+        float ms = 0;
+        if (hipEventElapsedTime(&ms, c->kt_ev[2 * i], c->kt_ev[2 * i + 1]) == hipSuccess) {
+            c->kt_s[c->kt_cls[i]] += ms * 1e-3;
+            c->kt_cnt[c->kt_cls[i]]++;
+        }
+    }
+    c->kt_n = 0;
+    return RQ_OK;
+}
+
+static void kt_next(RqCtx *c, int cls) {
+    /* the next matmul launch (of class cls) is timed */
+    if (!c->kt_on) return;
+    if (c->kt_n == GW_KT_MAX && kt_collect(c) != RQ_OK) return;
+    gw_time_next_launch(c->kt_ev[2 * c->kt_n], c->kt_ev[2 * c->kt_n + 1]);
+    c->kt_cls[c->kt_n++] = (unsigned char)(cls + 16 * c->kt_multi);
+}
+
+int gw_ctx_kernel_timing(RqCtx *c, int on) {
+    if (on && !c->kt_ev) {
+        c->kt_ev = calloc(2 * GW_KT_MAX, sizeof(hipEvent_t));
+        c->kt_cls = calloc(GW_KT_MAX, 1);
+        if (!c->kt_ev || !c->kt_cls) return ctx_fail(c, RQ_ERR_NOMEM, "malloc failed");
+        for (int i = 0; i < 2 * GW_KT_MAX; i++)
+            HIPCHK(c, "hipEventCreate", hipEventCreate(&c->kt_ev[i]));
+    }
+    int rc = kt_collect(c);
+    c->kt_on = on;
+    memset(c->kt_s, 0, sizeof c->kt_s);
+    memset(c->kt_cnt, 0, sizeof c->kt_cnt);
+    return rc;
+}
+
+int gw_ctx_kernel_times(RqCtx *c, int multi, const char **names, double *seconds, long *launches, int max) {
+    if (multi < 0 || multi > 1) return ctx_fail(c, RQ_ERR_ARG, "multi %d", multi);
+    if (kt_collect(c) != RQ_OK) return RQ_ERR_STATE;
+    int n = max < GW_PF_N ? max : GW_PF_N;
+    for (int i = 0; i < n; i++) {
+        if (names) names[i] = pf_name[i];
+        if (seconds) seconds[i] = c->kt_s[16 * multi + i];
+        if (launches) launches[i] = c->kt_cnt[16 * multi + i];
+    }
+    return n;
+}
+
 /* ------------------------------------------------------------------------------------------- passes */
+
+static int fused_shape(const RqModel *m) {
+    /* an all-Q8_0 model whose matrices fit the fused single-row GEMVs of gw_gemv.hip */
+    int dim = m->dim, H = m->hidden, q = m->n_heads * m->head_dim;
+    return !m->kq && dim <= 4096 && H <= 12288 && q <= 4096 && dim % 64 == 0 && H % 64 == 0 && q % 64 == 0;
+}
 
 typedef struct { int x, y, z, w; } Item; /* attention work item: first row, rows, kv head, key block */
 
@@ -322,9 +415,11 @@ typedef struct {
 
 static int run_mm(RqCtx *c, const GwMat *w, int nmat, const int8_t *xq, const float *xs, int ldx, int M, float *out, int ldo,
                   int mode) {
-    for (int i = 0, col = 0; i < nmat; col += w[i].rows, i++)
+    for (int i = 0, col = 0; i < nmat; col += w[i].rows, i++) {
+        if (i) kt_next(c, c->kt_cur); /* (the first matrix's pair is set by the class mark) */
         if (gw_k_matmul(&w[i], xq, xs, ldx, M, out + col, ldo, mode, c->stream))
             return ctx_fail(c, RQ_ERR_STATE, "matmul launch failed (%d x %d, type %d)", w[i].rows, w[i].cols, w[i].type);
+    }
     return RQ_OK;
 }
 
@@ -385,13 +480,13 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
     int K = c->kmax;
 
     c->nev = 0;
+    c->kt_multi = n > 1;
     pf_mark(c, GW_PF_EMBED);
     if (m->embd.type == GW_Q8_0) KCHK(gw_k_embed_q8(c->x, dim, (const uint8_t *)m->embd.codes, m->embd.scales, tok_d, n, s));
     else KCHK(gw_k_embed_kq(c->x, dim, m->embd.type, m->embd.blocks, tok_d, n, s));
     /* one row of an all-Q8_0 model: the fused decode sequence (gw_gemv.hip: each matmul computes its activation from
      * the producer's fp32 output; the residual adds go straight into x) */
-    int fused = n == 1 && !m->kq && dim <= 4096 && H <= 12288 && nh * hd <= 4096 && dim % 64 == 0 && H % 64 == 0 &&
-                (nh * hd) % 64 == 0;
+    int fused = n == 1 && fused_shape(m);
     for (int l = 0; l < L; l++) {
         const GwLayer *y = &m->layer[l];
         if (fused) {
@@ -443,7 +538,10 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
         KCHK(gw_k_rmsnorm_quant(c->x, c->xb, dim, m->final_norm, NULL, n, c->xq, c->xs, K, c->hid_d, s));
         resid_done = 1;
     }
-    if (P->nsel > 0) {
+    if (fused && P->nsel == 1 && !P->want_hidden) { /* the final rmsnorm computed by the classifier's GEMV itself */
+        pf_mark(c, GW_PF_CLS);
+        KCHK(gw_k_gemv1_norm(&m->cls, GW_GV_R_CLS, c->x, m->final_norm, c->logits_d, 0, 0, s));
+    } else if (P->nsel > 0) {
         pf_mark(c, GW_PF_NORM);
         KCHK(gw_k_rmsnorm_quant(c->x, resid_done ? NULL : c->xb, dim, m->final_norm, sel_d, P->nsel, c->xq, c->xs, K, NULL, s));
         pf_mark(c, GW_PF_CLS);
@@ -636,29 +734,41 @@ int rq_prefill(RqCtx *c, RqSeq *s, const int *tokens, int n, int mode, float *ou
 }
 
 int gw_ctx_gemv_sweep(RqCtx *c, int reps, double *seconds, double *bytes, int *launches) {
-    /* the weight matmuls of one decode step (every layer's q / k / v, wo, w1 / w3, w2, then the classifier) on one
-     * activation row, back to back on the context's stream, reps times, between two HIP events: the device time of the
-     * decode path's weight streaming without the other kernels between them. *bytes: the file-format bytes of those
-     * weights per sweep (Q8_0 34 / 32, Q4_K 144 / 256, Q6_K 210 / 256 per weight); *launches: kernels per sweep */
+    /* the weight matmuls of one decode step (every layer's q / k / v, wo, w1 / w3, w2, then the classifier), launched
+     * as a one-row pass launches them (an all-Q8_0 model: the fused GEMVs with their prologues and epilogues, the
+     * attention combine over one key block), back to back on the context's stream, reps times, between two HIP
+     * events: the device time of the decode path's weight streaming without the other kernels between them. The
+     * inputs are whatever the context's buffers hold (the kernels' time does not depend on the values); the outputs go
+     * to the context's scratch rows. *bytes: the file-format bytes of those weights per sweep (Q8_0 34 / 32, Q4_K
+     * 144 / 256, Q6_K 210 / 256 per weight); *launches: kernels per sweep */
     const RqModel *m = c->m;
     if (reps < 1) return ctx_fail(c, RQ_ERR_ARG, "reps %d", reps);
     double b = 0;
-    int nl = 0, rc;
+    int nl = 0, rc, fused = fused_shape(m);
+    hipStream_t s = c->stream;
     hipEvent_t e0, e1;
     HIPCHK(c, "hipEventCreate", hipEventCreate(&e0));
     HIPCHK(c, "hipEventCreate", hipEventCreate(&e1));
-    HIPCHK(c, "hipEventRecord", hipEventRecord(e0, c->stream));
+    HIPCHK(c, "hipEventRecord", hipEventRecord(e0, s));
     for (int r = 0; r < reps; r++) {
         for (int l = 0; l < m->n_layers; l++) {
             const GwLayer *y = &m->layer[l];
+            if (fused) {
+                KCHK(gw_k_gemv1_norm(&y->qkv[0], GW_GV_R_QKV, c->x, y->att_norm, c->qkv, 0, 0, s));
+                KCHK(gw_k_gemv1_combine(&y->wo, GW_GV_R_WO, c->part, c->pstride, m->head_dim, 1, c->xb, 0, s));
+                KCHK(gw_k_gemv1_norm(&y->w13[0], GW_GV_R_W13, c->x, y->ffn_norm, c->hb, 0, y->w13_il, s));
+                KCHK(gw_k_gemv1_qf(&y->w2, GW_GV_R_W2, c->hb, c->xb, 0, s));
+                continue;
+            }
             if ((rc = run_mm(c, y->qkv, y->nqkv, c->xq, c->xs, c->kmax, 1, c->qkv, c->ldqkv, 0)) != RQ_OK) return rc;
             if ((rc = run_mm(c, &y->wo, 1, c->xq, c->xs, c->kmax, 1, c->xb, m->dim, 0)) != RQ_OK) return rc;
             if ((rc = run_mm(c, y->w13, y->nw13, c->xq, c->xs, c->kmax, 1, c->hb, 2 * m->hidden, 0)) != RQ_OK) return rc;
             if ((rc = run_mm(c, &y->w2, 1, c->hq, c->hs, m->hidden, 1, c->xb, m->dim, 0)) != RQ_OK) return rc;
         }
-        if ((rc = run_mm(c, &m->cls, 1, c->xq, c->xs, c->kmax, 1, c->logits_d, m->vocab, 0)) != RQ_OK) return rc;
+        if (fused) KCHK(gw_k_gemv1_norm(&m->cls, GW_GV_R_CLS, c->x, m->final_norm, c->logits_d, 0, 0, s));
+        else if ((rc = run_mm(c, &m->cls, 1, c->xq, c->xs, c->kmax, 1, c->logits_d, m->vocab, 0)) != RQ_OK) return rc;
     }
-    HIPCHK(c, "hipEventRecord", hipEventRecord(e1, c->stream));
+    HIPCHK(c, "hipEventRecord", hipEventRecord(e1, s));
     HIPCHK(c, "hipEventSynchronize", hipEventSynchronize(e1));
     float ms = 0;
     hipEventElapsedTime(&ms, e0, e1);
@@ -666,8 +776,8 @@ int gw_ctx_gemv_sweep(RqCtx *c, int reps, double *seconds, double *bytes, int *l
     hipEventDestroy(e1);
     for (int l = 0; l < m->n_layers; l++) {
         const GwLayer *y = &m->layer[l];
-        const GwMat *ws[8] = { &y->qkv[0], y->nqkv > 1 ? &y->qkv[1] : NULL, y->nqkv > 2 ? &y->qkv[2] : NULL, &y->wo, &y->w13[0],
-                               y->nw13 > 1 ? &y->w13[1] : NULL, &y->w2, NULL };
+        const GwMat *ws[7] = { &y->qkv[0], y->nqkv > 1 ? &y->qkv[1] : NULL, y->nqkv > 2 ? &y->qkv[2] : NULL, &y->wo, &y->w13[0],
+                               y->nw13 > 1 ? &y->w13[1] : NULL, &y->w2 };
         for (int i = 0; i < 7; i++)
             if (ws[i]) {
                 b += gw_mat_file_bytes(ws[i]);

@@ -1,6 +1,7 @@
 // The matmul dispatch of the forward passes (gw_k_matmul), the load-time repack, and the isolated Q8_0 / K-quant
 // operator of the public ABI (gw_q8_*, gw_kq_matmul, gw_quantize).
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
@@ -286,17 +287,20 @@ static int launch_gemv_kq(const uint8_t *W, int nrows, int K, const int8_t *xq, 
                           int ldo, int mode, hipStream_t s) {
     const int R = 4;
     size_t lds = (size_t)4 * R * (K / 32 + 1) * sizeof(float);
+    hipEvent_t t0, t1; // (timing: the first launch's start, the last one's stop)
+    gw_take_launch_events(&t0, &t1);
     for (int m0 = 0; m0 < M; m0 += 4) {
         int mm = M - m0 < 4 ? M - m0 : 4;
+        hipEvent_t e0 = m0 == 0 ? t0 : NULL, e1 = m0 + 4 >= M ? t1 : NULL;
         dim3 grid((nrows + R - 1) / R);
         const int8_t *x = xq + (size_t)m0 * ldx;
         const float *xsc = xs + (size_t)m0 * (ldx / 32);
         float *o = out + (size_t)m0 * ldo;
         switch (mm) {
-        case 1: hipLaunchKernelGGL((k_gemv_kq<TYPE, 1, R>), grid, dim3(256), lds, s, W, nrows, K, x, xsc, ldx, o, ldo, mode); break;
-        case 2: hipLaunchKernelGGL((k_gemv_kq<TYPE, 2, R>), grid, dim3(256), lds, s, W, nrows, K, x, xsc, ldx, o, ldo, mode); break;
-        case 3: hipLaunchKernelGGL((k_gemv_kq<TYPE, 3, R>), grid, dim3(256), lds, s, W, nrows, K, x, xsc, ldx, o, ldo, mode); break;
-        default: hipLaunchKernelGGL((k_gemv_kq<TYPE, 4, R>), grid, dim3(256), lds, s, W, nrows, K, x, xsc, ldx, o, ldo, mode); break;
+        case 1: hipExtLaunchKernelGGL((k_gemv_kq<TYPE, 1, R>), grid, dim3(256), lds, s, e0, e1, 0, W, nrows, K, x, xsc, ldx, o, ldo, mode); break;
+        case 2: hipExtLaunchKernelGGL((k_gemv_kq<TYPE, 2, R>), grid, dim3(256), lds, s, e0, e1, 0, W, nrows, K, x, xsc, ldx, o, ldo, mode); break;
+        case 3: hipExtLaunchKernelGGL((k_gemv_kq<TYPE, 3, R>), grid, dim3(256), lds, s, e0, e1, 0, W, nrows, K, x, xsc, ldx, o, ldo, mode); break;
+        default: hipExtLaunchKernelGGL((k_gemv_kq<TYPE, 4, R>), grid, dim3(256), lds, s, e0, e1, 0, W, nrows, K, x, xsc, ldx, o, ldo, mode); break;
         }
     }
     return (int)hipGetLastError();
@@ -305,7 +309,9 @@ static int launch_gemv_kq(const uint8_t *W, int nrows, int K, const int8_t *xq, 
 extern "C" {
 
 int gw_k_embed_kq(float *x, int dim, int type, const uint8_t *blocks, const int *tok, int n, hipStream_t s) {
-    hipLaunchKernelGGL(k_embed_kq, dim3(n), dim3(256), 0, s, x, dim, type, blocks, tok);
+    hipEvent_t e0, e1;
+    gw_take_launch_events(&e0, &e1);
+    hipExtLaunchKernelGGL(k_embed_kq, dim3(n), dim3(256), 0, s, e0, e1, 0, x, dim, type, blocks, tok);
     return (int)hipGetLastError();
 }
 
@@ -321,10 +327,26 @@ int gw_k_fill_synthetic(uint16_t *kc, uint16_t *vc, size_t n, unsigned long long
     return (int)hipGetLastError();
 }
 
+static hipEvent_t tev0, tev1; // the pending timing pair of the next matmul launch (calls are single-threaded)
+
+void gw_time_next_launch(hipEvent_t a, hipEvent_t b) {
+    tev0 = a;
+    tev1 = b;
+}
+
+void gw_take_launch_events(hipEvent_t *a, hipEvent_t *b) {
+    *a = tev0;
+    *b = tev1;
+    tev0 = tev1 = NULL;
+}
+
 int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int M, float *out, int ldo, int mode, hipStream_t s) {
     if (w->type == GW_Q8_0 && M > GW_GEMV_MAX_ROWS && mode == 0) {
         dim3 grid((w->rows + GN - 1) / GN, (M + GM - 1) / GM);
-        hipLaunchKernelGGL(k_gemm_q8, grid, dim3(256), 0, s, w->codes, w->scales, w->rows, w->cols, xq, xs, ldx, M, out, ldo);
+        hipEvent_t e0, e1;
+        gw_take_launch_events(&e0, &e1);
+        hipExtLaunchKernelGGL(k_gemm_q8, grid, dim3(256), 0, s, e0, e1, 0, (const int8_t *)w->codes, (const uint16_t *)w->scales,
+                              w->rows, w->cols, xq, xs, ldx, M, out, ldo);
         return (int)hipGetLastError();
     }
     if (w->type == GW_Q8_0)

@@ -16,6 +16,8 @@
 // waits leave the weight loads in flight), the weight loads before any prologue arithmetic.
 // Then as k_gemv_q8: the exact int32 sum of a half-group by 4 v_dot4, the lane pair's sums added, the even lane's
 // (ws * xs) * (float) isum into LDS, one lane per row folding the groups in order (forward.c:906-916).
+#include <hip/hip_ext.h>
+
 #include "gw_internal.h"
 #include "gw_device.h"
 
@@ -349,7 +351,9 @@ static int gv_launch(int pro, int R, const GvArgs &a, hipStream_t s) {
     b.cmax = tpw < cmax ? tpw : cmax;
     size_t lds = (size_t)b.cmax * slot_bytes + (pro == GV_NORM ? (size_t)(16 * (a.K / 16 + 4) + 4) * sizeof(float) : 0);
     dim3 grid(nwg);
-#define GV_L(RR, PP, NN) hipLaunchKernelGGL((k_gemv1<RR, PP, NN>), grid, dim3(nt), lds, s, b)
+    hipEvent_t e0, e1;
+    gw_take_launch_events(&e0, &e1);
+#define GV_L(RR, PP, NN) hipExtLaunchKernelGGL((k_gemv1<RR, PP, NN>), grid, dim3(nt), (uint32_t)lds, s, e0, e1, 0, b)
 #define GV_R(PP)                                                                                                        \
     if (nt <= 256) {                                                                                                    \
         if (R == 4) GV_L(4, PP, 256);                                                                                   \

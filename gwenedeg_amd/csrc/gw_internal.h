@@ -86,12 +86,22 @@ struct RqCtx {
     size_t lg_h_rows;
     char err[256];
     int last_nsel;     /* logits rows the last pass left on the device (gw_ctx_argmax) */
+    void *smp, *smp_t; /* host scratch of the reference's sampler (ctx_sampler_scratch[_threads]): vocab x 8 bytes */
+    int smp_nt;
     /* profiling (gw_ctx_profile_enable): HIP events around each kernel class of a pass, summed per class */
     int prof_on, nev;
     hipEvent_t *ev;
     int *ev_class;
     double prof_s[16];
     long prof_n[16];
+    /* kernel timing (gw_ctx_kernel_timing): each matmul launch records its own start / stop (a pair of the pool),
+     * collected when the pool is full or read; per class: summed seconds and launches */
+    int kt_on, kt_n, kt_cur, kt_multi; /* kt_cur: the class of the kernels being launched (set with the profiling
+                                        * marks); kt_multi: the pass has several rows */
+    hipEvent_t *kt_ev;
+    unsigned char *kt_cls;
+    double kt_s[32];                   /* [multi][class] */
+    long kt_cnt[32];
 };
 
 enum { GW_PF_EMBED, GW_PF_NORM, GW_PF_QKV, GW_PF_ROPE, GW_PF_ATT, GW_PF_COMBINE, GW_PF_WO, GW_PF_W13, GW_PF_SWIGLU, GW_PF_W2,
@@ -146,11 +156,18 @@ int gw_k_fill_synthetic(uint16_t *kc, uint16_t *vc, size_t n, unsigned long long
 #define GW_GV_R_WO 8
 #define GW_GV_R_W13 8
 #define GW_GV_R_W2 4
+#define GW_GV_R_CLS 4
 int gw_k_gemv1_q(const GwMat *w, int R, const int8_t *xq, const float *xs, float *out, int mode, hipStream_t s);
 int gw_k_gemv1_norm(const GwMat *w, int R, const float *x, const float *nw, float *out, int mode, int swiglu_il, hipStream_t s);
 int gw_k_gemv1_qf(const GwMat *w, int R, const float *x, float *out, int mode, hipStream_t s);
 int gw_k_gemv1_combine(const GwMat *w, int R, const float *part, int pstride, int hd, int nb, float *out, int mode,
                        hipStream_t s);
+
+/* per-launch kernel timing (gw_ctx_kernel_timing): gw_time_next_launch(a, b) makes the next matmul launch (k_gemv1,
+ * k_gemm_q8, k_gemv_q8, k_gemv_kq) record its own start and stop in events a and b (hipExtLaunchKernel's events: the
+ * dispatch's timestamps, no extra packets on the stream); each launcher takes the pair once (gw_take_launch_events) */
+void gw_time_next_launch(hipEvent_t a, hipEvent_t b);
+void gw_take_launch_events(hipEvent_t *a, hipEvent_t *b);
 
 /* the matmul dispatch (gw_gemm.hip): out[m * ldo + row] (+)= W row . X row m for M rows, any supported type */
 int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int M, float *out, int ldo, int mode,

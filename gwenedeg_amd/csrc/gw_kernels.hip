@@ -17,6 +17,7 @@
 //                :1894-1951
 //   SwiGLU       forward.c:1953-1958     swiglu_ref: the reference's vector expf and rcp14 + Newton (host tables)
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
@@ -602,13 +603,13 @@ __global__ __launch_bounds__(64) void k_argmax_final(const float2 *__restrict__ 
 extern "C" {
 
 int gw_k_embed_q8(float *x, int dim, const uint8_t *codes, const uint16_t *scales, const int *tok, int n, hipStream_t s) {
-    hipLaunchKernelGGL(k_embed_q8, dim3(n, (dim + 255) / 256), dim3(256), 0, s, x, dim, codes, scales, tok);
+    GW_LAUNCH(k_embed_q8, dim3(n, (dim + 255) / 256), dim3(256), 0, s, x, dim, codes, scales, tok);
     return (int)hipGetLastError();
 }
 
 int gw_k_rmsnorm_quant(float *x, const float *d, int dim, const float *w, const int *sel, int n, int8_t *xq, float *xs, int ldq,
                        float *hid, hipStream_t s) {
-    hipLaunchKernelGGL(k_rmsnorm_quant, dim3(n), dim3(NORM_T), (size_t)dim * sizeof(float), s, x, d, dim, w, sel, xq, xs, ldq, hid);
+    GW_LAUNCH(k_rmsnorm_quant, dim3(n), dim3(NORM_T), (size_t)dim * sizeof(float), s, x, d, dim, w, sel, xq, xs, ldq, hid);
     return (int)hipGetLastError();
 }
 
@@ -628,14 +629,17 @@ int gw_k_gemv_q8(const int8_t *W, const uint16_t *WS, int nrows, int K, const in
     const int R = 4;
     int H = K / 16, U = (H + 255) / 256;
     U = U < 1 ? 1 : U > 4 ? 4 : U;
+    hipEvent_t t0, t1; // (timing: the first launch's start, the last one's stop)
+    gw_take_launch_events(&t0, &t1);
     for (int m0 = 0; m0 < M; m0 += 4) {
         int mm = M - m0 < 4 ? M - m0 : 4;
+        hipEvent_t e0 = m0 == 0 ? t0 : NULL, e1 = m0 + 4 >= M ? t1 : NULL;
         size_t lds = (size_t)mm * R * ((K / 32 + 7) & ~3) * sizeof(float);
         dim3 grid((nrows + R - 1) / R);
         const int8_t *x = xq + (size_t)m0 * ldx;
         const float *xsc = xs + (size_t)m0 * (ldx / 32);
         float *o = out + (size_t)m0 * ldo;
-#define GEMV_L(MM, UU) hipLaunchKernelGGL((k_gemv_q8<MM, R, UU>), grid, dim3(256), lds, s, W, WS, nrows, K, x, xsc, ldx, o, ldo, mode)
+#define GEMV_L(MM, UU) hipExtLaunchKernelGGL((k_gemv_q8<MM, R, UU>), grid, dim3(256), (uint32_t)lds, s, e0, e1, 0, W, WS, nrows, K, x, xsc, ldx, o, ldo, mode)
 #define GEMV_U(MM)                                                                                                      \
     switch (U) {                                                                                                        \
     case 1: GEMV_L(MM, 1); break;                                                                                       \
@@ -657,7 +661,7 @@ int gw_k_gemv_q8(const int8_t *W, const uint16_t *WS, int nrows, int K, const in
 
 int gw_k_qknorm_rope_store(float *qkv, int ldqkv, int n, int nh, int nkv, int hd, const float *qn, const float *kn,
                            const float *rope, const int *pos, uint16_t *const *kc, uint16_t *const *vc, hipStream_t s) {
-    hipLaunchKernelGGL(k_qknorm_rope_store, dim3(n, nh + 2 * nkv), dim3(64), 0, s, qkv, ldqkv, nh, nkv, hd, qn, kn, rope, pos, kc, vc);
+    GW_LAUNCH(k_qknorm_rope_store, dim3(n, nh + 2 * nkv), dim3(64), 0, s, qkv, ldqkv, nh, nkv, hd, qn, kn, rope, pos, kc, vc);
     return (int)hipGetLastError();
 }
 
@@ -665,7 +669,7 @@ int gw_k_attn_part(const void *items, int nitems, int nq_max, const float *qkv, 
                    const int *pos, uint16_t *const *kc, uint16_t *const *vc, float *part, int pstride, hipStream_t s) {
     int nq = nq_max;
     const int4 *it = (const int4 *)items;
-#define ATT_LAUNCH(Q) hipLaunchKernelGGL(k_attn_part<Q>, dim3(nitems), dim3(ATT_TH), 0, s, it, qkv, ldqkv, nh, nkv, hd, scale, pos, kc, vc, part, pstride)
+#define ATT_LAUNCH(Q) GW_LAUNCH(k_attn_part<Q>, dim3(nitems), dim3(ATT_TH), 0, s, it, qkv, ldqkv, nh, nkv, hd, scale, pos, kc, vc, part, pstride)
     if (nq <= 1) ATT_LAUNCH(1);
     else if (nq <= 2) ATT_LAUNCH(2);
     else if (nq <= 4) ATT_LAUNCH(4);
@@ -678,24 +682,26 @@ int gw_k_attn_part(const void *items, int nitems, int nq_max, const float *qkv, 
 int gw_k_attn_combine_quant(const float *part, int pstride, int nh, int hd, const int *pos, int n, int8_t *aq, float *as,
                             int ldq, float *att_out, hipStream_t s) {
     (void)hd;
-    hipLaunchKernelGGL(k_attn_combine_quant, dim3(n), dim3(COMB_T), (size_t)nh * (2 * (pstride / (hd + 2)) + 1) * sizeof(float), s, part,
-                       pstride, nh, hd, pos, aq, as, ldq, att_out);
+    GW_LAUNCH(k_attn_combine_quant, dim3(n), dim3(COMB_T), (size_t)nh * (2 * (pstride / (hd + 2)) + 1) * sizeof(float), s, part,
+              pstride, nh, hd, pos, aq, as, ldq, att_out);
     return (int)hipGetLastError();
 }
 
 int gw_k_swiglu_quant(const float *hb, int H, int il, int n, int8_t *hq, float *hs, hipStream_t s) {
-    hipLaunchKernelGGL(k_swiglu_quant, dim3(n, H / 256), dim3(256), 0, s, hb, H, il, hq, hs);
+    GW_LAUNCH(k_swiglu_quant, dim3(n, H / 256), dim3(256), 0, s, hb, H, il, hq, hs);
     return (int)hipGetLastError();
 }
 
 int gw_k_quant_rows(const float *x, int n, int ldxf, int rows, int8_t *q, float *sc, int ldq, hipStream_t s) {
-    hipLaunchKernelGGL(k_quant_rows, dim3(rows, (n + 255) / 256), dim3(256), 0, s, x, n, ldxf, q, sc, ldq);
+    GW_LAUNCH(k_quant_rows, dim3(rows, (n + 255) / 256), dim3(256), 0, s, x, n, ldxf, q, sc, ldq);
     return (int)hipGetLastError();
 }
 
 int gw_k_argmax(const float *lg, int n, int ld, int rows, int *out, void *scratch, hipStream_t s) {
-    hipLaunchKernelGGL(k_argmax_part, dim3(rows, ARGMAX_CH), dim3(256), 0, s, lg, n, ld, (float2 *)scratch);
-    hipLaunchKernelGGL(k_argmax_final, dim3(rows), dim3(64), 0, s, (const float2 *)scratch, out);
+    hipEvent_t e0, e1; // (timing: the first kernel's start, the second one's stop)
+    gw_take_launch_events(&e0, &e1);
+    hipExtLaunchKernelGGL(k_argmax_part, dim3(rows, ARGMAX_CH), dim3(256), 0, s, e0, (hipEvent_t)NULL, 0, lg, n, ld, (float2 *)scratch);
+    hipExtLaunchKernelGGL(k_argmax_final, dim3(rows), dim3(64), 0, s, (hipEvent_t)NULL, e1, 0, (const float2 *)scratch, out);
     return (int)hipGetLastError();
 }
 

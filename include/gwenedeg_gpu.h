@@ -134,6 +134,13 @@ int rq_forward_batch(RqCtx *c, const RqSegment *seg, int nseg, float *out, float
 /* runq.h:561 */
 unsigned long long rq_logits_hash(const float *logits, int n);
 
+/* The reference's internal accessors that its sampler.c links against (internal.h:326-328, defined in forward.c:772-784):
+ * the context's host scratch of vocab x 8 bytes (and of nt such rows for rq_sample_batch; NULL: no memory) and the
+ * vocabulary size. They let sampler.c (rq_sample, rq_sample_batch) run unchanged on this library's contexts */
+void *ctx_sampler_scratch(RqCtx *c);
+void *ctx_sampler_scratch_threads(RqCtx *c, int nt);
+int ctx_vocab(const RqCtx *c);
+
 /* ------------------------------------------------------------------------------------- extensions (gw_) */
 
 /* Device-side greedy sampling of a pass's logits rows: the first maximum of each row (the reference's
@@ -153,12 +160,23 @@ int gw_decode_argmax(RqCtx *c, RqSeq *s, int token, int *next);
  * gw_ctx_profile_launches the number of intervals of class i (its launches). 0 turns it off */
 int gw_ctx_profile_enable(RqCtx *c, int on);
 
-/* The weight matmuls of one decode step (per layer q / k / v, wo, w1 / w3, w2; then the classifier) on one activation
- * row, back to back, reps times, timed with HIP events on the context's stream: *seconds per sweep, *bytes = their
- * file-format weight bytes (the algorithmic bytes of a decode step's weight streaming), *launches per sweep. The
- * counterpart of the reference's pass timing (rq_pass_times, runq.h:196-199) for the GEMV alone */
+/* The weight matmuls of one decode step (per layer q / k / v, wo, w1 / w3, w2; then the classifier), launched as a
+ * one-row pass launches them (all-Q8_0 models: the fused GEMVs), back to back, reps times, timed with HIP events on
+ * the context's stream: *seconds per sweep, *bytes = their file-format weight bytes (the algorithmic bytes of a decode
+ * step's weight streaming), *launches per sweep. Inputs are the context's buffers as they are (call it after a pass);
+ * outputs go to its scratch rows. The counterpart of the reference's pass timing (rq_pass_times, runq.h:196-199) for
+ * the GEMV alone */
 int gw_ctx_gemv_sweep(RqCtx *c, int reps, double *seconds, double *bytes, int *launches);
 long gw_ctx_profile_launches(const RqCtx *c, int cls);
+
+/* Kernel timing, for roofline figures: gw_ctx_kernel_timing(c, 1) resets the counters and makes every later kernel of
+ * c's passes record its own start and stop (hipExtLaunchKernel's events: the dispatch's timestamps, no packets between
+ * kernels, so the passes run as they do untimed); 0 turns it off. gw_ctx_kernel_times synchronizes c's stream and
+ * returns, per kernel class of rq_ctx_profile's names (embed, matmul qkv, attention, ..., classifier), the summed
+ * kernel seconds and launches of the one-row passes (multi 0: decode) or of the passes of several rows (multi 1:
+ * prefill, batches); the return value is the class count */
+int gw_ctx_kernel_timing(RqCtx *c, int on);
+int gw_ctx_kernel_times(RqCtx *c, int multi, const char **names, double *seconds, long *launches, int max);
 
 /* The isolated Q8_0 operator (the reference's kernels_avx512.h q8p_pack_blocks :113, q8p_gemv_rows :286 and
  * q8p_gemm_item :235, and forward.c's quantize :803), on device pointers, on the given HIP stream (NULL: the null

@@ -7,16 +7,26 @@
  * operation rounded to nearest, in the order written; fmaf() is written where the reference's definition has a
  * fused multiply-add (the attention's chains: forward.c:1295-1299 with FP_FAST_FMAF on the AVX-512 builds).
  *
- * How each part is pinned (tests/test_oracle.py):
- *   fp16 / f32_f16 / quantize / Q8_0 fold: against the reference's own compiled kernels (oracle/_ref/ref_q8op:
- *     q8p_gemv_rows / q8p_gemm_item, bit-exact), brute-force integer sums, closed forms and edge cases;
- *   K-quant fold: against the reference's kq_dot (oracle/_ref/ref_q8op kq, bit-exact) and a float64 dequantized
- *     product; the dequantization against an independent numpy decode of the block formats;
- *   attention: one block against a float64 softmax; several blocks against the single-block result (combine);
- *   the whole forward: against the compiled reference (oracle/_ref/ref_driver) on synthetic models, logits within
- *     tolerance and identical greedy tokens. rmsnorm / RoPE / SwiGLU are pinned only through that comparison: the
- *     reference's bits there come from -Ofast (rsqrt estimate + Newton for 1 / sqrtf, reassociated sums) and from
- *     glibc's vector expf / sincosf, so they are reproduced to tolerance, not to the bit (parity unpinned at bit level).
+ * How each part is pinned (tests/test_oracle.py; every check chosen so that a dropped term, a wrong sign or index or a
+ * transposed operand fails it):
+ *   fp16 widening: all 65536 halves against numpy; f32_f16: numpy's round-to-nearest-even below 65520, the
+ *     reference's saturation above, subnormals, NaN;
+ *   quantize: the closed form on random rows, hand-computed half-way cases (round half away from zero), all-zero groups;
+ *   Q8_0 fold: per-block int32 sums by integer brute force; the group-order fold rebuilt in numpy float32; the whole
+ *     matmul bit for bit against the reference's own compiled kernels (oracle/_ref/ref_q8op: q8p_gemv_rows,
+ *     q8p_gemm_item) at M = 1, 3, 8, 13, and against the golden vectors of tests/golden/ref_kernels.npz;
+ *   K-quant fold: bit for bit against the reference's kq_dot (ref_q8op kq); the dequantization against an
+ *     independent numpy decoder of the Q4_K / Q6_K block formats;
+ *   exp_att: within 2 ulp of expf, the -86 clamp; attention: one block against a float64 softmax, several blocks
+ *     against the one-block result (the combine's invariant);
+ *   rsqrt (or_rsqrt_ref: the reference's -Ofast 1.0f / sqrtf = rsqrtss + one Newton step): within 3 ulp of IEEE and,
+ *     through the whole forward, bit for bit; RoPE: against float64 cos / sin; SwiGLU on AVX-512 hosts (libmvec's
+ *     vector expf + vrcp14ps + Newton, the -Ofast lowering of forward.c:1953-1958): against the product's
+ *     host-measured tables and, through the whole forward, bit for bit;
+ *   the whole forward (or_forward_token): logits bit for bit against the compiled reference (oracle/_ref/ref_driver)
+ *     on synthetic Q8_0 and Q4_K_M models, including a Qwen3-0.6B-shaped model with 3 layers.
+ * On a host without AVX-512 the oracle's SwiGLU falls back to the portable form (1 / (1 + expf)); the reference built
+ * for such a host lowers the loop to other instructions, so there the SwiGLU is pinned only to tolerance.
  */
 #define _GNU_SOURCE
 #include <immintrin.h>

@@ -12,7 +12,7 @@ def declared_functions():
         if fn.endswith(".h"):
             src = open(os.path.join(ROOT, "include", fn)).read()
             src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-            for m in re.finditer(r"^[A-Za-z_][\w \*]*?\b((?:rq|gw)_\w+)\s*\(", src, flags=re.M):
+            for m in re.finditer(r"^[A-Za-z_][\w \*]*?\b((?:rq|gw|ctx)_\w+)\s*\(", src, flags=re.M):
                 names.add(m.group(1))
     return names
 
@@ -89,3 +89,19 @@ def test_cpu_only_paths_fail_cleanly():
         assert e.code == gw.RQ_ERR_LOAD
     else:
         raise AssertionError("expected an error")
+
+
+def test_one_hip_runtime_per_process():
+    """importing the package before torch still leaves one HIP runtime in the process (two copies of libamdhip64, the
+    system's and torch's, cannot both see the device)"""
+    import subprocess
+    import sys
+    code = ("import sys; sys.path.insert(0, %r)\n"
+            "import gwenedeg_amd\n"
+            "import torch\n"
+            "libs = {l.split()[-1] for l in open('/proc/self/maps') if 'libamdhip64' in l}\n"
+            "print(len(libs), sorted(libs))\n") % ROOT
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr[-2000:]
+    n = int(out.stdout.split()[0])
+    assert n == 1, out.stdout
