@@ -486,7 +486,7 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
     else KCHK(gw_k_embed_kq(c->x, dim, m->embd.type, m->embd.blocks, tok_d, n, s));
     /* one row of an all-Q8_0 model: the fused decode sequence (gw_gemv.hip: each matmul computes its activation from
      * the producer's fp32 output; the residual adds go straight into x) */
-    int fused = n == 1 && fused_shape(m);
+    int fused = n == 1 && fused_shape(m), fused_att = fused && (hd == 128 || hd == 64 || hd == 32);
     for (int l = 0; l < L; l++) {
         const GwLayer *y = &m->layer[l];
         if (fused) {
@@ -498,12 +498,20 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
             pf_mark(c, GW_PF_QKV);
             if ((rc = run_mm(c, y->qkv, y->nqkv, c->xq, c->xs, K, n, c->qkv, c->ldqkv, 0)) != RQ_OK) return rc;
         }
-        pf_mark(c, GW_PF_ROPE);
-        KCHK(gw_k_qknorm_rope_store(c->qkv, c->ldqkv, n, nh, nkv, hd, y->q_norm, y->k_norm, m->rope, pos_d,
-                                    kc_d + (size_t)l * n, vc_d + (size_t)l * n, s));
-        pf_mark(c, GW_PF_ATT);
-        KCHK(gw_k_attn_part(items_d, nitems, nq_max, c->qkv, c->ldqkv, nh, nkv, hd, m->att_scale, pos_d, kc_d + (size_t)l * n,
-                            vc_d + (size_t)l * n, c->part, c->pstride, s));
+        if (fused_att) { /* QK-norm + RoPE + K / V store inside the decode attention */
+            pf_mark(c, GW_PF_ATT);
+            RqSeq *sq = P->seq[0];
+            KCHK(gw_k_attn_decode(c->qkv, nh, nkv, hd, m->att_scale, y->q_norm, y->k_norm, m->rope, P->pos[0],
+                                  sq->kc + (size_t)l * seq_layer_elems(sq), sq->vc + (size_t)l * seq_layer_elems(sq),
+                                  c->part, c->pstride, s));
+        } else {
+            pf_mark(c, GW_PF_ROPE);
+            KCHK(gw_k_qknorm_rope_store(c->qkv, c->ldqkv, n, nh, nkv, hd, y->q_norm, y->k_norm, m->rope, pos_d,
+                                        kc_d + (size_t)l * n, vc_d + (size_t)l * n, s));
+            pf_mark(c, GW_PF_ATT);
+            KCHK(gw_k_attn_part(items_d, nitems, nq_max, c->qkv, c->ldqkv, nh, nkv, hd, m->att_scale, pos_d,
+                                kc_d + (size_t)l * n, vc_d + (size_t)l * n, c->part, c->pstride, s));
+        }
         if (fused) {
             if (nbmax <= GW_GV_NBMAX) {
                 pf_mark(c, GW_PF_WO);

@@ -136,6 +136,10 @@ int gw_k_qknorm_rope_store(float *qkv, int ldqkv, int n, int nh, int nkv, int hd
                            const float *rope, const int *pos, uint16_t *const *kc, uint16_t *const *vc, hipStream_t s);
 int gw_k_attn_part(const void *items, int nitems, int nq_max, const float *qkv, int ldqkv, int nh, int nkv, int hd, float scale,
                    const int *pos, uint16_t *const *kc, uint16_t *const *vc, float *part, int pstride, hipStream_t s);
+/* the one-row pass's attention with its QK-norm, RoPE and K / V store (hd 32, 64 or 128; pos: the row's position;
+ * kl / vl: its sequence's K / V cache of the layer) */
+int gw_k_attn_decode(const float *qkv, int nh, int nkv, int hd, float scale, const float *qn, const float *kn, const float *rope,
+                     int pos, uint16_t *kl, uint16_t *vl, float *part, int pstride, hipStream_t s);
 int gw_k_attn_combine_quant(const float *part, int pstride, int nh, int hd, const int *pos, int n, int8_t *aq, float *as,
                             int ldq, float *att_out, hipStream_t s);
 /* hb row: [h (H) | h2 (H)] (il = 0) or blocks of il h then il h2 (w1 / w3 rows interleaved by il) */

@@ -443,6 +443,204 @@ __global__ __launch_bounds__(ATT_TH) void k_attn_part(const int4 *__restrict__ i
     }
 }
 
+// The attention of the one-row (decode) pass, one block of 1024 threads per (query vector v, kv head g, key block kb),
+// with the row's QK-norm, RoPE and K / V store fused in (forward.c:1266-1284, :1901-1951). The row's position and its
+// sequence's cache bases of the layer (kl, vl) are arguments (no memory round trip before the loads). The block normalizes and
+// rotates its query head h = g kv_mul + v; the blocks of the last key block (the one holding the row's position pos)
+// also compute the row's key and value of head g, write them into their own LDS copy of the block (so no block waits
+// for another's store) and, for v = 0, into the cache. Then the partial result of block kb for vector v exactly as
+// k_attn_part computes it: part[h pstride + kb (HD + 2)] = o[HD], m, l.
+//   scores: thread (position p, chunk c): the fma chain over the chunk's 32 dims in order; the chunks added in order
+//     (neighbouring lanes), times scale; softmax: m = max, e = exp_att(s - m), l = 16 lane chains + the tree (wave 15);
+//     o: thread i < HD (a dim), the fma chain over the positions in order, two register sets of 16 positions'
+//     loads alternating (a copy between sets would wait for the loads).
+// 16 waves: the block's 2 x 32 HD bytes of K / V are loaded in HD / 32 rounds of 16 bytes per thread (a CU's loads in
+// flight grow with its waves). Blocks b: XCD x = b % 8, y = b / 8, v = y % kv_mul, item = x + 8 (y / kv_mul) (an
+// item's kv_mul blocks share an XCD and its L2); item = kb nkv + g. K / V blocks are loaded whole (the cache holds
+// every 256-position block whole).
+#define ATD_T 1024
+#define ATD_KR 1056                 // LDS bytes of a K chunk row: 32 dims x 16 positions x 2 + 32 padding
+#define ATD_KT (4 * ATD_KR + 32)    // LDS bytes of a K tile: the 4 tiles of a wave's 64 positions in distinct banks
+template <int HD>
+__global__ __launch_bounds__(ATD_T) void k_attn_decode(const float *__restrict__ qkv, int nh, int nkv, float scale,
+                                                       const float *__restrict__ qn, const float *__restrict__ kn,
+                                                       const float *__restrict__ rope, int pos, uint16_t *__restrict__ kl,
+                                                       uint16_t *__restrict__ vl, float *__restrict__ part, int pstride) {
+    constexpr int NCH = HD / 32, TB = 32 * HD, NR = 256 * HD * 2 / (ATD_T * 16); // chunks, tile bytes, load rounds
+    __shared__ __align__(16) uint8_t ks[16 * ATD_KT];
+    __shared__ __align__(16) uint8_t vs[256 * HD * 2];
+    __shared__ __align__(16) float qs[HD];
+    __shared__ float qx[HD], kx[HD], S[256], red[20];
+    const int kv_mul = nh / nkv, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int x = blockIdx.x & 7, y = blockIdx.x >> 3, v = y % kv_mul, item = x + 8 * (y / kv_mul);
+    const int nb = pos / ATT_P + 1;
+    if (item >= nkv * nb) return;
+    const int g = item % nkv, kb = item / nkv, h = g * kv_mul + v, half = HD / 2, pp = pos % ATT_P;
+    const bool last = kb == nb - 1;
+    const int n = last ? pp + 1 : ATT_P; // positions of this block up to pos
+    // 1. the row's q, k and v heads (lane i % HD: no branch around the loads), issued before the cache loads
+    const int ti = t % HD;
+    const float qr = qkv[(size_t)h * HD + ti], kr = qkv[(size_t)(nh + g) * HD + ti], vr = qkv[(size_t)(nh + nkv + g) * HD + ti];
+    // 2. the cache's K and V blocks (whole: NR rounds of 16 bytes per thread)
+    const uint8_t *K = (const uint8_t *)(kl + ((size_t)kb * nkv + g) * ATT_P * HD);
+    const uint8_t *V = (const uint8_t *)(vl + ((size_t)kb * nkv + g) * ATT_P * HD);
+    static_assert(NR >= 1 && NR <= 4, "HD in 32, 64, 128");
+    uint4 k0, k1, k2, k3, v0, v1, v2, v3; // (named: an array here is placed in scratch memory)
+#define ATD_LD(k, KR, VR)                                                                                               \
+    if constexpr (NR > k) {                                                                                         \
+        KR = *(const uint4 *)(K + (size_t)(t + ATD_T * k) * 16);                                                     \
+        VR = *(const uint4 *)(V + (size_t)(t + ATD_T * k) * 16);                                                     \
+    }
+    ATD_LD(0, k0, v0) ATD_LD(1, k1, v1) ATD_LD(2, k2, v2) ATD_LD(3, k3, v3)
+#undef ATD_LD
+    // 3. QK-norm + RoPE (k_qknorm_rope_store's arithmetic): the raw heads into LDS, the scales by waves 0 / 1
+    if (t < HD) {
+        qx[t] = qr;
+        kx[t] = kr;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float r = rms_scale_lds(qx, HD);
+        if (lane == 0) red[0] = r;
+    } else if (wave == 1 && last) {
+        float r = rms_scale_lds(kx, HD);
+        if (lane == 0) red[1] = r;
+    }
+    // 4. the K / V blocks into LDS (K tiles: chunk rows ATD_KR apart, tiles ATD_KT apart; V rows as in the cache)
+#define ATD_ST(k, KR, VR)                                                                                               \
+    if constexpr (NR > k) {                                                                                         \
+        int o = (t + ATD_T * k) * 16, tile = o / TB, w = o % TB;                                                     \
+        *(uint4 *)(ks + tile * ATD_KT + (w >> 10) * ATD_KR + (w & 1023)) = KR;                                       \
+        *(uint4 *)(vs + o) = VR;                                                                                     \
+    }
+    ATD_ST(0, k0, v0) ATD_ST(1, k1, v1) ATD_ST(2, k2, v2) ATD_ST(3, k3, v3)
+#undef ATD_ST
+    __syncthreads();
+    const float *cs = rope + (size_t)pos * HD;
+    if (t < half) {
+        int i = t;
+        float r = red[0];
+        float xq = (qn[i] * qx[i]) * r, yq = (qn[i + half] * qx[i + half]) * r;
+        float c = cs[i], s = cs[i + half];
+        float ys = yq * s, yc = yq * c;
+        qs[i] = __builtin_fmaf(xq, c, -ys);
+        qs[i + half] = __builtin_fmaf(xq, s, yc);
+        if (last) { // the row's key: into this block's LDS copy at pp, and (v = 0) into the cache
+            float rk = red[1];
+            float xk = (kn[i] * kx[i]) * rk, yk = (kn[i + half] * kx[i + half]) * rk;
+            float ysk = yk * s, yck = yk * c;
+            uint16_t kh0 = f2h_ref(__builtin_fmaf(xk, c, -ysk)), kh1 = f2h_ref(__builtin_fmaf(xk, s, yck));
+            int tile = pp / ATT_T, col = pp % ATT_T;
+            *(uint16_t *)(ks + tile * ATD_KT + (i >> 5) * ATD_KR + ((i & 31) * 16 + col) * 2) = kh0;
+            *(uint16_t *)(ks + tile * ATD_KT + ((i + half) >> 5) * ATD_KR + (((i + half) & 31) * 16 + col) * 2) = kh1;
+            if (v == 0) {
+                uint16_t *kd = kl + (((size_t)kb * nkv + g) * ATT_P + (size_t)tile * ATT_T) * HD + col;
+                kd[(size_t)i * ATT_T] = kh0;
+                kd[(size_t)(i + half) * ATT_T] = kh1;
+            }
+        }
+    }
+    if (last && t < HD) { // the row's value
+        uint16_t vh = f2h_ref(vr);
+        *(uint16_t *)(vs + ((size_t)pp * HD + t) * 2) = vh;
+        if (v == 0) vl[(((size_t)kb * nkv + g) * ATT_P + pp) * HD + t] = vh;
+    }
+    __syncthreads();
+    // 5. scores: thread (p, c)
+    const int p = t >> 2, c = t & 3;
+    float acc = 0.0f;
+    if (p < n && c < NCH) {
+        const uint8_t *kt = ks + (p / ATT_T) * ATD_KT + c * ATD_KR + (p % ATT_T) * 2;
+        const float *qc = qs + 32 * c;
+        float kf[32];
+        #pragma unroll
+        for (int i = 0; i < 32; i++) kf[i] = h2f(*(const uint16_t *)(kt + i * 32));
+        #pragma unroll
+        for (int i = 0; i < 32; i += 4) {
+            float4 q4 = *(const float4 *)(qc + i);
+            acc = __builtin_fmaf(q4.x, kf[i], acc);
+            acc = __builtin_fmaf(q4.y, kf[i + 1], acc);
+            acc = __builtin_fmaf(q4.z, kf[i + 2], acc);
+            acc = __builtin_fmaf(q4.w, kf[i + 3], acc);
+        }
+    }
+    float c1 = __shfl_down(acc, 1), c2 = __shfl_down(acc, 2), c3 = __shfl_down(acc, 3);
+    float a = acc;
+    if (NCH > 1) a = a + c1;
+    if (NCH > 2) a = a + c2;
+    if (NCH > 3) a = a + c3;
+    const float sc = c == 0 && p < n ? a * scale : -3.402823466e38f;
+    // 6. softmax
+    float m = wave_max(sc);
+    if (lane == 0) red[4 + wave] = m;
+    __syncthreads();
+    m = red[4];
+    #pragma unroll
+    for (int w = 1; w < 16; w++) m = fmaxf(m, red[4 + w]);
+    if (c == 0 && p < n) S[p] = exp_att(sc - m);
+    __syncthreads();
+    // 7. l (wave 15, lanes 0..15: chains over p = lane, lane + 16, ... then the tree) beside o (threads i < HD)
+    if (wave == 15) {
+        float s = 0.0f;
+        if (lane < 16) {
+            int q = lane;
+            for (; q + 48 < n; q += 64) {
+                float e0 = S[q], e1 = S[q + 16], e2 = S[q + 32], e3 = S[q + 48];
+                s = s + e0;
+                s = s + e1;
+                s = s + e2;
+                s = s + e3;
+            }
+            for (; q < n; q += 16) s = s + S[q];
+        }
+        for (int w = 8; w >= 1; w >>= 1) {
+            float o = __shfl_down(s, w);
+            s = s + o;
+        }
+        if (lane == 0) {
+            float *ml = part + (size_t)h * pstride + (size_t)kb * (HD + 2) + HD;
+            ml[0] = m;
+            ml[1] = s;
+        }
+    } else if (t < HD) {
+        const uint16_t *vcol = (const uint16_t *)vs + t;
+        float o = 0.0f;
+        int q = 0;
+        uint16_t va[16], vb[16];
+        float ea[16], eb[16];
+        auto ld = [&](uint16_t (&vv)[16], float (&ee)[16], int q0) {
+            #pragma unroll
+            for (int u = 0; u < 16; u++) {
+                vv[u] = vcol[(size_t)(q0 + u) * HD];
+                ee[u] = S[q0 + u];
+            }
+        };
+        auto fold = [&](const uint16_t (&vv)[16], const float (&ee)[16]) {
+            #pragma unroll
+            for (int u = 0; u < 16; u++) o = __builtin_fmaf(ee[u], h2f(vv[u]), o);
+        };
+        if (n >= 16) {
+            ld(va, ea, 0);
+            for (q = 16; q + 32 <= n; q += 32) {
+                ld(vb, eb, q);
+                fold(va, ea);
+                ld(va, ea, q + 16);
+                fold(vb, eb);
+            }
+            if (q + 16 <= n) {
+                ld(vb, eb, q);
+                fold(va, ea);
+                fold(vb, eb);
+                q += 16;
+            } else {
+                fold(va, ea);
+            }
+        }
+        for (; q < n; q++) o = __builtin_fmaf(S[q], h2f(vcol[(size_t)q * HD]), o);
+        part[(size_t)h * pstride + (size_t)kb * (HD + 2) + t] = o;
+    }
+}
+
 // one block per row: the attention of each head from its block partials in block order (att_combine,
 // forward.c:1405-1431), then the row's quantization for wo (aq row b, all_heads = nh * hd values, a multiple of 256).
 // Steps: every block's (m, l) into LDS and the first 8 blocks' o values of the thread's elements into registers, all
@@ -676,6 +874,17 @@ int gw_k_attn_part(const void *items, int nitems, int nq_max, const float *qkv, 
     else if (nq <= 8) ATT_LAUNCH(8);
     else ATT_LAUNCH(16);
 #undef ATT_LAUNCH
+    return (int)hipGetLastError();
+}
+
+int gw_k_attn_decode(const float *qkv, int nh, int nkv, int hd, float scale, const float *qn, const float *kn, const float *rope,
+                     int pos, uint16_t *kl, uint16_t *vl, float *part, int pstride, hipStream_t s) {
+    int kvm = nh / nkv, nitems = nkv * (pos / ATT_P + 1);
+    dim3 grid(8 * kvm * ((nitems + 7) / 8));
+    if (hd == 128) GW_LAUNCH(k_attn_decode<128>, grid, dim3(ATD_T), 0, s, qkv, nh, nkv, scale, qn, kn, rope, pos, kl, vl, part, pstride);
+    else if (hd == 64) GW_LAUNCH(k_attn_decode<64>, grid, dim3(ATD_T), 0, s, qkv, nh, nkv, scale, qn, kn, rope, pos, kl, vl, part, pstride);
+    else if (hd == 32) GW_LAUNCH(k_attn_decode<32>, grid, dim3(ATD_T), 0, s, qkv, nh, nkv, scale, qn, kn, rope, pos, kl, vl, part, pstride);
+    else return (int)hipErrorInvalidValue;
     return (int)hipGetLastError();
 }
 
