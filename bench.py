@@ -1,8 +1,8 @@
 """Benchmark of the forward hot path on one MI355X: decode + prefill tok/s of a Qwen3-8B-shaped Q8_0 model.
 
 One step = the run shape of the reference's config 1 on the metric's model: reset the sequence, prefill a 512-token
-prompt of seeded random ids (rq_prefill, one 512-row pass), then 128 greedy decode steps (rq_decode with the argmax on
-the device, gw_decode_argmax). value = (512 + 128) tokens per step / seconds per step, whole job (one GPU), inputs
+prompt of seeded random ids (rq_prefill, one 512-row pass), then 128 greedy decode steps (gw_decode_greedy: rq_decode
+with the argmax on the device, each step's token fed to the next on the device, one wait for the 128). value = (512 + 128) tokens per step / seconds per step, whole job (one GPU), inputs
 (weights, prompt ids) resident on the device before the timed region starts.
 Weights: random-init, N(0, 0.02) then Q8_0 (a synthetic GGUF written by gwenedeg_amd.synth, seeded); no checkpoint.
 
@@ -95,10 +95,7 @@ def main():
         c.prefill(s, ids, mode=gw.RQ_LOGITS_LAST)
         tok = int(c.argmax(1)[0])
         t1 = time.perf_counter()
-        toks = [tok]
-        for _ in range(a.gen):
-            tok = c.decode_argmax(s, tok)
-            toks.append(tok)
+        toks = [tok] + [int(t) for t in c.decode_greedy(s, tok, a.gen)]
         t2 = time.perf_counter()
         return t1 - t0, t2 - t1, toks
 
@@ -211,9 +208,7 @@ def probe(torch, gw, c, s, ids, a):
     c.prefill(s, ids[:16], mode=gw.RQ_LOGITS_LAST)
     s.reset()
     c.prefill(s, ids, mode=gw.RQ_LOGITS_LAST)
-    tok = int(c.argmax(1)[0])
-    for _ in range(a.gen):
-        tok = c.decode_argmax(s, tok)
+    c.decode_greedy(s, int(c.argmax(1)[0]), a.gen)
     src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
     torch.cuda.synchronize()

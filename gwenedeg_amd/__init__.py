@@ -116,6 +116,7 @@ _sig = {
     "gw_ctx_argmax": (_I, [_P, ctypes.POINTER(_I), _I]),
     "gw_ctx_stream": (_P, [_P]),
     "gw_decode_argmax": (_I, [_P, _P, _I, ctypes.POINTER(_I)]),
+    "gw_decode_greedy": (_I, [_P, _P, _I, _I, ctypes.POINTER(_I)]),
     "gw_ctx_profile_enable": (_I, [_P, _I]),
     "gw_ctx_gemv_sweep": (_I, [_P, _I, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),
     "gw_ctx_profile_launches": (ctypes.c_long, [_P, _I]),
@@ -306,6 +307,12 @@ class Ctx:
         nxt = ctypes.c_int(0)
         self._check(lib.gw_decode_argmax(self._h, seq._h, int(token), ctypes.byref(nxt)), "gw_decode_argmax")
         return nxt.value
+
+    def decode_greedy(self, seq: Seq, token: int, n: int) -> np.ndarray:
+        """gw_decode_greedy: n greedy steps from token, the tokens chosen on the device (one wait for all n)"""
+        out = np.zeros(n, np.int32)
+        self._check(lib.gw_decode_greedy(self._h, seq._h, int(token), int(n), _iptr(out)), "gw_decode_greedy")
+        return out
 
     def profile(self, on: bool = True):
         self._check(lib.gw_ctx_profile_enable(self._h, 1 if on else 0), "gw_ctx_profile_enable")

@@ -154,11 +154,13 @@ static void dfree(void *p) { if (p) hipFree(p); }
 
 void rq_ctx_free(RqCtx *c) {
     if (!c) return;
-    void *d[] = { c->x, c->xb, c->qkv, c->hb, c->part, c->logits_d, c->hid_d, c->xq, c->hq, c->xs, c->hs, c->argmax_d, c->argmax_scr, c->meta_d };
+    void *d[] = { c->x, c->xb, c->qkv, c->hb, c->part, c->logits_d, c->hid_d, c->xq, c->hq, c->xs, c->hs, c->argmax_d, c->argmax_scr, c->meta_d,
+                  c->gtok_d, c->gpos_d };
     for (size_t i = 0; i < sizeof d / sizeof d[0]; i++) dfree(d[i]);
     if (c->meta_h) hipHostFree(c->meta_h);
     if (c->logits) hipHostFree(c->logits);
     if (c->lg_h) hipHostFree(c->lg_h);
+    if (c->g_h) hipHostFree(c->g_h);
     if (c->ev) {
         for (int i = 0; i < 2048; i++)
             if (c->ev[i]) hipEventDestroy(c->ev[i]);
@@ -218,6 +220,7 @@ static int ctx_meta(RqCtx *c, size_t bytes) {
 static int ctx_lg(RqCtx *c, size_t rows) {
     if (rows <= c->lg_h_rows) return RQ_OK;
     if (c->lg_h) hipHostFree(c->lg_h);
+    if (c->g_h) hipHostFree(c->g_h);
     c->lg_h = NULL;
     c->lg_h_rows = 0;
     HIPCHK(c, "hipHostMalloc (logits)", hipHostMalloc((void **)&c->lg_h, rows * c->m->vocab * sizeof(float), hipHostMallocDefault));
@@ -425,6 +428,37 @@ static int run_mm(RqCtx *c, const GwMat *w, int nmat, const int8_t *xq, const fl
 
 #define KCHK(x) do { if (x) return ctx_fail(c, RQ_ERR_STATE, "kernel launch failed: %s", #x); } while (0)
 
+static int fused_layer(RqCtx *c, int l, RqSeq *sq, int pos, const int *pos_d) {
+    /* layer l of the one-row pass of an all-Q8_0 model (the fused decode sequence, x in place): qkv GEMV (rmsnorm +
+     * quantize prologue) -> attention (QK-norm, RoPE, K / V store inside) -> wo GEMV (combine prologue, + residual) ->
+     * w1 / w3 GEMV (rmsnorm prologue, SwiGLU epilogue) -> w2 GEMV (+ residual). pos: the row's position (pos_d: the
+     * same on the device, for the combine kernel past GW_GV_NBMAX key blocks) */
+    const RqModel *m = c->m;
+    const GwLayer *y = &m->layer[l];
+    hipStream_t s = c->stream;
+    int nh = m->n_heads, hd = m->head_dim, nb = pos / GW_ATT_P + 1;
+    pf_mark(c, GW_PF_QKV);
+    KCHK(gw_k_gemv1_norm(&y->qkv[0], GW_GV_R_QKV, c->x, y->att_norm, c->qkv, 0, 0, s));
+    pf_mark(c, GW_PF_ATT);
+    KCHK(gw_k_attn_decode(c->qkv, nh, m->n_kv_heads, hd, m->att_scale, y->q_norm, y->k_norm, m->rope, pos,
+                          sq->kc + (size_t)l * seq_layer_elems(sq), sq->vc + (size_t)l * seq_layer_elems(sq), c->part,
+                          c->pstride, s));
+    if (nb <= GW_GV_NBMAX) {
+        pf_mark(c, GW_PF_WO);
+        KCHK(gw_k_gemv1_combine(&y->wo, GW_GV_R_WO, c->part, c->pstride, hd, nb, c->x, 1, s));
+    } else {
+        pf_mark(c, GW_PF_COMBINE);
+        KCHK(gw_k_attn_combine_quant(c->part, c->pstride, nh, hd, pos_d, 1, c->xq, c->xs, c->kmax, NULL, s));
+        pf_mark(c, GW_PF_WO);
+        KCHK(gw_k_gemv1_q(&y->wo, GW_GV_R_WO, c->xq, c->xs, c->x, 1, s));
+    }
+    pf_mark(c, GW_PF_W13);
+    KCHK(gw_k_gemv1_norm(&y->w13[0], GW_GV_R_W13, c->x, y->ffn_norm, c->hb, 0, y->w13_il, s));
+    pf_mark(c, GW_PF_W2);
+    KCHK(gw_k_gemv1_qf(&y->w2, GW_GV_R_W2, c->hb, c->x, 1, s));
+    return RQ_OK;
+}
+
 static int fw_pass(RqCtx *c, Pass *P, float *out) {
     /* the rows of P through the model (every validation done by the caller); out: nsel x vocab logits (host), or
      * NULL with nsel == 0 */
@@ -489,6 +523,10 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
     int fused = n == 1 && fused_shape(m), fused_att = fused && (hd == 128 || hd == 64 || hd == 32);
     for (int l = 0; l < L; l++) {
         const GwLayer *y = &m->layer[l];
+        if (fused_att) {
+            if ((rc = fused_layer(c, l, P->seq[0], P->pos[0], pos_d)) != RQ_OK) return rc;
+            continue;
+        }
         if (fused) {
             pf_mark(c, GW_PF_QKV);
             KCHK(gw_k_gemv1_norm(&y->qkv[0], GW_GV_R_QKV, c->x, y->att_norm, c->qkv, 0, 0, s));
@@ -498,20 +536,12 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
             pf_mark(c, GW_PF_QKV);
             if ((rc = run_mm(c, y->qkv, y->nqkv, c->xq, c->xs, K, n, c->qkv, c->ldqkv, 0)) != RQ_OK) return rc;
         }
-        if (fused_att) { /* QK-norm + RoPE + K / V store inside the decode attention */
-            pf_mark(c, GW_PF_ATT);
-            RqSeq *sq = P->seq[0];
-            KCHK(gw_k_attn_decode(c->qkv, nh, nkv, hd, m->att_scale, y->q_norm, y->k_norm, m->rope, P->pos[0],
-                                  sq->kc + (size_t)l * seq_layer_elems(sq), sq->vc + (size_t)l * seq_layer_elems(sq),
-                                  c->part, c->pstride, s));
-        } else {
-            pf_mark(c, GW_PF_ROPE);
-            KCHK(gw_k_qknorm_rope_store(c->qkv, c->ldqkv, n, nh, nkv, hd, y->q_norm, y->k_norm, m->rope, pos_d,
-                                        kc_d + (size_t)l * n, vc_d + (size_t)l * n, s));
-            pf_mark(c, GW_PF_ATT);
-            KCHK(gw_k_attn_part(items_d, nitems, nq_max, c->qkv, c->ldqkv, nh, nkv, hd, m->att_scale, pos_d,
-                                kc_d + (size_t)l * n, vc_d + (size_t)l * n, c->part, c->pstride, s));
-        }
+        pf_mark(c, GW_PF_ROPE);
+        KCHK(gw_k_qknorm_rope_store(c->qkv, c->ldqkv, n, nh, nkv, hd, y->q_norm, y->k_norm, m->rope, pos_d,
+                                    kc_d + (size_t)l * n, vc_d + (size_t)l * n, s));
+        pf_mark(c, GW_PF_ATT);
+        KCHK(gw_k_attn_part(items_d, nitems, nq_max, c->qkv, c->ldqkv, nh, nkv, hd, m->att_scale, pos_d,
+                            kc_d + (size_t)l * n, vc_d + (size_t)l * n, c->part, c->pstride, s));
         if (fused) {
             if (nbmax <= GW_GV_NBMAX) {
                 pf_mark(c, GW_PF_WO);
@@ -637,6 +667,73 @@ int gw_decode_argmax(RqCtx *c, RqSeq *s, int token, int *next) {
     s->tokens[s->len] = token;
     s->len++;
     return gw_ctx_argmax(c, next, 1);
+}
+
+int gw_decode_greedy(RqCtx *c, RqSeq *s, int token, int n, int *tokens) {
+    /* n greedy decode steps from token (the generation loop of chat.c:348 with sample_argmax, sampler.c:40-60):
+     * tokens[i] = the first maximum of step i's logits, the token step i + 1 is fed. The token of each step stays on the
+     * device (the argmax kernel writes it where the next step's embedding reads it), so the n passes are enqueued
+     * without waiting for each other and the host waits once. The same kernels and results as n gw_decode_argmax calls;
+     * a model outside the fused decode shapes runs exactly those calls */
+    c->err[0] = 0;
+    int e = check_seq(c, s);
+    if (e != RQ_OK) return e;
+    const RqModel *m = c->m;
+    if (n < 1 || !tokens) return ctx_fail(c, RQ_ERR_ARG, "bad greedy arguments (n %d)", n);
+    if (token < 0 || token >= m->vocab) return ctx_fail(c, RQ_ERR_ARG, "token %d out of range", token);
+    if (s->len + n > s->cap) return ctx_fail(c, RQ_ERR_CONTEXT, "%d steps at position %d: past the capacity %d", n, s->len, s->cap);
+    int hd = m->head_dim;
+    if (!(fused_shape(m) && (hd == 128 || hd == 64 || hd == 32))) {
+        for (int i = 0; i < n; i++) {
+            if ((e = gw_decode_argmax(c, s, i ? tokens[i - 1] : token, &tokens[i])) != RQ_OK) return e;
+        }
+        return RQ_OK;
+    }
+    if (n > c->g_cap) {
+        HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));
+        dfree(c->gtok_d);
+        dfree(c->gpos_d);
+        if (c->g_h) hipHostFree(c->g_h);
+        c->gtok_d = c->gpos_d = c->g_h = NULL;
+        c->g_cap = 0;
+        HIPCHK(c, "hipMalloc (greedy tokens)", hipMalloc((void **)&c->gtok_d, (size_t)(n + 1) * sizeof(int)));
+        HIPCHK(c, "hipMalloc (greedy positions)", hipMalloc((void **)&c->gpos_d, (size_t)n * sizeof(int)));
+        HIPCHK(c, "hipHostMalloc (greedy staging)", hipHostMalloc((void **)&c->g_h, (size_t)(2 * n + 1) * sizeof(int), 0));
+        c->g_cap = n;
+    }
+    int p0 = s->len;
+    if ((e = ctx_part(c, 1, (p0 + n - 1) / GW_ATT_P + 1)) != RQ_OK) return e;
+    hipStream_t st = c->stream;
+    HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(st)); /* (the staging may still be read by a previous call) */
+    c->g_h[0] = token;
+    for (int i = 0; i < n; i++) c->g_h[1 + i] = p0 + i;
+    HIPCHK(c, "hipMemcpyAsync (greedy token)", hipMemcpyAsync(c->gtok_d, c->g_h, sizeof(int), hipMemcpyHostToDevice, st));
+    HIPCHK(c, "hipMemcpyAsync (greedy positions)", hipMemcpyAsync(c->gpos_d, c->g_h + 1, (size_t)n * sizeof(int),
+                                                                  hipMemcpyHostToDevice, st));
+    c->kt_multi = 0;
+    for (int i = 0; i < n; i++) {
+        c->nev = 0;
+        pf_mark(c, GW_PF_EMBED);
+        KCHK(gw_k_embed_q8(c->x, m->dim, (const uint8_t *)m->embd.codes, m->embd.scales, c->gtok_d + i, 1, st));
+        for (int l = 0; l < m->n_layers; l++)
+            if ((e = fused_layer(c, l, s, p0 + i, c->gpos_d + i)) != RQ_OK) return e;
+        pf_mark(c, GW_PF_CLS);
+        KCHK(gw_k_gemv1_norm(&m->cls, GW_GV_R_CLS, c->x, m->final_norm, c->logits_d, 0, 0, st));
+        pf_mark(c, -1);
+        KCHK(gw_k_argmax(c->logits_d, m->vocab, m->vocab, 1, c->gtok_d + i + 1, c->argmax_scr, st));
+        if (c->prof_on) { /* (profiling: each pass's intervals, as the passes of fw_pass) */
+            HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(st));
+            pf_collect(c);
+        }
+    }
+    HIPCHK(c, "hipMemcpyAsync (greedy tokens)", hipMemcpyAsync(c->g_h, c->gtok_d + 1, (size_t)n * sizeof(int),
+                                                               hipMemcpyDeviceToHost, st));
+    HIPCHK(c, "hipStreamSynchronize (greedy)", hipStreamSynchronize(st));
+    memcpy(tokens, c->g_h, (size_t)n * sizeof(int));
+    for (int i = 0; i < n; i++) s->tokens[p0 + i] = i ? tokens[i - 1] : token;
+    s->len = p0 + n;
+    c->last_nsel = 1;
+    return RQ_OK;
 }
 
 int rq_decode_hidden(RqCtx *c, RqSeq *s, int token, float **logits, float *hidden, const float *h_in) {

@@ -38,6 +38,7 @@ struct GvArgs {
     float *out;       // out[row] (mode 1: out[row] + val, a residual add)
     int mode;
     int cmax;         // tiles whose partials the block keeps in LDS between folds
+    float inv_k;      // GV_NORM: 1.0f / K (the host's division, as the reference's 1.0f / size)
 };
 
 __device__ __forceinline__ float gv_fold(const float *p, int G) {
@@ -167,48 +168,48 @@ __global__ __launch_bounds__(NT) void k_gemv1(GvArgs a) {
             if (t < 64) {
                 float ss = 0.0f;
                 if (t < 16) {
+                    // the chain over the row's K / 16 values of lane t (K % 64 == 0): two sets of QS float4 LDS reads
+                    // take turns (a copy from one set into the other would wait for its reads)
+                    constexpr int QS = NT <= 256 ? 16 : 4; // (768 threads: 168 registers)
                     const float4 *c = (const float4 *)(xf + t * LS);
-                    const int n4 = K >> 6; // the chain's float4s (K % 64 == 0)
-                    int i = 0;
-                    if (n4 >= 8) {
-                        float4 q[8];
+                    const int n4 = K >> 6; // the chain's float4s
+                    auto fma4 = [&](const float4 (&q)[QS], int m) {
                         #pragma unroll
-                        for (int u = 0; u < 8; u++) q[u] = c[u];
-                        for (i = 8; i + 8 <= n4; i += 8) {
-                            float4 q2[8];
-                            #pragma unroll
-                            for (int u = 0; u < 8; u++) q2[u] = c[i + u];
-                            #pragma unroll
-                            for (int u = 0; u < 8; u++) {
+                        for (int u = 0; u < QS; u++)
+                            if (u < m) {
                                 ss = __builtin_fmaf(q[u].x, q[u].x, ss);
                                 ss = __builtin_fmaf(q[u].y, q[u].y, ss);
                                 ss = __builtin_fmaf(q[u].z, q[u].z, ss);
                                 ss = __builtin_fmaf(q[u].w, q[u].w, ss);
                             }
-                            #pragma unroll
-                            for (int u = 0; u < 8; u++) q[u] = q2[u];
-                        }
+                    };
+                    auto ld4 = [&](float4 (&q)[QS], int i0) {
                         #pragma unroll
-                        for (int u = 0; u < 8; u++) {
-                            ss = __builtin_fmaf(q[u].x, q[u].x, ss);
-                            ss = __builtin_fmaf(q[u].y, q[u].y, ss);
-                            ss = __builtin_fmaf(q[u].z, q[u].z, ss);
-                            ss = __builtin_fmaf(q[u].w, q[u].w, ss);
-                        }
+                        for (int u = 0; u < QS; u++) q[u] = c[i0 + u < n4 ? i0 + u : 0];
+                    };
+                    float4 qa[QS], qb[QS];
+                    int i = 0;
+                    ld4(qa, 0);
+                    for (; i + 2 * QS <= n4; i += 2 * QS) {
+                        ld4(qb, i + QS);
+                        fma4(qa, QS);
+                        ld4(qa, i + 2 * QS);
+                        fma4(qb, QS);
                     }
-                    for (; i < n4; i++) {
-                        float4 q = c[i];
-                        ss = __builtin_fmaf(q.x, q.x, ss);
-                        ss = __builtin_fmaf(q.y, q.y, ss);
-                        ss = __builtin_fmaf(q.z, q.z, ss);
-                        ss = __builtin_fmaf(q.w, q.w, ss);
+                    // (qa holds i .. i + QS - 1)
+                    if (i + QS <= n4) {
+                        ld4(qb, i + QS);
+                        fma4(qa, QS);
+                        fma4(qb, n4 - i - QS);
+                    } else {
+                        fma4(qa, n4 - i);
                     }
                 }
                 for (int w = 8; w >= 1; w >>= 1) {
                     float o = __shfl_down(ss, w);
                     ss = ss + o;
                 }
-                if (t == 0) xf[16 * LS] = rsqrt_ref(__builtin_fmaf(ss, 1.0f / (float)K, 1e-6f));
+                if (t == 0) xf[16 * LS] = rsqrt_ref(__builtin_fmaf(ss, a.inv_k, 1e-6f));
             }
             __syncthreads();
             float r = xf[16 * LS];
@@ -349,6 +350,7 @@ static int gv_launch(int pro, int R, const GvArgs &a, hipStream_t s) {
     cmax = cmax < 1 ? 1 : cmax > 16 ? 16 : cmax;
     GvArgs b = a;
     b.cmax = tpw < cmax ? tpw : cmax;
+    b.inv_k = 1.0f / (float)a.K;
     size_t lds = (size_t)b.cmax * slot_bytes + (pro == GV_NORM ? (size_t)(16 * (a.K / 16 + 4) + 4) * sizeof(float) : 0);
     dim3 grid(nwg);
     hipEvent_t e0, e1;

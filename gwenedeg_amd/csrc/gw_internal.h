@@ -86,6 +86,8 @@ struct RqCtx {
     size_t lg_h_rows;
     char err[256];
     int last_nsel;     /* logits rows the last pass left on the device (gw_ctx_argmax) */
+    int *gtok_d, *gpos_d, *g_h; /* gw_decode_greedy: tokens and positions on the device, pinned staging; g_cap steps */
+    int g_cap;
     void *smp, *smp_t; /* host scratch of the reference's sampler (ctx_sampler_scratch[_threads]): vocab x 8 bytes */
     int smp_nt;
     /* profiling (gw_ctx_profile_enable): HIP events around each kernel class of a pass, summed per class */

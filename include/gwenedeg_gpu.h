@@ -154,6 +154,12 @@ int gw_ctx_argmax(RqCtx *c, int *tokens, int n);
  * greedy generation (rq_gen_step + sample_argmax, chat.c:348, sampler.c:40) without the logits transfer */
 int gw_decode_argmax(RqCtx *c, RqSeq *s, int token, int *next);
 
+/* n greedy decode steps from token (the generation loop of chat.c:348 with sample_argmax, sampler.c:40-60):
+ * tokens[i] = the first maximum of step i's logits, the token fed to step i + 1; the sequence grows by n (token,
+ * tokens[0 .. n - 2] are its new tokens). Each step's token stays on the device, so the n passes run back to back and
+ * the host waits once. Results equal n gw_decode_argmax calls. RQ_ERR_CONTEXT past the capacity, nothing done */
+int gw_decode_greedy(RqCtx *c, RqSeq *s, int token, int n, int *tokens);
+
 /* Per-kernel-class device time (the GPU counterpart of the reference's -DRUNQ_PROFILE phases, forward.c:13-24):
  * gw_ctx_profile_enable(c, 1) resets the counters and brackets each kernel class of every later pass with HIP events
  * on the context's stream; rq_ctx_profile then returns the classes' names and summed seconds, and

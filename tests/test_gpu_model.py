@@ -133,3 +133,32 @@ def test_device_argmax(gw, synth_models):
     s = m.seq(256)
     lg = c.prefill(s, _ids(m.vocab, 9, 2))
     assert int(c.argmax(1)[0]) == int(np.argmax(lg))
+
+
+@pytest.mark.parametrize("shape,n_prompt,steps", [("tiny", 9, 40), ("tiny_hd64", 250, 20), ("tiny_gqa4", 1000, 40),
+                                                  ("tiny_kq", 5, 6)])
+def test_decode_greedy_equals_step_by_step(gw, synth_models, shape, n_prompt, steps):
+    """gw_decode_greedy (tokens fed on the device, one wait) against gw_decode_argmax step by step and the host argmax
+    of rq_decode's logits: the same tokens, the same cache (the logits of a later step agree bit for bit); across
+    key-block boundaries (250 + 20 passes position 256, 1000 + 40 passes 1024: the combine past GW_GV_NBMAX blocks);
+    a K-quant model takes the step-by-step path"""
+    path = synth_models(shape)
+    m = gw.Model(path, ctx_len=2048)
+    c = m.ctx(max_batch=64, max_ctx=2048)
+    ids = _ids(m.vocab, n_prompt, 4)
+    s1, s2 = m.seq(2048), m.seq(2048)
+    lg = c.prefill(s1, ids)
+    c.prefill(s2, ids)
+    t0 = int(np.argmax(lg))
+    got = c.decode_greedy(s1, t0, steps)
+    ref, tok = [], t0
+    for _ in range(steps):
+        lg = c.decode(s2, tok)
+        tok = int(np.argmax(lg))
+        ref.append(tok)
+    assert [int(t) for t in got] == ref
+    assert len(s1) == len(s2) == n_prompt + steps
+    assert np.array_equal(s1.tokens(), s2.tokens())
+    a = c.decode(s1, 7)
+    b = c.decode(s2, 7)
+    assert _bits_equal(a, b)
