@@ -62,37 +62,39 @@ __global__ __launch_bounds__(256) void k_fill_synthetic(uint16_t *kc, uint16_t *
 // out[m * ldo + n] = W row n . X row m for m < M, n < N (prefill / batched rows): per group g of 32 (one K step of
 // v_mfma_i32_32x32x32_i8), the exact int32 sums of a 32 x 32 output tile, then per output the reference's fold
 // val = val + (ws * xs) * (float) isum, groups in order (forward.c:906-916). A block of 256 threads (4 waves) computes a
-// GM x GN tile (wave w: rows 32 (w / (GN / 64)) .., columns 64 (w % (GN / 64)) .., two MFMA tiles); X and W are staged
-// in LDS 4 groups (128 bytes of each row) at a time with 16-byte loads, rows padded to 144 bytes.
+// GM x GN tile, GN = 128: GM = 64, wave w takes rows 32 (w / 2) .., columns 64 (w % 2) .. (two MFMA tiles); GM = 32 (for
+// matrices whose 64-row tiles leave CUs with one wave per SIMD), wave w takes columns 32 w .. (one MFMA tile). X and W
+// are staged in LDS 4 groups (128 bytes of each row) at a time with 16-byte loads, rows padded to 144 bytes.
 // MFMA operand layout (32 x 32 x 32, int8): lane l holds A[l % 32][16 (l / 32) .. + 15] and B[16 (l / 32) .. + 15][l % 32];
 // result register r of lane l is C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32]
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
-#define GM 64
 #define GN 128
 #define GKB 128
 #define GROW 144
+template <int GM>
 __global__ __launch_bounds__(256) void k_gemm_q8(const int8_t *__restrict__ W, const uint16_t *__restrict__ WS, int N, int K,
                                                  const int8_t *__restrict__ X, const float *__restrict__ XS, int ldx, int M,
                                                  float *__restrict__ out, int ldo) {
+    constexpr int TJ = GM == 64 ? 2 : 1, XC = GM * 8 / 256; // MFMA tiles per wave, X chunks of 16 B per thread
     __shared__ __align__(16) int8_t xl[GM * GROW];
     __shared__ __align__(16) int8_t wl[GN * GROW];
     __shared__ __align__(16) float xsl[4][GM];
     __shared__ float wsl[GN][4];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int m0 = blockIdx.y * GM, n0 = blockIdx.x * GN, G = K >> 5;
-    const int wm = (wave >> 1) * 32, wn = (wave & 1) * 64; // the wave's sub-tile
-    float acc[2][16];
+    const int wm = GM == 64 ? (wave >> 1) * 32 : 0, wn = GM == 64 ? (wave & 1) * 64 : wave * 32; // the wave's sub-tile
+    float acc[TJ][16];
     #pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int j = 0; j < TJ; j++)
         #pragma unroll
         for (int r = 0; r < 16; r++) acc[j][r] = 0.0f;
     for (int k0 = 0; k0 < K; k0 += GKB) {
         const int ng = (K - k0) < GKB ? (K - k0) >> 5 : 4; // groups in this stage
-        // stage: X rows m0.. (GM x 128 B: 512 chunks of 16 B, 2 per thread), W rows n0.. (GN x 128 B: 4 per thread)
-        uint4 xr[2], wr[4];
+        // stage: X rows m0.. (GM x 128 B: XC chunks of 16 B per thread), W rows n0.. (GN x 128 B: 4 per thread)
+        uint4 xr[XC], wr[4];
         #pragma unroll
-        for (int k = 0; k < 2; k++) {
+        for (int k = 0; k < XC; k++) {
             int c = t + 256 * k, row = c >> 3, col = (c & 7) * 16, m = m0 + row < M ? m0 + row : M - 1;
             xr[k] = col < ng * 32 ? *(const uint4 *)(X + (size_t)m * ldx + k0 + col) : make_uint4(0, 0, 0, 0);
         }
@@ -113,7 +115,7 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const int8_t *__restrict__ W, c
         }
         __syncthreads(); // (the previous stage's readers are done)
         #pragma unroll
-        for (int k = 0; k < 2; k++) {
+        for (int k = 0; k < XC; k++) {
             int c = t + 256 * k;
             *(uint4 *)(xl + (c >> 3) * GROW + (c & 7) * 16) = xr[k];
         }
@@ -132,7 +134,7 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const int8_t *__restrict__ W, c
         for (int gg = 0; gg < ng; gg++) {
             i32x4 a = *(const i32x4 *)(xl + (wm + (lane & 31)) * GROW + gg * 32 + 16 * (lane >> 5));
             #pragma unroll
-            for (int j = 0; j < 2; j++) {
+            for (int j = 0; j < TJ; j++) {
                 i32x4 b = *(const i32x4 *)(wl + (wn + 32 * j + (lane & 31)) * GROW + gg * 32 + 16 * (lane >> 5));
                 i32x16 z = { 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0 };
                 i32x16 I = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
@@ -152,7 +154,7 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const int8_t *__restrict__ W, c
         }
     }
     #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < TJ; j++) {
         int n = n0 + wn + 32 * j + (lane & 31);
         #pragma unroll
         for (int r = 0; r < 16; r++) {
@@ -342,11 +344,21 @@ void gw_take_launch_events(hipEvent_t *a, hipEvent_t *b) {
 
 int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int M, float *out, int ldo, int mode, hipStream_t s) {
     if (w->type == GW_Q8_0 && M > GW_GEMV_MAX_ROWS && mode == 0) {
-        dim3 grid((w->rows + GN - 1) / GN, (M + GM - 1) / GM);
         hipEvent_t e0, e1;
         gw_take_launch_events(&e0, &e1);
-        hipExtLaunchKernelGGL(k_gemm_q8, grid, dim3(256), 0, s, e0, e1, 0, (const int8_t *)w->codes, (const uint16_t *)w->scales,
-                              w->rows, w->cols, xq, xs, ldx, M, out, ldo);
+        static int cus = 0;
+        if (!cus) {
+            int dev = 0;
+            if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+                cus = 256;
+        }
+        int nt = (w->rows + GN - 1) / GN;
+        if ((size_t)nt * ((M + 63) / 64) >= (size_t)4 * cus) // enough 64-row tiles for several waves per SIMD
+            hipExtLaunchKernelGGL(k_gemm_q8<64>, dim3(nt, (M + 63) / 64), dim3(256), 0, s, e0, e1, 0, (const int8_t *)w->codes,
+                                  (const uint16_t *)w->scales, w->rows, w->cols, xq, xs, ldx, M, out, ldo);
+        else
+            hipExtLaunchKernelGGL(k_gemm_q8<32>, dim3(nt, (M + 31) / 32), dim3(256), 0, s, e0, e1, 0, (const int8_t *)w->codes,
+                                  (const uint16_t *)w->scales, w->rows, w->cols, xq, xs, ldx, M, out, ldo);
         return (int)hipGetLastError();
     }
     if (w->type == GW_Q8_0)
