@@ -59,6 +59,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--probe", action="store_true")
+    ap.add_argument("--workload", default="step", choices=["step", "batch32_4b", "long_8b"],
+                    help="step: the metric's workload (default); batch32_4b / long_8b: the batched decode of the "
+                         "reference's configs 3 / 4, a JSON line of their own")
     ap.add_argument("--workdir", default=os.environ.get("GW_BENCH_DIR", "/dev/shm/gwenedeg_bench" if os.path.isdir("/dev/shm")
                                                                       else "/tmp/gwenedeg_bench"))
     a = ap.parse_args()
@@ -71,6 +74,9 @@ def main():
     from gwenedeg_amd import synth
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if a.workload != "step":
+        batched(torch, gw, synth, a)
+        return
     os.makedirs(a.workdir, exist_ok=True)
     path = a.model or os.path.join(a.workdir, f"{a.shape}_seed{a.seed}.gguf")
     if not os.path.exists(path):
@@ -189,6 +195,75 @@ def main():
             cb["greedy_tokens_identical"] = ref_toks == toks[:len(ref_toks)]
         out["cpu_baseline"] = cb
     print(json.dumps(out), flush=True)
+
+
+BATCHED = {  # the reference's configs 3 and 4: shape, sequences, cached positions per sequence, timed decode steps
+    "batch32_4b": ("qwen3_4b_q4km", 32, 2048, 16),
+    "long_8b": ("qwen3_8b", 8, 32768, 8),
+}
+
+
+def batched(torch, gw, synth, a):
+    """Batched greedy decode: nseq sequences with `ctx` cached positions each (rq_seq_fill_synthetic: the K / V of a
+    prefix, whose cost does not depend on the values, runq.h:721-726), then decode passes of one row per sequence
+    (gw_forward_batch_device + gw_ctx_argmax: rq_forward_batch with the greedy choice on the device). value = rows per
+    second; the HBM bytes of a step = the weights' file bytes + the K / V bytes the attention reads"""
+    shape, nseq, ctx, steps = BATCHED[a.workload]
+    steps = a.steps if a.steps != 3 else steps
+    os.makedirs(a.workdir, exist_ok=True)
+    path = os.path.join(a.workdir, f"{shape}_seed{a.seed}.gguf")
+    if not os.path.exists(path):
+        synth.write_gguf(path, shape, seed=a.seed)
+    cap = ctx + steps + a.warmup + 16
+    m = gw.Model(path, ctx_len=cap)
+    c = m.ctx(max_batch=max(nseq, 2), max_ctx=cap)
+    seqs = [m.seq(cap) for _ in range(nseq)]
+    for i, sq in enumerate(seqs):
+        sq.fill_synthetic(ctx, seed=a.seed + i)
+    toks = [int(t) for t in np.random.default_rng(a.seed).integers(0, m.vocab, nseq)]
+
+    def one():
+        nonlocal toks
+        toks = [int(t) for t in c.forward_batch_argmax([gw.Segment(sq, [t], gw.RQ_LOGITS_LAST) for sq, t in zip(seqs, toks)])]
+
+    for _ in range(a.warmup):
+        one()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        one()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    c.kernel_timing(True)
+    one()
+    kt = c.kernel_times(multi=True)
+    c.kernel_timing(False)
+    info = m.info
+    kv_pos = info.n_layers * info.n_kv_heads * info.head_dim * 2 * 2  # f16 K and V bytes per position
+    mean_ctx = ctx + a.warmup + steps + 0.5
+    kv_bytes = nseq * mean_ctx * kv_pos
+    w_bytes = weight_file_bytes(path)
+    step_s = el / steps
+    att_s = kt.get("attention", (0, 0))[0]
+    out = {
+        "metric": f"batched greedy decode rows/s ({a.workload}: the reference's config {3 if nseq == 32 else 4}, 1 GPU)",
+        "value": round(nseq * steps / el, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": a.warmup,
+        "ms_per_step": round(1e3 * step_s, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 x int8 -> int32, fp32 fold; f16 KV", "data": "synthetic weights; K / V of the prefixes by rq_seq_fill_synthetic",
+        "config": {"workload": f"{shape}: {nseq} sequences x {ctx} cached positions, one row per sequence per step",
+                   "global_batch": nseq, "seq_len": ctx},
+        "hbm_bytes_per_step": {"weights": w_bytes, "kv_read": kv_bytes},
+        "achieved_gbs": round((w_bytes + kv_bytes) / step_s / 1e9, 1),
+        "attention": {"kernel_ms_per_step": round(att_s * 1e3, 3),
+                      "kv_gbs": round(kv_bytes / att_s / 1e9, 1) if att_s else None},
+        "kernel_ms_per_step": {k: round(v[0] * 1e3, 3) for k, v in kt.items() if v[1]},
+    }
+    print(json.dumps(out), flush=True)
+
+
+def weight_file_bytes(path):
+    """the file bytes of the GGUF's matrices (everything but the header and the f32 norms: the tensors data section)"""
+    return float(os.path.getsize(path))
 
 
 def traffic_per_launch():

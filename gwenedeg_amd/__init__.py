@@ -117,6 +117,7 @@ _sig = {
     "gw_ctx_stream": (_P, [_P]),
     "gw_decode_argmax": (_I, [_P, _P, _I, ctypes.POINTER(_I)]),
     "gw_decode_greedy": (_I, [_P, _P, _I, _I, ctypes.POINTER(_I)]),
+    "gw_forward_batch_device": (_I, [_P, ctypes.POINTER(RqSegment), _I]),
     "gw_ctx_profile_enable": (_I, [_P, _I]),
     "gw_ctx_gemv_sweep": (_I, [_P, _I, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),
     "gw_ctx_profile_launches": (ctypes.c_long, [_P, _I]),
@@ -301,6 +302,20 @@ class Ctx:
         p = ctypes.POINTER(ctypes.c_float)()
         self._check(lib.rq_forward_batch(self._h, arr, n, _fptr(out), ctypes.byref(p)), "rq_forward_batch")
         return (out[:nsel] if nsel else None), hids
+
+    def forward_batch_argmax(self, segments: Sequence[Segment]) -> np.ndarray:
+        """gw_forward_batch_device + gw_ctx_argmax: the greedy token of every selected row, chosen on the device"""
+        n = len(segments)
+        arr = (RqSegment * n)()
+        keep = []
+        nsel = 0
+        for i, sg in enumerate(segments):
+            t = np.ascontiguousarray(sg.tokens, dtype=np.int32)
+            keep.append(t)
+            arr[i] = RqSegment(sg.seq._h, _iptr(t), len(t), sg.logits, None, None)
+            nsel += len(t) if sg.logits == RQ_LOGITS_ALL else (1 if sg.logits == RQ_LOGITS_LAST else 0)
+        self._check(lib.gw_forward_batch_device(self._h, arr, n), "gw_forward_batch_device")
+        return self.argmax(nsel) if nsel else np.zeros(0, np.int32)
 
     def decode_argmax(self, seq: Seq, token: int) -> int:
         """gw_decode_argmax: a decode step whose greedy next token is chosen on the device"""

@@ -517,7 +517,7 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
     c->kt_multi = n > 1;
     pf_mark(c, GW_PF_EMBED);
     if (m->embd.type == GW_Q8_0) KCHK(gw_k_embed_q8(c->x, dim, (const uint8_t *)m->embd.codes, m->embd.scales, tok_d, n, s));
-    else KCHK(gw_k_embed_kq(c->x, dim, m->embd.type, m->embd.blocks, tok_d, n, s));
+    else KCHK(gw_k_embed_kq(c->x, dim, m->embd.type, m->embd.blocks, m->embd.bstride, tok_d, n, s));
     /* one row of an all-Q8_0 model: the fused decode sequence (gw_gemv.hip: each matmul computes its activation from
      * the producer's fp32 output; the residual adds go straight into x) */
     int fused = n == 1 && fused_shape(m), fused_att = fused && (hd == 128 || hd == 64 || hd == 32);
@@ -749,9 +749,9 @@ int rq_decode_hidden(RqCtx *c, RqSeq *s, int token, float **logits, float *hidde
     return e;
 }
 
-int rq_forward_batch(RqCtx *c, const RqSegment *sg, int nseg, float *out, float **logits) {
+static int fw_batch(RqCtx *c, const RqSegment *sg, int nseg, float *out, float **logits, int on_device) {
     /* forward.c:3762-3878's contract: validation first, rows in segment order, selected rows' logits to out in row
-     * order (one selected row and out NULL: the context's buffer) */
+     * order (one selected row and out NULL: the context's buffer); on_device: the logits rows stay on the device */
     static Pass P;
     const RqModel *m = c->m;
     int n = 0, nsel = 0, any_all = 0;
@@ -779,8 +779,9 @@ int rq_forward_batch(RqCtx *c, const RqSegment *sg, int nseg, float *out, float 
         any_all |= sg[i].logits == RQ_LOGITS_ALL;
     }
     int gemv = nsel == 1 && !any_all && !out;
-    if (nsel > 0 && !out && !gemv) return ctx_fail(c, RQ_ERR_ARG, "logits of %d rows need an output buffer", nsel);
+    if (nsel > 0 && !out && !gemv && !on_device) return ctx_fail(c, RQ_ERR_ARG, "logits of %d rows need an output buffer", nsel);
     if (gemv) out = c->logits;
+    if (on_device) out = NULL;
     P.n = n;
     P.nsel = 0;
     P.want_hidden = 0;
@@ -802,6 +803,16 @@ int rq_forward_batch(RqCtx *c, const RqSegment *sg, int nseg, float *out, float 
     }
     if (logits) *logits = nsel ? out : NULL;
     return RQ_OK;
+}
+
+int rq_forward_batch(RqCtx *c, const RqSegment *sg, int nseg, float *out, float **logits) {
+    return fw_batch(c, sg, nseg, out, logits, 0);
+}
+
+int gw_forward_batch_device(RqCtx *c, const RqSegment *sg, int nseg) {
+    /* rq_forward_batch with the selected rows' logits left on the device (gw_ctx_argmax chooses their greedy tokens):
+     * the batched decode step of a serving loop without the vocab-size copy per row */
+    return fw_batch(c, sg, nseg, NULL, NULL, 1);
 }
 
 int rq_prefill(RqCtx *c, RqSeq *s, const int *tokens, int n, int mode, float *out, float **logits) {

@@ -166,77 +166,154 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const int8_t *__restrict__ W, c
 
 // --------------------------------------------------------------------------------------------- K-quants
 
-// the per-group term of the K-quant fold (kquants.h:86-109) for weight row `row` (its blocks at rb) and group g:
-//   Q4_K: a - b, a = (ds * xs) * (float) isum, b = dm * xf, ds = d * sc_j, dm = dmin * m_j (sub-block j = g % 8)
-//   Q6_K: (d * xs) * (float) I, I = sc_j0 * t_j0 + sc_j1 * t_j1, t_j = sum q * xq - 32 * sum xq over 16 values
-template <int TYPE>
-__device__ __forceinline__ float kq_term(const uint8_t *__restrict__ rb, int g, const int8_t *__restrict__ x, float xsg, float xfg) {
-    int s = g >> 3, j = g & 7;
-    if (TYPE == GW_Q4_K) {
-        const uint8_t *b = rb + (size_t)s * 144;
-        const uint8_t *sc = b + 4;
-        int scj, mj;
-        if (j < 4) {
-            scj = sc[j] & 63;
-            mj = sc[j + 4] & 63;
-        } else {
-            scj = (sc[j + 4] & 15) | (sc[j - 4] >> 6) << 4;
-            mj = (sc[j + 4] >> 4) | (sc[j] >> 6) << 4;
-        }
-        const uint8_t *qs = b + 16 + 32 * (j >> 1);
-        int sh = 4 * (j & 1), isum = 0;
-        #pragma unroll
-        for (int l = 0; l < 32; l++) isum += ((qs[l] >> sh) & 15) * (int)x[l];
-        float d = __half2float(__ushort_as_half((uint16_t)(b[0] | b[1] << 8)));
-        float dmin = __half2float(__ushort_as_half((uint16_t)(b[2] | b[3] << 8)));
-        float ds = d * (float)scj, dm = dmin * (float)mj;
-        float a = (ds * xsg) * (float)isum;
-        float bb = dm * xfg;
-        return a - bb;
-    } else {
-        const uint8_t *b = rb + (size_t)s * 210;
-        int n = j >> 2, p = j & 3, I = 0;
-        #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            int t = 0, xsum = 0;
-            #pragma unroll
-            for (int l0 = 0; l0 < 16; l0++) {
-                int l = 16 * h + l0;
-                int lo = (b[64 * n + 32 * (p & 1) + l] >> (4 * (p >> 1))) & 15;
-                int hi = (b[128 + 32 * n + l] >> (2 * p)) & 3;
-                t += (lo | hi << 4) * (int)x[l];
-                xsum += x[l];
-            }
-            I += (int)(int8_t)b[192 + 2 * j + h] * (t - 32 * xsum);
-        }
-        float d = __half2float(__ushort_as_half((uint16_t)(b[208] | b[209] << 8)));
-        return (d * xsg) * (float)I;
-    }
-}
-
-// out[m * ldo + row] = W row . X row m for the K-quant blocks (row-major: K / 256 blocks per row), R rows per block:
-// each thread takes groups g = t, t + 256, ... of every row, its term into LDS; one lane per (m, row) folds in order
-template <int TYPE, int M, int R>
-__global__ __launch_bounds__(256) void k_gemv_kq(const uint8_t *__restrict__ W, int nrows, int K, const int8_t *__restrict__ xq,
-                                                 const float *__restrict__ xs, int ldx, float *out, int ldo, int mode) {
+// The batched GEMV of all three formats: out[m * ldo + row] (+)= W row . X row m for M <= 8 activation rows, R weight
+// rows per block. Each thread takes half-groups (16 weights) j = t, t + 256, ..., U per pass, with every load of the
+// pass issued before the first dot; the 16 weights become 16 int8 codes in four 32-bit words, the exact int32 sums by
+// 4 v_dot4 per (row, activation row), and the group's term (the even lane of the pair) goes into LDS:
+//   Q8_0 (codes row-major, fp16 scales): (ws * xs) * (float) isum                                   (forward.c:906-916)
+//   Q4_K (144-byte super-blocks of 256: d, dmin, 12 bytes of 6-bit scales / mins, 128 of nibbles):
+//     a - b, a = ((d * sc_j) * xs) * (float) isum, b = (dmin * m_j) * (xs * (float) sum x)            (kquants.h:86-109)
+//   Q6_K (224-byte super-blocks: the file's 210 bytes, 16-byte aligned: ql 128, qh 64, 16 int8 scales, fp16 d):
+//     (d * xs) * (float) (sc_0 (sum q x - 32 sum x) + sc_1 (...)), over the group's two halves of 16
+// then one lane per (activation row, weight row) folds the groups in order: val = val + term. mode 1: out = out + val.
+// K % 32 == 0 (Q8_0), % 256 (K-quants); the K-quants' q are 0 .. 15 / 0 .. 63, so v_dot4 with signed codes is exact
+template <int TYPE, int M, int R, int U>
+__global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, const uint16_t *__restrict__ WS, int nrows,
+                                                 int K, int bstride, const int8_t *__restrict__ xq, const float *__restrict__ xs,
+                                                 int ldx, float *out, int ldo, int mode) {
     extern __shared__ float P[];
-    const int G = K >> 5, PS = G + 1, row0 = blockIdx.x * R, t = threadIdx.x;
-    const size_t rowb = (size_t)(K / 256) * (TYPE == GW_Q4_K ? 144 : 210);
-    for (int g = t; g < G; g += 256) {
+    const int G = K >> 5, H = K >> 4, PS = (G + 7) & ~3; // (rows 16-byte aligned)
+    const int row0 = blockIdx.x * R, t = threadIdx.x;
+    const size_t rowb = TYPE == GW_Q8_0 ? (size_t)K : (size_t)(K >> 8) * bstride;
+    for (int j0 = 0; j0 < H; j0 += 256 * U) {
+        // the pass's loads (past the row's end: its last half-group again, unconditionally; only the stores below are
+        // predicated, so no load waits for a branch)
+        int4 wv[U][R];
+        float f0[U][R], f1[U][R]; // Q8_0: ws; Q4_K: d sc_j, dmin m_j; Q6_K: d
+        int isc[U][R];            // Q6_K: the half-group's int8 scale
         #pragma unroll
-        for (int m = 0; m < M; m++) {
-            const int8_t *x = xq + (size_t)m * ldx + 32 * g;
-            float xsg = xs[(size_t)m * (ldx >> 5) + g], xfg = 0.0f;
-            if (TYPE == GW_Q4_K) {
-                int sum = 0;
-                #pragma unroll
-                for (int l = 0; l < 32; l++) sum += x[l];
-                xfg = xsg * (float)sum; // kq_act_prep (kquants.h:392-400)
-            }
+        for (int u = 0; u < U; u++) {
+            const int j = j0 + 256 * u + t < H ? j0 + 256 * u + t : H - 1;
             #pragma unroll
             for (int r = 0; r < R; r++) {
-                int row = row0 + r < nrows ? row0 + r : nrows - 1;
-                P[(m * R + r) * PS + g] = kq_term<TYPE>(W + (size_t)row * rowb, g, x, xsg, xfg);
+                const int row = row0 + r < nrows ? row0 + r : nrows - 1;
+                const uint8_t *rb = W + (size_t)row * rowb;
+                if (TYPE == GW_Q8_0) {
+                    wv[u][r] = *(const int4 *)(rb + 16 * j);
+                } else {
+                    const int sblk = j >> 4, sb = (j >> 1) & 7, h = j & 1;
+                    const uint8_t *b = rb + (size_t)sblk * bstride;
+                    if (TYPE == GW_Q4_K) { // (sub-block sb: the low nibbles of its byte pair's run for even sb, high for odd)
+                        const int4 q = *(const int4 *)(b + 16 + 32 * (sb >> 1) + 16 * h);
+                        const int sl = 4 * (sb & 1);
+                        wv[u][r].x = (int)(((uint32_t)q.x >> sl) & 0x0F0F0F0Fu);
+                        wv[u][r].y = (int)(((uint32_t)q.y >> sl) & 0x0F0F0F0Fu);
+                        wv[u][r].z = (int)(((uint32_t)q.z >> sl) & 0x0F0F0F0Fu);
+                        wv[u][r].w = (int)(((uint32_t)q.w >> sl) & 0x0F0F0F0Fu);
+                    } else {
+                        const int n = sb >> 2, p = sb & 3;
+                        int4 lo = *(const int4 *)(b + 64 * n + 32 * (p & 1) + 16 * h);
+                        int4 hi = *(const int4 *)(b + 128 + 32 * n + 16 * h);
+                        const int sl = 4 * (p >> 1), sh = 2 * p;
+                        wv[u][r].x = (int)((((uint32_t)lo.x >> sl) & 0x0F0F0F0Fu) | ((((uint32_t)hi.x >> sh) & 0x03030303u) << 4));
+                        wv[u][r].y = (int)((((uint32_t)lo.y >> sl) & 0x0F0F0F0Fu) | ((((uint32_t)hi.y >> sh) & 0x03030303u) << 4));
+                        wv[u][r].z = (int)((((uint32_t)lo.z >> sl) & 0x0F0F0F0Fu) | ((((uint32_t)hi.z >> sh) & 0x03030303u) << 4));
+                        wv[u][r].w = (int)((((uint32_t)lo.w >> sl) & 0x0F0F0F0Fu) | ((((uint32_t)hi.w >> sh) & 0x03030303u) << 4));
+                    }
+                }
+            }
+        }
+        #pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int j = j0 + 256 * u + t < H ? j0 + 256 * u + t : H - 1;
+            #pragma unroll
+            for (int r = 0; r < R; r++) {
+                const int row = row0 + r < nrows ? row0 + r : nrows - 1;
+                const uint8_t *rb = W + (size_t)row * rowb;
+                if (TYPE == GW_Q8_0) {
+                    f0[u][r] = h2f_g(WS[(size_t)row * G + (j >> 1)]);
+                    f1[u][r] = 0.0f;
+                    isc[u][r] = 0;
+                } else if (TYPE == GW_Q4_K) {
+                    const int sblk = j >> 4, sb = (j >> 1) & 7;
+                    const uint8_t *b = rb + (size_t)sblk * bstride;
+                    const uint4 hd = *(const uint4 *)b; // d, dmin, then scale bytes 0 .. 11 in words y, z, w
+                    auto scb = [&](int k) -> int { // (k < 12)
+                        uint32_t w = k < 4 ? hd.y : k < 8 ? hd.z : hd.w;
+                        return (int)((w >> (8 * (k & 3))) & 0xffu);
+                    };
+                    int scj, mj;
+                    if (sb < 4) {
+                        scj = scb(sb) & 63;
+                        mj = scb(sb + 4) & 63;
+                    } else {
+                        scj = (scb(sb + 4) & 15) | (scb(sb - 4) >> 6) << 4;
+                        mj = (scb(sb + 4) >> 4) | (scb(sb) >> 6) << 4;
+                    }
+                    f0[u][r] = h2f_g((uint16_t)(hd.x & 0xffffu)) * (float)scj;
+                    f1[u][r] = h2f_g((uint16_t)(hd.x >> 16)) * (float)mj;
+                    isc[u][r] = 0;
+                } else {
+                    const int sblk = j >> 4, sb = (j >> 1) & 7, h = j & 1;
+                    const uint8_t *b = rb + (size_t)sblk * bstride;
+                    const uint4 sw = *(const uint4 *)(b + 192); // the 16 int8 scales
+                    const int k = 2 * sb + h;
+                    uint32_t w = k < 4 ? sw.x : k < 8 ? sw.y : k < 12 ? sw.z : sw.w;
+                    isc[u][r] = (int)(int8_t)((w >> (8 * (k & 3))) & 0xffu);
+                    f0[u][r] = h2f_g((uint16_t)(*(const uint4 *)(b + 208)).x);
+                    f1[u][r] = 0.0f;
+                }
+            }
+        }
+        int4 xv[U][M];
+        float xsg[U][M];
+        #pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int j = j0 + 256 * u + t < H ? j0 + 256 * u + t : H - 1;
+            #pragma unroll
+            for (int m = 0; m < M; m++) {
+                xv[u][m] = *(const int4 *)(xq + (size_t)m * ldx + 16 * j);
+                xsg[u][m] = xs[(size_t)m * (ldx >> 5) + (j >> 1)];
+            }
+        }
+        #pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int j = j0 + 256 * u + t;
+            if (j < H) { // (whole lane pairs: H is even)
+                #pragma unroll
+                for (int m = 0; m < M; m++) {
+                    int xsum = 0; // K-quants: the sum of the half-group's activation codes
+                    if (TYPE != GW_Q8_0) {
+                        xsum = __builtin_amdgcn_sdot4(xv[u][m].x, 0x01010101, 0, false);
+                        xsum = __builtin_amdgcn_sdot4(xv[u][m].y, 0x01010101, xsum, false);
+                        xsum = __builtin_amdgcn_sdot4(xv[u][m].z, 0x01010101, xsum, false);
+                        xsum = __builtin_amdgcn_sdot4(xv[u][m].w, 0x01010101, xsum, false);
+                    }
+                    const int xsum2 = TYPE == GW_Q4_K ? xsum + __shfl_xor(xsum, 1) : 0;
+                    #pragma unroll
+                    for (int r = 0; r < R; r++) {
+                        int sd = __builtin_amdgcn_sdot4(wv[u][r].x, xv[u][m].x, 0, false);
+                        sd = __builtin_amdgcn_sdot4(wv[u][r].y, xv[u][m].y, sd, false);
+                        sd = __builtin_amdgcn_sdot4(wv[u][r].z, xv[u][m].z, sd, false);
+                        sd = __builtin_amdgcn_sdot4(wv[u][r].w, xv[u][m].w, sd, false);
+                        float term;
+                        if (TYPE == GW_Q8_0) {
+                            int is = sd + __shfl_xor(sd, 1);
+                            float sc = f0[u][r] * xsg[u][m];
+                            term = sc * (float)is;
+                        } else if (TYPE == GW_Q4_K) {
+                            int is = sd + __shfl_xor(sd, 1);
+                            float a = (f0[u][r] * xsg[u][m]) * (float)is;
+                            float bb = f1[u][r] * (xsg[u][m] * (float)xsum2);
+                            term = a - bb;
+                        } else {
+                            int I = isc[u][r] * (sd - 32 * xsum);
+                            I = I + __shfl_xor(I, 1);
+                            term = (f0[u][r] * xsg[u][m]) * (float)I;
+                        }
+                        if (!(j & 1)) P[(m * R + r) * PS + (j >> 1)] = term;
+                    }
+                }
             }
         }
     }
@@ -246,7 +323,41 @@ __global__ __launch_bounds__(256) void k_gemv_kq(const uint8_t *__restrict__ W, 
         if (row < nrows) {
             const float *p = P + t * PS;
             float v = 0.0f;
-            for (int g = 0; g < G; g++) v = v + p[g];
+            int g = 0;
+            if (G >= 32) {
+                float4 a[8], b[8];
+                #pragma unroll
+                for (int u = 0; u < 8; u++) a[u] = *(const float4 *)(p + 4 * u);
+                for (g = 32; g + 64 <= G; g += 64) {
+                    #pragma unroll
+                    for (int u = 0; u < 8; u++) b[u] = *(const float4 *)(p + g + 4 * u);
+                    #pragma unroll
+                    for (int u = 0; u < 8; u++) {
+                        v = v + a[u].x;
+                        v = v + a[u].y;
+                        v = v + a[u].z;
+                        v = v + a[u].w;
+                    }
+                    #pragma unroll
+                    for (int u = 0; u < 8; u++) a[u] = *(const float4 *)(p + g + 32 + 4 * u);
+                    #pragma unroll
+                    for (int u = 0; u < 8; u++) {
+                        v = v + b[u].x;
+                        v = v + b[u].y;
+                        v = v + b[u].z;
+                        v = v + b[u].w;
+                    }
+                }
+                // (a holds groups g - 32 .. g - 1)
+                #pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    v = v + a[u].x;
+                    v = v + a[u].y;
+                    v = v + a[u].z;
+                    v = v + a[u].w;
+                }
+            }
+            for (; g < G; g++) v = v + p[g];
             float *o = out + (size_t)m * ldo + row;
             *o = mode == 1 ? *o + v : v;
         }
@@ -256,15 +367,15 @@ __global__ __launch_bounds__(256) void k_gemv_kq(const uint8_t *__restrict__ W, 
 // x[b] = row tok[b] of a K-quant table, dequantized (kq_dequant_row, kquants.h:222-251; every value one rounding
 // of an exact expression)
 __global__ __launch_bounds__(256) void k_embed_kq(float *__restrict__ x, int dim, int type, const uint8_t *__restrict__ W,
-                                                  const int *__restrict__ tok) {
+                                                  int bstride, const int *__restrict__ tok) {
     int bidx = blockIdx.x;
-    size_t rowb = (size_t)(dim / 256) * (type == GW_Q4_K ? 144 : 210);
+    size_t rowb = (size_t)(dim / 256) * bstride;
     const uint8_t *rb = W + (size_t)tok[bidx] * rowb;
     for (int i = threadIdx.x; i < dim; i += blockDim.x) {
         int s = i >> 8, k = i & 255;
         float y;
         if (type == GW_Q4_K) {
-            const uint8_t *b = rb + (size_t)s * 144, *sc = b + 4;
+            const uint8_t *b = rb + (size_t)s * bstride, *sc = b + 4;
             int j = k >> 5, scj, mj;
             if (j < 4) { scj = sc[j] & 63; mj = sc[j + 4] & 63; }
             else { scj = (sc[j + 4] & 15) | (sc[j - 4] >> 6) << 4; mj = (sc[j + 4] >> 4) | (sc[j] >> 6) << 4; }
@@ -274,7 +385,7 @@ __global__ __launch_bounds__(256) void k_embed_kq(float *__restrict__ x, int dim
             float d1 = d * (float)scj, m1 = dmin * (float)mj;
             y = d1 * (float)q - m1;
         } else {
-            const uint8_t *b = rb + (size_t)s * 210;
+            const uint8_t *b = rb + (size_t)s * bstride;
             int n = k / 128, p = k / 32 % 4, l = k % 32;
             int q = ((b[64 * n + 32 * (p & 1) + l] >> (4 * (p >> 1))) & 15) | ((b[128 + 32 * n + l] >> (2 * p)) & 3) << 4;
             float d = __half2float(__ushort_as_half((uint16_t)(b[208] | b[209] << 8)));
@@ -285,35 +396,65 @@ __global__ __launch_bounds__(256) void k_embed_kq(float *__restrict__ x, int dim
 }
 
 template <int TYPE>
-static int launch_gemv_kq(const uint8_t *W, int nrows, int K, const int8_t *xq, const float *xs, int ldx, int M, float *out,
-                          int ldo, int mode, hipStream_t s) {
-    const int R = 4;
-    size_t lds = (size_t)4 * R * (K / 32 + 1) * sizeof(float);
+static int launch_gemv_mr(const uint8_t *W, const uint16_t *WS, int nrows, int K, int bstride, const int8_t *xq, const float *xs,
+                          int ldx, int M, float *out, int ldo, int mode, hipStream_t s) {
+    // launches of up to 8 activation rows; U = the half-groups per thread and pass (all loads of a row of K <= 16384
+    // issued at once)
+    const int R = 4, H = K / 16;
+    int U = (H + 255) / 256;
+    U = U < 1 ? 1 : U > 4 ? 4 : U;
     hipEvent_t t0, t1; // (timing: the first launch's start, the last one's stop)
     gw_take_launch_events(&t0, &t1);
-    for (int m0 = 0; m0 < M; m0 += 4) {
-        int mm = M - m0 < 4 ? M - m0 : 4;
-        hipEvent_t e0 = m0 == 0 ? t0 : NULL, e1 = m0 + 4 >= M ? t1 : NULL;
-        dim3 grid((nrows + R - 1) / R);
+    dim3 grid((nrows + R - 1) / R);
+    for (int m0 = 0; m0 < M; m0 += 8) {
+        const int mm = M - m0 < 8 ? M - m0 : 8;
+        hipEvent_t e0 = m0 == 0 ? t0 : NULL, e1 = m0 + 8 >= M ? t1 : NULL;
+        const uint32_t lds = (uint32_t)((size_t)mm * R * ((K / 32 + 7) & ~3) * sizeof(float));
         const int8_t *x = xq + (size_t)m0 * ldx;
         const float *xsc = xs + (size_t)m0 * (ldx / 32);
         float *o = out + (size_t)m0 * ldo;
+#define MR_L(MM, UU) hipExtLaunchKernelGGL((k_gemv_mr<TYPE, MM, R, UU>), grid, dim3(256), lds, s, e0, e1, 0, W, WS, nrows, K, bstride, x, xsc, ldx, o, ldo, mode)
+#define MR_U(MM)                                                                                                        \
+    switch (U) {                                                                                                        \
+    case 1: MR_L(MM, 1); break;                                                                                         \
+    case 2: MR_L(MM, 2); break;                                                                                         \
+    case 3: MR_L(MM, 3); break;                                                                                         \
+    default: MR_L(MM, 4); break;                                                                                        \
+    }
         switch (mm) {
-        case 1: hipExtLaunchKernelGGL((k_gemv_kq<TYPE, 1, R>), grid, dim3(256), lds, s, e0, e1, 0, W, nrows, K, x, xsc, ldx, o, ldo, mode); break;
-        case 2: hipExtLaunchKernelGGL((k_gemv_kq<TYPE, 2, R>), grid, dim3(256), lds, s, e0, e1, 0, W, nrows, K, x, xsc, ldx, o, ldo, mode); break;
-        case 3: hipExtLaunchKernelGGL((k_gemv_kq<TYPE, 3, R>), grid, dim3(256), lds, s, e0, e1, 0, W, nrows, K, x, xsc, ldx, o, ldo, mode); break;
-        default: hipExtLaunchKernelGGL((k_gemv_kq<TYPE, 4, R>), grid, dim3(256), lds, s, e0, e1, 0, W, nrows, K, x, xsc, ldx, o, ldo, mode); break;
+        case 1: MR_U(1); break;
+        case 2: MR_U(2); break;
+        case 3: MR_U(3); break;
+        case 4: MR_U(4); break;
+        case 5: MR_U(5); break;
+        case 6: MR_U(6); break;
+        case 7: MR_U(7); break;
+        default: MR_U(8); break;
         }
+#undef MR_U
+#undef MR_L
     }
     return (int)hipGetLastError();
 }
 
+// dst super-block i (GW_Q6K_DEV bytes) = src super-block i (GW_Q6K_BYTES) and zero padding
+__global__ __launch_bounds__(256) void k_q6k_pad(const uint8_t *__restrict__ src, size_t nblk, uint8_t *__restrict__ dst) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, b = i / GW_Q6K_DEV, k = i % GW_Q6K_DEV;
+    if (b < nblk) dst[i] = k < GW_Q6K_BYTES ? src[b * GW_Q6K_BYTES + k] : 0;
+}
+
 extern "C" {
 
-int gw_k_embed_kq(float *x, int dim, int type, const uint8_t *blocks, const int *tok, int n, hipStream_t s) {
+int gw_k_q6k_pad(const uint8_t *src, size_t nblk, uint8_t *dst, hipStream_t s) {
+    size_t n = nblk * GW_Q6K_DEV;
+    hipLaunchKernelGGL(k_q6k_pad, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, nblk, dst);
+    return (int)hipGetLastError();
+}
+
+int gw_k_embed_kq(float *x, int dim, int type, const uint8_t *blocks, int bstride, const int *tok, int n, hipStream_t s) {
     hipEvent_t e0, e1;
     gw_take_launch_events(&e0, &e1);
-    hipExtLaunchKernelGGL(k_embed_kq, dim3(n), dim3(256), 0, s, e0, e1, 0, x, dim, type, blocks, tok);
+    hipExtLaunchKernelGGL(k_embed_kq, dim3(n), dim3(256), 0, s, e0, e1, 0, x, dim, type, blocks, bstride, tok);
     return (int)hipGetLastError();
 }
 
@@ -362,11 +503,11 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
         return (int)hipGetLastError();
     }
     if (w->type == GW_Q8_0)
-        return gw_k_gemv_q8(w->codes, w->scales, w->rows, w->cols, xq, xs, ldx, M, out, ldo, mode, s);
+        return launch_gemv_mr<GW_Q8_0>((const uint8_t *)w->codes, w->scales, w->rows, w->cols, 0, xq, xs, ldx, M, out, ldo, mode, s);
     if (w->type == GW_Q4_K)
-        return launch_gemv_kq<GW_Q4_K>(w->blocks, w->rows, w->cols, xq, xs, ldx, M, out, ldo, mode, s);
+        return launch_gemv_mr<GW_Q4_K>(w->blocks, NULL, w->rows, w->cols, w->bstride, xq, xs, ldx, M, out, ldo, mode, s);
     if (w->type == GW_Q6_K)
-        return launch_gemv_kq<GW_Q6_K>(w->blocks, w->rows, w->cols, xq, xs, ldx, M, out, ldo, mode, s);
+        return launch_gemv_mr<GW_Q6_K>(w->blocks, NULL, w->rows, w->cols, w->bstride, xq, xs, ldx, M, out, ldo, mode, s);
     return (int)hipErrorInvalidValue;
 }
 
@@ -398,8 +539,19 @@ int gw_q8_block_sums(int32_t *isum, const int8_t *codes, int N, int K, const int
 int gw_kq_matmul(float *out, int type, const void *blocks, int N, int K, const int8_t *xq, const float *xs, int M, void *stream) {
     if (N <= 0 || K <= 0 || M <= 0 || K % 256 || (type != GW_Q4_K && type != GW_Q6_K) || !out || !blocks || !xq || !xs)
         return RQ_ERR_ARG;
-    GwMat w = { type, N, K, NULL, NULL, (uint8_t *)blocks };
-    return gw_k_matmul(&w, xq, xs, K, M, out, N, 0, (hipStream_t)stream) ? RQ_ERR_STATE : RQ_OK;
+    GwMat w = { type, N, K, NULL, NULL, (uint8_t *)blocks, GW_Q4K_BYTES };
+    if (type == GW_Q4_K) return gw_k_matmul(&w, xq, xs, K, M, out, N, 0, (hipStream_t)stream) ? RQ_ERR_STATE : RQ_OK;
+    // Q6_K: the file's blocks padded into the device layout first (a temporary copy)
+    size_t nblk = (size_t)N * (K / 256);
+    uint8_t *pad = NULL;
+    if (hipMalloc((void **)&pad, nblk * GW_Q6K_DEV) != hipSuccess) return RQ_ERR_NOMEM;
+    w.blocks = pad;
+    w.bstride = GW_Q6K_DEV;
+    int rc = gw_k_q6k_pad((const uint8_t *)blocks, nblk, pad, (hipStream_t)stream) ||
+             gw_k_matmul(&w, xq, xs, K, M, out, N, 0, (hipStream_t)stream) ? RQ_ERR_STATE : RQ_OK;
+    if (hipStreamSynchronize((hipStream_t)stream) != hipSuccess) rc = RQ_ERR_STATE;
+    (void)hipFree(pad);
+    return rc;
 }
 
 } // extern "C"

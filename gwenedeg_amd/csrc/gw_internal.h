@@ -22,15 +22,20 @@ enum { GW_F32 = 0, GW_Q8_0 = 8, GW_Q4_K = 12, GW_Q6_K = 14 }; /* ggml type numbe
 #define GW_ATT_P 256  /* positions per attention block */
 #define GW_RMAX 512   /* rows per pass (RQ_BATCH_MAX) */
 #define GW_W13_IL 4 /* w1 / w3 rows interleaved in the fused Q8_0 matrix (blocks of 4) */
-#define GW_GEMV_MAX_ROWS 4 /* activation rows up to which a Q8_0 matmul takes the GEMV (else the MFMA GEMM) */
+#define GW_GEMV_MAX_ROWS 32 /* activation rows up to which a Q8_0 matmul takes the batched GEMV (else the MFMA GEMM) */
+#define GW_Q4K_BYTES 144    /* bytes of a Q4_K super-block (256 weights), file and device */
+#define GW_Q6K_BYTES 210    /* bytes of a Q6_K super-block in the file */
+#define GW_Q6K_DEV 224      /* ... on the device: the file's 210 bytes padded to a 16-byte multiple (aligned loads) */
 
 /* A weight matrix on the device (rows x cols). Q8_0: int8 codes, row-major, and fp16 scales (cols / 32 per row),
- * the file's bytes split (34 bytes per 32 weights, as the file). K-quants: the file's blocks, row-major */
+ * the file's bytes split (34 bytes per 32 weights, as the file). K-quants: the file's super-blocks, row-major, each
+ * bstride bytes apart (Q4_K 144; Q6_K 224: the file's 210 bytes and 14 of padding) */
 typedef struct {
     int type, rows, cols;
     int8_t *codes;
     uint16_t *scales;
     uint8_t *blocks;
+    int bstride;
 } GwMat;
 
 typedef struct {
@@ -129,11 +134,11 @@ int gw_hip_fail(char *err, size_t errlen, const char *what, hipError_t e);
 
 /* kernels (gw_kernels.hip) */
 int gw_k_embed_q8(float *x, int dim, const uint8_t *codes, const uint16_t *scales, const int *tok, int n, hipStream_t s);
-int gw_k_embed_kq(float *x, int dim, int type, const uint8_t *blocks, const int *tok, int n, hipStream_t s);
+int gw_k_embed_kq(float *x, int dim, int type, const uint8_t *blocks, int bstride, const int *tok, int n, hipStream_t s);
+/* Q6_K super-blocks (file, 210 bytes) -> the device layout (GW_Q6K_DEV bytes apart) */
+int gw_k_q6k_pad(const uint8_t *src, size_t nblk, uint8_t *dst, hipStream_t s);
 int gw_k_rmsnorm_quant(float *x, const float *d, int dim, const float *w, const int *sel, int n, int8_t *xq, float *xs,
                        int ldq, float *hid, hipStream_t s);
-int gw_k_gemv_q8(const int8_t *W, const uint16_t *WS, int nrows, int K, const int8_t *xq, const float *xs, int ldx, int M,
-                 float *out, int ldo, int mode, hipStream_t s);
 int gw_k_qknorm_rope_store(float *qkv, int ldqkv, int n, int nh, int nkv, int hd, const float *qn, const float *kn,
                            const float *rope, const int *pos, uint16_t *const *kc, uint16_t *const *vc, hipStream_t s);
 int gw_k_attn_part(const void *items, int nitems, int nq_max, const float *qkv, int ldqkv, int nh, int nkv, int hd, float scale,

@@ -115,118 +115,6 @@ __global__ __launch_bounds__(NORM_T) void k_rmsnorm_quant(float *__restrict__ x,
 
 // ------------------------------------------------------------------------------------- Q8_0 GEMV
 
-// out[m * ldo + row] = W row . X row m for M activation rows, R weight rows per block. Each thread takes half-groups
-// (16 codes) j = t, t + 256, ..., U of them per pass with every weight load of the pass issued before the first dot (a
-// row of K <= 4096 U codes is one pass): an exact int32 sum by 4 v_dot4 (sdot4), the lane pair's sums added (exact),
-// the even lane's product (ws * xs) * (float) isum into LDS; then one lane per (m, row) folds the groups in order, the
-// LDS reads of the next 32 groups issued before the adds of the current ones. W: row-major int8 codes (K per row) +
-// fp16 scales (K / 32 per row); X: int8 rows at xq + m * ldx, fp32 scales at xs + m * ldx / 32. mode 1: out = out + val
-// (a residual add)
-template <int M, int R, int U>
-__global__ __launch_bounds__(256) void k_gemv_q8(const int8_t *__restrict__ W, const uint16_t *__restrict__ WS, int nrows,
-                                                 int K, const int8_t *__restrict__ xq, const float *__restrict__ xs, int ldx,
-                                                 float *out, int ldo, int mode) {
-    extern __shared__ float P[];
-    const int G = K >> 5, H = K >> 4, PS = (G + 7) & ~3; // (rows 16-byte aligned)
-    const int row0 = blockIdx.x * R, t = threadIdx.x;
-    const int8_t *wr[R];
-    const uint16_t *sr[R];
-    #pragma unroll
-    for (int r = 0; r < R; r++) {
-        int row = row0 + r < nrows ? row0 + r : nrows - 1;
-        wr[r] = W + (size_t)row * K;
-        sr[r] = WS + (size_t)row * G;
-    }
-    for (int j0 = 0; j0 < H; j0 += 256 * U) {
-        // (loads past the row's end read its last chunk again, unconditionally: a load under a branch would wait for
-        // every earlier load first; only the dots below are predicated)
-        int4 wv[U][R];
-        float ws[U][R];
-        #pragma unroll
-        for (int u = 0; u < U; u++) {
-            int j = j0 + 256 * u + t < H ? j0 + 256 * u + t : H - 1;
-            #pragma unroll
-            for (int r = 0; r < R; r++) wv[u][r] = *(const int4 *)(wr[r] + 16 * j);
-        }
-        #pragma unroll
-        for (int u = 0; u < U; u++) {
-            int j = j0 + 256 * u + t < H ? j0 + 256 * u + t : H - 1;
-            #pragma unroll
-            for (int r = 0; r < R; r++) ws[u][r] = h2f(sr[r][j >> 1]);
-        }
-        int4 xv[U][M];
-        float xsg[U][M];
-        #pragma unroll
-        for (int u = 0; u < U; u++) {
-            int j = j0 + 256 * u + t < H ? j0 + 256 * u + t : H - 1;
-            #pragma unroll
-            for (int m = 0; m < M; m++) {
-                xv[u][m] = *(const int4 *)(xq + (size_t)m * ldx + 16 * j);
-                xsg[u][m] = xs[(size_t)m * (ldx >> 5) + (j >> 1)];
-            }
-        }
-        #pragma unroll
-        for (int u = 0; u < U; u++) {
-            int j = j0 + 256 * u + t;
-            if (j < H) { // (whole lane pairs: H is even)
-                #pragma unroll
-                for (int r = 0; r < R; r++) {
-                    #pragma unroll
-                    for (int m = 0; m < M; m++) {
-                        int s = __builtin_amdgcn_sdot4(wv[u][r].x, xv[u][m].x, 0, false);
-                        s = __builtin_amdgcn_sdot4(wv[u][r].y, xv[u][m].y, s, false);
-                        s = __builtin_amdgcn_sdot4(wv[u][r].z, xv[u][m].z, s, false);
-                        s = __builtin_amdgcn_sdot4(wv[u][r].w, xv[u][m].w, s, false);
-                        s = s + __shfl_xor(s, 1);
-                        if (!(j & 1)) {
-                            float sc = ws[u][r] * xsg[u][m];
-                            P[(m * R + r) * PS + (j >> 1)] = sc * (float)s;
-                        }
-                    }
-                }
-            }
-        }
-    }
-    __syncthreads();
-    if (t < M * R) {
-        int m = t / R, r = t % R, row = row0 + r;
-        if (row < nrows) {
-            const float *p = P + t * PS;
-            float v = 0.0f;
-            int g = 0;
-            if (G >= 32) {
-                float4 a[8];
-                #pragma unroll
-                for (int u = 0; u < 8; u++) a[u] = *(const float4 *)(p + 4 * u);
-                for (g = 32; g + 32 <= G; g += 32) {
-                    float4 b[8];
-                    #pragma unroll
-                    for (int u = 0; u < 8; u++) b[u] = *(const float4 *)(p + g + 4 * u);
-                    #pragma unroll
-                    for (int u = 0; u < 8; u++) {
-                        v = v + a[u].x;
-                        v = v + a[u].y;
-                        v = v + a[u].z;
-                        v = v + a[u].w;
-                    }
-                    #pragma unroll
-                    for (int u = 0; u < 8; u++) a[u] = b[u];
-                }
-                #pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    v = v + a[u].x;
-                    v = v + a[u].y;
-                    v = v + a[u].z;
-                    v = v + a[u].w;
-                }
-            }
-            for (; g < G; g++) v = v + p[g];
-            float *o = out + (size_t)m * ldo + row;
-            *o = mode == 1 ? *o + v : v;
-        }
-    }
-}
-
 // ------------------------------------------------------------------- QK-norm + RoPE + KV cache store
 
 // one 64-lane block per (row, head): heads 0..nh-1 the query heads (rmsnorm with qn, RoPE, in place), nh..nh+nkv-1
@@ -818,43 +706,6 @@ int gw_k_set_exact(const float *rsq, int bits, const float *rcp, const uint8_t *
     if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(gw_rcp_tab), &rcp, sizeof(rcp));
     if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(gw_exp_delta), &expd, sizeof(expd));
     return (int)e;
-}
-
-int gw_k_gemv_q8(const int8_t *W, const uint16_t *WS, int nrows, int K, const int8_t *xq, const float *xs, int ldx, int M,
-                 float *out, int ldo, int mode, hipStream_t s) {
-    // M activation rows in launches of up to 4; U = the 16-code chunks per thread and pass (all loads of a row issued at
-    // once up to K = 16384)
-    const int R = 4;
-    int H = K / 16, U = (H + 255) / 256;
-    U = U < 1 ? 1 : U > 4 ? 4 : U;
-    hipEvent_t t0, t1; // (timing: the first launch's start, the last one's stop)
-    gw_take_launch_events(&t0, &t1);
-    for (int m0 = 0; m0 < M; m0 += 4) {
-        int mm = M - m0 < 4 ? M - m0 : 4;
-        hipEvent_t e0 = m0 == 0 ? t0 : NULL, e1 = m0 + 4 >= M ? t1 : NULL;
-        size_t lds = (size_t)mm * R * ((K / 32 + 7) & ~3) * sizeof(float);
-        dim3 grid((nrows + R - 1) / R);
-        const int8_t *x = xq + (size_t)m0 * ldx;
-        const float *xsc = xs + (size_t)m0 * (ldx / 32);
-        float *o = out + (size_t)m0 * ldo;
-#define GEMV_L(MM, UU) hipExtLaunchKernelGGL((k_gemv_q8<MM, R, UU>), grid, dim3(256), (uint32_t)lds, s, e0, e1, 0, W, WS, nrows, K, x, xsc, ldx, o, ldo, mode)
-#define GEMV_U(MM)                                                                                                      \
-    switch (U) {                                                                                                        \
-    case 1: GEMV_L(MM, 1); break;                                                                                       \
-    case 2: GEMV_L(MM, 2); break;                                                                                       \
-    case 3: GEMV_L(MM, 3); break;                                                                                       \
-    default: GEMV_L(MM, 4); break;                                                                                      \
-    }
-        switch (mm) {
-        case 1: GEMV_U(1); break;
-        case 2: GEMV_U(2); break;
-        case 3: GEMV_U(3); break;
-        default: GEMV_U(4); break;
-        }
-#undef GEMV_U
-#undef GEMV_L
-    }
-    return (int)hipGetLastError();
 }
 
 int gw_k_qknorm_rope_store(float *qkv, int ldqkv, int n, int nh, int nkv, int hd, const float *qn, const float *kn,

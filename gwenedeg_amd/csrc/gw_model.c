@@ -310,9 +310,20 @@ static int load_mat_il(Loader *L, GwMat *dst, int r0, const char *name, int rows
     if (t->type != GW_Q4_K && t->type != GW_Q6_K) return lfail(L, RQ_ERR_LOAD, "GGUF: %s: ggml type %u not supported", name, t->type);
     if (r0 != 0 || dst->rows != rows) return lfail(L, RQ_ERR_LOAD, "GGUF: %s: internal shape mismatch", name);
     dst->type = (int)t->type;
-    if ((rc = dmalloc(L, (void **)&dst->blocks, t->size)) != RQ_OK) return rc;
-    hipError_t e = hipMemcpy(dst->blocks, L->g.map + t->off, t->size, hipMemcpyHostToDevice);
-    return e == hipSuccess ? RQ_OK : gw_hip_fail(L->err, L->errlen, "hipMemcpy (weights)", e);
+    if (t->type == GW_Q4_K) {
+        dst->bstride = GW_Q4K_BYTES;
+        if ((rc = dmalloc(L, (void **)&dst->blocks, t->size)) != RQ_OK) return rc;
+        hipError_t e = hipMemcpy(dst->blocks, L->g.map + t->off, t->size, hipMemcpyHostToDevice);
+        return e == hipSuccess ? RQ_OK : gw_hip_fail(L->err, L->errlen, "hipMemcpy (weights)", e);
+    }
+    /* Q6_K: staged as the file's blocks, then padded to GW_Q6K_DEV bytes each (16-byte aligned loads) */
+    size_t nblk = t->size / GW_Q6K_BYTES;
+    dst->bstride = GW_Q6K_DEV;
+    if ((rc = dmalloc(L, (void **)&dst->blocks, nblk * GW_Q6K_DEV)) != RQ_OK) return rc;
+    if ((rc = stage(L, t)) != RQ_OK) return rc;
+    if (gw_k_q6k_pad(L->stage, nblk, dst->blocks, 0)) return lfail(L, RQ_ERR_STATE, "GGUF: %s: repack kernel failed", name);
+    hipError_t e = hipDeviceSynchronize();
+    return e == hipSuccess ? RQ_OK : gw_hip_fail(L->err, L->errlen, "repack", e);
 }
 
 static int alloc_q8(Loader *L, GwMat *w, int rows, int cols) {

@@ -160,6 +160,11 @@ int gw_decode_argmax(RqCtx *c, RqSeq *s, int token, int *next);
  * the host waits once. Results equal n gw_decode_argmax calls. RQ_ERR_CONTEXT past the capacity, nothing done */
 int gw_decode_greedy(RqCtx *c, RqSeq *s, int token, int n, int *tokens);
 
+/* rq_forward_batch (runq.h:375) with the selected rows' logits left on the device instead of copied to the host: the
+ * batched decode step of a serving loop (engine.c:3230-3253 samples every row), followed by gw_ctx_argmax for greedy
+ * rows. Same validation and errors as rq_forward_batch */
+int gw_forward_batch_device(RqCtx *c, const RqSegment *seg, int nseg);
+
 /* Per-kernel-class device time (the GPU counterpart of the reference's -DRUNQ_PROFILE phases, forward.c:13-24):
  * gw_ctx_profile_enable(c, 1) resets the counters and brackets each kernel class of every later pass with HIP events
  * on the context's stream; rq_ctx_profile then returns the classes' names and summed seconds, and
