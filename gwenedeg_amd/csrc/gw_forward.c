@@ -186,8 +186,8 @@ static int ctx_part(RqCtx *c, int rows, int nb) {
     size_t need = (size_t)rows * m->n_heads * nb * (m->head_dim + 2) * sizeof(float);
     if (nb > c->att_nb || need > c->part_bytes) {
         int nbn = nb > c->att_nb ? nb : c->att_nb;
-        /* the combine kernel keeps (m, l, coefficient) of every head and block of a row in LDS */
-        if ((size_t)m->n_heads * (2 * (size_t)nbn + 1) * sizeof(float) > 65536)
+        /* the combine kernel keeps (m, l, coefficient) of every block of its 256 / head_dim heads in LDS */
+        if ((size_t)(256 / m->head_dim) * (2 * (size_t)nbn + 1) * sizeof(float) > 65536)
             return ctx_fail(c, RQ_ERR_ARG, "context of %d positions too long for %d heads (attention combine)",
                             nbn * GW_ATT_P, m->n_heads);
         int B = c->nb_max > 1 ? c->nb_max : 1;

@@ -182,12 +182,11 @@ __global__ __launch_bounds__(64) void k_qknorm_rope_store(float *__restrict__ qk
 #define ATT_QC 36                       // LDS floats per 32-dim chunk of a query vector (32 + 4 padding)
 #define ATT_QS (4 * ATT_QC)             // LDS floats per query vector
 template <int NQ>
-__global__ __launch_bounds__(ATT_TH) void k_attn_part(const int4 *__restrict__ items, const float *__restrict__ qkv, int ldqkv,
-                                                      int nh, int nkv, int hd, float scale, const int *__restrict__ pos,
-                                                      uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc,
-                                                      float *__restrict__ part, int pstride) {
+__device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, const float *__restrict__ qkv, int ldqkv, int nh,
+                                               int nkv, int hd, float scale, const int *__restrict__ pos,
+                                               uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc,
+                                               float *__restrict__ part, int pstride) {
     __shared__ __align__(16) uint8_t ks[16 * ATT_KTILE];
-    __shared__ __align__(16) uint8_t vs[16 * 32 * ATT_HDMAX];
     __shared__ __align__(16) float qs[NQ * ATT_QS];
     __shared__ float S[NQ][ATT_P];
     __shared__ int np[NQ];
@@ -199,14 +198,12 @@ __global__ __launch_bounds__(ATT_TH) void k_attn_part(const int4 *__restrict__ i
     int nmx = pos[r0 + nr - 1] + 1 - kb * ATT_P;
     nmx = nmx < ATT_P ? nmx : ATT_P;
     int nbytes = (nmx + ATT_T - 1) / ATT_T * TB; // the tiles holding positions < nmx
-    // staging: 16 bytes of K and of V per thread and round, up to 4 rounds (hd <= 128), loads issued before any use
-    uint4 k0, k1, k2, k3, v0, v1, v2, v3;
-#define ATT_LD(k, KR, VR)                                                                                                \
-    if ((t + ATT_TH * k) * 16 < nbytes) {                                                                            \
-        KR = *(const uint4 *)(K + (t + ATT_TH * k) * 16);                                                             \
-        VR = *(const uint4 *)(V + (t + ATT_TH * k) * 16);                                                             \
-    }
-    ATT_LD(0, k0, v0) ATT_LD(1, k1, v1) ATT_LD(2, k2, v2) ATT_LD(3, k3, v3)
+    // staging of K: 16 bytes per thread and round, up to 4 rounds (hd <= 128), loads issued before any use (V is read
+    // from memory by the o chains: a position's row is one coalesced 2 hd-byte load per vector's wave)
+    uint4 k0, k1, k2, k3;
+#define ATT_LD(k, KR)                                                                                                    \
+    if ((t + ATT_TH * k) * 16 < nbytes) KR = *(const uint4 *)(K + (t + ATT_TH * k) * 16);
+    ATT_LD(0, k0) ATT_LD(1, k1) ATT_LD(2, k2) ATT_LD(3, k3)
 #undef ATT_LD
     for (int e = t; e < NQ * ATT_QS; e += ATT_TH) { // (padding and vectors past nq: zeros)
         int v = e / ATT_QS, c = e % ATT_QS / ATT_QC, i = e % ATT_QC, d = 32 * c + i;
@@ -216,13 +213,12 @@ __global__ __launch_bounds__(ATT_TH) void k_attn_part(const int4 *__restrict__ i
         int n = t < nq ? pos[r0 + t / kv_mul] + 1 - kb * ATT_P : 0;
         np[t] = n < 0 ? 0 : n < ATT_P ? n : ATT_P;
     }
-#define ATT_ST(k, KR, VR)                                                                                                \
+#define ATT_ST(k, KR)                                                                                                    \
     if ((t + ATT_TH * k) * 16 < nbytes) {                                                                            \
         int o = (t + ATT_TH * k) * 16, tile = o / TB, w = o % TB;                                                     \
         *(uint4 *)(ks + tile * ATT_KTILE + (w >> 10) * ATT_KROW + (w & 1023)) = KR;                                   \
-        *(uint4 *)(vs + o) = VR; /* (V: position p's row at p hd 2 bytes) */                                          \
     }
-    ATT_ST(0, k0, v0) ATT_ST(1, k1, v1) ATT_ST(2, k2, v2) ATT_ST(3, k3, v3)
+    ATT_ST(0, k0) ATT_ST(1, k1) ATT_ST(2, k2) ATT_ST(3, k3)
 #undef ATT_ST
     __syncthreads();
     // scores: lane (position p, chunk c), all NQ vectors (no per-vector branches in the chain)
@@ -295,30 +291,52 @@ __global__ __launch_bounds__(ATT_TH) void k_attn_part(const int4 *__restrict__ i
         }
     }
     __syncthreads();
-    // o: lane (vector v = wave, dim pair d2): the chains over the positions, 8 at a time, then the rest
+    // o: lane (vector v = wave, dim pair d2): the chains over the positions in order, V pairs from memory, two register
+    // sets of PB positions' loads alternating (a copy between sets would wait for the loads)
     {
         int v = wave, d2 = lane, i0 = 2 * d2;
         if (v < nq && i0 < hd && np[v] > 0) {
-            int n = np[v], p = 0;
+            const int n = np[v];
+            int p = 0;
             float o0 = 0.0f, o1 = 0.0f;
-            const uint8_t *vb = vs + i0 * 2;
-            const int rs = hd * 2;
-            for (; p + 8 <= n; p += 8) {
-                uint32_t vv[8];
-                float e[8];
+            const uint32_t *vb = (const uint32_t *)(V + i0 * 2);
+            const int rs = hd >> 1; // (uint32 words per position's row)
+            constexpr int PB = 16;
+            uint32_t va[PB], vbb[PB];
+            float ea[PB], eb[PB];
+            auto ld = [&](uint32_t (&vv)[PB], float (&ee)[PB], int q0) {
                 #pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    vv[u] = *(const uint32_t *)(vb + (p + u) * rs);
-                    e[u] = S[v][p + u];
+                for (int u = 0; u < PB; u++) {
+                    vv[u] = vb[(size_t)(q0 + u) * rs];
+                    ee[u] = S[v][q0 + u];
                 }
+            };
+            auto fold = [&](const uint32_t (&vv)[PB], const float (&ee)[PB]) {
                 #pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    o0 = __builtin_fmaf(e[u], h2f((uint16_t)(vv[u] & 0xffff)), o0);
-                    o1 = __builtin_fmaf(e[u], h2f((uint16_t)(vv[u] >> 16)), o1);
+                for (int u = 0; u < PB; u++) {
+                    o0 = __builtin_fmaf(ee[u], h2f((uint16_t)(vv[u] & 0xffff)), o0);
+                    o1 = __builtin_fmaf(ee[u], h2f((uint16_t)(vv[u] >> 16)), o1);
+                }
+            };
+            if (n >= PB) {
+                ld(va, ea, 0);
+                for (p = PB; p + 2 * PB <= n; p += 2 * PB) {
+                    ld(vbb, eb, p);
+                    fold(va, ea);
+                    ld(va, ea, p + PB);
+                    fold(vbb, eb);
+                }
+                if (p + PB <= n) {
+                    ld(vbb, eb, p);
+                    fold(va, ea);
+                    fold(vbb, eb);
+                    p += PB;
+                } else {
+                    fold(va, ea);
                 }
             }
             for (; p < n; p++) {
-                uint32_t vv = *(const uint32_t *)(vb + p * rs);
+                uint32_t vv = vb[(size_t)p * rs];
                 float e = S[v][p];
                 o0 = __builtin_fmaf(e, h2f((uint16_t)(vv & 0xffff)), o0);
                 o1 = __builtin_fmaf(e, h2f((uint16_t)(vv >> 16)), o1);
@@ -329,6 +347,14 @@ __global__ __launch_bounds__(ATT_TH) void k_attn_part(const int4 *__restrict__ i
             o[i0 + 1] = o1;
         }
     }
+}
+
+template <int NQ>
+__global__ __launch_bounds__(ATT_TH) void k_attn_part(const int4 *__restrict__ items, const float *__restrict__ qkv, int ldqkv,
+                                                      int nh, int nkv, int hd, float scale, const int *__restrict__ pos,
+                                                      uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc,
+                                                      float *__restrict__ part, int pstride) {
+    attn_part_body<NQ>(items, qkv, ldqkv, nh, nkv, hd, scale, pos, kc, vc, part, pstride);
 }
 
 // The attention of the one-row (decode) pass, one block of 1024 threads per (query vector v, kv head g, key block kb),
@@ -529,86 +555,78 @@ __global__ __launch_bounds__(ATD_T) void k_attn_decode(const float *__restrict__
     }
 }
 
-// one block per row: the attention of each head from its block partials in block order (att_combine,
+// the attention of each head of a row from its key blocks' partials, in block order (att_combine,
 // forward.c:1405-1431), then the row's quantization for wo (aq row b, all_heads = nh * hd values, a multiple of 256).
-// Steps: every block's (m, l) into LDS and the first 8 blocks' o values of the thread's elements into registers, all
-// loads in flight together; per head the coefficients c_b = exp_att(m_b - M) and 1 / L (LDS); then per element the fma
-// chain over the blocks in order
-#define COMB_T 1024
-#define COMB_B 8
+// One block of 256 threads per (row b, 256 consecutive values of the row: 256 / hd heads); thread e: value e, head
+// h = e / hd, dim e % hd. Per head: M = max m_k, c_k = exp_att(m_k - M) (lanes in parallel), L = the fma chain of
+// c_k l_k in block order (one lane), inv = 1 / L; per value the fma chain of c_k o_k in block order, 8 blocks' loads
+// ahead, times inv (one block: o inv). The quantization groups (32 consecutive values) lie inside a head
+#define COMB_T 256
 __global__ __launch_bounds__(COMB_T) void k_attn_combine_quant(const float *__restrict__ part, int pstride, int nh, int hd,
                                                             const int *__restrict__ pos, int8_t *__restrict__ aq,
                                                             float *__restrict__ as, int ldq, float *__restrict__ att_out) {
-    extern __shared__ float cl[]; // [nh][nb] m then coefficients, [nh][nb] l, [nh] inverses
-    int b = blockIdx.x, nb = (pos[b] + 1 + ATT_P - 1) / ATT_P, st = hd + 2, t = threadIdx.x, ne = nh * hd;
-    float *ll = cl + (size_t)nh * nb, *inv = ll + (size_t)nh * nb;
+    extern __shared__ float cl[]; // [hpb][nb] m then coefficients, [hpb][nb] l, [hpb] inverses
+    const int b = blockIdx.x, nb = (pos[b] + 1 + ATT_P - 1) / ATT_P, st = hd + 2, t = threadIdx.x, hpb = COMB_T / hd;
+    const int e = blockIdx.y * COMB_T + t, h0 = blockIdx.y * hpb, hl = t / hd, ne = nh * hd;
+    float *ll = cl + (size_t)hpb * nb, *inv = ll + (size_t)hpb * nb;
     const float *pr = part + (size_t)b * nh * pstride;
-    float o[4][COMB_B];
+    const float *pb = pr + (size_t)(e / hd) * pstride + e % hd; // this value's o in block 0
+    float o[8];
     #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        int e = t + COMB_T * k;
-        if (e < ne) {
-            const float *pb = pr + (size_t)(e / hd) * pstride + e % hd;
-            #pragma unroll
-            for (int u = 0; u < COMB_B; u++)
-                if (u < nb) o[k][u] = pb[(size_t)u * st];
-        }
-    }
-    for (int i = t; i < nh * nb; i += COMB_T) {
-        const float *ml = pr + (size_t)(i / nb) * pstride + (size_t)(i % nb) * st + hd;
+    for (int u = 0; u < 8; u++)
+        if (u < nb) o[u] = pb[(size_t)u * st];
+    for (int i = t; i < hpb * nb; i += COMB_T) {
+        const float *ml = pr + (size_t)(h0 + i / nb) * pstride + (size_t)(i % nb) * st + hd;
         cl[i] = ml[0];
         ll[i] = ml[1];
     }
     __syncthreads();
-    for (int h = t; h < nh; h += COMB_T) {
-        float *ch = cl + (size_t)h * nb;
-        const float *lh = ll + (size_t)h * nb;
+    // coefficients: wave w (w < hpb) takes head w; its lanes the exp of blocks k = lane, lane + 64, ...
+    const int wave = t >> 6, lane = t & 63;
+    for (int hh = wave; hh < hpb; hh += COMB_T / 64) {
+        float *ch = cl + (size_t)hh * nb;
+        const float *lh = ll + (size_t)hh * nb;
         if (nb == 1) {
-            inv[h] = 1.0f / lh[0];
-            ch[0] = 1.0f;
+            if (lane == 0) {
+                inv[hh] = 1.0f / lh[0];
+                ch[0] = 1.0f;
+            }
             continue;
         }
-        float M = ch[0];
-        for (int k = 1; k < nb; k++) M = ch[k] > M ? ch[k] : M;
-        float L = 0.0f;
-        for (int k = 0; k < nb; k++) {
-            float c = exp_att(ch[k] - M);
-            ch[k] = c;
-            L = __builtin_fmaf(c, lh[k], L);
+        float M = -3.402823466e38f;
+        for (int k = lane; k < nb; k += 64) M = fmaxf(M, ch[k]);
+        M = wave_max(M);
+        for (int k = lane; k < nb; k += 64) ch[k] = exp_att(ch[k] - M);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        if (lane == 0) {
+            float L = 0.0f;
+            for (int k = 0; k < nb; k++) L = __builtin_fmaf(ch[k], lh[k], L);
+            inv[hh] = 1.0f / L;
         }
-        inv[h] = 1.0f / L;
     }
     __syncthreads();
-    #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        int e = t + COMB_T * k;
-        if (e < ne) { // (whole waves: ne % 256 == 0)
-            int h = e / hd;
-            const float *ch = cl + (size_t)h * nb;
-            float out;
-            if (nb == 1) {
-                out = o[k][0] * inv[h];
-            } else {
-                float acc = 0.0f;
-                #pragma unroll
-                for (int u = 0; u < COMB_B; u++)
-                    if (u < nb) acc = __builtin_fmaf(ch[u], o[k][u], acc);
-                const float *pb = pr + (size_t)h * pstride + e % hd;
-                for (int kb = COMB_B; kb < nb; kb += COMB_B) {
-                    float w[COMB_B];
-                    #pragma unroll
-                    for (int u = 0; u < COMB_B; u++)
-                        if (kb + u < nb) w[u] = pb[(size_t)(kb + u) * st];
-                    #pragma unroll
-                    for (int u = 0; u < COMB_B; u++)
-                        if (kb + u < nb) acc = __builtin_fmaf(ch[kb + u], w[u], acc);
-                }
-                out = acc * inv[h];
-            }
-            if (att_out) att_out[(size_t)b * ne + e] = out;
-            quant_lane32(out, aq + (size_t)b * ldq + e, as + (size_t)b * (ldq / 32) + (e >> 5));
+    const float *ch = cl + (size_t)hl * nb;
+    float out;
+    if (nb == 1) {
+        out = o[0] * inv[hl];
+    } else {
+        float acc = 0.0f;
+        #pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (u < nb) acc = __builtin_fmaf(ch[u], o[u], acc);
+        for (int kb = 8; kb < nb; kb += 8) {
+            float w[8];
+            #pragma unroll
+            for (int u = 0; u < 8; u++) w[u] = pb[(size_t)(kb + u < nb ? kb + u : nb - 1) * st];
+            #pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (kb + u < nb) acc = __builtin_fmaf(ch[kb + u], w[u], acc);
         }
+        out = acc * inv[hl];
     }
+    if (att_out) att_out[(size_t)b * ne + e] = out;
+    quant_lane32(out, aq + (size_t)b * ldq + e, as + (size_t)b * (ldq / 32) + (e >> 5));
 }
 
 // ------------------------------------------------------------------------------------ SwiGLU + quantize
@@ -741,9 +759,10 @@ int gw_k_attn_decode(const float *qkv, int nh, int nkv, int hd, float scale, con
 
 int gw_k_attn_combine_quant(const float *part, int pstride, int nh, int hd, const int *pos, int n, int8_t *aq, float *as,
                             int ldq, float *att_out, hipStream_t s) {
-    (void)hd;
-    GW_LAUNCH(k_attn_combine_quant, dim3(n), dim3(COMB_T), (size_t)nh * (2 * (pstride / (hd + 2)) + 1) * sizeof(float), s, part,
-              pstride, nh, hd, pos, aq, as, ldq, att_out);
+    // (nh hd % 256 == 0, hd | 256); LDS: the per-block (m, l) of the block's heads up to pstride / (hd + 2) blocks
+    int hpb = COMB_T / hd, nbm = pstride / (hd + 2);
+    GW_LAUNCH(k_attn_combine_quant, dim3(n, nh * hd / COMB_T), dim3(COMB_T), (size_t)hpb * (2 * nbm + 1) * sizeof(float), s,
+              part, pstride, nh, hd, pos, aq, as, ldq, att_out);
     return (int)hipGetLastError();
 }
 

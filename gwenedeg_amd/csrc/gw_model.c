@@ -500,7 +500,7 @@ RqModel *rq_model_load(const char *path, const RqModelOpts *o, char *err, size_t
     m->tied = gguf_tensor(&L.g, "output.weight") == NULL;
     int hd = m->head_dim, nh = m->n_heads, nkv = m->n_kv_heads, dim = m->dim, H = m->hidden, qd = nh * hd, kvd = nkv * hd;
     /* the shapes the kernels take (forward_model_init, forward.c:127-144, plus the device kernels' limits) */
-    if (nh % nkv || hd % 32 || hd > 128 || dim % 256 || H % 256 || qd % 256 || (nh / nkv) > 16 || dim > 16384 || qd > 4096 || H > 65536) {
+    if (nh % nkv || hd % 32 || hd > 128 || 256 % hd || dim % 256 || H % 256 || qd % 256 || (nh / nkv) > 16 || dim > 16384 || qd > 4096 || H > 65536) {
         rc = lfail(&L, RQ_ERR_LOAD, "unsupported shape (dim %d, hidden %d, heads %d / %d, head_dim %d)", dim, H, nh, nkv, hd);
         goto out;
     }
