@@ -186,7 +186,10 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
                                                int nkv, int hd, float scale, const int *__restrict__ pos,
                                                uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc,
                                                float *__restrict__ part, int pstride) {
+    // V staged in LDS for NQ = 16 (prefill row blocks: 16 vectors read every V row), else read from memory by the chains
+    constexpr bool VL = NQ == 16;
     __shared__ __align__(16) uint8_t ks[16 * ATT_KTILE];
+    __shared__ __align__(16) uint8_t vs[VL ? 16 * 32 * ATT_HDMAX : 16];
     __shared__ __align__(16) float qs[NQ * ATT_QS];
     __shared__ float S[NQ][ATT_P];
     __shared__ int np[NQ];
@@ -198,12 +201,15 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
     int nmx = pos[r0 + nr - 1] + 1 - kb * ATT_P;
     nmx = nmx < ATT_P ? nmx : ATT_P;
     int nbytes = (nmx + ATT_T - 1) / ATT_T * TB; // the tiles holding positions < nmx
-    // staging of K: 16 bytes per thread and round, up to 4 rounds (hd <= 128), loads issued before any use (V is read
-    // from memory by the o chains: a position's row is one coalesced 2 hd-byte load per vector's wave)
-    uint4 k0, k1, k2, k3;
-#define ATT_LD(k, KR)                                                                                                    \
-    if ((t + ATT_TH * k) * 16 < nbytes) KR = *(const uint4 *)(K + (t + ATT_TH * k) * 16);
-    ATT_LD(0, k0) ATT_LD(1, k1) ATT_LD(2, k2) ATT_LD(3, k3)
+    // staging of K (and V when VL): 16 bytes per thread and round, up to 4 rounds (hd <= 128), loads issued before any
+    // use (otherwise V is read from memory by the o chains: a position's row is one coalesced 2 hd-byte load per wave)
+    uint4 k0, k1, k2, k3, v0, v1, v2, v3;
+#define ATT_LD(k, KR, VR)                                                                                                \
+    if ((t + ATT_TH * k) * 16 < nbytes) {                                                                            \
+        KR = *(const uint4 *)(K + (t + ATT_TH * k) * 16);                                                             \
+        if (VL) VR = *(const uint4 *)(V + (t + ATT_TH * k) * 16);                                                     \
+    }
+    ATT_LD(0, k0, v0) ATT_LD(1, k1, v1) ATT_LD(2, k2, v2) ATT_LD(3, k3, v3)
 #undef ATT_LD
     for (int e = t; e < NQ * ATT_QS; e += ATT_TH) { // (padding and vectors past nq: zeros)
         int v = e / ATT_QS, c = e % ATT_QS / ATT_QC, i = e % ATT_QC, d = 32 * c + i;
@@ -213,12 +219,13 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
         int n = t < nq ? pos[r0 + t / kv_mul] + 1 - kb * ATT_P : 0;
         np[t] = n < 0 ? 0 : n < ATT_P ? n : ATT_P;
     }
-#define ATT_ST(k, KR)                                                                                                    \
+#define ATT_ST(k, KR, VR)                                                                                                \
     if ((t + ATT_TH * k) * 16 < nbytes) {                                                                            \
         int o = (t + ATT_TH * k) * 16, tile = o / TB, w = o % TB;                                                     \
         *(uint4 *)(ks + tile * ATT_KTILE + (w >> 10) * ATT_KROW + (w & 1023)) = KR;                                   \
+        if (VL) *(uint4 *)(vs + o) = VR; /* (V: position p's row at p hd 2 bytes) */                                  \
     }
-    ATT_ST(0, k0) ATT_ST(1, k1) ATT_ST(2, k2) ATT_ST(3, k3)
+    ATT_ST(0, k0, v0) ATT_ST(1, k1, v1) ATT_ST(2, k2, v2) ATT_ST(3, k3, v3)
 #undef ATT_ST
     __syncthreads();
     // scores: lane (position p, chunk c), all NQ vectors (no per-vector branches in the chain)
@@ -299,7 +306,7 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
             const int n = np[v];
             int p = 0;
             float o0 = 0.0f, o1 = 0.0f;
-            const uint32_t *vb = (const uint32_t *)(V + i0 * 2);
+            const uint32_t *vb = (const uint32_t *)((VL ? (const uint8_t *)vs : V) + i0 * 2);
             const int rs = hd >> 1; // (uint32 words per position's row)
             constexpr int PB = 16;
             uint32_t va[PB], vbb[PB];
