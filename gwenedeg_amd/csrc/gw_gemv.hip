@@ -14,7 +14,7 @@
 // instead of the two dots
 // The prologue's loads are issued before the weight loads (vector memory counts complete in order, so the prologue's
 // waits leave the weight loads in flight), the weight loads before any prologue arithmetic.
-// Then as k_gemv_q8: the exact int32 sum of a half-group by 4 v_dot4, the lane pair's sums added, the even lane's
+// Then, as in every Q8_0 kernel here: the exact int32 sum of a half-group by 4 v_dot4, the lane pair's sums added, the even lane's
 // (ws * xs) * (float) isum into LDS, one lane per row folding the groups in order (forward.c:906-916).
 #include <hip/hip_ext.h>
 

@@ -175,7 +175,7 @@ int gw_k_gemv1_combine(const GwMat *w, int R, const float *part, int pstride, in
                        hipStream_t s);
 
 /* per-launch kernel timing (gw_ctx_kernel_timing): gw_time_next_launch(a, b) makes the next matmul launch (k_gemv1,
- * k_gemm_q8, k_gemv_q8, k_gemv_kq) record its own start and stop in events a and b (hipExtLaunchKernel's events: the
+ * k_gemm_q8, k_gemv_mr) record its own start and stop in events a and b (hipExtLaunchKernel's events: the
  * dispatch's timestamps, no extra packets on the stream); each launcher takes the pair once (gw_take_launch_events) */
 void gw_time_next_launch(hipEvent_t a, hipEvent_t b);
 void gw_take_launch_events(hipEvent_t *a, hipEvent_t *b);
