@@ -84,22 +84,50 @@ __device__ __forceinline__ float gv_fold(const float *p, int G) {
 // loaded as its aligned 32-bit word (G is even) and kept raw until used: a conversion, or two 16-bit values packed into
 // one register, would wait for the loads just issued
 #define GV_RSRC_DW3 0x00020000 // buffer descriptor word 3 of gfx9-family targets (raw loads)
+// the weight loads are non-temporal (cache policy nt): each weight byte is read once per token, and a streaming
+// insert keeps the caches for what is read again (the K / V cache, the activations, the exactness tables). Measured
+// on the 8B decode step: 2.59 -> 2.51 ms per token
+#ifndef GV_WNT
+#define GV_WNT 2
+#endif
 template <int R>
 __device__ __forceinline__ void gv_load_tile(__amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t rs, int nrows, int tile, int j,
                                              int K, int G, int4 (&wv)[R], uint32_t (&ws)[R]) {
     #pragma unroll
     for (int r = 0; r < R; r++) {
         int row = tile * R + r < nrows ? tile * R + r : nrows - 1;
-        wv[r] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(rw, 16 * j, row * K, 0));
+        wv[r] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(rw, 16 * j, row * K, GV_WNT));
     }
     #pragma unroll
     for (int r = 0; r < R; r++) {
         int row = tile * R + r < nrows ? tile * R + r : nrows - 1;
-        ws[r] = __builtin_amdgcn_raw_buffer_load_b32(rs, ((j >> 1) & ~1) * 2, row * G * 2, 0);
+        ws[r] = __builtin_amdgcn_raw_buffer_load_b32(rs, ((j >> 1) & ~1) * 2, row * G * 2, GV_WNT);
     }
 }
 
-template <int R, int PRO, int NT>
+// the group of 32 (this lane's 16 values and its pair's): wmax, s = wmax / 127, q = trunc(v * inv + copysign(.49999997))
+// (forward.c:803-836); the pair is lanes t, t ^ 1
+__device__ __forceinline__ void gv_quant16(const float (&v)[16], int4 &xq, float &xs) {
+    float wm = 0.0f;
+    #pragma unroll
+    for (int i = 0; i < 16; i++) wm = fmaxf(wm, fabsf(v[i]));
+    float wo = __shfl_xor(wm, 1);
+    wm = wo > wm ? wo : wm;
+    xs = wm * (1.0f / 127.0f);
+    uint32_t pk[4] = { 0, 0, 0, 0 };
+    if (wm > 0.0f) {
+        float inv = 127.0f / wm;
+        #pragma unroll
+        for (int i = 0; i < 16; i++) {
+            float y = v[i] * inv;
+            int32_t qi = (int32_t)(y + copysignf(0.49999997f, y));
+            pk[i >> 2] |= ((uint32_t)qi & 0xffu) << (8 * (i & 3));
+        }
+    }
+    xq = make_int4((int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]);
+}
+
+template <int R, int PRO, int NT, int D>
 __global__ __launch_bounds__(NT) void k_gemv1(GvArgs a) {
     extern __shared__ float lds[];
     const int K = a.K, G = K >> 5, H = K >> 4, PS = (G + 7) & ~3; // (rows 16-byte aligned, 4+ banks apart)
@@ -109,7 +137,13 @@ __global__ __launch_bounds__(NT) void k_gemv1(GvArgs a) {
     float *xf = lds + a.cmax * R * PS; // GV_NORM: the row transposed, then its scale
     int tile = blockIdx.x;
 
-    // 1. the prologue's loads
+    // 1. the prologue's loads (GV_Q: the row's codes and its group's scale themselves)
+    int4 xv;
+    float xsg;
+    if (PRO == GV_Q) {
+        xv = *(const int4 *)(a.xq + 16 * j);
+        xsg = a.xs[j >> 1];
+    }
     float4 p0[4], p1[4];
     float2 po[GV_NBMAX][8];
     float pm[GV_NBMAX], pl[GV_NBMAX];
@@ -135,23 +169,29 @@ __global__ __launch_bounds__(NT) void k_gemv1(GvArgs a) {
             pl[b] = pb[bb * st + a.hd - i0 + 1];
         }
     }
-    // 2. the weight loads of the block's first two tiles (a block with one tile loads it twice)
+    // 2. the weight loads of the block's first D - 1 tiles (past the block's last tile: its first again)
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)a.W, (short)0, a.nrows * K, GV_RSRC_DW3);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)a.WS, (short)0, (a.nrows * G * 2 + 3) & ~3, GV_RSRC_DW3);
     const int odd = (j >> 1) & 1; // (the half of the scale's word)
-    int4 wv[R], wb[R], wc[R];
-    uint32_t ws[R], sb[R], sc[R];
-    gv_load_tile<R>(rw, rs, a.nrows, tile, j, K, G, wv, ws);
-    gv_load_tile<R>(rw, rs, a.nrows, tile + (int)gridDim.x < ntiles ? tile + (int)gridDim.x : tile, j, K, G, wb, sb);
+    int4 wv[D][R];
+    uint32_t ws[D][R];
+    #pragma unroll
+    for (int d = 0; d + 1 < D; d++) {
+        const int td = tile + d * (int)gridDim.x;
+        gv_load_tile<R>(rw, rs, a.nrows, td < ntiles ? td : tile, j, K, G, wv[d], ws[d]);
+    }
     // 3. this thread's 16 activation codes and its group's scale
-    int4 xv;
-    float xsg;
-    if (PRO == GV_Q) {
-        xv = *(const int4 *)(a.xq + 16 * j);
-        xsg = a.xs[j >> 1];
-    } else {
+    if (PRO != GV_Q) {
         float v[16];
-        if (PRO == GV_NORM) {
+        if (PRO == GV_QF) {
+            #pragma unroll
+            for (int u = 0; u < 4; u++) {
+                v[4 * u + 0] = p0[u].x;
+                v[4 * u + 1] = p0[u].y;
+                v[4 * u + 2] = p0[u].z;
+                v[4 * u + 3] = p0[u].w;
+            }
+        } else if (PRO == GV_NORM) {
             // the row transposed: value e at xt[(e % 16) LS + e / 16] (LS = K / 16 + 4: chain j's values contiguous,
             // the 16 chains 4 banks apart)
             const int LS = (K >> 4) + 4;
@@ -220,14 +260,6 @@ __global__ __launch_bounds__(NT) void k_gemv1(GvArgs a) {
                 v[4 * u + 2] = (p1[u].z * p0[u].z) * r;
                 v[4 * u + 3] = (p1[u].w * p0[u].w) * r;
             }
-        } else if (PRO == GV_QF) {
-            #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                v[4 * u + 0] = p0[u].x;
-                v[4 * u + 1] = p0[u].y;
-                v[4 * u + 2] = p0[u].z;
-                v[4 * u + 3] = p0[u].w;
-            }
         } else { // GV_COMBINE
             if (nb == 1) {
                 float inv = 1.0f / pl[0];
@@ -263,36 +295,19 @@ __global__ __launch_bounds__(NT) void k_gemv1(GvArgs a) {
                 }
             }
         }
-        // the group (this lane's 16 values and its pair's): wmax, s = wmax / 127, q = trunc(v * inv + copysign(.49999997))
-        float wm = 0.0f;
-        #pragma unroll
-        for (int i = 0; i < 16; i++) wm = fmaxf(wm, fabsf(v[i]));
-        float wo = __shfl_xor(wm, 1);
-        wm = wo > wm ? wo : wm;
-        xsg = wm * (1.0f / 127.0f);
-        uint32_t pk[4] = { 0, 0, 0, 0 };
-        if (wm > 0.0f) {
-            float inv = 127.0f / wm;
-            #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                float y = v[i] * inv;
-                int32_t qi = (int32_t)(y + copysignf(0.49999997f, y));
-                pk[i >> 2] |= ((uint32_t)qi & 0xffu) << (8 * (i & 3));
-            }
-        }
-        xv = make_int4((int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]);
+        gv_quant16(v, xv, xsg);
     }
-    // 4. the tiles: the next tile's loads, this tile's dots into LDS slot k % C; every C tiles (and after the last) one
-    // barrier and the fold of all C x R rows in parallel (one lane per row), so no fold stands between one tile's
-    // loads and the next. Three register sets take turns, two tiles in flight (a copy from a later tile's registers
-    // would wait for their loads)
+    // 4. the tiles: the load of the tile D - 1 ahead, this tile's dots into LDS slot k % C; every C tiles (and after the
+    // last) one barrier and the fold of all C x R rows in parallel (one lane per row), so no fold stands between one
+    // tile's loads and the next. D register sets take turns, D - 1 tiles in flight (a copy from a later tile's
+    // registers would wait for their loads)
     const int C = a.cmax;
     auto step = [&](const int4 (&cw)[R], const uint32_t (&cs)[R], int4 (&nw)[R], uint32_t (&ns)[R], int k) -> bool {
-        const int nt = tile + gridDim.x, nt2 = nt + gridDim.x;
+        const int nt = tile + gridDim.x, nta = tile + (D - 1) * (int)gridDim.x;
         const bool more = nt < ntiles;
-        // the tile after next (unconditional: past the block's last tile it loads that again, from L2; loads under a
-        // branch would make every later wait count for the path without them)
-        gv_load_tile<R>(rw, rs, a.nrows, nt2 < ntiles ? nt2 : nt < ntiles ? nt : tile, j, K, G, nw, ns);
+        // the tile D - 1 ahead (unconditional: past the block's last tile it loads this one again, from L2; loads under
+        // a branch would make every later wait count for the path without them)
+        gv_load_tile<R>(rw, rs, a.nrows, nta < ntiles ? nta : tile, j, K, G, nw, ns);
         const int slot = k % C;
         float *P = lds + slot * R * PS;
         #pragma unroll
@@ -324,10 +339,14 @@ __global__ __launch_bounds__(NT) void k_gemv1(GvArgs a) {
         tile = nt;
         return more;
     };
-    for (int k = 0;; k += 3) {
-        if (!step(wv, ws, wc, sc, k)) break;
-        if (!step(wb, sb, wv, ws, k + 1)) break;
-        if (!step(wc, sc, wb, sb, k + 2)) break;
+    for (int k = 0;; k += D) {
+        bool more = true;
+        #pragma unroll
+        for (int d = 0; d < D; d++) {
+            more = step(wv[d], ws[d], wv[(d + D - 1) % D], ws[(d + D - 1) % D], k + d);
+            if (!more) break;
+        }
+        if (!more) break;
     }
 }
 
@@ -343,11 +362,13 @@ static int gv_launch(int pro, int R, const GvArgs &a, hipStream_t s) {
             return (int)hipErrorInvalidDevice;
         gv_nwg = cus > 0 ? cus : 256;
     }
-    int H = a.K / 16, nt = (H + 63) / 64 * 64, ntiles = (a.nrows + R - 1) / R, nwg = ntiles < gv_nwg ? ntiles : gv_nwg;
-    // partial slots: the block's tile count, at most 16 and 96 KiB of LDS
+    const int H = a.K / 16, nt = (H + 63) / 64 * 64, ntiles = (a.nrows + R - 1) / R, nwg = ntiles < gv_nwg ? ntiles : gv_nwg;
+    // partial slots: the block's tile count, at most 16, 96 KiB of LDS and one fold lane per slot row (C R <= threads)
     size_t slot_bytes = (size_t)R * ((a.K / 32 + 7) & ~3) * sizeof(float);
     int tpw = (ntiles + nwg - 1) / nwg, cmax = (int)((96 << 10) / slot_bytes);
-    cmax = cmax < 1 ? 1 : cmax > 16 ? 16 : cmax;
+    cmax = cmax > 16 ? 16 : cmax;
+    cmax = cmax > nt / R ? nt / R : cmax;
+    cmax = cmax < 1 ? 1 : cmax;
     GvArgs b = a;
     b.cmax = tpw < cmax ? tpw : cmax;
     b.inv_k = 1.0f / (float)a.K;
@@ -355,14 +376,16 @@ static int gv_launch(int pro, int R, const GvArgs &a, hipStream_t s) {
     dim3 grid(nwg);
     hipEvent_t e0, e1;
     gw_take_launch_events(&e0, &e1);
-#define GV_L(RR, PP, NN) hipExtLaunchKernelGGL((k_gemv1<RR, PP, NN>), grid, dim3(nt), (uint32_t)lds, s, e0, e1, 0, b)
+#define GV_L(RR, PP, NN) hipExtLaunchKernelGGL((k_gemv1<RR, PP, NN, 3>), grid, dim3(nt), (uint32_t)lds, s, e0, e1, 0, b)
 #define GV_R(PP)                                                                                                        \
     if (nt <= 256) {                                                                                                    \
-        if (R == 4) GV_L(4, PP, 256);                                                                                   \
+        if (R == 2) GV_L(2, PP, 256);                                                                                   \
+        else if (R == 4) GV_L(4, PP, 256);                                                                              \
         else if (R == 8) GV_L(8, PP, 256);                                                                              \
         else GV_L(16, PP, 256);                                                                                         \
     } else {                                                                                                            \
-        if (R == 4 || PP == GV_NORM) GV_L(4, PP, 768); /* (R = 8 with the norm's registers would spill at 768) */       \
+        if (R == 2) GV_L(2, PP, 768);                                                                                   \
+        else if (R == 4 || PP == GV_NORM) GV_L(4, PP, 768); /* (R = 8 with the norm's registers would spill) */         \
         else GV_L(8, PP, 768);                                                                                          \
     }
     switch (pro) {
@@ -386,10 +409,10 @@ int gw_v_set_exact(const float *rsq, int bits, const float *rcp, const uint8_t *
 }
 
 static int gv_check(const GwMat *w, int R) {
-    /* (K <= 4096: 256 threads, R 4, 8 or 16; K <= 12288: 768 threads, R 4 or 8; K % 64 == 0: whole scale words per row;
+    /* (K <= 4096: 256 threads, R 2, 4, 8 or 16; K <= 12288: 768 threads, R 2, 4 or 8; K % 64 == 0: whole scale words per row;
      * the matrix under 2 GiB: 32-bit buffer offsets) */
     return w->type == GW_Q8_0 && w->cols % 64 == 0 && w->cols <= 12288 && (size_t)w->rows * w->cols < ((size_t)1 << 31) &&
-                   (R == 4 || R == 8 || (R == 16 && w->cols <= 4096)) ? 0 : (int)hipErrorInvalidValue;
+                   (R == 2 || R == 4 || R == 8 || (R == 16 && w->cols <= 4096)) ? 0 : (int)hipErrorInvalidValue;
 }
 
 int gw_k_gemv1_q(const GwMat *w, int R, const int8_t *xq, const float *xs, float *out, int mode, hipStream_t s) {

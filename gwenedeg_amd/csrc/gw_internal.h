@@ -159,15 +159,15 @@ int gw_k_q8_unpack(const uint8_t *blocks, size_t nblk, int8_t *codes, uint16_t *
 int gw_k_fill_synthetic(uint16_t *kc, uint16_t *vc, size_t n, unsigned long long seed, hipStream_t s);
 
 /* the single-row Q8_0 GEMV with the activation's producer fused in front (gw_gemv.hip): out[row] (+)= W row . act for
- * R rows per tile (4, 8, 16); act = the quantized row (q), rmsnorm(x, nw) (norm), the fp32 row x (qf) or the attention
+ * R rows per tile (2, 4, 8, 16); act = the quantized row (q), rmsnorm(x, nw) (norm), the fp32 row x (qf) or the attention
  * combine of part over the row's nb <= GW_GV_NBMAX key blocks (combine); W Q8_0, W->cols % 64 == 0, <= 12288 (4096 for
  * R = 16), under 2 GiB. norm with swiglu_il = GW_W13_IL (R = 8, w1 / w3 interleaved): out[j] = swiglu(h_j, h2_j) */
 #define GW_GV_NBMAX 4
 #define GW_GV_R_QKV 4  /* weight rows per tile of the fused decode matmuls */
-#define GW_GV_R_WO 8
+#define GW_GV_R_WO 2
 #define GW_GV_R_W13 8
-#define GW_GV_R_W2 4
-#define GW_GV_R_CLS 4
+#define GW_GV_R_W2 2
+#define GW_GV_R_CLS 8
 int gw_k_gemv1_q(const GwMat *w, int R, const int8_t *xq, const float *xs, float *out, int mode, hipStream_t s);
 int gw_k_gemv1_norm(const GwMat *w, int R, const float *x, const float *nw, float *out, int mode, int swiglu_il, hipStream_t s);
 int gw_k_gemv1_qf(const GwMat *w, int R, const float *x, float *out, int mode, hipStream_t s);
