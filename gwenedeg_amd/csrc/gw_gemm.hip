@@ -164,6 +164,211 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const int8_t *__restrict__ W, c
     }
 }
 
+// ------------------------------------------------------------------------------------- K-quant MFMA GEMM
+
+// out[m * ldo + n] (+)= W row n . X row m for m < M, n < N, W in the file's Q4_K / Q6_K super-blocks (batched rows,
+// prefill): the tiling of k_gemm_q8 (GM x 128 outputs per block of 4 waves, stages of 128 values = 4 groups of 32 = half
+// a super-block), each stage's weights unpacked into int8 rows in LDS, then per group the reference's term and fold
+// (kquants.h:86-109, :410-554):
+//   Q4_K: codes 0 .. 15; I = the exact sum q x (v_mfma_i32_32x32x32_i8), S = the exact sum of x (the same MFMA with
+//     B = 1); term = ((d sc_j) xs) I - (dmin m_j) (xs S)
+//   Q6_K: codes q - 32 (-32 .. 31, exact in int8; q 6-bit from ql / qh); per half-group of 16 the exact sum
+//     (v_mfma_i32_32x32x16_i8), I = sc_0 I_0 + sc_1 I_1 (exact int); term = (d xs) I
+// then val = val + term in group order. mode 1: out = out + val. K % 256 == 0.
+typedef long i64;
+template <int TYPE, int GM>
+__global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, int bstride, int N, int K,
+                                                 const int8_t *__restrict__ X, const float *__restrict__ XS, int ldx, int M,
+                                                 float *out, int ldo, int mode) {
+    constexpr int TJ = GM == 64 ? 2 : 1, XC = GM * 8 / 256;
+    __shared__ __align__(16) int8_t xl[GM * GROW];
+    __shared__ __align__(16) int8_t wl[GN * GROW];
+    __shared__ __align__(16) float xsl[4][GM];
+    __shared__ float f0l[GN][5], f1l[GN][5]; // Q4_K: d sc_j, dmin m_j of the stage's groups; Q6_K: f0l[n][0] = d
+    __shared__ int scl[GN][9];               // Q6_K: the stage's 8 half-group scales
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int m0 = blockIdx.y * GM, n0 = blockIdx.x * GN;
+    const int wm = GM == 64 ? (wave >> 1) * 32 : 0, wn = GM == 64 ? (wave & 1) * 64 : wave * 32;
+    const size_t rowb = (size_t)(K >> 8) * bstride;
+    float acc[TJ][16];
+    #pragma unroll
+    for (int j = 0; j < TJ; j++)
+        #pragma unroll
+        for (int r = 0; r < 16; r++) acc[j][r] = 0.0f;
+    for (int k0 = 0; k0 < K; k0 += GKB) {
+        const int hs = (k0 >> 7) & 1; // (the stage's half of super-block k0 / 256)
+        const uint8_t *sbk = W + (size_t)(k0 >> 8) * bstride;
+        // loads: X as in k_gemm_q8; W: Q4_K 2 x 16 bytes of the stage's 64 bytes of nibbles per thread, Q6_K 4 units
+        // (row, group p, half h) of 16 bytes of ql and 16 of qh; the headers (threads < 128: one row each)
+        // (named registers: an array here was placed in scratch memory)
+        auto xload = [&](int k) -> uint4 {
+            int c = t + 256 * k, row = c >> 3, col = (c & 7) * 16, m = m0 + row < M ? m0 + row : M - 1;
+            return *(const uint4 *)(X + (size_t)m * ldx + k0 + col);
+        };
+        const uint4 xr0 = xload(0), xr1 = XC > 1 ? xload(1) : xr0;
+        constexpr int NW = TYPE == GW_Q4_K ? 2 : 4;
+        uint4 wa[NW], wb[NW];
+        #pragma unroll
+        for (int k = 0; k < NW; k++) {
+            int c = t + 256 * k;
+            if (TYPE == GW_Q4_K) {
+                int row = c >> 2, q = c & 3, n = n0 + row < N ? n0 + row : N - 1;
+                wa[k] = *(const uint4 *)(sbk + (size_t)n * rowb + 16 + 64 * hs + 16 * q);
+            } else {
+                int row = c >> 3, u = c & 7, p = u >> 1, h = u & 1, n = n0 + row < N ? n0 + row : N - 1;
+                const uint8_t *b = sbk + (size_t)n * rowb;
+                wa[k] = *(const uint4 *)(b + 64 * hs + 32 * (p & 1) + 16 * h);
+                wb[k] = *(const uint4 *)(b + 128 + 32 * hs + 16 * h);
+            }
+        }
+        uint4 hd0 = make_uint4(0, 0, 0, 0), hd1 = make_uint4(0, 0, 0, 0);
+        if (t < GN) {
+            int n = n0 + t < N ? n0 + t : N - 1;
+            const uint8_t *b = sbk + (size_t)n * rowb;
+            if (TYPE == GW_Q4_K) {
+                hd0 = *(const uint4 *)b; // d, dmin, then scale bytes 0 .. 11 in words y, z, w
+            } else {
+                hd0 = *(const uint4 *)(b + 192); // the 16 int8 scales
+                hd1 = *(const uint4 *)(b + 208); // d
+            }
+        }
+        float xsv = 0.0f;
+        {
+            int row = t >> 2, gg = t & 3, m = m0 + row < M ? m0 + row : M - 1;
+            if (row < GM) xsv = XS[(size_t)m * (ldx >> 5) + (k0 >> 5) + gg];
+        }
+        __syncthreads(); // (the previous stage's readers are done)
+        *(uint4 *)(xl + (t >> 3) * GROW + (t & 7) * 16) = xr0;
+        if (XC > 1) *(uint4 *)(xl + ((t + 256) >> 3) * GROW + ((t + 256) & 7) * 16) = xr1;
+        #pragma unroll
+        for (int k = 0; k < NW; k++) {
+            int c = t + 256 * k;
+            if (TYPE == GW_Q4_K) {
+                // piece q: run i = q / 2 (32 bytes: low nibbles = group 2 i, high = group 2 i + 1), positions 16 (q % 2) ..
+                int row = c >> 2, q = c & 3, i = q >> 1, o = 16 * (q & 1);
+                uint4 lo = make_uint4(wa[k].x & 0x0F0F0F0Fu, wa[k].y & 0x0F0F0F0Fu, wa[k].z & 0x0F0F0F0Fu, wa[k].w & 0x0F0F0F0Fu);
+                uint4 hi = make_uint4((wa[k].x >> 4) & 0x0F0F0F0Fu, (wa[k].y >> 4) & 0x0F0F0F0Fu, (wa[k].z >> 4) & 0x0F0F0F0Fu,
+                                      (wa[k].w >> 4) & 0x0F0F0F0Fu);
+                *(uint4 *)(wl + row * GROW + 32 * (2 * i) + o) = lo;
+                *(uint4 *)(wl + row * GROW + 32 * (2 * i + 1) + o) = hi;
+            } else {
+                // q = ((ql >> 4 (p / 2)) & 15) | ((qh >> 2 p) & 3) << 4; q - 32 as int8: the 6-bit value with bit 5
+                // flipped, sign-extended
+                int row = c >> 3, u = c & 7, p = u >> 1, h = u & 1, sl = 4 * (p >> 1), sh = 2 * p;
+                uint32_t a4[4] = { wa[k].x, wa[k].y, wa[k].z, wa[k].w }, b4[4] = { wb[k].x, wb[k].y, wb[k].z, wb[k].w }, o4[4];
+                #pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    uint32_t q = ((a4[e] >> sl) & 0x0F0F0F0Fu) | (((b4[e] >> sh) & 0x03030303u) << 4);
+                    uint32_t f = q ^ 0x20202020u, sg = f & 0x20202020u;
+                    o4[e] = f | (sg << 1) | (sg << 2);
+                }
+                *(uint4 *)(wl + row * GROW + 32 * p + 16 * h) = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+            }
+        }
+        if (t < GN) {
+            if (TYPE == GW_Q4_K) {
+                auto scb = [&](int k) -> int { // (k < 12)
+                    uint32_t w = k < 4 ? hd0.y : k < 8 ? hd0.z : hd0.w;
+                    return (int)((w >> (8 * (k & 3))) & 0xffu);
+                };
+                const float d = h2f_g((uint16_t)(hd0.x & 0xffffu)), dmin = h2f_g((uint16_t)(hd0.x >> 16));
+                #pragma unroll
+                for (int gg = 0; gg < 4; gg++) {
+                    const int sb = 4 * hs + gg;
+                    int scj, mj;
+                    if (sb < 4) {
+                        scj = scb(sb) & 63;
+                        mj = scb(sb + 4) & 63;
+                    } else {
+                        scj = (scb(sb + 4) & 15) | (scb(sb - 4) >> 6) << 4;
+                        mj = (scb(sb + 4) >> 4) | (scb(sb) >> 6) << 4;
+                    }
+                    f0l[t][gg] = d * (float)scj;
+                    f1l[t][gg] = dmin * (float)mj;
+                }
+            } else {
+                uint32_t sw[4] = { hd0.x, hd0.y, hd0.z, hd0.w };
+                #pragma unroll
+                for (int k = 0; k < 8; k++) { // (half-group k of the stage: the super-block's scale 8 hs + k)
+                    const int ks = 8 * hs + k;
+                    scl[t][k] = (int)(int8_t)((sw[ks >> 2] >> (8 * (ks & 3))) & 0xffu);
+                }
+                f0l[t][0] = h2f_g((uint16_t)(hd1.x & 0xffffu));
+            }
+        }
+        {
+            int row = t >> 2, gg = t & 3;
+            if (row < GM) xsl[gg][row] = xsv;
+        }
+        __syncthreads();
+        #pragma unroll
+        for (int gg = 0; gg < 4; gg++) {
+            const int8_t *xa = xl + (wm + (lane & 31)) * GROW + gg * 32;
+            i32x16 S;
+            i32x4 a;
+            i64 a0, a1;
+            const i32x16 z = { 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0 };
+            if (TYPE == GW_Q4_K) {
+                a = *(const i32x4 *)(xa + 16 * (lane >> 5));
+                const i32x4 ones = { 0x01010101, 0x01010101, 0x01010101, 0x01010101 };
+                S = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, ones, z, 0, 0, 0);
+            } else {
+                a0 = *(const i64 *)(xa + 8 * (lane >> 5));
+                a1 = *(const i64 *)(xa + 16 + 8 * (lane >> 5));
+            }
+            #pragma unroll
+            for (int j = 0; j < TJ; j++) {
+                const int nl = wn + 32 * j + (lane & 31);
+                const int8_t *wbp = wl + nl * GROW + gg * 32;
+                if (TYPE == GW_Q4_K) {
+                    i32x4 b = *(const i32x4 *)(wbp + 16 * (lane >> 5));
+                    i32x16 I = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
+                    const float f0 = f0l[nl][gg], f1 = f1l[nl][gg];
+                    #pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        float4 xs4 = *(const float4 *)(&xsl[gg][wm + 8 * q + 4 * (lane >> 5)]);
+                        float xsq[4] = { xs4.x, xs4.y, xs4.z, xs4.w };
+                        #pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            float pa = (f0 * xsq[e]) * (float)I[4 * q + e];
+                            float pb = f1 * (xsq[e] * (float)S[4 * q + e]);
+                            acc[j][4 * q + e] = acc[j][4 * q + e] + (pa - pb);
+                        }
+                    }
+                } else {
+                    i64 b0 = *(const i64 *)(wbp + 8 * (lane >> 5)), b1 = *(const i64 *)(wbp + 16 + 8 * (lane >> 5));
+                    i32x16 I0 = __builtin_amdgcn_mfma_i32_32x32x16_i8(a0, b0, z, 0, 0, 0);
+                    i32x16 I1 = __builtin_amdgcn_mfma_i32_32x32x16_i8(a1, b1, z, 0, 0, 0);
+                    const int s0 = scl[nl][2 * gg], s1 = scl[nl][2 * gg + 1];
+                    const float d = f0l[nl][0];
+                    #pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        float4 xs4 = *(const float4 *)(&xsl[gg][wm + 8 * q + 4 * (lane >> 5)]);
+                        float xsq[4] = { xs4.x, xs4.y, xs4.z, xs4.w };
+                        #pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            int I = s0 * I0[4 * q + e] + s1 * I1[4 * q + e];
+                            acc[j][4 * q + e] = acc[j][4 * q + e] + (d * xsq[e]) * (float)I;
+                        }
+                    }
+                }
+            }
+        }
+    }
+    #pragma unroll
+    for (int j = 0; j < TJ; j++) {
+        int n = n0 + wn + 32 * j + (lane & 31);
+        #pragma unroll
+        for (int r = 0; r < 16; r++) {
+            int m = m0 + wm + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (m < M && n < N) {
+                float *o = out + (size_t)m * ldo + n;
+                *o = mode == 1 ? *o + acc[j][r] : acc[j][r];
+            }
+        }
+    }
+}
+
 // --------------------------------------------------------------------------------------------- K-quants
 
 // The batched GEMV of all three formats: out[m * ldo + row] (+)= W row . X row m for M <= 8 activation rows, R weight
@@ -483,18 +688,24 @@ void gw_take_launch_events(hipEvent_t *a, hipEvent_t *b) {
     tev0 = tev1 = NULL;
 }
 
+static int g_tile_rows = 0; // gw_matmul_tile_rows
+
+static int gemm_cus(void) { // the device's compute units
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            cus = 256;
+    }
+    return cus;
+}
+
 int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int M, float *out, int ldo, int mode, hipStream_t s) {
     if (w->type == GW_Q8_0 && M > GW_GEMV_MAX_ROWS && mode == 0) {
         hipEvent_t e0, e1;
         gw_take_launch_events(&e0, &e1);
-        static int cus = 0;
-        if (!cus) {
-            int dev = 0;
-            if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-                cus = 256;
-        }
-        int nt = (w->rows + GN - 1) / GN;
-        if ((size_t)nt * ((M + 63) / 64) >= (size_t)4 * cus) // enough 64-row tiles for several waves per SIMD
+        const int cus = gemm_cus(), nt = (w->rows + GN - 1) / GN;
+        if (g_tile_rows ? g_tile_rows == 64 : (size_t)nt * ((M + 63) / 64) >= (size_t)4 * cus) // (64-row tiles: enough for several waves per SIMD)
             hipExtLaunchKernelGGL(k_gemm_q8<64>, dim3(nt, (M + 63) / 64), dim3(256), 0, s, e0, e1, 0, (const int8_t *)w->codes,
                                   (const uint16_t *)w->scales, w->rows, w->cols, xq, xs, ldx, M, out, ldo);
         else
@@ -504,6 +715,26 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
     }
     if (w->type == GW_Q8_0)
         return launch_gemv_mr<GW_Q8_0>((const uint8_t *)w->codes, w->scales, w->rows, w->cols, 0, xq, xs, ldx, M, out, ldo, mode, s);
+    // K-quants above 8 rows: the MFMA GEMM where it has 64 blocks or more (a block streams its 128 rows' full K in
+    // order, so a narrow matrix leaves the device idle), else the batched GEMV in passes of 8 rows
+    if ((w->type == GW_Q4_K || w->type == GW_Q6_K) && M > 8 && (size_t)((w->rows + GN - 1) / GN) * ((M + 31) / 32) >= 64) {
+        hipEvent_t e0, e1;
+        gw_take_launch_events(&e0, &e1);
+        const int cus = gemm_cus(), nt = (w->rows + GN - 1) / GN;
+        const bool g64 = g_tile_rows ? g_tile_rows == 64 : (size_t)nt * ((M + 63) / 64) >= (size_t)4 * cus;
+        const dim3 grid(nt, g64 ? (M + 63) / 64 : (M + 31) / 32);
+#define KQ_L(TT, GG) hipExtLaunchKernelGGL((k_gemm_kq<TT, GG>), grid, dim3(256), 0, s, e0, e1, 0, (const uint8_t *)w->blocks, \
+                                           w->bstride, w->rows, w->cols, xq, xs, ldx, M, out, ldo, mode)
+        if (w->type == GW_Q4_K) {
+            if (g64) KQ_L(GW_Q4_K, 64);
+            else KQ_L(GW_Q4_K, 32);
+        } else {
+            if (g64) KQ_L(GW_Q6_K, 64);
+            else KQ_L(GW_Q6_K, 32);
+        }
+#undef KQ_L
+        return (int)hipGetLastError();
+    }
     if (w->type == GW_Q4_K)
         return launch_gemv_mr<GW_Q4_K>(w->blocks, NULL, w->rows, w->cols, w->bstride, xq, xs, ldx, M, out, ldo, mode, s);
     if (w->type == GW_Q6_K)
@@ -534,6 +765,13 @@ int gw_q8_block_sums(int32_t *isum, const int8_t *codes, int N, int K, const int
     hipLaunchKernelGGL(k_q8_block_sums, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, (hipStream_t)stream, isum, codes, N,
                        K, xq, M);
     return hipGetLastError() ? RQ_ERR_STATE : RQ_OK;
+}
+
+int gw_matmul_tile_rows(int rows) {
+    if (rows != 0 && rows != 32 && rows != 64) return -1;
+    int prev = g_tile_rows;
+    g_tile_rows = rows;
+    return prev;
 }
 
 int gw_kq_matmul(float *out, int type, const void *blocks, int N, int K, const int8_t *xq, const float *xs, int M, void *stream) {

@@ -210,6 +210,12 @@ int gw_q8_block_sums(int32_t *isum, const int8_t *codes, int N, int K, const int
 int gw_kq_matmul(float *out, int type, const void *blocks, int N, int K, const int8_t *xq, const float *xs, int M,
                  void *stream);
 
+/* The row tile of the MFMA GEMMs (prefill and batched rows: k_gemm_q8 for Q8_0 above 32 rows, k_gemm_kq for Q4_K /
+ * Q6_K above 8 rows): 0 chosen per launch (64-row tiles when they give each SIMD several waves, else 32; the
+ * default), 32 or 64 forced. Returns the previous setting, or -1 (and changes nothing) for another value. A tuning
+ * and test hook with no counterpart in runq.h; results do not depend on it */
+int gw_matmul_tile_rows(int rows);
+
 /* The context's stream (a hipStream_t), for callers that time the passes with events on it */
 void *gw_ctx_stream(RqCtx *c);
 

@@ -45,9 +45,11 @@ def test_quantize_bitexact(dev, M, K):
     assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 256, 1024), (1, 1024, 4096), (2, 512, 12288), (4, 64, 2560), (7, 128, 4096),
-                                   (16, 48, 1024), (64, 32, 1024)])
-def test_q8_matmul_bitexact(dev, M, N, K):
+@pytest.mark.parametrize("M,N,K,tile", [(1, 256, 1024, 0), (1, 1024, 4096, 0), (2, 512, 12288, 0), (4, 64, 2560, 0),
+                                        (7, 128, 4096, 0), (16, 48, 1024, 0), (64, 32, 1024, 0), (40, 208, 768, 32),
+                                        (100, 208, 768, 64)])
+def test_q8_matmul_bitexact(dev, M, N, K, tile):
+    """the Q8_0 operator against the oracle bit for bit (above 32 rows the MFMA GEMM, its row tile forced where given)"""
     torch, gw = dev
     from oracle import oracle as orc
     rng = np.random.default_rng(N + 7 * K + M)
@@ -57,8 +59,12 @@ def test_q8_matmul_bitexact(dev, M, N, K):
     ref = orc.q8_matmul(wq, ws16.astype(np.float32), xq, xs)
     out = torch.zeros((M, N), dtype=torch.float32, device="cuda")
     W, WS, XQ, XS = (_to_dev(torch, a) for a in (wq, ws16.view(np.int16), xq, xs))
-    assert gw.lib.gw_q8_matmul(out.data_ptr(), W.data_ptr(), WS.data_ptr(), N, K, XQ.data_ptr(), XS.data_ptr(), M, None) == 0
-    torch.cuda.synchronize()
+    prev = gw.lib.gw_matmul_tile_rows(tile)
+    try:
+        assert gw.lib.gw_q8_matmul(out.data_ptr(), W.data_ptr(), WS.data_ptr(), N, K, XQ.data_ptr(), XS.data_ptr(), M, None) == 0
+        torch.cuda.synchronize()
+    finally:
+        gw.lib.gw_matmul_tile_rows(prev)
     got = out.cpu().numpy()
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"max diff {np.abs(got - ref).max()}"
 
@@ -97,13 +103,15 @@ def test_q8_pack_and_block_sums(dev):
 
 
 @pytest.mark.parametrize("typ", [12, 14])
-@pytest.mark.parametrize("M", [1, 3, 6])
-def test_kq_matmul_bitexact(dev, typ, M):
+@pytest.mark.parametrize("M,tile", [(1, 0), (3, 0), (6, 0), (9, 32), (40, 32), (40, 64), (100, 64)])
+def test_kq_matmul_bitexact(dev, typ, M, tile):
+    """the K-quant operator against the oracle bit for bit: up to 8 rows the batched GEMV, above it the MFMA GEMM with
+    32- and 64-row tiles (N not a multiple of the 128-column tile)"""
     torch, gw = dev
     from oracle import oracle as orc
     from gwenedeg_amd import synth
     rng = np.random.default_rng(typ * 10 + M)
-    N, K = 64, 1024
+    N, K = (64, 1024) if M <= 8 else (200, 768)
     sl = synth.synth_library()
     rb = sl.gw_synth_row_bytes(typ, K)
     blocks = np.zeros((N, rb), np.uint8)
@@ -115,7 +123,11 @@ def test_kq_matmul_bitexact(dev, typ, M):
     ref = orc.kq_matmul(typ, blocks, xq, xs, N, K)
     out = torch.zeros((M, N), dtype=torch.float32, device="cuda")
     Bd, XQ, XS = (_to_dev(torch, a) for a in (blocks.reshape(-1), xq, xs))
-    assert gw.lib.gw_kq_matmul(out.data_ptr(), typ, Bd.data_ptr(), N, K, XQ.data_ptr(), XS.data_ptr(), M, None) == 0
-    torch.cuda.synchronize()
+    prev = gw.lib.gw_matmul_tile_rows(tile)
+    try:
+        assert gw.lib.gw_kq_matmul(out.data_ptr(), typ, Bd.data_ptr(), N, K, XQ.data_ptr(), XS.data_ptr(), M, None) == 0
+        torch.cuda.synchronize()
+    finally:
+        gw.lib.gw_matmul_tile_rows(prev)
     got = out.cpu().numpy()
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"max diff {np.abs(got - ref).max()}"
