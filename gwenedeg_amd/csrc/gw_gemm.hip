@@ -195,19 +195,22 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
     for (int j = 0; j < TJ; j++)
         #pragma unroll
         for (int r = 0; r < 16; r++) acc[j][r] = 0.0f;
-    for (int k0 = 0; k0 < K; k0 += GKB) {
+    // stage k0's loads into registers (the next stage's issued before this stage's MFMAs): X as in k_gemm_q8; W: Q4_K
+    // 2 x 16 bytes of the stage's 64 bytes of nibbles per thread, Q6_K 4 units (row, group p, half h) of 16 bytes of
+    // ql and 16 of qh; the headers (threads < 128: one row each). (xr0 / xr1 named: an array here was placed in
+    // scratch memory)
+    constexpr int NW = TYPE == GW_Q4_K ? 2 : 4;
+    uint4 xr0, xr1, wa[NW], wb[NW], hd0, hd1;
+    float xsv;
+    auto load = [&](int k0) {
         const int hs = (k0 >> 7) & 1; // (the stage's half of super-block k0 / 256)
         const uint8_t *sbk = W + (size_t)(k0 >> 8) * bstride;
-        // loads: X as in k_gemm_q8; W: Q4_K 2 x 16 bytes of the stage's 64 bytes of nibbles per thread, Q6_K 4 units
-        // (row, group p, half h) of 16 bytes of ql and 16 of qh; the headers (threads < 128: one row each)
-        // (named registers: an array here was placed in scratch memory)
         auto xload = [&](int k) -> uint4 {
             int c = t + 256 * k, row = c >> 3, col = (c & 7) * 16, m = m0 + row < M ? m0 + row : M - 1;
             return *(const uint4 *)(X + (size_t)m * ldx + k0 + col);
         };
-        const uint4 xr0 = xload(0), xr1 = XC > 1 ? xload(1) : xr0;
-        constexpr int NW = TYPE == GW_Q4_K ? 2 : 4;
-        uint4 wa[NW], wb[NW];
+        xr0 = xload(0);
+        xr1 = XC > 1 ? xload(1) : xr0;
         #pragma unroll
         for (int k = 0; k < NW; k++) {
             int c = t + 256 * k;
@@ -221,7 +224,7 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
                 wb[k] = *(const uint4 *)(b + 128 + 32 * hs + 16 * h);
             }
         }
-        uint4 hd0 = make_uint4(0, 0, 0, 0), hd1 = make_uint4(0, 0, 0, 0);
+        hd0 = make_uint4(0, 0, 0, 0), hd1 = make_uint4(0, 0, 0, 0);
         if (t < GN) {
             int n = n0 + t < N ? n0 + t : N - 1;
             const uint8_t *b = sbk + (size_t)n * rowb;
@@ -232,11 +235,13 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
                 hd1 = *(const uint4 *)(b + 208); // d
             }
         }
-        float xsv = 0.0f;
-        {
-            int row = t >> 2, gg = t & 3, m = m0 + row < M ? m0 + row : M - 1;
-            if (row < GM) xsv = XS[(size_t)m * (ldx >> 5) + (k0 >> 5) + gg];
-        }
+        xsv = 0.0f;
+        int row = t >> 2, gg = t & 3, m = m0 + row < M ? m0 + row : M - 1;
+        if (row < GM) xsv = XS[(size_t)m * (ldx >> 5) + (k0 >> 5) + gg];
+    };
+    load(0);
+    for (int k0 = 0; k0 < K; k0 += GKB) {
+        const int hs = (k0 >> 7) & 1;
         __syncthreads(); // (the previous stage's readers are done)
         *(uint4 *)(xl + (t >> 3) * GROW + (t & 7) * 16) = xr0;
         if (XC > 1) *(uint4 *)(xl + ((t + 256) >> 3) * GROW + ((t + 256) & 7) * 16) = xr1;
@@ -301,6 +306,7 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
             if (row < GM) xsl[gg][row] = xsv;
         }
         __syncthreads();
+        if (k0 + GKB < K) load(k0 + GKB);
         #pragma unroll
         for (int gg = 0; gg < 4; gg++) {
             const int8_t *xa = xl + (wm + (lane & 31)) * GROW + gg * 32;
