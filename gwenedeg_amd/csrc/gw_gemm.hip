@@ -375,6 +375,159 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
     }
 }
 
+// K-quant GEMM for 9 .. 32 activation rows (batched decode): one block of 512 threads per 32 weight rows, the 8 waves
+// taking the 8 groups of each super-block (wave w: group w), so the blocks are N / 32 and each wave's VALU work is one
+// group in eight. Each wave loads its MFMA operands straight from memory (X row l % 32, W row n0 + l % 32), 5
+// super-blocks ahead; per super-block: the exact int32 sums (MFMA, as k_gemm_kq), the wave's terms
+// (k_gemm_kq's expressions) into LDS, one barrier, then each thread adds the 8 terms of its 2 outputs in group order
+// (val = val + term, kquants.h:86-109, :410-554). M <= 32, K % 256 == 0, mode 1: out = out + val
+#define SK_T 512
+template <int TYPE>
+struct SkOps { // Q4_K: X 16 bytes, the group's 16 nibble bytes, the super-block header
+    uint4 x, q, hd;
+    float xs; // threads < 256: XS[m][8 s + g] for m = t / 8, g = t % 8
+};
+template <>
+struct SkOps<GW_Q6_K> { // X halves, ql halves, qh halves (8 bytes each), the group's two scale bytes (in a word), d
+    uint2 x0, x1, l0, l1, h0, h1;
+    uint32_t sc, dw;
+    float xs;
+};
+template <int TYPE>
+__global__ __launch_bounds__(SK_T) void k_gemm_kq32(const uint8_t *__restrict__ W, int bstride, int N, int K,
+                                                    const int8_t *__restrict__ X, const float *__restrict__ XS, int ldx,
+                                                    int M, float *out, int ldo, int mode) {
+    __shared__ __align__(16) float Tl[8][1024]; // group g's term of output o = r * 64 + lane (r: MFMA result register)
+    __shared__ __align__(16) float xsl[2][8][32]; // the super-block's activation scales [group][m], two buffers
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6, hi = lane >> 5;
+    const int n0 = blockIdx.x * 32, S = K >> 8;
+    const int nl = n0 + (lane & 31) < N ? n0 + (lane & 31) : N - 1, ml = (lane & 31) < M ? (lane & 31) : M - 1;
+    const uint8_t *wrow = W + (size_t)nl * S * bstride;
+    const int8_t *xrow = X + (size_t)ml * ldx + 32 * w;
+    const int xm = (t >> 3) < M ? (t >> 3) : M - 1;
+    const float *xsr = XS + (size_t)xm * (ldx >> 5) + (t & 7);
+    auto load = [&](SkOps<TYPE> &o, int s) __attribute__((always_inline)) {
+        s = s < S ? s : S - 1; // (past the last super-block: the last again)
+        const uint8_t *b = wrow + (size_t)s * bstride;
+        const int8_t *x = xrow + 256 * s;
+        if constexpr (TYPE == GW_Q4_K) {
+            o.x = *(const uint4 *)(x + 16 * hi);
+            o.q = *(const uint4 *)(b + 16 + 32 * (w >> 1) + 16 * hi);
+            o.hd = *(const uint4 *)b;
+        } else {
+            const int nn = w >> 2, p = w & 3;
+            o.x0 = *(const uint2 *)(x + 8 * hi);
+            o.x1 = *(const uint2 *)(x + 16 + 8 * hi);
+            o.l0 = *(const uint2 *)(b + 64 * nn + 32 * (p & 1) + 8 * hi);
+            o.l1 = *(const uint2 *)(b + 64 * nn + 32 * (p & 1) + 16 + 8 * hi);
+            o.h0 = *(const uint2 *)(b + 128 + 32 * nn + 8 * hi);
+            o.h1 = *(const uint2 *)(b + 128 + 32 * nn + 16 + 8 * hi);
+            o.sc = *(const uint32_t *)(b + 192 + 4 * (w >> 1));
+            o.dw = *(const uint32_t *)(b + 208);
+        }
+        o.xs = t < 256 ? xsr[8 * s] : 0.0f;
+    };
+    float acc0 = 0.0f, acc1 = 0.0f; // outputs t and t + 512
+    const i32x16 z = { 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0 };
+    auto step = [&](const SkOps<TYPE> &c, SkOps<TYPE> &nx, int s) __attribute__((always_inline)) -> bool {
+        load(nx, s + 5);
+        const int buf = s & 1;
+        if (t < 256) xsl[buf][t & 7][t >> 3] = c.xs;
+        float f0, f1 = 0.0f;
+        int s0 = 0, s1 = 0;
+        i32x16 I, I1;
+        if constexpr (TYPE == GW_Q4_K) {
+            const int sh = 4 * (w & 1);
+            const i32x4 b = { (int)((c.q.x >> sh) & 0x0F0F0F0Fu), (int)((c.q.y >> sh) & 0x0F0F0F0Fu),
+                              (int)((c.q.z >> sh) & 0x0F0F0F0Fu), (int)((c.q.w >> sh) & 0x0F0F0F0Fu) };
+            const i32x4 a = { (int)c.x.x, (int)c.x.y, (int)c.x.z, (int)c.x.w };
+            const i32x4 ones = { 0x01010101, 0x01010101, 0x01010101, 0x01010101 };
+            I = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
+            I1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, ones, z, 0, 0, 0); // (the sums of x)
+            // the scale bytes k = w, w + 4 and w - 4 (the 12 bytes in words y, z, w of the header)
+            const int bs = 8 * (w & 3);
+            const int bw = (int)(((w < 4 ? c.hd.y : c.hd.z) >> bs) & 0xffu), bw4 = (int)(((w < 4 ? c.hd.z : c.hd.w) >> bs) & 0xffu);
+            const int bm4 = (int)((c.hd.y >> bs) & 0xffu);
+            int scj, mj;
+            if (w < 4) {
+                scj = bw & 63;
+                mj = bw4 & 63;
+            } else {
+                scj = (bw4 & 15) | (bm4 >> 6) << 4;
+                mj = (bw4 >> 4) | (bw >> 6) << 4;
+            }
+            f0 = h2f_g((uint16_t)(c.hd.x & 0xffffu)) * (float)scj;
+            f1 = h2f_g((uint16_t)(c.hd.x >> 16)) * (float)mj;
+        } else {
+            const int p = w & 3, sl = 4 * (p >> 1), sh = 2 * p;
+            auto code = [&](uint32_t lo, uint32_t hq) -> int { // 4 codes q - 32 (q = lo nibble | 2 bits of qh << 4)
+                uint32_t q = ((lo >> sl) & 0x0F0F0F0Fu) | (((hq >> sh) & 0x03030303u) << 4);
+                uint32_t f = q ^ 0x20202020u, sg = f & 0x20202020u;
+                return (int)(f | (sg << 1) | (sg << 2));
+            };
+            const i64 b0 = (i64)(uint32_t)code(c.l0.x, c.h0.x) | (i64)(uint32_t)code(c.l0.y, c.h0.y) << 32;
+            const i64 b1 = (i64)(uint32_t)code(c.l1.x, c.h1.x) | (i64)(uint32_t)code(c.l1.y, c.h1.y) << 32;
+            const i64 a0 = (i64)c.x0.x | (i64)c.x0.y << 32, a1 = (i64)c.x1.x | (i64)c.x1.y << 32;
+            I = __builtin_amdgcn_mfma_i32_32x32x16_i8(a0, b0, z, 0, 0, 0);
+            I1 = __builtin_amdgcn_mfma_i32_32x32x16_i8(a1, b1, z, 0, 0, 0);
+            const uint32_t sc2 = c.sc >> (16 * (w & 1)); // (scales 2 w, 2 w + 1)
+            s0 = (int)(int8_t)(sc2 & 0xffu);
+            s1 = (int)(int8_t)((sc2 >> 8) & 0xffu);
+            f0 = h2f_g((uint16_t)(c.dw & 0xffffu));
+        }
+        __syncthreads(); // (xsl[buf] written; the previous super-block's term readers are done)
+        #pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 x4 = *(const float4 *)(&xsl[buf][w][8 * q + 4 * hi]);
+            const float xsq[4] = { x4.x, x4.y, x4.z, x4.w };
+            #pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int r = 4 * q + e;
+                float term;
+                if (TYPE == GW_Q4_K) {
+                    float pa = (f0 * xsq[e]) * (float)I[r];
+                    float pb = f1 * (xsq[e] * (float)I1[r]);
+                    term = pa - pb;
+                } else {
+                    int Ii = s0 * I[r] + s1 * I1[r];
+                    term = (f0 * xsq[e]) * (float)Ii;
+                }
+                Tl[w][r * 64 + lane] = term;
+            }
+        }
+        __syncthreads();
+        #pragma unroll
+        for (int g = 0; g < 8; g++) {
+            acc0 = acc0 + Tl[g][t];
+            acc1 = acc1 + Tl[g][t + 512];
+        }
+        return s + 1 < S;
+    };
+    // six register sets take turns, five super-blocks' loads in flight (named: an array of them was placed in scratch
+    // memory)
+    SkOps<TYPE> o0, o1, o2, o3, o4, o5;
+    load(o0, 0);
+    load(o1, 1);
+    load(o2, 2);
+    load(o3, 3);
+    load(o4, 4);
+    for (int s0 = 0;; s0 += 6) {
+        if (!step(o0, o5, s0) || !step(o1, o0, s0 + 1) || !step(o2, o1, s0 + 2) || !step(o3, o2, s0 + 3) ||
+            !step(o4, o3, s0 + 4) || !step(o5, o4, s0 + 5))
+            break;
+    }
+    #pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int o = t + 512 * k, r = o >> 6, ln = o & 63;
+        const int m = 8 * (r >> 2) + 4 * (ln >> 5) + (r & 3), n = n0 + (ln & 31);
+        if (m < M && n < N) {
+            float *po = out + (size_t)m * ldo + n;
+            const float v = k ? acc1 : acc0;
+            *po = mode == 1 ? *po + v : v;
+        }
+    }
+}
+
 // --------------------------------------------------------------------------------------------- K-quants
 
 // The batched GEMV of all three formats: out[m * ldo + row] (+)= W row . X row m for M <= 8 activation rows, R weight
@@ -721,9 +874,25 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
     }
     if (w->type == GW_Q8_0)
         return launch_gemv_mr<GW_Q8_0>((const uint8_t *)w->codes, w->scales, w->rows, w->cols, 0, xq, xs, ldx, M, out, ldo, mode, s);
-    // K-quants above 8 rows: the MFMA GEMM where it has 64 blocks or more (a block streams its 128 rows' full K in
-    // order, so a narrow matrix leaves the device idle), else the batched GEMV in passes of 8 rows
-    if ((w->type == GW_Q4_K || w->type == GW_Q6_K) && M > 8 && (size_t)((w->rows + GN - 1) / GN) * ((M + 31) / 32) >= 64) {
+    // K-quants, 9 .. 32 rows: the 32-row GEMM with the groups spread over a block's waves (a matrix of 32768 rows or
+    // more, the classifier: the 128-column MFMA GEMM, a block for every compute unit)
+    if ((w->type == GW_Q4_K || w->type == GW_Q6_K) && M > 8 && M <= 32 && !g_tile_rows && w->rows < 32768) {
+        hipEvent_t e0, e1;
+        gw_take_launch_events(&e0, &e1);
+        const dim3 grid((w->rows + 31) / 32);
+        if (w->type == GW_Q4_K)
+            hipExtLaunchKernelGGL((k_gemm_kq32<GW_Q4_K>), grid, dim3(SK_T), 0, s, e0, e1, 0, (const uint8_t *)w->blocks,
+                                  w->bstride, w->rows, w->cols, xq, xs, ldx, M, out, ldo, mode);
+        else
+            hipExtLaunchKernelGGL((k_gemm_kq32<GW_Q6_K>), grid, dim3(SK_T), 0, s, e0, e1, 0, (const uint8_t *)w->blocks,
+                                  w->bstride, w->rows, w->cols, xq, xs, ldx, M, out, ldo, mode);
+        return (int)hipGetLastError();
+    }
+    // K-quants above 32 rows: the MFMA GEMM where it has 64 blocks or more (a block streams its 128 rows' full K in
+    // order, so a narrow matrix leaves the device idle) or its row tile is forced, else the batched GEMV in passes of
+    // 8 rows
+    if ((w->type == GW_Q4_K || w->type == GW_Q6_K) && M > 8 &&
+        (g_tile_rows || (size_t)((w->rows + GN - 1) / GN) * ((M + 31) / 32) >= 64)) {
         hipEvent_t e0, e1;
         gw_take_launch_events(&e0, &e1);
         const int cus = gemm_cus(), nt = (w->rows + GN - 1) / GN;

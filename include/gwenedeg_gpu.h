@@ -211,8 +211,9 @@ int gw_kq_matmul(float *out, int type, const void *blocks, int N, int K, const i
                  void *stream);
 
 /* The row tile of the MFMA GEMMs (prefill and batched rows: k_gemm_q8 for Q8_0 above 32 rows, k_gemm_kq for Q4_K /
- * Q6_K above 8 rows): 0 chosen per launch (64-row tiles when they give each SIMD several waves, else 32; the
- * default), 32 or 64 forced. Returns the previous setting, or -1 (and changes nothing) for another value. A tuning
+ * Q6_K above 32 rows): 0 chosen per launch (64-row tiles when they give each SIMD several waves, else 32; a K-quant
+ * matrix too narrow for 64 blocks takes the batched GEMV; the default), 32 or 64 forced (and the K-quant GEMM
+ * taken whatever the width). Returns the previous setting, or -1 (and changes nothing) for another value. A tuning
  * and test hook with no counterpart in runq.h; results do not depend on it */
 int gw_matmul_tile_rows(int rows);
 

@@ -103,10 +103,12 @@ def test_q8_pack_and_block_sums(dev):
 
 
 @pytest.mark.parametrize("typ", [12, 14])
-@pytest.mark.parametrize("M,tile", [(1, 0), (3, 0), (6, 0), (9, 32), (40, 32), (40, 64), (100, 64)])
+@pytest.mark.parametrize("M,tile", [(1, 0), (3, 0), (6, 0), (9, 0), (20, 0), (32, 0), (40, 0), (40, 32), (40, 64),
+                                    (100, 64)])
 def test_kq_matmul_bitexact(dev, typ, M, tile):
-    """the K-quant operator against the oracle bit for bit: up to 8 rows the batched GEMV, above it the MFMA GEMM with
-    32- and 64-row tiles (N not a multiple of the 128-column tile)"""
+    """the K-quant operator against the oracle bit for bit: up to 8 rows the batched GEMV, 9 .. 32 the 32-row GEMM
+    (k_gemm_kq32), above it the MFMA GEMM with 32- and 64-row tiles (forced) or, this narrow, the GEMV again (N not a
+    multiple of the column tiles)"""
     torch, gw = dev
     from oracle import oracle as orc
     from gwenedeg_amd import synth
