@@ -172,7 +172,8 @@ __global__ __launch_bounds__(64) void k_qknorm_rope_store(float *__restrict__ qk
 //   scores: lane (position p, chunk c): the fma chain over dims 32c .. 32c + 31 of every vector; the 4 chunks of a
 //     position are neighbouring lanes, added in order (a = c0 + c1 + c2 + c3, left to right), times scale
 //   softmax: one wave per vector: m = max, e = exp_att(s - m), l = 16 lane chains + the tree
-//   o: lane (vector, dim pair): the fma chains over the positions in order
+//   o: lane (vector, dim pair): the fma chains over the positions in order, V from LDS (NQ = 16: its own buffer,
+//     staged with K; else the K buffer, rewritten once the scores are done: a block's LDS stays under half a CU's)
 // hd <= 128 (hd % 32 == 0), nq <= 16.
 #define ATT_NQ 16
 #define ATT_HDMAX 128
@@ -186,7 +187,8 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
                                                int nkv, int hd, float scale, const int *__restrict__ pos,
                                                uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc,
                                                float *__restrict__ part, int pstride) {
-    // V staged in LDS for NQ = 16 (prefill row blocks: 16 vectors read every V row), else read from memory by the chains
+    // V staged in its own LDS buffer for NQ = 16 (prefill row blocks), else into the K buffer once the scores are done
+    // (the block's LDS stays under half a CU's: two blocks per CU); its loads are issued with K's either way
     constexpr bool VL = NQ == 16;
     __shared__ __align__(16) uint8_t ks[16 * ATT_KTILE];
     __shared__ __align__(16) uint8_t vs[VL ? 16 * 32 * ATT_HDMAX : 16];
@@ -201,13 +203,12 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
     int nmx = pos[r0 + nr - 1] + 1 - kb * ATT_P;
     nmx = nmx < ATT_P ? nmx : ATT_P;
     int nbytes = (nmx + ATT_T - 1) / ATT_T * TB; // the tiles holding positions < nmx
-    // staging of K (and V when VL): 16 bytes per thread and round, up to 4 rounds (hd <= 128), loads issued before any
-    // use (otherwise V is read from memory by the o chains: a position's row is one coalesced 2 hd-byte load per wave)
+    // staging of K and V: 16 bytes per thread and round, up to 4 rounds (hd <= 128), loads issued before any use
     uint4 k0, k1, k2, k3, v0, v1, v2, v3;
 #define ATT_LD(k, KR, VR)                                                                                                \
     if ((t + ATT_TH * k) * 16 < nbytes) {                                                                            \
         KR = *(const uint4 *)(K + (t + ATT_TH * k) * 16);                                                             \
-        if (VL) VR = *(const uint4 *)(V + (t + ATT_TH * k) * 16);                                                     \
+        VR = *(const uint4 *)(V + (t + ATT_TH * k) * 16);                                                             \
     }
     ATT_LD(0, k0, v0) ATT_LD(1, k1, v1) ATT_LD(2, k2, v2) ATT_LD(3, k3, v3)
 #undef ATT_LD
@@ -264,6 +265,12 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
         }
     }
     __syncthreads();
+    if (!VL) { // V into the K buffer (its readers are done), position p's row at p hd 2 bytes
+#define ATT_SV(k, VR)                                                                                                    \
+        if ((t + ATT_TH * k) * 16 < nbytes) *(uint4 *)(ks + (t + ATT_TH * k) * 16) = VR;
+        ATT_SV(0, v0) ATT_SV(1, v1) ATT_SV(2, v2) ATT_SV(3, v3)
+#undef ATT_SV
+    }
     // softmax: wave v takes vector v
     int wave = t >> 6, lane = t & 63;
     if (wave < nq && np[wave] > 0) {
@@ -298,7 +305,7 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
         }
     }
     __syncthreads();
-    // o: lane (vector v = wave, dim pair d2): the chains over the positions in order, V pairs from memory, two register
+    // o: lane (vector v = wave, dim pair d2): the chains over the positions in order, V pairs from LDS, two register
     // sets of PB positions' loads alternating (a copy between sets would wait for the loads)
     {
         int v = wave, d2 = lane, i0 = 2 * d2;
@@ -306,7 +313,7 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
             const int n = np[v];
             int p = 0;
             float o0 = 0.0f, o1 = 0.0f;
-            const uint32_t *vb = (const uint32_t *)((VL ? (const uint8_t *)vs : V) + i0 * 2);
+            const uint32_t *vb = (const uint32_t *)((VL ? vs : ks) + i0 * 2);
             const int rs = hd >> 1; // (uint32 words per position's row)
             constexpr int PB = 16;
             uint32_t va[PB], vbb[PB];
