@@ -315,7 +315,7 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
             float o0 = 0.0f, o1 = 0.0f;
             const uint32_t *vb = (const uint32_t *)((VL ? vs : ks) + i0 * 2);
             const int rs = hd >> 1; // (uint32 words per position's row)
-            constexpr int PB = 16;
+            constexpr int PB = VL ? 16 : 8; // (8: 64 registers, two blocks per CU)
             uint32_t va[PB], vbb[PB];
             float ea[PB], eb[PB];
             auto ld = [&](uint32_t (&vv)[PB], float (&ee)[PB], int q0) {
@@ -364,7 +364,7 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
 }
 
 template <int NQ>
-__global__ __launch_bounds__(ATT_TH) void k_attn_part(const int4 *__restrict__ items, const float *__restrict__ qkv, int ldqkv,
+__global__ __launch_bounds__(ATT_TH, NQ <= 4 ? 8 : 4) void k_attn_part(const int4 *__restrict__ items, const float *__restrict__ qkv, int ldqkv,
                                                       int nh, int nkv, int hd, float scale, const int *__restrict__ pos,
                                                       uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc,
                                                       float *__restrict__ part, int pstride) {
