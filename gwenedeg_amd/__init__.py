@@ -111,6 +111,7 @@ _sig = {
     "rq_decode": (_I, [_P, _P, _I, ctypes.POINTER(_F)]),
     "rq_decode_hidden": (_I, [_P, _P, _I, ctypes.POINTER(_F), _F, _F]),
     "rq_prefill": (_I, [_P, _P, ctypes.POINTER(_I), _I, _I, _F, ctypes.POINTER(_F)]),
+    "fw_rows": (_I, [_P, _P, ctypes.POINTER(_I), _I, _I, _F, ctypes.POINTER(_F), _F, _F]),
     "rq_forward_batch": (_I, [_P, ctypes.POINTER(RqSegment), _I, _F, ctypes.POINTER(_F)]),
     "rq_logits_hash": (ctypes.c_ulonglong, [_F, _I]),
     "gw_ctx_argmax": (_I, [_P, ctypes.POINTER(_I), _I]),
@@ -284,6 +285,20 @@ class Ctx:
         if mode == RQ_LOGITS_LAST:
             return np.ctypeslib.as_array(p, shape=(self.model.vocab,)).copy()
         return None
+
+    def prefill_hidden(self, seq: Seq, tokens, mode: int = RQ_LOGITS_LAST):
+        """fw_rows: rq_prefill plus every row's final hidden state. Returns (logits as prefill returns them, hidden rows
+        (n x dim))"""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.zeros((len(t), self.model.vocab), np.float32) if mode == RQ_LOGITS_ALL else None
+        hid = np.zeros((len(t), self.model.dim), np.float32)
+        p = ctypes.POINTER(ctypes.c_float)()
+        self._check(lib.fw_rows(self._h, seq._h, _iptr(t), len(t), mode, _fptr(out), ctypes.byref(p), _fptr(hid), None), "fw_rows")
+        if mode == RQ_LOGITS_ALL:
+            return out, hid
+        if mode == RQ_LOGITS_LAST:
+            return np.ctypeslib.as_array(p, shape=(self.model.vocab,)).copy(), hid
+        return None, hid
 
     def forward_batch(self, segments: Sequence[Segment]):
         """Returns (logits rows in row order or None, hidden arrays per segment (or None))."""

@@ -815,14 +815,17 @@ int gw_forward_batch_device(RqCtx *c, const RqSegment *sg, int nseg) {
     return fw_batch(c, sg, nseg, NULL, NULL, 1);
 }
 
-int rq_prefill(RqCtx *c, RqSeq *s, const int *tokens, int n, int mode, float *out, float **logits) {
-    /* fw_rows (forward.c:3880-3916): chunks of max_batch rows, or token by token through the decode path */
-    int V = c->m->vocab, e = check_seq(c, s);
+int fw_rows(RqCtx *c, RqSeq *s, const int *tokens, int n, int mode, float *out, float **logits, float *hidden, const float *h_in) {
+    /* forward.c:3880-3916: tokens at positions len.. in chunks of max_batch rows, or token by token through the decode
+     * path (max_batch <= 1), the same results either way; every row's final hidden state (the normed row, dim floats)
+     * into hidden when given. h_in (an MTP view's input rows, Qwen3.5) is refused: no model here is such a view */
+    int V = c->m->vocab, dim = c->m->dim, e = check_seq(c, s);
     c->err[0] = 0;
     if (logits) *logits = NULL;
     if (e != RQ_OK) return e;
     if (n < 1 || mode < RQ_LOGITS_NONE || mode > RQ_LOGITS_ALL || (mode == RQ_LOGITS_ALL && !out))
         return ctx_fail(c, RQ_ERR_ARG, "bad prefill arguments (n %d, mode %d)", n, mode);
+    if (h_in) return ctx_fail(c, RQ_ERR_ARG, "h_in on a model that is not an MTP view");
     if (s->len + n > s->cap) return ctx_fail(c, RQ_ERR_CONTEXT, "%d tokens at position %d: past the capacity %d", n, s->len, s->cap);
     for (int i = 0; i < n; i++)
         if (tokens[i] < 0 || tokens[i] >= V) return ctx_fail(c, RQ_ERR_ARG, "token %d out of range", tokens[i]);
@@ -830,7 +833,7 @@ int rq_prefill(RqCtx *c, RqSeq *s, const int *tokens, int n, int mode, float *ou
     if (c->nb_max <= 1) {
         for (int i = 0; i < n && e == RQ_OK; i++) {
             int want = mode == RQ_LOGITS_ALL || (mode == RQ_LOGITS_LAST && i == n - 1);
-            e = decode_one(c, s, tokens[i], want ? c->logits : NULL, NULL);
+            e = decode_one(c, s, tokens[i], want ? c->logits : NULL, hidden ? hidden + (size_t)i * dim : NULL);
             if (mode == RQ_LOGITS_ALL && e == RQ_OK) memcpy(out + (size_t)i * V, c->logits, (size_t)V * sizeof(float));
         }
         lg = mode == RQ_LOGITS_ALL ? out : mode == RQ_LOGITS_LAST ? c->logits : NULL;
@@ -840,13 +843,17 @@ int rq_prefill(RqCtx *c, RqSeq *s, const int *tokens, int n, int mode, float *ou
             int k = n - i < nb ? n - i : nb;
             RqSegment sg = { s, tokens + i, k,
                              mode == RQ_LOGITS_ALL ? RQ_LOGITS_ALL : mode == RQ_LOGITS_LAST && i + k == n ? RQ_LOGITS_LAST : RQ_LOGITS_NONE,
-                             NULL, NULL };
+                             hidden ? hidden + (size_t)i * dim : NULL, NULL };
             e = rq_forward_batch(c, &sg, 1, mode == RQ_LOGITS_ALL ? out + (size_t)i * V : NULL, &lg);
         }
         lg = mode == RQ_LOGITS_ALL ? out : lg;
     }
     if (logits && e == RQ_OK) *logits = lg;
     return e;
+}
+
+int rq_prefill(RqCtx *c, RqSeq *s, const int *tokens, int n, int mode, float *out, float **logits) {
+    return fw_rows(c, s, tokens, n, mode, out, logits, NULL, NULL);
 }
 
 int gw_ctx_gemv_sweep(RqCtx *c, int reps, double *seconds, double *bytes, int *launches) {

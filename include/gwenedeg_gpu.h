@@ -141,6 +141,12 @@ void *ctx_sampler_scratch(RqCtx *c);
 void *ctx_sampler_scratch_threads(RqCtx *c, int nt);
 int ctx_vocab(const RqCtx *c);
 
+/* The reference's internal prefill with hidden rows that its spec.c links against (internal.h:339, forward.c:3880-3916):
+ * rq_prefill's rows (chunks of max_batch, or token by token with max_batch <= 1) with every row's final hidden state
+ * (the final-normed row, dim floats) into hidden (n x dim; NULL: none). h_in, an MTP view's input rows (Qwen3.5),
+ * is refused with RQ_ERR_ARG: no model loaded here is such a view. rq_prefill is fw_rows without hidden and h_in */
+int fw_rows(RqCtx *c, RqSeq *s, const int *tokens, int n, int mode, float *out, float **logits, float *hidden, const float *h_in);
+
 /* ------------------------------------------------------------------------------------- extensions (gw_) */
 
 /* Device-side greedy sampling of a pass's logits rows: the first maximum of each row (the reference's

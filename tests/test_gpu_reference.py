@@ -148,3 +148,29 @@ def test_config4_long_context_8b_shape(gw, orc, tmp_path):
             tok = int(np.argmax(lg))
             assert tok == int(rtok[step])
             lg = c.decode(s, tok)
+
+
+@pytest.mark.parametrize("shape,layers", [("qwen3_0_6b", 3), ("qwen3_4b_q4km", 2)])
+def test_hidden_rows_bit_identical(gw, orc, tmp_path, shape, layers):
+    """the rows' final hidden states (after output_norm: runq.h:347-350, :369) against the reference's
+    rq_decode_hidden token by token, bit for bit with the logits: rq_decode_hidden one row at a time, and fw_rows
+    (internal.h:339, the spec loop's prefill) in chunks of 8 rows and as one 40-row pass"""
+    path, d = _synth(str(tmp_path), shape, n_layers=layers)
+    m = gw.Model(path, ctx_len=256)
+    if not _exact(gw):
+        pytest.skip("this host does not provide the reference's float operations (AVX-512)")
+    ids = np.random.default_rng(7).integers(0, m.vocab, 40).astype(np.int32)
+    _, rlg, rhid, _ = orc.run_ref_driver(path, ids, str(tmp_path / "ref"), threads=_threads(), cap=256, hidden=True)
+    assert rhid.shape == (40, m.dim)
+    c1 = m.ctx(max_batch=1, max_ctx=256)
+    s1 = m.seq(256)
+    for j, t in enumerate(ids):
+        lg, hid = c1.decode_hidden(s1, int(t))
+        assert np.array_equal(_bits(hid), _bits(rhid[j])), f"rq_decode_hidden row {j}"
+        assert np.array_equal(_bits(lg), _bits(rlg[j])), f"rq_decode_hidden logits row {j}"
+    for nb in (8, 64):
+        c = m.ctx(max_batch=nb, max_ctx=256)
+        s = m.seq(256)
+        lg, hid = c.prefill_hidden(s, ids, mode=gw.RQ_LOGITS_ALL)
+        assert np.array_equal(_bits(hid), _bits(rhid)), f"fw_rows (max_batch {nb}): hidden rows"
+        assert np.array_equal(_bits(lg), _bits(rlg)), f"fw_rows (max_batch {nb}): logits rows"
