@@ -105,6 +105,17 @@ int rq_seq_common_prefix(const RqSeq *s, const int *tokens, int n) {
 
 int rq_seq_release(RqSeq *s, int keep) { return !s || keep < 0 ? RQ_ERR_ARG : RQ_OK; }
 
+/* Qwen3.5's checkpoints: a Qwen3 sequence holds none (runq.h:257-259) */
+int rq_seq_checkpoint_drop(RqSeq *s, int pos) { (void)s; (void)pos; return RQ_ERR_ARG; }
+
+void rq_seq_resident(const RqSeq *s, RqSeqMem *out) {
+    /* runq.h:271-274: the K / V halves are device memory allocated whole at rq_seq_new, so the bound is all of it */
+    memset(out, 0, sizeof(*out));
+    if (!s) return;
+    out->kv = rq_seq_kv_bytes(s, s->cap);
+    out->total = out->kv;
+}
+
 size_t rq_seq_kv_bytes(const RqSeq *s, int n) {
     n = n < 0 ? 0 : n > s->cap ? s->cap : n;
     size_t nb = ((size_t)n + GW_ATT_P - 1) / GW_ATT_P;
@@ -226,6 +237,77 @@ static int ctx_lg(RqCtx *c, size_t rows) {
     HIPCHK(c, "hipHostMalloc (logits)", hipHostMalloc((void **)&c->lg_h, rows * c->m->vocab * sizeof(float), hipHostMallocDefault));
     c->lg_h_rows = rows;
     return RQ_OK;
+}
+
+static size_t ctx_bytes(const RqModel *m, int B, int max_ctx) {
+    /* what rq_ctx_new allocates for B rows and max_ctx positions (device buffers, the attention partials, the host
+     * logits row) */
+    size_t dim = m->dim, H = m->hidden, qd = (size_t)m->n_heads * m->head_dim, kvd = (size_t)m->n_kv_heads * m->head_dim;
+    size_t kmax = dim > qd ? dim : qd;
+    kmax = H > kmax ? H : kmax;
+    size_t row = dim * 4 * 3 + (qd + 2 * kvd) * 4 + 2 * H * 4 + kmax + kmax / 32 * 4 + H + H / 32 * 4 + (size_t)m->vocab * 4 + 4 + 512;
+    size_t nb = ((size_t)max_ctx + GW_ATT_P - 1) / GW_ATT_P;
+    return (size_t)B * row + (size_t)B * m->n_heads * nb * (m->head_dim + 2) * 4 + (size_t)m->vocab * 4;
+}
+
+int rq_seq_mem(const RqModel *m, int capacity, int kv_type, RqSeqMem *mem) {
+    /* model.c:765-772: one sequence's memory as rq_seq_new allocates it (RQ_ERR_ARG as rq_seq_new): the K / V halves
+     * in device memory (whole 256-position blocks) and the token array; no recurrent state (Qwen3) */
+    memset(mem, 0, sizeof(*mem));
+    if (!m) return RQ_ERR_STATE;
+    if (capacity <= 0) capacity = m->seq_len;
+    if (capacity > m->seq_len || kv_type != RQ_KV_F16) return RQ_ERR_ARG;
+    size_t kv_len = ((size_t)capacity + GW_ATT_P - 1) / GW_ATT_P * GW_ATT_P;
+    mem->kv = (size_t)m->n_layers * kv_len * m->n_kv_heads * m->head_dim * 2 * 2 + (size_t)capacity * sizeof(int);
+    mem->total = mem->kv;
+    return RQ_OK;
+}
+
+int rq_model_mem(const RqModel *m, RqModelMem *mem) {
+    /* model.c:758-763 over this library's memory: weights = the device copies of the matrices, norms and tables of the
+     * model; runtime = a context of RQ_BATCH_MAX rows at the model's context length plus the exactness tables each
+     * device holds (288 MiB); seq = one sequence of that length. No budget is checked (budget 0, budget_src 0); a
+     * one-row pass reads every weight (read = weights) */
+    memset(mem, 0, sizeof(*mem));
+    if (!m) return RQ_ERR_STATE;
+    mem->weights = m->dev_bytes;
+    mem->runtime = ctx_bytes(m, RQ_BATCH_MAX, m->seq_len) + ((size_t)288 << 20);
+    rq_seq_mem(m, m->seq_len, RQ_KV_F16, &mem->seq);
+    mem->total = mem->weights + mem->runtime + mem->seq.total;
+    mem->read = mem->weights;
+    return RQ_OK;
+}
+
+int rq_pass_times(const RqModel *m, int reps, double *t1, double *t4) {
+    /* runq.h:196-199: a decode step and a 4-row pass with every row's logits at position 32 (rq_seq_fill_synthetic),
+     * the fastest of reps each after a warm-up, seconds; its own context and sequence */
+    if (!m || reps < 1 || !t1 || !t4) return RQ_ERR_ARG;
+    int e = RQ_OK;
+    RqCtx *c = rq_ctx_new(m, 4, 64, &e);
+    if (!c) return e;
+    RqSeq *s = rq_seq_new(m, 64, RQ_KV_F16, &e);
+    float *out = malloc((size_t)4 * m->vocab * sizeof(float));
+    if (!s || !out) e = e != RQ_OK ? e : RQ_ERR_NOMEM;
+    const int toks[4] = { 1, 2, 3, 4 };
+    double b1 = 1e30, b4 = 1e30;
+    for (int r = -1; r < reps && e == RQ_OK; r++) { /* (r = -1: the warm-up) */
+        float *lg = NULL;
+        if ((e = rq_seq_fill_synthetic(s, 32, 1)) != RQ_OK) break;
+        double t = rq_now();
+        if ((e = rq_decode(c, s, 1, &lg)) != RQ_OK) break;
+        t = rq_now() - t;
+        if (r >= 0 && t < b1) b1 = t;
+        if ((e = rq_seq_fill_synthetic(s, 32, 1)) != RQ_OK) break;
+        t = rq_now();
+        if ((e = rq_prefill(c, s, toks, 4, RQ_LOGITS_ALL, out, NULL)) != RQ_OK) break;
+        t = rq_now() - t;
+        if (r >= 0 && t < b4) b4 = t;
+    }
+    free(out);
+    rq_seq_free(s);
+    rq_ctx_free(c);
+    if (e == RQ_OK) *t1 = b1, *t4 = b4;
+    return e;
 }
 
 RqCtx *rq_ctx_new(const RqModel *m, int nb_max, int max_ctx, int *err) {

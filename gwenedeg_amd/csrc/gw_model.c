@@ -41,6 +41,45 @@ const char *rq_strerror(int e) {
     }
 }
 
+double rq_mem_available(void) {
+    /* runq.h:172-173: MemAvailable of /proc/meminfo in bytes, -1 where unknown */
+    FILE *f = fopen("/proc/meminfo", "r");
+    char line[256];
+    long long kb = -1;
+    while (f && fgets(line, sizeof(line), f))
+        if (sscanf(line, "MemAvailable: %lld kB", &kb) == 1) break;
+    if (f) fclose(f);
+    return kb >= 0 ? (double)kb * 1024.0 : -1.0;
+}
+
+RqModel *rq_mtp_load(const RqModel *target, const RqMtpOpts *o, char *err, size_t errlen) {
+    /* runq.h:100-112: MTP views are Qwen3.5's; a Qwen3 model has no MTP block */
+    (void)target;
+    (void)o;
+    if (err && errlen) snprintf(err, errlen, "no MTP block (MTP views are Qwen3.5's; this library loads Qwen3 models)");
+    return NULL;
+}
+
+int rq_repack_info(const RqModel *m, RqRepackInfo *info) {
+    /* runq.h:175-195: the CPU repack does not exist here (available 0, no types): the weights are always the device
+     * layout, whose bytes are the weights' */
+    memset(info, 0, sizeof(*info));
+    if (!m) return RQ_ERR_STATE;
+    info->weights = m->dev_bytes;
+    return RQ_OK;
+}
+
+int rq_dequant_rows(const RqModel *m, const char *name, size_t name_len, long r0, long nr, float **rows, float **packed,
+                    int *ncols, int *npacked, char *err, size_t errlen) {
+    /* runq.h:716-720 (a test hook reading the file's blocks): the file is not kept after the load here */
+    (void)m, (void)name, (void)name_len, (void)r0, (void)nr, (void)ncols;
+    if (rows) *rows = NULL;
+    if (packed) *packed = NULL;
+    if (npacked) *npacked = 0;
+    if (err && errlen) snprintf(err, errlen, "rq_dequant_rows: the weights live in device memory; the file is not kept");
+    return RQ_ERR_STATE;
+}
+
 double rq_now(void) {
     struct timespec ts;
     clock_gettime(CLOCK_MONOTONIC, &ts);

@@ -79,6 +79,57 @@ typedef struct {
 } RqModelInfo;
 void rq_model_info(const RqModel *m, RqModelInfo *info);
 
+/* memory estimates: runq.h:150-171 (the layouts are runq.h's). This library counts device memory: the weights' device
+ * copies, a context of RQ_BATCH_MAX rows plus the 288 MiB of exactness tables per device, and a sequence's K / V
+ * halves; there is no recurrent state, no checkpoint and no budget check (budget 0, budget_src 0) */
+typedef struct {
+    size_t kv;
+    size_t state;
+    int checkpoints;
+    size_t total;
+} RqSeqMem; /* runq.h:152-157 */
+typedef struct {
+    size_t weights;
+    size_t runtime;
+    RqSeqMem seq;
+    size_t total;
+    double budget;
+    int budget_src;
+    size_t read;
+} RqModelMem; /* runq.h:158-167 */
+int rq_model_mem(const RqModel *m, RqModelMem *mem);                          /* runq.h:168 */
+int rq_seq_mem(const RqModel *m, int capacity, int kv_type, RqSeqMem *mem);    /* runq.h:171 */
+double rq_mem_available(void);                                                /* runq.h:173 */
+/* the CPU repack (runq.h:175-195) does not exist here: available 0, no types, weights = the device bytes */
+#define RQ_REPACK_TYPES 4
+typedef struct {
+    const char *type;
+    int bit;
+    int repacked;
+    int mats;
+    double share;
+    size_t bytes, extra;
+} RqRepackType;
+typedef struct {
+    int available;
+    int n;
+    RqRepackType t[RQ_REPACK_TYPES];
+    size_t weights;
+    size_t extra;
+} RqRepackInfo;
+int rq_repack_info(const RqModel *m, RqRepackInfo *info);                     /* runq.h:195 */
+/* runq.h:196-199: a decode step and a 4-row all-logits pass at position 32, the fastest of reps, seconds */
+int rq_pass_times(const RqModel *m, int reps, double *t1, double *t4);
+/* MTP views (runq.h:100-112) are Qwen3.5's: NULL, with the reason in err */
+typedef struct {
+    int vocab;
+    double mem;
+} RqMtpOpts;
+RqModel *rq_mtp_load(const RqModel *target, const RqMtpOpts *o, char *err, size_t errlen);
+/* runq.h:716-720's test hook: RQ_ERR_STATE (the file is not kept after the load) */
+int rq_dequant_rows(const RqModel *m, const char *name, size_t name_len, long r0, long nr, float **rows, float **packed,
+                    int *ncols, int *npacked, char *err, size_t errlen);
+
 /* runq.h:214-219 */
 enum { RQ_KV_F32 = 0, RQ_KV_BF16 = 1, RQ_KV_F16 = 2, RQ_KV_Q8 = 3, RQ_KV_BF16_DOT = 5, RQ_KV_F16_DOT = 6, RQ_KV_Q8_DOT = 7,
        RQ_KV_Q4 = 8, RQ_KV_Q4K4 = 9, RQ_KV_Q4_DOT = 12, RQ_KV_Q4K4_DOT = 13, RQ_KV_DEFAULT = RQ_KV_F16 };
@@ -97,11 +148,13 @@ int rq_seq_checkpoint_rows(RqSeq *s, int pos, int n);                     /* run
 void rq_seq_checkpoint_rows_drop(RqSeq *s);                               /* runq.h:248 */
 int rq_seq_set_checkpoints(RqSeq *s, int n);                              /* runq.h:252 */
 int rq_seq_checkpoints(const RqSeq *s, int *pos, int max);                /* runq.h:256: 0 */
+int rq_seq_checkpoint_drop(RqSeq *s, int pos);                            /* runq.h:259: RQ_ERR_ARG (none held) */
 int rq_seq_len(const RqSeq *s);                                           /* runq.h:260 */
 int rq_seq_capacity(const RqSeq *s);                                      /* runq.h:261 */
 const int *rq_seq_tokens(const RqSeq *s);                                 /* runq.h:262 */
 int rq_seq_common_prefix(const RqSeq *s, const int *tokens, int n);       /* runq.h:263 */
 int rq_seq_release(RqSeq *s, int keep);                                   /* runq.h:270 */
+void rq_seq_resident(const RqSeq *s, RqSeqMem *out);                      /* runq.h:274: all of its device K / V */
 size_t rq_seq_kv_bytes(const RqSeq *s, int n);                            /* runq.h:277 */
 int rq_seq_copy(RqSeq *dst, const RqSeq *src, int n);                     /* runq.h:282: device-to-device */
 void rq_seq_seed(RqSeq *s, unsigned long long seed);                      /* runq.h:315 */

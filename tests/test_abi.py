@@ -33,13 +33,18 @@ def test_python_binding_covers_the_passes():
 
 
 def _offsets(header_dir, tmp):
-    """sizes and field offsets of RqModelOpts / RqModelInfo / RqSegment as gcc lays them out from a header"""
+    """sizes and field offsets of RqModelOpts / RqModelInfo / RqSegment / RqSeqMem / RqModelMem as gcc lays them out
+    from a header"""
     import subprocess
     src = os.path.join(tmp, "off.c")
     hdr = "gwenedeg_gpu.h" if os.path.exists(os.path.join(header_dir, "gwenedeg_gpu.h")) else "runq.h"
     fields = {"RqModelOpts": ["ctx_len", "no_tokenizer", "mem", "kv_bits", "repack"],
               "RqModelInfo": ["vocab_size", "warning", "chat", "rope_theta", "linear_layers", "fingerprint"],
-              "RqSegment": ["seq", "tokens", "n", "logits", "hidden", "h_in"]}
+              "RqSegment": ["seq", "tokens", "n", "logits", "hidden", "h_in"],
+              "RqSeqMem": ["kv", "state", "checkpoints", "total"],
+              "RqModelMem": ["weights", "runtime", "seq", "total", "budget", "budget_src", "read"],
+              "RqRepackInfo": ["available", "n", "t", "weights", "extra"],
+              "RqMtpOpts": ["vocab", "mem"]}
     lines = [f'#include "{hdr}"', "#include <stdio.h>", "#include <stddef.h>", "int main(void) {"]
     for t, fs in fields.items():
         lines.append(f'printf("{t} %zu\\n", sizeof({t}));')
@@ -105,3 +110,38 @@ def test_one_hip_runtime_per_process():
     assert out.returncode == 0, out.stderr[-2000:]
     n = int(out.stdout.split()[0])
     assert n == 1, out.stdout
+
+
+# What each of the reference's host modules still needs once libgwenedeg_amd.so replaces its model.o, gguf.o, forward.o
+# and seqfile.o (and gguf.o is kept for the tokenizer): the functions outside the hot path that stay with the host
+# (model.c's chat templates and load error helper, seqfile.c's KV disk tier). Everything else on the reference's
+# runq.h / internal.h surface those modules call resolves to the library.
+HOST_NEEDS = {
+    "sampler": set(), "threads": set(), "spec": set(), "constrain": set(), "http": set(), "json": set(),
+    "chat": {"chat_gen_suffix"},
+    "tokenizer": {"load_fail"},
+    "engine": {"rq_seq_file_info", "rq_seq_file_keep", "rq_seq_load", "rq_seq_save", "rq_seq_save_bytes"},
+    "cli": {"rq_chat_check", "rq_chat_name"},
+    "serve": {"rq_chat_check", "rq_chat_name"},
+    "tools": {"rq_chat_name"},
+}
+
+
+def test_reference_host_modules_link():
+    """the reference's host modules (compiled from its sources by oracle/Makefile into oracle/_ref) against the
+    library's exports: the unresolved symbols of the reference's own namespace are exactly HOST_NEEDS"""
+    import subprocess
+    ref = os.path.join(ROOT, "oracle", "_ref")
+    objs = {m: os.path.join(ref, m + ".o") for m in list(HOST_NEEDS) + ["gguf"]}
+    if not all(os.path.exists(p) for p in objs.values()):
+        pytest.skip("the reference's host objects are not built (oracle/Makefile needs the reference tree)")
+    def syms(args, path):
+        out = subprocess.run(["nm", *args, path], capture_output=True, text=True, check=True).stdout
+        return {ln.split()[-1] for ln in out.splitlines() if ln.strip()}
+    provided = syms(["-D", "--defined-only"], os.path.join(ROOT, "gwenedeg_amd", "lib", "libgwenedeg_amd.so"))
+    for p in objs.values():
+        provided |= syms(["--defined-only"], p)
+    ours = ("rq_", "gguf", "load_", "chat_", "fw_", "seq_", "ctx_", "embed_", "forward_", "mtp_", "kq_", "q8p_")
+    for mod, need in HOST_NEEDS.items():
+        und = {s for s in syms(["-u"], objs[mod]) if s.startswith(ours)} - provided
+        assert und == need, f"{mod}.o: unresolved {sorted(und)}, documented {sorted(need)}"
