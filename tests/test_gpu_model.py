@@ -162,3 +162,33 @@ def test_decode_greedy_equals_step_by_step(gw, synth_models, shape, n_prompt, st
     a = c.decode(s1, 7)
     b = c.decode(s2, 7)
     assert _bits_equal(a, b)
+
+
+def test_memory_and_pass_times(gw, synth_models):
+    """rq_model_mem / rq_seq_mem / rq_seq_resident (runq.h:150-171, :274) count the device bytes the library holds,
+    and rq_pass_times (runq.h:196-199) times a decode step and a 4-row pass on its own context"""
+    import ctypes
+    class SeqMem(ctypes.Structure):
+        _fields_ = [("kv", ctypes.c_size_t), ("state", ctypes.c_size_t), ("checkpoints", ctypes.c_int), ("total", ctypes.c_size_t)]
+    class ModelMem(ctypes.Structure):
+        _fields_ = [("weights", ctypes.c_size_t), ("runtime", ctypes.c_size_t), ("seq", SeqMem), ("total", ctypes.c_size_t),
+                    ("budget", ctypes.c_double), ("budget_src", ctypes.c_int), ("read", ctypes.c_size_t)]
+    lib = gw.lib
+    path = synth_models("tiny_gqa4")
+    m = gw.Model(path, ctx_len=1024)
+    mm = ModelMem()
+    assert lib.rq_model_mem(ctypes.c_void_p(m._h), ctypes.byref(mm)) == 0
+    assert mm.weights > 0 and mm.read == mm.weights and mm.budget == 0
+    assert mm.total == mm.weights + mm.runtime + mm.seq.total
+    sm = SeqMem()
+    assert lib.rq_seq_mem(ctypes.c_void_p(m._h), 300, 2, ctypes.byref(sm)) == 0
+    s = m.seq(300)
+    lib.rq_seq_kv_bytes.restype = ctypes.c_size_t
+    assert sm.kv == lib.rq_seq_kv_bytes(ctypes.c_void_p(s._h), 300) and sm.total == sm.kv and sm.state == 0
+    res = SeqMem()
+    lib.rq_seq_resident(ctypes.c_void_p(s._h), ctypes.byref(res))
+    assert res.kv == sm.kv
+    assert lib.rq_seq_mem(ctypes.c_void_p(m._h), 300, 0, ctypes.byref(sm)) != 0  # (f32 KV: not supported, RQ_ERR_ARG)
+    t1, t4 = ctypes.c_double(), ctypes.c_double()
+    assert lib.rq_pass_times(ctypes.c_void_p(m._h), 2, ctypes.byref(t1), ctypes.byref(t4)) == 0
+    assert 0 < t1.value < 1 and 0 < t4.value < 1
