@@ -446,9 +446,11 @@ void rq_model_free(RqModel *m) {
 }
 
 static unsigned long long fingerprint(const uint8_t *map, size_t size) {
-    /* the file's size, its first MiB and last 64 KiB (FNV-1a), as the reference's owner check of saved sequences */
-    unsigned long long h = 1469598103934665603ull ^ (unsigned long long)size;
+    /* model.c:949-953: FNV-1a 64 over the file size's 8 bytes (little-endian), its first MiB and its last 64 KiB: the
+     * owner of saved sequences (rq_seq_save) and RqModelInfo.fingerprint, equal to the reference's for the same file */
+    unsigned long long h = 1469598103934665603ull, sz = (unsigned long long)size;
     size_t a = size < (1u << 20) ? size : (1u << 20), b = size < 65536 ? size : 65536;
+    for (int i = 0; i < 8; i++) h = (h ^ ((sz >> (8 * i)) & 0xffu)) * 1099511628211ull;
     for (size_t i = 0; i < a; i++) h = (h ^ map[i]) * 1099511628211ull;
     for (size_t i = size - b; i < size; i++) h = (h ^ map[i]) * 1099511628211ull;
     return h;

@@ -157,6 +157,25 @@ int rq_seq_release(RqSeq *s, int keep);                                   /* run
 void rq_seq_resident(const RqSeq *s, RqSeqMem *out);                      /* runq.h:274: all of its device K / V */
 size_t rq_seq_kv_bytes(const RqSeq *s, int n);                            /* runq.h:277 */
 int rq_seq_copy(RqSeq *dst, const RqSeq *src, int n);                     /* runq.h:282: device-to-device */
+
+/* Saved sequences, the KV disk tier (runq.h:283-314; seqfile.c's file format, version 1, so files move between this
+ * library and the reference for the same model file): rq_seq_save writes positions 0..len-1 (tokens, K / V blocks
+ * through a host staging buffer, the RNG state) as path.tmp, synced, then renamed to path; rq_seq_load restores the
+ * first n positions. RQ_ERR_IO, RQ_ERR_MISMATCH (another model file, shape or KV type; a corrupt header) */
+#define RQ_CHECKPOINTS_MAX 32
+typedef struct {
+    int len;
+    int kv_type;
+    int linear;
+    int n_ck;
+    int ck[RQ_CHECKPOINTS_MAX];
+    long long bytes;
+} RqSeqFile; /* runq.h:295-302 */
+int rq_seq_save(const RqSeq *s, const char *path);                                  /* runq.h:293 */
+long long rq_seq_save_bytes(const RqSeq *s);                                        /* runq.h:294 */
+int rq_seq_file_info(const RqModel *m, const char *path, RqSeqFile *info, int **tokens); /* runq.h:305 */
+int rq_seq_file_keep(const RqSeqFile *f, int n);                                    /* runq.h:308 */
+int rq_seq_load(RqSeq *dst, const char *path, int n);                               /* runq.h:314 */
 void rq_seq_seed(RqSeq *s, unsigned long long seed);                      /* runq.h:315 */
 unsigned long long *rq_seq_rng(RqSeq *s);                                 /* runq.h:319 */
 int rq_seq_fill_synthetic(RqSeq *s, int n, unsigned long long seed);      /* runq.h:726 */

@@ -105,7 +105,8 @@ int main(int argc, char **argv) {
             }
             fclose(hf);
             free(hid);
-            printf("{\"threads\": %d, \"vocab\": %d, \"dim\": %d, \"prompt\": %d}\n", rq_threads(), V, info.dim, n);
+            printf("{\"threads\": %d, \"vocab\": %d, \"dim\": %d, \"prompt\": %d, \"fingerprint\": \"%016llx\"}\n", rq_threads(), V,
+                   info.dim, n, (unsigned long long)info.fingerprint);
             if (lf) fclose(lf);
             return 0;
         }
@@ -137,9 +138,9 @@ int main(int argc, char **argv) {
     if (lf) fclose(lf);
     if (tf) fclose(tf);
     printf("{\"threads\": %d, \"vocab\": %d, \"prompt\": %d, \"seqs\": %d, \"steps\": %d, \"prefill_s\": %.6f, "
-           "\"decode_s\": %.6f, \"prefill_tok_s\": %.3f, \"decode_tok_s\": %.3f}\n",
+           "\"decode_s\": %.6f, \"prefill_tok_s\": %.3f, \"decode_tok_s\": %.3f, \"fingerprint\": \"%016llx\"}\n",
            rq_threads(), V, n, ns, steps, tp_best, td_best, tp_best > 0 ? (double)n * ns / tp_best : 0.0,
-           td_best > 0 && steps ? (double)steps * ns / td_best : 0.0);
+           td_best > 0 && steps ? (double)steps * ns / td_best : 0.0, (unsigned long long)info.fingerprint);
     for (int i = 0; i < ns; i++) rq_seq_free(sq[i]);
     rq_ctx_free(c);
     rq_model_free(m);

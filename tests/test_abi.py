@@ -44,7 +44,8 @@ def _offsets(header_dir, tmp):
               "RqSeqMem": ["kv", "state", "checkpoints", "total"],
               "RqModelMem": ["weights", "runtime", "seq", "total", "budget", "budget_src", "read"],
               "RqRepackInfo": ["available", "n", "t", "weights", "extra"],
-              "RqMtpOpts": ["vocab", "mem"]}
+              "RqMtpOpts": ["vocab", "mem"],
+              "RqSeqFile": ["len", "kv_type", "linear", "n_ck", "ck", "bytes"]}
     lines = [f'#include "{hdr}"', "#include <stdio.h>", "#include <stddef.h>", "int main(void) {"]
     for t, fs in fields.items():
         lines.append(f'printf("{t} %zu\\n", sizeof({t}));')
@@ -114,13 +115,13 @@ def test_one_hip_runtime_per_process():
 
 # What each of the reference's host modules still needs once libgwenedeg_amd.so replaces its model.o, gguf.o, forward.o
 # and seqfile.o (and gguf.o is kept for the tokenizer): the functions outside the hot path that stay with the host
-# (model.c's chat templates and load error helper, seqfile.c's KV disk tier). Everything else on the reference's
+# (model.c's chat templates and load error helper). Everything else on the reference's
 # runq.h / internal.h surface those modules call resolves to the library.
 HOST_NEEDS = {
     "sampler": set(), "threads": set(), "spec": set(), "constrain": set(), "http": set(), "json": set(),
     "chat": {"chat_gen_suffix"},
     "tokenizer": {"load_fail"},
-    "engine": {"rq_seq_file_info", "rq_seq_file_keep", "rq_seq_load", "rq_seq_save", "rq_seq_save_bytes"},
+    "engine": set(),
     "cli": {"rq_chat_check", "rq_chat_name"},
     "serve": {"rq_chat_check", "rq_chat_name"},
     "tools": {"rq_chat_name"},
