@@ -132,6 +132,7 @@ _sig = {
     "gw_q8_block_sums": (_I, [_P, _P, _I, _I, _P, _I, _P]),
     "gw_kq_matmul": (_I, [_P, _I, _P, _I, _I, _P, _P, _I, _P]),
     "gw_matmul_tile_rows": (_I, [_I]),
+    "gw_gemv_warm_next": (_I, [_I]),
 }
 for _name, (_res, _args) in _sig.items():
     _fn = getattr(lib, _name)

@@ -519,25 +519,28 @@ static int fused_layer(RqCtx *c, int l, RqSeq *sq, int pos, const int *pos_d) {
     const GwLayer *y = &m->layer[l];
     hipStream_t s = c->stream;
     int nh = m->n_heads, hd = m->head_dim, nb = pos / GW_ATT_P + 1;
+    /* (the matmul after w2: the next layer's qkv, or after the last layer the classifier) */
+    const GwMat *nx = l + 1 < m->n_layers ? &m->layer[l + 1].qkv[0] : &m->cls;
+    const int nxr = l + 1 < m->n_layers ? GW_GV_R_QKV : GW_GV_R_CLS;
     pf_mark(c, GW_PF_QKV);
-    KCHK(gw_k_gemv1_norm(&y->qkv[0], GW_GV_R_QKV, c->x, y->att_norm, c->qkv, 0, 0, s));
+    KCHK(gw_k_gemv1_norm(&y->qkv[0], GW_GV_R_QKV, c->x, y->att_norm, c->qkv, 0, 0, &y->wo, GW_GV_R_WO, s));
     pf_mark(c, GW_PF_ATT);
     KCHK(gw_k_attn_decode(c->qkv, nh, m->n_kv_heads, hd, m->att_scale, y->q_norm, y->k_norm, m->rope, pos,
                           sq->kc + (size_t)l * seq_layer_elems(sq), sq->vc + (size_t)l * seq_layer_elems(sq), c->part,
                           c->pstride, s));
     if (nb <= GW_GV_NBMAX) {
         pf_mark(c, GW_PF_WO);
-        KCHK(gw_k_gemv1_combine(&y->wo, GW_GV_R_WO, c->part, c->pstride, hd, nb, c->x, 1, s));
+        KCHK(gw_k_gemv1_combine(&y->wo, GW_GV_R_WO, c->part, c->pstride, hd, nb, c->x, 1, &y->w13[0], GW_GV_R_W13, s));
     } else {
         pf_mark(c, GW_PF_COMBINE);
         KCHK(gw_k_attn_combine_quant(c->part, c->pstride, nh, hd, pos_d, 1, c->xq, c->xs, c->kmax, NULL, s));
         pf_mark(c, GW_PF_WO);
-        KCHK(gw_k_gemv1_q(&y->wo, GW_GV_R_WO, c->xq, c->xs, c->x, 1, s));
+        KCHK(gw_k_gemv1_q(&y->wo, GW_GV_R_WO, c->xq, c->xs, c->x, 1, &y->w13[0], GW_GV_R_W13, s));
     }
     pf_mark(c, GW_PF_W13);
-    KCHK(gw_k_gemv1_norm(&y->w13[0], GW_GV_R_W13, c->x, y->ffn_norm, c->hb, 0, y->w13_il, s));
+    KCHK(gw_k_gemv1_norm(&y->w13[0], GW_GV_R_W13, c->x, y->ffn_norm, c->hb, 0, y->w13_il, &y->w2, GW_GV_R_W2, s));
     pf_mark(c, GW_PF_W2);
-    KCHK(gw_k_gemv1_qf(&y->w2, GW_GV_R_W2, c->hb, c->x, 1, s));
+    KCHK(gw_k_gemv1_qf(&y->w2, GW_GV_R_W2, c->hb, c->x, 1, nx, nxr, s));
     return RQ_OK;
 }
 
@@ -611,7 +614,7 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
         }
         if (fused) {
             pf_mark(c, GW_PF_QKV);
-            KCHK(gw_k_gemv1_norm(&y->qkv[0], GW_GV_R_QKV, c->x, y->att_norm, c->qkv, 0, 0, s));
+            KCHK(gw_k_gemv1_norm(&y->qkv[0], GW_GV_R_QKV, c->x, y->att_norm, c->qkv, 0, 0, NULL, 0, s));
         } else {
             pf_mark(c, GW_PF_NORM);
             KCHK(gw_k_rmsnorm_quant(c->x, l ? c->xb : NULL, dim, y->att_norm, NULL, n, c->xq, c->xs, K, NULL, s));
@@ -627,17 +630,17 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
         if (fused) {
             if (nbmax <= GW_GV_NBMAX) {
                 pf_mark(c, GW_PF_WO);
-                KCHK(gw_k_gemv1_combine(&y->wo, GW_GV_R_WO, c->part, c->pstride, hd, nbmax, c->x, 1, s));
+                KCHK(gw_k_gemv1_combine(&y->wo, GW_GV_R_WO, c->part, c->pstride, hd, nbmax, c->x, 1, NULL, 0, s));
             } else {
                 pf_mark(c, GW_PF_COMBINE);
                 KCHK(gw_k_attn_combine_quant(c->part, c->pstride, nh, hd, pos_d, n, c->xq, c->xs, K, NULL, s));
                 pf_mark(c, GW_PF_WO);
-                KCHK(gw_k_gemv1_q(&y->wo, GW_GV_R_WO, c->xq, c->xs, c->x, 1, s));
+                KCHK(gw_k_gemv1_q(&y->wo, GW_GV_R_WO, c->xq, c->xs, c->x, 1, NULL, 0, s));
             }
             pf_mark(c, GW_PF_W13);
-            KCHK(gw_k_gemv1_norm(&y->w13[0], GW_GV_R_W13, c->x, y->ffn_norm, c->hb, 0, y->w13_il, s));
+            KCHK(gw_k_gemv1_norm(&y->w13[0], GW_GV_R_W13, c->x, y->ffn_norm, c->hb, 0, y->w13_il, NULL, 0, s));
             pf_mark(c, GW_PF_W2);
-            KCHK(gw_k_gemv1_qf(&y->w2, GW_GV_R_W2, c->hb, c->x, 1, s));
+            KCHK(gw_k_gemv1_qf(&y->w2, GW_GV_R_W2, c->hb, c->x, 1, NULL, 0, s));
             continue;
         }
         pf_mark(c, GW_PF_COMBINE);
@@ -660,7 +663,7 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
     }
     if (fused && P->nsel == 1 && !P->want_hidden) { /* the final rmsnorm computed by the classifier's GEMV itself */
         pf_mark(c, GW_PF_CLS);
-        KCHK(gw_k_gemv1_norm(&m->cls, GW_GV_R_CLS, c->x, m->final_norm, c->logits_d, 0, 0, s));
+        KCHK(gw_k_gemv1_norm(&m->cls, GW_GV_R_CLS, c->x, m->final_norm, c->logits_d, 0, 0, NULL, 0, s));
     } else if (P->nsel > 0) {
         pf_mark(c, GW_PF_NORM);
         KCHK(gw_k_rmsnorm_quant(c->x, resid_done ? NULL : c->xb, dim, m->final_norm, sel_d, P->nsel, c->xq, c->xs, K, NULL, s));
@@ -800,7 +803,7 @@ int gw_decode_greedy(RqCtx *c, RqSeq *s, int token, int n, int *tokens) {
         for (int l = 0; l < m->n_layers; l++)
             if ((e = fused_layer(c, l, s, p0 + i, c->gpos_d + i)) != RQ_OK) return e;
         pf_mark(c, GW_PF_CLS);
-        KCHK(gw_k_gemv1_norm(&m->cls, GW_GV_R_CLS, c->x, m->final_norm, c->logits_d, 0, 0, st));
+        KCHK(gw_k_gemv1_norm(&m->cls, GW_GV_R_CLS, c->x, m->final_norm, c->logits_d, 0, 0, NULL, 0, st));
         pf_mark(c, -1);
         KCHK(gw_k_argmax(c->logits_d, m->vocab, m->vocab, 1, c->gtok_d + i + 1, c->argmax_scr, st));
         if (c->prof_on) { /* (profiling: each pass's intervals, as the passes of fw_pass) */
@@ -959,10 +962,13 @@ int gw_ctx_gemv_sweep(RqCtx *c, int reps, double *seconds, double *bytes, int *l
         for (int l = 0; l < m->n_layers; l++) {
             const GwLayer *y = &m->layer[l];
             if (fused) {
-                KCHK(gw_k_gemv1_norm(&y->qkv[0], GW_GV_R_QKV, c->x, y->att_norm, c->qkv, 0, 0, s));
-                KCHK(gw_k_gemv1_combine(&y->wo, GW_GV_R_WO, c->part, c->pstride, m->head_dim, 1, c->xb, 0, s));
-                KCHK(gw_k_gemv1_norm(&y->w13[0], GW_GV_R_W13, c->x, y->ffn_norm, c->hb, 0, y->w13_il, s));
-                KCHK(gw_k_gemv1_qf(&y->w2, GW_GV_R_W2, c->hb, c->xb, 0, s));
+                const int last = l + 1 == m->n_layers;
+                KCHK(gw_k_gemv1_norm(&y->qkv[0], GW_GV_R_QKV, c->x, y->att_norm, c->qkv, 0, 0, &y->wo, GW_GV_R_WO, s));
+                KCHK(gw_k_gemv1_combine(&y->wo, GW_GV_R_WO, c->part, c->pstride, m->head_dim, 1, c->xb, 0, &y->w13[0],
+                                        GW_GV_R_W13, s));
+                KCHK(gw_k_gemv1_norm(&y->w13[0], GW_GV_R_W13, c->x, y->ffn_norm, c->hb, 0, y->w13_il, &y->w2, GW_GV_R_W2, s));
+                KCHK(gw_k_gemv1_qf(&y->w2, GW_GV_R_W2, c->hb, c->xb, 0, last ? &m->cls : &m->layer[l + 1].qkv[0],
+                                   last ? GW_GV_R_CLS : GW_GV_R_QKV, s));
                 continue;
             }
             if ((rc = run_mm(c, y->qkv, y->nqkv, c->xq, c->xs, c->kmax, 1, c->qkv, c->ldqkv, 0)) != RQ_OK) return rc;
@@ -970,7 +976,7 @@ int gw_ctx_gemv_sweep(RqCtx *c, int reps, double *seconds, double *bytes, int *l
             if ((rc = run_mm(c, y->w13, y->nw13, c->xq, c->xs, c->kmax, 1, c->hb, 2 * m->hidden, 0)) != RQ_OK) return rc;
             if ((rc = run_mm(c, &y->w2, 1, c->hq, c->hs, m->hidden, 1, c->xb, m->dim, 0)) != RQ_OK) return rc;
         }
-        if (fused) KCHK(gw_k_gemv1_norm(&m->cls, GW_GV_R_CLS, c->x, m->final_norm, c->logits_d, 0, 0, s));
+        if (fused) KCHK(gw_k_gemv1_norm(&m->cls, GW_GV_R_CLS, c->x, m->final_norm, c->logits_d, 0, 0, NULL, 0, s));
         else if ((rc = run_mm(c, &m->cls, 1, c->xq, c->xs, c->kmax, 1, c->logits_d, m->vocab, 0)) != RQ_OK) return rc;
     }
     HIPCHK(c, "hipEventRecord", hipEventRecord(e1, s));

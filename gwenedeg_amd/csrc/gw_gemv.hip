@@ -39,6 +39,11 @@ struct GvArgs {
     int mode;
     int cmax;         // tiles whose partials the block keeps in LDS between folds
     float inv_k;      // GV_NORM: 1.0f / K (the host's division, as the reference's 1.0f / size)
+    // the next matmul of the sequence (NULL: none): its codes and scales (n_cbytes, n_sbytes), its whole tiles' bytes
+    // (n_tb codes, n_tsb scales; n_tb >= K), whole-tile count and grid; block b warms that matmul's tiles b, b + n_grid
+    const int8_t *nW;
+    const uint16_t *nWS;
+    int n_cbytes, n_sbytes, n_tb, n_tsb, n_tiles, n_grid;
 };
 
 __device__ __forceinline__ float gv_fold(const float *p, int G) {
@@ -91,18 +96,27 @@ __device__ __forceinline__ float gv_fold(const float *p, int G) {
 #define GV_WNT 2
 #endif
 template <int R>
+__device__ __forceinline__ void gv_load_rows(__amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t rs, int cb, int cl, int sb, int sl,
+                                             int j, int K, int G, int4 (&wv)[R], uint32_t (&ws)[R]) {
+    // R rows' loads: row r's codes at byte cb + min(r K, cl) of rw, its scales at sb + min(r 2 G, sl) of rs (the clamps:
+    // a partial last tile loads its last row again)
+    #pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int o = r * K < cl ? r * K : cl;
+        wv[r] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(rw, 16 * j, cb + o, GV_WNT));
+    }
+    #pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int o = r * G * 2 < sl ? r * G * 2 : sl;
+        ws[r] = __builtin_amdgcn_raw_buffer_load_b32(rs, ((j >> 1) & ~1) * 2, sb + o, GV_WNT);
+    }
+}
+
+template <int R>
 __device__ __forceinline__ void gv_load_tile(__amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t rs, int nrows, int tile, int j,
                                              int K, int G, int4 (&wv)[R], uint32_t (&ws)[R]) {
-    #pragma unroll
-    for (int r = 0; r < R; r++) {
-        int row = tile * R + r < nrows ? tile * R + r : nrows - 1;
-        wv[r] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(rw, 16 * j, row * K, GV_WNT));
-    }
-    #pragma unroll
-    for (int r = 0; r < R; r++) {
-        int row = tile * R + r < nrows ? tile * R + r : nrows - 1;
-        ws[r] = __builtin_amdgcn_raw_buffer_load_b32(rs, ((j >> 1) & ~1) * 2, row * G * 2, GV_WNT);
-    }
+    const int last = nrows - 1 - tile * R; // (the tile's rows past the matrix's last row load that row)
+    gv_load_rows<R>(rw, rs, tile * R * K, last * K, tile * R * G * 2, last * G * 2, j, K, G, wv, ws);
 }
 
 // the group of 32 (this lane's 16 values and its pair's): wmax, s = wmax / 127, q = trunc(v * inv + copysign(.49999997))
@@ -302,12 +316,26 @@ __global__ __launch_bounds__(NT) void k_gemv1(GvArgs a) {
     // tile's loads and the next. D register sets take turns, D - 1 tiles in flight (a copy from a later tile's
     // registers would wait for their loads)
     const int C = a.cmax;
+    // past the block's last tile, the loads of the tile D - 1 ahead warm the next matmul's first tiles for the block of
+    // the same index instead (the same L2: a block's XCD is its index modulo the XCD count, and both grids are the
+    // device's CUs), or load this tile again. Their registers are never read: the data go no further than the caches
+    const bool pfon = a.nW && (int)blockIdx.x < a.n_grid;
+    const __amdgpu_buffer_rsrc_t rwn = __builtin_amdgcn_make_buffer_rsrc((void *)(pfon ? a.nW : a.W), (short)0,
+                                                                          pfon ? a.n_cbytes : a.nrows * K, GV_RSRC_DW3);
+    const __amdgpu_buffer_rsrc_t rsn = __builtin_amdgcn_make_buffer_rsrc((void *)(pfon ? a.nWS : a.WS), (short)0,
+                                                                          pfon ? a.n_sbytes : (a.nrows * G * 2 + 3) & ~3, GV_RSRC_DW3);
+    int pfi = 0; // (the next matmul's tile blockIdx.x + pfi n_grid comes next)
     auto step = [&](const int4 (&cw)[R], const uint32_t (&cs)[R], int4 (&nw)[R], uint32_t (&ns)[R], int k) -> bool {
         const int nt = tile + gridDim.x, nta = tile + (D - 1) * (int)gridDim.x;
         const bool more = nt < ntiles;
-        // the tile D - 1 ahead (unconditional: past the block's last tile it loads this one again, from L2; loads under
-        // a branch would make every later wait count for the path without them)
-        gv_load_tile<R>(rw, rs, a.nrows, nta < ntiles ? nta : tile, j, K, G, nw, ns);
+        // the tile D - 1 ahead (unconditional, every choice below uniform: loads under a branch would make every later
+        // wait count for the path without them)
+        const int ti = (int)blockIdx.x + pfi * a.n_grid;
+        const bool ahead = nta < ntiles, pf = !ahead && pfon && ti < a.n_tiles;
+        const int tl = ahead ? nta : tile, last = a.nrows - 1 - tl * R;
+        pfi += ahead ? 0 : 1;
+        gv_load_rows<R>(pf ? rwn : rw, pf ? rsn : rs, pf ? ti * a.n_tb : tl * R * K, pf ? a.n_tb - K : last * K,
+                        pf ? ti * a.n_tsb : tl * R * G * 2, pf ? a.n_tsb - G * 2 : last * G * 2, j, K, G, nw, ns);
         const int slot = k % C;
         float *P = lds + slot * R * PS;
         #pragma unroll
@@ -354,8 +382,9 @@ extern "C" {
 
 // the matmul out[row] (+)= W row . act, act = the prologue's quantized row; R weight rows per block (4, 8 or 16)
 static int gv_nwg = 0; // blocks per launch: the device's compute units (one block each)
+static int gv_warm = 1; // gw_gemv_warm_next
 
-static int gv_launch(int pro, int R, const GvArgs &a, hipStream_t s) {
+static int gv_launch(int pro, int R, const GvArgs &a, const GwMat *nx, int nR, hipStream_t s) {
     if (!gv_nwg) {
         int dev = 0, cus = 0;
         if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
@@ -372,6 +401,15 @@ static int gv_launch(int pro, int R, const GvArgs &a, hipStream_t s) {
     GvArgs b = a;
     b.cmax = tpw < cmax ? tpw : cmax;
     b.inv_k = 1.0f / (float)a.K;
+    if (gv_warm && nx && nR > 0 && nx->type == GW_Q8_0 && nx->cols % 64 == 0 && (size_t)nx->rows * nx->cols < ((size_t)1 << 31) &&
+        nx->rows >= nR && (size_t)nR * nx->cols >= (size_t)a.K) {
+        /* the next matmul's launch as gv_launch makes it (whole tiles only: every warm load inside the matrix) */
+        const int nnt = (nx->rows + nR - 1) / nR;
+        b.nW = nx->codes, b.nWS = nx->scales;
+        b.n_cbytes = nx->rows * nx->cols, b.n_sbytes = (nx->rows * (nx->cols / 32) * 2 + 3) & ~3;
+        b.n_tb = nR * nx->cols, b.n_tsb = nR * (nx->cols / 32) * 2;
+        b.n_tiles = nx->rows / nR, b.n_grid = nnt < gv_nwg ? nnt : gv_nwg;
+    }
     size_t lds = (size_t)b.cmax * slot_bytes + (pro == GV_NORM ? (size_t)(16 * (a.K / 16 + 4) + 4) * sizeof(float) : 0);
     dim3 grid(nwg);
     hipEvent_t e0, e1;
@@ -415,36 +453,44 @@ static int gv_check(const GwMat *w, int R) {
                    (R == 2 || R == 4 || R == 8 || (R == 16 && w->cols <= 4096)) ? 0 : (int)hipErrorInvalidValue;
 }
 
-int gw_k_gemv1_q(const GwMat *w, int R, const int8_t *xq, const float *xs, float *out, int mode, hipStream_t s) {
+int gw_gemv_warm_next(int on) {
+    int prev = gv_warm;
+    if (on >= 0) gv_warm = on ? 1 : 0;
+    return prev;
+}
+
+int gw_k_gemv1_q(const GwMat *w, int R, const int8_t *xq, const float *xs, float *out, int mode, const GwMat *nx, int nR,
+                 hipStream_t s) {
     if (gv_check(w, R)) return (int)hipErrorInvalidValue;
     GvArgs a = {};
     a.W = w->codes, a.WS = w->scales, a.nrows = w->rows, a.K = w->cols, a.xq = xq, a.xs = xs, a.out = out, a.mode = mode;
-    return gv_launch(GV_Q, R, a, s);
+    return gv_launch(GV_Q, R, a, nx, nR, s);
 }
 
-int gw_k_gemv1_norm(const GwMat *w, int R, const float *x, const float *nw, float *out, int mode, int swiglu_il, hipStream_t s) {
+int gw_k_gemv1_norm(const GwMat *w, int R, const float *x, const float *nw, float *out, int mode, int swiglu_il,
+                    const GwMat *nx, int nR, hipStream_t s) {
     if (gv_check(w, R) || (R == 8 && w->cols > 4096) || (swiglu_il && (swiglu_il != 4 || R != 8 || w->rows % 8)))
         return (int)hipErrorInvalidValue;
     GvArgs a = {};
     a.W = w->codes, a.WS = w->scales, a.nrows = w->rows, a.K = w->cols, a.x = x, a.nw = nw, a.out = out, a.mode = mode;
     a.swiglu_il = swiglu_il;
-    return gv_launch(GV_NORM, R, a, s);
+    return gv_launch(GV_NORM, R, a, nx, nR, s);
 }
 
-int gw_k_gemv1_qf(const GwMat *w, int R, const float *x, float *out, int mode, hipStream_t s) {
+int gw_k_gemv1_qf(const GwMat *w, int R, const float *x, float *out, int mode, const GwMat *nx, int nR, hipStream_t s) {
     if (gv_check(w, R)) return (int)hipErrorInvalidValue;
     GvArgs a = {};
     a.W = w->codes, a.WS = w->scales, a.nrows = w->rows, a.K = w->cols, a.x = x, a.out = out, a.mode = mode;
-    return gv_launch(GV_QF, R, a, s);
+    return gv_launch(GV_QF, R, a, nx, nR, s);
 }
 
 int gw_k_gemv1_combine(const GwMat *w, int R, const float *part, int pstride, int hd, int nb, float *out, int mode,
-                       hipStream_t s) {
+                       const GwMat *nx, int nR, hipStream_t s) {
     if (gv_check(w, R) || hd % 16 || nb < 1 || nb > GV_NBMAX) return (int)hipErrorInvalidValue;
     GvArgs a = {};
     a.W = w->codes, a.WS = w->scales, a.nrows = w->rows, a.K = w->cols, a.part = part, a.pstride = pstride, a.hd = hd;
     a.nb = nb, a.out = out, a.mode = mode;
-    return gv_launch(GV_COMBINE, R, a, s);
+    return gv_launch(GV_COMBINE, R, a, nx, nR, s);
 }
 
 } // extern "C"

@@ -168,11 +168,15 @@ int gw_k_fill_synthetic(uint16_t *kc, uint16_t *vc, size_t n, unsigned long long
 #define GW_GV_R_W13 8
 #define GW_GV_R_W2 2
 #define GW_GV_R_CLS 8
-int gw_k_gemv1_q(const GwMat *w, int R, const int8_t *xq, const float *xs, float *out, int mode, hipStream_t s);
-int gw_k_gemv1_norm(const GwMat *w, int R, const float *x, const float *nw, float *out, int mode, int swiglu_il, hipStream_t s);
-int gw_k_gemv1_qf(const GwMat *w, int R, const float *x, float *out, int mode, hipStream_t s);
+/* nx, nR: the matmul launched next on the stream and its R (NULL: none, or not known); the blocks of this launch
+ * warm its first tiles in L2 once their own loads are done (gw_gemv_warm_next) */
+int gw_k_gemv1_q(const GwMat *w, int R, const int8_t *xq, const float *xs, float *out, int mode, const GwMat *nx, int nR,
+                 hipStream_t s);
+int gw_k_gemv1_norm(const GwMat *w, int R, const float *x, const float *nw, float *out, int mode, int swiglu_il,
+                    const GwMat *nx, int nR, hipStream_t s);
+int gw_k_gemv1_qf(const GwMat *w, int R, const float *x, float *out, int mode, const GwMat *nx, int nR, hipStream_t s);
 int gw_k_gemv1_combine(const GwMat *w, int R, const float *part, int pstride, int hd, int nb, float *out, int mode,
-                       hipStream_t s);
+                       const GwMat *nx, int nR, hipStream_t s);
 
 /* per-launch kernel timing (gw_ctx_kernel_timing): gw_time_next_launch(a, b) makes the next matmul launch (k_gemv1,
  * k_gemm_q8, k_gemv_mr) record its own start and stop in events a and b (hipExtLaunchKernel's events: the

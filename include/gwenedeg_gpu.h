@@ -295,6 +295,12 @@ int gw_kq_matmul(float *out, int type, const void *blocks, int N, int K, const i
  * and test hook with no counterpart in runq.h; results do not depend on it */
 int gw_matmul_tile_rows(int rows);
 
+/* Whether each decode GEMV, once its blocks have issued their last weight loads, warms the first weight tiles of the
+ * matmul launched after it (the next layer's included) in L2: 1 on (the default), 0 off, a negative value only
+ * queries. Returns the previous setting. A tuning and test hook with no counterpart in runq.h; results do not depend
+ * on it */
+int gw_gemv_warm_next(int on);
+
 /* The context's stream (a hipStream_t), for callers that time the passes with events on it */
 void *gw_ctx_stream(RqCtx *c);
 

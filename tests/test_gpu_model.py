@@ -192,3 +192,28 @@ def test_memory_and_pass_times(gw, synth_models):
     t1, t4 = ctypes.c_double(), ctypes.c_double()
     assert lib.rq_pass_times(ctypes.c_void_p(m._h), 2, ctypes.byref(t1), ctypes.byref(t4)) == 0
     assert 0 < t1.value < 1 and 0 < t4.value < 1
+
+
+@pytest.mark.parametrize("shape", ["tiny", "tiny_gqa4"])
+def test_decode_same_bits_without_warm_next(gw, synth_models, shape):
+    """gw_gemv_warm_next (each decode GEMV warming the next matmul's first tiles) changes no bit: the same prefill and
+    decode steps with it off and on give the same logits"""
+    path = synth_models(shape)
+    m = gw.Model(path, ctx_len=1024)
+    c = m.ctx(max_batch=16)
+    ids = _ids(m.vocab, 300, 9)
+    out = {}
+    prev = gw.lib.gw_gemv_warm_next(-1)
+    try:
+        for on in (0, 1):
+            gw.lib.gw_gemv_warm_next(on)
+            s = m.seq(1024)
+            rows = [c.prefill(s, ids)]
+            tok = int(np.argmax(rows[-1]))
+            for _ in range(5):
+                rows.append(c.decode(s, tok))
+                tok = int(np.argmax(rows[-1]))
+            out[on] = rows
+    finally:
+        gw.lib.gw_gemv_warm_next(prev)
+    assert all(_bits_equal(a, b) for a, b in zip(out[0], out[1]))
