@@ -184,8 +184,9 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
     __shared__ __align__(16) int8_t xl[GM * GROW];
     __shared__ __align__(16) int8_t wl[GN * GROW];
     __shared__ __align__(16) float xsl[4][GM];
-    __shared__ float f0l[GN][5], f1l[GN][5]; // Q4_K: d sc_j, dmin m_j of the stage's groups; Q6_K: f0l[n][0] = d
-    __shared__ int scl[GN][9];               // Q6_K: the stage's 8 half-group scales
+    __shared__ float f0l[GN][5], f1l[GN][5]; // Q4_K, Q5_K: d sc_j, dmin m_j of the stage's groups; Q6_K, Q3_K: f0l[n][0] = d
+    __shared__ int scl[GN][9];               // Q6_K, Q3_K: the stage's 8 half-group scales (Q3_K: sc - 32)
+    constexpr bool Q45 = TYPE == GW_Q4_K || TYPE == GW_Q5_K; // (else Q6_K, Q3_K: half-groups of 16)
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int m0 = blockIdx.y * GM, n0 = blockIdx.x * GN;
     const int wm = GM == 64 ? (wave >> 1) * 32 : 0, wn = GM == 64 ? (wave & 1) * 64 : wave * 32;
@@ -199,7 +200,7 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
     // 2 x 16 bytes of the stage's 64 bytes of nibbles per thread, Q6_K 4 units (row, group p, half h) of 16 bytes of
     // ql and 16 of qh; the headers (threads < 128: one row each). (xr0 / xr1 named: an array here was placed in
     // scratch memory)
-    constexpr int NW = TYPE == GW_Q4_K ? 2 : 4;
+    constexpr int NW = Q45 ? 2 : 4;
     uint4 xr0, xr1, wa[NW], wb[NW], hd0, hd1;
     float xsv;
     auto load = [&](int k0) {
@@ -217,6 +218,15 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
             if (TYPE == GW_Q4_K) {
                 int row = c >> 2, q = c & 3, n = n0 + row < N ? n0 + row : N - 1;
                 wa[k] = *(const uint4 *)(sbk + (size_t)n * rowb + 16 + 64 * hs + 16 * q);
+            } else if (TYPE == GW_Q5_K) { // (the nibbles at +48; the 16 qh bytes of the piece's positions)
+                int row = c >> 2, q = c & 3, n = n0 + row < N ? n0 + row : N - 1;
+                wa[k] = *(const uint4 *)(sbk + (size_t)n * rowb + 48 + 64 * hs + 16 * q);
+                wb[k] = *(const uint4 *)(sbk + (size_t)n * rowb + 16 + 16 * (q & 1));
+            } else if (TYPE == GW_Q3_K) { // (unit (row, group p, half h): 16 bytes of qs and of hmask)
+                int row = c >> 3, u = c & 7, h = u & 1, n = n0 + row < N ? n0 + row : N - 1;
+                const uint8_t *b = sbk + (size_t)n * rowb;
+                wa[k] = *(const uint4 *)(b + 32 + 32 * hs + 16 * h);
+                wb[k] = *(const uint4 *)(b + 16 * h);
             } else {
                 int row = c >> 3, u = c & 7, p = u >> 1, h = u & 1, n = n0 + row < N ? n0 + row : N - 1;
                 const uint8_t *b = sbk + (size_t)n * rowb;
@@ -228,8 +238,10 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
         if (t < GN) {
             int n = n0 + t < N ? n0 + t : N - 1;
             const uint8_t *b = sbk + (size_t)n * rowb;
-            if (TYPE == GW_Q4_K) {
+            if (Q45) {
                 hd0 = *(const uint4 *)b; // d, dmin, then scale bytes 0 .. 11 in words y, z, w
+            } else if (TYPE == GW_Q3_K) {
+                hd0 = *(const uint4 *)(b + 96); // the 12 scale bytes, then d
             } else {
                 hd0 = *(const uint4 *)(b + 192); // the 16 int8 scales
                 hd1 = *(const uint4 *)(b + 208); // d
@@ -256,6 +268,27 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
                                       (wa[k].w >> 4) & 0x0F0F0F0Fu);
                 *(uint4 *)(wl + row * GROW + 32 * (2 * i) + o) = lo;
                 *(uint4 *)(wl + row * GROW + 32 * (2 * i + 1) + o) = hi;
+            } else if (TYPE == GW_Q5_K) { // (Q4_K's pieces with bit 4 of each code from qh: bit j of qh[l], j the sub-block)
+                int row = c >> 2, q = c & 3, i = q >> 1, o = 16 * (q & 1), jl = 4 * hs + 2 * i;
+                uint32_t a4[4] = { wa[k].x, wa[k].y, wa[k].z, wa[k].w }, b4[4] = { wb[k].x, wb[k].y, wb[k].z, wb[k].w }, lo[4], hi[4];
+                #pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    lo[e] = (a4[e] & 0x0F0F0F0Fu) | ((b4[e] >> jl) & 0x01010101u) << 4;
+                    hi[e] = ((a4[e] >> 4) & 0x0F0F0F0Fu) | ((b4[e] >> (jl + 1)) & 0x01010101u) << 4;
+                }
+                *(uint4 *)(wl + row * GROW + 32 * (2 * i) + o) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+                *(uint4 *)(wl + row * GROW + 32 * (2 * i + 1) + o) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+            } else if (TYPE == GW_Q3_K) {
+                // q' = ((qs >> 2 p) & 3) | (hmask bit 4 hs + p) << 2; q = q' - 4 as int8: q' with bit 2 flipped, sign-extended
+                int row = c >> 3, u = c & 7, p = u >> 1, h = u & 1, hb = 4 * hs + p;
+                uint32_t a4[4] = { wa[k].x, wa[k].y, wa[k].z, wa[k].w }, b4[4] = { wb[k].x, wb[k].y, wb[k].z, wb[k].w }, o4[4];
+                #pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    uint32_t q = ((a4[e] >> (2 * p)) & 0x03030303u) | ((b4[e] >> hb) & 0x01010101u) << 2;
+                    uint32_t f = q ^ 0x04040404u, sg = f & 0x04040404u;
+                    o4[e] = f | sg * 62u; // (bits 3 .. 7 of each byte whose bit 2 is set)
+                }
+                *(uint4 *)(wl + row * GROW + 32 * p + 16 * h) = make_uint4(o4[0], o4[1], o4[2], o4[3]);
             } else {
                 // q = ((ql >> 4 (p / 2)) & 15) | ((qh >> 2 p) & 3) << 4; q - 32 as int8: the 6-bit value with bit 5
                 // flipped, sign-extended
@@ -271,7 +304,7 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
             }
         }
         if (t < GN) {
-            if (TYPE == GW_Q4_K) {
+            if (Q45) {
                 auto scb = [&](int k) -> int { // (k < 12)
                     uint32_t w = k < 4 ? hd0.y : k < 8 ? hd0.z : hd0.w;
                     return (int)((w >> (8 * (k & 3))) & 0xffu);
@@ -291,6 +324,17 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
                     f0l[t][gg] = d * (float)scj;
                     f1l[t][gg] = dmin * (float)mj;
                 }
+            } else if (TYPE == GW_Q3_K) {
+                // 6-bit sc_j = (s[j % 8] >> 4 (j / 8)) & 15 | ((s[8 + j % 4] >> 2 (j / 4)) & 3) << 4, j = 8 hs + k
+                uint32_t sw[3] = { hd0.x, hd0.y, hd0.z };
+                auto sbyte = [&](int i) -> uint32_t { return (sw[i >> 2] >> (8 * (i & 3))) & 0xffu; };
+                #pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const int j = 8 * hs + k;
+                    const uint32_t lo = (sbyte(j & 7) >> (4 * (j >> 3))) & 15u, hi = (sbyte(8 + (j & 3)) >> (2 * (j >> 2))) & 3u;
+                    scl[t][k] = (int)(lo | hi << 4) - 32;
+                }
+                f0l[t][0] = h2f_g((uint16_t)(hd0.w & 0xffffu));
             } else {
                 uint32_t sw[4] = { hd0.x, hd0.y, hd0.z, hd0.w };
                 #pragma unroll
@@ -314,7 +358,7 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
             i32x4 a;
             i64 a0, a1;
             const i32x16 z = { 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0 };
-            if (TYPE == GW_Q4_K) {
+            if (Q45) {
                 a = *(const i32x4 *)(xa + 16 * (lane >> 5));
                 const i32x4 ones = { 0x01010101, 0x01010101, 0x01010101, 0x01010101 };
                 S = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, ones, z, 0, 0, 0);
@@ -326,7 +370,7 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
             for (int j = 0; j < TJ; j++) {
                 const int nl = wn + 32 * j + (lane & 31);
                 const int8_t *wbp = wl + nl * GROW + gg * 32;
-                if (TYPE == GW_Q4_K) {
+                if (Q45) {
                     i32x4 b = *(const i32x4 *)(wbp + 16 * (lane >> 5));
                     i32x16 I = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
                     const float f0 = f0l[nl][gg], f1 = f1l[nl][gg];
@@ -539,8 +583,11 @@ __global__ __launch_bounds__(SK_T) void k_gemm_kq32(const uint8_t *__restrict__ 
 //     a - b, a = ((d * sc_j) * xs) * (float) isum, b = (dmin * m_j) * (xs * (float) sum x)            (kquants.h:86-109)
 //   Q6_K (224-byte super-blocks: the file's 210 bytes, 16-byte aligned: ql 128, qh 64, 16 int8 scales, fp16 d):
 //     (d * xs) * (float) (sc_0 (sum q x - 32 sum x) + sc_1 (...)), over the group's two halves of 16
+//   Q5_K (176 bytes: Q4_K's header, qh 32, nibbles 128): Q4_K's term with q 0 .. 31 (bit 4 from qh)
+//   Q3_K (112 bytes: hmask 32, qs 64, 12 bytes of 6-bit scales, fp16 d, 2 of padding): Q6_K's term with q' 0 .. 7
+//     (2 bits from qs, bit 2 from hmask), - 4 sum x and the scales sc - 32
 // then one lane per (activation row, weight row) folds the groups in order: val = val + term. mode 1: out = out + val.
-// K % 32 == 0 (Q8_0), % 256 (K-quants); the K-quants' q are 0 .. 15 / 0 .. 63, so v_dot4 with signed codes is exact
+// K % 32 == 0 (Q8_0), % 256 (K-quants); the K-quants' q are 0 .. 63, so v_dot4 with signed codes is exact
 template <int TYPE, int M, int R, int U>
 __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, const uint16_t *__restrict__ WS, int nrows,
                                                  int K, int bstride, const int8_t *__restrict__ xq, const float *__restrict__ xs,
@@ -553,8 +600,8 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
         // the pass's loads (past the row's end: its last half-group again, unconditionally; only the stores below are
         // predicated, so no load waits for a branch)
         int4 wv[U][R];
-        float f0[U][R], f1[U][R]; // Q8_0: ws; Q4_K: d sc_j, dmin m_j; Q6_K: d
-        int isc[U][R];            // Q6_K: the half-group's int8 scale
+        float f0[U][R], f1[U][R]; // Q8_0: ws; Q4_K, Q5_K: d sc_j, dmin m_j; Q6_K, Q3_K: d
+        int isc[U][R];            // Q6_K: the half-group's int8 scale; Q3_K: its scale - 32
         #pragma unroll
         for (int u = 0; u < U; u++) {
             const int j = j0 + 256 * u + t < H ? j0 + 256 * u + t : H - 1;
@@ -574,6 +621,22 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
                         wv[u][r].y = (int)(((uint32_t)q.y >> sl) & 0x0F0F0F0Fu);
                         wv[u][r].z = (int)(((uint32_t)q.z >> sl) & 0x0F0F0F0Fu);
                         wv[u][r].w = (int)(((uint32_t)q.w >> sl) & 0x0F0F0F0Fu);
+                    } else if (TYPE == GW_Q5_K) { // (Q4_K's nibbles at +48, and bit sb of qh[l] as bit 4)
+                        const int4 q = *(const int4 *)(b + 48 + 32 * (sb >> 1) + 16 * h);
+                        const int4 qh = *(const int4 *)(b + 16 + 16 * h);
+                        const int sl = 4 * (sb & 1);
+                        wv[u][r].x = (int)((((uint32_t)q.x >> sl) & 0x0F0F0F0Fu) | ((((uint32_t)qh.x >> sb) & 0x01010101u) << 4));
+                        wv[u][r].y = (int)((((uint32_t)q.y >> sl) & 0x0F0F0F0Fu) | ((((uint32_t)qh.y >> sb) & 0x01010101u) << 4));
+                        wv[u][r].z = (int)((((uint32_t)q.z >> sl) & 0x0F0F0F0Fu) | ((((uint32_t)qh.z >> sb) & 0x01010101u) << 4));
+                        wv[u][r].w = (int)((((uint32_t)q.w >> sl) & 0x0F0F0F0Fu) | ((((uint32_t)qh.w >> sb) & 0x01010101u) << 4));
+                    } else if (TYPE == GW_Q3_K) { // (values 32 sb + 16 h ..: 2 bits 2 (sb % 4) of qs[32 (sb / 4) + l], hmask bit sb)
+                        const int4 q = *(const int4 *)(b + 32 + 32 * (sb >> 2) + 16 * h);
+                        const int4 hm = *(const int4 *)(b + 16 * h);
+                        const int sl = 2 * (sb & 3);
+                        wv[u][r].x = (int)((((uint32_t)q.x >> sl) & 0x03030303u) | ((((uint32_t)hm.x >> sb) & 0x01010101u) << 2));
+                        wv[u][r].y = (int)((((uint32_t)q.y >> sl) & 0x03030303u) | ((((uint32_t)hm.y >> sb) & 0x01010101u) << 2));
+                        wv[u][r].z = (int)((((uint32_t)q.z >> sl) & 0x03030303u) | ((((uint32_t)hm.z >> sb) & 0x01010101u) << 2));
+                        wv[u][r].w = (int)((((uint32_t)q.w >> sl) & 0x03030303u) | ((((uint32_t)hm.w >> sb) & 0x01010101u) << 2));
                     } else {
                         const int n = sb >> 2, p = sb & 3;
                         int4 lo = *(const int4 *)(b + 64 * n + 32 * (p & 1) + 16 * h);
@@ -598,7 +661,7 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
                     f0[u][r] = h2f_g(WS[(size_t)row * G + (j >> 1)]);
                     f1[u][r] = 0.0f;
                     isc[u][r] = 0;
-                } else if (TYPE == GW_Q4_K) {
+                } else if (TYPE == GW_Q4_K || TYPE == GW_Q5_K) {
                     const int sblk = j >> 4, sb = (j >> 1) & 7;
                     const uint8_t *b = rb + (size_t)sblk * bstride;
                     const uint4 hd = *(const uint4 *)b; // d, dmin, then scale bytes 0 .. 11 in words y, z, w
@@ -617,7 +680,7 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
                     f0[u][r] = h2f_g((uint16_t)(hd.x & 0xffffu)) * (float)scj;
                     f1[u][r] = h2f_g((uint16_t)(hd.x >> 16)) * (float)mj;
                     isc[u][r] = 0;
-                } else {
+                } else if (TYPE == GW_Q6_K) {
                     const int sblk = j >> 4, sb = (j >> 1) & 7, h = j & 1;
                     const uint8_t *b = rb + (size_t)sblk * bstride;
                     const uint4 sw = *(const uint4 *)(b + 192); // the 16 int8 scales
@@ -625,6 +688,19 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
                     uint32_t w = k < 4 ? sw.x : k < 8 ? sw.y : k < 12 ? sw.z : sw.w;
                     isc[u][r] = (int)(int8_t)((w >> (8 * (k & 3))) & 0xffu);
                     f0[u][r] = h2f_g((uint16_t)(*(const uint4 *)(b + 208)).x);
+                    f1[u][r] = 0.0f;
+                } else { // Q3_K (the 12 scale bytes s and d: 6-bit sc_k = low 4 bits of s[k % 8] (k / 8: high nibble) |
+                         // bits 2 (k / 4) of s[8 + k % 4] << 4)
+                    const int sblk = j >> 4, k = j & 15;
+                    const uint8_t *b = rb + (size_t)sblk * bstride;
+                    const uint4 sw = *(const uint4 *)(b + 96);
+                    auto sbyte = [&](int i) -> uint32_t { // (i < 12)
+                        uint32_t w = i < 4 ? sw.x : i < 8 ? sw.y : sw.z;
+                        return (w >> (8 * (i & 3))) & 0xffu;
+                    };
+                    const uint32_t lo = (sbyte(k & 7) >> (4 * (k >> 3))) & 15u, hi = (sbyte(8 + (k & 3)) >> (2 * (k >> 2))) & 3u;
+                    isc[u][r] = (int)(lo | hi << 4) - 32;
+                    f0[u][r] = h2f_g((uint16_t)(sw.w & 0xffffu));
                     f1[u][r] = 0.0f;
                 }
             }
@@ -653,7 +729,7 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
                         xsum = __builtin_amdgcn_sdot4(xv[u][m].z, 0x01010101, xsum, false);
                         xsum = __builtin_amdgcn_sdot4(xv[u][m].w, 0x01010101, xsum, false);
                     }
-                    const int xsum2 = TYPE == GW_Q4_K ? xsum + __shfl_xor(xsum, 1) : 0;
+                    const int xsum2 = TYPE == GW_Q4_K || TYPE == GW_Q5_K ? xsum + __shfl_xor(xsum, 1) : 0;
                     #pragma unroll
                     for (int r = 0; r < R; r++) {
                         int sd = __builtin_amdgcn_sdot4(wv[u][r].x, xv[u][m].x, 0, false);
@@ -665,11 +741,15 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
                             int is = sd + __shfl_xor(sd, 1);
                             float sc = f0[u][r] * xsg[u][m];
                             term = sc * (float)is;
-                        } else if (TYPE == GW_Q4_K) {
+                        } else if (TYPE == GW_Q4_K || TYPE == GW_Q5_K) {
                             int is = sd + __shfl_xor(sd, 1);
                             float a = (f0[u][r] * xsg[u][m]) * (float)is;
                             float bb = f1[u][r] * (xsg[u][m] * (float)xsum2);
                             term = a - bb;
+                        } else if (TYPE == GW_Q3_K) {
+                            int I = isc[u][r] * (sd - 4 * xsum);
+                            I = I + __shfl_xor(I, 1);
+                            term = (f0[u][r] * xsg[u][m]) * (float)I;
                         } else {
                             int I = isc[u][r] * (sd - 32 * xsum);
                             I = I + __shfl_xor(I, 1);
@@ -728,8 +808,8 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
     }
 }
 
-// x[b] = row tok[b] of a K-quant table, dequantized (kq_dequant_row, kquants.h:222-251; every value one rounding
-// of an exact expression)
+// x[b] = row tok[b] of a K-quant table (Q3_K .. Q6_K), dequantized (kq_dequant_row, kquants.h:222-251; every value
+// one rounding of an exact expression)
 __global__ __launch_bounds__(256) void k_embed_kq(float *__restrict__ x, int dim, int type, const uint8_t *__restrict__ W,
                                                   int bstride, const int *__restrict__ tok) {
     int bidx = blockIdx.x;
@@ -738,16 +818,24 @@ __global__ __launch_bounds__(256) void k_embed_kq(float *__restrict__ x, int dim
     for (int i = threadIdx.x; i < dim; i += blockDim.x) {
         int s = i >> 8, k = i & 255;
         float y;
-        if (type == GW_Q4_K) {
+        if (type == GW_Q4_K || type == GW_Q5_K) {
             const uint8_t *b = rb + (size_t)s * bstride, *sc = b + 4;
             int j = k >> 5, scj, mj;
             if (j < 4) { scj = sc[j] & 63; mj = sc[j + 4] & 63; }
             else { scj = (sc[j + 4] & 15) | (sc[j - 4] >> 6) << 4; mj = (sc[j + 4] >> 4) | (sc[j] >> 6) << 4; }
             float d = __half2float(__ushort_as_half((uint16_t)(b[0] | b[1] << 8)));
             float dmin = __half2float(__ushort_as_half((uint16_t)(b[2] | b[3] << 8)));
-            int q = (b[16 + 32 * (k / 64) + k % 32] >> (4 * (k / 32 % 2))) & 15;
+            int q = type == GW_Q4_K ? (b[16 + 32 * (k / 64) + k % 32] >> (4 * (k / 32 % 2))) & 15
+                                    : ((b[48 + 32 * (j / 2) + k % 32] >> (4 * (j % 2))) & 15) | ((b[16 + k % 32] >> j) & 1) << 4;
             float d1 = d * (float)scj, m1 = dmin * (float)mj;
             y = d1 * (float)q - m1;
+        } else if (type == GW_Q3_K) { // (d (sc_j - 32)) (q' - 4), sub-blocks j of 16
+            const uint8_t *b = rb + (size_t)s * bstride;
+            int j = k >> 4, n = k / 128, p = k / 32 % 4, l = k % 32;
+            int scj = (j < 8 ? b[96 + j] & 15 : b[96 + j - 8] >> 4) | ((b[104 + j % 4] >> (2 * (j / 4))) & 3) << 4;
+            int q = ((b[32 + 32 * n + l] >> (2 * p)) & 3) | ((b[l] >> (k / 32)) & 1) << 2;
+            float d = __half2float(__ushort_as_half((uint16_t)(b[108] | b[109] << 8)));
+            y = (d * (float)(scj - 32)) * (float)(q - 4);
         } else {
             const uint8_t *b = rb + (size_t)s * bstride;
             int n = k / 128, p = k / 32 % 4, l = k % 32;
@@ -801,17 +889,18 @@ static int launch_gemv_mr(const uint8_t *W, const uint16_t *WS, int nrows, int K
     return (int)hipGetLastError();
 }
 
-// dst super-block i (GW_Q6K_DEV bytes) = src super-block i (GW_Q6K_BYTES) and zero padding
-__global__ __launch_bounds__(256) void k_q6k_pad(const uint8_t *__restrict__ src, size_t nblk, uint8_t *__restrict__ dst) {
-    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, b = i / GW_Q6K_DEV, k = i % GW_Q6K_DEV;
-    if (b < nblk) dst[i] = k < GW_Q6K_BYTES ? src[b * GW_Q6K_BYTES + k] : 0;
+// dst super-block i (db bytes) = src super-block i (sb bytes) and zero padding
+__global__ __launch_bounds__(256) void k_kq_pad(const uint8_t *__restrict__ src, size_t nblk, int sb, int db, uint8_t *__restrict__ dst) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, b = i / (size_t)db, k = i % (size_t)db;
+    if (b < nblk) dst[i] = k < (size_t)sb ? src[b * sb + k] : 0;
 }
 
 extern "C" {
 
-int gw_k_q6k_pad(const uint8_t *src, size_t nblk, uint8_t *dst, hipStream_t s) {
-    size_t n = nblk * GW_Q6K_DEV;
-    hipLaunchKernelGGL(k_q6k_pad, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, nblk, dst);
+int gw_k_kq_pad(const uint8_t *src, size_t nblk, int sbytes, int dbytes, uint8_t *dst, hipStream_t s) {
+    if (sbytes < 1 || dbytes < sbytes) return (int)hipErrorInvalidValue;
+    size_t n = nblk * (size_t)dbytes;
+    hipLaunchKernelGGL(k_kq_pad, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, nblk, sbytes, dbytes, dst);
     return (int)hipGetLastError();
 }
 
@@ -891,8 +980,7 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
     // K-quants above 32 rows: the MFMA GEMM where it has 64 blocks or more (a block streams its 128 rows' full K in
     // order, so a narrow matrix leaves the device idle) or its row tile is forced, else the batched GEMV in passes of
     // 8 rows
-    if ((w->type == GW_Q4_K || w->type == GW_Q6_K) && M > 8 &&
-        (g_tile_rows || (size_t)((w->rows + GN - 1) / GN) * ((M + 31) / 32) >= 64)) {
+    if (GW_IS_KQ(w->type) && M > 8 && (g_tile_rows || (size_t)((w->rows + GN - 1) / GN) * ((M + 31) / 32) >= 64)) {
         hipEvent_t e0, e1;
         gw_take_launch_events(&e0, &e1);
         const int cus = gemm_cus(), nt = (w->rows + GN - 1) / GN;
@@ -903,17 +991,25 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
         if (w->type == GW_Q4_K) {
             if (g64) KQ_L(GW_Q4_K, 64);
             else KQ_L(GW_Q4_K, 32);
-        } else {
+        } else if (w->type == GW_Q6_K) {
             if (g64) KQ_L(GW_Q6_K, 64);
             else KQ_L(GW_Q6_K, 32);
+        } else if (w->type == GW_Q5_K) {
+            if (g64) KQ_L(GW_Q5_K, 64);
+            else KQ_L(GW_Q5_K, 32);
+        } else {
+            if (g64) KQ_L(GW_Q3_K, 64);
+            else KQ_L(GW_Q3_K, 32);
         }
 #undef KQ_L
         return (int)hipGetLastError();
     }
-    if (w->type == GW_Q4_K)
-        return launch_gemv_mr<GW_Q4_K>(w->blocks, NULL, w->rows, w->cols, w->bstride, xq, xs, ldx, M, out, ldo, mode, s);
-    if (w->type == GW_Q6_K)
-        return launch_gemv_mr<GW_Q6_K>(w->blocks, NULL, w->rows, w->cols, w->bstride, xq, xs, ldx, M, out, ldo, mode, s);
+#define MRQ_L(TT) return launch_gemv_mr<TT>(w->blocks, NULL, w->rows, w->cols, w->bstride, xq, xs, ldx, M, out, ldo, mode, s)
+    if (w->type == GW_Q4_K) MRQ_L(GW_Q4_K);
+    if (w->type == GW_Q6_K) MRQ_L(GW_Q6_K);
+    if (w->type == GW_Q5_K) MRQ_L(GW_Q5_K);
+    if (w->type == GW_Q3_K) MRQ_L(GW_Q3_K);
+#undef MRQ_L
     return (int)hipErrorInvalidValue;
 }
 
@@ -950,17 +1046,17 @@ int gw_matmul_tile_rows(int rows) {
 }
 
 int gw_kq_matmul(float *out, int type, const void *blocks, int N, int K, const int8_t *xq, const float *xs, int M, void *stream) {
-    if (N <= 0 || K <= 0 || M <= 0 || K % 256 || (type != GW_Q4_K && type != GW_Q6_K) || !out || !blocks || !xq || !xs)
-        return RQ_ERR_ARG;
-    GwMat w = { type, N, K, NULL, NULL, (uint8_t *)blocks, GW_Q4K_BYTES };
-    if (type == GW_Q4_K) return gw_k_matmul(&w, xq, xs, K, M, out, N, 0, (hipStream_t)stream) ? RQ_ERR_STATE : RQ_OK;
-    // Q6_K: the file's blocks padded into the device layout first (a temporary copy)
+    if (N <= 0 || K <= 0 || M <= 0 || K % 256 || !GW_IS_KQ(type) || !out || !blocks || !xq || !xs) return RQ_ERR_ARG;
+    const int fb = gw_kq_file_bytes(type), db = gw_kq_dev_bytes(type);
+    GwMat w = { type, N, K, NULL, NULL, (uint8_t *)blocks, fb };
+    if (fb == db) return gw_k_matmul(&w, xq, xs, K, M, out, N, 0, (hipStream_t)stream) ? RQ_ERR_STATE : RQ_OK;
+    // Q6_K, Q3_K: the file's blocks padded into the device layout first (a temporary copy)
     size_t nblk = (size_t)N * (K / 256);
     uint8_t *pad = NULL;
-    if (hipMalloc((void **)&pad, nblk * GW_Q6K_DEV) != hipSuccess) return RQ_ERR_NOMEM;
+    if (hipMalloc((void **)&pad, nblk * db) != hipSuccess) return RQ_ERR_NOMEM;
     w.blocks = pad;
-    w.bstride = GW_Q6K_DEV;
-    int rc = gw_k_q6k_pad((const uint8_t *)blocks, nblk, pad, (hipStream_t)stream) ||
+    w.bstride = db;
+    int rc = gw_k_kq_pad((const uint8_t *)blocks, nblk, fb, db, pad, (hipStream_t)stream) ||
              gw_k_matmul(&w, xq, xs, K, M, out, N, 0, (hipStream_t)stream) ? RQ_ERR_STATE : RQ_OK;
     if (hipStreamSynchronize((hipStream_t)stream) != hipSuccess) rc = RQ_ERR_STATE;
     (void)hipFree(pad);

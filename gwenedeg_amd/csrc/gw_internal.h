@@ -16,7 +16,7 @@
 extern "C" {
 #endif
 
-enum { GW_F32 = 0, GW_Q8_0 = 8, GW_Q4_K = 12, GW_Q6_K = 14 }; /* ggml type numbers */
+enum { GW_F32 = 0, GW_Q8_0 = 8, GW_Q3_K = 11, GW_Q4_K = 12, GW_Q5_K = 13, GW_Q6_K = 14 }; /* ggml type numbers */
 
 #define GW_ATT_T 16   /* positions per KV cache tile */
 #define GW_ATT_P 256  /* positions per attention block */
@@ -24,12 +24,25 @@ enum { GW_F32 = 0, GW_Q8_0 = 8, GW_Q4_K = 12, GW_Q6_K = 14 }; /* ggml type numbe
 #define GW_W13_IL 4 /* w1 / w3 rows interleaved in the fused Q8_0 matrix (blocks of 4) */
 #define GW_GEMV_MAX_ROWS 32 /* activation rows up to which a Q8_0 matmul takes the batched GEMV (else the MFMA GEMM) */
 #define GW_Q4K_BYTES 144    /* bytes of a Q4_K super-block (256 weights), file and device */
+#define GW_Q5K_BYTES 176    /* Q5_K, file and device */
 #define GW_Q6K_BYTES 210    /* bytes of a Q6_K super-block in the file */
 #define GW_Q6K_DEV 224      /* ... on the device: the file's 210 bytes padded to a 16-byte multiple (aligned loads) */
+#define GW_Q3K_BYTES 110    /* Q3_K in the file */
+#define GW_Q3K_DEV 112      /* ... on the device, padded as Q6_K */
+#define GW_IS_KQ(t) ((t) >= GW_Q3_K && (t) <= GW_Q6_K)
+
+/* a K-quant super-block's bytes in the file and on the device (0: not a K-quant) */
+static inline int gw_kq_file_bytes(int type) {
+    return type == GW_Q3_K ? GW_Q3K_BYTES : type == GW_Q4_K ? GW_Q4K_BYTES : type == GW_Q5_K ? GW_Q5K_BYTES
+         : type == GW_Q6_K ? GW_Q6K_BYTES : 0;
+}
+static inline int gw_kq_dev_bytes(int type) {
+    return type == GW_Q3_K ? GW_Q3K_DEV : type == GW_Q6_K ? GW_Q6K_DEV : gw_kq_file_bytes(type);
+}
 
 /* A weight matrix on the device (rows x cols). Q8_0: int8 codes, row-major, and fp16 scales (cols / 32 per row),
  * the file's bytes split (34 bytes per 32 weights, as the file). K-quants: the file's super-blocks, row-major, each
- * bstride bytes apart (Q4_K 144; Q6_K 224: the file's 210 bytes and 14 of padding) */
+ * bstride bytes apart (Q4_K 144, Q5_K 176; Q6_K 224: the file's 210 bytes and 14 of padding; Q3_K 112: 110 and 2) */
 typedef struct {
     int type, rows, cols;
     int8_t *codes;
@@ -114,10 +127,10 @@ struct RqCtx {
 enum { GW_PF_EMBED, GW_PF_NORM, GW_PF_QKV, GW_PF_ROPE, GW_PF_ATT, GW_PF_COMBINE, GW_PF_WO, GW_PF_W13, GW_PF_SWIGLU, GW_PF_W2,
        GW_PF_CLS, GW_PF_N };
 
-/* the file-format bytes of a matrix (Q8_0 34 per 32 weights, Q4_K 144 / 256, Q6_K 210 / 256) */
+/* the file-format bytes of a matrix (Q8_0 34 per 32 weights, K-quants their super-block's bytes per 256) */
 static inline double gw_mat_file_bytes(const GwMat *w) {
     double n = (double)w->rows * w->cols;
-    return w->type == GW_Q8_0 ? n * 34 / 32 : w->type == GW_Q4_K ? n * 144 / 256 : w->type == GW_Q6_K ? n * 210 / 256 : n * 4;
+    return w->type == GW_Q8_0 ? n * 34 / 32 : GW_IS_KQ(w->type) ? n * gw_kq_file_bytes(w->type) / 256 : n * 4;
 }
 
 /* model / device helpers (gw_model.c) */
@@ -135,8 +148,8 @@ int gw_hip_fail(char *err, size_t errlen, const char *what, hipError_t e);
 /* kernels (gw_kernels.hip) */
 int gw_k_embed_q8(float *x, int dim, const uint8_t *codes, const uint16_t *scales, const int *tok, int n, hipStream_t s);
 int gw_k_embed_kq(float *x, int dim, int type, const uint8_t *blocks, int bstride, const int *tok, int n, hipStream_t s);
-/* Q6_K super-blocks (file, 210 bytes) -> the device layout (GW_Q6K_DEV bytes apart) */
-int gw_k_q6k_pad(const uint8_t *src, size_t nblk, uint8_t *dst, hipStream_t s);
+/* K-quant super-blocks of sbytes (the file) -> dbytes apart with zero padding (the device layout of Q6_K, Q3_K) */
+int gw_k_kq_pad(const uint8_t *src, size_t nblk, int sbytes, int dbytes, uint8_t *dst, hipStream_t s);
 int gw_k_rmsnorm_quant(float *x, const float *d, int dim, const float *w, const int *sel, int n, int8_t *xq, float *xs,
                        int ldq, float *hid, hipStream_t s);
 int gw_k_qknorm_rope_store(float *qkv, int ldqkv, int n, int nh, int nkv, int hd, const float *qn, const float *kn,

@@ -156,8 +156,9 @@ static size_t type_row_bytes(uint32_t type, uint64_t k, int *ok) {
     switch (type) {
     case GW_F32: return (size_t)k * 4;
     case GW_Q8_0: if (k % 32) break; return (size_t)k / 32 * 34;
-    case GW_Q4_K: if (k % 256) break; return (size_t)k / 256 * 144;
-    case GW_Q6_K: if (k % 256) break; return (size_t)k / 256 * 210;
+    case GW_Q3_K: case GW_Q4_K: case GW_Q5_K: case GW_Q6_K:
+        if (k % 256) break;
+        return (size_t)k / 256 * (size_t)gw_kq_file_bytes((int)type);
     default: break;
     }
     *ok = 0;
@@ -346,21 +347,20 @@ static int load_mat_il(Loader *L, GwMat *dst, int r0, const char *name, int rows
         hipError_t e = hipDeviceSynchronize();
         return e == hipSuccess ? RQ_OK : gw_hip_fail(L->err, L->errlen, "repack", e);
     }
-    if (t->type != GW_Q4_K && t->type != GW_Q6_K) return lfail(L, RQ_ERR_LOAD, "GGUF: %s: ggml type %u not supported", name, t->type);
+    if (!GW_IS_KQ((int)t->type)) return lfail(L, RQ_ERR_LOAD, "GGUF: %s: ggml type %u not supported", name, t->type);
     if (r0 != 0 || dst->rows != rows) return lfail(L, RQ_ERR_LOAD, "GGUF: %s: internal shape mismatch", name);
     dst->type = (int)t->type;
-    if (t->type == GW_Q4_K) {
-        dst->bstride = GW_Q4K_BYTES;
-        if ((rc = dmalloc(L, (void **)&dst->blocks, t->size)) != RQ_OK) return rc;
+    const int fb = gw_kq_file_bytes(dst->type), db = gw_kq_dev_bytes(dst->type);
+    size_t nblk = t->size / (size_t)fb;
+    dst->bstride = db;
+    if ((rc = dmalloc(L, (void **)&dst->blocks, nblk * (size_t)db)) != RQ_OK) return rc;
+    if (fb == db) { /* Q4_K, Q5_K: the file's blocks as they are */
         hipError_t e = hipMemcpy(dst->blocks, L->g.map + t->off, t->size, hipMemcpyHostToDevice);
         return e == hipSuccess ? RQ_OK : gw_hip_fail(L->err, L->errlen, "hipMemcpy (weights)", e);
     }
-    /* Q6_K: staged as the file's blocks, then padded to GW_Q6K_DEV bytes each (16-byte aligned loads) */
-    size_t nblk = t->size / GW_Q6K_BYTES;
-    dst->bstride = GW_Q6K_DEV;
-    if ((rc = dmalloc(L, (void **)&dst->blocks, nblk * GW_Q6K_DEV)) != RQ_OK) return rc;
+    /* Q6_K, Q3_K: staged as the file's blocks, then padded to a 16-byte multiple each (aligned loads) */
     if ((rc = stage(L, t)) != RQ_OK) return rc;
-    if (gw_k_q6k_pad(L->stage, nblk, dst->blocks, 0)) return lfail(L, RQ_ERR_STATE, "GGUF: %s: repack kernel failed", name);
+    if (gw_k_kq_pad(L->stage, nblk, fb, db, dst->blocks, 0)) return lfail(L, RQ_ERR_STATE, "GGUF: %s: repack kernel failed", name);
     hipError_t e = hipDeviceSynchronize();
     return e == hipSuccess ? RQ_OK : gw_hip_fail(L->err, L->errlen, "repack", e);
 }

@@ -12,6 +12,8 @@
  *   Q8_0: d = amax / 127 (fp16), q = round(x / d) clamped to [-127, 127]
  *   Q4_K: 8 sub-blocks of 32, per sub-block scale / offset from its range, 6-bit sc and m against d / dmin
  *   Q6_K: 16 sub-blocks of 16, int8 sub-scales against d, q in 0..63 (value q - 32)
+ *   Q5_K: as Q4_K with q in 0..31 (bit 4 in qh)
+ *   Q3_K: 16 sub-blocks of 16, 6-bit scales sc (value (d (sc - 32)) q) with sc - 32 in 0..31 here, q in -4..3
  * Any valid block decodes the same way on both sides, so these simple encoders suffice for parity. */
 #include <math.h>
 #include <pthread.h>
@@ -22,7 +24,7 @@
 
 #include "gw_synth.h"
 
-enum { T_F32 = 0, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
+enum { T_F32 = 0, T_Q8_0 = 8, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14 };
 
 static uint16_t f32_to_f16_rne(float f) {
     uint32_t u;
@@ -75,6 +77,8 @@ static void normal_row(float *y, int n, uint64_t seed, uint64_t tensor, uint64_t
 size_t gw_synth_row_bytes(int type, int k) {
     if (type == T_Q8_0) return (size_t)k / 32 * 34;
     if (type == T_Q4_K) return (size_t)k / 256 * 144;
+    if (type == T_Q5_K) return (size_t)k / 256 * 176;
+    if (type == T_Q3_K) return (size_t)k / 256 * 110;
     if (type == T_Q6_K) return (size_t)k / 256 * 210;
     return (size_t)k * 4;
 }
@@ -94,8 +98,10 @@ static void enc_q8_0(uint8_t *o, const float *x, int k) {
     }
 }
 
-static void enc_q4_k(uint8_t *o, const float *x, int k) {
-    for (int sb = 0; sb < k / 256; sb++, o += 144, x += 256) {
+static void enc_q45_k(uint8_t *o, const float *x, int k, int q5) {
+    /* Q4_K (q5 = 0: 144-byte blocks, q 0..15) or Q5_K (176 bytes, q 0..31: the 5th bit in qh, the nibbles at +48) */
+    const int qmax = q5 ? 31 : 15, bytes = q5 ? 176 : 144, qs = q5 ? 48 : 16;
+    for (int sb = 0; sb < k / 256; sb++, o += bytes, x += 256) {
         float sc[8], mn[8], smax = 0, mmax = 0;
         for (int j = 0; j < 8; j++) {
             float lo = x[32 * j], hi = x[32 * j];
@@ -104,7 +110,7 @@ static void enc_q4_k(uint8_t *o, const float *x, int k) {
                 hi = x[32 * j + i] > hi ? x[32 * j + i] : hi;
             }
             if (lo > 0) lo = 0; /* w = s * q - m with m >= 0 */
-            sc[j] = (hi - lo) / 15.0f;
+            sc[j] = (hi - lo) / (float)qmax;
             mn[j] = -lo;
             smax = sc[j] > smax ? sc[j] : smax;
             mmax = mn[j] > mmax ? mn[j] : mmax;
@@ -130,12 +136,59 @@ static void enc_q4_k(uint8_t *o, const float *x, int k) {
             float ds = d * isc[j], dm = dmin * im[j];
             for (int i = 0; i < 32; i++) {
                 int v = ds > 0 ? (int)lroundf((x[32 * j + i] + dm) / ds) : 0;
-                q[32 * j + i] = (uint8_t)(v < 0 ? 0 : v > 15 ? 15 : v);
+                q[32 * j + i] = (uint8_t)(v < 0 ? 0 : v > qmax ? qmax : v);
             }
         }
         for (int c = 0; c < 4; c++)
             for (int l = 0; l < 32; l++)
-                o[16 + 32 * c + l] = (uint8_t)(q[64 * c + l] | q[64 * c + 32 + l] << 4);
+                o[qs + 32 * c + l] = (uint8_t)((q[64 * c + l] & 15) | (q[64 * c + 32 + l] & 15) << 4);
+        if (q5) {
+            for (int l = 0; l < 32; l++) {
+                uint8_t h = 0;
+                for (int j = 0; j < 8; j++) h |= (uint8_t)(((q[32 * j + l] >> 4) & 1) << j);
+                o[16 + l] = h;
+            }
+        }
+    }
+}
+
+static void enc_q3_k(uint8_t *o, const float *x, int k) {
+    for (int sb = 0; sb < k / 256; sb++, o += 110, x += 256) {
+        float ss[16], smax = 0;
+        for (int j = 0; j < 16; j++) {
+            float amax = 0;
+            for (int i = 0; i < 16; i++) amax = fabsf(x[16 * j + i]) > amax ? fabsf(x[16 * j + i]) : amax;
+            ss[j] = amax / 4.0f;
+            smax = ss[j] > smax ? ss[j] : smax;
+        }
+        uint16_t hd = f32_to_f16_rne(smax / 31.0f);
+        float d = f16_to_f32(hd);
+        int isc[16];
+        uint8_t q[256]; /* q' = q + 4, 0..7 */
+        for (int j = 0; j < 16; j++) {
+            int a = d > 0 ? (int)lroundf(ss[j] / d) : 0;
+            isc[j] = a < 0 ? 0 : a > 31 ? 31 : a;
+            float dl = d * (float)isc[j];
+            for (int i = 0; i < 16; i++) {
+                int v = dl > 0 ? (int)lroundf(x[16 * j + i] / dl) : 0;
+                v = v < -4 ? -4 : v > 3 ? 3 : v;
+                q[16 * j + i] = (uint8_t)(v + 4);
+            }
+        }
+        memset(o, 0, 110);
+        for (int i = 0; i < 256; i++) {
+            int n = i / 128, p = i / 32 % 4, l = i % 32;
+            o[32 + 32 * n + l] |= (uint8_t)((q[i] & 3) << (2 * p));
+            o[l] |= (uint8_t)(((q[i] >> 2) & 1) << (i / 32));
+        }
+        uint8_t *sc = o + 96;
+        for (int j = 0; j < 16; j++) {
+            int v = isc[j] + 32; /* the stored 6-bit scale */
+            if (j < 8) sc[j] |= (uint8_t)(v & 15);
+            else sc[j - 8] |= (uint8_t)((v & 15) << 4);
+            sc[8 + j % 4] |= (uint8_t)(((v >> 4) & 3) << (2 * (j / 4)));
+        }
+        memcpy(o + 108, &hd, 2);
     }
 }
 
@@ -176,7 +229,9 @@ static void enc_q6_k(uint8_t *o, const float *x, int k) {
 
 void gw_synth_encode_row(int type, uint8_t *o, const float *x, int k) {
     if (type == T_Q8_0) enc_q8_0(o, x, k);
-    else if (type == T_Q4_K) enc_q4_k(o, x, k);
+    else if (type == T_Q4_K) enc_q45_k(o, x, k, 0);
+    else if (type == T_Q5_K) enc_q45_k(o, x, k, 1);
+    else if (type == T_Q3_K) enc_q3_k(o, x, k);
     else if (type == T_Q6_K) enc_q6_k(o, x, k);
     else memcpy(o, x, (size_t)k * 4);
 }
@@ -259,7 +314,7 @@ int gw_synth_gguf(const char *path, const GwSynthCfg *c, unsigned long long seed
     const uint64_t align = 32;
     uint64_t off = 0;
     for (int i = 0; i < nt; i++) {
-        if ((T[i].type == T_Q4_K || T[i].type == T_Q6_K) && T[i].cols % 256) { free(T); return -1; }
+        if (T[i].type >= T_Q3_K && T[i].type <= T_Q6_K && T[i].cols % 256) { free(T); return -1; }
         if (T[i].type == T_Q8_0 && T[i].cols % 32) { free(T); return -1; }
         T[i].off = off;
         uint64_t sz = T[i].rows ? (uint64_t)T[i].rows * gw_synth_row_bytes(T[i].type, T[i].cols) : (uint64_t)T[i].cols * 4;

@@ -152,7 +152,7 @@ void or_q8_from_blocks(int8_t *q, float *s, const uint8_t *blk, size_t nblk) {
 
 /* ---------------------------------------------------------------------------------------- K-quants */
 
-enum { T_F32 = 0, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
+enum { T_F32 = 0, T_Q8_0 = 8, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14 };
 
 static uint16_t u16(const uint8_t *p) { uint16_t v; memcpy(&v, p, 2); return v; }
 
@@ -169,24 +169,46 @@ static void q4k_scale_min(const uint8_t *s, int j, int *sc, int *m) {
 
 static int q4k_q(const uint8_t *b, int i) { return (b[16 + 32 * (i / 64) + i % 32] >> (4 * (i / 32 % 2))) & 15; } /* :180 */
 
+static int q5k_q(const uint8_t *b, int i) { /* kquants.h:185-190: Q4_K's nibble (qs at +48) | bit j of qh[l] << 4 */
+    int j = i / 32, l = i % 32;
+    return ((b[48 + 32 * (j / 2) + l] >> (4 * (j % 2))) & 15) | ((b[16 + l] >> j) & 1) << 4;
+}
+
 static int q6k_q(const uint8_t *b, int i) { /* kquants.h:192-198 */
     int n = i / 128, p = i / 32 % 4, l = i % 32;
     return ((b[64 * n + 32 * (p & 1) + l] >> (4 * (p >> 1))) & 15) | ((b[128 + 32 * n + l] >> (2 * p)) & 3) << 4;
 }
 
-static int kq_bytes(int type) { return type == T_Q4_K ? 144 : 210; }
+static int q3k_q(const uint8_t *b, int i) { /* kquants.h:200-206: q' = q + 4 = 2 bits of qs (+32) | hmask bit i / 32 << 2 */
+    int n = i / 128, p = i / 32 % 4, l = i % 32;
+    return ((b[32 + 32 * n + l] >> (2 * p)) & 3) | ((b[l] >> (i / 32)) & 1) << 2;
+}
+
+static int q3k_scale(const uint8_t *b, int j) { /* kquants.h:207-212: the 6-bit scale (before the - 32) of sub-block j */
+    const uint8_t *sc = b + 96;
+    return (j < 8 ? sc[j] & 15 : sc[j - 8] >> 4) | ((sc[8 + j % 4] >> (2 * (j / 4))) & 3) << 4;
+}
+
+static int kq_bytes(int type) { return type == T_Q4_K ? 144 : type == T_Q5_K ? 176 : type == T_Q3_K ? 110 : 210; }
 
 void or_kq_dequant_row(int type, const uint8_t *blk, int n, float *y) {
-    /* kquants.h:222-251 (Q4_K, Q6_K) */
+    /* kquants.h:222-251 */
     for (int s = 0; s < n / 256; s++, y += 256) {
         const uint8_t *b = blk + (size_t)s * kq_bytes(type);
-        if (type == T_Q4_K) {
+        if (type == T_Q4_K || type == T_Q5_K) {
             float d = or_fp16_to_f32(u16(b)), dmin = or_fp16_to_f32(u16(b + 2));
             for (int j = 0; j < 8; j++) {
                 int sc, m;
                 q4k_scale_min(b + 4, j, &sc, &m);
                 float d1 = d * sc, m1 = dmin * m;
-                for (int l = 0; l < 32; l++) y[32 * j + l] = d1 * q4k_q(b, 32 * j + l) - m1;
+                for (int l = 0; l < 32; l++)
+                    y[32 * j + l] = d1 * (type == T_Q5_K ? q5k_q(b, 32 * j + l) : q4k_q(b, 32 * j + l)) - m1;
+            }
+        } else if (type == T_Q3_K) {
+            float d = or_fp16_to_f32(u16(b + 108));
+            for (int j = 0; j < 16; j++) {
+                float dl = d * (float)(q3k_scale(b, j) - 32);
+                for (int l = 0; l < 16; l++) y[16 * j + l] = dl * (float)(q3k_q(b, 16 * j + l) - 4);
             }
         } else {
             float d = or_fp16_to_f32(u16(b + 208));
@@ -212,15 +234,28 @@ static float kq_dot_row(int type, const uint8_t *row, const int8_t *x, const flo
         for (int j = 0; j < 8; j++) {
             int g = 8 * s + j;
             const int8_t *xg = x + 32 * g;
-            if (type == T_Q4_K) {
+            if (type == T_Q4_K || type == T_Q5_K) { /* Q5_K: Q4_K's fold with its 5-bit q (kquants.h:95) */
                 int sc, m;
                 q4k_scale_min(b + 4, j, &sc, &m);
                 int32_t isum = 0;
-                for (int i = 0; i < 32; i++) isum += q4k_q(b, 32 * j + i) * xg[i];
+                for (int i = 0; i < 32; i++) isum += (type == T_Q5_K ? q5k_q(b, 32 * j + i) : q4k_q(b, 32 * j + i)) * xg[i];
                 float ds = or_fp16_to_f32(u16(b)) * (float)sc, dm = or_fp16_to_f32(u16(b + 2)) * (float)m;
                 float a = (ds * xs[g]) * (float)isum;
                 float bb = dm * xf[g];
                 val = val + (a - bb);
+            } else if (type == T_Q3_K) { /* Q6_K's fold with q' - 4 and the signed scales sc - 32 (kquants.h:101-104) */
+                int32_t I = 0;
+                for (int h = 0; h < 2; h++) {
+                    int jj = 2 * j + h;
+                    int32_t t = 0, xsum = 0;
+                    for (int i = 0; i < 16; i++) {
+                        t += q3k_q(b, 16 * jj + i) * xg[16 * h + i];
+                        xsum += xg[16 * h + i];
+                    }
+                    I += (q3k_scale(b, jj) - 32) * (t - 4 * xsum);
+                }
+                float d = or_fp16_to_f32(u16(b + 108));
+                val = val + (d * xs[g]) * (float)I;
             } else {
                 int32_t I = 0;
                 for (int h = 0; h < 2; h++) {
@@ -481,7 +516,7 @@ static int rd(const uint8_t *f, size_t sz, size_t *p, void *dst, size_t n) {
 }
 
 static size_t row_bytes(int type, int k) {
-    return type == T_Q8_0 ? (size_t)k / 32 * 34 : type == T_Q4_K ? (size_t)k / 256 * 144 : type == T_Q6_K ? (size_t)k / 256 * 210 : (size_t)k * 4;
+    return type == T_Q8_0 ? (size_t)k / 32 * 34 : (type >= T_Q3_K && type <= T_Q6_K) ? (size_t)k / 256 * kq_bytes(type) : (size_t)k * 4;
 }
 
 OrModel *or_model_load(const char *path, int cap, char *err, size_t errlen) {

@@ -8,7 +8,7 @@
  *       q8p_gemv_rows (:286), M > 1: q8p_gemm_item (:235) over every (32-row tile, chunk) item; OUT: M x N fp32.
  *       reps > 0: also times reps runs on `threads` threads (items split evenly), prints JSON seconds per run.
  *   ref_q8op kq TYPE BLK X XS M N K OUT
- *       BLK: N rows of K / 256 GGUF K-quant blocks (TYPE 12 Q4_K, 14 Q6_K), packed by kq_pack_blocks
+ *       BLK: N rows of K / 256 GGUF K-quant blocks (TYPE 11 Q3_K, 12 Q4_K, 13 Q5_K, 14 Q6_K), packed by kq_pack_blocks
  *       (kquants.h:253) and multiplied by the generic kq_dot (:608) with kq_act_prep's xf (:392).
  * All files raw little-endian arrays. */
 #include <pthread.h>
@@ -102,7 +102,7 @@ int main(int argc, char **argv) {
     }
     if (argc >= 10 && !strcmp(argv[1], "kq")) {
         int type = atoi(argv[2]), M = atoi(argv[6]), N = atoi(argv[7]), K = atoi(argv[8]);
-        if ((type != GGML_Q4_K && type != GGML_Q6_K) || M < 1 || N % 16 || K % 256) { fprintf(stderr, "ref_q8op: bad kq args\n"); return 2; }
+        if (type < GGML_Q3_K || type > GGML_Q6_K || M < 1 || N % 16 || K % 256) { fprintf(stderr, "ref_q8op: bad kq args\n"); return 2; }
         size_t bb = (size_t)kq_block_bytes(type) * (K / 256);
         uint8_t *blk = slurp(argv[3], (size_t)N * bb);
         int8_t *X = slurp(argv[4], (size_t)M * K);

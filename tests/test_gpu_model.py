@@ -23,7 +23,7 @@ def _bits_equal(a, b):
     return np.array_equal(np.ascontiguousarray(a, np.float32).view(np.uint32), np.ascontiguousarray(b, np.float32).view(np.uint32))
 
 
-@pytest.mark.parametrize("shape", ["tiny", "tiny_gqa4", "tiny_kq", "tiny_hd64", "tiny_hd32"])
+@pytest.mark.parametrize("shape", ["tiny", "tiny_gqa4", "tiny_kq", "tiny_q5k", "tiny_q3k", "tiny_hd64", "tiny_hd32"])
 def test_prefill_decode_bitexact_vs_oracle(gw, synth_models, shape):
     from oracle import oracle as orc
     path = synth_models(shape)

@@ -239,3 +239,24 @@ def test_seqfile_with_reference(gw, orc, tmp_path):
     p3 = str(tmp_path / "bad.seq")
     bad.tofile(p3)
     assert lib.rq_seq_load(ctypes.c_void_p(m.seq(1024)._h), p3.encode(), 10) == -7  # RQ_ERR_MISMATCH
+
+
+@pytest.mark.parametrize("shape", ["tiny_q5k", "tiny_q3k"])
+def test_q5k_q3k_models_greedy_bit_identical(gw, orc, tmp_path, shape):
+    """Q5_K_M- and Q3_K_M-style models (Q5_K / Q3_K matrices beside Q5_K / Q6_K ones, the K-quant embedding): a
+    64-token prefill and 24 greedy steps, every logits row equal bit for bit to the reference's, the same tokens"""
+    path, d = _synth(str(tmp_path), shape, seed=7)
+    m = gw.Model(path, ctx_len=512)
+    if not _exact(gw):
+        pytest.skip("this host does not provide the reference's float operations (AVX-512)")
+    ids = np.random.default_rng(5).integers(0, m.vocab, 64).astype(np.int32)
+    _, rlg, rtok, _ = orc.run_ref_driver(path, ids, str(tmp_path / "ref"), steps=24, threads=_threads(), cap=512)
+    c = m.ctx(max_batch=64, max_ctx=512)
+    s = m.seq(512)
+    lg = c.prefill(s, ids, mode=gw.RQ_LOGITS_LAST)
+    for step in range(25):
+        assert np.array_equal(_bits(lg), _bits(rlg[step])), f"row {step}: max diff {np.abs(lg - rlg[step]).max()}"
+        tok = int(np.argmax(lg))
+        if step < 24:
+            assert tok == int(rtok[step]), f"step {step}"
+            lg = c.decode(s, tok)

@@ -5,8 +5,8 @@
   whole forward passes (every logit, bit for bit) on synthetic models;
 * where the reference exposes no entry point, against what the mathematics fixes: brute-force integer block sums,
   every fp16 value, IEEE float16 rounding and the reference's saturation, the quantizer's closed form and its
-  rounding of exact halves away from zero, float64 exp / attention / RoPE, an independent numpy decoder of the ggml Q4_K /
-  Q6_K block formats (the published layout);
+  rounding of exact halves away from zero, float64 exp / attention / RoPE, an independent numpy decoder of the ggml Q3_K /
+  Q4_K / Q5_K / Q6_K block formats (the published layout);
 * the product's host-measured tables (gwenedeg_amd/csrc/gw_exact.c: the reference's rsqrtss / vrcp14ps / libmvec expf
   as the device reproduces them) against the reference's own operations on this host.
 The reference's fixtures for this path (tests/golden/logits, dequant) need model files absent here; the golden vectors
@@ -192,12 +192,64 @@ def _np_dequant_q6k(b):
     return y
 
 
-@pytest.mark.parametrize("typ", [12, 14])
+def _np_dequant_q5k(b):
+    """ggml's dequantize_row_q5_K on one 176-byte block (d, dmin, scales[12], qh[32], qs[128]): per 64 values c, the
+    nibbles of qs[32 c ..] plus 16 where bit 2 c (low nibbles) / 2 c + 1 (high) of qh[l] is set"""
+    d, dmin = b[0:2].view(np.float16)[0].astype(np.float32), b[2:4].view(np.float16)[0].astype(np.float32)
+    sc, qh, qs = b[4:16], b[16:48], b[48:176]
+
+    def scale_min(j):
+        if j < 4:
+            return int(sc[j]) & 63, int(sc[j + 4]) & 63
+        return (int(sc[j + 4]) & 0xF) | ((int(sc[j - 4]) >> 6) << 4), (int(sc[j + 4]) >> 4) | ((int(sc[j]) >> 6) << 4)
+    y = np.zeros(256, np.float32)
+    for c in range(4):
+        q = qs[32 * c:32 * c + 32].astype(np.int32)
+        for half in range(2):
+            s, m = scale_min(2 * c + half)
+            d1, m1 = np.float32(d * np.float32(s)), np.float32(dmin * np.float32(m))
+            nib = (q & 0xF) if half == 0 else (q >> 4)
+            nib = nib + np.where(qh.astype(np.int32) & (1 << (2 * c + half)), 16, 0)
+            y[64 * c + 32 * half:64 * c + 32 * half + 32] = d1 * nib.astype(np.float32) - m1
+    return y
+
+
+def _np_dequant_q3k(b):
+    """ggml's dequantize_row_q3_K on one 110-byte block (hmask[32], qs[64], scales[12], fp16 d): the 16 6-bit scales
+    unpacked as ggml's kmask shuffle on 32-bit words, then per 128 values and shift 2 j the 2-bit quants minus 4 where
+    the hmask bit is clear"""
+    hm, qs = b[0:32].astype(np.int32), b[32:96].astype(np.int32)
+    d = b[108:110].view(np.float16)[0].astype(np.float32)
+    aux = [int(v) for v in b[96:108].view(np.uint32)] + [0]
+    k1, k2, tmp = 0x03030303, 0x0F0F0F0F, aux[2]
+    aux[2] = ((aux[0] >> 4) & k2) | (((tmp >> 4) & k1) << 4)
+    aux[3] = ((aux[1] >> 4) & k2) | (((tmp >> 6) & k1) << 4)
+    aux[0] = (aux[0] & k2) | (((tmp >> 0) & k1) << 4)
+    aux[1] = (aux[1] & k2) | (((tmp >> 2) & k1) << 4)
+    scales = np.array(aux, np.uint32).view(np.int8).astype(np.int32)
+    y = np.zeros(256, np.float32)
+    i, m, o = 0, 1, 0
+    for n in range(2):
+        q = qs[32 * n:32 * n + 32]
+        for j in range(4):
+            for half in range(2):
+                dl = np.float32(d * np.float32(scales[i] - 32))
+                i += 1
+                qq = ((q[16 * half:16 * half + 16] >> (2 * j)) & 3) - np.where(hm[16 * half:16 * half + 16] & m, 0, 4)
+                y[o:o + 16] = dl * qq.astype(np.float32)
+                o += 16
+            m <<= 1
+    return y
+
+
+_KQ_DEC = {11: (_np_dequant_q3k, 110), 12: (_np_dequant_q4k, 144), 13: (_np_dequant_q5k, 176), 14: (_np_dequant_q6k, 210)}
+
+
+@pytest.mark.parametrize("typ", [11, 12, 13, 14])
 def test_kq_dequant_vs_independent_decoder(typ):
     """or_kq_dequant_row (kquants.h:222-251) against a numpy decoder written from ggml's block layout: bit for bit"""
     blk = _kq_blocks(typ, 4, 512, 20 + typ)
-    dec = _np_dequant_q4k if typ == 12 else _np_dequant_q6k
-    bs = 144 if typ == 12 else 210
+    dec, bs = _KQ_DEC[typ]
     for n in range(4):
         mine = orc.kq_dequant_row(typ, blk[n], 512)
         ref = np.concatenate([dec(blk[n][i * bs:(i + 1) * bs]) for i in range(2)])
@@ -205,7 +257,7 @@ def test_kq_dequant_vs_independent_decoder(typ):
 
 
 @need_ref
-@pytest.mark.parametrize("typ", [12, 14])
+@pytest.mark.parametrize("typ", [11, 12, 13, 14])
 @pytest.mark.parametrize("M", [1, 5])
 def test_kq_matmul_vs_reference(tmp_path, typ, M):
     """or_kq_matmul (kquants.h:86-109's fold) against the reference's kq dot compiled from its sources: bit for bit;
