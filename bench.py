@@ -59,9 +59,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--probe", action="store_true")
-    ap.add_argument("--workload", default="step", choices=["step", "batch32_4b", "long_8b"],
+    ap.add_argument("--workload", default="step", choices=["step", "batch32_4b", "long_8b", "cb_8b"],
                     help="step: the metric's workload (default); batch32_4b / long_8b: the batched decode of the "
-                         "reference's configs 3 / 4, a JSON line of their own")
+                         "reference's configs 3 / 4; cb_8b: config 5's continuous-batching steps; a JSON line of their own")
     ap.add_argument("--workdir", default=os.environ.get("GW_BENCH_DIR", "/dev/shm/gwenedeg_bench" if os.path.isdir("/dev/shm")
                                                                       else "/tmp/gwenedeg_bench"))
     a = ap.parse_args()
@@ -74,6 +74,9 @@ def main():
     from gwenedeg_amd import synth
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if a.workload == "cb_8b":
+        continuous(torch, gw, synth, a)
+        return
     if a.workload != "step":
         batched(torch, gw, synth, a)
         return
@@ -257,6 +260,107 @@ def batched(torch, gw, synth, a):
         "attention": {"kernel_ms_per_step": round(att_s * 1e3, 3),
                       "kv_gbs": round(kv_bytes / att_s / 1e9, 1) if att_s else None},
         "kernel_ms_per_step": {k: round(v[0] * 1e3, 3) for k, v in kt.items() if v[1]},
+    }
+    print(json.dumps(out), flush=True)
+
+
+def continuous(torch, gw, synth, a):
+    """Config 5: continuous batching on the 8B-shaped Q8_0 model. A step is what the reference's engine runs for 48
+    decoding sequences and 2 prompt chunks of 512 tokens (engine.c:3027-3255: decode rows first, then prompt chunks
+    within the budget): 1,072 rows in passes of at most RQ_BATCH_MAX = 512 rows (rq_forward_batch with the greedy
+    choice on the device): [48 decode rows + 464 prompt rows], [48 + 464], [96]. The decoding sequences start at
+    contexts uniform in [256, 8192] (rq_seq_fill_synthetic); prompts are 2,048 tokens, two prompt slots each taking a
+    512-token chunk per step, and a finished prompt starts a new request: one in four begins with the 1,024-token shared
+    prefix copied from the cache (rq_seq_copy) and prefills the rest. value = rows per second; per-step latency"""
+    shape, ndec, chunk, prompt, prefix = "qwen3_8b", 48, 512, 2048, 1024
+    steps = a.steps if a.steps != 3 else 40
+    rng = np.random.default_rng(a.seed)
+    os.makedirs(a.workdir, exist_ok=True)
+    path = os.path.join(a.workdir, f"{shape}_seed{a.seed}.gguf")
+    if not os.path.exists(path):
+        synth.write_gguf(path, shape, seed=a.seed)
+    ctxs = rng.integers(256, 8193, ndec)
+    cap = 8192 + steps + a.warmup + 16
+    m = gw.Model(path, ctx_len=max(cap, prompt + 16))
+    c = m.ctx(max_batch=512, max_ctx=max(cap, prompt + 16))
+    dec = [m.seq(cap) for _ in range(ndec)]
+    for i, sq in enumerate(dec):
+        sq.fill_synthetic(int(ctxs[i]), seed=a.seed + i)
+    shared = m.seq(prompt + 16)
+    shared.fill_synthetic(prefix, seed=a.seed + 999)
+    slots = [m.seq(prompt + 16) for _ in range(2)]
+    toks = [int(t) for t in rng.integers(0, m.vocab, ndec)]
+    nreq, nshared = [0], [0]
+
+    def start(sq):
+        # a new request in a prompt slot: one in four starts from the shared prefix
+        nreq[0] += 1
+        if nreq[0] % 4 == 0:
+            sq.copy_from(shared, prefix)
+            nshared[0] += 1
+        else:
+            sq.reset()
+
+    for sq in slots:
+        start(sq)
+
+    def one_step():
+        nonlocal toks
+        # this step's prompt rows: 512 from each slot (a prompt ending here: its last row's logits)
+        rows = []
+        for sq in slots:
+            n0 = len(sq)
+            ids = [int(t) for t in rng.integers(0, m.vocab, chunk)]
+            rows.append((sq, ids, n0 + chunk >= prompt))
+        dsegs = [gw.Segment(sq, [t], gw.RQ_LOGITS_LAST) for sq, t in zip(dec, toks)]
+        budget, passes, cur = 512, [], list(dsegs)
+        used = len(cur)
+        for sq, ids, last in rows:
+            o = 0
+            while o < len(ids):
+                take = min(budget - used, len(ids) - o)
+                end = o + take == len(ids)
+                cur.append(gw.Segment(sq, ids[o:o + take], gw.RQ_LOGITS_LAST if (end and last) else gw.RQ_LOGITS_NONE))
+                used += take
+                o += take
+                if used == budget:
+                    passes.append(cur)
+                    cur, used = [], 0
+        if cur:
+            passes.append(cur)
+        for i, segs in enumerate(passes):
+            out = c.forward_batch_argmax(segs)
+            if i == 0:
+                toks = [int(t) for t in out[:ndec]]
+        for sq, _, last in rows:
+            if last:
+                start(sq)
+
+    for _ in range(a.warmup):
+        one_step()
+    lat = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        t1 = time.perf_counter()
+        one_step()
+        lat.append(time.perf_counter() - t1)
+    el = time.perf_counter() - t0
+    lat = np.sort(np.array(lat))
+    rows_per_step = ndec + 2 * chunk
+    out = {
+        "metric": "continuous-batching tok/s and per-step latency (cb_8b: the reference's config 5, 1 GPU)",
+        "value": round(rows_per_step * steps / el, 1), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": a.warmup,
+        "ms_per_step": round(1e3 * el / steps, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 x int8 -> int32, fp32 fold; f16 KV", "data": "synthetic weights, random prompt ids; the decoding "
+                "sequences' K / V by rq_seq_fill_synthetic",
+        "config": {"workload": f"{shape}: per step {ndec} decode rows at contexts U[256, 8192] + 2 x {chunk} prompt rows "
+                               f"(prompts of {prompt}, 1 in 4 from a {prefix}-token shared prefix), passes of <= 512 rows",
+                   "global_batch": rows_per_step, "seq_len": 8192},
+        "step_latency_ms": {"p50": round(1e3 * float(lat[len(lat) // 2]), 3), "p90": round(1e3 * float(lat[int(0.9 * (len(lat) - 1))]), 3),
+                            "max": round(1e3 * float(lat[-1]), 3)},
+        "decode_tok_s": round(ndec * steps / el, 1), "prompt_tok_s": round(2 * chunk * steps / el, 1),
+        "requests_started": nreq[0], "requests_from_shared_prefix": nshared[0],
     }
     print(json.dumps(out), flush=True)
 

@@ -217,3 +217,44 @@ def test_decode_same_bits_without_warm_next(gw, synth_models, shape):
     finally:
         gw.lib.gw_gemv_warm_next(prev)
     assert all(_bits_equal(a, b) for a, b in zip(out[0], out[1]))
+
+
+def test_config5_mixed_pass_equals_each_sequence_alone(gw, tmp_path):
+    """config 5's pass shape at the 8B model's widths (2 layers): decoding sequences at contexts up to 3000 (past the
+    combine-in-GEMV limit), a fresh prompt chunk and a chunk that continues a shared 1,024-token prefix copied from the
+    cache (rq_seq_copy), all in one rq_forward_batch, twice: every logits row equal bit for bit to the row the same
+    sequence gives when it runs alone (runq.h:22-24)"""
+    import os
+    from gwenedeg_amd import synth
+    d = dict(synth.SHAPES["qwen3_8b"], n_layers=2, vocab=4096)
+    path = os.path.join(str(tmp_path), "c5.gguf")
+    synth.write_gguf(path, d, seed=3)
+    m = gw.Model(path, ctx_len=4096)
+    c = m.ctx(max_batch=512, max_ctx=4096)
+    rng = np.random.default_rng(8)
+    ctxs = [256, 700, 1100, 1800, 2500, 3000]
+    dec = [m.seq(4096) for _ in ctxs]
+    for i, (sq, n) in enumerate(zip(dec, ctxs)):
+        sq.fill_synthetic(n, seed=40 + i)
+    shared = m.seq(4096)
+    shared.fill_synthetic(1024, seed=77)
+    fresh, cont = m.seq(4096), m.seq(4096)
+    cont.copy_from(shared, 1024)
+    seqs = dec + [fresh, cont]
+    twins = [m.seq(4096) for _ in seqs]
+    for tw, sq in zip(twins, seqs):
+        if len(sq):
+            tw.copy_from(sq, len(sq))
+    toks = [int(t) for t in rng.integers(0, m.vocab, len(dec))]
+    for rnd in range(2):
+        ca = [int(t) for t in rng.integers(0, m.vocab, 200)]
+        cb = [int(t) for t in rng.integers(0, m.vocab, 150)]
+        segs = [gw.Segment(sq, [t], gw.RQ_LOGITS_LAST) for sq, t in zip(dec, toks)]
+        segs += [gw.Segment(fresh, ca, gw.RQ_LOGITS_ALL), gw.Segment(cont, cb, gw.RQ_LOGITS_ALL)]
+        lg, _ = c.forward_batch(segs)
+        alone = [c.decode(tw, t) for tw, t in zip(twins[:len(dec)], toks)]
+        alone += list(c.prefill(twins[-2], ca, mode=gw.RQ_LOGITS_ALL)) + list(c.prefill(twins[-1], cb, mode=gw.RQ_LOGITS_ALL))
+        assert lg.shape[0] == len(alone) == len(dec) + 350
+        for r, (a, b) in enumerate(zip(lg, alone)):
+            assert _bits_equal(a, b), f"round {rnd} row {r}: max diff {np.abs(a - b).max()}"
+        toks = [int(np.argmax(lg[i])) for i in range(len(dec))]
