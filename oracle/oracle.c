@@ -314,9 +314,32 @@ size_t or_kv_tile(int t, int h, int n_kv, int hd) {
     return (((size_t)(t / ATT_P) * n_kv + h) * ATT_P + (size_t)(t % ATT_P / ATT_T) * ATT_T) * hd;
 }
 
-void or_attention_block(float *o, float *ml, const float *q, const uint16_t *kc, const uint16_t *vc, int n, int b, int h,
-                        int n_kv, int hd, float scale) {
-    /* attention_vec (forward.c:1346-1403) on block b of kv head h: positions t0 .. t0 + nb - 1 */
+/* The 16-bit caches' layouts inside a tile (forward.c:1901-1951): f16 K at [i][j], V rows [j][i]; bf16 K in dim pairs,
+ * dims 2p, 2p + 1 of position j at 32 p + 2 j (+ 1), V rows with dims 32 c + l, 32 c + 16 + l at 32 c + 2 l (+ 1) */
+static size_t kv_k_at(int bf, int i, int j) { return bf ? (size_t)(i & ~1) * ATT_T + 2 * j + (i & 1) : (size_t)i * ATT_T + j; }
+static size_t kv_v_at(int bf, int i, int j, int hd) {
+    return (size_t)j * hd + (bf ? (size_t)((i & ~31) + 2 * (i & 15) + ((i >> 4) & 1)) : (size_t)i);
+}
+static float kv_f32(int bf, uint16_t h) { /* exact */
+    if (!bf) return or_fp16_to_f32(h);
+    uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+uint16_t or_f32_bf16(float f) {
+    /* kernels_avx512.h:60-69: round to nearest even; NaN stays a quiet NaN */
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    uint32_t r = (u + 0x7fffu + ((u >> 16) & 1)) >> 16;
+    return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? (u >> 16) | 0x40 : r);
+}
+
+static void attention_block(int bf, float *o, float *ml, const float *q, const uint16_t *kc, const uint16_t *vc, int n, int b,
+                            int h, int n_kv, int hd, float scale) {
+    /* attention_vec (forward.c:1346-1403) on block b of kv head h: positions t0 .. t0 + nb - 1; an f16 (bf 0) or bf16
+     * cache, the values converted exactly (kv_block_f32, forward.c:1433-1451) */
     int t0 = b * ATT_P, nb = n - t0 < ATT_P ? n - t0 : ATT_P;
     float S[ATT_P] = { 0 };
     for (int t = 0; t < nb; t++) {
@@ -325,7 +348,7 @@ void or_attention_block(float *o, float *ml, const float *q, const uint16_t *kc,
         float a = 0;
         for (int i0 = 0; i0 < hd; i0 += ATT_DC) {
             float c = 0;
-            for (int i = i0; i < i0 + ATT_DC; i++) c = fmaf(q[i], or_fp16_to_f32(k[i * ATT_T + j]), c);
+            for (int i = i0; i < i0 + ATT_DC; i++) c = fmaf(q[i], kv_f32(bf, k[kv_k_at(bf, i, j)]), c);
             a = i0 > 0 ? a + c : c;
         }
         S[t] = a * scale;
@@ -346,9 +369,14 @@ void or_attention_block(float *o, float *ml, const float *q, const uint16_t *kc,
     ml[1] = sum[0];
     for (int i = 0; i < hd; i++) o[i] = 0.0f;
     for (int t = 0; t < nb; t++) {
-        const uint16_t *v = vc + or_kv_tile(t0 + t, h, n_kv, hd) + (size_t)(t % ATT_T) * hd;
-        for (int i = 0; i < hd; i++) o[i] = fmaf(S[t], or_fp16_to_f32(v[i]), o[i]);
+        const uint16_t *v = vc + or_kv_tile(t0 + t, h, n_kv, hd);
+        for (int i = 0; i < hd; i++) o[i] = fmaf(S[t], kv_f32(bf, v[kv_v_at(bf, i, t % ATT_T, hd)]), o[i]);
     }
+}
+
+void or_attention_block(float *o, float *ml, const float *q, const uint16_t *kc, const uint16_t *vc, int n, int b, int h,
+                        int n_kv, int hd, float scale) {
+    attention_block(0, o, ml, q, kc, vc, n, b, h, n_kv, hd, scale);
 }
 
 void or_att_combine(float *out, int nb, const float *part, size_t stride, int hd) {
@@ -373,16 +401,21 @@ void or_att_combine(float *out, int nb, const float *part, size_t stride, int hd
     for (int i = 0; i < hd; i++) out[i] = out[i] * inv;
 }
 
-void or_attention(float *out, const float *q, const uint16_t *kc, const uint16_t *vc, int n, int h, int n_kv, int hd,
-                  float scale) {
+static void attention(int bf, float *out, const float *q, const uint16_t *kc, const uint16_t *vc, int n, int h, int n_kv,
+                      int hd, float scale) {
     /* attention_kv (forward.c:1871-1892): one block directly, else the partials of every block, combined */
     int nb = (n + ATT_P - 1) / ATT_P;
     size_t st = (size_t)hd + 16;
     float *part = malloc((size_t)nb * st * sizeof(float));
     for (int b = 0; b < nb; b++)
-        or_attention_block(part + b * st, part + b * st + hd, q, kc, vc, n, b, h, n_kv, hd, scale);
+        attention_block(bf, part + b * st, part + b * st + hd, q, kc, vc, n, b, h, n_kv, hd, scale);
     or_att_combine(out, nb, part, st, hd);
     free(part);
+}
+
+void or_attention(float *out, const float *q, const uint16_t *kc, const uint16_t *vc, int n, int h, int n_kv, int hd,
+                  float scale) {
+    attention(0, out, q, kc, vc, n, h, n_kv, hd, scale);
 }
 
 /* ------------------------------------------------------------------------------- norms, RoPE, SwiGLU */
@@ -502,7 +535,7 @@ struct OrModel {
 
 struct OrSeq {
     const OrModel *m;
-    int len;
+    int len, bf; /* bf: a bf16 cache (RQ_KV_BF16), else f16 */
     uint16_t *kc, *vc;
 };
 
@@ -665,6 +698,13 @@ OrSeq *or_seq_new(const OrModel *m) {
     return s;
 }
 
+OrSeq *or_seq_new_kv(const OrModel *m, int bf16) {
+    /* a sequence whose cache is bf16 (RQ_KV_BF16: the same tiles, the bf16 layouts) or f16 */
+    OrSeq *s = or_seq_new(m);
+    if (s) s->bf = bf16 != 0;
+    return s;
+}
+
 void or_seq_free(OrSeq *s) {
     if (!s) return;
     free(s->kc);
@@ -682,10 +722,10 @@ void or_seq_copy(OrSeq *dst, const OrSeq *src, int n) {
         for (int t = 0; t < n; t++)
             for (int h = 0; h < src->m->nkv; h++) {
                 size_t o = (size_t)l * per + or_kv_tile(t, h, src->m->nkv, src->m->hd);
-                int j = t % ATT_T, hd = src->m->hd;
+                int j = t % ATT_T, hd = src->m->hd, bf = src->bf;
                 for (int i = 0; i < hd; i++) {
-                    dst->kc[o + (size_t)i * ATT_T + j] = src->kc[o + (size_t)i * ATT_T + j];
-                    dst->vc[o + (size_t)j * hd + i] = src->vc[o + (size_t)j * hd + i];
+                    dst->kc[o + kv_k_at(bf, i, j)] = src->kc[o + kv_k_at(bf, i, j)];
+                    dst->vc[o + kv_v_at(bf, i, j, hd)] = src->vc[o + kv_v_at(bf, i, j, hd)];
                 }
             }
     dst->len = n;
@@ -752,16 +792,16 @@ int or_forward_token(const OrModel *m, OrSeq *s, int token, float *logits, float
         or_qk_norm_rope(q, nh, m->q_norm[l], hd, cs);
         or_qk_norm_rope(k, nkv, m->k_norm[l], hd, cs);
         uint16_t *kc = s->kc + (size_t)l * per, *vc = s->vc + (size_t)l * per;
-        for (int g = 0; g < nkv; g++) { /* kv_store (forward.c:1901-1951), f16 */
+        for (int g = 0; g < nkv; g++) { /* kv_store (forward.c:1901-1951), f16 or bf16, rounded to nearest even */
             size_t o = or_kv_tile(pos, g, nkv, hd);
-            int j = pos % ATT_T;
+            int j = pos % ATT_T, bf = s->bf;
             for (int i = 0; i < hd; i++) {
-                kc[o + (size_t)i * ATT_T + j] = or_f32_f16(k[g * hd + i]);
-                vc[o + (size_t)j * hd + i] = or_f32_f16(v[g * hd + i]);
+                kc[o + kv_k_at(bf, i, j)] = bf ? or_f32_bf16(k[g * hd + i]) : or_f32_f16(k[g * hd + i]);
+                vc[o + kv_v_at(bf, i, j, hd)] = bf ? or_f32_bf16(v[g * hd + i]) : or_f32_f16(v[g * hd + i]);
             }
         }
         for (int h = 0; h < nh; h++)
-            or_attention(att + h * hd, q + h * hd, kc, vc, pos + 1, h / kv_mul, nkv, hd, m->att_scale);
+            attention(s->bf, att + h * hd, q + h * hd, kc, vc, pos + 1, h / kv_mul, nkv, hd, m->att_scale);
         or_quantize(xq, xs, att, qd);
         matvec(xb, &m->wo[l], xq, xs);
         for (int i = 0; i < dim; i++) x[i] += xb[i];

@@ -57,6 +57,8 @@ void or_model_free(OrModel *m);
 void or_model_dims(const OrModel *m, int *d8);
 float or_model_att_scale(const OrModel *m);
 OrSeq *or_seq_new(const OrModel *m);
+OrSeq *or_seq_new_kv(const OrModel *m, int bf16); /* bf16 1: a bf16 cache (RQ_KV_BF16) */
+uint16_t or_f32_bf16(float f);
 void or_seq_free(OrSeq *s);
 int or_seq_len(const OrSeq *s);
 void or_seq_truncate(OrSeq *s, int n);

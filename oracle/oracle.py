@@ -56,6 +56,7 @@ def lib() -> ctypes.CDLL:
             "or_model_dims": (None, [P, P]),
             "or_model_att_scale": (F, [P]),
             "or_seq_new": (P, [P]),
+            "or_seq_new_kv": (P, [P, I]),
             "or_seq_free": (None, [P]),
             "or_seq_len": (I, [P]),
             "or_seq_truncate": (None, [P, I]),
@@ -130,8 +131,8 @@ class Model:
         self.dim, self.hidden, self.n_layers, self.n_heads, self.n_kv_heads, self.head_dim, self.vocab, self.kv_len = \
             (int(v) for v in d)
 
-    def seq(self) -> "Seq":
-        return Seq(self)
+    def seq(self, bf16: bool = False) -> "Seq":
+        return Seq(self, bf16)
 
     def __del__(self):
         if getattr(self, "_h", None):
@@ -140,9 +141,9 @@ class Model:
 
 
 class Seq:
-    def __init__(self, m: Model):
+    def __init__(self, m: Model, bf16: bool = False):
         self.m = m
-        self._h = lib().or_seq_new(m._h)
+        self._h = lib().or_seq_new_kv(m._h, 1 if bf16 else 0)
 
     def __len__(self):
         return lib().or_seq_len(self._h)
@@ -178,7 +179,7 @@ def have_ref() -> bool:
 
 def run_ref_driver(model: str, ids: np.ndarray, workdir: str, steps: int = 0, threads: int = 0, cap: int = 0,
                    batch: int = 512, all_logits: bool = False, batch_decode: int = 0, reps: int = 1, kv: bool = False,
-                   hidden: bool = False, timeout: float = 600):
+                   hidden: bool = False, kv_type: int = 2, timeout: float = 600):
     """The reference's own CPU path (oracle/_ref/ref_driver) on a GGUF file and token ids: returns (info JSON,
     logits rows written, generated tokens, KV file path or None)."""
     os.makedirs(workdir, exist_ok=True)
@@ -197,6 +198,8 @@ def run_ref_driver(model: str, ids: np.ndarray, workdir: str, steps: int = 0, th
         cmd += ["--batch-decode", str(batch_decode)]
     if kv:
         cmd += ["--kv", kv_path]
+    if kv_type != 2:  # (RQ_KV_F16, the default)
+        cmd += ["--kv-type", str(kv_type)]
     hid_path = os.path.join(workdir, "hidden.bin")
     if hidden:
         cmd += ["--hidden", hid_path]

@@ -10,6 +10,7 @@
  *   passes of one row per sequence (rq_forward_batch, RQ_LOGITS_LAST each: batch_decode_worker).
  *   --hidden FILE: instead, the prompt token by token through rq_decode_hidden (runq.h:350), every row's logits and
  *   final hidden state (after output_norm, dim floats) written.
+ *   --kv-type T: the sequences' KV cache type (runq.h:214; default RQ_KV_F16).
  * Output: one JSON line on stdout. */
 #include <stdint.h>
 #include <stdio.h>
@@ -42,7 +43,7 @@ static void write_all(FILE *f, const void *p, size_t n) {
 
 int main(int argc, char **argv) {
     const char *model = NULL, *ids_path = NULL, *logits_path = NULL, *tokens_path = NULL, *kv_path = NULL, *hidden_path = NULL;
-    int threads = 0, cap = 0, maxb = 512, steps = 0, reps = 1, all_logits = 0, nbd = 0;
+    int threads = 0, cap = 0, maxb = 512, steps = 0, reps = 1, all_logits = 0, nbd = 0, kv_type = RQ_KV_F16;
     for (int i = 1; i < argc; i++) {
         const char *a = argv[i], *v = i + 1 < argc ? argv[i + 1] : NULL;
         if (!strcmp(a, "-m") && v) model = v, i++;
@@ -58,6 +59,7 @@ int main(int argc, char **argv) {
         else if (!strcmp(a, "--batch-decode") && v) nbd = atoi(v), i++;
         else if (!strcmp(a, "--all-logits")) all_logits = 1;
         else if (!strcmp(a, "--hidden") && v) hidden_path = v, i++;
+        else if (!strcmp(a, "--kv-type") && v) kv_type = atoi(v), i++;
         else { fprintf(stderr, "ref_driver: bad argument %s\n", a); return 2; }
     }
     if (!model || !ids_path) { fprintf(stderr, "usage: ref_driver -m MODEL --ids FILE [--steps K] ...\n"); return 2; }
@@ -81,7 +83,7 @@ int main(int argc, char **argv) {
     if (!c) die("rq_ctx_new", e, NULL);
     RqSeq **sq = calloc((size_t)ns, sizeof(RqSeq *));
     for (int i = 0; i < ns; i++)
-        if (!(sq[i] = rq_seq_new(m, cap, RQ_KV_F16, &e))) die("rq_seq_new", e, NULL);
+        if (!(sq[i] = rq_seq_new(m, cap, kv_type, &e))) die("rq_seq_new", e, NULL);
     FILE *lf = logits_path ? fopen(logits_path, "wb") : NULL, *tf = tokens_path ? fopen(tokens_path, "wb") : NULL;
     if ((logits_path && !lf) || (tokens_path && !tf)) { perror("output"); return 1; }
     float *out = malloc((size_t)(all_logits ? n : ns) * V * sizeof(float));

@@ -389,24 +389,28 @@ def test_attention_combine_matches_single_pass():
 
 
 @need_ref
-@pytest.mark.parametrize("shape,over,n", [
-    ("tiny", {}, 40),
-    ("tiny_kq", {}, 20),
-    ("qwen3_0_6b", dict(n_layers=3, vocab=4096, tied=0), 12),
+@pytest.mark.parametrize("shape,over,n,bf16", [
+    ("tiny", {}, 40, False),
+    ("tiny_kq", {}, 20, False),
+    ("qwen3_0_6b", dict(n_layers=3, vocab=4096, tied=0), 12, False),
+    ("tiny", {}, 40, True),
+    ("qwen3_0_6b", dict(n_layers=2, vocab=4096, tied=0), 270, True),
 ])
-def test_forward_bit_exact_vs_reference(tmp_path, shape, over, n):
+def test_forward_bit_exact_vs_reference(tmp_path, shape, over, n, bf16):
     """or_forward_token position by position against the reference compiled from its sources (rq_prefill with every
     row's logits, ref_driver), on seeded synthetic models: every logit bit for bit. On an AVX-512 host the oracle's
-    SwiGLU runs the reference's own vector expf and rcp14; nothing else in the pass depends on the host"""
+    SwiGLU runs the reference's own vector expf and rcp14; nothing else in the pass depends on the host. bf16: both
+    with a bf16 KV cache (RQ_KV_BF16; 270 positions: two attention blocks)"""
     from gwenedeg_amd import synth
     d = dict(synth.SHAPES[shape])
     d.update(over)
     path = str(tmp_path / "m.gguf")
     synth.write_gguf(path, d, seed=1)
     ids = np.random.default_rng(7).integers(0, d["vocab"], n).astype(np.int32)
-    _, lg, _, _ = orc.run_ref_driver(path, ids, str(tmp_path / "ref"), threads=4, cap=512, all_logits=True)
+    _, lg, _, _ = orc.run_ref_driver(path, ids, str(tmp_path / "ref"), threads=4, cap=512, all_logits=True,
+                                     kv_type=1 if bf16 else 2)
     om = orc.Model(path, cap=512)
-    s = om.seq()
+    s = om.seq(bf16=bf16)
     for i, t in enumerate(ids):
         mine = s.forward(int(t))
         assert np.array_equal(_u32(mine), _u32(lg[i])), f"position {i}: max diff {np.abs(mine - lg[i]).max()}"
