@@ -66,6 +66,21 @@ __device__ __forceinline__ uint16_t f2h_ref(float f) {
     return (uint16_t)(sign | h);
 }
 
+__device__ __forceinline__ uint16_t f2bf_ref(float f) {
+    // fp32 -> bf16 as the reference's f32_bf16 (kernels_avx512.h:60-69): round to nearest even, NaN quiet
+    uint32_t u = __float_as_uint(f);
+    uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? (u >> 16) | 0x40u : r);
+}
+
+__device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); } // (h < 2^16: exact)
+
+// The 16-bit KV caches inside a tile of 16 positions j (forward.c:1901-1951): f16 K at [i][j], V rows [j][i]; bf16
+// (RQ_KV_BF16) K in dim pairs, dims 2p, 2p + 1 of position j at 32 p + 2 j (+ 1), V rows with dims 32 c + l and
+// 32 c + 16 + l (l < 16) at 32 c + 2 l (+ 1). Offsets in 16-bit elements
+__device__ __forceinline__ int kv_k_at(bool bf, int i, int j) { return bf ? (i & ~1) * 16 + 2 * j + (i & 1) : i * 16 + j; }
+__device__ __forceinline__ int kv_v_col(bool bf, int i) { return bf ? (i & ~31) + 2 * (i & 15) + ((i >> 4) & 1) : i; }
+
 __device__ __forceinline__ float exp_att(float x) {
     // forward.c:1301-1321 (att512_exp): Cephes-style expf, x clamped at -86
     x = x > -86.0f ? x : -86.0f;

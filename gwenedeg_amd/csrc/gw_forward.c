@@ -48,10 +48,12 @@ RqSeq *rq_seq_new(const RqModel *m, int capacity, int kv_type, int *err) {
     RqSeq *s = NULL;
     if (!m) { e = RQ_ERR_STATE; goto fail; }
     if (capacity <= 0) capacity = m->seq_len;
-    if (capacity > m->seq_len || kv_type != RQ_KV_F16) { e = RQ_ERR_ARG; goto fail; }
+    /* f16 and bf16 caches (the fp32 attention on the exactly converted values, runq.h:204-213); other types RQ_ERR_ARG */
+    if (capacity > m->seq_len || (kv_type != RQ_KV_F16 && kv_type != RQ_KV_BF16)) { e = RQ_ERR_ARG; goto fail; }
     s = calloc(1, sizeof(RqSeq));
     if (!s) { e = RQ_ERR_NOMEM; goto fail; }
     s->m = m;
+    s->kvt = kv_type;
     s->cap = capacity;
     s->kv_len = (capacity + GW_ATT_P - 1) / GW_ATT_P * GW_ATT_P;
     size_t bytes = (size_t)m->n_layers * seq_layer_elems(s) * 2;
@@ -125,7 +127,8 @@ size_t rq_seq_kv_bytes(const RqSeq *s, int n) {
 int rq_seq_copy(RqSeq *dst, const RqSeq *src, int n) {
     /* forward.c:553-576: dst := the first n positions of src (whole blocks below n, then the last block's tiles up to
      * position n - 1 per kv head: the tiled layout of forward.c:1894-1899), device to device */
-    if (!dst || !src || dst == src || dst->m != src->m || n < 0 || n > src->len || n > dst->cap) return RQ_ERR_ARG;
+    if (!dst || !src || dst == src || dst->m != src->m || dst->kvt != src->kvt || n < 0 || n > src->len || n > dst->cap)
+        return RQ_ERR_ARG;
     const RqModel *m = src->m;
     int nkv = m->n_kv_heads, hd = m->head_dim, full = n / GW_ATT_P, rem = n % GW_ATT_P;
     size_t kvd = (size_t)nkv * hd, ntl = (size_t)(rem + GW_ATT_T - 1) / GW_ATT_T;
@@ -256,7 +259,7 @@ int rq_seq_mem(const RqModel *m, int capacity, int kv_type, RqSeqMem *mem) {
     memset(mem, 0, sizeof(*mem));
     if (!m) return RQ_ERR_STATE;
     if (capacity <= 0) capacity = m->seq_len;
-    if (capacity > m->seq_len || kv_type != RQ_KV_F16) return RQ_ERR_ARG;
+    if (capacity > m->seq_len || (kv_type != RQ_KV_F16 && kv_type != RQ_KV_BF16)) return RQ_ERR_ARG;
     size_t kv_len = ((size_t)capacity + GW_ATT_P - 1) / GW_ATT_P * GW_ATT_P;
     mem->kv = (size_t)m->n_layers * kv_len * m->n_kv_heads * m->head_dim * 2 * 2 + (size_t)capacity * sizeof(int);
     mem->total = mem->kv;
@@ -527,7 +530,7 @@ static int fused_layer(RqCtx *c, int l, RqSeq *sq, int pos, const int *pos_d) {
     pf_mark(c, GW_PF_ATT);
     KCHK(gw_k_attn_decode(c->qkv, nh, m->n_kv_heads, hd, m->att_scale, y->q_norm, y->k_norm, m->rope, pos,
                           sq->kc + (size_t)l * seq_layer_elems(sq), sq->vc + (size_t)l * seq_layer_elems(sq), c->part,
-                          c->pstride, s));
+                          c->pstride, sq->kvt == RQ_KV_BF16, s));
     if (nb <= GW_GV_NBMAX) {
         pf_mark(c, GW_PF_WO);
         KCHK(gw_k_gemv1_combine(&y->wo, GW_GV_R_WO, c->part, c->pstride, hd, nb, c->x, 1, &y->w13[0], GW_GV_R_W13, s));
@@ -567,7 +570,8 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
         b = e;
     }
     /* metadata block: tok, pos, sel (int), kc / vc tables per layer (pointers), items */
-    size_t o_tok = 0, o_pos = o_tok + (size_t)n * 4, o_sel = o_pos + (size_t)n * 4, o_ptr = (o_sel + (size_t)n * 4 + 15) / 16 * 16;
+    size_t o_tok = 0, o_pos = o_tok + (size_t)n * 4, o_sel = o_pos + (size_t)n * 4, o_kbf = o_sel + (size_t)n * 4;
+    size_t o_ptr = (o_kbf + (size_t)n * 4 + 15) / 16 * 16;
     size_t o_items = o_ptr + (size_t)2 * L * n * sizeof(void *), total = o_items + (size_t)nitems * sizeof(Item);
     if ((rc = ctx_meta(c, total)) != RQ_OK) return rc;
     HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream)); /* (the pinned block may still feed a copy) */
@@ -575,6 +579,8 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
     memcpy(h + o_tok, P->tok, (size_t)n * 4);
     memcpy(h + o_pos, P->pos, (size_t)n * 4);
     memcpy(h + o_sel, P->sel, (size_t)n * 4);
+    int *kbf = (int *)(h + o_kbf), nbf = 0; /* (rows of bf16 caches; their attention items go last) */
+    for (int b = 0; b < n; b++) kbf[b] = P->seq[b]->kvt == RQ_KV_BF16;
     uint16_t **ptr = (uint16_t **)(h + o_ptr);
     for (int l = 0; l < L; l++)
         for (int b = 0; b < n; b++) {
@@ -583,16 +589,21 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
             ptr[(size_t)(L + l) * n + b] = P->seq[b]->vc + lo;
         }
     Item *it = (Item *)(h + o_items);
-    for (int b = 0, k = 0; b < n;) {
-        int e = b + 1;
-        while (e < n && e - b < rb && P->seq[e] == P->seq[b] && P->pos[e] == P->pos[e - 1] + 1) e++;
-        int nb = (P->pos[e - 1] + 1 + GW_ATT_P - 1) / GW_ATT_P;
-        for (int g = 0; g < nkv; g++)
-            for (int kb = 0; kb < nb; kb++) it[k++] = (Item){ b, e - b, g, kb };
-        b = e;
-    }
+    for (int pass = 0, k = 0; pass < 2; pass++) /* the f16 caches' items, then the bf16 caches' */
+        for (int b = 0; b < n;) {
+            int e = b + 1;
+            while (e < n && e - b < rb && P->seq[e] == P->seq[b] && P->pos[e] == P->pos[e - 1] + 1) e++;
+            int nb = (P->pos[e - 1] + 1 + GW_ATT_P - 1) / GW_ATT_P;
+            if (kbf[b] == pass) {
+                for (int g = 0; g < nkv; g++)
+                    for (int kb = 0; kb < nb; kb++) it[k++] = (Item){ b, e - b, g, kb };
+                nbf += pass ? nkv * nb : 0;
+            }
+            b = e;
+        }
     HIPCHK(c, "hipMemcpyAsync (pass metadata)", hipMemcpyAsync(d, h, total, hipMemcpyHostToDevice, c->stream));
     const int *tok_d = (const int *)(d + o_tok), *pos_d = (const int *)(d + o_pos), *sel_d = (const int *)(d + o_sel);
+    const int *kbf_d = (const int *)(d + o_kbf);
     uint16_t *const *kc_d = (uint16_t *const *)(d + o_ptr), *const *vc_d = kc_d + (size_t)L * n;
     const void *items_d = d + o_items;
     hipStream_t s = c->stream;
@@ -623,10 +634,14 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
         }
         pf_mark(c, GW_PF_ROPE);
         KCHK(gw_k_qknorm_rope_store(c->qkv, c->ldqkv, n, nh, nkv, hd, y->q_norm, y->k_norm, m->rope, pos_d,
-                                    kc_d + (size_t)l * n, vc_d + (size_t)l * n, s));
+                                    kc_d + (size_t)l * n, vc_d + (size_t)l * n, nbf ? kbf_d : NULL, s));
         pf_mark(c, GW_PF_ATT);
-        KCHK(gw_k_attn_part(items_d, nitems, nq_max, c->qkv, c->ldqkv, nh, nkv, hd, m->att_scale, pos_d,
-                            kc_d + (size_t)l * n, vc_d + (size_t)l * n, c->part, c->pstride, s));
+        if (nitems > nbf)
+            KCHK(gw_k_attn_part(items_d, nitems - nbf, nq_max, c->qkv, c->ldqkv, nh, nkv, hd, m->att_scale, pos_d,
+                                kc_d + (size_t)l * n, vc_d + (size_t)l * n, c->part, c->pstride, 0, s));
+        if (nbf)
+            KCHK(gw_k_attn_part((const Item *)items_d + (nitems - nbf), nbf, nq_max, c->qkv, c->ldqkv, nh, nkv, hd,
+                                m->att_scale, pos_d, kc_d + (size_t)l * n, vc_d + (size_t)l * n, c->part, c->pstride, 1, s));
         if (fused) {
             if (nbmax <= GW_GV_NBMAX) {
                 pf_mark(c, GW_PF_WO);

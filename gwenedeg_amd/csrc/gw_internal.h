@@ -79,7 +79,8 @@ struct RqModel {
 struct RqSeq {
     const RqModel *m;
     int cap, kv_len, len, hwm;
-    uint16_t *kc, *vc; /* device: n_layers x kv_len x kv_dim f16 each */
+    uint16_t *kc, *vc; /* device: n_layers x kv_len x kv_dim 16-bit values each (f16, or bf16 when kvt is) */
+    int kvt;           /* RQ_KV_F16 or RQ_KV_BF16 */
     int *tokens;       /* host */
     unsigned long long rng;
 };
@@ -153,13 +154,14 @@ int gw_k_kq_pad(const uint8_t *src, size_t nblk, int sbytes, int dbytes, uint8_t
 int gw_k_rmsnorm_quant(float *x, const float *d, int dim, const float *w, const int *sel, int n, int8_t *xq, float *xs,
                        int ldq, float *hid, hipStream_t s);
 int gw_k_qknorm_rope_store(float *qkv, int ldqkv, int n, int nh, int nkv, int hd, const float *qn, const float *kn,
-                           const float *rope, const int *pos, uint16_t *const *kc, uint16_t *const *vc, hipStream_t s);
+                           const float *rope, const int *pos, uint16_t *const *kc, uint16_t *const *vc,
+                           const int *kbf, hipStream_t s); /* kbf: per row, 1 for a bf16 cache (NULL: all f16) */
 int gw_k_attn_part(const void *items, int nitems, int nq_max, const float *qkv, int ldqkv, int nh, int nkv, int hd, float scale,
-                   const int *pos, uint16_t *const *kc, uint16_t *const *vc, float *part, int pstride, hipStream_t s);
+                   const int *pos, uint16_t *const *kc, uint16_t *const *vc, float *part, int pstride, int kbf, hipStream_t s);
 /* the one-row pass's attention with its QK-norm, RoPE and K / V store (hd 32, 64 or 128; pos: the row's position;
  * kl / vl: its sequence's K / V cache of the layer) */
 int gw_k_attn_decode(const float *qkv, int nh, int nkv, int hd, float scale, const float *qn, const float *kn, const float *rope,
-                     int pos, uint16_t *kl, uint16_t *vl, float *part, int pstride, hipStream_t s);
+                     int pos, uint16_t *kl, uint16_t *vl, float *part, int pstride, int kbf, hipStream_t s);
 int gw_k_attn_combine_quant(const float *part, int pstride, int nh, int hd, const int *pos, int n, int8_t *aq, float *as,
                             int ldq, float *att_out, hipStream_t s);
 /* hb row: [h (H) | h2 (H)] (il = 0) or blocks of il h then il h2 (w1 / w3 rows interleaved by il) */

@@ -124,9 +124,11 @@ __global__ __launch_bounds__(NORM_T) void k_rmsnorm_quant(float *__restrict__ x,
 __global__ __launch_bounds__(64) void k_qknorm_rope_store(float *__restrict__ qkv, int ldqkv, int nh, int nkv, int hd,
                                                           const float *__restrict__ qn, const float *__restrict__ kn,
                                                           const float *__restrict__ rope, const int *__restrict__ pos,
-                                                          uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc) {
+                                                          uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc,
+                                                          const int *__restrict__ kbf) {
     __shared__ float v[256];
     int b = blockIdx.x, h = blockIdx.y, lane = threadIdx.x, p = pos[b];
+    const bool bf = kbf && kbf[b]; // (row b's sequence has a bf16 cache)
     float *row = qkv + (size_t)b * ldqkv;
     int half = hd / 2;
     if (h >= nh + nkv) { // value head: store
@@ -134,7 +136,7 @@ __global__ __launch_bounds__(64) void k_qknorm_rope_store(float *__restrict__ qk
         const float *src = row + (size_t)(nh + nkv) * hd + g * hd;
         uint16_t *dst = vc[b] + (((size_t)(p / ATT_P) * nkv + g) * ATT_P + (size_t)(p % ATT_P / ATT_T) * ATT_T) * hd +
                         (size_t)(p % ATT_T) * hd;
-        for (int i = lane; i < hd; i += 64) dst[i] = f2h_ref(src[i]);
+        for (int i = lane; i < hd; i += 64) dst[kv_v_col(bf, i)] = bf ? f2bf_ref(src[i]) : f2h_ref(src[i]);
         return;
     }
     float *src = row + (size_t)h * hd;
@@ -153,10 +155,9 @@ __global__ __launch_bounds__(64) void k_qknorm_rope_store(float *__restrict__ qk
             src[i + half] = yo;
         } else {
             int g = h - nh;
-            uint16_t *dst = kc[b] + (((size_t)(p / ATT_P) * nkv + g) * ATT_P + (size_t)(p % ATT_P / ATT_T) * ATT_T) * hd +
-                            (p % ATT_T);
-            dst[(size_t)i * ATT_T] = f2h_ref(xo);
-            dst[(size_t)(i + half) * ATT_T] = f2h_ref(yo);
+            uint16_t *dst = kc[b] + (((size_t)(p / ATT_P) * nkv + g) * ATT_P + (size_t)(p % ATT_P / ATT_T) * ATT_T) * hd;
+            dst[kv_k_at(bf, i, p % ATT_T)] = bf ? f2bf_ref(xo) : f2h_ref(xo);
+            dst[kv_k_at(bf, i + half, p % ATT_T)] = bf ? f2bf_ref(yo) : f2h_ref(yo);
         }
     }
 }
@@ -182,7 +183,7 @@ __global__ __launch_bounds__(64) void k_qknorm_rope_store(float *__restrict__ qk
 #define ATT_KTILE (4 * ATT_KROW)        // LDS bytes of a K tile (hd <= 128)
 #define ATT_QC 36                       // LDS floats per 32-dim chunk of a query vector (32 + 4 padding)
 #define ATT_QS (4 * ATT_QC)             // LDS floats per query vector
-template <int NQ>
+template <int NQ, bool KB>
 __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, const float *__restrict__ qkv, int ldqkv, int nh,
                                                int nkv, int hd, float scale, const int *__restrict__ pos,
                                                uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc,
@@ -240,8 +241,14 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
         if (p < nmx && c < nchk) {
             for (int i = 0; i < 32; i += 4) {
                 float k[4];
-                #pragma unroll
-                for (int u = 0; u < 4; u++) k[u] = h2f(*(const uint16_t *)(kt + (i + u) * 32));
+                if (KB) { // (dims i, i + 1 of position p in one word at i 32 + 4 p of the chunk row; i + 2, i + 3 below)
+                    const uint8_t *kw = kt + (p % ATT_T) * 2;
+                    const uint32_t d0 = *(const uint32_t *)(kw + i * 32), d1 = *(const uint32_t *)(kw + (i + 2) * 32);
+                    k[0] = bf2f(d0 & 0xffffu), k[1] = bf2f(d0 >> 16), k[2] = bf2f(d1 & 0xffffu), k[3] = bf2f(d1 >> 16);
+                } else {
+                    #pragma unroll
+                    for (int u = 0; u < 4; u++) k[u] = h2f(*(const uint16_t *)(kt + (i + u) * 32));
+                }
                 float4 q4[NQ];
                 #pragma unroll
                 for (int v = 0; v < NQ; v++) q4[v] = *(const float4 *)(qc + v * ATT_QS + i);
@@ -328,8 +335,8 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
             auto fold = [&](const uint32_t (&vv)[PB], const float (&ee)[PB]) {
                 #pragma unroll
                 for (int u = 0; u < PB; u++) {
-                    o0 = __builtin_fmaf(ee[u], h2f((uint16_t)(vv[u] & 0xffff)), o0);
-                    o1 = __builtin_fmaf(ee[u], h2f((uint16_t)(vv[u] >> 16)), o1);
+                    o0 = __builtin_fmaf(ee[u], KB ? bf2f(vv[u] & 0xffffu) : h2f((uint16_t)(vv[u] & 0xffff)), o0);
+                    o1 = __builtin_fmaf(ee[u], KB ? bf2f(vv[u] >> 16) : h2f((uint16_t)(vv[u] >> 16)), o1);
                 }
             };
             if (n >= PB) {
@@ -352,23 +359,25 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
             for (; p < n; p++) {
                 uint32_t vv = vb[(size_t)p * rs];
                 float e = S[v][p];
-                o0 = __builtin_fmaf(e, h2f((uint16_t)(vv & 0xffff)), o0);
-                o1 = __builtin_fmaf(e, h2f((uint16_t)(vv >> 16)), o1);
+                o0 = __builtin_fmaf(e, KB ? bf2f(vv & 0xffffu) : h2f((uint16_t)(vv & 0xffff)), o0);
+                o1 = __builtin_fmaf(e, KB ? bf2f(vv >> 16) : h2f((uint16_t)(vv >> 16)), o1);
             }
             int row = r0 + v / kv_mul, h = g * kv_mul + v % kv_mul;
             float *o = part + ((size_t)row * nh + h) * pstride + (size_t)kb * (hd + 2);
-            o[i0] = o0;
-            o[i0 + 1] = o1;
+            // (a V word holds dims i0, i0 + 1; in a bf16 row, dims 32 c + l and 32 c + 16 + l, d2 = 16 c + l)
+            const int da = KB ? 32 * (d2 >> 4) + (d2 & 15) : i0, db = KB ? da + 16 : i0 + 1;
+            o[da] = o0;
+            o[db] = o1;
         }
     }
 }
 
-template <int NQ>
+template <int NQ, bool KB>
 __global__ __launch_bounds__(ATT_TH, NQ <= 4 ? 8 : 4) void k_attn_part(const int4 *__restrict__ items, const float *__restrict__ qkv, int ldqkv,
                                                       int nh, int nkv, int hd, float scale, const int *__restrict__ pos,
                                                       uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc,
                                                       float *__restrict__ part, int pstride) {
-    attn_part_body<NQ>(items, qkv, ldqkv, nh, nkv, hd, scale, pos, kc, vc, part, pstride);
+    attn_part_body<NQ, KB>(items, qkv, ldqkv, nh, nkv, hd, scale, pos, kc, vc, part, pstride);
 }
 
 // The attention of the one-row (decode) pass, one block of 1024 threads per (query vector v, kv head g, key block kb),
@@ -389,7 +398,7 @@ __global__ __launch_bounds__(ATT_TH, NQ <= 4 ? 8 : 4) void k_attn_part(const int
 #define ATD_T 1024
 #define ATD_KR 1056                 // LDS bytes of a K chunk row: 32 dims x 16 positions x 2 + 32 padding
 #define ATD_KT (4 * ATD_KR + 32)    // LDS bytes of a K tile: the 4 tiles of a wave's 64 positions in distinct banks
-template <int HD>
+template <int HD, bool KB>
 __global__ __launch_bounds__(ATD_T) void k_attn_decode(const float *__restrict__ qkv, int nh, int nkv, float scale,
                                                        const float *__restrict__ qn, const float *__restrict__ kn,
                                                        const float *__restrict__ rope, int pos, uint16_t *__restrict__ kl,
@@ -457,21 +466,22 @@ __global__ __launch_bounds__(ATD_T) void k_attn_decode(const float *__restrict__
             float rk = red[1];
             float xk = (kn[i] * kx[i]) * rk, yk = (kn[i + half] * kx[i + half]) * rk;
             float ysk = yk * s, yck = yk * c;
-            uint16_t kh0 = f2h_ref(__builtin_fmaf(xk, c, -ysk)), kh1 = f2h_ref(__builtin_fmaf(xk, s, yck));
+            const float k0v = __builtin_fmaf(xk, c, -ysk), k1v = __builtin_fmaf(xk, s, yck);
+            uint16_t kh0 = KB ? f2bf_ref(k0v) : f2h_ref(k0v), kh1 = KB ? f2bf_ref(k1v) : f2h_ref(k1v);
             int tile = pp / ATT_T, col = pp % ATT_T;
-            *(uint16_t *)(ks + tile * ATD_KT + (i >> 5) * ATD_KR + ((i & 31) * 16 + col) * 2) = kh0;
-            *(uint16_t *)(ks + tile * ATD_KT + ((i + half) >> 5) * ATD_KR + (((i + half) & 31) * 16 + col) * 2) = kh1;
+            *(uint16_t *)(ks + tile * ATD_KT + (i >> 5) * ATD_KR + kv_k_at(KB, i & 31, col) * 2) = kh0;
+            *(uint16_t *)(ks + tile * ATD_KT + ((i + half) >> 5) * ATD_KR + kv_k_at(KB, (i + half) & 31, col) * 2) = kh1;
             if (v == 0) {
-                uint16_t *kd = kl + (((size_t)kb * nkv + g) * ATT_P + (size_t)tile * ATT_T) * HD + col;
-                kd[(size_t)i * ATT_T] = kh0;
-                kd[(size_t)(i + half) * ATT_T] = kh1;
+                uint16_t *kd = kl + (((size_t)kb * nkv + g) * ATT_P + (size_t)tile * ATT_T) * HD;
+                kd[kv_k_at(KB, i, col)] = kh0;
+                kd[kv_k_at(KB, i + half, col)] = kh1;
             }
         }
     }
     if (last && t < HD) { // the row's value
-        uint16_t vh = f2h_ref(vr);
-        *(uint16_t *)(vs + ((size_t)pp * HD + t) * 2) = vh;
-        if (v == 0) vl[(((size_t)kb * nkv + g) * ATT_P + pp) * HD + t] = vh;
+        uint16_t vh = KB ? f2bf_ref(vr) : f2h_ref(vr);
+        *(uint16_t *)(vs + ((size_t)pp * HD + kv_v_col(KB, t)) * 2) = vh;
+        if (v == 0) vl[(((size_t)kb * nkv + g) * ATT_P + pp) * HD + kv_v_col(KB, t)] = vh;
     }
     __syncthreads();
     // 5. scores: thread (p, c)
@@ -481,8 +491,17 @@ __global__ __launch_bounds__(ATD_T) void k_attn_decode(const float *__restrict__
         const uint8_t *kt = ks + (p / ATT_T) * ATD_KT + c * ATD_KR + (p % ATT_T) * 2;
         const float *qc = qs + 32 * c;
         float kf[32];
-        #pragma unroll
-        for (int i = 0; i < 32; i++) kf[i] = h2f(*(const uint16_t *)(kt + i * 32));
+        if (KB) { // (dims 2 q, 2 q + 1 of position p: one word at 2 q 32 + 4 p of the chunk row)
+            #pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const uint32_t w = *(const uint32_t *)(kt + (p % ATT_T) * 2 + q * 64);
+                kf[2 * q] = bf2f(w & 0xffffu);
+                kf[2 * q + 1] = bf2f(w >> 16);
+            }
+        } else {
+            #pragma unroll
+            for (int i = 0; i < 32; i++) kf[i] = h2f(*(const uint16_t *)(kt + i * 32));
+        }
         #pragma unroll
         for (int i = 0; i < 32; i += 4) {
             float4 q4 = *(const float4 *)(qc + i);
@@ -531,7 +550,7 @@ __global__ __launch_bounds__(ATD_T) void k_attn_decode(const float *__restrict__
             ml[1] = s;
         }
     } else if (t < HD) {
-        const uint16_t *vcol = (const uint16_t *)vs + t;
+        const uint16_t *vcol = (const uint16_t *)vs + kv_v_col(KB, t);
         float o = 0.0f;
         int q = 0;
         uint16_t va[16], vb[16];
@@ -545,7 +564,7 @@ __global__ __launch_bounds__(ATD_T) void k_attn_decode(const float *__restrict__
         };
         auto fold = [&](const uint16_t (&vv)[16], const float (&ee)[16]) {
             #pragma unroll
-            for (int u = 0; u < 16; u++) o = __builtin_fmaf(ee[u], h2f(vv[u]), o);
+            for (int u = 0; u < 16; u++) o = __builtin_fmaf(ee[u], KB ? bf2f(vv[u]) : h2f(vv[u]), o);
         };
         if (n >= 16) {
             ld(va, ea, 0);
@@ -564,7 +583,7 @@ __global__ __launch_bounds__(ATD_T) void k_attn_decode(const float *__restrict__
                 fold(va, ea);
             }
         }
-        for (; q < n; q++) o = __builtin_fmaf(S[q], h2f(vcol[(size_t)q * HD]), o);
+        for (; q < n; q++) o = __builtin_fmaf(S[q], KB ? bf2f(vcol[(size_t)q * HD]) : h2f(vcol[(size_t)q * HD]), o);
         part[(size_t)h * pstride + (size_t)kb * (HD + 2) + t] = o;
     }
 }
@@ -741,16 +760,21 @@ int gw_k_set_exact(const float *rsq, int bits, const float *rcp, const uint8_t *
 }
 
 int gw_k_qknorm_rope_store(float *qkv, int ldqkv, int n, int nh, int nkv, int hd, const float *qn, const float *kn,
-                           const float *rope, const int *pos, uint16_t *const *kc, uint16_t *const *vc, hipStream_t s) {
-    GW_LAUNCH(k_qknorm_rope_store, dim3(n, nh + 2 * nkv), dim3(64), 0, s, qkv, ldqkv, nh, nkv, hd, qn, kn, rope, pos, kc, vc);
+                           const float *rope, const int *pos, uint16_t *const *kc, uint16_t *const *vc, const int *kbf,
+                           hipStream_t s) {
+    GW_LAUNCH(k_qknorm_rope_store, dim3(n, nh + 2 * nkv), dim3(64), 0, s, qkv, ldqkv, nh, nkv, hd, qn, kn, rope, pos, kc, vc, kbf);
     return (int)hipGetLastError();
 }
 
 int gw_k_attn_part(const void *items, int nitems, int nq_max, const float *qkv, int ldqkv, int nh, int nkv, int hd, float scale,
-                   const int *pos, uint16_t *const *kc, uint16_t *const *vc, float *part, int pstride, hipStream_t s) {
+                   const int *pos, uint16_t *const *kc, uint16_t *const *vc, float *part, int pstride, int kbf, hipStream_t s) {
     int nq = nq_max;
     const int4 *it = (const int4 *)items;
-#define ATT_LAUNCH(Q) GW_LAUNCH(k_attn_part<Q>, dim3(nitems), dim3(ATT_TH), 0, s, it, qkv, ldqkv, nh, nkv, hd, scale, pos, kc, vc, part, pstride)
+#define ATT_LAUNCH(Q)                                                                                                   \
+    do {                                                                                                                \
+        if (kbf) GW_LAUNCH((k_attn_part<Q, true>), dim3(nitems), dim3(ATT_TH), 0, s, it, qkv, ldqkv, nh, nkv, hd, scale, pos, kc, vc, part, pstride); \
+        else GW_LAUNCH((k_attn_part<Q, false>), dim3(nitems), dim3(ATT_TH), 0, s, it, qkv, ldqkv, nh, nkv, hd, scale, pos, kc, vc, part, pstride); \
+    } while (0)
     if (nq <= 1) ATT_LAUNCH(1);
     else if (nq <= 2) ATT_LAUNCH(2);
     else if (nq <= 4) ATT_LAUNCH(4);
@@ -761,13 +785,15 @@ int gw_k_attn_part(const void *items, int nitems, int nq_max, const float *qkv, 
 }
 
 int gw_k_attn_decode(const float *qkv, int nh, int nkv, int hd, float scale, const float *qn, const float *kn, const float *rope,
-                     int pos, uint16_t *kl, uint16_t *vl, float *part, int pstride, hipStream_t s) {
+                     int pos, uint16_t *kl, uint16_t *vl, float *part, int pstride, int kbf, hipStream_t s) {
     int kvm = nh / nkv, nitems = nkv * (pos / ATT_P + 1);
     dim3 grid(8 * kvm * ((nitems + 7) / 8));
-    if (hd == 128) GW_LAUNCH(k_attn_decode<128>, grid, dim3(ATD_T), 0, s, qkv, nh, nkv, scale, qn, kn, rope, pos, kl, vl, part, pstride);
-    else if (hd == 64) GW_LAUNCH(k_attn_decode<64>, grid, dim3(ATD_T), 0, s, qkv, nh, nkv, scale, qn, kn, rope, pos, kl, vl, part, pstride);
-    else if (hd == 32) GW_LAUNCH(k_attn_decode<32>, grid, dim3(ATD_T), 0, s, qkv, nh, nkv, scale, qn, kn, rope, pos, kl, vl, part, pstride);
+#define ATD_L(H, B) GW_LAUNCH((k_attn_decode<H, B>), grid, dim3(ATD_T), 0, s, qkv, nh, nkv, scale, qn, kn, rope, pos, kl, vl, part, pstride)
+    if (hd == 128) { if (kbf) ATD_L(128, true); else ATD_L(128, false); }
+    else if (hd == 64) { if (kbf) ATD_L(64, true); else ATD_L(64, false); }
+    else if (hd == 32) { if (kbf) ATD_L(32, true); else ATD_L(32, false); }
     else return (int)hipErrorInvalidValue;
+#undef ATD_L
     return (int)hipGetLastError();
 }
 

@@ -3,7 +3,7 @@
  * 4 KiB, then per layer its K blocks and its V blocks (the first nblk blocks of 256 positions, as the cache holds them:
  * the tiled layout of forward.c:1894-1899, which the device cache keeps byte for byte), each section at a multiple of
  * 4 KiB. The blocks go through a host staging buffer (device to host on save, host to device on load), one (layer, K /
- * V) section at a time. Qwen3 only: no recurrent state, no checkpoints; f16 KV. Plain buffered I/O, written as
+ * V) section at a time. Qwen3 only: no recurrent state, no checkpoints; f16 or bf16 KV. Plain buffered I/O, written as
  * path.tmp, synced and renamed (a reader never sees a partial file). */
 #include <fcntl.h>
 #include <stdio.h>
@@ -48,8 +48,8 @@ static uint64_t sf_hash(const SfHdr *h, const int *tokens) {
 
 static uint64_t sf_blk(const RqModel *m) { return (uint64_t)GW_ATT_P * m->n_kv_heads * m->head_dim * 2; } /* f16, K or V */
 
-static void sf_shape(const RqModel *m, int len, SfHdr *h) {
-    /* every field but rng and hash, as the reference writes them for this model and length */
+static void sf_shape(const RqModel *m, int len, int kvt, SfHdr *h) {
+    /* every field but rng and hash, as the reference writes them for this model, length and cache type (f16 / bf16) */
     memset(h, 0, sizeof(*h));
     memcpy(h->magic, sf_magic, 8);
     h->version = SF_VERSION;
@@ -61,7 +61,7 @@ static void sf_shape(const RqModel *m, int len, SfHdr *h) {
     h->head_dim = m->head_dim;
     h->att_p = GW_ATT_P;
     h->att_t = GW_ATT_T;
-    h->att = RQ_KV_F16;
+    h->att = kvt;
     h->kv_esz = 2;
     h->len = len;
     h->nblk = (len + GW_ATT_P - 1) / GW_ATT_P;
@@ -111,7 +111,7 @@ int rq_seq_save(const RqSeq *s, const char *path) {
     /* seqfile.c:236-297 (runq.h:283-293) */
     if (!s || !path || s->len < 1) return RQ_ERR_ARG;
     SfHdr h;
-    sf_shape(s->m, s->len, &h);
+    sf_shape(s->m, s->len, s->kvt, &h);
     h.rng = s->rng;
     h.hash = sf_hash(&h, s->tokens);
     size_t pl = strlen(path), hn = (size_t)h.off_kv;
@@ -146,7 +146,7 @@ done:
 long long rq_seq_save_bytes(const RqSeq *s) {
     if (!s || s->len < 1) return 0;
     SfHdr h;
-    sf_shape(s->m, s->len, &h);
+    sf_shape(s->m, s->len, s->kvt, &h);
     return (long long)h.file_bytes;
 }
 
@@ -162,7 +162,7 @@ static int sf_open_check(const RqModel *m, const char *path, int *fd, SfHdr *h, 
     int lmax = m->seq_len;
     if (h->len < 1 || h->len > lmax) goto fail;
     SfHdr w;
-    sf_shape(m, h->len, &w);
+    sf_shape(m, h->len, h->att == RQ_KV_BF16 ? RQ_KV_BF16 : RQ_KV_F16, &w);
     w.rng = h->rng;
     w.hash = h->hash;
     if (memcmp(&w, h, sizeof(w)) || (uint64_t)st.st_size != h->file_bytes) goto fail;
@@ -213,6 +213,8 @@ int rq_seq_load(RqSeq *dst, const char *path, int n) {
     if (rc != RQ_OK) return rc;
     if (n > h.len) {
         rc = RQ_ERR_ARG;
+    } else if (h.att != dst->kvt) { /* (the cache's type is the sequence's: runq.h:309-314) */
+        rc = RQ_ERR_MISMATCH;
     } else {
         dst->len = 0;
         rc = sf_blocks(dst, fd, 0, &h, (n + GW_ATT_P - 1) / GW_ATT_P);

@@ -258,3 +258,54 @@ def test_config5_mixed_pass_equals_each_sequence_alone(gw, tmp_path):
         for r, (a, b) in enumerate(zip(lg, alone)):
             assert _bits_equal(a, b), f"round {rnd} row {r}: max diff {np.abs(a - b).max()}"
         toks = [int(np.argmax(lg[i])) for i in range(len(dec))]
+
+
+@pytest.mark.parametrize("shape,n_prompt", [("tiny", 300), ("tiny_gqa4", 40), ("tiny_hd64", 600)])
+def test_bf16_kv_bitexact_vs_oracle(gw, synth_models, shape, n_prompt):
+    """a bf16 KV cache (RQ_KV_BF16: the reference's bf16 tile layouts, round to nearest even, the same fp32 attention on
+    the exactly converted values): the prefill's rows and decode steps bit for bit against the oracle's bf16 cache,
+    across key blocks; the cache bytes themselves equal the oracle's"""
+    from oracle import oracle as orc
+    path = synth_models(shape)
+    m = gw.Model(path, ctx_len=1024)
+    om = orc.Model(path, cap=1024)
+    ids = _ids(m.vocab, n_prompt, 12)
+    c = m.ctx(max_batch=128)
+    s = m.seq(1024, kv_type=gw.RQ_KV_BF16)
+    lg_all = c.prefill(s, ids, mode=gw.RQ_LOGITS_ALL)
+    os_ = om.seq(bf16=True)
+    for i, t in enumerate(ids):
+        ref = os_.forward(int(t))
+        assert _bits_equal(lg_all[i], ref), f"row {i}: max diff {np.abs(lg_all[i] - ref).max()}"
+    tok = int(np.argmax(lg_all[-1]))
+    for step in range(5):
+        lg = c.decode(s, tok)
+        ref = os_.forward(tok)
+        assert _bits_equal(lg, ref), f"decode step {step}: max diff {np.abs(lg - ref).max()}"
+        tok = int(np.argmax(ref))
+
+
+def test_bf16_and_f16_sequences_in_one_pass(gw, synth_models):
+    """one rq_forward_batch over f16 and bf16 sequences (the attention items of each cache type in a launch of their
+    own) gives every row the bits it gets alone; copies keep the type (rq_seq_copy refuses mixing)"""
+    path = synth_models("tiny_gqa4")
+    m = gw.Model(path, ctx_len=1024)
+    c = m.ctx(max_batch=128)
+    rng = np.random.default_rng(21)
+    kinds = [gw.RQ_KV_F16, gw.RQ_KV_BF16, gw.RQ_KV_BF16, gw.RQ_KV_F16]
+    seqs = [m.seq(1024, kv_type=k) for k in kinds]
+    for sq, n in zip(seqs, (30, 270, 5, 300)):
+        c.prefill(sq, _ids(m.vocab, n, n))
+    twins = [m.seq(1024, kv_type=k) for k in kinds]
+    for tw, sq in zip(twins, seqs):
+        tw.copy_from(sq, len(sq))
+    with pytest.raises(gw.RqError):
+        twins[0].copy_from(seqs[1], 5)
+    chunks = [[int(t) for t in rng.integers(0, m.vocab, k)] for k in (1, 7, 1, 20)]
+    lg, _ = c.forward_batch([gw.Segment(sq, ch, gw.RQ_LOGITS_ALL) for sq, ch in zip(seqs, chunks)])
+    alone = []
+    for tw, ch in zip(twins, chunks):
+        alone += list(c.prefill(tw, ch, mode=gw.RQ_LOGITS_ALL))
+    assert lg.shape[0] == len(alone)
+    for r, (a, b) in enumerate(zip(lg, alone)):
+        assert _bits_equal(a, b), f"row {r}"

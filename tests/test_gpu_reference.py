@@ -260,3 +260,24 @@ def test_q5k_q3k_models_greedy_bit_identical(gw, orc, tmp_path, shape):
         if step < 24:
             assert tok == int(rtok[step]), f"step {step}"
             lg = c.decode(s, tok)
+
+
+def test_bf16_kv_greedy_bit_identical(gw, orc, tmp_path):
+    """a bf16 KV cache (RQ_KV_BF16) on a Qwen3-0.6B-shaped model (2 layers): a 300-token prefill (two key blocks) and
+    24 greedy steps, every logits row equal bit for bit to the reference's own bf16 cache, the same tokens"""
+    path, d = _synth(str(tmp_path), "qwen3_0_6b", seed=4, n_layers=2)
+    m = gw.Model(path, ctx_len=512)
+    if not _exact(gw):
+        pytest.skip("this host does not provide the reference's float operations (AVX-512)")
+    ids = np.random.default_rng(9).integers(0, m.vocab, 300).astype(np.int32)
+    _, rlg, rtok, _ = orc.run_ref_driver(path, ids, str(tmp_path / "ref"), steps=24, threads=_threads(), cap=512,
+                                         kv_type=gw.RQ_KV_BF16)
+    c = m.ctx(max_batch=512, max_ctx=512)
+    s = m.seq(512, kv_type=gw.RQ_KV_BF16)
+    lg = c.prefill(s, ids, mode=gw.RQ_LOGITS_LAST)
+    for step in range(25):
+        assert np.array_equal(_bits(lg), _bits(rlg[step])), f"row {step}: max diff {np.abs(lg - rlg[step]).max()}"
+        tok = int(np.argmax(lg))
+        if step < 24:
+            assert tok == int(rtok[step]), f"step {step}"
+            lg = c.decode(s, tok)
