@@ -176,18 +176,21 @@ def test_hidden_rows_bit_identical(gw, orc, tmp_path, shape, layers):
         assert np.array_equal(_bits(lg), _bits(rlg)), f"fw_rows (max_batch {nb}): logits rows"
 
 
-def test_seqfile_with_reference(gw, orc, tmp_path):
+@pytest.mark.parametrize("kvt", [2, 1])  # RQ_KV_F16, RQ_KV_BF16
+def test_seqfile_with_reference(gw, orc, tmp_path, kvt):
     """the KV disk tier (runq.h:283-314) against the reference's seqfile.c: the same model fingerprint; the reference's
     saved sequence (300-token prompt + 4 greedy steps) read by rq_seq_file_info and loaded by rq_seq_load continues bit
     for bit as the device's own sequence of the same tokens; the device's saved file matches the reference's header
-    and tokens (all but the RNG word and the hash over it) and its whole K / V blocks byte for byte, and loads back"""
+    and tokens (all but the RNG word and the hash over it) and its whole K / V blocks byte for byte, and loads back;
+    with an f16 and a bf16 cache (a file loads only into a sequence of its cache type)"""
     import ctypes
     path, d = _synth(str(tmp_path), "qwen3_0_6b", n_layers=2)
     m = gw.Model(path, ctx_len=1024)
     if not _exact(gw):
         pytest.skip("this host does not provide the reference's float operations (AVX-512)")
     ids = np.random.default_rng(11).integers(0, m.vocab, 300).astype(np.int32)
-    info, rlg, rtok, kvp = orc.run_ref_driver(path, ids, str(tmp_path / "ref"), steps=4, threads=_threads(), cap=1024, kv=True)
+    info, rlg, rtok, kvp = orc.run_ref_driver(path, ids, str(tmp_path / "ref"), steps=4, threads=_threads(), cap=1024, kv=True,
+                                              kv_type=kvt)
     assert int(info["fingerprint"], 16) == m.info.fingerprint
     lib = gw.lib
 
@@ -197,20 +200,20 @@ def test_seqfile_with_reference(gw, orc, tmp_path):
     fi, tk = SeqFile(), ctypes.POINTER(ctypes.c_int)()
     assert lib.rq_seq_file_info(ctypes.c_void_p(m._h), kvp.encode(), ctypes.byref(fi), ctypes.byref(tk)) == 0
     L = fi.len
-    assert L == 304 and fi.kv_type == 2 and fi.bytes == os.path.getsize(kvp)
+    assert L == 304 and fi.kv_type == kvt and fi.bytes == os.path.getsize(kvp)
     saved = np.ctypeslib.as_array(tk, shape=(L,)).copy()
     assert np.array_equal(saved[:300], ids) and np.array_equal(saved[300:], rtok[:4])
     # the device's own sequence of the same tokens, and the reference's file loaded, each continued by one token
     c = m.ctx(max_batch=512, max_ctx=1024)
-    own = m.seq(1024)
+    own = m.seq(1024, kv_type=kvt)
     c.prefill(own, saved, mode=gw.RQ_LOGITS_NONE)
-    loaded = m.seq(1024)
+    loaded = m.seq(1024, kv_type=kvt)
     assert lib.rq_seq_load(ctypes.c_void_p(loaded._h), kvp.encode(), L) == 0
     assert lib.rq_seq_len(ctypes.c_void_p(loaded._h)) == L
     a, b = c.decode(own, 7), c.decode(loaded, 7)
     assert np.array_equal(_bits(a), _bits(b))
     # the device's file of the same sequence (before the extra token: a fresh copy of it)
-    mine = m.seq(1024)
+    mine = m.seq(1024, kv_type=kvt)
     assert lib.rq_seq_load(ctypes.c_void_p(mine._h), kvp.encode(), L) == 0
     p2 = str(tmp_path / "mine.seq")
     assert lib.rq_seq_save(ctypes.c_void_p(mine._h), p2.encode()) == 0
@@ -226,19 +229,21 @@ def test_seqfile_with_reference(gw, orc, tmp_path):
     for sec in range(2 * 2):  # (layer, K / V): the first block is whole (positions 0..255 < L)
         s0 = off_kv + sec * nblk * blk
         assert np.array_equal(r[s0:s0 + blk], o[s0:s0 + blk]), f"section {sec}"
-    again = m.seq(1024)
+    again = m.seq(1024, kv_type=kvt)
     assert lib.rq_seq_load(ctypes.c_void_p(again._h), p2.encode(), 200) == 0
     assert lib.rq_seq_len(ctypes.c_void_p(again._h)) == 200
-    c2 = m.seq(1024)
+    c2 = m.seq(1024, kv_type=kvt)
     c.prefill(c2, saved[:200], mode=gw.RQ_LOGITS_NONE)
     assert np.array_equal(_bits(c.decode(again, 9)), _bits(c.decode(c2, 9)))
     # errors: another length past the file, a corrupt header
-    assert lib.rq_seq_load(ctypes.c_void_p(m.seq(1024)._h), p2.encode(), L + 1) == -1  # RQ_ERR_ARG
+    assert lib.rq_seq_load(ctypes.c_void_p(m.seq(1024, kv_type=kvt)._h), p2.encode(), L + 1) == -1  # RQ_ERR_ARG
     bad = o.copy()
     bad[100] ^= 1
     p3 = str(tmp_path / "bad.seq")
     bad.tofile(p3)
-    assert lib.rq_seq_load(ctypes.c_void_p(m.seq(1024)._h), p3.encode(), 10) == -7  # RQ_ERR_MISMATCH
+    assert lib.rq_seq_load(ctypes.c_void_p(m.seq(1024, kv_type=kvt)._h), p3.encode(), 10) == -7  # RQ_ERR_MISMATCH
+    other = gw.RQ_KV_BF16 if kvt == gw.RQ_KV_F16 else gw.RQ_KV_F16
+    assert lib.rq_seq_load(ctypes.c_void_p(m.seq(1024, kv_type=other)._h), p2.encode(), 10) == -7
 
 
 @pytest.mark.parametrize("shape", ["tiny_q5k", "tiny_q3k"])
