@@ -133,6 +133,8 @@ _sig = {
     "gw_kq_matmul": (_I, [_P, _I, _P, _I, _I, _P, _P, _I, _P]),
     "gw_matmul_tile_rows": (_I, [_I]),
     "gw_gemv_warm_next": (_I, [_I]),
+    "gw_ctx_topk": (_I, [_P, _I, _I, _F, ctypes.POINTER(_I)]),
+    "gw_sample_topk": (_I, [_F, ctypes.POINTER(_I), _I, ctypes.c_float, ctypes.c_float, ctypes.POINTER(ctypes.c_ulonglong)]),
 }
 for _name, (_res, _args) in _sig.items():
     _fn = getattr(lib, _name)
@@ -376,6 +378,12 @@ class Ctx:
         t, b, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int()
         self._check(lib.gw_ctx_gemv_sweep(self._h, reps, ctypes.byref(t), ctypes.byref(b), ctypes.byref(n)), "gw_ctx_gemv_sweep")
         return t.value, b.value, n.value
+
+    def topk(self, n: int, k: int):
+        """gw_ctx_topk: the k best logits of the first n rows on the device and their ids, (n x k) each"""
+        vals, idx = np.zeros((n, k), np.float32), np.zeros((n, k), np.int32)
+        self._check(lib.gw_ctx_topk(self._h, n, k, _fptr(vals), _iptr(idx)), "gw_ctx_topk")
+        return vals, idx
 
     def argmax(self, n: int = 1) -> np.ndarray:
         """gw_ctx_argmax: device-side greedy tokens of the last pass's first n logits rows."""

@@ -19,6 +19,7 @@
 #define _GNU_SOURCE
 #include <stdarg.h>
 #include <stdio.h>
+#include <math.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -169,7 +170,7 @@ static void dfree(void *p) { if (p) hipFree(p); }
 void rq_ctx_free(RqCtx *c) {
     if (!c) return;
     void *d[] = { c->x, c->xb, c->qkv, c->hb, c->part, c->logits_d, c->hid_d, c->xq, c->hq, c->xs, c->hs, c->argmax_d, c->argmax_scr, c->meta_d,
-                  c->gtok_d, c->gpos_d };
+                  c->gtok_d, c->gpos_d, c->topk_scr, c->topk_v, c->topk_i };
     for (size_t i = 0; i < sizeof d / sizeof d[0]; i++) dfree(d[i]);
     if (c->meta_h) hipHostFree(c->meta_h);
     if (c->logits) hipHostFree(c->logits);
@@ -1016,6 +1017,62 @@ int gw_ctx_gemv_sweep(RqCtx *c, int reps, double *seconds, double *bytes, int *l
     if (bytes) *bytes = b;
     if (launches) *launches = nl;
     return RQ_OK;
+}
+
+int gw_ctx_topk(RqCtx *c, int n, int k, float *vals, int *idx) {
+    /* the k best logits of each of the first n rows on the device (sampler.c:186-217's candidates c_0 .. c_{k-1}:
+     * larger first, the lower index first on ties): vals / idx, n x k each (host) */
+    int rows = c->last_nsel;
+    if (rows <= 0 || n < 1 || n > rows) return ctx_fail(c, RQ_ERR_STATE, "no logits rows on the device (%d)", rows);
+    if (k < 1 || k > 64 || k >= c->m->vocab || !vals || !idx) return ctx_fail(c, RQ_ERR_ARG, "top-k %d", k);
+    if (!c->topk_scr) {
+        size_t sb = (size_t)c->nb_max * 64 * 64 * 8, ob = (size_t)c->nb_max * 64 * 4;
+        if (hipMalloc(&c->topk_scr, sb) != hipSuccess || hipMalloc((void **)&c->topk_v, ob) != hipSuccess ||
+            hipMalloc((void **)&c->topk_i, ob) != hipSuccess)
+            return ctx_fail(c, RQ_ERR_NOMEM, "top-k scratch");
+    }
+    if (gw_k_topk(c->logits_d, c->m->vocab, c->m->vocab, n, k, c->topk_v, c->topk_i, c->topk_scr, c->stream))
+        return ctx_fail(c, RQ_ERR_STATE, "top-k launch failed");
+    HIPCHK(c, "hipMemcpyAsync (top-k)", hipMemcpyAsync(vals, c->topk_v, (size_t)n * k * 4, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, "hipMemcpyAsync (top-k)", hipMemcpyAsync(idx, c->topk_i, (size_t)n * k * 4, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, "hipStreamSynchronize (top-k)", hipStreamSynchronize(c->stream));
+    return RQ_OK;
+}
+
+int gw_sample_topk(const float *vals, const int *idx, int k, float temperature, float topp, unsigned long long *rng) {
+    /* sample_topk (sampler.c:186-256) from its candidates (gw_ctx_topk's row): w_j = expf((x_j - x_0) * (1 / T)),
+     * S = w_0 + .. in order, the nucleus by prefix sums against topp * S, the draw r = coin * W with coin the next
+     * xorshift draw of *rng (sampler.c:258-269); the token. temperature > 0 */
+    if (!vals || !idx || !rng || k < 1 || k > 64 || !(temperature > 0)) return RQ_ERR_ARG;
+    *rng ^= *rng >> 12;
+    *rng ^= *rng << 25;
+    *rng ^= *rng >> 27;
+    const float coin = (float)((unsigned)((*rng * 0x2545F4914F6CDD1Dull) >> 32) >> 8) / 16777216.0f;
+    float w[64];
+    const float mx = vals[0], inv_t = 1.0f / temperature;
+    volatile float vs = 0;
+    for (int j = 0; j < k; j++) {
+        w[j] = expf((vals[j] - mx) * inv_t);
+        vs = vs + w[j];
+    }
+    float sum = vs, cum = 0, wsum = sum;
+    int m = k;
+    if (topp > 0 && topp < 1) {
+        const float t = topp * sum;
+        for (int j = 0; j < k; j++) {
+            cum += w[j];
+            if (cum > t) { m = j + 1; wsum = cum; break; }
+        }
+    }
+    const float r = coin * wsum;
+    float cdf = 0;
+    int last = 0;
+    for (int j = 0; j < m; j++) {
+        cdf += w[j];
+        if (r < cdf) return idx[j];
+        if (w[j] > 0) last = j;
+    }
+    return idx[last];
 }
 
 int gw_ctx_argmax(RqCtx *c, int *tokens, int n) {

@@ -95,6 +95,9 @@ struct RqCtx {
     float *xs, *hs;
     int *argmax_d;
     void *argmax_scr;
+    void *topk_scr; /* gw_ctx_topk's scratch (allocated at its first call): nb_max x 64 x 64 (value, index) pairs */
+    float *topk_v;  /* ... and its device outputs, nb_max x 64 each */
+    int *topk_i;
     int kmax, ldqkv, pstride;
     size_t part_bytes;
     /* per-pass row metadata: one device block, filled from one pinned host block */
@@ -168,6 +171,8 @@ int gw_k_attn_combine_quant(const float *part, int pstride, int nh, int hd, cons
 int gw_k_swiglu_quant(const float *hb, int H, int il, int n, int8_t *hq, float *hs, hipStream_t s);
 int gw_k_quant_rows(const float *x, int n, int ldxf, int rows, int8_t *q, float *sc, int ldq, hipStream_t s);
 int gw_k_argmax(const float *lg, int n, int ld, int rows, int *out, void *scratch, hipStream_t s); /* scratch: rows x 512 B */
+/* the k best of each row in sample_topk's order (larger first, lower index on ties); scratch rows x 32 KiB, k <= 64 */
+int gw_k_topk(const float *lg, int n, int ld, int rows, int k, float *vals, int *idx, void *scratch, hipStream_t s);
 /* GGUF Q8_0 blocks (gpr per row) -> codes + scales; il > 0: source row i to row (i / il) 2 il + off + i % il (two
  * matrices interleaved in blocks of il rows) */
 int gw_k_q8_unpack(const uint8_t *blocks, size_t nblk, int8_t *codes, uint16_t *scales, int gpr, int il, int off, hipStream_t s);

@@ -735,6 +735,86 @@ __global__ __launch_bounds__(64) void k_argmax_final(const float2 *__restrict__ 
     if (l == 0) out[row] = idx;
 }
 
+// Top-k candidates of each row, in sample_topk's order (sampler.c:186-217): the k largest values, the lower index
+// first on ties, larger first. Two steps, each a selection by repeated "best element after the previous one" (the
+// order is total, so nothing is marked: an element is eligible iff it comes after the last one taken), one block
+// reduction per pick: per chunk of TOPK_CH of a row its k best into scratch, then per row the k best of those.
+// Empty picks are (-inf, INT_MAX), after every real element. k <= TOPK_KMAX
+#define TOPK_CH 64
+#define TOPK_KMAX 64
+__device__ __forceinline__ bool tk_before(float a, int ia, float b, int ib) { return a > b || (a == b && ia < ib); }
+
+template <int L>
+__device__ void tk_select(const float (&v)[L], const int (&ix)[L], int k, float2 *out) {
+    // the block's k best of its threads' L values each (index -1: none) into out[0 .. k): (value, index as float bits)
+    __shared__ float rv[4];
+    __shared__ int ri[4];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    float pv = __builtin_inff();
+    int pi = -1; // (the previous pick: every element comes after (+inf, -1))
+    for (int it = 0; it < k; it++) {
+        float bv = -__builtin_inff();
+        int bi = 0x7fffffff;
+        #pragma unroll
+        for (int u = 0; u < L; u++)
+            if (ix[u] >= 0 && tk_before(pv, pi, v[u], ix[u]) && tk_before(v[u], ix[u], bv, bi)) bv = v[u], bi = ix[u];
+        for (int o = 32; o >= 1; o >>= 1) {
+            float ov = __shfl_xor(bv, o);
+            int oi = __shfl_xor(bi, o);
+            if (tk_before(ov, oi, bv, bi)) bv = ov, bi = oi;
+        }
+        if (lane == 0) rv[w] = bv, ri[w] = bi;
+        __syncthreads();
+        bv = rv[0], bi = ri[0];
+        for (int q = 1; q < (int)(blockDim.x >> 6); q++)
+            if (tk_before(rv[q], ri[q], bv, bi)) bv = rv[q], bi = ri[q];
+        __syncthreads();
+        if (t == 0) out[it] = make_float2(bv, __int_as_float(bi));
+        pv = bv, pi = bi;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_topk_part(const float *__restrict__ lg, int n, int ld, int k, float2 *__restrict__ scr) {
+    // block (row, chunk): the chunk's k best (chunks of ceil(n / TOPK_CH) <= 16 x 256 values)
+    const int row = blockIdx.x, ch = blockIdx.y, len = (n + TOPK_CH - 1) / TOPK_CH, i0 = ch * len;
+    const float *r = lg + (size_t)row * ld;
+    float v[16];
+    int ix[16];
+    #pragma unroll
+    for (int u = 0; u < 16; u++) {
+        const int i = i0 + (int)threadIdx.x + 256 * u;
+        const bool ok = i < i0 + len && i < n;
+        v[u] = ok ? r[i] : 0.0f;
+        ix[u] = ok ? i : -1;
+    }
+    tk_select<16>(v, ix, k, scr + ((size_t)row * TOPK_CH + ch) * TOPK_KMAX);
+}
+
+__global__ __launch_bounds__(256) void k_topk_final(const float2 *__restrict__ scr, int k, float *__restrict__ vals,
+                                                    int *__restrict__ idx) {
+    // block row: the k best of its TOPK_CH x k chunk candidates (sentinels never win), into vals / idx row
+    const int row = blockIdx.x;
+    const float2 *c = scr + (size_t)row * TOPK_CH * TOPK_KMAX;
+    float v[16];
+    int ix[16];
+    #pragma unroll
+    for (int u = 0; u < 16; u++) { // (candidate e = t + 256 u: chunk e / k, pick e % k)
+        const int e = (int)threadIdx.x + 256 * u, ch = e / k, j = e % k;
+        const bool ok = ch < TOPK_CH;
+        const float2 x = ok ? c[ch * TOPK_KMAX + j] : make_float2(0.0f, 0.0f);
+        const int i = __float_as_int(x.y);
+        v[u] = x.x;
+        ix[u] = ok && i != 0x7fffffff ? i : -1;
+    }
+    __shared__ float2 out[TOPK_KMAX];
+    tk_select<16>(v, ix, k, out);
+    __syncthreads();
+    if ((int)threadIdx.x < k) {
+        vals[(size_t)row * k + threadIdx.x] = out[threadIdx.x].x;
+        idx[(size_t)row * k + threadIdx.x] = __float_as_int(out[threadIdx.x].y);
+    }
+}
+
 // ------------------------------------------------------------------------------------------ launchers
 
 extern "C" {
@@ -813,6 +893,14 @@ int gw_k_swiglu_quant(const float *hb, int H, int il, int n, int8_t *hq, float *
 
 int gw_k_quant_rows(const float *x, int n, int ldxf, int rows, int8_t *q, float *sc, int ldq, hipStream_t s) {
     GW_LAUNCH(k_quant_rows, dim3(rows, (n + 255) / 256), dim3(256), 0, s, x, n, ldxf, q, sc, ldq);
+    return (int)hipGetLastError();
+}
+
+int gw_k_topk(const float *lg, int n, int ld, int rows, int k, float *vals, int *idx, void *scratch, hipStream_t s) {
+    /* scratch: rows x TOPK_CH x TOPK_KMAX float2; n <= TOPK_CH x 16 x 256, k <= TOPK_KMAX and < n */
+    if (k < 1 || k > TOPK_KMAX || k >= n || n > TOPK_CH * 16 * 256) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_topk_part, dim3(rows, TOPK_CH), dim3(256), 0, s, lg, n, ld, k, (float2 *)scratch);
+    hipLaunchKernelGGL(k_topk_final, dim3(rows), dim3(256), 0, s, (const float2 *)scratch, k, vals, idx);
     return (int)hipGetLastError();
 }
 

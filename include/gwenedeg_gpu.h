@@ -227,6 +227,17 @@ int fw_rows(RqCtx *c, RqSeq *s, const int *tokens, int n, int mode, float *out, 
  * RQ_ERR_STATE if the last pass produced no logits */
 int gw_ctx_argmax(RqCtx *c, int *tokens, int n);
 
+/* Top-k on the device (sampler.c:186-217): for the first n logits rows of the context's last pass (as gw_ctx_argmax),
+ * the k largest logits of each row and their token ids, larger first and the lower id first on ties (the reference's
+ * candidate order c_0 .. c_{k-1}), into vals / idx (host, n x k each); 1 <= k <= 64, k < vocab. 64 x 8 bytes per row
+ * cross the bus instead of the row's logits. No counterpart in runq.h: a sampler over the candidates replaces
+ * rq_sample_batch's top-k rows (engine.c:3230-3253) */
+int gw_ctx_topk(RqCtx *c, int n, int k, float *vals, int *idx);
+/* sample_topk (sampler.c:186-256) on such a row's candidates, with temperature > 0, top-p topp (<= 0 or >= 1: off) and
+ * the sequence's RNG state (rq_seq_rng, runq.h:319; advanced by one draw as rq_sample does): the same token as the
+ * reference's rq_sample with cfg->top_k = k on the full row; RQ_ERR_ARG for bad arguments */
+int gw_sample_topk(const float *vals, const int *idx, int k, float temperature, float topp, unsigned long long *rng);
+
 /* rq_decode (runq.h:346) followed by the greedy choice on the device: *next = the first maximum of the row's logits,
  * which stay on the device (no vocab-size copy per step; gw_ctx_argmax can read them again). The decode loop of a
  * greedy generation (rq_gen_step + sample_argmax, chat.c:348, sampler.c:40) without the logits transfer */

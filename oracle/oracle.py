@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 REF_DIR = os.path.join(HERE, "_ref")
 REF_DRIVER = os.path.join(REF_DIR, "ref_driver")
 REF_Q8OP = os.path.join(REF_DIR, "ref_q8op")
+REF_SAMPLE = os.path.join(REF_DIR, "ref_sample")
 
 _lib = None
 
@@ -242,3 +243,18 @@ def run_ref_kq(workdir: str, typ: int, blocks, xq, xs, N: int, K: int, timeout: 
     if r.returncode != 0:
         raise RuntimeError(f"ref_q8op kq failed: {r.stderr[-2000:]}")
     return np.fromfile(paths[3], np.float32).reshape(M, N)
+
+
+def run_ref_sample(workdir: str, logits, k: int, temperature: float, topp: float, rng: int, timeout: float = 120):
+    """the reference's sample_topk (sampler.c, oracle/_ref/ref_sample) on each row of logits with the coin of
+    rq_rng_f32: (tokens, the RNG state after the last draw)"""
+    os.makedirs(workdir, exist_ok=True)
+    lp = os.path.join(workdir, "sample_logits.bin")
+    x = np.ascontiguousarray(logits, np.float32)
+    x.tofile(lp)
+    cmd = [REF_SAMPLE, lp, str(x.shape[0]), str(x.shape[1]), str(k), repr(float(temperature)), repr(float(topp)), str(rng)]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)
+    if r.returncode != 0:
+        raise RuntimeError(f"ref_sample failed: {r.stderr[-2000:]}")
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    return [int(t) for t in out["tokens"]], int(out["rng"], 16)

@@ -309,3 +309,20 @@ def test_bf16_and_f16_sequences_in_one_pass(gw, synth_models):
     assert lg.shape[0] == len(alone)
     for r, (a, b) in enumerate(zip(lg, alone)):
         assert _bits_equal(a, b), f"row {r}"
+
+
+
+@pytest.mark.parametrize("k", [1, 7, 40, 64])
+def test_device_topk(gw, synth_models, k):
+    """gw_ctx_topk: the k best logits of each row on the device and their ids, in sample_topk's order (larger first,
+    the lower id first on ties: numpy's lexsort of the host logits), for the rows of a batched pass"""
+    path = synth_models("tiny_gqa4")
+    m = gw.Model(path, ctx_len=512)
+    c = m.ctx(max_batch=64)
+    seqs = [m.seq(512) for _ in range(5)]
+    segs = [gw.Segment(sq, [int(t) for t in _ids(m.vocab, n, n)], gw.RQ_LOGITS_LAST) for sq, n in zip(seqs, (1, 3, 9, 30, 2))]
+    lg, _ = c.forward_batch(segs)
+    vals, idx = c.topk(5, k)
+    order = np.lexsort((np.arange(m.vocab)[None, :].repeat(5, 0), -lg), axis=1)[:, :k]
+    assert np.array_equal(idx, order)
+    assert _bits_equal(vals, np.take_along_axis(lg, order, 1))

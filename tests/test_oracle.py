@@ -428,3 +428,32 @@ def test_golden_vectors():
         blk = z[f"kq{typ}_blk"]
         got = orc.kq_matmul(typ, blk, z[f"kq{typ}_xq"], z[f"kq{typ}_xs"], blk.shape[0], 512)
         assert np.array_equal(_u32(got), _u32(z[f"kq{typ}_out"])), f"type {typ}"
+
+
+@need_ref
+@pytest.mark.parametrize("V,k,T,topp", [(1000, 1, 0.8, 0.0), (5000, 7, 1.0, 0.9), (151936, 40, 0.7, 0.95),
+                                        (151936, 64, 1.3, 0.0), (4096, 64, 0.5, 0.5)])
+def test_sample_topk_vs_reference(tmp_path, V, k, T, topp):
+    """gw_sample_topk (the library's host replay of sample_topk on a row's k candidates) against the reference's own
+    sample_topk on the full row (oracle/_ref/ref_sample): the same token and RNG state, row after row; candidates in
+    the reference's order (larger first, lower index on ties), ties planted"""
+    import ctypes
+    import gwenedeg_amd as gw
+    rng = np.random.default_rng(V + k)
+    rows = 12
+    x = (rng.standard_normal((rows, V)) * 2).astype(np.float32)
+    x[1, 10] = x[1, 20] = x[1, 30] = np.float32(x[1].max() + 1)  # a three-way tie at the top
+    x[2, :] = np.float32(0.25)  # a row of equal values
+    state = 0x2545F4914F6CDD1D
+    ref_tok, ref_state = orc.run_ref_sample(str(tmp_path), x, k, T, topp, state)
+    order = np.lexsort((np.arange(V)[None, :].repeat(rows, 0), -x), axis=1)[:, :k]
+    st = ctypes.c_ulonglong(state)
+    mine = []
+    for r in range(rows):
+        vals = np.ascontiguousarray(x[r, order[r]], np.float32)
+        idx = np.ascontiguousarray(order[r], np.int32)
+        t = gw.lib.gw_sample_topk(vals.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                  idx.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), k, T, topp, ctypes.byref(st))
+        mine.append(int(t))
+    assert mine == ref_tok
+    assert st.value == ref_state
