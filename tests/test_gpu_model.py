@@ -1,6 +1,8 @@
 """Whole-model parity on the GPU through the rq_* C ABI: the device forward passes against the oracle's forward pass
 (or_forward_token) on seeded synthetic models, bit for bit (the logits; the KV cache through the logits of every later position), plus the reference's own invariants
 (batched == sequential, chunking, sequence copy / truncate, long context past one attention block)."""
+import os
+
 import numpy as np
 import pytest
 
@@ -326,3 +328,24 @@ def test_device_topk(gw, synth_models, k):
     order = np.lexsort((np.arange(m.vocab)[None, :].repeat(5, 0), -lg), axis=1)[:, :k]
     assert np.array_equal(idx, order)
     assert _bits_equal(vals, np.take_along_axis(lg, order, 1))
+
+
+def test_device_topk_full_vocab(gw, workdir):
+    """gw_ctx_topk over a 151,936-id row (the Qwen3 vocabulary: 64 chunks of 2,374 logits, the last one short) against
+    numpy's order of the host logits, k = 1 and 64; k above 64 is refused before any launch"""
+    from gwenedeg_amd import synth
+    d = dict(synth.SHAPES["tiny"])
+    d["vocab"] = 151936
+    path = synth.write_gguf(os.path.join(workdir, "tiny_v151936.gguf"), d, seed=3)
+    m = gw.Model(path, ctx_len=256)
+    c = m.ctx(max_batch=32)
+    seqs = [m.seq(256) for _ in range(3)]
+    segs = [gw.Segment(sq, [int(t) for t in _ids(m.vocab, n, n)], gw.RQ_LOGITS_LAST) for sq, n in zip(seqs, (1, 5, 17))]
+    lg, _ = c.forward_batch(segs)
+    ref = np.lexsort((np.arange(m.vocab)[None, :].repeat(3, 0), -lg), axis=1)
+    for k in (1, 64):
+        vals, idx = c.topk(3, k)
+        assert np.array_equal(idx, ref[:, :k]), k
+        assert _bits_equal(vals, np.take_along_axis(lg, ref[:, :k], 1))
+    with pytest.raises(Exception):
+        c.topk(3, 65)
