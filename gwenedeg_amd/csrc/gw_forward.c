@@ -1025,10 +1025,11 @@ int gw_ctx_topk(RqCtx *c, int n, int k, float *vals, int *idx) {
     int rows = c->last_nsel;
     if (rows <= 0 || n < 1 || n > rows) return ctx_fail(c, RQ_ERR_STATE, "no logits rows on the device (%d)", rows);
     if (k < 1 || k > 64 || k >= c->m->vocab || !vals || !idx) return ctx_fail(c, RQ_ERR_ARG, "top-k %d", k);
-    if (!c->topk_scr) {
+    {   /* each buffer on first use; one that failed before is tried again, never launched on as null */
         size_t sb = (size_t)c->nb_max * 64 * 64 * 8, ob = (size_t)c->nb_max * 64 * 4;
-        if (hipMalloc(&c->topk_scr, sb) != hipSuccess || hipMalloc((void **)&c->topk_v, ob) != hipSuccess ||
-            hipMalloc((void **)&c->topk_i, ob) != hipSuccess)
+        if ((!c->topk_scr && hipMalloc(&c->topk_scr, sb) != hipSuccess) ||
+            (!c->topk_v && hipMalloc((void **)&c->topk_v, ob) != hipSuccess) ||
+            (!c->topk_i && hipMalloc((void **)&c->topk_i, ob) != hipSuccess))
             return ctx_fail(c, RQ_ERR_NOMEM, "top-k scratch");
     }
     if (gw_k_topk(c->logits_d, c->m->vocab, c->m->vocab, n, k, c->topk_v, c->topk_i, c->topk_scr, c->stream))

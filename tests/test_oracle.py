@@ -457,3 +457,21 @@ def test_sample_topk_vs_reference(tmp_path, V, k, T, topp):
         mine.append(int(t))
     assert mine == ref_tok
     assert st.value == ref_state
+
+
+def test_sample_topk_argument_checks():
+    """gw_sample_topk refuses what sample_topk's candidate array cannot hold (k above 64, below 1), a temperature that
+    is not positive, and null pointers, without touching the RNG state; k = 1 returns the first candidate and still
+    advances the RNG by one draw, as sample_topk does (sampler.c:186-256)"""
+    import ctypes
+    import gwenedeg_amd as gw
+    v = np.linspace(3, 1, 65).astype(np.float32)
+    i = np.arange(100, 165, dtype=np.int32)
+    fp, ip = v.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), i.ctypes.data_as(ctypes.POINTER(ctypes.c_int))
+    st = ctypes.c_ulonglong(12345)
+    for k, T in ((65, 1.0), (0, 1.0), (8, 0.0), (8, -1.0), (8, float("nan"))):
+        assert gw.lib.gw_sample_topk(fp, ip, k, T, 0.9, ctypes.byref(st)) == gw.RQ_ERR_ARG
+        assert st.value == 12345
+    assert gw.lib.gw_sample_topk(None, ip, 8, 1.0, 0.9, ctypes.byref(st)) == gw.RQ_ERR_ARG
+    assert gw.lib.gw_sample_topk(fp, ip, 1, 1.0, 0.9, ctypes.byref(st)) == 100
+    assert st.value != 12345
