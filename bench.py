@@ -150,6 +150,7 @@ def main():
     m_s = sum(pre[k][0] for k in GEMV_CLASSES[:4])
     m_n = sum(pre[k][1] for k in GEMV_CLASSES[:4])
     tops = pre_ops / m_s / 1e12
+    sampling = sampling_cost(c)
     sw_s, sw_bytes, sw_n = c.gemv_sweep(2)
 
     out = {
@@ -190,6 +191,7 @@ def main():
         "kernel_us_per_decode_token": {k: round(v[0] * 1e6 / a.gen, 2) for k, v in dec.items() if v[1]},
         "kernel_ms_prefill": {k: round(v[0] * 1e3, 3) for k, v in pre.items() if v[1]},
         "tokens_head": toks[:8],
+        "sampling_topk40": sampling,
     }
     if not a.no_cpu_baseline:
         cb = cpu_baseline(path, ids, a)
@@ -394,6 +396,30 @@ def probe(torch, gw, c, s, ids, a):
     torch.neg(src, out=dst)  # one elementwise kernel: 1 GiB read, 1 GiB written
     torch.cuda.synchronize()
     log(f"probe done: prefill {len(ids)} + {a.gen} decode steps, copy of {src.numel() * 4} bytes")
+
+
+def sampling_cost(c, k=40, reps=200, temperature=0.7, topp=0.9):
+    """Host wall time per token of top-k sampling on the last decode pass's logits row, after the timed region: the
+    device top-k (gw_ctx_topk: two kernels, k (value, id) pairs back over PCIe, one synchronisation) and the host draw
+    (gw_sample_topk), each averaged over reps calls. Outside the metric; an error is reported, not raised."""
+    import ctypes
+    import gwenedeg_amd as gw
+    try:
+        c.topk(1, k)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            vals, idx = c.topk(1, k)
+        t_dev = (time.perf_counter() - t0) / reps
+        st = ctypes.c_ulonglong(0x9E3779B97F4A7C15)
+        fp, ip = vals.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), idx.ctypes.data_as(ctypes.POINTER(ctypes.c_int))
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            tok = gw.lib.gw_sample_topk(fp, ip, k, temperature, topp, ctypes.byref(st))
+        t_draw = (time.perf_counter() - t0) / reps
+        return {"device_topk_us": round(t_dev * 1e6, 2), "host_draw_us": round(t_draw * 1e6, 2), "k": k,
+                "temperature": temperature, "top_p": topp, "last_token": int(tok)}
+    except Exception as e:  # noqa: BLE001 - a side figure must not cost the bench line
+        return {"error": str(e)}
 
 
 def cpu_baseline(path, ids, a):
