@@ -674,7 +674,7 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
     }
     int resid_done = fused; /* (the fused sequence leaves no pending residual in xb) */
     if (P->want_hidden) { /* every row's final hidden state (the normed row), then the logits rows below */
-        KCHK(gw_k_rmsnorm_quant(c->x, c->xb, dim, m->final_norm, NULL, n, c->xq, c->xs, K, c->hid_d, s));
+        KCHK(gw_k_rmsnorm_quant(c->x, resid_done ? NULL : c->xb, dim, m->final_norm, NULL, n, c->xq, c->xs, K, c->hid_d, s));
         resid_done = 1;
     }
     if (fused && P->nsel == 1 && !P->want_hidden) { /* the final rmsnorm computed by the classifier's GEMV itself */
@@ -1025,8 +1025,10 @@ int gw_ctx_topk(RqCtx *c, int n, int k, float *vals, int *idx) {
     int rows = c->last_nsel;
     if (rows <= 0 || n < 1 || n > rows) return ctx_fail(c, RQ_ERR_STATE, "no logits rows on the device (%d)", rows);
     if (k < 1 || k > 64 || k >= c->m->vocab || !vals || !idx) return ctx_fail(c, RQ_ERR_ARG, "top-k %d", k);
-    {   /* each buffer on first use; one that failed before is tried again, never launched on as null */
-        size_t sb = (size_t)c->nb_max * 64 * 64 * 8, ob = (size_t)c->nb_max * 64 * 4;
+    {   /* each buffer on first use, for the context's rows (one for a context of max_batch 0 or 1, whose decode leaves
+         * one row); one that failed before is tried again, never launched on as null */
+        const size_t B = c->nb_max > 1 ? (size_t)c->nb_max : 1;
+        size_t sb = B * 64 * 64 * 8, ob = B * 64 * 4;
         if ((!c->topk_scr && hipMalloc(&c->topk_scr, sb) != hipSuccess) ||
             (!c->topk_v && hipMalloc((void **)&c->topk_v, ob) != hipSuccess) ||
             (!c->topk_i && hipMalloc((void **)&c->topk_i, ob) != hipSuccess))

@@ -898,7 +898,8 @@ int gw_k_quant_rows(const float *x, int n, int ldxf, int rows, int8_t *q, float 
 
 int gw_k_topk(const float *lg, int n, int ld, int rows, int k, float *vals, int *idx, void *scratch, hipStream_t s) {
     /* scratch: rows x TOPK_CH x TOPK_KMAX float2; n <= TOPK_CH x 16 x 256, k <= TOPK_KMAX and < n */
-    if (k < 1 || k > TOPK_KMAX || k >= n || n > TOPK_CH * 16 * 256) return (int)hipErrorInvalidValue;
+    if (k < 1 || k > TOPK_KMAX || k >= n || n > TOPK_CH * 16 * 256 || rows < 1 || !lg || !vals || !idx || !scratch)
+        return (int)hipErrorInvalidValue;
     hipLaunchKernelGGL(k_topk_part, dim3(rows, TOPK_CH), dim3(256), 0, s, lg, n, ld, k, (float2 *)scratch);
     hipLaunchKernelGGL(k_topk_final, dim3(rows), dim3(256), 0, s, (const float2 *)scratch, k, vals, idx);
     return (int)hipGetLastError();

@@ -328,6 +328,16 @@ def test_device_topk(gw, synth_models, k):
     order = np.lexsort((np.arange(m.vocab)[None, :].repeat(5, 0), -lg), axis=1)[:, :k]
     assert np.array_equal(idx, order)
     assert _bits_equal(vals, np.take_along_axis(lg, order, 1))
+    # decode contexts without batch buffers (max_batch 0 and 1, runq.h:329): their decode leaves one row
+    for mb in (0, 1):
+        c1 = m.ctx(max_batch=mb, max_ctx=512)
+        s1 = m.seq(512)
+        c1.prefill(s1, _ids(m.vocab, 6, 40 + mb), mode=gw.RQ_LOGITS_NONE)
+        row = c1.decode(s1, 5)
+        v1, i1 = c1.topk(1, k)
+        o1 = np.lexsort((np.arange(m.vocab), -row))[:k]
+        assert np.array_equal(i1[0], o1), f"max_batch {mb}"
+        assert _bits_equal(v1[0], row[o1])
 
 
 def test_device_topk_full_vocab(gw, workdir):

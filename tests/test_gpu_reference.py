@@ -176,6 +176,30 @@ def test_hidden_rows_bit_identical(gw, orc, tmp_path, shape, layers):
         assert np.array_equal(_bits(lg), _bits(rlg)), f"fw_rows (max_batch {nb}): logits rows"
 
 
+def test_hidden_rows_after_batched_passes_on_one_context(gw, orc, tmp_path):
+    """hidden rows from one-row passes that follow multi-row passes on the same context (the speculative loop's
+    pattern, spec.c:336-350): a 20-token prefill in passes of 8 rows, then rq_decode_hidden, then fw_rows of 41 tokens
+    with max_batch 8 (its last chunk one row), on an all-Q8_0 model (the one-row passes take the fused decode
+    sequence, which keeps no pending residual): every hidden row and logits row bit for bit against the reference's
+    rq_decode_hidden token by token"""
+    path, d = _synth(str(tmp_path), "qwen3_0_6b", n_layers=3)
+    m = gw.Model(path, ctx_len=256)
+    if not _exact(gw):
+        pytest.skip("this host does not provide the reference's float operations (AVX-512)")
+    ids = np.random.default_rng(12).integers(0, m.vocab, 62).astype(np.int32)
+    _, rlg, rhid, _ = orc.run_ref_driver(path, ids, str(tmp_path / "ref"), threads=_threads(), cap=256, hidden=True)
+    c = m.ctx(max_batch=8, max_ctx=256)
+    s = m.seq(256)
+    lg, hid = c.prefill_hidden(s, ids[:20], mode=gw.RQ_LOGITS_ALL)
+    assert np.array_equal(_bits(hid), _bits(rhid[:20])) and np.array_equal(_bits(lg), _bits(rlg[:20]))
+    lg, hid = c.decode_hidden(s, int(ids[20]))
+    assert np.array_equal(_bits(hid), _bits(rhid[20])), "rq_decode_hidden after a batched prefill: hidden row"
+    assert np.array_equal(_bits(lg), _bits(rlg[20])), "rq_decode_hidden after a batched prefill: logits"
+    lg, hid = c.prefill_hidden(s, ids[21:62], mode=gw.RQ_LOGITS_ALL)
+    assert np.array_equal(_bits(hid), _bits(rhid[21:62])), "fw_rows n 41, max_batch 8: hidden rows"
+    assert np.array_equal(_bits(lg), _bits(rlg[21:62])), "fw_rows n 41, max_batch 8: logits rows"
+
+
 @pytest.mark.parametrize("kvt", [2, 1])  # RQ_KV_F16, RQ_KV_BF16
 def test_seqfile_with_reference(gw, orc, tmp_path, kvt):
     """the KV disk tier (runq.h:283-314) against the reference's seqfile.c: the same model fingerprint; the reference's
