@@ -104,6 +104,8 @@ _sig = {
     "rq_seq_copy": (_I, [_P, _P, _I]),
     "rq_seq_fill_synthetic": (_I, [_P, _I, ctypes.c_ulonglong]),
     "rq_seq_common_prefix": (_I, [_P, ctypes.POINTER(_I), _I]),
+    "rq_seq_save": (_I, [_P, ctypes.c_char_p]),
+    "rq_seq_load": (_I, [_P, ctypes.c_char_p, _I]),
     "rq_ctx_new": (_P, [_P, _I, _I, ctypes.POINTER(_I)]),
     "rq_ctx_free": (None, [_P]),
     "rq_ctx_error": (ctypes.c_char_p, [_P]),
@@ -223,6 +225,18 @@ class Seq:
         r = lib.rq_seq_fill_synthetic(self._h, n, seed)
         if r != RQ_OK:
             raise RqError(r, "rq_seq_fill_synthetic")
+
+    def save(self, path: str):
+        """rq_seq_save (runq.h:293): the sequence in the reference's saved-sequence format"""
+        r = lib.rq_seq_save(self._h, path.encode())
+        if r != RQ_OK:
+            raise RqError(r, "rq_seq_save")
+
+    def load(self, path: str, n: int):
+        """rq_seq_load (runq.h:314): the first n positions of a saved sequence"""
+        r = lib.rq_seq_load(self._h, path.encode(), n)
+        if r != RQ_OK:
+            raise RqError(r, "rq_seq_load")
 
     def close(self):
         if self._h:

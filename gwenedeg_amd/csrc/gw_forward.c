@@ -57,6 +57,9 @@ RqSeq *rq_seq_new(const RqModel *m, int capacity, int kv_type, int *err) {
     s->kvt = kv_type;
     s->cap = capacity;
     s->kv_len = (capacity + GW_ATT_P - 1) / GW_ATT_P * GW_ATT_P;
+    s->att_nb = s->kv_len / GW_ATT_P;
+    s->nck = 2;   /* (RQ_SEQ_CK, internal.h:66) */
+    s->hpos = -1; /* (not an MTP view's sequence) */
     size_t bytes = (size_t)m->n_layers * seq_layer_elems(s) * 2;
     if (hipMalloc((void **)&s->kc, bytes) != hipSuccess || hipMalloc((void **)&s->vc, bytes) != hipSuccess) {
         e = RQ_ERR_NOMEM;
@@ -80,11 +83,27 @@ void rq_seq_free(RqSeq *s) {
     free(s);
 }
 
-void rq_seq_reset(RqSeq *s) { s->len = 0; }
+/* the length grows to n (the high-water mark with it: internal.h:400-411's seq_grow) */
+static void seq_grow(RqSeq *s, int n) {
+    if (n > s->hwm) s->hwm = n;
+    s->len = n;
+}
+
+/* an MTP view's rows past n are gone (internal.h:383-393: hvalid = min(hvalid, n), hpos past n - 1 -> -1) */
+static void seq_cut_view_state(RqSeq *s, int n) {
+    if (s->hvalid > n) s->hvalid = n;
+    if (s->hpos > n - 1) s->hpos = -1;
+}
+
+void rq_seq_reset(RqSeq *s) {
+    s->len = 0;
+    seq_cut_view_state(s, 0);
+}
 
 int rq_seq_truncate(RqSeq *s, int n) {
     if (n < 0 || n > s->len) return RQ_ERR_ARG;
     s->len = n;
+    seq_cut_view_state(s, n);
     return RQ_OK;
 }
 
@@ -92,7 +111,13 @@ int rq_seq_keep(const RqSeq *s, int n) { return n < 0 || n > s->len ? RQ_ERR_ARG
 int rq_seq_checkpoint_at(RqSeq *s, int pos) { (void)s; (void)pos; return RQ_OK; }
 int rq_seq_checkpoint_rows(RqSeq *s, int pos, int n) { (void)s; (void)pos; (void)n; return RQ_OK; }
 void rq_seq_checkpoint_rows_drop(RqSeq *s) { (void)s; }
-int rq_seq_set_checkpoints(RqSeq *s, int n) { (void)s; return n < 1 || n > 32 ? RQ_ERR_ARG : RQ_OK; }
+int rq_seq_set_checkpoints(RqSeq *s, int n) {
+    /* runq.h:250-252 (forward.c:360-373): the slot count is kept (spec.c reads and restores it); a Qwen3 sequence holds
+     * no checkpoint in them */
+    if (n < 1 || n > RQ_CHECKPOINTS_MAX) return RQ_ERR_ARG;
+    s->nck = n;
+    return RQ_OK;
+}
 int rq_seq_checkpoints(const RqSeq *s, int *pos, int max) { (void)s; (void)pos; (void)max; return 0; }
 int rq_seq_len(const RqSeq *s) { return s->len; }
 int rq_seq_capacity(const RqSeq *s) { return s->cap; }
@@ -145,7 +170,10 @@ int rq_seq_copy(RqSeq *dst, const RqSeq *src, int n) {
             }
         }
     memcpy(dst->tokens, src->tokens, (size_t)n * sizeof(int));
-    dst->len = n;
+    seq_grow(dst, n);
+    dst->hvalid = src->hvalid;
+    dst->hpos = src->hpos;
+    seq_cut_view_state(dst, n);
     return RQ_OK;
 }
 
@@ -159,7 +187,8 @@ int rq_seq_fill_synthetic(RqSeq *s, int n, unsigned long long seed) {
             return RQ_ERR_STATE;
     if (hipDeviceSynchronize() != hipSuccess) return RQ_ERR_STATE;
     for (int i = 0; i < n; i++) s->tokens[i] = (int)((seed + (unsigned long long)i * 7919u) % (unsigned long long)s->m->vocab);
-    s->len = n;
+    seq_grow(s, n);
+    seq_cut_view_state(s, n);
     return RQ_OK;
 }
 
@@ -731,7 +760,7 @@ static int decode_one(RqCtx *c, RqSeq *s, int token, float *logits, float *hidde
     int rc = fw_pass(c, &P, logits);
     if (rc != RQ_OK) return rc;
     s->tokens[s->len] = token;
-    s->len++;
+    seq_grow(s, s->len + 1);
     return RQ_OK;
 }
 
@@ -766,7 +795,7 @@ int gw_decode_argmax(RqCtx *c, RqSeq *s, int token, int *next) {
     P.hid[0] = NULL;
     if ((e = fw_pass(c, &P, NULL)) != RQ_OK) return e;
     s->tokens[s->len] = token;
-    s->len++;
+    seq_grow(s, s->len + 1);
     return gw_ctx_argmax(c, next, 1);
 }
 
@@ -832,7 +861,7 @@ int gw_decode_greedy(RqCtx *c, RqSeq *s, int token, int n, int *tokens) {
     HIPCHK(c, "hipStreamSynchronize (greedy)", hipStreamSynchronize(st));
     memcpy(tokens, c->g_h, (size_t)n * sizeof(int));
     for (int i = 0; i < n; i++) s->tokens[p0 + i] = i ? tokens[i - 1] : token;
-    s->len = p0 + n;
+    seq_grow(s, p0 + n);
     c->last_nsel = 1;
     return RQ_OK;
 }
@@ -900,7 +929,7 @@ static int fw_batch(RqCtx *c, const RqSegment *sg, int nseg, float *out, float *
     for (int i = 0; i < nseg; i++) {
         RqSeq *s = sg[i].seq;
         memcpy(s->tokens + s->len, sg[i].tokens, (size_t)sg[i].n * sizeof(int));
-        s->len += sg[i].n;
+        seq_grow(s, s->len + sg[i].n);
     }
     if (logits) *logits = nsel ? out : NULL;
     return RQ_OK;

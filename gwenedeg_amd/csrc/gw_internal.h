@@ -62,7 +62,39 @@ typedef struct {
     float *att_norm, *ffn_norm, *q_norm, *k_norm; /* device */
 } GwLayer;
 
+/* The reference's host modules that stay on the host (sampler.c, spec.c, chat.c, tokenizer.c's rq_token_bytes) read some
+ * RqModel / RqSeq fields directly (internal.h:229-306, :353-398), compiled against the reference's layout. So both
+ * structs begin with that layout as gcc lays it out on x86-64 (RqModel 9,208 bytes, RqSeq 1,832): the fields those
+ * modules read sit at the reference's offsets, with this library's values, and every other byte of that prefix stays
+ * zero. This library's own fields follow the prefix. The offsets are checked at compile time below and against the
+ * reference's internal.h by tests/test_abi.py */
+typedef struct { /* Config (internal.h:72-86): the first 48 bytes of the reference's RqModel */
+    int magic_number, version, dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len, head_dim,
+        shared_classifier, group_size;
+} GwRefConfig;
+
+#define GW_REF_MODEL_BYTES 9208
+#define GW_REF_SEQ_BYTES 1832
+
 struct RqModel {
+    /* the reference's prefix (the readers: spec.c:32-54 config.vocab_size, :271-326 config.dim, :48 has_tok, :219 hy.on,
+     * :292-330 mtp_of; sampler.c:328-331 samp_*; chat.c:38-295 chat, has_tok, the templates; tokenizer.c:812 has_tok) */
+    GwRefConfig config;            /* @0: this model's shape, group_size 32 */
+    unsigned char ref0_[1752 - 48];
+    uint64_t ref_fp;               /* @1752: the file's fingerprint (model.c:949-953) */
+    int has_weights, has_tok, is_gguf; /* @1760: 1, 0 (no tokenizer is built: rq_token_bytes gives "", spec.c's draft
+                                        * check RQ_ERR_STATE, chat.c's functions RQ_ERR_STATE), 1 */
+    unsigned char ref1_[2080 - 1772];
+    int hy_on;                     /* @2080: Hybrid.on, 0 (Qwen3: no linear-attention layers) */
+    unsigned char ref2_[2684 - 2084];
+    int chat;                      /* @2684: RQ_CHAT_* 0 */
+    unsigned char ref3_[2768 - 2688];
+    float samp_temp, samp_topp;    /* @2768: the file's recommended sampling, none (samp_set 0) */
+    int samp_topk, samp_set;
+    char user_tmpl[2][1024], sys_tmpl[2][1024], tmpl_missing[2][1088]; /* @2784, @4832, @6880: empty */
+    const RqModel *mtp_of;         /* @9056: NULL (not an MTP view) */
+    unsigned char ref4_[GW_REF_MODEL_BYTES - 9064];
+    /* this library's own */
     int dim, hidden, n_layers, n_heads, n_kv_heads, head_dim, vocab, seq_len, ctx_max, tied;
     float rope_theta, log_theta, att_scale;
     unsigned long long fingerprint;
@@ -77,13 +109,43 @@ struct RqModel {
 };
 
 struct RqSeq {
-    const RqModel *m;
-    int cap, kv_len, len, hwm;
+    /* the reference's prefix (the readers: spec.c:219 / :426 / :590 nck, :292-402 len, tokens, hvalid, hpos, hprev;
+     * sampler.c:321-323 rng; chat.c:357 m) */
+    const RqModel *m;  /* @0 */
+    int cap;           /* @8: positions */
+    int kv_len;        /* @12: cap rounded up to whole 256-position blocks (the cache layout) */
+    int att_nb;        /* @16: kv_len / 256 */
+    int kvt;           /* @20: RQ_KV_F16 or RQ_KV_BF16 */
+    unsigned char ref0_[80 - 24];
+    int len;           /* @80: positions in the cache */
+    int hwm;           /* @84 */
+    unsigned char ref1_[96 - 88];
+    int *tokens;       /* @96: host, cap tokens */
+    unsigned char ref2_[120 - 104];
+    int nck;           /* @120: checkpoint slots (rq_seq_set_checkpoints; RQ_SEQ_CK 2 at rq_seq_new). Qwen3 keeps no
+                        * checkpoint: the count is only kept */
+    unsigned char ref3_[1808 - 124];
+    unsigned long long rng; /* @1808: the sampler's xorshift state */
+    int hvalid, hpos;  /* @1816: an MTP view's state (spec.c); 0 and -1 here (no sequence is a view's) */
+    float *hprev;      /* @1824: NULL */
+    /* this library's own */
     uint16_t *kc, *vc; /* device: n_layers x kv_len x kv_dim 16-bit values each (f16, or bf16 when kvt is) */
-    int kvt;           /* RQ_KV_F16 or RQ_KV_BF16 */
-    int *tokens;       /* host */
-    unsigned long long rng;
 };
+
+#ifndef __cplusplus
+_Static_assert(sizeof(GwRefConfig) == 48, "Config");
+_Static_assert(offsetof(struct RqModel, ref_fp) == 1752 && offsetof(struct RqModel, has_tok) == 1764 &&
+               offsetof(struct RqModel, hy_on) == 2080 && offsetof(struct RqModel, chat) == 2684 &&
+               offsetof(struct RqModel, samp_temp) == 2768 && offsetof(struct RqModel, samp_set) == 2780 &&
+               offsetof(struct RqModel, user_tmpl) == 2784 && offsetof(struct RqModel, sys_tmpl) == 4832 &&
+               offsetof(struct RqModel, tmpl_missing) == 6880 && offsetof(struct RqModel, mtp_of) == 9056 &&
+               offsetof(struct RqModel, dim) == GW_REF_MODEL_BYTES, "RqModel: the reference's offsets");
+_Static_assert(offsetof(struct RqSeq, cap) == 8 && offsetof(struct RqSeq, kvt) == 20 && offsetof(struct RqSeq, len) == 80 &&
+               offsetof(struct RqSeq, tokens) == 96 && offsetof(struct RqSeq, nck) == 120 &&
+               offsetof(struct RqSeq, rng) == 1808 && offsetof(struct RqSeq, hvalid) == 1816 &&
+               offsetof(struct RqSeq, hpos) == 1820 && offsetof(struct RqSeq, hprev) == 1824 &&
+               offsetof(struct RqSeq, kc) == GW_REF_SEQ_BYTES, "RqSeq: the reference's offsets");
+#endif
 
 struct RqCtx {
     const RqModel *m;

@@ -635,6 +635,12 @@ RqModel *rq_model_load(const char *path, const RqModelOpts *o, char *err, size_t
         if (rc != RQ_OK) goto out;
     }
     hipGetDevice(&m->device);
+    /* the reference's view of the model (its host modules read these: the layout note in gw_internal.h) */
+    m->config = (GwRefConfig){ 0, 0, m->dim, m->hidden, m->n_layers, m->n_heads, m->n_kv_heads, m->vocab, m->seq_len,
+                               m->head_dim, m->tied, 32 };
+    m->ref_fp = m->fingerprint;
+    m->has_weights = 1;
+    m->is_gguf = 1;
 out:
     if (L.stage) hipFree(L.stage);
     free(L.g.kv);

@@ -221,7 +221,10 @@ int rq_seq_load(RqSeq *dst, const char *path, int n) {
         if (rc == RQ_OK) {
             memcpy(dst->tokens, tk, (size_t)n * sizeof(int));
             dst->len = n;
+            if (n > dst->hwm) dst->hwm = n;
             dst->rng = h.rng;
+            dst->hvalid = n; /* (seqfile.c:385; no view here, so no kept hidden state: hpos -1) */
+            dst->hpos = -1;
         }
     }
     close(fd);

@@ -215,6 +215,31 @@ def run_ref_driver(model: str, ids: np.ndarray, workdir: str, steps: int = 0, th
     return info, lg, toks, (kv_path if kv else None)
 
 
+def run_ref_plan(model: str, plan: str, workdir: str, threads: int = 0, cap: int = 0, kv_type: int = 2,
+                 timeout: float = 900):
+    """The reference's own CPU path on a script of passes (ref_driver --plan: sequences loaded from saved KV files,
+    prefix copies, rq_forward_batch passes with greedy feeds; the command list is in oracle/ref_driver.c): returns
+    (info JSON, every selected logits row in pass order, the tokens the greedy feeds chose)."""
+    os.makedirs(workdir, exist_ok=True)
+    plan_path, lg_path, tok_path = (os.path.join(workdir, n) for n in ("plan.txt", "plan_logits.bin", "plan_tokens.bin"))
+    with open(plan_path, "w") as f:
+        f.write(plan)
+    cmd = [REF_DRIVER, "-m", model, "--plan", plan_path, "--logits", lg_path, "--tokens", tok_path]
+    if threads:
+        cmd += ["-t", str(threads)]
+    if cap:
+        cmd += ["-c", str(cap)]
+    if kv_type != 2:
+        cmd += ["--kv-type", str(kv_type)]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)
+    if r.returncode != 0:
+        raise RuntimeError(f"ref_driver --plan failed: {r.stderr[-2000:]}")
+    info = json.loads(r.stdout.strip().splitlines()[-1])
+    lg = np.fromfile(lg_path, np.float32).reshape(-1, info["vocab"])
+    toks = np.fromfile(tok_path, np.int32) if os.path.getsize(tok_path) else np.zeros(0, np.int32)
+    return info, lg, toks
+
+
 def run_ref_q8op(workdir: str, wq, ws, xq, xs, reps: int = 0, threads: int = 1, timeout: float = 600):
     """The reference's q8p_gemv_rows / q8p_gemm_item on given int8 inputs: returns (out M x N, timing JSON or None)."""
     os.makedirs(workdir, exist_ok=True)

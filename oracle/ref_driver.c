@@ -11,6 +11,8 @@
  *   --hidden FILE: instead, the prompt token by token through rq_decode_hidden (runq.h:350), every row's logits and
  *   final hidden state (after output_norm, dim floats) written.
  *   --kv-type T: the sequences' KV cache type (runq.h:214; default RQ_KV_F16).
+ *   --plan FILE: instead, a script of passes over sequences loaded from saved KV files (the configs' pass shapes on
+ *   caches the device filled: run_plan below); --ids is not read then.
  * Output: one JSON line on stdout. */
 #include <stdint.h>
 #include <stdio.h>
@@ -41,8 +43,105 @@ static void write_all(FILE *f, const void *p, size_t n) {
     if (f && fwrite(p, 1, n, f) != n) { perror("write"); exit(1); }
 }
 
+/* --plan: a text script, one command per line
+ *   seqs N CAP              N sequences of capacity CAP (the --kv-type cache)
+ *   load I PATH             rq_seq_load of the whole saved sequence PATH into sequence I (rq_seq_file_info's length)
+ *   copy I J N              rq_seq_copy: sequence I := the first N positions of sequence J
+ *   pass NSEG               one rq_forward_batch of the NSEG segments on the next NSEG lines:
+ *   seg I MODE N T1 .. TN   N tokens for sequence I, RQ_LOGITS_* MODE; a token -1 is the first maximum of the last
+ *                           logits row this run produced for sequence I (the greedy feed, sampler.c:40-60)
+ * Every selected logits row goes to --logits in pass order, every token a -1 stood for to --tokens. */
+static int run_plan(RqModel *m, RqCtx *c, int V, int kv_type, const char *plan, FILE *lf, FILE *tf) {
+    FILE *f = fopen(plan, "r");
+    if (!f) { perror(plan); return 1; }
+    char cmd[32], path[4096];
+    int ns = 0, e, passes = 0, rows = 0;
+    RqSeq **sq = NULL;
+    float *out = malloc((size_t)RQ_BATCH_MAX * V * sizeof(float)), **last = NULL;
+    RqSegment *sg = malloc((size_t)RQ_BATCH_MAX * sizeof(RqSegment));
+    int *sgi = malloc((size_t)RQ_BATCH_MAX * sizeof(int)); /* each segment's sequence index */
+    if (!out || !sg || !sgi) { perror("malloc"); return 1; }
+    while (fscanf(f, "%31s", cmd) == 1) {
+        if (!strcmp(cmd, "seqs")) {
+            int cap;
+            if (fscanf(f, "%d %d", &ns, &cap) != 2 || ns < 1) { fprintf(stderr, "plan: bad seqs\n"); return 1; }
+            sq = calloc((size_t)ns, sizeof(RqSeq *));
+            last = calloc((size_t)ns, sizeof(float *));
+            for (int i = 0; i < ns; i++)
+                if (!(sq[i] = rq_seq_new(m, cap, kv_type, &e))) die("rq_seq_new", e, NULL);
+        } else if (!strcmp(cmd, "load")) {
+            int i;
+            RqSeqFile fi;
+            int *ft = NULL;
+            if (fscanf(f, "%d %4095s", &i, path) != 2 || i < 0 || i >= ns) { fprintf(stderr, "plan: bad load\n"); return 1; }
+            if ((e = rq_seq_file_info(m, path, &fi, &ft)) != RQ_OK) die("rq_seq_file_info", e, NULL);
+            free(ft);
+            if ((e = rq_seq_load(sq[i], path, fi.len)) != RQ_OK) die("rq_seq_load", e, NULL);
+        } else if (!strcmp(cmd, "copy")) {
+            int i, j, n;
+            if (fscanf(f, "%d %d %d", &i, &j, &n) != 3 || i < 0 || i >= ns || j < 0 || j >= ns) {
+                fprintf(stderr, "plan: bad copy\n");
+                return 1;
+            }
+            if ((e = rq_seq_copy(sq[i], sq[j], n)) != RQ_OK) die("rq_seq_copy", e, NULL);
+        } else if (!strcmp(cmd, "pass")) {
+            int nseg, nt = 0;
+            if (fscanf(f, "%d", &nseg) != 1 || nseg < 1 || nseg > RQ_BATCH_MAX) { fprintf(stderr, "plan: bad pass\n"); return 1; }
+            int *all = malloc((size_t)RQ_BATCH_MAX * sizeof(int)), nsel = 0;
+            for (int k = 0; k < nseg; k++) {
+                int i, mode, n;
+                if (fscanf(f, "%31s %d %d %d", cmd, &i, &mode, &n) != 4 || strcmp(cmd, "seg") || i < 0 || i >= ns || n < 1 ||
+                    nt + n > RQ_BATCH_MAX) {
+                    fprintf(stderr, "plan: bad segment\n");
+                    return 1;
+                }
+                for (int j = 0; j < n; j++) {
+                    if (fscanf(f, "%d", &all[nt + j]) != 1) { fprintf(stderr, "plan: bad token\n"); return 1; }
+                    if (all[nt + j] < 0) { /* the greedy feed */
+                        if (!last[i]) { fprintf(stderr, "plan: no logits row yet for sequence %d\n", i); return 1; }
+                        int best = 0;
+                        for (int v = 1; v < V; v++)
+                            if (last[i][v] > last[i][best]) best = v;
+                        all[nt + j] = best;
+                        write_all(tf, &best, sizeof(int));
+                    }
+                }
+                sg[k] = (RqSegment){ sq[i], all + nt, n, mode, NULL, NULL };
+                sgi[k] = i;
+                nt += n;
+                nsel += mode == RQ_LOGITS_ALL ? n : mode == RQ_LOGITS_LAST;
+            }
+            if ((e = rq_forward_batch(c, sg, nseg, nsel ? out : NULL, NULL)) != RQ_OK) die("rq_forward_batch", e, c);
+            write_all(lf, out, (size_t)nsel * V * sizeof(float));
+            for (int k = 0, r = 0; k < nseg; k++) { /* each sequence's last row of this pass, for a later greedy feed */
+                int i = sgi[k], sel = sg[k].logits == RQ_LOGITS_ALL ? sg[k].n : sg[k].logits == RQ_LOGITS_LAST;
+                if (sel) {
+                    if (!last[i]) last[i] = malloc((size_t)V * sizeof(float));
+                    memcpy(last[i], out + (size_t)(r + sel - 1) * V, (size_t)V * sizeof(float));
+                }
+                r += sel;
+            }
+            free(all);
+            passes++;
+            rows += nt;
+        } else {
+            fprintf(stderr, "plan: unknown command %s\n", cmd);
+            return 1;
+        }
+    }
+    fclose(f);
+    printf("{\"threads\": %d, \"vocab\": %d, \"passes\": %d, \"rows\": %d}\n", rq_threads(), V, passes, rows);
+    for (int i = 0; i < ns; i++) {
+        rq_seq_free(sq[i]);
+        free(last[i]);
+    }
+    free(sq); free(last); free(out); free(sg); free(sgi);
+    return 0;
+}
+
 int main(int argc, char **argv) {
-    const char *model = NULL, *ids_path = NULL, *logits_path = NULL, *tokens_path = NULL, *kv_path = NULL, *hidden_path = NULL;
+    const char *model = NULL, *ids_path = NULL, *logits_path = NULL, *tokens_path = NULL, *kv_path = NULL, *hidden_path = NULL,
+               *plan = NULL;
     int threads = 0, cap = 0, maxb = 512, steps = 0, reps = 1, all_logits = 0, nbd = 0, kv_type = RQ_KV_F16;
     for (int i = 1; i < argc; i++) {
         const char *a = argv[i], *v = i + 1 < argc ? argv[i + 1] : NULL;
@@ -60,9 +159,10 @@ int main(int argc, char **argv) {
         else if (!strcmp(a, "--all-logits")) all_logits = 1;
         else if (!strcmp(a, "--hidden") && v) hidden_path = v, i++;
         else if (!strcmp(a, "--kv-type") && v) kv_type = atoi(v), i++;
+        else if (!strcmp(a, "--plan") && v) plan = v, i++;
         else { fprintf(stderr, "ref_driver: bad argument %s\n", a); return 2; }
     }
-    if (!model || !ids_path) { fprintf(stderr, "usage: ref_driver -m MODEL --ids FILE [--steps K] ...\n"); return 2; }
+    if (!model || (!ids_path && !plan)) { fprintf(stderr, "usage: ref_driver -m MODEL --ids FILE [--steps K] ...\n"); return 2; }
     const char *warn = rq_threads_init(threads);
     if (warn) fprintf(stderr, "ref_driver: %s\n", warn);
     char err[512];
@@ -76,6 +176,18 @@ int main(int argc, char **argv) {
     RqModelInfo info;
     rq_model_info(m, &info);
     int V = info.vocab_size, e, n;
+    if (plan) {
+        RqCtx *pc = rq_ctx_new(m, RQ_BATCH_MAX, cap, &e);
+        if (!pc) die("rq_ctx_new", e, NULL);
+        FILE *lf = logits_path ? fopen(logits_path, "wb") : NULL, *tf = tokens_path ? fopen(tokens_path, "wb") : NULL;
+        if ((logits_path && !lf) || (tokens_path && !tf)) { perror("output"); return 1; }
+        int r = run_plan(m, pc, V, kv_type, plan, lf, tf);
+        if (lf) fclose(lf);
+        if (tf) fclose(tf);
+        rq_ctx_free(pc);
+        rq_model_free(m);
+        return r;
+    }
     int *ids = read_ids(ids_path, &n);
     int ns = nbd > 0 ? nbd : 1;
     if (nbd > 0 && maxb < ns) maxb = ns;

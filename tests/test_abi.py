@@ -148,3 +148,55 @@ def test_reference_host_modules_link():
     for mod, need in HOST_NEEDS.items():
         und = {s for s in syms(["-u"], objs[mod]) if s.startswith(ours)} - provided
         assert und == need, f"{mod}.o: unresolved {sorted(und)}, documented {sorted(need)}"
+
+
+# The RqModel / RqSeq fields the reference's host modules read directly (sampler.c:321-331, spec.c:32-54 / :219 /
+# :271-429, chat.c:38-357, tokenizer.c:812): their offsets and sizes in the reference's internal.h as gcc lays it out
+# on x86-64, which the library's structs keep (the reference's field names; the library's own fields follow)
+REF_FIELDS = {
+    "RqModel": {"config": (0, 48), "config.dim": (8, 4), "config.vocab_size": (28, 4), "config.seq_len": (32, 4),
+                "config.shared_classifier": (40, 4), "config.group_size": (44, 4), "fp": (1752, 8),
+                "has_weights": (1760, 4), "has_tok": (1764, 4), "is_gguf": (1768, 4), "hy.on": (2080, 4),
+                "chat": (2684, 4), "samp_temp": (2768, 4), "samp_topp": (2772, 4), "samp_topk": (2776, 4),
+                "samp_set": (2780, 4), "user_tmpl": (2784, 2048), "sys_tmpl": (4832, 2048),
+                "tmpl_missing": (6880, 2176), "mtp_of": (9056, 8)},
+    "RqSeq": {"m": (0, 8), "cap": (8, 4), "kv_len": (12, 4), "att_nb": (16, 4), "kvt": (20, 4), "len": (80, 4),
+              "hwm": (84, 4), "tokens": (96, 8), "nck": (120, 4), "rng": (1808, 8), "hvalid": (1816, 4),
+              "hpos": (1820, 4), "hprev": (1824, 8)},
+}
+REF_SIZES = {"RqModel": 9208, "RqSeq": 1832}
+# the library's names for the fields it keeps under its own name (the reference's nested Hybrid.on, the fingerprint)
+OURS = {"hy.on": "hy_on", "fp": "ref_fp"}
+
+
+def _field_offsets(tmp, include_dirs, header, names):
+    import subprocess
+    lines = [f'#include "{header}"', "#include <stdio.h>", "#include <stddef.h>", "int main(void) {"]
+    for t, fs in REF_FIELDS.items():
+        for f in fs:
+            g = names.get(f, f)
+            lines.append(f'printf("{t}.{f} %zu %zu\\n", offsetof(struct {t}, {g}), sizeof(((struct {t} *)0)->{g}));')
+    lines.append("return 0; }")
+    src = os.path.join(tmp, "fo.c")
+    open(src, "w").write("\n".join(lines))
+    exe = os.path.join(tmp, "fo")
+    cmd = ["gcc", "-D__HIP_PLATFORM_AMD__", *sum((["-I", d] for d in include_dirs), []), src, "-o", exe]
+    subprocess.run(cmd, check=True, capture_output=True)
+    out = subprocess.run([exe], capture_output=True, text=True, check=True).stdout
+    return {k: (int(a), int(b)) for k, a, b in (ln.split() for ln in out.strip().splitlines())}
+
+
+def test_internal_layouts_keep_the_reference_offsets(tmp_path):
+    """the library's RqModel / RqSeq keep, at the reference's offsets and widths, every field the reference's host
+    modules read (so its sampler.o, spec.o and chat.o run unmodified against the library): against the committed
+    table, and against the reference's own internal.h compiled here where the reference tree exists"""
+    inc = [os.path.join(ROOT, "gwenedeg_amd", "csrc"), os.path.join(ROOT, "include"), "/opt/rocm/include"]
+    if not os.path.exists("/opt/rocm/include/hip/hip_runtime_api.h"):
+        pytest.skip("ROCm headers not present")
+    ours = _field_offsets(str(tmp_path), inc, "gw_internal.h", OURS)
+    table = {f"{t}.{f}": v for t, fs in REF_FIELDS.items() for f, v in fs.items()}
+    assert ours == table
+    ref = "/root/reference/src"
+    if os.path.exists(os.path.join(ref, "internal.h")):
+        theirs = _field_offsets(str(tmp_path), [ref], "internal.h", {})
+        assert theirs == table

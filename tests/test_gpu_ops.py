@@ -133,3 +133,32 @@ def test_kq_matmul_bitexact(dev, typ, M, tile):
         gw.lib.gw_matmul_tile_rows(prev)
     got = out.cpu().numpy()
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"max diff {np.abs(got - ref).max()}"
+
+
+@pytest.mark.parametrize("typ", [12, 14])
+@pytest.mark.parametrize("K", [2560, 9728])
+@pytest.mark.parametrize("M", [9, 20, 32])
+def test_kq32_at_the_4b_widths(dev, typ, K, M):
+    """the 9..32-row K-quant GEMM (k_gemm_kq32: Q4_K, Q6_K) at the Qwen3-4B widths (K = 2560: q / k / v / gate / up,
+    K = 9728: down), 1,024 weight rows: its load pipeline in steady state (10 and 38 super-blocks per row against its
+    look-ahead of five), bit for bit against the oracle"""
+    torch, gw = dev
+    from oracle import oracle as orc
+    from gwenedeg_amd import synth
+    rng = np.random.default_rng(typ * 100 + M + K)
+    N = 1024
+    sl = synth.synth_library()
+    rb = sl.gw_synth_row_bytes(typ, K)
+    blocks = np.zeros((N, rb), np.uint8)
+    w = rng.normal(0, 0.02, size=(N, K)).astype(np.float32)
+    for r in range(N):
+        sl.gw_synth_encode_row(typ, blocks[r].ctypes.data, w[r].ctypes.data, K)
+    x = rng.normal(0, 1, size=(M, K)).astype(np.float32)
+    xq, xs = orc.quantize(x)
+    ref = orc.kq_matmul(typ, blocks, xq, xs, N, K)
+    out = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+    Bd, XQ, XS = (_to_dev(torch, a) for a in (blocks.reshape(-1), xq, xs))
+    assert gw.lib.gw_kq_matmul(out.data_ptr(), typ, Bd.data_ptr(), N, K, XQ.data_ptr(), XS.data_ptr(), M, None) == 0
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"max diff {np.abs(got - ref).max()}"
