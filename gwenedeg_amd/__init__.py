@@ -136,6 +136,7 @@ _sig = {
     "gw_matmul_tile_rows": (_I, [_I]),
     "gw_gemv_warm_next": (_I, [_I]),
     "gw_ctx_topk": (_I, [_P, _I, _I, _F, ctypes.POINTER(_I)]),
+    "gw_ctx_topk_noalloc": (_I, [_P, _I, _I, _F, ctypes.POINTER(_I)]),
     "gw_sample_topk": (_I, [_F, ctypes.POINTER(_I), _I, ctypes.c_float, ctypes.c_float, ctypes.POINTER(ctypes.c_ulonglong)]),
 }
 for _name, (_res, _args) in _sig.items():

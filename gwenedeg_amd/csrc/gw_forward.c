@@ -1071,6 +1071,24 @@ int gw_ctx_topk(RqCtx *c, int n, int k, float *vals, int *idx) {
     return RQ_OK;
 }
 
+int gw_ctx_topk_noalloc(RqCtx *c, int n, int k, float *vals, int *idx) {
+    /* gw_ctx_topk without any allocation: the candidates and the device outputs live in the device's static scratch
+     * array (gw_kernels.hip), at most GW_TOPK_NA_ROWS rows per call; calls that overlap on one device race */
+    int rows = c->last_nsel;
+    if (rows <= 0 || n < 1 || n > rows) return ctx_fail(c, RQ_ERR_STATE, "no logits rows on the device (%d)", rows);
+    if (n > GW_TOPK_NA_ROWS)
+        return ctx_fail(c, RQ_ERR_ARG, "top-k without allocation: %d rows, at most %d per call", n, GW_TOPK_NA_ROWS);
+    if (k < 1 || k > 64 || k >= c->m->vocab || !vals || !idx) return ctx_fail(c, RQ_ERR_ARG, "top-k %d", k);
+    float *vd = NULL;
+    int *id = NULL;
+    int e = gw_k_topk_noalloc(c->logits_d, c->m->vocab, c->m->vocab, n, k, &vd, &id, c->stream);
+    if (e) return ctx_hip(c, "top-k (no allocation)", (hipError_t)e);
+    HIPCHK(c, "hipMemcpyAsync (top-k)", hipMemcpyAsync(vals, vd, (size_t)n * k * 4, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, "hipMemcpyAsync (top-k)", hipMemcpyAsync(idx, id, (size_t)n * k * 4, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, "hipStreamSynchronize (top-k)", hipStreamSynchronize(c->stream));
+    return RQ_OK;
+}
+
 int gw_sample_topk(const float *vals, const int *idx, int k, float temperature, float topp, unsigned long long *rng) {
     /* sample_topk (sampler.c:186-256) from its candidates (gw_ctx_topk's row): w_j = expf((x_j - x_0) * (1 / T)),
      * S = w_0 + .. in order, the nucleus by prefix sums against topp * S, the draw r = coin * W with coin the next

@@ -235,6 +235,10 @@ int gw_k_quant_rows(const float *x, int n, int ldxf, int rows, int8_t *q, float 
 int gw_k_argmax(const float *lg, int n, int ld, int rows, int *out, void *scratch, hipStream_t s); /* scratch: rows x 512 B */
 /* the k best of each row in sample_topk's order (larger first, lower index on ties); scratch rows x 32 KiB, k <= 64 */
 int gw_k_topk(const float *lg, int n, int ld, int rows, int k, float *vals, int *idx, void *scratch, hipStream_t s);
+/* the same on the current device's static scratch array (no allocation; rows <= GW_TOPK_NA_ROWS): *vals / *idx, device
+ * pointers into that array, get the rows x k outputs */
+#define GW_TOPK_NA_ROWS 16
+int gw_k_topk_noalloc(const float *lg, int n, int ld, int rows, int k, float **vals, int **idx, hipStream_t s);
 /* GGUF Q8_0 blocks (gpr per row) -> codes + scales; il > 0: source row i to row (i / il) 2 il + off + i % il (two
  * matrices interleaved in blocks of il rows) */
 int gw_k_q8_unpack(const uint8_t *blocks, size_t nblk, int8_t *codes, uint16_t *scales, int gpr, int il, int off, hipStream_t s);

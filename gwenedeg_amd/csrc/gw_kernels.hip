@@ -815,9 +815,49 @@ __global__ __launch_bounds__(256) void k_topk_final(const float2 *__restrict__ s
     }
 }
 
+// The no-allocation top-k's scratch (gw_ctx_topk_noalloc): one array per device for the process's lifetime, holding the
+// chunk candidates of GW_TOPK_NA_ROWS rows (TOPK_CH x TOPK_KMAX (value, index) pairs each) and then the outputs (rows x
+// TOPK_KMAX values, rows x TOPK_KMAX indices). Every call on a device uses the same array and leaves its contents there;
+// nothing in it needs to start at zero (each call writes every candidate and output it reads). Calls that overlap on one
+// device race
+#define GW_NA_CAND_BYTES ((size_t)GW_TOPK_NA_ROWS * TOPK_CH * TOPK_KMAX * 8)
+#define GW_NA_BYTES (GW_NA_CAND_BYTES + (size_t)GW_TOPK_NA_ROWS * TOPK_KMAX * 8)
+static __device__ __align__(256) unsigned char scratch[GW_NA_BYTES];
+
 // ------------------------------------------------------------------------------------------ launchers
 
+#include <pthread.h>
+
 extern "C" {
+
+/* the device address of this device's scratch array (the array's name in host code is a host-side stand-in, not a
+ * device address): taken once per device with that device current, then kept */
+#define GW_NA_MAXDEV 64
+static void *na_ptr[GW_NA_MAXDEV];
+static pthread_mutex_t na_mu = PTHREAD_MUTEX_INITIALIZER;
+
+int gw_k_topk_noalloc(const float *lg, int n, int ld, int rows, int k, float **vals, int **idx, hipStream_t s) {
+    /* gw_k_topk with this device's scratch array as its candidates and outputs (*vals, *idx: where the outputs are,
+     * rows x k each, device memory); rows <= GW_TOPK_NA_ROWS. Allocates nothing */
+    if (rows < 1 || rows > GW_TOPK_NA_ROWS || !vals || !idx) return (int)hipErrorInvalidValue;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= GW_NA_MAXDEV) return (int)hipErrorInvalidDevice;
+    pthread_mutex_lock(&na_mu);
+    if (!na_ptr[dev]) {
+        void *p = NULL;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e == hipSuccess && p) na_ptr[dev] = p;
+        else if (e == hipSuccess) e = hipErrorInvalidSymbol;
+    }
+    unsigned char *base = (unsigned char *)na_ptr[dev];
+    pthread_mutex_unlock(&na_mu);
+    if (e != hipSuccess) return (int)e;
+    *vals = (float *)(base + GW_NA_CAND_BYTES);
+    *idx = (int *)(base + GW_NA_CAND_BYTES + (size_t)GW_TOPK_NA_ROWS * TOPK_KMAX * 4);
+    return gw_k_topk(lg, n, ld, rows, k, *vals, *idx, base, s);
+}
 
 int gw_k_embed_q8(float *x, int dim, const uint8_t *codes, const uint16_t *scales, const int *tok, int n, hipStream_t s) {
     GW_LAUNCH(k_embed_q8, dim3(n, (dim + 255) / 256), dim3(256), 0, s, x, dim, codes, scales, tok);

@@ -233,6 +233,11 @@ int gw_ctx_argmax(RqCtx *c, int *tokens, int n);
  * cross the bus instead of the row's logits. No counterpart in runq.h: a sampler over the candidates replaces
  * rq_sample_batch's top-k rows (engine.c:3230-3253) */
 int gw_ctx_topk(RqCtx *c, int n, int k, float *vals, int *idx);
+/* gw_ctx_topk without any allocation, for callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops that forbid hipMalloc): the same results; no counterpart in the reference. The candidates and the device
+ * outputs live in a static array of 520 KiB per device (held until the process ends), so at most 16 rows per call
+ * (n > 16: RQ_ERR_ARG); every call on a device uses the same array, so calls that overlap on one device race */
+int gw_ctx_topk_noalloc(RqCtx *c, int n, int k, float *vals, int *idx);
 /* sample_topk (sampler.c:186-256) on such a row's candidates, with temperature > 0, top-p topp (<= 0 or >= 1: off) and
  * the sequence's RNG state (rq_seq_rng, runq.h:319; advanced by one draw as rq_sample does): the same token as the
  * reference's rq_sample with cfg->top_k = k on the full row; RQ_ERR_ARG for bad arguments */
