@@ -533,10 +533,19 @@ typedef struct {
 
 static int run_mm(RqCtx *c, const GwMat *w, int nmat, const int8_t *xq, const float *xs, int ldx, int M, float *out, int ldo,
                   int mode) {
-    for (int i = 0, col = 0; i < nmat; col += w[i].rows, i++) {
-        if (i) kt_next(c, c->kt_cur); /* (the first matrix's pair is set by the class mark) */
-        if (gw_k_matmul(&w[i], xq, xs, ldx, M, out + col, ldo, mode, c->stream))
-            return ctx_fail(c, RQ_ERR_STATE, "matmul launch failed (%d x %d, type %d)", w[i].rows, w[i].cols, w[i].type);
+    /* the matrices side by side in out's columns; two neighbours of one K-quant type share a launch where the kernel
+     * allows (gw_k_matmul2) */
+    for (int i = 0, col = 0; i < nmat;) {
+        if (i) kt_next(c, c->kt_cur); /* (the first launch's pair is set by the class mark) */
+        int two = i + 1 < nmat, e = -1;
+        if (two) e = gw_k_matmul2(&w[i], &w[i + 1], w[i].rows, xq, xs, ldx, M, out + col, ldo, mode, c->stream);
+        if (e == -1) {
+            two = 0;
+            e = gw_k_matmul(&w[i], xq, xs, ldx, M, out + col, ldo, mode, c->stream);
+        }
+        if (e) return ctx_fail(c, RQ_ERR_STATE, "matmul launch failed (%d x %d, type %d)", w[i].rows, w[i].cols, w[i].type);
+        col += w[i].rows + (two ? w[i + 1].rows : 0);
+        i += two ? 2 : 1;
     }
     return RQ_OK;
 }

@@ -420,78 +420,92 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
 }
 
 // K-quant GEMM for 9 .. 32 activation rows (batched decode): one block of 512 threads per 32 weight rows, the 8 waves
-// taking the 8 groups of each super-block (wave w: group w), so the blocks are N / 32 and each wave's VALU work is one
-// group in eight. Each wave loads its MFMA operands straight from memory (X row l % 32, W row n0 + l % 32), 5
-// super-blocks ahead; per super-block: the exact int32 sums (MFMA, as k_gemm_kq), the wave's terms
-// (k_gemm_kq's expressions) into LDS, one barrier, then each thread adds the 8 terms of its 2 outputs in group order
-// (val = val + term, kquants.h:86-109, :410-554). M <= 32, K % 256 == 0, mode 1: out = out + val
+// taking the 8 groups of each super-block (wave w: group w), each wave's VALU work one group in eight. Per super-block s,
+// the block stages the 32 rows' super-blocks and the activation rows' 256 codes and 8 scales in LDS (double-buffered),
+// loaded with coalesced 16-byte loads (consecutive threads: consecutive 16 bytes of one row) SK_P super-blocks ahead;
+// each wave reads its MFMA operands (X row l % 32, W row l % 32: k_gemm_kq's layouts) from LDS: the exact int32 sums
+// (MFMA), the wave's terms (k_gemm_kq's expressions) into LDS, one barrier, then each thread adds the 8 terms of its 2
+// outputs in group order (val = val + term, kquants.h:86-109, :410-554). Two matrices of one type and width may share
+// a launch (blocks below nb1 take the first, the others the second; each writes at its own column offset of out).
+// M <= 32, K % 256 == 0, mode 1: out = out + val
 #define SK_T 512
+#define SK_P 4                      // super-blocks whose loads are in flight beyond the one computed
+#define SK_XR 272                   // LDS bytes per activation row (256 codes + 16: rows 4 banks apart)
 template <int TYPE>
-struct SkOps { // Q4_K: X 16 bytes, the group's 16 nibble bytes, the super-block header
-    uint4 x, q, hd;
-    float xs; // threads < 256: XS[m][8 s + g] for m = t / 8, g = t % 8
-};
-template <>
-struct SkOps<GW_Q6_K> { // X halves, ql halves, qh halves (8 bytes each), the group's two scale bytes (in a word), d
-    uint2 x0, x1, l0, l1, h0, h1;
-    uint32_t sc, dw;
+struct SkStage { // one thread's share of a super-block's staging: a 16-byte piece of W and of X, an activation scale
+    uint4 w, x;
     float xs;
 };
+struct SkMats { // the launch's matrices: blocks [0, nb1) the first, [nb1, grid) the second
+    const uint8_t *W[2];
+    int N[2], col[2], nb1;
+};
 template <int TYPE>
-__global__ __launch_bounds__(SK_T) void k_gemm_kq32(const uint8_t *__restrict__ W, int bstride, int N, int K,
-                                                    const int8_t *__restrict__ X, const float *__restrict__ XS, int ldx,
-                                                    int M, float *out, int ldo, int mode) {
-    __shared__ __align__(16) float Tl[8][1024]; // group g's term of output o = r * 64 + lane (r: MFMA result register)
-    __shared__ __align__(16) float xsl[2][8][32]; // the super-block's activation scales [group][m], two buffers
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6, hi = lane >> 5;
-    const int n0 = blockIdx.x * 32, S = K >> 8;
-    const int nl = n0 + (lane & 31) < N ? n0 + (lane & 31) : N - 1, ml = (lane & 31) < M ? (lane & 31) : M - 1;
-    const uint8_t *wrow = W + (size_t)nl * S * bstride;
-    const int8_t *xrow = X + (size_t)ml * ldx + 32 * w;
-    const int xm = (t >> 3) < M ? (t >> 3) : M - 1;
-    const float *xsr = XS + (size_t)xm * (ldx >> 5) + (t & 7);
-    auto load = [&](SkOps<TYPE> &o, int s) __attribute__((always_inline)) {
+__global__ __launch_bounds__(SK_T) void k_gemm_kq32(SkMats mats, int bstride, int K, const int8_t *__restrict__ X,
+                                                    const float *__restrict__ XS, int ldx, int M, float *out, int ldo,
+                                                    int mode) {
+    constexpr int WST = TYPE == GW_Q4_K ? 160 : 240;            // LDS bytes per weight row (bstride + 16)
+    constexpr int PW = TYPE == GW_Q4_K ? GW_Q4K_BYTES / 16 : GW_Q6K_DEV / 16; // 16-byte pieces per weight row
+    __shared__ __align__(16) float Tl[2][8][1024];              // group g's term of output o = r * 64 + lane
+    __shared__ __align__(16) uint8_t Ws[2][32 * WST];
+    __shared__ __align__(16) uint8_t Xs[2][32 * SK_XR];
+    __shared__ __align__(16) float xsl[2][8][32];               // [group][m]
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6, hi = lane >> 5, r32 = lane & 31;
+    const int mi = blockIdx.x >= mats.nb1;
+    const int n0 = (blockIdx.x - (mi ? mats.nb1 : 0)) * 32, N = mats.N[mi], S = K >> 8;
+    const size_t rowb = (size_t)S * bstride;
+    out += mats.col[mi];
+    // this thread's staging pieces: W row t / PW piece t % PW (t < 32 PW), X row t / 16 piece t % 16, XS (t < 256);
+    // every thread loads (the others a piece of row 31 again, never staged), so no load sits under a branch
+    const int wr = t / PW < 32 ? t / PW : 31, wp = t % PW, wn = n0 + wr < N ? n0 + wr : N - 1;
+    const uint8_t *wsrc = mats.W[mi] + (size_t)wn * rowb + 16 * wp;
+    const int xr = t >> 4, xm = xr < M ? xr : M - 1;
+    const int8_t *xsrc = X + (size_t)xm * ldx + 16 * (t & 15);
+    const int sm = (t >> 3) < M ? (t >> 3) : M - 1;
+    const float *xssrc = XS + (size_t)sm * (ldx >> 5) + (t & 7);
+    auto load = [&](int s) __attribute__((always_inline)) -> SkStage<TYPE> {
         s = s < S ? s : S - 1; // (past the last super-block: the last again)
-        const uint8_t *b = wrow + (size_t)s * bstride;
-        const int8_t *x = xrow + 256 * s;
-        if constexpr (TYPE == GW_Q4_K) {
-            o.x = *(const uint4 *)(x + 16 * hi);
-            o.q = *(const uint4 *)(b + 16 + 32 * (w >> 1) + 16 * hi);
-            o.hd = *(const uint4 *)b;
-        } else {
-            const int nn = w >> 2, p = w & 3;
-            o.x0 = *(const uint2 *)(x + 8 * hi);
-            o.x1 = *(const uint2 *)(x + 16 + 8 * hi);
-            o.l0 = *(const uint2 *)(b + 64 * nn + 32 * (p & 1) + 8 * hi);
-            o.l1 = *(const uint2 *)(b + 64 * nn + 32 * (p & 1) + 16 + 8 * hi);
-            o.h0 = *(const uint2 *)(b + 128 + 32 * nn + 8 * hi);
-            o.h1 = *(const uint2 *)(b + 128 + 32 * nn + 16 + 8 * hi);
-            o.sc = *(const uint32_t *)(b + 192 + 4 * (w >> 1));
-            o.dw = *(const uint32_t *)(b + 208);
-        }
-        o.xs = t < 256 ? xsr[8 * s] : 0.0f;
+        SkStage<TYPE> o;
+        o.w = *(const uint4 *)(wsrc + (size_t)s * bstride);
+        o.x = *(const uint4 *)(xsrc + 256 * s);
+        o.xs = xssrc[8 * s];
+        return o;
+    };
+    auto stage = [&](const SkStage<TYPE> &o, int buf) __attribute__((always_inline)) {
+        if (t < 32 * PW) *(uint4 *)(&Ws[buf][wr * WST + 16 * wp]) = o.w;
+        *(uint4 *)(&Xs[buf][xr * SK_XR + 16 * (t & 15)]) = o.x;
+        if (t < 256) xsl[buf][t & 7][t >> 3] = o.xs;
     };
     float acc0 = 0.0f, acc1 = 0.0f; // outputs t and t + 512
     const i32x16 z = { 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0 };
-    auto step = [&](const SkOps<TYPE> &c, SkOps<TYPE> &nx, int s) __attribute__((always_inline)) -> bool {
-        load(nx, s + 5);
+    const uint8_t *wrow_l = &Ws[0][r32 * WST], *xrow_l = &Xs[0][r32 * SK_XR + 32 * w];
+    auto step = [&](const SkStage<TYPE> nx, int s) __attribute__((always_inline)) -> SkStage<TYPE> {
+        // nx holds super-block s + 1: staged into the other buffer (its readers, step s - 1, are past the barrier of
+        // step s - 1); returned: the set reloaded with super-block s + 1 + SK_P (values, not references: a set passed
+        // by reference was placed in memory)
         const int buf = s & 1;
-        if (t < 256) xsl[buf][t & 7][t >> 3] = c.xs;
+        if (s + 1 < S) stage(nx, buf ^ 1);
+        const SkStage<TYPE> nl = load(s + 1 + SK_P);
+        if (s >= S) return nl; // (the last group of four steps past the end: its loads only, uniform)
+        const uint8_t *wb = wrow_l + buf * (32 * WST), *xb = xrow_l + buf * (32 * SK_XR);
         float f0, f1 = 0.0f;
         int s0 = 0, s1 = 0;
         i32x16 I, I1;
         if constexpr (TYPE == GW_Q4_K) {
+            const uint4 xq = *(const uint4 *)(xb + 16 * hi);
+            const uint4 q = *(const uint4 *)(wb + 16 + 32 * (w >> 1) + 16 * hi);
+            const uint4 hd = *(const uint4 *)wb;
             const int sh = 4 * (w & 1);
-            const i32x4 b = { (int)((c.q.x >> sh) & 0x0F0F0F0Fu), (int)((c.q.y >> sh) & 0x0F0F0F0Fu),
-                              (int)((c.q.z >> sh) & 0x0F0F0F0Fu), (int)((c.q.w >> sh) & 0x0F0F0F0Fu) };
-            const i32x4 a = { (int)c.x.x, (int)c.x.y, (int)c.x.z, (int)c.x.w };
+            const i32x4 bq = { (int)((q.x >> sh) & 0x0F0F0F0Fu), (int)((q.y >> sh) & 0x0F0F0F0Fu),
+                               (int)((q.z >> sh) & 0x0F0F0F0Fu), (int)((q.w >> sh) & 0x0F0F0F0Fu) };
+            const i32x4 a = { (int)xq.x, (int)xq.y, (int)xq.z, (int)xq.w };
             const i32x4 ones = { 0x01010101, 0x01010101, 0x01010101, 0x01010101 };
-            I = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
+            I = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, z, 0, 0, 0);
             I1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, ones, z, 0, 0, 0); // (the sums of x)
             // the scale bytes k = w, w + 4 and w - 4 (the 12 bytes in words y, z, w of the header)
             const int bs = 8 * (w & 3);
-            const int bw = (int)(((w < 4 ? c.hd.y : c.hd.z) >> bs) & 0xffu), bw4 = (int)(((w < 4 ? c.hd.z : c.hd.w) >> bs) & 0xffu);
-            const int bm4 = (int)((c.hd.y >> bs) & 0xffu);
+            const int bw = (int)(((w < 4 ? hd.y : hd.z) >> bs) & 0xffu), bw4 = (int)(((w < 4 ? hd.z : hd.w) >> bs) & 0xffu);
+            const int bm4 = (int)((hd.y >> bs) & 0xffu);
             int scj, mj;
             if (w < 4) {
                 scj = bw & 63;
@@ -500,26 +514,30 @@ __global__ __launch_bounds__(SK_T) void k_gemm_kq32(const uint8_t *__restrict__ 
                 scj = (bw4 & 15) | (bm4 >> 6) << 4;
                 mj = (bw4 >> 4) | (bw >> 6) << 4;
             }
-            f0 = h2f_g((uint16_t)(c.hd.x & 0xffffu)) * (float)scj;
-            f1 = h2f_g((uint16_t)(c.hd.x >> 16)) * (float)mj;
+            f0 = h2f_g((uint16_t)(hd.x & 0xffffu)) * (float)scj;
+            f1 = h2f_g((uint16_t)(hd.x >> 16)) * (float)mj;
         } else {
-            const int p = w & 3, sl = 4 * (p >> 1), sh = 2 * p;
+            const int nn = w >> 2, p = w & 3, sl = 4 * (p >> 1), sh = 2 * p;
+            const uint2 x0 = *(const uint2 *)(xb + 8 * hi), x1 = *(const uint2 *)(xb + 16 + 8 * hi);
+            const uint2 l0 = *(const uint2 *)(wb + 64 * nn + 32 * (p & 1) + 8 * hi);
+            const uint2 l1 = *(const uint2 *)(wb + 64 * nn + 32 * (p & 1) + 16 + 8 * hi);
+            const uint2 h0 = *(const uint2 *)(wb + 128 + 32 * nn + 8 * hi), h1 = *(const uint2 *)(wb + 128 + 32 * nn + 16 + 8 * hi);
+            const uint32_t sc = *(const uint32_t *)(wb + 192 + 4 * (w >> 1)), dw = *(const uint32_t *)(wb + 208);
             auto code = [&](uint32_t lo, uint32_t hq) -> int { // 4 codes q - 32 (q = lo nibble | 2 bits of qh << 4)
                 uint32_t q = ((lo >> sl) & 0x0F0F0F0Fu) | (((hq >> sh) & 0x03030303u) << 4);
                 uint32_t f = q ^ 0x20202020u, sg = f & 0x20202020u;
                 return (int)(f | (sg << 1) | (sg << 2));
             };
-            const i64 b0 = (i64)(uint32_t)code(c.l0.x, c.h0.x) | (i64)(uint32_t)code(c.l0.y, c.h0.y) << 32;
-            const i64 b1 = (i64)(uint32_t)code(c.l1.x, c.h1.x) | (i64)(uint32_t)code(c.l1.y, c.h1.y) << 32;
-            const i64 a0 = (i64)c.x0.x | (i64)c.x0.y << 32, a1 = (i64)c.x1.x | (i64)c.x1.y << 32;
+            const i64 b0 = (i64)(uint32_t)code(l0.x, h0.x) | (i64)(uint32_t)code(l0.y, h0.y) << 32;
+            const i64 b1 = (i64)(uint32_t)code(l1.x, h1.x) | (i64)(uint32_t)code(l1.y, h1.y) << 32;
+            const i64 a0 = (i64)x0.x | (i64)x0.y << 32, a1 = (i64)x1.x | (i64)x1.y << 32;
             I = __builtin_amdgcn_mfma_i32_32x32x16_i8(a0, b0, z, 0, 0, 0);
             I1 = __builtin_amdgcn_mfma_i32_32x32x16_i8(a1, b1, z, 0, 0, 0);
-            const uint32_t sc2 = c.sc >> (16 * (w & 1)); // (scales 2 w, 2 w + 1)
+            const uint32_t sc2 = sc >> (16 * (w & 1)); // (scales 2 w, 2 w + 1)
             s0 = (int)(int8_t)(sc2 & 0xffu);
             s1 = (int)(int8_t)((sc2 >> 8) & 0xffu);
-            f0 = h2f_g((uint16_t)(c.dw & 0xffffu));
+            f0 = h2f_g((uint16_t)(dw & 0xffffu));
         }
-        __syncthreads(); // (xsl[buf] written; the previous super-block's term readers are done)
         #pragma unroll
         for (int q = 0; q < 4; q++) {
             const float4 x4 = *(const float4 *)(&xsl[buf][w][8 * q + 4 * hi]);
@@ -536,29 +554,31 @@ __global__ __launch_bounds__(SK_T) void k_gemm_kq32(const uint8_t *__restrict__ 
                     int Ii = s0 * I[r] + s1 * I1[r];
                     term = (f0 * xsq[e]) * (float)Ii;
                 }
-                Tl[w][r * 64 + lane] = term;
+                Tl[buf][w][r * 64 + lane] = term;
             }
         }
-        __syncthreads();
+        __syncthreads(); // (the terms of super-block s written; super-block s + 1 staged)
         #pragma unroll
         for (int g = 0; g < 8; g++) {
-            acc0 = acc0 + Tl[g][t];
-            acc1 = acc1 + Tl[g][t + 512];
+            acc0 = acc0 + Tl[buf][g][t];
+            acc1 = acc1 + Tl[buf][g][t + 512];
         }
-        return s + 1 < S;
+        return nl;
     };
-    // six register sets take turns, five super-blocks' loads in flight (named: an array of them was placed in scratch
-    // memory)
-    SkOps<TYPE> o0, o1, o2, o3, o4, o5;
-    load(o0, 0);
-    load(o1, 1);
-    load(o2, 2);
-    load(o3, 3);
-    load(o4, 4);
-    for (int s0 = 0;; s0 += 6) {
-        if (!step(o0, o5, s0) || !step(o1, o0, s0 + 1) || !step(o2, o1, s0 + 2) || !step(o3, o2, s0 + 3) ||
-            !step(o4, o3, s0 + 4) || !step(o5, o4, s0 + 5))
-            break;
+    // four register sets take turns (super-block s + 1 + k in set (s + 1 + k) % 4; named: an array of them was placed
+    // in scratch memory): super-block 0 staged, set 0 reloaded with 4, then step s stages s + 1 and reloads with s + 5
+    static_assert(SK_P == 4, "four register sets");
+    SkStage<TYPE> o0 = load(0), o1 = load(1), o2 = load(2), o3 = load(3);
+    stage(o0, 0);
+    o0 = load(4);
+    __syncthreads();
+    // (one exit, at the end of each group of four: a break after each step made the compiler wait for every load in
+    // flight at the top of the loop)
+    for (int s0 = 0; s0 < S; s0 += 4) {
+        o1 = step(o1, s0);
+        o2 = step(o2, s0 + 1);
+        o3 = step(o3, s0 + 2);
+        o0 = step(o0, s0 + 3);
     }
     #pragma unroll
     for (int k = 0; k < 2; k++) {
@@ -948,6 +968,44 @@ static int gemm_cus(void) { // the device's compute units
     return cus;
 }
 
+static bool kq32_takes(const GwMat *w, int M) {
+    // K-quants, 9 .. 32 rows: the 32-row GEMM with the groups spread over a block's waves (a matrix of 32768 rows or
+    // more, the classifier: the 128-column MFMA GEMM, a block for every compute unit)
+    return (w->type == GW_Q4_K || w->type == GW_Q6_K) && M > 8 && M <= 32 && !g_tile_rows && w->rows < 32768;
+}
+
+static int launch_kq32(const GwMat *a, const GwMat *b, int col_b, const int8_t *xq, const float *xs, int ldx, int M,
+                       float *out, int ldo, int mode, hipStream_t s) {
+    // a, and b (NULL: none; same type and width as a) written from column col_b of out
+    hipEvent_t e0, e1;
+    gw_take_launch_events(&e0, &e1);
+    SkMats mt;
+    mt.W[0] = a->blocks;
+    mt.N[0] = a->rows;
+    mt.col[0] = 0;
+    mt.nb1 = (a->rows + 31) / 32;
+    mt.W[1] = b ? b->blocks : a->blocks;
+    mt.N[1] = b ? b->rows : a->rows;
+    mt.col[1] = b ? col_b : 0;
+    const dim3 grid(mt.nb1 + (b ? (b->rows + 31) / 32 : 0));
+    if (a->type == GW_Q4_K)
+        hipExtLaunchKernelGGL((k_gemm_kq32<GW_Q4_K>), grid, dim3(SK_T), 0, s, e0, e1, 0, mt, a->bstride, a->cols, xq, xs, ldx, M,
+                              out, ldo, mode);
+    else
+        hipExtLaunchKernelGGL((k_gemm_kq32<GW_Q6_K>), grid, dim3(SK_T), 0, s, e0, e1, 0, mt, a->bstride, a->cols, xq, xs, ldx, M,
+                              out, ldo, mode);
+    return (int)hipGetLastError();
+}
+
+int gw_k_matmul2(const GwMat *a, const GwMat *b, int col_b, const int8_t *xq, const float *xs, int ldx, int M, float *out,
+                 int ldo, int mode, hipStream_t s) {
+    /* a and b (b from column col_b of out) in one launch where the 9 .. 32-row K-quant GEMM takes both with one type
+     * and width; else -1 and nothing launched (the caller launches them one by one) */
+    if (kq32_takes(a, M) && kq32_takes(b, M) && a->type == b->type && a->cols == b->cols && a->bstride == b->bstride)
+        return launch_kq32(a, b, col_b, xq, xs, ldx, M, out, ldo, mode, s);
+    return -1;
+}
+
 int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int M, float *out, int ldo, int mode, hipStream_t s) {
     if (w->type == GW_Q8_0 && M > GW_GEMV_MAX_ROWS && mode == 0) {
         hipEvent_t e0, e1;
@@ -963,20 +1021,7 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
     }
     if (w->type == GW_Q8_0)
         return launch_gemv_mr<GW_Q8_0>((const uint8_t *)w->codes, w->scales, w->rows, w->cols, 0, xq, xs, ldx, M, out, ldo, mode, s);
-    // K-quants, 9 .. 32 rows: the 32-row GEMM with the groups spread over a block's waves (a matrix of 32768 rows or
-    // more, the classifier: the 128-column MFMA GEMM, a block for every compute unit)
-    if ((w->type == GW_Q4_K || w->type == GW_Q6_K) && M > 8 && M <= 32 && !g_tile_rows && w->rows < 32768) {
-        hipEvent_t e0, e1;
-        gw_take_launch_events(&e0, &e1);
-        const dim3 grid((w->rows + 31) / 32);
-        if (w->type == GW_Q4_K)
-            hipExtLaunchKernelGGL((k_gemm_kq32<GW_Q4_K>), grid, dim3(SK_T), 0, s, e0, e1, 0, (const uint8_t *)w->blocks,
-                                  w->bstride, w->rows, w->cols, xq, xs, ldx, M, out, ldo, mode);
-        else
-            hipExtLaunchKernelGGL((k_gemm_kq32<GW_Q6_K>), grid, dim3(SK_T), 0, s, e0, e1, 0, (const uint8_t *)w->blocks,
-                                  w->bstride, w->rows, w->cols, xq, xs, ldx, M, out, ldo, mode);
-        return (int)hipGetLastError();
-    }
+    if (kq32_takes(w, M)) return launch_kq32(w, NULL, 0, xq, xs, ldx, M, out, ldo, mode, s);
     // K-quants above 32 rows: the MFMA GEMM where it has 64 blocks or more (a block streams its 128 rows' full K in
     // order, so a narrow matrix leaves the device idle) or its row tile is forced, else the batched GEMV in passes of
     // 8 rows

@@ -250,7 +250,7 @@ int gw_k_fill_synthetic(uint16_t *kc, uint16_t *vc, size_t n, unsigned long long
  * R = 16), under 2 GiB. norm with swiglu_il = GW_W13_IL (R = 8, w1 / w3 interleaved): out[j] = swiglu(h_j, h2_j) */
 #define GW_GV_NBMAX 4
 #define GW_GV_R_QKV 4  /* weight rows per tile of the fused decode matmuls */
-#define GW_GV_R_WO 2
+#define GW_GV_R_WO 4
 #define GW_GV_R_W13 8
 #define GW_GV_R_W2 2
 #define GW_GV_R_CLS 8
@@ -273,6 +273,10 @@ void gw_take_launch_events(hipEvent_t *a, hipEvent_t *b);
 /* the matmul dispatch (gw_gemm.hip): out[m * ldo + row] (+)= W row . X row m for M rows, any supported type */
 int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int M, float *out, int ldo, int mode,
                 hipStream_t s);
+/* a and b (out from column col_b) in one launch where the kernel allows (two K-quant matrices of one type and width,
+ * 9 .. 32 rows); else -1, nothing launched */
+int gw_k_matmul2(const GwMat *a, const GwMat *b, int col_b, const int8_t *xq, const float *xs, int ldx, int M, float *out,
+                 int ldo, int mode, hipStream_t s);
 
 #ifdef __cplusplus
 }
