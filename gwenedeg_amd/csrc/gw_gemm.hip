@@ -76,72 +76,90 @@ template <int GM>
 __global__ __launch_bounds__(256) void k_gemm_q8(const int8_t *__restrict__ W, const uint16_t *__restrict__ WS, int N, int K,
                                                  const int8_t *__restrict__ X, const float *__restrict__ XS, int ldx, int M,
                                                  float *__restrict__ out, int ldo) {
+    // software-pipelined: the stage after the current one is loaded into registers while the current one is computed
+    // from LDS (two LDS buffers), then stored into the other buffer; one barrier per stage and one loop exit (a loop
+    // that can leave after each step makes the compiler wait for every load in flight at its top)
     constexpr int TJ = GM == 64 ? 2 : 1, XC = GM * 8 / 256; // MFMA tiles per wave, X chunks of 16 B per thread
-    __shared__ __align__(16) int8_t xl[GM * GROW];
-    __shared__ __align__(16) int8_t wl[GN * GROW];
-    __shared__ __align__(16) float xsl[4][GM];
-    __shared__ float wsl[GN][4];
+    __shared__ __align__(16) int8_t xl[2][GM * GROW];
+    __shared__ __align__(16) int8_t wl[2][GN * GROW];
+    __shared__ __align__(16) float xsl[2][4][GM];
+    __shared__ float wsl[2][GN][4];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int m0 = blockIdx.y * GM, n0 = blockIdx.x * GN, G = K >> 5;
+    const int m0 = blockIdx.y * GM, n0 = blockIdx.x * GN, G = K >> 5, NS = (K + GKB - 1) / GKB;
     const int wm = GM == 64 ? (wave >> 1) * 32 : 0, wn = GM == 64 ? (wave & 1) * 64 : wave * 32; // the wave's sub-tile
     float acc[TJ][16];
     #pragma unroll
     for (int j = 0; j < TJ; j++)
         #pragma unroll
         for (int r = 0; r < 16; r++) acc[j][r] = 0.0f;
-    for (int k0 = 0; k0 < K; k0 += GKB) {
-        const int ng = (K - k0) < GKB ? (K - k0) >> 5 : 4; // groups in this stage
-        // stage: X rows m0.. (GM x 128 B: XC chunks of 16 B per thread), W rows n0.. (GN x 128 B: 4 per thread)
-        uint4 xr[XC], wr[4];
-        #pragma unroll
-        for (int k = 0; k < XC; k++) {
-            int c = t + 256 * k, row = c >> 3, col = (c & 7) * 16, m = m0 + row < M ? m0 + row : M - 1;
-            xr[k] = col < ng * 32 ? *(const uint4 *)(X + (size_t)m * ldx + k0 + col) : make_uint4(0, 0, 0, 0);
-        }
-        #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            int c = t + 256 * k, row = c >> 3, col = (c & 7) * 16, n = n0 + row < N ? n0 + row : N - 1;
-            wr[k] = col < ng * 32 ? *(const uint4 *)(W + (size_t)n * K + k0 + col) : make_uint4(0, 0, 0, 0);
-        }
-        float xsv = 0.0f, wsv0 = 0.0f, wsv1 = 0.0f;
-        {
-            int row = t >> 2, gg = t & 3, m = m0 + row < M ? m0 + row : M - 1;
-            if (row < GM && gg < ng) xsv = XS[(size_t)m * (ldx >> 5) + (k0 >> 5) + gg];
-            int n = n0 + row < N ? n0 + row : N - 1, n2 = n0 + row + 64 < N ? n0 + row + 64 : N - 1;
-            if (gg < ng) {
-                wsv0 = h2f_g(WS[(size_t)n * G + (k0 >> 5) + gg]);
-                wsv1 = h2f_g(WS[(size_t)n2 * G + (k0 >> 5) + gg]);
-            }
-        }
-        __syncthreads(); // (the previous stage's readers are done)
-        #pragma unroll
-        for (int k = 0; k < XC; k++) {
-            int c = t + 256 * k;
-            *(uint4 *)(xl + (c >> 3) * GROW + (c & 7) * 16) = xr[k];
-        }
-        #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            int c = t + 256 * k;
-            *(uint4 *)(wl + (c >> 3) * GROW + (c & 7) * 16) = wr[k];
-        }
-        {
-            int row = t >> 2, gg = t & 3;
-            if (row < GM) xsl[gg][row] = xsv;
-            wsl[row][gg] = wsv0;
-            wsl[row + 64][gg] = wsv1;
-        }
-        __syncthreads();
+    // a stage in registers: X rows m0.. (GM x 128 B: XC chunks of 16 B per thread), W rows n0.. (GN x 128 B: 4 per
+    // thread), this thread's activation scale and two weight scales (every load unconditional: past K or the last
+    // row, clamped addresses; the values past K are zeroed when stored, not here, where it would wait for the loads)
+    const int srow = t >> 2, sgg = t & 3;
+    const int sm = m0 + srow < M ? m0 + srow : M - 1;
+    const int sn = n0 + srow < N ? n0 + srow : N - 1, sn2 = n0 + srow + 64 < N ? n0 + srow + 64 : N - 1;
+    struct St { // (named fields, passed by value: arrays captured by the lambdas were placed in scratch memory)
+        uint4 x0, x1, w0, w1, w2, w3;
+        float xs, ws0, ws1;
+    };
+    auto xptr = [&](int k, int k0, int ng) __attribute__((always_inline)) -> const uint4 * {
+        const int c = t + 256 * k, row = c >> 3, col = (c & 7) * 16, m = m0 + row < M ? m0 + row : M - 1;
+        return (const uint4 *)(X + (size_t)m * ldx + k0 + (col < ng * 32 ? col : 0));
+    };
+    auto wptr = [&](int k, int k0, int ng) __attribute__((always_inline)) -> const uint4 * {
+        const int c = t + 256 * k, row = c >> 3, col = (c & 7) * 16, n = n0 + row < N ? n0 + row : N - 1;
+        return (const uint4 *)(W + (size_t)n * K + k0 + (col < ng * 32 ? col : 0));
+    };
+    auto load = [&](int st) __attribute__((always_inline)) -> St {
+        st = st < NS ? st : NS - 1;
+        const int k0 = st * GKB, ng = (K - k0) < GKB ? (K - k0) >> 5 : 4, gq = sgg < ng ? sgg : 0;
+        St o;
+        o.x0 = *xptr(0, k0, ng);
+        o.x1 = XC > 1 ? *xptr(1, k0, ng) : o.x0;
+        o.w0 = *wptr(0, k0, ng);
+        o.w1 = *wptr(1, k0, ng);
+        o.w2 = *wptr(2, k0, ng);
+        o.w3 = *wptr(3, k0, ng);
+        o.xs = XS[(size_t)sm * (ldx >> 5) + (k0 >> 5) + gq];
+        o.ws0 = h2f_g(WS[(size_t)sn * G + (k0 >> 5) + gq]);
+        o.ws1 = h2f_g(WS[(size_t)sn2 * G + (k0 >> 5) + gq]);
+        return o;
+    };
+    auto store = [&](const St o, int buf, int st) __attribute__((always_inline)) {
+        // stage st's registers into buffer buf (codes past K and scales of missing groups: 0)
+        const int ng = (K - st * GKB) < GKB ? (K - st * GKB) >> 5 : 4;
+        const bool in = (t & 7) * 16 < ng * 32; // (c & 7 is t & 7 for every chunk c = t + 256 k)
+        // (the select per component: a ?: between two uint4 values went through scratch memory)
+        auto sel = [&](const uint4 v) __attribute__((always_inline)) -> uint4 {
+            return make_uint4(in ? v.x : 0u, in ? v.y : 0u, in ? v.z : 0u, in ? v.w : 0u);
+        };
+        const int r0 = (t >> 3) * GROW + (t & 7) * 16; // (chunk t + 256 k: row (t >> 3) + 32 k, the same column)
+        *(uint4 *)(&xl[buf][r0]) = sel(o.x0);
+        if (XC > 1) *(uint4 *)(&xl[buf][r0 + 32 * GROW]) = sel(o.x1);
+        *(uint4 *)(&wl[buf][r0]) = sel(o.w0);
+        *(uint4 *)(&wl[buf][r0 + 32 * GROW]) = sel(o.w1);
+        *(uint4 *)(&wl[buf][r0 + 64 * GROW]) = sel(o.w2);
+        *(uint4 *)(&wl[buf][r0 + 96 * GROW]) = sel(o.w3);
+        if (srow < GM) xsl[buf][sgg][srow] = sgg < ng ? o.xs : 0.0f;
+        wsl[buf][srow][sgg] = sgg < ng ? o.ws0 : 0.0f;
+        wsl[buf][srow + 64][sgg] = sgg < ng ? o.ws1 : 0.0f;
+    };
+    store(load(0), 0, 0);
+    __syncthreads();
+    for (int st = 0; st < NS; st++) {
+        const int buf = st & 1, k0 = st * GKB, ng = (K - k0) < GKB ? (K - k0) >> 5 : 4; // groups in this stage
+        const St nx = load(st + 1); // (past the last stage: the last again, never stored)
         for (int gg = 0; gg < ng; gg++) {
-            i32x4 a = *(const i32x4 *)(xl + (wm + (lane & 31)) * GROW + gg * 32 + 16 * (lane >> 5));
+            i32x4 a = *(const i32x4 *)(&xl[buf][(wm + (lane & 31)) * GROW + gg * 32 + 16 * (lane >> 5)]);
             #pragma unroll
             for (int j = 0; j < TJ; j++) {
-                i32x4 b = *(const i32x4 *)(wl + (wn + 32 * j + (lane & 31)) * GROW + gg * 32 + 16 * (lane >> 5));
+                i32x4 b = *(const i32x4 *)(&wl[buf][(wn + 32 * j + (lane & 31)) * GROW + gg * 32 + 16 * (lane >> 5)]);
                 i32x16 z = { 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0 };
                 i32x16 I = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
-                float ws = wsl[wn + 32 * j + (lane & 31)][gg];
+                float ws = wsl[buf][wn + 32 * j + (lane & 31)][gg];
                 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    float4 xs4 = *(const float4 *)(&xsl[gg][wm + 8 * q + 4 * (lane >> 5)]);
+                    float4 xs4 = *(const float4 *)(&xsl[buf][gg][wm + 8 * q + 4 * (lane >> 5)]);
                     float xsq[4] = { xs4.x, xs4.y, xs4.z, xs4.w };
                     #pragma unroll
                     for (int s = 0; s < 4; s++) {
@@ -152,6 +170,8 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const int8_t *__restrict__ W, c
                 }
             }
         }
+        if (st + 1 < NS) store(nx, buf ^ 1, st + 1); // (the other buffer's readers, stage st - 1, are past the last barrier)
+        __syncthreads();
     }
     #pragma unroll
     for (int j = 0; j < TJ; j++) {
