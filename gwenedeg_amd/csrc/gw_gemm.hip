@@ -615,8 +615,8 @@ __global__ __launch_bounds__(SK_T) void k_gemm_kq32(SkMats mats, int bstride, in
 // --------------------------------------------------------------------------------------------- K-quants
 
 // The batched GEMV of all three formats: out[m * ldo + row] (+)= W row . X row m for M <= 8 activation rows, R weight
-// rows per block. Each thread takes half-groups (16 weights) j = t, t + 256, ..., U per pass, with every load of the
-// pass issued before the first dot; the 16 weights become 16 int8 codes in four 32-bit words, the exact int32 sums by
+// rows per block. Each thread takes half-groups (16 weights) j = t, t + 256, ..., U per pass (the launcher uses U = 1),
+// with every load of the pass issued before the first dot; the 16 weights become 16 int8 codes in four 32-bit words, the exact int32 sums by
 // 4 v_dot4 per (row, activation row), and the group's term (the even lane of the pair) goes into LDS:
 //   Q8_0 (codes row-major, fp16 scales): (ws * xs) * (float) isum                                   (forward.c:906-916)
 //   Q4_K (144-byte super-blocks of 256: d, dmin, 12 bytes of 6-bit scales / mins, 128 of nibbles):
@@ -890,11 +890,10 @@ __global__ __launch_bounds__(256) void k_embed_kq(float *__restrict__ x, int dim
 template <int TYPE>
 static int launch_gemv_mr(const uint8_t *W, const uint16_t *WS, int nrows, int K, int bstride, const int8_t *xq, const float *xs,
                           int ldx, int M, float *out, int ldo, int mode, hipStream_t s) {
-    // launches of up to 8 activation rows; U = the half-groups per thread and pass (all loads of a row of K <= 16384
-    // issued at once)
-    const int R = 4, H = K / 16;
-    int U = (H + 255) / 256;
-    U = U < 1 ? 1 : U > 4 ? 4 : U;
+    // launches of up to 8 activation rows, one half-group per thread and pass (a row of K > 4096 in several passes: a
+    // pass holding a longer row's loads needed every register, one wave per SIMD, and ran the K = 12288 matrix at half
+    // the speed)
+    const int R = 4;
     hipEvent_t t0, t1; // (timing: the first launch's start, the last one's stop)
     gw_take_launch_events(&t0, &t1);
     dim3 grid((nrows + R - 1) / R);
@@ -905,25 +904,17 @@ static int launch_gemv_mr(const uint8_t *W, const uint16_t *WS, int nrows, int K
         const int8_t *x = xq + (size_t)m0 * ldx;
         const float *xsc = xs + (size_t)m0 * (ldx / 32);
         float *o = out + (size_t)m0 * ldo;
-#define MR_L(MM, UU) hipExtLaunchKernelGGL((k_gemv_mr<TYPE, MM, R, UU>), grid, dim3(256), lds, s, e0, e1, 0, W, WS, nrows, K, bstride, x, xsc, ldx, o, ldo, mode)
-#define MR_U(MM)                                                                                                        \
-    switch (U) {                                                                                                        \
-    case 1: MR_L(MM, 1); break;                                                                                         \
-    case 2: MR_L(MM, 2); break;                                                                                         \
-    case 3: MR_L(MM, 3); break;                                                                                         \
-    default: MR_L(MM, 4); break;                                                                                        \
-    }
+#define MR_L(MM) hipExtLaunchKernelGGL((k_gemv_mr<TYPE, MM, R, 1>), grid, dim3(256), lds, s, e0, e1, 0, W, WS, nrows, K, bstride, x, xsc, ldx, o, ldo, mode)
         switch (mm) {
-        case 1: MR_U(1); break;
-        case 2: MR_U(2); break;
-        case 3: MR_U(3); break;
-        case 4: MR_U(4); break;
-        case 5: MR_U(5); break;
-        case 6: MR_U(6); break;
-        case 7: MR_U(7); break;
-        default: MR_U(8); break;
+        case 1: MR_L(1); break;
+        case 2: MR_L(2); break;
+        case 3: MR_L(3); break;
+        case 4: MR_L(4); break;
+        case 5: MR_L(5); break;
+        case 6: MR_L(6); break;
+        case 7: MR_L(7); break;
+        default: MR_L(8); break;
         }
-#undef MR_U
 #undef MR_L
     }
     return (int)hipGetLastError();
