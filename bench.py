@@ -59,9 +59,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--probe", action="store_true")
-    ap.add_argument("--workload", default="step", choices=["step", "batch32_4b", "long_8b", "cb_8b"],
-                    help="step: the metric's workload (default); batch32_4b / long_8b: the batched decode of the "
-                         "reference's configs 3 / 4; cb_8b: config 5's continuous-batching steps; a JSON line of their own")
+    ap.add_argument("--workload", default="step", choices=["step", "op_q8", "batch32_4b", "long_8b", "cb_8b"],
+                    help="step: the metric's workload (default); op_q8: the isolated 12288 x 4096 Q8_0 operator of the "
+                         "reference's config 2; batch32_4b / long_8b: the batched decode of configs 3 / 4; cb_8b: config "
+                         "5's continuous-batching steps; each a JSON line of its own")
     ap.add_argument("--workdir", default=os.environ.get("GW_BENCH_DIR", "/dev/shm/gwenedeg_bench" if os.path.isdir("/dev/shm")
                                                                       else "/tmp/gwenedeg_bench"))
     a = ap.parse_args()
@@ -76,6 +77,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     if a.workload == "cb_8b":
         continuous(torch, gw, synth, a)
+        return
+    if a.workload == "op_q8":
+        op_q8(torch, gw, a)
         return
     if a.workload != "step":
         batched(torch, gw, synth, a)
@@ -202,9 +206,10 @@ def main():
     print(json.dumps(out), flush=True)
 
 
-BATCHED = {  # the reference's configs 3 and 4: shape, sequences, cached positions per sequence, timed decode steps
-    "batch32_4b": ("qwen3_4b_q4km", 32, 2048, 16),
-    "long_8b": ("qwen3_8b", 8, 32768, 8),
+BATCHED = {  # the reference's configs 3 and 4: shape, sequences, cached positions per sequence, timed decode steps,
+    # timed steps of the CPU baseline
+    "batch32_4b": ("qwen3_4b_q4km", 32, 2048, 16, 48),
+    "long_8b": ("qwen3_8b", 8, 32768, 8, 12),
 }
 
 
@@ -213,7 +218,7 @@ def batched(torch, gw, synth, a):
     prefix, whose cost does not depend on the values, runq.h:721-726), then decode passes of one row per sequence
     (gw_forward_batch_device + gw_ctx_argmax: rq_forward_batch with the greedy choice on the device). value = rows per
     second; the HBM bytes of a step = the weights' file bytes + the K / V bytes the attention reads"""
-    shape, nseq, ctx, steps = BATCHED[a.workload]
+    shape, nseq, ctx, steps, cpu_steps = BATCHED[a.workload]
     steps = a.steps if a.steps != 3 else steps
     os.makedirs(a.workdir, exist_ok=True)
     path = os.path.join(a.workdir, f"{shape}_seed{a.seed}.gguf")
@@ -263,6 +268,18 @@ def batched(torch, gw, synth, a):
                       "kv_gbs": round(kv_bytes / att_s / 1e9, 1) if att_s else None},
         "kernel_ms_per_step": {k: round(v[0] * 1e3, 3) for k, v in kt.items() if v[1]},
     }
+    if not a.no_cpu_baseline:
+        # the same shape on the reference: nseq sequences filled to ctx positions, one untimed pass, then cpu_steps
+        # timed greedy passes of one row per sequence
+        t0 = [int(t) for t in np.random.default_rng(a.seed).integers(0, m.vocab, nseq)]
+        ln = [f"seqs {nseq} {ctx + cpu_steps + 16}"] + [f"fill {i} {ctx} {a.seed + i}" for i in range(nseq)]
+        for r in range(cpu_steps + 1):
+            ln.append(f"pass {nseq}")
+            ln += [f"seg {i} {gw.RQ_LOGITS_LAST} 1 {t0[i] if r == 0 else -1}" for i in range(nseq)]
+        out["cpu_baseline"] = plan_baseline(path, "\n".join(ln) + "\n", a, ctx + cpu_steps + 16,
+                                            [[k] for k in range(1, cpu_steps + 1)], nseq,
+                                            f"{nseq} sequences x {ctx} cached positions (rq_seq_fill_synthetic), one untimed "
+                                            f"pass, then {cpu_steps} greedy passes of {nseq} one-row segments")
     print(json.dumps(out), flush=True)
 
 
@@ -270,7 +287,7 @@ def continuous(torch, gw, synth, a):
     """Config 5: continuous batching on the 8B-shaped Q8_0 model. A step is what the reference's engine runs for 48
     decoding sequences and 2 prompt chunks of 512 tokens (engine.c:3027-3255: decode rows first, then prompt chunks
     within the budget): 1,072 rows in passes of at most RQ_BATCH_MAX = 512 rows (rq_forward_batch with the greedy
-    choice on the device): [48 decode rows + 464 prompt rows], [48 + 464], [96]. The decoding sequences start at
+    choice on the device): [48 decode rows + 464 prompt rows], [48 + 464], [48]. The decoding sequences start at
     contexts uniform in [256, 8192] (rq_seq_fill_synthetic); prompts are 2,048 tokens, two prompt slots each taking a
     512-token chunk per step, and a finished prompt starts a new request: one in four begins with the 1,024-token shared
     prefix copied from the cache (rq_seq_copy) and prefills the rest. value = rows per second; per-step latency"""
@@ -364,7 +381,53 @@ def continuous(torch, gw, synth, a):
         "decode_tok_s": round(ndec * steps / el, 1), "prompt_tok_s": round(2 * chunk * steps / el, 1),
         "requests_started": nreq[0], "requests_from_shared_prefix": nshared[0],
     }
+    if not a.no_cpu_baseline:
+        out["cpu_baseline"] = cb_cpu_baseline(path, a, ctxs, ndec, chunk, prompt, prefix, m.vocab)
     print(json.dumps(out), flush=True)
+
+
+def cb_cpu_baseline(path, a, ctxs, ndec, chunk, prompt, prefix, vocab):
+    """Config 5 on the reference: three steps of the device's shape (48 decode rows at the same contexts + two 512-token
+    prompt chunks, passes of <= 512 rows); slot A continues a request started from the 1,024-token shared prefix
+    (rq_seq_copy), slot B a fresh one; when A's prompt ends (step 2) a fresh request takes its slot. Steps 2 and 3 are
+    timed (step 1 warms the host's caches and pages)"""
+    import gwenedeg_amd as gw
+    rng = np.random.default_rng(a.seed + 5)
+    S, A, B, C = ndec, ndec + 1, ndec + 2, ndec + 3  # shared prefix, the three prompt requests
+    ln = [f"seqs {ndec + 4} {8192 + 32}"] + [f"fill {i} {int(ctxs[i])} {a.seed + i}" for i in range(ndec)]
+    ln += [f"fill {S} {prefix} {a.seed + 999}", f"copy {A} {S} {prefix}"]
+    pos = {A: prefix, B: 0, C: 0}
+    slots, npass, groups = [A, B], 0, []
+    for step in range(3):
+        segs = [(i, gw.RQ_LOGITS_LAST, "1 " + (str(int(rng.integers(0, vocab))) if step == 0 else "-1")) for i in range(ndec)]
+        used, passes, cur = ndec, [], segs
+        for k, sq in enumerate(slots):
+            ids = [int(t) for t in rng.integers(0, vocab, chunk)]
+            last = pos[sq] + chunk >= prompt
+            o = 0
+            while o < chunk:
+                take = min(512 - used, chunk - o)
+                mode = gw.RQ_LOGITS_LAST if (o + take == chunk and last) else gw.RQ_LOGITS_NONE
+                cur.append((sq, mode, f"{take} " + " ".join(map(str, ids[o:o + take]))))
+                used += take
+                o += take
+                if used == 512:
+                    passes.append(cur)
+                    cur, used = [], 0
+            pos[sq] += chunk
+            if last:
+                slots[k] = C
+        if cur:
+            passes.append(cur)
+        for segs_ in passes:
+            ln.append(f"pass {len(segs_)}")
+            ln += [f"seg {i} {mode} {rest}" for i, mode, rest in segs_]
+        groups.append(list(range(npass, npass + len(passes))))
+        npass += len(passes)
+    return plan_baseline(path, "\n".join(ln) + "\n", a, 8192 + 32, groups[1:], ndec + 2 * chunk,
+                         f"config 5's step three times ({ndec} decode rows at the device's contexts + 2 x {chunk} prompt "
+                         f"rows, passes of <= 512 rows), steps 2 and 3 timed", timeout=1800)
+
 
 
 def weight_file_bytes(path):
@@ -422,25 +485,177 @@ def sampling_cost(c, k=40, reps=200, temperature=0.7, topp=0.9):
         return {"error": str(e)}
 
 
+def host_cpu():
+    """The host the CPU baseline runs on: CPU model, the physical cores of this process's CPU set (distinct (package,
+    core) pairs: the reference's threads, one per core, as its own benchmarks run it), logical CPUs, 1-minute load"""
+    cpus = sorted(os.sched_getaffinity(0))
+    cores = set()
+    for c in cpus:
+        t = f"/sys/devices/system/cpu/cpu{c}/topology/"
+        try:
+            with open(t + "physical_package_id") as f1, open(t + "core_id") as f2:
+                cores.add((f1.read().strip(), f2.read().strip()))
+        except OSError:
+            cores.add(("?", str(c)))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "physical_cores": len(cores), "logical_cpus": len(cpus),
+            "load_1min": round(os.getloadavg()[0], 2)}
+
+
+def _stats(xs):
+    xs = sorted(xs)
+    n = len(xs)
+    return xs[0], (xs[n // 2] if n % 2 else 0.5 * (xs[n // 2 - 1] + xs[n // 2]))
+
+
 def cpu_baseline(path, ids, a):
     """The reference's CPU path on the same file, prompt and step (oracle/_ref/ref_driver): the 512-token prefill and
-    the gen greedy decode steps, all host threads, best of cpu_reps runs (about 10 s of CPU work at 8B)"""
+    the gen greedy decode steps, one thread per physical core, best and median of cpu_reps runs (about 10 s of CPU
+    work at 8B)"""
     from oracle import oracle as orc
     if not os.path.exists(orc.REF_DRIVER):
         return {"value": None, "unit": "tok/s", "cores": 0, "kind": "reference",
                 "sample": "oracle/_ref/ref_driver not built (needs the reference tree at build time)"}
-    cores = len(os.sched_getaffinity(0))
+    host = host_cpu()
+    cores = host["physical_cores"]
+    log(f"cpu baseline: the reference's step on {cores} threads ...")
     t0 = time.time()
     info, _, toks, _ = orc.run_ref_driver(path, ids, os.path.join(a.workdir, "cpu"), steps=a.gen, threads=cores,
                                           cap=(a.prompt + a.gen + 255) // 256 * 256, reps=a.cpu_reps, timeout=900)
     wall = time.time() - t0
-    step_s = info["prefill_s"] + info["decode_s"]
-    return {"value": round((a.prompt + a.gen) / step_s, 3), "unit": "tok/s", "cores": cores, "kind": "reference",
-            "sample": f"the reference's CPU path (oracle/_ref/ref_driver, -Ofast AVX-512 VNNI, {cores} threads) on the same "
-                      f"GGUF and prompt: the whole step ({a.prompt}-token prefill + {a.gen} greedy decode steps), best of "
-                      f"{a.cpu_reps} runs ({wall:.0f} s wall incl. load)",
+    best, med = _stats(info["run_s"])
+    n = a.prompt + a.gen
+    return {"value": round(n / best, 3), "unit": "tok/s", "cores": info["threads"], "kind": "reference",
+            "sample": f"the reference's CPU path (oracle/_ref/ref_driver, -Ofast AVX-512 VNNI, {info['threads']} threads, one per "
+                      f"physical core) on the same GGUF and prompt: the whole step ({a.prompt}-token prefill + {a.gen} greedy "
+                      f"decode steps), best of {a.cpu_reps} runs ({wall:.0f} s wall incl. load)",
+            "median": round(n / med, 3), **host,
             "prefill_tok_s": round(info["prefill_tok_s"], 2), "decode_tok_s": round(info["decode_tok_s"], 3),
             "tokens": [int(t) for t in toks]}
+
+
+def plan_baseline(path, plan, a, cap, timed, rows, what, timeout=1500):
+    """The reference's CPU path on a script of passes (ref_driver --plan: synthetic caches by rq_seq_fill_synthetic,
+    rq_forward_batch passes with greedy feeds), one thread per physical core: `timed` lists the groups of passes
+    (indices into the run's passes) that each make one timed step of `rows` rows; value = rows / best step time"""
+    from oracle import oracle as orc
+    if not os.path.exists(orc.REF_DRIVER):
+        return {"value": None, "unit": "tok/s", "cores": 0, "kind": "reference",
+                "sample": "oracle/_ref/ref_driver not built (needs the reference tree at build time)"}
+    host = host_cpu()
+    log(f"cpu baseline: the reference on {what} ...")
+    t0 = time.time()
+    info, _, _ = orc.run_ref_plan(path, plan, os.path.join(a.workdir, "cpu_plan"), threads=host["physical_cores"], cap=cap,
+                                  timeout=timeout)
+    wall = time.time() - t0
+    steps = [sum(info["pass_s"][k] for k in g) for g in timed]
+    best, med = _stats(steps)
+    return {"value": round(rows / best, 3), "unit": "tok/s", "cores": info["threads"], "kind": "reference",
+            "sample": f"the reference's CPU path (oracle/_ref/ref_driver --plan, {info['threads']} threads, one per physical "
+                      f"core) on the same GGUF: {what}; best of {len(steps)} timed steps ({wall:.0f} s wall incl. load and "
+                      "cache fill)", "median": round(rows / med, 3), "step_ms": [round(1e3 * x, 1) for x in steps], **host}
+
+
+OP_N, OP_K, OP_COPIES = 12288, 4096, 8
+
+
+def op_q8(torch, gw, a):
+    """Config 2: the isolated Q8_0 operator, W = 12288 x 4096 (int8 codes uniform in [-127, 127], fp16 scales
+    |N(0, 1e-3)|), X = M rows of N(0, 1) quantized per 32 on the device (gw_quantize), out = M x 12288 fp32, at M = 1
+    (the decode GEMV, k_gemv1), 8 (k_gemv_mr), 64 and 512 (k_gemm_q8). OP_COPIES copies of W in device memory (428 MB,
+    more than the 256 MB memory-side cache) and each launch takes the next copy, as a model's matrices follow one
+    another. gw_q8_matmul on torch's current stream, timed with its events over reps launches after a warm-up.
+    Beside each M: the reference's q8p_gemv_rows / q8p_gemm_item on the same int8 inputs (oracle/_ref/ref_q8op), one
+    thread per physical core, OP_COPIES rotated packed copies, best and median; its output must equal the device's bit
+    for bit. value = the M = 1 GEMV's HBM GB/s (file bytes: 34 per 32 weights)"""
+    N, K = OP_N, OP_K
+    rng = np.random.default_rng(a.seed)
+    wq = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    ws16 = np.abs(rng.normal(0, 1e-3, size=(N, K // 32))).astype(np.float16)
+    W0, WS0 = torch.from_numpy(wq).cuda(), torch.from_numpy(ws16.view(np.int16)).cuda()
+    Ws = [W0] + [W0.clone() for _ in range(OP_COPIES - 1)]
+    WSs = [WS0] + [WS0.clone() for _ in range(OP_COPIES - 1)]
+    st = torch.cuda.current_stream()
+    sp = st.cuda_stream
+    w_bytes = N * K * 34 / 32
+    host = host_cpu() if not a.no_cpu_baseline else None
+    have_ref = False
+    if not a.no_cpu_baseline:
+        from oracle import oracle as orc
+        have_ref = os.path.exists(orc.REF_Q8OP)
+    per_m = []
+    for M in (1, 8, 64, 512):
+        x = torch.from_numpy(rng.normal(0, 1, size=(M, K)).astype(np.float32)).cuda()
+        xq = torch.empty((M, K), dtype=torch.int8, device="cuda")
+        xs = torch.empty((M, K // 32), dtype=torch.float32, device="cuda")
+        assert gw.lib.gw_quantize(x.data_ptr(), M, K, xq.data_ptr(), xs.data_ptr(), sp) == 0
+        out = torch.empty((M, N), dtype=torch.float32, device="cuda")
+
+        def launch(r):
+            e = gw.lib.gw_q8_matmul(out.data_ptr(), Ws[r % OP_COPIES].data_ptr(), WSs[r % OP_COPIES].data_ptr(), N, K,
+                                    xq.data_ptr(), xs.data_ptr(), M, sp)
+            assert e == 0, f"gw_q8_matmul: {e}"
+
+        reps = 256 if M <= 8 else 128 if M <= 64 else 64
+        for r in range(2 * OP_COPIES):
+            launch(r)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for r in range(reps):
+            launch(r)
+        e1.record(st)
+        torch.cuda.synchronize()
+        us = 1e3 * e0.elapsed_time(e1) / reps
+        ops = 2.0 * M * N * K
+        row = {"M": M, "us_per_op": round(us, 3), "hbm_gbs": round(w_bytes / us / 1e3, 1),
+               "hbm_frac": round(w_bytes / us / 1e3 / HBM_PEAK_GBS, 4), "tops": round(ops / us / 1e6, 2),
+               "mfma_frac": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4), "reps": reps}
+        if have_ref:
+            launch(0)  # (copy 0: the inputs written below)
+            torch.cuda.synchronize()
+            got = out.cpu().numpy()
+            wd = os.path.join(a.workdir, "op_q8")
+            ref, t = orc.run_ref_q8op(wd, wq, ws16.astype(np.float32), xq.cpu().numpy(), xs.cpu().numpy(),
+                                      reps=max(8, min(200, int(2e4 / (M + 8)))), threads=host["physical_cores"],
+                                      copies=OP_COPIES)
+            row["bit_exact_vs_reference"] = bool(np.array_equal(got.view(np.uint32), ref.view(np.uint32)))
+            row["cpu"] = {"best_us": round(1e6 * t["best_s"], 1), "median_us": round(1e6 * t["median_s"], 1),
+                          "threads": t["threads"], "reps": t["reps"], "copies": t["copies"],
+                          "hbm_gbs_equiv": round(w_bytes / t["best_s"] / 1e9, 1), "tops": round(ops / t["best_s"] / 1e12, 3)}
+            row["speedup_vs_cpu_best"] = round(1e6 * t["best_s"] / us, 1)
+        per_m.append(row)
+        log(f"op_q8 M={M}: {row}")
+    m1, m512 = per_m[0], per_m[-1]
+    out = {
+        "metric": "isolated Q8_0 matmul 12288 x 4096 (the reference's config 2, 1 GPU): M = 1 GEMV HBM GB/s",
+        "value": m1["hbm_gbs"], "unit": "GB/s", "n_gpus": 1, "steps": m1["reps"], "warmup": 2 * OP_COPIES,
+        "ms_per_step": round(m1["us_per_op"] / 1e3, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 x int8 -> int32, fp32 fold (Q8_0)",
+        "data": "synthetic: int8 codes uniform in [-127, 127], fp16 scales |N(0, 1e-3)|, X ~ N(0, 1) quantized per 32",
+        "config": {"workload": f"Q8_0 W {N} x {K} ({OP_COPIES} rotated copies), M = 1, 8, 64, 512", "global_batch": 1,
+                   "seq_len": 1},
+        "roofline": {"bound": "hbm", "kernel": "k_gemv1 (M = 1)", "achieved": m1["hbm_gbs"], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": m1["hbm_frac"], "traffic": None,
+                     "algorithmic_bytes_per_launch": w_bytes},
+        "roofline_gemm": {"bound": "mfma", "kernel": "k_gemm_q8 (M = 512)", "achieved": m512["tops"], "peak": INT8_PEAK_TOPS,
+                          "unit": "TOP/s", "frac": m512["mfma_frac"], "fold_bound_tops": round(FOLD_BOUND_TOPS, 1)},
+        "per_m": per_m,
+    }
+    if have_ref:
+        out["cpu_baseline"] = {"value": m1["cpu"]["hbm_gbs_equiv"], "unit": "GB/s", "cores": m1["cpu"]["threads"],
+                               "kind": "reference",
+                               "sample": f"the reference's q8p_gemv_rows (M = 1) / q8p_gemm_item (oracle/_ref/ref_q8op) on the "
+                                         f"same int8 inputs, {m1['cpu']['threads']} threads, {OP_COPIES} rotated packed copies "
+                                         "of W; per M in per_m[].cpu", **host}
+    print(json.dumps(out), flush=True)
 
 
 if __name__ == "__main__":

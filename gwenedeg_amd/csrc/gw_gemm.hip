@@ -1083,6 +1083,9 @@ int gw_q8_matmul(float *out, const int8_t *codes, const uint16_t *scales, int N,
                  int M, void *stream) {
     if (N <= 0 || K <= 0 || M <= 0 || N % 16 || K % 32 || !out || !codes || !scales || !xq || !xs) return RQ_ERR_ARG;
     GwMat w = { GW_Q8_0, N, K, (int8_t *)codes, (uint16_t *)scales, NULL };
+    // one row: the decode GEMV (k_gemv1, as a decode step runs it: 8-row tiles, 2 above K = 4096) where it takes K
+    if (M == 1 && K % 64 == 0 && K <= 12288 && (size_t)N * K < ((size_t)1 << 31))
+        return gw_k_gemv1_q(&w, K <= 4096 ? 8 : 2, xq, xs, out, 0, NULL, 0, (hipStream_t)stream) ? RQ_ERR_STATE : RQ_OK;
     return gw_k_matmul(&w, xq, xs, K, M, out, N, 0, (hipStream_t)stream) ? RQ_ERR_STATE : RQ_OK;
 }
 

@@ -240,15 +240,16 @@ def run_ref_plan(model: str, plan: str, workdir: str, threads: int = 0, cap: int
     return info, lg, toks
 
 
-def run_ref_q8op(workdir: str, wq, ws, xq, xs, reps: int = 0, threads: int = 1, timeout: float = 600):
-    """The reference's q8p_gemv_rows / q8p_gemm_item on given int8 inputs: returns (out M x N, timing JSON or None)."""
+def run_ref_q8op(workdir: str, wq, ws, xq, xs, reps: int = 0, threads: int = 1, copies: int = 1, timeout: float = 600):
+    """The reference's q8p_gemv_rows / q8p_gemm_item on given int8 inputs: returns (out M x N, timing JSON or None;
+    timed runs rotate over `copies` packed copies of W)."""
     os.makedirs(workdir, exist_ok=True)
     N, K = wq.shape
     M = xq.shape[0]
     paths = [os.path.join(workdir, n) for n in ("w.bin", "ws.bin", "x.bin", "xs.bin", "out.bin")]
     for a, p in zip((wq, ws, xq, xs), paths):
         np.ascontiguousarray(a).tofile(p)
-    cmd = [REF_Q8OP, "q8", *paths[:4], str(M), str(N), str(K), paths[4], str(reps), str(threads)]
+    cmd = [REF_Q8OP, "q8", *paths[:4], str(M), str(N), str(K), paths[4], str(reps), str(threads), str(copies)]
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)
     if r.returncode != 0:
         raise RuntimeError(f"ref_q8op failed: {r.stderr[-2000:]}")

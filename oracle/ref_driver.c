@@ -5,7 +5,8 @@
  *   prefill of the ids in a file (rq_prefill, chunks of max_batch rows), then greedy decode steps (rq_decode +
  *   rq_sample at temperature 0: sampler.c:40-60's first maximum), optionally writing every logits row it
  *   produced (float32), the generated tokens (int32) and the KV cache of the sequence (rq_seq_save's file:
- *   the blocks "as in memory", seqfile.c:8-27), and timing each phase (best of --reps runs).
+ *   the blocks "as in memory", seqfile.c:8-27), and timing each phase (best of --reps runs; run_s: every run's
+ *   prefill + decode wall time).
  *   --batch-decode N: N independent sequences, each prefilled with the same prompt, then --steps batched decode
  *   passes of one row per sequence (rq_forward_batch, RQ_LOGITS_LAST each: batch_decode_worker).
  *   --hidden FILE: instead, the prompt token by token through rq_decode_hidden (runq.h:350), every row's logits and
@@ -47,20 +48,23 @@ static void write_all(FILE *f, const void *p, size_t n) {
  *   seqs N CAP              N sequences of capacity CAP (the --kv-type cache)
  *   load I PATH             rq_seq_load of the whole saved sequence PATH into sequence I (rq_seq_file_info's length)
  *   copy I J N              rq_seq_copy: sequence I := the first N positions of sequence J
+ *   fill I N SEED           rq_seq_fill_synthetic: sequence I := N cached positions of synthetic K / V (runq.h:726)
  *   pass NSEG               one rq_forward_batch of the NSEG segments on the next NSEG lines:
  *   seg I MODE N T1 .. TN   N tokens for sequence I, RQ_LOGITS_* MODE; a token -1 is the first maximum of the last
  *                           logits row this run produced for sequence I (the greedy feed, sampler.c:40-60)
- * Every selected logits row goes to --logits in pass order, every token a -1 stood for to --tokens. */
+ * Every selected logits row goes to --logits in pass order, every token a -1 stood for to --tokens; the JSON line
+ * lists each pass's rq_forward_batch wall time (pass_s). */
 static int run_plan(RqModel *m, RqCtx *c, int V, int kv_type, const char *plan, FILE *lf, FILE *tf) {
     FILE *f = fopen(plan, "r");
     if (!f) { perror(plan); return 1; }
     char cmd[32], path[4096];
-    int ns = 0, e, passes = 0, rows = 0;
+    int ns = 0, e, passes = 0, rows = 0, tcap = 64;
     RqSeq **sq = NULL;
+    double *pass_s = malloc((size_t)tcap * sizeof(double));
     float *out = malloc((size_t)RQ_BATCH_MAX * V * sizeof(float)), **last = NULL;
     RqSegment *sg = malloc((size_t)RQ_BATCH_MAX * sizeof(RqSegment));
     int *sgi = malloc((size_t)RQ_BATCH_MAX * sizeof(int)); /* each segment's sequence index */
-    if (!out || !sg || !sgi) { perror("malloc"); return 1; }
+    if (!out || !sg || !sgi || !pass_s) { perror("malloc"); return 1; }
     while (fscanf(f, "%31s", cmd) == 1) {
         if (!strcmp(cmd, "seqs")) {
             int cap;
@@ -84,6 +88,11 @@ static int run_plan(RqModel *m, RqCtx *c, int V, int kv_type, const char *plan, 
                 return 1;
             }
             if ((e = rq_seq_copy(sq[i], sq[j], n)) != RQ_OK) die("rq_seq_copy", e, NULL);
+        } else if (!strcmp(cmd, "fill")) {
+            int i, n;
+            unsigned long long seed;
+            if (fscanf(f, "%d %d %llu", &i, &n, &seed) != 3 || i < 0 || i >= ns) { fprintf(stderr, "plan: bad fill\n"); return 1; }
+            if ((e = rq_seq_fill_synthetic(sq[i], n, seed)) != RQ_OK) die("rq_seq_fill_synthetic", e, NULL);
         } else if (!strcmp(cmd, "pass")) {
             int nseg, nt = 0;
             if (fscanf(f, "%d", &nseg) != 1 || nseg < 1 || nseg > RQ_BATCH_MAX) { fprintf(stderr, "plan: bad pass\n"); return 1; }
@@ -111,7 +120,10 @@ static int run_plan(RqModel *m, RqCtx *c, int V, int kv_type, const char *plan, 
                 nt += n;
                 nsel += mode == RQ_LOGITS_ALL ? n : mode == RQ_LOGITS_LAST;
             }
+            double t0 = rq_now();
             if ((e = rq_forward_batch(c, sg, nseg, nsel ? out : NULL, NULL)) != RQ_OK) die("rq_forward_batch", e, c);
+            if (passes == tcap && !(pass_s = realloc(pass_s, (size_t)(tcap *= 2) * sizeof(double)))) { perror("realloc"); return 1; }
+            pass_s[passes] = rq_now() - t0;
             write_all(lf, out, (size_t)nsel * V * sizeof(float));
             for (int k = 0, r = 0; k < nseg; k++) { /* each sequence's last row of this pass, for a later greedy feed */
                 int i = sgi[k], sel = sg[k].logits == RQ_LOGITS_ALL ? sg[k].n : sg[k].logits == RQ_LOGITS_LAST;
@@ -130,12 +142,14 @@ static int run_plan(RqModel *m, RqCtx *c, int V, int kv_type, const char *plan, 
         }
     }
     fclose(f);
-    printf("{\"threads\": %d, \"vocab\": %d, \"passes\": %d, \"rows\": %d}\n", rq_threads(), V, passes, rows);
+    printf("{\"threads\": %d, \"vocab\": %d, \"passes\": %d, \"rows\": %d, \"pass_s\": [", rq_threads(), V, passes, rows);
+    for (int i = 0; i < passes; i++) printf("%s%.6f", i ? ", " : "", pass_s[i]);
+    printf("]}\n");
     for (int i = 0; i < ns; i++) {
         rq_seq_free(sq[i]);
         free(last[i]);
     }
-    free(sq); free(last); free(out); free(sg); free(sgi);
+    free(sq); free(last); free(out); free(sg); free(sgi); free(pass_s);
     return 0;
 }
 
@@ -202,7 +216,7 @@ int main(int argc, char **argv) {
     int *tok = malloc((size_t)ns * sizeof(int));
     RqSegment *sg = malloc((size_t)ns * sizeof(RqSegment));
     RqSampling smp = { 0 };
-    double tp_best = 1e30, td_best = 1e30;
+    double tp_best = 1e30, td_best = 1e30, *run_s = malloc((size_t)(reps > 0 ? reps : 1) * sizeof(double));
     for (int r = 0; r < reps; r++) {
         int last = r == reps - 1; /* outputs of the last run only */
         for (int i = 0; i < ns; i++) rq_seq_reset(sq[i]);
@@ -247,14 +261,18 @@ int main(int argc, char **argv) {
         double t2 = rq_now();
         tp_best = t1 - t0 < tp_best ? t1 - t0 : tp_best;
         td_best = t2 - t1 < td_best ? t2 - t1 : td_best;
+        run_s[r] = t2 - t0;
     }
     if (kv_path && (e = rq_seq_save(sq[0], kv_path)) != RQ_OK) die("rq_seq_save", e, NULL);
     if (lf) fclose(lf);
     if (tf) fclose(tf);
     printf("{\"threads\": %d, \"vocab\": %d, \"prompt\": %d, \"seqs\": %d, \"steps\": %d, \"prefill_s\": %.6f, "
-           "\"decode_s\": %.6f, \"prefill_tok_s\": %.3f, \"decode_tok_s\": %.3f, \"fingerprint\": \"%016llx\"}\n",
+           "\"decode_s\": %.6f, \"prefill_tok_s\": %.3f, \"decode_tok_s\": %.3f, \"fingerprint\": \"%016llx\", \"run_s\": [",
            rq_threads(), V, n, ns, steps, tp_best, td_best, tp_best > 0 ? (double)n * ns / tp_best : 0.0,
            td_best > 0 && steps ? (double)steps * ns / td_best : 0.0, (unsigned long long)info.fingerprint);
+    for (int r = 0; r < reps; r++) printf("%s%.6f", r ? ", " : "", run_s[r]);
+    printf("]}\n");
+    free(run_s);
     for (int i = 0; i < ns; i++) rq_seq_free(sq[i]);
     rq_ctx_free(c);
     rq_model_free(m);

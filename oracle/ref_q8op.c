@@ -2,11 +2,13 @@
  * against the reference's kernels_avx512.h / kquants.h where they lie, into oracle/_ref/ref_q8op; never part of
  * the product). Pins the oracle's matmul fold to the reference's code bit for bit, and times the isolated Q8_0
  * op on the host cores as the CPU baseline.
- *   ref_q8op q8 W WS X XS M N K OUT [reps threads]
+ *   ref_q8op q8 W WS X XS M N K OUT [reps threads copies]
  *       W: N x K int8 codes, WS: N x K/32 fp32 weight scales (q8_from_blocks, model.c:47-59), X: M x K int8,
  *       XS: M x K/32 fp32 activation scales. Packs W (q8p_pack_blocks, kernels_avx512.h:113), then M = 1:
  *       q8p_gemv_rows (:286), M > 1: q8p_gemm_item (:235) over every (32-row tile, chunk) item; OUT: M x N fp32.
- *       reps > 0: also times reps runs on `threads` threads (items split evenly), prints JSON seconds per run.
+ *       reps > 0: also times reps runs on `threads` threads (items split evenly), prints JSON seconds per run (best,
+ *       mean, median); run r reads packed copy r % copies of W (copies > 1: more weight bytes than the host's caches
+ *       hold, as a model's matrices follow one another).
  *   ref_q8op kq TYPE BLK X XS M N K OUT
  *       BLK: N rows of K / 256 GGUF K-quant blocks (TYPE 11 Q3_K, 12 Q4_K, 13 Q5_K, 14 Q6_K), packed by kq_pack_blocks
  *       (kquants.h:253) and multiplied by the generic kq_dot (:608) with kq_act_prep's xf (:392).
@@ -59,7 +61,7 @@ static void *part_thread(void *a) { run_part(a); return NULL; }
 int main(int argc, char **argv) {
     if (argc >= 10 && !strcmp(argv[1], "q8")) {
         int M = atoi(argv[6]), N = atoi(argv[7]), K = atoi(argv[8]);
-        int reps = argc > 10 ? atoi(argv[10]) : 0, nt = argc > 11 ? atoi(argv[11]) : 1;
+        int reps = argc > 10 ? atoi(argv[10]) : 0, nt = argc > 11 ? atoi(argv[11]) : 1, ncp = argc > 12 ? atoi(argv[12]) : 1;
         if (M < 1 || N % 32 || K % 32) { fprintf(stderr, "ref_q8op: bad shape\n"); return 2; }
         int8_t *W = slurp(argv[2], (size_t)N * K), *X = slurp(argv[4], (size_t)M * K);
         float *WS = slurp(argv[3], (size_t)N * (K / 32) * 4), *XS = slurp(argv[5], (size_t)M * (K / 32) * 4);
@@ -79,13 +81,23 @@ int main(int argc, char **argv) {
         if (reps > 0) {
             if (nt < 1) nt = 1;
             if (nt > 256) nt = 256;
+            if (ncp < 1) ncp = 1;
+            if (ncp > 64) ncp = 64;
+            const size_t pb = q8p_size(N, K, 32);
+            uint8_t **cp = malloc((size_t)ncp * sizeof(uint8_t *));
+            cp[0] = wp;
+            for (int i = 1; i < ncp; i++) {
+                if (!(cp[i] = aligned_alloc(64, (pb + 63) / 64 * 64))) { perror("copies"); return 1; }
+                memcpy(cp[i], wp, pb);
+            }
             Part *pp = malloc((size_t)nt * sizeof(Part));
             pthread_t *th = malloc((size_t)nt * sizeof(pthread_t));
-            double best = 1e30, tot = 0;
+            double best = 1e30, tot = 0, *ts = malloc((size_t)reps * sizeof(double));
             for (int r = 0; r < reps; r++) {
                 double t0 = now();
                 for (int i = 0; i < nt; i++) {
                     pp[i] = one;
+                    pp[i].wp = cp[r % ncp];
                     pp[i].it0 = (int)((long)nitems * i / nt);
                     pp[i].it1 = (int)((long)nitems * (i + 1) / nt);
                     pthread_create(&th[i], NULL, part_thread, &pp[i]);
@@ -94,9 +106,17 @@ int main(int argc, char **argv) {
                 double t = now() - t0;
                 best = t < best ? t : best;
                 tot += t;
+                ts[r] = t;
             }
-            printf("{\"op\": \"q8\", \"M\": %d, \"N\": %d, \"K\": %d, \"threads\": %d, \"reps\": %d, \"best_s\": %.9f, \"mean_s\": %.9f}\n",
-                   M, N, K, nt, reps, best, tot / reps);
+            for (int i = 1; i < reps; i++) /* (insertion sort: the median) */
+                for (int j = i; j > 0 && ts[j - 1] > ts[j]; j--) {
+                    double x = ts[j];
+                    ts[j] = ts[j - 1];
+                    ts[j - 1] = x;
+                }
+            const double med = reps % 2 ? ts[reps / 2] : 0.5 * (ts[reps / 2 - 1] + ts[reps / 2]);
+            printf("{\"op\": \"q8\", \"M\": %d, \"N\": %d, \"K\": %d, \"threads\": %d, \"reps\": %d, \"copies\": %d, "
+                   "\"best_s\": %.9f, \"mean_s\": %.9f, \"median_s\": %.9f}\n", M, N, K, nt, reps, ncp, best, tot / reps, med);
         }
         return 0;
     }
