@@ -199,12 +199,13 @@ static void dfree(void *p) { if (p) hipFree(p); }
 void rq_ctx_free(RqCtx *c) {
     if (!c) return;
     void *d[] = { c->x, c->xb, c->qkv, c->hb, c->part, c->logits_d, c->hid_d, c->xq, c->hq, c->xs, c->hs, c->argmax_d, c->argmax_scr, c->meta_d,
-                  c->gtok_d, c->gpos_d, c->topk_scr, c->topk_v, c->topk_i };
+                  c->gtok_d, c->gpos_d, c->topk_scr };
     for (size_t i = 0; i < sizeof d / sizeof d[0]; i++) dfree(d[i]);
     if (c->meta_h) hipHostFree(c->meta_h);
     if (c->logits) hipHostFree(c->logits);
     if (c->lg_h) hipHostFree(c->lg_h);
     if (c->g_h) hipHostFree(c->g_h);
+    if (c->topk_h) hipHostFree(c->topk_h);
     if (c->ev) {
         for (int i = 0; i < 2048; i++)
             if (c->ev[i]) hipEventDestroy(c->ev[i]);
@@ -1063,20 +1064,27 @@ int gw_ctx_topk(RqCtx *c, int n, int k, float *vals, int *idx) {
     int rows = c->last_nsel;
     if (rows <= 0 || n < 1 || n > rows) return ctx_fail(c, RQ_ERR_STATE, "no logits rows on the device (%d)", rows);
     if (k < 1 || k > 64 || k >= c->m->vocab || !vals || !idx) return ctx_fail(c, RQ_ERR_ARG, "top-k %d", k);
-    {   /* each buffer on first use, for the context's rows (one for a context of max_batch 0 or 1, whose decode leaves
-         * one row); one that failed before is tried again, never launched on as null */
-        const size_t B = c->nb_max > 1 ? (size_t)c->nb_max : 1;
-        size_t sb = B * 64 * 64 * 8, ob = B * 64 * 4;
-        if ((!c->topk_scr && hipMalloc(&c->topk_scr, sb) != hipSuccess) ||
-            (!c->topk_v && hipMalloc((void **)&c->topk_v, ob) != hipSuccess) ||
-            (!c->topk_i && hipMalloc((void **)&c->topk_i, ob) != hipSuccess))
-            return ctx_fail(c, RQ_ERR_NOMEM, "top-k scratch");
+    /* each buffer on first use, for the context's rows (one for a context of max_batch 0 or 1, whose decode leaves one
+     * row); one that failed before is tried again, never launched on as null. The outputs: pinned host memory mapped
+     * for the device, written by the selection kernel itself (no copy after it) */
+    const size_t B = c->nb_max > 1 ? (size_t)c->nb_max : 1, ob = B * 64 * 4;
+    if (!c->topk_scr && hipMalloc(&c->topk_scr, B * 64 * 64 * 8) != hipSuccess) return ctx_fail(c, RQ_ERR_NOMEM, "top-k scratch");
+    if (!c->topk_h) {
+        void *h = NULL, *d = NULL;
+        if (hipHostMalloc(&h, 2 * ob, hipHostMallocMapped) != hipSuccess) return ctx_fail(c, RQ_ERR_NOMEM, "top-k outputs");
+        if (hipHostGetDevicePointer(&d, h, 0) != hipSuccess || !d) {
+            hipHostFree(h);
+            return ctx_fail(c, RQ_ERR_STATE, "top-k outputs: no device address");
+        }
+        c->topk_h = h;
+        c->topk_v = (float *)d;
+        c->topk_i = (int *)((char *)d + ob);
     }
     if (gw_k_topk(c->logits_d, c->m->vocab, c->m->vocab, n, k, c->topk_v, c->topk_i, c->topk_scr, c->stream))
         return ctx_fail(c, RQ_ERR_STATE, "top-k launch failed");
-    HIPCHK(c, "hipMemcpyAsync (top-k)", hipMemcpyAsync(vals, c->topk_v, (size_t)n * k * 4, hipMemcpyDeviceToHost, c->stream));
-    HIPCHK(c, "hipMemcpyAsync (top-k)", hipMemcpyAsync(idx, c->topk_i, (size_t)n * k * 4, hipMemcpyDeviceToHost, c->stream));
     HIPCHK(c, "hipStreamSynchronize (top-k)", hipStreamSynchronize(c->stream));
+    memcpy(vals, c->topk_h, (size_t)n * k * 4);
+    memcpy(idx, (char *)c->topk_h + ob, (size_t)n * k * 4);
     return RQ_OK;
 }
 

@@ -157,8 +157,10 @@ struct RqCtx {
     float *xs, *hs;
     int *argmax_d;
     void *argmax_scr;
-    void *topk_scr; /* gw_ctx_topk's scratch (allocated at its first call): nb_max x 64 x 64 (value, index) pairs */
-    float *topk_v;  /* ... and its device outputs, nb_max x 64 each */
+    void *topk_scr; /* gw_ctx_topk's scratch (allocated at its first call): nb_max x 64 x 64 keys */
+    void *topk_h;   /* ... and its outputs, in pinned host memory the selection kernel writes directly: nb_max x 64
+                     * values, then nb_max x 64 indices */
+    float *topk_v;  /* (the device addresses of those two) */
     int *topk_i;
     int kmax, ldqkv, pstride;
     size_t part_bytes;

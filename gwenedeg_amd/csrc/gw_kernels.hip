@@ -736,90 +736,182 @@ __global__ __launch_bounds__(64) void k_argmax_final(const float2 *__restrict__ 
 }
 
 // Top-k candidates of each row, in sample_topk's order (sampler.c:186-217): the k largest values, the lower index
-// first on ties, larger first. Two steps, each a selection by repeated "best element after the previous one" (the
-// order is total, so nothing is marked: an element is eligible iff it comes after the last one taken), one block
-// reduction per pick: per chunk of TOPK_CH of a row its k best into scratch, then per row the k best of those.
-// Empty picks are (-inf, INT_MAX), after every real element. k <= TOPK_KMAX
+// first on ties, larger first. Every element gets a 64-bit key, unique within its row, whose order is that order:
+//   (ordered bits of the value: -0 as +0, NaN below -inf) << 32 | (2^32 - 1 - index)
+// Step 1, per chunk of TOPK_CH of a row: the chunk's k largest keys by radix select (8-bit digits from the top, a
+// 256-bin LDS histogram per digit, stopping at the first digit whose bin holds exactly the keys still needed; at most
+// 8 digits, usually 2 or 3), sorted by one wave (a bitonic network over its 64 lanes) into scratch: 64 keys per chunk,
+// 0 after the chunk's own. Step 2, per row: the 64 largest of the 64 sorted lists by a merge tree (the larger half of
+// two sorted lists: lane l's max of a_l and b_(63 - l), a bitonic sequence, sorted by 6 exchange steps); the first k
+// are the row's candidates, their values read back from the row. k <= TOPK_KMAX
 #define TOPK_CH 64
 #define TOPK_KMAX 64
-__device__ __forceinline__ bool tk_before(float a, int ia, float b, int ib) { return a > b || (a == b && ia < ib); }
+
+__device__ __forceinline__ uint64_t tk_key(float v, int i) {
+    uint32_t b = __float_as_uint(v), key;
+    if ((b & 0x7fffffffu) > 0x7f800000u) key = 0u; // NaN: after every number
+    else {
+        if (b == 0x80000000u) b = 0u;               // -0 ties +0 (sample_topk compares the values)
+        key = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    }
+    return ((uint64_t)key << 32) | (uint64_t)(~(uint32_t)i);
+}
+
+__device__ __forceinline__ uint64_t tk_shfl(uint64_t x, int src) {
+    const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)x, src), hi = (uint32_t)__shfl((int)(uint32_t)(x >> 32), src);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t tk_shfl_xor(uint64_t x, int m) {
+    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)x, m), hi = (uint32_t)__shfl_xor((int)(uint32_t)(x >> 32), m);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t tk_bitonic_desc(uint64_t x, int l) {
+    // a bitonic sequence over the wave's 64 lanes, sorted descending (lane 0 the largest)
+    #pragma unroll
+    for (int st = 32; st > 0; st >>= 1) {
+        const uint64_t y = tk_shfl_xor(x, st);
+        x = ((l & st) == 0) == (x > y) ? x : y;
+    }
+    return x;
+}
+
+__device__ __forceinline__ uint64_t tk_sort_desc(uint64_t x, int l) {
+    // any 64 keys over the wave's lanes, sorted descending
+    #pragma unroll
+    for (int size = 2; size <= 64; size <<= 1)
+        #pragma unroll
+        for (int st = size >> 1; st > 0; st >>= 1) {
+            const uint64_t y = tk_shfl_xor(x, st);
+            const bool keep_max = ((l & size) == 0) == ((l & st) == 0);
+            x = keep_max == (x > y) ? x : y;
+        }
+    return x;
+}
+
+__device__ __forceinline__ uint64_t tk_max(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint64_t tk_merge(uint64_t a, uint64_t b, int l) {
+    // the 64 largest of two descending lists (lane l: a_l, b_l), descending
+    return tk_bitonic_desc(tk_max(a, tk_shfl(b, 63 - l)), l);
+}
 
 template <int L>
-__device__ void tk_select(const float (&v)[L], const int (&ix)[L], int k, float2 *out) {
-    // the block's k best of its threads' L values each (index -1: none) into out[0 .. k): (value, index as float bits)
-    __shared__ float rv[4];
-    __shared__ int ri[4];
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    float pv = __builtin_inff();
-    int pi = -1; // (the previous pick: every element comes after (+inf, -1))
-    for (int it = 0; it < k; it++) {
-        float bv = -__builtin_inff();
-        int bi = 0x7fffffff;
+__device__ __forceinline__ void tk_radix(const uint64_t (&c)[L], int need, uint64_t &P, int &shift, int (*hist)[256], int *sh) {
+    // the block's `need` largest keys (0: no element; at least `need` others, 256 threads): on return every thread
+    // holds P and shift such that exactly the `need` keys c != 0 with (c >> shift) >= P are those. Two histograms in
+    // turn: a digit's counts go into one while the next one is cleared
+    const int t = threadIdx.x, l = t & 63;
+    uint64_t pre = 0;
+    int p = 0;
+    hist[0][t] = 0;
+    __syncthreads();
+    for (int sft = 56;; sft -= 8, p ^= 1) {
         #pragma unroll
         for (int u = 0; u < L; u++)
-            if (ix[u] >= 0 && tk_before(pv, pi, v[u], ix[u]) && tk_before(v[u], ix[u], bv, bi)) bv = v[u], bi = ix[u];
-        for (int o = 32; o >= 1; o >>= 1) {
-            float ov = __shfl_xor(bv, o);
-            int oi = __shfl_xor(bi, o);
-            if (tk_before(ov, oi, bv, bi)) bv = ov, bi = oi;
+            if (c[u] && (sft == 56 || (c[u] >> (sft + 8)) == pre)) atomicAdd(&hist[p][(int)(c[u] >> sft) & 255], 1);
+        hist[p ^ 1][t] = 0;
+        __syncthreads();
+        if (t < 64) { // lane l: bins 255 - 4 l down to 252 - 4 l; the bin where the count from the top reaches need
+            const int *hp = hist[p];
+            const int b0 = 255 - 4 * l, h0 = hp[b0], h1 = hp[b0 - 1], h2 = hp[b0 - 2], h3 = hp[b0 - 3];
+            const int own = h0 + h1 + h2 + h3;
+            int inc = own;
+            #pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int y = __shfl_up(inc, o);
+                if (l >= o) inc += y;
+            }
+            const int ex = inc - own;
+            if (ex < need && need <= inc) {
+                int cum = ex, d = b0, h = h0;
+                if (cum + h0 < need) {
+                    cum += h0, d = b0 - 1, h = h1;
+                    if (cum + h1 < need) {
+                        cum += h1, d = b0 - 2, h = h2;
+                        if (cum + h2 < need) cum += h2, d = b0 - 3, h = h3;
+                    }
+                }
+                sh[0] = d, sh[1] = need - cum, sh[2] = h;
+            }
         }
-        if (lane == 0) rv[w] = bv, ri[w] = bi;
         __syncthreads();
-        bv = rv[0], bi = ri[0];
-        for (int q = 1; q < (int)(blockDim.x >> 6); q++)
-            if (tk_before(rv[q], ri[q], bv, bi)) bv = rv[q], bi = ri[q];
-        __syncthreads();
-        if (t == 0) out[it] = make_float2(bv, __int_as_float(bi));
-        pv = bv, pi = bi;
+        const int d = sh[0], h = sh[2];
+        need = sh[1];
+        pre = (pre << 8) | (uint64_t)d;
+        if (h == need || sft == 0) {
+            P = pre, shift = sft;
+            return;
+        }
     }
 }
 
-__global__ __launch_bounds__(256) void k_topk_part(const float *__restrict__ lg, int n, int ld, int k, float2 *__restrict__ scr) {
-    // block (row, chunk): the chunk's k best (chunks of ceil(n / TOPK_CH) <= 16 x 256 values)
-    const int row = blockIdx.x, ch = blockIdx.y, len = (n + TOPK_CH - 1) / TOPK_CH, i0 = ch * len;
+__global__ __launch_bounds__(256) void k_topk_part(const float *__restrict__ lg, int n, int ld, int k, uint64_t *__restrict__ scr) {
+    // block (row, chunk): step 1 on the chunk (chunks of ceil(n / TOPK_CH) <= 16 x 256 values): its min(k, its length)
+    // largest keys, sorted, then 0 up to 64
+    __shared__ int hist[2][256], sh[4];
+    __shared__ uint64_t best[TOPK_KMAX];
+    const int row = blockIdx.x, ch = blockIdx.y, len = (n + TOPK_CH - 1) / TOPK_CH, i0 = ch * len, t = threadIdx.x;
+    const int nv = n - i0 < len ? n - i0 : len, kc = nv < k ? (nv > 0 ? nv : 0) : k;
     const float *r = lg + (size_t)row * ld;
-    float v[16];
-    int ix[16];
+    uint64_t c[16];
     #pragma unroll
     for (int u = 0; u < 16; u++) {
-        const int i = i0 + (int)threadIdx.x + 256 * u;
-        const bool ok = i < i0 + len && i < n;
-        v[u] = ok ? r[i] : 0.0f;
-        ix[u] = ok ? i : -1;
+        const int i = i0 + t + 256 * u;
+        c[u] = t + 256 * u < nv ? tk_key(r[i], i) : 0;
     }
-    tk_select<16>(v, ix, k, scr + ((size_t)row * TOPK_CH + ch) * TOPK_KMAX);
+    if (kc > 0) {
+        uint64_t P;
+        int shift;
+        tk_radix<16>(c, kc, P, shift, hist, sh);
+        if (t == 0) sh[3] = 0;
+        __syncthreads();
+        #pragma unroll
+        for (int u = 0; u < 16; u++)
+            if (c[u] && (c[u] >> shift) >= P) {
+                const int slot = atomicAdd(&sh[3], 1); // (< kc: exactly kc keys pass)
+                if (slot < kc) best[slot] = c[u];
+            }
+        __syncthreads();
+    }
+    if (t < 64) scr[((size_t)row * TOPK_CH + ch) * TOPK_KMAX + t] = tk_sort_desc(t < kc ? best[t] : 0, t);
 }
 
-__global__ __launch_bounds__(256) void k_topk_final(const float2 *__restrict__ scr, int k, float *__restrict__ vals,
-                                                    int *__restrict__ idx) {
-    // block row: the k best of its TOPK_CH x k chunk candidates (sentinels never win), into vals / idx row
-    const int row = blockIdx.x;
-    const float2 *c = scr + (size_t)row * TOPK_CH * TOPK_KMAX;
-    float v[16];
-    int ix[16];
+__global__ __launch_bounds__(256) void k_topk_final(const float *__restrict__ lg, int ld, const uint64_t *__restrict__ scr, int k,
+                                                    float *__restrict__ vals, int *__restrict__ idx) {
+    // block row: step 2 on the row's TOPK_CH sorted lists: wave w merges lists 16 w .. 16 w + 15 (four levels in
+    // registers), then the four waves' lists meet in LDS (two levels); the first k into vals / idx, the values read back
+    // from the row (their bits, -0 included)
+    __shared__ uint64_t lv[4][64], lv2[2][64];
+    const int row = blockIdx.x, t = threadIdx.x, l = t & 63, w = t >> 6;
+    const uint64_t *cc = scr + ((size_t)row * TOPK_CH + 16 * w) * TOPK_KMAX;
+    uint64_t m[8];
     #pragma unroll
-    for (int u = 0; u < 16; u++) { // (candidate e = t + 256 u: chunk e / k, pick e % k)
-        const int e = (int)threadIdx.x + 256 * u, ch = e / k, j = e % k;
-        const bool ok = ch < TOPK_CH;
-        const float2 x = ok ? c[ch * TOPK_KMAX + j] : make_float2(0.0f, 0.0f);
-        const int i = __float_as_int(x.y);
-        v[u] = x.x;
-        ix[u] = ok && i != 0x7fffffff ? i : -1;
-    }
-    __shared__ float2 out[TOPK_KMAX];
-    tk_select<16>(v, ix, k, out);
+    for (int q = 0; q < 8; q++) // (level 1: lists 16 w + 2 q and 16 w + 2 q + 1, the second read reversed)
+        m[q] = tk_bitonic_desc(tk_max(cc[(2 * q) * TOPK_KMAX + l], cc[(2 * q + 1) * TOPK_KMAX + 63 - l]), l);
+    #pragma unroll
+    for (int q = 0; q < 4; q++) m[q] = tk_merge(m[2 * q], m[2 * q + 1], l);
+    #pragma unroll
+    for (int q = 0; q < 2; q++) m[q] = tk_merge(m[2 * q], m[2 * q + 1], l);
+    lv[w][l] = tk_merge(m[0], m[1], l);
     __syncthreads();
-    if ((int)threadIdx.x < k) {
-        vals[(size_t)row * k + threadIdx.x] = out[threadIdx.x].x;
-        idx[(size_t)row * k + threadIdx.x] = __float_as_int(out[threadIdx.x].y);
+    if (w < 2) lv2[w][l] = tk_bitonic_desc(tk_max(lv[2 * w][l], lv[2 * w + 1][63 - l]), l);
+    __syncthreads();
+    if (w == 0) {
+        const uint64_t x = tk_bitonic_desc(tk_max(lv2[0][l], lv2[1][63 - l]), l);
+        if (l < k && x) {
+            const int i = (int)~(uint32_t)x;
+            vals[(size_t)row * k + l] = lg[(size_t)row * ld + i];
+            idx[(size_t)row * k + l] = i;
+        }
     }
 }
 
 // The no-allocation top-k's scratch (gw_ctx_topk_noalloc): one array per device for the process's lifetime, holding the
-// chunk candidates of GW_TOPK_NA_ROWS rows (TOPK_CH x TOPK_KMAX (value, index) pairs each) and then the outputs (rows x
-// TOPK_KMAX values, rows x TOPK_KMAX indices). Every call on a device uses the same array and leaves its contents there;
-// nothing in it needs to start at zero (each call writes every candidate and output it reads). Calls that overlap on one
-// device race
+// chunk lists of GW_TOPK_NA_ROWS rows (TOPK_CH x TOPK_KMAX keys each) and then the outputs (rows x TOPK_KMAX values, rows
+// x TOPK_KMAX indices). Every call on a device uses the same array and leaves its contents there; nothing in it needs
+// to start at zero (each call writes every key and output it reads). Calls that overlap on one device race
 #define GW_NA_CAND_BYTES ((size_t)GW_TOPK_NA_ROWS * TOPK_CH * TOPK_KMAX * 8)
 #define GW_NA_BYTES (GW_NA_CAND_BYTES + (size_t)GW_TOPK_NA_ROWS * TOPK_KMAX * 8)
 static __device__ __align__(256) unsigned char scratch[GW_NA_BYTES];
@@ -937,12 +1029,18 @@ int gw_k_quant_rows(const float *x, int n, int ldxf, int rows, int8_t *q, float 
 }
 
 int gw_k_topk(const float *lg, int n, int ld, int rows, int k, float *vals, int *idx, void *scratch, hipStream_t s) {
-    /* scratch: rows x TOPK_CH x TOPK_KMAX float2; n <= TOPK_CH x 16 x 256, k <= TOPK_KMAX and < n */
-    if (k < 1 || k > TOPK_KMAX || k >= n || n > TOPK_CH * 16 * 256 || rows < 1 || !lg || !vals || !idx || !scratch)
+    /* scratch: rows x TOPK_CH x TOPK_KMAX keys; n <= TOPK_CH x 16 x 256, k <= TOPK_KMAX and < n */
+    if (k < 1 || k > TOPK_KMAX || k >= n || n > TOPK_CH * 16 * 256 || ld < n || rows < 1 || !lg || !vals || !idx || !scratch)
         return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_topk_part, dim3(rows, TOPK_CH), dim3(256), 0, s, lg, n, ld, k, (float2 *)scratch);
-    hipLaunchKernelGGL(k_topk_final, dim3(rows), dim3(256), 0, s, (const float2 *)scratch, k, vals, idx);
+    hipLaunchKernelGGL(k_topk_part, dim3(rows, TOPK_CH), dim3(256), 0, s, lg, n, ld, k, (uint64_t *)scratch);
+    hipLaunchKernelGGL(k_topk_final, dim3(rows), dim3(256), 0, s, lg, ld, (const uint64_t *)scratch, k, vals, idx);
     return (int)hipGetLastError();
+}
+
+int gw_topk_rows(const float *logits, int n, int ld, int rows, int k, float *vals, int *idx, void *scratch, void *stream) {
+    if (k < 1 || k > TOPK_KMAX || k >= n || n > TOPK_CH * 16 * 256 || ld < n || rows < 1 || !logits || !vals || !idx || !scratch)
+        return RQ_ERR_ARG;
+    return gw_k_topk(logits, n, ld, rows, k, vals, idx, scratch, (hipStream_t)stream) ? RQ_ERR_STATE : RQ_OK;
 }
 
 int gw_k_argmax(const float *lg, int n, int ld, int rows, int *out, void *scratch, hipStream_t s) {

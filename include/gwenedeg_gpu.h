@@ -304,6 +304,12 @@ int gw_q8_block_sums(int32_t *isum, const int8_t *codes, int N, int K, const int
 int gw_kq_matmul(float *out, int type, const void *blocks, int N, int K, const int8_t *xq, const float *xs, int M,
                  void *stream);
 
+/* The top-k selection of gw_ctx_topk on device logits (sample_topk's candidate order, sampler.c:186-217: the k
+ * largest values of each row, ties to the lower index, larger first; -0 ties +0, NaN after -inf): rows rows of n
+ * values, ld floats apart; vals / idx: rows x k (device memory); scratch: rows x 32 KiB of device memory. 1 <= k <= 64,
+ * k < n <= 262144. RQ_OK, RQ_ERR_ARG (nothing launched) or RQ_ERR_STATE; asynchronous on stream */
+int gw_topk_rows(const float *logits, int n, int ld, int rows, int k, float *vals, int *idx, void *scratch, void *stream);
+
 /* The row tile of the MFMA GEMMs (prefill and batched rows: k_gemm_q8 for Q8_0 above 32 rows, k_gemm_kq for Q4_K /
  * Q6_K above 32 rows): 0 chosen per launch (64-row tiles when they give each SIMD several waves, else 32; a K-quant
  * matrix too narrow for 64 blocks takes the batched GEMV; the default), 32 or 64 forced (and the K-quant GEMM

@@ -328,6 +328,9 @@ def test_device_topk(gw, synth_models, k):
     order = np.lexsort((np.arange(m.vocab)[None, :].repeat(5, 0), -lg), axis=1)[:, :k]
     assert np.array_equal(idx, order)
     assert _bits_equal(vals, np.take_along_axis(lg, order, 1))
+    for n in (1, 3, 5, 2, 1):  # calls of fewer rows in a row on the same buffers
+        v, i = c.topk(n, k)
+        assert np.array_equal(i, order[:n]) and _bits_equal(v, np.take_along_axis(lg[:n], order[:n], 1)), n
     # decode contexts without batch buffers (max_batch 0 and 1, runq.h:329): their decode leaves one row
     for mb in (0, 1):
         c1 = m.ctx(max_batch=mb, max_ctx=512)

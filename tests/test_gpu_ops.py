@@ -162,3 +162,63 @@ def test_kq32_at_the_4b_widths(dev, typ, K, M):
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"max diff {np.abs(got - ref).max()}"
+
+
+def _topk_rows_case(name, rng):
+    """(logits rows x n, k) of a top-k case"""
+    if name == "normal_151936":
+        return rng.normal(0, 3, size=(3, 151936)).astype(np.float32), 40
+    if name == "ties":  # values on a grid of 0.5: long runs of equal values, the k-th inside a tie
+        return (np.round(rng.normal(0, 2, size=(4, 20000)) * 2) / 2).astype(np.float32), 64
+    if name == "all_equal":  # every key's value digits equal: the index decides, 8 digits
+        return np.full((2, 5000), 1.25, np.float32), 33
+    if name == "signed_zeros_inf":  # -0 and +0 tie (the lower index first), -inf after every number
+        x = np.zeros((2, 3000), np.float32)
+        x[:, ::2] = -0.0
+        x[0, 100:200] = -np.inf
+        x[1, :1500] = -np.inf
+        x[1, 2000] = 1.0
+        return x, 50
+    if name == "short":  # n below 64 x k: chunks of one or two values, empty chunks at the end
+        return rng.normal(0, 1, size=(5, 70)).astype(np.float32), 64
+    if name == "nan_tail":  # fewer numbers than k: NaN after -inf, the lower index first
+        x = rng.normal(0, 1, size=(2, 70)).astype(np.float32)
+        x[:, 3::7] = np.nan
+        x[1, 0] = -np.inf
+        return x, 64
+    if name == "max_n":
+        return rng.normal(0, 1, size=(1, 262144)).astype(np.float32), 64
+    raise KeyError(name)
+
+
+@pytest.mark.parametrize("name", ["normal_151936", "ties", "all_equal", "signed_zeros_inf", "short", "nan_tail", "max_n"])
+def test_topk_rows_order(dev, name):
+    """gw_topk_rows (the selection of gw_ctx_topk) against numpy's lexsort on the same rows: the k largest values,
+    ties to the lower index, larger first (sampler.c:186-217); the values' bits as in the row (-0 kept)"""
+    torch, gw = dev
+    rng = np.random.default_rng(len(name))
+    x, k = _topk_rows_case(name, rng)
+    rows, n = x.shape
+    ld = n + 3  # (a row pitch above n)
+    xp = np.zeros((rows, ld), np.float32)
+    xp[:, :n] = x
+    X = _to_dev(torch, xp)
+    vals = torch.zeros((rows, k), dtype=torch.float32, device="cuda")
+    idx = torch.zeros((rows, k), dtype=torch.int32, device="cuda")
+    scr = torch.empty(rows * 32768, dtype=torch.uint8, device="cuda")
+    assert gw.lib.gw_topk_rows(X.data_ptr(), n, ld, rows, k, vals.data_ptr(), idx.data_ptr(), scr.data_ptr(), None) == 0
+    torch.cuda.synchronize()
+    order = np.lexsort((np.arange(n)[None, :].repeat(rows, 0), -x), axis=1)[:, :k]
+    assert np.array_equal(idx.cpu().numpy(), order)
+    assert np.array_equal(vals.cpu().numpy().view(np.uint32), np.take_along_axis(x, order, 1).view(np.uint32))
+
+
+def test_topk_rows_refuses(dev):
+    """k above 64, k >= n, n above 262144 or ld below n: RQ_ERR_ARG before any launch"""
+    torch, gw = dev
+    X = torch.zeros(300000, dtype=torch.float32, device="cuda")
+    v = torch.zeros(64, dtype=torch.float32, device="cuda")
+    i = torch.zeros(64, dtype=torch.int32, device="cuda")
+    s = torch.empty(32768, dtype=torch.uint8, device="cuda")
+    for n, ld, k in ((1000, 1000, 65), (10, 10, 10), (262145, 262145, 8), (1000, 999, 8), (1000, 1000, 0)):
+        assert gw.lib.gw_topk_rows(X.data_ptr(), n, ld, 1, k, v.data_ptr(), i.data_ptr(), s.data_ptr(), None) == -1, (n, ld, k)
