@@ -26,13 +26,15 @@
 //     [1, 4) by exponent parity and leading mantissa bits, exact up to the power of 4) and one Newton step
 //     r = fma(t r0, r0, -3) (r0 * -0.5); bits 0: IEEE 1 / sqrtf
 //   swiglu_ref(h, h2): its SwiGLU (forward.c:1953-1958, vectorized): x = min(-h, 80), e = libmvec expf(x) (= exp_base(x)
-//     + the measured ulp difference, gw_exp_delta), d = 1 + e, r0 = vrcp14ps(d) (gw_rcp_tab by mantissa, exact up to
-//     the power of 2), r = (r0 + r0) - r0 (r0 d), (h h2) r; without the tables (a host without AVX-512): (h h2) *
-//     (1 / (1 + exp_att(min(-h, 80)))), the portable definition
+//     + the measured ulp difference, gw_exp_delta), d = 1 + e, r0 = vrcp14ps(d) (by mantissa from gw_rcp_blk, one
+//     64-bit word per 128 mantissas: vrcp14ps on [1, 2) is a non-increasing step function with at most one step per
+//     such block, checked for every mantissa on the host; exact up to the power of 2), r = (r0 + r0) - r0 (r0 d),
+//     (h h2) r; without the tables (a host without AVX-512): (h h2) * (1 / (1 + exp_att(min(-h, 80)))), the portable
+//     definition
 #define GW_RSQRT_MAXBITS 14
 static __constant__ float gw_rsqrt_tab[1 << GW_RSQRT_MAXBITS];
 static __constant__ int gw_rsqrt_bits;
-static __constant__ const float *gw_rcp_tab;
+static __constant__ const uint64_t *gw_rcp_blk;
 static __constant__ const uint8_t *gw_exp_delta;
 
 __device__ __forceinline__ float rsqrt_ref(float t) {
@@ -119,7 +121,7 @@ __device__ __forceinline__ float exp_base(float x) {
 }
 
 __device__ __forceinline__ float swiglu_ref(float h, float h2) {
-    const float *rt = gw_rcp_tab;
+    const uint64_t *rt = gw_rcp_blk;
     const uint8_t *et = gw_exp_delta;
     if (!rt) {
         float ex = silu_exp(-h);
@@ -140,8 +142,10 @@ __device__ __forceinline__ float swiglu_ref(float h, float h2) {
         }
         d = e + 1.0f;
     }
-    uint32_t v = __float_as_uint(d);
-    float r0 = __uint_as_float(__float_as_uint(rt[v & 0x7fffffu]) - (((v >> 23) - 127u) << 23));
+    const uint32_t v = __float_as_uint(d), m = v & 0x7fffffu;
+    const uint64_t w = rt[m >> 7];
+    const uint32_t a = (m & 127u) < (uint32_t)(w >> 48) ? (uint32_t)w : (uint32_t)(w >> 24);
+    float r0 = __uint_as_float(0x3f000000u + (a & 0xffffffu) - (((v >> 23) - 127u) << 23));
     float t = r0 * (r0 * d);
     float r = (r0 + r0) - t;
     return p * r;

@@ -102,6 +102,7 @@ float gw_exp_base(float x) {
 }
 
 static float *rcp_tab;       /* vrcp14ps of 1.m, 2^23 floats */
+static uint64_t *rcp_blk;    /* the same in 2^16 words, one per block of 128 mantissas (RCP_BLK_BITS) */
 static uint8_t *exp_delta;   /* 2^29 nibbles: libmvec expf - exp_base in ulps, + 8 */
 static int swiglu_ok = -1;   /* -1 not measured, 0 not reproducible here, 1 tables ready */
 
@@ -131,12 +132,41 @@ __attribute__((target("avx512f"))) static float host_rcp14(float x) {
     return _mm512_cvtss_f32(_mm512_rcp14_ps(_mm512_set1_ps(x)));
 }
 
+static int rcp_compact(void) {
+    /* vrcp14ps on [1, 2) is a non-increasing step function of the mantissa whose values lie in [0.5, 1] with at most
+     * one step inside any block of 128 consecutive mantissas (measured here, not assumed: any block with two is a
+     * failure): per block b, a = its first value, c = its value after the step, p = the step's offset (128: none),
+     * packed as (a - 0.5's bits) | (c - 0.5's bits) << 24 | p << 48; then every mantissa checked against the table */
+    rcp_blk = malloc(sizeof(uint64_t) << (23 - RCP_BLK_BITS));
+    if (!rcp_blk) return 1;
+    const uint32_t B = 1u << RCP_BLK_BITS, half = 0x3f000000u;
+    for (uint32_t b = 0; b < (1u << (23 - RCP_BLK_BITS)); b++) {
+        const uint32_t m0 = b << RCP_BLK_BITS, a = u_of(rcp_tab[m0]);
+        uint32_t p = B, c = a;
+        for (uint32_t o = 1; o < B; o++) {
+            const uint32_t v = u_of(rcp_tab[m0 + o]);
+            if (v == c) continue;
+            if (p != B || v > c) return 1; /* (a second step, or not non-increasing) */
+            p = o, c = v;
+        }
+        if (a < half || a > 0x3f800000u || c < half) return 1;
+        rcp_blk[b] = (uint64_t)(a - half) | (uint64_t)(c - half) << 24 | (uint64_t)p << 48;
+    }
+    for (uint32_t m = 0; m < (1u << 23); m++) {
+        const uint64_t w = rcp_blk[m >> RCP_BLK_BITS];
+        const uint32_t o = m & (B - 1), v = 0x3f000000u + (uint32_t)(o < ((w >> 48) & 0xffu) ? w : w >> 24) % (1u << 24);
+        if (v != u_of(rcp_tab[m])) return 1;
+    }
+    return 0;
+}
+
 static int swiglu_measure(void) {
     if (!__builtin_cpu_supports("avx512f")) return 0;
     rcp_tab = malloc((size_t)4 << 23);
     exp_delta = malloc((size_t)1 << 28);
     if (!rcp_tab || !exp_delta) return 0;
     for (uint32_t m = 0; m < (1u << 23); m++) rcp_tab[m] = host_rcp14(f_of(0x3f800000u | m));
+    if (rcp_compact()) return 0;
     for (uint64_t k = 1; k <= (1u << 20); k++) { /* exact up to the power of 2, on d in [1, 2^120) */
         uint64_t r = mix64(k * 0xd1b54a32d192ed03ull);
         float d = f_of(((uint32_t)(127 + (int)(r % 120)) << 23) | (uint32_t)((r >> 8) & 0x7fffffu));
@@ -177,9 +207,10 @@ int gw_exact_init(char *err, size_t errlen) {
     if (dev < 64 && !dev_done[dev]) {
         void *rp = NULL, *ep = NULL;
         if (swiglu_ok) {
-            e = hipMalloc(&rp, (size_t)4 << 23);
+            const size_t rb = sizeof(uint64_t) << (23 - RCP_BLK_BITS);
+            e = hipMalloc(&rp, rb);
             if (e == hipSuccess) e = hipMalloc(&ep, (size_t)1 << 28);
-            if (e == hipSuccess) e = hipMemcpy(rp, rcp_tab, (size_t)4 << 23, hipMemcpyHostToDevice);
+            if (e == hipSuccess) e = hipMemcpy(rp, rcp_blk, rb, hipMemcpyHostToDevice);
             if (e == hipSuccess) e = hipMemcpy(ep, exp_delta, (size_t)1 << 28, hipMemcpyHostToDevice);
             if (e != hipSuccess) {
                 if (rp) hipFree(rp);
@@ -188,8 +219,8 @@ int gw_exact_init(char *err, size_t errlen) {
             }
         }
         if (rc == RQ_OK) {
-            int k = gw_k_set_exact(rsq_tab, rsq_bits, (const float *)rp, (const uint8_t *)ep);
-            if (!k) k = gw_v_set_exact(rsq_tab, rsq_bits, (const float *)rp, (const uint8_t *)ep);
+            int k = gw_k_set_exact(rsq_tab, rsq_bits, (const uint64_t *)rp, (const uint8_t *)ep);
+            if (!k) k = gw_v_set_exact(rsq_tab, rsq_bits, (const uint64_t *)rp, (const uint8_t *)ep);
             if (k) rc = gw_hip_fail(err, errlen, "hipMemcpyToSymbol (exact tables)", (hipError_t)k);
             else {
                 dev_done[dev] = 1;
@@ -226,7 +257,7 @@ float gw_swiglu_tab_host(float h, float h2) {
         d = e + 1.0f;
     }
     uint32_t v = u_of(d);
-    float r0 = f_of(u_of(rcp_tab[v & 0x7fffffu]) - (((v >> 23) - 127u) << 23));
+    float r0 = f_of(gw_rcp_bits(rcp_blk, v));
     float t = r0 * (r0 * d);
     float r = (r0 + r0) - t;
     return p * r;

@@ -437,11 +437,11 @@ static int gv_launch(int pro, int R, const GvArgs &a, const GwMat *nx, int nR, h
     return (int)hipGetLastError();
 }
 
-int gw_v_set_exact(const float *rsq, int bits, const float *rcp, const uint8_t *expd) {
+int gw_v_set_exact(const float *rsq, int bits, const uint64_t *rcp, const uint8_t *expd) {
     /* this file's copy of the host-measured tables (rsqrt_ref, swiglu_ref) on the current device */
     hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(gw_rsqrt_bits), &bits, sizeof(int));
     if (e == hipSuccess && bits) e = hipMemcpyToSymbol(HIP_SYMBOL(gw_rsqrt_tab), rsq, sizeof(float) << bits);
-    if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(gw_rcp_tab), &rcp, sizeof(rcp));
+    if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(gw_rcp_blk), &rcp, sizeof(rcp));
     if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(gw_exp_delta), &expd, sizeof(expd));
     return (int)e;
 }

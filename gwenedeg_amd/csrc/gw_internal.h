@@ -209,8 +209,17 @@ int gw_exact_init(char *err, size_t errlen);
 int gw_exact_mode(void);        /* bit 0: 1 / sqrtf reproduced, bit 1: SwiGLU reproduced */
 float gw_rsqrt_host(float t);   /* the reference's 1.0f / sqrtf(t) on this host */
 float gw_exp_base(float x);     /* the device's exp_base, for the table */
-int gw_k_set_exact(const float *rsq, int bits, const float *rcp, const uint8_t *expd); /* gw_kernels.hip's copy */
-int gw_v_set_exact(const float *rsq, int bits, const float *rcp, const uint8_t *expd); /* gw_gemv.hip's copy */
+int gw_k_set_exact(const float *rsq, int bits, const uint64_t *rcp, const uint8_t *expd); /* gw_kernels.hip's copy */
+int gw_v_set_exact(const float *rsq, int bits, const uint64_t *rcp, const uint8_t *expd); /* gw_gemv.hip's copy */
+/* vrcp14ps of d >= 1 from the compact table (one word per RCP_BLK_BITS-bit block of mantissas: the block's first value
+ * and the value after its one step, as bits above 0.5's, and the step's offset): the result's bits */
+#define RCP_BLK_BITS 7
+static inline uint32_t gw_rcp_bits(const uint64_t *blk, uint32_t v) {
+    const uint32_t m = v & 0x7fffffu;
+    const uint64_t w = blk[m >> RCP_BLK_BITS];
+    const uint32_t f = 0x3f000000u + (uint32_t)((m & ((1u << RCP_BLK_BITS) - 1)) < ((w >> 48) & 0xffu) ? w : w >> 24) % (1u << 24);
+    return f - (((v >> 23) - 127u) << 23);
+}
 int gw_hip_fail(char *err, size_t errlen, const char *what, hipError_t e);
 
 /* kernels (gw_kernels.hip) */
