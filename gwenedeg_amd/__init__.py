@@ -64,7 +64,8 @@ lib.gw_exact_mode.argtypes = []
 
 
 def exact_mode() -> int:
-    """gw_exact_mode: 3 when the device reproduces the reference's host float operations bit for bit (after a load)"""
+    """gw_exact_mode: bits 0 and 1 set when the device reproduces the reference's host float operations bit for bit
+    (after a load); bit 2: libmvec's expf by its method, no table"""
     return lib.gw_exact_mode()
 
 

@@ -25,8 +25,9 @@
 //   rsqrt_ref(t): its 1.0f / sqrtf(t) = r0 = rsqrtss(t) (the CPU's estimate: gw_rsqrt_tab, 2^bits values for t in
 //     [1, 4) by exponent parity and leading mantissa bits, exact up to the power of 4) and one Newton step
 //     r = fma(t r0, r0, -3) (r0 * -0.5); bits 0: IEEE 1 / sqrtf
-//   swiglu_ref(h, h2): its SwiGLU (forward.c:1953-1958, vectorized): x = min(-h, 80), e = libmvec expf(x) (= exp_base(x)
-//     + the measured ulp difference, gw_exp_delta), d = 1 + e, r0 = vrcp14ps(d) (by mantissa from gw_rcp_blk, one
+//   swiglu_ref(h, h2): its SwiGLU (forward.c:1953-1958, vectorized): x = min(-h, 80), e = libmvec expf(x) (exp_mvec:
+//     its published method, equal to the host's on every input the host checked; else plus the measured ulp difference,
+//     gw_exp_delta), d = 1 + e, r0 = vrcp14ps(d) (by mantissa from gw_rcp_blk, one
 //     64-bit word per 128 mantissas: vrcp14ps on [1, 2) is a non-increasing step function with at most one step per
 //     such block, checked for every mantissa on the host; exact up to the power of 2), r = (r0 + r0) - r0 (r0 d),
 //     (h h2) r; without the tables (a host without AVX-512): (h h2) * (1 / (1 + exp_att(min(-h, 80)))), the portable
@@ -103,21 +104,20 @@ __device__ __forceinline__ float exp_att(float x) {
 
 __device__ __forceinline__ float silu_exp(float x) { return exp_att(x < 80.0f ? x : 80.0f); }
 
-__device__ __forceinline__ float exp_base(float x) {
-    // exp_att's operations without its clamp, for x in [-32, 80] (gw_exact.c's gw_exp_base, operation for operation)
-    float n = rintf(x * 1.44269504088896341f);
-    float r = __builtin_fmaf(n, -0.693359375f, x);
-    r = __builtin_fmaf(n, 2.12194440e-4f, r);
-    float z = r * r;
-    float y = 1.9875691500e-4f;
-    y = __builtin_fmaf(y, r, 1.3981999507e-3f);
-    y = __builtin_fmaf(y, r, 8.3334519073e-3f);
-    y = __builtin_fmaf(y, r, 4.1665795894e-2f);
-    y = __builtin_fmaf(y, r, 1.6666665459e-1f);
-    y = __builtin_fmaf(y, r, 5.0000001201e-1f);
-    y = __builtin_fmaf(y, z, r);
-    y = y + 1.0f;
-    return __uint_as_float(__float_as_uint(y) + ((uint32_t)(int32_t)n << 23));
+__device__ __forceinline__ float exp_mvec(float x) {
+    // glibc libmvec's expf (its AVX-512 method: shifter rounding, ln2 in two parts, degree-5 Horner polynomial, 2^n by
+    // the exponent field), for x in [-32, 80]: gw_exact.c's gw_exp_mvec, operation for operation
+    const float sh = 12582912.0f;
+    float n = __builtin_fmaf(x, __uint_as_float(0x3fb8aa3bu), sh) - sh;
+    float r = __builtin_fmaf(-n, __uint_as_float(0x3f317200u), x);
+    r = __builtin_fmaf(-n, __uint_as_float(0x35bfbe8eu), r);
+    float p = __uint_as_float(0x3c07d9feu);
+    p = __builtin_fmaf(p, r, __uint_as_float(0x3d2b8392u));
+    p = __builtin_fmaf(p, r, __uint_as_float(0x3e2aacacu));
+    p = __builtin_fmaf(p, r, __uint_as_float(0x3effff34u));
+    p = __builtin_fmaf(p, r, __uint_as_float(0x3f7ffffeu));
+    p = __builtin_fmaf(p, r, 1.0f);
+    return __uint_as_float(__float_as_uint(p) + ((uint32_t)(int32_t)n << 23));
 }
 
 __device__ __forceinline__ float swiglu_ref(float h, float h2) {
@@ -134,8 +134,8 @@ __device__ __forceinline__ float swiglu_ref(float h, float h2) {
     uint32_t u = __float_as_uint(x), E = (u >> 23) & 0xffu;
     float d = 1.0f; // (x <= -32: e < 2^-24, 1 + e = 1)
     if (!(u >> 31) || E < 132u) {
-        float e = exp_base(x);
-        if (E >= 101u) { // the tabulated binades: |x| >= 2^-26 (below it libmvec's expf equals exp_base)
+        float e = exp_mvec(x);
+        if (et && E >= 101u) { // (a host whose libmvec differs: the tabulated binades, |x| >= 2^-26)
             uint32_t slot = (u >> 31) ? 33u + (E - 101u) : E - 101u, idx = slot << 23 | (u & 0x7fffffu);
             int dl = (int)((et[idx >> 1] >> ((idx & 1u) * 4u)) & 15u) - 8;
             e = __uint_as_float(__float_as_uint(e) + (uint32_t)dl);

@@ -7,13 +7,17 @@
  *   SwiGLU's 1 / d   (d = 1 + e): a vector division, r0 = vrcp14ps(d) (the CPU's estimate) and the Newton step
  *                    r = (r0 + r0) - r0 (r0 d); out = (h h2) r
  * The estimates (rsqrtss, vrcp14ps) are table lookups inside the CPU, exact up to the power of 2, so a table of their
- * values measured here on one binade reproduces them everywhere (verified on seeded inputs before use). libmvec's
- * expf is a function of the full input: the device computes the attention's Cephes-style exp (exp_att's operations,
- * no clamp: identical on host and device) and adds libmvec's difference from it, measured here for every float the
- * SwiGLU can meet where the difference matters (|x| in [2^-26, 32) negative, [2^-26, 128) positive: 64 binades, one
- * signed 4-bit ulp difference each, 256 MiB). Outside: |x| < 2^-26 the two agree (checked exhaustively for
- * |x| < 2^-20 on the development host: 36 differences among 1.8e9 inputs, all above 2^-26), x <= -32 gives
- * 1 + e = 1 exactly either way (e < 2^-24), x is clamped at 80.
+ * values measured here on one binade reproduces them everywhere (verified on seeded inputs before use; vrcp14ps's is
+ * kept in the compact form of rcp_compact). libmvec's expf is glibc's published AVX-512 method (its
+ * svml_s_expf16_core_avx512 and data table): n = fma(x, 1/ln2, 1.5 2^23) - 1.5 2^23 (round to nearest by the shifter),
+ * r = fma(-n, ln2_hi, x), r = fma(-n, ln2_lo, r) (ln2 split as 0x3f317200 + 0x35bfbe8e), a degree-5 polynomial in
+ * Horner form with fma (c0 = 1, c1 .. c5 below), scaled by 2^n through the exponent field. The device computes that
+ * (gw_exp_mvec here, exp_mvec there, operation for operation); the library still calls the host's libmvec on every
+ * float the SwiGLU can meet where a difference could arise (|x| in [2^-26, 32) negative, [2^-26, 128) positive: 64
+ * binades) and compares: equal everywhere (the development host: 0 differences among 5.1e8 inputs), no table; else the
+ * signed ulp differences (4 bits each, 256 MiB) go to the device too, as a host with another libmvec needs. Outside:
+ * |x| < 2^-26 both give 1 (r = x, and 1 + c1 x rounds to 1), x <= -32 gives 1 + e = 1 exactly either way (e < 2^-24),
+ * x is clamped at 80.
  *
  * The tables are the host's, not constants: the reference's own results differ between CPUs the same way. A host
  * without AVX-512 leaves them unset, and the device falls back to IEEE 1 / sqrtf and division and the Cephes exp
@@ -83,9 +87,9 @@ __m512 _ZGVeN16v_expf(__m512);
 #define EXP_POS 33   /* binades of x > 0: exponents 101..133 ([2^-26, 128)) */
 #define EXP_NEG 31   /* binades of x < 0: exponents 101..131 ((-32, -2^-26]) */
 
-float gw_exp_base(float x) {
-    /* the attention's Cephes-style exp (forward.c:1301-1321's operations) without its clamp, for x in [-32, 80]: the
-     * device's exp_base, operation for operation */
+static float exp_cephes(float x) {
+    /* the attention's Cephes-style exp (forward.c:1301-1321's operations) without its clamp, for x in [-86, 80]: the
+     * portable SwiGLU's exp on a host without the tables */
     float n = rintf(x * 1.44269504088896341f);
     float r = fmaf(n, -0.693359375f, x);
     r = fmaf(n, 2.12194440e-4f, r);
@@ -101,12 +105,28 @@ float gw_exp_base(float x) {
     return f_of(u_of(y) + ((uint32_t)(int32_t)n << 23));
 }
 
+float gw_exp_mvec(float x) {
+    /* libmvec's expf by its published method (see above), for x in [-32, 80]: the device's exp_mvec, operation for
+     * operation */
+    const float sh = 12582912.0f; /* 1.5 2^23 */
+    float n = fmaf(x, f_of(0x3fb8aa3bu), sh) - sh;
+    float r = fmaf(-n, f_of(0x3f317200u), x);
+    r = fmaf(-n, f_of(0x35bfbe8eu), r);
+    float p = f_of(0x3c07d9feu);
+    p = fmaf(p, r, f_of(0x3d2b8392u));
+    p = fmaf(p, r, f_of(0x3e2aacacu));
+    p = fmaf(p, r, f_of(0x3effff34u));
+    p = fmaf(p, r, f_of(0x3f7ffffeu));
+    p = fmaf(p, r, 1.0f);
+    return f_of(u_of(p) + ((uint32_t)(int32_t)n << 23));
+}
+
 static float *rcp_tab;       /* vrcp14ps of 1.m, 2^23 floats */
 static uint64_t *rcp_blk;    /* the same in 2^16 words, one per block of 128 mantissas (RCP_BLK_BITS) */
-static uint8_t *exp_delta;   /* 2^29 nibbles: libmvec expf - exp_base in ulps, + 8 */
+static uint8_t *exp_delta;   /* 2^29 nibbles: libmvec expf - gw_exp_mvec in ulps, + 8 (NULL: no difference anywhere) */
 static int swiglu_ok = -1;   /* -1 not measured, 0 not reproducible here, 1 tables ready */
 
-typedef struct { int slot0, slot1, bad; } ExpJob;
+typedef struct { int slot0, slot1, bad; long nz; } ExpJob;
 
 __attribute__((target("avx512f"))) static void *exp_worker(void *arg) {
     ExpJob *j = arg;
@@ -118,9 +138,10 @@ __attribute__((target("avx512f"))) static void *exp_worker(void *arg) {
             _mm512_store_ps(ys, _ZGVeN16v_expf(_mm512_load_ps(xs)));
             for (int k = 0; k < 16; k += 2) {
                 /* (x > 80: never met, the argument is clamped; no difference stored) */
-                int d0 = xs[k] > 80.0f ? 0 : (int)(u_of(ys[k]) - u_of(gw_exp_base(xs[k])));
-                int d1 = xs[k + 1] > 80.0f ? 0 : (int)(u_of(ys[k + 1]) - u_of(gw_exp_base(xs[k + 1])));
+                int d0 = xs[k] > 80.0f ? 0 : (int)(u_of(ys[k]) - u_of(gw_exp_mvec(xs[k])));
+                int d1 = xs[k + 1] > 80.0f ? 0 : (int)(u_of(ys[k + 1]) - u_of(gw_exp_mvec(xs[k + 1])));
                 if (d0 < -7 || d0 > 7 || d1 < -7 || d1 > 7) { j->bad = 1; break; }
+                j->nz += (d0 != 0) + (d1 != 0);
                 exp_delta[(((size_t)slot << 23) | (m + (uint32_t)k)) >> 1] = (uint8_t)((d0 + 8) | (d1 + 8) << 4);
             }
         }
@@ -177,14 +198,20 @@ static int swiglu_measure(void) {
     pthread_t th[NT];
     ExpJob job[NT];
     int ns = EXP_POS + EXP_NEG, bad = 0, started = 0;
+    long nz = 0;
     for (int i = 0; i < NT; i++) {
-        job[i] = (ExpJob){ ns * i / NT, ns * (i + 1) / NT, 0 };
+        job[i] = (ExpJob){ ns * i / NT, ns * (i + 1) / NT, 0, 0 };
         if (pthread_create(&th[i], NULL, exp_worker, &job[i])) { exp_worker(&job[i]); continue; }
         started |= 1 << i;
     }
     for (int i = 0; i < NT; i++) {
         if (started & (1 << i)) pthread_join(th[i], NULL);
         bad |= job[i].bad;
+        nz += job[i].nz;
+    }
+    if (!bad && !nz) { /* libmvec's expf is gw_exp_mvec for every input: no table */
+        free(exp_delta);
+        exp_delta = NULL;
     }
     return !bad;
 }
@@ -209,9 +236,9 @@ int gw_exact_init(char *err, size_t errlen) {
         if (swiglu_ok) {
             const size_t rb = sizeof(uint64_t) << (23 - RCP_BLK_BITS);
             e = hipMalloc(&rp, rb);
-            if (e == hipSuccess) e = hipMalloc(&ep, (size_t)1 << 28);
+            if (e == hipSuccess && exp_delta) e = hipMalloc(&ep, (size_t)1 << 28);
             if (e == hipSuccess) e = hipMemcpy(rp, rcp_blk, rb, hipMemcpyHostToDevice);
-            if (e == hipSuccess) e = hipMemcpy(ep, exp_delta, (size_t)1 << 28, hipMemcpyHostToDevice);
+            if (e == hipSuccess && exp_delta) e = hipMemcpy(ep, exp_delta, (size_t)1 << 28, hipMemcpyHostToDevice);
             if (e != hipSuccess) {
                 if (rp) hipFree(rp);
                 if (ep) hipFree(ep);
@@ -241,15 +268,15 @@ float gw_swiglu_tab_host(float h, float h2) {
         float x = -h;
         x = x < 80.0f ? x : 80.0f;
         x = x > -86.0f ? x : -86.0f;
-        return (h * h2) * (1.0f / (1.0f + gw_exp_base(x)));
+        return (h * h2) * (1.0f / (1.0f + exp_cephes(x)));
     }
     float p = h * h2, x = -h;
     x = x < 80.0f ? x : 80.0f;
     uint32_t u = u_of(x), E = (u >> 23) & 0xffu;
     float d = 1.0f;
     if (!(u >> 31) || E < 132u) {
-        float e = gw_exp_base(x);
-        if (E >= 101u) {
+        float e = gw_exp_mvec(x);
+        if (exp_delta && E >= 101u) {
             uint32_t slot = (u >> 31) ? 33u + (E - 101u) : E - 101u, idx = slot << 23 | (u & 0x7fffffu);
             int dl = (int)((exp_delta[idx >> 1] >> ((idx & 1u) * 4u)) & 15u) - 8;
             e = f_of(u_of(e) + (uint32_t)dl);
@@ -264,6 +291,7 @@ float gw_swiglu_tab_host(float h, float h2) {
 }
 
 int gw_exact_mode(void) {
-    /* bit 0: the reference's 1 / sqrtf reproduced; bit 1: its SwiGLU reproduced (after gw_exact_init) */
-    return (rsq_bits > 0) | (swiglu_ok > 0) << 1;
+    /* bit 0: the reference's 1 / sqrtf reproduced; bit 1: its SwiGLU reproduced (after gw_exact_init); bit 2: with
+     * libmvec's expf computed by its method everywhere (no difference table) */
+    return (rsq_bits > 0) | (swiglu_ok > 0) << 1 | (swiglu_ok > 0 && !exp_delta) << 2;
 }

@@ -208,7 +208,7 @@ int gw_device_init(char *err, size_t errlen);
 int gw_exact_init(char *err, size_t errlen);
 int gw_exact_mode(void);        /* bit 0: 1 / sqrtf reproduced, bit 1: SwiGLU reproduced */
 float gw_rsqrt_host(float t);   /* the reference's 1.0f / sqrtf(t) on this host */
-float gw_exp_base(float x);     /* the device's exp_base, for the table */
+float gw_exp_mvec(float x);     /* libmvec's expf by its method: the device's exp_mvec */
 int gw_k_set_exact(const float *rsq, int bits, const uint64_t *rcp, const uint8_t *expd); /* gw_kernels.hip's copy */
 int gw_v_set_exact(const float *rsq, int bits, const uint64_t *rcp, const uint8_t *expd); /* gw_gemv.hip's copy */
 /* vrcp14ps of d >= 1 from the compact table (one word per RCP_BLK_BITS-bit block of mantissas: the block's first value

@@ -329,8 +329,10 @@ void *gw_ctx_stream(RqCtx *c);
 /* Which of the reference's host-specific float operations the device reproduces, measured on this host at the first
  * rq_model_load (no counterpart in runq.h): bit 0 its 1.0f / sqrtf (rsqrtss + Newton: rmsnorm forward.c:896,
  * QK-norm, the attention scale forward.c:137), bit 1 its SwiGLU (libmvec vector expf, vrcp14ps + Newton,
- * forward.c:1953-1958). 3: the device's results equal the reference's CPU path on this host bit for bit; otherwise
- * the missing operation falls back to IEEE (sqrtf, division) and the attention's exp. 0 before any model load */
+ * forward.c:1953-1958). Bits 0 and 1 both set: the device's results equal the reference's CPU path on this host bit
+ * for bit; otherwise the missing operation falls back to IEEE (sqrtf, division) and the attention's exp. Bit 2 (with
+ * bit 1): the host's libmvec expf equals its published method on every input checked, so the device needs no table
+ * of differences. 0 before any model load */
 int gw_exact_mode(void);
 
 #ifdef __cplusplus

@@ -29,7 +29,7 @@ def orc():
 
 
 def _exact(gw):
-    return gw.exact_mode() == 3
+    return gw.exact_mode() & 3 == 3
 
 
 def _bits(a):

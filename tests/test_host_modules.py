@@ -70,7 +70,7 @@ def test_reference_host_modules_run_unmodified(tmp_path):
     d["n_layers"] = 2
     path = synth.write_gguf(str(tmp_path / "m.gguf"), d, seed=21)
     m = gw.Model(path, ctx_len=512)
-    if gw.exact_mode() != 3:
+    if gw.exact_mode() & 3 != 3:
         pytest.skip("this host does not provide the reference's float operations (AVX-512)")
     del m
     base = np.random.default_rng(21).integers(0, d["vocab"], 16).astype(np.int32)
