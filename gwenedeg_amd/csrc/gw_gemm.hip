@@ -184,6 +184,114 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const int8_t *__restrict__ W, c
     }
 }
 
+// k_gemm_q8 for K % GKB == 0 (every stage full: the model's widths): the same tiles, pipeline and fold, with fewer
+// instructions around the fold (which needs 4 VALU instructions per output and group: the bound of this GEMM). Loads
+// through buffer descriptors over the block's own rows: rows past M or N read as 0 (the descriptor's range), so no
+// clamped addresses and no selects; each thread's offsets are fixed and a stage moves the scalar offset only
+#define GQ_RSRC_DW3 0x00020000 // buffer descriptor word 3 of gfx9-family targets (raw loads)
+template <int GM>
+__global__ __launch_bounds__(256) void k_gemm_q8f(const int8_t *__restrict__ W, const uint16_t *__restrict__ WS, int N, int K,
+                                                  const int8_t *__restrict__ X, const float *__restrict__ XS, int ldx, int M,
+                                                  float *__restrict__ out, int ldo) {
+    constexpr int TJ = GM == 64 ? 2 : 1, XC = GM * 8 / 256;
+    __shared__ __align__(16) int8_t xl[2][GM * GROW];
+    __shared__ __align__(16) int8_t wl[2][GN * GROW];
+    __shared__ __align__(16) float xsl[2][4][GM];
+    __shared__ float wsl[2][GN][4];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int m0 = blockIdx.y * GM, n0 = blockIdx.x * GN, G = K >> 5, NS = K / GKB, gx = ldx >> 5;
+    const int wm = GM == 64 ? (wave >> 1) * 32 : 0, wn = GM == 64 ? (wave & 1) * 64 : wave * 32;
+    const int mr = M - m0 < GM ? M - m0 : GM, nr = N - n0 < GN ? N - n0 : GN; // (the block's rows)
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void *)(X + (size_t)m0 * ldx), (short)0, mr * ldx, GQ_RSRC_DW3);
+    const __amdgpu_buffer_rsrc_t rxs = __builtin_amdgcn_make_buffer_rsrc((void *)(XS + (size_t)m0 * gx), (short)0, mr * gx * 4, GQ_RSRC_DW3);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)(W + (size_t)n0 * K), (short)0, nr * K, GQ_RSRC_DW3);
+    const __amdgpu_buffer_rsrc_t rws = __builtin_amdgcn_make_buffer_rsrc((void *)(WS + (size_t)n0 * G), (short)0, nr * G * 2, GQ_RSRC_DW3);
+    float acc[TJ][16];
+    #pragma unroll
+    for (int j = 0; j < TJ; j++)
+        #pragma unroll
+        for (int r = 0; r < 16; r++) acc[j][r] = 0.0f;
+    // this thread's chunks (16 B: chunk c = t + 256 k is row c / 8, bytes 16 (c % 8) .. of the stage's 128) and scales
+    // (row t / 4, group t % 4 of the stage; W rows t / 4 and t / 4 + 64)
+    const int crow = t >> 3, ccol = (t & 7) * 16, srow = t >> 2, sgg = t & 3;
+    const int xo = crow * ldx + ccol, wo = crow * K + ccol, xso = (srow * gx + sgg) * 4, wso = (srow * G + sgg) * 2;
+    struct St {
+        uint4 x0, x1, w0, w1, w2, w3;
+        float xs, ws0, ws1;
+    };
+    auto ld16 = [&](__amdgpu_buffer_rsrc_t r, int vo, int so) __attribute__((always_inline)) -> uint4 {
+        return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0));
+    };
+    auto load = [&](int st) __attribute__((always_inline)) -> St {
+        const int k0 = st * GKB; // (st = NS: past the last stage, inside the buffers or read as 0; never stored)
+        St o;
+        o.x0 = ld16(rx, xo, k0);
+        o.x1 = XC > 1 ? ld16(rx, xo + 32 * ldx, k0) : o.x0;
+        o.w0 = ld16(rw, wo, k0);
+        o.w1 = ld16(rw, wo + 32 * K, k0);
+        o.w2 = ld16(rw, wo + 64 * K, k0);
+        o.w3 = ld16(rw, wo + 96 * K, k0);
+        o.xs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rxs, xso, st * 16, 0));
+        o.ws0 = h2f_g(__builtin_amdgcn_raw_buffer_load_b16(rws, wso, st * 8, 0));
+        o.ws1 = h2f_g(__builtin_amdgcn_raw_buffer_load_b16(rws, wso + 64 * G * 2, st * 8, 0));
+        return o;
+    };
+    auto store = [&](const St o, int buf) __attribute__((always_inline)) {
+        const int r0 = crow * GROW + ccol;
+        *(uint4 *)(&xl[buf][r0]) = o.x0;
+        if (XC > 1) *(uint4 *)(&xl[buf][r0 + 32 * GROW]) = o.x1;
+        *(uint4 *)(&wl[buf][r0]) = o.w0;
+        *(uint4 *)(&wl[buf][r0 + 32 * GROW]) = o.w1;
+        *(uint4 *)(&wl[buf][r0 + 64 * GROW]) = o.w2;
+        *(uint4 *)(&wl[buf][r0 + 96 * GROW]) = o.w3;
+        if (srow < GM) xsl[buf][sgg][srow] = o.xs;
+        wsl[buf][srow][sgg] = o.ws0;
+        wsl[buf][srow + 64][sgg] = o.ws1;
+    };
+    store(load(0), 0);
+    __syncthreads();
+    const int xa = (wm + (lane & 31)) * GROW + 16 * (lane >> 5), wa = (wn + (lane & 31)) * GROW + 16 * (lane >> 5);
+    for (int st = 0; st < NS; st++) {
+        const int buf = st & 1;
+        const St nx = load(st + 1);
+        // (rolled: unrolled, the compiler keeps every MFMA result live at once: 280 registers with two tiles per wave;
+        // with one tile, 191 registers and qkv / wo / w2 20-35 % slower, measured)
+        #pragma unroll 1
+        for (int gg = 0; gg < 4; gg++) {
+            const i32x4 a = *(const i32x4 *)(&xl[buf][xa + gg * 32]);
+            #pragma unroll
+            for (int j = 0; j < TJ; j++) {
+                const i32x4 b = *(const i32x4 *)(&wl[buf][wa + 32 * j * GROW + gg * 32]);
+                const i32x16 z = { 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0 };
+                const i32x16 I = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
+                const float ws = wsl[buf][wn + 32 * j + (lane & 31)][gg];
+                #pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float4 xs4 = *(const float4 *)(&xsl[buf][gg][wm + 8 * q + 4 * (lane >> 5)]);
+                    const float xsq[4] = { xs4.x, xs4.y, xs4.z, xs4.w };
+                    #pragma unroll
+                    for (int s = 0; s < 4; s++) {
+                        const float sc = ws * xsq[s];
+                        const float p = sc * (float)I[4 * q + s];
+                        acc[j][4 * q + s] = acc[j][4 * q + s] + p;
+                    }
+                }
+            }
+        }
+        if (st + 1 < NS) store(nx, buf ^ 1);
+        __syncthreads();
+    }
+    #pragma unroll
+    for (int j = 0; j < TJ; j++) {
+        const int n = n0 + wn + 32 * j + (lane & 31);
+        #pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int m = m0 + wm + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (m < M && n < N) out[(size_t)m * ldo + n] = acc[j][r];
+        }
+    }
+}
+
 // ------------------------------------------------------------------------------------- K-quant MFMA GEMM
 
 // out[m * ldo + n] (+)= W row n . X row m for m < M, n < N, W in the file's Q4_K / Q6_K super-blocks (batched rows,
@@ -1022,12 +1130,16 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
         hipEvent_t e0, e1;
         gw_take_launch_events(&e0, &e1);
         const int cus = gemm_cus(), nt = (w->rows + GN - 1) / GN;
-        if (g_tile_rows ? g_tile_rows == 64 : (size_t)nt * ((M + 63) / 64) >= (size_t)4 * cus) // (64-row tiles: enough for several waves per SIMD)
-            hipExtLaunchKernelGGL(k_gemm_q8<64>, dim3(nt, (M + 63) / 64), dim3(256), 0, s, e0, e1, 0, (const int8_t *)w->codes,
-                                  (const uint16_t *)w->scales, w->rows, w->cols, xq, xs, ldx, M, out, ldo);
-        else
-            hipExtLaunchKernelGGL(k_gemm_q8<32>, dim3(nt, (M + 31) / 32), dim3(256), 0, s, e0, e1, 0, (const int8_t *)w->codes,
-                                  (const uint16_t *)w->scales, w->rows, w->cols, xq, xs, ldx, M, out, ldo);
+        const bool g64 = g_tile_rows ? g_tile_rows == 64 : (size_t)nt * ((M + 63) / 64) >= (size_t)4 * cus; // (64-row tiles: enough for several waves per SIMD)
+        // (full stages, and every buffer offset inside 2^31: the descriptor-based kernel)
+        const bool full = w->cols % GKB == 0 && (size_t)(M + 64) * ldx < ((size_t)1 << 31) && (size_t)GN * w->cols < ((size_t)1 << 31);
+#define GQ_L(KK, GG) hipExtLaunchKernelGGL(KK<GG>, dim3(nt, (M + GG - 1) / GG), dim3(256), 0, s, e0, e1, 0, (const int8_t *)w->codes, \
+                                           (const uint16_t *)w->scales, w->rows, w->cols, xq, xs, ldx, M, out, ldo)
+        if (full && g64) GQ_L(k_gemm_q8f, 64);
+        else if (full) GQ_L(k_gemm_q8f, 32);
+        else if (g64) GQ_L(k_gemm_q8, 64);
+        else GQ_L(k_gemm_q8, 32);
+#undef GQ_L
         return (int)hipGetLastError();
     }
     if (w->type == GW_Q8_0)

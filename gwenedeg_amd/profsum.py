@@ -7,6 +7,15 @@
       HBM bytes per dispatch of the kernels matching REGEX from two counter runs (--pmc FETCH_SIZE, --pmc WRITE_SIZE:
       *_counter_collection.csv), each counter scaled by what it reads for the calibration kernel (a kernel of known
       traffic: CALIB_BYTES read and CALIB_BYTES written), against A algorithmic bytes per dispatch
+  python -m gwenedeg_amd.profsum busy DIR [DIR ...] --kernel REGEX [--cus 256] [--ses 32]
+      per kernel matching REGEX: the mean per dispatch of every counter in the runs (SQ_* summed over their instances,
+      GRBM_* the largest instance), and rocprofv3's derived metrics where their counters are there:
+      MfmaUtil = 100 SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x SIMDs), VALUBusy = 100 SQ_ACTIVE_INST_VALU / CUs /
+      GRBM_GUI_ACTIVE (SQ_ACTIVE_INST_VALU: quad-cycles summed over the SIMDs of each shader engine); and the same
+      normalised by the cycles the kernel's waves were present (SQ_BUSY_CYCLES, summed over the --ses shader engines,
+      each with 4 x CUs / SEs SIMDs), which counter collection does not dilute as it does GRBM_GUI_ACTIVE:
+      valu_issue = 4 SQ_INSTS_VALU / (SIMDs x busy), valu_active = 4 SQ_ACTIVE_INST_VALU / (SIMDs x busy),
+      mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs x busy), busy = SQ_BUSY_CYCLES / SEs
 """
 from __future__ import annotations
 
@@ -90,6 +99,39 @@ def traffic(fetch_dir, write_dir, kernel, calib="neg_kernel", calib_bytes=1 << 3
     return out
 
 
+def busy(dirs, kernel, cus=256, ses=32):
+    per = {}  # kernel -> counter -> {dispatch: value}
+    for d in dirs:
+        for r in _rows(d, "counter_collection.csv"):
+            kn = re.sub(r"\(.*$", "", _col(r, "Kernel_Name"))
+            if not re.search(kernel, kn):
+                continue
+            c, disp, v = _col(r, "Counter_Name"), (d, _col(r, "Dispatch_Id")), float(_col(r, "Counter_Value"))
+            slot = per.setdefault(kn, {}).setdefault(c, {})
+            slot[disp] = max(slot.get(disp, 0.0), v) if c.startswith("GRBM_") else slot.get(disp, 0.0) + v
+    out = {}
+    for kn, cs in per.items():
+        mean = {c: sum(v.values()) / len(v) for c, v in cs.items()}
+        o = {"dispatches": max(len(v) for v in cs.values()), "mean_per_dispatch": {c: round(x, 1) for c, x in mean.items()}}
+        g = mean.get("GRBM_GUI_ACTIVE")
+        if g and "SQ_VALU_MFMA_BUSY_CYCLES" in mean:
+            o["MfmaUtil_pct"] = round(100 * mean["SQ_VALU_MFMA_BUSY_CYCLES"] / (g * 4 * cus), 2)
+        if g and "SQ_ACTIVE_INST_VALU" in mean:
+            o["VALUBusy_pct"] = round(100 * mean["SQ_ACTIVE_INST_VALU"] / cus / g, 2)
+        if mean.get("SQ_INSTS_MFMA") and "SQ_INSTS_VALU" in mean:
+            o["valu_insts_per_mfma"] = round(mean["SQ_INSTS_VALU"] / mean["SQ_INSTS_MFMA"], 3)
+        b = mean.get("SQ_BUSY_CYCLES")
+        if b:
+            simd_cycles = 4 * cus * b / ses  # (every SIMD over the cycles one shader engine had waves)
+            o["busy_cycles_per_se"] = round(b / ses)
+            for key, c, f in (("valu_issue_pct", "SQ_INSTS_VALU", 4), ("valu_active_pct", "SQ_ACTIVE_INST_VALU", 4),
+                              ("mfma_busy_pct", "SQ_VALU_MFMA_BUSY_CYCLES", 1)):
+                if c in mean:
+                    o[key] = round(100 * f * mean[c] / simd_cycles, 2)
+        out[kn] = o
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -104,7 +146,15 @@ def main(argv=None):
     a2.add_argument("--calib-bytes", type=float, default=float(1 << 30))
     a2.add_argument("--algo-bytes", type=float, default=None)
     a2.add_argument("--json", default=None)
+    a3 = sub.add_parser("busy")
+    a3.add_argument("dirs", nargs="+")
+    a3.add_argument("--kernel", required=True)
+    a3.add_argument("--cus", type=int, default=256)
+    a3.add_argument("--ses", type=int, default=32)
     a = ap.parse_args(argv)
+    if a.cmd == "busy":
+        print(json.dumps(busy(a.dirs, a.kernel, a.cus, a.ses), indent=1))
+        return
     if a.cmd == "stats":
         print(stats(a.dir, a.top))
         return

@@ -47,9 +47,10 @@ def test_quantize_bitexact(dev, M, K):
 
 @pytest.mark.parametrize("M,N,K,tile", [(1, 256, 1024, 0), (1, 1024, 4096, 0), (2, 512, 12288, 0), (4, 64, 2560, 0),
                                         (7, 128, 4096, 0), (16, 48, 1024, 0), (64, 32, 1024, 0), (40, 208, 768, 32),
-                                        (100, 208, 768, 64)])
+                                        (100, 208, 768, 64), (40, 208, 800, 32), (100, 208, 864, 64), (512, 384, 4096, 0)])
 def test_q8_matmul_bitexact(dev, M, N, K, tile):
-    """the Q8_0 operator against the oracle bit for bit (above 32 rows the MFMA GEMM, its row tile forced where given)"""
+    """the Q8_0 operator against the oracle bit for bit (above 32 rows the MFMA GEMM, its row tile forced where given;
+    K % 128 == 0: k_gemm_q8f, else k_gemm_q8 with a partial last stage)"""
     torch, gw = dev
     from oracle import oracle as orc
     rng = np.random.default_rng(N + 7 * K + M)
