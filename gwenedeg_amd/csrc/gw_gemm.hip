@@ -552,10 +552,15 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
 // the block stages the 32 rows' super-blocks and the activation rows' 256 codes and 8 scales in LDS (double-buffered),
 // loaded with coalesced 16-byte loads (consecutive threads: consecutive 16 bytes of one row) SK_P super-blocks ahead;
 // each wave reads its MFMA operands (X row l % 32, W row l % 32: k_gemm_kq's layouts) from LDS: the exact int32 sums
-// (MFMA), the wave's terms (k_gemm_kq's expressions) into LDS, one barrier, then each thread adds the 8 terms of its 2
-// outputs in group order (val = val + term, kquants.h:86-109, :410-554). Two matrices of one type and width may share
-// a launch (blocks below nb1 take the first, the others the second; each writes at its own column offset of out).
-// M <= 32, K % 256 == 0, mode 1: out = out + val
+// (MFMA), the wave's terms (k_gemm_kq's expressions) into LDS, a barrier, then each thread adds the 8 terms of its 2
+// outputs in group order (val = val + term, kquants.h:86-109, :410-554). A tile's 32 activation rows are 4 quads of
+// 8 (the MFMA result's registers 4 q .. 4 q + 3 of every lane): a block takes NQR of them, the tile's 4 / NQR blocks
+// on one XCD (blocks b and b + 8 k share b % 8), each staging the whole tile (the second reads hit that XCD's L2) and
+// computing the terms and folds of its own quads only: a matrix of few rows fills the device with 4 / NQR times the
+// blocks, each with 1 / (4 / NQR) of the VALU work. The terms go through one LDS buffer (a barrier before they are
+// written, one after), so with 128 registers two blocks share a CU (double-buffered terms: 95 KB of LDS, one block per
+// CU, 15 % slower). Two matrices of one type and width may share a launch (blocks below nb1 take the first, the
+// others the second; each writes at its own column offset of out). M <= 32, K % 256 == 0, mode 1: out = out + val
 #define SK_T 512
 #define SK_P 4                      // super-blocks whose loads are in flight beyond the one computed
 #define SK_XR 272                   // LDS bytes per activation row (256 codes + 16: rows 4 banks apart)
@@ -568,19 +573,44 @@ struct SkMats { // the launch's matrices: blocks [0, nb1) the first, [nb1, grid)
     const uint8_t *W[2];
     int N[2], col[2], nb1;
 };
-template <int TYPE>
-__global__ __launch_bounds__(SK_T) void k_gemm_kq32(SkMats mats, int bstride, int K, const int8_t *__restrict__ X,
+template <int TYPE, int Q>
+__device__ __forceinline__ void kq32_terms(const i32x16 &I, const i32x16 &I1, float f0, float f1, int s0, int s1,
+                                           const float *xsw, int hi, int lane, float *Tq) {
+    // quad Q's 4 terms of this lane (registers 4 Q + e: activation rows 8 Q + 4 hi + e) into Tq[e * 64 + lane]
+    const float4 x4 = *(const float4 *)(xsw + 8 * Q + 4 * hi);
+    const float xsq[4] = { x4.x, x4.y, x4.z, x4.w };
+    #pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int r = 4 * Q + e;
+        float term;
+        if (TYPE == GW_Q4_K) {
+            float pa = (f0 * xsq[e]) * (float)I[r];
+            float pb = f1 * (xsq[e] * (float)I1[r]);
+            term = pa - pb;
+        } else {
+            int Ii = s0 * I[r] + s1 * I1[r];
+            term = (f0 * xsq[e]) * (float)Ii;
+        }
+        Tq[e * 64 + lane] = term;
+    }
+}
+template <int TYPE, int NQR>
+__global__ __launch_bounds__(SK_T, 2) void k_gemm_kq32(SkMats mats, int bstride, int K, const int8_t *__restrict__ X,
                                                     const float *__restrict__ XS, int ldx, int M, float *out, int ldo,
                                                     int mode) {
     constexpr int WST = TYPE == GW_Q4_K ? 160 : 240;            // LDS bytes per weight row (bstride + 16)
     constexpr int PW = TYPE == GW_Q4_K ? GW_Q4K_BYTES / 16 : GW_Q6K_DEV / 16; // 16-byte pieces per weight row
-    __shared__ __align__(16) float Tl[2][8][1024];              // group g's term of output o = r * 64 + lane
+    constexpr int PARTS = 4 / NQR, NO = NQR * 256;              // blocks per tile, outputs per block
+    __shared__ __align__(16) float Tl[8][NO];                   // group g's term of output o = (r - 4 q0) * 64 + lane
     __shared__ __align__(16) uint8_t Ws[2][32 * WST];
     __shared__ __align__(16) uint8_t Xs[2][32 * SK_XR];
     __shared__ __align__(16) float xsl[2][8][32];               // [group][m]
     const int t = threadIdx.x, lane = t & 63, w = t >> 6, hi = lane >> 5, r32 = lane & 31;
     const int mi = blockIdx.x >= mats.nb1;
-    const int n0 = (blockIdx.x - (mi ? mats.nb1 : 0)) * 32, N = mats.N[mi], S = K >> 8;
+    // block b of its matrix: XCD b % 8, then (b / 8) % PARTS its quads, tile 8 (b / 8 / PARTS) + b % 8
+    const int bl = blockIdx.x - (mi ? mats.nb1 : 0), part = (bl >> 3) % PARTS, q0 = part * NQR;
+    const int n0 = (((bl >> 3) / PARTS) * 8 + (bl & 7)) * 32, N = mats.N[mi], S = K >> 8;
+    if (n0 >= N || 8 * q0 >= M) return; // (the grid's padding to 8 tiles; quads past the last activation row)
     const size_t rowb = (size_t)S * bstride;
     out += mats.col[mi];
     // this thread's staging pieces: W row t / PW piece t % PW (t < 32 PW), X row t / 16 piece t % 16, XS (t < 256);
@@ -666,30 +696,37 @@ __global__ __launch_bounds__(SK_T) void k_gemm_kq32(SkMats mats, int bstride, in
             s1 = (int)(int8_t)((sc2 >> 8) & 0xffu);
             f0 = h2f_g((uint16_t)(dw & 0xffffu));
         }
-        #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float4 x4 = *(const float4 *)(&xsl[buf][w][8 * q + 4 * hi]);
-            const float xsq[4] = { x4.x, x4.y, x4.z, x4.w };
-            #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int r = 4 * q + e;
-                float term;
-                if (TYPE == GW_Q4_K) {
-                    float pa = (f0 * xsq[e]) * (float)I[r];
-                    float pb = f1 * (xsq[e] * (float)I1[r]);
-                    term = pa - pb;
-                } else {
-                    int Ii = s0 * I[r] + s1 * I1[r];
-                    term = (f0 * xsq[e]) * (float)Ii;
-                }
-                Tl[buf][w][r * 64 + lane] = term;
+        // this block's quads (uniform branches: a register index must be a constant)
+        const float *xsw = &xsl[buf][w][0];
+        float *Tw = &Tl[w][0];
+        __syncthreads(); // (every wave's fold of the previous step has read the terms)
+        if (NQR == 4) {
+            kq32_terms<TYPE, 0>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw);
+            kq32_terms<TYPE, 1>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw + 256);
+            kq32_terms<TYPE, 2>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw + 512);
+            kq32_terms<TYPE, 3>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw + 768);
+        } else if (NQR == 2) {
+            if (q0 == 0) {
+                kq32_terms<TYPE, 0>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw);
+                kq32_terms<TYPE, 1>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw + 256);
+            } else {
+                kq32_terms<TYPE, 2>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw);
+                kq32_terms<TYPE, 3>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw + 256);
             }
+        } else {
+            if (q0 == 0) kq32_terms<TYPE, 0>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw);
+            else if (q0 == 1) kq32_terms<TYPE, 1>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw);
+            else if (q0 == 2) kq32_terms<TYPE, 2>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw);
+            else kq32_terms<TYPE, 3>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw);
         }
         __syncthreads(); // (the terms of super-block s written; super-block s + 1 staged)
-        #pragma unroll
-        for (int g = 0; g < 8; g++) {
-            acc0 = acc0 + Tl[buf][g][t];
-            acc1 = acc1 + Tl[buf][g][t + 512];
+        if (t < NO) {
+            #pragma unroll
+            for (int g = 0; g < 8; g++) acc0 = acc0 + Tl[g][t];
+        }
+        if (NO > 512) {
+            #pragma unroll
+            for (int g = 0; g < 8; g++) acc1 = acc1 + Tl[g][t + 512];
         }
         return nl;
     };
@@ -709,10 +746,10 @@ __global__ __launch_bounds__(SK_T) void k_gemm_kq32(SkMats mats, int bstride, in
         o0 = step(o0, s0 + 3);
     }
     #pragma unroll
-    for (int k = 0; k < 2; k++) {
-        const int o = t + 512 * k, r = o >> 6, ln = o & 63;
+    for (int k = 0; k < (NO + 511) / 512; k++) {
+        const int o = t + 512 * k, r = (o >> 6) + 4 * q0, ln = o & 63;
         const int m = 8 * (r >> 2) + 4 * (ln >> 5) + (r & 3), n = n0 + (ln & 31);
-        if (m < M && n < N) {
+        if (o < NO && m < M && n < N) {
             float *po = out + (size_t)m * ldo + n;
             const float v = k ? acc1 : acc0;
             *po = mode == 1 ? *po + v : v;
@@ -1087,6 +1124,8 @@ static int gemm_cus(void) { // the device's compute units
     return cus;
 }
 
+static int g_kq32_nqr; // (0: chosen per launch; 1, 2 or 4: forced, gw_kq32_quads)
+
 static bool kq32_takes(const GwMat *w, int M) {
     // K-quants, 9 .. 32 rows: the 32-row GEMM with the groups spread over a block's waves (a matrix of 32768 rows or
     // more, the classifier: the 128-column MFMA GEMM, a block for every compute unit)
@@ -1098,21 +1137,32 @@ static int launch_kq32(const GwMat *a, const GwMat *b, int col_b, const int8_t *
     // a, and b (NULL: none; same type and width as a) written from column col_b of out
     hipEvent_t e0, e1;
     gw_take_launch_events(&e0, &e1);
+    // quads per block: the whole tile (splitting a tile's activation rows over 2 or 4 blocks, each staging the whole
+    // tile, measured slower at the 4B widths even where the tiles alone leave CUs idle: with one block per CU 4.3 ->
+    // 4.8 ms of matmuls per 32-row step, with two (2 quads for matrices of fewer tiles than CUs) 3.9 -> 4.1 ms; kept as
+    // a forced setting)
+    const int nqr = g_kq32_nqr ? g_kq32_nqr : 4, parts = 4 / nqr;
     SkMats mt;
     mt.W[0] = a->blocks;
     mt.N[0] = a->rows;
     mt.col[0] = 0;
-    mt.nb1 = (a->rows + 31) / 32;
+    mt.nb1 = ((a->rows + 255) / 256) * 8 * parts; // (tiles padded to 8: one per XCD)
     mt.W[1] = b ? b->blocks : a->blocks;
     mt.N[1] = b ? b->rows : a->rows;
     mt.col[1] = b ? col_b : 0;
-    const dim3 grid(mt.nb1 + (b ? (b->rows + 31) / 32 : 0));
-    if (a->type == GW_Q4_K)
-        hipExtLaunchKernelGGL((k_gemm_kq32<GW_Q4_K>), grid, dim3(SK_T), 0, s, e0, e1, 0, mt, a->bstride, a->cols, xq, xs, ldx, M,
-                              out, ldo, mode);
-    else
-        hipExtLaunchKernelGGL((k_gemm_kq32<GW_Q6_K>), grid, dim3(SK_T), 0, s, e0, e1, 0, mt, a->bstride, a->cols, xq, xs, ldx, M,
-                              out, ldo, mode);
+    const dim3 grid(mt.nb1 + (b ? ((b->rows + 255) / 256) * 8 * parts : 0));
+#define SK_L(TT, NQ) hipExtLaunchKernelGGL((k_gemm_kq32<TT, NQ>), grid, dim3(SK_T), 0, s, e0, e1, 0, mt, a->bstride, a->cols, xq, \
+                                           xs, ldx, M, out, ldo, mode)
+    if (a->type == GW_Q4_K) {
+        if (nqr == 4) SK_L(GW_Q4_K, 4);
+        else if (nqr == 2) SK_L(GW_Q4_K, 2);
+        else SK_L(GW_Q4_K, 1);
+    } else {
+        if (nqr == 4) SK_L(GW_Q6_K, 4);
+        else if (nqr == 2) SK_L(GW_Q6_K, 2);
+        else SK_L(GW_Q6_K, 1);
+    }
+#undef SK_L
     return (int)hipGetLastError();
 }
 
@@ -1207,6 +1257,13 @@ int gw_q8_block_sums(int32_t *isum, const int8_t *codes, int N, int K, const int
     hipLaunchKernelGGL(k_q8_block_sums, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, (hipStream_t)stream, isum, codes, N,
                        K, xq, M);
     return hipGetLastError() ? RQ_ERR_STATE : RQ_OK;
+}
+
+int gw_kq32_quads(int nqr) {
+    if (nqr != 0 && nqr != 1 && nqr != 2 && nqr != 4) return -1;
+    int prev = g_kq32_nqr;
+    g_kq32_nqr = nqr;
+    return prev;
 }
 
 int gw_matmul_tile_rows(int rows) {

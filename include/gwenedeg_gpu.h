@@ -317,6 +317,11 @@ int gw_topk_rows(const float *logits, int n, int ld, int rows, int k, float *val
  * and test hook with no counterpart in runq.h; results do not depend on it */
 int gw_matmul_tile_rows(int rows);
 
+/* The activation-row quads (of 8 rows) per block of the 9 .. 32-row K-quant GEMM (k_gemm_kq32): 0 the default (4: a
+ * block folds all 32 rows of its weight tile), 1 or 2 forced (more blocks, each folding fewer outputs), 4 forced. Returns the previous setting, or -1 (and changes nothing) for another value. A tuning and
+ * test hook with no counterpart in runq.h; results do not depend on it */
+int gw_kq32_quads(int nqr);
+
 /* Whether each decode GEMV, once its blocks have issued their last weight loads, warms the first weight tiles of the
  * matmul launched after it (the next layer's included) in L2: 1 on (the default), 0 off, a negative value only
  * queries. Returns the previous setting. A tuning and test hook with no counterpart in runq.h; results do not depend
