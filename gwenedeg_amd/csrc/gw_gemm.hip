@@ -594,58 +594,64 @@ __device__ __forceinline__ void kq32_terms(const i32x16 &I, const i32x16 &I1, fl
         Tq[e * 64 + lane] = term;
     }
 }
-template <int TYPE, int NQR>
-__global__ __launch_bounds__(SK_T, 2) void k_gemm_kq32(SkMats mats, int bstride, int K, const int8_t *__restrict__ X,
-                                                    const float *__restrict__ XS, int ldx, int M, float *out, int ldo,
-                                                    int mode) {
+template <int TYPE, int NQR, int SB>
+__global__ __launch_bounds__(SK_T * SB, SB == 1 ? 2 : 1) void k_gemm_kq32(SkMats mats, int bstride, int K,
+                                                                          const int8_t *__restrict__ X,
+                                                                          const float *__restrict__ XS, int ldx, int M,
+                                                                          float *out, int ldo, int mode) {
     constexpr int WST = TYPE == GW_Q4_K ? 160 : 240;            // LDS bytes per weight row (bstride + 16)
     constexpr int PW = TYPE == GW_Q4_K ? GW_Q4K_BYTES / 16 : GW_Q6K_DEV / 16; // 16-byte pieces per weight row
-    constexpr int PARTS = 4 / NQR, NO = NQR * 256;              // blocks per tile, outputs per block
-    __shared__ __align__(16) float Tl[8][NO];                   // group g's term of output o = (r - 4 q0) * 64 + lane
-    __shared__ __align__(16) uint8_t Ws[2][32 * WST];
-    __shared__ __align__(16) uint8_t Xs[2][32 * SK_XR];
-    __shared__ __align__(16) float xsl[2][8][32];               // [group][m]
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6, hi = lane >> 5, r32 = lane & 31;
+    constexpr int PARTS = 4 / NQR, NO = NQR * 256, NT = SK_T * SB; // blocks per tile, outputs per block, threads
+    __shared__ __align__(16) float Tl[8 * SB][NO];              // term of group g of super-block b (row 8 b + g)
+    __shared__ __align__(16) uint8_t Ws[2][SB][32 * WST];
+    __shared__ __align__(16) uint8_t Xs[2][SB][32 * SK_XR];
+    __shared__ __align__(16) float xsl[2][SB][8][32];           // [super-block][group][m]
+    // wave wv: group w = wv % 8 of super-block sb = wv / 8 of the step; thread t stages super-block ts = t / SK_T
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6, w = wv & 7, sb = wv >> 3, hi = lane >> 5, r32 = lane & 31;
+    const int tt = t & (SK_T - 1), ts = t / SK_T;
     const int mi = blockIdx.x >= mats.nb1;
     // block b of its matrix: XCD b % 8, then (b / 8) % PARTS its quads, tile 8 (b / 8 / PARTS) + b % 8
     const int bl = blockIdx.x - (mi ? mats.nb1 : 0), part = (bl >> 3) % PARTS, q0 = part * NQR;
     const int n0 = (((bl >> 3) / PARTS) * 8 + (bl & 7)) * 32, N = mats.N[mi], S = K >> 8;
     if (n0 >= N || 8 * q0 >= M) return; // (the grid's padding to 8 tiles; quads past the last activation row)
+    const int S2 = (S + SB - 1) / SB; // (steps of SB super-blocks)
     const size_t rowb = (size_t)S * bstride;
     out += mats.col[mi];
-    // this thread's staging pieces: W row t / PW piece t % PW (t < 32 PW), X row t / 16 piece t % 16, XS (t < 256);
-    // every thread loads (the others a piece of row 31 again, never staged), so no load sits under a branch
-    const int wr = t / PW < 32 ? t / PW : 31, wp = t % PW, wn = n0 + wr < N ? n0 + wr : N - 1;
+    // this thread's staging pieces of super-block ts of a step: W row tt / PW piece tt % PW (tt < 32 PW), X row tt / 16
+    // piece tt % 16, XS (tt < 256); every thread loads (the others a piece of row 31 again, never staged), so no load
+    // sits under a branch
+    const int wr = tt / PW < 32 ? tt / PW : 31, wp = tt % PW, wn = n0 + wr < N ? n0 + wr : N - 1;
     const uint8_t *wsrc = mats.W[mi] + (size_t)wn * rowb + 16 * wp;
-    const int xr = t >> 4, xm = xr < M ? xr : M - 1;
-    const int8_t *xsrc = X + (size_t)xm * ldx + 16 * (t & 15);
-    const int sm = (t >> 3) < M ? (t >> 3) : M - 1;
-    const float *xssrc = XS + (size_t)sm * (ldx >> 5) + (t & 7);
+    const int xr = tt >> 4, xm = xr < M ? xr : M - 1;
+    const int8_t *xsrc = X + (size_t)xm * ldx + 16 * (tt & 15);
+    const int sm = (tt >> 3) < M ? (tt >> 3) : M - 1;
+    const float *xssrc = XS + (size_t)sm * (ldx >> 5) + (tt & 7);
     auto load = [&](int s) __attribute__((always_inline)) -> SkStage<TYPE> {
-        s = s < S ? s : S - 1; // (past the last super-block: the last again)
+        int b = s * SB + ts;
+        b = b < S ? b : S - 1; // (past the last super-block: the last again)
         SkStage<TYPE> o;
-        o.w = *(const uint4 *)(wsrc + (size_t)s * bstride);
-        o.x = *(const uint4 *)(xsrc + 256 * s);
-        o.xs = xssrc[8 * s];
+        o.w = *(const uint4 *)(wsrc + (size_t)b * bstride);
+        o.x = *(const uint4 *)(xsrc + 256 * b);
+        o.xs = xssrc[8 * b];
         return o;
     };
     auto stage = [&](const SkStage<TYPE> &o, int buf) __attribute__((always_inline)) {
-        if (t < 32 * PW) *(uint4 *)(&Ws[buf][wr * WST + 16 * wp]) = o.w;
-        *(uint4 *)(&Xs[buf][xr * SK_XR + 16 * (t & 15)]) = o.x;
-        if (t < 256) xsl[buf][t & 7][t >> 3] = o.xs;
+        if (tt < 32 * PW) *(uint4 *)(&Ws[buf][ts][wr * WST + 16 * wp]) = o.w;
+        *(uint4 *)(&Xs[buf][ts][xr * SK_XR + 16 * (tt & 15)]) = o.x;
+        if (tt < 256) xsl[buf][ts][tt & 7][tt >> 3] = o.xs;
     };
-    float acc0 = 0.0f, acc1 = 0.0f; // outputs t and t + 512
+    float acc0 = 0.0f, acc1 = 0.0f; // outputs t and t + NT
     const i32x16 z = { 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0 };
-    const uint8_t *wrow_l = &Ws[0][r32 * WST], *xrow_l = &Xs[0][r32 * SK_XR + 32 * w];
+    const uint8_t *wrow_l = &Ws[0][sb][r32 * WST], *xrow_l = &Xs[0][sb][r32 * SK_XR + 32 * w];
     auto step = [&](const SkStage<TYPE> nx, int s) __attribute__((always_inline)) -> SkStage<TYPE> {
-        // nx holds super-block s + 1: staged into the other buffer (its readers, step s - 1, are past the barrier of
-        // step s - 1); returned: the set reloaded with super-block s + 1 + SK_P (values, not references: a set passed
-        // by reference was placed in memory)
+        // step s (super-blocks SB s ..): nx holds step s + 1's pieces: staged into the other buffer (its readers, step
+        // s - 1, are past the barriers of step s - 1); returned: the set reloaded with step s + 1 + SK_P (values, not
+        // references: a set passed by reference was placed in memory)
         const int buf = s & 1;
-        if (s + 1 < S) stage(nx, buf ^ 1);
+        if (s + 1 < S2) stage(nx, buf ^ 1);
         const SkStage<TYPE> nl = load(s + 1 + SK_P);
-        if (s >= S) return nl; // (the last group of four steps past the end: its loads only, uniform)
-        const uint8_t *wb = wrow_l + buf * (32 * WST), *xb = xrow_l + buf * (32 * SK_XR);
+        if (s >= S2) return nl; // (the last group of four steps past the end: its loads only, uniform)
+        const uint8_t *wb = wrow_l + buf * (SB * 32 * WST), *xb = xrow_l + buf * (SB * 32 * SK_XR);
         float f0, f1 = 0.0f;
         int s0 = 0, s1 = 0;
         i32x16 I, I1;
@@ -697,8 +703,8 @@ __global__ __launch_bounds__(SK_T, 2) void k_gemm_kq32(SkMats mats, int bstride,
             f0 = h2f_g((uint16_t)(dw & 0xffffu));
         }
         // this block's quads (uniform branches: a register index must be a constant)
-        const float *xsw = &xsl[buf][w][0];
-        float *Tw = &Tl[w][0];
+        const float *xsw = &xsl[buf][sb][w][0];
+        float *Tw = &Tl[wv][0];
         __syncthreads(); // (every wave's fold of the previous step has read the terms)
         if (NQR == 4) {
             kq32_terms<TYPE, 0>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw);
@@ -719,14 +725,17 @@ __global__ __launch_bounds__(SK_T, 2) void k_gemm_kq32(SkMats mats, int bstride,
             else if (q0 == 2) kq32_terms<TYPE, 2>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw);
             else kq32_terms<TYPE, 3>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw);
         }
-        __syncthreads(); // (the terms of super-block s written; super-block s + 1 staged)
+        __syncthreads(); // (the terms of step s written; step s + 1 staged)
+        const int ng = 8 * (S - s * SB < SB ? S - s * SB : SB); // (a last step past K: its terms not added)
         if (t < NO) {
             #pragma unroll
-            for (int g = 0; g < 8; g++) acc0 = acc0 + Tl[g][t];
+            for (int g = 0; g < 8 * SB; g++)
+                if (g < ng) acc0 = acc0 + Tl[g][t];
         }
-        if (NO > 512) {
+        if (NO > NT) {
             #pragma unroll
-            for (int g = 0; g < 8; g++) acc1 = acc1 + Tl[g][t + 512];
+            for (int g = 0; g < 8 * SB; g++)
+                if (g < ng) acc1 = acc1 + Tl[g][t + NT];
         }
         return nl;
     };
@@ -739,15 +748,15 @@ __global__ __launch_bounds__(SK_T, 2) void k_gemm_kq32(SkMats mats, int bstride,
     __syncthreads();
     // (one exit, at the end of each group of four: a break after each step made the compiler wait for every load in
     // flight at the top of the loop)
-    for (int s0 = 0; s0 < S; s0 += 4) {
+    for (int s0 = 0; s0 < S2; s0 += 4) {
         o1 = step(o1, s0);
         o2 = step(o2, s0 + 1);
         o3 = step(o3, s0 + 2);
         o0 = step(o0, s0 + 3);
     }
     #pragma unroll
-    for (int k = 0; k < (NO + 511) / 512; k++) {
-        const int o = t + 512 * k, r = (o >> 6) + 4 * q0, ln = o & 63;
+    for (int k = 0; k < (NO + NT - 1) / NT; k++) {
+        const int o = t + NT * k, r = (o >> 6) + 4 * q0, ln = o & 63;
         const int m = 8 * (r >> 2) + 4 * (ln >> 5) + (r & 3), n = n0 + (ln & 31);
         if (o < NO && m < M && n < N) {
             float *po = out + (size_t)m * ldo + n;
@@ -1125,6 +1134,7 @@ static int gemm_cus(void) { // the device's compute units
 }
 
 static int g_kq32_nqr; // (0: chosen per launch; 1, 2 or 4: forced, gw_kq32_quads)
+static int g_kq32_sb;  // (0: chosen per launch; 1 or 2 super-blocks per step: forced, gw_kq32_step)
 
 static bool kq32_takes(const GwMat *w, int M) {
     // K-quants, 9 .. 32 rows: the 32-row GEMM with the groups spread over a block's waves (a matrix of 32768 rows or
@@ -1151,17 +1161,21 @@ static int launch_kq32(const GwMat *a, const GwMat *b, int col_b, const int8_t *
     mt.N[1] = b ? b->rows : a->rows;
     mt.col[1] = b ? col_b : 0;
     const dim3 grid(mt.nb1 + (b ? ((b->rows + 255) / 256) * 8 * parts : 0));
-#define SK_L(TT, NQ) hipExtLaunchKernelGGL((k_gemm_kq32<TT, NQ>), grid, dim3(SK_T), 0, s, e0, e1, 0, mt, a->bstride, a->cols, xq, \
-                                           xs, ldx, M, out, ldo, mode)
+    // (two super-blocks per step, 16 waves: half the steps, each twice as long: measured slower on every 4B matrix,
+    // 3.9 -> 4.7 ms of matmuls per 32-row step; kept as a forced setting)
+    const int sbs = g_kq32_sb ? g_kq32_sb : 1;
+#define SK_L(TT, NQ, SS) hipExtLaunchKernelGGL((k_gemm_kq32<TT, NQ, SS>), grid, dim3(SK_T * SS), 0, s, e0, e1, 0, mt, a->bstride, \
+                                               a->cols, xq, xs, ldx, M, out, ldo, mode)
+#define SK_N(TT, SS)                \
+    if (nqr == 4) SK_L(TT, 4, SS);  \
+    else if (nqr == 2) SK_L(TT, 2, SS); \
+    else SK_L(TT, 1, SS);
     if (a->type == GW_Q4_K) {
-        if (nqr == 4) SK_L(GW_Q4_K, 4);
-        else if (nqr == 2) SK_L(GW_Q4_K, 2);
-        else SK_L(GW_Q4_K, 1);
+        if (sbs == 2) { SK_N(GW_Q4_K, 2) } else { SK_N(GW_Q4_K, 1) }
     } else {
-        if (nqr == 4) SK_L(GW_Q6_K, 4);
-        else if (nqr == 2) SK_L(GW_Q6_K, 2);
-        else SK_L(GW_Q6_K, 1);
+        if (sbs == 2) { SK_N(GW_Q6_K, 2) } else { SK_N(GW_Q6_K, 1) }
     }
+#undef SK_N
 #undef SK_L
     return (int)hipGetLastError();
 }
@@ -1257,6 +1271,13 @@ int gw_q8_block_sums(int32_t *isum, const int8_t *codes, int N, int K, const int
     hipLaunchKernelGGL(k_q8_block_sums, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, (hipStream_t)stream, isum, codes, N,
                        K, xq, M);
     return hipGetLastError() ? RQ_ERR_STATE : RQ_OK;
+}
+
+int gw_kq32_step(int sb) {
+    if (sb != 0 && sb != 1 && sb != 2) return -1;
+    int prev = g_kq32_sb;
+    g_kq32_sb = sb;
+    return prev;
 }
 
 int gw_kq32_quads(int nqr) {

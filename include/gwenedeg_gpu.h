@@ -322,6 +322,12 @@ int gw_matmul_tile_rows(int rows);
  * test hook with no counterpart in runq.h; results do not depend on it */
 int gw_kq32_quads(int nqr);
 
+/* The super-blocks per step of the 9 .. 32-row K-quant GEMM (k_gemm_kq32): 0 the default (1), 1 or 2 forced (2: 16
+ * waves, each on one group of one of the step's two super-blocks, half the steps). Returns the previous setting, or -1
+ * (and changes nothing) for another value. A tuning and test hook with no counterpart in runq.h; results do not depend
+ * on it */
+int gw_kq32_step(int sb);
+
 /* Whether each decode GEMV, once its blocks have issued their last weight loads, warms the first weight tiles of the
  * matmul launched after it (the next layer's included) in L2: 1 on (the default), 0 off, a negative value only
  * queries. Returns the previous setting. A tuning and test hook with no counterpart in runq.h; results do not depend
