@@ -4,6 +4,7 @@
 #include <hip/hip_ext.h>
 #include <hip/hip_fp16.h>
 #include <stdint.h>
+#include <type_traits>
 
 #include "gw_internal.h"
 
@@ -1080,6 +1081,161 @@ __global__ __launch_bounds__(256) void k_kq_pad(const uint8_t *__restrict__ src,
     if (b < nblk) dst[i] = k < (size_t)sb ? src[b * sb + k] : 0;
 }
 
+// K-quant GEMM for 9 .. 32 activation rows: k_gemm_kq32's tiles (32 weight rows x 32 activation rows per block) and
+// staging (per super-block, the 32 rows' blocks and the activation rows' codes and scales loaded with coalesced 16-byte
+// loads into double-buffered LDS, four register sets ahead), but 4 waves, each on 16 weight rows x 16 activation rows
+// over all 8 groups: per group one v_mfma_i32_16x16x32_i8 (lane l: A = X row l % 16, B = W row l % 16, bytes
+// 8 (l / 16) .. + 7 of the group; result register r: activation row 4 (l / 16) + r, weight row l % 16), so each lane's
+// weight row is its own and the fold (val = val + term, groups in order) stays in registers: no exchange of terms, one
+// barrier per super-block. Q4_K: a second MFMA against ones gives the sums of x; Q6_K: one MFMA per half-group of 16
+// (the other half's codes zero: its scale differs), I = sc_0 I_0 + sc_1 I_1. Terms as k_gemm_kq32's (kquants.h:86-109,
+// :410-554). Blocks: k_gemm_kq32's (tiles padded to 8 per XCD). M <= 32, K % 256 == 0, mode 1: out = out + val.
+// Measured against k_gemm_kq32 at the 4B widths (32 rows): slower on every matrix (4.8 against 3.9 ms of matmuls per
+// step; half the waves per CU, each with a chain of 8 groups per super-block; with one wave per tile and no staging,
+// scattered 8-byte loads, 6.6 ms; at three blocks per CU it spills), so k_gemm_kq32 is the default
+#define KQ16_T 256
+template <int TYPE>
+struct K16Stage { // one thread's share of a super-block's staging (two 16-byte pieces of W and of X, one scale)
+    uint4 w0, w1, x0, x1;
+    float xs;
+};
+template <int TYPE>
+__global__ __launch_bounds__(KQ16_T, 2) void k_gemm_kq16(SkMats mats, int bstride, int K, const int8_t *__restrict__ X,
+                                                         const float *__restrict__ XS, int ldx, int M, float *out, int ldo,
+                                                         int mode) {
+    typedef int i32x4v __attribute__((ext_vector_type(4)));
+    constexpr int WST = TYPE == GW_Q4_K ? 160 : 240;            // LDS bytes per weight row (bstride + 16)
+    constexpr int PW = TYPE == GW_Q4_K ? GW_Q4K_BYTES / 16 : GW_Q6K_DEV / 16; // 16-byte pieces per weight row
+    __shared__ __align__(16) uint8_t Ws[2][32 * WST];
+    __shared__ __align__(16) uint8_t Xs[2][32 * SK_XR];
+    __shared__ __align__(16) float xsl[2][8][32];               // [group][activation row]
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6, c = lane >> 4, rr = lane & 15;
+    const int wn = 16 * (w & 1), wm = 16 * (w >> 1);            // the wave's weight rows and activation rows in the tile
+    const int mi = blockIdx.x >= mats.nb1, bl = blockIdx.x - (mi ? mats.nb1 : 0);
+    const int n0 = 32 * ((bl >> 3) * 8 + (bl & 7)), N = mats.N[mi], S = K >> 8;
+    if (n0 >= N) return; // (tiles padded to 8 per XCD)
+    const size_t rowb = (size_t)S * bstride;
+    out += mats.col[mi];
+    // staging pieces: W piece t and t + 256 of the tile's 32 PW (row p / PW, piece p % PW; pieces past 32 PW: row 31's
+    // again, never staged), X piece t and t + 256 (row p / 16, piece p % 16), XS t (row t / 8, group t % 8)
+    const int p1 = t + KQ16_T;
+    const int wr0 = t / PW, wr1 = p1 / PW < 32 ? p1 / PW : 31, wp0 = t % PW, wp1 = p1 % PW;
+    const uint8_t *ws0 = mats.W[mi] + (size_t)(n0 + wr0 < N ? n0 + wr0 : N - 1) * rowb + 16 * wp0;
+    const uint8_t *ws1 = mats.W[mi] + (size_t)(n0 + wr1 < N ? n0 + wr1 : N - 1) * rowb + 16 * wp1;
+    const int xr0 = t >> 4, xr1 = xr0 + 16;
+    const int8_t *xs0 = X + (size_t)(xr0 < M ? xr0 : M - 1) * ldx + 16 * (t & 15);
+    const int8_t *xs1 = X + (size_t)(xr1 < M ? xr1 : M - 1) * ldx + 16 * (t & 15);
+    const int sm = (t >> 3) < M ? (t >> 3) : M - 1;
+    const float *xssrc = XS + (size_t)sm * (ldx >> 5) + (t & 7);
+    auto load = [&](int s) __attribute__((always_inline)) -> K16Stage<TYPE> {
+        s = s < S ? s : S - 1; // (past the last super-block: the last again)
+        K16Stage<TYPE> o;
+        o.w0 = *(const uint4 *)(ws0 + (size_t)s * bstride);
+        o.w1 = *(const uint4 *)(ws1 + (size_t)s * bstride);
+        o.x0 = *(const uint4 *)(xs0 + 256 * s);
+        o.x1 = *(const uint4 *)(xs1 + 256 * s);
+        o.xs = xssrc[8 * s];
+        return o;
+    };
+    auto stage = [&](const K16Stage<TYPE> &o, int buf) __attribute__((always_inline)) {
+        *(uint4 *)(&Ws[buf][wr0 * WST + 16 * wp0]) = o.w0;
+        if (p1 < 32 * PW) *(uint4 *)(&Ws[buf][wr1 * WST + 16 * wp1]) = o.w1;
+        *(uint4 *)(&Xs[buf][xr0 * SK_XR + 16 * (t & 15)]) = o.x0;
+        *(uint4 *)(&Xs[buf][xr1 * SK_XR + 16 * (t & 15)]) = o.x1;
+        xsl[buf][t & 7][t >> 3] = o.xs;
+    };
+    float acc0 = 0.0f, acc1 = 0.0f, acc2 = 0.0f, acc3 = 0.0f; // activation rows wm + 4 c + r, weight row n0 + wn + rr
+    const i32x4v z = { 0, 0, 0, 0 };
+    const uint8_t *wrow_l = &Ws[0][(wn + rr) * WST];
+    const uint8_t *xrow_l = &Xs[0][(wm + rr) * SK_XR + 8 * c];
+    auto step = [&](const K16Stage<TYPE> nx, int s) __attribute__((always_inline)) -> K16Stage<TYPE> {
+        // nx holds super-block s + 1: staged into the other buffer (its readers, step s - 1, are past the barrier of
+        // step s - 1); returned: the set reloaded with super-block s + 1 + SK_P
+        const int buf = s & 1;
+        if (s + 1 < S) stage(nx, buf ^ 1);
+        const K16Stage<TYPE> nl = load(s + 1 + SK_P);
+        if (s >= S) return nl; // (the last group of four steps past the end: its loads only, uniform)
+        const uint8_t *wb = wrow_l + buf * (32 * WST), *xb = xrow_l + buf * (32 * SK_XR);
+        const float *xsb = &xsl[buf][0][wm + 4 * c];
+        if constexpr (TYPE == GW_Q4_K) {
+            const uint4 hd = *(const uint4 *)wb;
+            const float d = h2f_g((uint16_t)(hd.x & 0xffffu)), dm = h2f_g((uint16_t)(hd.x >> 16));
+            #pragma unroll
+            for (int g = 0; g < 8; g++) {
+                const uint2 xg = *(const uint2 *)(xb + 32 * g);
+                const uint2 qq = *(const uint2 *)(wb + 16 + 32 * (g >> 1) + 8 * c);
+                const int sh = 4 * (g & 1);
+                const i64 a = (i64)xg.x | (i64)xg.y << 32;
+                const i64 b = (i64)((qq.x >> sh) & 0x0F0F0F0Fu) | (i64)((qq.y >> sh) & 0x0F0F0F0Fu) << 32;
+                const i32x4v I = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
+                const i32x4v I1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, (i64)0x0101010101010101ll, z, 0, 0, 0);
+                const int bs = 8 * (g & 3);
+                const int bw = (int)(((g < 4 ? hd.y : hd.z) >> bs) & 0xffu), bw4 = (int)(((g < 4 ? hd.z : hd.w) >> bs) & 0xffu);
+                const int bm4 = (int)((hd.y >> bs) & 0xffu);
+                const int scj = g < 4 ? bw & 63 : (bw4 & 15) | (bm4 >> 6) << 4;
+                const int mj = g < 4 ? bw4 & 63 : (bw4 >> 4) | (bw >> 6) << 4;
+                const float f0 = d * (float)scj, f1 = dm * (float)mj;
+                const float4 x4 = *(const float4 *)(xsb + 32 * g);
+                acc0 = acc0 + ((f0 * x4.x) * (float)I[0] - f1 * (x4.x * (float)I1[0]));
+                acc1 = acc1 + ((f0 * x4.y) * (float)I[1] - f1 * (x4.y * (float)I1[1]));
+                acc2 = acc2 + ((f0 * x4.z) * (float)I[2] - f1 * (x4.z * (float)I1[2]));
+                acc3 = acc3 + ((f0 * x4.w) * (float)I[3] - f1 * (x4.w * (float)I1[3]));
+            }
+        } else {
+            const uint4 scv = *(const uint4 *)(wb + 192);
+            const float d = h2f_g((uint16_t)(*(const uint32_t *)(wb + 208) & 0xffffu));
+            #pragma unroll
+            for (int g = 0; g < 8; g++) {
+                const int nn = g >> 2, p = g & 3, sl = 4 * (p >> 1), shh = 2 * p;
+                const uint2 xg = *(const uint2 *)(xb + 32 * g);
+                const uint2 lo = *(const uint2 *)(wb + 64 * nn + 32 * (p & 1) + 8 * c);
+                const uint2 hq = *(const uint2 *)(wb + 128 + 32 * nn + 8 * c);
+                auto code = [&](uint32_t lw, uint32_t hw) -> uint32_t { // 4 codes q - 32 (q = nibble | 2 bits of qh << 4)
+                    uint32_t q = ((lw >> sl) & 0x0F0F0F0Fu) | (((hw >> shh) & 0x03030303u) << 4);
+                    uint32_t f = q ^ 0x20202020u, sg = f & 0x20202020u;
+                    return f | (sg << 1) | (sg << 2);
+                };
+                const i64 a = (i64)xg.x | (i64)xg.y << 32;
+                const i64 b = (i64)code(lo.x, hq.x) | (i64)code(lo.y, hq.y) << 32;
+                const i64 b0 = c < 2 ? b : 0, b1 = c < 2 ? 0 : b; // (half-group 0: bytes 0 .. 15 of the group)
+                const i32x4v I0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b0, z, 0, 0, 0);
+                const i32x4v I1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b1, z, 0, 0, 0);
+                const uint32_t scw = (g >> 1) == 0 ? scv.x : (g >> 1) == 1 ? scv.y : (g >> 1) == 2 ? scv.z : scv.w;
+                const int sb = 16 * (g & 1);
+                const int s0 = (int)(int8_t)((scw >> sb) & 0xffu), s1 = (int)(int8_t)((scw >> (sb + 8)) & 0xffu);
+                const float4 x4 = *(const float4 *)(xsb + 32 * g);
+                acc0 = acc0 + (d * x4.x) * (float)(s0 * I0[0] + s1 * I1[0]);
+                acc1 = acc1 + (d * x4.y) * (float)(s0 * I0[1] + s1 * I1[1]);
+                acc2 = acc2 + (d * x4.z) * (float)(s0 * I0[2] + s1 * I1[2]);
+                acc3 = acc3 + (d * x4.w) * (float)(s0 * I0[3] + s1 * I1[3]);
+            }
+        }
+        __syncthreads(); // (super-block s + 1 staged; this buffer's readers done)
+        return nl;
+    };
+    static_assert(SK_P == 4, "four register sets");
+    K16Stage<TYPE> o0 = load(0), o1 = load(1), o2 = load(2), o3 = load(3);
+    stage(o0, 0);
+    o0 = load(4);
+    __syncthreads();
+    for (int s0 = 0; s0 < S; s0 += 4) { // (one exit per group of four steps)
+        o1 = step(o1, s0);
+        o2 = step(o2, s0 + 1);
+        o3 = step(o3, s0 + 2);
+        o0 = step(o0, s0 + 3);
+    }
+    const int n = n0 + wn + rr;
+    const float accs[4] = { acc0, acc1, acc2, acc3 };
+    #pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int m = wm + 4 * c + r;
+        if (m < M && n < N) {
+            float *po = out + (size_t)m * ldo + n;
+            *po = mode == 1 ? *po + accs[r] : accs[r];
+        }
+    }
+}
+
 extern "C" {
 
 int gw_k_kq_pad(const uint8_t *src, size_t nblk, int sbytes, int dbytes, uint8_t *dst, hipStream_t s) {
@@ -1135,6 +1291,7 @@ static int gemm_cus(void) { // the device's compute units
 
 static int g_kq32_nqr; // (0: chosen per launch; 1, 2 or 4: forced, gw_kq32_quads)
 static int g_kq32_sb;  // (0: chosen per launch; 1 or 2 super-blocks per step: forced, gw_kq32_step)
+static int g_kq16;     // (9 .. 32 K-quant rows: 0 k_gemm_kq32, 1 k_gemm_kq16; gw_kq_small_kernel)
 
 static bool kq32_takes(const GwMat *w, int M) {
     // K-quants, 9 .. 32 rows: the 32-row GEMM with the groups spread over a block's waves (a matrix of 32768 rows or
@@ -1147,6 +1304,24 @@ static int launch_kq32(const GwMat *a, const GwMat *b, int col_b, const int8_t *
     // a, and b (NULL: none; same type and width as a) written from column col_b of out
     hipEvent_t e0, e1;
     gw_take_launch_events(&e0, &e1);
+    if (g_kq16) { // 16 x 16 sub-tiles per wave, the fold in registers
+        SkMats m16;
+        m16.W[0] = a->blocks;
+        m16.N[0] = a->rows;
+        m16.col[0] = 0;
+        m16.nb1 = ((a->rows + 255) / 256) * 8; // (32-row tiles padded to 8, one per XCD)
+        m16.W[1] = b ? b->blocks : a->blocks;
+        m16.N[1] = b ? b->rows : a->rows;
+        m16.col[1] = b ? col_b : 0;
+        const dim3 g16(m16.nb1 + (b ? ((b->rows + 255) / 256) * 8 : 0));
+        if (a->type == GW_Q4_K)
+            hipExtLaunchKernelGGL(k_gemm_kq16<GW_Q4_K>, g16, dim3(KQ16_T), 0, s, e0, e1, 0, m16, a->bstride, a->cols, xq, xs, ldx,
+                                  M, out, ldo, mode);
+        else
+            hipExtLaunchKernelGGL(k_gemm_kq16<GW_Q6_K>, g16, dim3(KQ16_T), 0, s, e0, e1, 0, m16, a->bstride, a->cols, xq, xs, ldx,
+                                  M, out, ldo, mode);
+        return (int)hipGetLastError();
+    }
     // quads per block: the whole tile (splitting a tile's activation rows over 2 or 4 blocks, each staging the whole
     // tile, measured slower at the 4B widths even where the tiles alone leave CUs idle: with one block per CU 4.3 ->
     // 4.8 ms of matmuls per 32-row step, with two (2 quads for matrices of fewer tiles than CUs) 3.9 -> 4.1 ms; kept as
@@ -1271,6 +1446,13 @@ int gw_q8_block_sums(int32_t *isum, const int8_t *codes, int N, int K, const int
     hipLaunchKernelGGL(k_q8_block_sums, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, (hipStream_t)stream, isum, codes, N,
                        K, xq, M);
     return hipGetLastError() ? RQ_ERR_STATE : RQ_OK;
+}
+
+int gw_kq_small_kernel(int kq16) {
+    if (kq16 != 0 && kq16 != 1) return -1;
+    int prev = g_kq16;
+    g_kq16 = kq16;
+    return prev;
 }
 
 int gw_kq32_step(int sb) {

@@ -317,6 +317,12 @@ int gw_topk_rows(const float *logits, int n, int ld, int rows, int k, float *val
  * and test hook with no counterpart in runq.h; results do not depend on it */
 int gw_matmul_tile_rows(int rows);
 
+/* The kernel of the 9 .. 32-row K-quant GEMM (Q4_K / Q6_K, batched decode rows): 0 k_gemm_kq32 (32-row tiles, the
+ * groups spread over 8 waves, the terms exchanged in LDS; the default), 1 k_gemm_kq16 (each wave on 16 weight rows x 16
+ * activation rows over all of K, the fold in registers). Returns the previous setting, or -1 (and changes
+ * nothing) for another value. A tuning and test hook with no counterpart in runq.h; results do not depend on it */
+int gw_kq_small_kernel(int kq16);
+
 /* The activation-row quads (of 8 rows) per block of the 9 .. 32-row K-quant GEMM (k_gemm_kq32): 0 the default (4: a
  * block folds all 32 rows of its weight tile), 1 or 2 forced (more blocks, each folding fewer outputs), 4 forced. Returns the previous setting, or -1 (and changes nothing) for another value. A tuning and
  * test hook with no counterpart in runq.h; results do not depend on it */

@@ -139,9 +139,9 @@ def test_kq_matmul_bitexact(dev, typ, M, tile):
 @pytest.mark.parametrize("typ", [12, 14])
 @pytest.mark.parametrize("K", [2560, 9728])
 @pytest.mark.parametrize("M", [9, 20, 32])
-@pytest.mark.parametrize("nqr,sb", [(0, 0), (1, 2), (2, 2), (4, 1), (2, 1)])
-def test_kq32_at_the_4b_widths(dev, typ, K, M, nqr, sb):
-    """the 9..32-row K-quant GEMM (k_gemm_kq32: Q4_K, Q6_K) at the Qwen3-4B widths (K = 2560: q / k / v / gate / up,
+@pytest.mark.parametrize("kq16,nqr,sb", [(1, 0, 0), (0, 0, 0), (0, 1, 2), (0, 2, 2), (0, 4, 1), (0, 2, 1)])
+def test_kq32_at_the_4b_widths(dev, typ, K, M, kq16, nqr, sb):
+    """the 9..32-row K-quant GEMMs (k_gemm_kq16 and k_gemm_kq32: Q4_K, Q6_K) at the Qwen3-4B widths (K = 2560: q / k / v / gate / up,
     K = 9728: down), 1,024 weight rows (1,008: a partial last tile), each split of a tile's activation rows over blocks
     (nqr quads of 8 per block, 0: chosen by the launch) and step width (sb super-blocks per step, 0: chosen): its load
     pipeline in steady state (10 and 38 super-blocks per row against its look-ahead of five), bit for bit against the
@@ -150,7 +150,7 @@ def test_kq32_at_the_4b_widths(dev, typ, K, M, nqr, sb):
     from oracle import oracle as orc
     from gwenedeg_amd import synth
     rng = np.random.default_rng(typ * 100 + M + K)
-    N = 1008 if nqr == 2 else 1024
+    N = 1008 if nqr == 2 or kq16 else 1024
     sl = synth.synth_library()
     rb = sl.gw_synth_row_bytes(typ, K)
     blocks = np.zeros((N, rb), np.uint8)
@@ -162,13 +162,14 @@ def test_kq32_at_the_4b_widths(dev, typ, K, M, nqr, sb):
     ref = orc.kq_matmul(typ, blocks, xq, xs, N, K)
     out = torch.zeros((M, N), dtype=torch.float32, device="cuda")
     Bd, XQ, XS = (_to_dev(torch, a) for a in (blocks.reshape(-1), xq, xs))
-    prev, prev_sb = gw.lib.gw_kq32_quads(nqr), gw.lib.gw_kq32_step(sb)
+    prev, prev_sb, prev_k = gw.lib.gw_kq32_quads(nqr), gw.lib.gw_kq32_step(sb), gw.lib.gw_kq_small_kernel(kq16)
     try:
         assert gw.lib.gw_kq_matmul(out.data_ptr(), typ, Bd.data_ptr(), N, K, XQ.data_ptr(), XS.data_ptr(), M, None) == 0
         torch.cuda.synchronize()
     finally:
         gw.lib.gw_kq32_quads(prev)
         gw.lib.gw_kq32_step(prev_sb)
+        gw.lib.gw_kq_small_kernel(prev_k)
     got = out.cpu().numpy()
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"max diff {np.abs(got - ref).max()}"
 
