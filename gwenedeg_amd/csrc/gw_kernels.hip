@@ -189,16 +189,23 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
                                                uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc,
                                                float *__restrict__ part, int pstride) {
     // V staged in its own LDS buffer for NQ = 16 (prefill row blocks), else into the K buffer once the scores are done
-    // (the block's LDS stays under half a CU's: two blocks per CU); its loads are issued with K's either way
+    // (the block's LDS stays under half a CU's: two blocks per CU); its loads are issued with K's either way.
+    // One LDS block: the query vectors, scores and lengths first (below 64 KiB, so every read of them is a base
+    // register plus an immediate offset), then the K tiles, then (NQ = 16) V. V rows at a fixed 256-byte stride,
+    // whatever hd: the o chains' reads are immediate offsets from one pointer
     constexpr bool VL = NQ == 16;
-    __shared__ __align__(16) uint8_t ks[16 * ATT_KTILE];
-    __shared__ __align__(16) uint8_t vs[VL ? 16 * 32 * ATT_HDMAX : 16];
-    __shared__ __align__(16) float qs[NQ * ATT_QS];
-    __shared__ float S[NQ][ATT_P];
-    __shared__ int np[NQ];
+    constexpr int QS_B = NQ * ATT_QS * 4, S_B = NQ * ATT_P * 4, KS_OFF = (QS_B + S_B + NQ * 4 + 15) & ~15;
+    __shared__ __align__(16) uint8_t lds[KS_OFF + 16 * ATT_KTILE + (VL ? ATT_P * 2 * ATT_HDMAX : 0)];
+    float *const qs = (float *)lds;
+    float (*const S)[ATT_P] = (float (*)[ATT_P])(lds + QS_B);
+    int *const np = (int *)(lds + QS_B + S_B);
+    uint8_t *const ks = lds + KS_OFF;
+    uint8_t *const vs = lds + KS_OFF + 16 * ATT_KTILE; // (VL only)
+    static_assert(QS_B + S_B + NQ * 4 <= 65536, "scores below 64 KiB");
+    static_assert(16 * ATT_KTILE >= ATT_P * 2 * ATT_HDMAX, "V rows at 256 bytes fit the K buffer");
     int4 it = items[blockIdx.x];
     int r0 = it.x, nr = it.y, g = it.z, kb = it.w, kv_mul = nh / nkv, nq = nr * kv_mul, t = threadIdx.x;
-    const int TB = 32 * hd, nchk = hd / 32;
+    const int TB = 32 * hd, nchk = hd / 32, vmg = (65536 + nchk - 1) / nchk; // (x / nchk = x vmg >> 16, x < 2^15)
     const uint8_t *K = (const uint8_t *)(kc[r0] + ((size_t)kb * nkv + g) * ATT_P * hd);
     const uint8_t *V = (const uint8_t *)(vc[r0] + ((size_t)kb * nkv + g) * ATT_P * hd);
     int nmx = pos[r0 + nr - 1] + 1 - kb * ATT_P;
@@ -221,11 +228,16 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
         int n = t < nq ? pos[r0 + t / kv_mul] + 1 - kb * ATT_P : 0;
         np[t] = n < 0 ? 0 : n < ATT_P ? n : ATT_P;
     }
+    // (V: 16-byte piece o of the block's rows, position o / (2 hd), into that position's 256-byte LDS row)
+    auto vrow = [&](int o) __attribute__((always_inline)) -> int {
+        const int pp = (o >> 6) * vmg >> 16;
+        return pp * 2 * ATT_HDMAX + (o - pp * 64 * nchk);
+    };
 #define ATT_ST(k, KR, VR)                                                                                                \
     if ((t + ATT_TH * k) * 16 < nbytes) {                                                                            \
         int o = (t + ATT_TH * k) * 16, tile = o / TB, w = o % TB;                                                     \
         *(uint4 *)(ks + tile * ATT_KTILE + (w >> 10) * ATT_KROW + (w & 1023)) = KR;                                   \
-        if (VL) *(uint4 *)(vs + o) = VR; /* (V: position p's row at p hd 2 bytes) */                                  \
+        if (VL) *(uint4 *)(vs + vrow(o)) = VR;                                                                        \
     }
     ATT_ST(0, k0, v0) ATT_ST(1, k1, v1) ATT_ST(2, k2, v2) ATT_ST(3, k3, v3)
 #undef ATT_ST
@@ -272,9 +284,9 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
         }
     }
     __syncthreads();
-    if (!VL) { // V into the K buffer (its readers are done), position p's row at p hd 2 bytes
+    if (!VL) { // V into the K buffer (its readers are done), position p's row at p 256 bytes
 #define ATT_SV(k, VR)                                                                                                    \
-        if ((t + ATT_TH * k) * 16 < nbytes) *(uint4 *)(ks + (t + ATT_TH * k) * 16) = VR;
+        if ((t + ATT_TH * k) * 16 < nbytes) *(uint4 *)(ks + vrow((t + ATT_TH * k) * 16)) = VR;
         ATT_SV(0, v0) ATT_SV(1, v1) ATT_SV(2, v2) ATT_SV(3, v3)
 #undef ATT_SV
     }
@@ -321,14 +333,14 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
             int p = 0;
             float o0 = 0.0f, o1 = 0.0f;
             const uint32_t *vb = (const uint32_t *)((VL ? vs : ks) + i0 * 2);
-            const int rs = hd >> 1; // (uint32 words per position's row)
+            constexpr int rs = ATT_HDMAX / 2; // (uint32 words per position's LDS row)
             constexpr int PB = VL ? 16 : 8; // (8: 64 registers, two blocks per CU)
             uint32_t va[PB], vbb[PB];
             float ea[PB], eb[PB];
             auto ld = [&](uint32_t (&vv)[PB], float (&ee)[PB], int q0) {
                 #pragma unroll
                 for (int u = 0; u < PB; u++) {
-                    vv[u] = vb[(size_t)(q0 + u) * rs];
+                    vv[u] = vb[(q0 + u) * rs];
                     ee[u] = S[v][q0 + u];
                 }
             };
@@ -357,7 +369,7 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
                 }
             }
             for (; p < n; p++) {
-                uint32_t vv = vb[(size_t)p * rs];
+                uint32_t vv = vb[p * rs];
                 float e = S[v][p];
                 o0 = __builtin_fmaf(e, KB ? bf2f(vv & 0xffffu) : h2f((uint16_t)(vv & 0xffff)), o0);
                 o1 = __builtin_fmaf(e, KB ? bf2f(vv >> 16) : h2f((uint16_t)(vv >> 16)), o1);
