@@ -156,6 +156,12 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// lane Q's value of each lane's quad of 4 neighbouring lanes (a DPP quad_perm move: no LDS, no address)
+template <int Q>
+__device__ __forceinline__ float quad_lane(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), Q * 0x55, 0xF, 0xF, false));
+}
+
 // rmsnorm scale of n floats in LDS (n % 128 == 0), computed by lanes 0..15 of the calling wave, returned to all lanes
 // of that wave: forward.c:886-901 in the reference's compiled order (lane j: an fma chain over x[j], x[j + 16], ...,
 // the tree +8 +4 +2 +1, t = fma(ss, 1/n, 1e-6), rsqrt_ref(t)); n % 16 == 0. The chain's next 16 LDS reads are

@@ -205,7 +205,8 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
     static_assert(16 * ATT_KTILE >= ATT_P * 2 * ATT_HDMAX, "V rows at 256 bytes fit the K buffer");
     int4 it = items[blockIdx.x];
     int r0 = it.x, nr = it.y, g = it.z, kb = it.w, kv_mul = nh / nkv, nq = nr * kv_mul, t = threadIdx.x;
-    const int TB = 32 * hd, nchk = hd / 32, vmg = (65536 + nchk - 1) / nchk; // (x / nchk = x vmg >> 16, x < 2^15)
+    // (x / nchk = x vmg >> 16 and x / kv_mul = x kmg >> 16 for the x < 2^10 they divide here)
+    const int TB = 32 * hd, nchk = hd / 32, vmg = (65536 + nchk - 1) / nchk, kmg = (65536 + kv_mul - 1) / kv_mul;
     const uint8_t *K = (const uint8_t *)(kc[r0] + ((size_t)kb * nkv + g) * ATT_P * hd);
     const uint8_t *V = (const uint8_t *)(vc[r0] + ((size_t)kb * nkv + g) * ATT_P * hd);
     int nmx = pos[r0 + nr - 1] + 1 - kb * ATT_P;
@@ -221,11 +222,11 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
     ATT_LD(0, k0, v0) ATT_LD(1, k1, v1) ATT_LD(2, k2, v2) ATT_LD(3, k3, v3)
 #undef ATT_LD
     for (int e = t; e < NQ * ATT_QS; e += ATT_TH) { // (padding and vectors past nq: zeros)
-        int v = e / ATT_QS, c = e % ATT_QS / ATT_QC, i = e % ATT_QC, d = 32 * c + i;
-        qs[e] = v < nq && i < 32 && d < hd ? qkv[(size_t)(r0 + v / kv_mul) * ldqkv + (size_t)(g * kv_mul + v % kv_mul) * hd + d] : 0.0f;
+        int v = e / ATT_QS, c = e % ATT_QS / ATT_QC, i = e % ATT_QC, d = 32 * c + i, vr = v * kmg >> 16;
+        qs[e] = v < nq && i < 32 && d < hd ? qkv[(size_t)(r0 + vr) * ldqkv + (size_t)(g * kv_mul + v - vr * kv_mul) * hd + d] : 0.0f;
     }
     if (t < NQ) {
-        int n = t < nq ? pos[r0 + t / kv_mul] + 1 - kb * ATT_P : 0;
+        int n = t < nq ? pos[r0 + (t * kmg >> 16)] + 1 - kb * ATT_P : 0;
         np[t] = n < 0 ? 0 : n < ATT_P ? n : ATT_P;
     }
     // (V: 16-byte piece o of the block's rows, position o / (2 hd), into that position's 256-byte LDS row)
@@ -235,7 +236,7 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
     };
 #define ATT_ST(k, KR, VR)                                                                                                \
     if ((t + ATT_TH * k) * 16 < nbytes) {                                                                            \
-        int o = (t + ATT_TH * k) * 16, tile = o / TB, w = o % TB;                                                     \
+        int o = (t + ATT_TH * k) * 16, tile = ((t >> 6) + 16 * k) * vmg >> 16, w = o - tile * TB;                    \
         *(uint4 *)(ks + tile * ATT_KTILE + (w >> 10) * ATT_KROW + (w & 1023)) = KR;                                   \
         if (VL) *(uint4 *)(vs + vrow(o)) = VR;                                                                        \
     }
@@ -275,7 +276,7 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
         }
         #pragma unroll
         for (int v = 0; v < NQ; v++) {
-            float c1 = __shfl_down(acc[v], 1), c2 = __shfl_down(acc[v], 2), c3 = __shfl_down(acc[v], 3);
+            float c1 = quad_lane<1>(acc[v]), c2 = quad_lane<2>(acc[v]), c3 = quad_lane<3>(acc[v]); // (chunks of lane c = 0)
             float a = acc[v];
             if (nchk > 1) a = a + c1;
             if (nchk > 2) a = a + c2;
@@ -523,7 +524,7 @@ __global__ __launch_bounds__(ATD_T) void k_attn_decode(const float *__restrict__
             acc = __builtin_fmaf(q4.w, kf[i + 3], acc);
         }
     }
-    float c1 = __shfl_down(acc, 1), c2 = __shfl_down(acc, 2), c3 = __shfl_down(acc, 3);
+    float c1 = quad_lane<1>(acc), c2 = quad_lane<2>(acc), c3 = quad_lane<3>(acc);
     float a = acc;
     if (NCH > 1) a = a + c1;
     if (NCH > 2) a = a + c2;
