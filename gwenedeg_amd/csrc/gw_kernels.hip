@@ -192,16 +192,20 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
     // (the block's LDS stays under half a CU's: two blocks per CU); its loads are issued with K's either way.
     // One LDS block: the query vectors, scores and lengths first (below 64 KiB, so every read of them is a base
     // register plus an immediate offset), then the K tiles, then (NQ = 16) V. V rows at a fixed 256-byte stride,
-    // whatever hd: the o chains' reads are immediate offsets from one pointer
-    constexpr bool VL = NQ == 16;
-    constexpr int QS_B = NQ * ATT_QS * 4, S_B = NQ * ATT_P * 4, KS_OFF = (QS_B + S_B + NQ * 4 + 15) & ~15;
+    // whatever hd: the o chains' reads are immediate offsets from one pointer. Up to 4 vectors (SE), the exponentials
+    // go to their own array E, written by all 16 waves, and the sums l are added while the o chains run
+    constexpr bool VL = NQ == 16, SE = NQ <= 4;
+    constexpr int QS_B = NQ * ATT_QS * 4, S_B = NQ * ATT_P * 4, E_B = SE ? S_B : 0;
+    constexpr int KS_OFF = (QS_B + S_B + E_B + NQ * 4 + 15) & ~15;
     __shared__ __align__(16) uint8_t lds[KS_OFF + 16 * ATT_KTILE + (VL ? ATT_P * 2 * ATT_HDMAX : 0)];
     float *const qs = (float *)lds;
     float (*const S)[ATT_P] = (float (*)[ATT_P])(lds + QS_B);
-    int *const np = (int *)(lds + QS_B + S_B);
+    float (*const E)[ATT_P] = (float (*)[ATT_P])(lds + QS_B + (SE ? S_B : 0)); // (the exponentials; S itself otherwise)
+    int *const np = (int *)(lds + QS_B + S_B + E_B);
     uint8_t *const ks = lds + KS_OFF;
     uint8_t *const vs = lds + KS_OFF + 16 * ATT_KTILE; // (VL only)
-    static_assert(QS_B + S_B + NQ * 4 <= 65536, "scores below 64 KiB");
+    static_assert(QS_B + S_B + E_B + NQ * 4 <= 65536, "scores below 64 KiB");
+    static_assert(!SE || 2 * sizeof(lds) <= 160 * 1024, "two blocks per CU");
     static_assert(16 * ATT_KTILE >= ATT_P * 2 * ATT_HDMAX, "V rows at 256 bytes fit the K buffer");
     int4 it = items[blockIdx.x];
     int r0 = it.x, nr = it.y, g = it.z, kb = it.w, kv_mul = nh / nkv, nq = nr * kv_mul, t = threadIdx.x;
@@ -291,9 +295,23 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
         ATT_SV(0, v0) ATT_SV(1, v1) ATT_SV(2, v2) ATT_SV(3, v3)
 #undef ATT_SV
     }
-    // softmax: wave v takes vector v
     int wave = t >> 6, lane = t & 63;
-    if (wave < nq && np[wave] > 0) {
+    // (a vector's part of block kb: m, l after its hd values o)
+    auto mlp = [&](int v) __attribute__((always_inline)) -> float * {
+        return part + ((size_t)(r0 + v / kv_mul) * nh + g * kv_mul + v % kv_mul) * pstride + (size_t)kb * (hd + 2) + hd;
+    };
+    if (SE) { // softmax: wave w takes vector w & 3 (its max over the block, each of its 4 waves alike), positions
+              // 64 (w >> 2) + lane: E = exp_att(s - m); l is added after the barrier, beside the o chains
+        const int v = wave & 3, p = 64 * (wave >> 2) + lane;
+        if (v < nq && np[v] > 0) {
+            const int n = np[v];
+            float m = -3.402823466e38f;
+            for (int q = lane; q < n; q += 64) m = fmaxf(m, S[v][q]);
+            m = wave_max(m);
+            if (p < n) E[v][p] = exp_att(S[v][p] - m);
+            if (wave < 4 && lane == 0) mlp(v)[0] = m;
+        }
+    } else if (wave < nq && np[wave] > 0) { // softmax: wave v takes vector v
         int v = wave, n = np[v];
         float m = -3.402823466e38f;
         for (int p = lane; p < n; p += 64) m = fmaxf(m, S[v][p]);
@@ -318,13 +336,32 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
             s = s + o;
         }
         if (lane == 0) {
-            int row = r0 + v / kv_mul, h = g * kv_mul + v % kv_mul;
-            float *ml = part + ((size_t)row * nh + h) * pstride + (size_t)kb * (hd + 2) + hd;
+            float *ml = mlp(v);
             ml[0] = m;
             ml[1] = s;
         }
     }
     __syncthreads();
+    if (SE && wave >= 4 && wave < 8 && wave - 4 < nq && np[wave - 4] > 0) { // l of vector wave - 4: 16 lane chains
+        const int v = wave - 4, n = np[v];                                  // over p = lane (mod 16), then the tree
+        float s = 0.0f;
+        if (lane < 16) {
+            int p = lane;
+            for (; p + 48 < n; p += 64) {
+                float e0 = E[v][p], e1 = E[v][p + 16], e2 = E[v][p + 32], e3 = E[v][p + 48];
+                s = s + e0;
+                s = s + e1;
+                s = s + e2;
+                s = s + e3;
+            }
+            for (; p < n; p += 16) s = s + E[v][p];
+        }
+        for (int w = 8; w >= 1; w >>= 1) {
+            float o = __shfl_down(s, w);
+            s = s + o;
+        }
+        if (lane == 0) mlp(v)[1] = s;
+    }
     // o: lane (vector v = wave, dim pair d2): the chains over the positions in order, V pairs from LDS, two register
     // sets of PB positions' loads alternating (a copy between sets would wait for the loads)
     {
@@ -342,7 +379,7 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
                 #pragma unroll
                 for (int u = 0; u < PB; u++) {
                     vv[u] = vb[(q0 + u) * rs];
-                    ee[u] = S[v][q0 + u];
+                    ee[u] = E[v][q0 + u];
                 }
             };
             auto fold = [&](const uint32_t (&vv)[PB], const float (&ee)[PB]) {
@@ -371,7 +408,7 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
             }
             for (; p < n; p++) {
                 uint32_t vv = vb[p * rs];
-                float e = S[v][p];
+                float e = E[v][p];
                 o0 = __builtin_fmaf(e, KB ? bf2f(vv & 0xffffu) : h2f((uint16_t)(vv & 0xffff)), o0);
                 o1 = __builtin_fmaf(e, KB ? bf2f(vv >> 16) : h2f((uint16_t)(vv >> 16)), o1);
             }
