@@ -156,6 +156,8 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+#define GW_RSRC_DW3 0x00020000 // buffer descriptor word 3 of gfx9-family targets (raw loads; out-of-range reads give 0)
+
 // lane Q's value of each lane's quad of 4 neighbouring lanes (a DPP quad_perm move: no LDS, no address)
 template <int Q>
 __device__ __forceinline__ float quad_lane(float x) {

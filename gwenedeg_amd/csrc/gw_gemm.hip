@@ -7,6 +7,7 @@
 #include <type_traits>
 
 #include "gw_internal.h"
+#include "gw_device.h"
 
 __device__ __forceinline__ float h2f_g(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 
@@ -189,7 +190,6 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const int8_t *__restrict__ W, c
 // instructions around the fold (which needs 4 VALU instructions per output and group: the bound of this GEMM). Loads
 // through buffer descriptors over the block's own rows: rows past M or N read as 0 (the descriptor's range), so no
 // clamped addresses and no selects; each thread's offsets are fixed and a stage moves the scalar offset only
-#define GQ_RSRC_DW3 0x00020000 // buffer descriptor word 3 of gfx9-family targets (raw loads)
 template <int GM>
 __global__ __launch_bounds__(256) void k_gemm_q8f(const int8_t *__restrict__ W, const uint16_t *__restrict__ WS, int N, int K,
                                                   const int8_t *__restrict__ X, const float *__restrict__ XS, int ldx, int M,
@@ -203,10 +203,10 @@ __global__ __launch_bounds__(256) void k_gemm_q8f(const int8_t *__restrict__ W, 
     const int m0 = blockIdx.y * GM, n0 = blockIdx.x * GN, G = K >> 5, NS = K / GKB, gx = ldx >> 5;
     const int wm = GM == 64 ? (wave >> 1) * 32 : 0, wn = GM == 64 ? (wave & 1) * 64 : wave * 32;
     const int mr = M - m0 < GM ? M - m0 : GM, nr = N - n0 < GN ? N - n0 : GN; // (the block's rows)
-    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void *)(X + (size_t)m0 * ldx), (short)0, mr * ldx, GQ_RSRC_DW3);
-    const __amdgpu_buffer_rsrc_t rxs = __builtin_amdgcn_make_buffer_rsrc((void *)(XS + (size_t)m0 * gx), (short)0, mr * gx * 4, GQ_RSRC_DW3);
-    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)(W + (size_t)n0 * K), (short)0, nr * K, GQ_RSRC_DW3);
-    const __amdgpu_buffer_rsrc_t rws = __builtin_amdgcn_make_buffer_rsrc((void *)(WS + (size_t)n0 * G), (short)0, nr * G * 2, GQ_RSRC_DW3);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void *)(X + (size_t)m0 * ldx), (short)0, mr * ldx, GW_RSRC_DW3);
+    const __amdgpu_buffer_rsrc_t rxs = __builtin_amdgcn_make_buffer_rsrc((void *)(XS + (size_t)m0 * gx), (short)0, mr * gx * 4, GW_RSRC_DW3);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)(W + (size_t)n0 * K), (short)0, nr * K, GW_RSRC_DW3);
+    const __amdgpu_buffer_rsrc_t rws = __builtin_amdgcn_make_buffer_rsrc((void *)(WS + (size_t)n0 * G), (short)0, nr * G * 2, GW_RSRC_DW3);
     float acc[TJ][16];
     #pragma unroll
     for (int j = 0; j < TJ; j++)

@@ -88,7 +88,6 @@ __device__ __forceinline__ float gv_fold(const float *p, int G) {
 // thread's part (16 j bytes) in the vector one, so no per-row address arithmetic in vector registers. Each scale is
 // loaded as its aligned 32-bit word (G is even) and kept raw until used: a conversion, or two 16-bit values packed into
 // one register, would wait for the loads just issued
-#define GV_RSRC_DW3 0x00020000 // buffer descriptor word 3 of gfx9-family targets (raw loads)
 // the weight loads are non-temporal (cache policy nt): each weight byte is read once per token, and a streaming
 // insert keeps the caches for what is read again (the K / V cache, the activations, the exactness tables). Measured
 // on the 8B decode step: 2.59 -> 2.51 ms per token
@@ -184,8 +183,8 @@ __global__ __launch_bounds__(NT) void k_gemv1(GvArgs a) {
         }
     }
     // 2. the weight loads of the block's first D - 1 tiles (past the block's last tile: its first again)
-    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)a.W, (short)0, a.nrows * K, GV_RSRC_DW3);
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)a.WS, (short)0, (a.nrows * G * 2 + 3) & ~3, GV_RSRC_DW3);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)a.W, (short)0, a.nrows * K, GW_RSRC_DW3);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)a.WS, (short)0, (a.nrows * G * 2 + 3) & ~3, GW_RSRC_DW3);
     const int odd = (j >> 1) & 1; // (the half of the scale's word)
     int4 wv[D][R];
     uint32_t ws[D][R];
@@ -321,9 +320,9 @@ __global__ __launch_bounds__(NT) void k_gemv1(GvArgs a) {
     // device's CUs), or load this tile again. Their registers are never read: the data go no further than the caches
     const bool pfon = a.nW && (int)blockIdx.x < a.n_grid;
     const __amdgpu_buffer_rsrc_t rwn = __builtin_amdgcn_make_buffer_rsrc((void *)(pfon ? a.nW : a.W), (short)0,
-                                                                          pfon ? a.n_cbytes : a.nrows * K, GV_RSRC_DW3);
+                                                                          pfon ? a.n_cbytes : a.nrows * K, GW_RSRC_DW3);
     const __amdgpu_buffer_rsrc_t rsn = __builtin_amdgcn_make_buffer_rsrc((void *)(pfon ? a.nWS : a.WS), (short)0,
-                                                                          pfon ? a.n_sbytes : (a.nrows * G * 2 + 3) & ~3, GV_RSRC_DW3);
+                                                                          pfon ? a.n_sbytes : (a.nrows * G * 2 + 3) & ~3, GW_RSRC_DW3);
     int pfi = 0; // (the next matmul's tile blockIdx.x + pfi n_grid comes next)
     auto step = [&](const int4 (&cw)[R], const uint32_t (&cs)[R], int4 (&nw)[R], uint32_t (&ns)[R], int k) -> bool {
         const int nt = tile + gridDim.x, nta = tile + (D - 1) * (int)gridDim.x;

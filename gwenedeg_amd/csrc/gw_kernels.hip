@@ -639,74 +639,98 @@ __global__ __launch_bounds__(ATD_T) void k_attn_decode(const float *__restrict__
 }
 
 // the attention of each head of a row from its key blocks' partials, in block order (att_combine,
-// forward.c:1405-1431), then the row's quantization for wo (aq row b, all_heads = nh * hd values, a multiple of 256).
-// One block of 256 threads per (row b, 256 consecutive values of the row: 256 / hd heads); thread e: value e, head
-// h = e / hd, dim e % hd. Per head: M = max m_k, c_k = exp_att(m_k - M) (lanes in parallel), L = the fma chain of
-// c_k l_k in block order (one lane), inv = 1 / L; per value the fma chain of c_k o_k in block order, 8 blocks' loads
-// ahead, times inv (one block: o inv). The quantization groups (32 consecutive values) lie inside a head
-#define COMB_T 256
-__global__ __launch_bounds__(COMB_T) void k_attn_combine_quant(const float *__restrict__ part, int pstride, int nh, int hd,
+// forward.c:1405-1431), then the row's quantization for wo (aq row b, all_heads = nh * HD values, a multiple of 64).
+// One wave per (row b, 64 consecutive values of the row: one head, or two of HD = 32); lane: value e, head h = e / HD,
+// dim e % HD. Per head: M = max m_k, c_k = exp_att(m_k - M) (lanes over k in parallel, into LDS), L = the fma chain
+// of c_k l_k in block order (every lane of the head alike, its LDS reads 16 ahead), inv = 1 / L; per value the fma
+// chain of c_k o_k in block order, times inv (one block: o inv). The values' o_k load in batches of 32 blocks, the
+// next batch in flight while the current one is folded (the partials come from beyond L2: a batch at a time would
+// wait one load latency each), the first batch issued before the coefficients; raw buffer loads over the row's
+// partials (past its last block they read 0, never folded), 8 blocks per scalar offset with the rest immediate.
+// The quantization groups (32 consecutive values) lie inside a head
+#define COMB_T 64
+#define COMB_B 32
+template <int HD>
+__global__ __launch_bounds__(COMB_T) void k_attn_combine_quant(const float *__restrict__ part, int pstride, int nh,
                                                             const int *__restrict__ pos, int8_t *__restrict__ aq,
                                                             float *__restrict__ as, int ldq, float *__restrict__ att_out) {
-    extern __shared__ float cl[]; // [hpb][nb] m then coefficients, [hpb][nb] l, [hpb] inverses
-    const int b = blockIdx.x, nb = (pos[b] + 1 + ATT_P - 1) / ATT_P, st = hd + 2, t = threadIdx.x, hpb = COMB_T / hd;
-    const int e = blockIdx.y * COMB_T + t, h0 = blockIdx.y * hpb, hl = t / hd, ne = nh * hd;
-    float *ll = cl + (size_t)hpb * nb, *inv = ll + (size_t)hpb * nb;
+    constexpr int ST = HD + 2, HPW = HD < COMB_T ? COMB_T / HD : 1;
+    extern __shared__ float cl[]; // [HPW][nbm] coefficients, then [HPW][nbm] l
+    const int b = blockIdx.x, nb = (pos[b] + 1 + ATT_P - 1) / ATT_P, lane = threadIdx.x, nbm = pstride / ST;
+    const int e = blockIdx.y * COMB_T + lane, h0 = blockIdx.y * COMB_T / HD, hl = e / HD - h0, ne = nh * HD;
+    float *ll = cl + HPW * nbm;
     const float *pr = part + (size_t)b * nh * pstride;
-    const float *pb = pr + (size_t)(e / hd) * pstride + e % hd; // this value's o in block 0
-    float o[8];
-    #pragma unroll
-    for (int u = 0; u < 8; u++)
-        if (u < nb) o[u] = pb[(size_t)u * st];
-    for (int i = t; i < hpb * nb; i += COMB_T) {
-        const float *ml = pr + (size_t)(h0 + i / nb) * pstride + (size_t)(i % nb) * st + hd;
-        cl[i] = ml[0];
-        ll[i] = ml[1];
-    }
-    __syncthreads();
-    // coefficients: wave w (w < hpb) takes head w; its lanes the exp of blocks k = lane, lane + 64, ...
-    const int wave = t >> 6, lane = t & 63;
-    for (int hh = wave; hh < hpb; hh += COMB_T / 64) {
-        float *ch = cl + (size_t)hh * nb;
-        const float *lh = ll + (size_t)hh * nb;
-        if (nb == 1) {
-            if (lane == 0) {
-                inv[hh] = 1.0f / lh[0];
-                ch[0] = 1.0f;
-            }
-            continue;
-        }
-        float M = -3.402823466e38f;
-        for (int k = lane; k < nb; k += 64) M = fmaxf(M, ch[k]);
-        M = wave_max(M);
-        for (int k = lane; k < nb; k += 64) ch[k] = exp_att(ch[k] - M);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        __builtin_amdgcn_wave_barrier();
-        if (lane == 0) {
-            float L = 0.0f;
-            for (int k = 0; k < nb; k++) L = __builtin_fmaf(ch[k], lh[k], L);
-            inv[hh] = 1.0f / L;
-        }
-    }
-    __syncthreads();
-    const float *ch = cl + (size_t)hl * nb;
-    float out;
-    if (nb == 1) {
-        out = o[0] * inv[hl];
-    } else {
-        float acc = 0.0f;
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc((void *)pr, (short)0, nh * pstride * 4, GW_RSRC_DW3);
+    const int vo = ((e / HD) * pstride + e % HD) * 4; // (this value's o in block 0, bytes)
+    float wa[COMB_B], wb[COMB_B];
+    auto ld = [&](float (&w)[COMB_B], int k0) __attribute__((always_inline)) {
         #pragma unroll
-        for (int u = 0; u < 8; u++)
-            if (u < nb) acc = __builtin_fmaf(ch[u], o[u], acc);
-        for (int kb = 8; kb < nb; kb += 8) {
-            float w[8];
-            #pragma unroll
-            for (int u = 0; u < 8; u++) w[u] = pb[(size_t)(kb + u < nb ? kb + u : nb - 1) * st];
+        for (int u8 = 0; u8 < COMB_B; u8 += 8) {
+            const int so = (k0 + u8) * ST * 4;
             #pragma unroll
             for (int u = 0; u < 8; u++)
-                if (kb + u < nb) acc = __builtin_fmaf(ch[kb + u], w[u], acc);
+                w[u8 + u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, vo + u * ST * 4, so, 0));
         }
-        out = acc * inv[hl];
+    };
+    ld(wa, 0);
+    // coefficients of the wave's heads
+    #pragma unroll
+    for (int hh = 0; hh < HPW; hh++) {
+        const float *ml = pr + (size_t)(h0 + hh) * pstride + HD;
+        float *ch = cl + hh * nbm, *lh = ll + hh * nbm;
+        float M = -3.402823466e38f;
+        for (int k = lane; k < nb; k += COMB_T) {
+            const float mk = ml[(size_t)k * ST];
+            ch[k] = mk;
+            lh[k] = ml[(size_t)k * ST + 1];
+            M = fmaxf(M, mk);
+        }
+        M = wave_max(M);
+        if (nb > 1)
+            for (int k = lane; k < nb; k += COMB_T) ch[k] = exp_att(ch[k] - M);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    const float *ch = cl + hl * nbm, *lh = ll + hl * nbm;
+    float out;
+    if (nb == 1) {
+        out = wa[0] * (1.0f / lh[0]);
+    } else {
+        float L = 0.0f;
+        {
+            int k = 0;
+            for (; k + 16 <= nb; k += 16) {
+                float c16[16], l16[16];
+                #pragma unroll
+                for (int u = 0; u < 16; u++) c16[u] = ch[k + u], l16[u] = lh[k + u];
+                #pragma unroll
+                for (int u = 0; u < 16; u++) L = __builtin_fmaf(c16[u], l16[u], L);
+            }
+            for (; k < nb; k++) L = __builtin_fmaf(ch[k], lh[k], L);
+        }
+        const float inv = 1.0f / L;
+        float acc = 0.0f;
+        auto fold = [&](const float (&w)[COMB_B], int k0, int m) __attribute__((always_inline)) { // (blocks k0 .. k0 + m - 1)
+            #pragma unroll
+            for (int u = 0; u < COMB_B; u++)
+                if (u < m) acc = __builtin_fmaf(ch[k0 + u], w[u], acc);
+        };
+        int k = 0; // (wa holds blocks k .. k + COMB_B - 1; the loads of whole pairs of batches unconditional)
+        for (; k + 2 * COMB_B <= nb; k += 2 * COMB_B) {
+            ld(wb, k + COMB_B);
+            fold(wa, k, COMB_B);
+            ld(wa, k + 2 * COMB_B);
+            fold(wb, k + COMB_B, COMB_B);
+        }
+        if (k + COMB_B < nb) {
+            ld(wb, k + COMB_B);
+            fold(wa, k, COMB_B);
+            fold(wb, k + COMB_B, nb - k - COMB_B);
+        } else {
+            fold(wa, k, nb - k);
+        }
+        out = acc * inv;
     }
     if (att_out) att_out[(size_t)b * ne + e] = out;
     quant_lane32(out, aq + (size_t)b * ldq + e, as + (size_t)b * (ldq / 32) + (e >> 5));
@@ -1061,10 +1085,14 @@ int gw_k_attn_decode(const float *qkv, int nh, int nkv, int hd, float scale, con
 
 int gw_k_attn_combine_quant(const float *part, int pstride, int nh, int hd, const int *pos, int n, int8_t *aq, float *as,
                             int ldq, float *att_out, hipStream_t s) {
-    // (nh hd % 256 == 0, hd | 256); LDS: the per-block (m, l) of the block's heads up to pstride / (hd + 2) blocks
-    int hpb = COMB_T / hd, nbm = pstride / (hd + 2);
-    GW_LAUNCH(k_attn_combine_quant, dim3(n, nh * hd / COMB_T), dim3(COMB_T), (size_t)hpb * (2 * nbm + 1) * sizeof(float), s,
-              part, pstride, nh, hd, pos, aq, as, ldq, att_out);
+    // (nh hd % 64 == 0, hd in 32, 64, 128); LDS: the coefficients and l of the wave's heads, up to pstride / (hd + 2)
+    // blocks
+    if ((nh * hd) % COMB_T || (hd != 32 && hd != 64 && hd != 128)) return (int)hipErrorInvalidValue;
+    const size_t sh = (size_t)(hd < COMB_T ? COMB_T / hd : 1) * 2 * (pstride / (hd + 2)) * sizeof(float);
+    const dim3 grid(n, nh * hd / COMB_T);
+    if (hd == 128) GW_LAUNCH(k_attn_combine_quant<128>, grid, dim3(COMB_T), sh, s, part, pstride, nh, pos, aq, as, ldq, att_out);
+    else if (hd == 64) GW_LAUNCH(k_attn_combine_quant<64>, grid, dim3(COMB_T), sh, s, part, pstride, nh, pos, aq, as, ldq, att_out);
+    else GW_LAUNCH(k_attn_combine_quant<32>, grid, dim3(COMB_T), sh, s, part, pstride, nh, pos, aq, as, ldq, att_out);
     return (int)hipGetLastError();
 }
 
