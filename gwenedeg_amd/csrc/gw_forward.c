@@ -600,13 +600,10 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
         nbmax = nb > nbmax ? nb : nbmax;
     }
     if ((rc = ctx_part(c, n, nbmax)) != RQ_OK) return rc;
-    int nrb = 0, nq_max = 1;
     for (int b = 0; b < n;) {
         int e = b + 1;
         while (e < n && e - b < rb && P->seq[e] == P->seq[b] && P->pos[e] == P->pos[e - 1] + 1) e++;
         nitems += nkv * ((P->pos[e - 1] + 1 + GW_ATT_P - 1) / GW_ATT_P);
-        nq_max = (e - b) * kv_mul > nq_max ? (e - b) * kv_mul : nq_max;
-        nrb++;
         b = e;
     }
     /* metadata block: tok, pos, sel (int), kc / vc tables per layer (pointers), items */
@@ -628,19 +625,26 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
             ptr[(size_t)l * n + b] = P->seq[b]->kc + lo;
             ptr[(size_t)(L + l) * n + b] = P->seq[b]->vc + lo;
         }
+    /* the items in four groups, each launched with its own query-vector bound: the f16 caches', then the bf16
+     * caches'; in each, the row blocks of <= 4 query vectors (decode rows: the narrow kernel, two blocks per CU), then
+     * the wider ones (prompt row blocks). A pass of both kinds of rows would otherwise run every decode row's items in
+     * the 16-vector kernel */
     Item *it = (Item *)(h + o_items);
-    for (int pass = 0, k = 0; pass < 2; pass++) /* the f16 caches' items, then the bf16 caches' */
+    int gcnt[4] = { 0, 0, 0, 0 }, gnq[4] = { 1, 1, 1, 1 };
+    for (int grp = 0, k = 0; grp < 4; grp++)
         for (int b = 0; b < n;) {
             int e = b + 1;
             while (e < n && e - b < rb && P->seq[e] == P->seq[b] && P->pos[e] == P->pos[e - 1] + 1) e++;
-            int nb = (P->pos[e - 1] + 1 + GW_ATT_P - 1) / GW_ATT_P;
-            if (kbf[b] == pass) {
+            int nb = (P->pos[e - 1] + 1 + GW_ATT_P - 1) / GW_ATT_P, nq = (e - b) * kv_mul;
+            if (kbf[b] == grp >> 1 && (nq > 4) == (grp & 1)) {
                 for (int g = 0; g < nkv; g++)
                     for (int kb = 0; kb < nb; kb++) it[k++] = (Item){ b, e - b, g, kb };
-                nbf += pass ? nkv * nb : 0;
+                gcnt[grp] += nkv * nb;
+                gnq[grp] = nq > gnq[grp] ? nq : gnq[grp];
             }
             b = e;
         }
+    nbf = gcnt[2] + gcnt[3];
     HIPCHK(c, "hipMemcpyAsync (pass metadata)", hipMemcpyAsync(d, h, total, hipMemcpyHostToDevice, c->stream));
     const int *tok_d = (const int *)(d + o_tok), *pos_d = (const int *)(d + o_pos), *sel_d = (const int *)(d + o_sel);
     const int *kbf_d = (const int *)(d + o_kbf);
@@ -676,12 +680,11 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
         KCHK(gw_k_qknorm_rope_store(c->qkv, c->ldqkv, n, nh, nkv, hd, y->q_norm, y->k_norm, m->rope, pos_d,
                                     kc_d + (size_t)l * n, vc_d + (size_t)l * n, nbf ? kbf_d : NULL, s));
         pf_mark(c, GW_PF_ATT);
-        if (nitems > nbf)
-            KCHK(gw_k_attn_part(items_d, nitems - nbf, nq_max, c->qkv, c->ldqkv, nh, nkv, hd, m->att_scale, pos_d,
-                                kc_d + (size_t)l * n, vc_d + (size_t)l * n, c->part, c->pstride, 0, s));
-        if (nbf)
-            KCHK(gw_k_attn_part((const Item *)items_d + (nitems - nbf), nbf, nq_max, c->qkv, c->ldqkv, nh, nkv, hd,
-                                m->att_scale, pos_d, kc_d + (size_t)l * n, vc_d + (size_t)l * n, c->part, c->pstride, 1, s));
+        for (int grp = 0, off = 0; grp < 4; off += gcnt[grp], grp++)
+            if (gcnt[grp])
+                KCHK(gw_k_attn_part((const Item *)items_d + off, gcnt[grp], gnq[grp], c->qkv, c->ldqkv, nh, nkv, hd,
+                                    m->att_scale, pos_d, kc_d + (size_t)l * n, vc_d + (size_t)l * n, c->part, c->pstride,
+                                    grp >> 1, s));
         if (fused) {
             if (nbmax <= GW_GV_NBMAX) {
                 pf_mark(c, GW_PF_WO);
