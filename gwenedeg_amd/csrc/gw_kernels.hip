@@ -176,6 +176,26 @@ __global__ __launch_bounds__(64) void k_qknorm_rope_store(float *__restrict__ qk
 //   o: lane (vector, dim pair): the fma chains over the positions in order, V from LDS (NQ = 16: its own buffer,
 //     staged with K; else the K buffer, rewritten once the scores are done: a block's LDS stays under half a CU's)
 // hd <= 128 (hd % 32 == 0), nq <= 16.
+// a0..a7 += (q0..q7 of lane N of this lane's 16-lane row) * k: v_fmac_f32_dpp with row_newbcast, the broadcast folded
+// into the fma (one rounding, as __builtin_fmaf; the compiler does not fold a separate DPP move into v_fmac). A VALU
+// write of a DPP source needs 2 wait states before the read: the s_nop, whatever the compiler placed before the block
+// (not volatile: the compiler schedules the K reads around the blocks)
+template <int N>
+__device__ __forceinline__ void fmac8_row(float &a0, float &a1, float &a2, float &a3, float &a4, float &a5, float &a6, float &a7,
+                                          float q0, float q1, float q2, float q3, float q4, float q5, float q6, float q7, float k) {
+    asm("s_nop 1\n\t"
+                 "v_fmac_f32_dpp %0, %8, %16 row_newbcast:%17 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %1, %9, %16 row_newbcast:%17 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %2, %10, %16 row_newbcast:%17 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %3, %11, %16 row_newbcast:%17 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %4, %12, %16 row_newbcast:%17 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %5, %13, %16 row_newbcast:%17 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %6, %14, %16 row_newbcast:%17 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %7, %15, %16 row_newbcast:%17 row_mask:0xf bank_mask:0xf"
+                 : "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3), "+v"(a4), "+v"(a5), "+v"(a6), "+v"(a7)
+                 : "v"(q0), "v"(q1), "v"(q2), "v"(q3), "v"(q4), "v"(q5), "v"(q6), "v"(q7), "v"(k), "n"(N));
+}
+
 #define ATT_NQ 16
 #define ATT_HDMAX 128
 #define ATT_TH 1024
@@ -194,7 +214,7 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
     // register plus an immediate offset), then the K tiles, then (NQ = 16) V. V rows at a fixed 256-byte stride,
     // whatever hd: the o chains' reads are immediate offsets from one pointer. Up to 4 vectors (SE), the exponentials
     // go to their own array E, written by all 16 waves, and the sums l are added while the o chains run
-    constexpr bool VL = NQ == 16, SE = NQ <= 4;
+    constexpr bool VL = NQ == 16, SE = NQ <= 4, DQ = NQ >= 8;
     constexpr int QS_B = NQ * ATT_QS * 4, S_B = NQ * ATT_P * 4, E_B = SE ? S_B : 0;
     constexpr int KS_OFF = (QS_B + S_B + E_B + NQ * 4 + 15) & ~15;
     __shared__ __align__(16) uint8_t lds[KS_OFF + 16 * ATT_KTILE + (VL ? ATT_P * 2 * ATT_HDMAX : 0)];
@@ -247,8 +267,63 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
     ATT_ST(0, k0, v0) ATT_ST(1, k1, v1) ATT_ST(2, k2, v2) ATT_ST(3, k3, v3)
 #undef ATT_ST
     __syncthreads();
-    // scores: lane (position p, chunk c), all NQ vectors (no per-vector branches in the chain)
-    {
+    // scores, 8 or 16 vectors (DQ): lane 16 c + n of wave w takes position p = 16 w + n (the wave's tile w) and chunk
+    // c; the lane holds q[v][32 c + n] and q[v][32 c + 16 + n] of every vector in registers, and dim i of the chunk's
+    // chain takes the row's lane i % 16's (a DPP broadcast inside the fma): no query reads from LDS in the chains.
+    // The chunks of position p are rows 0 .. 3 of lane n, added in order. Every lane of a wave whose tile holds a
+    // position of the block runs the chains (no lane masked: a DPP source lane must be active); lanes past the block
+    // or the head's chunks compute values never written
+    if constexpr (DQ) {
+        const int n = t & 15, c = (t >> 4) & 3, wv = __builtin_amdgcn_readfirstlane(t >> 6), p = 16 * wv + n;
+        float qa[NQ], qb[NQ], acc[NQ];
+        #pragma unroll
+        for (int v = 0; v < NQ; v++) {
+            qa[v] = qs[v * ATT_QS + c * ATT_QC + n];
+            qb[v] = qs[v * ATT_QS + c * ATT_QC + 16 + n];
+            acc[v] = 0.0f;
+        }
+        if (16 * wv < nmx) {
+            const uint8_t *kt = ks + wv * ATT_KTILE + c * ATT_KROW + (KB ? 4 : 2) * n;
+#define ATT_DQ(I, KF)                                                                                                   \
+            {                                                                                                           \
+                const float kf_ = (KF);                                                                                 \
+                const float *qq = (I) < 16 ? qa : qb;                                                                   \
+                fmac8_row<(I) & 15>(acc[0], acc[1], acc[2], acc[3], acc[4], acc[5], acc[6], acc[7], qq[0], qq[1], qq[2],  \
+                                    qq[3], qq[4], qq[5], qq[6], qq[7], kf_);                                            \
+                if constexpr (NQ > 8)                                                                                   \
+                    fmac8_row<(I) & 15>(acc[8], acc[9], acc[10], acc[11], acc[12], acc[13], acc[14], acc[15], qq[8],      \
+                                        qq[9], qq[10], qq[11], qq[12], qq[13], qq[14], qq[15], kf_);                    \
+            }
+            if constexpr (KB) { // (dims i, i + 1 of position p: one word at i 32 + 4 p of the chunk row, i even)
+#define ATT_DQ2(I)                                                                                                      \
+                {                                                                                                       \
+                    const uint32_t w_ = *(const uint32_t *)(kt + (I) * 32);                                             \
+                    ATT_DQ(I, bf2f(w_ & 0xffffu))                                                                       \
+                    ATT_DQ((I) + 1, bf2f(w_ >> 16))                                                                     \
+                }
+                ATT_DQ2(0) ATT_DQ2(2) ATT_DQ2(4) ATT_DQ2(6) ATT_DQ2(8) ATT_DQ2(10) ATT_DQ2(12) ATT_DQ2(14)
+                ATT_DQ2(16) ATT_DQ2(18) ATT_DQ2(20) ATT_DQ2(22) ATT_DQ2(24) ATT_DQ2(26) ATT_DQ2(28) ATT_DQ2(30)
+#undef ATT_DQ2
+            } else {
+#define ATT_DQ1(I) ATT_DQ(I, h2f(*(const uint16_t *)(kt + (I) * 32)))
+                ATT_DQ1(0) ATT_DQ1(1) ATT_DQ1(2) ATT_DQ1(3) ATT_DQ1(4) ATT_DQ1(5) ATT_DQ1(6) ATT_DQ1(7)
+                ATT_DQ1(8) ATT_DQ1(9) ATT_DQ1(10) ATT_DQ1(11) ATT_DQ1(12) ATT_DQ1(13) ATT_DQ1(14) ATT_DQ1(15)
+                ATT_DQ1(16) ATT_DQ1(17) ATT_DQ1(18) ATT_DQ1(19) ATT_DQ1(20) ATT_DQ1(21) ATT_DQ1(22) ATT_DQ1(23)
+                ATT_DQ1(24) ATT_DQ1(25) ATT_DQ1(26) ATT_DQ1(27) ATT_DQ1(28) ATT_DQ1(29) ATT_DQ1(30) ATT_DQ1(31)
+#undef ATT_DQ1
+            }
+#undef ATT_DQ
+        }
+        #pragma unroll
+        for (int v = 0; v < NQ; v++) {
+            float c1 = __shfl_down(acc[v], 16), c2 = __shfl_down(acc[v], 32), c3 = __shfl_down(acc[v], 48);
+            float a = acc[v];
+            if (nchk > 1) a = a + c1;
+            if (nchk > 2) a = a + c2;
+            if (nchk > 3) a = a + c3;
+            if (c == 0 && p < nmx && v < nq) S[v][p] = a * scale;
+        }
+    } else { // scores, up to 4 vectors: lane (position p, chunk c), all NQ vectors (no per-vector branches in the chain)
         int p = t >> 2, c = t & 3;
         const uint8_t *kt = ks + (p / ATT_T) * ATT_KTILE + c * ATT_KROW + (p % ATT_T) * 2;
         const float *qc = qs + c * ATT_QC;
