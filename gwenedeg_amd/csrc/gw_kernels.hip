@@ -445,7 +445,11 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
             const int n = np[v];
             int p = 0;
             float o0 = 0.0f, o1 = 0.0f;
-            const uint32_t *vb = (const uint32_t *)((VL ? vs : ks) + i0 * 2);
+            // (the V rows' byte offset opaque to the compiler: one base register with immediate offsets, not a sum
+            // folded into every read past 64 KiB (NQ = 16: V lies above the K tiles))
+            int vo = (int)((VL ? vs : ks) - lds) + i0 * 2;
+            asm volatile("" : "+v"(vo));
+            const uint32_t *vb = (const uint32_t *)(lds + vo);
             constexpr int rs = ATT_HDMAX / 2; // (uint32 words per position's LDS row)
             constexpr int PB = VL ? 16 : 8; // (8: 64 registers, two blocks per CU)
             uint32_t va[PB], vbb[PB];
