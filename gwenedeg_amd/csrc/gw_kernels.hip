@@ -370,7 +370,8 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
         ATT_SV(0, v0) ATT_SV(1, v1) ATT_SV(2, v2) ATT_SV(3, v3)
 #undef ATT_SV
     }
-    int wave = t >> 6, lane = t & 63;
+    // (the wave and a wave's vector length as uniform values: scalar loop bounds, no exec-masked loops)
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
     // (a vector's part of block kb: m, l after its hd values o)
     auto mlp = [&](int v) __attribute__((always_inline)) -> float * {
         return part + ((size_t)(r0 + v / kv_mul) * nh + g * kv_mul + v % kv_mul) * pstride + (size_t)kb * (hd + 2) + hd;
@@ -438,11 +439,11 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
         if (lane == 0) mlp(v)[1] = s;
     }
     // o: lane (vector v = wave, dim pair d2): the chains over the positions in order, V pairs from LDS, two register
-    // sets of PB positions' loads alternating (a copy between sets would wait for the loads)
+    // sets of PB positions' loads per step
     {
         int v = wave, d2 = lane, i0 = 2 * d2;
-        if (v < nq && i0 < hd && np[v] > 0) {
-            const int n = np[v];
+        const int n = v < NQ ? __builtin_amdgcn_readfirstlane(np[v < NQ ? v : 0]) : 0;
+        if (v < nq && i0 < hd && n > 0) {
             int p = 0;
             float o0 = 0.0f, o1 = 0.0f;
             // (the V rows' byte offset opaque to the compiler: one base register with immediate offsets, not a sum
@@ -468,22 +469,18 @@ __device__ __forceinline__ void attn_part_body(const int4 *__restrict__ items, c
                     o1 = __builtin_fmaf(ee[u], KB ? bf2f(vv[u] >> 16) : h2f((uint16_t)(vv[u] >> 16)), o1);
                 }
             };
-            if (n >= PB) {
-                ld(va, ea, 0);
-                for (p = PB; p + 2 * PB <= n; p += 2 * PB) {
-                    ld(vbb, eb, p);
-                    fold(va, ea);
-                    ld(va, ea, p + PB);
-                    fold(vbb, eb);
-                }
-                if (p + PB <= n) {
-                    ld(vbb, eb, p);
-                    fold(va, ea);
-                    fold(vbb, eb);
-                    p += PB;
-                } else {
-                    fold(va, ea);
-                }
+            // (each step loads both sets, then folds them: no register set carried across steps, whose copies had
+            // cost a fifth of the loop's instructions; the block's other waves cover the loads' latency)
+            for (; p + 2 * PB <= n; p += 2 * PB) {
+                ld(va, ea, p);
+                ld(vbb, eb, p + PB);
+                fold(va, ea);
+                fold(vbb, eb);
+            }
+            if (p + PB <= n) {
+                ld(va, ea, p);
+                fold(va, ea);
+                p += PB;
             }
             for (; p < n; p++) {
                 uint32_t vv = vb[p * rs];
