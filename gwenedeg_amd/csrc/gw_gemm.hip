@@ -783,13 +783,58 @@ __global__ __launch_bounds__(SK_T * SB, SB == 1 ? 2 : 1) void k_gemm_kq32(SkMats
 //     (2 bits from qs, bit 2 from hmask), - 4 sum x and the scales sc - 32
 // then one lane per (activation row, weight row) folds the groups in order: val = val + term. mode 1: out = out + val.
 // K % 32 == 0 (Q8_0), % 256 (K-quants); the K-quants' q are 0 .. 63, so v_dot4 with signed codes is exact
-template <int TYPE, int M, int R, int U>
+template <int TYPE, int M, int R, int U, bool PF>
 __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, const uint16_t *__restrict__ WS, int nrows,
                                                  int K, int bstride, const int8_t *__restrict__ xq, const float *__restrict__ xs,
                                                  int ldx, float *out, int ldo, int mode) {
     extern __shared__ float P[];
-    const int G = K >> 5, H = K >> 4, PS = (G + 7) & ~3; // (rows 16-byte aligned)
+    // (P: the terms of the row, or with PF of one pass (128 U groups), folded after each pass with the running value
+    // in the fold lane: rows of several passes (K = 12288) no longer held to three blocks per CU by a whole row's
+    // terms. A separate instance: the fold inside the pass loop keeps 106 registers, the row's fold after it 70, and
+    // the one-pass matrices run seven blocks per CU on 70; rows 16-byte aligned)
+    constexpr int GPASS = PF ? 128 * U : 1 << 30;
+    const int G = K >> 5, H = K >> 4, PS = ((G < GPASS ? G : GPASS) + 7) & ~3;
     const int row0 = blockIdx.x * R, t = threadIdx.x;
+    float vf = 0.0f; // (fold lane t < M R: the value of activation row t / R, weight row t % R so far)
+    // v + the terms p[0 .. ng - 1] in order (sets of 32 terms' LDS reads alternating)
+    auto fold_terms = [&](const float *p, int ng, float v) __attribute__((always_inline)) -> float {
+        int g = 0;
+        if (ng >= 32) {
+            float4 a[8], b[8];
+            #pragma unroll
+            for (int u = 0; u < 8; u++) a[u] = *(const float4 *)(p + 4 * u);
+            for (g = 32; g + 64 <= ng; g += 64) {
+                #pragma unroll
+                for (int u = 0; u < 8; u++) b[u] = *(const float4 *)(p + g + 4 * u);
+                #pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    v = v + a[u].x;
+                    v = v + a[u].y;
+                    v = v + a[u].z;
+                    v = v + a[u].w;
+                }
+                #pragma unroll
+                for (int u = 0; u < 8; u++) a[u] = *(const float4 *)(p + g + 32 + 4 * u);
+                #pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    v = v + b[u].x;
+                    v = v + b[u].y;
+                    v = v + b[u].z;
+                    v = v + b[u].w;
+                }
+            }
+            // (a holds groups g - 32 .. g - 1)
+            #pragma unroll
+            for (int u = 0; u < 8; u++) {
+                v = v + a[u].x;
+                v = v + a[u].y;
+                v = v + a[u].z;
+                v = v + a[u].w;
+            }
+        }
+        for (; g < ng; g++) v = v + p[g];
+        return v;
+    };
     const size_t rowb = TYPE == GW_Q8_0 ? (size_t)K : (size_t)(K >> 8) * bstride;
     for (int j0 = 0; j0 < H; j0 += 256 * U) {
         // the pass's loads (past the row's end: its last half-group again, unconditionally; only the stores below are
@@ -950,55 +995,26 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
                             I = I + __shfl_xor(I, 1);
                             term = (f0[u][r] * xsg[u][m]) * (float)I;
                         }
-                        if (!(j & 1)) P[(m * R + r) * PS + (j >> 1)] = term;
+                        if (!(j & 1)) P[(m * R + r) * PS + ((j - (PF ? j0 : 0)) >> 1)] = term;
                     }
                 }
             }
         }
+        if constexpr (PF) { // this pass's groups j0 / 2 .. into the fold lanes' values
+            __syncthreads();
+            if (t < M * R) vf = fold_terms(P + t * PS, G - (j0 >> 1) < GPASS ? G - (j0 >> 1) : GPASS, vf);
+            __syncthreads();
+        }
     }
-    __syncthreads();
+    if constexpr (!PF) { // the row's groups
+        __syncthreads();
+        if (t < M * R) vf = fold_terms(P + t * PS, G, 0.0f);
+    }
     if (t < M * R) {
-        int m = t / R, r = t % R, row = row0 + r;
+        const int m = t / R, r = t % R, row = row0 + r;
         if (row < nrows) {
-            const float *p = P + t * PS;
-            float v = 0.0f;
-            int g = 0;
-            if (G >= 32) {
-                float4 a[8], b[8];
-                #pragma unroll
-                for (int u = 0; u < 8; u++) a[u] = *(const float4 *)(p + 4 * u);
-                for (g = 32; g + 64 <= G; g += 64) {
-                    #pragma unroll
-                    for (int u = 0; u < 8; u++) b[u] = *(const float4 *)(p + g + 4 * u);
-                    #pragma unroll
-                    for (int u = 0; u < 8; u++) {
-                        v = v + a[u].x;
-                        v = v + a[u].y;
-                        v = v + a[u].z;
-                        v = v + a[u].w;
-                    }
-                    #pragma unroll
-                    for (int u = 0; u < 8; u++) a[u] = *(const float4 *)(p + g + 32 + 4 * u);
-                    #pragma unroll
-                    for (int u = 0; u < 8; u++) {
-                        v = v + b[u].x;
-                        v = v + b[u].y;
-                        v = v + b[u].z;
-                        v = v + b[u].w;
-                    }
-                }
-                // (a holds groups g - 32 .. g - 1)
-                #pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    v = v + a[u].x;
-                    v = v + a[u].y;
-                    v = v + a[u].z;
-                    v = v + a[u].w;
-                }
-            }
-            for (; g < G; g++) v = v + p[g];
             float *o = out + (size_t)m * ldo + row;
-            *o = mode == 1 ? *o + v : v;
+            *o = mode == 1 ? *o + vf : vf;
         }
     }
 }
@@ -1055,11 +1071,16 @@ static int launch_gemv_mr(const uint8_t *W, const uint16_t *WS, int nrows, int K
     for (int m0 = 0; m0 < M; m0 += 8) {
         const int mm = M - m0 < 8 ? M - m0 : 8;
         hipEvent_t e0 = m0 == 0 ? t0 : NULL, e1 = m0 + 8 >= M ? t1 : NULL;
-        const uint32_t lds = (uint32_t)((size_t)mm * R * ((K / 32 + 7) & ~3) * sizeof(float));
+        const bool pf = K > 4096; // (several passes: the terms folded per pass)
+        const uint32_t lds = (uint32_t)((size_t)mm * R * (((pf ? 128 : K / 32) + 7) & ~3) * sizeof(float));
         const int8_t *x = xq + (size_t)m0 * ldx;
         const float *xsc = xs + (size_t)m0 * (ldx / 32);
         float *o = out + (size_t)m0 * ldo;
-#define MR_L(MM) hipExtLaunchKernelGGL((k_gemv_mr<TYPE, MM, R, 1>), grid, dim3(256), lds, s, e0, e1, 0, W, WS, nrows, K, bstride, x, xsc, ldx, o, ldo, mode)
+#define MR_L(MM)                                                                                                        \
+    do {                                                                                                                \
+        if (pf) hipExtLaunchKernelGGL((k_gemv_mr<TYPE, MM, R, 1, true>), grid, dim3(256), lds, s, e0, e1, 0, W, WS, nrows, K, bstride, x, xsc, ldx, o, ldo, mode); \
+        else hipExtLaunchKernelGGL((k_gemv_mr<TYPE, MM, R, 1, false>), grid, dim3(256), lds, s, e0, e1, 0, W, WS, nrows, K, bstride, x, xsc, ldx, o, ldo, mode); \
+    } while (0)
         switch (mm) {
         case 1: MR_L(1); break;
         case 2: MR_L(2); break;
