@@ -231,8 +231,8 @@ static int ctx_part(RqCtx *c, int rows, int nb) {
     size_t need = (size_t)rows * m->n_heads * nb * (m->head_dim + 2) * sizeof(float);
     if (nb > c->att_nb || need > c->part_bytes) {
         int nbn = nb > c->att_nb ? nb : c->att_nb;
-        /* the combine kernel keeps (m, l, coefficient) of every block of its 256 / head_dim heads in LDS */
-        if ((size_t)(256 / m->head_dim) * (2 * (size_t)nbn + 1) * sizeof(float) > 65536)
+        /* the combine kernel keeps the coefficient and l of every block of its wave's heads in LDS */
+        if ((size_t)(m->head_dim < 64 ? 64 / m->head_dim : 1) * 2 * (size_t)nbn * sizeof(float) > 65536)
             return ctx_fail(c, RQ_ERR_ARG, "context of %d positions too long for %d heads (attention combine)",
                             nbn * GW_ATT_P, m->n_heads);
         int B = c->nb_max > 1 ? c->nb_max : 1;
@@ -576,7 +576,7 @@ static int fused_layer(RqCtx *c, int l, RqSeq *sq, int pos, const int *pos_d) {
         KCHK(gw_k_gemv1_combine(&y->wo, GW_GV_R_WO, c->part, c->pstride, hd, nb, c->x, 1, &y->w13[0], GW_GV_R_W13, s));
     } else {
         pf_mark(c, GW_PF_COMBINE);
-        KCHK(gw_k_attn_combine_quant(c->part, c->pstride, nh, hd, pos_d, 1, c->xq, c->xs, c->kmax, NULL, s));
+        KCHK(gw_k_attn_combine_quant(c->part, c->pstride, nh, hd, pos_d, 1, nb, c->xq, c->xs, c->kmax, NULL, s));
         pf_mark(c, GW_PF_WO);
         KCHK(gw_k_gemv1_q(&y->wo, GW_GV_R_WO, c->xq, c->xs, c->x, 1, &y->w13[0], GW_GV_R_W13, s));
     }
@@ -691,7 +691,7 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
                 KCHK(gw_k_gemv1_combine(&y->wo, GW_GV_R_WO, c->part, c->pstride, hd, nbmax, c->x, 1, NULL, 0, s));
             } else {
                 pf_mark(c, GW_PF_COMBINE);
-                KCHK(gw_k_attn_combine_quant(c->part, c->pstride, nh, hd, pos_d, n, c->xq, c->xs, K, NULL, s));
+                KCHK(gw_k_attn_combine_quant(c->part, c->pstride, nh, hd, pos_d, n, nbmax, c->xq, c->xs, K, NULL, s));
                 pf_mark(c, GW_PF_WO);
                 KCHK(gw_k_gemv1_q(&y->wo, GW_GV_R_WO, c->xq, c->xs, c->x, 1, NULL, 0, s));
             }
@@ -702,7 +702,7 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
             continue;
         }
         pf_mark(c, GW_PF_COMBINE);
-        KCHK(gw_k_attn_combine_quant(c->part, c->pstride, nh, hd, pos_d, n, c->xq, c->xs, K, NULL, s));
+        KCHK(gw_k_attn_combine_quant(c->part, c->pstride, nh, hd, pos_d, n, nbmax, c->xq, c->xs, K, NULL, s));
         pf_mark(c, GW_PF_WO);
         if ((rc = run_mm(c, &y->wo, 1, c->xq, c->xs, K, n, c->xb, dim, 0)) != RQ_OK) return rc;
         pf_mark(c, GW_PF_NORM);

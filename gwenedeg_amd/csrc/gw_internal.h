@@ -238,8 +238,9 @@ int gw_k_attn_part(const void *items, int nitems, int nq_max, const float *qkv, 
  * kl / vl: its sequence's K / V cache of the layer) */
 int gw_k_attn_decode(const float *qkv, int nh, int nkv, int hd, float scale, const float *qn, const float *kn, const float *rope,
                      int pos, uint16_t *kl, uint16_t *vl, float *part, int pstride, int kbf, hipStream_t s);
-int gw_k_attn_combine_quant(const float *part, int pstride, int nh, int hd, const int *pos, int n, int8_t *aq, float *as,
-                            int ldq, float *att_out, hipStream_t s);
+/* the rows' attention from their key blocks' partials, quantized for wo (nbmax: the most key blocks of any row) */
+int gw_k_attn_combine_quant(const float *part, int pstride, int nh, int hd, const int *pos, int n, int nbmax, int8_t *aq,
+                            float *as, int ldq, float *att_out, hipStream_t s);
 /* hb row: [h (H) | h2 (H)] (il = 0) or blocks of il h then il h2 (w1 / w3 rows interleaved by il) */
 int gw_k_swiglu_quant(const float *hb, int H, int il, int n, int8_t *hq, float *hs, hipStream_t s);
 int gw_k_quant_rows(const float *x, int n, int ldxf, int rows, int8_t *q, float *sc, int ldq, hipStream_t s);

@@ -718,15 +718,15 @@ __global__ __launch_bounds__(ATD_T) void k_attn_decode(const float *__restrict__
 // forward.c:1405-1431), then the row's quantization for wo (aq row b, all_heads = nh * HD values, a multiple of 64).
 // One wave per (row b, 64 consecutive values of the row: one head, or two of HD = 32); lane: value e, head h = e / HD,
 // dim e % HD. Per head: M = max m_k, c_k = exp_att(m_k - M) (lanes over k in parallel, into LDS), L = the fma chain
-// of c_k l_k in block order (every lane of the head alike, its LDS reads 16 ahead), inv = 1 / L; per value the fma
+// of c_k l_k in block order (every lane of the head alike, its LDS reads up to 16 ahead), inv = 1 / L; per value the fma
 // chain of c_k o_k in block order, times inv (one block: o inv). The values' o_k load in batches of 32 blocks, the
 // next batch in flight while the current one is folded (the partials come from beyond L2: a batch at a time would
-// wait one load latency each), the first batch issued before the coefficients; raw buffer loads over the row's
-// partials (past its last block they read 0, never folded), 8 blocks per scalar offset with the rest immediate.
+// wait one load latency each), the first batch issued before the coefficients; raw buffer loads over the wave's
+// heads' partials (past their last block they read 0, never folded), 8 blocks per scalar offset with the rest
+// immediate.
 // The quantization groups (32 consecutive values) lie inside a head
 #define COMB_T 64
-#define COMB_B 32
-template <int HD>
+template <int HD, int COMB_B> // (COMB_B: blocks per batch, 32, or 8 for passes of short rows: fewer registers)
 __global__ __launch_bounds__(COMB_T) void k_attn_combine_quant(const float *__restrict__ part, int pstride, int nh,
                                                             const int *__restrict__ pos, int8_t *__restrict__ aq,
                                                             float *__restrict__ as, int ldq, float *__restrict__ att_out) {
@@ -736,8 +736,11 @@ __global__ __launch_bounds__(COMB_T) void k_attn_combine_quant(const float *__re
     const int e = blockIdx.y * COMB_T + lane, h0 = blockIdx.y * COMB_T / HD, hl = e / HD - h0, ne = nh * HD;
     float *ll = cl + HPW * nbm;
     const float *pr = part + (size_t)b * nh * pstride;
-    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc((void *)pr, (short)0, nh * pstride * 4, GW_RSRC_DW3);
-    const int vo = ((e / HD) * pstride + e % HD) * 4; // (this value's o in block 0, bytes)
+    // (the descriptor spans the wave's heads up to their last block: the batch's loads past it read 0 and touch no
+    // memory; with few blocks (prefill rows: 1 or 2) nearly all of a batch is past it)
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc((void *)(pr + (size_t)h0 * pstride), (short)0,
+                                                                        ((HPW - 1) * pstride + nb * ST) * 4, GW_RSRC_DW3);
+    const int vo = (hl * pstride + e % HD) * 4; // (this value's o in block 0, bytes from the wave's first head)
     float wa[COMB_B], wb[COMB_B];
     auto ld = [&](float (&w)[COMB_B], int k0) __attribute__((always_inline)) {
         #pragma unroll
@@ -748,7 +751,13 @@ __global__ __launch_bounds__(COMB_T) void k_attn_combine_quant(const float *__re
                 w[u8 + u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, vo + u * ST * 4, so, 0));
         }
     };
-    ld(wa, 0);
+    if (COMB_B > 8 && nb <= 8) { // (short rows in a pass of long ones: the 8 loads they need)
+        #pragma unroll
+        for (int u = 0; u < 8; u++)
+            wa[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, vo + u * ST * 4, 0, 0));
+    } else {
+        ld(wa, 0);
+    }
     // coefficients of the wave's heads
     #pragma unroll
     for (int hh = 0; hh < HPW; hh++) {
@@ -775,13 +784,14 @@ __global__ __launch_bounds__(COMB_T) void k_attn_combine_quant(const float *__re
     } else {
         float L = 0.0f;
         {
+            constexpr int LB = COMB_B < 16 ? COMB_B : 16; // (the chain's reads LB ahead)
             int k = 0;
-            for (; k + 16 <= nb; k += 16) {
-                float c16[16], l16[16];
+            for (; k + LB <= nb; k += LB) {
+                float c16[LB], l16[LB];
                 #pragma unroll
-                for (int u = 0; u < 16; u++) c16[u] = ch[k + u], l16[u] = lh[k + u];
+                for (int u = 0; u < LB; u++) c16[u] = ch[k + u], l16[u] = lh[k + u];
                 #pragma unroll
-                for (int u = 0; u < 16; u++) L = __builtin_fmaf(c16[u], l16[u], L);
+                for (int u = 0; u < LB; u++) L = __builtin_fmaf(c16[u], l16[u], L);
             }
             for (; k < nb; k++) L = __builtin_fmaf(ch[k], lh[k], L);
         }
@@ -1159,16 +1169,24 @@ int gw_k_attn_decode(const float *qkv, int nh, int nkv, int hd, float scale, con
     return (int)hipGetLastError();
 }
 
-int gw_k_attn_combine_quant(const float *part, int pstride, int nh, int hd, const int *pos, int n, int8_t *aq, float *as,
-                            int ldq, float *att_out, hipStream_t s) {
+int gw_k_attn_combine_quant(const float *part, int pstride, int nh, int hd, const int *pos, int n, int nbmax, int8_t *aq,
+                            float *as, int ldq, float *att_out, hipStream_t s) {
     // (nh hd % 64 == 0, hd in 32, 64, 128); LDS: the coefficients and l of the wave's heads, up to pstride / (hd + 2)
     // blocks
     if ((nh * hd) % COMB_T || (hd != 32 && hd != 64 && hd != 128)) return (int)hipErrorInvalidValue;
     const size_t sh = (size_t)(hd < COMB_T ? COMB_T / hd : 1) * 2 * (pstride / (hd + 2)) * sizeof(float);
     const dim3 grid(n, nh * hd / COMB_T);
-    if (hd == 128) GW_LAUNCH(k_attn_combine_quant<128>, grid, dim3(COMB_T), sh, s, part, pstride, nh, pos, aq, as, ldq, att_out);
-    else if (hd == 64) GW_LAUNCH(k_attn_combine_quant<64>, grid, dim3(COMB_T), sh, s, part, pstride, nh, pos, aq, as, ldq, att_out);
-    else GW_LAUNCH(k_attn_combine_quant<32>, grid, dim3(COMB_T), sh, s, part, pstride, nh, pos, aq, as, ldq, att_out);
+#define COMB_L(H, B) GW_LAUNCH((k_attn_combine_quant<H, B>), grid, dim3(COMB_T), sh, s, part, pstride, nh, pos, aq, as, ldq, att_out)
+    if (nbmax <= 8) { // (prefill passes: rows of 1 or 2 blocks)
+        if (hd == 128) COMB_L(128, 8);
+        else if (hd == 64) COMB_L(64, 8);
+        else COMB_L(32, 8);
+    } else {
+        if (hd == 128) COMB_L(128, 32);
+        else if (hd == 64) COMB_L(64, 32);
+        else COMB_L(32, 32);
+    }
+#undef COMB_L
     return (int)hipGetLastError();
 }
 
