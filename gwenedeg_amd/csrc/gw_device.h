@@ -151,6 +151,40 @@ __device__ __forceinline__ float swiglu_ref(float h, float h2) {
     return p * r;
 }
 
+// swiglu_ref of N values in place (v[k] = swiglu_ref(v[k], v2[k])), the same operations, the branch on e a select and
+// the N table reads issued together (as separate calls, each read waited for before the next value's); a host with a
+// difference table (gw_exp_delta) or without the tables takes swiglu_ref per value
+template <int N>
+__device__ __forceinline__ void swiglu_ref_n(float (&v)[N], const float (&v2)[N]) {
+    const uint64_t *rt = gw_rcp_blk;
+    if (!rt || gw_exp_delta) {
+        #pragma unroll
+        for (int k = 0; k < N; k++) v[k] = swiglu_ref(v[k], v2[k]);
+        return;
+    }
+    float d[N];
+    uint64_t w[N];
+    #pragma unroll
+    for (int k = 0; k < N; k++) {
+        float x = -v[k];
+        x = x < 80.0f ? x : 80.0f;
+        const uint32_t u = __float_as_uint(x), E = (u >> 23) & 0xffu;
+        const float e = exp_mvec(x); // (x <= -32: unused, d = 1)
+        d[k] = !(u >> 31) || E < 132u ? e + 1.0f : 1.0f;
+    }
+    #pragma unroll
+    for (int k = 0; k < N; k++) w[k] = rt[(__float_as_uint(d[k]) & 0x7fffffu) >> 7];
+    #pragma unroll
+    for (int k = 0; k < N; k++) {
+        const uint32_t b = __float_as_uint(d[k]), m = b & 0x7fffffu;
+        const uint32_t a = (m & 127u) < (uint32_t)(w[k] >> 48) ? (uint32_t)w[k] : (uint32_t)(w[k] >> 24);
+        const float r0 = __uint_as_float(0x3f000000u + (a & 0xffffffu) - (((b >> 23) - 127u) << 23));
+        const float t = r0 * (r0 * d[k]);
+        const float r = (r0 + r0) - t;
+        v[k] = (v[k] * v2[k]) * r;
+    }
+}
+
 __device__ __forceinline__ float wave_max(float v) {
     for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
     return v;

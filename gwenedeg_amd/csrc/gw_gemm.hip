@@ -189,11 +189,17 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const int8_t *__restrict__ W, c
 // k_gemm_q8 for K % GKB == 0 (every stage full: the model's widths): the same tiles, pipeline and fold, with fewer
 // instructions around the fold (which needs 4 VALU instructions per output and group: the bound of this GEMM). Loads
 // through buffer descriptors over the block's own rows: rows past M or N read as 0 (the descriptor's range), so no
-// clamped addresses and no selects; each thread's offsets are fixed and a stage moves the scalar offset only
-template <int GM>
+// clamped addresses and no selects; each thread's offsets are fixed and a stage moves the scalar offset only.
+// SW (GM = 64, w1 / w3 rows interleaved by 4, N % 128 == 0): the SwiGLU and its quantization in the epilogue instead
+// of the fp32 outputs: column n of the matrix is h (n % 8 < 4) or h2 of output 4 (n / 8) + n % 8 - 4; a wave's 64
+// columns are outputs f0 .. f0 + 31, one quantization group of each of its rows: v = swiglu_ref(h, h2), one value
+// per lane and row (pairs exchanged between lanes c and c + 4), the group max over the half-wave's 32 lanes, then the
+// bytes and scale as k_swiglu_quant's quant_lane32 (hq / hs rows of ldq values)
+template <int GM, bool SW>
 __global__ __launch_bounds__(256) void k_gemm_q8f(const int8_t *__restrict__ W, const uint16_t *__restrict__ WS, int N, int K,
                                                   const int8_t *__restrict__ X, const float *__restrict__ XS, int ldx, int M,
-                                                  float *__restrict__ out, int ldo) {
+                                                  float *__restrict__ out, int ldo, int8_t *__restrict__ hq,
+                                                  float *__restrict__ hs, int ldq) {
     constexpr int TJ = GM == 64 ? 2 : 1, XC = GM * 8 / 256;
     __shared__ __align__(16) int8_t xl[2][GM * GROW];
     __shared__ __align__(16) int8_t wl[2][GN * GROW];
@@ -282,13 +288,49 @@ __global__ __launch_bounds__(256) void k_gemm_q8f(const int8_t *__restrict__ W, 
         if (st + 1 < NS) store(nx, buf ^ 1);
         __syncthreads();
     }
-    #pragma unroll
-    for (int j = 0; j < TJ; j++) {
-        const int n = n0 + wn + 32 * j + (lane & 31);
+    if constexpr (SW) {
+        static_assert(TJ == 2, "the SwiGLU epilogue takes a wave's 64 columns");
+        // (lane c of a half-wave: an h lane (c % 8 < 4) takes the pair of column tile 0 (h2 from lane c + 4), an h2 lane
+        // the pair of tile 1 (h from lane c - 4): 16 values per lane, each of the 32 lanes one output of the group)
+        const int c = lane & 31, f0 = (n0 + wn) >> 1;
+        const bool hlane = (c & 7) < 4;
+        const int f = f0 + (hlane ? 0 : 16) + 4 * (c >> 3) + (c & 3);
+        float hv[16], h2v[16];
+        #pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const float a = __shfl_down(acc[0][r], 4), b = __shfl_up(acc[1][r], 4);
+            hv[r] = hlane ? acc[0][r] : b;
+            h2v[r] = hlane ? a : acc[1][r];
+        }
+        swiglu_ref_n<16>(hv, h2v); // (the table reads of all 16 in flight together)
         #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int m = m0 + wm + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            if (m < M && n < N) out[(size_t)m * ldo + n] = acc[j][r];
+            float wmax = fabsf(hv[r]);
+            #pragma unroll
+            for (int o = 16; o >= 1; o >>= 1) {
+                const float tt = __shfl_xor(wmax, o);
+                wmax = tt > wmax ? tt : wmax;
+            }
+            if (m < M) {
+                if (c == 0) hs[(size_t)m * (ldq >> 5) + (f0 >> 5)] = wmax * (1.0f / 127.0f);
+                int32_t qi = 0;
+                if (wmax > 0.0f) {
+                    const float inv = 127.0f / wmax, x = hv[r] * inv;
+                    qi = (int32_t)(x + copysignf(0.49999997f, x));
+                }
+                hq[(size_t)m * ldq + f] = (int8_t)qi;
+            }
+        }
+    } else {
+        #pragma unroll
+        for (int j = 0; j < TJ; j++) {
+            const int n = n0 + wn + 32 * j + (lane & 31);
+            #pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + wm + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m < M && n < N) out[(size_t)m * ldo + n] = acc[j][r];
+            }
         }
     }
 }
@@ -1393,13 +1435,13 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
         const bool g64 = g_tile_rows ? g_tile_rows == 64 : (size_t)nt * ((M + 63) / 64) >= (size_t)4 * cus; // (64-row tiles: enough for several waves per SIMD)
         // (full stages, and every buffer offset inside 2^31: the descriptor-based kernel)
         const bool full = w->cols % GKB == 0 && (size_t)(M + 64) * ldx < ((size_t)1 << 31) && (size_t)GN * w->cols < ((size_t)1 << 31);
-#define GQ_L(KK, GG) hipExtLaunchKernelGGL(KK<GG>, dim3(nt, (M + GG - 1) / GG), dim3(256), 0, s, e0, e1, 0, (const int8_t *)w->codes, \
-                                           (const uint16_t *)w->scales, w->rows, w->cols, xq, xs, ldx, M, out, ldo)
-        if (full && g64) GQ_L(k_gemm_q8f, 64);
-        else if (full) GQ_L(k_gemm_q8f, 32);
-        else if (g64) GQ_L(k_gemm_q8, 64);
-        else GQ_L(k_gemm_q8, 32);
-#undef GQ_L
+        const dim3 g64g(nt, (M + 63) / 64), g32g(nt, (M + 31) / 32);
+#define GQ_ARGS (const int8_t *)w->codes, (const uint16_t *)w->scales, w->rows, w->cols, xq, xs, ldx, M, out, ldo
+        if (full && g64) hipExtLaunchKernelGGL((k_gemm_q8f<64, false>), g64g, dim3(256), 0, s, e0, e1, 0, GQ_ARGS, (int8_t *)NULL, (float *)NULL, 0);
+        else if (full) hipExtLaunchKernelGGL((k_gemm_q8f<32, false>), g32g, dim3(256), 0, s, e0, e1, 0, GQ_ARGS, (int8_t *)NULL, (float *)NULL, 0);
+        else if (g64) hipExtLaunchKernelGGL((k_gemm_q8<64>), g64g, dim3(256), 0, s, e0, e1, 0, GQ_ARGS);
+        else hipExtLaunchKernelGGL((k_gemm_q8<32>), g32g, dim3(256), 0, s, e0, e1, 0, GQ_ARGS);
+#undef GQ_ARGS
         return (int)hipGetLastError();
     }
     if (w->type == GW_Q8_0)
@@ -1439,6 +1481,32 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
     if (w->type == GW_Q3_K) MRQ_L(GW_Q3_K);
 #undef MRQ_L
     return (int)hipErrorInvalidValue;
+}
+
+int gw_k_matmul_swiglu(const GwMat *w, int il, const int8_t *xq, const float *xs, int ldx, int M, int8_t *hq, float *hs, int ldq,
+                       hipStream_t s) {
+    // the w1 / w3 matmul (rows interleaved by il = 4) with the SwiGLU and its quantization in the GEMM's epilogue, where
+    // the prefill GEMM takes 64-row tiles of full stages; -1 (nothing launched): not this case
+    const int nt = (w->rows + GN - 1) / GN;
+    if (w->type != GW_Q8_0 || il != 4 || M <= GW_GEMV_MAX_ROWS || w->rows % GN || ldq != w->rows / 2 || ldq % 32) return -1;
+    const bool g64 = g_tile_rows ? g_tile_rows == 64 : (size_t)nt * ((M + 63) / 64) >= (size_t)4 * gemm_cus();
+    const bool full = w->cols % GKB == 0 && (size_t)(M + 64) * ldx < ((size_t)1 << 31) && (size_t)GN * w->cols < ((size_t)1 << 31);
+    if (!g64 || !full) return -1;
+    hipEvent_t e0, e1;
+    gw_take_launch_events(&e0, &e1);
+    hipExtLaunchKernelGGL((k_gemm_q8f<64, true>), dim3(nt, (M + 63) / 64), dim3(256), 0, s, e0, e1, 0, (const int8_t *)w->codes,
+                          (const uint16_t *)w->scales, w->rows, w->cols, xq, xs, ldx, M, (float *)NULL, 0, hq, hs, ldq);
+    return (int)hipGetLastError();
+}
+
+int gw_g_set_exact(const float *rsq, int bits, const uint64_t *rcp, const uint8_t *expd) {
+    /* this file's copy of the SwiGLU tables (swiglu_ref in the SwiGLU epilogue) on the current device; no kernel here
+     * takes rsqrt_ref (its table is not in this file's code object) */
+    (void)rsq;
+    (void)bits;
+    hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(gw_rcp_blk), &rcp, sizeof(rcp));
+    if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(gw_exp_delta), &expd, sizeof(expd));
+    return (int)e;
 }
 
 int gw_q8_pack(const void *blocks, int N, int K, int8_t *codes, uint16_t *scales, void *stream) {

@@ -211,6 +211,7 @@ float gw_rsqrt_host(float t);   /* the reference's 1.0f / sqrtf(t) on this host 
 float gw_exp_mvec(float x);     /* libmvec's expf by its method: the device's exp_mvec */
 int gw_k_set_exact(const float *rsq, int bits, const uint64_t *rcp, const uint8_t *expd); /* gw_kernels.hip's copy */
 int gw_v_set_exact(const float *rsq, int bits, const uint64_t *rcp, const uint8_t *expd); /* gw_gemv.hip's copy */
+int gw_g_set_exact(const float *rsq, int bits, const uint64_t *rcp, const uint8_t *expd); /* gw_gemm.hip's copy */
 /* vrcp14ps of d >= 1 from the compact table (one word per RCP_BLK_BITS-bit block of mantissas: the block's first value
  * and the value after its one step, as bits above 0.5's, and the step's offset): the result's bits */
 #define RCP_BLK_BITS 7
@@ -283,6 +284,10 @@ void gw_time_next_launch(hipEvent_t a, hipEvent_t b);
 void gw_take_launch_events(hipEvent_t *a, hipEvent_t *b);
 
 /* the matmul dispatch (gw_gemm.hip): out[m * ldo + row] (+)= W row . X row m for M rows, any supported type */
+/* w1 / w3 (rows interleaved by il) with SwiGLU and quantize into hq / hs (rows of ldq = rows / 2) fused into the prefill
+ * GEMM's epilogue; -1 when this matrix / row count does not take that path (nothing launched) */
+int gw_k_matmul_swiglu(const GwMat *w, int il, const int8_t *xq, const float *xs, int ldx, int M, int8_t *hq, float *hs, int ldq,
+                       hipStream_t s);
 int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int M, float *out, int ldo, int mode,
                 hipStream_t s);
 /* a and b (out from column col_b) in one launch where the kernel allows (two K-quant matrices of one type and width,
