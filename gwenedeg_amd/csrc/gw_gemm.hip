@@ -345,6 +345,7 @@ __global__ __launch_bounds__(256) void k_gemm_q8f(const int8_t *__restrict__ W, 
 //     B = 1); term = ((d sc_j) xs) I - (dmin m_j) (xs S)
 //   Q6_K: codes q - 32 (-32 .. 31, exact in int8; q 6-bit from ql / qh); per half-group of 16 the exact sum
 //     (v_mfma_i32_32x32x16_i8), I = sc_0 I_0 + sc_1 I_1 (exact int); term = (d xs) I
+//   IQ4_XS (its integer form: int8 v, int8 S per 16, fp32 D): Q6_K's term with v and S as stored (iquants.h:49-55)
 // then val = val + term in group order. mode 1: out = out + val. K % 256 == 0.
 typedef long i64;
 template <int TYPE, int GM>
@@ -398,6 +399,9 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
                 const uint8_t *b = sbk + (size_t)n * rowb;
                 wa[k] = *(const uint4 *)(b + 32 + 32 * hs + 16 * h);
                 wb[k] = *(const uint4 *)(b + 16 * h);
+            } else if (TYPE == GW_IQ4_XS) { // (unit (row, group p, half h): its 16 int8 values)
+                int row = c >> 3, u = c & 7, p = u >> 1, h = u & 1, n = n0 + row < N ? n0 + row : N - 1;
+                wa[k] = *(const uint4 *)(sbk + (size_t)n * rowb + 128 * hs + 32 * p + 16 * h);
             } else {
                 int row = c >> 3, u = c & 7, p = u >> 1, h = u & 1, n = n0 + row < N ? n0 + row : N - 1;
                 const uint8_t *b = sbk + (size_t)n * rowb;
@@ -413,6 +417,9 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
                 hd0 = *(const uint4 *)b; // d, dmin, then scale bytes 0 .. 11 in words y, z, w
             } else if (TYPE == GW_Q3_K) {
                 hd0 = *(const uint4 *)(b + 96); // the 12 scale bytes, then d
+            } else if (TYPE == GW_IQ4_XS) {
+                hd0 = *(const uint4 *)(b + 256); // the 16 int8 S
+                hd1 = *(const uint4 *)(b + 272); // D (fp32)
             } else {
                 hd0 = *(const uint4 *)(b + 192); // the 16 int8 scales
                 hd1 = *(const uint4 *)(b + 208); // d
@@ -460,6 +467,9 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
                     o4[e] = f | sg * 62u; // (bits 3 .. 7 of each byte whose bit 2 is set)
                 }
                 *(uint4 *)(wl + row * GROW + 32 * p + 16 * h) = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+            } else if (TYPE == GW_IQ4_XS) { // (already int8)
+                int row = c >> 3, u = c & 7, p = u >> 1, h = u & 1;
+                *(uint4 *)(wl + row * GROW + 32 * p + 16 * h) = wa[k];
             } else {
                 // q = ((ql >> 4 (p / 2)) & 15) | ((qh >> 2 p) & 3) << 4; q - 32 as int8: the 6-bit value with bit 5
                 // flipped, sign-extended
@@ -513,7 +523,7 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
                     const int ks = 8 * hs + k;
                     scl[t][k] = (int)(int8_t)((sw[ks >> 2] >> (8 * (ks & 3))) & 0xffu);
                 }
-                f0l[t][0] = h2f_g((uint16_t)(hd1.x & 0xffffu));
+                f0l[t][0] = TYPE == GW_IQ4_XS ? __uint_as_float(hd1.x) : h2f_g((uint16_t)(hd1.x & 0xffffu));
             }
         }
         {
@@ -811,7 +821,7 @@ __global__ __launch_bounds__(SK_T * SB, SB == 1 ? 2 : 1) void k_gemm_kq32(SkMats
 
 // --------------------------------------------------------------------------------------------- K-quants
 
-// The batched GEMV of all three formats: out[m * ldo + row] (+)= W row . X row m for M <= 8 activation rows, R weight
+// The batched GEMV of every weight format: out[m * ldo + row] (+)= W row . X row m for M <= 8 activation rows, R weight
 // rows per block. Each thread takes half-groups (16 weights) j = t, t + 256, ..., U per pass (the launcher uses U = 1),
 // with every load of the pass issued before the first dot; the 16 weights become 16 int8 codes in four 32-bit words, the exact int32 sums by
 // 4 v_dot4 per (row, activation row), and the group's term (the even lane of the pair) goes into LDS:
@@ -823,6 +833,8 @@ __global__ __launch_bounds__(SK_T * SB, SB == 1 ? 2 : 1) void k_gemm_kq32(SkMats
 //   Q5_K (176 bytes: Q4_K's header, qh 32, nibbles 128): Q4_K's term with q 0 .. 31 (bit 4 from qh)
 //   Q3_K (112 bytes: hmask 32, qs 64, 12 bytes of 6-bit scales, fp16 d, 2 of padding): Q6_K's term with q' 0 .. 7
 //     (2 bits from qs, bit 2 from hmask), - 4 sum x and the scales sc - 32
+//   IQ4_XS (its integer form w = D S v, 288 bytes: v as int8, the 16 int8 S, fp32 D): (D * xs) * (float) (S_0 sum v x
+//     + S_1 (...)) over the group's two halves of 16                                                  (iquants.h:49-55)
 // then one lane per (activation row, weight row) folds the groups in order: val = val + term. mode 1: out = out + val.
 // K % 32 == 0 (Q8_0), % 256 (K-quants); the K-quants' q are 0 .. 63, so v_dot4 with signed codes is exact
 template <int TYPE, int M, int R, int U, bool PF>
@@ -919,6 +931,8 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
                         wv[u][r].y = (int)((((uint32_t)q.y >> sl) & 0x03030303u) | ((((uint32_t)hm.y >> sb) & 0x01010101u) << 2));
                         wv[u][r].z = (int)((((uint32_t)q.z >> sl) & 0x03030303u) | ((((uint32_t)hm.z >> sb) & 0x01010101u) << 2));
                         wv[u][r].w = (int)((((uint32_t)q.w >> sl) & 0x03030303u) | ((((uint32_t)hm.w >> sb) & 0x01010101u) << 2));
+                    } else if (TYPE == GW_IQ4_XS) { // (the integer form: the half-group's 16 values v as int8)
+                        wv[u][r] = *(const int4 *)(b + 16 * (j & 15));
                     } else {
                         const int n = sb >> 2, p = sb & 3;
                         int4 lo = *(const int4 *)(b + 64 * n + 32 * (p & 1) + 16 * h);
@@ -962,14 +976,14 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
                     f0[u][r] = h2f_g((uint16_t)(hd.x & 0xffffu)) * (float)scj;
                     f1[u][r] = h2f_g((uint16_t)(hd.x >> 16)) * (float)mj;
                     isc[u][r] = 0;
-                } else if (TYPE == GW_Q6_K) {
-                    const int sblk = j >> 4, sb = (j >> 1) & 7, h = j & 1;
+                } else if (TYPE == GW_Q6_K || TYPE == GW_IQ4_XS) { // (IQ4_XS: the 16 int8 S at 256, D as fp32 at 272)
+                    const int sblk = j >> 4, k = j & 15;
                     const uint8_t *b = rb + (size_t)sblk * bstride;
-                    const uint4 sw = *(const uint4 *)(b + 192); // the 16 int8 scales
-                    const int k = 2 * sb + h;
+                    const uint4 sw = *(const uint4 *)(b + (TYPE == GW_Q6_K ? 192 : 256)); // the 16 int8 scales
                     uint32_t w = k < 4 ? sw.x : k < 8 ? sw.y : k < 12 ? sw.z : sw.w;
                     isc[u][r] = (int)(int8_t)((w >> (8 * (k & 3))) & 0xffu);
-                    f0[u][r] = h2f_g((uint16_t)(*(const uint4 *)(b + 208)).x);
+                    const uint32_t dw = (*(const uint4 *)(b + (TYPE == GW_Q6_K ? 208 : 272))).x;
+                    f0[u][r] = TYPE == GW_Q6_K ? h2f_g((uint16_t)dw) : __uint_as_float(dw);
                     f1[u][r] = 0.0f;
                 } else { // Q3_K (the 12 scale bytes s and d: 6-bit sc_k = low 4 bits of s[k % 8] (k / 8: high nibble) |
                          // bits 2 (k / 4) of s[8 + k % 4] << 4)
@@ -1005,7 +1019,7 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
                 #pragma unroll
                 for (int m = 0; m < M; m++) {
                     int xsum = 0; // K-quants: the sum of the half-group's activation codes
-                    if (TYPE != GW_Q8_0) {
+                    if (TYPE != GW_Q8_0 && TYPE != GW_IQ4_XS) {
                         xsum = __builtin_amdgcn_sdot4(xv[u][m].x, 0x01010101, 0, false);
                         xsum = __builtin_amdgcn_sdot4(xv[u][m].y, 0x01010101, xsum, false);
                         xsum = __builtin_amdgcn_sdot4(xv[u][m].z, 0x01010101, xsum, false);
@@ -1030,6 +1044,10 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
                             term = a - bb;
                         } else if (TYPE == GW_Q3_K) {
                             int I = isc[u][r] * (sd - 4 * xsum);
+                            I = I + __shfl_xor(I, 1);
+                            term = (f0[u][r] * xsg[u][m]) * (float)I;
+                        } else if (TYPE == GW_IQ4_XS) { // (I = S_0 T_0 + S_1 T_1, iquants.h:49-55)
+                            int I = isc[u][r] * sd;
                             I = I + __shfl_xor(I, 1);
                             term = (f0[u][r] * xsg[u][m]) * (float)I;
                         } else {
@@ -1061,8 +1079,8 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
     }
 }
 
-// x[b] = row tok[b] of a K-quant table (Q3_K .. Q6_K), dequantized (kq_dequant_row, kquants.h:222-251; every value
-// one rounding of an exact expression)
+// x[b] = row tok[b] of a K-quant table (Q3_K .. Q6_K) or an IQ4_XS one, dequantized (kq_dequant_row, kquants.h:222-251;
+// iq_dequant_row, iquants.h:217; every value one rounding of an exact expression)
 __global__ __launch_bounds__(256) void k_embed_kq(float *__restrict__ x, int dim, int type, const uint8_t *__restrict__ W,
                                                   int bstride, const int *__restrict__ tok) {
     int bidx = blockIdx.x;
@@ -1089,6 +1107,10 @@ __global__ __launch_bounds__(256) void k_embed_kq(float *__restrict__ x, int dim
             int q = ((b[32 + 32 * n + l] >> (2 * p)) & 3) | ((b[l] >> (k / 32)) & 1) << 2;
             float d = __half2float(__ushort_as_half((uint16_t)(b[108] | b[109] << 8)));
             y = (d * (float)(scj - 32)) * (float)(q - 4);
+        } else if (type == GW_IQ4_XS) { // (D S) v on the integer form (iquants.h:330-340: (d (ls - 32)) kvalues_iq4nl[q])
+            const uint8_t *b = rb + (size_t)s * bstride;
+            const float D = *(const float *)(b + 272);
+            y = (D * (float)(int8_t)b[256 + k / 16]) * (float)(int8_t)b[k];
         } else {
             const uint8_t *b = rb + (size_t)s * bstride;
             int n = k / 128, p = k / 32 % 4, l = k % 32;
@@ -1136,6 +1158,32 @@ static int launch_gemv_mr(const uint8_t *W, const uint16_t *WS, int nrows, int K
 #undef MR_L
     }
     return (int)hipGetLastError();
+}
+
+// IQ4_XS's code values (ggml's kvalues_iq4nl, iq_grids.h:1082)
+static __constant__ int8_t gw_kv_iq4nl[16] = { -127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113 };
+
+// IQ4_XS super-block b (136 bytes: fp16 d, u16 scales_h, scales_l[4], qs[128]; iquants.h:28-30) -> its integer form
+// (GW_QI8_DEV bytes): thread (b, h) writes the 16 values v = kvalues_iq4nl[q] of half-group h (h = 2 ib + hi: the low
+// (hi 0) or high nibbles of qs[16 ib ..]) as int8 at 16 h, and S = ls - 32 of its group at 256 + h; h = 0 also D = d
+// (fp32) at 272 and the zero padding
+__global__ __launch_bounds__(256) void k_iq4xs_to_dev(const uint8_t *__restrict__ src, size_t nblk, uint8_t *__restrict__ dst) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, b = i >> 4;
+    const int h = (int)(i & 15), ib = h >> 1, hi = h & 1;
+    if (b >= nblk) return;
+    const uint8_t *s = src + b * GW_IQ4XS_BYTES;
+    uint8_t *d = dst + b * GW_QI8_DEV;
+    uint32_t w[4] = { 0, 0, 0, 0 };
+    #pragma unroll
+    for (int j = 0; j < 16; j++)
+        w[j >> 2] |= (uint32_t)(uint8_t)gw_kv_iq4nl[(s[8 + 16 * ib + j] >> (4 * hi)) & 15] << (8 * (j & 3));
+    *(uint4 *)(d + 16 * h) = make_uint4(w[0], w[1], w[2], w[3]);
+    const int sh = s[2] | s[3] << 8, ls = ((s[4 + ib / 2] >> (4 * (ib % 2))) & 15) | ((sh >> (2 * ib)) & 3) << 4;
+    d[256 + h] = (uint8_t)(int8_t)(ls - 32);
+    if (h == 0) {
+        const float D = __half2float(__ushort_as_half((uint16_t)(s[0] | s[1] << 8)));
+        *(uint4 *)(d + 272) = make_uint4(__float_as_uint(D), 0u, 0u, 0u);
+    }
 }
 
 // dst super-block i (db bytes) = src super-block i (sb bytes) and zero padding
@@ -1301,8 +1349,13 @@ __global__ __launch_bounds__(KQ16_T, 2) void k_gemm_kq16(SkMats mats, int bstrid
 
 extern "C" {
 
-int gw_k_kq_pad(const uint8_t *src, size_t nblk, int sbytes, int dbytes, uint8_t *dst, hipStream_t s) {
+int gw_k_kq_to_dev(const uint8_t *src, size_t nblk, int type, uint8_t *dst, hipStream_t s) {
+    const int sbytes = gw_kq_file_bytes(type), dbytes = gw_kq_dev_bytes(type);
     if (sbytes < 1 || dbytes < sbytes) return (int)hipErrorInvalidValue;
+    if (type == GW_IQ4_XS) {
+        hipLaunchKernelGGL(k_iq4xs_to_dev, dim3((unsigned)((nblk * 16 + 255) / 256)), dim3(256), 0, s, src, nblk, dst);
+        return (int)hipGetLastError();
+    }
     size_t n = nblk * (size_t)dbytes;
     hipLaunchKernelGGL(k_kq_pad, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, nblk, sbytes, dbytes, dst);
     return (int)hipGetLastError();
@@ -1467,6 +1520,9 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
         } else if (w->type == GW_Q5_K) {
             if (g64) KQ_L(GW_Q5_K, 64);
             else KQ_L(GW_Q5_K, 32);
+        } else if (w->type == GW_IQ4_XS) {
+            if (g64) KQ_L(GW_IQ4_XS, 64);
+            else KQ_L(GW_IQ4_XS, 32);
         } else {
             if (g64) KQ_L(GW_Q3_K, 64);
             else KQ_L(GW_Q3_K, 32);
@@ -1479,6 +1535,7 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
     if (w->type == GW_Q6_K) MRQ_L(GW_Q6_K);
     if (w->type == GW_Q5_K) MRQ_L(GW_Q5_K);
     if (w->type == GW_Q3_K) MRQ_L(GW_Q3_K);
+    if (w->type == GW_IQ4_XS) MRQ_L(GW_IQ4_XS);
 #undef MRQ_L
     return (int)hipErrorInvalidValue;
 }
@@ -1570,13 +1627,13 @@ int gw_kq_matmul(float *out, int type, const void *blocks, int N, int K, const i
     const int fb = gw_kq_file_bytes(type), db = gw_kq_dev_bytes(type);
     GwMat w = { type, N, K, NULL, NULL, (uint8_t *)blocks, fb };
     if (fb == db) return gw_k_matmul(&w, xq, xs, K, M, out, N, 0, (hipStream_t)stream) ? RQ_ERR_STATE : RQ_OK;
-    // Q6_K, Q3_K: the file's blocks padded into the device layout first (a temporary copy)
+    // Q6_K, Q3_K, IQ4_XS: the file's blocks put into the device layout first (a temporary copy)
     size_t nblk = (size_t)N * (K / 256);
     uint8_t *pad = NULL;
     if (hipMalloc((void **)&pad, nblk * db) != hipSuccess) return RQ_ERR_NOMEM;
     w.blocks = pad;
     w.bstride = db;
-    int rc = gw_k_kq_pad((const uint8_t *)blocks, nblk, fb, db, pad, (hipStream_t)stream) ||
+    int rc = gw_k_kq_to_dev((const uint8_t *)blocks, nblk, type, pad, (hipStream_t)stream) ||
              gw_k_matmul(&w, xq, xs, K, M, out, N, 0, (hipStream_t)stream) ? RQ_ERR_STATE : RQ_OK;
     if (hipStreamSynchronize((hipStream_t)stream) != hipSuccess) rc = RQ_ERR_STATE;
     (void)hipFree(pad);

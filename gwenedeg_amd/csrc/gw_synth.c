@@ -14,6 +14,8 @@
  *   Q6_K: 16 sub-blocks of 16, int8 sub-scales against d, q in 0..63 (value q - 32)
  *   Q5_K: as Q4_K with q in 0..31 (bit 4 in qh)
  *   Q3_K: 16 sub-blocks of 16, 6-bit scales sc (value (d (sc - 32)) q) with sc - 32 in 0..31 here, q in -4..3
+ *   IQ4_XS (iquants.h:28-30): 8 groups of 32, 6-bit ls (value (d (ls - 32)) kvalues_iq4nl[q]) with ls - 32 in 0..31
+ *     for even groups and -31..0 for odd ones (both signs of the scale), q the nearest of the 16 code values
  * Any valid block decodes the same way on both sides, so these simple encoders suffice for parity. */
 #include <math.h>
 #include <pthread.h>
@@ -24,7 +26,11 @@
 
 #include "gw_synth.h"
 
-enum { T_F32 = 0, T_Q8_0 = 8, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14 };
+enum { T_F32 = 0, T_Q8_0 = 8, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ4_XS = 23 };
+#define IS_SB(t) (((t) >= T_Q3_K && (t) <= T_Q6_K) || (t) == T_IQ4_XS) /* (super-blocks of 256) */
+
+/* IQ4_XS's code values (ggml's kvalues_iq4nl) */
+static const int8_t kv_iq4nl[16] = { -127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113 };
 
 static uint16_t f32_to_f16_rne(float f) {
     uint32_t u;
@@ -80,6 +86,7 @@ size_t gw_synth_row_bytes(int type, int k) {
     if (type == T_Q5_K) return (size_t)k / 256 * 176;
     if (type == T_Q3_K) return (size_t)k / 256 * 110;
     if (type == T_Q6_K) return (size_t)k / 256 * 210;
+    if (type == T_IQ4_XS) return (size_t)k / 256 * 136;
     return (size_t)k * 4;
 }
 
@@ -227,12 +234,48 @@ static void enc_q6_k(uint8_t *o, const float *x, int k) {
     }
 }
 
+static void enc_iq4_xs(uint8_t *o, const float *x, int k) {
+    /* 136 bytes: fp16 d, u16 scales_h (bits 2 ib, 2 ib + 1: ls >> 4), scales_l[4] (nibble ib % 2 of byte ib / 2: ls & 15),
+     * qs[128] (qs[16 ib + j]: low nibble the code of value j of group ib, high nibble of value 16 + j) */
+    for (int sb = 0; sb < k / 256; sb++, o += 136, x += 256) {
+        float sg[8], smax = 0;
+        for (int ib = 0; ib < 8; ib++) {
+            float amax = 0;
+            for (int i = 0; i < 32; i++) amax = fabsf(x[32 * ib + i]) > amax ? fabsf(x[32 * ib + i]) : amax;
+            sg[ib] = amax / 113.0f;
+            smax = sg[ib] > smax ? sg[ib] : smax;
+        }
+        uint16_t hd = f32_to_f16_rne(smax / 31.0f);
+        float d = f16_to_f32(hd);
+        memset(o, 0, 136);
+        memcpy(o, &hd, 2);
+        uint16_t sh = 0;
+        for (int ib = 0; ib < 8; ib++) {
+            int a = d > 0 ? (int)lroundf(sg[ib] / d) : 0;
+            a = a > 31 ? 31 : a;
+            const int S = ib & 1 ? -a : a, ls = S + 32;
+            o[4 + ib / 2] |= (uint8_t)((ls & 15) << (4 * (ib % 2)));
+            sh |= (uint16_t)(((ls >> 4) & 3) << (2 * ib));
+            const float dl = d * (float)S;
+            for (int i = 0; i < 32; i++) {
+                const float t = dl != 0 ? x[32 * ib + i] / dl : 0.0f;
+                int best = 0;
+                for (int q = 1; q < 16; q++)
+                    if (fabsf((float)kv_iq4nl[q] - t) < fabsf((float)kv_iq4nl[best] - t)) best = q;
+                o[8 + 16 * ib + i % 16] |= (uint8_t)(best << (4 * (i / 16)));
+            }
+        }
+        memcpy(o + 2, &sh, 2);
+    }
+}
+
 void gw_synth_encode_row(int type, uint8_t *o, const float *x, int k) {
     if (type == T_Q8_0) enc_q8_0(o, x, k);
     else if (type == T_Q4_K) enc_q45_k(o, x, k, 0);
     else if (type == T_Q5_K) enc_q45_k(o, x, k, 1);
     else if (type == T_Q3_K) enc_q3_k(o, x, k);
     else if (type == T_Q6_K) enc_q6_k(o, x, k);
+    else if (type == T_IQ4_XS) enc_iq4_xs(o, x, k);
     else memcpy(o, x, (size_t)k * 4);
 }
 
@@ -314,7 +357,7 @@ int gw_synth_gguf(const char *path, const GwSynthCfg *c, unsigned long long seed
     const uint64_t align = 32;
     uint64_t off = 0;
     for (int i = 0; i < nt; i++) {
-        if (T[i].type >= T_Q3_K && T[i].type <= T_Q6_K && T[i].cols % 256) { free(T); return -1; }
+        if (IS_SB(T[i].type) && T[i].cols % 256) { free(T); return -1; }
         if (T[i].type == T_Q8_0 && T[i].cols % 32) { free(T); return -1; }
         T[i].off = off;
         uint64_t sz = T[i].rows ? (uint64_t)T[i].rows * gw_synth_row_bytes(T[i].type, T[i].cols) : (uint64_t)T[i].cols * 4;

@@ -16,7 +16,9 @@
  *     matmul bit for bit against the reference's own compiled kernels (oracle/_ref/ref_q8op: q8p_gemv_rows,
  *     q8p_gemm_item) at M = 1, 3, 8, 13, and against the golden vectors of tests/golden/ref_kernels.npz;
  *   K-quant fold: bit for bit against the reference's kq_dot (ref_q8op kq); the dequantization against an
- *     independent numpy decoder of the Q4_K / Q6_K block formats;
+ *     independent numpy decoder of the Q3_K / Q4_K / Q5_K / Q6_K block formats;
+ *   IQ4_XS fold: bit for bit against the reference's iq_rows (ref_q8op iq: its AVX-512 i-quant kernels at 1 row and in
+ *     blocks of 8); the dequantization against an independent numpy decoder of the block format;
  *   exp_att: within 2 ulp of expf, the -86 clamp; attention: one block against a float64 softmax, several blocks
  *     against the one-block result (the combine's invariant);
  *   rsqrt (or_rsqrt_ref: the reference's -Ofast 1.0f / sqrtf = rsqrtss + one Newton step): within 3 ulp of IEEE and,
@@ -24,7 +26,7 @@
  *     vector expf + vrcp14ps + Newton, the -Ofast lowering of forward.c:1953-1958): against the product's
  *     host-measured tables and, through the whole forward, bit for bit;
  *   the whole forward (or_forward_token): logits bit for bit against the compiled reference (oracle/_ref/ref_driver)
- *     on synthetic Q8_0 and Q4_K_M models, including a Qwen3-0.6B-shaped model with 3 layers.
+ *     on synthetic Q8_0, Q4_K_M and IQ4_XS models, including a Qwen3-0.6B-shaped model with 3 layers.
  * On a host without AVX-512 the oracle's SwiGLU falls back to the portable form (1 / (1 + expf)); the reference built
  * for such a host lowers the loop to other instructions, so there the SwiGLU is pinned only to tolerance.
  */
@@ -152,7 +154,11 @@ void or_q8_from_blocks(int8_t *q, float *s, const uint8_t *blk, size_t nblk) {
 
 /* ---------------------------------------------------------------------------------------- K-quants */
 
-enum { T_F32 = 0, T_Q8_0 = 8, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14 };
+enum { T_F32 = 0, T_Q8_0 = 8, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ4_XS = 23 };
+#define IS_KQ(t) (((t) >= T_Q3_K && (t) <= T_Q6_K) || (t) == T_IQ4_XS)
+
+/* IQ4_XS's 16 code values (ggml's kvalues_iq4nl, iq_grids.h:1082; iquants.h:28-30) */
+static const int8_t kv_iq4nl[16] = { -127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113 };
 
 static uint16_t u16(const uint8_t *p) { uint16_t v; memcpy(&v, p, 2); return v; }
 
@@ -189,7 +195,18 @@ static int q3k_scale(const uint8_t *b, int j) { /* kquants.h:207-212: the 6-bit 
     return (j < 8 ? sc[j] & 15 : sc[j - 8] >> 4) | ((sc[8 + j % 4] >> (2 * (j / 4))) & 3) << 4;
 }
 
-static int kq_bytes(int type) { return type == T_Q4_K ? 144 : type == T_Q5_K ? 176 : type == T_Q3_K ? 110 : 210; }
+static int kq_bytes(int type) {
+    return type == T_Q4_K ? 144 : type == T_Q5_K ? 176 : type == T_Q3_K ? 110 : type == T_IQ4_XS ? 136 : 210;
+}
+
+static int iq4xs_ls(const uint8_t *b, int ib) { /* iquants.h:28-29: the 6-bit scale of group ib (before the - 32) */
+    return ((b[4 + ib / 2] >> (4 * (ib % 2))) & 15) | ((u16(b + 2) >> (2 * ib)) & 3) << 4;
+}
+
+static int iq4xs_v(const uint8_t *b, int i) { /* iquants.h:29: value i's code, qs[16 ib + j] low nibble j, high 16 + j */
+    int ib = i / 32, l = i % 32;
+    return kv_iq4nl[(b[8 + 16 * ib + l % 16] >> (4 * (l / 16))) & 15];
+}
 
 void or_kq_dequant_row(int type, const uint8_t *blk, int n, float *y) {
     /* kquants.h:222-251 */
@@ -209,6 +226,12 @@ void or_kq_dequant_row(int type, const uint8_t *blk, int n, float *y) {
             for (int j = 0; j < 16; j++) {
                 float dl = d * (float)(q3k_scale(b, j) - 32);
                 for (int l = 0; l < 16; l++) y[16 * j + l] = dl * (float)(q3k_q(b, 16 * j + l) - 4);
+            }
+        } else if (type == T_IQ4_XS) { /* iquants.h:330-340 (ggml's dequantize_row_iq4_xs): (d (ls - 32)) v */
+            float d = or_fp16_to_f32(u16(b));
+            for (int ib = 0; ib < 8; ib++) {
+                float dl = d * (float)(iq4xs_ls(b, ib) - 32);
+                for (int l = 0; l < 32; l++) y[32 * ib + l] = dl * (float)iq4xs_v(b, 32 * ib + l);
             }
         } else {
             float d = or_fp16_to_f32(u16(b + 208));
@@ -256,6 +279,14 @@ static float kq_dot_row(int type, const uint8_t *row, const int8_t *x, const flo
                 }
                 float d = or_fp16_to_f32(u16(b + 108));
                 val = val + (d * xs[g]) * (float)I;
+            } else if (type == T_IQ4_XS) { /* iquants.h:49-55: I = S_0 T_0 + S_1 T_1, S = ls - 32 on both halves, D = d */
+                int32_t I = 0, S = iq4xs_ls(b, j) - 32;
+                for (int h = 0; h < 2; h++) {
+                    int32_t t = 0;
+                    for (int i = 0; i < 16; i++) t += iq4xs_v(b, 32 * j + 16 * h + i) * xg[16 * h + i];
+                    I += S * t;
+                }
+                val = val + (or_fp16_to_f32(u16(b)) * xs[g]) * (float)I;
             } else {
                 int32_t I = 0;
                 for (int h = 0; h < 2; h++) {
@@ -549,7 +580,7 @@ static int rd(const uint8_t *f, size_t sz, size_t *p, void *dst, size_t n) {
 }
 
 static size_t row_bytes(int type, int k) {
-    return type == T_Q8_0 ? (size_t)k / 32 * 34 : (type >= T_Q3_K && type <= T_Q6_K) ? (size_t)k / 256 * kq_bytes(type) : (size_t)k * 4;
+    return type == T_Q8_0 ? (size_t)k / 32 * 34 : IS_KQ(type) ? (size_t)k / 256 * kq_bytes(type) : (size_t)k * 4;
 }
 
 OrModel *or_model_load(const char *path, int cap, char *err, size_t errlen) {

@@ -18,6 +18,7 @@ REF_DIR = os.path.join(HERE, "_ref")
 REF_DRIVER = os.path.join(REF_DIR, "ref_driver")
 REF_Q8OP = os.path.join(REF_DIR, "ref_q8op")
 REF_SAMPLE = os.path.join(REF_DIR, "ref_sample")
+IQ4_XS = 23  # (ggml type number)
 
 _lib = None
 
@@ -264,10 +265,11 @@ def run_ref_kq(workdir: str, typ: int, blocks, xq, xs, N: int, K: int, timeout: 
     paths = [os.path.join(workdir, n) for n in ("blk.bin", "x.bin", "xs.bin", "out.bin")]
     for a, p in zip((blocks, xq, xs), paths):
         np.ascontiguousarray(a).tofile(p)
-    cmd = [REF_Q8OP, "kq", str(typ), *paths[:3], str(M), str(N), str(K), paths[3]]
+    mode = "iq" if typ == IQ4_XS else "kq"  # (the i-quants: iquants.h's packing and kernels)
+    cmd = [REF_Q8OP, mode, str(typ), *paths[:3], str(M), str(N), str(K), paths[3]]
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)
     if r.returncode != 0:
-        raise RuntimeError(f"ref_q8op kq failed: {r.stderr[-2000:]}")
+        raise RuntimeError(f"ref_q8op {mode} failed: {r.stderr[-2000:]}")
     return np.fromfile(paths[3], np.float32).reshape(M, N)
 
 

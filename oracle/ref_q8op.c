@@ -12,6 +12,10 @@
  *   ref_q8op kq TYPE BLK X XS M N K OUT
  *       BLK: N rows of K / 256 GGUF K-quant blocks (TYPE 11 Q3_K, 12 Q4_K, 13 Q5_K, 14 Q6_K), packed by kq_pack_blocks
  *       (kquants.h:253) and multiplied by the generic kq_dot (:608) with kq_act_prep's xf (:392).
+ *   ref_q8op iq TYPE BLK X XS M N K OUT
+ *       BLK: N rows of K / 256 GGUF i-quant blocks (TYPE 23 IQ4_XS), packed by iq_pack_blocks (iquants.h:503) and
+ *       multiplied by iq_rows (:1478), the forward's dispatch (the AVX-512 kernels of this build), with the activation
+ *       sums of 16 of kq512_c16 (kernels_avx512.h:342).
  * All files raw little-endian arrays. */
 #include <pthread.h>
 #include <stdint.h>
@@ -21,6 +25,9 @@
 #include <time.h>
 
 #include "kernels_avx512.h"
+#include "iquants.h"
+
+int rq_iq_gather = 0; /* (model.c:9: the VBMI decode, as the forward runs it) */
 
 #ifndef RUNQ_VNNI
 #error "needs the AVX-512 VNNI kernels (an AVX-512 VNNI -march)"
@@ -144,6 +151,23 @@ int main(int argc, char **argv) {
         fclose(f);
         return 0;
     }
-    fprintf(stderr, "usage: ref_q8op q8 W WS X XS M N K OUT [reps threads] | kq TYPE BLK X XS M N K OUT\n");
+    if (argc >= 10 && !strcmp(argv[1], "iq")) {
+        int type = atoi(argv[2]), M = atoi(argv[6]), N = atoi(argv[7]), K = atoi(argv[8]);
+        if (type != GGML_IQ4_XS || M < 1 || N % 16 || K % 256) { fprintf(stderr, "ref_q8op: bad iq args\n"); return 2; }
+        uint8_t *blk = slurp(argv[3], (size_t)N * (K / 256) * iq_block_bytes(type));
+        int8_t *X = slurp(argv[4], (size_t)M * K);
+        float *XS = slurp(argv[5], (size_t)M * (K / 32) * 4);
+        uint8_t *kp = aligned_alloc(64, (iq_size(type, N, K) + 63) / 64 * 64);
+        iq_pack_blocks(type, kp, blk, N / 16, K);
+        int32_t *c16 = malloc((size_t)M * (K / 16) * sizeof(int32_t));
+        for (int b = 0; b < M; b++) kq512_c16(c16 + (size_t)b * (K / 16), X + (size_t)b * K, K);
+        float *out = calloc((size_t)M * N, sizeof(float));
+        iq_rows(type, out, N, X, K, XS, c16, M, kp, K, 0, N / 16);
+        FILE *f = fopen(argv[9], "wb");
+        if (!f || fwrite(out, sizeof(float), (size_t)M * N, f) != (size_t)M * N) { perror(argv[9]); return 1; }
+        fclose(f);
+        return 0;
+    }
+    fprintf(stderr, "usage: ref_q8op q8 W WS X XS M N K OUT [reps threads] | kq|iq TYPE BLK X XS M N K OUT\n");
     return 2;
 }

@@ -6,7 +6,7 @@
 * where the reference exposes no entry point, against what the mathematics fixes: brute-force integer block sums,
   every fp16 value, IEEE float16 rounding and the reference's saturation, the quantizer's closed form and its
   rounding of exact halves away from zero, float64 exp / attention / RoPE, an independent numpy decoder of the ggml Q3_K /
-  Q4_K / Q5_K / Q6_K block formats (the published layout);
+  Q4_K / Q5_K / Q6_K / IQ4_XS block formats (the published layout);
 * the product's host-measured tables (gwenedeg_amd/csrc/gw_exact.c: the reference's rsqrtss / vrcp14ps / libmvec expf
   as the device reproduces them) against the reference's own operations on this host.
 The reference's fixtures for this path (tests/golden/logits, dequant) need model files absent here; the golden vectors
@@ -242,12 +242,33 @@ def _np_dequant_q3k(b):
     return y
 
 
-_KQ_DEC = {11: (_np_dequant_q3k, 110), 12: (_np_dequant_q4k, 144), 13: (_np_dequant_q5k, 176), 14: (_np_dequant_q6k, 210)}
+_KV_IQ4NL = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.float32)
 
 
-@pytest.mark.parametrize("typ", [11, 12, 13, 14])
+def _np_dequant_iq4xs(b):
+    """ggml's dequantize_row_iq4_xs on one 136-byte block (fp16 d, u16 scales_h, scales_l[4], qs[128]): group ib's
+    6-bit ls from nibble ib % 2 of scales_l[ib / 2] and bits 2 ib .. 2 ib + 1 of scales_h, values d (ls - 32) times the
+    code value of the low (first 16) and high (last 16) nibbles of qs[16 ib ..]"""
+    d = b[0:2].view(np.float16)[0].astype(np.float32)
+    sh = int(b[2:4].view(np.uint16)[0])
+    y = np.zeros(256, np.float32)
+    for ib in range(8):
+        ls = ((int(b[4 + ib // 2]) >> (4 * (ib % 2))) & 15) | (((sh >> (2 * ib)) & 3) << 4)
+        dl = np.float32(d * np.float32(ls - 32))
+        q = b[8 + 16 * ib:8 + 16 * ib + 16].astype(np.int32)
+        y[32 * ib:32 * ib + 16] = dl * _KV_IQ4NL[q & 15]
+        y[32 * ib + 16:32 * ib + 32] = dl * _KV_IQ4NL[q >> 4]
+    return y
+
+
+_KQ_DEC = {11: (_np_dequant_q3k, 110), 12: (_np_dequant_q4k, 144), 13: (_np_dequant_q5k, 176), 14: (_np_dequant_q6k, 210),
+           23: (_np_dequant_iq4xs, 136)}
+
+
+@pytest.mark.parametrize("typ", [11, 12, 13, 14, 23])
 def test_kq_dequant_vs_independent_decoder(typ):
-    """or_kq_dequant_row (kquants.h:222-251) against a numpy decoder written from ggml's block layout: bit for bit"""
+    """or_kq_dequant_row (kquants.h:222-251; IQ4_XS iquants.h:330-340) against a numpy decoder written from ggml's block
+    layout: bit for bit"""
     blk = _kq_blocks(typ, 4, 512, 20 + typ)
     dec, bs = _KQ_DEC[typ]
     for n in range(4):
@@ -257,11 +278,12 @@ def test_kq_dequant_vs_independent_decoder(typ):
 
 
 @need_ref
-@pytest.mark.parametrize("typ", [11, 12, 13, 14])
-@pytest.mark.parametrize("M", [1, 5])
+@pytest.mark.parametrize("typ", [11, 12, 13, 14, 23])
+@pytest.mark.parametrize("M", [1, 5, 11])
 def test_kq_matmul_vs_reference(tmp_path, typ, M):
-    """or_kq_matmul (kquants.h:86-109's fold) against the reference's kq dot compiled from its sources: bit for bit;
-    and close to the float64 product of the dequantized rows"""
+    """or_kq_matmul (kquants.h:86-109's fold; IQ4_XS iquants.h:49-55's) against the reference's kernels compiled from
+    its sources (K-quants: the generic kq_dot; IQ4_XS: iq_rows, the forward's AVX-512 dispatch, 1 row and blocks of 8):
+    bit for bit; and close to the float64 product of the dequantized rows"""
     N, K = 32, 1024
     blk = _kq_blocks(typ, N, K, 30 + typ + M)
     xq, xs = orc.quantize(np.random.default_rng(M).standard_normal((M, K)).astype(np.float32))
@@ -398,6 +420,7 @@ def test_attention_combine_matches_single_pass():
 @pytest.mark.parametrize("shape,over,n,bf16", [
     ("tiny", {}, 40, False),
     ("tiny_kq", {}, 20, False),
+    ("tiny_iq4xs", {}, 20, False),
     ("qwen3_0_6b", dict(n_layers=3, vocab=4096, tied=0), 12, False),
     ("tiny", {}, 40, True),
     ("qwen3_0_6b", dict(n_layers=2, vocab=4096, tied=0), 270, True),
