@@ -38,8 +38,9 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
 # the prefill GEMM's exact fold (val = val + (ws * xs) * (float) isum per output and group of 32, each op rounded):
-# 4 VALU lane-ops (convert, 2 multiplies, add) per 64 int8 ops; 256 CUs x 64 fp32 lanes x 2.4 GHz = 39.3 T lane-ops/s
-FOLD_BOUND_TOPS = 256 * 64 * 2.4e9 / 4 * 64 / 1e12
+# ws * xs from an outer-product MFMA, then 3 VALU lane-ops (convert, multiply, add) per 64 int8 ops; 256 CUs x 64 fp32
+# lanes x 2.4 GHz = 39.3 T lane-ops/s
+FOLD_BOUND_TOPS = 256 * 64 * 2.4e9 / 3 * 64 / 1e12
 GEMV_CLASSES = ("matmul qkv", "matmul wo", "matmul w1+w3", "matmul w2", "classifier")
 
 

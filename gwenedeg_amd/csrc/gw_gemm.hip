@@ -71,6 +71,7 @@ __global__ __launch_bounds__(256) void k_fill_synthetic(uint16_t *kc, uint16_t *
 // result register r of lane l is C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32]
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x32 __attribute__((ext_vector_type(32)));
 #define GN 128
 #define GKB 128
 #define GROW 144
@@ -255,39 +256,53 @@ __global__ __launch_bounds__(256) void k_gemm_q8f(const int8_t *__restrict__ W, 
         wsl[buf][srow][sgg] = o.ws0;
         wsl[buf][srow + 64][sgg] = o.ws1;
     };
-    store(load(0), 0);
-    __syncthreads();
     const int xa = (wm + (lane & 31)) * GROW + 16 * (lane >> 5), wa = (wn + (lane & 31)) * GROW + 16 * (lane >> 5);
-    for (int st = 0; st < NS; st++) {
-        const int buf = st & 1;
-        const St nx = load(st + 1);
-        // (rolled: unrolled, the compiler keeps every MFMA result live at once: 280 registers with two tiles per wave;
-        // with one tile, 191 registers and qkv / wo / w2 20-35 % slower, measured)
+    auto compute = [&](int buf) __attribute__((always_inline)) {
+        // the stage's groups in pairs (g0, g0 + 1): per 32 x 32 tile the two exact sums (int8 MFMA) and the two groups'
+        // scale products ws * xs as one outer-product MFMA (v_mfma_f32_32x32x1f32, two blocks: lane i gives group
+        // g0 + i / 32's xs of row i % 32 and ws of column i % 32; each result one fp32 product rounded once, as the
+        // VALU's multiply), so the VALU's fold is 3 instructions per output and group: (float) isum, the multiply by
+        // the product, the add. (rolled: unrolled, the compiler keeps every MFMA result live at once; an explicit
+        // software pipeline, the next tile's MFMAs issued before this tile's fold and pinned there, measured 17 % slower)
         #pragma unroll 1
-        for (int gg = 0; gg < 4; gg++) {
-            const i32x4 a = *(const i32x4 *)(&xl[buf][xa + gg * 32]);
+        for (int g0 = 0; g0 < 4; g0 += 2) {
+            const i32x4 a0 = *(const i32x4 *)(&xl[buf][xa + g0 * 32]), a1 = *(const i32x4 *)(&xl[buf][xa + g0 * 32 + 32]);
+            const float xsa = xsl[buf][g0 + (lane >> 5)][wm + (lane & 31)];
             #pragma unroll
             for (int j = 0; j < TJ; j++) {
-                const i32x4 b = *(const i32x4 *)(&wl[buf][wa + 32 * j * GROW + gg * 32]);
+                const i32x4 b0 = *(const i32x4 *)(&wl[buf][wa + 32 * j * GROW + g0 * 32]);
+                const i32x4 b1 = *(const i32x4 *)(&wl[buf][wa + 32 * j * GROW + g0 * 32 + 32]);
                 const i32x16 z = { 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0 };
-                const i32x16 I = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
-                const float ws = wsl[buf][wn + 32 * j + (lane & 31)][gg];
+                const f32x32 zf = {};
+                const i32x16 I0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, z, 0, 0, 0);
+                const i32x16 I1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, z, 0, 0, 0);
+                const float wsb = wsl[buf][wn + 32 * j + (lane & 31)][g0 + (lane >> 5)];
+                const f32x32 C = __builtin_amdgcn_mfma_f32_32x32x1f32(xsa, wsb, zf, 0, 0, 0);
                 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const float4 xs4 = *(const float4 *)(&xsl[buf][gg][wm + 8 * q + 4 * (lane >> 5)]);
-                    const float xsq[4] = { xs4.x, xs4.y, xs4.z, xs4.w };
-                    #pragma unroll
-                    for (int s = 0; s < 4; s++) {
-                        const float sc = ws * xsq[s];
-                        const float p = sc * (float)I[4 * q + s];
-                        acc[j][4 * q + s] = acc[j][4 * q + s] + p;
-                    }
-                }
+                for (int r = 0; r < 16; r++) acc[j][r] = acc[j][r] + C[r] * (float)I0[r];
+                #pragma unroll
+                for (int r = 0; r < 16; r++) acc[j][r] = acc[j][r] + C[16 + r] * (float)I1[r];
             }
         }
-        if (st + 1 < NS) store(nx, buf ^ 1);
+    };
+    // two stages' loads in flight: register sets sa and sb take turns (stage st + 1 in sa, st + 2 loaded into sb while
+    // stage st is computed, and so on; a copy from one set into the other would wait for its loads), the stages in LDS
+    // buffers 0 / 1 by parity; each buffer is rewritten only after the barrier that follows its readers
+    St sa = load(1);
+    store(load(0), 0);
+    __syncthreads();
+    int st = 0;
+    for (; st + 1 < NS; st += 2) {
+        const St sb = load(st + 2); // (past the last stage: inside the buffers or read as 0; never stored)
+        compute(0);
+        store(sa, 1);
+        __syncthreads();
+        sa = load(st + 3);
+        compute(1);
+        if (st + 2 < NS) store(sb, 0);
         __syncthreads();
     }
+    if (st < NS) compute(0); // (an odd stage count: the last stage, in buffer 0)
     if constexpr (SW) {
         static_assert(TJ == 2, "the SwiGLU epilogue takes a wave's 64 columns");
         // (lane c of a half-wave: an h lane (c % 8 < 4) takes the pair of column tile 0 (h2 from lane c + 4), an h2 lane
