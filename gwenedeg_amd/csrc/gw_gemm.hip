@@ -361,6 +361,8 @@ __global__ __launch_bounds__(256) void k_gemm_q8f(const int8_t *__restrict__ W, 
 //   Q6_K: codes q - 32 (-32 .. 31, exact in int8; q 6-bit from ql / qh); per half-group of 16 the exact sum
 //     (v_mfma_i32_32x32x16_i8), I = sc_0 I_0 + sc_1 I_1 (exact int); term = (d xs) I
 //   IQ4_XS (its integer form: int8 v, int8 S per 16, fp32 D): Q6_K's term with v and S as stored (iquants.h:49-55)
+//   Q2_K (96 bytes: the file's 84 and padding; q 0 .. 3): Q6_K's term with the 4-bit scales sc, minus the mins' term
+//     (dmin xs) M, M = m_0 X_0 + m_1 X_1 from the sums of x of each half (the same MFMA with B = 1)   (iquants.h:56-57)
 // then val = val + term in group order. mode 1: out = out + val. K % 256 == 0.
 typedef long i64;
 template <int TYPE, int GM>
@@ -417,6 +419,9 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
             } else if (TYPE == GW_IQ4_XS) { // (unit (row, group p, half h): its 16 int8 values)
                 int row = c >> 3, u = c & 7, p = u >> 1, h = u & 1, n = n0 + row < N ? n0 + row : N - 1;
                 wa[k] = *(const uint4 *)(sbk + (size_t)n * rowb + 128 * hs + 32 * p + 16 * h);
+            } else if (TYPE == GW_Q2_K) { // (unit (row, group p, half h): sub-block 8 hs + 2 p + h, 16 bytes of qs)
+                int row = c >> 3, u = c & 7, h = u & 1, n = n0 + row < N ? n0 + row : N - 1;
+                wa[k] = *(const uint4 *)(sbk + (size_t)n * rowb + 16 + 32 * hs + 16 * h);
             } else {
                 int row = c >> 3, u = c & 7, p = u >> 1, h = u & 1, n = n0 + row < N ? n0 + row : N - 1;
                 const uint8_t *b = sbk + (size_t)n * rowb;
@@ -435,6 +440,9 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
             } else if (TYPE == GW_IQ4_XS) {
                 hd0 = *(const uint4 *)(b + 256); // the 16 int8 S
                 hd1 = *(const uint4 *)(b + 272); // D (fp32)
+            } else if (TYPE == GW_Q2_K) {
+                hd0 = *(const uint4 *)b;        // the 16 scale bytes (sc | m << 4)
+                hd1 = *(const uint4 *)(b + 80); // d, dmin
             } else {
                 hd0 = *(const uint4 *)(b + 192); // the 16 int8 scales
                 hd1 = *(const uint4 *)(b + 208); // d
@@ -485,6 +493,11 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
             } else if (TYPE == GW_IQ4_XS) { // (already int8)
                 int row = c >> 3, u = c & 7, p = u >> 1, h = u & 1;
                 *(uint4 *)(wl + row * GROW + 32 * p + 16 * h) = wa[k];
+            } else if (TYPE == GW_Q2_K) { // q = 2 bits 2 p of each byte (0 .. 3)
+                int row = c >> 3, u = c & 7, p = u >> 1, h = u & 1, sl = 2 * p;
+                *(uint4 *)(wl + row * GROW + 32 * p + 16 * h) =
+                    make_uint4((wa[k].x >> sl) & 0x03030303u, (wa[k].y >> sl) & 0x03030303u, (wa[k].z >> sl) & 0x03030303u,
+                               (wa[k].w >> sl) & 0x03030303u);
             } else {
                 // q = ((ql >> 4 (p / 2)) & 15) | ((qh >> 2 p) & 3) << 4; q - 32 as int8: the 6-bit value with bit 5
                 // flipped, sign-extended
@@ -539,6 +552,11 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
                     scl[t][k] = (int)(int8_t)((sw[ks >> 2] >> (8 * (ks & 3))) & 0xffu);
                 }
                 f0l[t][0] = TYPE == GW_IQ4_XS ? __uint_as_float(hd1.x) : h2f_g((uint16_t)(hd1.x & 0xffffu));
+                if (TYPE == GW_Q2_K) { // (scl: the raw byte sc | m << 4; f1l: dmin)
+                    #pragma unroll
+                    for (int k = 0; k < 8; k++) scl[t][k] = (int)(uint8_t)(sw[(8 * hs + k) >> 2] >> (8 * ((8 * hs + k) & 3)));
+                    f1l[t][0] = h2f_g((uint16_t)(hd1.x >> 16));
+                }
             }
         }
         {
@@ -561,6 +579,12 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
             } else {
                 a0 = *(const i64 *)(xa + 8 * (lane >> 5));
                 a1 = *(const i64 *)(xa + 16 + 8 * (lane >> 5));
+            }
+            i32x16 X0, X1; // Q2_K: the sums of x of the group's two halves (the same MFMA with B = 1)
+            if (TYPE == GW_Q2_K) {
+                const i64 ones = 0x0101010101010101l;
+                X0 = __builtin_amdgcn_mfma_i32_32x32x16_i8(a0, ones, z, 0, 0, 0);
+                X1 = __builtin_amdgcn_mfma_i32_32x32x16_i8(a1, ones, z, 0, 0, 0);
             }
             #pragma unroll
             for (int j = 0; j < TJ; j++) {
@@ -593,8 +617,15 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
                         float xsq[4] = { xs4.x, xs4.y, xs4.z, xs4.w };
                         #pragma unroll
                         for (int e = 0; e < 4; e++) {
-                            int I = s0 * I0[4 * q + e] + s1 * I1[4 * q + e];
-                            acc[j][4 * q + e] = acc[j][4 * q + e] + (d * xsq[e]) * (float)I;
+                            if (TYPE == GW_Q2_K) { // (iquants.h:56-57: the mins' term beside the scales')
+                                const int I = (s0 & 15) * I0[4 * q + e] + (s1 & 15) * I1[4 * q + e];
+                                const int Mi = (s0 >> 4) * X0[4 * q + e] + (s1 >> 4) * X1[4 * q + e];
+                                const float dm = f1l[nl][0];
+                                acc[j][4 * q + e] = acc[j][4 * q + e] + ((d * xsq[e]) * (float)I - (dm * xsq[e]) * (float)Mi);
+                            } else {
+                                int I = s0 * I0[4 * q + e] + s1 * I1[4 * q + e];
+                                acc[j][4 * q + e] = acc[j][4 * q + e] + (d * xsq[e]) * (float)I;
+                            }
                         }
                     }
                 }
@@ -850,6 +881,8 @@ __global__ __launch_bounds__(SK_T * SB, SB == 1 ? 2 : 1) void k_gemm_kq32(SkMats
 //     (2 bits from qs, bit 2 from hmask), - 4 sum x and the scales sc - 32
 //   IQ4_XS (its integer form w = D S v, 288 bytes: v as int8, the 16 int8 S, fp32 D): (D * xs) * (float) (S_0 sum v x
 //     + S_1 (...)) over the group's two halves of 16                                                  (iquants.h:49-55)
+//   Q2_K (96 bytes: 16 scale bytes sc | m << 4, qs 64, fp16 d, dmin, padding; q 0 .. 3): (d * xs) * (float) (sc_0 sum q x
+//     + sc_1 (...)) - (dmin * xs) * (float) (m_0 sum x + m_1 (...))                                  (iquants.h:49-57)
 // then one lane per (activation row, weight row) folds the groups in order: val = val + term. mode 1: out = out + val.
 // K % 32 == 0 (Q8_0), % 256 (K-quants); the K-quants' q are 0 .. 63, so v_dot4 with signed codes is exact
 template <int TYPE, int M, int R, int U, bool PF>
@@ -948,6 +981,13 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
                         wv[u][r].w = (int)((((uint32_t)q.w >> sl) & 0x03030303u) | ((((uint32_t)hm.w >> sb) & 0x01010101u) << 2));
                     } else if (TYPE == GW_IQ4_XS) { // (the integer form: the half-group's 16 values v as int8)
                         wv[u][r] = *(const int4 *)(b + 16 * (j & 15));
+                    } else if (TYPE == GW_Q2_K) { // (sub-block k = j % 16: 16 bytes of qs at 32 (k / 8) + 16 (k % 2), 2 bits 2 ((k / 2) % 4))
+                        const int k = j & 15, sl = 2 * ((k >> 1) & 3);
+                        const int4 q = *(const int4 *)(b + 16 + 32 * (k >> 3) + 16 * (k & 1));
+                        wv[u][r].x = (int)(((uint32_t)q.x >> sl) & 0x03030303u);
+                        wv[u][r].y = (int)(((uint32_t)q.y >> sl) & 0x03030303u);
+                        wv[u][r].z = (int)(((uint32_t)q.z >> sl) & 0x03030303u);
+                        wv[u][r].w = (int)(((uint32_t)q.w >> sl) & 0x03030303u);
                     } else {
                         const int n = sb >> 2, p = sb & 3;
                         int4 lo = *(const int4 *)(b + 64 * n + 32 * (p & 1) + 16 * h);
@@ -991,6 +1031,15 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
                     f0[u][r] = h2f_g((uint16_t)(hd.x & 0xffffu)) * (float)scj;
                     f1[u][r] = h2f_g((uint16_t)(hd.x >> 16)) * (float)mj;
                     isc[u][r] = 0;
+                } else if (TYPE == GW_Q2_K) { // (isc: the raw scale byte sc | m << 4; f0 d, f1 dmin)
+                    const int sblk = j >> 4, k = j & 15;
+                    const uint8_t *b = rb + (size_t)sblk * bstride;
+                    const uint4 sw = *(const uint4 *)b;
+                    uint32_t w = k < 4 ? sw.x : k < 8 ? sw.y : k < 12 ? sw.z : sw.w;
+                    isc[u][r] = (int)((w >> (8 * (k & 3))) & 0xffu);
+                    const uint32_t dw = (*(const uint4 *)(b + 80)).x;
+                    f0[u][r] = h2f_g((uint16_t)(dw & 0xffffu));
+                    f1[u][r] = h2f_g((uint16_t)(dw >> 16));
                 } else if (TYPE == GW_Q6_K || TYPE == GW_IQ4_XS) { // (IQ4_XS: the 16 int8 S at 256, D as fp32 at 272)
                     const int sblk = j >> 4, k = j & 15;
                     const uint8_t *b = rb + (size_t)sblk * bstride;
@@ -1061,6 +1110,11 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
                             int I = isc[u][r] * (sd - 4 * xsum);
                             I = I + __shfl_xor(I, 1);
                             term = (f0[u][r] * xsg[u][m]) * (float)I;
+                        } else if (TYPE == GW_Q2_K) { // (I = sc_0 T_0 + sc_1 T_1, M = m_0 X_0 + m_1 X_1, iquants.h:49-57)
+                            int I = (isc[u][r] & 15) * sd, Mi = (isc[u][r] >> 4) * xsum;
+                            I = I + __shfl_xor(I, 1);
+                            Mi = Mi + __shfl_xor(Mi, 1);
+                            term = (f0[u][r] * xsg[u][m]) * (float)I - (f1[u][r] * xsg[u][m]) * (float)Mi;
                         } else if (TYPE == GW_IQ4_XS) { // (I = S_0 T_0 + S_1 T_1, iquants.h:49-55)
                             int I = isc[u][r] * sd;
                             I = I + __shfl_xor(I, 1);
@@ -1094,7 +1148,7 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
     }
 }
 
-// x[b] = row tok[b] of a K-quant table (Q3_K .. Q6_K) or an IQ4_XS one, dequantized (kq_dequant_row, kquants.h:222-251;
+// x[b] = row tok[b] of a K-quant table (Q2_K .. Q6_K) or an IQ4_XS one, dequantized (kq_dequant_row, kquants.h:222-251;
 // iq_dequant_row, iquants.h:217; every value one rounding of an exact expression)
 __global__ __launch_bounds__(256) void k_embed_kq(float *__restrict__ x, int dim, int type, const uint8_t *__restrict__ W,
                                                   int bstride, const int *__restrict__ tok) {
@@ -1122,6 +1176,13 @@ __global__ __launch_bounds__(256) void k_embed_kq(float *__restrict__ x, int dim
             int q = ((b[32 + 32 * n + l] >> (2 * p)) & 3) | ((b[l] >> (k / 32)) & 1) << 2;
             float d = __half2float(__ushort_as_half((uint16_t)(b[108] | b[109] << 8)));
             y = (d * (float)(scj - 32)) * (float)(q - 4);
+        } else if (type == GW_Q2_K) { // (d sc) q - dmin m, sub-blocks of 16 (iquants.h:224-231)
+            const uint8_t *b = rb + (size_t)s * bstride;
+            const int sc = b[k >> 4], q = (b[16 + 32 * (k / 128) + k % 32] >> (2 * (k / 32 % 4))) & 3;
+            const float d = __half2float(__ushort_as_half((uint16_t)(b[80] | b[81] << 8)));
+            const float dmin = __half2float(__ushort_as_half((uint16_t)(b[82] | b[83] << 8)));
+            const float dl = d * (float)(sc & 15), ml = dmin * (float)(sc >> 4);
+            y = dl * (float)q - ml;
         } else if (type == GW_IQ4_XS) { // (D S) v on the integer form (iquants.h:330-340: (d (ls - 32)) kvalues_iq4nl[q])
             const uint8_t *b = rb + (size_t)s * bstride;
             const float D = *(const float *)(b + 272);
@@ -1538,6 +1599,9 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
         } else if (w->type == GW_IQ4_XS) {
             if (g64) KQ_L(GW_IQ4_XS, 64);
             else KQ_L(GW_IQ4_XS, 32);
+        } else if (w->type == GW_Q2_K) {
+            if (g64) KQ_L(GW_Q2_K, 64);
+            else KQ_L(GW_Q2_K, 32);
         } else {
             if (g64) KQ_L(GW_Q3_K, 64);
             else KQ_L(GW_Q3_K, 32);
@@ -1551,6 +1615,7 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
     if (w->type == GW_Q5_K) MRQ_L(GW_Q5_K);
     if (w->type == GW_Q3_K) MRQ_L(GW_Q3_K);
     if (w->type == GW_IQ4_XS) MRQ_L(GW_IQ4_XS);
+    if (w->type == GW_Q2_K) MRQ_L(GW_Q2_K);
 #undef MRQ_L
     return (int)hipErrorInvalidValue;
 }

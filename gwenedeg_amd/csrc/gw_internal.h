@@ -16,7 +16,7 @@
 extern "C" {
 #endif
 
-enum { GW_F32 = 0, GW_Q8_0 = 8, GW_Q3_K = 11, GW_Q4_K = 12, GW_Q5_K = 13, GW_Q6_K = 14, GW_IQ4_XS = 23 }; /* ggml type numbers */
+enum { GW_F32 = 0, GW_Q8_0 = 8, GW_Q2_K = 10, GW_Q3_K = 11, GW_Q4_K = 12, GW_Q5_K = 13, GW_Q6_K = 14, GW_IQ4_XS = 23 }; /* ggml type numbers */
 
 #define GW_ATT_T 16   /* positions per KV cache tile */
 #define GW_ATT_P 256  /* positions per attention block */
@@ -29,24 +29,28 @@ enum { GW_F32 = 0, GW_Q8_0 = 8, GW_Q3_K = 11, GW_Q4_K = 12, GW_Q5_K = 13, GW_Q6_
 #define GW_Q6K_DEV 224      /* ... on the device: the file's 210 bytes padded to a 16-byte multiple (aligned loads) */
 #define GW_Q3K_BYTES 110    /* Q3_K in the file */
 #define GW_Q3K_DEV 112      /* ... on the device, padded as Q6_K */
+#define GW_Q2K_BYTES 84     /* Q2_K in the file */
+#define GW_Q2K_DEV 96       /* ... on the device, padded as Q6_K */
 #define GW_IQ4XS_BYTES 136  /* IQ4_XS in the file */
 #define GW_QI8_DEV 288      /* ... on the device: its integer form w = D S v unpacked (the 256 v as int8, the 16 S of
                              * each 16 values as int8, D as fp32 at byte 272, zero padding) */
-/* the super-block types (256 values; the matmul kernels' K-quant paths): Q3_K .. Q6_K and IQ4_XS */
-#define GW_IS_KQ(t) (((t) >= GW_Q3_K && (t) <= GW_Q6_K) || (t) == GW_IQ4_XS)
+/* the super-block types (256 values; the matmul kernels' K-quant paths): Q2_K .. Q6_K and IQ4_XS */
+#define GW_IS_KQ(t) (((t) >= GW_Q2_K && (t) <= GW_Q6_K) || (t) == GW_IQ4_XS)
 
 /* a K-quant super-block's bytes in the file and on the device (0: not a K-quant) */
 static inline int gw_kq_file_bytes(int type) {
     return type == GW_Q3_K ? GW_Q3K_BYTES : type == GW_Q4_K ? GW_Q4K_BYTES : type == GW_Q5_K ? GW_Q5K_BYTES
-         : type == GW_Q6_K ? GW_Q6K_BYTES : type == GW_IQ4_XS ? GW_IQ4XS_BYTES : 0;
+         : type == GW_Q6_K ? GW_Q6K_BYTES : type == GW_IQ4_XS ? GW_IQ4XS_BYTES : type == GW_Q2_K ? GW_Q2K_BYTES : 0;
 }
 static inline int gw_kq_dev_bytes(int type) {
-    return type == GW_Q3_K ? GW_Q3K_DEV : type == GW_Q6_K ? GW_Q6K_DEV : type == GW_IQ4_XS ? GW_QI8_DEV : gw_kq_file_bytes(type);
+    return type == GW_Q3_K ? GW_Q3K_DEV : type == GW_Q6_K ? GW_Q6K_DEV : type == GW_IQ4_XS ? GW_QI8_DEV
+         : type == GW_Q2_K ? GW_Q2K_DEV : gw_kq_file_bytes(type);
 }
 
 /* A weight matrix on the device (rows x cols). Q8_0: int8 codes, row-major, and fp16 scales (cols / 32 per row),
  * the file's bytes split (34 bytes per 32 weights, as the file). K-quants: the file's super-blocks, row-major, each
- * bstride bytes apart (Q4_K 144, Q5_K 176; Q6_K 224: the file's 210 bytes and 14 of padding; Q3_K 112: 110 and 2);
+ * bstride bytes apart (Q4_K 144, Q5_K 176; Q6_K 224: the file's 210 bytes and 14 of padding; Q3_K 112: 110 and 2;
+ * Q2_K 96: 84 and 12);
  * IQ4_XS: GW_QI8_DEV-byte super-blocks of its integer form */
 typedef struct {
     int type, rows, cols;

@@ -14,6 +14,8 @@
  *   Q6_K: 16 sub-blocks of 16, int8 sub-scales against d, q in 0..63 (value q - 32)
  *   Q5_K: as Q4_K with q in 0..31 (bit 4 in qh)
  *   Q3_K: 16 sub-blocks of 16, 6-bit scales sc (value (d (sc - 32)) q) with sc - 32 in 0..31 here, q in -4..3
+ *   Q2_K (iquants.h:10-11): 16 sub-blocks of 16, 4-bit scale sc and min m per sub-block (value (d sc) q - dmin m),
+ *     q in 0..3
  *   IQ4_XS (iquants.h:28-30): 8 groups of 32, 6-bit ls (value (d (ls - 32)) kvalues_iq4nl[q]) with ls - 32 in 0..31
  *     for even groups and -31..0 for odd ones (both signs of the scale), q the nearest of the 16 code values
  * Any valid block decodes the same way on both sides, so these simple encoders suffice for parity. */
@@ -26,8 +28,8 @@
 
 #include "gw_synth.h"
 
-enum { T_F32 = 0, T_Q8_0 = 8, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ4_XS = 23 };
-#define IS_SB(t) (((t) >= T_Q3_K && (t) <= T_Q6_K) || (t) == T_IQ4_XS) /* (super-blocks of 256) */
+enum { T_F32 = 0, T_Q8_0 = 8, T_Q2_K = 10, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ4_XS = 23 };
+#define IS_SB(t) (((t) >= T_Q2_K && (t) <= T_Q6_K) || (t) == T_IQ4_XS) /* (super-blocks of 256) */
 
 /* IQ4_XS's code values (ggml's kvalues_iq4nl) */
 static const int8_t kv_iq4nl[16] = { -127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113 };
@@ -87,6 +89,7 @@ size_t gw_synth_row_bytes(int type, int k) {
     if (type == T_Q3_K) return (size_t)k / 256 * 110;
     if (type == T_Q6_K) return (size_t)k / 256 * 210;
     if (type == T_IQ4_XS) return (size_t)k / 256 * 136;
+    if (type == T_Q2_K) return (size_t)k / 256 * 84;
     return (size_t)k * 4;
 }
 
@@ -234,6 +237,44 @@ static void enc_q6_k(uint8_t *o, const float *x, int k) {
     }
 }
 
+static void enc_q2_k(uint8_t *o, const float *x, int k) {
+    /* 84 bytes: scales[16] (sc | m << 4), qs[64] (value i: 2 bits 2 (i / 32 % 4) of qs[32 (i / 128) + i % 32]), fp16 d,
+     * fp16 dmin */
+    for (int sb = 0; sb < k / 256; sb++, o += 84, x += 256) {
+        float sc[16], mn[16], smax = 0, mmax = 0;
+        for (int j = 0; j < 16; j++) {
+            float lo = x[16 * j], hi = x[16 * j];
+            for (int i = 1; i < 16; i++) {
+                lo = x[16 * j + i] < lo ? x[16 * j + i] : lo;
+                hi = x[16 * j + i] > hi ? x[16 * j + i] : hi;
+            }
+            if (lo > 0) lo = 0; /* w = s * q - m with m >= 0 */
+            sc[j] = (hi - lo) / 3.0f;
+            mn[j] = -lo;
+            smax = sc[j] > smax ? sc[j] : smax;
+            mmax = mn[j] > mmax ? mn[j] : mmax;
+        }
+        uint16_t hd = f32_to_f16_rne(smax / 15.0f), hm = f32_to_f16_rne(mmax / 15.0f);
+        float d = f16_to_f32(hd), dmin = f16_to_f32(hm);
+        memset(o, 0, 84);
+        for (int j = 0; j < 16; j++) {
+            int a = d > 0 ? (int)lroundf(sc[j] / d) : 0, b = dmin > 0 ? (int)lroundf(mn[j] / dmin) : 0;
+            a = a > 15 ? 15 : a;
+            b = b > 15 ? 15 : b;
+            o[j] = (uint8_t)(a | b << 4);
+            const float dl = d * (float)a, ml = dmin * (float)b;
+            for (int i = 0; i < 16; i++) {
+                const int e = 16 * j + i;
+                int q = dl > 0 ? (int)lroundf((x[e] + ml) / dl) : 0;
+                q = q < 0 ? 0 : q > 3 ? 3 : q;
+                o[16 + 32 * (e / 128) + e % 32] |= (uint8_t)(q << (2 * (e / 32 % 4)));
+            }
+        }
+        memcpy(o + 80, &hd, 2);
+        memcpy(o + 82, &hm, 2);
+    }
+}
+
 static void enc_iq4_xs(uint8_t *o, const float *x, int k) {
     /* 136 bytes: fp16 d, u16 scales_h (bits 2 ib, 2 ib + 1: ls >> 4), scales_l[4] (nibble ib % 2 of byte ib / 2: ls & 15),
      * qs[128] (qs[16 ib + j]: low nibble the code of value j of group ib, high nibble of value 16 + j) */
@@ -276,6 +317,7 @@ void gw_synth_encode_row(int type, uint8_t *o, const float *x, int k) {
     else if (type == T_Q3_K) enc_q3_k(o, x, k);
     else if (type == T_Q6_K) enc_q6_k(o, x, k);
     else if (type == T_IQ4_XS) enc_iq4_xs(o, x, k);
+    else if (type == T_Q2_K) enc_q2_k(o, x, k);
     else memcpy(o, x, (size_t)k * 4);
 }
 

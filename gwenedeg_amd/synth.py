@@ -13,7 +13,7 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _PATH = os.path.join(_HERE, "lib", "libgwsynth.so")
 
-Q8_0, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_XS = 8, 11, 12, 13, 14, 23
+Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_XS = 8, 10, 11, 12, 13, 14, 23
 
 
 class GwSynthCfg(ctypes.Structure):
@@ -48,6 +48,9 @@ SHAPES = {
     # IQ4_XS-style (the i-quant IQ4_XS on every matrix and the embedding, Q6_K output)
     "tiny_iq4xs": dict(dim=512, hidden=1024, n_layers=2, n_heads=8, n_kv_heads=2, head_dim=128, vocab=2048,
                        ctx_len=4096, tied=0, type_default=IQ4_XS, type_out=Q6_K),
+    # Q2_K-style (Q2_K on most matrices and the embedding, Q4_K on v, Q6_K output)
+    "tiny_q2k": dict(dim=512, hidden=1024, n_layers=2, n_heads=8, n_kv_heads=2, head_dim=128, vocab=2048,
+                     ctx_len=4096, tied=0, type_default=Q2_K, type_v=Q4_K, type_out=Q6_K),
     # head sizes below 128: 8 query heads on one KV head (hd 64), plain multi-head attention (hd 32)
     "tiny_hd64": dict(dim=256, hidden=512, n_layers=2, n_heads=8, n_kv_heads=1, head_dim=64, vocab=1000, ctx_len=4096,
                       tied=1, type_default=Q8_0),

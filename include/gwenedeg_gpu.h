@@ -5,7 +5,7 @@
  * link against this library instead of the reference's forward.c / model.c weight path. Each declaration cites the
  * runq.h line it replaces. Types are laid out exactly as runq.h's (same fields, order and widths).
  *
- * Scope of the device implementation: Qwen3 dense models (GGUF, Q8_0 / Q3_K / Q4_K / Q5_K / Q6_K / IQ4_XS matrices), the f16 KV cache
+ * Scope of the device implementation: Qwen3 dense models (GGUF, Q8_0 / Q2_K .. Q6_K / IQ4_XS matrices), the f16 KV cache
  * or bf16 one (RQ_KV_F16, RQ_KV_BF16; other KV types give RQ_ERR_ARG), one GPU, one HIP stream per context. Calls are synchronous at return
  * (logits valid on the host), as the reference's are. Results are bit-identical for any batch composition: a row's
  * logits do not depend on the rows it is batched with (the device kernels compute each output whole, in a fixed order).
@@ -58,7 +58,7 @@ typedef struct {
     int repack;
 } RqModelOpts;
 
-/* runq.h:87-88: a GGUF file (qwen3; Q8_0, Q3_K .. Q6_K, IQ4_XS matrices), its weights repacked into device memory */
+/* runq.h:87-88: a GGUF file (qwen3; Q8_0, Q2_K .. Q6_K, IQ4_XS matrices), its weights repacked into device memory */
 RqModel *rq_model_load(const char *path, const RqModelOpts *opts, char *err, size_t errlen);
 void rq_model_free(RqModel *m);
 
@@ -300,7 +300,7 @@ int gw_q8_matmul(float *out, const int8_t *codes, const uint16_t *scales, int N,
 int gw_q8_block_sums(int32_t *isum, const int8_t *codes, int N, int K, const int8_t *xq, int M, void *stream);
 
 /* The K-quant operator on the file's blocks (kquants.h:79-109's definition; type 11 Q3_K, 12 Q4_K, 13 Q5_K, 14 Q6_K;
- * and iquants.h:49-55's for type 23 IQ4_XS): out[m * N + n], blocks: N rows of K / 256 blocks, device memory */
+ * and iquants.h:49-57's for type 10 Q2_K and 23 IQ4_XS): out[m * N + n], blocks: N rows of K / 256 blocks, device memory */
 int gw_kq_matmul(float *out, int type, const void *blocks, int N, int K, const int8_t *xq, const float *xs, int M,
                  void *stream);
 

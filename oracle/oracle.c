@@ -17,7 +17,7 @@
  *     q8p_gemm_item) at M = 1, 3, 8, 13, and against the golden vectors of tests/golden/ref_kernels.npz;
  *   K-quant fold: bit for bit against the reference's kq_dot (ref_q8op kq); the dequantization against an
  *     independent numpy decoder of the Q3_K / Q4_K / Q5_K / Q6_K block formats;
- *   IQ4_XS fold: bit for bit against the reference's iq_rows (ref_q8op iq: its AVX-512 i-quant kernels at 1 row and in
+ *   Q2_K and IQ4_XS folds: bit for bit against the reference's iq_rows (ref_q8op iq: its AVX-512 i-quant kernels at 1 row and in
  *     blocks of 8); the dequantization against an independent numpy decoder of the block format;
  *   exp_att: within 2 ulp of expf, the -86 clamp; attention: one block against a float64 softmax, several blocks
  *     against the one-block result (the combine's invariant);
@@ -154,8 +154,8 @@ void or_q8_from_blocks(int8_t *q, float *s, const uint8_t *blk, size_t nblk) {
 
 /* ---------------------------------------------------------------------------------------- K-quants */
 
-enum { T_F32 = 0, T_Q8_0 = 8, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ4_XS = 23 };
-#define IS_KQ(t) (((t) >= T_Q3_K && (t) <= T_Q6_K) || (t) == T_IQ4_XS)
+enum { T_F32 = 0, T_Q8_0 = 8, T_Q2_K = 10, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ4_XS = 23 };
+#define IS_KQ(t) (((t) >= T_Q2_K && (t) <= T_Q6_K) || (t) == T_IQ4_XS)
 
 /* IQ4_XS's 16 code values (ggml's kvalues_iq4nl, iq_grids.h:1082; iquants.h:28-30) */
 static const int8_t kv_iq4nl[16] = { -127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113 };
@@ -196,7 +196,11 @@ static int q3k_scale(const uint8_t *b, int j) { /* kquants.h:207-212: the 6-bit 
 }
 
 static int kq_bytes(int type) {
-    return type == T_Q4_K ? 144 : type == T_Q5_K ? 176 : type == T_Q3_K ? 110 : type == T_IQ4_XS ? 136 : 210;
+    return type == T_Q4_K ? 144 : type == T_Q5_K ? 176 : type == T_Q3_K ? 110 : type == T_IQ4_XS ? 136 : type == T_Q2_K ? 84 : 210;
+}
+
+static int q2k_q(const uint8_t *b, int i) { /* iquants.h:10-11: 2 bits 2 (i / 32 % 4) of qs[32 (i / 128) + i % 32] */
+    return (b[16 + 32 * (i / 128) + i % 32] >> (2 * (i / 32 % 4))) & 3;
 }
 
 static int iq4xs_ls(const uint8_t *b, int ib) { /* iquants.h:28-29: the 6-bit scale of group ib (before the - 32) */
@@ -226,6 +230,12 @@ void or_kq_dequant_row(int type, const uint8_t *blk, int n, float *y) {
             for (int j = 0; j < 16; j++) {
                 float dl = d * (float)(q3k_scale(b, j) - 32);
                 for (int l = 0; l < 16; l++) y[16 * j + l] = dl * (float)(q3k_q(b, 16 * j + l) - 4);
+            }
+        } else if (type == T_Q2_K) { /* iquants.h:224-231 (ggml's dequantize_row_q2_K): (d sc) q - dmin m per 16 */
+            float d = or_fp16_to_f32(u16(b + 80)), dmin = or_fp16_to_f32(u16(b + 82));
+            for (int i = 0; i < 256; i++) {
+                float dl = d * (float)(b[i / 16] & 15), ml = dmin * (float)(b[i / 16] >> 4);
+                y[i] = dl * (float)q2k_q(b, i) - ml;
             }
         } else if (type == T_IQ4_XS) { /* iquants.h:330-340 (ggml's dequantize_row_iq4_xs): (d (ls - 32)) v */
             float d = or_fp16_to_f32(u16(b));
@@ -279,6 +289,20 @@ static float kq_dot_row(int type, const uint8_t *row, const int8_t *x, const flo
                 }
                 float d = or_fp16_to_f32(u16(b + 108));
                 val = val + (d * xs[g]) * (float)I;
+            } else if (type == T_Q2_K) { /* iquants.h:49-57: I = sc_0 T_0 + sc_1 T_1, M = m_0 X_0 + m_1 X_1 */
+                int32_t I = 0, Mi = 0;
+                for (int h = 0; h < 2; h++) {
+                    int jj = 2 * j + h;
+                    int32_t t = 0, xsum = 0;
+                    for (int i = 0; i < 16; i++) {
+                        t += q2k_q(b, 16 * jj + i) * xg[16 * h + i];
+                        xsum += xg[16 * h + i];
+                    }
+                    I += (b[jj] & 15) * t;
+                    Mi += (b[jj] >> 4) * xsum;
+                }
+                float d = or_fp16_to_f32(u16(b + 80)), dmin = or_fp16_to_f32(u16(b + 82));
+                val = val + ((d * xs[g]) * (float)I - (dmin * xs[g]) * (float)Mi);
             } else if (type == T_IQ4_XS) { /* iquants.h:49-55: I = S_0 T_0 + S_1 T_1, S = ls - 32 on both halves, D = d */
                 int32_t I = 0, S = iq4xs_ls(b, j) - 32;
                 for (int h = 0; h < 2; h++) {

@@ -22,7 +22,7 @@ void or_q8_block_sums(int32_t *isum, const int8_t *wq, const int8_t *xq, int M, 
 /* Q8_0 file blocks (34 bytes: fp16 d, 32 int8) -> codes + fp32 scales (model.c:47-59) */
 void or_q8_from_blocks(int8_t *q, float *s, const uint8_t *blk, size_t nblk);
 
-/* K-quants and IQ4_XS on GGUF blocks: the definition of kquants.h:79-109 (types 11-14) and iquants.h:49-55 (type 23) */
+/* K-quants and IQ4_XS on GGUF blocks: the definition of kquants.h:79-109 (types 11-14) and iquants.h:49-57 (types 10, 23) */
 void or_kq_dequant_row(int type, const uint8_t *blk, int n, float *y); /* kquants.h:222-251 */
 void or_kq_matmul(int type, float *out, const uint8_t *blocks, const int8_t *xq, const float *xs, int M, int N, int K);
 void or_kq_act_prep(float *xf, const int8_t *xq, const float *xs, int n); /* kquants.h:392-400 */

@@ -18,7 +18,7 @@ REF_DIR = os.path.join(HERE, "_ref")
 REF_DRIVER = os.path.join(REF_DIR, "ref_driver")
 REF_Q8OP = os.path.join(REF_DIR, "ref_q8op")
 REF_SAMPLE = os.path.join(REF_DIR, "ref_sample")
-IQ4_XS = 23  # (ggml type number)
+Q2_K, IQ4_XS = 10, 23  # (ggml type numbers: the types run by iquants.h's kernels)
 
 _lib = None
 
@@ -265,7 +265,7 @@ def run_ref_kq(workdir: str, typ: int, blocks, xq, xs, N: int, K: int, timeout: 
     paths = [os.path.join(workdir, n) for n in ("blk.bin", "x.bin", "xs.bin", "out.bin")]
     for a, p in zip((blocks, xq, xs), paths):
         np.ascontiguousarray(a).tofile(p)
-    mode = "iq" if typ == IQ4_XS else "kq"  # (the i-quants: iquants.h's packing and kernels)
+    mode = "iq" if typ in (Q2_K, IQ4_XS) else "kq"  # (Q2_K and the i-quants: iquants.h's packing and kernels)
     cmd = [REF_Q8OP, mode, str(typ), *paths[:3], str(M), str(N), str(K), paths[3]]
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)
     if r.returncode != 0:

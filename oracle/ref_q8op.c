@@ -13,7 +13,7 @@
  *       BLK: N rows of K / 256 GGUF K-quant blocks (TYPE 11 Q3_K, 12 Q4_K, 13 Q5_K, 14 Q6_K), packed by kq_pack_blocks
  *       (kquants.h:253) and multiplied by the generic kq_dot (:608) with kq_act_prep's xf (:392).
  *   ref_q8op iq TYPE BLK X XS M N K OUT
- *       BLK: N rows of K / 256 GGUF i-quant blocks (TYPE 23 IQ4_XS), packed by iq_pack_blocks (iquants.h:503) and
+ *       BLK: N rows of K / 256 GGUF blocks (TYPE 10 Q2_K, 23 IQ4_XS), packed by iq_pack_blocks (iquants.h:503) and
  *       multiplied by iq_rows (:1478), the forward's dispatch (the AVX-512 kernels of this build), with the activation
  *       sums of 16 of kq512_c16 (kernels_avx512.h:342).
  * All files raw little-endian arrays. */
@@ -153,7 +153,7 @@ int main(int argc, char **argv) {
     }
     if (argc >= 10 && !strcmp(argv[1], "iq")) {
         int type = atoi(argv[2]), M = atoi(argv[6]), N = atoi(argv[7]), K = atoi(argv[8]);
-        if (type != GGML_IQ4_XS || M < 1 || N % 16 || K % 256) { fprintf(stderr, "ref_q8op: bad iq args\n"); return 2; }
+        if ((type != GGML_IQ4_XS && type != GGML_Q2_K) || M < 1 || N % 16 || K % 256) { fprintf(stderr, "ref_q8op: bad iq args\n"); return 2; }
         uint8_t *blk = slurp(argv[3], (size_t)N * (K / 256) * iq_block_bytes(type));
         int8_t *X = slurp(argv[4], (size_t)M * K);
         float *XS = slurp(argv[5], (size_t)M * (K / 32) * 4);

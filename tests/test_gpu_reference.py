@@ -270,10 +270,10 @@ def test_seqfile_with_reference(gw, orc, tmp_path, kvt):
     assert lib.rq_seq_load(ctypes.c_void_p(m.seq(1024, kv_type=other)._h), p2.encode(), 10) == -7
 
 
-@pytest.mark.parametrize("shape", ["tiny_q5k", "tiny_q3k", "tiny_iq4xs"])
+@pytest.mark.parametrize("shape", ["tiny_q5k", "tiny_q3k", "tiny_iq4xs", "tiny_q2k"])
 def test_q5k_q3k_models_greedy_bit_identical(gw, orc, tmp_path, shape):
-    """Q5_K_M-, Q3_K_M- and IQ4_XS-style models (Q5_K / Q3_K / IQ4_XS matrices beside Q5_K / Q6_K ones, the K-quant or
-    IQ4_XS embedding): a 64-token prefill and 24 greedy steps, every logits row equal bit for bit to the reference's,
+    """Q5_K_M-, Q3_K_M-, IQ4_XS- and Q2_K-style models (Q5_K / Q3_K / IQ4_XS / Q2_K matrices beside Q4_K / Q5_K / Q6_K
+    ones, the K-quant or IQ4_XS embedding): a 64-token prefill and 24 greedy steps, every logits row equal bit for bit to the reference's,
     the same tokens"""
     path, d = _synth(str(tmp_path), shape, seed=7)
     m = gw.Model(path, ctx_len=512)

@@ -6,7 +6,7 @@
 * where the reference exposes no entry point, against what the mathematics fixes: brute-force integer block sums,
   every fp16 value, IEEE float16 rounding and the reference's saturation, the quantizer's closed form and its
   rounding of exact halves away from zero, float64 exp / attention / RoPE, an independent numpy decoder of the ggml Q3_K /
-  Q4_K / Q5_K / Q6_K / IQ4_XS block formats (the published layout);
+  Q4_K / Q5_K / Q6_K / Q2_K / IQ4_XS block formats (the published layout);
 * the product's host-measured tables (gwenedeg_amd/csrc/gw_exact.c: the reference's rsqrtss / vrcp14ps / libmvec expf
   as the device reproduces them) against the reference's own operations on this host.
 The reference's fixtures for this path (tests/golden/logits, dequant) need model files absent here; the golden vectors
@@ -261,14 +261,30 @@ def _np_dequant_iq4xs(b):
     return y
 
 
+def _np_dequant_q2k(b):
+    """ggml's dequantize_row_q2_K on one 84-byte block (scales[16], qs[64], fp16 d, fp16 dmin): per 128 values n and
+    shift 2 j, the 32 values l take bits 2 j of qs[32 n + l]; sub-block of 16 (scale byte: sc low nibble, m high)"""
+    sc, qs = b[0:16].astype(np.int32), b[16:80].astype(np.int32)
+    d, dmin = b[80:82].view(np.float16)[0].astype(np.float32), b[82:84].view(np.float16)[0].astype(np.float32)
+    y = np.zeros(256, np.float32)
+    for n in range(2):
+        for j in range(4):
+            for l in range(32):
+                i = 128 * n + 32 * j + l
+                s_ = sc[i // 16]
+                dl, ml = np.float32(d * np.float32(s_ & 15)), np.float32(dmin * np.float32(s_ >> 4))
+                y[i] = dl * np.float32((qs[32 * n + l] >> (2 * j)) & 3) - ml
+    return y
+
+
 _KQ_DEC = {11: (_np_dequant_q3k, 110), 12: (_np_dequant_q4k, 144), 13: (_np_dequant_q5k, 176), 14: (_np_dequant_q6k, 210),
-           23: (_np_dequant_iq4xs, 136)}
+           23: (_np_dequant_iq4xs, 136), 10: (_np_dequant_q2k, 84)}
 
 
-@pytest.mark.parametrize("typ", [11, 12, 13, 14, 23])
+@pytest.mark.parametrize("typ", [10, 11, 12, 13, 14, 23])
 def test_kq_dequant_vs_independent_decoder(typ):
-    """or_kq_dequant_row (kquants.h:222-251; IQ4_XS iquants.h:330-340) against a numpy decoder written from ggml's block
-    layout: bit for bit"""
+    """or_kq_dequant_row (kquants.h:222-251; Q2_K / IQ4_XS iquants.h:224-231, :330-340) against a numpy decoder written
+    from ggml's block layout: bit for bit"""
     blk = _kq_blocks(typ, 4, 512, 20 + typ)
     dec, bs = _KQ_DEC[typ]
     for n in range(4):
@@ -278,11 +294,12 @@ def test_kq_dequant_vs_independent_decoder(typ):
 
 
 @need_ref
-@pytest.mark.parametrize("typ", [11, 12, 13, 14, 23])
+@pytest.mark.parametrize("typ", [10, 11, 12, 13, 14, 23])
 @pytest.mark.parametrize("M", [1, 5, 11])
 def test_kq_matmul_vs_reference(tmp_path, typ, M):
-    """or_kq_matmul (kquants.h:86-109's fold; IQ4_XS iquants.h:49-55's) against the reference's kernels compiled from
-    its sources (K-quants: the generic kq_dot; IQ4_XS: iq_rows, the forward's AVX-512 dispatch, 1 row and blocks of 8):
+    """or_kq_matmul (kquants.h:86-109's fold; Q2_K / IQ4_XS iquants.h:49-57's) against the reference's kernels compiled
+    from its sources (K-quants: the generic kq_dot; Q2_K / IQ4_XS: iq_rows, the forward's AVX-512 dispatch, 1 row and
+    blocks of 8):
     bit for bit; and close to the float64 product of the dequantized rows"""
     N, K = 32, 1024
     blk = _kq_blocks(typ, N, K, 30 + typ + M)
@@ -421,6 +438,7 @@ def test_attention_combine_matches_single_pass():
     ("tiny", {}, 40, False),
     ("tiny_kq", {}, 20, False),
     ("tiny_iq4xs", {}, 20, False),
+    ("tiny_q2k", {}, 20, False),
     ("qwen3_0_6b", dict(n_layers=3, vocab=4096, tied=0), 12, False),
     ("tiny", {}, 40, True),
     ("qwen3_0_6b", dict(n_layers=2, vocab=4096, tied=0), 270, True),
