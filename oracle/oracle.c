@@ -391,19 +391,129 @@ uint16_t or_f32_bf16(float f) {
     return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? (u >> 16) | 0x40 : r);
 }
 
-static void attention_block(int bf, float *o, float *ml, const float *q, const uint16_t *kc, const uint16_t *vc, int n, int b,
-                            int h, int n_kv, int hd, float scale) {
-    /* attention_vec (forward.c:1346-1403) on block b of kv head h: positions t0 .. t0 + nb - 1; an f16 (bf 0) or bf16
-     * cache, the values converted exactly (kv_block_f32, forward.c:1433-1451) */
+/* ---- the 8-bit / 4-bit KV caches (RQ_KV_Q8, RQ_KV_Q4, RQ_KV_Q4K4; forward.c:1609-1790). A position's key and value
+ * rows are rotated, x' = H D x (D: signs kvq_neg, H: the unnormalized Walsh-Hadamard butterflies in the order h = 1, 2,
+ * .., each output one fp32 add or subtract), then quantized per group of 32 dims from the group's values alone:
+ *   q8: d = bf16 of max |x'| / 127 with its magnitude rounded up; n = rint(x' / d) in -127..127
+ *   q4: m = the x' of largest |x'| (the first), d = bf16 of m / -8, magnitude rounded up; n = rint(x' / d) in -8..7
+ *   (d zero or a bf16 denormal: the group is zero). Read back n d, exact.
+ * The attention runs on q' = H D q / hd and the values read back (the fp32 attention), and its output o' comes back as
+ * o = D H o' / hd. Tile layouts (16 positions j, hd dims i; the bf16 scales after the codes):
+ *   K q8 [i][j] int8, scales at 16 hd: [c][j];  K q4: byte [p][j] = (n_2p + 8) | (n_2p+1 + 8) << 4, scales at 8 hd: [c][j]
+ *   V q8 [j][i] int8, scales at 16 hd: [j][c];  V q4: byte [j][c][l] = (n_32c+l + 8) | (n_32c+16+l + 8) << 4, scales at
+ *   8 hd: [j][c] */
+enum { KVQ_Q8 = 3, KVQ_Q4 = 8, KVQ_Q4K4 = 9 };
+static int kvq_fmt(int kvt, int is_v) { return kvt == KVQ_Q4K4 ? KVQ_Q4 : kvt == KVQ_Q4 && !is_v ? KVQ_Q8 : kvt; }
+static size_t kvq_tile_bytes(int fmt, int hd) { return (size_t)hd * (fmt == KVQ_Q4 ? 9 : 17); }
+static int kvq_neg(int i) { return (int)(((uint32_t)i * 0x9E3779B9u) >> 31); } /* forward.c:1632 */
+
+static void kvq_rot(float *x, int n, int inv) {
+    /* forward.c:1634-1652: x <- H D x, or (inv) D H x */
+    if (!inv)
+        for (int i = 0; i < n; i++) x[i] = kvq_neg(i) ? -x[i] : x[i];
+    for (int h = 1; h < n; h *= 2)
+        for (int i0 = 0; i0 < n; i0 += 2 * h)
+            for (int i = i0; i < i0 + h; i++) {
+                const float a = x[i], b = x[i + h];
+                x[i] = a + b;
+                x[i + h] = a - b;
+            }
+    if (inv)
+        for (int i = 0; i < n; i++) x[i] = kvq_neg(i) ? -x[i] : x[i];
+}
+
+static void kvq_scale_by(float *x, int n) { /* forward.c:1654-1658: times 2^-log2(n), exact */
+    const float f = 1.0f / (float)n;
+    for (int i = 0; i < n; i++) x[i] = x[i] * f;
+}
+
+static uint16_t kvq_scale(float d) {
+    /* forward.c:1682-1689: bf16 of d with its magnitude rounded up, the sign kept; 0 for a zero or denormal result */
+    uint32_t u;
+    memcpy(&u, &d, 4);
+    const uint32_t r = (u >> 16) + ((u & 0xffffu) != 0);
+    return (r & 0x7f80u) ? (uint16_t)r : 0;
+}
+
+static float bf16_f32(uint16_t h) {
+    uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+static void kvq_store(int fmt, uint8_t *tile, int j, int hd, const float *x0, int is_v) {
+    /* forward.c:1691-1738: row x0 of position j into a q8 / q4 tile (kvq_group per 32 dims, then the layout) */
+    float x[256];
+    memcpy(x, x0, (size_t)hd * sizeof(float));
+    kvq_rot(x, hd, 0);
+    const int q4 = fmt == KVQ_Q4, ng = hd / 32;
+    uint8_t *sc = tile + (size_t)(q4 ? 8 : 16) * hd;
+    for (int c = 0; c < ng; c++) {
+        const float *g = x + 32 * c;
+        float a = 0.0f, m = 0.0f;
+        for (int i = 0; i < 32; i++)
+            if (fabsf(g[i]) > a) {
+                a = fabsf(g[i]);
+                m = g[i];
+            }
+        const uint16_t s = kvq_scale(q4 ? m / -8.0f : a / 127.0f);
+        const float d = bf16_f32(s);
+        int8_t n[32];
+        const int lo = q4 ? -8 : -127, hi = q4 ? 7 : 127;
+        for (int i = 0; i < 32; i++) {
+            const float t = s ? rintf(g[i] / d) : 0.0f;
+            n[i] = (int8_t)(t < (float)lo ? lo : t > (float)hi ? hi : (int)t);
+        }
+        const size_t so = 2 * (is_v ? (size_t)j * ng + c : (size_t)c * ATT_T + j);
+        memcpy(sc + so, &s, 2);
+        for (int l = 0; l < 32; l++) {
+            if (!is_v && !q4) tile[(size_t)(32 * c + l) * ATT_T + j] = (uint8_t)n[l];
+            if (is_v && !q4) tile[(size_t)j * hd + 32 * c + l] = (uint8_t)n[l];
+        }
+        for (int l = 0; l < 16; l++) {
+            if (!is_v && q4) tile[(size_t)(16 * c + l) * ATT_T + j] = (uint8_t)((n[2 * l] + 8) | (n[2 * l + 1] + 8) << 4);
+            if (is_v && q4) tile[(size_t)j * (hd / 2) + 16 * c + l] = (uint8_t)((n[l] + 8) | (n[l + 16] + 8) << 4);
+        }
+    }
+}
+
+static float kvq_val(int fmt, const uint8_t *tile, int i, int j, int hd, int is_v) {
+    /* forward.c:1740-1768: dim i of position j read back, n d (exact) */
+    const int q4 = fmt == KVQ_Q4, ng = hd / 32, c = i / 32;
+    const uint8_t *sc = tile + (size_t)(q4 ? 8 : 16) * hd;
+    uint16_t s;
+    memcpy(&s, sc + 2 * (is_v ? (size_t)j * ng + c : (size_t)c * ATT_T + j), 2);
+    int n;
+    if (!is_v) n = q4 ? ((tile[(size_t)(i / 2) * ATT_T + j] >> (4 * (i & 1))) & 15) - 8 : (int8_t)tile[(size_t)i * ATT_T + j];
+    else n = q4 ? ((tile[(size_t)j * (hd / 2) + c * 16 + i % 16] >> (4 * ((i / 16) & 1))) & 15) - 8 : (int8_t)tile[(size_t)j * hd + i];
+    return (float)n * bf16_f32(s);
+}
+
+/* the cache value of dim i, position t of kv head h (K: is_v 0); kvt 0 / 1: the 16-bit caches (f16 / bf16; c16 the
+ * layer's base), else a quantized type (cq the layer's base, tiles of kvq_tile_bytes) */
+static float kv_get(int kvt, const uint16_t *c16, const uint8_t *cq, int t, int h, int n_kv, int hd, int i, int is_v) {
+    const int j = t % ATT_T;
+    if (kvt == 0 || kvt == 1) {
+        const uint16_t *tl = c16 + or_kv_tile(t, h, n_kv, hd);
+        return kv_f32(kvt, tl[is_v ? kv_v_at(kvt, i, j, hd) : kv_k_at(kvt, i, j)]);
+    }
+    const int fmt = kvq_fmt(kvt, is_v);
+    const size_t nt = or_kv_tile(t, h, n_kv, hd) / ((size_t)ATT_T * hd);
+    return kvq_val(fmt, cq + nt * kvq_tile_bytes(fmt, hd), i, j, hd, is_v);
+}
+
+static void attention_block_t(int kvt, float *o, float *ml, const float *q, const uint16_t *kc, const uint16_t *vc,
+                              const uint8_t *kq, const uint8_t *vq, int n, int b, int h, int n_kv, int hd, float scale) {
+    /* attention_vec (forward.c:1346-1403) on block b of kv head h: positions t0 .. t0 + nb - 1; the cache's values read
+     * exactly (kv_block_f32, forward.c:1433-1451; the quantized caches: kvq_block_f32, n d), the fp32 attention */
     int t0 = b * ATT_P, nb = n - t0 < ATT_P ? n - t0 : ATT_P;
     float S[ATT_P] = { 0 };
     for (int t = 0; t < nb; t++) {
-        const uint16_t *k = kc + or_kv_tile(t0 + t, h, n_kv, hd);
-        int j = t % ATT_T;
         float a = 0;
         for (int i0 = 0; i0 < hd; i0 += ATT_DC) {
             float c = 0;
-            for (int i = i0; i < i0 + ATT_DC; i++) c = fmaf(q[i], kv_f32(bf, k[kv_k_at(bf, i, j)]), c);
+            for (int i = i0; i < i0 + ATT_DC; i++) c = fmaf(q[i], kv_get(kvt, kc, kq, t0 + t, h, n_kv, hd, i, 0), c);
             a = i0 > 0 ? a + c : c;
         }
         S[t] = a * scale;
@@ -423,10 +533,13 @@ static void attention_block(int bf, float *o, float *ml, const float *q, const u
     ml[0] = m;
     ml[1] = sum[0];
     for (int i = 0; i < hd; i++) o[i] = 0.0f;
-    for (int t = 0; t < nb; t++) {
-        const uint16_t *v = vc + or_kv_tile(t0 + t, h, n_kv, hd);
-        for (int i = 0; i < hd; i++) o[i] = fmaf(S[t], kv_f32(bf, v[kv_v_at(bf, i, t % ATT_T, hd)]), o[i]);
-    }
+    for (int t = 0; t < nb; t++)
+        for (int i = 0; i < hd; i++) o[i] = fmaf(S[t], kv_get(kvt, vc, vq, t0 + t, h, n_kv, hd, i, 1), o[i]);
+}
+
+static void attention_block(int bf, float *o, float *ml, const float *q, const uint16_t *kc, const uint16_t *vc, int n, int b,
+                            int h, int n_kv, int hd, float scale) {
+    attention_block_t(bf, o, ml, q, kc, vc, NULL, NULL, n, b, h, n_kv, hd, scale);
 }
 
 void or_attention_block(float *o, float *ml, const float *q, const uint16_t *kc, const uint16_t *vc, int n, int b, int h,
@@ -456,16 +569,21 @@ void or_att_combine(float *out, int nb, const float *part, size_t stride, int hd
     for (int i = 0; i < hd; i++) out[i] = out[i] * inv;
 }
 
-static void attention(int bf, float *out, const float *q, const uint16_t *kc, const uint16_t *vc, int n, int h, int n_kv,
-                      int hd, float scale) {
+static void attention_t(int kvt, float *out, const float *q, const uint16_t *kc, const uint16_t *vc, const uint8_t *kq,
+                        const uint8_t *vq, int n, int h, int n_kv, int hd, float scale) {
     /* attention_kv (forward.c:1871-1892): one block directly, else the partials of every block, combined */
     int nb = (n + ATT_P - 1) / ATT_P;
     size_t st = (size_t)hd + 16;
     float *part = malloc((size_t)nb * st * sizeof(float));
     for (int b = 0; b < nb; b++)
-        attention_block(bf, part + b * st, part + b * st + hd, q, kc, vc, n, b, h, n_kv, hd, scale);
+        attention_block_t(kvt, part + b * st, part + b * st + hd, q, kc, vc, kq, vq, n, b, h, n_kv, hd, scale);
     or_att_combine(out, nb, part, st, hd);
     free(part);
+}
+
+static void attention(int bf, float *out, const float *q, const uint16_t *kc, const uint16_t *vc, int n, int h, int n_kv,
+                      int hd, float scale) {
+    attention_t(bf, out, q, kc, vc, NULL, NULL, n, h, n_kv, hd, scale);
 }
 
 void or_attention(float *out, const float *q, const uint16_t *kc, const uint16_t *vc, int n, int h, int n_kv, int hd,
@@ -591,7 +709,10 @@ struct OrModel {
 struct OrSeq {
     const OrModel *m;
     int len, bf; /* bf: a bf16 cache (RQ_KV_BF16), else f16 */
+    int qt;      /* a quantized cache: RQ_KV_Q8, RQ_KV_Q4 or RQ_KV_Q4K4 (kq / vq), else 0 (kc / vc) */
     uint16_t *kc, *vc;
+    uint8_t *kq, *vq;
+    size_t kq_layer, vq_layer; /* bytes per layer of kq / vq */
 };
 
 typedef struct { const char *name; size_t nlen; uint64_t ne[4]; uint32_t nd, type; uint64_t off; } GT;
@@ -760,10 +881,29 @@ OrSeq *or_seq_new_kv(const OrModel *m, int bf16) {
     return s;
 }
 
+OrSeq *or_seq_new_type(const OrModel *m, int kv_type) {
+    /* a sequence of cache type kv_type (runq.h:214): RQ_KV_F16 2, RQ_KV_BF16 1, RQ_KV_Q8 3, RQ_KV_Q4 8, RQ_KV_Q4K4 9 */
+    if (kv_type == 1 || kv_type == 2) return or_seq_new_kv(m, kv_type == 1);
+    if (kv_type != KVQ_Q8 && kv_type != KVQ_Q4 && kv_type != KVQ_Q4K4) return NULL;
+    OrSeq *s = calloc(1, sizeof(OrSeq));
+    if (!s) return NULL;
+    const size_t tiles = (size_t)m->kv_len / ATT_T * m->nkv;
+    s->m = m;
+    s->qt = kv_type;
+    s->kq_layer = tiles * kvq_tile_bytes(kvq_fmt(kv_type, 0), m->hd);
+    s->vq_layer = tiles * kvq_tile_bytes(kvq_fmt(kv_type, 1), m->hd);
+    s->kq = calloc((size_t)m->L, s->kq_layer);
+    s->vq = calloc((size_t)m->L, s->vq_layer);
+    if (!s->kq || !s->vq) { or_seq_free(s); return NULL; }
+    return s;
+}
+
 void or_seq_free(OrSeq *s) {
     if (!s) return;
     free(s->kc);
     free(s->vc);
+    free(s->kq);
+    free(s->vq);
     free(s);
 }
 
@@ -772,6 +912,18 @@ void or_seq_truncate(OrSeq *s, int n) { if (n >= 0 && n <= s->len) s->len = n; }
 void or_seq_set_len(OrSeq *s, int n) { s->len = n; }
 
 void or_seq_copy(OrSeq *dst, const OrSeq *src, int n) {
+    if (src->qt) { /* (the tiles holding positions 0 .. n - 1, whole: later positions are stored before they are read) */
+        const size_t tb_k = kvq_tile_bytes(kvq_fmt(src->qt, 0), src->m->hd), tb_v = kvq_tile_bytes(kvq_fmt(src->qt, 1), src->m->hd);
+        for (int l = 0; l < src->m->L; l++)
+            for (int t = 0; t < n; t += ATT_T)
+                for (int h = 0; h < src->m->nkv; h++) {
+                    const size_t nt = or_kv_tile(t, h, src->m->nkv, src->m->hd) / ((size_t)ATT_T * src->m->hd);
+                    memcpy(dst->kq + l * src->kq_layer + nt * tb_k, src->kq + l * src->kq_layer + nt * tb_k, tb_k);
+                    memcpy(dst->vq + l * src->vq_layer + nt * tb_v, src->vq + l * src->vq_layer + nt * tb_v, tb_v);
+                }
+        dst->len = n;
+        return;
+    }
     size_t per = (size_t)src->m->kv_len * src->m->nkv * src->m->hd;
     for (int l = 0; l < src->m->L; l++)
         for (int t = 0; t < n; t++)
@@ -787,7 +939,14 @@ void or_seq_copy(OrSeq *dst, const OrSeq *src, int n) {
 }
 
 const uint16_t *or_seq_cache(const OrSeq *s, int layer, int v) {
+    if (s->qt) return NULL;
     return (v ? s->vc : s->kc) + (size_t)layer * s->m->kv_len * s->m->nkv * s->m->hd;
+}
+
+const uint8_t *or_seq_cache_q(const OrSeq *s, int layer, int v) {
+    /* a quantized cache's layer base (the tiles of kvq_tile_bytes each), else NULL */
+    if (!s->qt) return NULL;
+    return v ? s->vq + layer * s->vq_layer : s->kq + layer * s->kq_layer;
 }
 uint16_t *or_seq_cache_mut(OrSeq *s, int layer, int v) {
     return (v ? s->vc : s->kc) + (size_t)layer * s->m->kv_len * s->m->nkv * s->m->hd;
@@ -846,6 +1005,24 @@ int or_forward_token(const OrModel *m, OrSeq *s, int token, float *logits, float
         matvec(v, &m->wv[l], xq, xs);
         or_qk_norm_rope(q, nh, m->q_norm[l], hd, cs);
         or_qk_norm_rope(k, nkv, m->k_norm[l], hd, cs);
+        if (s->qt) { /* kv_store's quantized rows (forward.c:1907-1913), attention on q' (forward.c:2679, :2712) */
+            uint8_t *kq = s->kq + l * s->kq_layer, *vq = s->vq + l * s->vq_layer;
+            const int fk = kvq_fmt(s->qt, 0), fv = kvq_fmt(s->qt, 1);
+            for (int g = 0; g < nkv; g++) {
+                const size_t nt = or_kv_tile(pos, g, nkv, hd) / ((size_t)ATT_T * hd);
+                kvq_store(fk, kq + nt * kvq_tile_bytes(fk, hd), pos % ATT_T, hd, k + g * hd, 0);
+                kvq_store(fv, vq + nt * kvq_tile_bytes(fv, hd), pos % ATT_T, hd, v + g * hd, 1);
+            }
+            for (int h = 0; h < nh; h++) {
+                float qr[256];
+                memcpy(qr, q + h * hd, (size_t)hd * sizeof(float));
+                kvq_rot(qr, hd, 0);
+                kvq_scale_by(qr, hd);
+                attention_t(s->qt, att + h * hd, qr, NULL, NULL, kq, vq, pos + 1, h / kv_mul, nkv, hd, m->att_scale);
+                kvq_rot(att + h * hd, hd, 1);
+                kvq_scale_by(att + h * hd, hd);
+            }
+        } else {
         uint16_t *kc = s->kc + (size_t)l * per, *vc = s->vc + (size_t)l * per;
         for (int g = 0; g < nkv; g++) { /* kv_store (forward.c:1901-1951), f16 or bf16, rounded to nearest even */
             size_t o = or_kv_tile(pos, g, nkv, hd);
@@ -857,6 +1034,7 @@ int or_forward_token(const OrModel *m, OrSeq *s, int token, float *logits, float
         }
         for (int h = 0; h < nh; h++)
             attention(s->bf, att + h * hd, q + h * hd, kc, vc, pos + 1, h / kv_mul, nkv, hd, m->att_scale);
+        }
         or_quantize(xq, xs, att, qd);
         matvec(xb, &m->wo[l], xq, xs);
         for (int i = 0; i < dim; i++) x[i] += xb[i];

@@ -59,6 +59,7 @@ def lib() -> ctypes.CDLL:
             "or_model_att_scale": (F, [P]),
             "or_seq_new": (P, [P]),
             "or_seq_new_kv": (P, [P, I]),
+            "or_seq_new_type": (P, [P, I]),
             "or_seq_free": (None, [P]),
             "or_seq_len": (I, [P]),
             "or_seq_truncate": (None, [P, I]),
@@ -133,8 +134,9 @@ class Model:
         self.dim, self.hidden, self.n_layers, self.n_heads, self.n_kv_heads, self.head_dim, self.vocab, self.kv_len = \
             (int(v) for v in d)
 
-    def seq(self, bf16: bool = False) -> "Seq":
-        return Seq(self, bf16)
+    def seq(self, bf16: bool = False, kv_type: int = 0) -> "Seq":
+        """kv_type (runq.h:214) when given, else f16 (or bf16)"""
+        return Seq(self, bf16, kv_type)
 
     def __del__(self):
         if getattr(self, "_h", None):
@@ -143,9 +145,11 @@ class Model:
 
 
 class Seq:
-    def __init__(self, m: Model, bf16: bool = False):
+    def __init__(self, m: Model, bf16: bool = False, kv_type: int = 0):
         self.m = m
-        self._h = lib().or_seq_new_kv(m._h, 1 if bf16 else 0)
+        self._h = lib().or_seq_new_type(m._h, kv_type) if kv_type else lib().or_seq_new_kv(m._h, 1 if bf16 else 0)
+        if not self._h:
+            raise RuntimeError(f"or_seq_new: kv type {kv_type}")
 
     def __len__(self):
         return lib().or_seq_len(self._h)

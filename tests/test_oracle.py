@@ -434,30 +434,34 @@ def test_attention_combine_matches_single_pass():
 
 
 @need_ref
-@pytest.mark.parametrize("shape,over,n,bf16", [
-    ("tiny", {}, 40, False),
-    ("tiny_kq", {}, 20, False),
-    ("tiny_iq4xs", {}, 20, False),
-    ("tiny_q2k", {}, 20, False),
-    ("qwen3_0_6b", dict(n_layers=3, vocab=4096, tied=0), 12, False),
-    ("tiny", {}, 40, True),
-    ("qwen3_0_6b", dict(n_layers=2, vocab=4096, tied=0), 270, True),
+@pytest.mark.parametrize("shape,over,n,kvt", [
+    ("tiny", {}, 40, 2),
+    ("tiny_kq", {}, 20, 2),
+    ("tiny_iq4xs", {}, 20, 2),
+    ("tiny_q2k", {}, 20, 2),
+    ("qwen3_0_6b", dict(n_layers=3, vocab=4096, tied=0), 12, 2),
+    ("tiny", {}, 40, 1),
+    ("qwen3_0_6b", dict(n_layers=2, vocab=4096, tied=0), 270, 1),
+    ("tiny", {}, 270, 3),
+    ("tiny", {}, 270, 8),
+    ("tiny", {}, 270, 9),
+    ("tiny_hd64", {}, 40, 3),
 ])
-def test_forward_bit_exact_vs_reference(tmp_path, shape, over, n, bf16):
+def test_forward_bit_exact_vs_reference(tmp_path, shape, over, n, kvt):
     """or_forward_token position by position against the reference compiled from its sources (rq_prefill with every
     row's logits, ref_driver), on seeded synthetic models: every logit bit for bit. On an AVX-512 host the oracle's
-    SwiGLU runs the reference's own vector expf and rcp14; nothing else in the pass depends on the host. bf16: both
-    with a bf16 KV cache (RQ_KV_BF16; 270 positions: two attention blocks)"""
+    SwiGLU runs the reference's own vector expf and rcp14; nothing else in the pass depends on the host. kvt: both with
+    that KV cache type (runq.h:214: 2 f16, 1 bf16, 3 q8, 8 q4, 9 q4k4: the rotated, quantized caches of
+    forward.c:1609-1790; 270 positions: two attention blocks)"""
     from gwenedeg_amd import synth
     d = dict(synth.SHAPES[shape])
     d.update(over)
     path = str(tmp_path / "m.gguf")
     synth.write_gguf(path, d, seed=1)
     ids = np.random.default_rng(7).integers(0, d["vocab"], n).astype(np.int32)
-    _, lg, _, _ = orc.run_ref_driver(path, ids, str(tmp_path / "ref"), threads=4, cap=512, all_logits=True,
-                                     kv_type=1 if bf16 else 2)
+    _, lg, _, _ = orc.run_ref_driver(path, ids, str(tmp_path / "ref"), threads=4, cap=512, all_logits=True, kv_type=kvt)
     om = orc.Model(path, cap=512)
-    s = om.seq(bf16=bf16)
+    s = om.seq(kv_type=kvt)
     for i, t in enumerate(ids):
         mine = s.forward(int(t))
         assert np.array_equal(_u32(mine), _u32(lg[i])), f"position {i}: max diff {np.abs(mine - lg[i]).max()}"
