@@ -42,15 +42,27 @@ static int ctx_hip(RqCtx *c, const char *what, hipError_t e) {
 
 /* ---------------------------------------------------------------------------------------- sequences */
 
-static size_t seq_layer_elems(const RqSeq *s) { return (size_t)s->kv_len * s->m->n_kv_heads * s->m->head_dim; }
+/* bytes of one layer's K (kv 0) or V cache: kv_len / 16 x n_kv tiles */
+static size_t seq_layer_bytes(const RqSeq *s, int kv) {
+    return (size_t)s->kv_len / GW_ATT_T * s->m->n_kv_heads * gw_kv_tile_bytes(s->kvt, s->m->head_dim, kv);
+}
+/* layer l's K (kv 0) or V cache base */
+static uint16_t *seq_layer(const RqSeq *s, int l, int kv) {
+    return (uint16_t *)((uint8_t *)(kv ? s->vc : s->kc) + (size_t)l * seq_layer_bytes(s, kv));
+}
 
 RqSeq *rq_seq_new(const RqModel *m, int capacity, int kv_type, int *err) {
     int e = RQ_OK;
     RqSeq *s = NULL;
     if (!m) { e = RQ_ERR_STATE; goto fail; }
     if (capacity <= 0) capacity = m->seq_len;
-    /* f16 and bf16 caches (the fp32 attention on the exactly converted values, runq.h:204-213); other types RQ_ERR_ARG */
-    if (capacity > m->seq_len || (kv_type != RQ_KV_F16 && kv_type != RQ_KV_BF16)) { e = RQ_ERR_ARG; goto fail; }
+    /* f16 and bf16 caches (the fp32 attention on the exactly converted values, runq.h:204-213), and the rotated q8 / q4
+     * ones (head_dim a power of two, 32 .. 128); other types RQ_ERR_ARG */
+    int hd = m->head_dim, qok = hd >= 32 && hd <= 128 && !(hd & (hd - 1));
+    if (capacity > m->seq_len || (kv_type != RQ_KV_F16 && kv_type != RQ_KV_BF16 && !(gw_kv_quant(kv_type) && qok))) {
+        e = RQ_ERR_ARG;
+        goto fail;
+    }
     s = calloc(1, sizeof(RqSeq));
     if (!s) { e = RQ_ERR_NOMEM; goto fail; }
     s->m = m;
@@ -60,8 +72,8 @@ RqSeq *rq_seq_new(const RqModel *m, int capacity, int kv_type, int *err) {
     s->att_nb = s->kv_len / GW_ATT_P;
     s->nck = 2;   /* (RQ_SEQ_CK, internal.h:66) */
     s->hpos = -1; /* (not an MTP view's sequence) */
-    size_t bytes = (size_t)m->n_layers * seq_layer_elems(s) * 2;
-    if (hipMalloc((void **)&s->kc, bytes) != hipSuccess || hipMalloc((void **)&s->vc, bytes) != hipSuccess) {
+    if (hipMalloc((void **)&s->kc, (size_t)m->n_layers * seq_layer_bytes(s, 0)) != hipSuccess ||
+        hipMalloc((void **)&s->vc, (size_t)m->n_layers * seq_layer_bytes(s, 1)) != hipSuccess) {
         e = RQ_ERR_NOMEM;
         goto fail;
     }
@@ -146,8 +158,9 @@ void rq_seq_resident(const RqSeq *s, RqSeqMem *out) {
 
 size_t rq_seq_kv_bytes(const RqSeq *s, int n) {
     n = n < 0 ? 0 : n > s->cap ? s->cap : n;
-    size_t nb = ((size_t)n + GW_ATT_P - 1) / GW_ATT_P;
-    return 2 * (size_t)s->m->n_layers * nb * GW_ATT_P * s->m->n_kv_heads * s->m->head_dim * 2 + (size_t)s->cap * sizeof(int);
+    size_t nb = ((size_t)n + GW_ATT_P - 1) / GW_ATT_P, hd = (size_t)s->m->head_dim;
+    return (size_t)s->m->n_layers * nb * (GW_ATT_P / GW_ATT_T) * s->m->n_kv_heads *
+               (gw_kv_tile_bytes(s->kvt, (int)hd, 0) + gw_kv_tile_bytes(s->kvt, (int)hd, 1)) + (size_t)s->cap * sizeof(int);
 }
 
 int rq_seq_copy(RqSeq *dst, const RqSeq *src, int n) {
@@ -156,17 +169,18 @@ int rq_seq_copy(RqSeq *dst, const RqSeq *src, int n) {
     if (!dst || !src || dst == src || dst->m != src->m || dst->kvt != src->kvt || n < 0 || n > src->len || n > dst->cap)
         return RQ_ERR_ARG;
     const RqModel *m = src->m;
-    int nkv = m->n_kv_heads, hd = m->head_dim, full = n / GW_ATT_P, rem = n % GW_ATT_P;
-    size_t kvd = (size_t)nkv * hd, ntl = (size_t)(rem + GW_ATT_T - 1) / GW_ATT_T;
+    int nkv = m->n_kv_heads, hd = m->head_dim, full = n / GW_ATT_P, rem = n % GW_ATT_P, tpb = GW_ATT_P / GW_ATT_T;
+    size_t ntl = (size_t)(rem + GW_ATT_T - 1) / GW_ATT_T;
     for (int l = 0; l < m->n_layers && n > 0; l++)
         for (int kv = 0; kv < 2; kv++) {
-            const uint16_t *sb = (kv ? src->vc : src->kc) + (size_t)l * seq_layer_elems(src);
-            uint16_t *db = (kv ? dst->vc : dst->kc) + (size_t)l * seq_layer_elems(dst);
-            if (full && hipMemcpy(db, sb, (size_t)full * GW_ATT_P * kvd * 2, hipMemcpyDeviceToDevice) != hipSuccess)
+            const size_t tb = gw_kv_tile_bytes(src->kvt, hd, kv); /* (tiles in order: block, head, tile) */
+            const uint8_t *sb = (const uint8_t *)seq_layer(src, l, kv);
+            uint8_t *db = (uint8_t *)seq_layer(dst, l, kv);
+            if (full && hipMemcpy(db, sb, (size_t)full * tpb * nkv * tb, hipMemcpyDeviceToDevice) != hipSuccess)
                 return RQ_ERR_STATE;
             for (int h = 0; h < nkv && rem; h++) {
-                size_t o = (((size_t)full * nkv + h) * GW_ATT_P) * hd;
-                if (hipMemcpy(db + o, sb + o, ntl * GW_ATT_T * hd * 2, hipMemcpyDeviceToDevice) != hipSuccess) return RQ_ERR_STATE;
+                size_t o = ((size_t)full * nkv + h) * tpb * tb;
+                if (hipMemcpy(db + o, sb + o, ntl * tb, hipMemcpyDeviceToDevice) != hipSuccess) return RQ_ERR_STATE;
             }
         }
     memcpy(dst->tokens, src->tokens, (size_t)n * sizeof(int));
@@ -181,10 +195,13 @@ int rq_seq_fill_synthetic(RqSeq *s, int n, unsigned long long seed) {
     /* runq.h:721-726: n positions of pseudo-random K / V (|K| < 4, |V| < 1), arbitrary valid tokens */
     if (!s || n < 1 || n > s->cap) return RQ_ERR_ARG;
     size_t nb = ((size_t)n + GW_ATT_P - 1) / GW_ATT_P, per = nb * GW_ATT_P * s->m->n_kv_heads * s->m->head_dim;
-    for (int l = 0; l < s->m->n_layers; l++)
-        if (gw_k_fill_synthetic(s->kc + (size_t)l * seq_layer_elems(s), s->vc + (size_t)l * seq_layer_elems(s), per,
-                                seed + (unsigned long long)l * 0x1000193ull, 0))
-            return RQ_ERR_STATE;
+    for (int l = 0; l < s->m->n_layers; l++) {
+        unsigned long long sl = seed + (unsigned long long)l * 0x1000193ull;
+        int e = gw_kv_quant(s->kvt) ? gw_k_fill_synthetic_q(seq_layer(s, l, 0), seq_layer(s, l, 1), s->kvt, (int)(nb * GW_ATT_P),
+                                                             s->m->n_kv_heads, s->m->head_dim, sl, 0)
+                                    : gw_k_fill_synthetic(seq_layer(s, l, 0), seq_layer(s, l, 1), per, sl, 0);
+        if (e) return RQ_ERR_STATE;
+    }
     if (hipDeviceSynchronize() != hipSuccess) return RQ_ERR_STATE;
     for (int i = 0; i < n; i++) s->tokens[i] = (int)((seed + (unsigned long long)i * 7919u) % (unsigned long long)s->m->vocab);
     seq_grow(s, n);
@@ -290,9 +307,12 @@ int rq_seq_mem(const RqModel *m, int capacity, int kv_type, RqSeqMem *mem) {
     memset(mem, 0, sizeof(*mem));
     if (!m) return RQ_ERR_STATE;
     if (capacity <= 0) capacity = m->seq_len;
-    if (capacity > m->seq_len || (kv_type != RQ_KV_F16 && kv_type != RQ_KV_BF16)) return RQ_ERR_ARG;
+    int hd = m->head_dim, qok = hd >= 32 && hd <= 128 && !(hd & (hd - 1));
+    if (capacity > m->seq_len || (kv_type != RQ_KV_F16 && kv_type != RQ_KV_BF16 && !(gw_kv_quant(kv_type) && qok)))
+        return RQ_ERR_ARG;
     size_t kv_len = ((size_t)capacity + GW_ATT_P - 1) / GW_ATT_P * GW_ATT_P;
-    mem->kv = (size_t)m->n_layers * kv_len * m->n_kv_heads * m->head_dim * 2 * 2 + (size_t)capacity * sizeof(int);
+    mem->kv = (size_t)m->n_layers * kv_len / GW_ATT_T * m->n_kv_heads *
+                  (gw_kv_tile_bytes(kv_type, hd, 0) + gw_kv_tile_bytes(kv_type, hd, 1)) + (size_t)capacity * sizeof(int);
     mem->total = mem->kv;
     return RQ_OK;
 }
@@ -569,7 +589,7 @@ static int fused_layer(RqCtx *c, int l, RqSeq *sq, int pos, const int *pos_d) {
     KCHK(gw_k_gemv1_norm(&y->qkv[0], GW_GV_R_QKV, c->x, y->att_norm, c->qkv, 0, 0, &y->wo, GW_GV_R_WO, s));
     pf_mark(c, GW_PF_ATT);
     KCHK(gw_k_attn_decode(c->qkv, nh, m->n_kv_heads, hd, m->att_scale, y->q_norm, y->k_norm, m->rope, pos,
-                          sq->kc + (size_t)l * seq_layer_elems(sq), sq->vc + (size_t)l * seq_layer_elems(sq), c->part,
+                          seq_layer(sq, l, 0), seq_layer(sq, l, 1), c->part,
                           c->pstride, sq->kvt == RQ_KV_BF16, s));
     if (nb <= GW_GV_NBMAX) {
         pf_mark(c, GW_PF_WO);
@@ -616,27 +636,31 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
     memcpy(h + o_tok, P->tok, (size_t)n * 4);
     memcpy(h + o_pos, P->pos, (size_t)n * 4);
     memcpy(h + o_sel, P->sel, (size_t)n * 4);
-    int *kbf = (int *)(h + o_kbf), nbf = 0; /* (rows of bf16 caches; their attention items go last) */
-    for (int b = 0; b < n; b++) kbf[b] = P->seq[b]->kvt == RQ_KV_BF16;
+    int *kvt = (int *)(h + o_kbf), nbf = 0, nqz = 0; /* (each row's cache type; rows of bf16 / quantized caches) */
+    for (int b = 0; b < n; b++) {
+        kvt[b] = P->seq[b]->kvt;
+        nbf += kvt[b] == RQ_KV_BF16;
+        nqz += gw_kv_quant(kvt[b]);
+    }
     uint16_t **ptr = (uint16_t **)(h + o_ptr);
     for (int l = 0; l < L; l++)
         for (int b = 0; b < n; b++) {
-            size_t lo = (size_t)l * P->seq[b]->kv_len * nkv * hd;
-            ptr[(size_t)l * n + b] = P->seq[b]->kc + lo;
-            ptr[(size_t)(L + l) * n + b] = P->seq[b]->vc + lo;
+            ptr[(size_t)l * n + b] = seq_layer(P->seq[b], l, 0);
+            ptr[(size_t)(L + l) * n + b] = seq_layer(P->seq[b], l, 1);
         }
-    /* the items in four groups, each launched with its own query-vector bound: the f16 caches', then the bf16
+    /* the items in five groups, each launched with its own query-vector bound: the f16 caches', then the bf16
      * caches'; in each, the row blocks of <= 4 query vectors (decode rows: the narrow kernel, two blocks per CU), then
      * the wider ones (prompt row blocks). A pass of both kinds of rows would otherwise run every decode row's items in
-     * the 16-vector kernel */
+     * the 16-vector kernel. Then the quantized caches' (k_attn_q) */
     Item *it = (Item *)(h + o_items);
-    int gcnt[4] = { 0, 0, 0, 0 }, gnq[4] = { 1, 1, 1, 1 };
-    for (int grp = 0, k = 0; grp < 4; grp++)
+    int gcnt[5] = { 0, 0, 0, 0, 0 }, gnq[5] = { 1, 1, 1, 1, 1 };
+    for (int grp = 0, k = 0; grp < 5; grp++)
         for (int b = 0; b < n;) {
             int e = b + 1;
             while (e < n && e - b < rb && P->seq[e] == P->seq[b] && P->pos[e] == P->pos[e - 1] + 1) e++;
             int nb = (P->pos[e - 1] + 1 + GW_ATT_P - 1) / GW_ATT_P, nq = (e - b) * kv_mul;
-            if (kbf[b] == grp >> 1 && (nq > 4) == (grp & 1)) {
+            int kg = gw_kv_quant(kvt[b]) ? 4 : 2 * (kvt[b] == RQ_KV_BF16) + (nq > 4);
+            if (kg == grp) {
                 for (int g = 0; g < nkv; g++)
                     for (int kb = 0; kb < nb; kb++) it[k++] = (Item){ b, e - b, g, kb };
                 gcnt[grp] += nkv * nb;
@@ -644,10 +668,9 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
             }
             b = e;
         }
-    nbf = gcnt[2] + gcnt[3];
     HIPCHK(c, "hipMemcpyAsync (pass metadata)", hipMemcpyAsync(d, h, total, hipMemcpyHostToDevice, c->stream));
     const int *tok_d = (const int *)(d + o_tok), *pos_d = (const int *)(d + o_pos), *sel_d = (const int *)(d + o_sel);
-    const int *kbf_d = (const int *)(d + o_kbf);
+    const int *kvt_d = (const int *)(d + o_kbf);
     uint16_t *const *kc_d = (uint16_t *const *)(d + o_ptr), *const *vc_d = kc_d + (size_t)L * n;
     const void *items_d = d + o_items;
     hipStream_t s = c->stream;
@@ -660,7 +683,7 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
     else KCHK(gw_k_embed_kq(c->x, dim, m->embd.type, m->embd.blocks, m->embd.bstride, tok_d, n, s));
     /* one row of an all-Q8_0 model: the fused decode sequence (gw_gemv.hip: each matmul computes its activation from
      * the producer's fp32 output; the residual adds go straight into x) */
-    int fused = n == 1 && fused_shape(m), fused_att = fused && (hd == 128 || hd == 64 || hd == 32);
+    int fused = n == 1 && fused_shape(m) && !nqz, fused_att = fused && (hd == 128 || hd == 64 || hd == 32);
     for (int l = 0; l < L; l++) {
         const GwLayer *y = &m->layer[l];
         if (fused_att) {
@@ -678,13 +701,18 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
         }
         pf_mark(c, GW_PF_ROPE);
         KCHK(gw_k_qknorm_rope_store(c->qkv, c->ldqkv, n, nh, nkv, hd, y->q_norm, y->k_norm, m->rope, pos_d,
-                                    kc_d + (size_t)l * n, vc_d + (size_t)l * n, nbf ? kbf_d : NULL, s));
+                                    kc_d + (size_t)l * n, vc_d + (size_t)l * n, nbf || nqz ? kvt_d : NULL, s));
         pf_mark(c, GW_PF_ATT);
-        for (int grp = 0, off = 0; grp < 4; off += gcnt[grp], grp++)
-            if (gcnt[grp])
+        for (int grp = 0, off = 0; grp < 5; off += gcnt[grp], grp++) {
+            if (!gcnt[grp]) continue;
+            if (grp == 4)
+                KCHK(gw_k_attn_q((const Item *)items_d + off, gcnt[grp], c->qkv, c->ldqkv, nh, nkv, hd, m->att_scale, pos_d,
+                                 kc_d + (size_t)l * n, vc_d + (size_t)l * n, kvt_d, c->part, c->pstride, s));
+            else
                 KCHK(gw_k_attn_part((const Item *)items_d + off, gcnt[grp], gnq[grp], c->qkv, c->ldqkv, nh, nkv, hd,
                                     m->att_scale, pos_d, kc_d + (size_t)l * n, vc_d + (size_t)l * n, c->part, c->pstride,
                                     grp >> 1, s));
+        }
         if (fused) {
             if (nbmax <= GW_GV_NBMAX) {
                 pf_mark(c, GW_PF_WO);
@@ -702,7 +730,9 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
             continue;
         }
         pf_mark(c, GW_PF_COMBINE);
-        KCHK(gw_k_attn_combine_quant(c->part, c->pstride, nh, hd, pos_d, n, nbmax, c->xq, c->xs, K, NULL, s));
+        /* (rows of quantized caches: the combined o' into the free qkv buffer, then o = D H o' / hd quantized over theirs) */
+        KCHK(gw_k_attn_combine_quant(c->part, c->pstride, nh, hd, pos_d, n, nbmax, c->xq, c->xs, K, nqz ? c->qkv : NULL, s));
+        if (nqz) KCHK(gw_k_unrot_quant(c->qkv, n, nh, hd, kvt_d, c->xq, c->xs, K, s));
         pf_mark(c, GW_PF_WO);
         if ((rc = run_mm(c, &y->wo, 1, c->xq, c->xs, K, n, c->xb, dim, 0)) != RQ_OK) return rc;
         pf_mark(c, GW_PF_NORM);

@@ -37,6 +37,14 @@ enum { GW_F32 = 0, GW_Q8_0 = 8, GW_Q2_K = 10, GW_Q3_K = 11, GW_Q4_K = 12, GW_Q5_
 /* the super-block types (256 values; the matmul kernels' K-quant paths): Q2_K .. Q6_K and IQ4_XS */
 #define GW_IS_KQ(t) (((t) >= GW_Q2_K && (t) <= GW_Q6_K) || (t) == GW_IQ4_XS)
 
+/* KV cache types (runq.h:214): the rotated 8-bit / 4-bit ones, and the bytes of a tile (16 positions x hd of one kv
+ * head) of K (is_v 0) or V: 16-bit 32 hd, q8 17 hd, q4 9 hd (RQ_KV_Q4: K q8, V q4; RQ_KV_Q4K4: both q4) */
+static inline int gw_kv_quant(int kvt) { return kvt == RQ_KV_Q8 || kvt == RQ_KV_Q4 || kvt == RQ_KV_Q4K4; }
+static inline size_t gw_kv_tile_bytes(int kvt, int hd, int is_v) {
+    int q4 = kvt == RQ_KV_Q4K4 || (kvt == RQ_KV_Q4 && is_v);
+    return (size_t)hd * (!gw_kv_quant(kvt) ? 32 : q4 ? 9 : 17);
+}
+
 /* a K-quant super-block's bytes in the file and on the device (0: not a K-quant) */
 static inline int gw_kq_file_bytes(int type) {
     return type == GW_Q3_K ? GW_Q3K_BYTES : type == GW_Q4_K ? GW_Q4K_BYTES : type == GW_Q5_K ? GW_Q5K_BYTES
@@ -124,7 +132,7 @@ struct RqSeq {
     int cap;           /* @8: positions */
     int kv_len;        /* @12: cap rounded up to whole 256-position blocks (the cache layout) */
     int att_nb;        /* @16: kv_len / 256 */
-    int kvt;           /* @20: RQ_KV_F16 or RQ_KV_BF16 */
+    int kvt;           /* @20: RQ_KV_F16, RQ_KV_BF16, RQ_KV_Q8, RQ_KV_Q4 or RQ_KV_Q4K4 */
     unsigned char ref0_[80 - 24];
     int len;           /* @80: positions in the cache */
     int hwm;           /* @84 */
@@ -138,7 +146,8 @@ struct RqSeq {
     int hvalid, hpos;  /* @1816: an MTP view's state (spec.c); 0 and -1 here (no sequence is a view's) */
     float *hprev;      /* @1824: NULL */
     /* this library's own */
-    uint16_t *kc, *vc; /* device: n_layers x kv_len x kv_dim 16-bit values each (f16, or bf16 when kvt is) */
+    uint16_t *kc, *vc; /* device: n_layers x kv_len x kv_dim 16-bit values each (f16, or bf16 when kvt is); the quantized
+                        * types: n_layers x kv_len / 16 x n_kv tiles of gw_kv_tile_bytes each, in the same tile order */
 };
 
 #ifndef __cplusplus
@@ -242,7 +251,13 @@ int gw_k_rmsnorm_quant(float *x, const float *d, int dim, const float *w, const 
                        int ldq, float *hid, hipStream_t s);
 int gw_k_qknorm_rope_store(float *qkv, int ldqkv, int n, int nh, int nkv, int hd, const float *qn, const float *kn,
                            const float *rope, const int *pos, uint16_t *const *kc, uint16_t *const *vc,
-                           const int *kbf, hipStream_t s); /* kbf: per row, 1 for a bf16 cache (NULL: all f16) */
+                           const int *kvt, hipStream_t s); /* kvt: per row, its cache type (runq.h:214; NULL: all f16) */
+/* the attention partials of items on the quantized caches (RQ_KV_Q8 / Q4 / Q4K4; kvt: each row's type; hd a power of two,
+ * 32 .. 128) */
+int gw_k_attn_q(const void *items, int nitems, const float *qkv, int ldqkv, int nh, int nkv, int hd, float scale, const int *pos,
+                uint16_t *const *kc, uint16_t *const *vc, const int *kvt, float *part, int pstride, hipStream_t s);
+/* the rows of quantized caches: o = D H o' / hd from the combined attention att (n rows of nh hd), quantized into aq / as */
+int gw_k_unrot_quant(const float *att, int n, int nh, int hd, const int *kvt, int8_t *aq, float *as, int ldq, hipStream_t s);
 int gw_k_attn_part(const void *items, int nitems, int nq_max, const float *qkv, int ldqkv, int nh, int nkv, int hd, float scale,
                    const int *pos, uint16_t *const *kc, uint16_t *const *vc, float *part, int pstride, int kbf, hipStream_t s);
 /* the one-row pass's attention with its QK-norm, RoPE and K / V store (hd 32, 64 or 128; pos: the row's position;
@@ -266,6 +281,9 @@ int gw_k_topk_noalloc(const float *lg, int n, int ld, int rows, int k, float **v
  * matrices interleaved in blocks of il rows) */
 int gw_k_q8_unpack(const uint8_t *blocks, size_t nblk, int8_t *codes, uint16_t *scales, int gpr, int il, int off, hipStream_t s);
 int gw_k_fill_synthetic(uint16_t *kc, uint16_t *vc, size_t n, unsigned long long seed, hipStream_t s);
+/* the quantized caches' synthetic rows (|K| < 4, |V| < 1 before the rotation): positions 0 .. npos - 1 of one layer's K
+ * and V caches (kc / vc: the layer's bases), stored as k_qknorm_rope_store stores them */
+int gw_k_fill_synthetic_q(void *kc, void *vc, int kvt, int npos, int nkv, int hd, unsigned long long seed, hipStream_t s);
 
 /* the single-row Q8_0 GEMV with the activation's producer fused in front (gw_gemv.hip): out[row] (+)= W row . act for
  * R rows per tile (2, 4, 8, 16); act = the quantized row (q), rmsnorm(x, nw) (norm), the fp32 row x (qf) or the attention

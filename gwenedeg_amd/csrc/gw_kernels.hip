@@ -121,16 +121,113 @@ __global__ __launch_bounds__(NORM_T) void k_rmsnorm_quant(float *__restrict__ x,
 // the key heads (rmsnorm with kn, RoPE, f16 into the K cache), then the value heads (f16 into the V cache).
 // qkv row b: [q (nh hd) | k (nkv hd) | v (nkv hd)]; rope: cos / sin rows per position (hd floats: cos then sin).
 // Caches: row b's layer base kc[b] / vc[b] (f16, the tiled layout of forward.c:1894-1899)
+// ---- the 8-bit / 4-bit KV caches (RQ_KV_Q8, RQ_KV_Q4, RQ_KV_Q4K4; forward.c:1609-1790). A position's key and value
+// rows are rotated, x' = H D x (D: the signs kvq_neg, H: the unnormalized Walsh-Hadamard butterflies h = 1, 2, .. in that
+// order, each output one fp32 add or subtract), then quantized per 32 dims from the group's values alone (q8: d = bf16
+// of max |x'| / 127, its magnitude rounded up, n = rint(x' (1 / d)) in -127..127; q4: m = the first x' of largest |x'|,
+// d = bf16 of m / -8 rounded up in magnitude, n = rint(x' (1 / d)) in -8..7; d zero or denormal: the group is zero), read
+// back as n d (exact). The attention runs on q' = H D q / hd (rotated in k_qknorm_rope_store) and the values read
+// back, and its output o' comes back as o = D H o' / hd (k_unrot_quant). Tiles (16 positions j x hd dims i):
+//   K q8 [i][j] int8, the bf16 scales at 16 hd: [c][j];  K q4: byte [p][j] = (n_2p + 8) | (n_2p+1 + 8) << 4, scales at
+//   8 hd; V q8 [j][i] int8, scales at 16 hd: [j][c];  V q4: byte [j][c][l] = (n_32c+l + 8) | (n_32c+16+l + 8) << 4,
+//   scales at 8 hd: [j][c]
+__device__ __forceinline__ bool kvq_type(int kvt) { return kvt == 3 || kvt == 8 || kvt == 9; }
+__device__ __forceinline__ bool kvq_q4(int kvt, bool is_v) { return kvt == 9 || (kvt == 8 && is_v); } // (the half's format)
+__device__ __forceinline__ int kvq_tile_bytes(bool q4, int hd) { return hd * (q4 ? 9 : 17); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// x (hd values in LDS) <- H D x (inv false) or D H x (inv true) by the block's 64 threads
+__device__ void kvq_rot_lds(float *x, int n, bool inv) {
+    const int t = threadIdx.x;
+    if (!inv) {
+        for (int i = t; i < n; i += 64)
+            if ((((uint32_t)i * 0x9E3779B9u) >> 31) != 0u) x[i] = -x[i];
+        __syncthreads();
+    }
+    for (int h = 1; h < n; h *= 2) {
+        for (int k = t; k < n / 2; k += 64) {
+            const int i = (k / h) * 2 * h + k % h;
+            const float a = x[i], b = x[i + h];
+            x[i] = a + b;
+            x[i + h] = a - b;
+        }
+        __syncthreads();
+    }
+    if (inv) {
+        for (int i = t; i < n; i += 64)
+            if ((((uint32_t)i * 0x9E3779B9u) >> 31) != 0u) x[i] = -x[i];
+        __syncthreads();
+    }
+}
+
+// the rotated row x (hd values in LDS) quantized into position j of a q8 / q4 tile (K: is_v false), by the block's 64
+// threads; sc: LDS scratch of hd / 32 words
+__device__ void kvq_store_lds(const float *x, int hd, bool q4, bool is_v, uint8_t *tile, int j, uint32_t *sc) {
+    const int t = threadIdx.x, ng = hd >> 5;
+    if (t < ng) { // the group's scale: the first value of largest magnitude (q4), the largest magnitude (q8)
+        float a = 0.0f, m = 0.0f;
+        for (int i = 0; i < 32; i++)
+            if (fabsf(x[32 * t + i]) > a) {
+                a = fabsf(x[32 * t + i]);
+                m = x[32 * t + i];
+            }
+        const float d = q4 ? m / -8.0f : a / 127.0f;
+        const uint32_t u = __float_as_uint(d), r = (u >> 16) + ((u & 0xffffu) != 0u);
+        const uint16_t s16 = (r & 0x7f80u) ? (uint16_t)r : (uint16_t)0;
+        sc[t] = s16;
+        uint16_t *so = (uint16_t *)(tile + (size_t)(q4 ? 8 : 16) * hd) + (is_v ? j * ng + t : t * ATT_T + j);
+        *so = s16;
+    }
+    __syncthreads();
+    auto level = [&](int i) -> int { // (rint(x (1 / d)): the reference's build multiplies by the group's reciprocal)
+        const uint32_t s16 = sc[i >> 5];
+        const float d = bf16_to_f32((uint16_t)s16), tq = s16 ? __builtin_rintf(x[i] * (1.0f / d)) : 0.0f;
+        const float lo = q4 ? -8.0f : -127.0f, hi = q4 ? 7.0f : 127.0f;
+        return tq < lo ? (int)lo : tq > hi ? (int)hi : (int)tq;
+    };
+    if (!q4) {
+        for (int i = t; i < hd; i += 64) tile[is_v ? (size_t)j * hd + i : (size_t)i * ATT_T + j] = (uint8_t)(int8_t)level(i);
+    } else if (!is_v) {
+        for (int p2 = t; p2 < hd / 2; p2 += 64)
+            tile[(size_t)p2 * ATT_T + j] = (uint8_t)((level(2 * p2) + 8) | (level(2 * p2 + 1) + 8) << 4);
+    } else {
+        for (int k = t; k < hd / 2; k += 64) { // (byte 16 c + l of the position: dims 32 c + l and 32 c + 16 + l)
+            const int c = k >> 4, l = k & 15;
+            tile[(size_t)j * (hd / 2) + k] = (uint8_t)((level(32 * c + l) + 8) | (level(32 * c + 16 + l) + 8) << 4);
+        }
+    }
+}
+
+// the tile of position p, kv head g of a layer's quantized cache (base: the layer's first byte)
+__device__ __forceinline__ uint8_t *kvq_tile(void *base, int p, int g, int nkv, int hd, bool q4) {
+    const size_t nt = ((size_t)(p / ATT_P) * nkv + g) * (ATT_P / ATT_T) + (size_t)(p % ATT_P / ATT_T);
+    return (uint8_t *)base + nt * (size_t)kvq_tile_bytes(q4, hd);
+}
+
+// rows' QK-norm + RoPE and the K / V store (forward.c:1266-1284, :1901-1951); kvt: each row's cache type (runq.h:214;
+// NULL: all f16). A quantized row's query heads are rotated in place (q' = H D q / hd) and its key / value rows stored
+// rotated and quantized
 __global__ __launch_bounds__(64) void k_qknorm_rope_store(float *__restrict__ qkv, int ldqkv, int nh, int nkv, int hd,
                                                           const float *__restrict__ qn, const float *__restrict__ kn,
                                                           const float *__restrict__ rope, const int *__restrict__ pos,
                                                           uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc,
-                                                          const int *__restrict__ kbf) {
+                                                          const int *__restrict__ kvt) {
     __shared__ float v[256];
+    __shared__ uint32_t scw[8];
     int b = blockIdx.x, h = blockIdx.y, lane = threadIdx.x, p = pos[b];
-    const bool bf = kbf && kbf[b]; // (row b's sequence has a bf16 cache)
+    const int kt = kvt ? kvt[b] : 2;
+    const bool bf = kt == 1, qz = kvq_type(kt); // (row b's sequence has a bf16 / a quantized cache)
     float *row = qkv + (size_t)b * ldqkv;
     int half = hd / 2;
+    if (qz && h >= nh + nkv) { // value head: rotated and quantized
+        int g = h - nh - nkv;
+        const float *src = row + (size_t)(nh + nkv) * hd + g * hd;
+        for (int i = lane; i < hd; i += 64) v[i] = src[i];
+        __syncthreads();
+        kvq_rot_lds(v, hd, false);
+        kvq_store_lds(v, hd, kvq_q4(kt, true), true, kvq_tile(vc[b], p, g, nkv, hd, kvq_q4(kt, true)), p % ATT_T, scw);
+        return;
+    }
     if (h >= nh + nkv) { // value head: store
         int g = h - nh - nkv;
         const float *src = row + (size_t)(nh + nkv) * hd + g * hd;
@@ -150,7 +247,10 @@ __global__ __launch_bounds__(64) void k_qknorm_rope_store(float *__restrict__ qk
         float c = cs[i], s = cs[i + half];
         float ys = y * s, yc = y * c;
         float xo = __builtin_fmaf(x, c, -ys), yo = __builtin_fmaf(x, s, yc);
-        if (h < nh) {
+        if (qz) { // (rotated below: each thread rewrites only the values it read)
+            v[i] = xo;
+            v[i + half] = yo;
+        } else if (h < nh) {
             src[i] = xo;
             src[i + half] = yo;
         } else {
@@ -160,9 +260,171 @@ __global__ __launch_bounds__(64) void k_qknorm_rope_store(float *__restrict__ qk
             dst[kv_k_at(bf, i + half, p % ATT_T)] = bf ? f2bf_ref(yo) : f2h_ref(yo);
         }
     }
+    if (qz) {
+        __syncthreads();
+        kvq_rot_lds(v, hd, false);
+        if (h < nh) { // q' = H D q / hd (1 / hd: a power of two, exact)
+            const float f = 1.0f / (float)hd;
+            for (int i = lane; i < hd; i += 64) src[i] = v[i] * f;
+        } else {
+            const int g = h - nh;
+            kvq_store_lds(v, hd, kvq_q4(kt, false), false, kvq_tile(kc[b], p, g, nkv, hd, kvq_q4(kt, false)), p % ATT_T, scw);
+        }
+    }
+}
+
+// synthetic rows of the quantized caches (rq_seq_fill_synthetic): block (position p, kv head g, K / V) draws hd values
+// (|K| < 3.9, |V| < 0.99) from a hash of (seed, p, g, K / V, dim) and stores them as k_qknorm_rope_store does
+__global__ __launch_bounds__(64) void k_fill_synthetic_q(void *kc, void *vc, int kvt, int nkv, int hd, unsigned long long seed) {
+    __shared__ float v[256];
+    __shared__ uint32_t scw[8];
+    const int p = blockIdx.x, g = blockIdx.y, isv = blockIdx.z;
+    for (int i = threadIdx.x; i < hd; i += 64) {
+        unsigned long long z = seed + (((unsigned long long)p * nkv + g) * 2 + isv) * 0x100000001b3ull + (unsigned long long)i * 0x9e3779b97f4a7c15ull;
+        z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+        z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+        z ^= z >> 31;
+        const float a = (float)(z & 0xffffff) * (1.0f / 16777216.0f);
+        v[i] = (2.0f * a - 1.0f) * (isv ? 0.99f : 3.9f);
+    }
+    __syncthreads();
+    kvq_rot_lds(v, hd, false);
+    const bool q4 = kvq_q4(kvt, isv != 0);
+    kvq_store_lds(v, hd, q4, isv != 0, kvq_tile(isv ? vc : kc, p, g, nkv, hd, q4), p % ATT_T, scw);
+}
+
+// the rows of quantized caches: their attention output o' (att: rows of nh hd values) back to o = D H o' / hd, then
+// quantized for wo as k_attn_combine_quant quantizes (aq / as rows of ldq codes); other rows are left as they are
+__global__ __launch_bounds__(64) void k_unrot_quant(const float *__restrict__ att, int nh, int hd, const int *__restrict__ kvt,
+                                                    int8_t *__restrict__ aq, float *__restrict__ as, int ldq) {
+    __shared__ float v[256];
+    const int b = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
+    if (!kvq_type(kvt[b])) return;
+    const float *src = att + ((size_t)b * nh + h) * hd;
+    for (int i = t; i < hd; i += 64) v[i] = src[i];
+    __syncthreads();
+    kvq_rot_lds(v, hd, true);
+    const float f = 1.0f / (float)hd;
+    for (int i = t; i < hd; i += 64) { // (hd % 64 == 0 or hd = 32: whole groups of 32 lanes)
+        const int e = h * hd + i;
+        if (i < hd) quant_lane32(v[i] * f, aq + (size_t)b * ldq + e, as + (size_t)b * (ldq / 32) + (e >> 5));
+    }
 }
 
 // ----------------------------------------------------------------------------------------- attention
+
+// Attention on the quantized caches: one block of AQ_T threads per item (first row r0, rows nr of one sequence, kv head
+// g, key block kb; the items of k_attn_part) and each of its nq = nr kv_mul query vectors q' (rotated by
+// k_qknorm_rope_store) that reaches the block: the fp32 attention of the oracle's attention_block on the values read
+// back (n d, exact), as forward.c:1776-1803 runs it on kvq_block_f32's copy: scores by the chunk chains of 32 dims
+// (a = c0 + c1 + c2 + c3, times scale), m the max, e = exp_att(s - m), l the 16 chains over positions j % 16 and the tree,
+// o the fma chain over the positions. part[(row nh + h) pstride + kb (hd + 2)] = o, m, l. The block's K tiles are staged
+// into LDS, then its V tiles over them. hd <= 128 (a power of two), nq <= 16.
+#define AQ_T 512
+__global__ __launch_bounds__(AQ_T) void k_attn_q(const int4 *__restrict__ items, const float *__restrict__ qkv, int ldqkv,
+                                                 int nh, int nkv, int hd, float scale, const int *__restrict__ pos,
+                                                 uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc,
+                                                 const int *__restrict__ kvt, float *__restrict__ part, int pstride) {
+    __shared__ __align__(16) uint8_t tl[ATT_T * 17 * 128]; // the block's 16 tiles of K, then of V
+    __shared__ float qs[16 * 128];
+    __shared__ float S[16][ATT_P];
+    __shared__ float ms[16], ls[16];
+    const int4 it = items[blockIdx.x];
+    const int r0 = it.x, nr = it.y, g = it.z, kb = it.w, kv_mul = nh / nkv, nq = nr * kv_mul, t = threadIdx.x;
+    const int kt = kvt[r0], ng = hd >> 5;
+    const bool k4 = kvq_q4(kt, false), v4 = kvq_q4(kt, true);
+    const int tbk = kvq_tile_bytes(k4, hd), tbv = kvq_tile_bytes(v4, hd);
+    auto npos = [&](int v) -> int { // positions of block kb vector v reaches (<= 0: none)
+        const int n = pos[r0 + v / kv_mul] + 1 - kb * ATT_P;
+        return n < ATT_P ? n : ATT_P;
+    };
+    // 1. the K tiles (the block's 16 tiles of head g are consecutive) and the query vectors
+    {
+        const uint4 *src = (const uint4 *)kvq_tile(kc[r0], kb * ATT_P, g, nkv, hd, k4);
+        for (int i = t; i < ATT_T * tbk / 16; i += AQ_T) ((uint4 *)tl)[i] = src[i];
+        for (int i = t; i < nq * hd; i += AQ_T) {
+            const int v = i / hd, d = i % hd;
+            qs[i] = qkv[(size_t)(r0 + v / kv_mul) * ldqkv + (size_t)(g * kv_mul + v % kv_mul) * hd + d];
+        }
+    }
+    __syncthreads();
+    // 2. scores, thread per (vector, position)
+    for (int k = t; k < nq * ATT_P; k += AQ_T) {
+        const int v = k / ATT_P, p = k % ATT_P;
+        if (p >= npos(v)) continue;
+        const uint8_t *tb = tl + (size_t)(p / ATT_T) * tbk;
+        const uint16_t *sc = (const uint16_t *)(tb + (size_t)(k4 ? 8 : 16) * hd);
+        const int j = p % ATT_T;
+        const float *q = qs + v * hd;
+        float a = 0.0f;
+        for (int c = 0; c < ng; c++) {
+            const float d = bf16_to_f32(sc[c * ATT_T + j]);
+            float cc = 0.0f;
+            for (int i = 32 * c; i < 32 * c + 32; i++) {
+                const int n = k4 ? ((tb[(i >> 1) * ATT_T + j] >> (4 * (i & 1))) & 15) - 8 : (int)(int8_t)tb[i * ATT_T + j];
+                cc = __builtin_fmaf(q[i], (float)n * d, cc);
+            }
+            a = c ? a + cc : cc;
+        }
+        S[v][p] = a * scale;
+    }
+    __syncthreads();
+    // 3. softmax: wave w takes vectors w, w + 8: m, the exponentials, l (lane j < 16: the chain over positions j, j + 16,
+    // ...; then the tree)
+    {
+        const int wave = t >> 6, lane = t & 63;
+        for (int v = wave; v < nq; v += AQ_T / 64) {
+            const int n = npos(v);
+            if (n <= 0) continue;
+            float m = S[v][0];
+            for (int p = lane; p < n; p += 64) m = S[v][p] > m ? S[v][p] : m;
+            for (int o = 32; o >= 1; o >>= 1) {
+                const float u = __shfl_xor(m, o);
+                m = u > m ? u : m;
+            }
+            for (int p = lane; p < n; p += 64) S[v][p] = exp_att(S[v][p] - m);
+            __builtin_amdgcn_wave_barrier();
+            float sm = 0.0f;
+            if (lane < 16)
+                for (int p = lane; p < n; p += ATT_T) sm = sm + S[v][p];
+            for (int w = 8; w >= 1; w >>= 1) {
+                const float o = __shfl_down(sm, w);
+                if (lane < w) sm = sm + o;
+            }
+            if (lane == 0) {
+                ms[v] = m;
+                ls[v] = sm;
+            }
+        }
+    }
+    __syncthreads();
+    // 4. the V tiles over the K tiles
+    {
+        const uint4 *src = (const uint4 *)kvq_tile(vc[r0], kb * ATT_P, g, nkv, hd, v4);
+        for (int i = t; i < ATT_T * tbv / 16; i += AQ_T) ((uint4 *)tl)[i] = src[i];
+    }
+    __syncthreads();
+    // 5. o, thread per (vector, dim): the fma chain over the positions in order
+    for (int k = t; k < nq * hd; k += AQ_T) {
+        const int v = k / hd, i = k % hd, n = npos(v), c = i >> 5;
+        if (n <= 0) continue;
+        float o = 0.0f;
+        for (int p = 0; p < n; p++) {
+            const uint8_t *tb = tl + (size_t)(p / ATT_T) * tbv;
+            const int j = p % ATT_T;
+            const float d = bf16_to_f32(((const uint16_t *)(tb + (size_t)(v4 ? 8 : 16) * hd))[j * ng + c]);
+            const int nn = v4 ? ((tb[(size_t)j * (hd / 2) + 16 * c + (i & 15)] >> (4 * ((i >> 4) & 1))) & 15) - 8
+                              : (int)(int8_t)tb[(size_t)j * hd + i];
+            o = __builtin_fmaf(S[v][p], (float)nn * d, o);
+        }
+        float *dst = part + ((size_t)(r0 + v / kv_mul) * nh + g * kv_mul + v % kv_mul) * pstride + (size_t)kb * (hd + 2);
+        dst[i] = o;
+        if (i == 0) {
+            dst[hd] = ms[v];
+            dst[hd + 1] = ls[v];
+        }
+    }
+}
 
 // One block of 1024 threads per item (first row r0, rows nr of one sequence at consecutive positions, kv head g, key
 // block kb): the partial result of block kb (forward.c:1346-1403 with ml) for each of the nq = nr * kv_mul query vectors
@@ -1132,9 +1394,30 @@ int gw_k_set_exact(const float *rsq, int bits, const uint64_t *rcp, const uint8_
 }
 
 int gw_k_qknorm_rope_store(float *qkv, int ldqkv, int n, int nh, int nkv, int hd, const float *qn, const float *kn,
-                           const float *rope, const int *pos, uint16_t *const *kc, uint16_t *const *vc, const int *kbf,
+                           const float *rope, const int *pos, uint16_t *const *kc, uint16_t *const *vc, const int *kvt,
                            hipStream_t s) {
-    GW_LAUNCH(k_qknorm_rope_store, dim3(n, nh + 2 * nkv), dim3(64), 0, s, qkv, ldqkv, nh, nkv, hd, qn, kn, rope, pos, kc, vc, kbf);
+    GW_LAUNCH(k_qknorm_rope_store, dim3(n, nh + 2 * nkv), dim3(64), 0, s, qkv, ldqkv, nh, nkv, hd, qn, kn, rope, pos, kc, vc, kvt);
+    return (int)hipGetLastError();
+}
+
+int gw_k_attn_q(const void *items, int nitems, const float *qkv, int ldqkv, int nh, int nkv, int hd, float scale, const int *pos,
+                uint16_t *const *kc, uint16_t *const *vc, const int *kvt, float *part, int pstride, hipStream_t s) {
+    // (hd a power of two, 32 .. 128; at most 16 query vectors per item)
+    if (hd < 32 || hd > 128 || (hd & (hd - 1))) return (int)hipErrorInvalidValue;
+    GW_LAUNCH(k_attn_q, dim3(nitems), dim3(AQ_T), 0, s, (const int4 *)items, qkv, ldqkv, nh, nkv, hd, scale, pos, kc, vc, kvt,
+              part, pstride);
+    return (int)hipGetLastError();
+}
+
+int gw_k_fill_synthetic_q(void *kc, void *vc, int kvt, int npos, int nkv, int hd, unsigned long long seed, hipStream_t s) {
+    if (hd > 256 || npos < 1) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_fill_synthetic_q, dim3(npos, nkv, 2), dim3(64), 0, s, kc, vc, kvt, nkv, hd, seed);
+    return (int)hipGetLastError();
+}
+
+int gw_k_unrot_quant(const float *att, int n, int nh, int hd, const int *kvt, int8_t *aq, float *as, int ldq, hipStream_t s) {
+    if (hd > 256 || (hd != 32 && hd % 64)) return (int)hipErrorInvalidValue;
+    GW_LAUNCH(k_unrot_quant, dim3(n, nh), dim3(64), 0, s, att, nh, hd, kvt, aq, as, ldq);
     return (int)hipGetLastError();
 }
 

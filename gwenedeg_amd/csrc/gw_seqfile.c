@@ -46,10 +46,14 @@ static uint64_t sf_hash(const SfHdr *h, const int *tokens) {
     return fnv(fnv(1469598103934665603ull, &c, sizeof(c)), tokens, (size_t)h->len * sizeof(int));
 }
 
-static uint64_t sf_blk(const RqModel *m) { return (uint64_t)GW_ATT_P * m->n_kv_heads * m->head_dim * 2; } /* f16, K or V */
+/* a block's bytes of K (kv 0) or V: ATT_P / ATT_T x n_kv tiles (seqfile.c:49-53) */
+static uint64_t sf_blk(const RqModel *m, int kvt, int kv) {
+    return (uint64_t)(GW_ATT_P / GW_ATT_T) * m->n_kv_heads * gw_kv_tile_bytes(kvt, m->head_dim, kv);
+}
+static int sf_type_ok(int kvt) { return kvt == RQ_KV_F16 || kvt == RQ_KV_BF16 || gw_kv_quant(kvt); }
 
 static void sf_shape(const RqModel *m, int len, int kvt, SfHdr *h) {
-    /* every field but rng and hash, as the reference writes them for this model, length and cache type (f16 / bf16) */
+    /* every field but rng and hash, as the reference writes them for this model, length and cache type */
     memset(h, 0, sizeof(*h));
     memcpy(h->magic, sf_magic, 8);
     h->version = SF_VERSION;
@@ -62,12 +66,12 @@ static void sf_shape(const RqModel *m, int len, int kvt, SfHdr *h) {
     h->att_p = GW_ATT_P;
     h->att_t = GW_ATT_T;
     h->att = kvt;
-    h->kv_esz = 2;
+    h->kv_esz = (int32_t)(gw_kv_tile_bytes(kvt, m->head_dim, 1) / ((size_t)GW_ATT_T * m->head_dim)); /* (V's, rounded down) */
     h->len = len;
     h->nblk = (len + GW_ATT_P - 1) / GW_ATT_P;
-    h->blk_bytes = sf_blk(m);
+    h->blk_bytes = sf_blk(m, kvt, 0);
     h->off_kv = SF_ALIGN + sf_round((uint64_t)len * sizeof(int));
-    h->off_ssm = h->off_kv + (uint64_t)m->n_layers * h->nblk * 2 * h->blk_bytes;
+    h->off_ssm = h->off_kv + (uint64_t)m->n_layers * h->nblk * (h->blk_bytes + sf_blk(m, kvt, 1));
     h->file_bytes = h->off_ssm;
 }
 
@@ -86,15 +90,17 @@ static int sf_blocks(const RqSeq *s, int fd, int wr, const SfHdr *h, int nblk) {
     /* the first nblk blocks of every (layer, K / V) between the device cache and the file (the file's sections hold
      * h->nblk blocks each), through one host buffer of a section */
     const RqModel *m = s->m;
-    size_t bytes = (size_t)nblk * h->blk_bytes, per = (size_t)s->kv_len * m->n_kv_heads * m->head_dim;
+    const uint64_t bk = sf_blk(m, s->kvt, 0), bv = sf_blk(m, s->kvt, 1);
+    const size_t lk = (size_t)s->kv_len / GW_ATT_P * bk, lv = (size_t)s->kv_len / GW_ATT_P * bv; /* (a layer's bytes) */
     void *buf = NULL;
     int rc = 0;
     if (!nblk) return 0;
-    if (hipHostMalloc(&buf, bytes, hipHostMallocDefault) != hipSuccess) return RQ_ERR_NOMEM;
+    if (hipHostMalloc(&buf, (size_t)nblk * (bk > bv ? bk : bv), hipHostMallocDefault) != hipSuccess) return RQ_ERR_NOMEM;
     for (int l = 0; l < m->n_layers && !rc; l++)
         for (int kv = 0; kv < 2 && !rc; kv++) {
-            uint16_t *dev = (kv ? s->vc : s->kc) + (size_t)l * per;
-            uint64_t off = h->off_kv + (uint64_t)h->nblk * h->blk_bytes * (2 * (uint64_t)l + (uint64_t)kv);
+            size_t bytes = (size_t)nblk * (kv ? bv : bk);
+            uint8_t *dev = (uint8_t *)(kv ? s->vc : s->kc) + (size_t)l * (kv ? lv : lk);
+            uint64_t off = h->off_kv + (uint64_t)h->nblk * ((uint64_t)l * (bk + bv) + (kv ? bk : 0));
             if (wr) {
                 if (hipMemcpy(buf, dev, bytes, hipMemcpyDeviceToHost) != hipSuccess) rc = RQ_ERR_STATE;
                 else if (sf_rw(fd, 1, buf, bytes, off)) rc = RQ_ERR_IO;
@@ -162,7 +168,7 @@ static int sf_open_check(const RqModel *m, const char *path, int *fd, SfHdr *h, 
     int lmax = m->seq_len;
     if (h->len < 1 || h->len > lmax) goto fail;
     SfHdr w;
-    sf_shape(m, h->len, h->att == RQ_KV_BF16 ? RQ_KV_BF16 : RQ_KV_F16, &w);
+    sf_shape(m, h->len, sf_type_ok(h->att) ? h->att : RQ_KV_F16, &w);
     w.rng = h->rng;
     w.hash = h->hash;
     if (memcmp(&w, h, sizeof(w)) || (uint64_t)st.st_size != h->file_bytes) goto fail;

@@ -394,8 +394,9 @@ uint16_t or_f32_bf16(float f) {
 /* ---- the 8-bit / 4-bit KV caches (RQ_KV_Q8, RQ_KV_Q4, RQ_KV_Q4K4; forward.c:1609-1790). A position's key and value
  * rows are rotated, x' = H D x (D: signs kvq_neg, H: the unnormalized Walsh-Hadamard butterflies in the order h = 1, 2,
  * .., each output one fp32 add or subtract), then quantized per group of 32 dims from the group's values alone:
- *   q8: d = bf16 of max |x'| / 127 with its magnitude rounded up; n = rint(x' / d) in -127..127
- *   q4: m = the x' of largest |x'| (the first), d = bf16 of m / -8, magnitude rounded up; n = rint(x' / d) in -8..7
+ *   q8: d = bf16 of max |x'| / 127 with its magnitude rounded up; n = rint(x' (1 / d)) in -127..127
+ *   q4: m = the x' of largest |x'| (the first), d = bf16 of m / -8, magnitude rounded up; n = rint(x' (1 / d)) in -8..7
+ *   (the reference's source writes x' / d; its build, which parity follows, multiplies by the reciprocal)
  *   (d zero or a bf16 denormal: the group is zero). Read back n d, exact.
  * The attention runs on q' = H D q / hd and the values read back (the fp32 attention), and its output o' comes back as
  * o = D H o' / hd. Tile layouts (16 positions j, hd dims i; the bf16 scales after the codes):
@@ -458,11 +459,13 @@ static void kvq_store(int fmt, uint8_t *tile, int j, int hd, const float *x0, in
                 m = g[i];
             }
         const uint16_t s = kvq_scale(q4 ? m / -8.0f : a / 127.0f);
-        const float d = bf16_f32(s);
+        const float d = bf16_f32(s), r = 1.0f / d;
         int8_t n[32];
         const int lo = q4 ? -8 : -127, hi = q4 ? 7 : 127;
         for (int i = 0; i < 32; i++) {
-            const float t = s ? rintf(g[i] / d) : 0.0f;
+            /* rint(x' / d) as the reference's build computes it: x' times the one reciprocal 1 / d of the group (the
+             * compiled kvq_group divides once and multiplies; the two differ where x' / d lies within an ulp of a half) */
+            const float t = s ? rintf(g[i] * r) : 0.0f;
             n[i] = (int8_t)(t < (float)lo ? lo : t > (float)hi ? hi : (int)t);
         }
         const size_t so = 2 * (is_v ? (size_t)j * ng + c : (size_t)c * ATT_T + j);

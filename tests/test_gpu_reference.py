@@ -4,6 +4,7 @@ north star's three levels of correctness, here met exactly:
   per-block int32 dot sums bit-exact;  logits equal bit for bit (the tolerance's limit);  greedy tokens identical.
 The device reproduces the reference's host-specific float operations from tables measured on this host
 (gwenedeg_amd/csrc/gw_exact.c); where the host cannot provide them (no AVX-512) the tests are skipped."""
+import ctypes
 import os
 
 import numpy as np
@@ -200,13 +201,14 @@ def test_hidden_rows_after_batched_passes_on_one_context(gw, orc, tmp_path):
     assert np.array_equal(_bits(lg), _bits(rlg[21:62])), "fw_rows n 41, max_batch 8: logits rows"
 
 
-@pytest.mark.parametrize("kvt", [2, 1])  # RQ_KV_F16, RQ_KV_BF16
+@pytest.mark.parametrize("kvt", [2, 1, 3, 8, 9])  # RQ_KV_F16, RQ_KV_BF16, RQ_KV_Q8, RQ_KV_Q4, RQ_KV_Q4K4
 def test_seqfile_with_reference(gw, orc, tmp_path, kvt):
     """the KV disk tier (runq.h:283-314) against the reference's seqfile.c: the same model fingerprint; the reference's
     saved sequence (300-token prompt + 4 greedy steps) read by rq_seq_file_info and loaded by rq_seq_load continues bit
     for bit as the device's own sequence of the same tokens; the device's saved file matches the reference's header
     and tokens (all but the RNG word and the hash over it) and its whole K / V blocks byte for byte, and loads back;
-    with an f16 and a bf16 cache (a file loads only into a sequence of its cache type)"""
+    with each cache type the device keeps (a file loads only into a sequence of its cache type; the quantized caches'
+    blocks hold the rotated, quantized rows, so their bytes pin the store)"""
     import ctypes
     path, d = _synth(str(tmp_path), "qwen3_0_6b", n_layers=2)
     m = gw.Model(path, ctx_len=1024)
@@ -248,11 +250,15 @@ def test_seqfile_with_reference(gw, orc, tmp_path, kvt):
     hdr[248:264] = False  # (the RNG word and the hash)
     assert np.array_equal(r[:264][hdr], o[:264][hdr])
     assert np.array_equal(r[4096:4096 + 4 * L], o[4096:4096 + 4 * L])
-    off_kv, blk = int(np.frombuffer(r[224:232].tobytes(), np.uint64)[0]), 256 * m.info.n_kv_heads * m.info.head_dim * 2
+    hd = m.info.head_dim
+    tile = {2: (32, 32), 1: (32, 32), 3: (17, 17), 8: (17, 9), 9: (9, 9)}[kvt]  # (K, V tile bytes per dim)
+    off_kv = int(np.frombuffer(r[224:232].tobytes(), np.uint64)[0])
+    bk, bv = (16 * m.info.n_kv_heads * hd * t for t in tile)
     nblk = (L + 255) // 256
-    for sec in range(2 * 2):  # (layer, K / V): the first block is whole (positions 0..255 < L)
-        s0 = off_kv + sec * nblk * blk
-        assert np.array_equal(r[s0:s0 + blk], o[s0:s0 + blk]), f"section {sec}"
+    for l in range(2):
+        for kv in range(2):  # (the first block of each section is whole: positions 0..255 < L)
+            s0, blk = off_kv + nblk * (l * (bk + bv) + kv * bk), (bv if kv else bk)
+            assert np.array_equal(r[s0:s0 + blk], o[s0:s0 + blk]), f"layer {l} kv {kv}"
     again = m.seq(1024, kv_type=kvt)
     assert lib.rq_seq_load(ctypes.c_void_p(again._h), p2.encode(), 200) == 0
     assert lib.rq_seq_len(ctypes.c_void_p(again._h)) == 200
@@ -268,6 +274,38 @@ def test_seqfile_with_reference(gw, orc, tmp_path, kvt):
     assert lib.rq_seq_load(ctypes.c_void_p(m.seq(1024, kv_type=kvt)._h), p3.encode(), 10) == -7  # RQ_ERR_MISMATCH
     other = gw.RQ_KV_BF16 if kvt == gw.RQ_KV_F16 else gw.RQ_KV_F16
     assert lib.rq_seq_load(ctypes.c_void_p(m.seq(1024, kv_type=other)._h), p2.encode(), 10) == -7
+
+
+@pytest.mark.parametrize("kvt", [3, 8, 9])  # RQ_KV_Q8, RQ_KV_Q4, RQ_KV_Q4K4
+def test_quantized_kv_greedy_bit_identical(gw, orc, tmp_path, kvt):
+    """the rotated 8-bit / 4-bit KV caches (forward.c:1609-1790) on a Qwen3-0.6B-shaped model (2 layers): a 300-token
+    prefill (two key blocks, 16-vector row blocks) and 24 greedy steps, every logits row equal bit for bit to the
+    reference's own cache of that type, the same tokens; then a pass of that sequence's next token beside a fresh
+    sequence's prompt (both of the type) equal to each run alone"""
+    path, d = _synth(str(tmp_path), "qwen3_0_6b", seed=4, n_layers=2)
+    m = gw.Model(path, ctx_len=512)
+    if not _exact(gw):
+        pytest.skip("this host does not provide the reference's float operations (AVX-512)")
+    ids = np.random.default_rng(9).integers(0, m.vocab, 300).astype(np.int32)
+    _, rlg, rtok, _ = orc.run_ref_driver(path, ids, str(tmp_path / "ref"), steps=24, threads=_threads(), cap=512, kv_type=kvt)
+    c = m.ctx(max_batch=512, max_ctx=512)
+    s = m.seq(512, kv_type=kvt)
+    lg = c.prefill(s, ids, mode=gw.RQ_LOGITS_LAST)
+    for step in range(25):
+        assert np.array_equal(_bits(lg), _bits(rlg[step])), f"row {step}: max diff {np.abs(lg - rlg[step]).max()}"
+        tok = int(np.argmax(lg))
+        if step < 24:
+            assert tok == int(rtok[step]), f"step {step}"
+            lg = c.decode(s, tok)
+    # batch invariance: the next token of s beside a fresh prompt, against each alone
+    s2, s3 = m.seq(512, kv_type=kvt), m.seq(512, kv_type=kvt)
+    assert gw.lib.rq_seq_copy(ctypes.c_void_p(s2._h), ctypes.c_void_p(s._h), len(s)) == 0
+    p2 = ids[:40]
+    both, _ = c.forward_batch([gw.Segment(s, [tok], gw.RQ_LOGITS_LAST), gw.Segment(s3, p2, gw.RQ_LOGITS_LAST)])
+    alone_a = c.decode(s2, tok)
+    s4 = m.seq(512, kv_type=kvt)
+    alone_b = c.prefill(s4, p2, mode=gw.RQ_LOGITS_LAST)
+    assert np.array_equal(_bits(both[0]), _bits(alone_a)) and np.array_equal(_bits(both[1]), _bits(alone_b))
 
 
 @pytest.mark.parametrize("shape", ["tiny_q5k", "tiny_q3k", "tiny_iq4xs", "tiny_q2k"])
