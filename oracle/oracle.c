@@ -26,11 +26,13 @@
  *     vector expf + vrcp14ps + Newton, the -Ofast lowering of forward.c:1953-1958): against the product's
  *     host-measured tables and, through the whole forward, bit for bit;
  *   the whole forward (or_forward_token): logits bit for bit against the compiled reference (oracle/_ref/ref_driver)
- *     on synthetic Q8_0, Q4_K_M and IQ4_XS models, including a Qwen3-0.6B-shaped model with 3 layers.
+ *     on synthetic Q8_0, Q4_K_M and IQ4_XS models, including a Qwen3-0.6B-shaped model with 3 layers, and with every
+ *     KV cache type but f32 (the quantized caches and the bf16 dot-product attention over two key blocks).
  * On a host without AVX-512 the oracle's SwiGLU falls back to the portable form (1 / (1 + expf)); the reference built
  * for such a host lowers the loop to other instructions, so there the SwiGLU is pinned only to tolerance.
  */
 #define _GNU_SOURCE
+#include <float.h>
 #include <immintrin.h>
 #include <math.h>
 #include <stdio.h>
@@ -572,14 +574,82 @@ void or_att_combine(float *out, int nb, const float *part, size_t stride, int hd
     for (int i = 0; i < hd; i++) out[i] = out[i] * inv;
 }
 
+/* ---- the bf16 dot-product attention (the KV types with KV_DOT 4: RQ_KV_BF16_DOT 5, RQ_KV_F16_DOT 6, RQ_KV_Q8_DOT 7,
+ * RQ_KV_Q4_DOT 12, RQ_KV_Q4K4_DOT 13; kernels_avx512.h:1439-1475, forward.c:1452-1606). q, K, V and the softmax weights
+ * rounded to bf16 (vcvtneps2bf16: a denormal input flushed to a zero of its sign, then nearest even); each product pair
+ * as vdpbf16ps's lane, two fmas with the odd element first; every operation with denormal inputs read as zero and
+ * denormal results flushed (the call's FTZ / DAZ). A bf16-dot cache stores bf16 values, V in position pairs (dim i of
+ * positions 2m, 2m + 1 of a tile at 2m hd + 2 i, + 1); an f16-dot cache f16 values, read as bf16 of them; the
+ * quantized dot caches their values read back, rounded to bf16 */
+static float ftz(float x) { return fabsf(x) < FLT_MIN ? copysignf(0.0f, x) : x; }
+static float fma_ftz(float a, float b, float c) { return ftz(fmaf(ftz(a), ftz(b), ftz(c))); }
+static float bf16_round(float x) { return bf16_f32(or_f32_bf16(ftz(x))); } /* (kernels_avx512.h:71-77) */
+static size_t kv_v_dot_at(int i, int j, int hd) { return (size_t)(j & ~1) * hd + 2 * (size_t)i + (j & 1); }
+
+/* a dot cache's value of dim i, position t as the products read it (K: is_v 0); kt: the full type */
+static float kv_get_dot(int kt, const uint16_t *c16, const uint8_t *cq, int t, int h, int n_kv, int hd, int i, int is_v) {
+    const int base = kt & ~4, j = t % ATT_T;
+    if (base == 1) { /* bf16-dot: K as the bf16 cache, V in position pairs */
+        const uint16_t *tl = c16 + or_kv_tile(t, h, n_kv, hd);
+        return bf16_f32(tl[is_v ? kv_v_dot_at(i, j, hd) : kv_k_at(1, i, j)]);
+    }
+    if (base == 2) return bf16_round(kv_get(0, c16, cq, t, h, n_kv, hd, i, is_v)); /* f16-dot */
+    return bf16_round(kv_get(base, c16, cq, t, h, n_kv, hd, i, is_v));
+}
+
+static void attention_block_dot(int kt, float *o, float *ml, const float *qb, const uint16_t *kc, const uint16_t *vc,
+                                const uint8_t *kq, const uint8_t *vq, int n, int b, int h, int n_kv, int hd, float scale) {
+    /* attention_vec_dot (forward.c:1488-1549) on block b of kv head h; qb: q rounded to bf16 */
+    int t0 = b * ATT_P, nb = n - t0 < ATT_P ? n - t0 : ATT_P;
+    float S[ATT_P] = { 0 };
+    for (int t = 0; t < nb; t++) {
+        float a = 0;
+        for (int i0 = 0; i0 < hd; i0 += ATT_DC) {
+            float c = 0;
+            for (int i = i0; i < i0 + ATT_DC; i += 2) { /* (dim pairs, the odd one first) */
+                c = fma_ftz(qb[i + 1], kv_get_dot(kt, kc, kq, t0 + t, h, n_kv, hd, i + 1, 0), c);
+                c = fma_ftz(qb[i], kv_get_dot(kt, kc, kq, t0 + t, h, n_kv, hd, i, 0), c);
+            }
+            a = i0 > 0 ? ftz(a + c) : c;
+        }
+        S[t] = ftz(a * scale);
+    }
+    float m = S[0];
+    for (int t = 1; t < nb; t++)
+        if (S[t] > m) m = S[t];
+    float sum[ATT_T];
+    for (int j = 0; j < ATT_T; j++) sum[j] = 0.0f;
+    for (int t = 0; t < (nb + ATT_T - 1) / ATT_T * ATT_T; t++) {
+        const float w = bf16_round(t < nb ? or_exp_att(S[t] - m) : 0.0f);
+        if (t < nb) S[t] = w;
+        sum[t % ATT_T] = sum[t % ATT_T] + w;
+    }
+    for (int w = ATT_T / 2; w >= 1; w /= 2)
+        for (int j = 0; j < w; j++) sum[j] = sum[j] + sum[j + w];
+    ml[0] = m;
+    ml[1] = sum[0];
+    for (int i = 0; i < hd; i++) o[i] = 0.0f;
+    for (int t = 0; t < nb; t += 2) /* (position pairs, the odd one first; past the last: +0, +0) */
+        for (int i = 0; i < hd; i++) {
+            const float w1 = t + 1 < nb ? S[t + 1] : 0.0f;
+            const float v1 = t + 1 < nb ? kv_get_dot(kt, vc, vq, t0 + t + 1, h, n_kv, hd, i, 1) : 0.0f;
+            o[i] = fma_ftz(S[t], kv_get_dot(kt, vc, vq, t0 + t, h, n_kv, hd, i, 1), fma_ftz(w1, v1, o[i]));
+        }
+}
+
 static void attention_t(int kvt, float *out, const float *q, const uint16_t *kc, const uint16_t *vc, const uint8_t *kq,
                         const uint8_t *vq, int n, int h, int n_kv, int hd, float scale) {
     /* attention_kv (forward.c:1871-1892): one block directly, else the partials of every block, combined */
     int nb = (n + ATT_P - 1) / ATT_P;
     size_t st = (size_t)hd + 16;
     float *part = malloc((size_t)nb * st * sizeof(float));
-    for (int b = 0; b < nb; b++)
-        attention_block_t(kvt, part + b * st, part + b * st + hd, q, kc, vc, kq, vq, n, b, h, n_kv, hd, scale);
+    float qb[256];
+    if (kvt & 4) /* (a dot type: q rounded to bf16, forward.c:1599) */
+        for (int i = 0; i < hd; i++) qb[i] = bf16_round(q[i]);
+    for (int b = 0; b < nb; b++) {
+        if (kvt & 4) attention_block_dot(kvt, part + b * st, part + b * st + hd, qb, kc, vc, kq, vq, n, b, h, n_kv, hd, scale);
+        else attention_block_t(kvt, part + b * st, part + b * st + hd, q, kc, vc, kq, vq, n, b, h, n_kv, hd, scale);
+    }
     or_att_combine(out, nb, part, st, hd);
     free(part);
 }
@@ -713,6 +783,7 @@ struct OrSeq {
     const OrModel *m;
     int len, bf; /* bf: a bf16 cache (RQ_KV_BF16), else f16 */
     int qt;      /* a quantized cache: RQ_KV_Q8, RQ_KV_Q4 or RQ_KV_Q4K4 (kq / vq), else 0 (kc / vc) */
+    int dot;     /* the bf16 dot-product attention (the type's KV_DOT bit) */
     uint16_t *kc, *vc;
     uint8_t *kq, *vq;
     size_t kq_layer, vq_layer; /* bytes per layer of kq / vq */
@@ -885,11 +956,19 @@ OrSeq *or_seq_new_kv(const OrModel *m, int bf16) {
 }
 
 OrSeq *or_seq_new_type(const OrModel *m, int kv_type) {
-    /* a sequence of cache type kv_type (runq.h:214): RQ_KV_F16 2, RQ_KV_BF16 1, RQ_KV_Q8 3, RQ_KV_Q4 8, RQ_KV_Q4K4 9 */
-    if (kv_type == 1 || kv_type == 2) return or_seq_new_kv(m, kv_type == 1);
-    if (kv_type != KVQ_Q8 && kv_type != KVQ_Q4 && kv_type != KVQ_Q4K4) return NULL;
+    /* a sequence of cache type kv_type (runq.h:214): RQ_KV_F16 2, RQ_KV_BF16 1, RQ_KV_Q8 3, RQ_KV_Q4 8, RQ_KV_Q4K4 9, and
+     * their dot-product types (+ 4: 5, 6, 7, 12, 13) */
+    const int base = kv_type & ~4, dot = (kv_type & 4) != 0;
+    if (base == 1 || base == 2) {
+        OrSeq *s = or_seq_new_kv(m, base == 1);
+        if (s) s->dot = dot;
+        return s;
+    }
+    if (base != KVQ_Q8 && base != KVQ_Q4 && base != KVQ_Q4K4) return NULL;
+    kv_type = base;
     OrSeq *s = calloc(1, sizeof(OrSeq));
     if (!s) return NULL;
+    s->dot = dot;
     const size_t tiles = (size_t)m->kv_len / ATT_T * m->nkv;
     s->m = m;
     s->qt = kv_type;
@@ -1021,7 +1100,8 @@ int or_forward_token(const OrModel *m, OrSeq *s, int token, float *logits, float
                 memcpy(qr, q + h * hd, (size_t)hd * sizeof(float));
                 kvq_rot(qr, hd, 0);
                 kvq_scale_by(qr, hd);
-                attention_t(s->qt, att + h * hd, qr, NULL, NULL, kq, vq, pos + 1, h / kv_mul, nkv, hd, m->att_scale);
+                attention_t(s->qt | (s->dot ? 4 : 0), att + h * hd, qr, NULL, NULL, kq, vq, pos + 1, h / kv_mul, nkv, hd,
+                            m->att_scale);
                 kvq_rot(att + h * hd, hd, 1);
                 kvq_scale_by(att + h * hd, hd);
             }
@@ -1030,13 +1110,15 @@ int or_forward_token(const OrModel *m, OrSeq *s, int token, float *logits, float
         for (int g = 0; g < nkv; g++) { /* kv_store (forward.c:1901-1951), f16 or bf16, rounded to nearest even */
             size_t o = or_kv_tile(pos, g, nkv, hd);
             int j = pos % ATT_T, bf = s->bf;
-            for (int i = 0; i < hd; i++) {
+            for (int i = 0; i < hd; i++) { /* (a bf16-dot cache: V in position pairs, forward.c:1916-1924) */
                 kc[o + kv_k_at(bf, i, j)] = bf ? or_f32_bf16(k[g * hd + i]) : or_f32_f16(k[g * hd + i]);
-                vc[o + kv_v_at(bf, i, j, hd)] = bf ? or_f32_bf16(v[g * hd + i]) : or_f32_f16(v[g * hd + i]);
+                vc[o + (bf && s->dot ? kv_v_dot_at(i, j, hd) : kv_v_at(bf, i, j, hd))] =
+                    bf ? or_f32_bf16(v[g * hd + i]) : or_f32_f16(v[g * hd + i]);
             }
         }
-        for (int h = 0; h < nh; h++)
-            attention(s->bf, att + h * hd, q + h * hd, kc, vc, pos + 1, h / kv_mul, nkv, hd, m->att_scale);
+        for (int h = 0; h < nh; h++) /* (the dot types: kt = 1 / 2 | 4) */
+            attention_t(s->dot ? (s->bf ? 1 : 2) | 4 : s->bf, att + h * hd, q + h * hd, kc, vc, NULL, NULL, pos + 1, h / kv_mul,
+                        nkv, hd, m->att_scale);
         }
         or_quantize(xq, xs, att, qd);
         matvec(xb, &m->wo[l], xq, xs);

@@ -58,7 +58,8 @@ void or_model_dims(const OrModel *m, int *d8);
 float or_model_att_scale(const OrModel *m);
 OrSeq *or_seq_new(const OrModel *m);
 OrSeq *or_seq_new_kv(const OrModel *m, int bf16); /* bf16 1: a bf16 cache (RQ_KV_BF16) */
-/* a cache of type kv_type (runq.h:214: 2 f16, 1 bf16, 3 q8, 8 q4, 9 q4k4; the quantized ones forward.c:1609-1790) */
+/* a cache of type kv_type (runq.h:214: 2 f16, 1 bf16, 3 q8, 8 q4, 9 q4k4; the quantized ones forward.c:1609-1790; + 4:
+ * the bf16 dot-product attention on them, kernels_avx512.h:1439-1475) */
 OrSeq *or_seq_new_type(const OrModel *m, int kv_type);
 const uint8_t *or_seq_cache_q(const OrSeq *s, int layer, int v); /* a quantized cache's layer base, else NULL */
 uint16_t or_f32_bf16(float f);
