@@ -57,9 +57,9 @@ RqSeq *rq_seq_new(const RqModel *m, int capacity, int kv_type, int *err) {
     if (!m) { e = RQ_ERR_STATE; goto fail; }
     if (capacity <= 0) capacity = m->seq_len;
     /* f16 and bf16 caches (the fp32 attention on the exactly converted values, runq.h:204-213), and the rotated q8 / q4
-     * ones (head_dim a power of two, 32 .. 128); other types RQ_ERR_ARG */
+     * ones and the dot-product types (head_dim a power of two, 32 .. 128); f32 RQ_ERR_ARG */
     int hd = m->head_dim, qok = hd >= 32 && hd <= 128 && !(hd & (hd - 1));
-    if (capacity > m->seq_len || (kv_type != RQ_KV_F16 && kv_type != RQ_KV_BF16 && !(gw_kv_quant(kv_type) && qok))) {
+    if (capacity > m->seq_len || !gw_kv_ok(kv_type) || ((gw_kv_quant(kv_type) || gw_kv_dot(kv_type)) && !qok)) {
         e = RQ_ERR_ARG;
         goto fail;
     }
@@ -308,7 +308,7 @@ int rq_seq_mem(const RqModel *m, int capacity, int kv_type, RqSeqMem *mem) {
     if (!m) return RQ_ERR_STATE;
     if (capacity <= 0) capacity = m->seq_len;
     int hd = m->head_dim, qok = hd >= 32 && hd <= 128 && !(hd & (hd - 1));
-    if (capacity > m->seq_len || (kv_type != RQ_KV_F16 && kv_type != RQ_KV_BF16 && !(gw_kv_quant(kv_type) && qok)))
+    if (capacity > m->seq_len || !gw_kv_ok(kv_type) || ((gw_kv_quant(kv_type) || gw_kv_dot(kv_type)) && !qok))
         return RQ_ERR_ARG;
     size_t kv_len = ((size_t)capacity + GW_ATT_P - 1) / GW_ATT_P * GW_ATT_P;
     mem->kv = (size_t)m->n_layers * kv_len / GW_ATT_T * m->n_kv_heads *
@@ -636,11 +636,13 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
     memcpy(h + o_tok, P->tok, (size_t)n * 4);
     memcpy(h + o_pos, P->pos, (size_t)n * 4);
     memcpy(h + o_sel, P->sel, (size_t)n * 4);
-    int *kvt = (int *)(h + o_kbf), nbf = 0, nqz = 0; /* (each row's cache type; rows of bf16 / quantized caches) */
+    /* (each row's cache type; rows of bf16 caches, rows of quantized or dot-product ones (k_attn_q), rows to unrotate) */
+    int *kvt = (int *)(h + o_kbf), nbf = 0, nqz = 0, nrot = 0;
     for (int b = 0; b < n; b++) {
         kvt[b] = P->seq[b]->kvt;
         nbf += kvt[b] == RQ_KV_BF16;
-        nqz += gw_kv_quant(kvt[b]);
+        nqz += gw_kv_quant(kvt[b]) || gw_kv_dot(kvt[b]);
+        nrot += gw_kv_quant(kvt[b]);
     }
     uint16_t **ptr = (uint16_t **)(h + o_ptr);
     for (int l = 0; l < L; l++)
@@ -648,18 +650,18 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
             ptr[(size_t)l * n + b] = seq_layer(P->seq[b], l, 0);
             ptr[(size_t)(L + l) * n + b] = seq_layer(P->seq[b], l, 1);
         }
-    /* the items in five groups, each launched with its own query-vector bound: the f16 caches', then the bf16
+    /* the items in six groups, each launched with its own query-vector bound: the f16 caches', then the bf16
      * caches'; in each, the row blocks of <= 4 query vectors (decode rows: the narrow kernel, two blocks per CU), then
      * the wider ones (prompt row blocks). A pass of both kinds of rows would otherwise run every decode row's items in
-     * the 16-vector kernel. Then the quantized caches' (k_attn_q) */
+     * the 16-vector kernel. Then the quantized caches' and the dot-product types' (k_attn_q) */
     Item *it = (Item *)(h + o_items);
-    int gcnt[5] = { 0, 0, 0, 0, 0 }, gnq[5] = { 1, 1, 1, 1, 1 };
-    for (int grp = 0, k = 0; grp < 5; grp++)
+    int gcnt[6] = { 0, 0, 0, 0, 0, 0 }, gnq[6] = { 1, 1, 1, 1, 1, 1 };
+    for (int grp = 0, k = 0; grp < 6; grp++)
         for (int b = 0; b < n;) {
             int e = b + 1;
             while (e < n && e - b < rb && P->seq[e] == P->seq[b] && P->pos[e] == P->pos[e - 1] + 1) e++;
             int nb = (P->pos[e - 1] + 1 + GW_ATT_P - 1) / GW_ATT_P, nq = (e - b) * kv_mul;
-            int kg = gw_kv_quant(kvt[b]) ? 4 : 2 * (kvt[b] == RQ_KV_BF16) + (nq > 4);
+            int kg = gw_kv_dot(kvt[b]) ? 5 : gw_kv_quant(kvt[b]) ? 4 : 2 * (kvt[b] == RQ_KV_BF16) + (nq > 4);
             if (kg == grp) {
                 for (int g = 0; g < nkv; g++)
                     for (int kb = 0; kb < nb; kb++) it[k++] = (Item){ b, e - b, g, kb };
@@ -703,11 +705,11 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
         KCHK(gw_k_qknorm_rope_store(c->qkv, c->ldqkv, n, nh, nkv, hd, y->q_norm, y->k_norm, m->rope, pos_d,
                                     kc_d + (size_t)l * n, vc_d + (size_t)l * n, nbf || nqz ? kvt_d : NULL, s));
         pf_mark(c, GW_PF_ATT);
-        for (int grp = 0, off = 0; grp < 5; off += gcnt[grp], grp++) {
+        for (int grp = 0, off = 0; grp < 6; off += gcnt[grp], grp++) {
             if (!gcnt[grp]) continue;
-            if (grp == 4)
+            if (grp >= 4)
                 KCHK(gw_k_attn_q((const Item *)items_d + off, gcnt[grp], c->qkv, c->ldqkv, nh, nkv, hd, m->att_scale, pos_d,
-                                 kc_d + (size_t)l * n, vc_d + (size_t)l * n, kvt_d, c->part, c->pstride, s));
+                                 kc_d + (size_t)l * n, vc_d + (size_t)l * n, kvt_d, grp == 5, c->part, c->pstride, s));
             else
                 KCHK(gw_k_attn_part((const Item *)items_d + off, gcnt[grp], gnq[grp], c->qkv, c->ldqkv, nh, nkv, hd,
                                     m->att_scale, pos_d, kc_d + (size_t)l * n, vc_d + (size_t)l * n, c->part, c->pstride,
@@ -731,8 +733,8 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
         }
         pf_mark(c, GW_PF_COMBINE);
         /* (rows of quantized caches: the combined o' into the free qkv buffer, then o = D H o' / hd quantized over theirs) */
-        KCHK(gw_k_attn_combine_quant(c->part, c->pstride, nh, hd, pos_d, n, nbmax, c->xq, c->xs, K, nqz ? c->qkv : NULL, s));
-        if (nqz) KCHK(gw_k_unrot_quant(c->qkv, n, nh, hd, kvt_d, c->xq, c->xs, K, s));
+        KCHK(gw_k_attn_combine_quant(c->part, c->pstride, nh, hd, pos_d, n, nbmax, c->xq, c->xs, K, nrot ? c->qkv : NULL, s));
+        if (nrot) KCHK(gw_k_unrot_quant(c->qkv, n, nh, hd, kvt_d, c->xq, c->xs, K, s));
         pf_mark(c, GW_PF_WO);
         if ((rc = run_mm(c, &y->wo, 1, c->xq, c->xs, K, n, c->xb, dim, 0)) != RQ_OK) return rc;
         pf_mark(c, GW_PF_NORM);

@@ -39,9 +39,18 @@ enum { GW_F32 = 0, GW_Q8_0 = 8, GW_Q2_K = 10, GW_Q3_K = 11, GW_Q4_K = 12, GW_Q5_
 
 /* KV cache types (runq.h:214): the rotated 8-bit / 4-bit ones, and the bytes of a tile (16 positions x hd of one kv
  * head) of K (is_v 0) or V: 16-bit 32 hd, q8 17 hd, q4 9 hd (RQ_KV_Q4: K q8, V q4; RQ_KV_Q4K4: both q4) */
-static inline int gw_kv_quant(int kvt) { return kvt == RQ_KV_Q8 || kvt == RQ_KV_Q4 || kvt == RQ_KV_Q4K4; }
+/* ... and their bf16 dot-product types (the KV_DOT bit 4: RQ_KV_BF16_DOT 5, F16_DOT 6, Q8_DOT 7, Q4_DOT 12, Q4K4_DOT 13),
+ * stored as their base type (the bf16-dot V in position pairs) */
+static inline int gw_kv_dot(int kvt) { return kvt == 5 || kvt == 6 || kvt == 7 || kvt == 12 || kvt == 13; }
+static inline int gw_kv_base(int kvt) { return gw_kv_dot(kvt) ? kvt & ~4 : kvt; }
+static inline int gw_kv_quant(int kvt) {
+    int b = gw_kv_base(kvt);
+    return b == RQ_KV_Q8 || b == RQ_KV_Q4 || b == RQ_KV_Q4K4;
+}
+/* a type the device keeps: f16, bf16, the quantized ones and the dot-product types (not f32) */
+static inline int gw_kv_ok(int kvt) { return kvt == RQ_KV_F16 || kvt == RQ_KV_BF16 || gw_kv_quant(kvt) || gw_kv_dot(kvt); }
 static inline size_t gw_kv_tile_bytes(int kvt, int hd, int is_v) {
-    int q4 = kvt == RQ_KV_Q4K4 || (kvt == RQ_KV_Q4 && is_v);
+    int b = gw_kv_base(kvt), q4 = b == RQ_KV_Q4K4 || (b == RQ_KV_Q4 && is_v);
     return (size_t)hd * (!gw_kv_quant(kvt) ? 32 : q4 ? 9 : 17);
 }
 
@@ -252,10 +261,10 @@ int gw_k_rmsnorm_quant(float *x, const float *d, int dim, const float *w, const 
 int gw_k_qknorm_rope_store(float *qkv, int ldqkv, int n, int nh, int nkv, int hd, const float *qn, const float *kn,
                            const float *rope, const int *pos, uint16_t *const *kc, uint16_t *const *vc,
                            const int *kvt, hipStream_t s); /* kvt: per row, its cache type (runq.h:214; NULL: all f16) */
-/* the attention partials of items on the quantized caches (RQ_KV_Q8 / Q4 / Q4K4; kvt: each row's type; hd a power of two,
- * 32 .. 128) */
+/* the attention partials of items on the quantized caches (RQ_KV_Q8 / Q4 / Q4K4; dot 0) or on the dot-product types (dot
+ * 1: every item's row one of them); kvt: each row's type; hd a power of two, 32 .. 128 */
 int gw_k_attn_q(const void *items, int nitems, const float *qkv, int ldqkv, int nh, int nkv, int hd, float scale, const int *pos,
-                uint16_t *const *kc, uint16_t *const *vc, const int *kvt, float *part, int pstride, hipStream_t s);
+                uint16_t *const *kc, uint16_t *const *vc, const int *kvt, int dot, float *part, int pstride, hipStream_t s);
 /* the rows of quantized caches: o = D H o' / hd from the combined attention att (n rows of nh hd), quantized into aq / as */
 int gw_k_unrot_quant(const float *att, int n, int nh, int hd, const int *kvt, int8_t *aq, float *as, int ldq, hipStream_t s);
 int gw_k_attn_part(const void *items, int nitems, int nq_max, const float *qkv, int ldqkv, int nh, int nkv, int hd, float scale,

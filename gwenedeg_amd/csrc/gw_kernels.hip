@@ -131,8 +131,16 @@ __global__ __launch_bounds__(NORM_T) void k_rmsnorm_quant(float *__restrict__ x,
 //   K q8 [i][j] int8, the bf16 scales at 16 hd: [c][j];  K q4: byte [p][j] = (n_2p + 8) | (n_2p+1 + 8) << 4, scales at
 //   8 hd; V q8 [j][i] int8, scales at 16 hd: [j][c];  V q4: byte [j][c][l] = (n_32c+l + 8) | (n_32c+16+l + 8) << 4,
 //   scales at 8 hd: [j][c]
-__device__ __forceinline__ bool kvq_type(int kvt) { return kvt == 3 || kvt == 8 || kvt == 9; }
-__device__ __forceinline__ bool kvq_q4(int kvt, bool is_v) { return kvt == 9 || (kvt == 8 && is_v); } // (the half's format)
+// The dot-product types (runq.h:214, KV_DOT 4: 5 bf16-dot, 6 f16-dot, 7 q8-dot, 12 q4-dot, 13 q4k4-dot) keep their base
+// type's cache (kv_base), but for the bf16-dot V: position pairs, dim i of positions 2m, 2m + 1 of a tile at 2m hd + 2i
+// (+ 1) (forward.c:1916-1924)
+__device__ __forceinline__ bool kv_dot(int kvt) { return kvt == 5 || kvt == 6 || kvt == 7 || kvt == 12 || kvt == 13; }
+__device__ __forceinline__ int kv_base(int kvt) { return kv_dot(kvt) ? kvt & ~4 : kvt; }
+__device__ __forceinline__ bool kvq_type(int kvt) { const int b = kv_base(kvt); return b == 3 || b == 8 || b == 9; }
+__device__ __forceinline__ bool kvq_q4(int kvt, bool is_v) { // (the half's format)
+    const int b = kv_base(kvt);
+    return b == 9 || (b == 8 && is_v);
+}
 __device__ __forceinline__ int kvq_tile_bytes(bool q4, int hd) { return hd * (q4 ? 9 : 17); }
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
@@ -216,7 +224,7 @@ __global__ __launch_bounds__(64) void k_qknorm_rope_store(float *__restrict__ qk
     __shared__ uint32_t scw[8];
     int b = blockIdx.x, h = blockIdx.y, lane = threadIdx.x, p = pos[b];
     const int kt = kvt ? kvt[b] : 2;
-    const bool bf = kt == 1, qz = kvq_type(kt); // (row b's sequence has a bf16 / a quantized cache)
+    const bool bf = kv_base(kt) == 1, qz = kvq_type(kt); // (row b's sequence has a bf16 / a quantized cache)
     float *row = qkv + (size_t)b * ldqkv;
     int half = hd / 2;
     if (qz && h >= nh + nkv) { // value head: rotated and quantized
@@ -231,9 +239,12 @@ __global__ __launch_bounds__(64) void k_qknorm_rope_store(float *__restrict__ qk
     if (h >= nh + nkv) { // value head: store
         int g = h - nh - nkv;
         const float *src = row + (size_t)(nh + nkv) * hd + g * hd;
-        uint16_t *dst = vc[b] + (((size_t)(p / ATT_P) * nkv + g) * ATT_P + (size_t)(p % ATT_P / ATT_T) * ATT_T) * hd +
-                        (size_t)(p % ATT_T) * hd;
-        for (int i = lane; i < hd; i += 64) dst[kv_v_col(bf, i)] = bf ? f2bf_ref(src[i]) : f2h_ref(src[i]);
+        uint16_t *dst = vc[b] + (((size_t)(p / ATT_P) * nkv + g) * ATT_P + (size_t)(p % ATT_P / ATT_T) * ATT_T) * hd;
+        const int j = p % ATT_T;
+        if (kt == 5) // (bf16-dot: position pairs)
+            for (int i = lane; i < hd; i += 64) dst[(size_t)(j & ~1) * hd + 2 * i + (j & 1)] = f2bf_ref(src[i]);
+        else
+            for (int i = lane; i < hd; i += 64) dst[(size_t)j * hd + kv_v_col(bf, i)] = bf ? f2bf_ref(src[i]) : f2h_ref(src[i]);
         return;
     }
     float *src = row + (size_t)h * hd;
@@ -320,31 +331,67 @@ __global__ __launch_bounds__(64) void k_unrot_quant(const float *__restrict__ at
 // (a = c0 + c1 + c2 + c3, times scale), m the max, e = exp_att(s - m), l the 16 chains over positions j % 16 and the tree,
 // o the fma chain over the positions. part[(row nh + h) pstride + kb (hd + 2)] = o, m, l. The block's K tiles are staged
 // into LDS, then its V tiles over them. hd <= 128 (a power of two), nq <= 16.
+// DOT: the dot-product types (every row of the launch one), attention_vec_dot (forward.c:1488-1549, kernels_avx512.h:
+// 1439-1475): q, the values (16-bit caches: bf16 as stored, f16 rounded to bf16; quantized: n d rounded to bf16) and the
+// weights rounded to bf16; each product pair as vdpbf16ps's lane, two fmas with the odd element first (scores: dim
+// pairs; o: position pairs, a last odd position paired with +0, +0); the call's FTZ / DAZ mode as fma_ftz / ftz_f
 #define AQ_T 512
+__device__ __forceinline__ float ftz_f(float x) { return fabsf(x) < 1.17549435e-38f ? __builtin_copysignf(0.0f, x) : x; }
+__device__ __forceinline__ float fma_ftz(float a, float b, float c) { return ftz_f(__builtin_fmaf(ftz_f(a), ftz_f(b), ftz_f(c))); }
+__device__ __forceinline__ float bf16_round(float x) { return bf16_to_f32(f2bf_ref(ftz_f(x))); } // (vcvtneps2bf16)
+
+template <bool DOT>
 __global__ __launch_bounds__(AQ_T) void k_attn_q(const int4 *__restrict__ items, const float *__restrict__ qkv, int ldqkv,
                                                  int nh, int nkv, int hd, float scale, const int *__restrict__ pos,
                                                  uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc,
                                                  const int *__restrict__ kvt, float *__restrict__ part, int pstride) {
-    __shared__ __align__(16) uint8_t tl[ATT_T * 17 * 128]; // the block's 16 tiles of K, then of V
+    __shared__ __align__(16) uint8_t tl[ATT_T * (DOT ? 32 : 17) * 128]; // the block's 16 tiles of K, then of V
     __shared__ float qs[16 * 128];
     __shared__ float S[16][ATT_P];
     __shared__ float ms[16], ls[16];
     const int4 it = items[blockIdx.x];
     const int r0 = it.x, nr = it.y, g = it.z, kb = it.w, kv_mul = nh / nkv, nq = nr * kv_mul, t = threadIdx.x;
-    const int kt = kvt[r0], ng = hd >> 5;
+    const int kt = kvt[r0], base = kv_base(kt), ng = hd >> 5;
+    const bool b16 = DOT && (base == 1 || base == 2); // (a 16-bit dot cache: bf16-dot, f16-dot)
     const bool k4 = kvq_q4(kt, false), v4 = kvq_q4(kt, true);
-    const int tbk = kvq_tile_bytes(k4, hd), tbv = kvq_tile_bytes(v4, hd);
+    const int tbk = b16 ? 32 * hd : kvq_tile_bytes(k4, hd), tbv = b16 ? 32 * hd : kvq_tile_bytes(v4, hd);
     auto npos = [&](int v) -> int { // positions of block kb vector v reaches (<= 0: none)
         const int n = pos[r0 + v / kv_mul] + 1 - kb * ATT_P;
         return n < ATT_P ? n : ATT_P;
     };
+    auto tile_src = [&](uint16_t *const *c, bool q4, int tb) -> const uint4 * { // (the block's first tile, head g)
+        if (!b16) return (const uint4 *)kvq_tile(c[r0], kb * ATT_P, g, nkv, hd, q4);
+        return (const uint4 *)((const uint8_t *)c[r0] + ((size_t)kb * nkv + g) * (ATT_P / ATT_T) * (size_t)tb);
+    };
+    // the value of dim i, position j of a staged K (is_v false) or V tile tb, as the products read it
+    auto value = [&](const uint8_t *tb, int i, int j, bool is_v) -> float {
+        if (b16) {
+            const uint16_t *u = (const uint16_t *)tb;
+            if (base == 1) return bf16_to_f32(u[is_v ? (j & ~1) * hd + 2 * i + (j & 1) : kv_k_at(true, i, j)]);
+            return bf16_round(h2f(u[is_v ? j * hd + i : kv_k_at(false, i, j)]));
+        }
+        const bool q4 = is_v ? v4 : k4;
+        const int c = i >> 5;
+        float d;
+        int n;
+        if (!is_v) {
+            d = bf16_to_f32(((const uint16_t *)(tb + (size_t)(q4 ? 8 : 16) * hd))[c * ATT_T + j]);
+            n = q4 ? ((tb[(i >> 1) * ATT_T + j] >> (4 * (i & 1))) & 15) - 8 : (int)(int8_t)tb[i * ATT_T + j];
+        } else {
+            d = bf16_to_f32(((const uint16_t *)(tb + (size_t)(q4 ? 8 : 16) * hd))[j * ng + c]);
+            n = q4 ? ((tb[(size_t)j * (hd / 2) + 16 * c + (i & 15)] >> (4 * ((i >> 4) & 1))) & 15) - 8
+                   : (int)(int8_t)tb[(size_t)j * hd + i];
+        }
+        return DOT ? bf16_round((float)n * d) : (float)n * d;
+    };
     // 1. the K tiles (the block's 16 tiles of head g are consecutive) and the query vectors
     {
-        const uint4 *src = (const uint4 *)kvq_tile(kc[r0], kb * ATT_P, g, nkv, hd, k4);
+        const uint4 *src = tile_src(kc, k4, tbk);
         for (int i = t; i < ATT_T * tbk / 16; i += AQ_T) ((uint4 *)tl)[i] = src[i];
         for (int i = t; i < nq * hd; i += AQ_T) {
             const int v = i / hd, d = i % hd;
-            qs[i] = qkv[(size_t)(r0 + v / kv_mul) * ldqkv + (size_t)(g * kv_mul + v % kv_mul) * hd + d];
+            const float q = qkv[(size_t)(r0 + v / kv_mul) * ldqkv + (size_t)(g * kv_mul + v % kv_mul) * hd + d];
+            qs[i] = DOT ? bf16_round(q) : q;
         }
     }
     __syncthreads();
@@ -353,24 +400,27 @@ __global__ __launch_bounds__(AQ_T) void k_attn_q(const int4 *__restrict__ items,
         const int v = k / ATT_P, p = k % ATT_P;
         if (p >= npos(v)) continue;
         const uint8_t *tb = tl + (size_t)(p / ATT_T) * tbk;
-        const uint16_t *sc = (const uint16_t *)(tb + (size_t)(k4 ? 8 : 16) * hd);
         const int j = p % ATT_T;
         const float *q = qs + v * hd;
         float a = 0.0f;
         for (int c = 0; c < ng; c++) {
-            const float d = bf16_to_f32(sc[c * ATT_T + j]);
             float cc = 0.0f;
-            for (int i = 32 * c; i < 32 * c + 32; i++) {
-                const int n = k4 ? ((tb[(i >> 1) * ATT_T + j] >> (4 * (i & 1))) & 15) - 8 : (int)(int8_t)tb[i * ATT_T + j];
-                cc = __builtin_fmaf(q[i], (float)n * d, cc);
+            if (DOT) {
+                for (int i = 32 * c; i < 32 * c + 32; i += 2) {
+                    cc = fma_ftz(q[i + 1], value(tb, i + 1, j, false), cc);
+                    cc = fma_ftz(q[i], value(tb, i, j, false), cc);
+                }
+                a = c ? ftz_f(a + cc) : cc;
+            } else {
+                for (int i = 32 * c; i < 32 * c + 32; i++) cc = __builtin_fmaf(q[i], value(tb, i, j, false), cc);
+                a = c ? a + cc : cc;
             }
-            a = c ? a + cc : cc;
         }
-        S[v][p] = a * scale;
+        S[v][p] = DOT ? ftz_f(a * scale) : a * scale;
     }
     __syncthreads();
-    // 3. softmax: wave w takes vectors w, w + 8: m, the exponentials, l (lane j < 16: the chain over positions j, j + 16,
-    // ...; then the tree)
+    // 3. softmax: wave w takes vectors w, w + 8: m, the exponentials (DOT: rounded to bf16), l (lane j < 16: the chain
+    // over positions j, j + 16, ...; then the tree)
     {
         const int wave = t >> 6, lane = t & 63;
         for (int v = wave; v < nq; v += AQ_T / 64) {
@@ -382,7 +432,10 @@ __global__ __launch_bounds__(AQ_T) void k_attn_q(const int4 *__restrict__ items,
                 const float u = __shfl_xor(m, o);
                 m = u > m ? u : m;
             }
-            for (int p = lane; p < n; p += 64) S[v][p] = exp_att(S[v][p] - m);
+            for (int p = lane; p < n; p += 64) {
+                const float e = exp_att(S[v][p] - m);
+                S[v][p] = DOT ? bf16_round(e) : e;
+            }
             __builtin_amdgcn_wave_barrier();
             float sm = 0.0f;
             if (lane < 16)
@@ -400,22 +453,25 @@ __global__ __launch_bounds__(AQ_T) void k_attn_q(const int4 *__restrict__ items,
     __syncthreads();
     // 4. the V tiles over the K tiles
     {
-        const uint4 *src = (const uint4 *)kvq_tile(vc[r0], kb * ATT_P, g, nkv, hd, v4);
+        const uint4 *src = tile_src(vc, v4, tbv);
         for (int i = t; i < ATT_T * tbv / 16; i += AQ_T) ((uint4 *)tl)[i] = src[i];
     }
     __syncthreads();
-    // 5. o, thread per (vector, dim): the fma chain over the positions in order
+    // 5. o, thread per (vector, dim): the fma chain over the positions in order (DOT: over position pairs)
     for (int k = t; k < nq * hd; k += AQ_T) {
-        const int v = k / hd, i = k % hd, n = npos(v), c = i >> 5;
+        const int v = k / hd, i = k % hd, n = npos(v);
         if (n <= 0) continue;
         float o = 0.0f;
-        for (int p = 0; p < n; p++) {
-            const uint8_t *tb = tl + (size_t)(p / ATT_T) * tbv;
-            const int j = p % ATT_T;
-            const float d = bf16_to_f32(((const uint16_t *)(tb + (size_t)(v4 ? 8 : 16) * hd))[j * ng + c]);
-            const int nn = v4 ? ((tb[(size_t)j * (hd / 2) + 16 * c + (i & 15)] >> (4 * ((i >> 4) & 1))) & 15) - 8
-                              : (int)(int8_t)tb[(size_t)j * hd + i];
-            o = __builtin_fmaf(S[v][p], (float)nn * d, o);
+        if (DOT) {
+            for (int p = 0; p < n; p += 2) { // (p even: p and p + 1 share a tile)
+                const uint8_t *tb = tl + (size_t)(p / ATT_T) * tbv;
+                const int j = p % ATT_T;
+                const float w1 = p + 1 < n ? S[v][p + 1] : 0.0f, v1 = p + 1 < n ? value(tb, i, j + 1, true) : 0.0f;
+                o = fma_ftz(S[v][p], value(tb, i, j, true), fma_ftz(w1, v1, o));
+            }
+        } else {
+            for (int p = 0; p < n; p++)
+                o = __builtin_fmaf(S[v][p], value(tl + (size_t)(p / ATT_T) * tbv, i, p % ATT_T, true), o);
         }
         float *dst = part + ((size_t)(r0 + v / kv_mul) * nh + g * kv_mul + v % kv_mul) * pstride + (size_t)kb * (hd + 2);
         dst[i] = o;
@@ -1401,11 +1457,15 @@ int gw_k_qknorm_rope_store(float *qkv, int ldqkv, int n, int nh, int nkv, int hd
 }
 
 int gw_k_attn_q(const void *items, int nitems, const float *qkv, int ldqkv, int nh, int nkv, int hd, float scale, const int *pos,
-                uint16_t *const *kc, uint16_t *const *vc, const int *kvt, float *part, int pstride, hipStream_t s) {
+                uint16_t *const *kc, uint16_t *const *vc, const int *kvt, int dot, float *part, int pstride, hipStream_t s) {
     // (hd a power of two, 32 .. 128; at most 16 query vectors per item)
     if (hd < 32 || hd > 128 || (hd & (hd - 1))) return (int)hipErrorInvalidValue;
-    GW_LAUNCH(k_attn_q, dim3(nitems), dim3(AQ_T), 0, s, (const int4 *)items, qkv, ldqkv, nh, nkv, hd, scale, pos, kc, vc, kvt,
-              part, pstride);
+    if (dot)
+        GW_LAUNCH(k_attn_q<true>, dim3(nitems), dim3(AQ_T), 0, s, (const int4 *)items, qkv, ldqkv, nh, nkv, hd, scale, pos, kc,
+                  vc, kvt, part, pstride);
+    else
+        GW_LAUNCH(k_attn_q<false>, dim3(nitems), dim3(AQ_T), 0, s, (const int4 *)items, qkv, ldqkv, nh, nkv, hd, scale, pos, kc,
+                  vc, kvt, part, pstride);
     return (int)hipGetLastError();
 }
 

@@ -50,7 +50,7 @@ static uint64_t sf_hash(const SfHdr *h, const int *tokens) {
 static uint64_t sf_blk(const RqModel *m, int kvt, int kv) {
     return (uint64_t)(GW_ATT_P / GW_ATT_T) * m->n_kv_heads * gw_kv_tile_bytes(kvt, m->head_dim, kv);
 }
-static int sf_type_ok(int kvt) { return kvt == RQ_KV_F16 || kvt == RQ_KV_BF16 || gw_kv_quant(kvt); }
+static int sf_type_ok(int kvt) { return gw_kv_ok(kvt); }
 
 static void sf_shape(const RqModel *m, int len, int kvt, SfHdr *h) {
     /* every field but rng and hash, as the reference writes them for this model, length and cache type */

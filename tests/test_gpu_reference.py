@@ -201,14 +201,16 @@ def test_hidden_rows_after_batched_passes_on_one_context(gw, orc, tmp_path):
     assert np.array_equal(_bits(lg), _bits(rlg[21:62])), "fw_rows n 41, max_batch 8: logits rows"
 
 
-@pytest.mark.parametrize("kvt", [2, 1, 3, 8, 9])  # RQ_KV_F16, RQ_KV_BF16, RQ_KV_Q8, RQ_KV_Q4, RQ_KV_Q4K4
+# RQ_KV_F16, RQ_KV_BF16, RQ_KV_Q8, RQ_KV_Q4, RQ_KV_Q4K4, and the dot-product types RQ_KV_BF16_DOT, F16_DOT, Q8_DOT, Q4_DOT,
+# Q4K4_DOT
+@pytest.mark.parametrize("kvt", [2, 1, 3, 8, 9, 5, 6, 7, 12, 13])
 def test_seqfile_with_reference(gw, orc, tmp_path, kvt):
     """the KV disk tier (runq.h:283-314) against the reference's seqfile.c: the same model fingerprint; the reference's
     saved sequence (300-token prompt + 4 greedy steps) read by rq_seq_file_info and loaded by rq_seq_load continues bit
     for bit as the device's own sequence of the same tokens; the device's saved file matches the reference's header
     and tokens (all but the RNG word and the hash over it) and its whole K / V blocks byte for byte, and loads back;
     with each cache type the device keeps (a file loads only into a sequence of its cache type; the quantized caches'
-    blocks hold the rotated, quantized rows, so their bytes pin the store)"""
+    blocks hold the rotated, quantized rows, and the bf16-dot V its position pairs, so their bytes pin the store)"""
     import ctypes
     path, d = _synth(str(tmp_path), "qwen3_0_6b", n_layers=2)
     m = gw.Model(path, ctx_len=1024)
@@ -251,7 +253,8 @@ def test_seqfile_with_reference(gw, orc, tmp_path, kvt):
     assert np.array_equal(r[:264][hdr], o[:264][hdr])
     assert np.array_equal(r[4096:4096 + 4 * L], o[4096:4096 + 4 * L])
     hd = m.info.head_dim
-    tile = {2: (32, 32), 1: (32, 32), 3: (17, 17), 8: (17, 9), 9: (9, 9)}[kvt]  # (K, V tile bytes per dim)
+    tile = {2: (32, 32), 1: (32, 32), 3: (17, 17), 8: (17, 9), 9: (9, 9)}[kvt & ~4 if kvt in (5, 6, 7, 12, 13) else kvt]
+    # (K, V tile bytes per dim: a dot-product type's are its base type's)
     off_kv = int(np.frombuffer(r[224:232].tobytes(), np.uint64)[0])
     bk, bv = (16 * m.info.n_kv_heads * hd * t for t in tile)
     nblk = (L + 255) // 256
@@ -276,12 +279,14 @@ def test_seqfile_with_reference(gw, orc, tmp_path, kvt):
     assert lib.rq_seq_load(ctypes.c_void_p(m.seq(1024, kv_type=other)._h), p2.encode(), 10) == -7
 
 
-@pytest.mark.parametrize("kvt", [3, 8, 9])  # RQ_KV_Q8, RQ_KV_Q4, RQ_KV_Q4K4
+# RQ_KV_Q8, RQ_KV_Q4, RQ_KV_Q4K4; the dot-product types RQ_KV_BF16_DOT, F16_DOT, Q8_DOT, Q4_DOT, Q4K4_DOT
+@pytest.mark.parametrize("kvt", [3, 8, 9, 5, 6, 7, 12, 13])
 def test_quantized_kv_greedy_bit_identical(gw, orc, tmp_path, kvt):
-    """the rotated 8-bit / 4-bit KV caches (forward.c:1609-1790) on a Qwen3-0.6B-shaped model (2 layers): a 300-token
-    prefill (two key blocks, 16-vector row blocks) and 24 greedy steps, every logits row equal bit for bit to the
-    reference's own cache of that type, the same tokens; then a pass of that sequence's next token beside a fresh
-    sequence's prompt (both of the type) equal to each run alone"""
+    """the rotated 8-bit / 4-bit KV caches (forward.c:1609-1790) and the bf16 dot-product attention types
+    (forward.c:1452-1606: bf16 q, K, V and weights, vdpbf16ps's pairs, FTZ / DAZ) on a Qwen3-0.6B-shaped model (2
+    layers): a 300-token prefill (two key blocks, 16-vector row blocks) and 24 greedy steps, every logits row equal bit
+    for bit to the reference's own cache of that type, the same tokens; then a pass of that sequence's next token beside
+    a fresh sequence's prompt (both of the type) equal to each run alone"""
     path, d = _synth(str(tmp_path), "qwen3_0_6b", seed=4, n_layers=2)
     m = gw.Model(path, ctx_len=512)
     if not _exact(gw):
