@@ -30,7 +30,7 @@ SYNTH_PATH = os.path.join(LIB_DIR, "libgwsynth.so")
 
 RQ_OK, RQ_ERR_ARG, RQ_ERR_NOMEM, RQ_ERR_CONTEXT, RQ_ERR_STATE, RQ_ERR_LOAD, RQ_ERR_IO, RQ_ERR_MISMATCH = 0, -1, -2, -3, -4, -5, -6, -7
 RQ_LOGITS_NONE, RQ_LOGITS_LAST, RQ_LOGITS_ALL = 0, 1, 2
-RQ_KV_F32, RQ_KV_BF16, RQ_KV_F16, RQ_KV_Q8, RQ_KV_Q4, RQ_KV_Q4K4 = 0, 1, 2, 3, 8, 9  # runq.h:214 (the device takes all but f32)
+RQ_KV_F32, RQ_KV_BF16, RQ_KV_F16, RQ_KV_Q8, RQ_KV_Q4, RQ_KV_Q4K4 = 0, 1, 2, 3, 8, 9  # runq.h:214
 # the bf16 dot-product attention types (runq.h:214, KV_DOT 4)
 RQ_KV_BF16_DOT, RQ_KV_F16_DOT, RQ_KV_Q8_DOT, RQ_KV_Q4_DOT, RQ_KV_Q4K4_DOT = 5, 6, 7, 12, 13
 RQ_BATCH_MAX = 512

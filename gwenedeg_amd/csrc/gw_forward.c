@@ -56,10 +56,10 @@ RqSeq *rq_seq_new(const RqModel *m, int capacity, int kv_type, int *err) {
     RqSeq *s = NULL;
     if (!m) { e = RQ_ERR_STATE; goto fail; }
     if (capacity <= 0) capacity = m->seq_len;
-    /* f16 and bf16 caches (the fp32 attention on the exactly converted values, runq.h:204-213), and the rotated q8 / q4
-     * ones and the dot-product types (head_dim a power of two, 32 .. 128); f32 RQ_ERR_ARG */
+    /* f16 and bf16 caches (the fp32 attention on the exactly converted values, runq.h:204-213); f32, the rotated q8 / q4
+     * ones and the dot-product types with head_dim a power of two, 32 .. 128 */
     int hd = m->head_dim, qok = hd >= 32 && hd <= 128 && !(hd & (hd - 1));
-    if (capacity > m->seq_len || !gw_kv_ok(kv_type) || ((gw_kv_quant(kv_type) || gw_kv_dot(kv_type)) && !qok)) {
+    if (capacity > m->seq_len || !gw_kv_ok(kv_type) || (gw_kv_att_q(kv_type) && !qok)) {
         e = RQ_ERR_ARG;
         goto fail;
     }
@@ -197,9 +197,10 @@ int rq_seq_fill_synthetic(RqSeq *s, int n, unsigned long long seed) {
     size_t nb = ((size_t)n + GW_ATT_P - 1) / GW_ATT_P, per = nb * GW_ATT_P * s->m->n_kv_heads * s->m->head_dim;
     for (int l = 0; l < s->m->n_layers; l++) {
         unsigned long long sl = seed + (unsigned long long)l * 0x1000193ull;
-        int e = gw_kv_quant(s->kvt) ? gw_k_fill_synthetic_q(seq_layer(s, l, 0), seq_layer(s, l, 1), s->kvt, (int)(nb * GW_ATT_P),
-                                                             s->m->n_kv_heads, s->m->head_dim, sl, 0)
-                                    : gw_k_fill_synthetic(seq_layer(s, l, 0), seq_layer(s, l, 1), per, sl, 0);
+        int e = gw_kv_quant(s->kvt) || s->kvt == RQ_KV_F32
+                    ? gw_k_fill_synthetic_q(seq_layer(s, l, 0), seq_layer(s, l, 1), s->kvt, (int)(nb * GW_ATT_P),
+                                            s->m->n_kv_heads, s->m->head_dim, sl, 0)
+                    : gw_k_fill_synthetic(seq_layer(s, l, 0), seq_layer(s, l, 1), per, sl, 0);
         if (e) return RQ_ERR_STATE;
     }
     if (hipDeviceSynchronize() != hipSuccess) return RQ_ERR_STATE;
@@ -308,7 +309,7 @@ int rq_seq_mem(const RqModel *m, int capacity, int kv_type, RqSeqMem *mem) {
     if (!m) return RQ_ERR_STATE;
     if (capacity <= 0) capacity = m->seq_len;
     int hd = m->head_dim, qok = hd >= 32 && hd <= 128 && !(hd & (hd - 1));
-    if (capacity > m->seq_len || !gw_kv_ok(kv_type) || ((gw_kv_quant(kv_type) || gw_kv_dot(kv_type)) && !qok))
+    if (capacity > m->seq_len || !gw_kv_ok(kv_type) || (gw_kv_att_q(kv_type) && !qok))
         return RQ_ERR_ARG;
     size_t kv_len = ((size_t)capacity + GW_ATT_P - 1) / GW_ATT_P * GW_ATT_P;
     mem->kv = (size_t)m->n_layers * kv_len / GW_ATT_T * m->n_kv_heads *
@@ -636,12 +637,13 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
     memcpy(h + o_tok, P->tok, (size_t)n * 4);
     memcpy(h + o_pos, P->pos, (size_t)n * 4);
     memcpy(h + o_sel, P->sel, (size_t)n * 4);
-    /* (each row's cache type; rows of bf16 caches, rows of quantized or dot-product ones (k_attn_q), rows to unrotate) */
+    /* (each row's cache type; rows of bf16 caches, rows of f32, quantized or dot-product ones (k_attn_q), rows to
+     * unrotate) */
     int *kvt = (int *)(h + o_kbf), nbf = 0, nqz = 0, nrot = 0;
     for (int b = 0; b < n; b++) {
         kvt[b] = P->seq[b]->kvt;
         nbf += kvt[b] == RQ_KV_BF16;
-        nqz += gw_kv_quant(kvt[b]) || gw_kv_dot(kvt[b]);
+        nqz += gw_kv_att_q(kvt[b]);
         nrot += gw_kv_quant(kvt[b]);
     }
     uint16_t **ptr = (uint16_t **)(h + o_ptr);
@@ -653,7 +655,7 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
     /* the items in six groups, each launched with its own query-vector bound: the f16 caches', then the bf16
      * caches'; in each, the row blocks of <= 4 query vectors (decode rows: the narrow kernel, two blocks per CU), then
      * the wider ones (prompt row blocks). A pass of both kinds of rows would otherwise run every decode row's items in
-     * the 16-vector kernel. Then the quantized caches' and the dot-product types' (k_attn_q) */
+     * the 16-vector kernel. Then the f32 and quantized caches', and the dot-product types' (k_attn_q) */
     Item *it = (Item *)(h + o_items);
     int gcnt[6] = { 0, 0, 0, 0, 0, 0 }, gnq[6] = { 1, 1, 1, 1, 1, 1 };
     for (int grp = 0, k = 0; grp < 6; grp++)
@@ -661,7 +663,7 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
             int e = b + 1;
             while (e < n && e - b < rb && P->seq[e] == P->seq[b] && P->pos[e] == P->pos[e - 1] + 1) e++;
             int nb = (P->pos[e - 1] + 1 + GW_ATT_P - 1) / GW_ATT_P, nq = (e - b) * kv_mul;
-            int kg = gw_kv_dot(kvt[b]) ? 5 : gw_kv_quant(kvt[b]) ? 4 : 2 * (kvt[b] == RQ_KV_BF16) + (nq > 4);
+            int kg = gw_kv_dot(kvt[b]) ? 5 : gw_kv_att_q(kvt[b]) ? 4 : 2 * (kvt[b] == RQ_KV_BF16) + (nq > 4);
             if (kg == grp) {
                 for (int g = 0; g < nkv; g++)
                     for (int kb = 0; kb < nb; kb++) it[k++] = (Item){ b, e - b, g, kb };

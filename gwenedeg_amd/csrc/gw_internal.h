@@ -38,7 +38,7 @@ enum { GW_F32 = 0, GW_Q8_0 = 8, GW_Q2_K = 10, GW_Q3_K = 11, GW_Q4_K = 12, GW_Q5_
 #define GW_IS_KQ(t) (((t) >= GW_Q2_K && (t) <= GW_Q6_K) || (t) == GW_IQ4_XS)
 
 /* KV cache types (runq.h:214): the rotated 8-bit / 4-bit ones, and the bytes of a tile (16 positions x hd of one kv
- * head) of K (is_v 0) or V: 16-bit 32 hd, q8 17 hd, q4 9 hd (RQ_KV_Q4: K q8, V q4; RQ_KV_Q4K4: both q4) */
+ * head) of K (is_v 0) or V: f32 64 hd, 16-bit 32 hd, q8 17 hd, q4 9 hd (RQ_KV_Q4: K q8, V q4; RQ_KV_Q4K4: both q4) */
 /* ... and their bf16 dot-product types (the KV_DOT bit 4: RQ_KV_BF16_DOT 5, F16_DOT 6, Q8_DOT 7, Q4_DOT 12, Q4K4_DOT 13),
  * stored as their base type (the bf16-dot V in position pairs) */
 static inline int gw_kv_dot(int kvt) { return kvt == 5 || kvt == 6 || kvt == 7 || kvt == 12 || kvt == 13; }
@@ -47,11 +47,16 @@ static inline int gw_kv_quant(int kvt) {
     int b = gw_kv_base(kvt);
     return b == RQ_KV_Q8 || b == RQ_KV_Q4 || b == RQ_KV_Q4K4;
 }
-/* a type the device keeps: f16, bf16, the quantized ones and the dot-product types (not f32) */
-static inline int gw_kv_ok(int kvt) { return kvt == RQ_KV_F16 || kvt == RQ_KV_BF16 || gw_kv_quant(kvt) || gw_kv_dot(kvt); }
+/* a type the device keeps: every type of runq.h:214 (f32, f16, bf16, the quantized ones, the dot-product types) */
+static inline int gw_kv_ok(int kvt) {
+    return kvt == RQ_KV_F32 || kvt == RQ_KV_F16 || kvt == RQ_KV_BF16 || gw_kv_quant(kvt) || gw_kv_dot(kvt);
+}
+/* the types whose attention runs in k_attn_q (the f16 / bf16 caches have their own kernels), which need a power-of-two
+ * head_dim of 32 .. 128 */
+static inline int gw_kv_att_q(int kvt) { return kvt == RQ_KV_F32 || gw_kv_quant(kvt) || gw_kv_dot(kvt); }
 static inline size_t gw_kv_tile_bytes(int kvt, int hd, int is_v) {
     int b = gw_kv_base(kvt), q4 = b == RQ_KV_Q4K4 || (b == RQ_KV_Q4 && is_v);
-    return (size_t)hd * (!gw_kv_quant(kvt) ? 32 : q4 ? 9 : 17);
+    return (size_t)hd * (kvt == RQ_KV_F32 ? 64 : !gw_kv_quant(kvt) ? 32 : q4 ? 9 : 17);
 }
 
 /* a K-quant super-block's bytes in the file and on the device (0: not a K-quant) */

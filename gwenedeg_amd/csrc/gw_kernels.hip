@@ -224,7 +224,7 @@ __global__ __launch_bounds__(64) void k_qknorm_rope_store(float *__restrict__ qk
     __shared__ uint32_t scw[8];
     int b = blockIdx.x, h = blockIdx.y, lane = threadIdx.x, p = pos[b];
     const int kt = kvt ? kvt[b] : 2;
-    const bool bf = kv_base(kt) == 1, qz = kvq_type(kt); // (row b's sequence has a bf16 / a quantized cache)
+    const bool bf = kv_base(kt) == 1, qz = kvq_type(kt), f32 = kt == 0; // (row b's cache: bf16 / quantized / f32)
     float *row = qkv + (size_t)b * ldqkv;
     int half = hd / 2;
     if (qz && h >= nh + nkv) { // value head: rotated and quantized
@@ -239,9 +239,12 @@ __global__ __launch_bounds__(64) void k_qknorm_rope_store(float *__restrict__ qk
     if (h >= nh + nkv) { // value head: store
         int g = h - nh - nkv;
         const float *src = row + (size_t)(nh + nkv) * hd + g * hd;
-        uint16_t *dst = vc[b] + (((size_t)(p / ATT_P) * nkv + g) * ATT_P + (size_t)(p % ATT_P / ATT_T) * ATT_T) * hd;
+        const size_t o = (((size_t)(p / ATT_P) * nkv + g) * ATT_P + (size_t)(p % ATT_P / ATT_T) * ATT_T) * hd;
+        uint16_t *dst = vc[b] + o;
         const int j = p % ATT_T;
-        if (kt == 5) // (bf16-dot: position pairs)
+        if (f32) // (V [j][i] floats)
+            for (int i = lane; i < hd; i += 64) ((float *)vc[b])[o + (size_t)j * hd + i] = src[i];
+        else if (kt == 5) // (bf16-dot: position pairs)
             for (int i = lane; i < hd; i += 64) dst[(size_t)(j & ~1) * hd + 2 * i + (j & 1)] = f2bf_ref(src[i]);
         else
             for (int i = lane; i < hd; i += 64) dst[(size_t)j * hd + kv_v_col(bf, i)] = bf ? f2bf_ref(src[i]) : f2h_ref(src[i]);
@@ -266,9 +269,15 @@ __global__ __launch_bounds__(64) void k_qknorm_rope_store(float *__restrict__ qk
             src[i + half] = yo;
         } else {
             int g = h - nh;
-            uint16_t *dst = kc[b] + (((size_t)(p / ATT_P) * nkv + g) * ATT_P + (size_t)(p % ATT_P / ATT_T) * ATT_T) * hd;
-            dst[kv_k_at(bf, i, p % ATT_T)] = bf ? f2bf_ref(xo) : f2h_ref(xo);
-            dst[kv_k_at(bf, i + half, p % ATT_T)] = bf ? f2bf_ref(yo) : f2h_ref(yo);
+            const size_t o = (((size_t)(p / ATT_P) * nkv + g) * ATT_P + (size_t)(p % ATT_P / ATT_T) * ATT_T) * hd;
+            if (f32) { // (K [i][j] floats)
+                ((float *)kc[b])[o + (size_t)i * ATT_T + p % ATT_T] = xo;
+                ((float *)kc[b])[o + (size_t)(i + half) * ATT_T + p % ATT_T] = yo;
+            } else {
+                uint16_t *dst = kc[b] + o;
+                dst[kv_k_at(bf, i, p % ATT_T)] = bf ? f2bf_ref(xo) : f2h_ref(xo);
+                dst[kv_k_at(bf, i + half, p % ATT_T)] = bf ? f2bf_ref(yo) : f2h_ref(yo);
+            }
         }
     }
     if (qz) {
@@ -284,8 +293,8 @@ __global__ __launch_bounds__(64) void k_qknorm_rope_store(float *__restrict__ qk
     }
 }
 
-// synthetic rows of the quantized caches (rq_seq_fill_synthetic): block (position p, kv head g, K / V) draws hd values
-// (|K| < 3.9, |V| < 0.99) from a hash of (seed, p, g, K / V, dim) and stores them as k_qknorm_rope_store does
+// synthetic rows of the quantized and f32 caches (rq_seq_fill_synthetic): block (position p, kv head g, K / V) draws hd
+// values (|K| < 3.9, |V| < 0.99) from a hash of (seed, p, g, K / V, dim) and stores them as k_qknorm_rope_store does
 __global__ __launch_bounds__(64) void k_fill_synthetic_q(void *kc, void *vc, int kvt, int nkv, int hd, unsigned long long seed) {
     __shared__ float v[256];
     __shared__ uint32_t scw[8];
@@ -297,6 +306,11 @@ __global__ __launch_bounds__(64) void k_fill_synthetic_q(void *kc, void *vc, int
         z ^= z >> 31;
         const float a = (float)(z & 0xffffff) * (1.0f / 16777216.0f);
         v[i] = (2.0f * a - 1.0f) * (isv ? 0.99f : 3.9f);
+    }
+    if (kvt == 0) { // (f32: K [i][j], V [j][i] floats, not rotated)
+        float *t = (float *)(isv ? vc : kc) + (((size_t)(p / ATT_P) * nkv + g) * ATT_P + (size_t)(p % ATT_P / ATT_T) * ATT_T) * hd;
+        for (int i = threadIdx.x; i < hd; i += 64) t[isv ? (size_t)(p % ATT_T) * hd + i : (size_t)i * ATT_T + p % ATT_T] = v[i];
+        return;
     }
     __syncthreads();
     kvq_rot_lds(v, hd, false);
@@ -330,7 +344,9 @@ __global__ __launch_bounds__(64) void k_unrot_quant(const float *__restrict__ at
 // back (n d, exact), as forward.c:1776-1803 runs it on kvq_block_f32's copy: scores by the chunk chains of 32 dims
 // (a = c0 + c1 + c2 + c3, times scale), m the max, e = exp_att(s - m), l the 16 chains over positions j % 16 and the tree,
 // o the fma chain over the positions. part[(row nh + h) pstride + kb (hd + 2)] = o, m, l. The block's K tiles are staged
-// into LDS, then its V tiles over them. hd <= 128 (a power of two), nq <= 16.
+// into LDS, then its V tiles over them. hd <= 128 (a power of two), nq <= 16. The f32 cache (RQ_KV_F32: K [i][j], V
+// [j][i] floats, not rotated) runs the same fp32 attention on its values, read from HBM where they lie (its 64 KB of K
+// per block would not leave room in LDS for the rest).
 // DOT: the dot-product types (every row of the launch one), attention_vec_dot (forward.c:1488-1549, kernels_avx512.h:
 // 1439-1475): q, the values (16-bit caches: bf16 as stored, f16 rounded to bf16; quantized: n d rounded to bf16) and the
 // weights rounded to bf16; each product pair as vdpbf16ps's lane, two fmas with the odd element first (scores: dim
@@ -353,18 +369,21 @@ __global__ __launch_bounds__(AQ_T) void k_attn_q(const int4 *__restrict__ items,
     const int r0 = it.x, nr = it.y, g = it.z, kb = it.w, kv_mul = nh / nkv, nq = nr * kv_mul, t = threadIdx.x;
     const int kt = kvt[r0], base = kv_base(kt), ng = hd >> 5;
     const bool b16 = DOT && (base == 1 || base == 2); // (a 16-bit dot cache: bf16-dot, f16-dot)
+    const bool f32 = !DOT && kt == 0;                 // (the f32 cache: read from HBM, not staged; 64 KB per block)
     const bool k4 = kvq_q4(kt, false), v4 = kvq_q4(kt, true);
-    const int tbk = b16 ? 32 * hd : kvq_tile_bytes(k4, hd), tbv = b16 ? 32 * hd : kvq_tile_bytes(v4, hd);
+    const int tbk = f32 ? 64 * hd : b16 ? 32 * hd : kvq_tile_bytes(k4, hd);
+    const int tbv = f32 ? 64 * hd : b16 ? 32 * hd : kvq_tile_bytes(v4, hd);
     auto npos = [&](int v) -> int { // positions of block kb vector v reaches (<= 0: none)
         const int n = pos[r0 + v / kv_mul] + 1 - kb * ATT_P;
         return n < ATT_P ? n : ATT_P;
     };
     auto tile_src = [&](uint16_t *const *c, bool q4, int tb) -> const uint4 * { // (the block's first tile, head g)
-        if (!b16) return (const uint4 *)kvq_tile(c[r0], kb * ATT_P, g, nkv, hd, q4);
+        if (!b16 && !f32) return (const uint4 *)kvq_tile(c[r0], kb * ATT_P, g, nkv, hd, q4);
         return (const uint4 *)((const uint8_t *)c[r0] + ((size_t)kb * nkv + g) * (ATT_P / ATT_T) * (size_t)tb);
     };
     // the value of dim i, position j of a staged K (is_v false) or V tile tb, as the products read it
     auto value = [&](const uint8_t *tb, int i, int j, bool is_v) -> float {
+        if (f32) return ((const float *)tb)[is_v ? j * hd + i : i * ATT_T + j];
         if (b16) {
             const uint16_t *u = (const uint16_t *)tb;
             if (base == 1) return bf16_to_f32(u[is_v ? (j & ~1) * hd + 2 * i + (j & 1) : kv_k_at(true, i, j)]);
@@ -385,9 +404,12 @@ __global__ __launch_bounds__(AQ_T) void k_attn_q(const int4 *__restrict__ items,
         return DOT ? bf16_round((float)n * d) : (float)n * d;
     };
     // 1. the K tiles (the block's 16 tiles of head g are consecutive) and the query vectors
+    const uint8_t *kt0 = f32 ? (const uint8_t *)tile_src(kc, k4, tbk) : tl;
+    const uint8_t *vt0 = f32 ? (const uint8_t *)tile_src(vc, v4, tbv) : tl;
     {
         const uint4 *src = tile_src(kc, k4, tbk);
-        for (int i = t; i < ATT_T * tbk / 16; i += AQ_T) ((uint4 *)tl)[i] = src[i];
+        if (!f32)
+            for (int i = t; i < ATT_T * tbk / 16; i += AQ_T) ((uint4 *)tl)[i] = src[i];
         for (int i = t; i < nq * hd; i += AQ_T) {
             const int v = i / hd, d = i % hd;
             const float q = qkv[(size_t)(r0 + v / kv_mul) * ldqkv + (size_t)(g * kv_mul + v % kv_mul) * hd + d];
@@ -399,7 +421,7 @@ __global__ __launch_bounds__(AQ_T) void k_attn_q(const int4 *__restrict__ items,
     for (int k = t; k < nq * ATT_P; k += AQ_T) {
         const int v = k / ATT_P, p = k % ATT_P;
         if (p >= npos(v)) continue;
-        const uint8_t *tb = tl + (size_t)(p / ATT_T) * tbk;
+        const uint8_t *tb = kt0 + (size_t)(p / ATT_T) * tbk;
         const int j = p % ATT_T;
         const float *q = qs + v * hd;
         float a = 0.0f;
@@ -452,7 +474,7 @@ __global__ __launch_bounds__(AQ_T) void k_attn_q(const int4 *__restrict__ items,
     }
     __syncthreads();
     // 4. the V tiles over the K tiles
-    {
+    if (!f32) {
         const uint4 *src = tile_src(vc, v4, tbv);
         for (int i = t; i < ATT_T * tbv / 16; i += AQ_T) ((uint4 *)tl)[i] = src[i];
     }
@@ -464,14 +486,14 @@ __global__ __launch_bounds__(AQ_T) void k_attn_q(const int4 *__restrict__ items,
         float o = 0.0f;
         if (DOT) {
             for (int p = 0; p < n; p += 2) { // (p even: p and p + 1 share a tile)
-                const uint8_t *tb = tl + (size_t)(p / ATT_T) * tbv;
+                const uint8_t *tb = vt0 + (size_t)(p / ATT_T) * tbv;
                 const int j = p % ATT_T;
                 const float w1 = p + 1 < n ? S[v][p + 1] : 0.0f, v1 = p + 1 < n ? value(tb, i, j + 1, true) : 0.0f;
                 o = fma_ftz(S[v][p], value(tb, i, j, true), fma_ftz(w1, v1, o));
             }
         } else {
             for (int p = 0; p < n; p++)
-                o = __builtin_fmaf(S[v][p], value(tl + (size_t)(p / ATT_T) * tbv, i, p % ATT_T, true), o);
+                o = __builtin_fmaf(S[v][p], value(vt0 + (size_t)(p / ATT_T) * tbv, i, p % ATT_T, true), o);
         }
         float *dst = part + ((size_t)(r0 + v / kv_mul) * nh + g * kv_mul + v % kv_mul) * pstride + (size_t)kb * (hd + 2);
         dst[i] = o;

@@ -6,8 +6,8 @@
  * runq.h line it replaces. Types are laid out exactly as runq.h's (same fields, order and widths).
  *
  * Scope of the device implementation: Qwen3 dense models (GGUF, Q8_0 / Q2_K .. Q6_K / IQ4_XS matrices), the f16, bf16,
- * q8, q4 and q4k4 KV caches (RQ_KV_F16, RQ_KV_BF16, RQ_KV_Q8, RQ_KV_Q4, RQ_KV_Q4K4) and their bf16 dot-product types
- * (RQ_KV_BF16_DOT, F16_DOT, Q8_DOT, Q4_DOT, Q4K4_DOT; the f32 type gives RQ_ERR_ARG), one GPU, one HIP stream per context. Calls are synchronous at return
+ * q8, q4 and q4k4 KV caches (RQ_KV_F16, RQ_KV_BF16, RQ_KV_Q8, RQ_KV_Q4, RQ_KV_Q4K4), their bf16 dot-product types
+ * (RQ_KV_BF16_DOT, F16_DOT, Q8_DOT, Q4_DOT, Q4K4_DOT) and RQ_KV_F32, one GPU, one HIP stream per context. Calls are synchronous at return
  * (logits valid on the host), as the reference's are. Results are bit-identical for any batch composition: a row's
  * logits do not depend on the rows it is batched with (the device kernels compute each output whole, in a fixed order).
  *

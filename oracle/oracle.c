@@ -405,9 +405,11 @@ uint16_t or_f32_bf16(float f) {
  *   K q8 [i][j] int8, scales at 16 hd: [c][j];  K q4: byte [p][j] = (n_2p + 8) | (n_2p+1 + 8) << 4, scales at 8 hd: [c][j]
  *   V q8 [j][i] int8, scales at 16 hd: [j][c];  V q4: byte [j][c][l] = (n_32c+l + 8) | (n_32c+16+l + 8) << 4, scales at
  *   8 hd: [j][c] */
-enum { KVQ_Q8 = 3, KVQ_Q4 = 8, KVQ_Q4K4 = 9 };
+enum { KVQ_Q8 = 3, KVQ_Q4 = 8, KVQ_Q4K4 = 9, KVQ_F32 = 16 };
+/* KVQ_F32: the f32 cache (RQ_KV_F32) kept in the same byte tiles: 64 hd bytes, K [i][j], V [j][i] floats, not rotated
+ * (kv_store's fp32 case, forward.c:1945-1950); its attention the fp32 one of the 16-bit caches (forward.c:1827-1857) */
 static int kvq_fmt(int kvt, int is_v) { return kvt == KVQ_Q4K4 ? KVQ_Q4 : kvt == KVQ_Q4 && !is_v ? KVQ_Q8 : kvt; }
-static size_t kvq_tile_bytes(int fmt, int hd) { return (size_t)hd * (fmt == KVQ_Q4 ? 9 : 17); }
+static size_t kvq_tile_bytes(int fmt, int hd) { return (size_t)hd * (fmt == KVQ_F32 ? 64 : fmt == KVQ_Q4 ? 9 : 17); }
 static int kvq_neg(int i) { return (int)(((uint32_t)i * 0x9E3779B9u) >> 31); } /* forward.c:1632 */
 
 static void kvq_rot(float *x, int n, int inv) {
@@ -446,7 +448,12 @@ static float bf16_f32(uint16_t h) {
 }
 
 static void kvq_store(int fmt, uint8_t *tile, int j, int hd, const float *x0, int is_v) {
-    /* forward.c:1691-1738: row x0 of position j into a q8 / q4 tile (kvq_group per 32 dims, then the layout) */
+    /* forward.c:1691-1738: row x0 of position j into a q8 / q4 tile (kvq_group per 32 dims, then the layout); an f32
+     * tile takes the row as it is */
+    if (fmt == KVQ_F32) {
+        for (int i = 0; i < hd; i++) memcpy(tile + 4 * (is_v ? (size_t)j * hd + i : (size_t)i * ATT_T + j), &x0[i], 4);
+        return;
+    }
     float x[256];
     memcpy(x, x0, (size_t)hd * sizeof(float));
     kvq_rot(x, hd, 0);
@@ -484,7 +491,12 @@ static void kvq_store(int fmt, uint8_t *tile, int j, int hd, const float *x0, in
 }
 
 static float kvq_val(int fmt, const uint8_t *tile, int i, int j, int hd, int is_v) {
-    /* forward.c:1740-1768: dim i of position j read back, n d (exact) */
+    /* forward.c:1740-1768: dim i of position j read back, n d (exact); an f32 tile's value as stored */
+    if (fmt == KVQ_F32) {
+        float f;
+        memcpy(&f, tile + 4 * (is_v ? (size_t)j * hd + i : (size_t)i * ATT_T + j), 4);
+        return f;
+    }
     const int q4 = fmt == KVQ_Q4, ng = hd / 32, c = i / 32;
     const uint8_t *sc = tile + (size_t)(q4 ? 8 : 16) * hd;
     uint16_t s;
@@ -956,16 +968,17 @@ OrSeq *or_seq_new_kv(const OrModel *m, int bf16) {
 }
 
 OrSeq *or_seq_new_type(const OrModel *m, int kv_type) {
-    /* a sequence of cache type kv_type (runq.h:214): RQ_KV_F16 2, RQ_KV_BF16 1, RQ_KV_Q8 3, RQ_KV_Q4 8, RQ_KV_Q4K4 9, and
-     * their dot-product types (+ 4: 5, 6, 7, 12, 13) */
+    /* a sequence of cache type kv_type (runq.h:214): RQ_KV_F32 0, RQ_KV_F16 2, RQ_KV_BF16 1, RQ_KV_Q8 3, RQ_KV_Q4 8,
+     * RQ_KV_Q4K4 9, and the dot-product types of all but f32 (+ 4: 5, 6, 7, 12, 13) */
+    if (kv_type == 4) return NULL;
     const int base = kv_type & ~4, dot = (kv_type & 4) != 0;
     if (base == 1 || base == 2) {
         OrSeq *s = or_seq_new_kv(m, base == 1);
         if (s) s->dot = dot;
         return s;
     }
-    if (base != KVQ_Q8 && base != KVQ_Q4 && base != KVQ_Q4K4) return NULL;
-    kv_type = base;
+    if (base != KVQ_Q8 && base != KVQ_Q4 && base != KVQ_Q4K4 && base != 0) return NULL;
+    kv_type = base ? base : KVQ_F32;
     OrSeq *s = calloc(1, sizeof(OrSeq));
     if (!s) return NULL;
     s->dot = dot;
@@ -1098,12 +1111,16 @@ int or_forward_token(const OrModel *m, OrSeq *s, int token, float *logits, float
             for (int h = 0; h < nh; h++) {
                 float qr[256];
                 memcpy(qr, q + h * hd, (size_t)hd * sizeof(float));
-                kvq_rot(qr, hd, 0);
-                kvq_scale_by(qr, hd);
+                if (s->qt != KVQ_F32) {
+                    kvq_rot(qr, hd, 0);
+                    kvq_scale_by(qr, hd);
+                }
                 attention_t(s->qt | (s->dot ? 4 : 0), att + h * hd, qr, NULL, NULL, kq, vq, pos + 1, h / kv_mul, nkv, hd,
                             m->att_scale);
-                kvq_rot(att + h * hd, hd, 1);
-                kvq_scale_by(att + h * hd, hd);
+                if (s->qt != KVQ_F32) {
+                    kvq_rot(att + h * hd, hd, 1);
+                    kvq_scale_by(att + h * hd, hd);
+                }
             }
         } else {
         uint16_t *kc = s->kc + (size_t)l * per, *vc = s->vc + (size_t)l * per;

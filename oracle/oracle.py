@@ -134,8 +134,8 @@ class Model:
         self.dim, self.hidden, self.n_layers, self.n_heads, self.n_kv_heads, self.head_dim, self.vocab, self.kv_len = \
             (int(v) for v in d)
 
-    def seq(self, bf16: bool = False, kv_type: int = 0) -> "Seq":
-        """kv_type (runq.h:214) when given, else f16 (or bf16)"""
+    def seq(self, bf16: bool = False, kv_type: int = None) -> "Seq":
+        """kv_type (runq.h:214: 0 f32, 1 bf16, 2 f16, ...) when given, else f16 (or bf16)"""
         return Seq(self, bf16, kv_type)
 
     def __del__(self):
@@ -145,9 +145,9 @@ class Model:
 
 
 class Seq:
-    def __init__(self, m: Model, bf16: bool = False, kv_type: int = 0):
+    def __init__(self, m: Model, bf16: bool = False, kv_type: int = None):
         self.m = m
-        self._h = lib().or_seq_new_type(m._h, kv_type) if kv_type else lib().or_seq_new_kv(m._h, 1 if bf16 else 0)
+        self._h = lib().or_seq_new_type(m._h, kv_type) if kv_type is not None else lib().or_seq_new_kv(m._h, 1 if bf16 else 0)
         if not self._h:
             raise RuntimeError(f"or_seq_new: kv type {kv_type}")
 

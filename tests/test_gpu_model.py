@@ -190,7 +190,10 @@ def test_memory_and_pass_times(gw, synth_models):
     res = SeqMem()
     lib.rq_seq_resident(ctypes.c_void_p(s._h), ctypes.byref(res))
     assert res.kv == sm.kv
-    assert lib.rq_seq_mem(ctypes.c_void_p(m._h), 300, 0, ctypes.byref(sm)) != 0  # (f32 KV: not supported, RQ_ERR_ARG)
+    f16_kv = sm.kv - 300 * 4
+    assert lib.rq_seq_mem(ctypes.c_void_p(m._h), 300, 0, ctypes.byref(sm)) == 0  # (f32: twice the f16 tiles)
+    assert sm.kv - 300 * 4 == 2 * f16_kv
+    assert lib.rq_seq_mem(ctypes.c_void_p(m._h), 300, 4, ctypes.byref(sm)) == gw.RQ_ERR_ARG  # (4: not a type)
     t1, t4 = ctypes.c_double(), ctypes.c_double()
     assert lib.rq_pass_times(ctypes.c_void_p(m._h), 2, ctypes.byref(t1), ctypes.byref(t4)) == 0
     assert 0 < t1.value < 1 and 0 < t4.value < 1

@@ -201,9 +201,9 @@ def test_hidden_rows_after_batched_passes_on_one_context(gw, orc, tmp_path):
     assert np.array_equal(_bits(lg), _bits(rlg[21:62])), "fw_rows n 41, max_batch 8: logits rows"
 
 
-# RQ_KV_F16, RQ_KV_BF16, RQ_KV_Q8, RQ_KV_Q4, RQ_KV_Q4K4, and the dot-product types RQ_KV_BF16_DOT, F16_DOT, Q8_DOT, Q4_DOT,
-# Q4K4_DOT
-@pytest.mark.parametrize("kvt", [2, 1, 3, 8, 9, 5, 6, 7, 12, 13])
+# RQ_KV_F16, RQ_KV_BF16, RQ_KV_Q8, RQ_KV_Q4, RQ_KV_Q4K4, the dot-product types RQ_KV_BF16_DOT, F16_DOT, Q8_DOT, Q4_DOT,
+# Q4K4_DOT, and RQ_KV_F32
+@pytest.mark.parametrize("kvt", [2, 1, 3, 8, 9, 5, 6, 7, 12, 13, 0])
 def test_seqfile_with_reference(gw, orc, tmp_path, kvt):
     """the KV disk tier (runq.h:283-314) against the reference's seqfile.c: the same model fingerprint; the reference's
     saved sequence (300-token prompt + 4 greedy steps) read by rq_seq_file_info and loaded by rq_seq_load continues bit
@@ -253,7 +253,7 @@ def test_seqfile_with_reference(gw, orc, tmp_path, kvt):
     assert np.array_equal(r[:264][hdr], o[:264][hdr])
     assert np.array_equal(r[4096:4096 + 4 * L], o[4096:4096 + 4 * L])
     hd = m.info.head_dim
-    tile = {2: (32, 32), 1: (32, 32), 3: (17, 17), 8: (17, 9), 9: (9, 9)}[kvt & ~4 if kvt in (5, 6, 7, 12, 13) else kvt]
+    tile = {0: (64, 64), 2: (32, 32), 1: (32, 32), 3: (17, 17), 8: (17, 9), 9: (9, 9)}[kvt & ~4 if kvt in (5, 6, 7, 12, 13) else kvt]
     # (K, V tile bytes per dim: a dot-product type's are its base type's)
     off_kv = int(np.frombuffer(r[224:232].tobytes(), np.uint64)[0])
     bk, bv = (16 * m.info.n_kv_heads * hd * t for t in tile)
@@ -279,14 +279,15 @@ def test_seqfile_with_reference(gw, orc, tmp_path, kvt):
     assert lib.rq_seq_load(ctypes.c_void_p(m.seq(1024, kv_type=other)._h), p2.encode(), 10) == -7
 
 
-# RQ_KV_Q8, RQ_KV_Q4, RQ_KV_Q4K4; the dot-product types RQ_KV_BF16_DOT, F16_DOT, Q8_DOT, Q4_DOT, Q4K4_DOT
-@pytest.mark.parametrize("kvt", [3, 8, 9, 5, 6, 7, 12, 13])
+# RQ_KV_Q8, RQ_KV_Q4, RQ_KV_Q4K4; the dot-product types RQ_KV_BF16_DOT, F16_DOT, Q8_DOT, Q4_DOT, Q4K4_DOT; RQ_KV_F32
+@pytest.mark.parametrize("kvt", [3, 8, 9, 5, 6, 7, 12, 13, 0])
 def test_quantized_kv_greedy_bit_identical(gw, orc, tmp_path, kvt):
-    """the rotated 8-bit / 4-bit KV caches (forward.c:1609-1790) and the bf16 dot-product attention types
-    (forward.c:1452-1606: bf16 q, K, V and weights, vdpbf16ps's pairs, FTZ / DAZ) on a Qwen3-0.6B-shaped model (2
-    layers): a 300-token prefill (two key blocks, 16-vector row blocks) and 24 greedy steps, every logits row equal bit
-    for bit to the reference's own cache of that type, the same tokens; then a pass of that sequence's next token beside
-    a fresh sequence's prompt (both of the type) equal to each run alone"""
+    """the rotated 8-bit / 4-bit KV caches (forward.c:1609-1790), the bf16 dot-product attention types
+    (forward.c:1452-1606: bf16 q, K, V and weights, vdpbf16ps's pairs, FTZ / DAZ) and the f32 cache (forward.c:1945-1950:
+    fp32 tiles, the fp32 attention) on a Qwen3-0.6B-shaped model (2 layers): a 300-token prefill (two key blocks,
+    16-vector row blocks) and 24 greedy steps, every logits row equal bit for bit to the reference's own cache of that
+    type, the same tokens; then a pass of that sequence's next token beside a fresh sequence's prompt (both of the
+    type) equal to each run alone"""
     path, d = _synth(str(tmp_path), "qwen3_0_6b", seed=4, n_layers=2)
     m = gw.Model(path, ctx_len=512)
     if not _exact(gw):

@@ -451,12 +451,13 @@ def test_attention_combine_matches_single_pass():
     ("tiny", {}, 270, 7),
     ("tiny", {}, 270, 12),
     ("tiny", {}, 270, 13),
+    ("tiny", {}, 270, 0),
 ])
 def test_forward_bit_exact_vs_reference(tmp_path, shape, over, n, kvt):
     """or_forward_token position by position against the reference compiled from its sources (rq_prefill with every
     row's logits, ref_driver), on seeded synthetic models: every logit bit for bit. On an AVX-512 host the oracle's
     SwiGLU runs the reference's own vector expf and rcp14; nothing else in the pass depends on the host. kvt: both with
-    that KV cache type (runq.h:214: 2 f16, 1 bf16, 3 q8, 8 q4, 9 q4k4: the rotated, quantized caches of
+    that KV cache type (runq.h:214: 0 f32, 2 f16, 1 bf16, 3 q8, 8 q4, 9 q4k4: the rotated, quantized caches of
     forward.c:1609-1790; + 4: their bf16 dot-product attention, kernels_avx512.h:1439-1475; 270 positions: two
     attention blocks)"""
     from gwenedeg_amd import synth
