@@ -317,6 +317,38 @@ def test_bf16_and_f16_sequences_in_one_pass(gw, synth_models):
 
 
 
+@pytest.mark.parametrize("shape", ["tiny_gqa4", "tiny_hd64"])
+def test_every_kv_type_in_one_pass(gw, synth_models, shape):
+    """one rq_forward_batch over sequences of every KV cache type (runq.h:214: f32, bf16, f16, q8, q4, q4k4 and the five
+    dot-product types; each type's attention items in the launch of its kernel) at lengths on both sides of a
+    256-position key block, decode rows and prompt rows: every row gets the bits it gets alone, and a type's rows do
+    not depend on the other types beside them"""
+    path = synth_models(shape)
+    m = gw.Model(path, ctx_len=1024)
+    c = m.ctx(max_batch=256)
+    rng = np.random.default_rng(33)
+    kinds = [gw.RQ_KV_F32, gw.RQ_KV_BF16, gw.RQ_KV_F16, gw.RQ_KV_Q8, gw.RQ_KV_Q4, gw.RQ_KV_Q4K4, gw.RQ_KV_BF16_DOT,
+             gw.RQ_KV_F16_DOT, gw.RQ_KV_Q8_DOT, gw.RQ_KV_Q4_DOT, gw.RQ_KV_Q4K4_DOT]
+    lens = [int(x) for x in rng.integers(3, 520, len(kinds))]
+    seqs = [m.seq(1024, kv_type=k) for k in kinds]
+    for sq, n in zip(seqs, lens):
+        c.prefill(sq, _ids(m.vocab, n, n))
+    twins = [m.seq(1024, kv_type=k) for k in kinds]
+    for tw, sq in zip(twins, seqs):
+        tw.copy_from(sq, len(sq))
+    chunks = [[int(t) for t in rng.integers(0, m.vocab, 1 if i % 2 else 9)] for i in range(len(kinds))]
+    lg, _ = c.forward_batch([gw.Segment(sq, ch, gw.RQ_LOGITS_ALL) for sq, ch in zip(seqs, chunks)])
+    alone = []
+    for tw, ch in zip(twins, chunks):
+        alone += list(c.prefill(tw, ch, mode=gw.RQ_LOGITS_ALL))
+    assert lg.shape[0] == len(alone)
+    row = 0
+    for k, ch in zip(kinds, chunks):
+        for _ in ch:
+            assert _bits_equal(lg[row], alone[row]), f"kv type {k}, row {row}"
+            row += 1
+
+
 @pytest.mark.parametrize("k", [1, 7, 40, 64])
 def test_device_topk(gw, synth_models, k):
     """gw_ctx_topk: the k best logits of each row on the device and their ids, in sample_topk's order (larger first,
