@@ -61,6 +61,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--probe", action="store_true")
+    ap.add_argument("--kv-type", type=int, default=2,
+                    help="batch32_4b / long_8b: the sequences' KV cache type (runq.h:214; default 2, RQ_KV_F16); another "
+                         "type's line carries no cpu_baseline")
     ap.add_argument("--workload", default="step", choices=["step", "op_q8", "batch32_4b", "long_8b", "cb_8b"],
                     help="step: the metric's workload (default); op_q8: the isolated 12288 x 4096 Q8_0 operator of the "
                          "reference's config 2; batch32_4b / long_8b: the batched decode of configs 3 / 4; cb_8b: config "
@@ -231,7 +234,7 @@ def batched(torch, gw, synth, a):
     cap = ctx + steps + a.warmup + 16
     m = gw.Model(path, ctx_len=cap)
     c = m.ctx(max_batch=max(nseq, 2), max_ctx=cap)
-    seqs = [m.seq(cap) for _ in range(nseq)]
+    seqs = [m.seq(cap, kv_type=a.kv_type) for _ in range(nseq)]
     for i, sq in enumerate(seqs):
         sq.fill_synthetic(ctx, seed=a.seed + i)
     toks = [int(t) for t in np.random.default_rng(a.seed).integers(0, m.vocab, nseq)]
@@ -253,7 +256,11 @@ def batched(torch, gw, synth, a):
     kt = c.kernel_times(multi=True)
     c.kernel_timing(False)
     info = m.info
-    kv_pos = info.n_layers * info.n_kv_heads * info.head_dim * 2 * 2  # f16 K and V bytes per position
+    # K and V bytes per position (the tiles' bytes per dim: f32 4, 16-bit 2, q8 17 / 16, q4 9 / 16; a dot-product type
+    # its base type's)
+    base = a.kv_type & ~4 if a.kv_type in (5, 6, 7, 12, 13) else a.kv_type
+    kb, vb = {0: (4, 4), 1: (2, 2), 2: (2, 2), 3: (17 / 16, 17 / 16), 8: (17 / 16, 9 / 16), 9: (9 / 16, 9 / 16)}[base]
+    kv_pos = info.n_layers * info.n_kv_heads * info.head_dim * (kb + vb)
     mean_ctx = ctx + a.warmup + steps + 0.5
     kv_bytes = nseq * mean_ctx * kv_pos
     w_bytes = weight_file_bytes(path)
@@ -263,7 +270,8 @@ def batched(torch, gw, synth, a):
         "metric": f"batched greedy decode rows/s ({a.workload}: the reference's config {3 if nseq == 32 else 4}, 1 GPU)",
         "value": round(nseq * steps / el, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": a.warmup,
         "ms_per_step": round(1e3 * step_s, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "int8 x int8 -> int32, fp32 fold; f16 KV", "data": "synthetic weights; K / V of the prefixes by rq_seq_fill_synthetic",
+        "dtype": f"int8 x int8 -> int32, fp32 fold; KV type {a.kv_type}" + (" (f16)" if a.kv_type == 2 else ""),
+        "data": "synthetic weights; K / V of the prefixes by rq_seq_fill_synthetic",
         "config": {"workload": f"{shape}: {nseq} sequences x {ctx} cached positions, one row per sequence per step",
                    "global_batch": nseq, "seq_len": ctx},
         "hbm_bytes_per_step": {"weights": w_bytes, "kv_read": kv_bytes},
@@ -272,7 +280,7 @@ def batched(torch, gw, synth, a):
                       "kv_gbs": round(kv_bytes / att_s / 1e9, 1) if att_s else None},
         "kernel_ms_per_step": {k: round(v[0] * 1e3, 3) for k, v in kt.items() if v[1]},
     }
-    if not a.no_cpu_baseline:
+    if not a.no_cpu_baseline and a.kv_type == 2:
         # the same shape on the reference: nseq sequences filled to ctx positions, one untimed pass, then cpu_steps
         # timed greedy passes of one row per sequence
         t0 = [int(t) for t in np.random.default_rng(a.seed).integers(0, m.vocab, nseq)]

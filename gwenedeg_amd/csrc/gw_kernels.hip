@@ -356,21 +356,19 @@ __device__ __forceinline__ float ftz_f(float x) { return fabsf(x) < 1.17549435e-
 __device__ __forceinline__ float fma_ftz(float a, float b, float c) { return ftz_f(__builtin_fmaf(ftz_f(a), ftz_f(b), ftz_f(c))); }
 __device__ __forceinline__ float bf16_round(float x) { return bf16_to_f32(f2bf_ref(ftz_f(x))); } // (vcvtneps2bf16)
 
-template <bool DOT>
-__global__ __launch_bounds__(AQ_T) void k_attn_q(const int4 *__restrict__ items, const float *__restrict__ qkv, int ldqkv,
-                                                 int nh, int nkv, int hd, float scale, const int *__restrict__ pos,
-                                                 uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc,
-                                                 const int *__restrict__ kvt, float *__restrict__ part, int pstride) {
-    __shared__ __align__(16) uint8_t tl[ATT_T * (DOT ? 32 : 17) * 128]; // the block's 16 tiles of K, then of V
-    __shared__ float qs[16 * 128];
-    __shared__ float S[16][ATT_P];
-    __shared__ float ms[16], ls[16];
-    const int4 it = items[blockIdx.x];
+// the block's work for one cache type (BT: the row's base type, kv_base; LDS from the kernel), every format decision made
+// at compile time, so that a batch of operand loads is one straight run of loads
+template <bool DOT, int BT>
+__device__ __forceinline__ void attn_q_body(const int4 it, const float *__restrict__ qkv, int ldqkv, int nh, int nkv, int hd,
+                                            float scale, const int *__restrict__ pos, uint16_t *const *__restrict__ kc,
+                                            uint16_t *const *__restrict__ vc, float *__restrict__ part, int pstride,
+                                            uint8_t *tl, float *qs, float (*S)[ATT_P], float *ms, float *ls) {
     const int r0 = it.x, nr = it.y, g = it.z, kb = it.w, kv_mul = nh / nkv, nq = nr * kv_mul, t = threadIdx.x;
-    const int kt = kvt[r0], base = kv_base(kt), ng = hd >> 5;
-    const bool b16 = DOT && (base == 1 || base == 2); // (a 16-bit dot cache: bf16-dot, f16-dot)
-    const bool f32 = !DOT && kt == 0;                 // (the f32 cache: read from HBM, not staged; 64 KB per block)
-    const bool k4 = kvq_q4(kt, false), v4 = kvq_q4(kt, true);
+    const int ng = hd >> 5;
+    constexpr int base = BT;
+    constexpr bool b16 = DOT && (BT == 1 || BT == 2); // (a 16-bit dot cache: bf16-dot, f16-dot)
+    constexpr bool f32 = !DOT && BT == 0;             // (the f32 cache: read from HBM, not staged; 64 KB per block)
+    constexpr bool k4 = BT == 9, v4 = BT == 9 || BT == 8;
     const int tbk = f32 ? 64 * hd : b16 ? 32 * hd : kvq_tile_bytes(k4, hd);
     const int tbv = f32 ? 64 * hd : b16 ? 32 * hd : kvq_tile_bytes(v4, hd);
     auto npos = [&](int v) -> int { // positions of block kb vector v reaches (<= 0: none)
@@ -413,32 +411,50 @@ __global__ __launch_bounds__(AQ_T) void k_attn_q(const int4 *__restrict__ items,
         for (int i = t; i < nq * hd; i += AQ_T) {
             const int v = i / hd, d = i % hd;
             const float q = qkv[(size_t)(r0 + v / kv_mul) * ldqkv + (size_t)(g * kv_mul + v % kv_mul) * hd + d];
-            qs[i] = DOT ? bf16_round(q) : q;
+            qs[d * 16 + v] = DOT ? bf16_round(q) : q;
         }
     }
     __syncthreads();
-    // 2. scores, thread per (vector, position)
-    for (int k = t; k < nq * ATT_P; k += AQ_T) {
-        const int v = k / ATT_P, p = k % ATT_P;
-        if (p >= npos(v)) continue;
+    // 2. scores, thread per (position, group of 4 vectors): each K value read once for the group's 4 chains (vectors
+    // past nq, or positions past a vector's reach, computed on whatever LDS holds and not stored)
+    for (int k = t; k < (nq + 3) / 4 * ATT_P; k += AQ_T) {
+        const int v0 = 4 * (k / ATT_P), p = k % ATT_P;
+        int reach = 0;
+        #pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (v0 + u < nq) reach = npos(v0 + u) > reach ? npos(v0 + u) : reach;
+        if (p >= reach) continue;
         const uint8_t *tb = kt0 + (size_t)(p / ATT_T) * tbk;
         const int j = p % ATT_T;
-        const float *q = qs + v * hd;
-        float a = 0.0f;
+        float a[4] = { 0.0f, 0.0f, 0.0f, 0.0f };
         for (int c = 0; c < ng; c++) {
-            float cc = 0.0f;
+            float cc[4] = { 0.0f, 0.0f, 0.0f, 0.0f };
             if (DOT) {
                 for (int i = 32 * c; i < 32 * c + 32; i += 2) {
-                    cc = fma_ftz(q[i + 1], value(tb, i + 1, j, false), cc);
-                    cc = fma_ftz(q[i], value(tb, i, j, false), cc);
+                    const float k1 = value(tb, i + 1, j, false), k0 = value(tb, i, j, false);
+                    const float4 q1 = *(const float4 *)(qs + (i + 1) * 16 + v0), q0 = *(const float4 *)(qs + i * 16 + v0);
+                    const float q1v[4] = { q1.x, q1.y, q1.z, q1.w }, q0v[4] = { q0.x, q0.y, q0.z, q0.w };
+                    #pragma unroll
+                    for (int u = 0; u < 4; u++) cc[u] = fma_ftz(q0v[u], k0, fma_ftz(q1v[u], k1, cc[u]));
                 }
-                a = c ? ftz_f(a + cc) : cc;
+                #pragma unroll
+                for (int u = 0; u < 4; u++) a[u] = c ? ftz_f(a[u] + cc[u]) : cc[u];
             } else {
-                for (int i = 32 * c; i < 32 * c + 32; i++) cc = __builtin_fmaf(q[i], value(tb, i, j, false), cc);
-                a = c ? a + cc : cc;
+                for (int i = 32 * c; i < 32 * c + 32; i++) {
+                    const float kv = value(tb, i, j, false);
+                    const float4 q = *(const float4 *)(qs + i * 16 + v0);
+                    cc[0] = __builtin_fmaf(q.x, kv, cc[0]);
+                    cc[1] = __builtin_fmaf(q.y, kv, cc[1]);
+                    cc[2] = __builtin_fmaf(q.z, kv, cc[2]);
+                    cc[3] = __builtin_fmaf(q.w, kv, cc[3]);
+                }
+                #pragma unroll
+                for (int u = 0; u < 4; u++) a[u] = c ? a[u] + cc[u] : cc[u];
             }
         }
-        S[v][p] = DOT ? ftz_f(a * scale) : a * scale;
+        #pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (v0 + u < nq && p < npos(v0 + u)) S[v0 + u][p] = DOT ? ftz_f(a[u] * scale) : a[u] * scale;
     }
     __syncthreads();
     // 3. softmax: wave w takes vectors w, w + 8: m, the exponentials (DOT: rounded to bf16), l (lane j < 16: the chain
@@ -484,15 +500,41 @@ __global__ __launch_bounds__(AQ_T) void k_attn_q(const int4 *__restrict__ items,
         const int v = k / hd, i = k % hd, n = npos(v);
         if (n <= 0) continue;
         float o = 0.0f;
+        // (the operands of 8 positions loaded before their fmas: the chain waits on one batch of loads, not on each)
+        int p = 0;
         if (DOT) {
-            for (int p = 0; p < n; p += 2) { // (p even: p and p + 1 share a tile)
+            for (; p + 8 <= n; p += 8) { // (p % 8 == 0: the 8 positions share a tile)
+                const uint8_t *tb = vt0 + (size_t)(p / ATT_T) * tbv;
+                const int j = p % ATT_T;
+                float w[8], x[8];
+                #pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    w[u] = S[v][p + u];
+                    x[u] = value(tb, i, j + u, true);
+                }
+                #pragma unroll
+                for (int u = 0; u < 8; u += 2) o = fma_ftz(w[u], x[u], fma_ftz(w[u + 1], x[u + 1], o));
+            }
+            for (; p < n; p += 2) { // (p even: p and p + 1 share a tile)
                 const uint8_t *tb = vt0 + (size_t)(p / ATT_T) * tbv;
                 const int j = p % ATT_T;
                 const float w1 = p + 1 < n ? S[v][p + 1] : 0.0f, v1 = p + 1 < n ? value(tb, i, j + 1, true) : 0.0f;
                 o = fma_ftz(S[v][p], value(tb, i, j, true), fma_ftz(w1, v1, o));
             }
         } else {
-            for (int p = 0; p < n; p++)
+            for (; p + 8 <= n; p += 8) {
+                const uint8_t *tb = vt0 + (size_t)(p / ATT_T) * tbv;
+                const int j = p % ATT_T;
+                float w[8], x[8];
+                #pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    w[u] = S[v][p + u];
+                    x[u] = value(tb, i, j + u, true);
+                }
+                #pragma unroll
+                for (int u = 0; u < 8; u++) o = __builtin_fmaf(w[u], x[u], o);
+            }
+            for (; p < n; p++)
                 o = __builtin_fmaf(S[v][p], value(vt0 + (size_t)(p / ATT_T) * tbv, i, p % ATT_T, true), o);
         }
         float *dst = part + ((size_t)(r0 + v / kv_mul) * nh + g * kv_mul + v % kv_mul) * pstride + (size_t)kb * (hd + 2);
@@ -502,6 +544,33 @@ __global__ __launch_bounds__(AQ_T) void k_attn_q(const int4 *__restrict__ items,
             dst[hd + 1] = ls[v];
         }
     }
+}
+
+template <bool DOT>
+__global__ __launch_bounds__(AQ_T) void k_attn_q(const int4 *__restrict__ items, const float *__restrict__ qkv, int ldqkv,
+                                                 int nh, int nkv, int hd, float scale, const int *__restrict__ pos,
+                                                 uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc,
+                                                 const int *__restrict__ kvt, float *__restrict__ part, int pstride) {
+    __shared__ __align__(16) uint8_t tl[ATT_T * (DOT ? 32 : 17) * 128]; // the block's 16 tiles of K, then of V
+    __shared__ __align__(16) float qs[128 * 16]; // the query vectors, transposed: dim d of vector v at 16 d + v
+    __shared__ float S[16][ATT_P];
+    __shared__ float ms[16], ls[16];
+    const int4 it = items[blockIdx.x];
+    const int base = kv_base(kvt[it.x]); // (uniform over the block: one branch, then a body without type tests)
+#define AQ_BODY(B) attn_q_body<DOT, B>(it, qkv, ldqkv, nh, nkv, hd, scale, pos, kc, vc, part, pstride, tl, qs, S, ms, ls)
+    if constexpr (DOT) {
+        if (base == 1) AQ_BODY(1);
+        else if (base == 2) AQ_BODY(2);
+        else if (base == 3) AQ_BODY(3);
+        else if (base == 8) AQ_BODY(8);
+        else AQ_BODY(9);
+    } else {
+        if (base == 0) AQ_BODY(0);
+        else if (base == 3) AQ_BODY(3);
+        else if (base == 8) AQ_BODY(8);
+        else AQ_BODY(9);
+    }
+#undef AQ_BODY
 }
 
 // One block of 1024 threads per item (first row r0, rows nr of one sequence at consecutive positions, kv head g, key
