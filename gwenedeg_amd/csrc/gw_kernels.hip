@@ -350,11 +350,14 @@ __global__ __launch_bounds__(64) void k_unrot_quant(const float *__restrict__ at
 // DOT: the dot-product types (every row of the launch one), attention_vec_dot (forward.c:1488-1549, kernels_avx512.h:
 // 1439-1475): q, the values (16-bit caches: bf16 as stored, f16 rounded to bf16; quantized: n d rounded to bf16) and the
 // weights rounded to bf16; each product pair as vdpbf16ps's lane, two fmas with the odd element first (scores: dim
-// pairs; o: position pairs, a last odd position paired with +0, +0); the call's FTZ / DAZ mode as fma_ftz / ftz_f
+// pairs; o: position pairs, a last odd position paired with +0, +0); the call's FTZ / DAZ mode as ftz_f on each
+// value read and on each fma's result (fma_fz)
 #define AQ_T 512
 __device__ __forceinline__ float ftz_f(float x) { return fabsf(x) < 1.17549435e-38f ? __builtin_copysignf(0.0f, x) : x; }
-__device__ __forceinline__ float fma_ftz(float a, float b, float c) { return ftz_f(__builtin_fmaf(ftz_f(a), ftz_f(b), ftz_f(c))); }
 __device__ __forceinline__ float bf16_round(float x) { return bf16_to_f32(f2bf_ref(ftz_f(x))); } // (vcvtneps2bf16)
+// fma_ftz on operands already flushed (a bf16_round result, a value as the products read it, an earlier fma_fz, zero):
+// only the result needs the flush
+__device__ __forceinline__ float fma_fz(float a, float b, float c) { return ftz_f(__builtin_fmaf(a, b, c)); }
 
 // the block's work for one cache type (BT: the row's base type, kv_base; LDS from the kernel), every format decision made
 // at compile time, so that a batch of operand loads is one straight run of loads
@@ -384,7 +387,7 @@ __device__ __forceinline__ void attn_q_body(const int4 it, const float *__restri
         if (f32) return ((const float *)tb)[is_v ? j * hd + i : i * ATT_T + j];
         if (b16) {
             const uint16_t *u = (const uint16_t *)tb;
-            if (base == 1) return bf16_to_f32(u[is_v ? (j & ~1) * hd + 2 * i + (j & 1) : kv_k_at(true, i, j)]);
+            if (base == 1) return ftz_f(bf16_to_f32(u[is_v ? (j & ~1) * hd + 2 * i + (j & 1) : kv_k_at(true, i, j)]));
             return bf16_round(h2f(u[is_v ? j * hd + i : kv_k_at(false, i, j)]));
         }
         const bool q4 = is_v ? v4 : k4;
@@ -435,7 +438,7 @@ __device__ __forceinline__ void attn_q_body(const int4 it, const float *__restri
                     const float4 q1 = *(const float4 *)(qs + (i + 1) * 16 + v0), q0 = *(const float4 *)(qs + i * 16 + v0);
                     const float q1v[4] = { q1.x, q1.y, q1.z, q1.w }, q0v[4] = { q0.x, q0.y, q0.z, q0.w };
                     #pragma unroll
-                    for (int u = 0; u < 4; u++) cc[u] = fma_ftz(q0v[u], k0, fma_ftz(q1v[u], k1, cc[u]));
+                    for (int u = 0; u < 4; u++) cc[u] = fma_fz(q0v[u], k0, fma_fz(q1v[u], k1, cc[u]));
                 }
                 #pragma unroll
                 for (int u = 0; u < 4; u++) a[u] = c ? ftz_f(a[u] + cc[u]) : cc[u];
@@ -495,54 +498,74 @@ __device__ __forceinline__ void attn_q_body(const int4 it, const float *__restri
         for (int i = t; i < ATT_T * tbv / 16; i += AQ_T) ((uint4 *)tl)[i] = src[i];
     }
     __syncthreads();
-    // 5. o, thread per (vector, dim): the fma chain over the positions in order (DOT: over position pairs)
-    for (int k = t; k < nq * hd; k += AQ_T) {
-        const int v = k / hd, i = k % hd, n = npos(v);
-        if (n <= 0) continue;
-        float o = 0.0f;
-        // (the operands of 8 positions loaded before their fmas: the chain waits on one batch of loads, not on each)
-        int p = 0;
-        if (DOT) {
-            for (; p + 8 <= n; p += 8) { // (p % 8 == 0: the 8 positions share a tile)
-                const uint8_t *tb = vt0 + (size_t)(p / ATT_T) * tbv;
-                const int j = p % ATT_T;
-                float w[8], x[8];
-                #pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    w[u] = S[v][p + u];
-                    x[u] = value(tb, i, j + u, true);
-                }
-                #pragma unroll
-                for (int u = 0; u < 8; u += 2) o = fma_ftz(w[u], x[u], fma_ftz(w[u + 1], x[u + 1], o));
+    // 5. o, thread per (dim, group of 4 vectors): each V value read once for the group's 4 fma chains over the positions
+    // in order (DOT: over position pairs); the operands of 8 positions loaded before their fmas
+    for (int k = t; k < (nq + 3) / 4 * hd; k += AQ_T) {
+        const int v0 = 4 * (k / hd), i = k % hd, nv = nq - v0 < 4 ? nq - v0 : 4;
+        int nu[4], nmin = ATT_P, nmax = 0;
+        #pragma unroll
+        for (int u = 0; u < 4; u++) {
+            nu[u] = u < nv ? npos(v0 + u) : 0;
+            if (u < nv) {
+                nmin = nu[u] < nmin ? nu[u] : nmin;
+                nmax = nu[u] > nmax ? nu[u] : nmax;
             }
-            for (; p < n; p += 2) { // (p even: p and p + 1 share a tile)
+        }
+        if (nmax <= 0) continue;
+        float o[4] = { 0.0f, 0.0f, 0.0f, 0.0f };
+        int p = 0;
+        for (; p + 8 <= nmin; p += 8) { // (p % 8 == 0: the 8 positions share a tile)
+            const uint8_t *tb = vt0 + (size_t)(p / ATT_T) * tbv;
+            const int j = p % ATT_T;
+            float x[8], w[4][8];
+            #pragma unroll
+            for (int e = 0; e < 8; e++) {
+                x[e] = value(tb, i, j + e, true);
+                #pragma unroll
+                for (int u = 0; u < 4; u++) w[u][e] = S[v0 + u][p + e]; // (rows past nq: in the array, not stored)
+            }
+            #pragma unroll
+            for (int u = 0; u < 4; u++) {
+                if (DOT) {
+                    #pragma unroll
+                    for (int e = 0; e < 8; e += 2) o[u] = fma_fz(w[u][e], x[e], fma_fz(w[u][e + 1], x[e + 1], o[u]));
+                } else {
+                    #pragma unroll
+                    for (int e = 0; e < 8; e++) o[u] = __builtin_fmaf(w[u][e], x[e], o[u]);
+                }
+            }
+        }
+        if (DOT) {
+            for (; p < nmax; p += 2) { // (p even: p and p + 1 share a tile; each vector to its own reach)
                 const uint8_t *tb = vt0 + (size_t)(p / ATT_T) * tbv;
                 const int j = p % ATT_T;
-                const float w1 = p + 1 < n ? S[v][p + 1] : 0.0f, v1 = p + 1 < n ? value(tb, i, j + 1, true) : 0.0f;
-                o = fma_ftz(S[v][p], value(tb, i, j, true), fma_ftz(w1, v1, o));
+                const float x0 = value(tb, i, j, true), x1 = p + 1 < nmax ? value(tb, i, j + 1, true) : 0.0f;
+                #pragma unroll
+                for (int u = 0; u < 4; u++)
+                    if (p < nu[u]) {
+                        const float w1 = p + 1 < nu[u] ? S[v0 + u][p + 1] : 0.0f, v1 = p + 1 < nu[u] ? x1 : 0.0f;
+                        o[u] = fma_fz(S[v0 + u][p], x0, fma_fz(w1, v1, o[u]));
+                    }
             }
         } else {
-            for (; p + 8 <= n; p += 8) {
-                const uint8_t *tb = vt0 + (size_t)(p / ATT_T) * tbv;
-                const int j = p % ATT_T;
-                float w[8], x[8];
+            for (; p < nmax; p++) {
+                const float x0 = value(vt0 + (size_t)(p / ATT_T) * tbv, i, p % ATT_T, true);
                 #pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    w[u] = S[v][p + u];
-                    x[u] = value(tb, i, j + u, true);
-                }
-                #pragma unroll
-                for (int u = 0; u < 8; u++) o = __builtin_fmaf(w[u], x[u], o);
+                for (int u = 0; u < 4; u++)
+                    if (p < nu[u]) o[u] = __builtin_fmaf(S[v0 + u][p], x0, o[u]);
             }
-            for (; p < n; p++)
-                o = __builtin_fmaf(S[v][p], value(vt0 + (size_t)(p / ATT_T) * tbv, i, p % ATT_T, true), o);
         }
-        float *dst = part + ((size_t)(r0 + v / kv_mul) * nh + g * kv_mul + v % kv_mul) * pstride + (size_t)kb * (hd + 2);
-        dst[i] = o;
-        if (i == 0) {
-            dst[hd] = ms[v];
-            dst[hd + 1] = ls[v];
-        }
+        #pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (u < nv && nu[u] > 0) {
+                const int v = v0 + u;
+                float *dst = part + ((size_t)(r0 + v / kv_mul) * nh + g * kv_mul + v % kv_mul) * pstride + (size_t)kb * (hd + 2);
+                dst[i] = o[u];
+                if (i == 0) {
+                    dst[hd] = ms[v];
+                    dst[hd + 1] = ls[v];
+                }
+            }
     }
 }
 
