@@ -346,7 +346,7 @@ __global__ __launch_bounds__(64) void k_unrot_quant(const float *__restrict__ at
 // o the fma chain over the positions. part[(row nh + h) pstride + kb (hd + 2)] = o, m, l. The block's K tiles are staged
 // into LDS, then its V tiles over them. hd <= 128 (a power of two), nq <= 16. The f32 cache (RQ_KV_F32: K [i][j], V
 // [j][i] floats, not rotated) runs the same fp32 attention on its values, read from HBM where they lie (its 64 KB of K
-// per block would not leave room in LDS for the rest).
+// per block would not leave room in LDS for the rest); so do the 16-bit dot-product tiles (32 KB of K per block).
 // DOT: the dot-product types (every row of the launch one), attention_vec_dot (forward.c:1488-1549, kernels_avx512.h:
 // 1439-1475): q, the values (16-bit caches: bf16 as stored, f16 rounded to bf16; quantized: n d rounded to bf16) and the
 // weights rounded to bf16; each product pair as vdpbf16ps's lane, two fmas with the odd element first (scores: dim
@@ -371,6 +371,8 @@ __device__ __forceinline__ void attn_q_body(const int4 it, const float *__restri
     constexpr int base = BT;
     constexpr bool b16 = DOT && (BT == 1 || BT == 2); // (a 16-bit dot cache: bf16-dot, f16-dot)
     constexpr bool f32 = !DOT && BT == 0;             // (the f32 cache: read from HBM, not staged; 64 KB per block)
+    constexpr bool inplace = f32 || b16;              // (f32 and 16-bit dot tiles read where they lie: the LDS holds the
+                                                      // 8-bit tiles only, and two blocks fit a CU)
     constexpr bool k4 = BT == 9, v4 = BT == 9 || BT == 8;
     const int tbk = f32 ? 64 * hd : b16 ? 32 * hd : kvq_tile_bytes(k4, hd);
     const int tbv = f32 ? 64 * hd : b16 ? 32 * hd : kvq_tile_bytes(v4, hd);
@@ -405,11 +407,11 @@ __device__ __forceinline__ void attn_q_body(const int4 it, const float *__restri
         return DOT ? bf16_round((float)n * d) : (float)n * d;
     };
     // 1. the K tiles (the block's 16 tiles of head g are consecutive) and the query vectors
-    const uint8_t *kt0 = f32 ? (const uint8_t *)tile_src(kc, k4, tbk) : tl;
-    const uint8_t *vt0 = f32 ? (const uint8_t *)tile_src(vc, v4, tbv) : tl;
+    const uint8_t *kt0 = inplace ? (const uint8_t *)tile_src(kc, k4, tbk) : tl;
+    const uint8_t *vt0 = inplace ? (const uint8_t *)tile_src(vc, v4, tbv) : tl;
     {
         const uint4 *src = tile_src(kc, k4, tbk);
-        if (!f32)
+        if (!inplace)
             for (int i = t; i < ATT_T * tbk / 16; i += AQ_T) ((uint4 *)tl)[i] = src[i];
         for (int i = t; i < nq * hd; i += AQ_T) {
             const int v = i / hd, d = i % hd;
@@ -493,7 +495,7 @@ __device__ __forceinline__ void attn_q_body(const int4 it, const float *__restri
     }
     __syncthreads();
     // 4. the V tiles over the K tiles
-    if (!f32) {
+    if (!inplace) {
         const uint4 *src = tile_src(vc, v4, tbv);
         for (int i = t; i < ATT_T * tbv / 16; i += AQ_T) ((uint4 *)tl)[i] = src[i];
     }
@@ -574,7 +576,7 @@ __global__ __launch_bounds__(AQ_T) void k_attn_q(const int4 *__restrict__ items,
                                                  int nh, int nkv, int hd, float scale, const int *__restrict__ pos,
                                                  uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc,
                                                  const int *__restrict__ kvt, float *__restrict__ part, int pstride) {
-    __shared__ __align__(16) uint8_t tl[ATT_T * (DOT ? 32 : 17) * 128]; // the block's 16 tiles of K, then of V
+    __shared__ __align__(16) uint8_t tl[ATT_T * 17 * 128]; // the block's 16 tiles of K, then of V (8-bit / 4-bit types)
     __shared__ __align__(16) float qs[128 * 16]; // the query vectors, transposed: dim d of vector v at 16 d + v
     __shared__ float S[16][ATT_P];
     __shared__ float ms[16], ls[16];
