@@ -614,7 +614,11 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
     const RqModel *m = c->m;
     int n = P->n, L = m->n_layers, nh = m->n_heads, nkv = m->n_kv_heads, hd = m->head_dim, dim = m->dim, H = m->hidden;
     int kv_mul = nh / nkv, rb = 16 / kv_mul > 0 ? 16 / kv_mul : 1, rc;
-    /* attention items: row blocks of <= rb consecutive rows of one sequence, per kv head and key block */
+    /* (the f32 / quantized caches' items: <= 8 query vectors where one row's fit, so k_attn_q's LDS holds 3 blocks per
+     * CU; nqm: its vector bound) */
+    int nqm = kv_mul <= 8 ? 8 : 16, rbq = 8 / kv_mul > 0 ? 8 / kv_mul : rb;
+#define ROWS_OF(t) (gw_kv_att_q(t) && !gw_kv_dot(t) ? rbq : rb)
+    /* attention items: row blocks of <= rb (rbq) consecutive rows of one sequence, per kv head and key block */
     int nbmax = 1, nitems = 0;
     for (int b = 0; b < n; b++) {
         int nb = (P->pos[b] + 1 + GW_ATT_P - 1) / GW_ATT_P;
@@ -623,7 +627,7 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
     if ((rc = ctx_part(c, n, nbmax)) != RQ_OK) return rc;
     for (int b = 0; b < n;) {
         int e = b + 1;
-        while (e < n && e - b < rb && P->seq[e] == P->seq[b] && P->pos[e] == P->pos[e - 1] + 1) e++;
+        while (e < n && e - b < ROWS_OF(P->seq[b]->kvt) && P->seq[e] == P->seq[b] && P->pos[e] == P->pos[e - 1] + 1) e++;
         nitems += nkv * ((P->pos[e - 1] + 1 + GW_ATT_P - 1) / GW_ATT_P);
         b = e;
     }
@@ -661,7 +665,7 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
     for (int grp = 0, k = 0; grp < 6; grp++)
         for (int b = 0; b < n;) {
             int e = b + 1;
-            while (e < n && e - b < rb && P->seq[e] == P->seq[b] && P->pos[e] == P->pos[e - 1] + 1) e++;
+            while (e < n && e - b < ROWS_OF(kvt[b]) && P->seq[e] == P->seq[b] && P->pos[e] == P->pos[e - 1] + 1) e++;
             int nb = (P->pos[e - 1] + 1 + GW_ATT_P - 1) / GW_ATT_P, nq = (e - b) * kv_mul;
             int kg = gw_kv_dot(kvt[b]) ? 5 : gw_kv_att_q(kvt[b]) ? 4 : 2 * (kvt[b] == RQ_KV_BF16) + (nq > 4);
             if (kg == grp) {
@@ -672,6 +676,7 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
             }
             b = e;
         }
+#undef ROWS_OF
     HIPCHK(c, "hipMemcpyAsync (pass metadata)", hipMemcpyAsync(d, h, total, hipMemcpyHostToDevice, c->stream));
     const int *tok_d = (const int *)(d + o_tok), *pos_d = (const int *)(d + o_pos), *sel_d = (const int *)(d + o_sel);
     const int *kvt_d = (const int *)(d + o_kbf);
@@ -711,7 +716,8 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
             if (!gcnt[grp]) continue;
             if (grp >= 4)
                 KCHK(gw_k_attn_q((const Item *)items_d + off, gcnt[grp], c->qkv, c->ldqkv, nh, nkv, hd, m->att_scale, pos_d,
-                                 kc_d + (size_t)l * n, vc_d + (size_t)l * n, kvt_d, grp == 5, c->part, c->pstride, s));
+                                 kc_d + (size_t)l * n, vc_d + (size_t)l * n, kvt_d, grp == 5, grp == 5 ? 16 : nqm, c->part,
+                                 c->pstride, s));
             else
                 KCHK(gw_k_attn_part((const Item *)items_d + off, gcnt[grp], gnq[grp], c->qkv, c->ldqkv, nh, nkv, hd,
                                     m->att_scale, pos_d, kc_d + (size_t)l * n, vc_d + (size_t)l * n, c->part, c->pstride,

@@ -266,10 +266,12 @@ int gw_k_rmsnorm_quant(float *x, const float *d, int dim, const float *w, const 
 int gw_k_qknorm_rope_store(float *qkv, int ldqkv, int n, int nh, int nkv, int hd, const float *qn, const float *kn,
                            const float *rope, const int *pos, uint16_t *const *kc, uint16_t *const *vc,
                            const int *kvt, hipStream_t s); /* kvt: per row, its cache type (runq.h:214; NULL: all f16) */
-/* the attention partials of items on the quantized caches (RQ_KV_Q8 / Q4 / Q4K4; dot 0) or on the dot-product types (dot
- * 1: every item's row one of them); kvt: each row's type; hd a power of two, 32 .. 128 */
+/* the attention partials of items on the f32 and quantized caches (RQ_KV_F32, Q8, Q4, Q4K4; dot 0) or on the dot-product
+ * types (dot 1: every item's row one of them); kvt: each row's type; hd a power of two, 32 .. 128; nqm: the most query
+ * vectors an item holds, 8 or 16 (dot 1: 16) */
 int gw_k_attn_q(const void *items, int nitems, const float *qkv, int ldqkv, int nh, int nkv, int hd, float scale, const int *pos,
-                uint16_t *const *kc, uint16_t *const *vc, const int *kvt, int dot, float *part, int pstride, hipStream_t s);
+                uint16_t *const *kc, uint16_t *const *vc, const int *kvt, int dot, int nqm, float *part, int pstride,
+                hipStream_t s);
 /* the rows of quantized caches: o = D H o' / hd from the combined attention att (n rows of nh hd), quantized into aq / as */
 int gw_k_unrot_quant(const float *att, int n, int nh, int hd, const int *kvt, int8_t *aq, float *as, int ldq, hipStream_t s);
 int gw_k_attn_part(const void *items, int nitems, int nq_max, const float *qkv, int ldqkv, int nh, int nkv, int hd, float scale,

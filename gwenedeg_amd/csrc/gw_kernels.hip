@@ -344,7 +344,7 @@ __global__ __launch_bounds__(64) void k_unrot_quant(const float *__restrict__ at
 // back (n d, exact), as forward.c:1776-1803 runs it on kvq_block_f32's copy: scores by the chunk chains of 32 dims
 // (a = c0 + c1 + c2 + c3, times scale), m the max, e = exp_att(s - m), l the 16 chains over positions j % 16 and the tree,
 // o the fma chain over the positions. part[(row nh + h) pstride + kb (hd + 2)] = o, m, l. The block's K tiles are staged
-// into LDS, then its V tiles over them. hd <= 128 (a power of two), nq <= 16. The f32 cache (RQ_KV_F32: K [i][j], V
+// into LDS, then its V tiles over them. hd <= 128 (a power of two), nq <= NQM (8 or 16). The f32 cache (RQ_KV_F32: K [i][j], V
 // [j][i] floats, not rotated) runs the same fp32 attention on its values, read from HBM where they lie (its 64 KB of K
 // per block would not leave room in LDS for the rest); so do the 16-bit dot-product tiles (32 KB of K per block).
 // DOT: the dot-product types (every row of the launch one), attention_vec_dot (forward.c:1488-1549, kernels_avx512.h:
@@ -361,7 +361,7 @@ __device__ __forceinline__ float fma_fz(float a, float b, float c) { return ftz_
 
 // the block's work for one cache type (BT: the row's base type, kv_base; LDS from the kernel), every format decision made
 // at compile time, so that a batch of operand loads is one straight run of loads
-template <bool DOT, int BT>
+template <bool DOT, int BT, int NQM>
 __device__ __forceinline__ void attn_q_body(const int4 it, const float *__restrict__ qkv, int ldqkv, int nh, int nkv, int hd,
                                             float scale, const int *__restrict__ pos, uint16_t *const *__restrict__ kc,
                                             uint16_t *const *__restrict__ vc, float *__restrict__ part, int pstride,
@@ -416,7 +416,7 @@ __device__ __forceinline__ void attn_q_body(const int4 it, const float *__restri
         for (int i = t; i < nq * hd; i += AQ_T) {
             const int v = i / hd, d = i % hd;
             const float q = qkv[(size_t)(r0 + v / kv_mul) * ldqkv + (size_t)(g * kv_mul + v % kv_mul) * hd + d];
-            qs[d * 16 + v] = DOT ? bf16_round(q) : q;
+            qs[d * NQM + v] = DOT ? bf16_round(q) : q;
         }
     }
     __syncthreads();
@@ -424,7 +424,7 @@ __device__ __forceinline__ void attn_q_body(const int4 it, const float *__restri
     // chains into S (chunk 0 at S[v], chunk c > 0 at S[4 + 4 (c - 1) + v]: rows S has free), then per (vector,
     // position) a = ((c0 + c1) + c2) + c3, times scale, as the chain below adds them (for the fp32 types the extra
     // barrier and LDS round trip cost more than the shorter chains gain)
-    constexpr bool split = DOT;
+    constexpr bool split = DOT && NQM == 16;
     if (split && nq <= 4) {
         for (int k = t; k < ng * ATT_P; k += AQ_T) {
             const int c = k / ATT_P, p = k % ATT_P;
@@ -439,7 +439,7 @@ __device__ __forceinline__ void attn_q_body(const int4 it, const float *__restri
             if (DOT) {
                 for (int i = 32 * c; i < 32 * c + 32; i += 2) {
                     const float k1 = value(tb, i + 1, j, false), k0 = value(tb, i, j, false);
-                    const float4 q1 = *(const float4 *)(qs + (i + 1) * 16), q0 = *(const float4 *)(qs + i * 16);
+                    const float4 q1 = *(const float4 *)(qs + (i + 1) * NQM), q0 = *(const float4 *)(qs + i * NQM);
                     const float q1v[4] = { q1.x, q1.y, q1.z, q1.w }, q0v[4] = { q0.x, q0.y, q0.z, q0.w };
                     #pragma unroll
                     for (int u = 0; u < 4; u++) cc[u] = fma_fz(q0v[u], k0, fma_fz(q1v[u], k1, cc[u]));
@@ -447,7 +447,7 @@ __device__ __forceinline__ void attn_q_body(const int4 it, const float *__restri
             } else {
                 for (int i = 32 * c; i < 32 * c + 32; i++) {
                     const float kv = value(tb, i, j, false);
-                    const float4 q = *(const float4 *)(qs + i * 16);
+                    const float4 q = *(const float4 *)(qs + i * NQM);
                     cc[0] = __builtin_fmaf(q.x, kv, cc[0]);
                     cc[1] = __builtin_fmaf(q.y, kv, cc[1]);
                     cc[2] = __builtin_fmaf(q.z, kv, cc[2]);
@@ -483,7 +483,7 @@ __device__ __forceinline__ void attn_q_body(const int4 it, const float *__restri
             if (DOT) {
                 for (int i = 32 * c; i < 32 * c + 32; i += 2) {
                     const float k1 = value(tb, i + 1, j, false), k0 = value(tb, i, j, false);
-                    const float4 q1 = *(const float4 *)(qs + (i + 1) * 16 + v0), q0 = *(const float4 *)(qs + i * 16 + v0);
+                    const float4 q1 = *(const float4 *)(qs + (i + 1) * NQM + v0), q0 = *(const float4 *)(qs + i * NQM + v0);
                     const float q1v[4] = { q1.x, q1.y, q1.z, q1.w }, q0v[4] = { q0.x, q0.y, q0.z, q0.w };
                     #pragma unroll
                     for (int u = 0; u < 4; u++) cc[u] = fma_fz(q0v[u], k0, fma_fz(q1v[u], k1, cc[u]));
@@ -493,7 +493,7 @@ __device__ __forceinline__ void attn_q_body(const int4 it, const float *__restri
             } else {
                 for (int i = 32 * c; i < 32 * c + 32; i++) {
                     const float kv = value(tb, i, j, false);
-                    const float4 q = *(const float4 *)(qs + i * 16 + v0);
+                    const float4 q = *(const float4 *)(qs + i * NQM + v0);
                     cc[0] = __builtin_fmaf(q.x, kv, cc[0]);
                     cc[1] = __builtin_fmaf(q.y, kv, cc[1]);
                     cc[2] = __builtin_fmaf(q.z, kv, cc[2]);
@@ -617,18 +617,18 @@ __device__ __forceinline__ void attn_q_body(const int4 it, const float *__restri
     }
 }
 
-template <bool DOT>
+template <bool DOT, int NQM> // (NQM: the query vectors an item may hold, 8 or 16; LDS sized by it: 8 lets 3 blocks share a CU)
 __global__ __launch_bounds__(AQ_T) void k_attn_q(const int4 *__restrict__ items, const float *__restrict__ qkv, int ldqkv,
                                                  int nh, int nkv, int hd, float scale, const int *__restrict__ pos,
                                                  uint16_t *const *__restrict__ kc, uint16_t *const *__restrict__ vc,
                                                  const int *__restrict__ kvt, float *__restrict__ part, int pstride) {
     __shared__ __align__(16) uint8_t tl[ATT_T * 17 * 128]; // the block's 16 tiles of K, then of V (8-bit / 4-bit types)
-    __shared__ __align__(16) float qs[128 * 16]; // the query vectors, transposed: dim d of vector v at 16 d + v
-    __shared__ float S[16][ATT_P];
-    __shared__ float ms[16], ls[16];
+    __shared__ __align__(16) float qs[128 * NQM]; // the query vectors, transposed: dim d of vector v at NQM d + v
+    __shared__ float S[NQM][ATT_P];
+    __shared__ float ms[NQM], ls[NQM];
     const int4 it = items[blockIdx.x];
     const int base = kv_base(kvt[it.x]); // (uniform over the block: one branch, then a body without type tests)
-#define AQ_BODY(B) attn_q_body<DOT, B>(it, qkv, ldqkv, nh, nkv, hd, scale, pos, kc, vc, part, pstride, tl, qs, S, ms, ls)
+#define AQ_BODY(B) attn_q_body<DOT, B, NQM>(it, qkv, ldqkv, nh, nkv, hd, scale, pos, kc, vc, part, pstride, tl, qs, S, ms, ls)
     if constexpr (DOT) {
         if (base == 1) AQ_BODY(1);
         else if (base == 2) AQ_BODY(2);
@@ -1619,15 +1619,20 @@ int gw_k_qknorm_rope_store(float *qkv, int ldqkv, int n, int nh, int nkv, int hd
 }
 
 int gw_k_attn_q(const void *items, int nitems, const float *qkv, int ldqkv, int nh, int nkv, int hd, float scale, const int *pos,
-                uint16_t *const *kc, uint16_t *const *vc, const int *kvt, int dot, float *part, int pstride, hipStream_t s) {
-    // (hd a power of two, 32 .. 128; at most 16 query vectors per item)
-    if (hd < 32 || hd > 128 || (hd & (hd - 1))) return (int)hipErrorInvalidValue;
+                uint16_t *const *kc, uint16_t *const *vc, const int *kvt, int dot, int nqm, float *part, int pstride,
+                hipStream_t s) {
+    // (hd a power of two, 32 .. 128; at most nqm query vectors per item: 8 or 16, the dot-product types 16)
+    if (hd < 32 || hd > 128 || (hd & (hd - 1)) || (nqm != 8 && nqm != 16) || (dot && nqm != 16))
+        return (int)hipErrorInvalidValue;
     if (dot)
-        GW_LAUNCH(k_attn_q<true>, dim3(nitems), dim3(AQ_T), 0, s, (const int4 *)items, qkv, ldqkv, nh, nkv, hd, scale, pos, kc,
-                  vc, kvt, part, pstride);
+        GW_LAUNCH((k_attn_q<true, 16>), dim3(nitems), dim3(AQ_T), 0, s, (const int4 *)items, qkv, ldqkv, nh, nkv, hd, scale, pos,
+                  kc, vc, kvt, part, pstride);
+    else if (nqm == 8)
+        GW_LAUNCH((k_attn_q<false, 8>), dim3(nitems), dim3(AQ_T), 0, s, (const int4 *)items, qkv, ldqkv, nh, nkv, hd, scale, pos,
+                  kc, vc, kvt, part, pstride);
     else
-        GW_LAUNCH(k_attn_q<false>, dim3(nitems), dim3(AQ_T), 0, s, (const int4 *)items, qkv, ldqkv, nh, nkv, hd, scale, pos, kc,
-                  vc, kvt, part, pstride);
+        GW_LAUNCH((k_attn_q<false, 16>), dim3(nitems), dim3(AQ_T), 0, s, (const int4 *)items, qkv, ldqkv, nh, nkv, hd, scale,
+                  pos, kc, vc, kvt, part, pstride);
     return (int)hipGetLastError();
 }
 
