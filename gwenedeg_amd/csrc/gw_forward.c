@@ -614,10 +614,10 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
     const RqModel *m = c->m;
     int n = P->n, L = m->n_layers, nh = m->n_heads, nkv = m->n_kv_heads, hd = m->head_dim, dim = m->dim, H = m->hidden;
     int kv_mul = nh / nkv, rb = 16 / kv_mul > 0 ? 16 / kv_mul : 1, rc;
-    /* (the f32 / quantized caches' items: <= 8 query vectors where one row's fit, so k_attn_q's LDS holds 3 blocks per
-     * CU; nqm: its vector bound) */
+    /* (the items of the caches k_attn_q serves (f32, quantized, dot-product): <= 8 query vectors where one row's fit, so
+     * its LDS holds 3 blocks per CU; nqm: its vector bound) */
     int nqm = kv_mul <= 8 ? 8 : 16, rbq = 8 / kv_mul > 0 ? 8 / kv_mul : rb;
-#define ROWS_OF(t) (gw_kv_att_q(t) && !gw_kv_dot(t) ? rbq : rb)
+#define ROWS_OF(t) (gw_kv_att_q(t) ? rbq : rb)
     /* attention items: row blocks of <= rb (rbq) consecutive rows of one sequence, per kv head and key block */
     int nbmax = 1, nitems = 0;
     for (int b = 0; b < n; b++) {
@@ -716,7 +716,7 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
             if (!gcnt[grp]) continue;
             if (grp >= 4)
                 KCHK(gw_k_attn_q((const Item *)items_d + off, gcnt[grp], c->qkv, c->ldqkv, nh, nkv, hd, m->att_scale, pos_d,
-                                 kc_d + (size_t)l * n, vc_d + (size_t)l * n, kvt_d, grp == 5, grp == 5 ? 16 : nqm, c->part,
+                                 kc_d + (size_t)l * n, vc_d + (size_t)l * n, kvt_d, grp == 5, nqm, c->part,
                                  c->pstride, s));
             else
                 KCHK(gw_k_attn_part((const Item *)items_d + off, gcnt[grp], gnq[grp], c->qkv, c->ldqkv, nh, nkv, hd,

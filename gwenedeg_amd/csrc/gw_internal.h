@@ -268,7 +268,7 @@ int gw_k_qknorm_rope_store(float *qkv, int ldqkv, int n, int nh, int nkv, int hd
                            const int *kvt, hipStream_t s); /* kvt: per row, its cache type (runq.h:214; NULL: all f16) */
 /* the attention partials of items on the f32 and quantized caches (RQ_KV_F32, Q8, Q4, Q4K4; dot 0) or on the dot-product
  * types (dot 1: every item's row one of them); kvt: each row's type; hd a power of two, 32 .. 128; nqm: the most query
- * vectors an item holds, 8 or 16 (dot 1: 16) */
+ * vectors an item holds, 8 or 16 */
 int gw_k_attn_q(const void *items, int nitems, const float *qkv, int ldqkv, int nh, int nkv, int hd, float scale, const int *pos,
                 uint16_t *const *kc, uint16_t *const *vc, const int *kvt, int dot, int nqm, float *part, int pstride,
                 hipStream_t s);

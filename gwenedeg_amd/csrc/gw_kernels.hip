@@ -1621,10 +1621,12 @@ int gw_k_qknorm_rope_store(float *qkv, int ldqkv, int n, int nh, int nkv, int hd
 int gw_k_attn_q(const void *items, int nitems, const float *qkv, int ldqkv, int nh, int nkv, int hd, float scale, const int *pos,
                 uint16_t *const *kc, uint16_t *const *vc, const int *kvt, int dot, int nqm, float *part, int pstride,
                 hipStream_t s) {
-    // (hd a power of two, 32 .. 128; at most nqm query vectors per item: 8 or 16, the dot-product types 16)
-    if (hd < 32 || hd > 128 || (hd & (hd - 1)) || (nqm != 8 && nqm != 16) || (dot && nqm != 16))
-        return (int)hipErrorInvalidValue;
-    if (dot)
+    // (hd a power of two, 32 .. 128; at most nqm query vectors per item: 8 or 16)
+    if (hd < 32 || hd > 128 || (hd & (hd - 1)) || (nqm != 8 && nqm != 16)) return (int)hipErrorInvalidValue;
+    if (dot && nqm == 8)
+        GW_LAUNCH((k_attn_q<true, 8>), dim3(nitems), dim3(AQ_T), 0, s, (const int4 *)items, qkv, ldqkv, nh, nkv, hd, scale, pos,
+                  kc, vc, kvt, part, pstride);
+    else if (dot)
         GW_LAUNCH((k_attn_q<true, 16>), dim3(nitems), dim3(AQ_T), 0, s, (const int4 *)items, qkv, ldqkv, nh, nkv, hd, scale, pos,
                   kc, vc, kvt, part, pstride);
     else if (nqm == 8)
