@@ -100,8 +100,8 @@ class Plan:
     def text(self):
         return "\n".join(self.lines) + "\n"
 
-    def check(self, orc, path, workdir, cap):
-        info, rlg, rtok = orc.run_ref_plan(path, self.text(), workdir, threads=_threads(), cap=cap)
+    def check(self, orc, path, workdir, cap, kv_type=2):
+        info, rlg, rtok = orc.run_ref_plan(path, self.text(), workdir, threads=_threads(), cap=cap, kv_type=kv_type)
         ours = np.concatenate(self.rows)
         assert rlg.shape == ours.shape, (rlg.shape, ours.shape)
         assert [int(t) for t in rtok] == self.fed, "greedy tokens"
@@ -148,6 +148,31 @@ def test_config4_batch8_at_32k_vs_reference(gw, orc, tmp_path, model_8b_1l):
             p.run([(i, LAST, None) for i in range(ns)])
         p.check(orc, model_8b_1l, str(tmp_path / "ref"), cap)
         assert len(p.fed) == 3 * ns
+    finally:
+        _rm(files)
+
+
+@pytest.mark.parametrize("kvt", [3, 9, 5, 7, 0])  # RQ_KV_Q8, RQ_KV_Q4K4, RQ_KV_BF16_DOT, RQ_KV_Q8_DOT, RQ_KV_F32
+def test_long_context_kv_types_vs_reference(gw, orc, tmp_path, model_8b_1l, kvt):
+    """config 4's pass on the f32, quantized and dot-product caches (k_attn_q over 32 key blocks): 4 sequences at
+    8,192 - 7 i cached positions of the type (rq_seq_fill_synthetic stores them as the type stores a row), saved and
+    loaded by the reference, then 3 batched greedy passes of 4 one-row segments: every logits row bit for bit"""
+    m = gw.Model(model_8b_1l, ctx_len=8256)
+    if gw.exact_mode() & 3 != 3:
+        pytest.skip("this host does not provide the reference's float operations (AVX-512)")
+    cap, ns = 8256, 4
+    seqs = [m.seq(cap, kv_type=kvt) for _ in range(ns)]
+    files = _save_all(seqs, [8192 - 7 * i for i in range(ns)], str(tmp_path), f"lk{kvt}_", 700)
+    try:
+        c = m.ctx(max_batch=64, max_ctx=cap)
+        p = Plan(c, seqs, cap)
+        for i, f in enumerate(files):
+            p.load(i, f)
+        toks = [int(t) for t in np.random.default_rng(6).integers(0, m.vocab, ns)]
+        p.run([(i, LAST, [toks[i]]) for i in range(ns)])
+        for _ in range(2):
+            p.run([(i, LAST, None) for i in range(ns)])
+        p.check(orc, model_8b_1l, str(tmp_path / "ref"), cap, kv_type=kvt)
     finally:
         _rm(files)
 
