@@ -54,7 +54,7 @@ static uint16_t *seq_layer(const RqSeq *s, int l, int kv) {
 RqSeq *rq_seq_new(const RqModel *m, int capacity, int kv_type, int *err) {
     int e = RQ_OK;
     RqSeq *s = NULL;
-    if (!m) { e = RQ_ERR_STATE; goto fail; }
+    if (!m || !m->has_weights) { e = RQ_ERR_STATE; goto fail; } /* (forward.c:641: a tokenizer-only model) */
     if (capacity <= 0) capacity = m->seq_len;
     /* f16 and bf16 caches (the fp32 attention on the exactly converted values, runq.h:204-213); f32, the rotated q8 / q4
      * ones and the dot-product types with head_dim a power of two, 32 .. 128 */
@@ -200,7 +200,7 @@ int rq_seq_fill_synthetic(RqSeq *s, int n, unsigned long long seed) {
         int e = gw_kv_quant(s->kvt) || s->kvt == RQ_KV_F32
                     ? gw_k_fill_synthetic_q(seq_layer(s, l, 0), seq_layer(s, l, 1), s->kvt, (int)(nb * GW_ATT_P),
                                             s->m->n_kv_heads, s->m->head_dim, sl, 0)
-                    : gw_k_fill_synthetic(seq_layer(s, l, 0), seq_layer(s, l, 1), per, sl, 0);
+                    : gw_k_fill_synthetic(seq_layer(s, l, 0), seq_layer(s, l, 1), per, sl, gw_kv_base(s->kvt) == RQ_KV_BF16, 0);
         if (e) return RQ_ERR_STATE;
     }
     if (hipDeviceSynchronize() != hipSuccess) return RQ_ERR_STATE;
@@ -306,7 +306,7 @@ int rq_seq_mem(const RqModel *m, int capacity, int kv_type, RqSeqMem *mem) {
     /* model.c:765-772: one sequence's memory as rq_seq_new allocates it (RQ_ERR_ARG as rq_seq_new): the K / V halves
      * in device memory (whole 256-position blocks) and the token array; no recurrent state (Qwen3) */
     memset(mem, 0, sizeof(*mem));
-    if (!m) return RQ_ERR_STATE;
+    if (!m || !m->has_weights) return RQ_ERR_STATE;
     if (capacity <= 0) capacity = m->seq_len;
     int hd = m->head_dim, qok = hd >= 32 && hd <= 128 && !(hd & (hd - 1));
     if (capacity > m->seq_len || !gw_kv_ok(kv_type) || (gw_kv_att_q(kv_type) && !qok))
@@ -324,7 +324,7 @@ int rq_model_mem(const RqModel *m, RqModelMem *mem) {
      * device holds (288 MiB); seq = one sequence of that length. No budget is checked (budget 0, budget_src 0); a
      * one-row pass reads every weight (read = weights) */
     memset(mem, 0, sizeof(*mem));
-    if (!m) return RQ_ERR_STATE;
+    if (!m || !m->has_weights) return RQ_ERR_STATE;
     mem->weights = m->dev_bytes;
     mem->runtime = ctx_bytes(m, RQ_BATCH_MAX, m->seq_len) + ((size_t)288 << 20);
     rq_seq_mem(m, m->seq_len, RQ_KV_F16, &mem->seq);
@@ -337,6 +337,7 @@ int rq_pass_times(const RqModel *m, int reps, double *t1, double *t4) {
     /* runq.h:196-199: a decode step and a 4-row pass with every row's logits at position 32 (rq_seq_fill_synthetic),
      * the fastest of reps each after a warm-up, seconds; its own context and sequence */
     if (!m || reps < 1 || !t1 || !t4) return RQ_ERR_ARG;
+    if (!m->has_weights) return RQ_ERR_STATE;
     int e = RQ_OK;
     RqCtx *c = rq_ctx_new(m, 4, 64, &e);
     if (!c) return e;
@@ -368,7 +369,7 @@ int rq_pass_times(const RqModel *m, int reps, double *t1, double *t4) {
 RqCtx *rq_ctx_new(const RqModel *m, int nb_max, int max_ctx, int *err) {
     int e = RQ_ERR_NOMEM;
     RqCtx *c = NULL;
-    if (!m) { e = RQ_ERR_STATE; goto fail; }
+    if (!m || !m->has_weights) { e = RQ_ERR_STATE; goto fail; } /* (forward.c:152: a tokenizer-only model) */
     c = calloc(1, sizeof(RqCtx));
     if (!c) goto fail;
     c->m = m;
@@ -862,7 +863,8 @@ int gw_decode_greedy(RqCtx *c, RqSeq *s, int token, int n, int *tokens) {
      * tokens[i] = the first maximum of step i's logits, the token step i + 1 is fed. The token of each step stays on the
      * device (the argmax kernel writes it where the next step's embedding reads it), so the n passes are enqueued
      * without waiting for each other and the host waits once. The same kernels and results as n gw_decode_argmax calls;
-     * a model outside the fused decode shapes runs exactly those calls */
+     * a model outside the fused decode shapes, or a sequence whose cache k_attn_decode does not read (f32, quantized,
+     * dot-product: their attention is k_attn_q's), runs exactly those calls */
     c->err[0] = 0;
     int e = check_seq(c, s);
     if (e != RQ_OK) return e;
@@ -871,7 +873,7 @@ int gw_decode_greedy(RqCtx *c, RqSeq *s, int token, int n, int *tokens) {
     if (token < 0 || token >= m->vocab) return ctx_fail(c, RQ_ERR_ARG, "token %d out of range", token);
     if (s->len + n > s->cap) return ctx_fail(c, RQ_ERR_CONTEXT, "%d steps at position %d: past the capacity %d", n, s->len, s->cap);
     int hd = m->head_dim;
-    if (!(fused_shape(m) && (hd == 128 || hd == 64 || hd == 32))) {
+    if (!(fused_shape(m) && (hd == 128 || hd == 64 || hd == 32)) || gw_kv_att_q(s->kvt)) {
         for (int i = 0; i < n; i++) {
             if ((e = gw_decode_argmax(c, s, i ? tokens[i - 1] : token, &tokens[i])) != RQ_OK) return e;
         }

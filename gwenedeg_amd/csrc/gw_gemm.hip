@@ -46,8 +46,9 @@ __global__ __launch_bounds__(256) void k_q8_block_sums(int32_t *__restrict__ isu
     isum[i] = s;
 }
 
-// pseudo-random f16 K (|K| < 4) and V (|V| < 1) values, for timing runs (rq_seq_fill_synthetic)
-__global__ __launch_bounds__(256) void k_fill_synthetic(uint16_t *kc, uint16_t *vc, size_t n, unsigned long long seed) {
+// pseudo-random 16-bit K (|K| < 4) and V (|V| < 1) values, for timing runs (rq_seq_fill_synthetic): f16, or bf16 (bf:
+// the bf16 and bf16-dot caches; every element drawn alike, so any tile layout holds the same distribution)
+__global__ __launch_bounds__(256) void k_fill_synthetic(uint16_t *kc, uint16_t *vc, size_t n, unsigned long long seed, int bf) {
     size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
     unsigned long long z = seed + i * 0x9e3779b97f4a7c15ull;
@@ -55,8 +56,9 @@ __global__ __launch_bounds__(256) void k_fill_synthetic(uint16_t *kc, uint16_t *
     z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
     z ^= z >> 31;
     float a = (float)(z & 0xffffff) * (1.0f / 16777216.0f), b = (float)((z >> 24) & 0xffffff) * (1.0f / 16777216.0f);
-    kc[i] = __half_as_ushort(__float2half((2.0f * a - 1.0f) * 3.9f));
-    vc[i] = __half_as_ushort(__float2half((2.0f * b - 1.0f) * 0.99f));
+    const float k = (2.0f * a - 1.0f) * 3.9f, v = (2.0f * b - 1.0f) * 0.99f;
+    kc[i] = bf ? f2bf_ref(k) : __half_as_ushort(__float2half(k));
+    vc[i] = bf ? f2bf_ref(v) : __half_as_ushort(__float2half(v));
 }
 
 // ------------------------------------------------------------------------------------- Q8_0 MFMA GEMM
@@ -1450,9 +1452,9 @@ int gw_k_q8_unpack(const uint8_t *blocks, size_t nblk, int8_t *codes, uint16_t *
     return (int)hipGetLastError();
 }
 
-int gw_k_fill_synthetic(uint16_t *kc, uint16_t *vc, size_t n, unsigned long long seed, hipStream_t s) {
+int gw_k_fill_synthetic(uint16_t *kc, uint16_t *vc, size_t n, unsigned long long seed, int bf, hipStream_t s) {
     if (!n) return 0;
-    hipLaunchKernelGGL(k_fill_synthetic, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, kc, vc, n, seed);
+    hipLaunchKernelGGL(k_fill_synthetic, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, kc, vc, n, seed, bf);
     return (int)hipGetLastError();
 }
 

@@ -104,6 +104,25 @@ typedef struct { /* Config (internal.h:72-86): the first 48 bytes of the referen
         shared_classifier, group_size;
 } GwRefConfig;
 
+/* Tokenizer (internal.h:207-224): built in place by the host's tokenizer.o (build_tokenizer_gguf), read by its
+ * rq_tokenize / rq_token_bytes / rq_detok_* and by chat.c; this library reads bos / eos (rq_model_info) only */
+typedef struct {
+    char **vocab;
+    int *vocab_len;
+    float *merge_scores;
+    int vocab_size;
+    unsigned int max_token_length, bos_token_id, eos_token_id;
+    char *vocab_data;
+    int32_t *hash_ids;
+    uint32_t *hash_tags;
+    uint32_t hash_mask;
+    int byte_token[256];
+    int *added;
+    int n_added;
+    unsigned char added_first[256];
+    int marks35;
+} GwRefTokenizer;
+
 #define GW_REF_MODEL_BYTES 9208
 #define GW_REF_SEQ_BYTES 1832
 
@@ -111,18 +130,22 @@ struct RqModel {
     /* the reference's prefix (the readers: spec.c:32-54 config.vocab_size, :271-326 config.dim, :48 has_tok, :219 hy.on,
      * :292-330 mtp_of; sampler.c:328-331 samp_*; chat.c:38-295 chat, has_tok, the templates; tokenizer.c:812 has_tok) */
     GwRefConfig config;            /* @0: this model's shape, group_size 32 */
-    unsigned char ref0_[1752 - 48];
+    unsigned char ref0_[280 - 48];
+    GwRefTokenizer tok;            /* @280: the host's tokenizer (has_tok), else zero */
+    unsigned char ref0b_[1752 - 1648];
     uint64_t ref_fp;               /* @1752: the file's fingerprint (model.c:949-953) */
-    int has_weights, has_tok, is_gguf; /* @1760: 1, 0 (no tokenizer is built: rq_token_bytes gives "", spec.c's draft
-                                        * check RQ_ERR_STATE, chat.c's functions RQ_ERR_STATE), 1 */
-    unsigned char ref1_[2080 - 1772];
+    int has_weights, has_tok, is_gguf; /* @1760: weights on the device (0: tokenizer_only); the tokenizer built (the
+                                        * host linked tokenizer.o, no_tokenizer 0); 1 */
+    int gs_counted_;               /* @1772: 0 */
+    char warning[256];             /* @1776: a load-time warning (RqModelInfo.warning), or "" */
+    unsigned char ref1_[2080 - 2032];
     int hy_on;                     /* @2080: Hybrid.on, 0 (Qwen3: no linear-attention layers) */
     unsigned char ref2_[2684 - 2084];
-    int chat;                      /* @2684: RQ_CHAT_* 0 */
+    int chat;                      /* @2684: RQ_CHAT_* (gguf_chat_variant of the host's gguf.o; 0 without a tokenizer) */
     unsigned char ref3_[2768 - 2688];
-    float samp_temp, samp_topp;    /* @2768: the file's recommended sampling, none (samp_set 0) */
+    float samp_temp, samp_topp;    /* @2768: the file's recommended sampling (gguf_sampling; none without a tokenizer) */
     int samp_topk, samp_set;
-    char user_tmpl[2][1024], sys_tmpl[2][1024], tmpl_missing[2][1088]; /* @2784, @4832, @6880: empty */
+    char user_tmpl[2][1024], sys_tmpl[2][1024], tmpl_missing[2][1088]; /* @2784, @4832, @6880: the chat templates */
     const RqModel *mtp_of;         /* @9056: NULL (not an MTP view) */
     unsigned char ref4_[GW_REF_MODEL_BYTES - 9064];
     /* this library's own */
@@ -164,9 +187,17 @@ struct RqSeq {
                         * types: n_layers x kv_len / 16 x n_kv tiles of gw_kv_tile_bytes each, in the same tile order */
 };
 
+/* gw_host.c: model.c's host side (the tokenizer through the host's tokenizer.o / gguf.o, the chat templates) */
+int gw_host_tokenizer_linked(void);
+int gw_host_tokenizer(RqModel *m, const char *path, const void *map, size_t size, char *err, size_t errlen);
+void gw_host_free_tokenizer(RqModel *m);
+
 #ifndef __cplusplus
 _Static_assert(sizeof(GwRefConfig) == 48, "Config");
-_Static_assert(offsetof(struct RqModel, ref_fp) == 1752 && offsetof(struct RqModel, has_tok) == 1764 &&
+_Static_assert(sizeof(GwRefTokenizer) == 1368 && offsetof(GwRefTokenizer, bos_token_id) == 32 &&
+               offsetof(GwRefTokenizer, n_added) == 1104, "Tokenizer: the reference's layout");
+_Static_assert(offsetof(struct RqModel, tok) == 280 && offsetof(struct RqModel, warning) == 1776 &&
+               offsetof(struct RqModel, ref_fp) == 1752 && offsetof(struct RqModel, has_tok) == 1764 &&
                offsetof(struct RqModel, hy_on) == 2080 && offsetof(struct RqModel, chat) == 2684 &&
                offsetof(struct RqModel, samp_temp) == 2768 && offsetof(struct RqModel, samp_set) == 2780 &&
                offsetof(struct RqModel, user_tmpl) == 2784 && offsetof(struct RqModel, sys_tmpl) == 4832 &&
@@ -296,7 +327,7 @@ int gw_k_topk_noalloc(const float *lg, int n, int ld, int rows, int k, float **v
 /* GGUF Q8_0 blocks (gpr per row) -> codes + scales; il > 0: source row i to row (i / il) 2 il + off + i % il (two
  * matrices interleaved in blocks of il rows) */
 int gw_k_q8_unpack(const uint8_t *blocks, size_t nblk, int8_t *codes, uint16_t *scales, int gpr, int il, int off, hipStream_t s);
-int gw_k_fill_synthetic(uint16_t *kc, uint16_t *vc, size_t n, unsigned long long seed, hipStream_t s);
+int gw_k_fill_synthetic(uint16_t *kc, uint16_t *vc, size_t n, unsigned long long seed, int bf, hipStream_t s);
 /* the quantized caches' synthetic rows (|K| < 4, |V| < 1 before the rotation): positions 0 .. npos - 1 of one layer's K
  * and V caches (kc / vc: the layer's bases), stored as k_qknorm_rope_store stores them */
 int gw_k_fill_synthetic_q(void *kc, void *vc, int kvt, int npos, int nkv, int hd, unsigned long long seed, hipStream_t s);

@@ -420,55 +420,9 @@ __device__ __forceinline__ void attn_q_body(const int4 it, const float *__restri
         }
     }
     __syncthreads();
-    // 2. scores. DOT, up to 4 vectors (decode rows): thread per (position, chunk of 32 dims), the 4 vectors' chunk
-    // chains into S (chunk 0 at S[v], chunk c > 0 at S[4 + 4 (c - 1) + v]: rows S has free), then per (vector,
-    // position) a = ((c0 + c1) + c2) + c3, times scale, as the chain below adds them (for the fp32 types the extra
-    // barrier and LDS round trip cost more than the shorter chains gain)
-    constexpr bool split = DOT && NQM == 16;
-    if (split && nq <= 4) {
-        for (int k = t; k < ng * ATT_P; k += AQ_T) {
-            const int c = k / ATT_P, p = k % ATT_P;
-            int reach = 0;
-            #pragma unroll
-            for (int u = 0; u < 4; u++)
-                if (u < nq) reach = npos(u) > reach ? npos(u) : reach;
-            if (p >= reach) continue;
-            const uint8_t *tb = kt0 + (size_t)(p / ATT_T) * tbk;
-            const int j = p % ATT_T;
-            float cc[4] = { 0.0f, 0.0f, 0.0f, 0.0f };
-            if (DOT) {
-                for (int i = 32 * c; i < 32 * c + 32; i += 2) {
-                    const float k1 = value(tb, i + 1, j, false), k0 = value(tb, i, j, false);
-                    const float4 q1 = *(const float4 *)(qs + (i + 1) * NQM), q0 = *(const float4 *)(qs + i * NQM);
-                    const float q1v[4] = { q1.x, q1.y, q1.z, q1.w }, q0v[4] = { q0.x, q0.y, q0.z, q0.w };
-                    #pragma unroll
-                    for (int u = 0; u < 4; u++) cc[u] = fma_fz(q0v[u], k0, fma_fz(q1v[u], k1, cc[u]));
-                }
-            } else {
-                for (int i = 32 * c; i < 32 * c + 32; i++) {
-                    const float kv = value(tb, i, j, false);
-                    const float4 q = *(const float4 *)(qs + i * NQM);
-                    cc[0] = __builtin_fmaf(q.x, kv, cc[0]);
-                    cc[1] = __builtin_fmaf(q.y, kv, cc[1]);
-                    cc[2] = __builtin_fmaf(q.z, kv, cc[2]);
-                    cc[3] = __builtin_fmaf(q.w, kv, cc[3]);
-                }
-            }
-            #pragma unroll
-            for (int u = 0; u < 4; u++) S[c ? 4 + 4 * (c - 1) + u : u][p] = cc[u];
-        }
-        __syncthreads();
-        for (int k = t; k < nq * ATT_P; k += AQ_T) {
-            const int v = k / ATT_P, p = k % ATT_P;
-            if (p >= npos(v)) continue;
-            float a = S[v][p];
-            for (int c = 1; c < ng; c++) a = DOT ? ftz_f(a + S[4 + 4 * (c - 1) + v][p]) : a + S[4 + 4 * (c - 1) + v][p];
-            S[v][p] = DOT ? ftz_f(a * scale) : a * scale;
-        }
-    }
-    // Otherwise: thread per (position, group of 4 vectors): each K value read once for the group's 4 chains
+    // 2. scores: thread per (position, group of 4 vectors): each K value read once for the group's 4 chains
     // (vectors past nq, or positions past a vector's reach, computed on whatever LDS holds and not stored)
-    for (int k = t; k < (split && nq <= 4 ? 0 : (nq + 3) / 4 * ATT_P); k += AQ_T) {
+    for (int k = t; k < (nq + 3) / 4 * ATT_P; k += AQ_T) {
         const int v0 = 4 * (k / ATT_P), p = k % ATT_P;
         int reach = 0;
         #pragma unroll

@@ -432,6 +432,7 @@ static void free_mat(GwMat *w) {
 
 void rq_model_free(RqModel *m) {
     if (!m) return;
+    gw_host_free_tokenizer(m);
     if (m->layer)
         for (int l = 0; l < m->n_layers; l++) {
             for (int i = 0; i < 3; i++) free_mat(&m->layer[l].qkv[i]);
@@ -478,7 +479,11 @@ RqModel *rq_model_load(const char *path, const RqModelOpts *o, char *err, size_t
     RqModelOpts opts;
     memset(&opts, 0, sizeof opts);
     if (o) opts = *o;
-    if (gw_device_init(err, errlen) != RQ_OK || gw_exact_init(err, errlen) != RQ_OK) return NULL;
+    if (opts.tokenizer_only && !gw_host_tokenizer_linked()) {
+        snprintf(err, errlen, "tokenizer_only: the program does not link the tokenizer (tokenizer.o, gguf.o, threads.o)");
+        return NULL;
+    }
+    if (!opts.tokenizer_only && (gw_device_init(err, errlen) != RQ_OK || gw_exact_init(err, errlen) != RQ_OK)) return NULL;
     Loader L;
     memset(&L, 0, sizeof L);
     L.err = err;
@@ -554,6 +559,12 @@ RqModel *rq_model_load(const char *path, const RqModelOpts *o, char *err, size_t
     m->log_theta = (float)log((double)theta);
     m->att_scale = gw_rsqrt_host((float)hd); /* forward.c:137 as compiled: 1.0f / sqrtf(head_dim) */
     m->fingerprint = fingerprint(L.g.map, L.g.size);
+    /* the reference's view of the model (its host modules read these: the layout note in gw_internal.h) */
+    m->config = (GwRefConfig){ 0, 0, m->dim, m->hidden, m->n_layers, m->n_heads, m->n_kv_heads, m->vocab, m->seq_len,
+                               m->head_dim, m->tied, 32 };
+    m->ref_fp = m->fingerprint;
+    m->is_gguf = 1;
+    if (opts.tokenizer_only) goto tokenizer;
     /* device staging: the largest tensor */
     size_t big = 0;
     for (uint64_t i = 0; i < L.g.nt; i++)
@@ -637,12 +648,15 @@ RqModel *rq_model_load(const char *path, const RqModelOpts *o, char *err, size_t
         if (rc != RQ_OK) goto out;
     }
     hipGetDevice(&m->device);
-    /* the reference's view of the model (its host modules read these: the layout note in gw_internal.h) */
-    m->config = (GwRefConfig){ 0, 0, m->dim, m->hidden, m->n_layers, m->n_heads, m->n_kv_heads, m->vocab, m->seq_len,
-                               m->head_dim, m->tied, 32 };
-    m->ref_fp = m->fingerprint;
     m->has_weights = 1;
-    m->is_gguf = 1;
+tokenizer:
+    /* model.c:1010-1016: the tokenizer unless no_tokenizer (the host's tokenizer.o / gguf.o, gw_host.c) */
+    if (!opts.no_tokenizer) {
+        if (gw_host_tokenizer_linked()) rc = gw_host_tokenizer(m, path, L.g.map, L.g.size, err, errlen);
+        else
+            snprintf(m->warning, sizeof m->warning, "no tokenizer: the program does not link tokenizer.o / gguf.o "
+                                                    "(token ids only, as RqModelOpts.no_tokenizer)");
+    }
 out:
     if (L.stage) hipFree(L.stage);
     free(L.g.kv);
@@ -670,8 +684,10 @@ void rq_model_info(const RqModel *m, RqModelInfo *info) {
     info->group_size = 32;
     info->shared_classifier = m->tied;
     info->gguf = 1;
-    info->bos = -1;
-    info->eos = -1;
+    info->bos = m->has_tok ? (int)m->tok.bos_token_id : -1;
+    info->eos = m->has_tok ? (int)m->tok.eos_token_id : -1;
+    info->warning = m->warning[0] ? m->warning : NULL;
+    info->chat = m->chat;
     info->rope_theta = m->rope_theta;
     info->fingerprint = m->fingerprint;
 }

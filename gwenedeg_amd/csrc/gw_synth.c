@@ -3,8 +3,9 @@
  * Every matmul tensor is N(0, std) before quantization (std 0.02), the norms are a constant (1.0), the
  * metadata is what the reference's GGUF reader checks for a qwen3 file (gguf.c:230-336: block_count,
  * embedding_length, feed_forward_length, head counts, context_length, key/value length, rope.freq_base,
- * layer_norm_rms_epsilon 1e-6) and the tensor names are llama.cpp's (model.c:269-299). No tokenizer
- * block: readers load these files without a tokenizer (RqModelOpts.no_tokenizer).
+ * layer_norm_rms_epsilon 1e-6) and the tensor names are llama.cpp's (model.c:269-299). A tokenizer block only where
+ * cfg->tokenizer asks for one (a small byte-level BPE vocabulary, below); without it readers load the file without a
+ * tokenizer (RqModelOpts.no_tokenizer).
  *
  * Values: row r of tensor t draws from its own splitmix64 stream seeded by (seed, t, r), Box-Muller in
  * double precision, so a file is a pure function of (shape, types, seed) whatever the thread count.
@@ -342,6 +343,146 @@ static void kv_u32(W *w, const char *k, uint32_t v) { w_str(w, k); w_u32(w, 4 /*
 static void kv_f32(W *w, const char *k, float v) { w_str(w, k); w_u32(w, 6 /* GV_F32 */); w_bytes(w, &v, 4); }
 static void kv_s(W *w, const char *k, const char *v) { w_str(w, k); w_u32(w, 8 /* GV_STR */); w_str(w, v); }
 
+/* ------------------------------------------------------------------------- synthetic tokenizer (cfg->tokenizer) */
+
+/* A small byte-level BPE vocabulary in the form llama.cpp's "gpt2" model with the "qwen2" pre-tokenizer stores it (the
+ * metadata the reference's build_tokenizer_gguf reads, tokenizer.c:201-320): ids 0..255 the single bytes; then, for
+ * a fixed list of English words, with and without a leading space, each word's prefixes of two bytes and more, each
+ * made by the merge (its prefix one byte shorter, its last byte), merges in that order; then the added tokens
+ * (ChatML's control tokens and the think tags). Token strings and merges are in GPT-2's byte-to-unicode form. */
+
+static int gpt2_printable(int b) { return (b >= 33 && b <= 126) || (b >= 161 && b <= 172) || (b >= 174 && b <= 255); }
+
+static size_t gpt2_form(const unsigned char *p, size_t n, char *o) {
+    /* GPT-2's map: a printable byte stands for its own code point, the other 68 bytes for 256, 257, .. in byte order;
+     * UTF-8 encoded */
+    size_t k = 0;
+    for (size_t i = 0; i < n; i++) {
+        int b = p[i], cp = b;
+        if (!gpt2_printable(b)) {
+            cp = 256;
+            for (int x = 0; x < b; x++) cp += !gpt2_printable(x);
+        }
+        if (cp < 0x80) o[k++] = (char)cp;
+        else {
+            o[k++] = (char)(0xc0 | (cp >> 6));
+            o[k++] = (char)(0x80 | (cp & 63));
+        }
+    }
+    o[k] = 0;
+    return k;
+}
+
+typedef struct {
+    char **tok;     /* GPT-2 form of each token */
+    int32_t *type;  /* 1 normal, 3 control, 4 user-defined */
+    char **merge;   /* "left right", rank order */
+    int n_tok, n_merge, eos;
+} SynTok;
+
+static const char *const syn_words[] = {
+    "the", "and", "of", "to", "in", "is", "it", "you", "that", "was", "for", "on", "are", "with", "as", "this", "be",
+    "at", "have", "from", "or", "one", "had", "by", "word", "but", "not", "what", "all", "were", "we", "when", "your",
+    "can", "said", "there", "use", "an", "each", "which", "she", "do", "how", "their", "if", "will", "up", "other",
+    "about", "out", "many", "then", "them", "these", "so", "some", "her", "would", "make", "like", "him", "into",
+    "time", "has", "look", "two", "more", "write", "go", "see", "number", "no", "way", "could", "people", "my",
+    "than", "first", "water", "been", "call", "who", "its", "now", "find", "long", "down", "day", "did", "get",
+    "come", "made", "may", "part", "hello", "world", "answer", "question", "model", "token", "user", "assistant",
+    "system", "think", "Hello", "The", "What", "Why", "12", "42", "2024", "\n\n", "  ", "...", ", ",
+};
+
+static void syn_tok_free(SynTok *t) {
+    for (int i = 0; i < t->n_tok; i++) free(t->tok[i]);
+    for (int i = 0; i < t->n_merge; i++) free(t->merge[i]);
+    free(t->tok);
+    free(t->type);
+    free(t->merge);
+    memset(t, 0, sizeof *t);
+}
+
+static int syn_tok_build(SynTok *t, int vocab) {
+    /* -1: the vocabulary is too small (256 bytes + the added tokens) or no memory */
+    static const char *const added[] = { "<|endoftext|>", "<|im_start|>", "<|im_end|>", "<think>", "</think>" };
+    const int n_added = 5;
+    if (vocab < 256 + n_added) return -1;
+    memset(t, 0, sizeof *t);
+    t->tok = calloc((size_t)vocab, sizeof(char *));
+    t->type = calloc((size_t)vocab, sizeof(int32_t));
+    t->merge = calloc((size_t)vocab, sizeof(char *));
+    unsigned char **raw = calloc((size_t)vocab, sizeof(unsigned char *)); /* raw bytes of the regular tokens */
+    int *rawn = calloc((size_t)vocab, sizeof(int));
+    if (!t->tok || !t->type || !t->merge || !raw || !rawn) goto fail;
+    char g[512];
+    for (int b = 0; b < 256; b++) {
+        unsigned char c = (unsigned char)b;
+        gpt2_form(&c, 1, g);
+        raw[b] = malloc(1);
+        if (!(t->tok[b] = strdup(g)) || !raw[b]) goto fail;
+        raw[b][0] = c;
+        rawn[b] = 1;
+        t->type[b] = 1;
+    }
+    int n = 256;
+    for (size_t wi = 0; wi < sizeof syn_words / sizeof syn_words[0]; wi++)
+        for (int sp = 0; sp < 2; sp++) {
+            unsigned char w[64];
+            int len = 0;
+            if (sp) w[len++] = ' ';
+            for (const char *q = syn_words[wi]; *q && len < 60; q++) w[len++] = (unsigned char)*q;
+            for (int k = 2; k <= len && n < vocab - n_added; k++) {
+                int have = 0;
+                for (int i = 256; i < n && !have; i++) have = rawn[i] == k && !memcmp(raw[i], w, (size_t)k);
+                if (have) continue;
+                char a[256], c[16];
+                gpt2_form(w, (size_t)(k - 1), a);
+                gpt2_form(w + k - 1, 1, c);
+                snprintf(g, sizeof g, "%s %s", a, c);
+                if (!(t->merge[t->n_merge] = strdup(g))) goto fail;
+                t->n_merge++;
+                gpt2_form(w, (size_t)k, g);
+                if (!(t->tok[n] = strdup(g)) || !(raw[n] = malloc((size_t)k))) goto fail;
+                memcpy(raw[n], w, (size_t)k);
+                rawn[n] = k;
+                t->type[n++] = 1;
+            }
+        }
+    for (int i = 0; i < n_added; i++) {
+        if (!(t->tok[n] = strdup(added[i]))) goto fail;
+        t->type[n] = i < 3 ? 3 : 4;
+        if (i == 2) t->eos = n;
+        n++;
+    }
+    t->n_tok = n;
+    for (int i = 0; i < vocab; i++) free(raw[i]);
+    free(raw);
+    free(rawn);
+    return 0;
+fail:
+    if (raw)
+        for (int i = 0; i < vocab; i++) free(raw[i]);
+    free(raw);
+    free(rawn);
+    t->n_tok = vocab; /* (free every slot) */
+    syn_tok_free(t);
+    return -1;
+}
+
+static void kv_arr_s(W *w, const char *k, char *const *v, int n) {
+    w_str(w, k);
+    w_u32(w, 9 /* GV_ARR */);
+    w_u32(w, 8 /* GV_STR */);
+    w_u64(w, (uint64_t)n);
+    for (int i = 0; i < n; i++) w_str(w, v[i]);
+}
+
+static void kv_arr_i32(W *w, const char *k, const int32_t *v, int n) {
+    w_str(w, k);
+    w_u32(w, 9 /* GV_ARR */);
+    w_u32(w, 5 /* GV_I32 */);
+    w_u64(w, (uint64_t)n);
+    w_bytes(w, v, (size_t)n * 4);
+}
+
 typedef struct {
     const SynTensor *t;
     int tindex;
@@ -405,15 +546,18 @@ int gw_synth_gguf(const char *path, const GwSynthCfg *c, unsigned long long seed
         uint64_t sz = T[i].rows ? (uint64_t)T[i].rows * gw_synth_row_bytes(T[i].type, T[i].cols) : (uint64_t)T[i].cols * 4;
         off += (sz + align - 1) / align * align;
     }
+    SynTok tk;
+    memset(&tk, 0, sizeof tk);
+    if (c->tokenizer && syn_tok_build(&tk, c->vocab)) { free(T); return -1; }
     FILE *f = fopen(path, "wb");
-    if (!f) { free(T); return -3; }
+    if (!f) { free(T); syn_tok_free(&tk); return -3; }
     static char buf[1 << 22];
     setvbuf(f, buf, _IOFBF, sizeof buf);
     W w = { f, 0 };
     w_u32(&w, 0x46554747u);
     w_u32(&w, 3);
     w_u64(&w, (uint64_t)nt);
-    w_u64(&w, 13);
+    w_u64(&w, c->tokenizer ? 20 : 13);
     kv_s(&w, "general.architecture", "qwen3");
     kv_u32(&w, "general.alignment", (uint32_t)align);
     kv_u32(&w, "qwen3.block_count", (uint32_t)L);
@@ -427,6 +571,20 @@ int gw_synth_gguf(const char *path, const GwSynthCfg *c, unsigned long long seed
     kv_f32(&w, "qwen3.rope.freq_base", c->rope_theta > 0 ? c->rope_theta : 1e6f);
     kv_f32(&w, "qwen3.attention.layer_norm_rms_epsilon", 1e-6f);
     kv_s(&w, "general.name", "gwenedeg-amd synthetic");
+    if (c->tokenizer) {
+        kv_s(&w, "tokenizer.ggml.model", "gpt2");
+        kv_s(&w, "tokenizer.ggml.pre", "qwen2");
+        kv_arr_s(&w, "tokenizer.ggml.tokens", tk.tok, tk.n_tok);
+        kv_arr_i32(&w, "tokenizer.ggml.token_type", tk.type, tk.n_tok);
+        kv_arr_s(&w, "tokenizer.ggml.merges", tk.merge, tk.n_merge);
+        kv_u32(&w, "tokenizer.ggml.eos_token_id", (uint32_t)tk.eos);
+        /* (a ChatML template with enable_thinking: Qwen3's hybrid variant) */
+        kv_s(&w, "tokenizer.chat_template",
+             "{%- for message in messages %}{{- '<|im_start|>' + message.role + '\\n' + message.content + '<|im_end|>' + "
+             "'\\n' }}{%- endfor %}{%- if add_generation_prompt %}{{- '<|im_start|>assistant\\n' }}{%- if enable_thinking "
+             "is defined and enable_thinking is false %}{{- '<think>\\n\\n</think>\\n\\n' }}{%- endif %}{%- endif %}");
+        syn_tok_free(&tk);
+    }
     for (int i = 0; i < nt; i++) {
         w_str(&w, T[i].name);
         if (T[i].rows) {

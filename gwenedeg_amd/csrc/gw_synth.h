@@ -14,6 +14,7 @@ typedef struct {
     int type_embd, type_out, type_q, type_k, type_v, type_o, type_gate, type_up, type_down; /* 0: type_default */
     float std;         /* 0: 0.02 */
     float norm_value;  /* 0: 1.0 */
+    int tokenizer;     /* 1: a tokenizer block (byte-level BPE, gpt2 / qwen2, ChatML added tokens) */
 } GwSynthCfg;
 /* 0 on success; -1 bad shape, -2 no memory, -3 I/O, -4 threads */
 int gw_synth_gguf(const char *path, const GwSynthCfg *cfg, unsigned long long seed, int nthreads);

@@ -20,7 +20,7 @@ class GwSynthCfg(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in "dim hidden n_layers n_heads n_kv_heads head_dim vocab ctx_len".split()] + \
         [("rope_theta", ctypes.c_float), ("tied", ctypes.c_int), ("type_default", ctypes.c_int)] + \
         [(n, ctypes.c_int) for n in "type_embd type_out type_q type_k type_v type_o type_gate type_up type_down".split()] + \
-        [("std", ctypes.c_float), ("norm_value", ctypes.c_float)]
+        [("std", ctypes.c_float), ("norm_value", ctypes.c_float), ("tokenizer", ctypes.c_int)]
 
 
 SHAPES = {
@@ -53,6 +53,9 @@ SHAPES = {
                      ctx_len=4096, tied=0, type_default=Q2_K, type_v=Q4_K, type_out=Q6_K),
     # head sizes below 128: 8 query heads on one KV head (hd 64), plain multi-head attention (hd 32)
     "tiny_hd64": dict(dim=256, hidden=512, n_layers=2, n_heads=8, n_kv_heads=1, head_dim=64, vocab=1000, ctx_len=4096,
+                      tied=1, type_default=Q8_0),
+    # 16 query heads on one KV head (hd 64): the attention's items of more than 8 query vectors per row
+    "tiny_kv16": dict(dim=256, hidden=512, n_layers=2, n_heads=16, n_kv_heads=1, head_dim=64, vocab=1024, ctx_len=4096,
                       tied=1, type_default=Q8_0),
     "tiny_hd32": dict(dim=256, hidden=768, n_layers=2, n_heads=8, n_kv_heads=8, head_dim=32, vocab=1000, ctx_len=4096,
                       tied=0, type_default=Q8_0),

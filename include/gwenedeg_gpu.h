@@ -46,8 +46,10 @@ typedef struct RqCtx RqCtx;
 
 #define RQ_CTX_DEFAULT_MAX 40960 /* runq.h:61 */
 
-/* runq.h:63-81 (same layout; tokenizer_only / page_cache / checkpoints / repack are accepted and ignored here: no
- * tokenizer is built by this library, Qwen3 has no recurrent state, the device layouts are fixed) */
+/* runq.h:63-81 (same layout). tokenizer_only and no_tokenizer as the reference (model.c:1010-1016, :893-922): the
+ * tokenizer is built by the host's own tokenizer.o / gguf.o when the program links them (rq_chat_check below);
+ * page_cache / checkpoints / repack are accepted and ignored here: the file is read once, Qwen3 has no recurrent
+ * state, the device layouts are fixed */
 typedef struct {
     int ctx_len;
     int tokenizer_only;
@@ -59,9 +61,20 @@ typedef struct {
     int repack;
 } RqModelOpts;
 
-/* runq.h:87-88: a GGUF file (qwen3; Q8_0, Q2_K .. Q6_K, IQ4_XS matrices), its weights repacked into device memory */
+/* runq.h:87-88: a GGUF file (qwen3; Q8_0, Q2_K .. Q6_K, IQ4_XS matrices), its weights repacked into device memory.
+ * Unless opts->no_tokenizer, the tokenizer, chat variant, recommended sampling and chat templates too, where the
+ * program links the reference's tokenizer.o, gguf.o and threads.o (their build entry points are weak references
+ * here); without them the model loads without a tokenizer and RqModelInfo.warning says so. tokenizer_only: no
+ * weights, no device (needs those objects) */
 RqModel *rq_model_load(const char *path, const RqModelOpts *opts, char *err, size_t errlen);
 void rq_model_free(RqModel *m);
+
+/* the chat-template side of model.c that the reference's chat.o, cli.o, serve.o and tools.o call (runq.h:458-459;
+ * model.c:798-862) */
+enum { RQ_CHAT_HYBRID = 0, RQ_CHAT_INSTRUCT = 1, RQ_CHAT_THINKING = 2, RQ_CHAT_QWEN35 = 3, RQ_CHAT_QWEN38 = 4 };
+const char *rq_chat_name(int variant);                                      /* runq.h:459 */
+int rq_chat_check(const RqModel *m, int thinking, char *err, size_t errlen); /* runq.h:502 */
+const char *chat_gen_suffix(const RqModel *m, int thinking);                /* internal.h (model.c:803): chat.o */
 
 /* runq.h:132-147 */
 typedef struct {

@@ -1,10 +1,9 @@
 /* A host program of the reference's own host modules (test infrastructure: tests/test_host_modules.py builds it).
  *
  * It is linked twice from this one source:
- *   ours: libgwenedeg_amd.so (the forward half of runq.h) with the reference's sampler.o, threads.o, spec.o, chat.o,
- *         tokenizer.o and gguf.o compiled unmodified from its sources (oracle/_ref), plus the two model.c helpers
- *         those objects name (below, GW_HOST_STUBS: chat templates and the loader's error exit, never reached without
- *         a tokenizer);
+ *   ours: libgwenedeg_amd.so (the forward half of runq.h, the weight path of model.c and its chat-template helpers)
+ *         with the reference's sampler.o, threads.o, spec.o, chat.o, tokenizer.o and gguf.o compiled unmodified from
+ *         its sources (oracle/_ref);
  *   ref:  the reference's whole CPU library (oracle/_ref: model, gguf, forward, tokenizer, sampler, chat, threads,
  *         spec, seqfile).
  * Both runs print the same JSON only if the reference's modules read this library's RqModel / RqSeq fields and drive
@@ -13,7 +12,16 @@
  * row it samples from) and the speculative loop with prompt lookup (rq_generate_spec, spec.c:404-600: verify passes
  * of several rows through rq_forward_batch, rollbacks by rq_seq_truncate; its output must be rq_generate's).
  *
- *   host_modules MODEL IDS_FILE
+ * With --tok (a model file with a tokenizer block), the model is loaded with its tokenizer, which the library builds
+ * through the host's tokenizer.o / gguf.o at rq_model_load (model.c:1010-1016), and a last section prints what the
+ * text side gives on it: rq_model_info's bos / eos / chat variant, rq_chat_check, rq_tokenize and rq_token_bytes,
+ * rq_chat_render of a conversation in both thinking modes, rq_generate from that prompt (stopping at an end token)
+ * and its reply through rq_detok_push / rq_detok_flush.
+ *
+ * With --tokenizer-only, the model is loaded with RqModelOpts.tokenizer_only (no weights, no device: this mode runs
+ * on any host) and the text side is printed without the reply.
+ *
+ *   host_modules MODEL IDS_FILE [--tok] | MODEL --tokenizer-only
  */
 #include <stdio.h>
 #include <stdlib.h>
@@ -64,21 +72,28 @@ int rq_generate_spec(RqCtx *c, RqSeq *s, RqCtx *dc, RqSeq *ds, const int *tokens
                      int max_new, const RqSpecOpts *o, const RqCallbacks *cb, RqSpecStats *st);
 int rq_spec_check(const RqModel *target, const RqModel *draft, char *err, size_t errlen);
 
-#ifdef GW_HOST_STUBS
-/* model.c's two helpers that chat.o and tokenizer.o name (model.c:12, :803): the chat templates' generation suffix
- * and the loader's error exit. A maintainer keeps them with the chat templates on the host; without a tokenizer
- * (no_tokenizer, these synthetic files) neither is reached */
-const char *chat_gen_suffix(const RqModel *m, int thinking) {
-    (void)m;
-    (void)thinking;
-    return "";
-}
-void load_fail(void *e, const char *fmt, ...) {
-    (void)e;
-    fprintf(stderr, "host_modules: load_fail reached: %s\n", fmt);
-    abort();
-}
-#endif
+/* the tokenizer and chat API (runq.h:408-500), the reference's tokenizer.o and chat.o */
+typedef struct {
+    int *v;
+    int n, cap;
+} RqTokens;
+void rq_tokens_free(RqTokens *t);
+int rq_tokenize(const RqModel *m, const char *text, long len, RqTokens *out);
+const char *rq_token_bytes(const RqModel *m, int token, int *len);
+int rq_is_end_token(const RqModel *m, int token);
+int rq_token_is_added(const RqModel *m, int token);
+typedef struct {
+    unsigned char b[8];
+    int n;
+} RqDetok;
+int rq_detok_push(const RqModel *m, RqDetok *d, int token, char *out, size_t cap);
+int rq_detok_flush(RqDetok *d, char *out, size_t cap);
+enum { RQ_ROLE_SYSTEM = 0, RQ_ROLE_USER = 1, RQ_ROLE_ASSISTANT = 2 };
+typedef struct {
+    int role;
+    const char *content;
+} RqMessage;
+int rq_chat_render(const RqModel *m, const RqMessage *msgs, int n, int thinking, RqTokens *out);
 
 #define MAX_GEN 32
 
@@ -109,6 +124,93 @@ static void print_trace(const Trace *t) {
     printf("]");
 }
 
+static void print_ids(const RqTokens *t) {
+    printf("[");
+    for (int i = 0; i < t->n; i++) printf("%s%d", i ? ", " : "", t->v[i]);
+    printf("]");
+}
+
+static void print_hex(const char *p, int n) {
+    printf("\"");
+    for (int i = 0; i < n; i++) printf("%02x", (unsigned char)p[i]);
+    printf("\"");
+}
+
+static int collect(void *user, int token) {
+    RqTokens *t = user;
+    if (t->n < t->cap) t->v[t->n++] = token;
+    return 0;
+}
+
+static void text_side(RqModel *m, RqCtx *c, RqSeq *s) {
+    /* 5. the tokenizer and the chat templates the library built at rq_model_load, and a chat reply generated from
+     * them (--tok) */
+    char err[512];
+    RqModelInfo mi;
+    rq_model_info(m, &mi);
+    printf(", \"tok\": {\"bos\": %d, \"eos\": %d, \"chat\": \"%s\", \"check\": [%d, %d], \"end\": [%d, %d, %d], "
+           "\"added\": [%d, %d], \"tokenize\": [", mi.bos, mi.eos, rq_chat_name(mi.chat), rq_chat_check(m, 0, err, sizeof err),
+           rq_chat_check(m, 1, err, sizeof err), rq_is_end_token(m, mi.eos), rq_is_end_token(m, mi.bos),
+           rq_is_end_token(m, 300), rq_token_is_added(m, mi.eos), rq_token_is_added(m, 300));
+    static const char *const texts[3] = { "Hello world, the answer is 42.\n\nWhat do you think about the model?",
+                                          "<|im_start|>user\nwhy would you write that?<|im_end|>\n",
+                                          "  the  people   2024 ...  \t\xc3\xa9t\xc3\xa9 \xe2\x82\xac" "5" };
+    for (int k = 0; k < 3; k++) {
+        RqTokens t = { NULL, 0, 0 };
+        int e = rq_tokenize(m, texts[k], -1, &t);
+        printf("%s{\"rc\": %d, \"ids\": ", k ? ", " : "", e);
+        print_ids(&t);
+        char back[512];
+        int nb = 0;
+        for (int i = 0; i < t.n; i++) {
+            int len = 0;
+            const char *b = rq_token_bytes(m, t.v[i], &len);
+            if (nb + len < (int)sizeof back) memcpy(back + nb, b, (size_t)len), nb += len;
+        }
+        printf(", \"round_trip\": %d}", nb == (int)strlen(texts[k]) && !memcmp(back, texts[k], (size_t)nb));
+        rq_tokens_free(&t);
+    }
+    printf("], \"render\": [");
+    const RqMessage conv[4] = { { RQ_ROLE_SYSTEM, "You are a helpful model." }, { RQ_ROLE_USER, "What is the answer?" },
+                                { RQ_ROLE_ASSISTANT, "The answer is 42." }, { RQ_ROLE_USER, "Why would you think that?" } };
+    RqTokens prompt = { NULL, 0, 0 };
+    for (int th = 0; th < 2; th++) {
+        RqTokens t = { NULL, 0, 0 };
+        int e = rq_chat_render(m, conv, 4, th, &t);
+        printf("%s{\"rc\": %d, \"ids\": ", th ? ", " : "", e);
+        print_ids(&t);
+        printf("}");
+        if (!th) prompt = t;
+        else rq_tokens_free(&t);
+    }
+    if (!c) { /* (tokenizer_only: no passes) */
+        printf("]}");
+        rq_tokens_free(&prompt);
+        return;
+    }
+    /* the reply: greedy, until an end token or 24 tokens */
+    static int buf[64];
+    RqTokens reply = { buf, 0, 24 };
+    RqCallbacks cb = { collect, NULL, &reply };
+    RqGenStats gs;
+    memset(&gs, 0, sizeof gs);
+    const RqSampling greedy = { 0.0f, 0.0f, NULL, 0 };
+    rq_seq_reset(s);
+    int e = rq_generate(c, s, prompt.v, prompt.n, &greedy, 24, &cb, &gs);
+    printf("], \"reply\": {\"rc\": %d, \"n_gen\": %d, \"stop\": %d, \"ids\": ", e, gs.n_gen, gs.stop);
+    print_ids(&reply);
+    char text[4096];
+    int nt = 0;
+    RqDetok d;
+    memset(&d, 0, sizeof d);
+    for (int i = 0; i < reply.n; i++) nt += rq_detok_push(m, &d, reply.v[i], text + nt, sizeof text - (size_t)nt);
+    nt += rq_detok_flush(&d, text + nt, sizeof text - (size_t)nt);
+    printf(", \"text\": ");
+    print_hex(text, nt);
+    printf("}}");
+    rq_tokens_free(&prompt);
+}
+
 #include <stddef.h>
 static void layouts(void) {
     /* the sizes and offsets of the API types declared above (no device work: the CPU check of the declarations) */
@@ -120,6 +222,8 @@ static void layouts(void) {
     L(RqSpecOpts, cost); L(RqSpecOpts, dcost); L(RqSpecOpts, guess_hook); L(RqSpecOpts, hook_user); L(RqSpecOpts, prior);
     L(RqSpecStats, passes); L(RqSpecStats, refed); L(RqSpecStats, t_draft); L(RqSpecStats, t_verify);
     L(RqSpecStats, lookup_passes); L(RqSpecStats, lookup_accepted); L(RqSpecStats, mtp_approx);
+    printf("RqTokens %zu\nRqDetok %zu\nRqMessage %zu\n", sizeof(RqTokens), sizeof(RqDetok), sizeof(RqMessage));
+    L(RqTokens, n); L(RqTokens, cap); L(RqDetok, n); L(RqMessage, content);
 #undef L
 }
 
@@ -128,10 +232,32 @@ int main(int argc, char **argv) {
         layouts();
         return 0;
     }
-    if (argc != 3) {
-        fprintf(stderr, "usage: %s MODEL IDS_FILE | --layouts\n", argv[0]);
+    if (argc == 3 && !strcmp(argv[2], "--tokenizer-only")) {
+        /* the header and the tokenizer only (RqModelOpts.tokenizer_only, model.c:893-922): no weights, no device; a
+         * context or a sequence of it is refused (RQ_ERR_STATE) */
+        char err[512] = "";
+        RqModelOpts mo;
+        memset(&mo, 0, sizeof mo);
+        mo.tokenizer_only = 1;
+        RqModel *m = rq_model_load(argv[1], &mo, err, sizeof err);
+        if (!m) {
+            printf("{\"load\": \"%s\"}\n", err);
+            return 0;
+        }
+        int ec = 0, es = 0;
+        RqCtx *c = rq_ctx_new(m, 1, 64, &ec);
+        RqSeq *q = rq_seq_new(m, 64, RQ_KV_F16, &es);
+        printf("{\"ctx\": [%d, %d], \"seq\": [%d, %d]", c != NULL, ec, q != NULL, es);
+        text_side(m, NULL, NULL);
+        printf("}\n");
+        rq_model_free(m);
+        return 0;
+    }
+    if (argc != 3 && !(argc == 4 && !strcmp(argv[3], "--tok"))) {
+        fprintf(stderr, "usage: %s MODEL IDS_FILE [--tok] | --layouts\n", argv[0]);
         return 2;
     }
+    const int tok = argc == 4;
     FILE *f = fopen(argv[2], "rb");
     if (!f) { perror(argv[2]); return 1; }
     fseek(f, 0, SEEK_END);
@@ -145,7 +271,7 @@ int main(int argc, char **argv) {
     RqModelOpts mo;
     memset(&mo, 0, sizeof mo);
     mo.ctx_len = 512;
-    mo.no_tokenizer = 1;
+    mo.no_tokenizer = !tok;
     mo.mem = -1.0;
     RqModel *m = rq_model_load(argv[1], &mo, err, sizeof err);
     if (!m) { fprintf(stderr, "host_modules: load: %s\n", err); return 1; }
@@ -228,8 +354,11 @@ int main(int argc, char **argv) {
         printf("}}");
     }
     printf("], ");
-    /* 4. a draft model without its tokenizer is refused (spec.c:48: RQ_ERR_STATE), as the reference refuses it */
-    printf("\"spec_check\": %d}\n", rq_spec_check(m, m, err, sizeof err));
+    /* 4. a draft model without its tokenizer is refused (spec.c:48: RQ_ERR_STATE), as the reference refuses it; with
+     * the tokenizers of two models of one vocabulary it is accepted */
+    printf("\"spec_check\": %d", rq_spec_check(m, m, err, sizeof err));
+    if (tok) text_side(m, c, s[3]);
+    printf("}\n");
     free(rows);
     free(row);
     free(ids);

@@ -116,18 +116,27 @@ def test_one_hip_runtime_per_process():
 
 
 # What each of the reference's host modules still needs once libgwenedeg_amd.so replaces its model.o, gguf.o, forward.o
-# and seqfile.o (and gguf.o is kept for the tokenizer): the functions outside the hot path that stay with the host
-# (model.c's chat templates and load error helper). Everything else on the reference's
-# runq.h / internal.h surface those modules call resolves to the library.
+# and seqfile.o (gguf.o is kept for the tokenizer): nothing. model.c's chat templates (rq_chat_name, rq_chat_check,
+# chat_gen_suffix) and its load error exit (load_fail) are the library's too (gw_host.c); everything else on the
+# reference's runq.h / internal.h surface those modules call resolves to the library.
 HOST_NEEDS = {
     "sampler": set(), "threads": set(), "spec": set(), "constrain": set(), "http": set(), "json": set(),
-    "chat": {"chat_gen_suffix"},
-    "tokenizer": {"load_fail"},
-    "engine": set(),
-    "cli": {"rq_chat_check", "rq_chat_name"},
-    "serve": {"rq_chat_check", "rq_chat_name"},
-    "tools": {"rq_chat_name"},
+    "chat": set(), "tokenizer": set(), "engine": set(), "cli": set(), "serve": set(), "tools": set(),
 }
+
+
+def test_tokenizer_entry_points_are_weak():
+    """the library reaches the host's tokenizer.o / gguf.o only through weak references (a program without them, e.g.
+    the Python binding, loads the library and gets models without a tokenizer), and it exports the model.c host
+    helpers those objects call"""
+    import subprocess
+    lib = os.path.join(ROOT, "gwenedeg_amd", "lib", "libgwenedeg_amd.so")
+    out = subprocess.run(["nm", "-D", lib], capture_output=True, text=True, check=True).stdout
+    kind = {ln.split()[-1]: ln.split()[-2] for ln in out.splitlines() if ln.strip()}
+    for f in ("gguf_parse", "gguf_chat_variant", "gguf_sampling", "build_tokenizer_gguf", "free_tokenizer"):
+        assert kind.get(f) == "w", (f, kind.get(f))
+    for f in ("load_fail", "chat_gen_suffix", "rq_chat_name", "rq_chat_check"):
+        assert kind.get(f) == "T", (f, kind.get(f))
 
 
 def test_reference_host_modules_link():
@@ -151,12 +160,15 @@ def test_reference_host_modules_link():
 
 
 # The RqModel / RqSeq fields the reference's host modules read directly (sampler.c:321-331, spec.c:32-54 / :219 /
-# :271-429, chat.c:38-357, tokenizer.c:812): their offsets and sizes in the reference's internal.h as gcc lays it out
+# :271-429, chat.c:38-357, tokenizer.c:794-827: the Tokenizer the host's tokenizer.o builds in place): their offsets and sizes in the reference's internal.h as gcc lays it out
 # on x86-64, which the library's structs keep (the reference's field names; the library's own fields follow)
 REF_FIELDS = {
     "RqModel": {"config": (0, 48), "config.dim": (8, 4), "config.vocab_size": (28, 4), "config.seq_len": (32, 4),
                 "config.shared_classifier": (40, 4), "config.group_size": (44, 4), "fp": (1752, 8),
-                "has_weights": (1760, 4), "has_tok": (1764, 4), "is_gguf": (1768, 4), "hy.on": (2080, 4),
+                "tok": (280, 1368), "tok.vocab_size": (304, 4), "tok.bos_token_id": (312, 4),
+                "tok.eos_token_id": (316, 4), "tok.n_added": (1384, 4), "tok.marks35": (1644, 4),
+                "has_weights": (1760, 4), "has_tok": (1764, 4), "is_gguf": (1768, 4), "warning": (1776, 256),
+                "hy.on": (2080, 4),
                 "chat": (2684, 4), "samp_temp": (2768, 4), "samp_topp": (2772, 4), "samp_topk": (2776, 4),
                 "samp_set": (2780, 4), "user_tmpl": (2784, 2048), "sys_tmpl": (4832, 2048),
                 "tmpl_missing": (6880, 2176), "mtp_of": (9056, 8)},

@@ -166,6 +166,29 @@ def test_decode_greedy_equals_step_by_step(gw, synth_models, shape, n_prompt, st
     assert _bits_equal(a, b)
 
 
+@pytest.mark.parametrize("kvt", [3, 9, 0, 1, 5, 7])
+def test_decode_greedy_kv_types(gw, synth_models, kvt):
+    """gw_decode_greedy on sequences whose cache is not f16 (q8, q4k4, f32, bf16, bf16-dot, q8-dot): the tokens and the
+    cache of gw_decode_argmax step by step (the fused one-row sequence serves the f16 / bf16 caches; the others run the
+    per-step passes), across a key-block boundary"""
+    path = synth_models("tiny_gqa4")
+    m = gw.Model(path, ctx_len=1024)
+    c = m.ctx(max_batch=64, max_ctx=1024)
+    ids = _ids(m.vocab, 250, 5)
+    s1, s2 = m.seq(1024, kv_type=kvt), m.seq(1024, kv_type=kvt)
+    lg = c.prefill(s1, ids)
+    c.prefill(s2, ids)
+    t0 = int(np.argmax(lg))
+    got = c.decode_greedy(s1, t0, 12)
+    ref, tok = [], t0
+    for _ in range(12):
+        lg = c.decode(s2, tok)
+        tok = int(np.argmax(lg))
+        ref.append(tok)
+    assert [int(t) for t in got] == ref
+    assert _bits_equal(c.decode(s1, 7), c.decode(s2, 7))
+
+
 def test_memory_and_pass_times(gw, synth_models):
     """rq_model_mem / rq_seq_mem / rq_seq_resident (runq.h:150-171, :274) count the device bytes the library holds,
     and rq_pass_times (runq.h:196-199) times a decode step and a 4-row pass on its own context"""

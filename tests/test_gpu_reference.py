@@ -281,12 +281,12 @@ def test_seqfile_with_reference(gw, orc, tmp_path, kvt):
 
 # RQ_KV_Q8, RQ_KV_Q4, RQ_KV_Q4K4; the dot-product types RQ_KV_BF16_DOT, F16_DOT, Q8_DOT, Q4_DOT, Q4K4_DOT; RQ_KV_F32
 @pytest.mark.parametrize("shape,kvt", [("qwen3_0_6b", k) for k in (3, 8, 9, 5, 6, 7, 12, 13, 0)] +
-                         [("tiny_hd64", k) for k in (9, 12, 5, 0)])
+                         [("tiny_hd64", k) for k in (9, 12, 5, 0)] + [("tiny_kv16", k) for k in (2, 3, 9, 0, 5, 7)])
 def test_quantized_kv_greedy_bit_identical(gw, orc, tmp_path, shape, kvt):
     """the rotated 8-bit / 4-bit KV caches (forward.c:1609-1790), the bf16 dot-product attention types
     (forward.c:1452-1606: bf16 q, K, V and weights, vdpbf16ps's pairs, FTZ / DAZ) and the f32 cache (forward.c:1945-1950:
-    fp32 tiles, the fp32 attention) on a Qwen3-0.6B-shaped model (2 layers; and a head_dim-64 model of 8 query heads
-    on one kv head): a 300-token prefill (two key blocks,
+    fp32 tiles, the fp32 attention) on a Qwen3-0.6B-shaped model (2 layers; and head_dim-64 models of 8 and of 16
+    query heads on one kv head, the latter's rows past the 8-vector attention items): a 300-token prefill (two key blocks,
     16-vector row blocks) and 24 greedy steps, every logits row equal bit for bit to the reference's own cache of that
     type, the same tokens; then a pass of that sequence's next token beside a fresh sequence's prompt (both of the
     type) equal to each run alone"""

@@ -454,6 +454,9 @@ def test_attention_combine_matches_single_pass():
     ("tiny", {}, 270, 0),
     ("tiny_hd64", {}, 270, 12),
     ("tiny_hd64", {}, 270, 5),
+    ("tiny_kv16", {}, 270, 2),
+    ("tiny_kv16", {}, 270, 3),
+    ("tiny_kv16", {}, 270, 7),
 ])
 def test_forward_bit_exact_vs_reference(tmp_path, shape, over, n, kvt):
     """or_forward_token position by position against the reference compiled from its sources (rq_prefill with every
