@@ -109,6 +109,11 @@ _sig = {
     "rq_seq_common_prefix": (_I, [_P, ctypes.POINTER(_I), _I]),
     "rq_seq_save": (_I, [_P, ctypes.c_char_p]),
     "rq_seq_load": (_I, [_P, ctypes.c_char_p, _I]),
+    "rq_seq_release": (_I, [_P, _I]),
+    "rq_seq_kv_bytes": (ctypes.c_size_t, [_P, _I]),
+    "rq_seq_resident": (None, [_P, _P]),
+    "gw_seq_lazy": (_I, [_I]),
+    "gw_seq_device_bytes": (ctypes.c_size_t, [_P]),
     "rq_ctx_new": (_P, [_P, _I, _I, ctypes.POINTER(_I)]),
     "rq_ctx_free": (None, [_P]),
     "rq_ctx_error": (ctypes.c_char_p, [_P]),
@@ -194,6 +199,10 @@ class Model:
             pass
 
 
+class RqSeqMem(ctypes.Structure):  # runq.h:152-157
+    _fields_ = [("kv", ctypes.c_size_t), ("state", ctypes.c_size_t), ("checkpoints", ctypes.c_int), ("total", ctypes.c_size_t)]
+
+
 class Seq:
     """rq_seq_* (runq.h:222-282): a sequence and its device KV cache."""
 
@@ -245,6 +254,26 @@ class Seq:
         r = lib.rq_seq_load(self._h, path.encode(), n)
         if r != RQ_OK:
             raise RqError(r, "rq_seq_load")
+
+    def release(self, keep: int = 0):
+        """rq_seq_release (runq.h:270): the memory past max(keep, len) goes"""
+        r = lib.rq_seq_release(self._h, keep)
+        if r != RQ_OK:
+            raise RqError(r, "rq_seq_release")
+
+    def resident(self) -> RqSeqMem:
+        """rq_seq_resident (runq.h:274)"""
+        out = RqSeqMem()
+        lib.rq_seq_resident(self._h, ctypes.byref(out))
+        return out
+
+    def kv_bytes(self, n: int) -> int:
+        """rq_seq_kv_bytes (runq.h:277)"""
+        return lib.rq_seq_kv_bytes(self._h, n)
+
+    def device_bytes(self) -> int:
+        """gw_seq_device_bytes: the device memory the K / V caches hold now"""
+        return lib.gw_seq_device_bytes(self._h)
 
     def close(self):
         if self._h:

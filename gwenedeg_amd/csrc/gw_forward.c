@@ -46,9 +46,133 @@ static int ctx_hip(RqCtx *c, const char *what, hipError_t e) {
 static size_t seq_layer_bytes(const RqSeq *s, int kv) {
     return (size_t)s->kv_len / GW_ATT_T * s->m->n_kv_heads * gw_kv_tile_bytes(s->kvt, s->m->head_dim, kv);
 }
-/* layer l's K (kv 0) or V cache base */
-static uint16_t *seq_layer(const RqSeq *s, int l, int kv) {
-    return (uint16_t *)((uint8_t *)(kv ? s->vc : s->kc) + (size_t)l * seq_layer_bytes(s, kv));
+#define seq_layer gw_seq_layer
+
+/* Lazy device memory (HIP virtual memory). A sequence reserves the address range of its capacity at rq_seq_new and
+ * maps physical memory in chunks of GW_SEQ_CHUNK bytes per layer and half as positions are first written (gw_seq_map,
+ * called before every pass, copy, fill and load); rq_seq_release unmaps the chunks past the kept positions. So a
+ * sequence of a large capacity holds only what it has used, as the reference's host memory does (its pages are touched
+ * on first write and given back by madvise, forward.c:474-510). A chunk serves 2 MiB / (block bytes) 256-position
+ * blocks: 4 of a layer's blocks (1,024 positions) for 8 KV heads of 128 f16 values */
+#define GW_SEQ_CHUNK ((size_t)2 << 20)
+static int seq_lazy = 1; /* gw_seq_lazy */
+
+int gw_seq_lazy(int on) {
+    int prev = seq_lazy;
+    if (on >= 0) seq_lazy = on ? 1 : 0;
+    return prev;
+}
+
+/* a layer's chunks that hold positions 0 .. n - 1 (whole 256-position blocks: the attention kernels read whole
+ * blocks) */
+static int seq_chunks(const RqSeq *s, int n, int kv) {
+    size_t nb = ((size_t)(n < 0 ? 0 : n) + GW_ATT_P - 1) / GW_ATT_P;
+    size_t bytes = nb * (GW_ATT_P / GW_ATT_T) * s->m->n_kv_heads * gw_kv_tile_bytes(s->kvt, s->m->head_dim, kv);
+    return (int)((bytes + s->vm_chunk - 1) / s->vm_chunk);
+}
+
+static void vm_props(const RqSeq *s, hipMemAllocationProp *prop, hipMemAccessDesc *acc) {
+    memset(prop, 0, sizeof(*prop));
+    prop->type = hipMemAllocationTypePinned;
+    prop->requestedHandleType = hipMemHandleTypeNone;
+    prop->location.type = hipMemLocationTypeDevice;
+    prop->location.id = s->m->device;
+    if (acc) {
+        memset(acc, 0, sizeof(*acc));
+        acc->location = prop->location;
+        acc->flags = hipMemAccessFlagsProtReadWrite;
+    }
+}
+
+/* unmap and free chunks [from, to) of layer l's half kv (the ones mapped) */
+static void vm_unmap(RqSeq *s, int kv, int l, int from, int to) {
+    uint8_t *base = (uint8_t *)(kv ? s->vc : s->kc) + (size_t)l * s->lstride[kv];
+    hipMemGenericAllocationHandle_t *h = s->vm_h[kv] + (size_t)l * s->vm_max[kv];
+    for (int i = to - 1; i >= from; i--)
+        if (h[i]) {
+            (void)hipMemUnmap(base + (size_t)i * s->vm_chunk, s->vm_chunk);
+            (void)hipMemRelease(h[i]);
+            h[i] = NULL;
+        }
+}
+
+int gw_seq_map(RqSeq *s, int n) {
+    if (!s->vmm) return RQ_OK;
+    n = n > s->cap ? s->cap : n;
+    hipMemAllocationProp prop;
+    hipMemAccessDesc acc;
+    vm_props(s, &prop, &acc);
+    for (int kv = 0; kv < 2; kv++) {
+        int want = seq_chunks(s, n, kv), have = s->vm_n[kv];
+        if (want <= have) continue;
+        for (int l = 0; l < s->m->n_layers; l++) {
+            uint8_t *base = (uint8_t *)(kv ? s->vc : s->kc) + (size_t)l * s->lstride[kv];
+            hipMemGenericAllocationHandle_t *h = s->vm_h[kv] + (size_t)l * s->vm_max[kv];
+            for (int i = have; i < want; i++) {
+                void *a = base + (size_t)i * s->vm_chunk;
+                if (hipMemCreate(&h[i], s->vm_chunk, &prop, 0) != hipSuccess) {
+                    h[i] = NULL;
+                    goto fail;
+                }
+                if (hipMemMap(a, s->vm_chunk, 0, h[i], 0) != hipSuccess) {
+                    (void)hipMemRelease(h[i]);
+                    h[i] = NULL;
+                    goto fail;
+                }
+                if (hipMemSetAccess(a, s->vm_chunk, &acc, 1) != hipSuccess) {
+                    (void)hipMemUnmap(a, s->vm_chunk);
+                    (void)hipMemRelease(h[i]);
+                    h[i] = NULL;
+                    goto fail;
+                }
+            }
+            continue;
+        fail: /* (this half back to what it was: the chunks mapped by this call go) */
+            for (int j = 0; j <= l; j++) vm_unmap(s, kv, j, have, want);
+            (void)hipGetLastError();
+            return RQ_ERR_NOMEM;
+        }
+        s->vm_n[kv] = want;
+    }
+    return RQ_OK;
+}
+
+size_t gw_seq_device_bytes(const RqSeq *s) {
+    if (!s) return 0;
+    if (!s->vmm) return (size_t)s->m->n_layers * (seq_layer_bytes(s, 0) + seq_layer_bytes(s, 1));
+    return (size_t)s->m->n_layers * ((size_t)s->vm_n[0] + (size_t)s->vm_n[1]) * s->vm_chunk;
+}
+
+static int seq_reserve(RqSeq *s) {
+    /* the lazy layout: each half's address range (layer strides in whole chunks), nothing mapped; 1 where the device
+     * has no virtual memory management (the caller allocates whole), else RQ_OK / RQ_ERR_NOMEM */
+    const RqModel *m = s->m;
+    int ok = 0;
+    size_t g = 0;
+    hipMemAllocationProp prop;
+    vm_props(s, &prop, NULL);
+    if (hipDeviceGetAttribute(&ok, hipDeviceAttributeVirtualMemoryManagementSupported, m->device) != hipSuccess || !ok ||
+        (hipMemGetAllocationGranularity(&g, &prop, hipMemAllocationGranularityRecommended) != hipSuccess &&
+         hipMemGetAllocationGranularity(&g, &prop, hipMemAllocationGranularityMinimum) != hipSuccess) || !g) {
+        (void)hipGetLastError();
+        return 1;
+    }
+    s->vm_chunk = (GW_SEQ_CHUNK + g - 1) / g * g;
+    s->vmm = 1;
+    for (int kv = 0; kv < 2; kv++) {
+        s->lstride[kv] = (seq_layer_bytes(s, kv) + s->vm_chunk - 1) / s->vm_chunk * s->vm_chunk;
+        s->vm_max[kv] = (int)(s->lstride[kv] / s->vm_chunk);
+        s->vm_h[kv] = calloc((size_t)m->n_layers * s->vm_max[kv], sizeof(hipMemGenericAllocationHandle_t));
+        void *base = NULL;
+        if (!s->vm_h[kv]) return RQ_ERR_NOMEM;
+        if (hipMemAddressReserve(&base, (size_t)m->n_layers * s->lstride[kv], s->vm_chunk, NULL, 0) != hipSuccess) {
+            (void)hipGetLastError();
+            return RQ_ERR_NOMEM;
+        }
+        if (kv) s->vc = base;
+        else s->kc = base;
+    }
+    return RQ_OK;
 }
 
 RqSeq *rq_seq_new(const RqModel *m, int capacity, int kv_type, int *err) {
@@ -72,10 +196,17 @@ RqSeq *rq_seq_new(const RqModel *m, int capacity, int kv_type, int *err) {
     s->att_nb = s->kv_len / GW_ATT_P;
     s->nck = 2;   /* (RQ_SEQ_CK, internal.h:66) */
     s->hpos = -1; /* (not an MTP view's sequence) */
-    if (hipMalloc((void **)&s->kc, (size_t)m->n_layers * seq_layer_bytes(s, 0)) != hipSuccess ||
-        hipMalloc((void **)&s->vc, (size_t)m->n_layers * seq_layer_bytes(s, 1)) != hipSuccess) {
-        e = RQ_ERR_NOMEM;
-        goto fail;
+    if ((e = seq_lazy ? seq_reserve(s) : 1) < 0) goto fail;
+    if (e > 0) { /* (whole: one allocation per half) */
+        e = RQ_OK;
+        s->vmm = 0;
+        s->lstride[0] = seq_layer_bytes(s, 0);
+        s->lstride[1] = seq_layer_bytes(s, 1);
+        if (hipMalloc((void **)&s->kc, (size_t)m->n_layers * s->lstride[0]) != hipSuccess ||
+            hipMalloc((void **)&s->vc, (size_t)m->n_layers * s->lstride[1]) != hipSuccess) {
+            e = RQ_ERR_NOMEM;
+            goto fail;
+        }
     }
     s->tokens = malloc((size_t)capacity * sizeof(int));
     if (!s->tokens) { e = RQ_ERR_NOMEM; goto fail; }
@@ -89,8 +220,19 @@ fail:
 
 void rq_seq_free(RqSeq *s) {
     if (!s) return;
-    if (s->kc) hipFree(s->kc);
-    if (s->vc) hipFree(s->vc);
+    if (s->vmm) {
+        if (s->vm_n[0] || s->vm_n[1]) (void)hipDeviceSynchronize(); /* (no pass may still read what goes) */
+        for (int kv = 0; kv < 2; kv++) {
+            if (s->vm_h[kv])
+                for (int l = 0; l < s->m->n_layers; l++) vm_unmap(s, kv, l, 0, s->vm_max[kv]);
+            void *base = kv ? (void *)s->vc : (void *)s->kc;
+            if (base) (void)hipMemAddressFree(base, (size_t)s->m->n_layers * s->lstride[kv]);
+            free(s->vm_h[kv]);
+        }
+    } else {
+        if (s->kc) hipFree(s->kc);
+        if (s->vc) hipFree(s->vc);
+    }
     free(s->tokens);
     free(s);
 }
@@ -143,16 +285,34 @@ int rq_seq_common_prefix(const RqSeq *s, const int *tokens, int n) {
     return L;
 }
 
-int rq_seq_release(RqSeq *s, int keep) { return !s || keep < 0 ? RQ_ERR_ARG : RQ_OK; }
+int rq_seq_release(RqSeq *s, int keep) {
+    /* forward.c:474-510: the memory past max(keep, len) (capped at the capacity) goes, the high-water mark drops to it.
+     * A lazy sequence unmaps its chunks past that position's whole blocks; one allocated whole keeps its memory */
+    if (!s || keep < 0) return RQ_ERR_ARG;
+    int k = keep > s->len ? keep : s->len;
+    k = k > s->cap ? s->cap : k;
+    if (s->vmm && (seq_chunks(s, k, 0) < s->vm_n[0] || seq_chunks(s, k, 1) < s->vm_n[1])) {
+        (void)hipDeviceSynchronize(); /* (no pass may still read what goes) */
+        for (int kv = 0; kv < 2; kv++) {
+            int w = seq_chunks(s, k, kv);
+            if (w >= s->vm_n[kv]) continue;
+            for (int l = 0; l < s->m->n_layers; l++) vm_unmap(s, kv, l, w, s->vm_n[kv]);
+            s->vm_n[kv] = w;
+        }
+    }
+    if (k < s->hwm) s->hwm = k;
+    return RQ_OK;
+}
 
 /* Qwen3.5's checkpoints: a Qwen3 sequence holds none (runq.h:257-259) */
 int rq_seq_checkpoint_drop(RqSeq *s, int pos) { (void)s; (void)pos; return RQ_ERR_ARG; }
 
 void rq_seq_resident(const RqSeq *s, RqSeqMem *out) {
-    /* runq.h:271-274: the K / V halves are device memory allocated whole at rq_seq_new, so the bound is all of it */
+    /* runq.h:271-274 (forward.c:455-462): kv = rq_seq_kv_bytes up to the high-water mark. A lazy sequence's device
+     * memory is that within a chunk per layer and half (gw_seq_device_bytes); one allocated whole holds its capacity */
     memset(out, 0, sizeof(*out));
     if (!s) return;
-    out->kv = rq_seq_kv_bytes(s, s->cap);
+    out->kv = rq_seq_kv_bytes(s, s->vmm ? s->hwm : s->cap);
     out->total = out->kv;
 }
 
@@ -171,6 +331,7 @@ int rq_seq_copy(RqSeq *dst, const RqSeq *src, int n) {
     const RqModel *m = src->m;
     int nkv = m->n_kv_heads, hd = m->head_dim, full = n / GW_ATT_P, rem = n % GW_ATT_P, tpb = GW_ATT_P / GW_ATT_T;
     size_t ntl = (size_t)(rem + GW_ATT_T - 1) / GW_ATT_T;
+    if (gw_seq_map(dst, n) != RQ_OK) return RQ_ERR_NOMEM;
     for (int l = 0; l < m->n_layers && n > 0; l++)
         for (int kv = 0; kv < 2; kv++) {
             const size_t tb = gw_kv_tile_bytes(src->kvt, hd, kv); /* (tiles in order: block, head, tile) */
@@ -194,6 +355,7 @@ int rq_seq_copy(RqSeq *dst, const RqSeq *src, int n) {
 int rq_seq_fill_synthetic(RqSeq *s, int n, unsigned long long seed) {
     /* runq.h:721-726: n positions of pseudo-random K / V (|K| < 4, |V| < 1), arbitrary valid tokens */
     if (!s || n < 1 || n > s->cap) return RQ_ERR_ARG;
+    if (gw_seq_map(s, n) != RQ_OK) return RQ_ERR_NOMEM;
     size_t nb = ((size_t)n + GW_ATT_P - 1) / GW_ATT_P, per = nb * GW_ATT_P * s->m->n_kv_heads * s->m->head_dim;
     for (int l = 0; l < s->m->n_layers; l++) {
         unsigned long long sl = seed + (unsigned long long)l * 0x1000193ull;
@@ -303,8 +465,9 @@ static size_t ctx_bytes(const RqModel *m, int B, int max_ctx) {
 }
 
 int rq_seq_mem(const RqModel *m, int capacity, int kv_type, RqSeqMem *mem) {
-    /* model.c:765-772: one sequence's memory as rq_seq_new allocates it (RQ_ERR_ARG as rq_seq_new): the K / V halves
-     * in device memory (whole 256-position blocks) and the token array; no recurrent state (Qwen3) */
+    /* model.c:765-772: one sequence's memory at its capacity (RQ_ERR_ARG as rq_seq_new): the K / V halves in device
+     * memory (whole 256-position blocks) and the token array; no recurrent state (Qwen3). A lazy sequence maps it as
+     * it grows, so this is its bound */
     memset(mem, 0, sizeof(*mem));
     if (!m || !m->has_weights) return RQ_ERR_STATE;
     if (capacity <= 0) capacity = m->seq_len;
@@ -624,6 +787,8 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
     for (int b = 0; b < n; b++) {
         int nb = (P->pos[b] + 1 + GW_ATT_P - 1) / GW_ATT_P;
         nbmax = nb > nbmax ? nb : nbmax;
+        if ((b + 1 == n || P->seq[b + 1] != P->seq[b]) && gw_seq_map(P->seq[b], P->pos[b] + 1) != RQ_OK)
+            return ctx_fail(c, RQ_ERR_NOMEM, "no device memory for the KV cache up to position %d", P->pos[b]);
     }
     if ((rc = ctx_part(c, n, nbmax)) != RQ_OK) return rc;
     for (int b = 0; b < n;) {
@@ -893,6 +1058,8 @@ int gw_decode_greedy(RqCtx *c, RqSeq *s, int token, int n, int *tokens) {
     }
     int p0 = s->len;
     if ((e = ctx_part(c, 1, (p0 + n - 1) / GW_ATT_P + 1)) != RQ_OK) return e;
+    if (gw_seq_map(s, p0 + n) != RQ_OK)
+        return ctx_fail(c, RQ_ERR_NOMEM, "no device memory for the KV cache up to position %d", p0 + n - 1);
     hipStream_t st = c->stream;
     HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(st)); /* (the staging may still be read by a previous call) */
     c->g_h[0] = token;

@@ -183,9 +183,25 @@ struct RqSeq {
     int hvalid, hpos;  /* @1816: an MTP view's state (spec.c); 0 and -1 here (no sequence is a view's) */
     float *hprev;      /* @1824: NULL */
     /* this library's own */
-    uint16_t *kc, *vc; /* device: n_layers x kv_len x kv_dim 16-bit values each (f16, or bf16 when kvt is); the quantized
-                        * types: n_layers x kv_len / 16 x n_kv tiles of gw_kv_tile_bytes each, in the same tile order */
+    uint16_t *kc, *vc; /* device: per layer kv_len x kv_dim 16-bit values (f16, or bf16 when kvt is); the quantized
+                        * types: per layer kv_len / 16 x n_kv tiles of gw_kv_tile_bytes each, in the same tile order.
+                        * Layer l's at l x lstride[kv] bytes (gw_seq_layer) */
+    size_t lstride[2];  /* a layer's stride in kc (0) / vc (1): its bytes, rounded up to whole chunks when lazy */
+    /* lazy memory (vmm 1): kc / vc are reserved address ranges; the first vm_n[kv] chunks of vm_chunk bytes of every
+     * layer are mapped, each its own physical allocation vm_h[kv][l x vm_max[kv] + i] (gw_seq_map maps, rq_seq_release
+     * unmaps). vmm 0: one hipMalloc per half, all of it */
+    int vmm, vm_n[2], vm_max[2];
+    size_t vm_chunk;
+    hipMemGenericAllocationHandle_t *vm_h[2];
 };
+
+/* layer l's K (kv 0) or V (kv 1) cache base */
+static inline uint16_t *gw_seq_layer(const RqSeq *s, int l, int kv) {
+    return (uint16_t *)((uint8_t *)(kv ? s->vc : s->kc) + (size_t)l * s->lstride[kv]);
+}
+/* make positions 0 .. n - 1 of every layer writable (a lazy sequence maps the chunks not yet mapped): RQ_OK, or
+ * RQ_ERR_NOMEM with nothing newly mapped in the half that failed */
+int gw_seq_map(RqSeq *s, int n);
 
 /* gw_host.c: model.c's host side (the tokenizer through the host's tokenizer.o / gguf.o, the chat templates) */
 int gw_host_tokenizer_linked(void);

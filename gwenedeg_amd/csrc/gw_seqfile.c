@@ -91,7 +91,6 @@ static int sf_blocks(const RqSeq *s, int fd, int wr, const SfHdr *h, int nblk) {
      * h->nblk blocks each), through one host buffer of a section */
     const RqModel *m = s->m;
     const uint64_t bk = sf_blk(m, s->kvt, 0), bv = sf_blk(m, s->kvt, 1);
-    const size_t lk = (size_t)s->kv_len / GW_ATT_P * bk, lv = (size_t)s->kv_len / GW_ATT_P * bv; /* (a layer's bytes) */
     void *buf = NULL;
     int rc = 0;
     if (!nblk) return 0;
@@ -99,7 +98,7 @@ static int sf_blocks(const RqSeq *s, int fd, int wr, const SfHdr *h, int nblk) {
     for (int l = 0; l < m->n_layers && !rc; l++)
         for (int kv = 0; kv < 2 && !rc; kv++) {
             size_t bytes = (size_t)nblk * (kv ? bv : bk);
-            uint8_t *dev = (uint8_t *)(kv ? s->vc : s->kc) + (size_t)l * (kv ? lv : lk);
+            uint8_t *dev = (uint8_t *)gw_seq_layer(s, l, kv);
             uint64_t off = h->off_kv + (uint64_t)h->nblk * ((uint64_t)l * (bk + bv) + (kv ? bk : 0));
             if (wr) {
                 if (hipMemcpy(buf, dev, bytes, hipMemcpyDeviceToHost) != hipSuccess) rc = RQ_ERR_STATE;
@@ -223,7 +222,7 @@ int rq_seq_load(RqSeq *dst, const char *path, int n) {
         rc = RQ_ERR_MISMATCH;
     } else {
         dst->len = 0;
-        rc = sf_blocks(dst, fd, 0, &h, (n + GW_ATT_P - 1) / GW_ATT_P);
+        rc = gw_seq_map(dst, n) != RQ_OK ? RQ_ERR_NOMEM : sf_blocks(dst, fd, 0, &h, (n + GW_ATT_P - 1) / GW_ATT_P);
         if (rc == RQ_OK) {
             memcpy(dst->tokens, tk, (size_t)n * sizeof(int));
             dst->len = n;

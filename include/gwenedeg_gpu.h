@@ -354,6 +354,17 @@ int gw_kq32_step(int sb);
  * on it */
 int gw_gemv_warm_next(int on);
 
+/* How rq_seq_new gives a sequence its device KV memory: 1 lazily (the default, where the device has HIP virtual memory
+ * management): the address range of the capacity reserved, memory mapped in 2 MiB chunks per layer and half (K / V)
+ * as positions are first written, the chunks past max(keep, len) unmapped by rq_seq_release, so a sequence holds what
+ * it has used (the reference's host pages behave so, forward.c:474-510); 0 all of it allocated at rq_seq_new.
+ * Sequences made before a change keep theirs. A negative value only queries; returns the previous setting. No
+ * counterpart in runq.h; results do not depend on it */
+int gw_seq_lazy(int on);
+
+/* The device bytes s's K / V caches hold now: its mapped chunks (lazy), or the whole allocation */
+size_t gw_seq_device_bytes(const RqSeq *s);
+
 /* The context's stream (a hipStream_t), for callers that time the passes with events on it */
 void *gw_ctx_stream(RqCtx *c);
 

@@ -212,7 +212,10 @@ def test_memory_and_pass_times(gw, synth_models):
     assert sm.kv == lib.rq_seq_kv_bytes(ctypes.c_void_p(s._h), 300) and sm.total == sm.kv and sm.state == 0
     res = SeqMem()
     lib.rq_seq_resident(ctypes.c_void_p(s._h), ctypes.byref(res))
-    assert res.kv == sm.kv
+    assert res.kv == lib.rq_seq_kv_bytes(ctypes.c_void_p(s._h), 0) == 300 * 4  # (lazy: no position written yet)
+    s.fill_synthetic(20)
+    lib.rq_seq_resident(ctypes.c_void_p(s._h), ctypes.byref(res))
+    assert res.kv == lib.rq_seq_kv_bytes(ctypes.c_void_p(s._h), 256) and res.total == res.kv
     f16_kv = sm.kv - 300 * 4
     assert lib.rq_seq_mem(ctypes.c_void_p(m._h), 300, 0, ctypes.byref(sm)) == 0  # (f32: twice the f16 tiles)
     assert sm.kv - 300 * 4 == 2 * f16_kv
