@@ -8,6 +8,7 @@
 
 #include "gw_internal.h"
 #include "gw_device.h"
+#include "gw_iq.h"
 
 __device__ __forceinline__ float h2f_g(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 
@@ -362,7 +363,8 @@ __global__ __launch_bounds__(256) void k_gemm_q8f(const int8_t *__restrict__ W, 
 //     B = 1); term = ((d sc_j) xs) I - (dmin m_j) (xs S)
 //   Q6_K: codes q - 32 (-32 .. 31, exact in int8; q 6-bit from ql / qh); per half-group of 16 the exact sum
 //     (v_mfma_i32_32x32x16_i8), I = sc_0 I_0 + sc_1 I_1 (exact int); term = (d xs) I
-//   IQ4_XS (its integer form: int8 v, int8 S per 16, fp32 D): Q6_K's term with v and S as stored (iquants.h:49-55)
+//   the i-quants (IQ4_XS and the codebook types: each unit's 16 v and its S decoded by gw_iq.h when staged, D per
+//   super-block): Q6_K's term with v and S                                                            (iquants.h:49-55)
 //   Q2_K (96 bytes: the file's 84 and padding; q 0 .. 3): Q6_K's term with the 4-bit scales sc, minus the mins' term
 //     (dmin xs) M, M = m_0 X_0 + m_1 X_1 from the sums of x of each half (the same MFMA with B = 1)   (iquants.h:56-57)
 // then val = val + term in group order. mode 1: out = out + val. K % 256 == 0.
@@ -393,6 +395,7 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
     // scratch memory)
     constexpr int NW = Q45 ? 2 : 4;
     uint4 xr0, xr1, wa[NW], wb[NW], hd0, hd1;
+    IqRaw iqr[IqCb<TYPE>::iform ? NW : 1]; // (the i-quants: each unit's loads, decoded when staged)
     float xsv;
     auto load = [&](int k0) {
         const int hs = (k0 >> 7) & 1; // (the stage's half of super-block k0 / 256)
@@ -418,9 +421,9 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
                 const uint8_t *b = sbk + (size_t)n * rowb;
                 wa[k] = *(const uint4 *)(b + 32 + 32 * hs + 16 * h);
                 wb[k] = *(const uint4 *)(b + 16 * h);
-            } else if (TYPE == GW_IQ4_XS) { // (unit (row, group p, half h): its 16 int8 values)
+            } else if constexpr (IqCb<TYPE>::iform) { // (unit (row, group p, half h): its half-group's loads)
                 int row = c >> 3, u = c & 7, p = u >> 1, h = u & 1, n = n0 + row < N ? n0 + row : N - 1;
-                wa[k] = *(const uint4 *)(sbk + (size_t)n * rowb + 128 * hs + 32 * p + 16 * h);
+                iqr[k] = iq_raw<TYPE>(sbk + (size_t)n * rowb, 8 * hs + 2 * p + h);
             } else if (TYPE == GW_Q2_K) { // (unit (row, group p, half h): sub-block 8 hs + 2 p + h, 16 bytes of qs)
                 int row = c >> 3, u = c & 7, h = u & 1, n = n0 + row < N ? n0 + row : N - 1;
                 wa[k] = *(const uint4 *)(sbk + (size_t)n * rowb + 16 + 32 * hs + 16 * h);
@@ -439,9 +442,9 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
                 hd0 = *(const uint4 *)b; // d, dmin, then scale bytes 0 .. 11 in words y, z, w
             } else if (TYPE == GW_Q3_K) {
                 hd0 = *(const uint4 *)(b + 96); // the 12 scale bytes, then d
-            } else if (TYPE == GW_IQ4_XS) {
-                hd0 = *(const uint4 *)(b + 256); // the 16 int8 S
-                hd1 = *(const uint4 *)(b + 272); // D (fp32)
+            } else if constexpr (IqCb<TYPE>::iform) { // (the dwords of d)
+                hd0.x = *(const uint32_t *)(b + iq_d_off<TYPE>());
+                if (TYPE == GW_IQ1_M) hd0.y = *(const uint32_t *)(b + iq_d_off<TYPE>() + 4);
             } else if (TYPE == GW_Q2_K) {
                 hd0 = *(const uint4 *)b;        // the 16 scale bytes (sc | m << 4)
                 hd1 = *(const uint4 *)(b + 80); // d, dmin
@@ -492,9 +495,13 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
                     o4[e] = f | sg * 62u; // (bits 3 .. 7 of each byte whose bit 2 is set)
                 }
                 *(uint4 *)(wl + row * GROW + 32 * p + 16 * h) = make_uint4(o4[0], o4[1], o4[2], o4[3]);
-            } else if (TYPE == GW_IQ4_XS) { // (already int8)
+            } else if constexpr (IqCb<TYPE>::iform) { // (the 16 values v as int8; the half-group's S)
                 int row = c >> 3, u = c & 7, p = u >> 1, h = u & 1;
-                *(uint4 *)(wl + row * GROW + 32 * p + 16 * h) = wa[k];
+                int4 v;
+                int S;
+                iq_dec<TYPE>(iqr[k], 8 * hs + 2 * p + h, v, S);
+                *(int4 *)(wl + row * GROW + 32 * p + 16 * h) = v;
+                scl[row][2 * p + h] = S;
             } else if (TYPE == GW_Q2_K) { // q = 2 bits 2 p of each byte (0 .. 3)
                 int row = c >> 3, u = c & 7, p = u >> 1, h = u & 1, sl = 2 * p;
                 *(uint4 *)(wl + row * GROW + 32 * p + 16 * h) =
@@ -546,6 +553,8 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
                     scl[t][k] = (int)(lo | hi << 4) - 32;
                 }
                 f0l[t][0] = h2f_g((uint16_t)(hd0.w & 0xffffu));
+            } else if constexpr (IqCb<TYPE>::iform) { // (the S came with the units)
+                f0l[t][0] = iq_d_raw<TYPE>(hd0.x, hd0.y);
             } else {
                 uint32_t sw[4] = { hd0.x, hd0.y, hd0.z, hd0.w };
                 #pragma unroll
@@ -553,7 +562,7 @@ __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, 
                     const int ks = 8 * hs + k;
                     scl[t][k] = (int)(int8_t)((sw[ks >> 2] >> (8 * (ks & 3))) & 0xffu);
                 }
-                f0l[t][0] = TYPE == GW_IQ4_XS ? __uint_as_float(hd1.x) : h2f_g((uint16_t)(hd1.x & 0xffffu));
+                f0l[t][0] = h2f_g((uint16_t)(hd1.x & 0xffffu));
                 if (TYPE == GW_Q2_K) { // (scl: the raw byte sc | m << 4; f1l: dmin)
                     #pragma unroll
                     for (int k = 0; k < 8; k++) scl[t][k] = (int)(uint8_t)(sw[(8 * hs + k) >> 2] >> (8 * ((8 * hs + k) & 3)));
@@ -881,8 +890,9 @@ __global__ __launch_bounds__(SK_T * SB, SB == 1 ? 2 : 1) void k_gemm_kq32(SkMats
 //   Q5_K (176 bytes: Q4_K's header, qh 32, nibbles 128): Q4_K's term with q 0 .. 31 (bit 4 from qh)
 //   Q3_K (112 bytes: hmask 32, qs 64, 12 bytes of 6-bit scales, fp16 d, 2 of padding): Q6_K's term with q' 0 .. 7
 //     (2 bits from qs, bit 2 from hmask), - 4 sum x and the scales sc - 32
-//   IQ4_XS (its integer form w = D S v, 288 bytes: v as int8, the 16 int8 S, fp32 D): (D * xs) * (float) (S_0 sum v x
-//     + S_1 (...)) over the group's two halves of 16                                                  (iquants.h:49-55)
+//   the i-quants (IQ4_XS and the codebook types, their integer form w = D S v read by gw_iq.h: a half-group's 16 v and
+//     its S decoded from the super-block, D): (D * xs) * (float) (S_0 sum v x + S_1 (...)) over the group's two halves
+//     of 16                                                                                            (iquants.h:49-55)
 //   Q2_K (96 bytes: 16 scale bytes sc | m << 4, qs 64, fp16 d, dmin, padding; q 0 .. 3): (d * xs) * (float) (sc_0 sum q x
 //     + sc_1 (...)) - (dmin * xs) * (float) (m_0 sum x + m_1 (...))                                  (iquants.h:49-57)
 // then one lane per (activation row, weight row) folds the groups in order: val = val + term. mode 1: out = out + val.
@@ -981,8 +991,8 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
                         wv[u][r].y = (int)((((uint32_t)q.y >> sl) & 0x03030303u) | ((((uint32_t)hm.y >> sb) & 0x01010101u) << 2));
                         wv[u][r].z = (int)((((uint32_t)q.z >> sl) & 0x03030303u) | ((((uint32_t)hm.z >> sb) & 0x01010101u) << 2));
                         wv[u][r].w = (int)((((uint32_t)q.w >> sl) & 0x03030303u) | ((((uint32_t)hm.w >> sb) & 0x01010101u) << 2));
-                    } else if (TYPE == GW_IQ4_XS) { // (the integer form: the half-group's 16 values v as int8)
-                        wv[u][r] = *(const int4 *)(b + 16 * (j & 15));
+                    } else if constexpr (IqCb<TYPE>::iform) { // (the i-quants: the half-group's 16 values v, its S)
+                        iq_half<TYPE>(b, j & 15, wv[u][r], isc[u][r]);
                     } else if (TYPE == GW_Q2_K) { // (sub-block k = j % 16: 16 bytes of qs at 32 (k / 8) + 16 (k % 2), 2 bits 2 ((k / 2) % 4))
                         const int k = j & 15, sl = 2 * ((k >> 1) & 3);
                         const int4 q = *(const int4 *)(b + 16 + 32 * (k >> 3) + 16 * (k & 1));
@@ -1042,14 +1052,17 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
                     const uint32_t dw = (*(const uint4 *)(b + 80)).x;
                     f0[u][r] = h2f_g((uint16_t)(dw & 0xffffu));
                     f1[u][r] = h2f_g((uint16_t)(dw >> 16));
-                } else if (TYPE == GW_Q6_K || TYPE == GW_IQ4_XS) { // (IQ4_XS: the 16 int8 S at 256, D as fp32 at 272)
+                } else if constexpr (IqCb<TYPE>::iform) { // (S came with the values; D of the super-block)
+                    f0[u][r] = iq_d<TYPE>(rb + (size_t)(j >> 4) * bstride);
+                    f1[u][r] = 0.0f;
+                } else if (TYPE == GW_Q6_K) {
                     const int sblk = j >> 4, k = j & 15;
                     const uint8_t *b = rb + (size_t)sblk * bstride;
-                    const uint4 sw = *(const uint4 *)(b + (TYPE == GW_Q6_K ? 192 : 256)); // the 16 int8 scales
+                    const uint4 sw = *(const uint4 *)(b + 192); // the 16 int8 scales
                     uint32_t w = k < 4 ? sw.x : k < 8 ? sw.y : k < 12 ? sw.z : sw.w;
                     isc[u][r] = (int)(int8_t)((w >> (8 * (k & 3))) & 0xffu);
-                    const uint32_t dw = (*(const uint4 *)(b + (TYPE == GW_Q6_K ? 208 : 272))).x;
-                    f0[u][r] = TYPE == GW_Q6_K ? h2f_g((uint16_t)dw) : __uint_as_float(dw);
+                    const uint32_t dw = (*(const uint4 *)(b + 208)).x;
+                    f0[u][r] = h2f_g((uint16_t)dw);
                     f1[u][r] = 0.0f;
                 } else { // Q3_K (the 12 scale bytes s and d: 6-bit sc_k = low 4 bits of s[k % 8] (k / 8: high nibble) |
                          // bits 2 (k / 4) of s[8 + k % 4] << 4)
@@ -1085,7 +1098,7 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
                 #pragma unroll
                 for (int m = 0; m < M; m++) {
                     int xsum = 0; // K-quants: the sum of the half-group's activation codes
-                    if (TYPE != GW_Q8_0 && TYPE != GW_IQ4_XS) {
+                    if (TYPE != GW_Q8_0 && !IqCb<TYPE>::iform) {
                         xsum = __builtin_amdgcn_sdot4(xv[u][m].x, 0x01010101, 0, false);
                         xsum = __builtin_amdgcn_sdot4(xv[u][m].y, 0x01010101, xsum, false);
                         xsum = __builtin_amdgcn_sdot4(xv[u][m].z, 0x01010101, xsum, false);
@@ -1117,7 +1130,7 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
                             I = I + __shfl_xor(I, 1);
                             Mi = Mi + __shfl_xor(Mi, 1);
                             term = (f0[u][r] * xsg[u][m]) * (float)I - (f1[u][r] * xsg[u][m]) * (float)Mi;
-                        } else if (TYPE == GW_IQ4_XS) { // (I = S_0 T_0 + S_1 T_1, iquants.h:49-55)
+                        } else if (IqCb<TYPE>::iform) { // (I = S_0 T_0 + S_1 T_1, iquants.h:49-55)
                             int I = isc[u][r] * sd;
                             I = I + __shfl_xor(I, 1);
                             term = (f0[u][r] * xsg[u][m]) * (float)I;
@@ -1150,13 +1163,43 @@ __global__ __launch_bounds__(256) void k_gemv_mr(const uint8_t *__restrict__ W, 
     }
 }
 
-// x[b] = row tok[b] of a K-quant table (Q2_K .. Q6_K) or an IQ4_XS one, dequantized (kq_dequant_row, kquants.h:222-251;
+// an i-quant row's values (D S) v, one half-group per thread and step: exact in fp32 (iquants.h:211-216), so equal to
+// the reference's dequantization expressions (iq_dequant_row, iquants.h:217)
+template <int TYPE>
+__device__ __forceinline__ void embed_iq(float *__restrict__ y, int dim, const uint8_t *__restrict__ rb, int bstride) {
+    for (int j = threadIdx.x; j < dim / 16; j += blockDim.x) {
+        const uint8_t *b = rb + (size_t)(j >> 4) * bstride;
+        int4 v;
+        int S;
+        iq_half<TYPE>(b, j & 15, v, S);
+        const float ds = iq_d<TYPE>(b) * (float)S;
+        const uint32_t w[4] = { (uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w };
+        float o[16];
+        #pragma unroll
+        for (int e = 0; e < 16; e++) o[e] = ds * (float)(int8_t)(w[e >> 2] >> (8 * (e & 3)));
+        #pragma unroll
+        for (int e = 0; e < 16; e += 4) *(float4 *)(y + 16 * j + e) = make_float4(o[e], o[e + 1], o[e + 2], o[e + 3]);
+    }
+}
+
+// x[b] = row tok[b] of a K-quant table (Q2_K .. Q6_K) or an i-quant one, dequantized (kq_dequant_row, kquants.h:222-251;
 // iq_dequant_row, iquants.h:217; every value one rounding of an exact expression)
 __global__ __launch_bounds__(256) void k_embed_kq(float *__restrict__ x, int dim, int type, const uint8_t *__restrict__ W,
                                                   int bstride, const int *__restrict__ tok) {
     int bidx = blockIdx.x;
     size_t rowb = (size_t)(dim / 256) * bstride;
     const uint8_t *rb = W + (size_t)tok[bidx] * rowb;
+    float *xo = x + (size_t)bidx * dim;
+    switch (type) { // (the i-quants: whole half-groups)
+    case GW_IQ4_XS: embed_iq<GW_IQ4_XS>(xo, dim, rb, bstride); return;
+    case GW_IQ2_XXS: embed_iq<GW_IQ2_XXS>(xo, dim, rb, bstride); return;
+    case GW_IQ2_XS: embed_iq<GW_IQ2_XS>(xo, dim, rb, bstride); return;
+    case GW_IQ2_S: embed_iq<GW_IQ2_S>(xo, dim, rb, bstride); return;
+    case GW_IQ3_XXS: embed_iq<GW_IQ3_XXS>(xo, dim, rb, bstride); return;
+    case GW_IQ3_S: embed_iq<GW_IQ3_S>(xo, dim, rb, bstride); return;
+    case GW_IQ1_S: embed_iq<GW_IQ1_S>(xo, dim, rb, bstride); return;
+    case GW_IQ1_M: embed_iq<GW_IQ1_M>(xo, dim, rb, bstride); return;
+    }
     for (int i = threadIdx.x; i < dim; i += blockDim.x) {
         int s = i >> 8, k = i & 255;
         float y;
@@ -1185,10 +1228,6 @@ __global__ __launch_bounds__(256) void k_embed_kq(float *__restrict__ x, int dim
             const float dmin = __half2float(__ushort_as_half((uint16_t)(b[82] | b[83] << 8)));
             const float dl = d * (float)(sc & 15), ml = dmin * (float)(sc >> 4);
             y = dl * (float)q - ml;
-        } else if (type == GW_IQ4_XS) { // (D S) v on the integer form (iquants.h:330-340: (d (ls - 32)) kvalues_iq4nl[q])
-            const uint8_t *b = rb + (size_t)s * bstride;
-            const float D = *(const float *)(b + 272);
-            y = (D * (float)(int8_t)b[256 + k / 16]) * (float)(int8_t)b[k];
         } else {
             const uint8_t *b = rb + (size_t)s * bstride;
             int n = k / 128, p = k / 32 % 4, l = k % 32;
@@ -1238,30 +1277,41 @@ static int launch_gemv_mr(const uint8_t *W, const uint16_t *WS, int nrows, int K
     return (int)hipGetLastError();
 }
 
-// IQ4_XS's code values (ggml's kvalues_iq4nl, iq_grids.h:1082)
-static __constant__ int8_t gw_kv_iq4nl[16] = { -127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113 };
-
-// IQ4_XS super-block b (136 bytes: fp16 d, u16 scales_h, scales_l[4], qs[128]; iquants.h:28-30) -> its integer form
-// (GW_QI8_DEV bytes): thread (b, h) writes the 16 values v = kvalues_iq4nl[q] of half-group h (h = 2 ib + hi: the low
-// (hi 0) or high nibbles of qs[16 ib ..]) as int8 at 16 h, and S = ls - 32 of its group at 256 + h; h = 0 also D = d
-// (fp32) at 272 and the zero padding
-__global__ __launch_bounds__(256) void k_iq4xs_to_dev(const uint8_t *__restrict__ src, size_t nblk, uint8_t *__restrict__ dst) {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, b = i >> 4;
-    const int h = (int)(i & 15), ib = h >> 1, hi = h & 1;
-    if (b >= nblk) return;
-    const uint8_t *s = src + b * GW_IQ4XS_BYTES;
-    uint8_t *d = dst + b * GW_QI8_DEV;
-    uint32_t w[4] = { 0, 0, 0, 0 };
-    #pragma unroll
-    for (int j = 0; j < 16; j++)
-        w[j >> 2] |= (uint32_t)(uint8_t)gw_kv_iq4nl[(s[8 + 16 * ib + j] >> (4 * hi)) & 15] << (8 * (j & 3));
-    *(uint4 *)(d + 16 * h) = make_uint4(w[0], w[1], w[2], w[3]);
-    const int sh = s[2] | s[3] << 8, ls = ((s[4 + ib / 2] >> (4 * (ib % 2))) & 15) | ((sh >> (2 * ib)) & 3) << 4;
-    d[256 + h] = (uint8_t)(int8_t)(ls - 32);
-    if (h == 0) {
-        const float D = __half2float(__ushort_as_half((uint16_t)(s[0] | s[1] << 8)));
-        *(uint4 *)(d + 272) = make_uint4(__float_as_uint(D), 0u, 0u, 0u);
+// the device layout's byte k (gw_iq.h) of an i-quant super-block: its byte in the file's block, or -1 for padding;
+// IQ4_XS's S and D bytes (k 128 .. 139) are computed by k_iq_to_dev
+__device__ __forceinline__ int iq_src_byte(int type, int k) {
+    switch (type) {
+    case GW_IQ2_XXS: return k < 64 ? k + 2 : k < 66 ? k - 64 : -1;
+    case GW_IQ2_XS: return k < 72 ? k + 2 : k < 74 ? k - 72 : -1;
+    case GW_IQ2_S: return k < 80 ? k + 2 : k < 82 ? k - 80 : -1;
+    case GW_IQ3_XXS: return k < 96 ? k + 2 : k < 98 ? k - 96 : -1;
+    case GW_IQ3_S: return k < 64 ? k + 2 : k < 96 ? k + 10 : k < 104 ? k - 30 : k < 108 ? k + 2 : k < 110 ? k - 108 : -1;
+    case GW_IQ1_S: return k < 48 ? k + 2 : k < 50 ? k - 48 : -1;
+    case GW_IQ1_M: return k < 56 ? k : -1;
+    case GW_IQ4_XS: return k < 128 ? k + 8 : -1;
     }
+    return -1;
+}
+
+// an i-quant tensor's super-blocks (sb bytes each in the file) -> the device layout (db bytes), one thread per byte;
+// IQ4_XS: S = ls - 32 of group k - 128 (iquants.h:28-29) as int8, then D = d as fp32
+__global__ __launch_bounds__(256) void k_iq_to_dev(const uint8_t *__restrict__ src, size_t nblk, int type, int sb, int db,
+                                                   uint8_t *__restrict__ dst) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, b = i / (size_t)db;
+    const int k = (int)(i % (size_t)db);
+    if (b >= nblk) return;
+    const uint8_t *f = src + b * (size_t)sb;
+    int v = 0;
+    const int o = iq_src_byte(type, k);
+    if (o >= 0) v = f[o];
+    else if (type == GW_IQ4_XS && k < 136) {
+        const int ib = k - 128, sh = f[2] | f[3] << 8;
+        v = (uint8_t)(int8_t)((((f[4 + ib / 2] >> (4 * (ib % 2))) & 15) | ((sh >> (2 * ib)) & 3) << 4) - 32);
+    } else if (type == GW_IQ4_XS && k < 140) {
+        const float D = __half2float(__ushort_as_half((uint16_t)(f[0] | f[1] << 8)));
+        v = (__float_as_uint(D) >> (8 * (k - 136))) & 255u;
+    }
+    dst[i] = (uint8_t)v;
 }
 
 // dst super-block i (db bytes) = src super-block i (sb bytes) and zero padding
@@ -1430,8 +1480,9 @@ extern "C" {
 int gw_k_kq_to_dev(const uint8_t *src, size_t nblk, int type, uint8_t *dst, hipStream_t s) {
     const int sbytes = gw_kq_file_bytes(type), dbytes = gw_kq_dev_bytes(type);
     if (sbytes < 1 || dbytes < sbytes) return (int)hipErrorInvalidValue;
-    if (type == GW_IQ4_XS) {
-        hipLaunchKernelGGL(k_iq4xs_to_dev, dim3((unsigned)((nblk * 16 + 255) / 256)), dim3(256), 0, s, src, nblk, dst);
+    if (type == GW_IQ4_XS || GW_IS_CB(type)) {
+        const size_t n = nblk * (size_t)dbytes;
+        hipLaunchKernelGGL(k_iq_to_dev, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, nblk, type, sbytes, dbytes, dst);
         return (int)hipGetLastError();
     }
     size_t n = nblk * (size_t)dbytes;
@@ -1601,6 +1652,27 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
         } else if (w->type == GW_IQ4_XS) {
             if (g64) KQ_L(GW_IQ4_XS, 64);
             else KQ_L(GW_IQ4_XS, 32);
+        } else if (w->type == GW_IQ2_XXS) {
+            if (g64) KQ_L(GW_IQ2_XXS, 64);
+            else KQ_L(GW_IQ2_XXS, 32);
+        } else if (w->type == GW_IQ2_XS) {
+            if (g64) KQ_L(GW_IQ2_XS, 64);
+            else KQ_L(GW_IQ2_XS, 32);
+        } else if (w->type == GW_IQ2_S) {
+            if (g64) KQ_L(GW_IQ2_S, 64);
+            else KQ_L(GW_IQ2_S, 32);
+        } else if (w->type == GW_IQ3_XXS) {
+            if (g64) KQ_L(GW_IQ3_XXS, 64);
+            else KQ_L(GW_IQ3_XXS, 32);
+        } else if (w->type == GW_IQ3_S) {
+            if (g64) KQ_L(GW_IQ3_S, 64);
+            else KQ_L(GW_IQ3_S, 32);
+        } else if (w->type == GW_IQ1_S) {
+            if (g64) KQ_L(GW_IQ1_S, 64);
+            else KQ_L(GW_IQ1_S, 32);
+        } else if (w->type == GW_IQ1_M) {
+            if (g64) KQ_L(GW_IQ1_M, 64);
+            else KQ_L(GW_IQ1_M, 32);
         } else if (w->type == GW_Q2_K) {
             if (g64) KQ_L(GW_Q2_K, 64);
             else KQ_L(GW_Q2_K, 32);
@@ -1618,6 +1690,13 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
     if (w->type == GW_Q3_K) MRQ_L(GW_Q3_K);
     if (w->type == GW_IQ4_XS) MRQ_L(GW_IQ4_XS);
     if (w->type == GW_Q2_K) MRQ_L(GW_Q2_K);
+    if (w->type == GW_IQ2_XXS) MRQ_L(GW_IQ2_XXS);
+    if (w->type == GW_IQ2_XS) MRQ_L(GW_IQ2_XS);
+    if (w->type == GW_IQ2_S) MRQ_L(GW_IQ2_S);
+    if (w->type == GW_IQ3_XXS) MRQ_L(GW_IQ3_XXS);
+    if (w->type == GW_IQ3_S) MRQ_L(GW_IQ3_S);
+    if (w->type == GW_IQ1_S) MRQ_L(GW_IQ1_S);
+    if (w->type == GW_IQ1_M) MRQ_L(GW_IQ1_M);
 #undef MRQ_L
     return (int)hipErrorInvalidValue;
 }
@@ -1636,6 +1715,19 @@ int gw_k_matmul_swiglu(const GwMat *w, int il, const int8_t *xq, const float *xs
     hipExtLaunchKernelGGL((k_gemm_q8f<64, true>), dim3(nt, (M + 63) / 64), dim3(256), 0, s, e0, e1, 0, (const int8_t *)w->codes,
                           (const uint16_t *)w->scales, w->rows, w->cols, xq, xs, ldx, M, (float *)NULL, 0, hq, hs, ldq);
     return (int)hipGetLastError();
+}
+
+int gw_g_set_iq(const uint64_t *iq2xxs, const uint64_t *iq2xs, const uint64_t *iq2s, const uint64_t *iq1s,
+                const uint32_t *iq3xxs, const uint32_t *iq3s) {
+    /* the i-quant codebooks (gw_iq.h) on the current device: the 8-value grids as uint64, IQ1's as its two tables
+     * (2 x 2048: 8 grid + 1, 8 grid - 1), the 4-value grids as uint32 */
+    hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(gw_iq2xxs_g), iq2xxs, sizeof(uint64_t) * 256);
+    if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(gw_iq2xs_g), iq2xs, sizeof(uint64_t) * 512);
+    if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(gw_iq2s_g), iq2s, sizeof(uint64_t) * 1024);
+    if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(gw_iq1s_g), iq1s, sizeof(uint64_t) * 2 * 2048);
+    if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(gw_iq3xxs_g), iq3xxs, sizeof(uint32_t) * 256);
+    if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(gw_iq3s_g), iq3s, sizeof(uint32_t) * 512);
+    return (int)e;
 }
 
 int gw_g_set_exact(const float *rsq, int bits, const uint64_t *rcp, const uint8_t *expd) {
@@ -1706,10 +1798,11 @@ int gw_matmul_tile_rows(int rows) {
 
 int gw_kq_matmul(float *out, int type, const void *blocks, int N, int K, const int8_t *xq, const float *xs, int M, void *stream) {
     if (N <= 0 || K <= 0 || M <= 0 || K % 256 || !GW_IS_KQ(type) || !out || !blocks || !xq || !xs) return RQ_ERR_ARG;
+    if (GW_IS_CB(type) && gw_iq_init(NULL, 0) != RQ_OK) return RQ_ERR_STATE;
     const int fb = gw_kq_file_bytes(type), db = gw_kq_dev_bytes(type);
     GwMat w = { type, N, K, NULL, NULL, (uint8_t *)blocks, fb };
     if (fb == db) return gw_k_matmul(&w, xq, xs, K, M, out, N, 0, (hipStream_t)stream) ? RQ_ERR_STATE : RQ_OK;
-    // Q6_K, Q3_K, IQ4_XS: the file's blocks put into the device layout first (a temporary copy)
+    // Q6_K, Q3_K, Q2_K, the i-quants: the file's blocks put into the device layout first (a temporary copy)
     size_t nblk = (size_t)N * (K / 256);
     uint8_t *pad = NULL;
     if (hipMalloc((void **)&pad, nblk * db) != hipSuccess) return RQ_ERR_NOMEM;

@@ -16,7 +16,8 @@
 extern "C" {
 #endif
 
-enum { GW_F32 = 0, GW_Q8_0 = 8, GW_Q2_K = 10, GW_Q3_K = 11, GW_Q4_K = 12, GW_Q5_K = 13, GW_Q6_K = 14, GW_IQ4_XS = 23 }; /* ggml type numbers */
+enum { GW_F32 = 0, GW_Q8_0 = 8, GW_Q2_K = 10, GW_Q3_K = 11, GW_Q4_K = 12, GW_Q5_K = 13, GW_Q6_K = 14, GW_IQ2_XXS = 16,
+       GW_IQ2_XS = 17, GW_IQ3_XXS = 18, GW_IQ1_S = 19, GW_IQ3_S = 21, GW_IQ2_S = 22, GW_IQ4_XS = 23, GW_IQ1_M = 29 }; /* ggml type numbers */
 
 #define GW_ATT_T 16   /* positions per KV cache tile */
 #define GW_ATT_P 256  /* positions per attention block */
@@ -32,10 +33,27 @@ enum { GW_F32 = 0, GW_Q8_0 = 8, GW_Q2_K = 10, GW_Q3_K = 11, GW_Q4_K = 12, GW_Q5_
 #define GW_Q2K_BYTES 84     /* Q2_K in the file */
 #define GW_Q2K_DEV 96       /* ... on the device, padded as Q6_K */
 #define GW_IQ4XS_BYTES 136  /* IQ4_XS in the file */
-#define GW_QI8_DEV 288      /* ... on the device: its integer form w = D S v unpacked (the 256 v as int8, the 16 S of
-                             * each 16 values as int8, D as fp32 at byte 272, zero padding) */
-/* the super-block types (256 values; the matmul kernels' K-quant paths): Q2_K .. Q6_K and IQ4_XS */
-#define GW_IS_KQ(t) (((t) >= GW_Q2_K && (t) <= GW_Q6_K) || (t) == GW_IQ4_XS)
+#define GW_IQ4XS_DEV 144    /* ... on the device: the nibbles, the 8 S = ls - 32 as int8, D as fp32, padding (gw_iq.h) */
+/* the codebook i-quants (iquants.h:12-27), file and device bytes per super-block (gw_iq.h: the fields reordered so a
+ * half-group's are aligned dwords, d at the end, 2 bytes of padding; IQ1_M as the file) */
+#define GW_IQ2XXS_BYTES 66
+#define GW_IQ2XXS_DEV 68
+#define GW_IQ2XS_BYTES 74
+#define GW_IQ2XS_DEV 76
+#define GW_IQ2S_BYTES 82
+#define GW_IQ2S_DEV 84
+#define GW_IQ3XXS_BYTES 98
+#define GW_IQ3XXS_DEV 100
+#define GW_IQ3S_BYTES 110
+#define GW_IQ3S_DEV 112
+#define GW_IQ1S_BYTES 50
+#define GW_IQ1S_DEV 52
+#define GW_IQ1M_BYTES 56
+#define GW_IQ1M_DEV 56
+#define GW_IS_CB(t) ((t) == GW_IQ2_XXS || (t) == GW_IQ2_XS || (t) == GW_IQ2_S || (t) == GW_IQ3_XXS || (t) == GW_IQ3_S || \
+                     (t) == GW_IQ1_S || (t) == GW_IQ1_M)
+/* the super-block types (256 values; the matmul kernels' K-quant paths): Q2_K .. Q6_K and the i-quants */
+#define GW_IS_KQ(t) (((t) >= GW_Q2_K && (t) <= GW_Q6_K) || (t) == GW_IQ4_XS || GW_IS_CB(t))
 
 /* KV cache types (runq.h:214): the rotated 8-bit / 4-bit ones, and the bytes of a tile (16 positions x hd of one kv
  * head) of K (is_v 0) or V: f32 64 hd, 16-bit 32 hd, q8 17 hd, q4 9 hd (RQ_KV_Q4: K q8, V q4; RQ_KV_Q4K4: both q4) */
@@ -61,19 +79,45 @@ static inline size_t gw_kv_tile_bytes(int kvt, int hd, int is_v) {
 
 /* a K-quant super-block's bytes in the file and on the device (0: not a K-quant) */
 static inline int gw_kq_file_bytes(int type) {
-    return type == GW_Q3_K ? GW_Q3K_BYTES : type == GW_Q4_K ? GW_Q4K_BYTES : type == GW_Q5_K ? GW_Q5K_BYTES
-         : type == GW_Q6_K ? GW_Q6K_BYTES : type == GW_IQ4_XS ? GW_IQ4XS_BYTES : type == GW_Q2_K ? GW_Q2K_BYTES : 0;
+    switch (type) {
+    case GW_Q2_K: return GW_Q2K_BYTES;
+    case GW_Q3_K: return GW_Q3K_BYTES;
+    case GW_Q4_K: return GW_Q4K_BYTES;
+    case GW_Q5_K: return GW_Q5K_BYTES;
+    case GW_Q6_K: return GW_Q6K_BYTES;
+    case GW_IQ4_XS: return GW_IQ4XS_BYTES;
+    case GW_IQ2_XXS: return GW_IQ2XXS_BYTES;
+    case GW_IQ2_XS: return GW_IQ2XS_BYTES;
+    case GW_IQ2_S: return GW_IQ2S_BYTES;
+    case GW_IQ3_XXS: return GW_IQ3XXS_BYTES;
+    case GW_IQ3_S: return GW_IQ3S_BYTES;
+    case GW_IQ1_S: return GW_IQ1S_BYTES;
+    case GW_IQ1_M: return GW_IQ1M_BYTES;
+    }
+    return 0;
 }
 static inline int gw_kq_dev_bytes(int type) {
-    return type == GW_Q3_K ? GW_Q3K_DEV : type == GW_Q6_K ? GW_Q6K_DEV : type == GW_IQ4_XS ? GW_QI8_DEV
-         : type == GW_Q2_K ? GW_Q2K_DEV : gw_kq_file_bytes(type);
+    switch (type) {
+    case GW_Q2_K: return GW_Q2K_DEV;
+    case GW_Q3_K: return GW_Q3K_DEV;
+    case GW_Q6_K: return GW_Q6K_DEV;
+    case GW_IQ4_XS: return GW_IQ4XS_DEV;
+    case GW_IQ2_XXS: return GW_IQ2XXS_DEV;
+    case GW_IQ2_XS: return GW_IQ2XS_DEV;
+    case GW_IQ2_S: return GW_IQ2S_DEV;
+    case GW_IQ3_XXS: return GW_IQ3XXS_DEV;
+    case GW_IQ3_S: return GW_IQ3S_DEV;
+    case GW_IQ1_S: return GW_IQ1S_DEV;
+    case GW_IQ1_M: return GW_IQ1M_DEV;
+    }
+    return gw_kq_file_bytes(type);
 }
 
 /* A weight matrix on the device (rows x cols). Q8_0: int8 codes, row-major, and fp16 scales (cols / 32 per row),
  * the file's bytes split (34 bytes per 32 weights, as the file). K-quants: the file's super-blocks, row-major, each
  * bstride bytes apart (Q4_K 144, Q5_K 176; Q6_K 224: the file's 210 bytes and 14 of padding; Q3_K 112: 110 and 2;
  * Q2_K 96: 84 and 12);
- * IQ4_XS: GW_QI8_DEV-byte super-blocks of its integer form */
+ * the i-quants: their super-blocks with the fields reordered for aligned loads (gw_iq.h) */
 typedef struct {
     int type, rows, cols;
     int8_t *codes;
@@ -291,6 +335,11 @@ float gw_exp_mvec(float x);     /* libmvec's expf by its method: the device's ex
 int gw_k_set_exact(const float *rsq, int bits, const uint64_t *rcp, const uint8_t *expd); /* gw_kernels.hip's copy */
 int gw_v_set_exact(const float *rsq, int bits, const uint64_t *rcp, const uint8_t *expd); /* gw_gemv.hip's copy */
 int gw_g_set_exact(const float *rsq, int bits, const uint64_t *rcp, const uint8_t *expd); /* gw_gemm.hip's copy */
+/* the i-quant codebooks on the current device (gw_gemm.hip's kernels); gw_iq_init: expanded from gw_iq_tables.h once
+ * per process, installed once per device (the current one) */
+int gw_g_set_iq(const uint64_t *iq2xxs, const uint64_t *iq2xs, const uint64_t *iq2s, const uint64_t *iq1s,
+                const uint32_t *iq3xxs, const uint32_t *iq3s);
+int gw_iq_init(char *err, size_t errlen);
 /* vrcp14ps of d >= 1 from the compact table (one word per RCP_BLK_BITS-bit block of mantissas: the block's first value
  * and the value after its one step, as bits above 0.5's, and the step's offset): the result's bits */
 #define RCP_BLK_BITS 7
@@ -306,7 +355,7 @@ int gw_hip_fail(char *err, size_t errlen, const char *what, hipError_t e);
 int gw_k_embed_q8(float *x, int dim, const uint8_t *codes, const uint16_t *scales, const int *tok, int n, hipStream_t s);
 int gw_k_embed_kq(float *x, int dim, int type, const uint8_t *blocks, int bstride, const int *tok, int n, hipStream_t s);
 /* nblk super-blocks of type (the file's bytes at src) -> the device layout at dst (gw_kq_dev_bytes apart): Q6_K, Q3_K
- * zero-padded, IQ4_XS unpacked into its integer form (GW_QI8_DEV); a type whose layouts are equal: a copy */
+ * zero-padded, the i-quants' fields reordered (gw_iq.h); a type whose layouts are equal: a copy */
 int gw_k_kq_to_dev(const uint8_t *src, size_t nblk, int type, uint8_t *dst, hipStream_t s);
 int gw_k_rmsnorm_quant(float *x, const float *d, int dim, const float *w, const int *sel, int n, int8_t *xq, float *xs,
                        int ldq, float *hid, hipStream_t s);

@@ -156,7 +156,8 @@ static size_t type_row_bytes(uint32_t type, uint64_t k, int *ok) {
     switch (type) {
     case GW_F32: return (size_t)k * 4;
     case GW_Q8_0: if (k % 32) break; return (size_t)k / 32 * 34;
-    case GW_Q2_K: case GW_Q3_K: case GW_Q4_K: case GW_Q5_K: case GW_Q6_K: case GW_IQ4_XS:
+    case GW_Q2_K: case GW_Q3_K: case GW_Q4_K: case GW_Q5_K: case GW_Q6_K: case GW_IQ4_XS: case GW_IQ2_XXS: case GW_IQ2_XS:
+    case GW_IQ2_S: case GW_IQ3_XXS: case GW_IQ3_S: case GW_IQ1_S: case GW_IQ1_M:
         if (k % 256) break;
         return (size_t)k / 256 * (size_t)gw_kq_file_bytes((int)type);
     default: break;
@@ -358,8 +359,8 @@ static int load_mat_il(Loader *L, GwMat *dst, int r0, const char *name, int rows
         hipError_t e = hipMemcpy(dst->blocks, L->g.map + t->off, t->size, hipMemcpyHostToDevice);
         return e == hipSuccess ? RQ_OK : gw_hip_fail(L->err, L->errlen, "hipMemcpy (weights)", e);
     }
-    /* Q6_K, Q3_K, Q2_K: staged as the file's blocks, then padded to a 16-byte multiple each (aligned loads); IQ4_XS:
-     * staged, then unpacked into its integer form */
+    /* Q6_K, Q3_K, Q2_K: staged as the file's blocks, then padded to a 16-byte multiple each (aligned loads); the
+     * i-quants: staged, then their fields reordered (gw_iq.h) */
     if ((rc = stage(L, t)) != RQ_OK) return rc;
     if (gw_k_kq_to_dev(L->stage, nblk, dst->type, dst->blocks, 0))
         return lfail(L, RQ_ERR_STATE, "GGUF: %s: repack kernel failed", name);
@@ -483,7 +484,9 @@ RqModel *rq_model_load(const char *path, const RqModelOpts *o, char *err, size_t
         snprintf(err, errlen, "tokenizer_only: the program does not link the tokenizer (tokenizer.o, gguf.o, threads.o)");
         return NULL;
     }
-    if (!opts.tokenizer_only && (gw_device_init(err, errlen) != RQ_OK || gw_exact_init(err, errlen) != RQ_OK)) return NULL;
+    if (!opts.tokenizer_only && (gw_device_init(err, errlen) != RQ_OK || gw_exact_init(err, errlen) != RQ_OK ||
+                                 gw_iq_init(err, errlen) != RQ_OK))
+        return NULL;
     Loader L;
     memset(&L, 0, sizeof L);
     L.err = err;

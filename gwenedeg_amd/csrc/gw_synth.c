@@ -19,6 +19,10 @@
  *     q in 0..3
  *   IQ4_XS (iquants.h:28-30): 8 groups of 32, 6-bit ls (value (d (ls - 32)) kvalues_iq4nl[q]) with ls - 32 in 0..31
  *     for even groups and -31..0 for odd ones (both signs of the scale), q the nearest of the 16 code values
+ *   the codebook i-quants IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M (iquants.h:12-27): every grid index,
+ *     sign bit, scale and delta drawn uniformly from a stream seeded by the row's values (so every codebook entry and
+ *     sign pattern occurs), then d set so the block's rms equals the values' (a search for the nearest codebook
+ *     entries would not change what the parity tests check)
  * Any valid block decodes the same way on both sides, so these simple encoders suffice for parity. */
 #include <math.h>
 #include <pthread.h>
@@ -28,9 +32,19 @@
 #include <string.h>
 
 #include "gw_synth.h"
+#include "gw_iq_tables.h"
 
-enum { T_F32 = 0, T_Q8_0 = 8, T_Q2_K = 10, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ4_XS = 23 };
-#define IS_SB(t) (((t) >= T_Q2_K && (t) <= T_Q6_K) || (t) == T_IQ4_XS) /* (super-blocks of 256) */
+enum { T_F32 = 0, T_Q8_0 = 8, T_Q2_K = 10, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ2_XXS = 16, T_IQ2_XS = 17,
+       T_IQ3_XXS = 18, T_IQ1_S = 19, T_IQ3_S = 21, T_IQ2_S = 22, T_IQ4_XS = 23, T_IQ1_M = 29 };
+#define IS_CB(t) ((t) == T_IQ2_XXS || (t) == T_IQ2_XS || (t) == T_IQ2_S || (t) == T_IQ3_XXS || (t) == T_IQ3_S || \
+                  (t) == T_IQ1_S || (t) == T_IQ1_M)
+#define IS_SB(t) (((t) >= T_Q2_K && (t) <= T_Q6_K) || (t) == T_IQ4_XS || IS_CB(t)) /* (super-blocks of 256) */
+
+/* bytes per super-block of the codebook i-quants (iquants.h:140-154) */
+static int cb_bytes(int t) {
+    return t == T_IQ2_XXS ? 66 : t == T_IQ2_XS ? 74 : t == T_IQ2_S ? 82 : t == T_IQ3_XXS ? 98 : t == T_IQ3_S ? 110
+         : t == T_IQ1_S ? 50 : 56;
+}
 
 /* IQ4_XS's code values (ggml's kvalues_iq4nl) */
 static const int8_t kv_iq4nl[16] = { -127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113 };
@@ -91,6 +105,7 @@ size_t gw_synth_row_bytes(int type, int k) {
     if (type == T_Q6_K) return (size_t)k / 256 * 210;
     if (type == T_IQ4_XS) return (size_t)k / 256 * 136;
     if (type == T_Q2_K) return (size_t)k / 256 * 84;
+    if (IS_CB(type)) return (size_t)k / 256 * (size_t)cb_bytes(type);
     return (size_t)k * 4;
 }
 
@@ -311,6 +326,131 @@ static void enc_iq4_xs(uint8_t *o, const float *x, int k) {
     }
 }
 
+static void put16(uint8_t *p, uint16_t v) { memcpy(p, &v, 2); }
+static void put32(uint8_t *p, uint32_t v) { memcpy(p, &v, 4); }
+
+static void enc_iq_cb(int type, uint8_t *o, const float *x, int k) {
+    /* random valid blocks (see the header): fields drawn, the values' sum of squares of d = 1 accumulated as they are
+     * drawn (w = (d * mult) S v), then d = rms(x) / rms(w at d = 1) */
+    uint64_t st = 0x6a09e667f3bcc909ull;
+    for (int i = 0; i < k; i++) {
+        uint32_t u;
+        memcpy(&u, &x[i], 4);
+        st = (st ^ u) * 0x100000001b3ull;
+    }
+    const int bytes = cb_bytes(type);
+    const double mult = type == T_IQ3_XXS ? 0.25 : type == T_IQ3_S ? 1.0 : 0.125;
+    for (int sb = 0; sb < k / 256; sb++, o += bytes, x += 256) {
+        memset(o, 0, (size_t)bytes);
+        double ss = 0; /* sum of (S v)^2 */
+        for (int ib = 0; ib < 8; ib++) {
+            const uint32_t r0 = (uint32_t)splitmix(&st), r1 = (uint32_t)splitmix(&st);
+            if (type == T_IQ2_XXS) { /* a0: 4 indices; a1: 4 x 7 sign bits, ls */
+                put32(o + 2 + 8 * ib, r0);
+                put32(o + 6 + 8 * ib, r1);
+                const int S = 2 * (int)(r1 >> 28) + 1;
+                for (int l = 0; l < 4; l++)
+                    for (int j = 0; j < 8; j++) {
+                        const double v = GW_IQ2_VAL((gw_iq2xxs_codes[r0 >> 8 * l & 255] >> 2 * j) & 3);
+                        ss += (S * v) * (S * v);
+                    }
+            } else if (type == T_IQ2_XS || type == T_IQ2_S) {
+                const int sc = (int)(r1 & 255);
+                o[(type == T_IQ2_XS ? 66 : 74) + ib] = (uint8_t)sc;
+                const uint32_t r2 = (uint32_t)splitmix(&st);
+                for (int l = 0; l < 4; l++) {
+                    int idx;
+                    if (type == T_IQ2_XS) {
+                        const uint16_t q = (uint16_t)(l < 2 ? r0 >> 16 * l : r2 >> 16 * (l - 2));
+                        put16(o + 2 + 2 * (4 * ib + l), q);
+                        idx = q & 511;
+                    } else {
+                        o[2 + 4 * ib + l] = (uint8_t)(r0 >> 8 * l);
+                        o[34 + 4 * ib + l] = (uint8_t)(r2 >> 8 * l);
+                        idx = o[2 + 4 * ib + l] | ((r1 >> (8 + 2 * l)) & 3) << 8;
+                        o[66 + ib] |= (uint8_t)(((r1 >> (8 + 2 * l)) & 3) << 2 * l);
+                    }
+                    const int S = 2 * ((sc >> 4 * (l / 2)) & 15) + 1;
+                    const uint16_t *cd = type == T_IQ2_XS ? gw_iq2xs_codes : gw_iq2s_codes;
+                    for (int j = 0; j < 8; j++) {
+                        const double v = GW_IQ2_VAL((cd[idx] >> 2 * j) & 3);
+                        ss += (S * v) * (S * v);
+                    }
+                }
+            } else if (type == T_IQ3_XXS) { /* qs: 8 indices of 4 values; a: 4 x 7 sign bits, ls */
+                const uint32_t r2 = (uint32_t)splitmix(&st);
+                put32(o + 2 + 8 * ib, r0);
+                put32(o + 6 + 8 * ib, r2);
+                put32(o + 66 + 4 * ib, r1);
+                const int S = 2 * (int)(r1 >> 28) + 1;
+                for (int t = 0; t < 8; t++) {
+                    const int idx = o[2 + 8 * ib + t];
+                    for (int j = 0; j < 4; j++) {
+                        const double v = GW_IQ3XXS_VAL((gw_iq3xxs_codes[idx] >> 3 * j) & 7);
+                        ss += (S * v) * (S * v);
+                    }
+                }
+            } else if (type == T_IQ3_S) { /* qs, qh (index bit 8), raw signs, 4-bit scales */
+                const uint32_t r2 = (uint32_t)splitmix(&st), r3 = (uint32_t)splitmix(&st);
+                put32(o + 2 + 8 * ib, r0);
+                put32(o + 6 + 8 * ib, r2);
+                o[66 + ib] = (uint8_t)r1;
+                put32(o + 74 + 4 * ib, r3);
+                o[106 + ib / 2] |= (uint8_t)(((r1 >> 8) & 15) << 4 * (ib % 2));
+                const int S = 2 * (int)((r1 >> 8) & 15) + 1;
+                for (int t = 0; t < 8; t++) {
+                    const int idx = o[2 + 8 * ib + t] | ((r1 >> t) & 1) << 8;
+                    for (int j = 0; j < 4; j++) {
+                        const double v = 2 * ((gw_iq3s_codes[idx] >> 3 * j) & 7) + 1;
+                        ss += (S * v) * (S * v);
+                    }
+                }
+            } else if (type == T_IQ1_S) { /* qs; qh: 4 x 3 index bits, the 3-bit scale, the delta's sign */
+                put32(o + 2 + 4 * ib, r0);
+                const uint16_t qh = (uint16_t)r1;
+                put16(o + 34 + 2 * ib, qh);
+                const int S = 2 * ((qh >> 12) & 7) + 1, dl = qh & 0x8000 ? -1 : 1;
+                for (int l = 0; l < 4; l++) {
+                    const int idx = (int)(r0 >> 8 * l & 255) | ((qh >> 3 * l) & 7) << 8;
+                    for (int j = 0; j < 8; j++) {
+                        const double v = 8 * (((gw_iq1s_codes[idx] >> 2 * j) & 3) - 1) + dl;
+                        ss += (S * v) * (S * v);
+                    }
+                }
+            } else { /* IQ1_M: qs; qh nibbles (3 index bits, the delta's sign) per chunk; 3-bit scales per 16 */
+                put32(o + 4 * ib, r0);
+                o[32 + 2 * ib] = (uint8_t)r1;
+                o[33 + 2 * ib] = (uint8_t)(r1 >> 8);
+                const int s6 = (int)((r1 >> 16) & 63); /* (the group's two 3-bit scales, into sc[ib / 2] below) */
+                uint16_t scw;
+                memcpy(&scw, o + 48 + 2 * (ib / 2), 2);
+                scw |= (uint16_t)(s6 << 6 * (ib % 2));
+                put16(o + 48 + 2 * (ib / 2), scw);
+                for (int l = 0; l < 4; l++) {
+                    const int q = (o[32 + 2 * ib + l / 2] >> 4 * (l % 2)) & 15, dl = q & 8 ? -1 : 1;
+                    const int idx = (int)(r0 >> 8 * l & 255) | (q & 7) << 8, S = 2 * ((s6 >> 3 * (l / 2)) & 7) + 1;
+                    for (int j = 0; j < 8; j++) {
+                        const double v = 8 * (((gw_iq1s_codes[idx] >> 2 * j) & 3) - 1) + dl;
+                        ss += (S * v) * (S * v);
+                    }
+                }
+            }
+        }
+        double xs = 0;
+        for (int i = 0; i < 256; i++) xs += (double)x[i] * x[i];
+        const double rw = sqrt(ss / 256.0) * mult;
+        uint16_t hd = f32_to_f16_rne(rw > 0 ? (float)(sqrt(xs / 256.0) / rw) : 0.0f);
+        if (type == T_IQ1_M) { /* d in the top nibbles of sc[0..3] */
+            for (int w = 0; w < 4; w++) {
+                uint16_t scw;
+                memcpy(&scw, o + 48 + 2 * w, 2);
+                scw = (uint16_t)((scw & 0x0fff) | ((hd >> 4 * w) & 15) << 12);
+                put16(o + 48 + 2 * w, scw);
+            }
+        } else put16(o, hd);
+    }
+}
+
 void gw_synth_encode_row(int type, uint8_t *o, const float *x, int k) {
     if (type == T_Q8_0) enc_q8_0(o, x, k);
     else if (type == T_Q4_K) enc_q45_k(o, x, k, 0);
@@ -319,6 +459,7 @@ void gw_synth_encode_row(int type, uint8_t *o, const float *x, int k) {
     else if (type == T_Q6_K) enc_q6_k(o, x, k);
     else if (type == T_IQ4_XS) enc_iq4_xs(o, x, k);
     else if (type == T_Q2_K) enc_q2_k(o, x, k);
+    else if (IS_CB(type)) enc_iq_cb(type, o, x, k);
     else memcpy(o, x, (size_t)k * 4);
 }
 

@@ -14,6 +14,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _PATH = os.path.join(_HERE, "lib", "libgwsynth.so")
 
 Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_XS = 8, 10, 11, 12, 13, 14, 23
+IQ2_XXS, IQ2_XS, IQ3_XXS, IQ1_S, IQ3_S, IQ2_S, IQ1_M = 16, 17, 18, 19, 21, 22, 29
 
 
 class GwSynthCfg(ctypes.Structure):
@@ -48,6 +49,11 @@ SHAPES = {
     # IQ4_XS-style (the i-quant IQ4_XS on every matrix and the embedding, Q6_K output)
     "tiny_iq4xs": dict(dim=512, hidden=1024, n_layers=2, n_heads=8, n_kv_heads=2, head_dim=128, vocab=2048,
                        ctx_len=4096, tied=0, type_default=IQ4_XS, type_out=Q6_K),
+    # the codebook i-quants, each on every matrix and the embedding (Q6_K output), one shape per type
+    **{f"tiny_{n.lower()}": dict(dim=512, hidden=1024, n_layers=2, n_heads=8, n_kv_heads=2, head_dim=128, vocab=2048,
+                                 ctx_len=4096, tied=0, type_default=t, type_out=Q6_K)
+       for n, t in (("IQ2_XXS", IQ2_XXS), ("IQ2_XS", IQ2_XS), ("IQ2_S", IQ2_S), ("IQ3_XXS", IQ3_XXS), ("IQ3_S", IQ3_S),
+                    ("IQ1_S", IQ1_S), ("IQ1_M", IQ1_M))},
     # Q2_K-style (Q2_K on most matrices and the embedding, Q4_K on v, Q6_K output)
     "tiny_q2k": dict(dim=512, hidden=1024, n_layers=2, n_heads=8, n_kv_heads=2, head_dim=128, vocab=2048,
                      ctx_len=4096, tied=0, type_default=Q2_K, type_v=Q4_K, type_out=Q6_K),

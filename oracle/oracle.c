@@ -40,6 +40,7 @@
 #include <string.h>
 
 #include "oracle.h"
+#include "gw_iq_tables.h" /* (the i-quant codebooks, checked against the reference's own dequantization by the tests) */
 
 #define GS 32
 #define ATT_T 16
@@ -156,8 +157,12 @@ void or_q8_from_blocks(int8_t *q, float *s, const uint8_t *blk, size_t nblk) {
 
 /* ---------------------------------------------------------------------------------------- K-quants */
 
-enum { T_F32 = 0, T_Q8_0 = 8, T_Q2_K = 10, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ4_XS = 23 };
-#define IS_KQ(t) (((t) >= T_Q2_K && (t) <= T_Q6_K) || (t) == T_IQ4_XS)
+enum { T_F32 = 0, T_Q8_0 = 8, T_Q2_K = 10, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ2_XXS = 16, T_IQ2_XS = 17,
+       T_IQ3_XXS = 18, T_IQ1_S = 19, T_IQ3_S = 21, T_IQ2_S = 22, T_IQ4_XS = 23, T_IQ1_M = 29 };
+/* the codebook i-quants (iquants.h:12-27) */
+#define IS_CB(t) ((t) == T_IQ2_XXS || (t) == T_IQ2_XS || (t) == T_IQ2_S || (t) == T_IQ3_XXS || (t) == T_IQ3_S || \
+                  (t) == T_IQ1_S || (t) == T_IQ1_M)
+#define IS_KQ(t) (((t) >= T_Q2_K && (t) <= T_Q6_K) || (t) == T_IQ4_XS || IS_CB(t))
 
 /* IQ4_XS's 16 code values (ggml's kvalues_iq4nl, iq_grids.h:1082; iquants.h:28-30) */
 static const int8_t kv_iq4nl[16] = { -127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113 };
@@ -198,7 +203,148 @@ static int q3k_scale(const uint8_t *b, int j) { /* kquants.h:207-212: the 6-bit 
 }
 
 static int kq_bytes(int type) {
-    return type == T_Q4_K ? 144 : type == T_Q5_K ? 176 : type == T_Q3_K ? 110 : type == T_IQ4_XS ? 136 : type == T_Q2_K ? 84 : 210;
+    /* kquants.h:9-33; iquants.h:140-154 */
+    switch (type) {
+    case T_Q4_K: return 144;
+    case T_Q5_K: return 176;
+    case T_Q3_K: return 110;
+    case T_Q2_K: return 84;
+    case T_IQ4_XS: return 136;
+    case T_IQ2_XXS: return 66;
+    case T_IQ2_XS: return 74;
+    case T_IQ2_S: return 82;
+    case T_IQ3_XXS: return 98;
+    case T_IQ3_S: return 110;
+    case T_IQ1_S: return 50;
+    case T_IQ1_M: return 56;
+    }
+    return 210;
+}
+
+/* ------------------------------------------------------------------ the codebook i-quants (iquants.h:8-57) */
+
+static uint32_t u32le(const uint8_t *p) { uint32_t v; memcpy(&v, p, 4); return v; }
+static unsigned ksigns(unsigned s) { return s | (__builtin_popcount(s) & 1u) << 7; } /* iquants.h:9, :197 */
+
+static uint16_t iq1m_d16(const uint8_t *b) { /* iquants.h:200-205: the fp16 d in the 4 scale words' top nibbles */
+    uint16_t sc0 = u16(b + 48), sc1 = u16(b + 50), sc2 = u16(b + 52), sc3 = u16(b + 54);
+    return (uint16_t)((sc0 >> 12) | ((sc1 >> 8) & 0x00f0) | ((sc2 >> 4) & 0x0f00) | (sc3 & 0xf000));
+}
+
+/* group ib (32 values) of a block in its integer form (iquants.h:33-47): v[32], S[h] for the two halves of 16, D */
+static void cb_group(int type, const uint8_t *b, int ib, int v[32], int S[2], float *D) {
+    if (type == T_IQ2_XXS) { /* a0: 4 grid indices; a1: 4 x 7 sign bits, ls in the top 4 (iquants.h:12-13) */
+        uint32_t a0 = u32le(b + 2 + 8 * ib), a1 = u32le(b + 6 + 8 * ib);
+        for (int l = 0; l < 4; l++) {
+            uint64_t g = gw_iq2_entry(gw_iq2xxs_codes, (int)(a0 >> 8 * l & 255));
+            unsigned sg = ksigns(a1 >> 7 * l & 127);
+            for (int j = 0; j < 8; j++) v[8 * l + j] = (int)(g >> 8 * j & 255) * (sg >> j & 1 ? -1 : 1);
+        }
+        S[0] = S[1] = 2 * (int)(a1 >> 28) + 1;
+        *D = or_fp16_to_f32(u16(b)) * 0.125f;
+    } else if (type == T_IQ2_XS || type == T_IQ2_S) { /* iquants.h:14-17 */
+        for (int l = 0; l < 4; l++) {
+            uint64_t g;
+            unsigned sg;
+            if (type == T_IQ2_XS) {
+                int q = u16(b + 2 + 2 * (4 * ib + l));
+                g = gw_iq2_entry(gw_iq2xs_codes, q & 511);
+                sg = ksigns((unsigned)q >> 9);
+            } else {
+                g = gw_iq2_entry(gw_iq2s_codes, b[2 + 4 * ib + l] | (b[66 + ib] << (8 - 2 * l) & 0x300));
+                sg = b[34 + 4 * ib + l];
+            }
+            for (int j = 0; j < 8; j++) v[8 * l + j] = (int)(g >> 8 * j & 255) * (sg >> j & 1 ? -1 : 1);
+        }
+        int sc = b[(type == T_IQ2_XS ? 66 : 74) + ib];
+        S[0] = 2 * (sc & 15) + 1;
+        S[1] = 2 * (sc >> 4) + 1;
+        *D = or_fp16_to_f32(u16(b)) * 0.125f;
+    } else if (type == T_IQ3_XXS) { /* iquants.h:18-19: qs[8 ib + t] the index of values 4 t ..; then per group a u32 */
+        uint32_t a = u32le(b + 66 + 4 * ib);
+        for (int l = 0; l < 4; l++) {
+            unsigned sg = ksigns(a >> 7 * l & 127);
+            for (int hh = 0; hh < 2; hh++) {
+                uint32_t g = gw_iq3xxs_entry(b[2 + 8 * ib + 2 * l + hh]);
+                for (int j = 0; j < 4; j++) v[8 * l + 4 * hh + j] = (int)(g >> 8 * j & 255) * (sg >> (4 * hh + j) & 1 ? -1 : 1);
+            }
+        }
+        S[0] = S[1] = 2 * (int)(a >> 28) + 1;
+        *D = or_fp16_to_f32(u16(b)) * 0.25f;
+    } else if (type == T_IQ3_S) { /* iquants.h:20-21: qh bit t of group ib = index bit 8 of step t; raw signs */
+        int qh = b[66 + ib];
+        for (int l = 0; l < 4; l++) {
+            unsigned sg = b[74 + 4 * ib + l];
+            for (int hh = 0; hh < 2; hh++) {
+                uint32_t g = gw_iq3s_entry(b[2 + 8 * ib + 2 * l + hh] | (qh << (8 - 2 * l - hh) & 256));
+                for (int j = 0; j < 4; j++) v[8 * l + 4 * hh + j] = (int)(g >> 8 * j & 255) * (sg >> (4 * hh + j) & 1 ? -1 : 1);
+            }
+        }
+        S[0] = S[1] = 1 + 2 * (b[106 + ib / 2] >> 4 * (ib % 2) & 15);
+        *D = or_fp16_to_f32(u16(b));
+    } else if (type == T_IQ1_S) { /* iquants.h:22-24: v = 8 grid + (delta < 0 ? -1 : 1) */
+        int qh = u16(b + 34 + 2 * ib), dl = qh & 0x8000 ? -1 : 1;
+        for (int l = 0; l < 4; l++) {
+            uint64_t g = gw_iq1s_entry(b[2 + 4 * ib + l] | (qh >> 3 * l & 7) << 8);
+            for (int j = 0; j < 8; j++) v[8 * l + j] = 8 * (int)(int8_t)(g >> 8 * j) + dl;
+        }
+        S[0] = S[1] = 2 * (qh >> 12 & 7) + 1;
+        *D = or_fp16_to_f32(u16(b)) * 0.125f;
+    } else { /* IQ1_M, iquants.h:25-27: per chunk of 8 its delta sign; 3-bit scales per 16 */
+        int sc = u16(b + 48 + 2 * (ib / 2));
+        for (int l = 0; l < 4; l++) {
+            int q = b[32 + 2 * ib + l / 2] >> 4 * (l % 2), dl = q & 8 ? -1 : 1;
+            uint64_t g = gw_iq1s_entry(b[4 * ib + l] | (q & 7) << 8);
+            for (int j = 0; j < 8; j++) v[8 * l + j] = 8 * (int)(int8_t)(g >> 8 * j) + dl;
+        }
+        S[0] = 2 * (sc >> (6 * (ib % 2)) & 7) + 1;
+        S[1] = 2 * (sc >> (6 * (ib % 2) + 3) & 7) + 1;
+        *D = or_fp16_to_f32(iq1m_d16(b)) * 0.125f;
+    }
+}
+
+static void cb_dequant(int type, const uint8_t *b, float *y) {
+    /* iquants.h:217-345 (ggml's dequantize_row_*): one block, each type's own expression */
+    float d = or_fp16_to_f32(type == T_IQ1_M ? iq1m_d16(b) : u16(b));
+    for (int ib = 0; ib < 8; ib++) {
+        if (type == T_IQ1_S || type == T_IQ1_M) { /* d (2 s + 1) (grid + delta), delta = +-0.125 */
+            for (int l = 0; l < 4; l++) {
+                int idx, s3;
+                float delta;
+                if (type == T_IQ1_S) {
+                    int qh = u16(b + 34 + 2 * ib);
+                    idx = b[2 + 4 * ib + l] | (qh >> 3 * l & 7) << 8;
+                    s3 = qh >> 12 & 7;
+                    delta = qh & 0x8000 ? -0.125f : 0.125f;
+                } else {
+                    int sc = u16(b + 48 + 2 * (ib / 2)), q = b[32 + 2 * ib + l / 2] >> 4 * (l % 2);
+                    idx = b[4 * ib + l] | (q & 7) << 8;
+                    s3 = sc >> (6 * (ib % 2) + 3 * (l / 2)) & 7;
+                    delta = q & 8 ? -0.125f : 0.125f;
+                }
+                float dl = d * (float)(2 * s3 + 1);
+                uint64_t g = gw_iq1s_entry(idx);
+                for (int j = 0; j < 8; j++) y[32 * ib + 8 * l + j] = dl * ((float)(int8_t)(g >> 8 * j) + delta);
+            }
+            continue;
+        }
+        int v[32], S[2];
+        float D;
+        cb_group(type, b, ib, v, S, &D); /* (the grid values with their signs; the scales below from the block) */
+        for (int i = 0; i < 32; i++) {
+            int h = i / 16, gv = v[i] < 0 ? -v[i] : v[i];
+            float sg = v[i] < 0 ? -1.f : 1.f, y0;
+            if (type == T_IQ2_XXS) /* d (0.5 + ls) 0.25 */
+                y0 = d * (0.5f + (float)(u32le(b + 6 + 8 * ib) >> 28)) * 0.25f;
+            else if (type == T_IQ2_XS || type == T_IQ2_S) /* d (0.5 + sc) 0.25, sc the nibble of the half */
+                y0 = d * (0.5f + (float)(b[(type == T_IQ2_XS ? 66 : 74) + ib] >> 4 * h & 15)) * 0.25f;
+            else if (type == T_IQ3_XXS) /* d (0.5 + ls) 0.5 */
+                y0 = d * (0.5f + (float)(u32le(b + 66 + 4 * ib) >> 28)) * 0.5f;
+            else /* IQ3_S: d (1 + 2 sc) */
+                y0 = d * (float)(1 + 2 * (b[106 + ib / 2] >> 4 * (ib % 2) & 15));
+            y[32 * ib + i] = y0 * (float)gv * sg;
+        }
+    }
 }
 
 static int q2k_q(const uint8_t *b, int i) { /* iquants.h:10-11: 2 bits 2 (i / 32 % 4) of qs[32 (i / 128) + i % 32] */
@@ -239,6 +385,8 @@ void or_kq_dequant_row(int type, const uint8_t *blk, int n, float *y) {
                 float dl = d * (float)(b[i / 16] & 15), ml = dmin * (float)(b[i / 16] >> 4);
                 y[i] = dl * (float)q2k_q(b, i) - ml;
             }
+        } else if (IS_CB(type)) {
+            cb_dequant(type, b, y);
         } else if (type == T_IQ4_XS) { /* iquants.h:330-340 (ggml's dequantize_row_iq4_xs): (d (ls - 32)) v */
             float d = or_fp16_to_f32(u16(b));
             for (int ib = 0; ib < 8; ib++) {
@@ -305,6 +453,17 @@ static float kq_dot_row(int type, const uint8_t *row, const int8_t *x, const flo
                 }
                 float d = or_fp16_to_f32(u16(b + 80)), dmin = or_fp16_to_f32(u16(b + 82));
                 val = val + ((d * xs[g]) * (float)I - (dmin * xs[g]) * (float)Mi);
+            } else if (IS_CB(type)) { /* iquants.h:49-55: I = S_0 T_0 + S_1 T_1 (exact int), val = val + (D xs) I */
+                int v[32], S[2];
+                float D;
+                cb_group(type, b, j, v, S, &D);
+                int32_t I = 0;
+                for (int h = 0; h < 2; h++) {
+                    int32_t t = 0;
+                    for (int i = 0; i < 16; i++) t += v[16 * h + i] * xg[16 * h + i];
+                    I += S[h] * t;
+                }
+                val = val + (D * xs[g]) * (float)I;
             } else if (type == T_IQ4_XS) { /* iquants.h:49-55: I = S_0 T_0 + S_1 T_1, S = ls - 32 on both halves, D = d */
                 int32_t I = 0, S = iq4xs_ls(b, j) - 32;
                 for (int h = 0; h < 2; h++) {

@@ -18,7 +18,9 @@ REF_DIR = os.path.join(HERE, "_ref")
 REF_DRIVER = os.path.join(REF_DIR, "ref_driver")
 REF_Q8OP = os.path.join(REF_DIR, "ref_q8op")
 REF_SAMPLE = os.path.join(REF_DIR, "ref_sample")
-Q2_K, IQ4_XS = 10, 23  # (ggml type numbers: the types run by iquants.h's kernels)
+Q2_K, IQ4_XS = 10, 23  # (ggml type numbers: the types run by iquants.h's kernels, with the codebook i-quants below)
+IQ2_XXS, IQ2_XS, IQ3_XXS, IQ1_S, IQ3_S, IQ2_S, IQ1_M = 16, 17, 18, 19, 21, 22, 29
+IQ_TYPES = (Q2_K, IQ2_XXS, IQ2_XS, IQ3_XXS, IQ1_S, IQ3_S, IQ2_S, IQ4_XS, IQ1_M)
 
 _lib = None
 
@@ -269,12 +271,23 @@ def run_ref_kq(workdir: str, typ: int, blocks, xq, xs, N: int, K: int, timeout: 
     paths = [os.path.join(workdir, n) for n in ("blk.bin", "x.bin", "xs.bin", "out.bin")]
     for a, p in zip((blocks, xq, xs), paths):
         np.ascontiguousarray(a).tofile(p)
-    mode = "iq" if typ in (Q2_K, IQ4_XS) else "kq"  # (Q2_K and the i-quants: iquants.h's packing and kernels)
+    mode = "iq" if typ in IQ_TYPES else "kq"  # (Q2_K and the i-quants: iquants.h's packing and kernels)
     cmd = [REF_Q8OP, mode, str(typ), *paths[:3], str(M), str(N), str(K), paths[3]]
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)
     if r.returncode != 0:
         raise RuntimeError(f"ref_q8op {mode} failed: {r.stderr[-2000:]}")
     return np.fromfile(paths[3], np.float32).reshape(M, N)
+
+
+def run_ref_iq_dequant(workdir: str, typ: int, blocks, nblk: int, timeout: float = 120):
+    """the reference's iq_dequant_row (iquants.h:217) on nblk blocks of an i-quant type: 256 nblk floats"""
+    os.makedirs(workdir, exist_ok=True)
+    pb, po = os.path.join(workdir, "dq_blk.bin"), os.path.join(workdir, "dq_out.bin")
+    np.ascontiguousarray(blocks).tofile(pb)
+    r = subprocess.run([REF_Q8OP, "iqdq", str(typ), pb, str(nblk), po], capture_output=True, text=True, timeout=timeout)
+    if r.returncode != 0:
+        raise RuntimeError(f"ref_q8op iqdq failed: {r.stderr[-2000:]}")
+    return np.fromfile(po, np.float32)
 
 
 def run_ref_sample(workdir: str, logits, k: int, temperature: float, topp: float, rng: int, timeout: float = 120):

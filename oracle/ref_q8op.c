@@ -13,9 +13,11 @@
  *       BLK: N rows of K / 256 GGUF K-quant blocks (TYPE 11 Q3_K, 12 Q4_K, 13 Q5_K, 14 Q6_K), packed by kq_pack_blocks
  *       (kquants.h:253) and multiplied by the generic kq_dot (:608) with kq_act_prep's xf (:392).
  *   ref_q8op iq TYPE BLK X XS M N K OUT
- *       BLK: N rows of K / 256 GGUF blocks (TYPE 10 Q2_K, 23 IQ4_XS), packed by iq_pack_blocks (iquants.h:503) and
- *       multiplied by iq_rows (:1478), the forward's dispatch (the AVX-512 kernels of this build), with the activation
- *       sums of 16 of kq512_c16 (kernels_avx512.h:342).
+ *       BLK: N rows of K / 256 GGUF blocks (TYPE 10 Q2_K, 16 IQ2_XXS, 17 IQ2_XS, 18 IQ3_XXS, 19 IQ1_S, 21 IQ3_S, 22 IQ2_S,
+ *       23 IQ4_XS, 29 IQ1_M), packed by iq_pack_blocks (iquants.h:503) and multiplied by iq_rows (:1478), the forward's
+ *       dispatch (the AVX-512 kernels of this build), with the activation sums of 16 of kq512_c16 (kernels_avx512.h:342).
+ *   ref_q8op iqdq TYPE BLK NBLK OUT
+ *       NBLK blocks of one of those types dequantized by iq_dequant_row (iquants.h:217): OUT 256 NBLK fp32.
  * All files raw little-endian arrays. */
 #include <pthread.h>
 #include <stdint.h>
@@ -153,7 +155,7 @@ int main(int argc, char **argv) {
     }
     if (argc >= 10 && !strcmp(argv[1], "iq")) {
         int type = atoi(argv[2]), M = atoi(argv[6]), N = atoi(argv[7]), K = atoi(argv[8]);
-        if ((type != GGML_IQ4_XS && type != GGML_Q2_K) || M < 1 || N % 16 || K % 256) { fprintf(stderr, "ref_q8op: bad iq args\n"); return 2; }
+        if (!iq_type(type) || type & IQ_R || M < 1 || N % 16 || K % 256) { fprintf(stderr, "ref_q8op: bad iq args\n"); return 2; }
         uint8_t *blk = slurp(argv[3], (size_t)N * (K / 256) * iq_block_bytes(type));
         int8_t *X = slurp(argv[4], (size_t)M * K);
         float *XS = slurp(argv[5], (size_t)M * (K / 32) * 4);
@@ -168,6 +170,17 @@ int main(int argc, char **argv) {
         fclose(f);
         return 0;
     }
-    fprintf(stderr, "usage: ref_q8op q8 W WS X XS M N K OUT [reps threads] | kq|iq TYPE BLK X XS M N K OUT\n");
+    if (argc >= 6 && !strcmp(argv[1], "iqdq")) { /* iq_dequant_row (iquants.h:217): NBLK blocks of TYPE -> 256 NBLK floats */
+        int type = atoi(argv[2]), nblk = atoi(argv[4]);
+        if (!iq_type(type) || type & IQ_R || nblk < 1) { fprintf(stderr, "ref_q8op: bad iqdq args\n"); return 2; }
+        uint8_t *blk = slurp(argv[3], (size_t)nblk * iq_block_bytes(type));
+        float *y = malloc((size_t)nblk * 256 * sizeof(float));
+        iq_dequant_row(type, blk, 256 * nblk, y);
+        FILE *f = fopen(argv[5], "wb");
+        if (!f || fwrite(y, sizeof(float), (size_t)nblk * 256, f) != (size_t)nblk * 256) { perror(argv[5]); return 1; }
+        fclose(f);
+        return 0;
+    }
+    fprintf(stderr, "usage: ref_q8op q8 W WS X XS M N K OUT [reps threads] | kq|iq TYPE BLK X XS M N K OUT | iqdq TYPE BLK NBLK OUT\n");
     return 2;
 }

@@ -103,14 +103,14 @@ def test_q8_pack_and_block_sums(dev):
     assert np.array_equal(got[1, 7], (wq2[7].astype(np.int64).reshape(-1, 32) * xq[1].astype(np.int64).reshape(-1, 32)).sum(1))
 
 
-@pytest.mark.parametrize("typ", [10, 11, 12, 13, 14, 23])
+@pytest.mark.parametrize("typ", [10, 11, 12, 13, 14, 23, 16, 17, 22, 18, 21, 19, 29])
 @pytest.mark.parametrize("M,tile", [(1, 0), (3, 0), (6, 0), (9, 0), (20, 0), (32, 0), (40, 0), (40, 32), (40, 64),
                                     (100, 64)])
 def test_kq_matmul_bitexact(dev, typ, M, tile):
-    """the K-quant operator (Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, and IQ4_XS on its integer form) against the oracle bit for
-    bit: up to 8 rows the batched GEMV, 9 .. 32 the 32-row GEMM (k_gemm_kq32; Q2_K, Q3_K, Q5_K and IQ4_XS: the batched
-    GEMV in passes of 8), above it the MFMA GEMM with 32- and 64-row tiles (forced) or, this narrow, the GEMV again (N not a multiple
-    of the column tiles)"""
+    """the K-quant and i-quant operator (Q2_K, Q3_K, Q4_K, Q5_K, Q6_K; IQ4_XS and the codebook types IQ2_XXS, IQ2_XS,
+    IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M decoded in the kernels) against the oracle bit for bit: up to 8 rows the batched
+    GEMV, 9 .. 32 the 32-row GEMM (k_gemm_kq32; the other types: the batched GEMV in passes of 8), above it the MFMA
+    GEMM with 32- and 64-row tiles (forced) or, this narrow, the GEMV again (N not a multiple of the column tiles)"""
     torch, gw = dev
     from oracle import oracle as orc
     from gwenedeg_amd import synth

@@ -319,13 +319,30 @@ def test_quantized_kv_greedy_bit_identical(gw, orc, tmp_path, shape, kvt):
     assert np.array_equal(_bits(both[0]), _bits(alone_a)) and np.array_equal(_bits(both[1]), _bits(alone_b))
 
 
-@pytest.mark.parametrize("shape", ["tiny_q5k", "tiny_q3k", "tiny_iq4xs", "tiny_q2k"])
+@pytest.mark.parametrize("shape", ["tiny_q5k", "tiny_q3k", "tiny_iq4xs", "tiny_q2k", "tiny_iq2_xxs", "tiny_iq2_xs",
+                                   "tiny_iq2_s", "tiny_iq3_xxs", "tiny_iq3_s", "tiny_iq1_s", "tiny_iq1_m"])
 def test_q5k_q3k_models_greedy_bit_identical(gw, orc, tmp_path, shape):
     """Q5_K_M-, Q3_K_M-, IQ4_XS- and Q2_K-style models (Q5_K / Q3_K / IQ4_XS / Q2_K matrices beside Q4_K / Q5_K / Q6_K
-    ones, the K-quant or IQ4_XS embedding): a 64-token prefill and 24 greedy steps, every logits row equal bit for bit to the reference's,
-    the same tokens"""
+    ones, the K-quant or IQ4_XS embedding) and one model per codebook i-quant (every matrix and the embedding of that
+    type, Q6_K output): a 64-token prefill and 24 greedy steps, every logits row equal bit for bit to the reference's,
+    the same tokens. The i-quant models' matrices hold at most 1.25 times the file's bytes on the device"""
+    import ctypes
     path, d = _synth(str(tmp_path), shape, seed=7)
     m = gw.Model(path, ctx_len=512)
+    if "iq" in shape:
+        class SeqMem(ctypes.Structure):
+            _fields_ = [("kv", ctypes.c_size_t), ("state", ctypes.c_size_t), ("checkpoints", ctypes.c_int),
+                        ("total", ctypes.c_size_t)]
+        class ModelMem(ctypes.Structure):
+            _fields_ = [("weights", ctypes.c_size_t), ("runtime", ctypes.c_size_t), ("seq", SeqMem),
+                        ("total", ctypes.c_size_t), ("budget", ctypes.c_double), ("budget_src", ctypes.c_int),
+                        ("read", ctypes.c_size_t)]
+        mm = ModelMem()
+        assert gw.lib.rq_model_mem(ctypes.c_void_p(m._h), ctypes.byref(mm)) == 0
+        L, dim, hd = d["n_layers"], d["dim"], d["head_dim"]
+        norms = (2 * L * dim + 2 * L * hd + dim) * 4
+        rope = 512 * hd * 4
+        assert mm.weights - norms - rope <= 1.25 * (os.path.getsize(path) - norms), (mm.weights, os.path.getsize(path))
     if not _exact(gw):
         pytest.skip("this host does not provide the reference's float operations (AVX-512)")
     ids = np.random.default_rng(5).integers(0, m.vocab, 64).astype(np.int32)

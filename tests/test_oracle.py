@@ -277,11 +277,100 @@ def _np_dequant_q2k(b):
     return y
 
 
+def _iq_grids():
+    """the codebooks from their compact codes (gwenedeg_amd/csrc/gw_iq_tables.h, parsed as text), expanded here:
+    entry -> array of its 8 (or 4) values"""
+    import re
+    src = open(os.path.join(os.path.dirname(__file__), "..", "gwenedeg_amd", "csrc", "gw_iq_tables.h")).read()
+    tab = {m.group(1): [int(v, 16) for v in re.findall(r"0x[0-9a-f]+", m.group(2))]
+           for m in re.finditer(r"static const uint16_t (\w+)\[\d+\] = \{(.*?)\};", src, re.S)}
+    a2, a3x = [8, 25, 43], [4, 12, 20, 28, 36, 44, 52, 62]
+    g = {}
+    for n in ("iq2xxs", "iq2xs", "iq2s"):
+        g[n] = np.array([[a2[(c >> 2 * j) & 3] for j in range(8)] for c in tab[f"gw_{n}_codes"]], np.int32)
+    g["iq3xxs"] = np.array([[a3x[(c >> 3 * j) & 7] for j in range(4)] for c in tab["gw_iq3xxs_codes"]], np.int32)
+    g["iq3s"] = np.array([[2 * ((c >> 3 * j) & 7) + 1 for j in range(4)] for c in tab["gw_iq3s_codes"]], np.int32)
+    g["iq1s"] = np.array([[((c >> 2 * j) & 3) - 1 for j in range(8)] for c in tab["gw_iq1s_codes"]], np.int32)
+    return g
+
+
+_GRIDS = None
+
+
+def _ksigns(s7):
+    return s7 | ((bin(s7).count("1") & 1) << 7)
+
+
+def _np_dequant_cb(typ, b):
+    """ggml's dequantize_row_iq2_xxs / iq2_xs / iq2_s / iq3_xxs / iq3_s / iq1_s / iq1_m on one block, from the published
+    layouts (fp16 d first, IQ1_M's d in the top nibbles of its 4 scale words): values d * scale * grid * sign, with the
+    scale expressions of each type; IQ1: d (2 s + 1) (grid +- 1/8)"""
+    global _GRIDS
+    if _GRIDS is None:
+        _GRIDS = _iq_grids()
+    G = _GRIDS
+    f32, u16 = np.float32, lambda o: int(b[o:o + 2].view(np.uint16)[0])
+    u32 = lambda o: int(b[o:o + 4].view(np.uint32)[0])
+    h2f = lambda h: np.array([h], np.uint16).view(np.float16)[0].astype(np.float32)
+    y = np.zeros(256, np.float32)
+    if typ == 29:
+        sc = [u16(48 + 2 * i) for i in range(4)]
+        d = h2f((sc[0] >> 12) | ((sc[1] >> 8) & 0xF0) | ((sc[2] >> 4) & 0xF00) | (sc[3] & 0xF000))
+    else:
+        d = h2f(u16(0))
+    for ib in range(8):
+        for l in range(4):
+            o = 32 * ib + 8 * l
+            if typ == 16:
+                a0, a1 = u32(2 + 8 * ib), u32(6 + 8 * ib)
+                db = f32(f32(d * f32(0.5 + (a1 >> 28))) * f32(0.25))
+                gr, sg = G["iq2xxs"][(a0 >> 8 * l) & 255], _ksigns((a1 >> 7 * l) & 127)
+            elif typ in (17, 22):
+                sc = int(b[(66 if typ == 17 else 74) + ib])
+                db = f32(f32(d * f32(0.5 + ((sc >> 4 * (l // 2)) & 15))) * f32(0.25))
+                if typ == 17:
+                    q = u16(2 + 2 * (4 * ib + l))
+                    gr, sg = G["iq2xs"][q & 511], _ksigns(q >> 9)
+                else:
+                    gr = G["iq2s"][int(b[2 + 4 * ib + l]) | (((int(b[66 + ib]) >> 2 * l) & 3) << 8)]
+                    sg = int(b[34 + 4 * ib + l])
+            elif typ == 18:
+                a = u32(66 + 4 * ib)
+                db = f32(f32(d * f32(0.5 + (a >> 28))) * f32(0.5))
+                gr = np.concatenate([G["iq3xxs"][int(b[2 + 8 * ib + 2 * l])], G["iq3xxs"][int(b[3 + 8 * ib + 2 * l])]])
+                sg = _ksigns((a >> 7 * l) & 127)
+            elif typ == 21:
+                qh = int(b[66 + ib])
+                db = f32(d * f32(1 + 2 * ((int(b[106 + ib // 2]) >> 4 * (ib % 2)) & 15)))
+                gr = np.concatenate([G["iq3s"][int(b[2 + 8 * ib + 2 * l]) | (((qh >> 2 * l) & 1) << 8)],
+                                     G["iq3s"][int(b[3 + 8 * ib + 2 * l]) | (((qh >> (2 * l + 1)) & 1) << 8)]])
+                sg = int(b[74 + 4 * ib + l])
+            else:
+                if typ == 19:
+                    qh = u16(34 + 2 * ib)
+                    idx, s3, neg = int(b[2 + 4 * ib + l]) | (((qh >> 3 * l) & 7) << 8), (qh >> 12) & 7, qh & 0x8000
+                else:
+                    scw = u16(48 + 2 * (ib // 2))
+                    q = (int(b[32 + 2 * ib + l // 2]) >> 4 * (l % 2)) & 15
+                    idx, s3, neg = int(b[4 * ib + l]) | ((q & 7) << 8), (scw >> (6 * (ib % 2) + 3 * (l // 2))) & 7, q & 8
+                dl = f32(d * f32(2 * s3 + 1))
+                delta = f32(-0.125 if neg else 0.125)
+                y[o:o + 8] = dl * (G["iq1s"][idx].astype(np.float32) + delta)
+                continue
+            sgn = np.array([-1.0 if (sg >> j) & 1 else 1.0 for j in range(8)], np.float32)
+            y[o:o + 8] = (db * gr.astype(np.float32)) * sgn
+    return y
+
+
 _KQ_DEC = {11: (_np_dequant_q3k, 110), 12: (_np_dequant_q4k, 144), 13: (_np_dequant_q5k, 176), 14: (_np_dequant_q6k, 210),
            23: (_np_dequant_iq4xs, 136), 10: (_np_dequant_q2k, 84)}
+_CB_BYTES = {16: 66, 17: 74, 22: 82, 18: 98, 21: 110, 19: 50, 29: 56}  # (the codebook i-quants, iquants.h:140-154)
+for _t, _n in _CB_BYTES.items():
+    _KQ_DEC[_t] = ((lambda t: (lambda blk: _np_dequant_cb(t, blk)))(_t), _n)
+_ALL_KQ = [10, 11, 12, 13, 14, 23, 16, 17, 22, 18, 21, 19, 29]
 
 
-@pytest.mark.parametrize("typ", [10, 11, 12, 13, 14, 23])
+@pytest.mark.parametrize("typ", _ALL_KQ)
 def test_kq_dequant_vs_independent_decoder(typ):
     """or_kq_dequant_row (kquants.h:222-251; Q2_K / IQ4_XS iquants.h:224-231, :330-340) against a numpy decoder written
     from ggml's block layout: bit for bit"""
@@ -294,7 +383,20 @@ def test_kq_dequant_vs_independent_decoder(typ):
 
 
 @need_ref
-@pytest.mark.parametrize("typ", [10, 11, 12, 13, 14, 23])
+@pytest.mark.parametrize("typ", sorted(_CB_BYTES) + [23, 10])
+def test_iq_dequant_vs_reference(tmp_path, typ):
+    """or_kq_dequant_row on the i-quants against the reference's iq_dequant_row (iquants.h:217, compiled from its
+    sources: its own codebooks, iq_grids.h) on 1,024 random blocks (32,768 grid lookups: every entry of the largest
+    codebook, IQ1's 2,048, drawn with probability 1 - 3e-7): bit for bit. Pins the codebooks"""
+    nb = 1024
+    blk = _kq_blocks(typ, 1, 256 * nb, 90 + typ)[0]
+    mine = orc.kq_dequant_row(typ, blk, 256 * nb)
+    ref = orc.run_ref_iq_dequant(str(tmp_path), typ, blk, nb)
+    assert np.array_equal(_u32(mine), _u32(ref))
+
+
+@need_ref
+@pytest.mark.parametrize("typ", _ALL_KQ)
 @pytest.mark.parametrize("M", [1, 5, 11])
 def test_kq_matmul_vs_reference(tmp_path, typ, M):
     """or_kq_matmul (kquants.h:86-109's fold; Q2_K / IQ4_XS iquants.h:49-57's) against the reference's kernels compiled
@@ -439,6 +541,13 @@ def test_attention_combine_matches_single_pass():
     ("tiny_kq", {}, 20, 2),
     ("tiny_iq4xs", {}, 20, 2),
     ("tiny_q2k", {}, 20, 2),
+    ("tiny_iq2_xxs", {}, 20, 2),
+    ("tiny_iq2_xs", {}, 20, 2),
+    ("tiny_iq2_s", {}, 20, 2),
+    ("tiny_iq3_xxs", {}, 20, 2),
+    ("tiny_iq3_s", {}, 20, 2),
+    ("tiny_iq1_s", {}, 20, 2),
+    ("tiny_iq1_m", {}, 20, 2),
     ("qwen3_0_6b", dict(n_layers=3, vocab=4096, tied=0), 12, 2),
     ("tiny", {}, 40, 1),
     ("qwen3_0_6b", dict(n_layers=2, vocab=4096, tied=0), 270, 1),
