@@ -170,8 +170,8 @@ def _fptr(a: Optional[np.ndarray]):
 class Model:
     """rq_model_load / rq_model_free / rq_model_info (runq.h:87-147)."""
 
-    def __init__(self, path: str, ctx_len: int = 0):
-        opts = RqModelOpts(ctx_len=ctx_len, no_tokenizer=1, mem=-1.0)
+    def __init__(self, path: str, ctx_len: int = 0, repack: int = 0):
+        opts = RqModelOpts(ctx_len=ctx_len, no_tokenizer=1, mem=-1.0, repack=repack)
         err = ctypes.create_string_buffer(512)
         self._h = lib.rq_model_load(path.encode(), ctypes.byref(opts), err, 512)
         if not self._h:

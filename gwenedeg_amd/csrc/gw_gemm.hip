@@ -1199,6 +1199,8 @@ __global__ __launch_bounds__(256) void k_embed_kq(float *__restrict__ x, int dim
     case GW_IQ3_S: embed_iq<GW_IQ3_S>(xo, dim, rb, bstride); return;
     case GW_IQ1_S: embed_iq<GW_IQ1_S>(xo, dim, rb, bstride); return;
     case GW_IQ1_M: embed_iq<GW_IQ1_M>(xo, dim, rb, bstride); return;
+    case GW_IQ3_XXS_R: embed_iq<GW_IQ3_XXS_R>(xo, dim, rb, bstride); return;
+    case GW_IQ3_S_R: embed_iq<GW_IQ3_S_R>(xo, dim, rb, bstride); return;
     }
     for (int i = threadIdx.x; i < dim; i += blockDim.x) {
         int s = i >> 8, k = i & 255;
@@ -1312,6 +1314,50 @@ __global__ __launch_bounds__(256) void k_iq_to_dev(const uint8_t *__restrict__ s
         v = (__float_as_uint(D) >> (8 * (k - 136))) & 255u;
     }
     dst[i] = (uint8_t)v;
+}
+
+// the IQ3 repack (RqModelOpts.repack): IQ3_XXS / IQ3_S super-blocks (the file's, sb bytes) -> 4-bit codes (GW_IQ3R_DEV
+// bytes, gw_iq.h). A block of 256 threads takes 32 super-blocks: their device layouts assembled in LDS, then thread
+// (super-block, group) decodes its group's 32 values and S (the kernels' own decode, iq_half), writes the codes
+// n = e | (v < 0) << 3 in IQ4_XS's nibble order and S; group 0 also D (fp32) and the padding. The same v, S and D, so
+// every result is the same bits
+template <int BASE>
+__global__ __launch_bounds__(256) void k_iq3r_to_dev(const uint8_t *__restrict__ src, size_t nblk, int sb,
+                                                     uint8_t *__restrict__ dst) {
+    constexpr int DB = BASE == GW_IQ3_XXS ? GW_IQ3XXS_DEV : GW_IQ3S_DEV;
+    __shared__ __align__(16) uint8_t lb[32 * DB];
+    const size_t b0 = (size_t)blockIdx.x * 32;
+    for (int i = threadIdx.x; i < 32 * DB; i += 256) {
+        const size_t b = b0 + i / DB;
+        const int k = i % DB, o = iq_src_byte(BASE, k);
+        lb[i] = b < nblk && o >= 0 ? src[b * (size_t)sb + o] : 0;
+    }
+    __syncthreads();
+    const int lbk = threadIdx.x >> 3, ib = threadIdx.x & 7;
+    const size_t b = b0 + lbk;
+    if (b >= nblk) return;
+    const uint8_t *blk = lb + lbk * DB;
+    int4 v0, v1;
+    int S0, S1;
+    iq_half<BASE>(blk, 2 * ib, v0, S0);
+    iq_half<BASE>(blk, 2 * ib + 1, v1, S1);
+    auto code = [](int v) -> uint32_t {
+        const int a = v < 0 ? -v : v;
+        const int e = BASE == GW_IQ3_S ? (a - 1) >> 1 : a == 62 ? 7 : (a - 4) >> 3;
+        return (uint32_t)e | (v < 0 ? 8u : 0u);
+    };
+    const uint32_t w0[4] = { (uint32_t)v0.x, (uint32_t)v0.y, (uint32_t)v0.z, (uint32_t)v0.w };
+    const uint32_t w1[4] = { (uint32_t)v1.x, (uint32_t)v1.y, (uint32_t)v1.z, (uint32_t)v1.w };
+    uint32_t q[4] = { 0, 0, 0, 0 };
+    #pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const int lo = (int)(int8_t)(w0[j >> 2] >> (8 * (j & 3))), hi = (int)(int8_t)(w1[j >> 2] >> (8 * (j & 3)));
+        q[j >> 2] |= (code(lo) | code(hi) << 4) << (8 * (j & 3));
+    }
+    uint8_t *d = dst + b * GW_IQ3R_DEV;
+    *(uint4 *)(d + 16 * ib) = make_uint4(q[0], q[1], q[2], q[3]);
+    d[128 + ib] = (uint8_t)(int8_t)S0; // (S0 == S1: one scale per group, iquants.h:18-21)
+    if (ib == 0) *(uint2 *)(d + 136) = make_uint2(__float_as_uint(iq_d<BASE>(blk)), 0u);
 }
 
 // dst super-block i (db bytes) = src super-block i (sb bytes) and zero padding
@@ -1480,6 +1526,12 @@ extern "C" {
 int gw_k_kq_to_dev(const uint8_t *src, size_t nblk, int type, uint8_t *dst, hipStream_t s) {
     const int sbytes = gw_kq_file_bytes(type), dbytes = gw_kq_dev_bytes(type);
     if (sbytes < 1 || dbytes < sbytes) return (int)hipErrorInvalidValue;
+    if (type == GW_IQ3_XXS_R || type == GW_IQ3_S_R) { // (the file's IQ3 blocks -> the repacked codes)
+        const dim3 g((unsigned)((nblk + 31) / 32));
+        if (type == GW_IQ3_XXS_R) hipLaunchKernelGGL(k_iq3r_to_dev<GW_IQ3_XXS>, g, dim3(256), 0, s, src, nblk, sbytes, dst);
+        else hipLaunchKernelGGL(k_iq3r_to_dev<GW_IQ3_S>, g, dim3(256), 0, s, src, nblk, sbytes, dst);
+        return (int)hipGetLastError();
+    }
     if (type == GW_IQ4_XS || GW_IS_CB(type)) {
         const size_t n = nblk * (size_t)dbytes;
         hipLaunchKernelGGL(k_iq_to_dev, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, nblk, type, sbytes, dbytes, dst);
@@ -1673,6 +1725,12 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
         } else if (w->type == GW_IQ1_M) {
             if (g64) KQ_L(GW_IQ1_M, 64);
             else KQ_L(GW_IQ1_M, 32);
+        } else if (w->type == GW_IQ3_XXS_R) {
+            if (g64) KQ_L(GW_IQ3_XXS_R, 64);
+            else KQ_L(GW_IQ3_XXS_R, 32);
+        } else if (w->type == GW_IQ3_S_R) {
+            if (g64) KQ_L(GW_IQ3_S_R, 64);
+            else KQ_L(GW_IQ3_S_R, 32);
         } else if (w->type == GW_Q2_K) {
             if (g64) KQ_L(GW_Q2_K, 64);
             else KQ_L(GW_Q2_K, 32);
@@ -1697,6 +1755,8 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
     if (w->type == GW_IQ3_S) MRQ_L(GW_IQ3_S);
     if (w->type == GW_IQ1_S) MRQ_L(GW_IQ1_S);
     if (w->type == GW_IQ1_M) MRQ_L(GW_IQ1_M);
+    if (w->type == GW_IQ3_XXS_R) MRQ_L(GW_IQ3_XXS_R);
+    if (w->type == GW_IQ3_S_R) MRQ_L(GW_IQ3_S_R);
 #undef MRQ_L
     return (int)hipErrorInvalidValue;
 }
@@ -1798,7 +1858,7 @@ int gw_matmul_tile_rows(int rows) {
 
 int gw_kq_matmul(float *out, int type, const void *blocks, int N, int K, const int8_t *xq, const float *xs, int M, void *stream) {
     if (N <= 0 || K <= 0 || M <= 0 || K % 256 || !GW_IS_KQ(type) || !out || !blocks || !xq || !xs) return RQ_ERR_ARG;
-    if (GW_IS_CB(type) && gw_iq_init(NULL, 0) != RQ_OK) return RQ_ERR_STATE;
+    if ((GW_IS_CB(type) || type == GW_IQ3_XXS_R || type == GW_IQ3_S_R) && gw_iq_init(NULL, 0) != RQ_OK) return RQ_ERR_STATE;
     const int fb = gw_kq_file_bytes(type), db = gw_kq_dev_bytes(type);
     GwMat w = { type, N, K, NULL, NULL, (uint8_t *)blocks, fb };
     if (fb == db) return gw_k_matmul(&w, xq, xs, K, M, out, N, 0, (hipStream_t)stream) ? RQ_ERR_STATE : RQ_OK;

@@ -52,8 +52,14 @@ enum { GW_F32 = 0, GW_Q8_0 = 8, GW_Q2_K = 10, GW_Q3_K = 11, GW_Q4_K = 12, GW_Q5_
 #define GW_IQ1M_DEV 56
 #define GW_IS_CB(t) ((t) == GW_IQ2_XXS || (t) == GW_IQ2_XS || (t) == GW_IQ2_S || (t) == GW_IQ3_XXS || (t) == GW_IQ3_S || \
                      (t) == GW_IQ1_S || (t) == GW_IQ1_M)
+/* RqModelOpts.repack (runq.h:76-82): IQ3_XXS / IQ3_S matmul weights held as 4-bit codes instead (internal types, never
+ * in a file: the IQ_R bit of iquants.h:101-107), IQ4_XS's layout with a code table of their own (gw_iq.h) */
+#define GW_IQ_R 0x100
+enum { GW_IQ3_XXS_R = GW_IQ_R | GW_IQ3_XXS, GW_IQ3_S_R = GW_IQ_R | GW_IQ3_S };
+#define GW_IQ3R_DEV 144
 /* the super-block types (256 values; the matmul kernels' K-quant paths): Q2_K .. Q6_K and the i-quants */
-#define GW_IS_KQ(t) (((t) >= GW_Q2_K && (t) <= GW_Q6_K) || (t) == GW_IQ4_XS || GW_IS_CB(t))
+#define GW_IS_KQ(t) (((t) >= GW_Q2_K && (t) <= GW_Q6_K) || (t) == GW_IQ4_XS || GW_IS_CB(t) || (t) == GW_IQ3_XXS_R || \
+                     (t) == GW_IQ3_S_R)
 
 /* KV cache types (runq.h:214): the rotated 8-bit / 4-bit ones, and the bytes of a tile (16 positions x hd of one kv
  * head) of K (is_v 0) or V: f32 64 hd, 16-bit 32 hd, q8 17 hd, q4 9 hd (RQ_KV_Q4: K q8, V q4; RQ_KV_Q4K4: both q4) */
@@ -93,6 +99,8 @@ static inline int gw_kq_file_bytes(int type) {
     case GW_IQ3_S: return GW_IQ3S_BYTES;
     case GW_IQ1_S: return GW_IQ1S_BYTES;
     case GW_IQ1_M: return GW_IQ1M_BYTES;
+    case GW_IQ3_XXS_R: return GW_IQ3XXS_BYTES;
+    case GW_IQ3_S_R: return GW_IQ3S_BYTES;
     }
     return 0;
 }
@@ -109,6 +117,7 @@ static inline int gw_kq_dev_bytes(int type) {
     case GW_IQ3_S: return GW_IQ3S_DEV;
     case GW_IQ1_S: return GW_IQ1S_DEV;
     case GW_IQ1_M: return GW_IQ1M_DEV;
+    case GW_IQ3_XXS_R: case GW_IQ3_S_R: return GW_IQ3R_DEV;
     }
     return gw_kq_file_bytes(type);
 }
@@ -202,6 +211,7 @@ struct RqModel {
     float *rope;       /* device: seq_len rows of head_dim floats (cos | sin) */
     float *norms;      /* the one allocation the norms live in */
     size_t dev_bytes;  /* device memory held by the weights */
+    int repack;        /* RqModelOpts.repack (> 0: RQ_REPACK_* bits; else 0) */
     int kq;            /* a K-quant matrix present */
     int device;
 };

@@ -14,6 +14,9 @@
 //   IQ1_S    50: 52   +0 qs[32]  +32 u16 qh[8]  +48 d
 //   IQ1_M    56: 56   the file's (qs[32], qh[16], u16 sc[4] with d in their top nibbles)
 //   IQ4_XS  136: 144  +0 qs[128] (nibbles)  +128 int8 S = ls - 32 per group of 32  +136 D (fp32)
+// and the IQ3 repack (RqModelOpts.repack, iquants.h:101-107): IQ3_XXS / IQ3_S as 4-bit codes n = e | (v < 0) << 3 (e the
+// magnitude's index: |v| = 2 e + 1, IQ3_XXS 4, 12, .., 52, 62) in IQ4_XS's layout, S = 2 ls + 1, D as the base type's:
+//   IQ3_XXS_R, IQ3_S_R  98 / 110: 144
 #pragma once
 
 // the codebooks, value j of an entry in its byte j; IQ1's as v = 8 grid + 1 ([0]) and 8 grid - 1 ([1]), its two deltas
@@ -24,7 +27,8 @@ template <int TYPE>
 struct IqCb {
     static constexpr bool cb = TYPE == GW_IQ2_XXS || TYPE == GW_IQ2_XS || TYPE == GW_IQ2_S || TYPE == GW_IQ3_XXS ||
                                TYPE == GW_IQ3_S || TYPE == GW_IQ1_S || TYPE == GW_IQ1_M;
-    static constexpr bool iform = cb || TYPE == GW_IQ4_XS; // (the integer-form types: no Σx term)
+    static constexpr bool nib = TYPE == GW_IQ4_XS || TYPE == GW_IQ3_XXS_R || TYPE == GW_IQ3_S_R; // (4-bit codes)
+    static constexpr bool iform = cb || nib; // (the integer-form types: no Σx term)
 };
 
 // the bytes of one half-group's share of a super-block (fields as iq_raw documents per type)
@@ -45,16 +49,22 @@ __device__ __forceinline__ int4 iq_pair8(uint64_t e0, uint64_t e1, uint32_t s0, 
                      (int)iq_neg((uint32_t)e1, iq_sm(s1 & 15u)), (int)iq_neg((uint32_t)(e1 >> 32), iq_sm(s1 >> 4)));
 }
 
-// IQ4_XS's code values (ggml's kvalues_iq4nl, iq_grids.h:1082) as 4 dwords, value n in byte n
+// the 4-bit code tables, value of code n in byte n: IQ4_XS's (ggml's kvalues_iq4nl, iq_grids.h:1082), the repacked
+// IQ3 types' (iq_r_value, iquants.h:109-114: +m for n < 8, -m for n | 8)
 constexpr int8_t gw_kv_iq4nl_c[16] = { -127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113 };
+constexpr int8_t gw_kv_iq3xxs_r[16] = { 4, 12, 20, 28, 36, 44, 52, 62, -4, -12, -20, -28, -36, -44, -52, -62 };
+constexpr int8_t gw_kv_iq3s_r[16] = { 1, 3, 5, 7, 9, 11, 13, 15, -1, -3, -5, -7, -9, -11, -13, -15 };
+template <int TYPE>
 constexpr uint32_t iq4_tw(int k) {
-    return (uint32_t)(uint8_t)gw_kv_iq4nl_c[4 * k] | (uint32_t)(uint8_t)gw_kv_iq4nl_c[4 * k + 1] << 8 |
-           (uint32_t)(uint8_t)gw_kv_iq4nl_c[4 * k + 2] << 16 | (uint32_t)(uint8_t)gw_kv_iq4nl_c[4 * k + 3] << 24;
+    const int8_t *t = TYPE == GW_IQ3_XXS_R ? gw_kv_iq3xxs_r : TYPE == GW_IQ3_S_R ? gw_kv_iq3s_r : gw_kv_iq4nl_c;
+    return (uint32_t)(uint8_t)t[4 * k] | (uint32_t)(uint8_t)t[4 * k + 1] << 8 | (uint32_t)(uint8_t)t[4 * k + 2] << 16 |
+           (uint32_t)(uint8_t)t[4 * k + 3] << 24;
 }
 // 4 codes (0 .. 15, one per byte) -> their values: bytes 0 .. 7 of the table by one v_perm, 8 .. 15 by another, bit 3
 // choosing
+template <int TYPE>
 __device__ __forceinline__ uint32_t iq4_lut(uint32_t n) {
-    constexpr uint32_t t0 = iq4_tw(0), t1 = iq4_tw(1), t2 = iq4_tw(2), t3 = iq4_tw(3);
+    constexpr uint32_t t0 = iq4_tw<TYPE>(0), t1 = iq4_tw<TYPE>(1), t2 = iq4_tw<TYPE>(2), t3 = iq4_tw<TYPE>(3);
     const uint32_t s = n & 0x07070707u;
     const uint32_t lo = __builtin_amdgcn_perm(t1, t0, s), hi = __builtin_amdgcn_perm(t3, t2, s);
     const uint32_t m = ((n >> 3) & 0x01010101u) * 0xffu;
@@ -93,7 +103,7 @@ __device__ __forceinline__ IqRaw iq_raw(const uint8_t *b, int hg) {
         r.a = w(4 * ib);
         r.b = w(32 + 4 * (ib >> 1));
         r.c = w(48 + 4 * (ib >> 2));
-    } else if constexpr (TYPE == GW_IQ4_XS) { // the group's 16 nibble bytes; its S's dword
+    } else if constexpr (IqCb<TYPE>::nib) { // the group's 16 nibble bytes; its S's dword
         const uint4 q = *(const uint4 *)(b + 16 * ib);
         r.a = q.x;
         r.b = q.y;
@@ -149,10 +159,10 @@ __device__ __forceinline__ void iq_dec(const IqRaw &r, int hg, int4 &v, int &S) 
         v = make_int4((int)(uint32_t)e0, (int)(uint32_t)(e0 >> 32), (int)(uint32_t)e1, (int)(uint32_t)(e1 >> 32));
         const uint32_t sc = (r.c >> 16 * ((ib >> 1) & 1)) & 0xffffu;
         S = 2 * (int)((sc >> (6 * (ib & 1) + 3 * h)) & 7u) + 1;
-    } else if constexpr (TYPE == GW_IQ4_XS) { // nibble h of the group's 16 bytes: codes -> kvalues_iq4nl; S = ls - 32
+    } else if constexpr (IqCb<TYPE>::nib) { // nibble h of the group's 16 bytes: codes -> the type's values; S as stored
         const uint32_t sh = 4u * (uint32_t)h;
-        v = make_int4((int)iq4_lut((r.a >> sh) & 0x0f0f0f0fu), (int)iq4_lut((r.b >> sh) & 0x0f0f0f0fu),
-                      (int)iq4_lut((r.c >> sh) & 0x0f0f0f0fu), (int)iq4_lut((r.d >> sh) & 0x0f0f0f0fu));
+        v = make_int4((int)iq4_lut<TYPE>((r.a >> sh) & 0x0f0f0f0fu), (int)iq4_lut<TYPE>((r.b >> sh) & 0x0f0f0f0fu),
+                      (int)iq4_lut<TYPE>((r.c >> sh) & 0x0f0f0f0fu), (int)iq4_lut<TYPE>((r.d >> sh) & 0x0f0f0f0fu));
         S = (int)(int8_t)(r.e >> 8 * (ib & 3));
     }
 }
@@ -173,7 +183,7 @@ __device__ __forceinline__ float iq_d_raw(uint32_t w0, uint32_t w1) {
     else if constexpr (TYPE == GW_IQ1_M) { // (d in the top nibbles of sc[0..3], iquants.h:200-205)
         const uint32_t d = (w0 >> 12 & 0x000fu) | (w0 >> 24 & 0x00f0u) | (w1 >> 4 & 0x0f00u) | (w1 >> 16 & 0xf000u);
         return h16(d) * 0.125f;
-    } else return __uint_as_float(w0); // IQ4_XS
+    } else return __uint_as_float(w0); // IQ4_XS, the repacked IQ3 types
 }
 template <int TYPE>
 __device__ __forceinline__ float iq_d(const uint8_t *b) {

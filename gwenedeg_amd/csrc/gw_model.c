@@ -61,11 +61,48 @@ RqModel *rq_mtp_load(const RqModel *target, const RqMtpOpts *o, char *err, size_
 }
 
 int rq_repack_info(const RqModel *m, RqRepackInfo *info) {
-    /* runq.h:175-195: the CPU repack does not exist here (available 0, no types): the weights are always the device
-     * layout, whose bytes are the weights' */
+    /* runq.h:175-195 (model.c:1402-1438) for the device: per type among IQ3_S, IQ3_XXS (repackable) and IQ1_S, IQ1_M,
+     * over the matmul weights (the classifier, then every layer's q, k, v, o, gate, up, down) */
     memset(info, 0, sizeof(*info));
-    if (!m) return RQ_ERR_STATE;
+    if (!m || !m->has_weights) return RQ_ERR_STATE;
+    info->available = 1;
     info->weights = m->dev_bytes;
+    static const int types[RQ_REPACK_TYPES] = { GW_IQ3_S, GW_IQ3_XXS, GW_IQ1_S, GW_IQ1_M };
+    static const int bits[RQ_REPACK_TYPES] = { RQ_REPACK_IQ3_S, RQ_REPACK_IQ3_XXS, 0, 0 };
+    static const char *const names[RQ_REPACK_TYPES] = { "IQ3_S", "IQ3_XXS", "IQ1_S", "IQ1_M" };
+    double all = 0;
+    const GwMat **mats = malloc(((size_t)7 * m->n_layers + 1) * sizeof(*mats));
+    int nm = 0;
+    if (!mats) return RQ_ERR_NOMEM;
+    if (!m->tied) mats[nm++] = &m->cls;
+    for (int l = 0; l < m->n_layers; l++) {
+        const GwLayer *y = &m->layer[l];
+        for (int i = 0; i < y->nqkv; i++) mats[nm++] = &y->qkv[i];
+        mats[nm++] = &y->wo;
+        for (int i = 0; i < y->nw13; i++) mats[nm++] = &y->w13[i];
+        mats[nm++] = &y->w2;
+    }
+    for (int i = 0; i < nm; i++) all += (double)mats[i]->rows * mats[i]->cols;
+    for (int j = 0; j < RQ_REPACK_TYPES; j++) {
+        RqRepackType *x = &info->t[info->n];
+        for (int i = 0; i < nm; i++) {
+            const GwMat *w = mats[i];
+            if ((w->type & ~GW_IQ_R) != types[j]) continue;
+            const size_t nblk = (size_t)w->rows * (w->cols / 256);
+            x->mats++;
+            x->share += (double)w->rows * w->cols / all;
+            x->bytes += nblk * (size_t)gw_kq_dev_bytes(w->type);
+            x->repacked = w->type != types[j];
+            x->extra += bits[j] ? nblk * (size_t)(GW_IQ3R_DEV - gw_kq_dev_bytes(types[j]))
+                                : nblk * (size_t)(gw_kq_dev_bytes(types[j]) - gw_kq_file_bytes(types[j]));
+        }
+        if (!x->mats) continue;
+        x->type = names[j];
+        x->bit = bits[j];
+        if (x->bit && !x->repacked) info->extra += x->extra;
+        info->n++;
+    }
+    free(mats);
     return RQ_OK;
 }
 
@@ -294,6 +331,7 @@ typedef struct {
     char *err;
     size_t errlen;
     uint8_t *stage;     /* device staging buffer for a tensor's file bytes */
+    int repack;         /* RqModelOpts.repack for the matrices being loaded (0: the embedding table) */
     size_t stage_bytes;
     RqModel *m;
 } Loader;
@@ -351,6 +389,9 @@ static int load_mat_il(Loader *L, GwMat *dst, int r0, const char *name, int rows
     if (!GW_IS_KQ((int)t->type)) return lfail(L, RQ_ERR_LOAD, "GGUF: %s: ggml type %u not supported", name, t->type);
     if (r0 != 0 || dst->rows != rows) return lfail(L, RQ_ERR_LOAD, "GGUF: %s: internal shape mismatch", name);
     dst->type = (int)t->type;
+    /* RqModelOpts.repack (model.c:360-364): IQ3_XXS / IQ3_S as 4-bit codes */
+    const int rbit = dst->type == GW_IQ3_S ? RQ_REPACK_IQ3_S : dst->type == GW_IQ3_XXS ? RQ_REPACK_IQ3_XXS : 0;
+    if (rbit && L->repack > 0 && (L->repack & (RQ_REPACK_ALL | rbit))) dst->type |= GW_IQ_R;
     const int fb = gw_kq_file_bytes(dst->type), db = gw_kq_dev_bytes(dst->type);
     size_t nblk = t->size / (size_t)fb;
     dst->bstride = db;
@@ -577,6 +618,8 @@ RqModel *rq_model_load(const char *path, const RqModelOpts *o, char *err, size_t
     m->layer = calloc((size_t)m->n_layers, sizeof(GwLayer));
     if (!m->layer) { rc = lfail(&L, RQ_ERR_NOMEM, "malloc failed"); goto out; }
     if ((rc = load_single(&L, &m->embd, "token_embd.weight", m->vocab, dim)) != RQ_OK) goto out;
+    m->repack = opts.repack > 0 ? opts.repack : 0;
+    L.repack = m->repack; /* (the matmul weights from here on) */
     if (m->tied) m->cls = m->embd;
     else if ((rc = load_single(&L, &m->cls, "output.weight", m->vocab, dim)) != RQ_OK) goto out;
     char nm[3][96];

@@ -5,7 +5,7 @@
  * link against this library instead of the reference's forward.c / model.c weight path. Each declaration cites the
  * runq.h line it replaces. Types are laid out exactly as runq.h's (same fields, order and widths).
  *
- * Scope of the device implementation: Qwen3 dense models (GGUF, Q8_0 / Q2_K .. Q6_K / IQ4_XS matrices), the f16, bf16,
+ * Scope of the device implementation: Qwen3 dense models (GGUF, Q8_0 / Q2_K .. Q6_K / IQ1_S .. IQ4_XS matrices), the f16, bf16,
  * q8, q4 and q4k4 KV caches (RQ_KV_F16, RQ_KV_BF16, RQ_KV_Q8, RQ_KV_Q4, RQ_KV_Q4K4), their bf16 dot-product types
  * (RQ_KV_BF16_DOT, F16_DOT, Q8_DOT, Q4_DOT, Q4K4_DOT) and RQ_KV_F32, one GPU, one HIP stream per context. Calls are synchronous at return
  * (logits valid on the host), as the reference's are. Results are bit-identical for any batch composition: a row's
@@ -47,9 +47,11 @@ typedef struct RqCtx RqCtx;
 #define RQ_CTX_DEFAULT_MAX 40960 /* runq.h:61 */
 
 /* runq.h:63-81 (same layout). tokenizer_only and no_tokenizer as the reference (model.c:1010-1016, :893-922): the
- * tokenizer is built by the host's own tokenizer.o / gguf.o when the program links them (rq_chat_check below);
- * page_cache / checkpoints / repack are accepted and ignored here: the file is read once, Qwen3 has no recurrent
- * state, the device layouts are fixed */
+ * tokenizer is built by the host's own tokenizer.o / gguf.o when the program links them (rq_chat_check below).
+ * repack as the reference (model.c:360-364): the IQ3_XXS / IQ3_S matmul weights held as 4-bit codes on the device
+ * (144 bytes per 256 weights against 100 / 112: no codebook lookups in the kernels), the same values and results;
+ * RQ_REPACK_ALL or the type bits; the embedding table keeps the file's type (a tied classifier with it).
+ * page_cache / checkpoints are accepted and ignored here: the file is read once, Qwen3 has no recurrent state */
 typedef struct {
     int ctx_len;
     int tokenizer_only;
@@ -60,8 +62,10 @@ typedef struct {
     int checkpoints;
     int repack;
 } RqModelOpts;
+enum { RQ_REPACK_ALL = 1, RQ_REPACK_IQ3_S = 2, RQ_REPACK_IQ3_XXS = 4 }; /* runq.h:83 */
 
-/* runq.h:87-88: a GGUF file (qwen3; Q8_0, Q2_K .. Q6_K, IQ4_XS matrices), its weights repacked into device memory.
+/* runq.h:87-88: a GGUF file (qwen3; Q8_0, Q2_K .. Q6_K and the i-quants IQ1_S .. IQ4_XS as matrices and embedding),
+ * its weights repacked into device memory.
  * Unless opts->no_tokenizer, the tokenizer, chat variant, recommended sampling and chat templates too, where the
  * program links the reference's tokenizer.o, gguf.o and threads.o (their build entry points are weak references
  * here); without them the model loads without a tokenizer and RqModelInfo.warning says so. tokenizer_only: no
@@ -114,7 +118,10 @@ typedef struct {
 int rq_model_mem(const RqModel *m, RqModelMem *mem);                          /* runq.h:168 */
 int rq_seq_mem(const RqModel *m, int capacity, int kv_type, RqSeqMem *mem);    /* runq.h:171 */
 double rq_mem_available(void);                                                /* runq.h:173 */
-/* the CPU repack (runq.h:175-195) does not exist here: available 0, no types, weights = the device bytes */
+/* runq.h:175-195 (model.c:1402-1438): available 1 (the device has kernels for the repacked IQ3 codes); per type of the
+ * matmul weights among IQ3_S, IQ3_XXS (their RqModelOpts.repack bits) and IQ1_S, IQ1_M (bit 0): the matrices, their
+ * share of the values, their device bytes now, and extra = what the repack adds to the device layout's bytes (IQ1:
+ * the device layout's bytes over the file's); weights = the device bytes */
 #define RQ_REPACK_TYPES 4
 typedef struct {
     const char *type;

@@ -233,3 +233,35 @@ def test_topk_rows_refuses(dev):
     s = torch.empty(32768, dtype=torch.uint8, device="cuda")
     for n, ld, k in ((1000, 1000, 65), (10, 10, 10), (262145, 262145, 8), (1000, 999, 8), (1000, 1000, 0)):
         assert gw.lib.gw_topk_rows(X.data_ptr(), n, ld, 1, k, v.data_ptr(), i.data_ptr(), s.data_ptr(), None) == -1, (n, ld, k)
+
+
+@pytest.mark.parametrize("base", [18, 21])
+@pytest.mark.parametrize("M,tile", [(1, 0), (5, 0), (20, 0), (40, 32), (100, 64)])
+def test_iq3_repacked_matmul_bitexact(dev, base, M, tile):
+    """the IQ3 repack (RqModelOpts.repack: IQ3_XXS / IQ3_S held as 4-bit codes, types 0x112 / 0x115) through the
+    operator: the file's IQ3 blocks converted on the device, then every dispatch path (batched GEMV, MFMA GEMM with both
+    tiles) against the oracle's IQ3 result, bit for bit"""
+    torch, gw = dev
+    from oracle import oracle as orc
+    from gwenedeg_amd import synth
+    rng = np.random.default_rng(base * 10 + M)
+    N, K = (64, 1024) if M <= 8 else (200, 768)
+    sl = synth.synth_library()
+    rb = sl.gw_synth_row_bytes(base, K)
+    blocks = np.zeros((N, rb), np.uint8)
+    w = rng.normal(0, 0.02, size=(N, K)).astype(np.float32)
+    for r in range(N):
+        sl.gw_synth_encode_row(base, blocks[r].ctypes.data, w[r].ctypes.data, K)
+    xq, xs = orc.quantize(rng.normal(0, 1, size=(M, K)).astype(np.float32))
+    ref = orc.kq_matmul(base, blocks, xq, xs, N, K)
+    out = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+    Bd, XQ, XS = (_to_dev(torch, a) for a in (blocks.reshape(-1), xq, xs))
+    prev = gw.lib.gw_matmul_tile_rows(tile)
+    try:
+        assert gw.lib.gw_kq_matmul(out.data_ptr(), 0x100 | base, Bd.data_ptr(), N, K, XQ.data_ptr(), XS.data_ptr(), M,
+                                   None) == 0
+        torch.cuda.synchronize()
+    finally:
+        gw.lib.gw_matmul_tile_rows(prev)
+    got = out.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"max diff {np.abs(got - ref).max()}"

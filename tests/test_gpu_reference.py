@@ -358,6 +358,52 @@ def test_q5k_q3k_models_greedy_bit_identical(gw, orc, tmp_path, shape):
             lg = c.decode(s, tok)
 
 
+@pytest.mark.parametrize("shape,repack", [("tiny_iq3_xxs", 1), ("tiny_iq3_s", 1), ("tiny_iq3_xxs", 4), ("tiny_iq3_s", 2),
+                                          ("tiny_iq3_s", 4)])
+def test_iq3_repack_same_bits(gw, orc, tmp_path, shape, repack):
+    """RqModelOpts.repack (runq.h:76-82): an IQ3 model loaded with its matrices repacked as 4-bit codes (RQ_REPACK_ALL
+    or the type's bit; another type's bit repacks nothing) gives the same logits as loaded without, bit for bit, over a
+    64-token prefill and 24 greedy steps; rq_repack_info (model.c:1402-1438) reports the type, whether it is
+    repacked, and the repack's extra bytes, which the weights grow by"""
+    import ctypes
+
+    class RT(ctypes.Structure):
+        _fields_ = [("type", ctypes.c_char_p), ("bit", ctypes.c_int), ("repacked", ctypes.c_int), ("mats", ctypes.c_int),
+                    ("share", ctypes.c_double), ("bytes", ctypes.c_size_t), ("extra", ctypes.c_size_t)]
+
+    class RI(ctypes.Structure):
+        _fields_ = [("available", ctypes.c_int), ("n", ctypes.c_int), ("t", RT * 4), ("weights", ctypes.c_size_t),
+                    ("extra", ctypes.c_size_t)]
+    path, d = _synth(str(tmp_path), shape, seed=3)
+    base = 18 if "xxs" in shape else 21
+    hits = repack & 1 or (repack & 4 and base == 18) or (repack & 2 and base == 21)
+    ids = np.random.default_rng(8).integers(0, d["vocab"], 64).astype(np.int32)
+    runs, infos = [], []
+    for rp in (0, repack):
+        m = gw.Model(path, ctx_len=512, repack=rp)
+        ri = RI()
+        assert gw.lib.rq_repack_info(ctypes.c_void_p(m._h), ctypes.byref(ri)) == 0
+        infos.append(ri)
+        c = m.ctx(max_batch=64, max_ctx=512)
+        s = m.seq(512)
+        rows = [c.prefill(s, ids, mode=gw.RQ_LOGITS_LAST)]
+        for _ in range(24):
+            rows.append(c.decode(s, int(np.argmax(rows[-1]))))
+        runs.append(rows)
+        s.close()
+        c.close()
+        m.close()
+    assert all(np.array_equal(_bits(a), _bits(b)) for a, b in zip(runs[0], runs[1]))
+    a, b = infos
+    assert a.available == 1 and a.n == 1 and a.t[0].type.decode() == ("IQ3_XXS" if base == 18 else "IQ3_S")
+    assert a.t[0].bit == (4 if base == 18 else 2) and a.t[0].repacked == 0 and a.t[0].mats == 2 * 7
+    nblk = sum(r * c_ for r, c_ in [(1024, 512), (256, 512), (256, 512), (512, 1024), (1024, 512), (1024, 512),
+                                    (512, 1024)]) * 2 // 256
+    assert a.t[0].extra == nblk * (144 - (100 if base == 18 else 112)) and a.extra == a.t[0].extra
+    assert b.t[0].repacked == int(bool(hits)) and b.extra == (0 if hits else a.extra)
+    assert b.weights == a.weights + (a.t[0].extra if hits else 0)
+
+
 def test_bf16_kv_greedy_bit_identical(gw, orc, tmp_path):
     """a bf16 KV cache (RQ_KV_BF16) on a Qwen3-0.6B-shaped model (2 layers): a 300-token prefill (two key blocks) and
     24 greedy steps, every logits row equal bit for bit to the reference's own bf16 cache, the same tokens"""
