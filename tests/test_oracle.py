@@ -590,8 +590,8 @@ def test_forward_bit_exact_vs_reference(tmp_path, shape, over, n, kvt):
 
 def test_golden_vectors():
     """the oracle against the reference's kernel outputs committed in tests/golden/ref_kernels.npz (written by
-    tests/golden/make_golden.py from oracle/_ref): Q8_0 GEMV (M = 1) and GEMM item (M = 6), Q4_K and Q6_K dots, bit
-    for bit; holds without the reference's build"""
+    tests/golden/make_golden.py from oracle/_ref): Q8_0 GEMV (M = 1) and GEMM item (M = 6), Q4_K and Q6_K dots, Q2_K
+    and the i-quants' matmul and dequantization, bit for bit; holds without the reference's build"""
     z = np.load(os.path.join(os.path.dirname(__file__), "golden", "ref_kernels.npz"))
     for M in (1, 6):
         got = orc.q8_matmul(z[f"q8_m{M}_wq"], z[f"q8_m{M}_ws"], z[f"q8_m{M}_xq"], z[f"q8_m{M}_xs"])
@@ -600,6 +600,12 @@ def test_golden_vectors():
         blk = z[f"kq{typ}_blk"]
         got = orc.kq_matmul(typ, blk, z[f"kq{typ}_xq"], z[f"kq{typ}_xs"], blk.shape[0], 512)
         assert np.array_equal(_u32(got), _u32(z[f"kq{typ}_out"])), f"type {typ}"
+    for typ in orc.IQ_TYPES:  # (Q2_K and the i-quants: the matmul and the dequantization of every block)
+        blk = z[f"iq{typ}_blk"]
+        got = orc.kq_matmul(typ, blk, z[f"iq{typ}_xq"], z[f"iq{typ}_xs"], blk.shape[0], 512)
+        assert np.array_equal(_u32(got), _u32(z[f"iq{typ}_out"])), f"type {typ}"
+        dq = orc.kq_dequant_row(typ, blk.reshape(-1), blk.shape[0] * 512)
+        assert np.array_equal(_u32(dq), _u32(z[f"iq{typ}_dq"])), f"type {typ} dequant"
 
 
 @need_ref
