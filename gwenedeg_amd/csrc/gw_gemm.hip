@@ -353,6 +353,8 @@ __global__ __launch_bounds__(256) void k_gemm_q8f(const int8_t *__restrict__ W, 
     }
 }
 
+typedef long i64;
+
 // ------------------------------------------------------------------------------------- K-quant MFMA GEMM
 
 // out[m * ldo + n] (+)= W row n . X row m for m < M, n < N, W in the file's Q4_K / Q6_K super-blocks (batched rows,
@@ -368,7 +370,6 @@ __global__ __launch_bounds__(256) void k_gemm_q8f(const int8_t *__restrict__ W, 
 //   Q2_K (96 bytes: the file's 84 and padding; q 0 .. 3): Q6_K's term with the 4-bit scales sc, minus the mins' term
 //     (dmin xs) M, M = m_0 X_0 + m_1 X_1 from the sums of x of each half (the same MFMA with B = 1)   (iquants.h:56-57)
 // then val = val + term in group order. mode 1: out = out + val. K % 256 == 0.
-typedef long i64;
 template <int TYPE, int GM>
 __global__ __launch_bounds__(256) void k_gemm_kq(const uint8_t *__restrict__ W, int bstride, int N, int K,
                                                  const int8_t *__restrict__ X, const float *__restrict__ XS, int ldx, int M,
@@ -1589,6 +1590,16 @@ static int gemm_cus(void) { // the device's compute units
 static int g_kq32_nqr; // (0: chosen per launch; 1, 2 or 4: forced, gw_kq32_quads)
 static int g_kq32_sb;  // (0: chosen per launch; 1 or 2 super-blocks per step: forced, gw_kq32_step)
 static int g_kq16;     // (9 .. 32 K-quant rows: 0 k_gemm_kq32, 1 k_gemm_kq16; gw_kq_small_kernel)
+static int g_q8_batch;  // (Q8_0 at 2 .. 32 rows: 0 chosen per launch, 1 the batched GEMV, 2 the MFMA GEMM; gw_q8_batch_kernel)
+
+static bool q8_gemm_rows(const GwMat *w, int M) {
+    // a Q8_0 matmul of M activation rows takes the MFMA GEMM (else the batched GEMV in passes of 8 rows): above 32 rows,
+    // and from 16 rows for matrices of 8,192 rows or more. At 16 .. 32 rows the GEMM's time hardly depends on M or the
+    // width (its blocks' fold, 3 VALU operations per output and group over a 32-row tile, bounds it: 33 us at K =
+    // 4,096 whatever the width), the GEMV's grows with both (per 8 rows a pass over the weights): measured at the 8B
+    // widths, 16 rows: 24,576 x 4,096 58.7 -> 39.6 us, 12,288 x 4,096 34.8 -> 35.1 us, 6,144 x 4,096 20.3 -> 32.5 us
+    return M > GW_GEMV_MAX_ROWS || (M >= 16 && w->rows >= 8192);
+}
 
 static bool kq32_takes(const GwMat *w, int M) {
     // K-quants, 9 .. 32 rows: the 32-row GEMM with the groups spread over a block's waves (a matrix of 32768 rows or
@@ -1662,7 +1673,7 @@ int gw_k_matmul2(const GwMat *a, const GwMat *b, int col_b, const int8_t *xq, co
 }
 
 int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int M, float *out, int ldo, int mode, hipStream_t s) {
-    if (w->type == GW_Q8_0 && M > GW_GEMV_MAX_ROWS && mode == 0) {
+    if (w->type == GW_Q8_0 && mode == 0 && (g_q8_batch == 2 ? M >= 2 : g_q8_batch == 1 ? M > GW_GEMV_MAX_ROWS : q8_gemm_rows(w, M))) {
         hipEvent_t e0, e1;
         gw_take_launch_events(&e0, &e1);
         const int cus = gemm_cus(), nt = (w->rows + GN - 1) / GN;
@@ -1826,6 +1837,13 @@ int gw_q8_block_sums(int32_t *isum, const int8_t *codes, int N, int K, const int
     hipLaunchKernelGGL(k_q8_block_sums, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, (hipStream_t)stream, isum, codes, N,
                        K, xq, M);
     return hipGetLastError() ? RQ_ERR_STATE : RQ_OK;
+}
+
+int gw_q8_batch_kernel(int k) {
+    if (k < 0 || k > 2) return -1;
+    int prev = g_q8_batch;
+    g_q8_batch = k;
+    return prev;
 }
 
 int gw_kq_small_kernel(int kq16) {

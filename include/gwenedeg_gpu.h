@@ -338,6 +338,12 @@ int gw_topk_rows(const float *logits, int n, int ld, int rows, int k, float *val
  * and test hook with no counterpart in runq.h; results do not depend on it */
 int gw_matmul_tile_rows(int rows);
 
+/* The kernel of the Q8_0 matmuls of 2 .. 32 activation rows (batched decode rows): 0 chosen per launch (the default:
+ * the MFMA GEMM from 16 rows where the matrix has 8,192 rows or more, else the batched GEMV in passes of 8 rows), 1 the
+ * batched GEMV, 2 the MFMA GEMM (k_gemm_q8f / k_gemm_q8, 32-row tiles). Returns the previous setting, or -1 (and
+ * changes nothing) for another value. A tuning and test hook with no counterpart in runq.h; results do not depend on it */
+int gw_q8_batch_kernel(int k);
+
 /* The kernel of the 9 .. 32-row K-quant GEMM (Q4_K / Q6_K, batched decode rows): 0 k_gemm_kq32 (32-row tiles, the
  * groups spread over 8 waves, the terms exchanged in LDS; the default), 1 k_gemm_kq16 (each wave on 16 weight rows x 16
  * activation rows over all of K, the fold in registers). Returns the previous setting, or -1 (and changes

@@ -70,6 +70,38 @@ def test_q8_matmul_bitexact(dev, M, N, K, tile):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"max diff {np.abs(got - ref).max()}"
 
 
+_FEW_ROWS = {}
+
+
+@pytest.mark.parametrize("off", [0, 1, 2])
+@pytest.mark.parametrize("M", [2, 5, 8, 9, 16, 17, 24, 32, 33, 48, 64])
+@pytest.mark.parametrize("N,K", [(12288, 4096), (4096, 12288), (1008, 1056)])
+def test_q8_matmul_few_rows_bitexact(dev, M, N, K, off):
+    """the Q8_0 operator at 2 .. 64 activation rows against the oracle bit for bit, with each kernel choice
+    (gw_q8_batch_kernel: chosen per launch, the batched GEMV in passes of 8 rows, the MFMA GEMM): the 8B widths, and a
+    matrix of 1,008 rows (a partial column tile) by 33 groups (a partial stage: k_gemm_q8)"""
+    torch, gw = dev
+    from oracle import oracle as orc
+    key = (M, N, K)
+    if key not in _FEW_ROWS:  # (the inputs and the oracle's result, shared by both kernels' cases)
+        rng = np.random.default_rng(N + 3 * K + M)
+        wq, ws16 = _rand_q8(rng, N, K)
+        xq, xs = orc.quantize(rng.normal(0, 1, size=(M, K)).astype(np.float32))
+        _FEW_ROWS.clear()
+        _FEW_ROWS[key] = (wq, ws16, xq, xs, orc.q8_matmul(wq, ws16.astype(np.float32), xq, xs))
+    wq, ws16, xq, xs, ref = _FEW_ROWS[key]
+    out = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+    W, WS, XQ, XS = (_to_dev(torch, a) for a in (wq, ws16.view(np.int16), xq, xs))
+    prev = gw.lib.gw_q8_batch_kernel(off)
+    try:
+        assert gw.lib.gw_q8_matmul(out.data_ptr(), W.data_ptr(), WS.data_ptr(), N, K, XQ.data_ptr(), XS.data_ptr(), M, None) == 0
+        torch.cuda.synchronize()
+    finally:
+        gw.lib.gw_q8_batch_kernel(prev)
+    got = out.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"max diff {np.abs(got - ref).max()}"
+
+
 def test_q8_pack_and_block_sums(dev):
     torch, gw = dev
     from oracle import oracle as orc
