@@ -147,6 +147,7 @@ _sig = {
     "gw_kq32_step": (_I, [_I]),
     "gw_kq_small_kernel": (_I, [_I]),
     "gw_q8_batch_kernel": (_I, [_I]),
+    "gw_q8_gemm_kernel": (_I, [_I]),
     "gw_gemv_warm_next": (_I, [_I]),
     "gw_ctx_topk": (_I, [_P, _I, _I, _F, ctypes.POINTER(_I)]),
     "gw_ctx_topk_noalloc": (_I, [_P, _I, _I, _F, ctypes.POINTER(_I)]),

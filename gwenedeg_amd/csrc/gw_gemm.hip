@@ -75,6 +75,7 @@ __global__ __launch_bounds__(256) void k_fill_synthetic(uint16_t *kc, uint16_t *
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x32 __attribute__((ext_vector_type(32)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 #define GN 128
 #define GKB 128
 #define GROW 144
@@ -349,6 +350,164 @@ __global__ __launch_bounds__(256) void k_gemm_q8f(const int8_t *__restrict__ W, 
                 const int m = m0 + wm + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (m < M && n < N) out[(size_t)m * ldo + n] = acc[j][r];
             }
+        }
+    }
+}
+
+// Q8_0 GEMM whose stages reach LDS by the buffer unit's direct copies (buffer_load_dwordx4 ... lds): no staging
+// registers and no LDS writes by the waves, a ring of LQ_S stages so that two are in flight while one is computed.
+// Blocks of 64 rows x TN columns (TN = 128: 8 waves, two blocks per CU; TN = 64: 4 waves, three per CU): wave w takes
+// the 32 x 32 tile of rows 32 (w / NC), columns 32 (w % NC), NC = TN / 32.
+// A copy writes a wave's 64 lanes to 1 KB of consecutive LDS, so stage rows (128 bytes = 4 groups) cannot be padded
+// apart; chunk c (16 bytes) of row r is stored at chunk c ^ (r % 8), which keeps the MFMA operand reads of 8
+// consecutive rows on distinct banks. Per stage, wave w copies 8 / NW of the 8 X pieces and W pieces 2 w, 2 w + 1
+// (1 KB = 8 rows each), wave 0 the stage's xs (a lane per row), waves 1 .. NC the ws (fp16, a dword = 2 groups of one
+// row per lane). Per pair of groups the fold of k_gemm_q8f: two int8 MFMAs for the exact sums, the outer-product MFMA
+// of the scale products, then val = val + (ws xs) (float) isum per output in group order (forward.c:906-916). Blocks:
+// XCD b % 8 takes column tiles 8 q + b % 8 with their row tiles in a row (the W tile read once into that XCD's L2).
+// mode 0 (out = val), K % 128 == 0; rows past M / N read as 0 (the descriptors' ranges) and are not stored.
+// SW (w1 / w3 rows interleaved by 4, N % 128 == 0): the SwiGLU and its quantization in the epilogue instead of the
+// fp32 outputs (k_gemm_q8f's, with a wave's 32 columns = 16 outputs, half a quantization group: the row maxima of the
+// two halves exchanged through LDS between the waves of columns 32 h and 32 h + 32, waves w and w ^ 1)
+#define LQ_S 3
+#define LQ_X 0
+#define LQ_W 8192
+#define LQ_XS(TN) (8192 + 128 * (TN))
+#define LQ_WS(TN) (8192 + 128 * (TN) + 1024)
+#define LQ_STAGE(TN) (8192 + 136 * (TN) + 1024)
+#define LQ_AS3 __attribute__((address_space(3)))
+__device__ __forceinline__ void lq_copy(__amdgpu_buffer_rsrc_t r, uint8_t *lds, int voff, int bytes) {
+    // (the offset in the per-lane operand, so the descriptor's range check sees all of it)
+    if (bytes == 16) __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LQ_AS3 void *)lds, 16, voff, 0, 0, 0);
+    else __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LQ_AS3 void *)lds, 4, voff, 0, 0, 0);
+}
+template <int TN, bool SW>
+__global__ __launch_bounds__(TN * 4, TN == 128 ? 2 : 3) void k_gemm_q8l(const int8_t *__restrict__ W,
+                                                                       const uint16_t *__restrict__ WS, int N, int K,
+                                                                       const int8_t *__restrict__ X,
+                                                                       const float *__restrict__ XS, int ldx, int M,
+                                                                       float *__restrict__ out, int ldo, int MT,
+                                                                       int8_t *__restrict__ hq, float *__restrict__ hs,
+                                                                       int ldq) {
+    constexpr int NC = TN / 32, NW = 2 * NC, XP = 8 / NW; // (waves per row of tiles, waves, X pieces per wave)
+    __shared__ __align__(16) uint8_t sl[LQ_S * LQ_STAGE(TN)];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, hi = lane >> 5, r32 = lane & 31;
+    const int b = blockIdx.x, j = b >> 3, nt = (N + TN - 1) / TN;
+    const int ntile = (j / MT) * 8 + (b & 7), m0 = (j % MT) * 64, n0 = ntile * TN;
+    if (ntile >= nt) return; // (the grid's padding to 8 column tiles per XCD)
+    const int G = K >> 5, gx = ldx >> 5, NS = K >> 7;
+    const int mr = M - m0 < 64 ? M - m0 : 64, nr = N - n0 < TN ? N - n0 : TN;
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void *)(X + (size_t)m0 * ldx), (short)0, mr * ldx, GW_RSRC_DW3);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)(W + (size_t)n0 * K), (short)0, nr * K, GW_RSRC_DW3);
+    const __amdgpu_buffer_rsrc_t rxs = __builtin_amdgcn_make_buffer_rsrc((void *)(XS + (size_t)m0 * gx), (short)0, mr * gx * 4, GW_RSRC_DW3);
+    const __amdgpu_buffer_rsrc_t rws = __builtin_amdgcn_make_buffer_rsrc((void *)(WS + (size_t)n0 * G), (short)0, nr * G * 2, GW_RSRC_DW3);
+    // this lane's copies: row 8 p + lane / 8 of its 1 KB piece p, logical chunk (lane % 8) ^ (lane / 8)
+    const int pr = lane >> 3, pc = (lane & 7) ^ pr;
+    const int xo = (8 * XP * wave + pr) * ldx + 16 * pc, wo = (16 * wave + pr) * K + 16 * pc;
+    const int so = wave == 0 ? lane * gx * 4 : ((32 * (wave - 1) + (lane >> 1)) * G + 2 * (lane & 1)) * 2;
+    auto issue = [&](int st) __attribute__((always_inline)) {
+        uint8_t *bs = sl + (st % LQ_S) * LQ_STAGE(TN);
+        const int k0 = st * 128;
+        #pragma unroll
+        for (int p = 0; p < XP; p++) lq_copy(rx, bs + LQ_X + 1024 * (XP * wave + p), xo + 8 * p * ldx + k0, 16);
+        lq_copy(rw, bs + LQ_W + 2048 * wave, wo + k0, 16);
+        lq_copy(rw, bs + LQ_W + 2048 * wave + 1024, wo + 8 * K + k0, 16);
+        if (wave == 0) lq_copy(rxs, bs + LQ_XS(TN), so + 16 * st, 16);
+        else if (wave <= NC) lq_copy(rws, bs + LQ_WS(TN) + 256 * (wave - 1), so + 8 * st, 4);
+    };
+    const int wm = (wave / NC) * 32, wn = (wave % NC) * 32;
+    float acc[16];
+    #pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+    const int xa = LQ_X + (wm + r32) * 128, wa = LQ_W + (wn + r32) * 128, sw = r32 & 7;
+    const int xsa_o = LQ_XS(TN) + (wm + r32) * 16 + 4 * hi, wsb_o = LQ_WS(TN) + (wn + r32) * 8 + 2 * hi;
+    issue(0);
+    if (NS > 1) issue(1);
+    for (int st = 0; st < NS; st++) {
+        // stage st landed (this wave's copies: only stage st + 1's XP + 3 or XP + 2 outstanding), then every wave's
+        if (st + 1 < NS) {
+            if (wave <= NC) {
+                if (XP == 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+                else asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+            } else {
+                if (XP == 1) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
+                else asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+            }
+        } else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (st + 2 < NS) issue(st + 2); // (into the slot of stage st - 1, whose readers are past the barrier)
+        const uint8_t *bs = sl + (st % LQ_S) * LQ_STAGE(TN);
+        #pragma unroll 1
+        for (int g0 = 0; g0 < 4; g0 += 2) {
+            const int c0 = 16 * ((2 * g0 + hi) ^ sw), c1 = 16 * ((2 * g0 + 2 + hi) ^ sw);
+            const i32x4 a0 = *(const i32x4 *)(bs + xa + c0), a1 = *(const i32x4 *)(bs + xa + c1);
+            const i32x4 b0 = *(const i32x4 *)(bs + wa + c0), b1 = *(const i32x4 *)(bs + wa + c1);
+            const float xsa = *(const float *)(bs + xsa_o + 4 * g0);
+            const float wsb = h2f_g(*(const uint16_t *)(bs + wsb_o + 2 * g0));
+            const i32x16 z = { 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0 };
+            const f32x32 zf = {};
+            const i32x16 I0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, z, 0, 0, 0);
+            const i32x16 I1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, z, 0, 0, 0);
+            const f32x32 C = __builtin_amdgcn_mfma_f32_32x32x1f32(xsa, wsb, zf, 0, 0, 0);
+            #pragma unroll
+            for (int r = 0; r < 16; r++) acc[r] = acc[r] + C[r] * (float)I0[r];
+            #pragma unroll
+            for (int r = 0; r < 16; r++) acc[r] = acc[r] + C[16 + r] * (float)I1[r];
+        }
+    }
+    if constexpr (SW) {
+        // lane c of a half-wave: column wn + c, an h column where c % 8 < 4 (output 4 (c / 8) + c % 8 of the wave's 16),
+        // else the h2 of output 4 (c / 8) + c % 8 - 4; the h lane takes registers 0 .. 7 (rows 8 (i / 4) + 4 hi + i % 4),
+        // the h2 lane registers 8 .. 15 (rows 16 + ...), each with its partner's value (lanes c and c + 4)
+        __shared__ float pm[NW][32]; // [wave][row of its tile]: the row's max |v| over the wave's 16 outputs
+        const bool hl = (r32 & 7) < 4;
+        float hv[8], h2v[8];
+        #pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float dn = __shfl_down(acc[i], 4), up = __shfl_up(acc[8 + i], 4);
+            hv[i] = hl ? acc[i] : up;
+            h2v[i] = hl ? dn : acc[8 + i];
+        }
+        swiglu_ref_n<8>(hv, h2v); // (the table reads of all 8 in flight together)
+        float am[8];
+        #pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float v = fabsf(hv[i]);
+            #pragma unroll
+            for (int o = 1; o <= 16; o <<= 1) { // (xor 1, 2, 8, 16: the 16 lanes of this kind; xor 4 is the partner)
+                if (o == 4) continue;
+                const float tt = __shfl_xor(v, o);
+                v = tt > v ? tt : v;
+            }
+            am[i] = v;
+        }
+        const int rb = (hl ? 0 : 16) + 4 * hi; // (row of register i: rb + 8 (i / 4) + i % 4)
+        if ((r32 & 0x1b) == 0) {
+            #pragma unroll
+            for (int i = 0; i < 8; i++) pm[wave][rb + 8 * (i >> 2) + (i & 3)] = am[i];
+        }
+        __syncthreads();
+        const int f = ((n0 + wn) >> 1) + 4 * (r32 >> 3) + (r32 & 3), grp = (n0 + wn) >> 6; // (waves w, w ^ 1: one group)
+        #pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int rr = rb + 8 * (i >> 2) + (i & 3), m = m0 + wm + rr;
+            const float po = pm[wave ^ 1][rr], wmax = po > am[i] ? po : am[i];
+            if (m < M) {
+                if ((wave & 1) == 0 && (r32 & 0x1b) == 0) hs[(size_t)m * (ldq >> 5) + grp] = wmax * (1.0f / 127.0f);
+                int32_t qi = 0;
+                if (wmax > 0.0f) {
+                    const float inv = 127.0f / wmax, x = hv[i] * inv;
+                    qi = (int32_t)(x + copysignf(0.49999997f, x));
+                }
+                hq[(size_t)m * ldq + f] = (int8_t)qi;
+            }
+        }
+    } else {
+        const int n = n0 + wn + r32;
+        #pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int m = m0 + wm + 8 * (r >> 2) + 4 * hi + (r & 3);
+            if (m < M && n < N) out[(size_t)m * ldo + n] = acc[r];
         }
     }
 }
@@ -684,23 +843,22 @@ struct SkMats { // the launch's matrices: blocks [0, nb1) the first, [nb1, grid)
     const uint8_t *W[2];
     int N[2], col[2], nb1;
 };
-template <int TYPE, int Q>
-__device__ __forceinline__ void kq32_terms(const i32x16 &I, const i32x16 &I1, float f0, float f1, int s0, int s1,
-                                           const float *xsw, int hi, int lane, float *Tq) {
-    // quad Q's 4 terms of this lane (registers 4 Q + e: activation rows 8 Q + 4 hi + e) into Tq[e * 64 + lane]
-    const float4 x4 = *(const float4 *)(xsw + 8 * Q + 4 * hi);
-    const float xsq[4] = { x4.x, x4.y, x4.z, x4.w };
+template <int TYPE, int Q, typename CT>
+__device__ __forceinline__ void kq32_terms(const i32x16 &I, const i32x16 &I1, const CT &C, int s0, int s1, int lane,
+                                           float *Tq) {
+    // quad Q's 4 terms of this lane (registers 4 Q + e: activation rows 8 Q + 4 hi + e) into Tq[e * 64 + lane]. C: the
+    // outer-product MFMA's result, the same (row, column) per register as I: C[r] = f0 xs (the scale product of the
+    // first term), Q4_K: C[16 + r] = f1 xf (the mins' term, xf = xs (float) sum x as kq_act_prep's, kquants.h:392-400)
     #pragma unroll
     for (int e = 0; e < 4; e++) {
         const int r = 4 * Q + e;
         float term;
-        if (TYPE == GW_Q4_K) {
-            float pa = (f0 * xsq[e]) * (float)I[r];
-            float pb = f1 * (xsq[e] * (float)I1[r]);
-            term = pa - pb;
-        } else {
-            int Ii = s0 * I[r] + s1 * I1[r];
-            term = (f0 * xsq[e]) * (float)Ii;
+        if constexpr (TYPE == GW_Q4_K) {
+            float pa = C[r] * (float)I[r];
+            term = pa - C[16 + r];
+        } else { // (|s| <= 127, |I_h| < 2^17: the 24-bit multiplies are exact)
+            int Ii = __mul24(s0, I[r]) + __mul24(s1, I1[r]);
+            term = C[r] * (float)Ii;
         }
         Tq[e * 64 + lane] = term;
     }
@@ -740,10 +898,10 @@ __global__ __launch_bounds__(SK_T * SB, SB == 1 ? 2 : 1) void k_gemm_kq32(SkMats
     auto load = [&](int s) __attribute__((always_inline)) -> SkStage<TYPE> {
         int b = s * SB + ts;
         b = b < S ? b : S - 1; // (past the last super-block: the last again)
-        SkStage<TYPE> o;
-        o.w = *(const uint4 *)(wsrc + (size_t)b * bstride);
-        o.x = *(const uint4 *)(xsrc + 256 * b);
-        o.xs = xssrc[8 * b];
+        SkStage<TYPE> o; // (32-bit offsets: a 64-bit multiply per load was a quarter-rate v_mad_u64_u32)
+        o.w = *(const uint4 *)(wsrc + (uint32_t)(b * bstride));
+        o.x = *(const uint4 *)(xsrc + (uint32_t)(256 * b));
+        o.xs = xssrc[(uint32_t)(8 * b)];
         return o;
     };
     auto stage = [&](const SkStage<TYPE> &o, int buf) __attribute__((always_inline)) {
@@ -764,8 +922,8 @@ __global__ __launch_bounds__(SK_T * SB, SB == 1 ? 2 : 1) void k_gemm_kq32(SkMats
         if (s >= S2) return nl; // (the last group of four steps past the end: its loads only, uniform)
         const uint8_t *wb = wrow_l + buf * (SB * 32 * WST), *xb = xrow_l + buf * (SB * 32 * SK_XR);
         float f0, f1 = 0.0f;
-        int s0 = 0, s1 = 0;
-        i32x16 I, I1;
+        int s0 = 0, s1 = 0, sxs = 0;
+        i32x16 I, I1 = z;
         if constexpr (TYPE == GW_Q4_K) {
             const uint4 xq = *(const uint4 *)(xb + 16 * hi);
             const uint4 q = *(const uint4 *)(wb + 16 + 32 * (w >> 1) + 16 * hi);
@@ -774,9 +932,13 @@ __global__ __launch_bounds__(SK_T * SB, SB == 1 ? 2 : 1) void k_gemm_kq32(SkMats
             const i32x4 bq = { (int)((q.x >> sh) & 0x0F0F0F0Fu), (int)((q.y >> sh) & 0x0F0F0F0Fu),
                                (int)((q.z >> sh) & 0x0F0F0F0Fu), (int)((q.w >> sh) & 0x0F0F0F0Fu) };
             const i32x4 a = { (int)xq.x, (int)xq.y, (int)xq.z, (int)xq.w };
-            const i32x4 ones = { 0x01010101, 0x01010101, 0x01010101, 0x01010101 };
             I = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, z, 0, 0, 0);
-            I1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, ones, z, 0, 0, 0); // (the sums of x)
+            // the sum of x of activation row r32 (its two halves of 16 in lanes l and l ^ 32)
+            int sx = __builtin_amdgcn_sdot4((int)xq.x, 0x01010101, 0, false);
+            sx = __builtin_amdgcn_sdot4((int)xq.y, 0x01010101, sx, false);
+            sx = __builtin_amdgcn_sdot4((int)xq.z, 0x01010101, sx, false);
+            sx = __builtin_amdgcn_sdot4((int)xq.w, 0x01010101, sx, false);
+            sxs = sx + __shfl_xor(sx, 32);
             // the scale bytes k = w, w + 4 and w - 4 (the 12 bytes in words y, z, w of the header)
             const int bs = 8 * (w & 3);
             const int bw = (int)(((w < 4 ? hd.y : hd.z) >> bs) & 0xffu), bw4 = (int)(((w < 4 ? hd.z : hd.w) >> bs) & 0xffu);
@@ -813,28 +975,41 @@ __global__ __launch_bounds__(SK_T * SB, SB == 1 ? 2 : 1) void k_gemm_kq32(SkMats
             s1 = (int)(int8_t)((sc2 >> 8) & 0xffu);
             f0 = h2f_g((uint16_t)(dw & 0xffffu));
         }
+        // the scale products as an outer-product MFMA (each product one fp32 rounding, as the VALU's multiply): lanes
+        // 0 .. 31 xs of activation row r32 and f0 of weight row r32; Q4_K: two blocks, lanes 32 .. 63 the row's
+        // xf = xs (float) sum x and f1; Q6_K: one block of K = 2, lanes 32 .. 63 (k = 1) zero (x y + 0 0 = x y)
+        const float xsr = xsl[buf][sb][w][r32];
+        const float ca = hi ? (TYPE == GW_Q4_K ? xsr * (float)sxs : 0.0f) : xsr, cb = hi ? (TYPE == GW_Q4_K ? f1 : 0.0f) : f0;
+        using CT = typename std::conditional<TYPE == GW_Q4_K, f32x32, f32x16>::type;
+        CT C;
+        if constexpr (TYPE == GW_Q4_K) {
+            const f32x32 zf = {};
+            C = __builtin_amdgcn_mfma_f32_32x32x1f32(ca, cb, zf, 0, 0, 0);
+        } else {
+            const f32x16 zf = {};
+            C = __builtin_amdgcn_mfma_f32_32x32x2f32(ca, cb, zf, 0, 0, 0);
+        }
         // this block's quads (uniform branches: a register index must be a constant)
-        const float *xsw = &xsl[buf][sb][w][0];
         float *Tw = &Tl[wv][0];
         __syncthreads(); // (every wave's fold of the previous step has read the terms)
         if (NQR == 4) {
-            kq32_terms<TYPE, 0>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw);
-            kq32_terms<TYPE, 1>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw + 256);
-            kq32_terms<TYPE, 2>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw + 512);
-            kq32_terms<TYPE, 3>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw + 768);
+            kq32_terms<TYPE, 0, CT>(I, I1, C, s0, s1, lane, Tw);
+            kq32_terms<TYPE, 1, CT>(I, I1, C, s0, s1, lane, Tw + 256);
+            kq32_terms<TYPE, 2, CT>(I, I1, C, s0, s1, lane, Tw + 512);
+            kq32_terms<TYPE, 3, CT>(I, I1, C, s0, s1, lane, Tw + 768);
         } else if (NQR == 2) {
             if (q0 == 0) {
-                kq32_terms<TYPE, 0>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw);
-                kq32_terms<TYPE, 1>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw + 256);
+                kq32_terms<TYPE, 0, CT>(I, I1, C, s0, s1, lane, Tw);
+                kq32_terms<TYPE, 1, CT>(I, I1, C, s0, s1, lane, Tw + 256);
             } else {
-                kq32_terms<TYPE, 2>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw);
-                kq32_terms<TYPE, 3>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw + 256);
+                kq32_terms<TYPE, 2, CT>(I, I1, C, s0, s1, lane, Tw);
+                kq32_terms<TYPE, 3, CT>(I, I1, C, s0, s1, lane, Tw + 256);
             }
         } else {
-            if (q0 == 0) kq32_terms<TYPE, 0>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw);
-            else if (q0 == 1) kq32_terms<TYPE, 1>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw);
-            else if (q0 == 2) kq32_terms<TYPE, 2>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw);
-            else kq32_terms<TYPE, 3>(I, I1, f0, f1, s0, s1, xsw, hi, lane, Tw);
+            if (q0 == 0) kq32_terms<TYPE, 0, CT>(I, I1, C, s0, s1, lane, Tw);
+            else if (q0 == 1) kq32_terms<TYPE, 1, CT>(I, I1, C, s0, s1, lane, Tw);
+            else if (q0 == 2) kq32_terms<TYPE, 2, CT>(I, I1, C, s0, s1, lane, Tw);
+            else kq32_terms<TYPE, 3, CT>(I, I1, C, s0, s1, lane, Tw);
         }
         __syncthreads(); // (the terms of step s written; step s + 1 staged)
         const int ng = 8 * (S - s * SB < SB ? S - s * SB : SB); // (a last step past K: its terms not added)
@@ -1591,6 +1766,7 @@ static int g_kq32_nqr; // (0: chosen per launch; 1, 2 or 4: forced, gw_kq32_quad
 static int g_kq32_sb;  // (0: chosen per launch; 1 or 2 super-blocks per step: forced, gw_kq32_step)
 static int g_kq16;     // (9 .. 32 K-quant rows: 0 k_gemm_kq32, 1 k_gemm_kq16; gw_kq_small_kernel)
 static int g_q8_batch;  // (Q8_0 at 2 .. 32 rows: 0 chosen per launch, 1 the batched GEMV, 2 the MFMA GEMM; gw_q8_batch_kernel)
+static int g_q8_lds;    // (the Q8_0 GEMM: 0 chosen per launch, 1 k_gemm_q8f / k_gemm_q8, 2 / 3 k_gemm_q8l of 128 / 64 columns; gw_q8_gemm_kernel)
 
 static bool q8_gemm_rows(const GwMat *w, int M) {
     // a Q8_0 matmul of M activation rows takes the MFMA GEMM (else the batched GEMV in passes of 8 rows): above 32 rows,
@@ -1599,6 +1775,21 @@ static bool q8_gemm_rows(const GwMat *w, int M) {
     // 4,096 whatever the width), the GEMV's grows with both (per 8 rows a pass over the weights): measured at the 8B
     // widths, 16 rows: 24,576 x 4,096 58.7 -> 39.6 us, 12,288 x 4,096 34.8 -> 35.1 us, 6,144 x 4,096 20.3 -> 32.5 us
     return M > GW_GEMV_MAX_ROWS || (M >= 16 && w->rows >= 8192);
+}
+
+static int q8l_width(int N, int M) {
+    // the Q8_0 GEMM's kernel for N columns and M rows (K % 128 == 0): k_gemm_q8l with 128-column tiles (returns 128),
+    // with 64-column tiles (64), or 0: k_gemm_q8f. Forced by gw_q8_gemm_kernel (1, 2, 3), else: up to 32 rows
+    // k_gemm_q8f's 32-row tiles (k_gemm_q8l's fold would run over 64), 128 columns where those tiles give three
+    // blocks per CU or more, else 64. Measured at the 8B widths, us per launch (k_gemm_q8f / 128 / 64 columns):
+    //   512 rows: 24,576 x 4,096 208 / 188 / 201; 12,288 x 4,096 116 / 101 / 102; 6,144 x 4,096 63.1 / 65.3 / 58.6;
+    //             4,096 x 4,096 48.8 / 44.1 / 42.5; 4,096 x 12,288 133 / 122 / 119
+    //   256 rows: 24,576 x 4,096 123 / 109 / 109; 12,288 x 4,096 62.9 / 66.2 / 55.1; 4,096 x 12,288 91.2 / 122 / 88.8
+    //   64 rows: 24,576 x 4,096 47.3 / 43.7 / 44.2; 12,288 x 4,096 31.6 / 42.3 / 31.0; 4,096 x 12,288 86.1 / 120 / 87.6
+    if (g_q8_lds) return g_q8_lds == 2 ? 128 : g_q8_lds == 3 ? 64 : 0;
+    if (M <= 32) return 0;
+    const size_t t128 = (size_t)((N + 127) / 128) * ((M + 63) / 64);
+    return t128 >= (size_t)3 * gemm_cus() ? 128 : 64;
 }
 
 static bool kq32_takes(const GwMat *w, int M) {
@@ -1682,7 +1873,14 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
         const bool full = w->cols % GKB == 0 && (size_t)(M + 64) * ldx < ((size_t)1 << 31) && (size_t)GN * w->cols < ((size_t)1 << 31);
         const dim3 g64g(nt, (M + 63) / 64), g32g(nt, (M + 31) / 32);
 #define GQ_ARGS (const int8_t *)w->codes, (const uint16_t *)w->scales, w->rows, w->cols, xq, xs, ldx, M, out, ldo
-        if (full && g64) hipExtLaunchKernelGGL((k_gemm_q8f<64, false>), g64g, dim3(256), 0, s, e0, e1, 0, GQ_ARGS, (int8_t *)NULL, (float *)NULL, 0);
+        const int mt = (M + 63) / 64, lq = full ? q8l_width(w->rows, M) : 0;
+        if (lq == 128)
+            hipExtLaunchKernelGGL((k_gemm_q8l<128, false>), dim3(((nt + 7) / 8) * 8 * mt), dim3(512), 0, s, e0, e1, 0, GQ_ARGS,
+                                  mt, (int8_t *)NULL, (float *)NULL, 0);
+        else if (lq == 64)
+            hipExtLaunchKernelGGL((k_gemm_q8l<64, false>), dim3(((w->rows + 511) / 512) * 8 * mt), dim3(256), 0, s, e0, e1, 0,
+                                  GQ_ARGS, mt, (int8_t *)NULL, (float *)NULL, 0);
+        else if (full && g64) hipExtLaunchKernelGGL((k_gemm_q8f<64, false>), g64g, dim3(256), 0, s, e0, e1, 0, GQ_ARGS, (int8_t *)NULL, (float *)NULL, 0);
         else if (full) hipExtLaunchKernelGGL((k_gemm_q8f<32, false>), g32g, dim3(256), 0, s, e0, e1, 0, GQ_ARGS, (int8_t *)NULL, (float *)NULL, 0);
         else if (g64) hipExtLaunchKernelGGL((k_gemm_q8<64>), g64g, dim3(256), 0, s, e0, e1, 0, GQ_ARGS);
         else hipExtLaunchKernelGGL((k_gemm_q8<32>), g32g, dim3(256), 0, s, e0, e1, 0, GQ_ARGS);
@@ -1778,13 +1976,24 @@ int gw_k_matmul_swiglu(const GwMat *w, int il, const int8_t *xq, const float *xs
     // the prefill GEMM takes 64-row tiles of full stages; -1 (nothing launched): not this case
     const int nt = (w->rows + GN - 1) / GN;
     if (w->type != GW_Q8_0 || il != 4 || M <= GW_GEMV_MAX_ROWS || w->rows % GN || ldq != w->rows / 2 || ldq % 32) return -1;
-    const bool g64 = g_tile_rows ? g_tile_rows == 64 : (size_t)nt * ((M + 63) / 64) >= (size_t)4 * gemm_cus();
+    const int mt = (M + 63) / 64;
+    const bool g64 = g_tile_rows ? g_tile_rows == 64 : (size_t)nt * mt >= (size_t)4 * gemm_cus();
+    const int lq = q8l_width(w->rows, M);
     const bool full = w->cols % GKB == 0 && (size_t)(M + 64) * ldx < ((size_t)1 << 31) && (size_t)GN * w->cols < ((size_t)1 << 31);
-    if (!g64 || !full) return -1;
+    if (!(lq || g64) || !full) return -1;
     hipEvent_t e0, e1;
     gw_take_launch_events(&e0, &e1);
-    hipExtLaunchKernelGGL((k_gemm_q8f<64, true>), dim3(nt, (M + 63) / 64), dim3(256), 0, s, e0, e1, 0, (const int8_t *)w->codes,
-                          (const uint16_t *)w->scales, w->rows, w->cols, xq, xs, ldx, M, (float *)NULL, 0, hq, hs, ldq);
+    if (lq == 128)
+        hipExtLaunchKernelGGL((k_gemm_q8l<128, true>), dim3(((nt + 7) / 8) * 8 * mt), dim3(512), 0, s, e0, e1, 0,
+                              (const int8_t *)w->codes, (const uint16_t *)w->scales, w->rows, w->cols, xq, xs, ldx, M,
+                              (float *)NULL, 0, mt, hq, hs, ldq);
+    else if (lq == 64)
+        hipExtLaunchKernelGGL((k_gemm_q8l<64, true>), dim3(((w->rows + 511) / 512) * 8 * mt), dim3(256), 0, s, e0, e1, 0,
+                              (const int8_t *)w->codes, (const uint16_t *)w->scales, w->rows, w->cols, xq, xs, ldx, M,
+                              (float *)NULL, 0, mt, hq, hs, ldq);
+    else
+        hipExtLaunchKernelGGL((k_gemm_q8f<64, true>), dim3(nt, mt), dim3(256), 0, s, e0, e1, 0, (const int8_t *)w->codes,
+                              (const uint16_t *)w->scales, w->rows, w->cols, xq, xs, ldx, M, (float *)NULL, 0, hq, hs, ldq);
     return (int)hipGetLastError();
 }
 
@@ -1837,6 +2046,13 @@ int gw_q8_block_sums(int32_t *isum, const int8_t *codes, int N, int K, const int
     hipLaunchKernelGGL(k_q8_block_sums, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, (hipStream_t)stream, isum, codes, N,
                        K, xq, M);
     return hipGetLastError() ? RQ_ERR_STATE : RQ_OK;
+}
+
+int gw_q8_gemm_kernel(int k) {
+    if (k < 0 || k > 3) return -1;
+    int prev = g_q8_lds;
+    g_q8_lds = k;
+    return prev;
 }
 
 int gw_q8_batch_kernel(int k) {

@@ -340,9 +340,16 @@ int gw_matmul_tile_rows(int rows);
 
 /* The kernel of the Q8_0 matmuls of 2 .. 32 activation rows (batched decode rows): 0 chosen per launch (the default:
  * the MFMA GEMM from 16 rows where the matrix has 8,192 rows or more, else the batched GEMV in passes of 8 rows), 1 the
- * batched GEMV, 2 the MFMA GEMM (k_gemm_q8f / k_gemm_q8, 32-row tiles). Returns the previous setting, or -1 (and
+ * batched GEMV, 2 the MFMA GEMM (k_gemm_q8f / k_gemm_q8, 32-row tiles, up to 32 rows). Returns the previous setting, or -1 (and
  * changes nothing) for another value. A tuning and test hook with no counterpart in runq.h; results do not depend on it */
 int gw_q8_batch_kernel(int k);
+
+/* The kernel of the Q8_0 MFMA GEMM (K % 128 == 0): 0 chosen per launch (the default: k_gemm_q8f up to 32 rows, else
+ * k_gemm_q8l with 128-column tiles where they give 3 blocks per CU, else 64), 1 k_gemm_q8f (4 waves, stages staged
+ * through registers), 2 / 3 k_gemm_q8l with 128 / 64-column tiles (8 / 4 waves, stages copied into LDS by the buffer
+ * unit). Returns the previous setting, or -1 (and changes nothing) for another value. A tuning and test hook with no
+ * counterpart in runq.h; results do not depend on it */
+int gw_q8_gemm_kernel(int k);
 
 /* The kernel of the 9 .. 32-row K-quant GEMM (Q4_K / Q6_K, batched decode rows): 0 k_gemm_kq32 (32-row tiles, the
  * groups spread over 8 waves, the terms exchanged in LDS; the default), 1 k_gemm_kq16 (each wave on 16 weight rows x 16

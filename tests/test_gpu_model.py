@@ -47,6 +47,36 @@ def test_prefill_decode_bitexact_vs_oracle(gw, synth_models, shape):
         tok = int(np.argmax(ref))
 
 
+@pytest.mark.parametrize("kern,tile", [(1, 64), (1, 32), (2, 0), (3, 0)])
+def test_prefill_gemm_kernels_bitexact_vs_oracle(gw, synth_models, kern, tile):
+    """a 100-row prefill pass through each Q8_0 GEMM (gw_q8_gemm_kernel 1 with 64- or 32-row tiles: k_gemm_q8f, the
+    64-row w1 / w3 one with the SwiGLU epilogue; 2, 3: k_gemm_q8l of 128 / 64 columns and its SwiGLU epilogue), every row's logits against the
+    oracle bit for bit, then decode steps on the cache it wrote"""
+    from oracle import oracle as orc
+    path = synth_models("tiny")
+    m = gw.Model(path, ctx_len=1024)
+    om = orc.Model(path, cap=1024)
+    ids = _ids(m.vocab, 100, 21)
+    c = m.ctx(max_batch=128)
+    s = m.seq(1024)
+    pk, pt = gw.lib.gw_q8_gemm_kernel(kern), gw.lib.gw_matmul_tile_rows(tile)
+    try:
+        lg_all = c.prefill(s, ids, mode=gw.RQ_LOGITS_ALL)
+    finally:
+        gw.lib.gw_q8_gemm_kernel(pk)
+        gw.lib.gw_matmul_tile_rows(pt)
+    os_ = om.seq()
+    for i, t in enumerate(ids):
+        ref = os_.forward(int(t))
+        assert _bits_equal(lg_all[i], ref), f"row {i}: max diff {np.abs(lg_all[i] - ref).max()}"
+    tok = int(np.argmax(lg_all[-1]))
+    for step in range(3):
+        lg = c.decode(s, tok)
+        ref = os_.forward(tok)
+        assert _bits_equal(lg, ref), f"decode step {step}"
+        tok = int(np.argmax(ref))
+
+
 @pytest.mark.parametrize("n_prompt", [600, 1100])
 def test_long_context_multi_block(gw, synth_models, n_prompt):
     """positions past 256: the attention split into blocks and combined (att_combine), prefill and decode; 600 takes
