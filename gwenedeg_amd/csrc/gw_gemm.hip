@@ -359,8 +359,10 @@ __global__ __launch_bounds__(256) void k_gemm_q8f(const int8_t *__restrict__ W, 
 // Blocks of 64 rows x TN columns (TN = 128: 8 waves, two blocks per CU; TN = 64: 4 waves, three per CU): wave w takes
 // the 32 x 32 tile of rows 32 (w / NC), columns 32 (w % NC), NC = TN / 32.
 // A copy writes a wave's 64 lanes to 1 KB of consecutive LDS, so stage rows (128 bytes = 4 groups) cannot be padded
-// apart; chunk c (16 bytes) of row r is stored at chunk c ^ (r % 8), which keeps the MFMA operand reads of 8
-// consecutive rows on distinct banks. Per stage, wave w copies 8 / NW of the 8 X pieces and W pieces 2 w, 2 w + 1
+// apart; chunk c (16 bytes) of row r is stored at chunk c ^ ((r / 2) % 8), which puts the MFMA operand reads of 16
+// consecutive rows (a 16-byte read serves 16 lanes per cycle from the 64 banks) on distinct banks (c ^ (r % 8) had
+// rows r and r + 8 on one bank: 3 conflict cycles per LDS-active cycle). Per stage, wave w copies 8 / NW of the 8
+// X pieces and W pieces 2 w, 2 w + 1
 // (1 KB = 8 rows each), wave 0 the stage's xs (a lane per row), waves 1 .. NC the ws (fp16, a dword = 2 groups of one
 // row per lane). Per pair of groups the fold of k_gemm_q8f: two int8 MFMAs for the exact sums, the outer-product MFMA
 // of the scale products, then val = val + (ws xs) (float) isum per output in group order (forward.c:906-916). Blocks:
@@ -401,17 +403,19 @@ __global__ __launch_bounds__(TN * 4, TN == 128 ? 2 : 3) void k_gemm_q8l(const in
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)(W + (size_t)n0 * K), (short)0, nr * K, GW_RSRC_DW3);
     const __amdgpu_buffer_rsrc_t rxs = __builtin_amdgcn_make_buffer_rsrc((void *)(XS + (size_t)m0 * gx), (short)0, mr * gx * 4, GW_RSRC_DW3);
     const __amdgpu_buffer_rsrc_t rws = __builtin_amdgcn_make_buffer_rsrc((void *)(WS + (size_t)n0 * G), (short)0, nr * G * 2, GW_RSRC_DW3);
-    // this lane's copies: row 8 p + lane / 8 of its 1 KB piece p, logical chunk (lane % 8) ^ (lane / 8)
-    const int pr = lane >> 3, pc = (lane & 7) ^ pr;
-    const int xo = (8 * XP * wave + pr) * ldx + 16 * pc, wo = (16 * wave + pr) * K + 16 * pc;
+    // this lane's copies: row 8 p + lane / 8 of its 1 KB piece p, logical chunk (lane % 8) ^ ((row / 2) % 8), which is
+    // (lane % 8) ^ (lane / 16) in an even piece, (lane % 8) ^ (4 + lane / 16) in an odd one
+    const int pr = lane >> 3, pce = (lane & 7) ^ (pr >> 1), pco = (lane & 7) ^ (4 + (pr >> 1));
+    const int xo = (8 * XP * wave + pr) * ldx, wo = (16 * wave + pr) * K + 16 * pce, wo1 = (16 * wave + 8 + pr) * K + 16 * pco;
     const int so = wave == 0 ? lane * gx * 4 : ((32 * (wave - 1) + (lane >> 1)) * G + 2 * (lane & 1)) * 2;
     auto issue = [&](int st) __attribute__((always_inline)) {
         uint8_t *bs = sl + (st % LQ_S) * LQ_STAGE(TN);
         const int k0 = st * 128;
         #pragma unroll
-        for (int p = 0; p < XP; p++) lq_copy(rx, bs + LQ_X + 1024 * (XP * wave + p), xo + 8 * p * ldx + k0, 16);
+        for (int p = 0; p < XP; p++) // (piece XP wave + p: odd where XP == 1 and the wave is odd, or p is)
+            lq_copy(rx, bs + LQ_X + 1024 * (XP * wave + p), xo + 8 * p * ldx + 16 * (((XP * wave + p) & 1) ? pco : pce) + k0, 16);
         lq_copy(rw, bs + LQ_W + 2048 * wave, wo + k0, 16);
-        lq_copy(rw, bs + LQ_W + 2048 * wave + 1024, wo + 8 * K + k0, 16);
+        lq_copy(rw, bs + LQ_W + 2048 * wave + 1024, wo1 + k0, 16);
         if (wave == 0) lq_copy(rxs, bs + LQ_XS(TN), so + 16 * st, 16);
         else if (wave <= NC) lq_copy(rws, bs + LQ_WS(TN) + 256 * (wave - 1), so + 8 * st, 4);
     };
@@ -419,7 +423,7 @@ __global__ __launch_bounds__(TN * 4, TN == 128 ? 2 : 3) void k_gemm_q8l(const in
     float acc[16];
     #pragma unroll
     for (int r = 0; r < 16; r++) acc[r] = 0.0f;
-    const int xa = LQ_X + (wm + r32) * 128, wa = LQ_W + (wn + r32) * 128, sw = r32 & 7;
+    const int xa = LQ_X + (wm + r32) * 128, wa = LQ_W + (wn + r32) * 128, sw = (r32 >> 1) & 7;
     const int xsa_o = LQ_XS(TN) + (wm + r32) * 16 + 4 * hi, wsb_o = LQ_WS(TN) + (wn + r32) * 8 + 2 * hi;
     issue(0);
     if (NS > 1) issue(1);
