@@ -536,70 +536,89 @@ __global__ __launch_bounds__(TN * 4, TN == 128 ? 2 : 3) void k_gemm_q8l(const in
 // For few rows (one or two row tiles) the 32 x 32 waves sit one per SIMD with 16 outputs each, and their fold's
 // dependent chain of latencies sets the time. Copies per stage: wave w < 8 X piece w, wave 8 + p W piece p, wave 0 the
 // xs, waves 1 and 2 the ws. mode 0, K % 128 == 0
-template <int S>
+template <int S, int Q>
 __global__ __launch_bounds__(1024, 1) void k_gemm_q8t(const int8_t *__restrict__ W, const uint16_t *__restrict__ WS, int N,
                                                       int K, const int8_t *__restrict__ X, const float *__restrict__ XS,
                                                       int ldx, int M, float *__restrict__ out, int ldo, int MT) {
-    constexpr int TN = 64;
-    __shared__ __align__(16) uint8_t sl[S * LQ_STAGE(TN)];
+    // S stages in the ring, each of GK = 128 Q bytes of K (GP = 4 Q groups): X 64 x GK, W 64 x GK, xs 64 x GP floats,
+    // ws 64 x GP halves
+    constexpr int TN = 64, GK = 128 * Q, GP = 4 * Q, CH = GK / 16, RPP = 1024 / GK; // (chunks per row, rows per piece)
+    constexpr int OX = 0, OW = 64 * GK, OXS = 128 * GK, OWS = 128 * GK + 64 * GP * 4, STG = 128 * GK + 64 * GP * 6;
+    constexpr int NXS = Q, NWS = GP / 2; // (xs pieces of 1 KB, ws pieces of 256 bytes)
+    __shared__ __align__(16) uint8_t sl[S * STG];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, l16 = lane & 15, q4 = lane >> 4;
     const int b = blockIdx.x, j = b >> 3, nt = (N + TN - 1) / TN;
     const int ntile = (j / MT) * 8 + (b & 7), m0 = (j % MT) * 64, n0 = ntile * TN;
     if (ntile >= nt) return; // (the grid's padding to 8 column tiles per XCD)
-    const int G = K >> 5, gx = ldx >> 5, NS = K >> 7;
+    const int G = K >> 5, gx = ldx >> 5, NS = K / GK;
     const int mr = M - m0 < 64 ? M - m0 : 64, nr = N - n0 < TN ? N - n0 : TN;
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void *)(X + (size_t)m0 * ldx), (short)0, mr * ldx, GW_RSRC_DW3);
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)(W + (size_t)n0 * K), (short)0, nr * K, GW_RSRC_DW3);
     const __amdgpu_buffer_rsrc_t rxs = __builtin_amdgcn_make_buffer_rsrc((void *)(XS + (size_t)m0 * gx), (short)0, mr * gx * 4, GW_RSRC_DW3);
     const __amdgpu_buffer_rsrc_t rws = __builtin_amdgcn_make_buffer_rsrc((void *)(WS + (size_t)n0 * G), (short)0, nr * G * 2, GW_RSRC_DW3);
-    // this wave's piece p (X: p = wave, W: p = wave - 8): row 8 p + lane / 8, logical chunk (lane % 8) ^ ((row / 2) % 8)
-    const int pr = lane >> 3, pp = wave & 7, pc = (lane & 7) ^ (4 * (pp & 1) + (pr >> 1));
-    const int co = wave < 8 ? (8 * pp + pr) * ldx + 16 * pc : (8 * pp + pr) * K + 16 * pc;
-    const int so = wave == 0 ? lane * gx * 4 : ((32 * (wave - 1) + (lane >> 1)) * G + 2 * (lane & 1)) * 2;
+    // the swizzle: chunk c of row r at c ^ sw(r), so that 16 consecutive rows' reads of one chunk fall on distinct banks
+    auto swz = [](int r) -> int { return Q == 1 ? (r >> 1) & 7 : r & 15; };
+    // this wave's pieces (1 KB = RPP rows; lane: row RPP p + lane / CH, physical chunk lane % CH): Q = 1: waves 0 .. 7
+    // X piece wave, waves 8 .. 15 W piece wave - 8; Q = 2: X and W piece wave. Then xs (waves 0 .. NXS - 1) and ws
+    // (waves NXS .. NXS + NWS - 1)
+    const int xp = Q == 1 ? (wave & 7) : wave, prow = lane / CH, pch = lane % CH;
+    const int xrow = RPP * xp + prow, lcx = pch ^ swz(xrow);
+    const int xo = xrow * ldx + 16 * lcx, wo = xrow * K + 16 * lcx; // (W piece xp: the same rows and chunks)
+    const bool hx = Q == 2 || wave < 8, hw = Q == 2 || wave >= 8;
+    // xs: Q = 1 a lane per row (its 4 groups), Q = 2 rows 32 p + lane / 2, 16 bytes (lane % 2) of the row's 32; ws: a
+    // dword (2 groups) per lane, GP / 2 lanes per row
+    int so = 0;
+    if (wave < NXS) so = Q == 1 ? lane * gx * 4 : ((32 * wave + (lane >> 1)) * gx + 4 * (lane & 1)) * 4;
+    else if (wave < NXS + NWS) so = (((64 / (GP / 2)) * (wave - NXS) + lane / (GP / 2)) * G + 2 * (lane % (GP / 2))) * 2;
     auto issue = [&](int st) __attribute__((always_inline)) {
-        uint8_t *bs = sl + (st % S) * LQ_STAGE(TN);
-        const int k0 = st * 128;
-        if (wave < 8) lq_copy(rx, bs + LQ_X + 1024 * pp, co + k0, 16);
-        else lq_copy(rw, bs + LQ_W + 1024 * pp, co + k0, 16);
-        if (wave == 0) lq_copy(rxs, bs + LQ_XS(TN), so + 16 * st, 16);
-        else if (wave <= 2) lq_copy(rws, bs + LQ_WS(TN) + 256 * (wave - 1), so + 8 * st, 4);
+        uint8_t *bs = sl + (st % S) * STG;
+        const int k0 = st * GK;
+        if (hx) lq_copy(rx, bs + OX + 1024 * xp, xo + k0, 16);
+        if (hw) lq_copy(rw, bs + OW + 1024 * xp, wo + k0, 16);
+        if (wave < NXS) lq_copy(rxs, bs + OXS + 1024 * wave, so + 4 * GP * st, 16);
+        else if (wave < NXS + NWS) lq_copy(rws, bs + OWS + 256 * (wave - NXS), so + 2 * GP * st, 4);
     };
     const int wm = (wave >> 2) * 16, wn = (wave & 3) * 16; // (this wave's 16 x 16 tile)
     float acc[4] = { 0.0f, 0.0f, 0.0f, 0.0f };
-    // operands: A row wm + l16 (X), B row wn + l16 (W), bytes 32 g + 8 q4 .. + 7 of the stage row: 16-byte chunk
+    // operands: A row wm + l16 (X), B row wn + l16 (W), bytes 32 g + 8 q4 .. + 7 of the stage row: logical chunk
     // 2 g + q4 / 2, its half q4 % 2
     const int xr = wm + l16, wr = wn + l16;
-    const int xa = LQ_X + xr * 128 + 8 * (q4 & 1), wa = LQ_W + wr * 128 + 8 * (q4 & 1);
-    const int xsw = (xr >> 1) & 7, wsw = (wr >> 1) & 7;
-    const int xsa_o = LQ_XS(TN) + xr * 16 + 4 * q4, wsb_o = LQ_WS(TN) + wr * 8 + 2 * q4;
+    const int xa = OX + xr * GK + 8 * (q4 & 1), wa = OW + wr * GK + 8 * (q4 & 1);
+    const int xsw = swz(xr), wsw = swz(wr);
+    const int xsa_o = OXS + xr * GP * 4 + 4 * q4, wsb_o = OWS + wr * GP * 2 + 2 * q4;
+    // copies per stage of this wave: X and / or W, and one xs or ws piece
+    const int cnt = (Q == 2 ? 2 : 1) + (wave < NXS + NWS ? 1 : 0);
     // S - 1 stages in flight: the ring holds S; stage st's slot is refilled with stage st + S after the barrier of
     // stage st + 1 (its readers are past it)
     for (int p = 0; p < S - 1 && p < NS; p++) issue(p);
     for (int st = 0; st < NS; st++) {
-        // stage st landed: this wave's copies of the later stages issued (L of them, 2 copies each for waves 0 .. 2,
-        // else 1) may be outstanding
+        // stage st landed: this wave's copies of the later stages issued (L stages of cnt copies) may be outstanding
         const int L = NS - 1 - st < S - 2 ? NS - 1 - st : S - 2;
-        if (wave <= 2) lq_vmwait<2, S - 2>(L);
-        else lq_vmwait<1, S - 2>(L);
+        if (cnt == 1) lq_vmwait<1, S - 2>(L);
+        else if (cnt == 2) lq_vmwait<2, S - 2>(L);
+        else lq_vmwait<3, S - 2>(L);
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         if (st + S - 1 < NS) issue(st + S - 1); // (into the slot of stage st - 1, whose readers are past the barrier)
-        const uint8_t *bs = sl + (st % S) * LQ_STAGE(TN);
-        // the 4 groups' scale products (block g: group g's xs of row 4 (lane / 16) + r, ws of column lane % 16)
-        const float xsa = *(const float *)(bs + xsa_o), wsb = h2f_g(*(const uint16_t *)(bs + wsb_o));
-        const f32x16 zf = {};
-        const f32x16 C = __builtin_amdgcn_mfma_f32_16x16x1f32(xsa, wsb, zf, 0, 0, 0);
-        i32x4 I[4];
+        const uint8_t *bs = sl + (st % S) * STG;
         #pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const int ca = 16 * ((2 * g + (q4 >> 1)) ^ xsw), cb = 16 * ((2 * g + (q4 >> 1)) ^ wsw);
-            const long a = *(const long *)(bs + xa + ca), bb = *(const long *)(bs + wa + cb);
-            const i32x4 z = { 0, 0, 0, 0 };
-            I[g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bb, z, 0, 0, 0);
-        }
-        #pragma unroll
-        for (int g = 0; g < 4; g++)
+        for (int q = 0; q < Q; q++) {
+            // groups 4 q .. 4 q + 3: their scale products (block g: xs of row 4 (lane / 16) + r, ws of column lane % 16)
+            const float xsa = *(const float *)(bs + xsa_o + 16 * q), wsb = h2f_g(*(const uint16_t *)(bs + wsb_o + 8 * q));
+            const f32x16 zf = {};
+            const f32x16 C = __builtin_amdgcn_mfma_f32_16x16x1f32(xsa, wsb, zf, 0, 0, 0);
+            i32x4 I[4];
             #pragma unroll
-            for (int r = 0; r < 4; r++) acc[r] = acc[r] + C[4 * g + r] * (float)I[g][r];
+            for (int g = 0; g < 4; g++) {
+                const int c = 2 * (4 * q + g) + (q4 >> 1);
+                const long a = *(const long *)(bs + xa + 16 * (c ^ xsw)), bb = *(const long *)(bs + wa + 16 * (c ^ wsw));
+                const i32x4 z = { 0, 0, 0, 0 };
+                I[g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bb, z, 0, 0, 0);
+            }
+            #pragma unroll
+            for (int g = 0; g < 4; g++)
+                #pragma unroll
+                for (int r = 0; r < 4; r++) acc[r] = acc[r] + C[4 * g + r] * (float)I[g][r];
+        }
     }
     const int n = n0 + wn + l16;
     #pragma unroll
@@ -1867,13 +1886,13 @@ static int g_q8_lds;    // (the Q8_0 GEMM: 0 chosen per launch, 1 k_gemm_q8f / k
 
 static bool q8_gemm_rows(const GwMat *w, int M) {
     // a Q8_0 matmul of M activation rows takes the MFMA GEMM (else the batched GEMV in passes of 8 rows): above 24 rows;
-    // above 16 for matrices of 6,144 rows or more; from 9 for 8,192 or more. The GEMM's time hardly depends on M or the
-    // width (27-33 us at K = 4,096, 75-88 at 12,288: its stages' latency), the GEMV's grows with both (per 8 rows a
-    // pass over the weights). Measured at the 8B widths, us (GEMV / GEMM): 9 rows 24,576 x 4,096 48.5 / 33.1,
-    // 12,288 x 4,096 28.8 / 27.8, 6,144 x 4,096 17.4 / 27.1; 16 rows 12,288 x 4,096 33.5 / 27.6, 6,144 x 4,096 21.8 /
-    // 27.3, 4,096 x 12,288 39.3 / 75.1; 24 rows 6,144 x 4,096 32.2 / 27.6, 4,096 x 4,096 25.7 / 27.1, 4,096 x 12,288
-    // 57.9 / 75.0; 32 rows 4,096 x 4,096 33.4 / 27.2, 4,096 x 12,288 76.3 / 75.4
-    return M > 24 || (M > 16 && w->rows >= 6144) || (M > 8 && w->rows >= 8192);
+    // above 16 where K <= 4,096; above 8 for matrices of 8,192 rows or more. The GEMM's time hardly depends on M or the
+    // width (23-33 us at K = 4,096, 63-88 at 12,288), the GEMV's grows with both (per 8 rows a pass over the weights).
+    // Measured at the 8B widths, us (GEMV / GEMM): 9 rows 24,576 x 4,096 48.5 / 33.1, 12,288 x 4,096 28.8 / 23.1,
+    // 6,144 x 4,096 17.4 / 22.9; 16 rows 12,288 x 4,096 33.5 / 23.1, 6,144 x 4,096 21.8 / 22.9, 4,096 x 4,096 17.8 /
+    // 22.5, 4,096 x 12,288 39.3 / 62.6; 24 rows 6,144 x 4,096 32.2 / 23.3, 4,096 x 4,096 25.7 / 23.2, 4,096 x 12,288
+    // 57.9 / 62.5; 32 rows 4,096 x 12,288 76.3 / 62.5
+    return M > 24 || (M > 16 && w->cols <= 4096) || (M > 8 && w->rows >= 8192);
 }
 
 static int q8l_width(int N, int M) {
@@ -1881,15 +1900,16 @@ static int q8l_width(int N, int M) {
     // with 64-column tiles (64), k_gemm_q8t (16), or 0: k_gemm_q8f. Forced by gw_q8_gemm_kernel (1 .. 4), else:
     // k_gemm_q8t where its 64 x 64 tiles are at most one per CU; else up to 32 rows k_gemm_q8f's 32-row tiles, 128
     // columns where those tiles give three blocks per CU or more, else 64. Measured at the 8B widths, us per launch:
-    //   k_gemm_q8t / k_gemm_q8l 64 columns / k_gemm_q8f: 64 rows 12,288 x 4,096 28.7 / 31.4 / 32.1; 6,144 x 4,096
-    //   27.4 / 31.4 / 32.5; 4,096 x 12,288 75.5 / 87.1 / 88.0; 256 rows 4,096 x 4,096 28.6 / 31.9 / 32.8; 32 rows
-    //   12,288 x 4,096 28.2 / - / 32.0; 24,576 x 4,096 (384 tiles) 42.1 / - / 33.3
+    //   k_gemm_q8t (stages of 256 / 128 bytes of K) / k_gemm_q8l 64 columns / k_gemm_q8f: 64 rows 12,288 x 4,096
+    //   24.5 / 27.3 / 31.2 / 32.1; 6,144 x 4,096 23.8 / 26.9 / 30.7 / 32.5; 4,096 x 12,288 63.4 / 73.0 / 86.6 / 88.0;
+    //   256 rows 4,096 x 4,096 24.5 / 27.4 / 31.5 / 32.8; 32 rows 12,288 x 4,096 - / 28.2 / - / 32.0; 24,576 x 4,096
+    //   (384 tiles) 45.2 / 40.7 / 41.9 / 33.3
     // and (k_gemm_q8f / 128 / 64 columns):
     //   512 rows: 24,576 x 4,096 208 / 188 / 201; 12,288 x 4,096 116 / 101 / 102; 6,144 x 4,096 63.1 / 65.3 / 58.6;
     //             4,096 x 4,096 48.8 / 44.1 / 42.5; 4,096 x 12,288 133 / 122 / 119
     //   256 rows: 24,576 x 4,096 123 / 109 / 109; 12,288 x 4,096 62.9 / 66.2 / 55.1; 4,096 x 12,288 91.2 / 122 / 88.8
     //   64 rows: 24,576 x 4,096 47.3 / 43.7 / 44.2; 12,288 x 4,096 31.6 / 42.3 / 31.0; 4,096 x 12,288 86.1 / 120 / 87.6
-    if (g_q8_lds) return g_q8_lds == 2 ? 128 : g_q8_lds == 3 ? 64 : g_q8_lds == 4 ? 16 : 0;
+    if (g_q8_lds) return g_q8_lds == 2 ? 128 : g_q8_lds == 3 ? 64 : g_q8_lds == 4 ? 16 : g_q8_lds == 5 ? 17 : 0;
     const size_t cus = (size_t)gemm_cus(), mt = (size_t)((M + 63) / 64);
     if ((size_t)((N + 63) / 64) * mt <= cus) return 16;
     if (M <= 32) return 0;
@@ -1977,15 +1997,17 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
         const bool full = w->cols % GKB == 0 && (size_t)(M + 64) * ldx < ((size_t)1 << 31) && (size_t)GN * w->cols < ((size_t)1 << 31);
         const dim3 g64g(nt, (M + 63) / 64), g32g(nt, (M + 31) / 32);
 #define GQ_ARGS (const int8_t *)w->codes, (const uint16_t *)w->scales, w->rows, w->cols, xq, xs, ldx, M, out, ldo
-        const int mt = (M + 63) / 64, lq = full ? q8l_width(w->rows, M) : 0;
+        const int mt = (M + 63) / 64, lq0 = full ? q8l_width(w->rows, M) : 0, lq = lq0 == 16 && w->cols % 256 ? 17 : lq0;
         if (lq == 128)
             hipExtLaunchKernelGGL((k_gemm_q8l<128, false>), dim3(((nt + 7) / 8) * 8 * mt), dim3(512), 0, s, e0, e1, 0, GQ_ARGS,
                                   mt, (int8_t *)NULL, (float *)NULL, 0);
         else if (lq == 64)
             hipExtLaunchKernelGGL((k_gemm_q8l<64, false>), dim3(((w->rows + 511) / 512) * 8 * mt), dim3(256), 0, s, e0, e1, 0,
                                   GQ_ARGS, mt, (int8_t *)NULL, (float *)NULL, 0);
-        else if (lq == 16)
-            hipExtLaunchKernelGGL(k_gemm_q8t<4>, dim3(((w->rows + 511) / 512) * 8 * mt), dim3(1024), 0, s, e0, e1, 0, GQ_ARGS, mt);
+        else if (lq == 16) // (stages of 256 bytes of K)
+            hipExtLaunchKernelGGL((k_gemm_q8t<3, 2>), dim3(((w->rows + 511) / 512) * 8 * mt), dim3(1024), 0, s, e0, e1, 0, GQ_ARGS, mt);
+        else if (lq == 17) // (stages of 128)
+            hipExtLaunchKernelGGL((k_gemm_q8t<4, 1>), dim3(((w->rows + 511) / 512) * 8 * mt), dim3(1024), 0, s, e0, e1, 0, GQ_ARGS, mt);
         else if (full && g64) hipExtLaunchKernelGGL((k_gemm_q8f<64, false>), g64g, dim3(256), 0, s, e0, e1, 0, GQ_ARGS, (int8_t *)NULL, (float *)NULL, 0);
         else if (full) hipExtLaunchKernelGGL((k_gemm_q8f<32, false>), g32g, dim3(256), 0, s, e0, e1, 0, GQ_ARGS, (int8_t *)NULL, (float *)NULL, 0);
         else if (g64) hipExtLaunchKernelGGL((k_gemm_q8<64>), g64g, dim3(256), 0, s, e0, e1, 0, GQ_ARGS);
@@ -2155,7 +2177,7 @@ int gw_q8_block_sums(int32_t *isum, const int8_t *codes, int N, int K, const int
 }
 
 int gw_q8_gemm_kernel(int k) {
-    if (k < 0 || k > 4) return -1;
+    if (k < 0 || k > 5) return -1;
     int prev = g_q8_lds;
     g_q8_lds = k;
     return prev;
