@@ -64,10 +64,11 @@ def main():
     ap.add_argument("--kv-type", type=int, default=2,
                     help="batch32_4b / long_8b: the sequences' KV cache type (runq.h:214; default 2, RQ_KV_F16); another "
                          "type's line carries no cpu_baseline")
-    ap.add_argument("--workload", default="step", choices=["step", "op_q8", "batch32_4b", "long_8b", "cb_8b"],
+    ap.add_argument("--workload", default="step", choices=["step", "op_q8", "batch32_4b", "long_8b", "cb_8b", "batch32_8b"],
                     help="step: the metric's workload (default); op_q8: the isolated 12288 x 4096 Q8_0 operator of the "
-                         "reference's config 2; batch32_4b / long_8b: the batched decode of configs 3 / 4; cb_8b: config "
-                         "5's continuous-batching steps; each a JSON line of its own")
+                         "reference's config 2; batch32_4b / long_8b: the batched decode of configs 3 / 4; batch32_8b: "
+                         "config 3's 32 sequences x 2048 positions on the 8B-shaped Q8_0 model; cb_8b: config 5's "
+                         "continuous-batching steps; each a JSON line of its own")
     ap.add_argument("--workdir", default=os.environ.get("GW_BENCH_DIR", "/dev/shm/gwenedeg_bench" if os.path.isdir("/dev/shm")
                                                                       else "/tmp/gwenedeg_bench"))
     a = ap.parse_args()
@@ -213,10 +214,11 @@ def main():
     print(json.dumps(out), flush=True)
 
 
-BATCHED = {  # the reference's configs 3 and 4: shape, sequences, cached positions per sequence, timed decode steps,
+BATCHED = {  # the reference's configs 3 and 4 (and config 3's batch on the 8B shape): shape, sequences, cached positions per sequence, timed decode steps,
     # timed steps of the CPU baseline
     "batch32_4b": ("qwen3_4b_q4km", 32, 2048, 16, 48),
     "long_8b": ("qwen3_8b", 8, 32768, 8, 12),
+    "batch32_8b": ("qwen3_8b", 32, 2048, 16, 16),  # (config 3's batch on the 8B-shaped Q8_0 model: Q8_0 at 32 rows)
 }
 
 
@@ -267,7 +269,9 @@ def batched(torch, gw, synth, a):
     step_s = el / steps
     att_s = kt.get("attention", (0, 0))[0]
     out = {
-        "metric": f"batched greedy decode rows/s ({a.workload}: the reference's config {3 if nseq == 32 else 4}, 1 GPU)",
+        "metric": f"batched greedy decode rows/s ({a.workload}: " + {"batch32_4b": "the reference's config 3",
+                                                                       "long_8b": "the reference's config 4",
+                                                                       "batch32_8b": "config 3's batch on the 8B shape"}[a.workload] + ", 1 GPU)",
         "value": round(nseq * steps / el, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": a.warmup,
         "ms_per_step": round(1e3 * step_s, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": f"int8 x int8 -> int32, fp32 fold; KV type {a.kv_type}" + (" (f16)" if a.kv_type == 2 else ""),
