@@ -536,49 +536,72 @@ __global__ __launch_bounds__(TN * 4, TN == 128 ? 2 : 3) void k_gemm_q8l(const in
 // For few rows (one or two row tiles) the 32 x 32 waves sit one per SIMD with 16 outputs each, and their fold's
 // dependent chain of latencies sets the time. Copies per stage: wave w < 8 X piece w, wave 8 + p W piece p, wave 0 the
 // xs, waves 1 and 2 the ws. mode 0, K % 128 == 0
-template <int S, int Q>
-__global__ __launch_bounds__(1024, 1) void k_gemm_q8t(const int8_t *__restrict__ W, const uint16_t *__restrict__ WS, int N,
-                                                      int K, const int8_t *__restrict__ X, const float *__restrict__ XS,
-                                                      int ldx, int M, float *__restrict__ out, int ldo, int MT) {
-    // S stages in the ring, each of GK = 128 Q bytes of K (GP = 4 Q groups): X 64 x GK, W 64 x GK, xs 64 x GP floats,
-    // ws 64 x GP halves
-    constexpr int TN = 64, GK = 128 * Q, GP = 4 * Q, CH = GK / 16, RPP = 1024 / GK; // (chunks per row, rows per piece)
-    constexpr int OX = 0, OW = 64 * GK, OXS = 128 * GK, OWS = 128 * GK + 64 * GP * 4, STG = 128 * GK + 64 * GP * 6;
-    constexpr int NXS = Q, NWS = GP / 2; // (xs pieces of 1 KB, ws pieces of 256 bytes)
+template <int TM, int TN, int S, int Q>
+__global__ __launch_bounds__(TM * TN / 4, TM * TN >= 4096 ? 1 : 2) void k_gemm_q8t(const int8_t *__restrict__ W,
+                                                                               const uint16_t *__restrict__ WS, int N, int K,
+                                                                               const int8_t *__restrict__ X,
+                                                                               const float *__restrict__ XS, int ldx, int M,
+                                                                               float *__restrict__ out, int ldo, int MT) {
+    // blocks of TM x TN outputs (16 x 16 per wave, NW = TM TN / 256 waves); S stages in the ring, each of GK = 128 Q
+    // bytes of K (GP = 4 Q groups): X TM x GK, W TN x GK, xs TM x GP floats, ws TN x GP halves. A stage's copies are
+    // pieces of 1 KB (RPP = 1024 / GK rows) of X, then of W, then the xs pieces (1 KB: 1024 / (4 GP) rows) and the ws
+    // pieces (dwords, 256 bytes: 128 / GP rows), piece p copied by wave p % NW
+    constexpr int NW = TM * TN / 256, GK = 128 * Q, GP = 4 * Q, CH = GK / 16, RPP = 1024 / GK;
+    constexpr int PX = TM * GK / 1024, PW = TN * GK / 1024, PXS = (TM * GP * 4 + 1023) / 1024, PWS = TN * GP * 2 / 256;
+    constexpr int PT = PX + PW + PXS + PWS, PPW = (PT + NW - 1) / NW; // (pieces, per wave at most)
+    constexpr int OX = 0, OW = TM * GK, OXS = (TM + TN) * GK, OWS = OXS + PXS * 1024, STG = OWS + TN * GP * 2;
+    static_assert(PT <= 63 && TM % 16 == 0 && TN % 16 == 0 && PWS * 256 == TN * GP * 2, "tile shape");
     __shared__ __align__(16) uint8_t sl[S * STG];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, l16 = lane & 15, q4 = lane >> 4;
     const int b = blockIdx.x, j = b >> 3, nt = (N + TN - 1) / TN;
-    const int ntile = (j / MT) * 8 + (b & 7), m0 = (j % MT) * 64, n0 = ntile * TN;
+    const int ntile = (j / MT) * 8 + (b & 7), m0 = (j % MT) * TM, n0 = ntile * TN;
     if (ntile >= nt) return; // (the grid's padding to 8 column tiles per XCD)
     const int G = K >> 5, gx = ldx >> 5, NS = K / GK;
-    const int mr = M - m0 < 64 ? M - m0 : 64, nr = N - n0 < TN ? N - n0 : TN;
+    const int mr = M - m0 < TM ? M - m0 : TM, nr = N - n0 < TN ? N - n0 : TN;
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void *)(X + (size_t)m0 * ldx), (short)0, mr * ldx, GW_RSRC_DW3);
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)(W + (size_t)n0 * K), (short)0, nr * K, GW_RSRC_DW3);
     const __amdgpu_buffer_rsrc_t rxs = __builtin_amdgcn_make_buffer_rsrc((void *)(XS + (size_t)m0 * gx), (short)0, mr * gx * 4, GW_RSRC_DW3);
     const __amdgpu_buffer_rsrc_t rws = __builtin_amdgcn_make_buffer_rsrc((void *)(WS + (size_t)n0 * G), (short)0, nr * G * 2, GW_RSRC_DW3);
     // the swizzle: chunk c of row r at c ^ sw(r), so that 16 consecutive rows' reads of one chunk fall on distinct banks
     auto swz = [](int r) -> int { return Q == 1 ? (r >> 1) & 7 : r & 15; };
-    // this wave's pieces (1 KB = RPP rows; lane: row RPP p + lane / CH, physical chunk lane % CH): Q = 1: waves 0 .. 7
-    // X piece wave, waves 8 .. 15 W piece wave - 8; Q = 2: X and W piece wave. Then xs (waves 0 .. NXS - 1) and ws
-    // (waves NXS .. NXS + NWS - 1)
-    const int xp = Q == 1 ? (wave & 7) : wave, prow = lane / CH, pch = lane % CH;
-    const int xrow = RPP * xp + prow, lcx = pch ^ swz(xrow);
-    const int xo = xrow * ldx + 16 * lcx, wo = xrow * K + 16 * lcx; // (W piece xp: the same rows and chunks)
-    const bool hx = Q == 2 || wave < 8, hw = Q == 2 || wave >= 8;
-    // xs: Q = 1 a lane per row (its 4 groups), Q = 2 rows 32 p + lane / 2, 16 bytes (lane % 2) of the row's 32; ws: a
-    // dword (2 groups) per lane, GP / 2 lanes per row
-    int so = 0;
-    if (wave < NXS) so = Q == 1 ? lane * gx * 4 : ((32 * wave + (lane >> 1)) * gx + 4 * (lane & 1)) * 4;
-    else if (wave < NXS + NWS) so = (((64 / (GP / 2)) * (wave - NXS) + lane / (GP / 2)) * G + 2 * (lane % (GP / 2))) * 2;
+    // piece p's LDS offset in a stage, its buffer and its per-lane byte offset at K = 0 (stage st adds GK st, or 4 GP st
+    // for xs, 2 GP st for ws)
+    auto piece = [&](int p, int &lo, int &vo, int &kind) __attribute__((always_inline)) {
+        if (p < PX + PW) { // X or W: row RPP q + lane / CH, physical chunk lane % CH
+            const bool w = p >= PX;
+            const int q = w ? p - PX : p, row = RPP * q + lane / CH, lc = (lane % CH) ^ swz(row);
+            lo = (w ? OW : OX) + 1024 * q;
+            vo = row * (w ? K : ldx) + 16 * lc;
+            kind = w ? 1 : 0;
+        } else if (p < PX + PW + PXS) { // xs: 16 bytes per lane, GP / 4 lanes per row
+            const int q = p - PX - PW, row = (1024 / (4 * GP)) * q + lane / (GP / 4), h = lane % (GP / 4);
+            lo = OXS + 1024 * q;
+            vo = (row * gx + 4 * h) * 4;
+            kind = 2;
+        } else { // ws: a dword (2 groups) per lane, GP / 2 lanes per row
+            const int q = p - PX - PW - PXS, row = (128 / GP) * q + lane / (GP / 2), h = lane % (GP / 2);
+            lo = OWS + 256 * q;
+            vo = (row * G + 2 * h) * 2;
+            kind = 3;
+        }
+    };
+    int plo[PPW], pvo[PPW], pk[PPW];
+    #pragma unroll
+    for (int i = 0; i < PPW; i++) piece(wave + NW * i < PT ? wave + NW * i : 0, plo[i], pvo[i], pk[i]);
+    const int cnt = (PT - wave + NW - 1) / NW; // (this wave's pieces per stage)
     auto issue = [&](int st) __attribute__((always_inline)) {
         uint8_t *bs = sl + (st % S) * STG;
-        const int k0 = st * GK;
-        if (hx) lq_copy(rx, bs + OX + 1024 * xp, xo + k0, 16);
-        if (hw) lq_copy(rw, bs + OW + 1024 * xp, wo + k0, 16);
-        if (wave < NXS) lq_copy(rxs, bs + OXS + 1024 * wave, so + 4 * GP * st, 16);
-        else if (wave < NXS + NWS) lq_copy(rws, bs + OWS + 256 * (wave - NXS), so + 2 * GP * st, 4);
+        #pragma unroll
+        for (int i = 0; i < PPW; i++) {
+            if (i < cnt) {
+                if (pk[i] == 0) lq_copy(rx, bs + plo[i], pvo[i] + GK * st, 16);
+                else if (pk[i] == 1) lq_copy(rw, bs + plo[i], pvo[i] + GK * st, 16);
+                else if (pk[i] == 2) lq_copy(rxs, bs + plo[i], pvo[i] + 4 * GP * st, 16);
+                else lq_copy(rws, bs + plo[i], pvo[i] + 2 * GP * st, 4);
+            }
+        }
     };
-    const int wm = (wave >> 2) * 16, wn = (wave & 3) * 16; // (this wave's 16 x 16 tile)
+    const int wm = (wave / (TN / 16)) * 16, wn = (wave % (TN / 16)) * 16; // (this wave's 16 x 16 tile)
     float acc[4] = { 0.0f, 0.0f, 0.0f, 0.0f };
     // operands: A row wm + l16 (X), B row wn + l16 (W), bytes 32 g + 8 q4 .. + 7 of the stage row: logical chunk
     // 2 g + q4 / 2, its half q4 % 2
@@ -586,17 +609,15 @@ __global__ __launch_bounds__(1024, 1) void k_gemm_q8t(const int8_t *__restrict__
     const int xa = OX + xr * GK + 8 * (q4 & 1), wa = OW + wr * GK + 8 * (q4 & 1);
     const int xsw = swz(xr), wsw = swz(wr);
     const int xsa_o = OXS + xr * GP * 4 + 4 * q4, wsb_o = OWS + wr * GP * 2 + 2 * q4;
-    // copies per stage of this wave: X and / or W, and one xs or ws piece
-    const int cnt = (Q == 2 ? 2 : 1) + (wave < NXS + NWS ? 1 : 0);
     // S - 1 stages in flight: the ring holds S; stage st's slot is refilled with stage st + S after the barrier of
     // stage st + 1 (its readers are past it)
     for (int p = 0; p < S - 1 && p < NS; p++) issue(p);
     for (int st = 0; st < NS; st++) {
         // stage st landed: this wave's copies of the later stages issued (L stages of cnt copies) may be outstanding
         const int L = NS - 1 - st < S - 2 ? NS - 1 - st : S - 2;
-        if (cnt == 1) lq_vmwait<1, S - 2>(L);
-        else if (cnt == 2) lq_vmwait<2, S - 2>(L);
-        else lq_vmwait<3, S - 2>(L);
+        if (cnt == PPW) lq_vmwait<PPW, S - 2>(L);
+        else if (PPW > 1 && cnt == PPW - 1) lq_vmwait<(PPW > 1 ? PPW - 1 : 1), S - 2>(L);
+        else lq_vmwait<(PPW > 2 ? PPW - 2 : 1), S - 2>(L);
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         if (st + S - 1 < NS) issue(st + S - 1); // (into the slot of stage st - 1, whose readers are past the barrier)
         const uint8_t *bs = sl + (st % S) * STG;
@@ -1885,32 +1906,32 @@ static int g_q8_batch;  // (Q8_0 at 2 .. 32 rows: 0 chosen per launch, 1 the bat
 static int g_q8_lds;    // (the Q8_0 GEMM: 0 chosen per launch, 1 k_gemm_q8f / k_gemm_q8, 2 / 3 k_gemm_q8l of 128 / 64 columns; gw_q8_gemm_kernel)
 
 static bool q8_gemm_rows(const GwMat *w, int M) {
-    // a Q8_0 matmul of M activation rows takes the MFMA GEMM (else the batched GEMV in passes of 8 rows): above 24 rows;
-    // above 16 where K <= 4,096; above 8 for matrices of 8,192 rows or more. The GEMM's time hardly depends on M or the
-    // width (23-33 us at K = 4,096, 63-88 at 12,288), the GEMV's grows with both (per 8 rows a pass over the weights).
-    // Measured at the 8B widths, us (GEMV / GEMM): 9 rows 24,576 x 4,096 48.5 / 33.1, 12,288 x 4,096 28.8 / 23.1,
-    // 6,144 x 4,096 17.4 / 22.9; 16 rows 12,288 x 4,096 33.5 / 23.1, 6,144 x 4,096 21.8 / 22.9, 4,096 x 4,096 17.8 /
-    // 22.5, 4,096 x 12,288 39.3 / 62.6; 24 rows 6,144 x 4,096 32.2 / 23.3, 4,096 x 4,096 25.7 / 23.2, 4,096 x 12,288
-    // 57.9 / 62.5; 32 rows 4,096 x 12,288 76.3 / 62.5
-    return M > 24 || (M > 16 && w->cols <= 4096) || (M > 8 && w->rows >= 8192);
+    // a Q8_0 matmul of M activation rows takes the MFMA GEMM (else the batched GEMV in passes of 8 rows): above 16 rows;
+    // above 8 for matrices of 8,192 rows or more, above 12 for 6,144 or more at K <= 4,096. The GEMM's time hardly
+    // depends on M or the width (18-23 us at K = 4,096, 50 at 12,288, k_gemm_q8t), the GEMV's grows with both (per 8
+    // rows a pass over the weights). Measured at the 8B widths, us (GEMV / GEMM): 9 rows 24,576 x 4,096 48.5 / 32.8,
+    // 12,288 x 4,096 28.8 / 21.7, 6,144 x 4,096 17.4 / 18.4, 4,096 x 4,096 14.7 / 18.4, 4,096 x 12,288 34.0 / 49.4;
+    // 16 rows 6,144 x 4,096 21.8 / 18.3, 4,096 x 4,096 17.8 / 18.4, 4,096 x 12,288 39.3 / 49.3; 24 rows 4,096 x 4,096
+    // 25.7 / 18.4, 4,096 x 12,288 57.9 / 49.4
+    return M > 16 || (M > 8 && w->rows >= 8192) || (M > 12 && w->rows >= 6144 && w->cols <= 4096);
 }
 
 static int q8l_width(int N, int M) {
     // the Q8_0 GEMM's kernel for N columns and M rows (K % 128 == 0): k_gemm_q8l with 128-column tiles (returns 128),
-    // with 64-column tiles (64), k_gemm_q8t (16), or 0: k_gemm_q8f. Forced by gw_q8_gemm_kernel (1 .. 4), else:
-    // k_gemm_q8t where its 64 x 64 tiles are at most one per CU; else up to 32 rows k_gemm_q8f's 32-row tiles, 128
+    // with 64-column tiles (64), k_gemm_q8t of 64 x 64 tiles (16; 17: its 128-byte stages), of 32 x 32 (18) or 32 x 16
+    // (19), or 0: k_gemm_q8f. Forced by gw_q8_gemm_kernel (1 .. 7), else: k_gemm_q8t of 32 x 32 tiles where they are at
+    // most 1.5 per CU, of 64 x 64 where those are at most one per CU; else up to 32 rows k_gemm_q8f's 32-row tiles, 128
     // columns where those tiles give three blocks per CU or more, else 64. Measured at the 8B widths, us per launch:
-    //   k_gemm_q8t (stages of 256 / 128 bytes of K) / k_gemm_q8l 64 columns / k_gemm_q8f: 64 rows 12,288 x 4,096
-    //   24.5 / 27.3 / 31.2 / 32.1; 6,144 x 4,096 23.8 / 26.9 / 30.7 / 32.5; 4,096 x 12,288 63.4 / 73.0 / 86.6 / 88.0;
-    //   256 rows 4,096 x 4,096 24.5 / 27.4 / 31.5 / 32.8; 32 rows 12,288 x 4,096 - / 28.2 / - / 32.0; 24,576 x 4,096
-    //   (384 tiles) 45.2 / 40.7 / 41.9 / 33.3
-    // and (k_gemm_q8f / 128 / 64 columns):
+    //   k_gemm_q8t 32 x 32 / 64 x 64 / k_gemm_q8f: 32 rows 12,288 x 4,096 22.9 / 25.0 / 31.9; 6,144 x 4,096 18.8 / 23.9 /
+    //   31.4; 4,096 x 12,288 49.7 / 63.4 / 87.5; 24,576 x 4,096 38.4 / 47.6 / 34.1; 64 rows 12,288 x 4,096 38.4 / 25.6 /
+    //   33.0; 6,144 x 4,096 22.1 / 24.2 / 31.8; 4,096 x 4,096 18.8 / 24.1 / 31.4
+    // and (k_gemm_q8f / k_gemm_q8l 128 / 64 columns):
     //   512 rows: 24,576 x 4,096 208 / 188 / 201; 12,288 x 4,096 116 / 101 / 102; 6,144 x 4,096 63.1 / 65.3 / 58.6;
     //             4,096 x 4,096 48.8 / 44.1 / 42.5; 4,096 x 12,288 133 / 122 / 119
     //   256 rows: 24,576 x 4,096 123 / 109 / 109; 12,288 x 4,096 62.9 / 66.2 / 55.1; 4,096 x 12,288 91.2 / 122 / 88.8
-    //   64 rows: 24,576 x 4,096 47.3 / 43.7 / 44.2; 12,288 x 4,096 31.6 / 42.3 / 31.0; 4,096 x 12,288 86.1 / 120 / 87.6
-    if (g_q8_lds) return g_q8_lds == 2 ? 128 : g_q8_lds == 3 ? 64 : g_q8_lds == 4 ? 16 : g_q8_lds == 5 ? 17 : 0;
+    if (g_q8_lds) return g_q8_lds == 2 ? 128 : g_q8_lds == 3 ? 64 : g_q8_lds >= 4 ? 12 + g_q8_lds : 0;
     const size_t cus = (size_t)gemm_cus(), mt = (size_t)((M + 63) / 64);
+    if ((size_t)((N + 31) / 32) * ((M + 31) / 32) * 2 <= 3 * cus) return 18;
     if ((size_t)((N + 63) / 64) * mt <= cus) return 16;
     if (M <= 32) return 0;
     return (size_t)((N + 127) / 128) * mt >= 3 * cus ? 128 : 64;
@@ -1997,17 +2018,23 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
         const bool full = w->cols % GKB == 0 && (size_t)(M + 64) * ldx < ((size_t)1 << 31) && (size_t)GN * w->cols < ((size_t)1 << 31);
         const dim3 g64g(nt, (M + 63) / 64), g32g(nt, (M + 31) / 32);
 #define GQ_ARGS (const int8_t *)w->codes, (const uint16_t *)w->scales, w->rows, w->cols, xq, xs, ldx, M, out, ldo
-        const int mt = (M + 63) / 64, lq0 = full ? q8l_width(w->rows, M) : 0, lq = lq0 == 16 && w->cols % 256 ? 17 : lq0;
+        const int mt = (M + 63) / 64, lq0 = full ? q8l_width(w->rows, M) : 0, lq = lq0 >= 16 && w->cols % 256 ? 17 : lq0;
         if (lq == 128)
             hipExtLaunchKernelGGL((k_gemm_q8l<128, false>), dim3(((nt + 7) / 8) * 8 * mt), dim3(512), 0, s, e0, e1, 0, GQ_ARGS,
                                   mt, (int8_t *)NULL, (float *)NULL, 0);
         else if (lq == 64)
             hipExtLaunchKernelGGL((k_gemm_q8l<64, false>), dim3(((w->rows + 511) / 512) * 8 * mt), dim3(256), 0, s, e0, e1, 0,
                                   GQ_ARGS, mt, (int8_t *)NULL, (float *)NULL, 0);
-        else if (lq == 16) // (stages of 256 bytes of K)
-            hipExtLaunchKernelGGL((k_gemm_q8t<3, 2>), dim3(((w->rows + 511) / 512) * 8 * mt), dim3(1024), 0, s, e0, e1, 0, GQ_ARGS, mt);
+        else if (lq == 16) // (64 x 64 tiles, stages of 256 bytes of K)
+            hipExtLaunchKernelGGL((k_gemm_q8t<64, 64, 3, 2>), dim3(((w->rows + 511) / 512) * 8 * mt), dim3(1024), 0, s, e0, e1, 0, GQ_ARGS, mt);
         else if (lq == 17) // (stages of 128)
-            hipExtLaunchKernelGGL((k_gemm_q8t<4, 1>), dim3(((w->rows + 511) / 512) * 8 * mt), dim3(1024), 0, s, e0, e1, 0, GQ_ARGS, mt);
+            hipExtLaunchKernelGGL((k_gemm_q8t<64, 64, 4, 1>), dim3(((w->rows + 511) / 512) * 8 * mt), dim3(1024), 0, s, e0, e1, 0, GQ_ARGS, mt);
+        else if (lq == 18) // (32 x 32 tiles)
+            hipExtLaunchKernelGGL((k_gemm_q8t<32, 32, 4, 2>), dim3(((w->rows + 255) / 256) * 8 * ((M + 31) / 32)), dim3(256), 0, s, e0, e1, 0,
+                                  GQ_ARGS, (M + 31) / 32);
+        else if (lq == 19) // (32 x 16 tiles)
+            hipExtLaunchKernelGGL((k_gemm_q8t<32, 16, 4, 2>), dim3(((w->rows + 127) / 128) * 8 * ((M + 31) / 32)), dim3(128), 0, s, e0, e1, 0,
+                                  GQ_ARGS, (M + 31) / 32);
         else if (full && g64) hipExtLaunchKernelGGL((k_gemm_q8f<64, false>), g64g, dim3(256), 0, s, e0, e1, 0, GQ_ARGS, (int8_t *)NULL, (float *)NULL, 0);
         else if (full) hipExtLaunchKernelGGL((k_gemm_q8f<32, false>), g32g, dim3(256), 0, s, e0, e1, 0, GQ_ARGS, (int8_t *)NULL, (float *)NULL, 0);
         else if (g64) hipExtLaunchKernelGGL((k_gemm_q8<64>), g64g, dim3(256), 0, s, e0, e1, 0, GQ_ARGS);
@@ -2177,7 +2204,7 @@ int gw_q8_block_sums(int32_t *isum, const int8_t *codes, int N, int K, const int
 }
 
 int gw_q8_gemm_kernel(int k) {
-    if (k < 0 || k > 5) return -1;
+    if (k < 0 || k > 7) return -1;
     int prev = g_q8_lds;
     g_q8_lds = k;
     return prev;
