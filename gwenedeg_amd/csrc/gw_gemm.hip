@@ -454,22 +454,31 @@ __global__ __launch_bounds__(TN * 4, TN == 128 ? 2 : 3) void k_gemm_q8l(const in
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         if (st + 2 < NS) issue(st + 2); // (into the slot of stage st - 1, whose readers are past the barrier)
         const uint8_t *bs = sl + (st % LQ_S) * LQ_STAGE(TN);
-        #pragma unroll 1
-        for (int g0 = 0; g0 < 4; g0 += 2) {
-            const int c0 = 16 * ((2 * g0 + hi) ^ sw), c1 = 16 * ((2 * g0 + 2 + hi) ^ sw);
-            const i32x4 a0 = *(const i32x4 *)(bs + xa + c0), a1 = *(const i32x4 *)(bs + xa + c1);
-            const i32x4 b0 = *(const i32x4 *)(bs + wa + c0), b1 = *(const i32x4 *)(bs + wa + c1);
-            const float xsa = *(const float *)(bs + xsa_o + 4 * g0);
-            const float wsb = h2f_g(*(const uint16_t *)(bs + wsb_o + 2 * g0));
+        // both pairs' operands first: the second pair's LDS reads complete under the first pair's MFMAs and fold
+        i32x4 A[4], B[4];
+        float XA[2], WB[2];
+        #pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const int c0 = 16 * ((4 * p + hi) ^ sw), c1 = 16 * ((4 * p + 2 + hi) ^ sw);
+            A[2 * p] = *(const i32x4 *)(bs + xa + c0);
+            A[2 * p + 1] = *(const i32x4 *)(bs + xa + c1);
+            B[2 * p] = *(const i32x4 *)(bs + wa + c0);
+            B[2 * p + 1] = *(const i32x4 *)(bs + wa + c1);
+            XA[p] = *(const float *)(bs + xsa_o + 8 * p);
+            WB[p] = h2f_g(*(const uint16_t *)(bs + wsb_o + 4 * p));
+        }
+        #pragma unroll
+        for (int p = 0; p < 2; p++) {
             const i32x16 z = { 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0 };
             const f32x32 zf = {};
-            const i32x16 I0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, z, 0, 0, 0);
-            const i32x16 I1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, z, 0, 0, 0);
-            const f32x32 C = __builtin_amdgcn_mfma_f32_32x32x1f32(xsa, wsb, zf, 0, 0, 0);
+            const i32x16 I0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[2 * p], B[2 * p], z, 0, 0, 0);
+            const i32x16 I1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[2 * p + 1], B[2 * p + 1], z, 0, 0, 0);
+            const f32x32 C = __builtin_amdgcn_mfma_f32_32x32x1f32(XA[p], WB[p], zf, 0, 0, 0);
             #pragma unroll
             for (int r = 0; r < 16; r++) acc[r] = acc[r] + C[r] * (float)I0[r];
             #pragma unroll
             for (int r = 0; r < 16; r++) acc[r] = acc[r] + C[16 + r] * (float)I1[r];
+            if (p == 0) __builtin_amdgcn_sched_barrier(0); // (the second pair's MFMAs after the first pair's fold)
         }
     }
     if constexpr (SW) {
