@@ -14,9 +14,9 @@ Also on the JSON line:
                     cost host time per launch, so that step is not the timed one); achieved = file-format weight
                     bytes (Q8_0: 34 bytes per 32 weights) per launch / average launch duration, against 8 TB/s. traffic: HBM bytes per launch measured by rocprofv3 FETCH_SIZE +
                     WRITE_SIZE (scaled by a copy kernel of known size), read from profiles/decode_gemv_traffic.json
-  roofline_prefill  the prefill GEMM (k_gemm_q8, the 512-row matmuls) of the same step: 2 ops per weight per row
+  roofline_prefill  the prefill GEMM (k_gemm_q8l, the 512-row matmuls) of the same step: 2 ops per weight per row
                     against 5.0 POPS dense int8, with the bound the exact per-32 float fold sets on the VALU (the
-                    w1 / w3 launches include the SwiGLU + quantize epilogue)
+                    SwiGLU + quantize after w1 / w3 is its own kernel, in kernel_ms_prefill's swiglu+quant)
   cpu_baseline      the reference's own CPU path (oracle/_ref/ref_driver, -Ofast AVX-512 VNNI) on the same GGUF file,
                     prompt and step (512-token prefill + 128 greedy decode steps), all host threads, best of 3 runs
 
@@ -198,8 +198,8 @@ def main():
                              "algorithmic_ops_per_launch": round(pre_ops / m_n),
                              "fold_bound_tops": round(FOLD_BOUND_TOPS, 1),
                              "frac_of_fold_bound": round(tops / FOLD_BOUND_TOPS, 4),
-                             "note": "the w1 / w3 launches carry the SwiGLU and its quantization in their epilogue "
-                                     "(no separate kernel): their time includes it, their ops count the matmul only"},
+                             "note": "the four matmuls' launches (qkv, wo, w1 / w3, w2); the SwiGLU and its "
+                                     "quantization after w1 / w3 run in their own kernel (swiglu+quant)"},
         "kernel_us_per_decode_token": {k: round(v[0] * 1e6 / a.gen, 2) for k, v in dec.items() if v[1]},
         "kernel_ms_prefill": {k: round(v[0] * 1e3, 3) for k, v in pre.items() if v[1]},
         "tokens_head": toks[:8],

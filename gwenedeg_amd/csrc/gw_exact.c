@@ -248,7 +248,6 @@ int gw_exact_init(char *err, size_t errlen) {
         if (rc == RQ_OK) {
             int k = gw_k_set_exact(rsq_tab, rsq_bits, (const uint64_t *)rp, (const uint8_t *)ep);
             if (!k) k = gw_v_set_exact(rsq_tab, rsq_bits, (const uint64_t *)rp, (const uint8_t *)ep);
-            if (!k) k = gw_g_set_exact(rsq_tab, rsq_bits, (const uint64_t *)rp, (const uint8_t *)ep);
             if (k) rc = gw_hip_fail(err, errlen, "hipMemcpyToSymbol (exact tables)", (hipError_t)k);
             else {
                 dev_done[dev] = 1;

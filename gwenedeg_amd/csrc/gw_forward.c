@@ -914,14 +914,11 @@ static int fw_pass(RqCtx *c, Pass *P, float *out) {
         pf_mark(c, GW_PF_NORM);
         KCHK(gw_k_rmsnorm_quant(c->x, c->xb, dim, y->ffn_norm, NULL, n, c->xq, c->xs, K, NULL, s));
         pf_mark(c, GW_PF_W13);
-        /* (SwiGLU + quantize in the prefill GEMM's epilogue where it takes this matrix; else their own kernel) */
-        int e13 = y->nw13 == 1 ? gw_k_matmul_swiglu(&y->w13[0], y->w13_il, c->xq, c->xs, K, n, c->hq, c->hs, H, s) : -1;
-        if (e13 > 0) return ctx_fail(c, RQ_ERR_STATE, "kernel launch failed: gw_k_matmul_swiglu");
-        if (e13 < 0) {
-            if ((rc = run_mm(c, y->w13, y->nw13, c->xq, c->xs, K, n, c->hb, 2 * H, 0)) != RQ_OK) return rc;
-            pf_mark(c, GW_PF_SWIGLU);
-            KCHK(gw_k_swiglu_quant(c->hb, H, y->w13_il, n, c->hq, c->hs, s));
-        }
+        /* (the SwiGLU and its quantization in their own kernel: measured faster than in the GEMM's epilogue, whose table
+         * reads wait at the end of each block) */
+        if ((rc = run_mm(c, y->w13, y->nw13, c->xq, c->xs, K, n, c->hb, 2 * H, 0)) != RQ_OK) return rc;
+        pf_mark(c, GW_PF_SWIGLU);
+        KCHK(gw_k_swiglu_quant(c->hb, H, y->w13_il, n, c->hq, c->hs, s));
         pf_mark(c, GW_PF_W2);
         if ((rc = run_mm(c, &y->w2, 1, c->hq, c->hs, H, n, c->xb, dim, 0)) != RQ_OK) return rc;
     }

@@ -195,16 +195,10 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const int8_t *__restrict__ W, c
 // instructions around the fold (which needs 4 VALU instructions per output and group: the bound of this GEMM). Loads
 // through buffer descriptors over the block's own rows: rows past M or N read as 0 (the descriptor's range), so no
 // clamped addresses and no selects; each thread's offsets are fixed and a stage moves the scalar offset only.
-// SW (GM = 64, w1 / w3 rows interleaved by 4, N % 128 == 0): the SwiGLU and its quantization in the epilogue instead
-// of the fp32 outputs: column n of the matrix is h (n % 8 < 4) or h2 of output 4 (n / 8) + n % 8 - 4; a wave's 64
-// columns are outputs f0 .. f0 + 31, one quantization group of each of its rows: v = swiglu_ref(h, h2), one value
-// per lane and row (pairs exchanged between lanes c and c + 4), the group max over the half-wave's 32 lanes, then the
-// bytes and scale as k_swiglu_quant's quant_lane32 (hq / hs rows of ldq values)
-template <int GM, bool SW>
+template <int GM>
 __global__ __launch_bounds__(256) void k_gemm_q8f(const int8_t *__restrict__ W, const uint16_t *__restrict__ WS, int N, int K,
                                                   const int8_t *__restrict__ X, const float *__restrict__ XS, int ldx, int M,
-                                                  float *__restrict__ out, int ldo, int8_t *__restrict__ hq,
-                                                  float *__restrict__ hs, int ldq) {
+                                                  float *__restrict__ out, int ldo) {
     constexpr int TJ = GM == 64 ? 2 : 1, XC = GM * 8 / 256;
     __shared__ __align__(16) int8_t xl[2][GM * GROW];
     __shared__ __align__(16) int8_t wl[2][GN * GROW];
@@ -307,49 +301,13 @@ __global__ __launch_bounds__(256) void k_gemm_q8f(const int8_t *__restrict__ W, 
         __syncthreads();
     }
     if (st < NS) compute(0); // (an odd stage count: the last stage, in buffer 0)
-    if constexpr (SW) {
-        static_assert(TJ == 2, "the SwiGLU epilogue takes a wave's 64 columns");
-        // (lane c of a half-wave: an h lane (c % 8 < 4) takes the pair of column tile 0 (h2 from lane c + 4), an h2 lane
-        // the pair of tile 1 (h from lane c - 4): 16 values per lane, each of the 32 lanes one output of the group)
-        const int c = lane & 31, f0 = (n0 + wn) >> 1;
-        const bool hlane = (c & 7) < 4;
-        const int f = f0 + (hlane ? 0 : 16) + 4 * (c >> 3) + (c & 3);
-        float hv[16], h2v[16];
-        #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const float a = __shfl_down(acc[0][r], 4), b = __shfl_up(acc[1][r], 4);
-            hv[r] = hlane ? acc[0][r] : b;
-            h2v[r] = hlane ? a : acc[1][r];
-        }
-        swiglu_ref_n<16>(hv, h2v); // (the table reads of all 16 in flight together)
+    #pragma unroll
+    for (int j = 0; j < TJ; j++) {
+        const int n = n0 + wn + 32 * j + (lane & 31);
         #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int m = m0 + wm + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            float wmax = fabsf(hv[r]);
-            #pragma unroll
-            for (int o = 16; o >= 1; o >>= 1) {
-                const float tt = __shfl_xor(wmax, o);
-                wmax = tt > wmax ? tt : wmax;
-            }
-            if (m < M) {
-                if (c == 0) hs[(size_t)m * (ldq >> 5) + (f0 >> 5)] = wmax * (1.0f / 127.0f);
-                int32_t qi = 0;
-                if (wmax > 0.0f) {
-                    const float inv = 127.0f / wmax, x = hv[r] * inv;
-                    qi = (int32_t)(x + copysignf(0.49999997f, x));
-                }
-                hq[(size_t)m * ldq + f] = (int8_t)qi;
-            }
-        }
-    } else {
-        #pragma unroll
-        for (int j = 0; j < TJ; j++) {
-            const int n = n0 + wn + 32 * j + (lane & 31);
-            #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int m = m0 + wm + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < M && n < N) out[(size_t)m * ldo + n] = acc[j][r];
-            }
+            if (m < M && n < N) out[(size_t)m * ldo + n] = acc[j][r];
         }
     }
 }
@@ -367,10 +325,10 @@ __global__ __launch_bounds__(256) void k_gemm_q8f(const int8_t *__restrict__ W, 
 // row per lane). Per pair of groups the fold of k_gemm_q8f: two int8 MFMAs for the exact sums, the outer-product MFMA
 // of the scale products, then val = val + (ws xs) (float) isum per output in group order (forward.c:906-916). Blocks:
 // XCD b % 8 takes column tiles 8 q + b % 8 with their row tiles in a row (the W tile read once into that XCD's L2).
-// mode 0 (out = val), K % 128 == 0; rows past M / N read as 0 (the descriptors' ranges) and are not stored.
-// SW (w1 / w3 rows interleaved by 4, N % 128 == 0): the SwiGLU and its quantization in the epilogue instead of the
-// fp32 outputs (k_gemm_q8f's, with a wave's 32 columns = 16 outputs, half a quantization group: the row maxima of the
-// two halves exchanged through LDS between the waves of columns 32 h and 32 h + 32, waves w and w ^ 1)
+// mode 0 (out = val), K % 128 == 0; rows past M / N read as 0 (the descriptors' ranges) and are not stored. (The w1 / w3
+// SwiGLU with its quantization in this kernel's epilogue, the row maxima of a quantization group's two halves exchanged
+// between waves in LDS, was measured against its own kernel after the GEMM: 8B prefill 22.7 k against 23.2 k tok/s,
+// the epilogue's table reads waiting at the end of each block)
 #define LQ_S 3
 #define LQ_X 0
 #define LQ_W 8192
@@ -396,14 +354,12 @@ __device__ __forceinline__ void lq_copy(__amdgpu_buffer_rsrc_t r, uint8_t *lds, 
     if (bytes == 16) __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LQ_AS3 void *)lds, 16, voff, 0, 0, 0);
     else __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LQ_AS3 void *)lds, 4, voff, 0, 0, 0);
 }
-template <int TN, bool SW>
+template <int TN>
 __global__ __launch_bounds__(TN * 4, TN == 128 ? 2 : 3) void k_gemm_q8l(const int8_t *__restrict__ W,
                                                                        const uint16_t *__restrict__ WS, int N, int K,
                                                                        const int8_t *__restrict__ X,
                                                                        const float *__restrict__ XS, int ldx, int M,
-                                                                       float *__restrict__ out, int ldo, int MT,
-                                                                       int8_t *__restrict__ hq, float *__restrict__ hs,
-                                                                       int ldq) {
+                                                                       float *__restrict__ out, int ldo, int MT) {
     constexpr int NC = TN / 32, NW = 2 * NC, XP = 8 / NW; // (waves per row of tiles, waves, X pieces per wave)
     __shared__ __align__(16) uint8_t sl[LQ_S * LQ_STAGE(TN)];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, hi = lane >> 5, r32 = lane & 31;
@@ -481,60 +437,11 @@ __global__ __launch_bounds__(TN * 4, TN == 128 ? 2 : 3) void k_gemm_q8l(const in
             if (p == 0) __builtin_amdgcn_sched_barrier(0); // (the second pair's MFMAs after the first pair's fold)
         }
     }
-    if constexpr (SW) {
-        // lane c of a half-wave: column wn + c, an h column where c % 8 < 4 (output 4 (c / 8) + c % 8 of the wave's 16),
-        // else the h2 of output 4 (c / 8) + c % 8 - 4; the h lane takes registers 0 .. 7 (rows 8 (i / 4) + 4 hi + i % 4),
-        // the h2 lane registers 8 .. 15 (rows 16 + ...), each with its partner's value (lanes c and c + 4)
-        __shared__ float pm[NW][32]; // [wave][row of its tile]: the row's max |v| over the wave's 16 outputs
-        const bool hl = (r32 & 7) < 4;
-        float hv[8], h2v[8];
-        #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float dn = __shfl_down(acc[i], 4), up = __shfl_up(acc[8 + i], 4);
-            hv[i] = hl ? acc[i] : up;
-            h2v[i] = hl ? dn : acc[8 + i];
-        }
-        swiglu_ref_n<8>(hv, h2v); // (the table reads of all 8 in flight together)
-        float am[8];
-        #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            float v = fabsf(hv[i]);
-            #pragma unroll
-            for (int o = 1; o <= 16; o <<= 1) { // (xor 1, 2, 8, 16: the 16 lanes of this kind; xor 4 is the partner)
-                if (o == 4) continue;
-                const float tt = __shfl_xor(v, o);
-                v = tt > v ? tt : v;
-            }
-            am[i] = v;
-        }
-        const int rb = (hl ? 0 : 16) + 4 * hi; // (row of register i: rb + 8 (i / 4) + i % 4)
-        if ((r32 & 0x1b) == 0) {
-            #pragma unroll
-            for (int i = 0; i < 8; i++) pm[wave][rb + 8 * (i >> 2) + (i & 3)] = am[i];
-        }
-        __syncthreads();
-        const int f = ((n0 + wn) >> 1) + 4 * (r32 >> 3) + (r32 & 3), grp = (n0 + wn) >> 6; // (waves w, w ^ 1: one group)
-        #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int rr = rb + 8 * (i >> 2) + (i & 3), m = m0 + wm + rr;
-            const float po = pm[wave ^ 1][rr], wmax = po > am[i] ? po : am[i];
-            if (m < M) {
-                if ((wave & 1) == 0 && (r32 & 0x1b) == 0) hs[(size_t)m * (ldq >> 5) + grp] = wmax * (1.0f / 127.0f);
-                int32_t qi = 0;
-                if (wmax > 0.0f) {
-                    const float inv = 127.0f / wmax, x = hv[i] * inv;
-                    qi = (int32_t)(x + copysignf(0.49999997f, x));
-                }
-                hq[(size_t)m * ldq + f] = (int8_t)qi;
-            }
-        }
-    } else {
-        const int n = n0 + wn + r32;
-        #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int m = m0 + wm + 8 * (r >> 2) + 4 * hi + (r & 3);
-            if (m < M && n < N) out[(size_t)m * ldo + n] = acc[r];
-        }
+    const int n = n0 + wn + r32;
+    #pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int m = m0 + wm + 8 * (r >> 2) + 4 * hi + (r & 3);
+        if (m < M && n < N) out[(size_t)m * ldo + n] = acc[r];
     }
 }
 
@@ -2029,11 +1936,9 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
 #define GQ_ARGS (const int8_t *)w->codes, (const uint16_t *)w->scales, w->rows, w->cols, xq, xs, ldx, M, out, ldo
         const int mt = (M + 63) / 64, lq0 = full ? q8l_width(w->rows, M) : 0, lq = lq0 >= 16 && w->cols % 256 ? 17 : lq0;
         if (lq == 128)
-            hipExtLaunchKernelGGL((k_gemm_q8l<128, false>), dim3(((nt + 7) / 8) * 8 * mt), dim3(512), 0, s, e0, e1, 0, GQ_ARGS,
-                                  mt, (int8_t *)NULL, (float *)NULL, 0);
+            hipExtLaunchKernelGGL(k_gemm_q8l<128>, dim3(((nt + 7) / 8) * 8 * mt), dim3(512), 0, s, e0, e1, 0, GQ_ARGS, mt);
         else if (lq == 64)
-            hipExtLaunchKernelGGL((k_gemm_q8l<64, false>), dim3(((w->rows + 511) / 512) * 8 * mt), dim3(256), 0, s, e0, e1, 0,
-                                  GQ_ARGS, mt, (int8_t *)NULL, (float *)NULL, 0);
+            hipExtLaunchKernelGGL(k_gemm_q8l<64>, dim3(((w->rows + 511) / 512) * 8 * mt), dim3(256), 0, s, e0, e1, 0, GQ_ARGS, mt);
         else if (lq == 16) // (64 x 64 tiles, stages of 256 bytes of K)
             hipExtLaunchKernelGGL((k_gemm_q8t<64, 64, 3, 2>), dim3(((w->rows + 511) / 512) * 8 * mt), dim3(1024), 0, s, e0, e1, 0, GQ_ARGS, mt);
         else if (lq == 17) // (stages of 128)
@@ -2044,8 +1949,8 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
         else if (lq == 19) // (32 x 16 tiles)
             hipExtLaunchKernelGGL((k_gemm_q8t<32, 16, 4, 2>), dim3(((w->rows + 127) / 128) * 8 * ((M + 31) / 32)), dim3(128), 0, s, e0, e1, 0,
                                   GQ_ARGS, (M + 31) / 32);
-        else if (full && g64) hipExtLaunchKernelGGL((k_gemm_q8f<64, false>), g64g, dim3(256), 0, s, e0, e1, 0, GQ_ARGS, (int8_t *)NULL, (float *)NULL, 0);
-        else if (full) hipExtLaunchKernelGGL((k_gemm_q8f<32, false>), g32g, dim3(256), 0, s, e0, e1, 0, GQ_ARGS, (int8_t *)NULL, (float *)NULL, 0);
+        else if (full && g64) hipExtLaunchKernelGGL(k_gemm_q8f<64>, g64g, dim3(256), 0, s, e0, e1, 0, GQ_ARGS);
+        else if (full) hipExtLaunchKernelGGL(k_gemm_q8f<32>, g32g, dim3(256), 0, s, e0, e1, 0, GQ_ARGS);
         else if (g64) hipExtLaunchKernelGGL((k_gemm_q8<64>), g64g, dim3(256), 0, s, e0, e1, 0, GQ_ARGS);
         else hipExtLaunchKernelGGL((k_gemm_q8<32>), g32g, dim3(256), 0, s, e0, e1, 0, GQ_ARGS);
 #undef GQ_ARGS
@@ -2134,33 +2039,6 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
     return (int)hipErrorInvalidValue;
 }
 
-int gw_k_matmul_swiglu(const GwMat *w, int il, const int8_t *xq, const float *xs, int ldx, int M, int8_t *hq, float *hs, int ldq,
-                       hipStream_t s) {
-    // the w1 / w3 matmul (rows interleaved by il = 4) with the SwiGLU and its quantization in the GEMM's epilogue, where
-    // the prefill GEMM takes 64-row tiles of full stages; -1 (nothing launched): not this case
-    const int nt = (w->rows + GN - 1) / GN;
-    if (w->type != GW_Q8_0 || il != 4 || M <= GW_GEMV_MAX_ROWS || w->rows % GN || ldq != w->rows / 2 || ldq % 32) return -1;
-    const int mt = (M + 63) / 64;
-    const bool g64 = g_tile_rows ? g_tile_rows == 64 : (size_t)nt * mt >= (size_t)4 * gemm_cus();
-    const int lq = q8l_width(w->rows, M) >= 16 && q8l_width(w->rows, M) < 64 ? 64 : q8l_width(w->rows, M); // (no SwiGLU epilogue in k_gemm_q8t)
-    const bool full = w->cols % GKB == 0 && (size_t)(M + 64) * ldx < ((size_t)1 << 31) && (size_t)GN * w->cols < ((size_t)1 << 31);
-    if (!(lq || g64) || !full) return -1;
-    hipEvent_t e0, e1;
-    gw_take_launch_events(&e0, &e1);
-    if (lq == 128)
-        hipExtLaunchKernelGGL((k_gemm_q8l<128, true>), dim3(((nt + 7) / 8) * 8 * mt), dim3(512), 0, s, e0, e1, 0,
-                              (const int8_t *)w->codes, (const uint16_t *)w->scales, w->rows, w->cols, xq, xs, ldx, M,
-                              (float *)NULL, 0, mt, hq, hs, ldq);
-    else if (lq == 64)
-        hipExtLaunchKernelGGL((k_gemm_q8l<64, true>), dim3(((w->rows + 511) / 512) * 8 * mt), dim3(256), 0, s, e0, e1, 0,
-                              (const int8_t *)w->codes, (const uint16_t *)w->scales, w->rows, w->cols, xq, xs, ldx, M,
-                              (float *)NULL, 0, mt, hq, hs, ldq);
-    else
-        hipExtLaunchKernelGGL((k_gemm_q8f<64, true>), dim3(nt, mt), dim3(256), 0, s, e0, e1, 0, (const int8_t *)w->codes,
-                              (const uint16_t *)w->scales, w->rows, w->cols, xq, xs, ldx, M, (float *)NULL, 0, hq, hs, ldq);
-    return (int)hipGetLastError();
-}
-
 int gw_g_set_iq(const uint64_t *iq2xxs, const uint64_t *iq2xs, const uint64_t *iq2s, const uint64_t *iq1s,
                 const uint32_t *iq3xxs, const uint32_t *iq3s) {
     /* the i-quant codebooks (gw_iq.h) on the current device: the 8-value grids as uint64, IQ1's as its two tables
@@ -2171,16 +2049,6 @@ int gw_g_set_iq(const uint64_t *iq2xxs, const uint64_t *iq2xs, const uint64_t *i
     if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(gw_iq1s_g), iq1s, sizeof(uint64_t) * 2 * 2048);
     if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(gw_iq3xxs_g), iq3xxs, sizeof(uint32_t) * 256);
     if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(gw_iq3s_g), iq3s, sizeof(uint32_t) * 512);
-    return (int)e;
-}
-
-int gw_g_set_exact(const float *rsq, int bits, const uint64_t *rcp, const uint8_t *expd) {
-    /* this file's copy of the SwiGLU tables (swiglu_ref in the SwiGLU epilogue) on the current device; no kernel here
-     * takes rsqrt_ref (its table is not in this file's code object) */
-    (void)rsq;
-    (void)bits;
-    hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(gw_rcp_blk), &rcp, sizeof(rcp));
-    if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(gw_exp_delta), &expd, sizeof(expd));
     return (int)e;
 }
 

@@ -344,7 +344,6 @@ float gw_rsqrt_host(float t);   /* the reference's 1.0f / sqrtf(t) on this host 
 float gw_exp_mvec(float x);     /* libmvec's expf by its method: the device's exp_mvec */
 int gw_k_set_exact(const float *rsq, int bits, const uint64_t *rcp, const uint8_t *expd); /* gw_kernels.hip's copy */
 int gw_v_set_exact(const float *rsq, int bits, const uint64_t *rcp, const uint8_t *expd); /* gw_gemv.hip's copy */
-int gw_g_set_exact(const float *rsq, int bits, const uint64_t *rcp, const uint8_t *expd); /* gw_gemm.hip's copy */
 /* the i-quant codebooks on the current device (gw_gemm.hip's kernels); gw_iq_init: expanded from gw_iq_tables.h once
  * per process, installed once per device (the current one) */
 int gw_g_set_iq(const uint64_t *iq2xxs, const uint64_t *iq2xs, const uint64_t *iq2s, const uint64_t *iq1s,
@@ -434,10 +433,6 @@ void gw_time_next_launch(hipEvent_t a, hipEvent_t b);
 void gw_take_launch_events(hipEvent_t *a, hipEvent_t *b);
 
 /* the matmul dispatch (gw_gemm.hip): out[m * ldo + row] (+)= W row . X row m for M rows, any supported type */
-/* w1 / w3 (rows interleaved by il) with SwiGLU and quantize into hq / hs (rows of ldq = rows / 2) fused into the prefill
- * GEMM's epilogue; -1 when this matrix / row count does not take that path (nothing launched) */
-int gw_k_matmul_swiglu(const GwMat *w, int il, const int8_t *xq, const float *xs, int ldx, int M, int8_t *hq, float *hs, int ldq,
-                       hipStream_t s);
 int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int M, float *out, int ldo, int mode,
                 hipStream_t s);
 /* a and b (out from column col_b) in one launch where the kernel allows (two K-quant matrices of one type and width,
