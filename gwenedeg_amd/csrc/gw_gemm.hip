@@ -377,8 +377,8 @@ __global__ __launch_bounds__(TN * 4, TN == 128 ? 2 : 3) void k_gemm_q8l(const in
     const int pr = lane >> 3, pce = (lane & 7) ^ (pr >> 1), pco = (lane & 7) ^ (4 + (pr >> 1));
     const int xo = (8 * XP * wave + pr) * ldx, wo = (16 * wave + pr) * K + 16 * pce, wo1 = (16 * wave + 8 + pr) * K + 16 * pco;
     const int so = wave == 0 ? lane * gx * 4 : ((32 * (wave - 1) + (lane >> 1)) * G + 2 * (lane & 1)) * 2;
-    auto issue = [&](int st) __attribute__((always_inline)) {
-        uint8_t *bs = sl + (st % LQ_S) * LQ_STAGE(TN);
+    auto issue = [&](int st, int slot) __attribute__((always_inline)) { // (slot: st % LQ_S)
+        uint8_t *bs = sl + slot * LQ_STAGE(TN);
         const int k0 = st * 128;
         #pragma unroll
         for (int p = 0; p < XP; p++) // (piece XP wave + p: odd where XP == 1 and the wave is odd, or p is)
@@ -394,8 +394,16 @@ __global__ __launch_bounds__(TN * 4, TN == 128 ? 2 : 3) void k_gemm_q8l(const in
     for (int r = 0; r < 16; r++) acc[r] = 0.0f;
     const int xa = LQ_X + (wm + r32) * 128, wa = LQ_W + (wn + r32) * 128, sw = (r32 >> 1) & 7;
     const int xsa_o = LQ_XS(TN) + (wm + r32) * 16 + 4 * hi, wsb_o = LQ_WS(TN) + (wn + r32) * 8 + 2 * hi;
-    issue(0);
-    if (NS > 1) issue(1);
+    // the operands' offsets in a stage (the same every stage): group 2 p + u's 16 bytes of this lane, chunk 4 p + 2 u + hi
+    int oa[4], ob[4];
+    #pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int c = 16 * ((2 * q + hi) ^ sw);
+        oa[q] = xa + c;
+        ob[q] = wa + c;
+    }
+    issue(0, 0);
+    if (NS > 1) issue(1, 1);
     for (int st = 0; st < NS; st++) {
         // stage st landed (this wave's copies: only stage st + 1's XP + 3 or XP + 2 outstanding), then every wave's
         if (st + 1 < NS) {
@@ -408,18 +416,17 @@ __global__ __launch_bounds__(TN * 4, TN == 128 ? 2 : 3) void k_gemm_q8l(const in
             }
         } else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        if (st + 2 < NS) issue(st + 2); // (into the slot of stage st - 1, whose readers are past the barrier)
+        if (st + 2 < NS) issue(st + 2, (st + 2) % LQ_S); // (into the slot of stage st - 1, whose readers are past the barrier)
         const uint8_t *bs = sl + (st % LQ_S) * LQ_STAGE(TN);
         // both pairs' operands first: the second pair's LDS reads complete under the first pair's MFMAs and fold
         i32x4 A[4], B[4];
         float XA[2], WB[2];
         #pragma unroll
         for (int p = 0; p < 2; p++) {
-            const int c0 = 16 * ((4 * p + hi) ^ sw), c1 = 16 * ((4 * p + 2 + hi) ^ sw);
-            A[2 * p] = *(const i32x4 *)(bs + xa + c0);
-            A[2 * p + 1] = *(const i32x4 *)(bs + xa + c1);
-            B[2 * p] = *(const i32x4 *)(bs + wa + c0);
-            B[2 * p + 1] = *(const i32x4 *)(bs + wa + c1);
+            A[2 * p] = *(const i32x4 *)(bs + oa[2 * p]);
+            A[2 * p + 1] = *(const i32x4 *)(bs + oa[2 * p + 1]);
+            B[2 * p] = *(const i32x4 *)(bs + ob[2 * p]);
+            B[2 * p + 1] = *(const i32x4 *)(bs + ob[2 * p + 1]);
             XA[p] = *(const float *)(bs + xsa_o + 8 * p);
             WB[p] = h2f_g(*(const uint16_t *)(bs + wsb_o + 4 * p));
         }
