@@ -94,6 +94,12 @@ __device__ __forceinline__ float gv_fold(const float *p, int G) {
 #ifndef GV_WNT
 #define GV_WNT 2
 #endif
+// register sets of weight tiles per block (D - 1 tiles in flight): 3, and 4 behind the attention combine (wo: 4 tiles
+// of 4 rows per block, so three of them load during the prologue). Measured on the 8B decode step, µs per token:
+// D = 4 everywhere: wo 345 -> 304, qkv 324 -> 338, w1/w3 773 -> 804, w2 481 -> 511; D = 5 slower everywhere; wo alone
+// at 4: 345 -> 301, at 5: 331
+#define GV_DEPTH 3
+#define GV_DEPTH_COMBINE 4
 template <int R>
 __device__ __forceinline__ void gv_load_rows(__amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t rs, int cb, int cl, int sb, int sl,
                                              int j, int K, int G, int4 (&wv)[R], uint32_t (&ws)[R]) {
@@ -116,6 +122,40 @@ __device__ __forceinline__ void gv_load_tile(__amdgpu_buffer_rsrc_t rw, __amdgpu
                                              int K, int G, int4 (&wv)[R], uint32_t (&ws)[R]) {
     const int last = nrows - 1 - tile * R; // (the tile's rows past the matrix's last row load that row)
     gv_load_rows<R>(rw, rs, tile * R * K, last * K, tile * R * G * 2, last * G * 2, j, K, G, wv, ws);
+}
+
+// the rmsnorm's chains: their float4 count n4 = K / 64 rounded up to NF (16, 32 or 64), chain j's float4s
+// at row4 + j (NF + 1) in LDS, zeros past n4
+__host__ __device__ __forceinline__ int gv_nf(int n4) {
+    return n4 <= 16 ? 16 : n4 <= 32 ? 32 : 64; // (the rmsnorm prologue takes K <= 4096)
+}
+
+// the rmsnorm's sum of squares over one chain (forward.c:886-901): ss = fma(v, v, ss) over its NF float4s in order,
+// straight-line: a ring of 8 float4 reads at immediate offsets, each register's next read issued right after its four
+// fmas, so a read has the other seven registers' 28 fmas to land. The reads and their waits are inline asm, in the order
+// written (the compiler otherwise issued a chain's reads ahead of its fmas); each wait names its register, so that
+// register's fmas come after it. The zeros past the chain's end change no bit: fma(0, 0, ss) == ss for every ss >= 0.
+// (Measured per chain of 64 float4s on one wave: 1.9 us for two sets of 16 reads taking turns, 1.1 us for this ring,
+// 0.7 us for the fmas alone)
+typedef float gv_f4 __attribute__((ext_vector_type(4)));
+template <int NF>
+__device__ __forceinline__ float gv_chain(const float4 *c) {
+    const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)c;
+    float ss = 0.0f;
+    gv_f4 q[8];
+    #pragma unroll
+    for (int u = 0; u < 8; u++) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(q[u]) : "v"(base), "i"(16 * u));
+    #pragma unroll
+    for (int i = 0; i < NF; i++) {
+        // (reads issued after read i: i + 1 .. min(i + 7, NF - 1))
+        const int later = NF - 1 - i < 7 ? NF - 1 - i : 7;
+        asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(q[i & 7]) : "i"(later));
+        const gv_f4 v = q[i & 7];
+        asm volatile("v_fmac_f32 %0, %1, %1\n\tv_fmac_f32 %0, %2, %2\n\tv_fmac_f32 %0, %3, %3\n\tv_fmac_f32 %0, %4, %4"
+                     : "+v"(ss) : "v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w));
+        if (i + 8 < NF) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(q[i & 7]) : "v"(base), "i"(16 * (i + 8)));
+    }
+    return ss;
 }
 
 // the group of 32 (this lane's 16 values and its pair's): wmax, s = wmax / 127, q = trunc(v * inv + copysign(.49999997))
@@ -188,6 +228,9 @@ __global__ __launch_bounds__(NT) void k_gemv1(GvArgs a) {
     const int odd = (j >> 1) & 1; // (the half of the scale's word)
     int4 wv[D][R];
     uint32_t ws[D][R];
+    // the combine's partials arrive before the weight loads are issued: its 40 small loads per thread otherwise queue
+    // behind the tiles (wo 301 -> 292 us per token); the rmsnorm's row does not gain from it (its row arrives no sooner)
+    if (PRO == GV_COMBINE) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     #pragma unroll
     for (int d = 0; d + 1 < D; d++) {
         const int td = tile + d * (int)gridDim.x;
@@ -205,9 +248,9 @@ __global__ __launch_bounds__(NT) void k_gemv1(GvArgs a) {
                 v[4 * u + 3] = p0[u].w;
             }
         } else if (PRO == GV_NORM) {
-            // the row transposed: value e at xt[(e % 16) LS + e / 16] (LS = K / 16 + 4: chain j's values contiguous,
-            // the 16 chains 4 banks apart)
-            const int LS = (K >> 4) + 4;
+            // the row transposed: value e at xf[(e % 16) LS + e / 16], LS = 4 NF + 4 (chain j's values contiguous, the
+            // 16 chains 4 banks apart), zeros from e / 16 = K / 16 to 4 NF; the scale after the 16 chains
+            const int n4 = K >> 6, NF = gv_nf(n4), LS = 4 * NF + 4;
             if (act) {
                 #pragma unroll
                 for (int u = 0; u < 4; u++) {
@@ -217,51 +260,24 @@ __global__ __launch_bounds__(NT) void k_gemv1(GvArgs a) {
                     xf[(4 * u + 3) * LS + t] = p0[u].w;
                 }
             }
+            if (NF > n4)
+                for (int z = t; z < 16 * (NF - n4); z += (int)blockDim.x)
+                    ((float4 *)xf)[(z / (NF - n4)) * (NF + 1) + n4 + z % (NF - n4)] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             __syncthreads();
             if (t < 64) {
                 float ss = 0.0f;
                 if (t < 16) {
-                    // the chain over the row's K / 16 values of lane t (K % 64 == 0): two sets of QS float4 LDS reads
-                    // take turns (a copy from one set into the other would wait for its reads)
-                    constexpr int QS = NT <= 256 ? 16 : 4; // (768 threads: 168 registers)
-                    const float4 *c = (const float4 *)(xf + t * LS);
-                    const int n4 = K >> 6; // the chain's float4s
-                    auto fma4 = [&](const float4 (&q)[QS], int m) {
-                        #pragma unroll
-                        for (int u = 0; u < QS; u++)
-                            if (u < m) {
-                                ss = __builtin_fmaf(q[u].x, q[u].x, ss);
-                                ss = __builtin_fmaf(q[u].y, q[u].y, ss);
-                                ss = __builtin_fmaf(q[u].z, q[u].z, ss);
-                                ss = __builtin_fmaf(q[u].w, q[u].w, ss);
-                            }
-                    };
-                    auto ld4 = [&](float4 (&q)[QS], int i0) {
-                        #pragma unroll
-                        for (int u = 0; u < QS; u++) q[u] = c[i0 + u < n4 ? i0 + u : 0];
-                    };
-                    float4 qa[QS], qb[QS];
-                    int i = 0;
-                    ld4(qa, 0);
-                    for (; i + 2 * QS <= n4; i += 2 * QS) {
-                        ld4(qb, i + QS);
-                        fma4(qa, QS);
-                        ld4(qa, i + 2 * QS);
-                        fma4(qb, QS);
-                    }
-                    // (qa holds i .. i + QS - 1)
-                    if (i + QS <= n4) {
-                        ld4(qb, i + QS);
-                        fma4(qa, QS);
-                        fma4(qb, n4 - i - QS);
-                    } else {
-                        fma4(qa, n4 - i);
-                    }
+                    const float4 *c = (const float4 *)xf + t * (NF + 1);
+                    if (NF == 16) ss = gv_chain<16>(c);
+                    else if (NF == 32) ss = gv_chain<32>(c);
+                    else ss = gv_chain<64>(c); // (K <= 4096)
                 }
-                for (int w = 8; w >= 1; w >>= 1) {
-                    float o = __shfl_down(ss, w);
-                    ss = ss + o;
-                }
+                // the tree over the 16 chains, as ss + shfl_down(ss, w) for w = 8, 4, 2, 1: lane 0's value from lanes
+                // 0-15 by DPP row shifts (row_shl:w, lane j + w of the same 16-lane row), no LDS round trips
+                ss = ss + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ss), 0x108, 0xF, 0xF, true));
+                ss = ss + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ss), 0x104, 0xF, 0xF, true));
+                ss = ss + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ss), 0x102, 0xF, 0xF, true));
+                ss = ss + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ss), 0x101, 0xF, 0xF, true));
                 if (t == 0) xf[16 * LS] = rsqrt_ref(__builtin_fmaf(ss, a.inv_k, 1e-6f));
             }
             __syncthreads();
@@ -409,21 +425,24 @@ static int gv_launch(int pro, int R, const GvArgs &a, const GwMat *nx, int nR, h
         b.n_tb = nR * nx->cols, b.n_tsb = nR * (nx->cols / 32) * 2;
         b.n_tiles = nx->rows / nR, b.n_grid = nnt < gv_nwg ? nnt : gv_nwg;
     }
-    size_t lds = (size_t)b.cmax * slot_bytes + (pro == GV_NORM ? (size_t)(16 * (a.K / 16 + 4) + 4) * sizeof(float) : 0);
+    size_t lds = (size_t)b.cmax * slot_bytes + (pro == GV_NORM ? (size_t)(16 * (4 * gv_nf(a.K / 64) + 4) + 4) * sizeof(float) : 0);
     dim3 grid(nwg);
     hipEvent_t e0, e1;
     gw_take_launch_events(&e0, &e1);
-#define GV_L(RR, PP, NN) hipExtLaunchKernelGGL((k_gemv1<RR, PP, NN, 3>), grid, dim3(nt), (uint32_t)lds, s, e0, e1, 0, b)
+#define GV_L(RR, PP, NN)                                                                                               \
+    hipExtLaunchKernelGGL((k_gemv1<RR, PP, NN, PP == GV_COMBINE ? GV_DEPTH_COMBINE : GV_DEPTH>), grid, dim3(nt),          \
+                          (uint32_t)lds, s, e0, e1, 0, b)
 #define GV_R(PP)                                                                                                        \
     if (nt <= 256) {                                                                                                    \
         if (R == 2) GV_L(2, PP, 256);                                                                                   \
         else if (R == 4) GV_L(4, PP, 256);                                                                              \
         else if (R == 8) GV_L(8, PP, 256);                                                                              \
         else GV_L(16, PP, 256);                                                                                         \
-    } else {                                                                                                            \
-        if (R == 2) GV_L(2, PP, 768);                                                                                   \
-        else if (R == 4 || PP == GV_NORM) GV_L(4, PP, 768); /* (R = 8 with the norm's registers would spill) */         \
-        else GV_L(8, PP, 768);                                                                                          \
+    } else { /* (the rmsnorm prologue only with K <= 4096, 256 threads: gw_k_gemv1_norm) */                            \
+        constexpr int NTW = PP == GV_NORM ? 256 : 768;                                                                  \
+        if (R == 2) GV_L(2, PP, NTW);                                                                                   \
+        else if (R == 4) GV_L(4, PP, NTW);                                                                              \
+        else GV_L(8, PP, NTW);                                                                                          \
     }
     switch (pro) {
     case GV_Q: GV_R(GV_Q); break;
@@ -468,7 +487,7 @@ int gw_k_gemv1_q(const GwMat *w, int R, const int8_t *xq, const float *xs, float
 
 int gw_k_gemv1_norm(const GwMat *w, int R, const float *x, const float *nw, float *out, int mode, int swiglu_il,
                     const GwMat *nx, int nR, hipStream_t s) {
-    if (gv_check(w, R) || (R == 8 && w->cols > 4096) || (swiglu_il && (swiglu_il != 4 || R != 8 || w->rows % 8)))
+    if (gv_check(w, R) || w->cols > 4096 || (swiglu_il && (swiglu_il != 4 || R != 8 || w->rows % 8)))
         return (int)hipErrorInvalidValue;
     GvArgs a = {};
     a.W = w->codes, a.WS = w->scales, a.nrows = w->rows, a.K = w->cols, a.x = x, a.nw = nw, a.out = out, a.mode = mode;
