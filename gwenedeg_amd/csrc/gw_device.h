@@ -198,6 +198,65 @@ __device__ __forceinline__ float quad_lane(float x) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), Q * 0x55, 0xF, 0xF, false));
 }
 
+// The rmsnorm's 16 sum-of-squares chains (forward.c:886-901: chain j an fma chain over x[j], x[j + 16], ..., then the
+// tree +8 +4 +2 +1) from the chains' LDS layout: value e of the row at [(e % 16) (4 NF + 4) + e / 16] (chain j's values
+// contiguous, the 16 chains 4 banks apart), NF = rms_nf(n / 64) float4s per chain, zeros from n / 16 to 4 NF.
+__host__ __device__ __forceinline__ int rms_nf(int n4) {
+    return n4 <= 16 ? 16 : n4 <= 32 ? 32 : n4 <= 64 ? 64 : n4 <= 128 ? 128 : 256;
+}
+
+// one chain: ss = fma(v, v, ss) over its NF float4s in order, straight-line: a ring of 8 float4 reads at immediate
+// offsets, each register's next read issued right after its four fmas, so a read has the other seven registers' 28 fmas
+// to land. The reads, their waits and the fmas are inline asm in the order written (the compiler otherwise issued a
+// chain's reads ahead of its fmas, even volatile ones); each wait names its register, so that register's fmas come
+// after it. The zeros past the chain's end change no bit: fma(0, 0, ss) == ss for every ss >= 0. (Measured per chain
+// of 64 float4s on one wave: 1.9 us for two sets of 16 reads taking turns, 1.1 us for this ring, 0.7 us for the fmas
+// alone)
+typedef float rms_f4 __attribute__((ext_vector_type(4)));
+template <int NF>
+__device__ __forceinline__ float rms_chain(const float4 *c) {
+    const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)c;
+    float ss = 0.0f;
+    rms_f4 q[8];
+    #pragma unroll
+    for (int u = 0; u < 8; u++) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(q[u]) : "v"(base), "i"(16 * u));
+    #pragma unroll
+    for (int i = 0; i < NF; i++) {
+        // (reads issued after read i: i + 1 .. min(i + 7, NF - 1))
+        const int later = NF - 1 - i < 7 ? NF - 1 - i : 7;
+        asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(q[i & 7]) : "i"(later));
+        const rms_f4 v = q[i & 7];
+        asm volatile("v_fmac_f32 %0, %1, %1\n\tv_fmac_f32 %0, %2, %2\n\tv_fmac_f32 %0, %3, %3\n\tv_fmac_f32 %0, %4, %4"
+                     : "+v"(ss) : "v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w));
+        if (i + 8 < NF) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(q[i & 7]) : "v"(base), "i"(16 * (i + 8)));
+    }
+    return ss;
+}
+
+// the rmsnorm scale of a row of n floats (n % 64 == 0) in the chains' layout, by lanes 0..15 of the calling wave (all
+// 64 lanes active), returned to every lane: the 16 chains, the tree by DPP row shifts (row_shl:w, lane j + w of the
+// same 16-lane row: lane 0's value is that of ss + shfl_down(ss, w) for w = 8, 4, 2, 1), t = fma(ss, 1/n, 1e-6),
+// rsqrt_ref(t)
+__device__ __forceinline__ float rms_scale_t(const float *lds, int n) {
+    const int lane = threadIdx.x & 63, NF = rms_nf(n >> 6);
+    float ss = 0.0f;
+    if (lane < 16) {
+        const float4 *c = (const float4 *)lds + lane * (NF + 1);
+        if (NF == 16) ss = rms_chain<16>(c);
+        else if (NF == 32) ss = rms_chain<32>(c);
+        else if (NF == 64) ss = rms_chain<64>(c);
+        else if (NF == 128) ss = rms_chain<128>(c);
+        else ss = rms_chain<256>(c);
+    }
+    ss = ss + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ss), 0x108, 0xF, 0xF, true));
+    ss = ss + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ss), 0x104, 0xF, 0xF, true));
+    ss = ss + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ss), 0x102, 0xF, 0xF, true));
+    ss = ss + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ss), 0x101, 0xF, 0xF, true));
+    float r = 0.0f;
+    if (lane == 0) r = rsqrt_ref(__builtin_fmaf(ss, 1.0f / (float)n, 1e-6f));
+    return __shfl(r, 0);
+}
+
 // rmsnorm scale of n floats in LDS (n % 128 == 0), computed by lanes 0..15 of the calling wave, returned to all lanes
 // of that wave: forward.c:886-901 in the reference's compiled order (lane j: an fma chain over x[j], x[j + 16], ...,
 // the tree +8 +4 +2 +1, t = fma(ss, 1/n, 1e-6), rsqrt_ref(t)); n % 16 == 0. The chain's next 16 LDS reads are

@@ -124,40 +124,6 @@ __device__ __forceinline__ void gv_load_tile(__amdgpu_buffer_rsrc_t rw, __amdgpu
     gv_load_rows<R>(rw, rs, tile * R * K, last * K, tile * R * G * 2, last * G * 2, j, K, G, wv, ws);
 }
 
-// the rmsnorm's chains: their float4 count n4 = K / 64 rounded up to NF (16, 32 or 64), chain j's float4s
-// at row4 + j (NF + 1) in LDS, zeros past n4
-__host__ __device__ __forceinline__ int gv_nf(int n4) {
-    return n4 <= 16 ? 16 : n4 <= 32 ? 32 : 64; // (the rmsnorm prologue takes K <= 4096)
-}
-
-// the rmsnorm's sum of squares over one chain (forward.c:886-901): ss = fma(v, v, ss) over its NF float4s in order,
-// straight-line: a ring of 8 float4 reads at immediate offsets, each register's next read issued right after its four
-// fmas, so a read has the other seven registers' 28 fmas to land. The reads and their waits are inline asm, in the order
-// written (the compiler otherwise issued a chain's reads ahead of its fmas); each wait names its register, so that
-// register's fmas come after it. The zeros past the chain's end change no bit: fma(0, 0, ss) == ss for every ss >= 0.
-// (Measured per chain of 64 float4s on one wave: 1.9 us for two sets of 16 reads taking turns, 1.1 us for this ring,
-// 0.7 us for the fmas alone)
-typedef float gv_f4 __attribute__((ext_vector_type(4)));
-template <int NF>
-__device__ __forceinline__ float gv_chain(const float4 *c) {
-    const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)c;
-    float ss = 0.0f;
-    gv_f4 q[8];
-    #pragma unroll
-    for (int u = 0; u < 8; u++) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(q[u]) : "v"(base), "i"(16 * u));
-    #pragma unroll
-    for (int i = 0; i < NF; i++) {
-        // (reads issued after read i: i + 1 .. min(i + 7, NF - 1))
-        const int later = NF - 1 - i < 7 ? NF - 1 - i : 7;
-        asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(q[i & 7]) : "i"(later));
-        const gv_f4 v = q[i & 7];
-        asm volatile("v_fmac_f32 %0, %1, %1\n\tv_fmac_f32 %0, %2, %2\n\tv_fmac_f32 %0, %3, %3\n\tv_fmac_f32 %0, %4, %4"
-                     : "+v"(ss) : "v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w));
-        if (i + 8 < NF) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(q[i & 7]) : "v"(base), "i"(16 * (i + 8)));
-    }
-    return ss;
-}
-
 // the group of 32 (this lane's 16 values and its pair's): wmax, s = wmax / 127, q = trunc(v * inv + copysign(.49999997))
 // (forward.c:803-836); the pair is lanes t, t ^ 1
 __device__ __forceinline__ void gv_quant16(const float (&v)[16], int4 &xq, float &xs) {
@@ -248,9 +214,9 @@ __global__ __launch_bounds__(NT) void k_gemv1(GvArgs a) {
                 v[4 * u + 3] = p0[u].w;
             }
         } else if (PRO == GV_NORM) {
-            // the row transposed: value e at xf[(e % 16) LS + e / 16], LS = 4 NF + 4 (chain j's values contiguous, the
-            // 16 chains 4 banks apart), zeros from e / 16 = K / 16 to 4 NF; the scale after the 16 chains
-            const int n4 = K >> 6, NF = gv_nf(n4), LS = 4 * NF + 4;
+            // the row in the chains' layout (rms_chain): value e at xf[(e % 16) LS + e / 16], LS = 4 NF + 4, zeros from
+            // e / 16 = K / 16 to 4 NF; the scale after the 16 chains
+            const int n4 = K >> 6, NF = rms_nf(n4), LS = 4 * NF + 4;
             if (act) {
                 #pragma unroll
                 for (int u = 0; u < 4; u++) {
@@ -268,9 +234,9 @@ __global__ __launch_bounds__(NT) void k_gemv1(GvArgs a) {
                 float ss = 0.0f;
                 if (t < 16) {
                     const float4 *c = (const float4 *)xf + t * (NF + 1);
-                    if (NF == 16) ss = gv_chain<16>(c);
-                    else if (NF == 32) ss = gv_chain<32>(c);
-                    else ss = gv_chain<64>(c); // (K <= 4096)
+                    if (NF == 16) ss = rms_chain<16>(c);
+                    else if (NF == 32) ss = rms_chain<32>(c);
+                    else ss = rms_chain<64>(c); // (K <= 4096)
                 }
                 // the tree over the 16 chains, as ss + shfl_down(ss, w) for w = 8, 4, 2, 1: lane 0's value from lanes
                 // 0-15 by DPP row shifts (row_shl:w, lane j + w of the same 16-lane row), no LDS round trips
@@ -425,7 +391,7 @@ static int gv_launch(int pro, int R, const GvArgs &a, const GwMat *nx, int nR, h
         b.n_tb = nR * nx->cols, b.n_tsb = nR * (nx->cols / 32) * 2;
         b.n_tiles = nx->rows / nR, b.n_grid = nnt < gv_nwg ? nnt : gv_nwg;
     }
-    size_t lds = (size_t)b.cmax * slot_bytes + (pro == GV_NORM ? (size_t)(16 * (4 * gv_nf(a.K / 64) + 4) + 4) * sizeof(float) : 0);
+    size_t lds = (size_t)b.cmax * slot_bytes + (pro == GV_NORM ? (size_t)(16 * (4 * rms_nf(a.K / 64) + 4) + 4) * sizeof(float) : 0);
     dim3 grid(nwg);
     hipEvent_t e0, e1;
     gw_take_launch_events(&e0, &e1);

@@ -39,9 +39,11 @@ __global__ __launch_bounds__(256) void k_embed_q8(float *__restrict__ x, int dim
 // ---------------------------------------------------- residual + rmsnorm + quantize (one row per block)
 
 // row b (= sel[j] if sel, else j): x[b] += d[b] (if d), xn = rmsnorm(x[b], w); xq / xs row j = quantize(xn);
-// hid row j = xn (if hid). 1024 threads, n % 1024 == 0 and n <= 16384 (up to 4 float4 per thread, all loaded first);
-// the row in LDS for the scale's 16 chains
+// hid row j = xn (if hid). 1024 threads, n % 32 == 0 and n <= 16384 (up to 4 float4 per thread, all loaded first);
+// the row in LDS for the scale's 16 chains: in the chains' layout where n % 64 == 0 (TR: rms_scale_t), else as it is
+// (rms_scale_lds)
 #define NORM_T 1024
+template <bool TR>
 __global__ __launch_bounds__(NORM_T) void k_rmsnorm_quant(float *__restrict__ x, const float *__restrict__ d, int n,
                                                           const float *__restrict__ w, const int *__restrict__ sel,
                                                           int8_t *__restrict__ xq, float *__restrict__ xs, int ldq,
@@ -73,12 +75,24 @@ __global__ __launch_bounds__(NORM_T) void k_rmsnorm_quant(float *__restrict__ x,
                 v[k].w = v[k].w + e[k].w;
                 xr[i] = v[k];
             }
-            ((float4 *)lds)[i] = v[k];
+            if (TR) { // (element 4 i + c: chain 4 (i % 4) + c, position i / 4)
+                const int LS = 4 * rms_nf(n >> 6) + 4, p = i >> 2, c0 = 4 * (i & 3);
+                lds[(c0 + 0) * LS + p] = v[k].x;
+                lds[(c0 + 1) * LS + p] = v[k].y;
+                lds[(c0 + 2) * LS + p] = v[k].z;
+                lds[(c0 + 3) * LS + p] = v[k].w;
+            } else {
+                ((float4 *)lds)[i] = v[k];
+            }
         }
+    }
+    if (TR) { // (the chains' zeros: positions n / 16 .. 4 NF - 1)
+        const int NF = rms_nf(n >> 6), LS = 4 * NF + 4, zc = 4 * NF - (n >> 4);
+        for (int z = t; z < 16 * zc; z += NORM_T) lds[(z / zc) * LS + (n >> 4) + z % zc] = 0.0f;
     }
     __syncthreads();
     if (t < 64) {
-        float r = rms_scale_lds(lds, n);
+        float r = TR ? rms_scale_t(lds, n) : rms_scale_lds(lds, n);
         if (t == 0) rsh = r;
     }
     __syncthreads();
@@ -1552,7 +1566,11 @@ int gw_k_embed_q8(float *x, int dim, const uint8_t *codes, const uint16_t *scale
 
 int gw_k_rmsnorm_quant(float *x, const float *d, int dim, const float *w, const int *sel, int n, int8_t *xq, float *xs, int ldq,
                        float *hid, hipStream_t s) {
-    GW_LAUNCH(k_rmsnorm_quant, dim3(n), dim3(NORM_T), (size_t)dim * sizeof(float), s, x, d, dim, w, sel, xq, xs, ldq, hid);
+    if (dim % 64 == 0)
+        GW_LAUNCH(k_rmsnorm_quant<true>, dim3(n), dim3(NORM_T), (size_t)16 * (4 * rms_nf(dim / 64) + 4) * sizeof(float), s, x, d, dim,
+                  w, sel, xq, xs, ldq, hid);
+    else
+        GW_LAUNCH(k_rmsnorm_quant<false>, dim3(n), dim3(NORM_T), (size_t)dim * sizeof(float), s, x, d, dim, w, sel, xq, xs, ldq, hid);
     return (int)hipGetLastError();
 }
 
