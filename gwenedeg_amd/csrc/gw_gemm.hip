@@ -1946,8 +1946,8 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
             hipExtLaunchKernelGGL(k_gemm_q8l<128>, dim3(((nt + 7) / 8) * 8 * mt), dim3(512), 0, s, e0, e1, 0, GQ_ARGS, mt);
         else if (lq == 64)
             hipExtLaunchKernelGGL(k_gemm_q8l<64>, dim3(((w->rows + 511) / 512) * 8 * mt), dim3(256), 0, s, e0, e1, 0, GQ_ARGS, mt);
-        else if (lq == 16) // (64 x 64 tiles, stages of 256 bytes of K)
-            hipExtLaunchKernelGGL((k_gemm_q8t<64, 64, 3, 2>), dim3(((w->rows + 511) / 512) * 8 * mt), dim3(1024), 0, s, e0, e1, 0, GQ_ARGS, mt);
+        else if (lq == 16) // (64 x 64 tiles, 4 stages of 256 bytes of K in the ring: 139 KB of LDS)
+            hipExtLaunchKernelGGL((k_gemm_q8t<64, 64, 4, 2>), dim3(((w->rows + 511) / 512) * 8 * mt), dim3(1024), 0, s, e0, e1, 0, GQ_ARGS, mt);
         else if (lq == 17) // (stages of 128)
             hipExtLaunchKernelGGL((k_gemm_q8t<64, 64, 4, 1>), dim3(((w->rows + 511) / 512) * 8 * mt), dim3(1024), 0, s, e0, e1, 0, GQ_ARGS, mt);
         else if (lq == 18) // (32 x 32 tiles)
