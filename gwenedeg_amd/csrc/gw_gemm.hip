@@ -1830,20 +1830,28 @@ static int g_q8_lds;    // (the Q8_0 GEMM: 0 chosen per launch, 1 k_gemm_q8f / k
 
 static bool q8_gemm_rows(const GwMat *w, int M) {
     // a Q8_0 matmul of M activation rows takes the MFMA GEMM (else the batched GEMV in passes of 8 rows): above 16 rows;
-    // above 8 for matrices of 8,192 rows or more, above 12 for 6,144 or more at K <= 4,096. The GEMM's time hardly
+    // above 8 for matrices of 8,192 rows or more, above 12 for 6,144 or more at K <= 4,096; where the GEMM takes 512-byte
+    // stages (K % 512 == 0), above 8 for 6,144 rows or more and above 12 for 4,096 or more at K <= 4,096 (9 rows 6,144 x
+    // 4,096 17.4 / 16.4 us; 16 rows 4,096 x 4,096 17.8 / 16.3 us; 4,096 x 12,288 stays on the GEMV up to 16 rows,
+    // 39.3 / 43.5 us). The GEMM's time hardly
     // depends on M or the width (18-23 us at K = 4,096, 50 at 12,288, k_gemm_q8t), the GEMV's grows with both (per 8
     // rows a pass over the weights). Measured at the 8B widths, us (GEMV / GEMM): 9 rows 24,576 x 4,096 48.5 / 32.8,
     // 12,288 x 4,096 28.8 / 21.7, 6,144 x 4,096 17.4 / 18.4, 4,096 x 4,096 14.7 / 18.4, 4,096 x 12,288 34.0 / 49.4;
     // 16 rows 6,144 x 4,096 21.8 / 18.3, 4,096 x 4,096 17.8 / 18.4, 4,096 x 12,288 39.3 / 49.3; 24 rows 4,096 x 4,096
     // 25.7 / 18.4, 4,096 x 12,288 57.9 / 49.4
-    return M > 16 || (M > 8 && w->rows >= 8192) || (M > 12 && w->rows >= 6144 && w->cols <= 4096);
+    const bool s512 = w->cols % 512 == 0 && w->cols <= 4096;
+    return M > 16 || (M > 8 && w->rows >= 8192) || (M > 12 && w->rows >= 6144 && w->cols <= 4096) ||
+           (s512 && ((M > 8 && w->rows >= 6144) || (M > 12 && w->rows >= 4096)));
 }
 
-static int q8l_width(int N, int M) {
+static int q8l_width(int N, int M, int K) {
     // the Q8_0 GEMM's kernel for N columns and M rows (K % 128 == 0): k_gemm_q8l with 128-column tiles (returns 128),
-    // with 64-column tiles (64), k_gemm_q8t of 64 x 64 tiles (16; 17: its 128-byte stages), of 32 x 32 (18) or 32 x 16
-    // (19), or 0: k_gemm_q8f. Forced by gw_q8_gemm_kernel (1 .. 7), else: k_gemm_q8t of 32 x 32 tiles where they are at
-    // most 1.5 per CU, of 64 x 64 where those are at most one per CU; else up to 32 rows k_gemm_q8f's 32-row tiles, 128
+    // with 64-column tiles (64), k_gemm_q8t of 64 x 64 tiles (16; 17: its 128-byte stages), of 32 x 32 (18; 20: its
+    // 512-byte stages) or 32 x 16 (19), or 0: k_gemm_q8f. Forced by gw_q8_gemm_kernel (1 .. 8), else: k_gemm_q8t of
+    // 32 x 32 tiles with 512-byte stages where those tiles are at most one per CU and K % 512 == 0 (one block per CU
+    // by its LDS; 32 rows 4,096 x 4,096 18.3 -> 16.4, 6,144 x 4,096 18.3 -> 16.7, 4,096 x 12,288 49.9 -> 43.6 us), with
+    // 256-byte stages where they are at most 1.5 per CU, of 64 x 64 where those are at most one per CU; else up to 32
+    // rows k_gemm_q8f's 32-row tiles, 128
     // columns where those tiles give three blocks per CU or more, else 64. Measured at the 8B widths, us per launch:
     //   k_gemm_q8t 32 x 32 / 64 x 64 / k_gemm_q8f: 32 rows 12,288 x 4,096 22.9 / 25.0 / 31.9; 6,144 x 4,096 18.8 / 23.9 /
     //   31.4; 4,096 x 12,288 49.7 / 63.4 / 87.5; 24,576 x 4,096 38.4 / 47.6 / 34.1; 64 rows 12,288 x 4,096 38.4 / 25.6 /
@@ -1854,7 +1862,9 @@ static int q8l_width(int N, int M) {
     //   256 rows: 24,576 x 4,096 123 / 109 / 109; 12,288 x 4,096 62.9 / 66.2 / 55.1; 4,096 x 12,288 91.2 / 122 / 88.8
     if (g_q8_lds) return g_q8_lds == 2 ? 128 : g_q8_lds == 3 ? 64 : g_q8_lds >= 4 ? 12 + g_q8_lds : 0;
     const size_t cus = (size_t)gemm_cus(), mt = (size_t)((M + 63) / 64);
-    if ((size_t)((N + 31) / 32) * ((M + 31) / 32) * 2 <= 3 * cus) return 18;
+    const size_t t32 = (size_t)((N + 31) / 32) * ((M + 31) / 32);
+    if (t32 <= cus && K % 512 == 0) return 20;
+    if (t32 * 2 <= 3 * cus) return 18;
     if ((size_t)((N + 63) / 64) * mt <= cus) return 16;
     if (M <= 32) return 0;
     return (size_t)((N + 127) / 128) * mt >= 3 * cus ? 128 : 64;
@@ -1941,7 +1951,8 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
         const bool full = w->cols % GKB == 0 && (size_t)(M + 64) * ldx < ((size_t)1 << 31) && (size_t)GN * w->cols < ((size_t)1 << 31);
         const dim3 g64g(nt, (M + 63) / 64), g32g(nt, (M + 31) / 32);
 #define GQ_ARGS (const int8_t *)w->codes, (const uint16_t *)w->scales, w->rows, w->cols, xq, xs, ldx, M, out, ldo
-        const int mt = (M + 63) / 64, lq0 = full ? q8l_width(w->rows, M) : 0, lq = lq0 >= 16 && w->cols % 256 ? 17 : lq0;
+        const int mt = (M + 63) / 64, lq0 = full ? q8l_width(w->rows, M, w->cols) : 0,
+                  lq1 = lq0 == 20 && w->cols % 512 ? 18 : lq0, lq = lq1 >= 16 && w->cols % 256 ? 17 : lq1;
         if (lq == 128)
             hipExtLaunchKernelGGL(k_gemm_q8l<128>, dim3(((nt + 7) / 8) * 8 * mt), dim3(512), 0, s, e0, e1, 0, GQ_ARGS, mt);
         else if (lq == 64)
@@ -1952,6 +1963,9 @@ int gw_k_matmul(const GwMat *w, const int8_t *xq, const float *xs, int ldx, int 
             hipExtLaunchKernelGGL((k_gemm_q8t<64, 64, 4, 1>), dim3(((w->rows + 511) / 512) * 8 * mt), dim3(1024), 0, s, e0, e1, 0, GQ_ARGS, mt);
         else if (lq == 18) // (32 x 32 tiles)
             hipExtLaunchKernelGGL((k_gemm_q8t<32, 32, 4, 2>), dim3(((w->rows + 255) / 256) * 8 * ((M + 31) / 32)), dim3(256), 0, s, e0, e1, 0,
+                                  GQ_ARGS, (M + 31) / 32);
+        else if (lq == 20) // (32 x 32 tiles, stages of 512 bytes of K: 140 KB of LDS, one block per CU)
+            hipExtLaunchKernelGGL((k_gemm_q8t<32, 32, 4, 4>), dim3(((w->rows + 255) / 256) * 8 * ((M + 31) / 32)), dim3(256), 0, s, e0, e1, 0,
                                   GQ_ARGS, (M + 31) / 32);
         else if (lq == 19) // (32 x 16 tiles)
             hipExtLaunchKernelGGL((k_gemm_q8t<32, 16, 4, 2>), dim3(((w->rows + 127) / 128) * 8 * ((M + 31) / 32)), dim3(128), 0, s, e0, e1, 0,
@@ -2088,7 +2102,7 @@ int gw_q8_block_sums(int32_t *isum, const int8_t *codes, int N, int K, const int
 }
 
 int gw_q8_gemm_kernel(int k) {
-    if (k < 0 || k > 7) return -1;
+    if (k < 0 || k > 8) return -1;
     int prev = g_q8_lds;
     g_q8_lds = k;
     return prev;

@@ -339,20 +339,22 @@ int gw_topk_rows(const float *logits, int n, int ld, int rows, int k, float *val
 int gw_matmul_tile_rows(int rows);
 
 /* The kernel of the Q8_0 matmuls of 2 .. 32 activation rows (batched decode rows): 0 chosen per launch (the default:
- * the MFMA GEMM above 16 rows, above 8 for matrices of 8,192 rows or more, above 12 for 6,144 or more at K <= 4,096; else the
- * batched GEMV in passes of 8 rows), 1 the batched GEMV, 2 the MFMA GEMM (its kernel as gw_q8_gemm_kernel chooses).
+ * the MFMA GEMM above 16 rows, above 8 for matrices of 8,192 rows or more, above 12 for 6,144 or more at K <= 4,096, and
+ * where K <= 4,096 and K % 512 == 0 above 8 for 6,144 rows or more and above 12 for 4,096 or more; else the batched GEMV
+ * in passes of 8 rows), 1 the batched GEMV, 2 the MFMA GEMM (its kernel as gw_q8_gemm_kernel chooses).
  * Returns the previous setting, or -1 (and changes nothing) for another value. A tuning and test hook with no
  * counterpart in runq.h; results do not depend on it */
 int gw_q8_batch_kernel(int k);
 
-/* The kernel of the Q8_0 MFMA GEMM (K % 128 == 0): 0 chosen per launch (the default: k_gemm_q8t of 32 x 32 tiles where
- * they are at most 1.5 per CU, of 64 x 64 where those are at most one per CU; else up to 32 rows k_gemm_q8f, above
+/* The kernel of the Q8_0 MFMA GEMM (K % 128 == 0): 0 chosen per launch (the default: k_gemm_q8t of 32 x 32 tiles with
+ * 512-byte stages where they are at most one per CU and K % 512 == 0, with 256-byte stages where they are at most 1.5
+ * per CU, of 64 x 64 where those are at most one per CU; else up to 32 rows k_gemm_q8f, above
  * k_gemm_q8l with 128-column tiles where they give 3 blocks per CU, else 64), 1 k_gemm_q8f (4 waves, stages staged
  * through registers, 32-row tiles up to 32 rows), 2 / 3 k_gemm_q8l with 128 / 64-column tiles (8 / 4 waves of 32 x 32
  * tiles, stages copied into LDS by the buffer unit), 4 / 5 k_gemm_q8t of 64 x 64 tiles (16 waves of 16 x 16 tiles) with
  * stages of 256 bytes of K where K % 256 == 0, else 128 / with 128, 6 / 7 k_gemm_q8t of 32 x 32 / 32 x 16 tiles (256-byte
- * stages where K % 256 == 0, else the 64 x 64 tiles' 128-byte ones). The w1 / w3 launch with the SwiGLU epilogue takes
- * k_gemm_q8l's 64 columns under 4 .. 7. Returns the previous setting, or -1 (and changes nothing) for another value.
+ * stages where K % 256 == 0, else the 64 x 64 tiles' 128-byte ones), 8 k_gemm_q8t of 32 x 32 tiles with 512-byte
+ * stages where K % 512 == 0 (else as 6). Returns the previous setting, or -1 (and changes nothing) for another value.
  * A tuning and test hook with no counterpart in runq.h; results do not depend on it */
 int gw_q8_gemm_kernel(int k);
 

@@ -47,10 +47,10 @@ def test_prefill_decode_bitexact_vs_oracle(gw, synth_models, shape):
         tok = int(np.argmax(ref))
 
 
-@pytest.mark.parametrize("kern,tile", [(1, 64), (1, 32), (2, 0), (3, 0), (4, 0), (5, 0), (6, 0), (7, 0)])
+@pytest.mark.parametrize("kern,tile", [(1, 64), (1, 32), (2, 0), (3, 0), (4, 0), (5, 0), (6, 0), (7, 0), (8, 0)])
 def test_prefill_gemm_kernels_bitexact_vs_oracle(gw, synth_models, kern, tile):
     """a 100-row prefill pass through each Q8_0 GEMM (gw_q8_gemm_kernel 1 with 64- or 32-row tiles: k_gemm_q8f; 2, 3:
-    k_gemm_q8l of 128 / 64 columns; 4 .. 7: k_gemm_q8t's tiles and stages; 100 rows: 2 row tiles), every row's logits
+    k_gemm_q8l of 128 / 64 columns; 4 .. 8: k_gemm_q8t's tiles and stages; 100 rows: 2 row tiles), every row's logits
     against the oracle bit for bit, then decode steps on the cache it wrote"""
     from oracle import oracle as orc
     path = synth_models("tiny")

@@ -70,12 +70,12 @@ def test_q8_matmul_bitexact(dev, M, N, K, tile):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"max diff {np.abs(got - ref).max()}"
 
 
-@pytest.mark.parametrize("kern", [1, 2, 3, 4, 5, 6, 7])
+@pytest.mark.parametrize("kern", [1, 2, 3, 4, 5, 6, 7, 8])
 @pytest.mark.parametrize("M,N,K", [(9, 128, 128), (33, 208, 768), (64, 1008, 1024), (100, 384, 4096), (130, 256, 12288),
                                    (512, 1024, 4096), (512, 512, 12288)])
 def test_q8_gemm_kernels_bitexact(dev, M, N, K, kern):
     """the Q8_0 MFMA GEMM (K % 128 == 0) with each kernel forced (gw_q8_gemm_kernel: 1 k_gemm_q8f, 2 / 3 k_gemm_q8l of 128 / 64 columns, 4 / 5 k_gemm_q8t of 64 x 64 tiles with 256- /
-    128-byte stages, 6 / 7 of 32 x 32 / 32 x 16 tiles) against
+    128-byte stages, 6 / 7 of 32 x 32 / 32 x 16 tiles, 8 of 32 x 32 tiles with 512-byte stages where K % 512 == 0, else 6) against
     the oracle bit for bit: partial row tiles (9, 33, 100, 130 rows), partial column tiles (208, 1,008), one stage (K =
     128) and two (256 would be one pair of stages; 768 an odd count), the 8B widths at 512 rows"""
     torch, gw = dev
