@@ -99,7 +99,7 @@ __device__ __forceinline__ float gv_fold(const float *p, int G) {
 // D = 4 everywhere: wo 345 -> 304, qkv 324 -> 338, w1/w3 773 -> 804, w2 481 -> 511; D = 5 slower everywhere; wo alone
 // at 4: 345 -> 301, at 5: 331
 #define GV_DEPTH 3
-#define GV_DEPTH_COMBINE 4
+#define GV_DEPTH_COMBINE 4 // (256-thread blocks only: at 768 threads a wave has 168 registers, and 4 sets spilled 141)
 template <int R>
 __device__ __forceinline__ void gv_load_rows(__amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t rs, int cb, int cl, int sb, int sl,
                                              int j, int K, int G, int4 (&wv)[R], uint32_t (&ws)[R]) {
@@ -396,7 +396,7 @@ static int gv_launch(int pro, int R, const GvArgs &a, const GwMat *nx, int nR, h
     hipEvent_t e0, e1;
     gw_take_launch_events(&e0, &e1);
 #define GV_L(RR, PP, NN)                                                                                               \
-    hipExtLaunchKernelGGL((k_gemv1<RR, PP, NN, PP == GV_COMBINE ? GV_DEPTH_COMBINE : GV_DEPTH>), grid, dim3(nt),          \
+    hipExtLaunchKernelGGL((k_gemv1<RR, PP, NN, PP == GV_COMBINE && NN == 256 ? GV_DEPTH_COMBINE : GV_DEPTH>), grid, dim3(nt), \
                           (uint32_t)lds, s, e0, e1, 0, b)
 #define GV_R(PP)                                                                                                        \
     if (nt <= 256) {                                                                                                    \
